@@ -1,0 +1,153 @@
+"""Functional CPU restatements of the modules around the carrier hot path, driven by a state_dict.
+TEST INFRASTRUCTURE ONLY (see oracle/__init__).
+
+Parameter names are the reference modules' (`src/assoc.py:323-348`, `src/spin.py:69-94`, `src/model.py:629-702`),
+so a state_dict of the product modules in `pragnosia_amd` loads here unchanged. Everything runs in the dtype of the
+parameters passed in (fp64 for the truth).
+
+Pinning: these are compositions of the pinned scans in `oracle.aspin` / `oracle.diag` with torch built-ins
+(LayerNorm, Linear, RMSNorm, GELU, softplus, sigmoid). The compositions themselves are checked by invariants in
+tests/test_oracle_modules.py: causality, carried windows == one pass (plain rule exactly; across a position restart
+through the rebase), token-at-a-time decode == one pass, forward_carried's last window == the same window after a
+carried prefix. The order of the composition (which norm, which gate, where) has no independent golden vector:
+parity unpinned beyond those invariants.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import aspin as A_
+from . import diag as D_
+
+
+def _lin(x, sd, name):
+    return F.linear(x, sd[name + ".weight"], sd.get(name + ".bias"))
+
+
+def _ln(x, sd, name, eps=1e-5):
+    return F.layer_norm(x, (x.shape[-1],), sd[name + ".weight"], sd[name + ".bias"], eps)
+
+
+def _rms(x, weight):
+    """nn.RMSNorm with eps=None: eps = finfo(dtype).eps."""
+    return F.rms_norm(x, (x.shape[-1],), weight, torch.finfo(x.dtype).eps)
+
+
+def assoc_carrier(sd, x, h0=None, pos0=0, *, heads, delta=False, write_all=False, key_topk=0, la_floor=None,
+                  chunk=64, pos_wrap=None):
+    """AssocCarrier.forward, torch path (`src/assoc.py:384-512`, kernel=False, no fused projections, no short
+    convolution). h0 = (S, p0) or None. Returns (out, (S, p0 + T))."""
+    B, T, D = x.shape
+    H = heads
+    dk = D // H
+    z = _ln(x, sd, "ln")
+    S0, p0 = (None, pos0) if h0 is None else (h0[0], h0[1])
+    theta = sd["theta"]
+    if S0 is not None and float(p0) != 0.0:
+        S0 = A_.rebase(S0.to(x.dtype), theta.to(x.dtype), float(p0))
+    pos = torch.arange(T)
+    if pos_wrap:
+        pos = pos % pos_wrap
+    kp = _lin(z, sd, "k").reshape(B, T, H, dk)
+    if key_topk:
+        keep = torch.zeros_like(kp).scatter_(-1, kp.abs().topk(key_topk, dim=-1).indices, 1.0)
+        kp = kp * keep
+    qp = _lin(z, sd, "q").reshape(B, T, H, dk)
+    vp = _lin(z, sd, "v").reshape(B, T, H, dk)
+    gate = None if (delta or write_all) else _lin(z, sd, "wi")
+    q, k, v = A_.prep(qp, kp, vp, gate, theta, pos)
+    la = A_.logalpha(_lin(z, sd, "wa"), sd["A"], la_floor).transpose(1, 2)
+    beta = None
+    if delta:
+        beta = torch.sigmoid(_lin(z, sd, "wb")).transpose(1, 2)
+        if write_all:
+            beta = beta.clamp(min=0.75)
+    o, S = A_.assoc_scan(q, k, v, la, S0, chunk=chunk, beta=beta)
+    o = _rms(o.to(x.dtype), sd["on.weight"]).transpose(1, 2).reshape(B, T, D)
+    out = x + F.linear(o, sd["o.weight"] * torch.sigmoid(sd["gate"]))
+    return out, (S, T)
+
+
+def spin_rf(sd, x, h0=None, gate_c=8.0, nu_min=1e-3):
+    """SpinCarrier(gated="rf").forward (`src/spin.py:229-246`, `lam` at `:98-103`), through the chunked scan.
+    Returns (out, (Re h_T, Im h_T))."""
+    z = _ln(x, sd, "ln")
+    nu = nu_min + F.softplus(sd["nu_raw"])
+    logmag = -gate_c * torch.sigmoid(_lin(z, sd, "Wr")) * nu
+    gam = torch.sqrt((1.0 - torch.exp(2.0 * logmag)).clamp_min(1e-6))
+    u = _lin(z, sd, "B") * gam * torch.sigmoid(_lin(z, sd, "Wi"))
+    y, h = D_.scan_gated(u, logmag, sd["theta"].expand_as(logmag), h0)
+    return x + torch.sigmoid(sd["gate"]) * _lin(y.to(x.dtype), sd, "C"), h
+
+
+def _mixer(sd, prefix, mixer, heads, x, st):
+    sub = {k[len(prefix):]: v for k, v in sd.items() if k.startswith(prefix)}
+    if mixer in ("aspin", "dspin"):
+        return assoc_carrier(sub, x, st, heads=heads, delta=(mixer == "dspin"))
+    if mixer == "fspin":
+        return spin_rf(sub, x, st)
+    raise ValueError(mixer)
+
+
+def _mlp(sd, prefix, x):
+    h = _ln(x, sd, prefix + "n")
+    return x + _lin(F.gelu(_lin(h, sd, prefix + "a")), sd, prefix + "b")
+
+
+def lm_forward(sd, ids, *, layers, mixer, heads):
+    """LM.forward (`src/model.py:820-840`): token + position (mod the table), per layer mixer then MLP, final LN,
+    tied head."""
+    ctx = sd["p.weight"].shape[0]
+    T = ids.shape[1]
+    h = F.embedding(ids, sd["e.weight"]) + F.embedding(torch.arange(T) % ctx, sd["p.weight"])
+    for i in range(layers):
+        h, _ = _mixer(sd, f"mix.{i}.", mixer, heads, h, None)
+        h = _mlp(sd, f"mlp.{i}.", h)
+    return F.linear(_ln(h, sd, "n"), sd["e.weight"])
+
+
+def lm_forward_carried(sd, ids, window, *, layers, mixer, heads):
+    """LM.forward_carried (`src/model.py:842-864`): windows of `window` tokens, positions restarting per window,
+    every layer's state carried; returns the final window's logits."""
+    states = [None] * layers
+    logits = None
+    for s in range(0, ids.shape[1], window):
+        xw = ids[:, s:s + window]
+        h = F.embedding(xw, sd["e.weight"]) + F.embedding(torch.arange(xw.shape[1]), sd["p.weight"])
+        for i in range(layers):
+            h, states[i] = _mixer(sd, f"mix.{i}.", mixer, heads, h, states[i])
+            h = _mlp(sd, f"mlp.{i}.", h)
+        logits = F.linear(_ln(h, sd, "n"), sd["e.weight"])
+    return logits
+
+
+def greedy_decode(sd, prompt, n, *, layers, mixer, heads):
+    """Greedy incremental generation (`src/bench.py:192-239`): the prompt is read in ctx-sized windows with the
+    state carried, then each new token is one T=1 step through every layer; the position index is (prefill +
+    i) mod ctx and each carrier rebases its state by the previous call's length. prompt (B, P) ids.
+    Returns (tokens (B, n), logits of every step (B, n, V))."""
+    ctx = sd["p.weight"].shape[0]
+    states = [None] * layers
+    lg = None
+    pw = 0
+    for s in range(0, prompt.shape[1], ctx):
+        x = prompt[:, s:s + ctx]
+        h = F.embedding(x, sd["e.weight"]) + F.embedding(torch.arange(x.shape[1]), sd["p.weight"])
+        for i in range(layers):
+            h, states[i] = _mixer(sd, f"mix.{i}.", mixer, heads, h, states[i])
+            h = _mlp(sd, f"mlp.{i}.", h)
+        lg = F.linear(_ln(h[:, -1:], sd, "n"), sd["e.weight"])[:, -1]
+        pw = x.shape[1] % ctx
+    toks, lgs = [], []
+    for _ in range(n):
+        nxt = lg.argmax(-1)
+        toks.append(nxt)
+        lgs.append(lg)
+        h = F.embedding(nxt[:, None], sd["e.weight"]) + F.embedding(torch.tensor([pw]), sd["p.weight"])
+        for i in range(layers):
+            h, states[i] = _mixer(sd, f"mix.{i}.", mixer, heads, h, states[i])
+            h = _mlp(sd, f"mlp.{i}.", h)
+        lg = F.linear(_ln(h, sd, "n"), sd["e.weight"])[:, -1]
+        pw = (pw + 1) % ctx
+    return torch.stack(toks, 1), torch.stack(lgs, 1)

@@ -1,0 +1,52 @@
+"""ctypes binding of libpragnosia_hip.so (the C ABI declared in include/pragnosia_hip.h).
+
+There is no fallback: if the library is missing or a call is made on a non-ROCm tensor, this raises."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libpragnosia_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "pragnosia_hip.h")
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+# argument types of every entry point, in header order
+SIGNATURES = {
+    "pragnosia_abi_version": [],
+    "pragnosia_error_string": [_i32],
+    "pragnosia_diag_scan_fwd": [_p] * 7 + [_i64] * 3 + [_p],
+    "pragnosia_diag_scan_bwd": [_p] * 14 + [_i64] * 3 + [_p],
+}
+
+_lib = None
+
+
+class PragnosiaError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded library, with argument and return types set. Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise PragnosiaError(f"{LIB_PATH} is missing: build it with `python -m pragnosia_amd.build` "
+                                 "(there is no CPU or PyTorch fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_char_p if name == "pragnosia_error_string" else _i32
+        _lib = L
+    return _lib
+
+
+def check(code: int, what: str) -> None:
+    if code != 0:
+        msg = lib().pragnosia_error_string(code).decode()
+        raise PragnosiaError(f"{what} failed with code {code}: {msg}")

@@ -1,0 +1,37 @@
+// Shared definitions for the carrier-path HIP kernels (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+#include "../../include/pragnosia_hip.h"
+
+#define PGN_DEVICE __device__ __forceinline__
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+// Launch-time argument failures are reported with negative codes (hipError_t values are non-negative).
+#define PGN_CHECK_ARG(cond)                                   \
+  do {                                                        \
+    if (!(cond)) return PRAGNOSIA_ERR_INVALID_ARGUMENT;       \
+  } while (0)
+
+#define PGN_RETURN_LAUNCH()                                   \
+  do {                                                        \
+    hipError_t e_ = hipGetLastError();                        \
+    return e_ == hipSuccess ? PRAGNOSIA_OK : (int)e_;         \
+  } while (0)
+
+PGN_DEVICE float pgn_exp(float x) { return __expf(x); }
+
+// Round-to-nearest-even fp32 -> bf16 (finite inputs).
+PGN_DEVICE __bf16 pgn_bf16(float x) { return (__bf16)x; }
+PGN_DEVICE float pgn_f32(__bf16 x) { return (float)x; }
+
+// One 16x16x32 bf16 MFMA step: acc += A(16x32) B(32x16).
+PGN_DEVICE f32x4 pgn_mfma(bf16x8 a, bf16x8 b, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}

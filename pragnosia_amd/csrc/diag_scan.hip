@@ -1,0 +1,273 @@
+// Complex diagonal recurrence h_t = lambda_t h_{t-1} + u_t with per-token lambda_t = exp(logmag_t + i ang_t):
+// forward and adjoint backward, parallel over time.
+//
+// The recurrence composes associatively: a segment of tokens acts on its incoming state as the affine map
+// h -> P h + e, P = prod lambda_t (|P| <= 1), e = the segment's own contribution from zero. One workgroup owns
+// 32 channels of one sequence (a wave = 32 channels x 2 time segments, so every load instruction reads two
+// 128-byte rows of the D-fastest layout) and walks time in blocks of 2 * NW * SEG tokens:
+//   1. each lane loads its segment (SEG tokens of one channel, all loads issued up front), forms lambda in
+//      registers and scans it from zero, giving the segment's map (P, e);
+//   2. the maps go to LDS; after one barrier every lane folds the maps of the segments before it into the
+//      block's carry-in to get its own incoming state;
+//   3. the lane re-runs its SEG steps from that state out of registers and writes h.
+// The block carry and the map buffers are double-buffered, so each time block costs one barrier. Nothing is
+// re-read from HBM: the forward moves 20 B per (b, t, d) element, the backward 32 B.
+//
+// The backward is the same scan run in reverse on the adjoint a_t = g_t + conj(lambda_{t+1}) a_{t+1} (the
+// transpose of multiplication by lambda is multiplication by its conjugate), followed per token by
+//   du_t = Re a_t,  dlogmag_t = a_t . (lambda_t h_{t-1}),  dang_t = a_t . (i lambda_t h_{t-1}),
+// with (x . y) the real inner product of the complex numbers as 2-vectors. The final-state gradients enter as
+// the carry into t = T-1; the carry out of t = 0 is dh0. This restates `src/scan_kernel.py:12-17`.
+#include "common.h"
+
+namespace {
+
+constexpr int kCH = 32;  // channels per workgroup
+
+struct SegMaps {
+  float pr, pi, er, ei;
+};
+
+template <int NW, int SEG>
+__global__ __launch_bounds__(NW * 64) void diag_fwd_kernel(
+    const float* __restrict__ u, const float* __restrict__ lm, const float* __restrict__ an,
+    const float* __restrict__ h0r, const float* __restrict__ h0i, float* __restrict__ hr,
+    float* __restrict__ hi, int T, int D, int n_ctile) {
+  constexpr int NSEG = 2 * NW;
+  constexpr int TB = NSEG * SEG;
+  __shared__ SegMaps maps[2][NSEG][kCH];
+  __shared__ float2 carry[2][kCH];
+
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 31;
+  const int seg = 2 * (threadIdx.x >> 6) + (lane >> 5);
+  const int b = blockIdx.x / n_ctile;
+  const int d = (blockIdx.x - b * n_ctile) * kCH + c;
+  const bool dok = d < D;
+  const size_t base = (size_t)b * T * D + (dok ? d : 0);
+
+  if (threadIdx.x < kCH) {
+    float2 h = make_float2(0.f, 0.f);
+    if (h0r != nullptr && dok) h = make_float2(h0r[(size_t)b * D + d], h0i[(size_t)b * D + d]);
+    carry[0][c] = h;
+  }
+
+  for (int tb = 0, it = 0; tb < T; tb += TB, ++it) {
+    const int p = it & 1;
+    const int t0 = tb + seg * SEG;
+    float xr[SEG], xi[SEG], xu[SEG];
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+      const int t = t0 + j;
+      const bool ok = dok && t < T;
+      const size_t off = base + (size_t)(ok ? t : 0) * D;
+      xu[j] = ok ? u[off] : 0.f;
+      const float l = ok ? lm[off] : 0.f;
+      const float a = ok ? an[off] : 0.f;
+      const float m = expf(l);
+      float s, co;
+      sincosf(a, &s, &co);
+      xr[j] = m * co;
+      xi[j] = m * s;
+    }
+    // the segment's map from a zero state
+    float er = 0.f, ei = 0.f, pr = 1.f, pi = 0.f;
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+      const float nr = xr[j] * er - xi[j] * ei + xu[j];
+      const float ni = xi[j] * er + xr[j] * ei;
+      er = nr;
+      ei = ni;
+      const float qr = xr[j] * pr - xi[j] * pi;
+      const float qi = xi[j] * pr + xr[j] * pi;
+      pr = qr;
+      pi = qi;
+    }
+    maps[p][seg][c] = SegMaps{pr, pi, er, ei};
+    __syncthreads();
+    // incoming state: the block carry pushed through every earlier segment's map
+    float2 h = carry[p][c];
+    for (int s = 0; s < seg; ++s) {
+      const SegMaps m = maps[p][s][c];
+      const float nr = m.pr * h.x - m.pi * h.y + m.er;
+      const float ni = m.pi * h.x + m.pr * h.y + m.ei;
+      h = make_float2(nr, ni);
+    }
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+      const float nr = xr[j] * h.x - xi[j] * h.y + xu[j];
+      const float ni = xi[j] * h.x + xr[j] * h.y;
+      h = make_float2(nr, ni);
+      const int t = t0 + j;
+      if (dok && t < T) {
+        hr[base + (size_t)t * D] = h.x;
+        hi[base + (size_t)t * D] = h.y;
+      }
+    }
+    if (seg == NSEG - 1) carry[p ^ 1][c] = h;
+  }
+}
+
+template <int NW, int SEG>
+__global__ __launch_bounds__(NW * 64) void diag_bwd_kernel(
+    const float* __restrict__ g, const float* __restrict__ glr, const float* __restrict__ gli,
+    const float* __restrict__ lm, const float* __restrict__ an, const float* __restrict__ hr,
+    const float* __restrict__ hi, const float* __restrict__ h0r, const float* __restrict__ h0i,
+    float* __restrict__ du, float* __restrict__ dlm, float* __restrict__ dan, float* __restrict__ dh0r,
+    float* __restrict__ dh0i, int T, int D, int n_ctile) {
+  constexpr int NSEG = 2 * NW;
+  constexpr int TB = NSEG * SEG;
+  __shared__ SegMaps maps[2][NSEG][kCH];
+  __shared__ float2 carry[2][kCH];
+
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 31;
+  const int seg = 2 * (threadIdx.x >> 6) + (lane >> 5);
+  const int b = blockIdx.x / n_ctile;
+  const int d = (blockIdx.x - b * n_ctile) * kCH + c;
+  const bool dok = d < D;
+  const size_t base = (size_t)b * T * D + (dok ? d : 0);
+  const size_t bd = (size_t)b * D + (dok ? d : 0);
+
+  if (threadIdx.x < kCH) {
+    float2 a = make_float2(0.f, 0.f);
+    if (dok) {
+      if (glr != nullptr) a.x = glr[bd];
+      if (gli != nullptr) a.y = gli[bd];
+    }
+    carry[0][c] = a;
+  }
+
+  const int nblk = (T + TB - 1) / TB;
+  float2 cin = make_float2(0.f, 0.f);
+  for (int it = 0; it < nblk; ++it) {
+    const int p = it & 1;
+    const int t0 = (nblk - 1 - it) * TB + seg * SEG;
+    float xr[SEG], xi[SEG], xg[SEG];  // lambda_t (not conjugated) and g_t
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+      const int t = t0 + j;
+      const bool ok = dok && t < T;
+      const size_t off = base + (size_t)(ok ? t : 0) * D;
+      xg[j] = ok ? g[off] : 0.f;
+      const float l = ok ? lm[off] : 0.f;
+      const float a = ok ? an[off] : 0.f;
+      const float m = expf(l);
+      float s, co;
+      sincosf(a, &s, &co);
+      xr[j] = m * co;
+      xi[j] = m * s;
+    }
+    // the segment's map on the carry coming from its right: c_out = P c_in + e, where the carry out of a
+    // token is conj(lambda_t) a_t and a_t = g_t + (carry in)
+    float er = 0.f, ei = 0.f, pr = 1.f, pi = 0.f;
+#pragma unroll
+    for (int j = SEG - 1; j >= 0; --j) {
+      const float ar = xg[j] + er, ai = ei;
+      er = xr[j] * ar + xi[j] * ai;
+      ei = xr[j] * ai - xi[j] * ar;
+      const float qr = xr[j] * pr + xi[j] * pi;
+      const float qi = xr[j] * pi - xi[j] * pr;
+      pr = qr;
+      pi = qi;
+    }
+    maps[p][seg][c] = SegMaps{pr, pi, er, ei};
+    __syncthreads();
+    float2 a = carry[p][c];
+    for (int s = NSEG - 1; s > seg; --s) {
+      const SegMaps m = maps[p][s][c];
+      const float nr = m.pr * a.x - m.pi * a.y + m.er;
+      const float ni = m.pi * a.x + m.pr * a.y + m.ei;
+      a = make_float2(nr, ni);
+    }
+#pragma unroll
+    for (int j = SEG - 1; j >= 0; --j) {
+      const int t = t0 + j;
+      const bool ok = dok && t < T;
+      const float ar = xg[j] + a.x, ai = a.y;
+      float qr = 0.f, qi = 0.f;  // h_{t-1}
+      if (ok) {
+        if (t > 0) {
+          qr = hr[base + (size_t)(t - 1) * D];
+          qi = hi[base + (size_t)(t - 1) * D];
+        } else if (h0r != nullptr) {
+          qr = h0r[bd];
+          qi = h0i[bd];
+        }
+      }
+      const float rr = xr[j] * qr - xi[j] * qi;  // lambda_t h_{t-1}
+      const float ri = xi[j] * qr + xr[j] * qi;
+      if (ok) {
+        const size_t off = base + (size_t)t * D;
+        du[off] = ar;
+        dlm[off] = ar * rr + ai * ri;
+        dan[off] = ai * rr - ar * ri;  // i lambda h = (-ri, rr)
+      }
+      a = make_float2(xr[j] * ar + xi[j] * ai, xr[j] * ai - xi[j] * ar);
+    }
+    if (seg == 0) carry[p ^ 1][c] = a;
+    cin = a;
+  }
+  if (seg == 0 && dok && dh0r != nullptr) {
+    dh0r[bd] = cin.x;
+    dh0i[bd] = cin.y;
+  }
+}
+
+template <int NW, int SEG>
+int launch_fwd(const float* u, const float* lm, const float* an, const float* h0r, const float* h0i, float* hr,
+               float* hi, int B, int T, int D, hipStream_t st) {
+  const int nct = (D + kCH - 1) / kCH;
+  hipLaunchKernelGGL((diag_fwd_kernel<NW, SEG>), dim3(B * nct), dim3(NW * 64), 0, st, u, lm, an, h0r, h0i, hr,
+                     hi, T, D, nct);
+  PGN_RETURN_LAUNCH();
+}
+
+template <int NW, int SEG>
+int launch_bwd(const float* g, const float* glr, const float* gli, const float* lm, const float* an,
+               const float* hr, const float* hi, const float* h0r, const float* h0i, float* du, float* dlm,
+               float* dan, float* dh0r, float* dh0i, int B, int T, int D, hipStream_t st) {
+  const int nct = (D + kCH - 1) / kCH;
+  hipLaunchKernelGGL((diag_bwd_kernel<NW, SEG>), dim3(B * nct), dim3(NW * 64), 0, st, g, glr, gli, lm, an, hr,
+                     hi, h0r, h0i, du, dlm, dan, dh0r, dh0i, T, D, nct);
+  PGN_RETURN_LAUNCH();
+}
+
+bool shape_ok(int64_t B, int64_t T, int64_t D) {
+  if (B <= 0 || T < 0 || D <= 0) return false;
+  if (B * T * D >= ((int64_t)1 << 40)) return false;
+  if (T >= (1 << 30) || D >= (1 << 30)) return false;
+  const int64_t blocks = B * ((D + kCH - 1) / kCH);
+  return blocks < ((int64_t)1 << 31);
+}
+
+}  // namespace
+
+extern "C" int pragnosia_diag_scan_fwd(const float* u, const float* logmag, const float* ang, const float* h0r,
+                                       const float* h0i, float* hr, float* hi, int64_t B, int64_t T, int64_t D,
+                                       void* stream) {
+  PGN_CHECK_ARG(shape_ok(B, T, D));
+  PGN_CHECK_ARG((h0r == nullptr) == (h0i == nullptr));
+  if (T == 0) return PRAGNOSIA_OK;
+  PGN_CHECK_ARG(u && logmag && ang && hr && hi);
+  hipStream_t st = (hipStream_t)stream;
+  if (T >= 128) return launch_fwd<8, 8>(u, logmag, ang, h0r, h0i, hr, hi, (int)B, (int)T, (int)D, st);
+  return launch_fwd<2, 8>(u, logmag, ang, h0r, h0i, hr, hi, (int)B, (int)T, (int)D, st);
+}
+
+extern "C" int pragnosia_diag_scan_bwd(const float* g, const float* g_last_r, const float* g_last_i,
+                                       const float* logmag, const float* ang, const float* hr, const float* hi,
+                                       const float* h0r, const float* h0i, float* du, float* dlogmag, float* dang,
+                                       float* dh0r, float* dh0i, int64_t B, int64_t T, int64_t D, void* stream) {
+  PGN_CHECK_ARG(shape_ok(B, T, D));
+  PGN_CHECK_ARG((h0r == nullptr) == (h0i == nullptr));
+  PGN_CHECK_ARG((dh0r == nullptr) == (dh0i == nullptr));
+  hipStream_t st = (hipStream_t)stream;
+  if (T == 0) return PRAGNOSIA_ERR_INVALID_ARGUMENT;
+  PGN_CHECK_ARG(g && logmag && ang && hr && hi && du && dlogmag && dang);
+  if (T >= 128)
+    return launch_bwd<8, 8>(g, g_last_r, g_last_i, logmag, ang, hr, hi, h0r, h0i, du, dlogmag, dang, dh0r, dh0i,
+                             (int)B, (int)T, (int)D, st);
+  return launch_bwd<2, 8>(g, g_last_r, g_last_i, logmag, ang, hr, hi, h0r, h0i, du, dlogmag, dang, dh0r, dh0i,
+                          (int)B, (int)T, (int)D, st);
+}

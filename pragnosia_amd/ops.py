@@ -1,0 +1,106 @@
+"""torch custom ops (namespace `pragnosia`) over the C ABI of libpragnosia_hip.so.
+
+Every op allocates its outputs with torch on the input's device, makes its inputs contiguous, launches on the
+current HIP stream and returns; nothing synchronises, so the ops are hipGraph-capturable once shapes are fixed.
+Each op has a fake (meta) implementation for torch.compile and, where differentiable, a registered backward that is
+itself a custom op. There is no CPU path: a CPU tensor raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from ._lib import PragnosiaError, check, lib
+
+
+def _ptr(t: Optional[Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require_gpu(*ts: Optional[Tensor]) -> None:
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise PragnosiaError("pragnosia_amd runs on a ROCm GPU only: got a tensor on "
+                                 f"{t.device}; there is no CPU fallback")
+
+
+def _f32(t: Optional[Tensor]) -> Optional[Tensor]:
+    return None if t is None else t.to(torch.float32).contiguous()
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# complex diagonal scan (fspin): replaces src/scan_kernel.py:105-148
+@torch.library.custom_op("pragnosia::diag_scan", mutates_args=())
+def diag_scan(u: Tensor, logmag: Tensor, ang: Tensor, h0r: Optional[Tensor],
+              h0i: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """h_t = exp(logmag_t + i ang_t) h_{t-1} + u_t over (B, T, D) fp32. Returns (Re h, Re h_last, Im h_last, Im h);
+    the last output is the saved imaginary part for the backward (not differentiable)."""
+    _require_gpu(u, logmag, ang, h0r, h0i)
+    u, logmag, ang, h0r, h0i = _f32(u), _f32(logmag), _f32(ang), _f32(h0r), _f32(h0i)
+    B, T, D = u.shape
+    hr = torch.empty(B, T, D, device=u.device, dtype=torch.float32)
+    hi = torch.empty_like(hr)
+    check(lib().pragnosia_diag_scan_fwd(_ptr(u), _ptr(logmag), _ptr(ang), _ptr(h0r), _ptr(h0i), _ptr(hr), _ptr(hi),
+                                        B, T, D, _stream(u)), "pragnosia_diag_scan_fwd")
+    return hr, hr[:, -1].clone(), hi[:, -1].clone(), hi
+
+
+@diag_scan.register_fake
+def _(u, logmag, ang, h0r, h0i):
+    B, T, D = u.shape
+    e = lambda *s: u.new_empty(*s, dtype=torch.float32)
+    return e(B, T, D), e(B, D), e(B, D), e(B, T, D)
+
+
+@torch.library.custom_op("pragnosia::diag_scan_bwd", mutates_args=())
+def diag_scan_bwd(g: Tensor, g_last_r: Optional[Tensor], g_last_i: Optional[Tensor], logmag: Tensor, ang: Tensor,
+                  hr: Tensor, hi: Tensor, h0r: Optional[Tensor],
+                  h0i: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The adjoint recurrence. Returns (du, dlogmag, dang, dh0r, dh0i); dh0r/dh0i are empty when h0 was None."""
+    _require_gpu(g, logmag, ang, hr, hi)
+    g, g_last_r, g_last_i = _f32(g), _f32(g_last_r), _f32(g_last_i)
+    logmag, ang, hr, hi, h0r, h0i = _f32(logmag), _f32(ang), _f32(hr), _f32(hi), _f32(h0r), _f32(h0i)
+    B, T, D = g.shape
+    du, dlm, dan = (torch.empty(B, T, D, device=g.device, dtype=torch.float32) for _ in range(3))
+    has = h0r is not None
+    dh0r = torch.empty(B, D, device=g.device) if has else g.new_empty(0)
+    dh0i = torch.empty(B, D, device=g.device) if has else g.new_empty(0)
+    check(lib().pragnosia_diag_scan_bwd(_ptr(g), _ptr(g_last_r), _ptr(g_last_i), _ptr(logmag), _ptr(ang), _ptr(hr),
+                                        _ptr(hi), _ptr(h0r), _ptr(h0i), _ptr(du), _ptr(dlm), _ptr(dan),
+                                        _ptr(dh0r) if has else None, _ptr(dh0i) if has else None,
+                                        B, T, D, _stream(g)), "pragnosia_diag_scan_bwd")
+    return du, dlm, dan, dh0r, dh0i
+
+
+@diag_scan_bwd.register_fake
+def _(g, g_last_r, g_last_i, logmag, ang, hr, hi, h0r, h0i):
+    B, T, D = g.shape
+    e = lambda *s: g.new_empty(*s, dtype=torch.float32)
+    has = h0r is not None
+    return e(B, T, D), e(B, T, D), e(B, T, D), e(B, D) if has else e(0), e(B, D) if has else e(0)
+
+
+def _diag_setup(ctx, inputs, output):
+    u, logmag, ang, h0r, h0i = inputs
+    hr, _, _, hi = output
+    ctx.has_h0 = h0r is not None
+    ctx.save_for_backward(logmag, ang, hr, hi, h0r, h0i)
+    ctx.mark_non_differentiable(hi)
+
+
+def _diag_backward(ctx, gy, glr, gli, _ghi):
+    logmag, ang, hr, hi, h0r, h0i = ctx.saved_tensors
+    if gy is None:
+        gy = torch.zeros_like(hr)
+    du, dlm, dan, dh0r, dh0i = diag_scan_bwd(gy.contiguous(), glr, gli, logmag, ang, hr, hi, h0r, h0i)
+    return du, dlm, dan, (dh0r if ctx.has_h0 else None), (dh0i if ctx.has_h0 else None)
+
+
+diag_scan.register_autograd(_diag_backward, setup_context=_diag_setup)

@@ -1,0 +1,65 @@
+"""CPU checks of the C ABI boundary: the library loads, exports every entry point the header declares, and the
+Python binding declares exactly those; argument rejection happens on the host before any launch; the product
+package never imports the oracle."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    names = []
+    for fn in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if fn.endswith(".h"):
+            txt = open(os.path.join(ROOT, "include", fn)).read()
+            txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+            names += re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(pragnosia_\w+)\s*\(", txt, flags=re.M)
+    return names
+
+
+@pytest.fixture(scope="module")
+def L():
+    from pragnosia_amd._lib import lib
+    return lib()
+
+
+def test_header_declares_functions():
+    assert len(header_functions()) >= 4
+
+
+def test_library_exports_every_declared_symbol(L):
+    for name in header_functions():
+        assert hasattr(L, name), name
+
+
+def test_binding_matches_header():
+    from pragnosia_amd._lib import SIGNATURES
+    assert set(SIGNATURES) == set(header_functions())
+
+
+def test_abi_version_and_error_strings(L):
+    assert L.pragnosia_abi_version() == 1
+    assert L.pragnosia_error_string(0) == b"ok"
+    assert b"invalid argument" in L.pragnosia_error_string(-1)
+
+
+def test_arguments_rejected_before_launch(L):
+    """Shape errors return PRAGNOSIA_ERR_INVALID_ARGUMENT without touching a device."""
+    null = ctypes.c_void_p(0)
+    assert L.pragnosia_diag_scan_fwd(*([null] * 7), 0, 4, 8, null) == -1          # B = 0
+    assert L.pragnosia_diag_scan_fwd(*([null] * 7), 1, 4, -3, null) == -1         # D < 0
+    one = ctypes.c_void_p(16)
+    # h0r given without h0i
+    assert L.pragnosia_diag_scan_fwd(one, one, one, one, null, one, one, 1, 4, 8, null) == -1
+
+
+def test_product_never_imports_oracle():
+    pkg = os.path.join(ROOT, "pragnosia_amd")
+    for dp, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith(".py"):
+                src = open(os.path.join(dp, f)).read()
+                assert not re.search(r"^\s*(from|import)\s+oracle\b", src, flags=re.M), f
