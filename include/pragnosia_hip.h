@@ -48,6 +48,27 @@ int pragnosia_diag_scan_bwd(const float* g, const float* g_last_r, const float* 
                             float* du, float* dlogmag, float* dang, float* dh0r, float* dh0i,
                             int64_t B, int64_t T, int64_t D, void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * Associative carrier (aspin), plain write rule, chunked scan (chunk = 64, head dim D = 64), per (batch, head):
+ *     S_t = exp(la_t) S_{t-1} + k_t v_t^T,   o_t = S_t^T q_t,   S_{-1} = S0 (zero when NULL).
+ * q, k, v: (B, H, T, D) bf16; la: (B, H, T) fp32 (<= 0); S0: (B, H, D, D) fp32, keys on dim 2, or NULL.
+ * Writes o: (B, H, T, D) bf16; S_final: (B, H, D, D) fp32; sent (if non-NULL): the state entering every chunk,
+ * (B, H, ceil(T/64), D, D) bf16 -- required by the backward. T need not be a multiple of 64.
+ * Replaces `assoc_scan_kernel` and the ops under it (`prefix_scan`, `assoc_out`) of src/assoc_kernel.py:128-323.
+ * Returns PRAGNOSIA_ERR_UNSUPPORTED for D != 64 or chunk != 64. */
+int pragnosia_aspin_chunk_fwd(const void* q, const void* k, const void* v, const float* la, const float* S0,
+                              void* o, float* S_final, void* sent,
+                              int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
+
+/* Backward of pragnosia_aspin_chunk_fwd. dO: (B, H, T, D) bf16; dS_final: (B, H, D, D) fp32 or NULL (zero);
+ * sent: the forward's entering states. Writes dq, dk, dv (bf16, (B, H, T, D)), dla (fp32, (B, H, T)) and, if
+ * non-NULL, dS0 (fp32, (B, H, D, D)). Replaces the registered backward of the same ops
+ * (`assoc_out_bwd`, `prefix_scan_bwd` and the glue of src/assoc_kernel.py:146-299). */
+int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const void* v, const float* la, const void* sent,
+                              const void* dO, const float* dS_final,
+                              void* dq, void* dk, void* dv, float* dla, float* dS0,
+                              int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

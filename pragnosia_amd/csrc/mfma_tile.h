@@ -1,0 +1,126 @@
+// Wave-level 16x16 tile algebra on the gfx950 bf16 MFMA (v_mfma_f32_16x16x32_bf16), shared by the aspin kernels.
+//
+// Accumulator (D) layout of a 16x16 fp32 tile, as on every CDNA 16x16 MFMA: lane l = i + 16 g (i = l % 16,
+// g = l / 16) holds column i, rows 4g .. 4g + 3 (element r = row 4g + r).
+//
+// Operands. A (16 x K) and B (K x 16) tiles: lane i + 16 g holds row i of A (column i of B) and 8 values along the
+// contracted index. The pairing of (lane group, element) with k is the same for A and B by construction, so any
+// bijection gives the exact product. This file fixes one: within a 32-wide k block, lane group g holds
+//     k = 4g + {0,1,2,3}  (elements 0..3)   and   k = 16 + 4g + {0,1,2,3}  (elements 4..7).
+// With it, an accumulator tile pair (rows 0..15 and 16..31 of a 32-row block) IS an operand whose contracted index
+// is the tiles' row index: pack(D_lo, D_hi). Operands read from LDS are two 8-byte loads per lane.
+//
+// LDS tiles are row-major bf16 with a pitch of kPitch = 72 elements (144 bytes): the 16 rows an operand read
+// touches start on 16 distinct 4-bank boundaries, so a 64-lane 8-byte read runs at the 2-pass minimum.
+#pragma once
+#include "common.h"
+
+namespace pgn {
+
+constexpr int kPitch = 72;
+
+struct WaveIdx {
+  int w, l, g, i;
+};
+
+PGN_DEVICE WaveIdx wave_idx() {
+  const int tid = threadIdx.x;
+  return WaveIdx{tid >> 6, tid & 63, (tid & 63) >> 4, tid & 15};
+}
+
+PGN_DEVICE f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+PGN_DEVICE bf16x8 cat8(bf16x4 a, bf16x4 b) { return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7); }
+
+// Operand fragment of k block m from row `row` of an LDS tile.
+PGN_DEVICE bf16x8 frag(const __bf16* tile, int row, int m, int g) {
+  const __bf16* p = tile + row * kPitch + 32 * m + 4 * g;
+  return cat8(*reinterpret_cast<const bf16x4*>(p), *reinterpret_cast<const bf16x4*>(p + 16));
+}
+
+PGN_DEVICE bf16x4 to_bf16x4(f32x4 x) {
+  bf16x4 r;
+  r[0] = (__bf16)x[0];
+  r[1] = (__bf16)x[1];
+  r[2] = (__bf16)x[2];
+  r[3] = (__bf16)x[3];
+  return r;
+}
+
+PGN_DEVICE f32x4 to_f32x4(bf16x4 x) { return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]}; }
+
+// Operand from an accumulator tile pair (contracted index = the tiles' row index).
+PGN_DEVICE bf16x8 pack(f32x4 lo, f32x4 hi) { return cat8(to_bf16x4(lo), to_bf16x4(hi)); }
+
+// Fragment scaled by one factor (per lane: the operand's row), rounded back to bf16.
+PGN_DEVICE bf16x8 frag_scaled(const __bf16* tile, int row, int m, int g, float f) {
+  const __bf16* p = tile + row * kPitch + 32 * m + 4 * g;
+  f32x4 a = to_f32x4(*reinterpret_cast<const bf16x4*>(p)) * f;
+  f32x4 b = to_f32x4(*reinterpret_cast<const bf16x4*>(p + 16)) * f;
+  return pack(a, b);
+}
+
+// Fragment scaled per contracted index k by s[k] (fp32 LDS vector), rounded back to bf16.
+PGN_DEVICE bf16x8 frag_scaled_k(const __bf16* tile, int row, int m, int g, const float* s) {
+  const __bf16* p = tile + row * kPitch + 32 * m + 4 * g;
+  const f32x4 sa = *reinterpret_cast<const f32x4*>(s + 32 * m + 4 * g);
+  const f32x4 sb = *reinterpret_cast<const f32x4*>(s + 32 * m + 16 + 4 * g);
+  f32x4 a = to_f32x4(*reinterpret_cast<const bf16x4*>(p)) * sa;
+  f32x4 b = to_f32x4(*reinterpret_cast<const bf16x4*>(p + 16)) * sb;
+  return pack(a, b);
+}
+
+// Store an accumulator tile transposed into an LDS tile: rows 4g..4g+3 of column i land contiguously in row
+// (col0 + i) of `tile`, columns row0 + 4g .. +3 (one 8-byte write).
+PGN_DEVICE void store_T(__bf16* tile, int col0, int row0, int g, int i, f32x4 x) {
+  *reinterpret_cast<bf16x4*>(tile + (col0 + i) * kPitch + row0 + 4 * g) = to_bf16x4(x);
+}
+
+// Store an accumulator tile untransposed: element r to tile[row0 + 4g + r][col0 + i] (four 2-byte writes).
+PGN_DEVICE void store_N(__bf16* tile, int row0, int col0, int g, int i, f32x4 x) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) tile[(row0 + 4 * g + r) * kPitch + col0 + i] = (__bf16)x[r];
+}
+
+// Stage a 64 x 64 bf16 block (rows row0.., 64 contiguous columns, global row stride `ld` elements) into LDS, as-is
+// into `nt` (if non-null) and transposed into `tt` (if non-null). Rows at or beyond `nrows` are zero.
+// 256 threads, two 16-byte global loads each.
+PGN_DEVICE void stage64(const __bf16* __restrict__ src, int ld, int nrows, __bf16* nt, __bf16* tt) {
+#pragma unroll
+  for (int rep = 0; rep < 2; ++rep) {
+    const int idx = threadIdx.x + rep * 256;
+    const int row = idx >> 3, col = (idx & 7) * 8;
+    bf16x8 x;
+    if (row < nrows) {
+      x = *reinterpret_cast<const bf16x8*>(src + (size_t)row * ld + col);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = (__bf16)0.f;
+    }
+    if (nt) *reinterpret_cast<bf16x8*>(nt + row * kPitch + col) = x;
+    if (tt) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tt[(col + e) * kPitch + row] = x[e];
+    }
+  }
+}
+
+// Sum over the 16 lanes of a lane group (same g): butterfly over lane bits 0..3.
+PGN_DEVICE float sum16(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  return x;
+}
+
+// Sum over the 4 lane groups (same i): butterfly over lane bits 4..5.
+PGN_DEVICE float sum_groups(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+PGN_DEVICE float wave_sum(float x) { return sum_groups(sum16(x)); }
+
+}  // namespace pgn

@@ -104,3 +104,84 @@ def _diag_backward(ctx, gy, glr, gli, _ghi):
 
 
 diag_scan.register_autograd(_diag_backward, setup_context=_diag_setup)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# aspin chunked scan, plain rule: replaces assoc_scan_kernel and its ops, src/assoc_kernel.py:128-323
+CHUNK = 64
+
+
+def _bf16(t: Tensor) -> Tensor:
+    return t.to(torch.bfloat16).contiguous()
+
+
+@torch.library.custom_op("pragnosia::aspin_chunk", mutates_args=())
+def aspin_chunk(q: Tensor, k: Tensor, v: Tensor, la: Tensor, S0: Optional[Tensor],
+                want_sent: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """Plain-rule chunked scan. q, k, v (B, H, T, 64) (cast to bf16), la (B, H, T) fp32, S0 (B, H, 64, 64) fp32 or
+    None. Returns (o bf16, S_final fp32, sent bf16 (B, H, NC, 64, 64), or an empty tensor if not wanted)."""
+    _require_gpu(q, k, v, la, S0)
+    q, k, v, la, S0 = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(S0)
+    B, H, T, D = q.shape
+    NC = (T + CHUNK - 1) // CHUNK
+    o = torch.empty(B, H, T, D, device=q.device, dtype=torch.bfloat16)
+    S = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
+    sent = (torch.empty(B, H, NC, D, D, device=q.device, dtype=torch.bfloat16) if want_sent
+            else q.new_empty(0, dtype=torch.bfloat16))
+    check(lib().pragnosia_aspin_chunk_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(S0), _ptr(o), _ptr(S),
+                                          _ptr(sent) if want_sent else None, B, H, T, D, CHUNK, _stream(q)),
+          "pragnosia_aspin_chunk_fwd")
+    return o, S, sent
+
+
+@aspin_chunk.register_fake
+def _(q, k, v, la, S0, want_sent):
+    B, H, T, D = q.shape
+    NC = (T + CHUNK - 1) // CHUNK
+    sent = q.new_empty(B, H, NC, D, D, dtype=torch.bfloat16) if want_sent else q.new_empty(0, dtype=torch.bfloat16)
+    return q.new_empty(B, H, T, D, dtype=torch.bfloat16), q.new_empty(B, H, D, D, dtype=torch.float32), sent
+
+
+@torch.library.custom_op("pragnosia::aspin_chunk_bwd", mutates_args=())
+def aspin_chunk_bwd(q: Tensor, k: Tensor, v: Tensor, la: Tensor, sent: Tensor, do: Tensor,
+                    dS: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Backward of aspin_chunk. Returns (dq, dk, dv bf16, dla fp32, dS0 fp32)."""
+    _require_gpu(q, k, v, la, sent, do, dS)
+    q, k, v, la, sent, do, dS = _bf16(q), _bf16(k), _bf16(v), _f32(la), _bf16(sent), _bf16(do), _f32(dS)
+    B, H, T, D = q.shape
+    dq, dk, dv = (torch.empty(B, H, T, D, device=q.device, dtype=torch.bfloat16) for _ in range(3))
+    dla = torch.empty(B, H, T, device=q.device, dtype=torch.float32)
+    dS0 = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
+    check(lib().pragnosia_aspin_chunk_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(sent), _ptr(do), _ptr(dS),
+                                          _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla), _ptr(dS0),
+                                          B, H, T, D, CHUNK, _stream(q)), "pragnosia_aspin_chunk_bwd")
+    return dq, dk, dv, dla, dS0
+
+
+@aspin_chunk_bwd.register_fake
+def _(q, k, v, la, sent, do, dS):
+    B, H, T, D = q.shape
+    b = lambda *s: q.new_empty(*s, dtype=torch.bfloat16)
+    f = lambda *s: q.new_empty(*s, dtype=torch.float32)
+    return b(B, H, T, D), b(B, H, T, D), b(B, H, T, D), f(B, H, T), f(B, H, D, D)
+
+
+def _aspin_setup(ctx, inputs, output):
+    q, k, v, la, S0, want_sent = inputs
+    _, _, sent = output
+    if sent.numel() == 0 and any(ctx.needs_input_grad[:5]):
+        raise PragnosiaError("aspin_chunk: the backward needs the entering states; call with want_sent=True")
+    ctx.has_s0 = S0 is not None
+    ctx.save_for_backward(q, k, v, la, sent)
+    ctx.mark_non_differentiable(sent)
+
+
+def _aspin_backward(ctx, do, dS, _dsent):
+    q, k, v, la, sent = ctx.saved_tensors
+    if do is None:
+        do = torch.zeros(q.shape, device=q.device, dtype=torch.bfloat16)
+    dq, dk, dv, dla, dS0 = aspin_chunk_bwd(q, k, v, la, sent, do.contiguous(), dS)
+    return dq, dk, dv, dla, (dS0 if ctx.has_s0 else None), None
+
+
+aspin_chunk.register_autograd(_aspin_backward, setup_context=_aspin_setup)
