@@ -7,11 +7,12 @@
 //     S_{c+1} = a S_c + (K o w)^T V
 // (the reference's `_scan_twopass`, `src/assoc.py:118-165`; its GPU form `src/assoc_kernel.py:47-70,188-202`).
 //
-// One workgroup (4 waves) owns one (batch, head) and walks its chunks in order with the fp32 state in registers:
-// wave w holds rows 16w..16w+15 of S (keys) for all 64 value columns, as four accumulator tiles, and the state
-// update is an MFMA accumulating straight onto a*S. Each chunk's Q, K, V tiles are staged in LDS once (K and V also
-// transposed) and every contraction reads its operands from there, so HBM sees each input exactly once:
-// 8 B per (t, d) element forward (q, k, v read, o written) plus the optional bf16 entering states.
+// Forward: two workgroups (4 waves each) per (batch, head), each owning 32 of the 64 value columns (the plain rule
+// is independent per value column), walk the chunks in order with their fp32 state columns in registers: wave w
+// holds key rows 16w..16w+15 as accumulator tiles and the state update is an MFMA accumulating onto a*S. Each chunk's
+// Q, K, V tiles are staged in LDS once (K and V also transposed, through a 4x4 register transpose) from registers
+// loaded during the previous chunk's compute, and every contraction reads its operands from LDS, so HBM sees each
+// input once: 8 B per (t, d) element forward (q, k, v read, o written) plus the optional bf16 entering states.
 //
 // The backward walks the chunks in reverse with dS (the gradient on the state leaving the chunk) in registers and
 // the entering states S_c read back from the forward's bf16 copies. Per chunk, with dA = dO V^T, dP = dA o dec,
@@ -33,66 +34,95 @@ constexpr int C = 64;
 constexpr int DK = 64;
 constexpr int TILE = 64 * kPitch;  // one staged 64 x 64 tile
 
-// L, exp(L), exp(L_C - L) of the chunk starting at t0, into LDS (one wave, lane = token).
-PGN_DEVICE void chunk_decays(const float* __restrict__ la_bh, int t0, int T, int l, float* Ls, float* eLs,
-                             float* ws) {
-  float x = (t0 + l < T) ? la_bh[t0 + l] : 0.f;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float y = __shfl_up(x, off);
-    if (l >= off) x += y;
-  }
-  const float LC = __shfl(x, 63);
-  Ls[l] = x;
-  eLs[l] = __expf(x);
-  ws[l] = __expf(fminf(LC - x, 0.f));
+constexpr int FBV = 32;         // value columns per forward workgroup
+constexpr int FNB = DK / FBV;   // forward workgroups per (batch, head)
+
+// Forward block -> (batch-head, value block). The FNB workgroups of one head are 8 apart in launch order, and the
+// dispatcher deals workgroups round-robin over the 8 XCDs, so they run on the same XCD and the second one's reads
+// of Q and K hit in that XCD's L2.
+PGN_DEVICE void fwd_block(int& bh, int& jb) {
+  const int x = blockIdx.x;
+  const int grp = x / (8 * FNB), rem = x - grp * (8 * FNB);
+  jb = rem >> 3;
+  bh = grp * 8 + (rem & 7);
 }
 
 __global__ __launch_bounds__(256) void aspin_plain_fwd(const __bf16* __restrict__ q, const __bf16* __restrict__ k,
                                                        const __bf16* __restrict__ v, const float* __restrict__ la,
                                                        const float* __restrict__ S0, __bf16* __restrict__ o,
                                                        float* __restrict__ Sfin, __bf16* __restrict__ sent, int T,
-                                                       int NC) {
-  __shared__ __align__(16) __bf16 Qs[TILE], Ks[TILE], KT[TILE], VT[TILE], ST[TILE];
+                                                       int NC, int nbh) {
+  __shared__ __align__(16) __bf16 Qs[TILE], Ks[TILE], KT[TILE], VT[FBV * kPitch], ST[FBV * kPitch];
   __shared__ __align__(16) float Ls[C], eLs[C], ws[C];
 
+  int bh, jb;
+  fwd_block(bh, jb);
+  if (bh >= nbh) return;
   const WaveIdx x = wave_idx();
-  const int w = x.w, g = x.g, i = x.i;
-  const int bh = blockIdx.x;
+  const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
+  const int j0 = jb * FBV;  // first value column owned here
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
 
-  // state rows 16w + 4g + r, column 16 jt + i
-  f32x4 S[4];
+  // state rows 16w + 4g + r, columns j0 + 16 jt + i
+  f32x4 S[2];
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt) {
+  for (int jt = 0; jt < 2; ++jt) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) S[jt][r] = S0 ? S0[soff + (16 * w + 4 * g + r) * DK + 16 * jt + i] : 0.f;
+    for (int r = 0; r < 4; ++r) S[jt][r] = S0 ? S0[soff + (16 * w + 4 * g + r) * DK + j0 + 16 * jt + i] : 0.f;
     store_T(ST, 16 * jt, 16 * w, g, i, S[jt]);
   }
+
+  // this thread's 4x4 staging blocks: Q, K (64 x 64, all threads), V (64 x 32, threads < 128)
+  const int br = 4 * (tid >> 4), bc = 4 * (tid & 15);
+  const int vr = 4 * (tid >> 3), vc = 4 * (tid & 7);
+  const bool vthr = tid < 128;
+  Blk4 pq = load_blk(q + boff, DK, min(C, T), tid);
+  Blk4 pk = load_blk(k + boff, DK, min(C, T), tid);
+  Blk4 pv;
+  if (vthr) pv = load_blk_w(v + boff + j0, DK, min(C, T), FBV, tid);
+  float pla = (w == 0 && x.l < T) ? la[(size_t)bh * T + x.l] : 0.f;
 
   const int tq = 16 * w + i;  // this lane's token within the chunk for t-indexed operands
   for (int c = 0; c < NC; ++c) {
     const int t0 = c * C;
-    const int nrows = min(C, T - t0);
-    stage64(q + boff + (size_t)t0 * DK, DK, nrows, Qs, nullptr);
-    stage64(k + boff + (size_t)t0 * DK, DK, nrows, Ks, KT);
-    stage64(v + boff + (size_t)t0 * DK, DK, nrows, nullptr, VT);
-    if (w == 0) chunk_decays(la + (size_t)bh * T, t0, T, x.l, Ls, eLs, ws);
+    // publish chunk c (prefetched) to LDS
+    put_blk(Qs, pq, br, bc);
+    put_blk(Ks, pk, br, bc);
+    put_blk_T(KT, pk, br, bc);
+    if (vthr) put_blk_T(VT, pv, vr, vc);
+    if (w == 0) {
+      float L = pla;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(L, off);
+        if (x.l >= off) L += y;
+      }
+      const float LC = __shfl(L, 63);
+      Ls[x.l] = L;
+      eLs[x.l] = __expf(L);
+      ws[x.l] = __expf(fminf(LC - L, 0.f));
+    }
     __syncthreads();
+    // prefetch chunk c + 1 while this one computes
+    if (c + 1 < NC) {
+      const int n0 = t0 + C, nr = min(C, T - n0);
+      pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, tid);
+      pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, tid);
+      if (vthr) pv = load_blk_w(v + boff + (size_t)n0 * DK + j0, DK, nr, FBV, tid);
+      if (w == 0) pla = (n0 + x.l < T) ? la[(size_t)bh * T + n0 + x.l] : 0.f;
+    }
 
     // (Q K^T)^T tiles (s block sb, t block w), decayed and masked: lane holds column t = tq, rows s.
-    bf16x8 qf[2];
-    qf[0] = frag(Qs, tq, 0, g);
-    qf[1] = frag(Qs, tq, 1, g);
+    const bf16x8 qf0 = frag(Qs, tq, 0, g), qf1 = frag(Qs, tq, 1, g);
     const float Lt = Ls[tq];
     f32x4 pt[4];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       pt[sb] = zero4();
       if (sb <= w) {
-        pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf[0], pt[sb]);
-        pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf[1], pt[sb]);
+        pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
+        pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
         const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -107,49 +137,54 @@ __global__ __launch_bounds__(256) void aspin_plain_fwd(const __bf16* __restrict_
     const bf16x8 qe0 = frag_scaled(Qs, tq, 0, g, eLt);
     const bf16x8 qe1 = frag_scaled(Qs, tq, 1, g, eLt);
 
-    // O^T tiles (j block jt, t block w) = V^T A^T + S^T (Q o eL)^T; lane holds token tq, values 16jt+4g..+3
+    // O^T tiles (value block jt, t block w) = V^T A^T + S^T (Q o eL)^T; lane holds token tq, 4 value columns
     const bool t_ok = t0 + tq < T;
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
+    for (int jt = 0; jt < 2; ++jt) {
       f32x4 acc = zero4();
       acc = pgn_mfma(frag(VT, 16 * jt + i, 0, g), af0, acc);
       if (w >= 2) acc = pgn_mfma(frag(VT, 16 * jt + i, 1, g), af1, acc);
       acc = pgn_mfma(frag(ST, 16 * jt + i, 0, g), qe0, acc);
       acc = pgn_mfma(frag(ST, 16 * jt + i, 1, g), qe1, acc);
-      if (t_ok) *reinterpret_cast<bf16x4*>(o + boff + (size_t)(t0 + tq) * DK + 16 * jt + 4 * g) = to_bf16x4(acc);
+      if (t_ok)
+        *reinterpret_cast<bf16x4*>(o + boff + (size_t)(t0 + tq) * DK + j0 + 16 * jt + 4 * g) = to_bf16x4(acc);
     }
 
     // the entering state, bf16, (d, j) layout
     if (sent) {
       __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
+      for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[(16 * w + 4 * g + r) * DK + 16 * jt + i] = (__bf16)S[jt][r];
+        for (int r = 0; r < 4; ++r) sc[(16 * w + 4 * g + r) * DK + j0 + 16 * jt + i] = (__bf16)S[jt][r];
     }
 
-    // S <- a S + (K o w)^T V, rows 16w.. of S
+    // S <- a S + (K o w)^T V on this workgroup's columns, rows 16w.. of S
     const float a_c = __expf(Ls[C - 1]);
     const bf16x8 kw0 = frag_scaled_k(KT, 16 * w + i, 0, g, ws);
     const bf16x8 kw1 = frag_scaled_k(KT, 16 * w + i, 1, g, ws);
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
+    for (int jt = 0; jt < 2; ++jt) {
       S[jt] = S[jt] * a_c;
       S[jt] = pgn_mfma(kw0, frag(VT, 16 * jt + i, 0, g), S[jt]);
       S[jt] = pgn_mfma(kw1, frag(VT, 16 * jt + i, 1, g), S[jt]);
     }
     __syncthreads();
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) store_T(ST, 16 * jt, 16 * w, g, i, S[jt]);
+    for (int jt = 0; jt < 2; ++jt) store_T(ST, 16 * jt, 16 * w, g, i, S[jt]);
   }
 
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
+  for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) Sfin[soff + (16 * w + 4 * g + r) * DK + 16 * jt + i] = S[jt][r];
+    for (int r = 0; r < 4; ++r) Sfin[soff + (16 * w + 4 * g + r) * DK + j0 + 16 * jt + i] = S[jt][r];
 }
 
-__global__ __launch_bounds__(256) void aspin_plain_bwd(
+// Backward: 8 waves per (batch, head). Waves 0-3 (group D) own t block wl = w & 3 and compute everything that does
+// not depend on dS: dQ, the row sums of dA o A and q_t.(S_c dO_t). Waves 4-7 (group K) own s block wl and d block wl
+// and carry dS: dV, dK, the column sums of dA o A, k_s.(dS v_s), <S_c, dS> and the dS update. Waves w and w + 4 share
+// a SIMD, and the two groups' MFMA counts per SIMD are within 10% of each other.
+__global__ __launch_bounds__(512) void aspin_plain_bwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const __bf16* __restrict__ sent, const __bf16* __restrict__ dO,
     const float* __restrict__ dSfin, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
@@ -160,183 +195,222 @@ __global__ __launch_bounds__(256) void aspin_plain_bwd(
   __bf16* Ks = QT + TILE;
   __bf16* KT = Ks + TILE;
   __bf16* Vs = KT + TILE;
-  __bf16* VT = Vs + TILE;
-  __bf16* Os = VT + TILE;   // dO
-  __bf16* OT = Os + TILE;   // dO^T
-  __bf16* Ss = OT + TILE;   // S_c, (d, j)
-  __bf16* dSs = Ss + TILE;  // dS, (d, j)
-  __bf16* dST = dSs + TILE; // dS^T, (j, d)
+  __bf16* Os = Vs + TILE;    // dO
+  __bf16* OT = Os + TILE;    // dO^T
+  __bf16* Ss = OT + TILE;    // S_c, (d, j)
+  __bf16* dSs = Ss + TILE;   // dS, (d, j)
+  __bf16* dST = dSs + TILE;  // dS^T, (j, d)
   float* Ls = reinterpret_cast<float*>(dST + TILE);
   float* eLs = Ls + C;
   float* ws = eLs + C;
-  float* rowpart = ws + C;     // [4][C]: row sums of dA o A per s block (wave)
-  float* colM = rowpart + 4 * C;  // [C]
-  float* qz = colM + C;        // [C]: q_t . (S_c dO_t)
-  float* dwv = qz + C;         // [C]: k_s . (dS v_s)
-  float* sdot = dwv + C;       // [4]: per-wave <S_c, dS>
+  float* rowM = ws + C;   // row sums of dA o A (group D)
+  float* colM = rowM + C; // column sums of dA o A (group K)
+  float* qz = colM + C;   // q_t . (S_c dO_t)
+  float* dwv = qz + C;    // k_s . (dS v_s)
+  float* sdot = dwv + C;  // per-wave <S_c, dS>
 
   const WaveIdx x = wave_idx();
-  const int w = x.w, g = x.g, i = x.i;
+  const int w = x.w, wl = w & 3, g = x.g, i = x.i, tid = threadIdx.x;
+  const bool gk = w >= 4;
   const int bh = blockIdx.x;
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
 
-  // dS rows 16w + 4g + r, column 16 jt + i
+  // group K: dS rows 16wl + 4g + r, column 16 jt + i
   f32x4 dS[4];
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt) {
+  for (int jt = 0; jt < 4; ++jt) dS[jt] = zero4();
+  if (gk) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) dS[jt][r] = dSfin ? dSfin[soff + (16 * w + 4 * g + r) * DK + 16 * jt + i] : 0.f;
-    store_T(dST, 16 * jt, 16 * w, g, i, dS[jt]);
-    store_N(dSs, 16 * w, 16 * jt, g, i, dS[jt]);
+    for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        dS[jt][r] = dSfin ? dSfin[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] : 0.f;
+      store_T(dST, 16 * jt, 16 * wl, g, i, dS[jt]);
+      store_N(dSs, 16 * wl, 16 * jt, g, i, dS[jt]);
+    }
   }
 
-  const int sw = 16 * w + i;  // this lane's s (column) for s-indexed tiles, and t for t-indexed ones
+  // staging: threads 0-255 carry Q, V and S_c; threads 256-511 carry K and dO (one 4x4 block of each)
+  const int b = tid & 255;
+  const int br = 4 * (b >> 4), bc = 4 * (b & 15);
+  const bool lo = tid < 256;
+  Blk4 p1, p2, p3;
+  {
+    const int t0 = (NC - 1) * C, nr = min(C, T - t0);
+    if (lo) {
+      p1 = load_blk(q + boff + (size_t)t0 * DK, DK, nr, b);
+      p2 = load_blk(v + boff + (size_t)t0 * DK, DK, nr, b);
+      p3 = load_blk(sent + ((size_t)bh * NC + NC - 1) * DK * DK, DK, DK, b);
+    } else {
+      p1 = load_blk(k + boff + (size_t)t0 * DK, DK, nr, b);
+      p2 = load_blk(dO + boff + (size_t)t0 * DK, DK, nr, b);
+    }
+  }
+  float pla = (w == 0 && (NC - 1) * C + x.l < T) ? la[(size_t)bh * T + (NC - 1) * C + x.l] : 0.f;
+
+  const int me = 16 * wl + i;  // group D: this lane's t; group K: this lane's s
   for (int cc = NC - 1; cc >= 0; --cc) {
     const int t0 = cc * C;
-    const int nrows = min(C, T - t0);
-    stage64(q + boff + (size_t)t0 * DK, DK, nrows, Qs, QT);
-    stage64(k + boff + (size_t)t0 * DK, DK, nrows, Ks, KT);
-    stage64(v + boff + (size_t)t0 * DK, DK, nrows, Vs, VT);
-    stage64(dO + boff + (size_t)t0 * DK, DK, nrows, Os, OT);
-    stage64(sent + ((size_t)bh * NC + cc) * DK * DK, DK, DK, Ss, nullptr);
-    if (w == 0) chunk_decays(la + (size_t)bh * T, t0, T, x.l, Ls, eLs, ws);
+    if (lo) {
+      put_blk(Qs, p1, br, bc);
+      put_blk_T(QT, p1, br, bc);
+      put_blk(Vs, p2, br, bc);
+      put_blk(Ss, p3, br, bc);
+    } else {
+      put_blk(Ks, p1, br, bc);
+      put_blk_T(KT, p1, br, bc);
+      put_blk(Os, p2, br, bc);
+      put_blk_T(OT, p2, br, bc);
+    }
+    if (w == 0) {
+      float L = pla;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(L, off);
+        if (x.l >= off) L += y;
+      }
+      const float LC = __shfl(L, 63);
+      Ls[x.l] = L;
+      eLs[x.l] = __expf(L);
+      ws[x.l] = __expf(fminf(LC - L, 0.f));
+    }
     __syncthreads();
+    if (cc > 0) {
+      const int n0 = t0 - C;  // full chunk
+      if (lo) {
+        p1 = load_blk(q + boff + (size_t)n0 * DK, DK, C, b);
+        p2 = load_blk(v + boff + (size_t)n0 * DK, DK, C, b);
+        p3 = load_blk(sent + ((size_t)bh * NC + cc - 1) * DK * DK, DK, DK, b);
+      } else {
+        p1 = load_blk(k + boff + (size_t)n0 * DK, DK, C, b);
+        p2 = load_blk(dO + boff + (size_t)n0 * DK, DK, C, b);
+      }
+      if (w == 0) pla = la[(size_t)bh * T + n0 + x.l];
+    }
     const float a_c = __expf(Ls[C - 1]);
 
-    // (1) A and dP tiles (t block tb >= w, s block w): lane holds column s = sw, rows t = 16tb + 4g + r
-    f32x4 At[4], dPt[4];
-    const float Ls_s = Ls[sw];
-    const bf16x8 kf0 = frag(Ks, sw, 0, g), kf1 = frag(Ks, sw, 1, g);
-    const bf16x8 vf0 = frag(Vs, sw, 0, g), vf1 = frag(Vs, sw, 1, g);
-    float colsum = 0.f;
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      At[tb] = zero4();
-      dPt[tb] = zero4();
-      float rows[4] = {0.f, 0.f, 0.f, 0.f};
-      if (tb >= w) {
-        f32x4 P = zero4(), dA = zero4();
-        P = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, P);
-        P = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, P);
-        dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), vf0, dA);
-        dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), vf1, dA);
-        const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * tb + 4 * g + r;
-          const float dec = (t >= sw) ? __expf(fminf(Ltv[r] - Ls_s, 0.f)) : 0.f;
-          At[tb][r] = P[r] * dec;
-          dPt[tb][r] = dA[r] * dec;
-          const float m = dA[r] * At[tb][r];
-          colsum += m;
-          rows[r] = m;
-        }
-      }
-      // row sums of this s block for rows t = 16tb + 4g + r
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float s16 = sum16(rows[r]);
-        if (i == 0) rowpart[w * C + 16 * tb + 4 * g + r] = s16;
-      }
-    }
-    colsum = sum_groups(colsum);
-    if (g == 0) colM[sw] = colsum;
-    const bf16x8 A0 = pack(At[0], At[1]), A1 = pack(At[2], At[3]);
-    const bf16x8 dP0 = pack(dPt[0], dPt[1]), dP1 = pack(dPt[2], dPt[3]);
-    const float w_s = ws[sw];
-
-    // (2) dV^T tiles (j block jt, s block w) = dO^T A + w_s dS^T K^T
-    const bool s_ok = t0 + sw < T;
-    {
-      const bf16x8 kw0 = frag_scaled(Ks, sw, 0, g, w_s), kw1 = frag_scaled(Ks, sw, 1, g, w_s);
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        f32x4 acc = zero4();
-        acc = pgn_mfma(frag(OT, 16 * jt + i, 0, g), A0, acc);
-        acc = pgn_mfma(frag(OT, 16 * jt + i, 1, g), A1, acc);
-        acc = pgn_mfma(frag(dST, 16 * jt + i, 0, g), kw0, acc);
-        acc = pgn_mfma(frag(dST, 16 * jt + i, 1, g), kw1, acc);
-        if (s_ok) *reinterpret_cast<bf16x4*>(dv + boff + (size_t)(t0 + sw) * DK + 16 * jt + 4 * g) = to_bf16x4(acc);
-      }
-    }
-    // (3) dK^T tiles (d block dt, s block w) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
-    {
-      float dw_s = 0.f;
-      const __bf16* krow = Ks + sw * kPitch;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        f32x4 acc = zero4(), Y = zero4();
-        acc = pgn_mfma(frag(QT, 16 * dt + i, 0, g), dP0, acc);
-        acc = pgn_mfma(frag(QT, 16 * dt + i, 1, g), dP1, acc);
-        Y = pgn_mfma(frag(dSs, 16 * dt + i, 0, g), vf0, Y);
-        Y = pgn_mfma(frag(dSs, 16 * dt + i, 1, g), vf1, Y);
-        const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dw_s += kk[r] * Y[r];
-        acc = acc + Y * w_s;
-        if (s_ok) *reinterpret_cast<bf16x4*>(dk + boff + (size_t)(t0 + sw) * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
-      }
-      dw_s = sum_groups(dw_s);
-      if (g == 0) dwv[sw] = dw_s;
-    }
-    // (4) dP^T tiles (s block sb <= w, t block w): lane holds column t = sw, rows s
-    f32x4 dPT[4];
-    {
-      const float Lt = Ls[sw];
-      const bf16x8 of0 = frag(Os, sw, 0, g), of1 = frag(Os, sw, 1, g);
+    if (!gk) {
+      // ---------------- group D: t = me
+      const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
+      const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
+      const float Lt = Ls[me];
+      float rowacc = 0.f;
+      f32x4 dPT[4];
 #pragma unroll
       for (int sb = 0; sb < 4; ++sb) {
         dPT[sb] = zero4();
-        if (sb <= w) {
-          dPT[sb] = pgn_mfma(frag(Vs, 16 * sb + i, 0, g), of0, dPT[sb]);
-          dPT[sb] = pgn_mfma(frag(Vs, 16 * sb + i, 1, g), of1, dPT[sb]);
+        if (sb <= wl) {
+          f32x4 PT = zero4(), dAT = zero4();
+          PT = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, PT);
+          PT = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, PT);
+          dAT = pgn_mfma(frag(Vs, 16 * sb + i, 0, g), of0, dAT);
+          dAT = pgn_mfma(frag(Vs, 16 * sb + i, 1, g), of1, dAT);
           const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int s = 16 * sb + 4 * g + r;
-            dPT[sb][r] = (s <= sw) ? dPT[sb][r] * __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+            const float dec = (s <= me) ? __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+            rowacc += dAT[r] * (PT[r] * dec);
+            dPT[sb][r] = dAT[r] * dec;
           }
         }
       }
-    }
-    // (5) dQ^T tiles (d block dt, t block w) = K^T dP^T + eL_t (S_c dO^T); q_t.(S_c dO_t) on the way
-    {
+      rowacc = sum_groups(rowacc);
+      if (g == 0) rowM[me] = rowacc;
       const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
-      const bf16x8 of0 = frag(Os, sw, 0, g), of1 = frag(Os, sw, 1, g);
-      const float eLt = eLs[sw];
-      const __bf16* qrow = Qs + sw * kPitch;
+      const float eLt = eLs[me];
+      const __bf16* qrow = Qs + me * kPitch;
+      const bool t_ok = t0 + me < T;
       float qzt = 0.f;
-      const bool t_ok = t0 + sw < T;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         f32x4 acc = zero4(), Z = zero4();
         acc = pgn_mfma(frag(KT, 16 * dt + i, 0, g), b0, acc);
-        acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), b1, acc);
+        if (wl >= 2) acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), b1, acc);
         Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
         Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
         const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
 #pragma unroll
         for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
         acc = acc + Z * eLt;
-        if (t_ok) *reinterpret_cast<bf16x4*>(dq + boff + (size_t)(t0 + sw) * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
+        if (t_ok) *reinterpret_cast<bf16x4*>(dq + boff + (size_t)(t0 + me) * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
       }
       qzt = sum_groups(qzt);
-      if (g == 0) qz[sw] = qzt;
-    }
-    // (6) <S_c, dS> over this wave's rows of dS
-    {
+      if (g == 0) qz[me] = qzt;
+    } else {
+      // ---------------- group K: s = me, d block wl
+      const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
+      const bf16x8 vf0 = frag(Vs, me, 0, g), vf1 = frag(Vs, me, 1, g);
+      const float Ls_s = Ls[me];
+      float colacc = 0.f;
+      f32x4 At[4], dPt[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        At[tb] = zero4();
+        dPt[tb] = zero4();
+        if (tb >= wl) {
+          f32x4 P = zero4(), dA = zero4();
+          P = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, P);
+          P = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, P);
+          dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), vf0, dA);
+          dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), vf1, dA);
+          const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tb + 4 * g + r;
+            const float dec = (t >= me) ? __expf(fminf(Ltv[r] - Ls_s, 0.f)) : 0.f;
+            At[tb][r] = P[r] * dec;
+            dPt[tb][r] = dA[r] * dec;
+            colacc += dA[r] * At[tb][r];
+          }
+        }
+      }
+      colacc = sum_groups(colacc);
+      if (g == 0) colM[me] = colacc;
+      const bf16x8 A0 = pack(At[0], At[1]), A1 = pack(At[2], At[3]);
+      const bf16x8 dP0 = pack(dPt[0], dPt[1]), dP1 = pack(dPt[2], dPt[3]);
+      const float w_s = ws[me];
+      const bool s_ok = t0 + me < T;
+      // dV^T tiles (j block jt, s block wl) = dO^T A + dS^T (K o w)^T
+      const bf16x8 kw0 = frag_scaled(Ks, me, 0, g, w_s), kw1 = frag_scaled(Ks, me, 1, g, w_s);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        f32x4 acc = zero4();
+        if (wl < 2) acc = pgn_mfma(frag(OT, 16 * jt + i, 0, g), A0, acc);
+        acc = pgn_mfma(frag(OT, 16 * jt + i, 1, g), A1, acc);
+        acc = pgn_mfma(frag(dST, 16 * jt + i, 0, g), kw0, acc);
+        acc = pgn_mfma(frag(dST, 16 * jt + i, 1, g), kw1, acc);
+        if (s_ok) *reinterpret_cast<bf16x4*>(dv + boff + (size_t)(t0 + me) * DK + 16 * jt + 4 * g) = to_bf16x4(acc);
+      }
+      // dK^T tiles (d block dt, s block wl) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
+      const __bf16* krow = Ks + me * kPitch;
+      float dw = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        f32x4 acc = zero4(), Y = zero4();
+        if (wl < 2) acc = pgn_mfma(frag(QT, 16 * dt + i, 0, g), dP0, acc);
+        acc = pgn_mfma(frag(QT, 16 * dt + i, 1, g), dP1, acc);
+        Y = pgn_mfma(frag(dSs, 16 * dt + i, 0, g), vf0, Y);
+        Y = pgn_mfma(frag(dSs, 16 * dt + i, 1, g), vf1, Y);
+        const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
+        acc = acc + Y * w_s;
+        if (s_ok) *reinterpret_cast<bf16x4*>(dk + boff + (size_t)(t0 + me) * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
+      }
+      dw = sum_groups(dw);
+      if (g == 0) dwv[me] = dw;
+      // <S_c, dS> over this wave's rows of dS
       float sd = 0.f;
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * w + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
+        for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * wl + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
       sd = wave_sum(sd);
-      if (x.l == 0) sdot[w] = sd;
-    }
-    // (7) dS <- a dS + (Q o eL)^T dO, rows 16w.. of dS
-    {
-      const bf16x8 qe0 = frag_scaled_k(QT, 16 * w + i, 0, g, eLs), qe1 = frag_scaled_k(QT, 16 * w + i, 1, g, eLs);
+      if (x.l == 0) sdot[wl] = sd;
+      // dS <- a dS + (Q o eL)^T dO, rows 16wl.. of dS
+      const bf16x8 qe0 = frag_scaled_k(QT, 16 * wl + i, 0, g, eLs), qe1 = frag_scaled_k(QT, 16 * wl + i, 1, g, eLs);
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
         dS[jt] = dS[jt] * a_c;
@@ -345,14 +419,18 @@ __global__ __launch_bounds__(256) void aspin_plain_bwd(
       }
     }
     __syncthreads();
-    // (8) dla for this chunk (wave 0), while the others publish the new dS
-    if (w == 0) {
+    if (gk) {
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        store_T(dST, 16 * jt, 16 * wl, g, i, dS[jt]);
+        store_N(dSs, 16 * wl, 16 * jt, g, i, dS[jt]);
+      }
+    } else if (w == 0) {
+      // dla for this chunk: the reverse cumulative sum of dL
       const int t = x.l;
-      float dL = rowpart[t] + rowpart[C + t] + rowpart[2 * C + t] + rowpart[3 * C + t] - colM[t] +
-                 eLs[t] * qz[t] - ws[t] * dwv[t];
+      float dL = rowM[t] - colM[t] + eLs[t] * qz[t] - ws[t] * dwv[t];
       const float wdw = wave_sum(ws[t] * dwv[t]);
       if (t == C - 1) dL += wdw + a_c * (sdot[0] + sdot[1] + sdot[2] + sdot[3]);
-      // reverse inclusive cumulative sum over the chunk
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const float y = __shfl_down(dL, off);
@@ -360,22 +438,17 @@ __global__ __launch_bounds__(256) void aspin_plain_bwd(
       }
       if (t0 + t < T) dla[(size_t)bh * T + t0 + t] = dL;
     }
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      store_T(dST, 16 * jt, 16 * w, g, i, dS[jt]);
-      store_N(dSs, 16 * w, 16 * jt, g, i, dS[jt]);
-    }
     __syncthreads();
   }
-  if (dS0) {
+  if (gk && dS0) {
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dS0[soff + (16 * w + 4 * g + r) * DK + 16 * jt + i] = dS[jt][r];
+      for (int r = 0; r < 4; ++r) dS0[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] = dS[jt][r];
   }
 }
 
-constexpr size_t kBwdSmem = 11 * TILE * sizeof(__bf16) + (3 * C + 4 * C + 3 * C + 4) * sizeof(float);
+constexpr size_t kBwdSmem = 10 * TILE * sizeof(__bf16) + (7 * C + 4) * sizeof(float);
 
 bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
   if (B <= 0 || H <= 0 || T <= 0) return false;
@@ -392,9 +465,11 @@ extern "C" int pragnosia_aspin_chunk_fwd(const void* q, const void* k, const voi
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
   PGN_CHECK_ARG(q && k && v && la && o && S_final);
   const int NC = (int)((T + C - 1) / C);
-  hipLaunchKernelGGL(aspin_plain_fwd, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream,
-                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, S0, (__bf16*)o, S_final,
-                     (__bf16*)sent, (int)T, NC);
+  const int nbh = (int)(B * H);
+  const unsigned grid = (unsigned)(((nbh + 7) / 8) * 8 * FNB);
+  hipLaunchKernelGGL(aspin_plain_fwd, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const __bf16*)q,
+                     (const __bf16*)k, (const __bf16*)v, la, S0, (__bf16*)o, S_final, (__bf16*)sent, (int)T, NC,
+                     nbh);
   PGN_RETURN_LAUNCH();
 }
 
@@ -413,7 +488,7 @@ extern "C" int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const voi
     attr_set = true;
   }
   const int NC = (int)((T + C - 1) / C);
-  hipLaunchKernelGGL(aspin_plain_bwd, dim3((unsigned)(B * H)), dim3(256), kBwdSmem, (hipStream_t)stream,
+  hipLaunchKernelGGL(aspin_plain_bwd, dim3((unsigned)(B * H)), dim3(512), kBwdSmem, (hipStream_t)stream,
                      (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent,
                      (const __bf16*)dO, dS_final, (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, dla, dS0, (int)T, NC);
   PGN_RETURN_LAUNCH();

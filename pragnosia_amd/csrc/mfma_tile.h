@@ -10,14 +10,15 @@
 // With it, an accumulator tile pair (rows 0..15 and 16..31 of a 32-row block) IS an operand whose contracted index
 // is the tiles' row index: pack(D_lo, D_hi). Operands read from LDS are two 8-byte loads per lane.
 //
-// LDS tiles are row-major bf16 with a pitch of kPitch = 72 elements (144 bytes): the 16 rows an operand read
-// touches start on 16 distinct 4-bank boundaries, so a 64-lane 8-byte read runs at the 2-pass minimum.
+// LDS tiles are row-major bf16 with a pitch of kPitch = 68 elements (136 bytes, 34 banks): the 16 rows an
+// operand read touches start on 16 distinct even banks, and the transposed 4x4-block writes of the staging below
+// spread over all 64 banks, so both run at (or within one bank of) the 2-pass minimum of a 64-lane 8-byte access.
 #pragma once
 #include "common.h"
 
 namespace pgn {
 
-constexpr int kPitch = 72;
+constexpr int kPitch = 68;
 
 struct WaveIdx {
   int w, l, g, i;
@@ -82,26 +83,54 @@ PGN_DEVICE void store_N(__bf16* tile, int row0, int col0, int g, int i, f32x4 x)
   for (int r = 0; r < 4; ++r) tile[(row0 + 4 * g + r) * kPitch + col0 + i] = (__bf16)x[r];
 }
 
-// Stage a 64 x 64 bf16 block (rows row0.., 64 contiguous columns, global row stride `ld` elements) into LDS, as-is
-// into `nt` (if non-null) and transposed into `tt` (if non-null). Rows at or beyond `nrows` are zero.
-// 256 threads, two 16-byte global loads each.
-PGN_DEVICE void stage64(const __bf16* __restrict__ src, int ld, int nrows, __bf16* nt, __bf16* tt) {
+// Staging of 64-row bf16 blocks through registers. A thread owns a 4 x 4 sub-block (rows 4*(b/16).., columns
+// 4*(b%16).. for block index b): each of its four 8-byte global loads is part of a 128-byte row segment read by 16
+// consecutive lanes, and the transposed copy is a 4 x 4 register transpose followed by four 8-byte LDS writes.
+struct Blk4 {
+  bf16x4 r[4];
+};
+
+PGN_DEVICE bf16x4 zero_bf16x4() {
+  bf16x4 z;
+  z[0] = z[1] = z[2] = z[3] = (__bf16)0.f;
+  return z;
+}
+
+// Load block b of a (rows x 64-wide) region starting at src (row stride ld elements); rows >= nrows read as zero.
+PGN_DEVICE Blk4 load_blk(const __bf16* __restrict__ src, int ld, int nrows, int b) {
+  const int r0 = 4 * (b >> 4), c0 = 4 * (b & 15);
+  Blk4 x;
 #pragma unroll
-  for (int rep = 0; rep < 2; ++rep) {
-    const int idx = threadIdx.x + rep * 256;
-    const int row = idx >> 3, col = (idx & 7) * 8;
-    bf16x8 x;
-    if (row < nrows) {
-      x = *reinterpret_cast<const bf16x8*>(src + (size_t)row * ld + col);
-    } else {
+  for (int j = 0; j < 4; ++j)
+    x.r[j] = (r0 + j < nrows) ? *reinterpret_cast<const bf16x4*>(src + (size_t)(r0 + j) * ld + c0) : zero_bf16x4();
+  return x;
+}
+
+// The same for a region only `ncols` (multiple of 4) wide: block b covers rows 4*(b / (ncols/4)).. .
+PGN_DEVICE Blk4 load_blk_w(const __bf16* __restrict__ src, int ld, int nrows, int ncols, int b) {
+  const int per_row = ncols >> 2;
+  const int r0 = 4 * (b / per_row), c0 = 4 * (b % per_row);
+  Blk4 x;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = (__bf16)0.f;
-    }
-    if (nt) *reinterpret_cast<bf16x8*>(nt + row * kPitch + col) = x;
-    if (tt) {
+  for (int j = 0; j < 4; ++j)
+    x.r[j] = (r0 + j < nrows) ? *reinterpret_cast<const bf16x4*>(src + (size_t)(r0 + j) * ld + c0) : zero_bf16x4();
+  return x;
+}
+
+PGN_DEVICE void put_blk(__bf16* tile, const Blk4& x, int r0, int c0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) tt[(col + e) * kPitch + row] = x[e];
-    }
+  for (int j = 0; j < 4; ++j) *reinterpret_cast<bf16x4*>(tile + (r0 + j) * kPitch + c0) = x.r[j];
+}
+
+PGN_DEVICE void put_blk_T(__bf16* tile, const Blk4& x, int r0, int c0) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bf16x4 col;
+    col[0] = x.r[0][j];
+    col[1] = x.r[1][j];
+    col[2] = x.r[2][j];
+    col[3] = x.r[3][j];
+    *reinterpret_cast<bf16x4*>(tile + (c0 + j) * kPitch + r0) = col;
   }
 }
 
