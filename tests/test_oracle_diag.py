@@ -9,7 +9,15 @@ import torch
 
 from oracle import diag as O
 
-torch.set_default_dtype(torch.float64)
+
+
+@pytest.fixture(autouse=True)
+def _fp64_default():
+    """The oracle is pinned in fp64; the default dtype is restored after each test so other modules are unaffected."""
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
 
 
 def _inputs(B=2, T=45, D=6, seed=5):
