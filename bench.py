@@ -1,14 +1,17 @@
 """Benchmark of the carrier hot path on one MI355X: prints ONE JSON line.
 
-Workload (the configuration the headline metric is quoted on): the aspin chunked scan,
+Headline workload (the configuration the metric is quoted on): the aspin chunked scan,
 forward + backward, B16 T512 H12 D64, chunk 64, bf16 q/k/v, fp32 log-decays and state, synthetic seeded inputs
-resident in HBM. One step = one forward (writing o, the final state and the bf16 entering states) and one backward
-(dq, dk, dv, dla, dS0 from dO and dS_final) through the HIP kernels, on one stream.
+resident in HBM. One step = one forward (o, the final state and the bf16 entering states) and one backward
+(dq, dk, dv, dla, dS0 from dO and dS_final) through the HIP kernels, on one stream. `--rule` picks the write rule of
+the headline (plain by default); the other rule, the complex diagonal scan of configs[1] and the decode step are
+measured too and reported under "secondary".
 
-    python bench.py [--steps K] [--warmup W] [--rule plain|delta] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--rule plain|delta] [--no-cpu-baseline] [--no-secondary]
 
-`value` is tokens (B * T) per second over the K timed steps. `roofline` is the dominant kernel's algorithmic HBM
-bytes per launch over its average launch time, timed with HIP events on the stream it runs on. `cpu_baseline` is
+`value` is tokens (B * T) per second over the K timed steps, between two device synchronisations. `roofline` is the
+dominant kernel of the headline step: algorithmic HBM bytes per launch (every input read once, every output written
+once) over its average launch time, timed with HIP events on the stream the kernel is launched on. `cpu_baseline` is
 the CPU oracle (this repository's restatement of the reference's two-pass fp32 path, forward + autograd backward)
 timed on this host's cores over a bounded sample of the same workload.
 """
@@ -35,11 +38,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rule", choices=("plain", "delta"), default="plain")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
 
 
-def inputs(B, H, T, D, seed, rule, device):
+def aspin_inputs(B, H, T, D, seed, rule, device):
     """Seeded synthetic inputs following BASELINE.json configs[2]: q, k, v ~ N(0,1) with k L2-normalised per head,
     la = logsigmoid(N(3,1)), theta ~ U(0, 0.1) rotating q and k (interleaved pairs) at positions 0..T-1; delta rule:
     beta = sigmoid(N(0,1)). Upstream dO ~ N(0,1) and dS_final ~ N(0,1)."""
@@ -70,82 +74,158 @@ def inputs(B, H, T, D, seed, rule, device):
     return out
 
 
-def gpu_bench(args):
+def _time_ops(fns, n, stream):
+    """Average seconds per call of each fn, timed back to back with HIP events recorded on `stream` (the stream
+    the ops launch on)."""
+    import torch
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(fns) + 1)]
+    ev[0].record(stream)
+    for i, fn in enumerate(fns):
+        for _ in range(n):
+            fn()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) / n * 1e-3 for i in range(len(fns))]
+
+
+def aspin_bench(rule, steps, warmup):
+    """The cfg2 step for one write rule: wall-clock throughput over `steps` steps, plus per-op event timings."""
     import torch
     from pragnosia_amd import ops  # noqa: F401
     B, H, T, D, C = 16, 12, 512, 64, 64
     NC = T // C
     dev = torch.device("cuda:0")
-    x = inputs(B, H, T, D, 2, args.rule, dev)
+    x = aspin_inputs(B, H, T, D, 2, rule, dev)
     op = torch.ops.pragnosia
-    if args.rule != "plain":
-        raise SystemExit("bench.py: --rule delta is not built yet")
-
     stream = torch.cuda.current_stream(dev)
+    if rule == "plain":
+        fwd = lambda: op.aspin_chunk(x["q"], x["k"], x["v"], x["la"], None, True)
+        saved = fwd()
+        bwd = lambda: op.aspin_chunk_bwd(x["q"], x["k"], x["v"], x["la"], saved[2], x["do"], x["dS"])
 
-    def step():
-        o, S, sent = op.aspin_chunk(x["q"], x["k"], x["v"], x["la"], None, True)
-        grads = op.aspin_chunk_bwd(x["q"], x["k"], x["v"], x["la"], sent, x["do"], x["dS"])
-        return o, grads
+        def step():
+            o, S, sent = op.aspin_chunk(x["q"], x["k"], x["v"], x["la"], None, True)
+            return op.aspin_chunk_bwd(x["q"], x["k"], x["v"], x["la"], sent, x["do"], x["dS"])
+    else:
+        fwd = lambda: op.aspin_delta(x["q"], x["k"], x["v"], x["la"], x["beta"], None, True)
+        saved = fwd()
+        bwd = lambda: op.aspin_delta_bwd(x["q"], x["k"], x["v"], x["la"], x["beta"], saved[2], saved[3], saved[4],
+                                         x["do"], x["dS"])
 
-    for _ in range(args.warmup):
+        def step():
+            o, S, sent, W, X = op.aspin_delta(x["q"], x["k"], x["v"], x["la"], x["beta"], None, True)
+            return op.aspin_delta_bwd(x["q"], x["k"], x["v"], x["la"], x["beta"], sent, W, X, x["do"], x["dS"])
+
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = wall / args.steps * 1e3
+    wall = (time.perf_counter() - t0) / steps
+    t_fwd, t_bwd = _time_ops([fwd, bwd], max(20, min(steps, 200)), stream)
 
-    # per-kernel averages with HIP events on the launch stream
-    n_ev = max(20, min(args.steps, 200))
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    o, S, sent = op.aspin_chunk(x["q"], x["k"], x["v"], x["la"], None, True)
-    ev[0].record(stream)
-    for _ in range(n_ev):
-        op.aspin_chunk(x["q"], x["k"], x["v"], x["la"], None, True)
-    ev[1].record(stream)
-    for _ in range(n_ev):
-        op.aspin_chunk_bwd(x["q"], x["k"], x["v"], x["la"], sent, x["do"], x["dS"])
-    ev[2].record(stream)
-    torch.cuda.synchronize()
-    t_fwd = ev[0].elapsed_time(ev[1]) / n_ev * 1e-3     # seconds per launch
-    t_bwd = ev[1].elapsed_time(ev[2]) / n_ev * 1e-3
+    elem, ht, state, sent_n = B * H * T * D, B * H * T, B * H * D * D, B * H * NC * D * D
+    if rule == "plain":
+        # forward: q, k, v read, o written (bf16); la read; S_final and sent written
+        fwd_bytes = 4 * 2 * elem + 4 * ht + 4 * state + 2 * sent_n
+        # backward: q, k, v, dO, sent read; dq, dk, dv written; la read, dla written; dS_final read, dS0 written
+        bwd_bytes = 7 * 2 * elem + 2 * sent_n + 8 * ht + 8 * state
+        fwd_flops = 4 * D * (C + D) * ht
+        bwd_flops = 10 * D * (C + D) * ht
+        names = ("aspin_plain_fwd", "aspin_plain_bwd")
+    else:
+        # forward: q, k, v read; o, W written; X written and read back (bf16 C x C per chunk); la, beta read;
+        # S_final, sent written
+        x_n = B * H * NC * C * C
+        fwd_bytes = 5 * 2 * elem + 2 * 2 * x_n + 8 * ht + 4 * state + 2 * sent_n
+        # backward: q, k, v, dO, W, X, sent read; dq, dk, dv written; la, beta read, dla, dbeta written; the
+        # chain/local hand-off (drhs and per-chunk dS, bf16) written once and read once
+        bwd_bytes = 7 * 2 * elem + 2 * x_n + 2 * sent_n + 16 * ht + 8 * state + 2 * (2 * elem + 2 * sent_n)
+        fwd_flops = (4 * D * (C + D) + 2 * C * D + 2 * D * D + 2 * C * C) * ht
+        bwd_flops = (10 * D * (C + D) + 6 * C * D + 4 * D * D + 4 * C * C) * ht
+        names = ("aspin_delta_fwd (inv + fwd kernels)", "aspin_delta_bwd (chain + local kernels)")
+    return dict(B=B, H=H, T=T, D=D, C=C, wall=wall, t_fwd=t_fwd, t_bwd=t_bwd, fwd_bytes=fwd_bytes,
+                bwd_bytes=bwd_bytes, fwd_flops=fwd_flops, bwd_flops=bwd_flops, names=names)
 
-    elem = B * H * T * D
-    ht = B * H * T
-    state = B * H * D * D
-    # algorithmic HBM bytes per launch: every tensor read or written once
-    fwd_bytes = 3 * 2 * elem + 2 * elem + 4 * ht + 4 * state + 2 * (B * H * NC * D * D)   # q,k,v in; o, la, S, sent
-    bwd_bytes = 4 * 2 * elem + 2 * (B * H * NC * D * D) + 4 * ht + 4 * state + 3 * 2 * elem + 4 * ht + 4 * state
-    fwd_flops = 4 * D * (C + D) * ht
-    bwd_flops = 10 * D * (C + D) * ht
-    dom = ("aspin_plain_bwd", t_bwd, bwd_bytes, bwd_flops) if t_bwd >= t_fwd else \
-          ("aspin_plain_fwd", t_fwd, fwd_bytes, fwd_flops)
+
+def diag_bench(steps):
+    """the per-token-lambda complex diagonal scan, fwd + bwd, B16 T512 D768 fp32."""
+    import torch
+    import torch.nn.functional as F
+    from pragnosia_amd import ops  # noqa: F401
+    B, T, D = 16, 512, 768
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1)
+    u = (torch.randn(B, T, D, generator=g) * (torch.randn(D, generator=g) * 0.1)).to(dev)
+    lm = F.logsigmoid(torch.randn(B, T, D, generator=g) + 4.0).to(dev)
+    an = (torch.rand(B, T, D, generator=g) - 0.5).to(dev)
+    gy = torch.randn(B, T, D, generator=g).to(dev)
+    glr, gli = torch.randn(B, D, generator=g).to(dev), torch.randn(B, D, generator=g).to(dev)
+    op = torch.ops.pragnosia
+    hr, _, _, hi = op.diag_scan(u, lm, an, None, None)
+    fwd = lambda: op.diag_scan(u, lm, an, None, None)
+    bwd = lambda: op.diag_scan_bwd(gy, glr, gli, lm, an, hr, hi, None, None)
+    for _ in range(5):
+        fwd()
+        bwd()
+    t_fwd, t_bwd = _time_ops([fwd, bwd], max(20, min(steps, 200)), torch.cuda.current_stream(dev))
+    n = B * T * D
+    fb, bb = 20 * n, 32 * n
+    return {"workload": "complex diagonal scan fwd+bwd, B16 T512 D768 fp32 (configs[1])",
+            "Mtok_s": round(B * T / (t_fwd + t_bwd) / 1e6, 3),
+            "fwd_us": round(t_fwd * 1e6, 2), "bwd_us": round(t_bwd * 1e6, 2),
+            "fwd_GBs": round(fb / t_fwd / 1e9, 1), "bwd_GBs": round(bb / t_bwd / 1e9, 1),
+            "fwd_bwd_GBs": round((fb + bb) / (t_fwd + t_bwd) / 1e9, 1),
+            "hbm_frac": round((fb + bb) / (t_fwd + t_bwd) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def summarize(r, rule):
+    tokens = r["B"] * r["T"]
+    dom = (r["names"][1], r["t_bwd"], r["bwd_bytes"], r["bwd_flops"]) if r["t_bwd"] >= r["t_fwd"] else \
+          (r["names"][0], r["t_fwd"], r["fwd_bytes"], r["fwd_flops"])
     achieved = dom[2] / dom[1] / 1e9
-    tokens = B * T
+    return tokens, dom, achieved
+
+
+def gpu_bench(args):
+    r = aspin_bench(args.rule, args.steps, args.warmup)
+    tokens, dom, achieved = summarize(r, args.rule)
     res = {
         "metric": METRIC,
-        "value": round(tokens / (wall / args.steps) / 1e6, 3),
+        "value": round(tokens / r["wall"] / 1e6, 3),
         "unit": "Mtok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 5),
+        "ms_per_step": round(r["wall"] * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded, BASELINE.json configs[2] distributions)",
-        "config": {"workload": f"aspin chunked scan fwd+bwd, {args.rule} rule, B16 T512 H12 D64 chunk64",
-                   "B": B, "T": T, "H": H, "D": D, "chunk": C, "rule": args.rule},
+        "config": {"workload": f"aspin chunked scan fwd+bwd, {args.rule} rule, B16 T512 H12 D64 chunk64 (configs[2])",
+                   "B": r["B"], "T": r["T"], "H": r["H"], "D": r["D"], "chunk": r["C"], "rule": args.rule},
         "roofline": {"bound": "hbm", "kernel": dom[0], "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes": dom[2], "avg_launch_us": round(dom[1] * 1e6, 2),
-                     "mfma_tflops": round(dom[3] / dom[1] / 1e12, 2)},
-        "kernels_us": {"aspin_plain_fwd": round(t_fwd * 1e6, 2), "aspin_plain_bwd": round(t_bwd * 1e6, 2)},
+                     "mfma_tflops": round(dom[3] / dom[1] / 1e12, 2),
+                     "mfma_frac": round(dom[3] / dom[1] / 1e12 / BF16_PEAK_TFLOPS, 4)},
+        "kernels_us": {r["names"][0]: round(r["t_fwd"] * 1e6, 2), r["names"][1]: round(r["t_bwd"] * 1e6, 2)},
     }
+    if not args.no_secondary:
+        other = "delta" if args.rule == "plain" else "plain"
+        o = aspin_bench(other, max(20, args.steps // 4), 5)
+        ot, odom, oach = summarize(o, other)
+        sec = {f"aspin_{other}": {
+            "workload": f"aspin chunked scan fwd+bwd, {other} rule, B16 T512 H12 D64 (configs[2])",
+            "Mtok_s": round(ot / o["wall"] / 1e6, 3), "ms_per_step": round(o["wall"] * 1e3, 5),
+            "fwd_us": round(o["t_fwd"] * 1e6, 2), "bwd_us": round(o["t_bwd"] * 1e6, 2),
+            "fwd_bwd_GBs": round((o["fwd_bytes"] + o["bwd_bytes"]) / (o["t_fwd"] + o["t_bwd"]) / 1e9, 1),
+            "fwd_bwd_mfma_tflops": round((o["fwd_flops"] + o["bwd_flops"]) / (o["t_fwd"] + o["t_bwd"]) / 1e12, 2)}}
+        sec["diag_scan"] = diag_bench(args.steps)
+        res["secondary"] = sec
     return res
 
 
@@ -157,12 +237,15 @@ def cpu_baseline(args):
     torch.set_num_threads(os.cpu_count() if not os.environ.get("OMP_NUM_THREADS") else
                           int(os.environ["OMP_NUM_THREADS"]))
     B, H, T, D = 1, 12, 512, 64
-    x = inputs(B, H, T, D, 2, "plain", "cpu")
+    x = aspin_inputs(B, H, T, D, 2, args.rule, "cpu")
     S0 = torch.zeros(B, H, D, D)
 
     def it():
         a = [x[n].clone().requires_grad_(True) for n in ("q", "k", "v", "la")]
-        o, S, _ = O.scan_twopass(*a, S0, 64, None)
+        if args.rule == "plain":
+            o, S, _ = O.scan_twopass(*a, S0, 64, None)
+        else:
+            o, S, _, _ = O.scan_twopass_delta(*a, x["beta"], S0, 64, None)
         ((o * x["do"]).sum() + (S * x["dS"]).sum()).backward()
 
     for _ in range(3):
@@ -175,9 +258,10 @@ def cpu_baseline(args):
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
+    form = "src/assoc.py:118-165" if args.rule == "plain" else "src/assoc.py:168-251"
     return {"value": round(B * T / med / 1e6, 5), "unit": "Mtok/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"CPU oracle (two-pass fp32 restatement of src/assoc.py:118-165, autograd backward), "
+            "sample": f"CPU oracle ({args.rule} rule, two-pass fp32 restatement of {form}, autograd backward), "
                       f"B=1 x T512 H12 D64 per iteration, {len(times)} iterations (~{args.cpu_seconds:.0f} s), "
                       "median"}
 

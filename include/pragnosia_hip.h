@@ -69,6 +69,33 @@ int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const void* v, const
                               void* dq, void* dk, void* dv, float* dla, float* dS0,
                               int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * Associative carrier, DELTA write rule, chunked scan (chunk = 64, head dim D = 64), per (batch, head):
+ *     S_t = a_t S_{t-1} + beta_t k_t (v_t - (a_t S_{t-1})^T k_t)^T,   o_t = S_t^T q_t,   a_t = exp(la_t).
+ * Layouts as pragnosia_aspin_chunk_fwd; beta: (B, H, T) fp32 in (0, 1). Writes o (bf16), S_final (fp32), sent
+ * (bf16 entering states, required by the backward; may be NULL when no backward follows), and the two saved
+ * intermediates of the backward: W, the residuals actually written, (B, H, T, D) bf16, and X, the per-chunk
+ * inverse (I + diag(beta) strictly_lower((K K^T) o dec))^-1, (B, H, ceil(T/64), 64, 64) bf16, computed in fp32.
+ * Replaces `delta_scan_kernel` and the ops under it (`delta_inv`, `delta_loop_fwd`, `assoc_out`) of
+ * src/assoc_kernel.py:332-386, :512-704; the rule is `_scan_twopass_delta` of src/assoc.py:207-251. */
+int pragnosia_aspin_delta_fwd(const void* q, const void* k, const void* v, const float* la, const float* beta,
+                              const float* S0, void* o, float* S_final, void* sent, void* W, void* X,
+                              int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
+
+/* Bytes of device workspace pragnosia_aspin_delta_bwd needs at this shape (-1 if the shape is rejected). */
+int64_t pragnosia_aspin_delta_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk);
+
+/* Backward of pragnosia_aspin_delta_fwd. dO (B, H, T, D) bf16; dS_final fp32 or NULL (zero). Writes dq, dk, dv
+ * (bf16), dla and dbeta (fp32, (B, H, T)) and, if non-NULL, dS0 (fp32). `workspace` is caller-allocated device
+ * memory of at least pragnosia_aspin_delta_bwd_workspace_bytes(...) bytes (no alignment beyond 256 B needed).
+ * Replaces the registered backward of `delta_loop_fwd`, `delta_inv` and `assoc_out`
+ * (`_delta_loop_bwd`, `_inv_bwd`, `_bwd_chunk` of src/assoc_kernel.py:73-116, :389-509, :625-704). */
+int pragnosia_aspin_delta_bwd(const void* q, const void* k, const void* v, const float* la, const float* beta,
+                              const void* sent, const void* W, const void* X, const void* dO,
+                              const float* dS_final, void* dq, void* dk, void* dv, float* dla, float* dbeta,
+                              float* dS0, void* workspace, int64_t workspace_bytes,
+                              int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

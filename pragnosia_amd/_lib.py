@@ -23,7 +23,13 @@ SIGNATURES = {
     "pragnosia_diag_scan_bwd": [_p] * 14 + [_i64] * 3 + [_p],
     "pragnosia_aspin_chunk_fwd": [_p] * 8 + [_i64] * 5 + [_p],
     "pragnosia_aspin_chunk_bwd": [_p] * 12 + [_i64] * 5 + [_p],
+    "pragnosia_aspin_delta_fwd": [_p] * 11 + [_i64] * 5 + [_p],
+    "pragnosia_aspin_delta_bwd_workspace_bytes": [_i64] * 5,
+    "pragnosia_aspin_delta_bwd": [_p] * 17 + [_i64] * 6 + [_p],
 }
+
+# entry points that return a size (int64) rather than a status code
+_RET_I64 = {"pragnosia_aspin_delta_bwd_workspace_bytes"}
 
 _lib = None
 
@@ -43,7 +49,8 @@ def lib():
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_char_p if name == "pragnosia_error_string" else _i32
+            fn.restype = (ctypes.c_char_p if name == "pragnosia_error_string" else
+                          _i64 if name in _RET_I64 else _i32)
         _lib = L
     return _lib
 

@@ -1,0 +1,804 @@
+// The associative carrier's chunked scan, delta write rule: forward and hand-written backward.
+//
+// Per (batch, head), chunk C = 64, head dim D = 64, with L, eL, w, a and dec as in the plain rule and beta_t in (0, 1)
+// the write strength, the state S entering a chunk is updated by (the reference's `_scan_twopass_delta`,
+// `src/assoc.py:207-251`):
+//     N   = diag(beta) strictly_lower((K K^T) o dec),   X = (I + N)^-1
+//     U   = K S,   rhs = diag(beta) (V - diag(eL) U),   W = X rhs
+//     O   = ((Q K^T) o dec) W + (Q o eL) S,             S' = a S + (K o w)^T W
+//
+// Four kernels:
+//   aspin_delta_inv    one wave per (batch-head, chunk): N from a bf16 MFMA K K^T and fp32 decays, then X by exact
+//                      fp32 forward substitution, one column of X per lane (the reference sums 16 x 16 diagonal
+//                      blocks by doubling and substitutes across blocks, `src/assoc.py:168-204`; both are exact
+//                      in exact arithmetic, substitution is backward stable). X is stored bf16 for the products.
+//   aspin_delta_fwd    one workgroup of 4 waves per (batch, head) walks the chunks. The rule is independent per
+//                      value column given X, so wave w owns value columns 16w..16w+15 for all 64 tokens and the
+//                      whole state chain (U -> rhs -> W -> S') stays in that wave's MFMA accumulators: each
+//                      product's accumulator is the next product's operand, with no LDS round trip and no barrier
+//                      on the chain. Writes o, the residuals W and the entering states (both bf16) for the
+//                      backward, and the final fp32 state.
+//   aspin_delta_bwd_chain   one workgroup of 4 waves per (batch, head), chunks in reverse, wave w owning value
+//                      columns 16w.. again. Carries dS (gradient on the state leaving the chunk) in registers:
+//                          dW = A^T dO + w o (K dS),  drhs = X^T dW,  dU = -beta eL o drhs,
+//                          dS_prev = a dS + (Q o eL)^T dO + K^T dU,   dV = beta o drhs,
+//                      and writes drhs, the per-chunk dS (bf16) and the row sums over value columns that the decay
+//                      and beta gradients need: sum_j drhs (V - eL U) and -beta sum_j drhs U.
+//   aspin_delta_bwd_local   one workgroup of 8 waves per (batch-head, chunk), fully parallel: everything that is
+//                      local to a chunk once drhs and dS are known. With dN = -drhs W^T (the gradient through
+//                      W = X rhs, since dX = dW rhs^T and dN = -X^T dX X^T), dKK = diag(beta) dN o dec (strictly
+//                      lower), G = dKK + dKK^T, dA = dO W^T, dP = dA o dec:
+//                          dQ = dP K + eL o (dO S^T)
+//                          dK = dP^T Q + G K + dU S^T + w o (W dS^T)
+//                          dbeta_t = sum_j drhs (V - eL U) + sum_{s<t} dN_ts (KK o dec)_ts
+//                          dL_t = rowsum(dA o A) - colsum(dA o A) + rowsum(dKK o KK) - colsum(dKK o KK)
+//                                 + eL_t (q_t.(S dO_t) - beta_t sum_j drhs U) - w_t k_t.(dS W_t),
+//                          dL_{C-1} += sum_t w_t k_t.(dS W_t) + a <S, dS>;  dla = reverse cumsum of dL.
+// (the reference's loop kernels `src/assoc_kernel.py:332-458` and inverse `:555-704` compute the same quantities
+// with a different split.) Padded tokens of a partial last chunk load as zero with la = 0 and beta = 0: they write
+// nothing and receive no gradient.
+#include "mfma_tile.h"
+
+using namespace pgn;
+
+namespace {
+
+constexpr int C = 64;
+constexpr int DK = 64;
+constexpr int TILE = 64 * kPitch;
+constexpr int NP = C + 4;  // pitch of the fp32 N^T tile
+
+PGN_DEVICE float incl_scan64(float x, int l) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float y = __shfl_up(x, off);
+    if (l >= off) x += y;
+  }
+  return x;
+}
+
+PGN_DEVICE float rev_scan64(float x, int l) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float y = __shfl_down(x, off);
+    if (l + off < 64) x += y;
+  }
+  return x;
+}
+
+// Per-chunk decay statistics into LDS (one wave): L (inclusive cumsum of la), eL = exp(L), w = exp(L_C - L).
+PGN_DEVICE void chunk_decays(float la_l, int l, float* Ls, float* eLs, float* ws) {
+  const float L = incl_scan64(la_l, l);
+  const float LC = __shfl(L, 63);
+  Ls[l] = L;
+  eLs[l] = __expf(L);
+  ws[l] = __expf(fminf(LC - L, 0.f));
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// X = (I + N)^-1, one wave per (batch-head, chunk)
+__global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__ k, const float* __restrict__ la,
+                                                      const float* __restrict__ be, __bf16* __restrict__ X, int T,
+                                                      int NC) {
+  __shared__ __align__(16) __bf16 Ks[TILE];
+  __shared__ __align__(16) float NT[C * NP];  // NT[s][t] = N[t][s]
+  __shared__ __align__(16) float Ls[C], bs[C];
+
+  const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;
+  const int l = threadIdx.x, g = l >> 4, i = l & 15;
+  const int t0 = c * C, nr = min(C, T - t0);
+  const __bf16* kc = k + ((size_t)bh * T + t0) * DK;
+  for (int e = l; e < C * 16; e += 64) {
+    const int r = e >> 4, q4 = (e & 15) * 4;
+    const bf16x4 x = r < nr ? *reinterpret_cast<const bf16x4*>(kc + (size_t)r * DK + q4) : zero_bf16x4();
+    *reinterpret_cast<bf16x4*>(Ks + r * kPitch + q4) = x;
+  }
+  const float lav = l < nr ? la[(size_t)bh * T + t0 + l] : 0.f;
+  const float bev = l < nr ? be[(size_t)bh * T + t0 + l] : 0.f;
+  Ls[l] = incl_scan64(lav, l);
+  bs[l] = bev;
+  __syncthreads();
+
+  // N^T tiles: accumulator rows s (block sb), lane t (block tb), for sb <= tb
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int t = 16 * tb + i;
+    const float Lt = Ls[t], bt = bs[t];
+    const bf16x8 kt0 = frag(Ks, t, 0, g), kt1 = frag(Ks, t, 1, g);
+#pragma unroll
+    for (int sb = 0; sb <= tb; ++sb) {
+      f32x4 acc = zero4();
+      acc = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), kt0, acc);
+      acc = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), kt1, acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int s = 16 * sb + 4 * g + r;
+        NT[s * NP + t] = (s < t) ? bt * acc[r] * __expf(fminf(Lt - Ls[s], 0.f)) : 0.f;
+      }
+    }
+  }
+  __syncthreads();
+
+  // column l of X: (I + N) x = e_l, right-looking forward substitution
+  float x[C];
+#pragma unroll
+  for (int t = 0; t < C; ++t) x[t] = (t == l) ? 1.f : 0.f;
+#pragma unroll
+  for (int s = 0; s < C - 1; ++s) {
+    const float xs = x[s];
+#pragma unroll
+    for (int t4 = ((s + 1) >> 2) << 2; t4 < C; t4 += 4) {
+      const f32x4 n = *reinterpret_cast<const f32x4*>(NT + s * NP + t4);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (t4 + u > s) x[t4 + u] -= n[u] * xs;
+    }
+  }
+  __bf16* Xc = X + ((size_t)bh * NC + c) * C * C;
+#pragma unroll
+  for (int t = 0; t < C; ++t) Xc[t * C + l] = (__bf16)x[t];
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// forward: one workgroup of 4 waves per (batch, head); wave w owns value columns 16w..16w+15
+__global__ __launch_bounds__(256) void aspin_delta_fwd(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const float* __restrict__ la, const float* __restrict__ be, const __bf16* __restrict__ X,
+    const float* __restrict__ S0, __bf16* __restrict__ o, __bf16* __restrict__ Wout, float* __restrict__ Sfin,
+    __bf16* __restrict__ sent, int T, int NC) {
+  __shared__ __align__(16) __bf16 Qs[TILE], Ks[TILE], KT[TILE], VT[TILE], Xs[TILE], As[TILE];
+  __shared__ __align__(16) float Ls[C], eLs[C], ws[C], bs[C];
+
+  const WaveIdx x = wave_idx();
+  const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int j = 16 * w + i;  // this lane's value column
+  const size_t boff = (size_t)bh * T * DK;
+  const size_t soff = (size_t)bh * DK * DK;
+
+  // state columns j, key rows 16 db + 4g + r
+  f32x4 S[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) S[db][r] = S0 ? S0[soff + (size_t)(16 * db + 4 * g + r) * DK + j] : 0.f;
+
+  const int br = 4 * (tid >> 4), bc = 4 * (tid & 15);
+  Blk4 pq = load_blk(q + boff, DK, min(C, T), tid);
+  Blk4 pk = load_blk(k + boff, DK, min(C, T), tid);
+  Blk4 pv = load_blk(v + boff, DK, min(C, T), tid);
+  Blk4 px = load_blk(X + (size_t)bh * NC * C * C, C, C, tid);
+  float pla = 0.f, pbe = 0.f;
+  if (w == 0 && x.l < T) {
+    pla = la[(size_t)bh * T + x.l];
+    pbe = be[(size_t)bh * T + x.l];
+  }
+
+  for (int c = 0; c < NC; ++c) {
+    const int t0 = c * C;
+    put_blk(Qs, pq, br, bc);
+    put_blk(Ks, pk, br, bc);
+    put_blk_T(KT, pk, br, bc);
+    put_blk_T(VT, pv, br, bc);
+    put_blk(Xs, px, br, bc);
+    if (w == 0) {
+      chunk_decays(pla, x.l, Ls, eLs, ws);
+      bs[x.l] = pbe;
+    }
+    __syncthreads();
+    if (c + 1 < NC) {
+      const int n0 = t0 + C, nr = min(C, T - n0);
+      pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, tid);
+      pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, tid);
+      pv = load_blk(v + boff + (size_t)n0 * DK, DK, nr, tid);
+      px = load_blk(X + ((size_t)bh * NC + c + 1) * C * C, C, C, tid);
+      if (w == 0) {
+        const bool ok = n0 + x.l < T;
+        pla = ok ? la[(size_t)bh * T + n0 + x.l] : 0.f;
+        pbe = ok ? be[(size_t)bh * T + n0 + x.l] : 0.f;
+      }
+    }
+
+    // decayed scores for token block w: A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, into As (row t)
+    {
+      const int t = 16 * w + i;
+      const bf16x8 qf0 = frag(Qs, t, 0, g), qf1 = frag(Qs, t, 1, g);
+      const float Lt = Ls[t];
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) {
+        f32x4 pt = zero4();
+        if (sb <= w) {
+          pt = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt);
+          pt = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt);
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int s = 16 * sb + 4 * g + r;
+            pt[r] = (s <= t) ? pt[r] * __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+          }
+        }
+        store_T(As, 16 * w, 16 * sb, g, i, pt);
+      }
+    }
+
+    // U = K S (rows t, this wave's columns); rhs = beta (V - eL U)
+    const bf16x8 s01 = pack(S[0], S[1]), s23 = pack(S[2], S[3]);
+    f32x4 R[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      f32x4 u = zero4();
+      u = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), s01, u);
+      u = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), s23, u);
+      const f32x4 vv = to_f32x4(*reinterpret_cast<const bf16x4*>(VT + j * kPitch + 16 * tb + 4 * g));
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
+      const f32x4 ev = *reinterpret_cast<const f32x4*>(eLs + 16 * tb + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) R[tb][r] = bv[r] * (vv[r] - ev[r] * u[r]);
+    }
+    // W = X rhs (X lower triangular)
+    const bf16x8 r01 = pack(R[0], R[1]), r23 = pack(R[2], R[3]);
+    f32x4 Wt[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 0, g), r01, zero4());
+      if (tb >= 2) Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 1, g), r23, Wt[tb]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + 16 * tb + 4 * g + r;
+        if (t < T) Wout[boff + (size_t)t * DK + j] = (__bf16)Wt[tb][r];
+      }
+    }
+    if (sent) {
+      __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[(16 * db + 4 * g + r) * DK + j] = (__bf16)S[db][r];
+    }
+    __syncthreads();  // As complete
+
+    // O^T tiles (value rows 16w + 4g + r, token lane 16 tb + i) = W^T A^T + S^T (Q o eL)^T
+    const bf16x8 w01 = pack(Wt[0], Wt[1]), w23 = pack(Wt[2], Wt[3]);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const int tl = 16 * tb + i;
+      const float eLt = eLs[tl];
+      f32x4 acc = pgn_mfma(w01, frag(As, tl, 0, g), zero4());
+      if (tb >= 2) acc = pgn_mfma(w23, frag(As, tl, 1, g), acc);
+      acc = pgn_mfma(s01, frag_scaled(Qs, tl, 0, g, eLt), acc);
+      acc = pgn_mfma(s23, frag_scaled(Qs, tl, 1, g, eLt), acc);
+      if (t0 + tl < T) *reinterpret_cast<bf16x4*>(o + boff + (size_t)(t0 + tl) * DK + 16 * w + 4 * g) = to_bf16x4(acc);
+    }
+
+    // S <- a S + (K o w)^T W
+    const float a_c = __expf(Ls[C - 1]);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      S[db] = S[db] * a_c;
+      S[db] = pgn_mfma(frag_scaled_k(KT, 16 * db + i, 0, g, ws), w01, S[db]);
+      S[db] = pgn_mfma(frag_scaled_k(KT, 16 * db + i, 1, g, ws), w23, S[db]);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Sfin[soff + (size_t)(16 * db + 4 * g + r) * DK + j] = S[db][r];
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// backward, the sequential part: one workgroup of 4 waves per (batch, head), chunks in reverse
+__global__ __launch_bounds__(256) void aspin_delta_bwd_chain(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const float* __restrict__ la, const float* __restrict__ be, const __bf16* __restrict__ X,
+    const __bf16* __restrict__ sent, const __bf16* __restrict__ dO, const float* __restrict__ dSfin,
+    __bf16* __restrict__ dv, __bf16* __restrict__ drhs, __bf16* __restrict__ dSc, float* __restrict__ rsum,
+    float* __restrict__ dS0, int T, int NC) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __bf16* Qs = reinterpret_cast<__bf16*>(smem);
+  __bf16* QT = Qs + TILE;
+  __bf16* Ks = QT + TILE;
+  __bf16* KT = Ks + TILE;
+  __bf16* VT = KT + TILE;
+  __bf16* OT = VT + TILE;  // dO^T (row j, column t)
+  __bf16* XT = OT + TILE;  // XT[t][s] = X[s][t]
+  __bf16* ST = XT + TILE;  // ST[j][d] = S_c[d][j]
+  __bf16* AT = ST + TILE;  // AT[t][s] = A[s][t]
+  float* Ls = reinterpret_cast<float*>(AT + TILE);
+  float* eLs = Ls + C;
+  float* ws = eLs + C;
+  float* bs = ws + C;
+  float* redV = bs + C;       // [4][C] per-wave partial sums of drhs V
+  float* redU = redV + 4 * C; // [4][C] per-wave partial sums of drhs U
+
+  const WaveIdx x = wave_idx();
+  const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int j = 16 * w + i;
+  const size_t boff = (size_t)bh * T * DK;
+  const size_t soff = (size_t)bh * DK * DK;
+
+  f32x4 dS[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dS[db][r] = dSfin ? dSfin[soff + (size_t)(16 * db + 4 * g + r) * DK + j] : 0.f;
+
+  const int br = 4 * (tid >> 4), bc = 4 * (tid & 15);
+  Blk4 pq, pk, pv, po, px, ps;
+  float pla = 0.f, pbe = 0.f;
+  auto prefetch = [&](int cc) {
+    const int n0 = cc * C, nr = min(C, T - n0);
+    pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, tid);
+    pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, tid);
+    pv = load_blk(v + boff + (size_t)n0 * DK, DK, nr, tid);
+    po = load_blk(dO + boff + (size_t)n0 * DK, DK, nr, tid);
+    px = load_blk(X + ((size_t)bh * NC + cc) * C * C, C, C, tid);
+    ps = load_blk(sent + ((size_t)bh * NC + cc) * DK * DK, DK, DK, tid);
+    if (w == 0) {
+      const bool ok = n0 + x.l < T;
+      pla = ok ? la[(size_t)bh * T + n0 + x.l] : 0.f;
+      pbe = ok ? be[(size_t)bh * T + n0 + x.l] : 0.f;
+    }
+  };
+  prefetch(NC - 1);
+
+  for (int cc = NC - 1; cc >= 0; --cc) {
+    const int t0 = cc * C;
+    put_blk(Qs, pq, br, bc);
+    put_blk_T(QT, pq, br, bc);
+    put_blk(Ks, pk, br, bc);
+    put_blk_T(KT, pk, br, bc);
+    put_blk_T(VT, pv, br, bc);
+    put_blk_T(OT, po, br, bc);
+    put_blk_T(XT, px, br, bc);
+    put_blk_T(ST, ps, br, bc);
+    if (w == 0) {
+      chunk_decays(pla, x.l, Ls, eLs, ws);
+      bs[x.l] = pbe;
+    }
+    __syncthreads();
+    if (cc > 0) prefetch(cc - 1);
+
+    // scores, transposed, for token block w: AT[t][s] = (q_s . k_t) exp(L_s - L_t), s >= t
+    {
+      const int t = 16 * w + i;
+      const bf16x8 kf0 = frag(Ks, t, 0, g), kf1 = frag(Ks, t, 1, g);
+      const float Lt = Ls[t];
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) {
+        f32x4 a = zero4();
+        if (sb >= w) {
+          a = pgn_mfma(frag(Qs, 16 * sb + i, 0, g), kf0, a);
+          a = pgn_mfma(frag(Qs, 16 * sb + i, 1, g), kf1, a);
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int s = 16 * sb + 4 * g + r;
+            a[r] = (s >= t) ? a[r] * __expf(fminf(Lsv[r] - Lt, 0.f)) : 0.f;
+          }
+        }
+        store_T(AT, 16 * w, 16 * sb, g, i, a);
+      }
+    }
+    // U = K S_c and (Q o eL)^T dO on this wave's columns: neither depends on dS
+    f32x4 U[4], Yc[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      U[tb] = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), frag(ST, j, 0, g), zero4());
+      U[tb] = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), frag(ST, j, 1, g), U[tb]);
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      Yc[db] = pgn_mfma(frag_scaled_k(QT, 16 * db + i, 0, g, eLs), frag(OT, j, 0, g), zero4());
+      Yc[db] = pgn_mfma(frag_scaled_k(QT, 16 * db + i, 1, g, eLs), frag(OT, j, 1, g), Yc[db]);
+    }
+    // the gradient on the state leaving this chunk, for the chunk-local kernel
+    {
+      __bf16* dst = dSc + ((size_t)bh * NC + cc) * DK * DK;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * g + r) * DK + j] = (__bf16)dS[db][r];
+    }
+    __syncthreads();  // AT complete
+
+    // dW = A^T dO + w o (K dS)
+    const bf16x8 d01 = pack(dS[0], dS[1]), d23 = pack(dS[2], dS[3]);
+    f32x4 dW[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      f32x4 y = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), d01, zero4());
+      y = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), d23, y);
+      f32x4 acc = zero4();
+      if (tb < 2) acc = pgn_mfma(frag(AT, 16 * tb + i, 0, g), frag(OT, j, 0, g), acc);
+      acc = pgn_mfma(frag(AT, 16 * tb + i, 1, g), frag(OT, j, 1, g), acc);
+      const f32x4 wv = *reinterpret_cast<const f32x4*>(ws + 16 * tb + 4 * g);
+      dW[tb] = acc + wv * y;
+    }
+    // drhs = X^T dW (X^T upper triangular)
+    const bf16x8 w01 = pack(dW[0], dW[1]), w23 = pack(dW[2], dW[3]);
+    f32x4 dR[4], dU[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      f32x4 acc = zero4();
+      if (tb < 2) acc = pgn_mfma(frag(XT, 16 * tb + i, 0, g), w01, acc);
+      acc = pgn_mfma(frag(XT, 16 * tb + i, 1, g), w23, acc);
+      dR[tb] = acc;
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
+      const f32x4 ev = *reinterpret_cast<const f32x4*>(eLs + 16 * tb + 4 * g);
+      const f32x4 vv = to_f32x4(*reinterpret_cast<const bf16x4*>(VT + j * kPitch + 16 * tb + 4 * g));
+      float pv_[4], pu_[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + 16 * tb + 4 * g + r;
+        dU[tb][r] = -bv[r] * ev[r] * acc[r];
+        pv_[r] = sum16(acc[r] * vv[r]);
+        pu_[r] = sum16(acc[r] * U[tb][r]);
+        if (t < T) {
+          dv[boff + (size_t)t * DK + j] = (__bf16)(bv[r] * acc[r]);
+          drhs[boff + (size_t)t * DK + j] = (__bf16)acc[r];
+        }
+      }
+      if (i == 0) {
+        *reinterpret_cast<f32x4*>(redV + w * C + 16 * tb + 4 * g) = f32x4{pv_[0], pv_[1], pv_[2], pv_[3]};
+        *reinterpret_cast<f32x4*>(redU + w * C + 16 * tb + 4 * g) = f32x4{pu_[0], pu_[1], pu_[2], pu_[3]};
+      }
+    }
+    // dS_prev = a dS + (Q o eL)^T dO + K^T dU
+    const float a_c = __expf(Ls[C - 1]);
+    const bf16x8 u01 = pack(dU[0], dU[1]), u23 = pack(dU[2], dU[3]);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      f32x4 acc = dS[db] * a_c + Yc[db];
+      acc = pgn_mfma(frag(KT, 16 * db + i, 0, g), u01, acc);
+      acc = pgn_mfma(frag(KT, 16 * db + i, 1, g), u23, acc);
+      dS[db] = acc;
+    }
+    __syncthreads();  // partial sums complete
+    if (w == 0) {
+      const int t = x.l;
+      const float pv_ = redV[t] + redV[C + t] + redV[2 * C + t] + redV[3 * C + t];
+      const float pu_ = redU[t] + redU[C + t] + redU[2 * C + t] + redU[3 * C + t];
+      if (t0 + t < T) {
+        rsum[((size_t)bh * T + t0 + t) * 2 + 0] = pv_ - eLs[t] * pu_;   // sum_j drhs (V - eL U)
+        rsum[((size_t)bh * T + t0 + t) * 2 + 1] = -bs[t] * pu_;         // d eL from the right-hand side
+      }
+    }
+    __syncthreads();
+  }
+  if (dS0) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dS0[soff + (size_t)(16 * db + 4 * g + r) * DK + j] = dS[db][r];
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// backward, the chunk-local part: one workgroup of 8 waves per (batch-head, chunk). Waves 0-3 own token block
+// t = 16w.. (dQ, row sums), waves 4-7 own token block s = 16(w-4).. in the key role (dK, column sums).
+__global__ __launch_bounds__(512) void aspin_delta_bwd_local(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const float* __restrict__ la,
+    const float* __restrict__ be, const __bf16* __restrict__ Win, const __bf16* __restrict__ sent,
+    const __bf16* __restrict__ dO, const __bf16* __restrict__ drhs, const __bf16* __restrict__ dSc,
+    const float* __restrict__ rsum, __bf16* __restrict__ dq, __bf16* __restrict__ dk, float* __restrict__ dla,
+    float* __restrict__ dbe, int T, int NC) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __bf16* Qs = reinterpret_cast<__bf16*>(smem);
+  __bf16* QT = Qs + TILE;
+  __bf16* Ks = QT + TILE;
+  __bf16* KT = Ks + TILE;
+  __bf16* Ws = KT + TILE;
+  __bf16* Os = Ws + TILE;   // dO
+  __bf16* Ss = Os + TILE;   // S_c (d, j)
+  __bf16* dSs = Ss + TILE;  // dS (d, j)
+  __bf16* Rs = dSs + TILE;  // drhs (t, j)
+  float* Ls = reinterpret_cast<float*>(Rs + TILE);
+  float* eLs = Ls + C;
+  float* ws = eLs + C;
+  float* bs = ws + C;
+  float* rowT = bs + C;     // rowsum(dA o A) + rowsum(dKK o KK) + eL q.(S dO)
+  float* dbe2 = rowT + C;   // sum_{s<t} dN M
+  float* colS = dbe2 + C;   // colsum(dA o A) + colsum(dKK o KK)
+  float* dwv = colS + C;    // k_s . (dS W_s)
+  float* sdot = dwv + C;    // per-wave <S, dS>
+
+  const WaveIdx x = wave_idx();
+  const int w = x.w, wl = w & 3, g = x.g, i = x.i, tid = threadIdx.x;
+  const bool gk = w >= 4;
+  const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;
+  const int t0 = c * C, nr = min(C, T - t0);
+  const size_t coff = ((size_t)bh * T + t0) * DK;
+  const size_t soff = ((size_t)bh * NC + c) * DK * DK;
+
+  {
+    const int b = tid & 255;
+    const int br = 4 * (b >> 4), bc = 4 * (b & 15);
+    if (tid < 256) {
+      const Blk4 a = load_blk(q + coff, DK, nr, b);
+      const Blk4 b2 = load_blk(Win + coff, DK, nr, b);
+      const Blk4 b3 = load_blk(sent + soff, DK, DK, b);
+      const Blk4 b4 = load_blk(drhs + coff, DK, nr, b);
+      put_blk(Qs, a, br, bc);
+      put_blk_T(QT, a, br, bc);
+      put_blk(Ws, b2, br, bc);
+      put_blk(Ss, b3, br, bc);
+      put_blk(Rs, b4, br, bc);
+    } else {
+      const Blk4 a = load_blk(k + coff, DK, nr, b);
+      const Blk4 b2 = load_blk(dO + coff, DK, nr, b);
+      const Blk4 b3 = load_blk(dSc + soff, DK, DK, b);
+      put_blk(Ks, a, br, bc);
+      put_blk_T(KT, a, br, bc);
+      put_blk(Os, b2, br, bc);
+      put_blk(dSs, b3, br, bc);
+    }
+    if (w == 0) {
+      const bool ok = x.l < nr;
+      const float lav = ok ? la[(size_t)bh * T + t0 + x.l] : 0.f;
+      chunk_decays(lav, x.l, Ls, eLs, ws);
+      bs[x.l] = ok ? be[(size_t)bh * T + t0 + x.l] : 0.f;
+    }
+  }
+  __syncthreads();
+  const int me = 16 * wl + i;
+
+  if (!gk) {
+    // ---------------- token block wl in the query role: lane t = me
+    const float Lt = Ls[me], bt = bs[me];
+    const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
+    const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
+    const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
+    const bf16x8 rf0 = frag(Rs, me, 0, g), rf1 = frag(Rs, me, 1, g);
+    float rowacc = 0.f, db2 = 0.f;
+    f32x4 dPT[4];
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      dPT[sb] = zero4();
+      if (sb <= wl) {
+        // rows s, lane t: P[t][s], dA[t][s], KK[t][s], dN[t][s]
+        f32x4 P = zero4(), dA = zero4(), KK = zero4(), dN = zero4();
+        P = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, P);
+        P = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, P);
+        dA = pgn_mfma(frag(Ws, 16 * sb + i, 0, g), of0, dA);
+        dA = pgn_mfma(frag(Ws, 16 * sb + i, 1, g), of1, dA);
+        KK = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), kf0, KK);
+        KK = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), kf1, KK);
+        dN = pgn_mfma(frag(Ws, 16 * sb + i, 0, g), rf0, dN);
+        dN = pgn_mfma(frag(Ws, 16 * sb + i, 1, g), rf1, dN);
+        const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int s = 16 * sb + 4 * g + r;
+          const float dec = (s <= me) ? __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+          rowacc += dA[r] * P[r] * dec;
+          dPT[sb][r] = dA[r] * dec;
+          if (s < me) {
+            const float M = KK[r] * dec;
+            const float dn = -dN[r];
+            db2 += dn * M;
+            rowacc += bt * dn * M;
+          }
+        }
+      }
+    }
+    rowacc = sum_groups(rowacc);
+    db2 = sum_groups(db2);
+    const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
+    const float eLt = eLs[me];
+    const __bf16* qrow = Qs + me * kPitch;
+    const bool t_ok = me < nr;
+    float qzt = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      f32x4 acc = zero4(), Z = zero4();
+      acc = pgn_mfma(frag(KT, 16 * dt + i, 0, g), b0, acc);
+      if (wl >= 2) acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), b1, acc);
+      Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
+      Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
+      const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
+      acc = acc + Z * eLt;
+      if (t_ok) *reinterpret_cast<bf16x4*>(dq + coff + (size_t)me * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
+    }
+    qzt = sum_groups(qzt);
+    if (g == 0) {
+      rowT[me] = rowacc + eLt * qzt;
+      dbe2[me] = db2;
+    }
+  } else {
+    // ---------------- token block wl in the key role: lane s = me
+    const float Lsm = Ls[me], bsm = bs[me], wsm = ws[me], eLsm = eLs[me];
+    const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
+    const bf16x8 wf0 = frag(Ws, me, 0, g), wf1 = frag(Ws, me, 1, g);
+    const bf16x8 rf0 = frag(Rs, me, 0, g), rf1 = frag(Rs, me, 1, g);
+    float colacc = 0.f;
+    f32x4 dPt[4], Gt[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      dPt[tb] = zero4();
+      Gt[tb] = zero4();
+      if (tb >= wl) {
+        // rows t, lane s: P[t][s], dA[t][s], KK[t][s], dN[t][s]
+        f32x4 P = zero4(), dA = zero4(), KK = zero4(), dN = zero4();
+        P = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, P);
+        P = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, P);
+        dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), wf0, dA);
+        dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), wf1, dA);
+        KK = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), kf0, KK);
+        KK = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), kf1, KK);
+        dN = pgn_mfma(frag(Rs, 16 * tb + i, 0, g), wf0, dN);
+        dN = pgn_mfma(frag(Rs, 16 * tb + i, 1, g), wf1, dN);
+        const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+        const f32x4 btv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tb + 4 * g + r;
+          const float dec = (t >= me) ? __expf(fminf(Ltv[r] - Lsm, 0.f)) : 0.f;
+          colacc += dA[r] * P[r] * dec;
+          dPt[tb][r] = dA[r] * dec;
+          if (t > me) {
+            const float dkk = -btv[r] * dN[r] * dec;  // dKK[t][s]
+            colacc += dkk * KK[r];
+            Gt[tb][r] = dkk;
+          }
+        }
+      }
+      if (tb <= wl) {
+        // rows t, lane s: dN[s][t] = -sum_j W[t][j] drhs[s][j], for t < s
+        f32x4 dN = zero4();
+        dN = pgn_mfma(frag(Ws, 16 * tb + i, 0, g), rf0, dN);
+        dN = pgn_mfma(frag(Ws, 16 * tb + i, 1, g), rf1, dN);
+        const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tb + 4 * g + r;
+          if (t < me) Gt[tb][r] += -bsm * dN[r] * __expf(fminf(Lsm - Ltv[r], 0.f));  // dKK[s][t]
+        }
+      }
+    }
+    colacc = sum_groups(colacc);
+    const bf16x8 p0 = pack(dPt[0], dPt[1]), p1 = pack(dPt[2], dPt[3]);
+    const bf16x8 g0 = pack(Gt[0], Gt[1]), g1 = pack(Gt[2], Gt[3]);
+    const float us = -bsm * eLsm;  // dU[s] = us * drhs[s]
+    const bf16x8 du0 = frag_scaled(Rs, me, 0, g, us), du1 = frag_scaled(Rs, me, 1, g, us);
+    const __bf16* krow = Ks + me * kPitch;
+    const bool s_ok = me < nr;
+    float dw = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      f32x4 acc = zero4(), Y = zero4();
+      if (wl < 2) acc = pgn_mfma(frag(QT, 16 * dt + i, 0, g), p0, acc);
+      acc = pgn_mfma(frag(QT, 16 * dt + i, 1, g), p1, acc);
+      acc = pgn_mfma(frag(KT, 16 * dt + i, 0, g), g0, acc);
+      acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), g1, acc);
+      acc = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), du0, acc);
+      acc = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), du1, acc);
+      Y = pgn_mfma(frag(dSs, 16 * dt + i, 0, g), wf0, Y);
+      Y = pgn_mfma(frag(dSs, 16 * dt + i, 1, g), wf1, Y);
+      const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
+      acc = acc + Y * wsm;
+      if (s_ok) *reinterpret_cast<bf16x4*>(dk + coff + (size_t)me * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
+    }
+    dw = sum_groups(dw);
+    if (g == 0) {
+      colS[me] = colacc;
+      dwv[me] = dw;
+    }
+    // <S_c, dS> over key rows 16 wl ..
+    float sd = 0.f;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = 16 * wl + 4 * g + r;
+        sd += (float)Ss[d * kPitch + 16 * jt + i] * (float)dSs[d * kPitch + 16 * jt + i];
+      }
+    sd = wave_sum(sd);
+    if (x.l == 0) sdot[wl] = sd;
+  }
+  __syncthreads();
+  if (w == 0) {
+    const int t = x.l;
+    const bool ok = t < nr;
+    const size_t ti = (size_t)bh * T + t0 + t;
+    const float r0 = ok ? rsum[ti * 2 + 0] : 0.f, r1 = ok ? rsum[ti * 2 + 1] : 0.f;
+    const float wdw = ws[t] * dwv[t];
+    float dL = rowT[t] - colS[t] + eLs[t] * r1 - wdw;
+    const float tot = wave_sum(wdw);
+    const float a_c = __expf(Ls[C - 1]);
+    if (t == C - 1) dL += tot + a_c * (sdot[0] + sdot[1] + sdot[2] + sdot[3]);
+    dL = rev_scan64(dL, t);
+    if (ok) {
+      dla[ti] = dL;
+      dbe[ti] = r0 + dbe2[t];
+    }
+  }
+}
+
+constexpr size_t kChainSmem = 9 * TILE * sizeof(__bf16) + (4 * C + 8 * C) * sizeof(float);
+constexpr size_t kLocalSmem = 9 * TILE * sizeof(__bf16) + (9 * C + 4) * sizeof(float);
+
+bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
+  if (B <= 0 || H <= 0 || T <= 0) return false;
+  if (B * H >= ((int64_t)1 << 24) || T >= ((int64_t)1 << 28)) return false;
+  if (B * H * ((T + C - 1) / C) >= ((int64_t)1 << 31)) return false;
+  return D == DK && Cc == C;
+}
+
+int set_smem(const void* fn, size_t bytes, bool& done) {
+  if (done) return 0;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess) return (int)e;
+  done = true;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int64_t pragnosia_aspin_delta_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D,
+                                                             int64_t chunk) {
+  if (!shape_ok(B, H, T, D, chunk)) return -1;
+  const int64_t NC = (T + C - 1) / C;
+  const int64_t drhs = B * H * T * DK * 2, dsc = B * H * NC * DK * DK * 2, rs = B * H * T * 2 * 4;
+  return ((drhs + 255) / 256) * 256 + ((dsc + 255) / 256) * 256 + rs;
+}
+
+extern "C" int pragnosia_aspin_delta_fwd(const void* q, const void* k, const void* v, const float* la,
+                                         const float* beta, const float* S0, void* o, float* S_final, void* sent,
+                                         void* W, void* X, int64_t B, int64_t H, int64_t T, int64_t D,
+                                         int64_t chunk, void* stream) {
+  if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
+  PGN_CHECK_ARG(q && k && v && la && beta && o && S_final && W && X);
+  const int NC = (int)((T + C - 1) / C);
+  const int nbh = (int)(B * H);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(aspin_delta_inv, dim3((unsigned)(nbh * NC)), dim3(64), 0, st, (const __bf16*)k, la, beta,
+                     (__bf16*)X, (int)T, NC);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(aspin_delta_fwd, dim3((unsigned)nbh), dim3(256), 0, st, (const __bf16*)q, (const __bf16*)k,
+                     (const __bf16*)v, la, beta, (const __bf16*)X, S0, (__bf16*)o, (__bf16*)W, S_final,
+                     (__bf16*)sent, (int)T, NC);
+  PGN_RETURN_LAUNCH();
+}
+
+extern "C" int pragnosia_aspin_delta_bwd(const void* q, const void* k, const void* v, const float* la,
+                                         const float* beta, const void* sent, const void* W, const void* X,
+                                         const void* dO, const float* dS_final, void* dq, void* dk, void* dv,
+                                         float* dla, float* dbeta, float* dS0, void* workspace,
+                                         int64_t workspace_bytes, int64_t B, int64_t H, int64_t T, int64_t D,
+                                         int64_t chunk, void* stream) {
+  if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
+  PGN_CHECK_ARG(q && k && v && la && beta && sent && W && X && dO && dq && dk && dv && dla && dbeta && workspace);
+  const int64_t need = pragnosia_aspin_delta_bwd_workspace_bytes(B, H, T, D, chunk);
+  PGN_CHECK_ARG(workspace_bytes >= need);
+  static bool chain_set = false, local_set = false;
+  int rc = set_smem((const void*)aspin_delta_bwd_chain, kChainSmem, chain_set);
+  if (rc) return rc;
+  rc = set_smem((const void*)aspin_delta_bwd_local, kLocalSmem, local_set);
+  if (rc) return rc;
+  const int NC = (int)((T + C - 1) / C);
+  const int nbh = (int)(B * H);
+  unsigned char* ws = (unsigned char*)workspace;
+  __bf16* drhs = (__bf16*)ws;
+  __bf16* dsc = (__bf16*)(ws + ((B * H * T * DK * 2 + 255) / 256) * 256);
+  float* rs = (float*)((unsigned char*)dsc + ((B * H * NC * DK * DK * 2 + 255) / 256) * 256);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(aspin_delta_bwd_chain, dim3((unsigned)nbh), dim3(256), kChainSmem, st, (const __bf16*)q,
+                     (const __bf16*)k, (const __bf16*)v, la, beta, (const __bf16*)X, (const __bf16*)sent,
+                     (const __bf16*)dO, dS_final, (__bf16*)dv, drhs, dsc, rs, dS0, (int)T, NC);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(aspin_delta_bwd_local, dim3((unsigned)(nbh * NC)), dim3(512), kLocalSmem, st,
+                     (const __bf16*)q, (const __bf16*)k, la, beta, (const __bf16*)W, (const __bf16*)sent,
+                     (const __bf16*)dO, drhs, dsc, rs, (__bf16*)dq, (__bf16*)dk, dla, dbeta, (int)T, NC);
+  PGN_RETURN_LAUNCH();
+}

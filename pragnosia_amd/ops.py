@@ -185,3 +185,90 @@ def _aspin_backward(ctx, do, dS, _dsent):
 
 
 aspin_chunk.register_autograd(_aspin_backward, setup_context=_aspin_setup)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# aspin chunked scan, delta rule: replaces delta_scan_kernel and its ops, src/assoc_kernel.py:332-704
+@torch.library.custom_op("pragnosia::aspin_delta", mutates_args=())
+def aspin_delta(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor, S0: Optional[Tensor],
+                want_sent: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Delta-rule chunked scan. q, k, v (B, H, T, 64) (cast to bf16), la and beta (B, H, T) fp32, S0 (B, H, 64, 64)
+    fp32 or None. Returns (o bf16, S_final fp32, sent bf16 (B, H, NC, 64, 64) or empty, W bf16 (B, H, T, 64),
+    X bf16 (B, H, NC, 64, 64)); W and X are the intermediates the backward reads (not differentiable)."""
+    _require_gpu(q, k, v, la, beta, S0)
+    q, k, v, la, beta, S0 = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(beta), _f32(S0)
+    B, H, T, D = q.shape
+    NC = (T + CHUNK - 1) // CHUNK
+    dev = q.device
+    o = torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
+    S = torch.empty(B, H, D, D, device=dev, dtype=torch.float32)
+    sent = (torch.empty(B, H, NC, D, D, device=dev, dtype=torch.bfloat16) if want_sent
+            else q.new_empty(0, dtype=torch.bfloat16))
+    W = torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
+    X = torch.empty(B, H, NC, CHUNK, CHUNK, device=dev, dtype=torch.bfloat16)
+    check(lib().pragnosia_aspin_delta_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(beta), _ptr(S0), _ptr(o),
+                                          _ptr(S), _ptr(sent) if want_sent else None, _ptr(W), _ptr(X),
+                                          B, H, T, D, CHUNK, _stream(q)), "pragnosia_aspin_delta_fwd")
+    return o, S, sent, W, X
+
+
+@aspin_delta.register_fake
+def _(q, k, v, la, beta, S0, want_sent):
+    B, H, T, D = q.shape
+    NC = (T + CHUNK - 1) // CHUNK
+    b = lambda *s: q.new_empty(*s, dtype=torch.bfloat16)
+    sent = b(B, H, NC, D, D) if want_sent else b(0)
+    return b(B, H, T, D), q.new_empty(B, H, D, D, dtype=torch.float32), sent, b(B, H, T, D), b(B, H, NC, CHUNK, CHUNK)
+
+
+@torch.library.custom_op("pragnosia::aspin_delta_bwd", mutates_args=())
+def aspin_delta_bwd(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor, sent: Tensor, W: Tensor, X: Tensor,
+                    do: Tensor, dS: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Backward of aspin_delta. Returns (dq, dk, dv bf16, dla fp32, dbeta fp32, dS0 fp32)."""
+    _require_gpu(q, k, v, la, beta, sent, W, X, do, dS)
+    q, k, v, la, beta = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(beta)
+    sent, W, X, do, dS = _bf16(sent), _bf16(W), _bf16(X), _bf16(do), _f32(dS)
+    B, H, T, D = q.shape
+    dev = q.device
+    dq, dk, dv = (torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16) for _ in range(3))
+    dla = torch.empty(B, H, T, device=dev, dtype=torch.float32)
+    dbeta = torch.empty(B, H, T, device=dev, dtype=torch.float32)
+    dS0 = torch.empty(B, H, D, D, device=dev, dtype=torch.float32)
+    nbytes = lib().pragnosia_aspin_delta_bwd_workspace_bytes(B, H, T, D, CHUNK)
+    if nbytes < 0:
+        raise PragnosiaError(f"aspin_delta_bwd: shape {tuple(q.shape)} rejected")
+    ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+    check(lib().pragnosia_aspin_delta_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(beta), _ptr(sent), _ptr(W),
+                                          _ptr(X), _ptr(do), _ptr(dS), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla),
+                                          _ptr(dbeta), _ptr(dS0), _ptr(ws), nbytes, B, H, T, D, CHUNK, _stream(q)),
+          "pragnosia_aspin_delta_bwd")
+    return dq, dk, dv, dla, dbeta, dS0
+
+
+@aspin_delta_bwd.register_fake
+def _(q, k, v, la, beta, sent, W, X, do, dS):
+    B, H, T, D = q.shape
+    b = lambda *s: q.new_empty(*s, dtype=torch.bfloat16)
+    f = lambda *s: q.new_empty(*s, dtype=torch.float32)
+    return b(B, H, T, D), b(B, H, T, D), b(B, H, T, D), f(B, H, T), f(B, H, T), f(B, H, D, D)
+
+
+def _delta_setup(ctx, inputs, output):
+    q, k, v, la, beta, S0, want_sent = inputs
+    _, _, sent, W, X = output
+    if sent.numel() == 0 and any(ctx.needs_input_grad[:6]):
+        raise PragnosiaError("aspin_delta: the backward needs the entering states; call with want_sent=True")
+    ctx.has_s0 = S0 is not None
+    ctx.save_for_backward(q, k, v, la, beta, sent, W, X)
+    ctx.mark_non_differentiable(sent, W, X)
+
+
+def _delta_backward(ctx, do, dS, _dsent, _dW, _dX):
+    q, k, v, la, beta, sent, W, X = ctx.saved_tensors
+    if do is None:
+        do = torch.zeros(q.shape, device=q.device, dtype=torch.bfloat16)
+    dq, dk, dv, dla, dbeta, dS0 = aspin_delta_bwd(q, k, v, la, beta, sent, W, X, do.contiguous(), dS)
+    return dq, dk, dv, dla, dbeta, (dS0 if ctx.has_s0 else None), None
+
+
+aspin_delta.register_autograd(_delta_backward, setup_context=_delta_setup)
