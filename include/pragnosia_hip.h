@@ -96,6 +96,52 @@ int pragnosia_aspin_delta_bwd(const void* q, const void* k, const void* v, const
                               float* dS0, void* workspace, int64_t workspace_bytes,
                               int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * The plumbing between the carrier's projections and the scan (head dim D = 64): per (b, t, h) row, unit-normalise
+ * q, k, v (x / max(|x|, 1e-12)), scale k by sigmoid(gate) when `gate` is non-NULL (plain rule), rotate q and k on
+ * interleaved channel pairs (2i, 2i+1) by pos[t] * theta[h, i], cast to bf16 and transpose to the scan layout.
+ * qp, kp, vp: (B, T, H, D), fp32 (in_bf16 = 0) or bf16 (in_bf16 = 1); gate: (B, T, H) fp32 or NULL; theta: (H, D/2)
+ * fp32; pos: (T,) int64. Writes q, k, v: (B, H, T, D) bf16. Replaces `prep_kernel` / `_prep_fwd` of
+ * src/assoc_kernel.py:740-769, :828-891 (torch form src/assoc.py:453-460). */
+int pragnosia_aspin_prep_fwd(const void* qp, const void* kp, const void* vp, const float* gate, const float* theta,
+                             const int64_t* pos, void* q, void* k, void* v, int64_t B, int64_t T, int64_t H,
+                             int64_t D, int in_bf16, void* stream);
+
+/* Rows of the theta-gradient partial buffer of pragnosia_aspin_prep_bwd: (rows, H, D/2) fp32, summed by the caller. */
+int64_t pragnosia_aspin_prep_theta_partials(int64_t B, int64_t T);
+
+/* Backward of pragnosia_aspin_prep_fwd: from dq, dk, dv ((B, H, T, D) bf16) writes dqp, dkp, dvp in the projections'
+ * layout and dtype, dgate ((B, T, H) fp32, required iff gate is non-NULL) and dtheta_partial
+ * ((pragnosia_aspin_prep_theta_partials(B, T), H, D/2) fp32; theta's gradient is its sum over the first dim).
+ * Replaces `_prep_bwd` of src/assoc_kernel.py:772-822, :848-885. */
+int pragnosia_aspin_prep_bwd(const void* qp, const void* kp, const void* vp, const float* gate, const float* theta,
+                             const int64_t* pos, const void* dq, const void* dk, const void* dv, void* dqp,
+                             void* dkp, void* dvp, float* dgate, float* dtheta_partial, int64_t B, int64_t T,
+                             int64_t H, int64_t D, int in_bf16, void* stream);
+
+/* The carried-state rebase of src/assoc.py:399-402: S (B, H, D, D) fp32 with keys on dim 2; key rows (2i, 2i+1) are
+ * rotated by -p0 * theta[h, i], p0 = *p0_dev when p0_dev is non-NULL (a device fp32 scalar, as the graphed decode
+ * keeps it), else the host value p0. S_out must not alias S. */
+int pragnosia_aspin_rebase_fwd(const float* S, const float* theta, const float* p0_dev, float p0, float* S_out,
+                               int64_t B, int64_t H, int64_t D, void* stream);
+
+/* Backward of the rebase: dS = R^T dS_out (if dS is non-NULL) and the theta-gradient partials (B, H, D/2) fp32
+ * (if dtheta_partial is non-NULL; theta's gradient is their sum over B). */
+int pragnosia_aspin_rebase_bwd(const float* S, const float* theta, const float* p0_dev, float p0,
+                               const float* dS_out, float* dS, float* dtheta_partial, int64_t B, int64_t H,
+                               int64_t D, void* stream);
+
+/* The single-token recurrent step of one carrier layer (decode), fused: rebase S by -p0 * theta (as above),
+ * normalise the T = 1 projections qp, kp, vp ((B, H, D) fp32), gate k by sigmoid(gate) (plain rule, gate (B, H) fp32)
+ * or use the write strength beta ((B, H) fp32, delta rule; at most one of gate and beta is non-NULL), decay by
+ * exp(la) (la (B, H) fp32), write, and read o = S_new^T q ((B, H, D) fp32). S_out may alias S (in-place update).
+ * Replaces the T = 1 torch path of AssocCarrier.forward (src/assoc.py:391-411, :502) that `_generate_graphed`
+ * replays (src/bench.py:241-317). */
+int pragnosia_aspin_decode_step(const float* S, float* S_out, const float* qp, const float* kp, const float* vp,
+                                const float* gate, const float* la, const float* beta, const float* theta,
+                                const float* p0_dev, float p0, float* o, int64_t B, int64_t H, int64_t D,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,9 +29,12 @@ def _ln(x, sd, name, eps=1e-5):
     return F.layer_norm(x, (x.shape[-1],), sd[name + ".weight"], sd[name + ".bias"], eps)
 
 
-def _rms(x, weight):
-    """nn.RMSNorm with eps=None: eps = finfo(dtype).eps."""
-    return F.rms_norm(x, (x.shape[-1],), weight, torch.finfo(x.dtype).eps)
+def _rms(x, weight, eps=torch.finfo(torch.float32).eps):
+    """The carrier's per-head `nn.RMSNorm(dk)` (`src/assoc.py:347`). Its eps=None means finfo(input dtype).eps, and
+    the reference model runs it on fp32 activations, so the restatement uses fp32's eps (1.19e-7) whatever dtype it
+    computes in: with fp64's eps a head output row whose mean square is below 1e-7 would be normalised differently
+    from the reference."""
+    return F.rms_norm(x, (x.shape[-1],), weight, eps)
 
 
 def assoc_carrier(sd, x, h0=None, pos0=0, *, heads, delta=False, write_all=False, key_topk=0, la_floor=None,
@@ -122,10 +125,12 @@ def lm_forward_carried(sd, ids, window, *, layers, mixer, heads):
     return logits
 
 
-def greedy_decode(sd, prompt, n, *, layers, mixer, heads):
+def greedy_decode(sd, prompt, n, *, layers, mixer, heads, forced=None):
     """Greedy incremental generation (`src/bench.py:192-239`): the prompt is read in ctx-sized windows with the
     state carried, then each new token is one T=1 step through every layer; the position index is (prefill +
     i) mod ctx and each carrier rebases its state by the previous call's length. prompt (B, P) ids.
+    `forced` (B, n) replaces the argmax by the given tokens (teacher forcing), so a device run can be compared step
+    by step without a near-tie in the argmax sending the two runs down different continuations.
     Returns (tokens (B, n), logits of every step (B, n, V))."""
     ctx = sd["p.weight"].shape[0]
     states = [None] * layers
@@ -140,8 +145,8 @@ def greedy_decode(sd, prompt, n, *, layers, mixer, heads):
         lg = F.linear(_ln(h[:, -1:], sd, "n"), sd["e.weight"])[:, -1]
         pw = x.shape[1] % ctx
     toks, lgs = [], []
-    for _ in range(n):
-        nxt = lg.argmax(-1)
+    for step in range(n):
+        nxt = lg.argmax(-1) if forced is None else forced[:, step]
         toks.append(nxt)
         lgs.append(lg)
         h = F.embedding(nxt[:, None], sd["e.weight"]) + F.embedding(torch.tensor([pw]), sd["p.weight"])

@@ -1,21 +1,248 @@
-"""The associative carrier (aspin / dspin) on the HIP kernels: scan entry points and the AssocCarrier module.
+"""The associative carrier (aspin / dspin) on the HIP kernels: the scan entry points and the AssocCarrier module.
 
-Module and function signatures, parameter names and the state layout follow the reference (`src/assoc.py`), so
-checkpoints and callers (LM, forward_carried, the trainer, the decode loop) use this as a drop-in. Every scan runs
-on the hand-written gfx950 kernels; there is no PyTorch or CPU path."""
+Signatures, parameter names, initialisation and the state layout follow the reference (`src/assoc.py`), so a
+reference state_dict loads unchanged and the callers (LM, forward_carried, the trainer, the decode loop) use this as
+a drop-in. Every scan runs on the hand-written gfx950 kernels behind `torch.ops.pragnosia.*`:
+
+    T > 1 (or any T with autograd):  aspin_rebase (carried state) -> aspin_prep -> aspin_chunk / aspin_delta
+    T = 1 without autograd (decode): aspin_decode_step (rebase, normalise, gate, write and read fused)
+
+The projections, LayerNorm, the decay and write-strength gates, the per-head RMSNorm and the gated output projection
+are torch GEMMs and elementwise ops around them, as in the reference. There is no CPU path: a CPU tensor raises.
+"""
 from __future__ import annotations
 
+import math
+from contextlib import contextmanager
+
 import torch
+import torch.nn as nn
+import torch.nn.functional as F
 
 from . import ops  # noqa: F401  (registers torch.ops.pragnosia.*)
 from ._lib import PragnosiaError
 
+_op = torch.ops.pragnosia
 
-def assoc_scan_hip(q, k, v, logalpha, S0=None, need_sent=True):
-    """Plain rule, chunk 64, head dim 64: the contract of the reference's `assoc_scan_kernel`
-    (`src/assoc_kernel.py:302-323`). q, k, v (B, H, T, D) any float dtype (bf16 inside), logalpha (B, H, T),
-    S0 (B, H, D, D) or None. Returns (o in q's dtype, S_final fp32, sent bf16 (B, H, NC, D, D) or None)."""
-    grad = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, logalpha, S0))
-    want = bool(need_sent or grad)
-    o, S, sent = torch.ops.pragnosia.aspin_chunk(q, k, v, logalpha.float(), None if S0 is None else S0.float(), want)
-    return o.to(q.dtype), S, (sent if need_sent else None)
+# Module switches kept from the reference (`src/assoc.py:272-276`). FUSED_SCAN: skip the per-chunk entering states
+# when no later layer reads them (the reference switched to a third-party fused kernel there; here the same delta
+# kernel runs without writing them). FUSED_PROJ: one GEMM for the delta carrier's five input projections.
+FUSED_SCAN = False
+FUSED_PROJ = False
+
+HEAD_DIM_KERNEL = 64
+_POS_CACHE: dict = {}
+
+
+def rotate(x, theta, pos):
+    """Rotation of interleaved channel pairs (x[..., 2i], x[..., 2i+1]) by angle pos * theta[h, i]
+    (`src/assoc.py:34-39`): x (B, H, T, dk), theta (H, dk/2), pos (T,). A utility with the reference's signature;
+    the module's own rotations run inside the prep, rebase and decode kernels."""
+    ang = pos.reshape(1, 1, -1, 1).to(theta.dtype) * theta.reshape(1, theta.shape[0], 1, theta.shape[1])
+    c, s = torch.cos(ang), torch.sin(ang)
+    even, odd = x[..., 0::2], x[..., 1::2]
+    return torch.stack((even * c - odd * s, even * s + odd * c), dim=-1).flatten(-2)
+
+
+def _positions(T, device, wrap=None):
+    key = (T, str(device), wrap)
+    pos = _POS_CACHE.get(key)
+    if pos is None:
+        pos = torch.arange(T, device=device, dtype=torch.int64)
+        if wrap:
+            pos = pos % wrap
+        _POS_CACHE[key] = pos
+    return pos
+
+
+def _needs_grad(*ts):
+    return torch.is_grad_enabled() and any(t is not None and torch.is_tensor(t) and t.requires_grad for t in ts)
+
+
+def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = False, mm=None, beta=None,
+               kernel=True, need_sent: bool = False):
+    """The reference's dispatcher (`src/assoc.py:254-269`) on the HIP kernels: o_t = S_t^T q_t with
+    S_t = a_t S_{t-1} + k_t v_t^T (plain) or the delta rule when `beta` is given.
+
+    q, k, v: (B, H, T, 64); logalpha, beta: (B, H, T); S0: (B, H, 64, 64) or None. The kernels tile time in chunks
+    of 64 whatever `chunk` says: the result does not depend on the chunk size (the reference's own test), so the
+    argument is accepted for signature compatibility, as are `recompute` and `mm` (operands are bf16, accumulation
+    and state fp32). Returns (o in q's dtype, S_final fp32), plus the bf16 entering states when need_sent."""
+    if q.shape[-1] != HEAD_DIM_KERNEL:
+        raise PragnosiaError(f"assoc_scan: head dim {q.shape[-1]} is not supported by the HIP kernels (64 only)")
+    want = bool(need_sent or _needs_grad(q, k, v, logalpha, S0, beta))
+    S0 = None if S0 is None else S0.float()
+    if beta is None:
+        o, S, sent = _op.aspin_chunk(q, k, v, logalpha.float(), S0, want)
+    else:
+        o, S, sent, _, _ = _op.aspin_delta(q, k, v, logalpha.float(), beta.float(), S0, want)
+    o = o.to(q.dtype) if q.dtype != torch.bfloat16 else o
+    if need_sent:
+        return o, S, sent
+    return o, S
+
+
+def assoc_scan_kernel(q, k, v, logalpha, S0=None, bv: int = 16):
+    """Plain rule; the contract of the reference's `assoc_scan_kernel` (`src/assoc_kernel.py:302-323`):
+    returns (o in q's dtype, S_final fp32, sent bf16 (B, H, NC, 64, 64))."""
+    return assoc_scan(q, k, v, logalpha, S0, need_sent=True)
+
+
+def delta_scan_kernel(q, k, v, logalpha, beta, S0=None, chunk: int = 64, bv: int = 32, bv_bwd: int = 16):
+    """Delta rule; the contract of the reference's `delta_scan_kernel` (`src/assoc_kernel.py:512-546`)."""
+    return assoc_scan(q, k, v, logalpha, S0, beta=beta, need_sent=True)
+
+
+def prep_kernel(qp, kp, vp, gate_logits, theta, pos):
+    """The reference's `prep_kernel` (`src/assoc_kernel.py:888-891`): (B, T, H, D) projections -> bf16 q, k, v in
+    (B, H, T, D), unit-normalised, k gated, q and k rotated by pos * theta."""
+    return _op.aspin_prep(qp, kp, vp, gate_logits, theta, pos)
+
+
+class AssocCarrier(nn.Module):
+    """Per-head key-value outer-product memory with per-token forgetting, learned rotation frequencies and an
+    optional delta write rule (`src/assoc.py:279-512`). Constructor arguments and parameters are the reference's;
+    `kernel` is accepted and ignored (every path is the HIP kernel path). Supported on the kernels: head dim 64,
+    key_topk, hl_floor, write_all, beta_scale, FUSED_PROJ. The short causal convolution (add_short_conv) is not built
+    here and raises."""
+
+    def __init__(self, d: int, heads: int | None = None, chunk: int = 64, recompute: bool = False,
+                 delta: bool = False, head_dim: int | None = None, kernel: bool = True, key_topk: int = 0,
+                 hl_floor: bool = False, write_all: bool = False):
+        super().__init__()
+        self.d, self.recompute, self.delta = d, recompute, delta
+        self.key_topk, self.hl_floor, self.write_all = key_topk, hl_floor, write_all
+        self.need_sent = True
+        self.kernel = kernel
+        self.bv = 32
+        self.h = heads or max(1, d // (head_dim or 64))
+        if d % self.h or (d // self.h) % 2:
+            raise ValueError(f"AssocCarrier: d={d} must split into {self.h} heads of even width")
+        self.dk = d // self.h
+        self.chunk = chunk
+        self.ln = nn.LayerNorm(d)
+        self.q = nn.Linear(d, d, bias=False)
+        self.k = nn.Linear(d, d, bias=False)
+        self.v = nn.Linear(d, d, bias=False)
+        self.o = nn.Linear(d, d, bias=False)
+        self.wa = nn.Linear(d, self.h)
+        nn.init.zeros_(self.wa.weight)
+        nn.init.zeros_(self.wa.bias)
+        self.wi = nn.Linear(d, self.h)
+        if delta:
+            self.wb = nn.Linear(d, self.h)
+        # per-head timescales spread geometrically at init: softplus(0) * exp(A) from 0.1 down to 1e-4
+        self.A = nn.Parameter(torch.linspace(math.log(0.1 / 0.69), math.log(1e-4 / 0.69), self.h))
+        if hl_floor:
+            half_lives = torch.logspace(math.log10(8.0), math.log10(131072.0), self.h)
+            self.register_buffer("la_floor", -math.log(2.0) / half_lives, persistent=False)
+        inv_freq = 10000.0 ** (-torch.arange(0, self.dk, 2).float() / self.dk)
+        self.theta = nn.Parameter(inv_freq.unsqueeze(0).repeat(self.h, 1))
+        self.on = nn.RMSNorm(self.dk)
+        self.gate = nn.Parameter(torch.zeros(()))
+        self.sent = None
+
+    def spectral_parameters(self):
+        return [self.A, self.theta, self.gate]
+
+    def logalpha(self, z):
+        """la = -softplus(W_a z + b) exp(A_h) <= 0 per (b, t, h), floored per head when hl_floor
+        (`src/assoc.py:355-359`)."""
+        la = -F.softplus(self.wa(z)) * torch.exp(self.A)
+        return la.clamp(min=self.la_floor) if self.hl_floor else la
+
+    def add_short_conv(self, K: int):
+        raise PragnosiaError("AssocCarrier.add_short_conv: the short causal convolution is not part of this build")
+
+    def _projections(self, z):
+        B, T, _ = z.shape
+        fused = FUSED_PROJ and self.delta and not self.key_topk
+        if fused:
+            W = torch.cat([self.q.weight, self.k.weight, self.v.weight, self.wa.weight, self.wb.weight])
+            qo, ko, vo, ao, bo = F.linear(z, W).split([self.d, self.d, self.d, self.h, self.h], dim=-1)
+            la = -F.softplus(ao + self.wa.bias) * torch.exp(self.A)
+            if self.hl_floor:
+                la = la.clamp(min=self.la_floor)
+            bt = torch.sigmoid(bo + self.wb.bias)
+            qo, ko, vo = qo.contiguous(), ko.contiguous(), vo.contiguous()
+        else:
+            qo, ko, vo = self.q(z), self.k(z), self.v(z)
+            la = self.logalpha(z)
+            bt = torch.sigmoid(self.wb(z)) if self.delta else None
+        kp = ko.view(B, T, self.h, self.dk)
+        if self.key_topk:
+            keep = torch.zeros_like(kp).scatter_(-1, kp.abs().topk(self.key_topk, dim=-1).indices, 1.0)
+            kp = kp * keep
+        gate = None if (self.delta or self.write_all) else self.wi(z)
+        if bt is not None:
+            if getattr(self, "beta_scale", None) is not None:
+                bt = bt * self.beta_scale.transpose(1, 2).to(bt.dtype)
+            if self.write_all:
+                bt = bt.clamp(min=0.75)
+        return qo.view(B, T, self.h, self.dk), kp, vo.view(B, T, self.h, self.dk), gate, la, bt
+
+    def forward(self, x, h0=None, pos0: int = 0):
+        """x (B, T, d); h0 = (S (B, H, dk, dk) fp32, p0) from a previous call, or None. Returns
+        (x + gated output, (S, p0 + T)); positions restart at 0 every call and the carried state is rebased by -p0."""
+        if self.dk != HEAD_DIM_KERNEL:
+            raise PragnosiaError(f"AssocCarrier: head dim {self.dk} is not supported by the HIP kernels (64 only)")
+        if not x.is_cuda:
+            raise PragnosiaError("AssocCarrier runs on a ROCm GPU only; there is no CPU path")
+        B, T, D = x.shape
+        if h0 is None:
+            S0, p0 = None, pos0
+        elif len(h0) == 3:
+            raise PragnosiaError("AssocCarrier: a short-convolution cache in the state is not supported")
+        else:
+            S0, p0 = h0
+        z = self.ln(x)
+        qp, kp, vp, gate, la, bt = self._projections(z)
+        p_dev = p0.float().reshape(()) if torch.is_tensor(p0) else None
+        p_host = 0.0 if torch.is_tensor(p0) else float(p0)
+        decode = T == 1 and not _needs_grad(x, S0, *self.parameters())
+        if decode:
+            S_prev = S0 if S0 is not None else torch.zeros(B, self.h, self.dk, self.dk, device=x.device)
+            S, o = _op.aspin_decode_step(S_prev, qp.reshape(B, self.h, self.dk), kp.reshape(B, self.h, self.dk),
+                                         vp.reshape(B, self.h, self.dk),
+                                         None if gate is None else gate.reshape(B, self.h),
+                                         la.reshape(B, self.h), None if bt is None else bt.reshape(B, self.h),
+                                         self.theta, p_dev, p_host)
+            o = o.unsqueeze(2).to(qp.dtype)
+            sent = None
+        else:
+            if S0 is not None and (p_dev is not None or p_host != 0.0):
+                S0 = _op.aspin_rebase(S0, self.theta, p_dev, p_host)
+            pos = _positions(T, x.device, getattr(self, "pos_wrap", None))
+            q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
+            want = bool(self.need_sent or not (FUSED_SCAN and self.delta) or
+                        _needs_grad(x, S0, *self.parameters()))
+            if self.delta:
+                o, S, sent, _, _ = _op.aspin_delta(q, k, v, la.transpose(1, 2).float(),
+                                                   bt.transpose(1, 2).float(), S0, want)
+            else:
+                o, S, sent = _op.aspin_chunk(q, k, v, la.transpose(1, 2).float(), S0, want)
+            o = o.to(qp.dtype)
+            sent = sent if want else None
+        self.sent = sent
+        o = self.on(o).transpose(1, 2).reshape(B, T, D)
+        out = x + F.linear(o, self.o.weight * torch.sigmoid(self.gate))
+        # the state is now expressed in this call's positions 0..T-1: the next call rebases it by T
+        return out, (S, p0 * 0 + T if torch.is_tensor(p0) else T)
+
+
+@contextmanager
+def fused_scan(model):
+    """Within the block, carriers skip the per-chunk entering states no later layer reads (`src/assoc.py:518-532`);
+    restores the previous setting on exit."""
+    global FUSED_SCAN
+    prev = FUSED_SCAN
+    saved = [(m, m.need_sent) for m in model.modules() if isinstance(m, AssocCarrier)]
+    FUSED_SCAN = True
+    for m, _ in saved:
+        m.need_sent = False
+    try:
+        yield
+    finally:
+        FUSED_SCAN = prev
+        for m, v in saved:
+            m.need_sent = v

@@ -1,0 +1,289 @@
+// The plumbing between the carrier's projections and the scan, and the carried-state rebase.
+//
+// prep: per (batch, token, head) row of 64 channels: q, k, v are unit-normalised (x / max(|x|, 1e-12)), k is
+// scaled by the write gate sigmoid(g) (plain rule; no gate for the delta rule), q and k are rotated by the angle
+// pos_t * theta[h, i] on interleaved channel pairs (2i, 2i+1), and the three results are cast to bf16 and written in
+// the scan's (B, H, T, D) layout from the projections' (B, T, H, D) layout (the reference's `_prep_fwd`,
+// `src/assoc_kernel.py:740-769`; torch form `src/assoc.py:453-460`). The backward recomputes norms, gate and
+// angles from the same inputs and uses the closed forms (u = x/|x|, r = R u, g the gradient on r):
+//     du = R^T g,   dx = (du - u (u . du)) / |x|,   d(angle) = g2 r1 - g1 r2 per pair,
+// writing the projections' gradients in THEIR layout, the gate's per (b, t, h), and theta's as one partial sum per
+// (batch, 64-token block) that the caller reduces.
+//
+// One workgroup of 256 threads per (batch, head, 64-token block): 32 threads per row (one channel pair each), 8 rows
+// per pass, 8 passes. Row loads are 128 or 256 contiguous bytes; normalisation is a 32-lane butterfly.
+//
+// rebase: S (B, H, Dk, Dv) with keys on dim 2; key rows (2i, 2i+1) are rotated by -p0 * theta[h, i] (the state written
+// at positions up to p0 - 1, re-expressed for a window whose positions restart at 0: `src/assoc.py:399-402`).
+#include "common.h"
+
+namespace {
+
+constexpr int D = 64;
+constexpr int TB = 64;    // tokens per workgroup
+constexpr int ROWS = 8;   // rows per pass
+
+template <typename In>
+PGN_DEVICE float2 ld2(const In* p);
+template <>
+PGN_DEVICE float2 ld2<float>(const float* p) { return *reinterpret_cast<const float2*>(p); }
+template <>
+PGN_DEVICE float2 ld2<__bf16>(const __bf16* p) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+  const bf16x2 x = *reinterpret_cast<const bf16x2*>(p);
+  return make_float2((float)x[0], (float)x[1]);
+}
+
+template <typename Out>
+PGN_DEVICE void st2(Out* p, float a, float b);
+template <>
+PGN_DEVICE void st2<float>(float* p, float a, float b) { *reinterpret_cast<float2*>(p) = make_float2(a, b); }
+template <>
+PGN_DEVICE void st2<__bf16>(__bf16* p, float a, float b) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+  bf16x2 x;
+  x[0] = (__bf16)a;
+  x[1] = (__bf16)b;
+  *reinterpret_cast<bf16x2*>(p) = x;
+}
+
+// sum over the 32 lanes that share a row (lane bits 0..4)
+PGN_DEVICE float sum32(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  x += __shfl_xor(x, 16);
+  return x;
+}
+
+PGN_DEVICE float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+
+template <typename In>
+__global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const In* __restrict__ kp,
+                                                const In* __restrict__ vp, const float* __restrict__ gl,
+                                                const float* __restrict__ theta, const int64_t* __restrict__ pos,
+                                                __bf16* __restrict__ q, __bf16* __restrict__ k,
+                                                __bf16* __restrict__ v, int T, int H, int ntb) {
+  const int blk = blockIdx.x;
+  const int bh = blk / ntb, tb = blk - bh * ntb;
+  const int b = bh / H, h = bh - b * H;
+  const int i = threadIdx.x & 31, rs = threadIdx.x >> 5;
+  const float th = theta[h * (D / 2) + i];
+#pragma unroll 2
+  for (int p = 0; p < TB / ROWS; ++p) {
+    const int t = tb * TB + p * ROWS + rs;
+    if (t >= T) break;
+    const size_t in = (((size_t)b * T + t) * H + h) * D + 2 * i;
+    const size_t out = ((size_t)bh * T + t) * D + 2 * i;
+    const float2 xq = ld2<In>(qp + in), xk = ld2<In>(kp + in), xv = ld2<In>(vp + in);
+    const float nq = sum32(xq.x * xq.x + xq.y * xq.y);
+    const float nk = sum32(xk.x * xk.x + xk.y * xk.y);
+    const float nv = sum32(xv.x * xv.x + xv.y * xv.y);
+    const float iq = 1.f / fmaxf(sqrtf(nq), 1e-12f);
+    float ik = 1.f / fmaxf(sqrtf(nk), 1e-12f);
+    const float iv = 1.f / fmaxf(sqrtf(nv), 1e-12f);
+    if (gl) ik *= sigmoidf_(gl[((size_t)b * T + t) * H + h]);
+    float s, c;
+    sincosf((float)pos[t] * th, &s, &c);
+    st2<__bf16>(q + out, (xq.x * c - xq.y * s) * iq, (xq.x * s + xq.y * c) * iq);
+    st2<__bf16>(k + out, (xk.x * c - xk.y * s) * ik, (xk.x * s + xk.y * c) * ik);
+    st2<__bf16>(v + out, xv.x * iv, xv.y * iv);
+  }
+}
+
+template <typename In>
+__global__ __launch_bounds__(256) void prep_bwd(
+    const In* __restrict__ qp, const In* __restrict__ kp, const In* __restrict__ vp, const float* __restrict__ gl,
+    const float* __restrict__ theta, const int64_t* __restrict__ pos, const __bf16* __restrict__ dq,
+    const __bf16* __restrict__ dk, const __bf16* __restrict__ dv, In* __restrict__ dqp, In* __restrict__ dkp,
+    In* __restrict__ dvp, float* __restrict__ dgl, float* __restrict__ dth, int T, int H, int ntb) {
+  __shared__ float red[ROWS][D / 2];
+  const int blk = blockIdx.x;
+  const int bh = blk / ntb, tb = blk - bh * ntb;
+  const int b = bh / H, h = bh - b * H;
+  const int i = threadIdx.x & 31, rs = threadIdx.x >> 5;
+  const float th = theta[h * (D / 2) + i];
+  float dth_acc = 0.f;
+  for (int p = 0; p < TB / ROWS; ++p) {
+    const int t = tb * TB + p * ROWS + rs;
+    if (t >= T) break;
+    const size_t in = (((size_t)b * T + t) * H + h) * D + 2 * i;
+    const size_t out = ((size_t)bh * T + t) * D + 2 * i;
+    const float pt = (float)pos[t];
+    float s, c;
+    sincosf(pt * th, &s, &c);
+    float dang = 0.f;
+    {  // q: normalise, rotate
+      const float2 x = ld2<In>(qp + in);
+      const float2 gq = ld2<__bf16>(dq + out);
+      const float inv = 1.f / fmaxf(sqrtf(sum32(x.x * x.x + x.y * x.y)), 1e-12f);
+      const float u1 = x.x * inv, u2 = x.y * inv;
+      dang += gq.y * (u1 * c - u2 * s) - gq.x * (u1 * s + u2 * c);
+      const float du1 = gq.x * c + gq.y * s, du2 = gq.y * c - gq.x * s;
+      const float dot = sum32(u1 * du1 + u2 * du2);
+      st2<In>(dqp + in, (du1 - u1 * dot) * inv, (du2 - u2 * dot) * inv);
+    }
+    {  // k: normalise, gate, rotate
+      const float2 x = ld2<In>(kp + in);
+      float2 gk = ld2<__bf16>(dk + out);
+      const float inv = 1.f / fmaxf(sqrtf(sum32(x.x * x.x + x.y * x.y)), 1e-12f);
+      const float u1 = x.x * inv, u2 = x.y * inv;
+      const float r1 = u1 * c - u2 * s, r2 = u1 * s + u2 * c;
+      if (gl) {
+        const float sg = sigmoidf_(gl[((size_t)b * T + t) * H + h]);
+        const float dsg = sum32(gk.x * r1 + gk.y * r2);
+        if (i == 0) dgl[((size_t)b * T + t) * H + h] = dsg * sg * (1.f - sg);
+        gk.x *= sg;
+        gk.y *= sg;
+      }
+      dang += gk.y * r1 - gk.x * r2;
+      const float du1 = gk.x * c + gk.y * s, du2 = gk.y * c - gk.x * s;
+      const float dot = sum32(u1 * du1 + u2 * du2);
+      st2<In>(dkp + in, (du1 - u1 * dot) * inv, (du2 - u2 * dot) * inv);
+    }
+    {  // v: normalise
+      const float2 x = ld2<In>(vp + in);
+      const float2 gv = ld2<__bf16>(dv + out);
+      const float inv = 1.f / fmaxf(sqrtf(sum32(x.x * x.x + x.y * x.y)), 1e-12f);
+      const float u1 = x.x * inv, u2 = x.y * inv;
+      const float dot = sum32(u1 * gv.x + u2 * gv.y);
+      st2<In>(dvp + in, (gv.x - u1 * dot) * inv, (gv.y - u2 * dot) * inv);
+    }
+    dth_acc += dang * pt;
+  }
+  red[rs][i] = dth_acc;
+  __syncthreads();
+  if (threadIdx.x < D / 2) {
+    float a = 0.f;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) a += red[r][threadIdx.x];
+    dth[(((size_t)b * ntb + tb) * H + h) * (D / 2) + threadIdx.x] = a;
+  }
+}
+
+// rebase: one workgroup of 256 threads per (batch, head); thread = (value column j, group of 16 key rows)
+__global__ __launch_bounds__(256) void rebase_fwd(const float* __restrict__ S, const float* __restrict__ theta,
+                                                  const float* __restrict__ p0d, float p0h, float* __restrict__ So,
+                                                  int H) {
+  const int bh = blockIdx.x, h = bh % H;
+  const int j = threadIdx.x & 63, rg = threadIdx.x >> 6;
+  const float p0 = p0d ? *p0d : p0h;
+  const float* src = S + (size_t)bh * D * D;
+  float* dst = So + (size_t)bh * D * D;
+  float x[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) x[r] = src[(16 * rg + r) * D + j];
+#pragma unroll
+  for (int pr = 0; pr < 8; ++pr) {
+    const int ip = 8 * rg + pr;
+    float s, c;
+    sincosf(-p0 * theta[h * (D / 2) + ip], &s, &c);
+    const float a = x[2 * pr], bb = x[2 * pr + 1];
+    dst[(2 * ip) * D + j] = a * c - bb * s;
+    dst[(2 * ip + 1) * D + j] = a * s + bb * c;
+  }
+}
+
+// backward of rebase: dS = R^T g; d(angle) = g2 r1 - g1 r2 summed over value columns, times -p0 for theta
+__global__ __launch_bounds__(256) void rebase_bwd(const float* __restrict__ S, const float* __restrict__ theta,
+                                                  const float* __restrict__ p0d, float p0h,
+                                                  const float* __restrict__ g, float* __restrict__ dS,
+                                                  float* __restrict__ dth, int H) {
+  __shared__ float red[4][64][9];
+  const int bh = blockIdx.x, h = bh % H;
+  const int j = threadIdx.x & 63, rg = threadIdx.x >> 6;
+  const float p0 = p0d ? *p0d : p0h;
+  const size_t off = (size_t)bh * D * D;
+#pragma unroll
+  for (int pr = 0; pr < 8; ++pr) {
+    const int ip = 8 * rg + pr;
+    float s, c;
+    sincosf(-p0 * theta[h * (D / 2) + ip], &s, &c);
+    const float a = S[off + (2 * ip) * D + j], bb = S[off + (2 * ip + 1) * D + j];
+    const float g1 = g[off + (2 * ip) * D + j], g2 = g[off + (2 * ip + 1) * D + j];
+    const float r1 = a * c - bb * s, r2 = a * s + bb * c;
+    if (dS) {
+      dS[off + (2 * ip) * D + j] = g1 * c + g2 * s;
+      dS[off + (2 * ip + 1) * D + j] = g2 * c - g1 * s;
+    }
+    red[rg][j][pr] = (g2 * r1 - g1 * r2) * (-p0);
+  }
+  __syncthreads();
+  if (dth && threadIdx.x < D / 2) {
+    const int ip = threadIdx.x, rgi = ip >> 3, pr = ip & 7;
+    float acc = 0.f;
+    for (int jj = 0; jj < 64; ++jj) acc += red[rgi][jj][pr];
+    dth[(size_t)bh * (D / 2) + ip] = acc;
+  }
+}
+
+bool shape_ok(int64_t B, int64_t T, int64_t H) {
+  return B > 0 && T > 0 && H > 0 && B * H * ((T + TB - 1) / TB) < ((int64_t)1 << 31) && B * T * H < ((int64_t)1 << 40);
+}
+
+}  // namespace
+
+extern "C" int pragnosia_aspin_prep_fwd(const void* qp, const void* kp, const void* vp, const float* gate,
+                                        const float* theta, const int64_t* pos, void* q, void* k, void* v,
+                                        int64_t B, int64_t T, int64_t H, int64_t Dh, int in_bf16, void* stream) {
+  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(shape_ok(B, T, H));
+  PGN_CHECK_ARG(qp && kp && vp && theta && pos && q && k && v);
+  const int ntb = (int)((T + TB - 1) / TB);
+  const dim3 grid((unsigned)(B * H * ntb));
+  hipStream_t st = (hipStream_t)stream;
+  if (in_bf16)
+    hipLaunchKernelGGL(prep_fwd<__bf16>, grid, dim3(256), 0, st, (const __bf16*)qp, (const __bf16*)kp,
+                       (const __bf16*)vp, gate, theta, pos, (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb);
+  else
+    hipLaunchKernelGGL(prep_fwd<float>, grid, dim3(256), 0, st, (const float*)qp, (const float*)kp,
+                       (const float*)vp, gate, theta, pos, (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb);
+  PGN_RETURN_LAUNCH();
+}
+
+extern "C" int64_t pragnosia_aspin_prep_theta_partials(int64_t B, int64_t T) { return B * ((T + TB - 1) / TB); }
+
+extern "C" int pragnosia_aspin_prep_bwd(const void* qp, const void* kp, const void* vp, const float* gate,
+                                        const float* theta, const int64_t* pos, const void* dq, const void* dk,
+                                        const void* dv, void* dqp, void* dkp, void* dvp, float* dgate,
+                                        float* dtheta_partial, int64_t B, int64_t T, int64_t H, int64_t Dh,
+                                        int in_bf16, void* stream) {
+  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(shape_ok(B, T, H));
+  PGN_CHECK_ARG(qp && kp && vp && theta && pos && dq && dk && dv && dqp && dkp && dvp && dtheta_partial);
+  PGN_CHECK_ARG(gate == nullptr || dgate != nullptr);
+  const int ntb = (int)((T + TB - 1) / TB);
+  const dim3 grid((unsigned)(B * H * ntb));
+  hipStream_t st = (hipStream_t)stream;
+  if (in_bf16)
+    hipLaunchKernelGGL(prep_bwd<__bf16>, grid, dim3(256), 0, st, (const __bf16*)qp, (const __bf16*)kp,
+                       (const __bf16*)vp, gate, theta, pos, (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv,
+                       (__bf16*)dqp, (__bf16*)dkp, (__bf16*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb);
+  else
+    hipLaunchKernelGGL(prep_bwd<float>, grid, dim3(256), 0, st, (const float*)qp, (const float*)kp,
+                       (const float*)vp, gate, theta, pos, (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv,
+                       (float*)dqp, (float*)dkp, (float*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb);
+  PGN_RETURN_LAUNCH();
+}
+
+extern "C" int pragnosia_aspin_rebase_fwd(const float* S, const float* theta, const float* p0_dev, float p0,
+                                          float* S_out, int64_t B, int64_t H, int64_t Dh, void* stream) {
+  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(B > 0 && H > 0 && B * H < ((int64_t)1 << 31));
+  PGN_CHECK_ARG(S && theta && S_out && S != S_out);
+  hipLaunchKernelGGL(rebase_fwd, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, theta, p0_dev, p0,
+                     S_out, (int)H);
+  PGN_RETURN_LAUNCH();
+}
+
+extern "C" int pragnosia_aspin_rebase_bwd(const float* S, const float* theta, const float* p0_dev, float p0,
+                                          const float* dS_out, float* dS, float* dtheta_partial, int64_t B,
+                                          int64_t H, int64_t Dh, void* stream) {
+  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(B > 0 && H > 0 && B * H < ((int64_t)1 << 31));
+  PGN_CHECK_ARG(S && theta && dS_out);
+  hipLaunchKernelGGL(rebase_bwd, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, theta, p0_dev, p0,
+                     dS_out, dS, dtheta_partial, (int)H);
+  PGN_RETURN_LAUNCH();
+}

@@ -272,3 +272,164 @@ def _delta_backward(ctx, do, dS, _dsent, _dW, _dX):
 
 
 aspin_delta.register_autograd(_delta_backward, setup_context=_delta_setup)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# prep (normalise, gate, rotate, cast, transpose): replaces prep_kernel and its ops, src/assoc_kernel.py:740-891
+def _proj(t: Tensor) -> Tensor:
+    if t.dtype not in (torch.float32, torch.bfloat16):
+        t = t.float()
+    return t.contiguous()
+
+
+@torch.library.custom_op("pragnosia::aspin_prep", mutates_args=())
+def aspin_prep(qp: Tensor, kp: Tensor, vp: Tensor, gate: Optional[Tensor], theta: Tensor,
+               pos: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """qp, kp, vp (B, T, H, 64) fp32 or bf16 projections; gate (B, T, H) logits or None; theta (H, 32); pos (T,)
+    int64. Returns bf16 q, k, v in (B, H, T, 64)."""
+    _require_gpu(qp, kp, vp, gate, theta, pos)
+    qp, kp, vp = _proj(qp), _proj(kp).to(qp.dtype), _proj(vp).to(qp.dtype)
+    gate, theta, pos = _f32(gate), _f32(theta), pos.to(torch.int64).contiguous()
+    B, T, H, D = qp.shape
+    q, k, v = (torch.empty(B, H, T, D, device=qp.device, dtype=torch.bfloat16) for _ in range(3))
+    check(lib().pragnosia_aspin_prep_fwd(_ptr(qp), _ptr(kp), _ptr(vp), _ptr(gate), _ptr(theta), _ptr(pos), _ptr(q),
+                                         _ptr(k), _ptr(v), B, T, H, D, int(qp.dtype == torch.bfloat16),
+                                         _stream(qp)), "pragnosia_aspin_prep_fwd")
+    return q, k, v
+
+
+@aspin_prep.register_fake
+def _(qp, kp, vp, gate, theta, pos):
+    B, T, H, D = qp.shape
+    return tuple(qp.new_empty(B, H, T, D, dtype=torch.bfloat16) for _ in range(3))
+
+
+@torch.library.custom_op("pragnosia::aspin_prep_bwd", mutates_args=())
+def aspin_prep_bwd(qp: Tensor, kp: Tensor, vp: Tensor, gate: Optional[Tensor], theta: Tensor, pos: Tensor,
+                   dq: Tensor, dk: Tensor, dv: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Returns (dqp, dkp, dvp in the projections' dtype, dgate fp32 (B, T, H) or empty, dtheta fp32 (H, 32))."""
+    _require_gpu(qp, kp, vp, gate, theta, pos, dq, dk, dv)
+    qp, kp, vp = _proj(qp), _proj(kp).to(qp.dtype), _proj(vp).to(qp.dtype)
+    gate, theta, pos = _f32(gate), _f32(theta), pos.to(torch.int64).contiguous()
+    dq, dk, dv = _bf16(dq), _bf16(dk), _bf16(dv)
+    B, T, H, D = qp.shape
+    dqp, dkp, dvp = torch.empty_like(qp), torch.empty_like(qp), torch.empty_like(qp)
+    dgate = torch.empty(B, T, H, device=qp.device) if gate is not None else qp.new_empty(0, dtype=torch.float32)
+    rows = lib().pragnosia_aspin_prep_theta_partials(B, T)
+    dth = torch.empty(rows, H, D // 2, device=qp.device, dtype=torch.float32)
+    check(lib().pragnosia_aspin_prep_bwd(_ptr(qp), _ptr(kp), _ptr(vp), _ptr(gate), _ptr(theta), _ptr(pos), _ptr(dq),
+                                         _ptr(dk), _ptr(dv), _ptr(dqp), _ptr(dkp), _ptr(dvp),
+                                         _ptr(dgate) if gate is not None else None, _ptr(dth), B, T, H, D,
+                                         int(qp.dtype == torch.bfloat16), _stream(qp)), "pragnosia_aspin_prep_bwd")
+    return dqp, dkp, dvp, dgate, dth.sum(0)
+
+
+@aspin_prep_bwd.register_fake
+def _(qp, kp, vp, gate, theta, pos, dq, dk, dv):
+    B, T, H, D = qp.shape
+    dg = qp.new_empty(B, T, H, dtype=torch.float32) if gate is not None else qp.new_empty(0, dtype=torch.float32)
+    return (torch.empty_like(qp), torch.empty_like(qp), torch.empty_like(qp), dg,
+            qp.new_empty(H, D // 2, dtype=torch.float32))
+
+
+def _prep_setup(ctx, inputs, output):
+    qp, kp, vp, gate, theta, pos = inputs
+    ctx.has_gate = gate is not None
+    ctx.dtypes = (qp.dtype, kp.dtype, vp.dtype, None if gate is None else gate.dtype, theta.dtype)
+    ctx.save_for_backward(qp, kp, vp, gate, theta, pos)
+
+
+def _prep_backward(ctx, dq, dk, dv):
+    qp, kp, vp, gate, theta, pos = ctx.saved_tensors
+    z = lambda t, ref: torch.zeros(ref.shape[0], ref.shape[2], ref.shape[1], ref.shape[3], device=ref.device,
+                                   dtype=torch.bfloat16) if t is None else t
+    dq, dk, dv = z(dq, qp), z(dk, qp), z(dv, qp)
+    dqp, dkp, dvp, dgate, dth = aspin_prep_bwd(qp, kp, vp, gate, theta, pos, dq, dk, dv)
+    dt = ctx.dtypes
+    return (dqp.to(dt[0]), dkp.to(dt[1]), dvp.to(dt[2]), (dgate.to(dt[3]) if ctx.has_gate else None),
+            dth.to(dt[4]), None)
+
+
+aspin_prep.register_autograd(_prep_backward, setup_context=_prep_setup)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# carried-state rebase: replaces the rotate() of S0's key rows at src/assoc.py:399-402
+@torch.library.custom_op("pragnosia::aspin_rebase", mutates_args=())
+def aspin_rebase(S: Tensor, theta: Tensor, p0_dev: Optional[Tensor], p0: float) -> Tensor:
+    """Key rows (2i, 2i+1) of S (B, H, 64, 64) rotated by -p0 * theta[h, i]; p0 from the device scalar p0_dev when
+    given, else the float p0."""
+    _require_gpu(S, theta, p0_dev)
+    S, theta, p0_dev = _f32(S), _f32(theta), _f32(p0_dev)
+    B, H, D, _ = S.shape
+    out = torch.empty_like(S)
+    check(lib().pragnosia_aspin_rebase_fwd(_ptr(S), _ptr(theta), _ptr(p0_dev), float(p0), _ptr(out), B, H, D,
+                                           _stream(S)), "pragnosia_aspin_rebase_fwd")
+    return out
+
+
+@aspin_rebase.register_fake
+def _(S, theta, p0_dev, p0):
+    return torch.empty_like(S, dtype=torch.float32)
+
+
+@torch.library.custom_op("pragnosia::aspin_rebase_bwd", mutates_args=())
+def aspin_rebase_bwd(S: Tensor, theta: Tensor, p0_dev: Optional[Tensor], p0: float,
+                     g: Tensor) -> tuple[Tensor, Tensor]:
+    _require_gpu(S, theta, p0_dev, g)
+    S, theta, p0_dev, g = _f32(S), _f32(theta), _f32(p0_dev), _f32(g)
+    B, H, D, _ = S.shape
+    dS = torch.empty_like(S)
+    dth = torch.empty(B, H, D // 2, device=S.device, dtype=torch.float32)
+    check(lib().pragnosia_aspin_rebase_bwd(_ptr(S), _ptr(theta), _ptr(p0_dev), float(p0), _ptr(g), _ptr(dS),
+                                           _ptr(dth), B, H, D, _stream(S)), "pragnosia_aspin_rebase_bwd")
+    return dS, dth.sum(0)
+
+
+@aspin_rebase_bwd.register_fake
+def _(S, theta, p0_dev, p0, g):
+    B, H, D, _ = S.shape
+    return torch.empty_like(S, dtype=torch.float32), S.new_empty(H, D // 2, dtype=torch.float32)
+
+
+def _rebase_setup(ctx, inputs, output):
+    S, theta, p0_dev, p0 = inputs
+    ctx.p0 = p0
+    ctx.dtypes = (S.dtype, theta.dtype)
+    ctx.save_for_backward(S, theta, p0_dev)
+
+
+def _rebase_backward(ctx, g):
+    S, theta, p0_dev = ctx.saved_tensors
+    dS, dth = aspin_rebase_bwd(S, theta, p0_dev, ctx.p0, g.contiguous())
+    return dS.to(ctx.dtypes[0]), dth.to(ctx.dtypes[1]), None, None
+
+
+aspin_rebase.register_autograd(_rebase_backward, setup_context=_rebase_setup)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the single-token recurrent step (decode): replaces the T = 1 torch path of src/assoc.py:391-411, :502
+@torch.library.custom_op("pragnosia::aspin_decode_step", mutates_args=())
+def aspin_decode_step(S: Tensor, qp: Tensor, kp: Tensor, vp: Tensor, gate: Optional[Tensor], la: Tensor,
+                      beta: Optional[Tensor], theta: Tensor, p0_dev: Optional[Tensor],
+                      p0: float) -> tuple[Tensor, Tensor]:
+    """S (B, H, 64, 64) fp32 carried state; qp, kp, vp (B, H, 64) the T = 1 projections; gate (B, H) write-gate
+    logits (plain rule) or None; la (B, H) log-decay; beta (B, H) write strength (delta rule) or None; theta (H, 32).
+    Returns (S_new fp32, o (B, H, 64) fp32). Not differentiable (decode runs without autograd)."""
+    _require_gpu(S, qp, kp, vp, gate, la, beta, theta, p0_dev)
+    S, qp, kp, vp, gate = _f32(S), _f32(qp), _f32(kp), _f32(vp), _f32(gate)
+    la, beta, theta, p0_dev = _f32(la), _f32(beta), _f32(theta), _f32(p0_dev)
+    B, H, D, _ = S.shape
+    S_new = torch.empty_like(S)
+    o = torch.empty(B, H, D, device=S.device, dtype=torch.float32)
+    check(lib().pragnosia_aspin_decode_step(_ptr(S), _ptr(S_new), _ptr(qp), _ptr(kp), _ptr(vp), _ptr(gate), _ptr(la),
+                                            _ptr(beta), _ptr(theta), _ptr(p0_dev), float(p0), _ptr(o), B, H, D,
+                                            _stream(S)), "pragnosia_aspin_decode_step")
+    return S_new, o
+
+
+@aspin_decode_step.register_fake
+def _(S, qp, kp, vp, gate, la, beta, theta, p0_dev, p0):
+    B, H, D, _ = S.shape
+    return torch.empty_like(S, dtype=torch.float32), S.new_empty(B, H, D, dtype=torch.float32)
