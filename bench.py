@@ -181,6 +181,98 @@ def diag_bench(steps):
             "hbm_frac": round((fb + bb) / (t_fwd + t_bwd) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def carried_bench():
+    """B2 T8192 H12 D64 bf16 inputs, la = logsigmoid(N(4,1)); (i) 16 windows of 512 with the
+    fp32 state carried and rebased by -512 theta between windows (positions restart per window, as
+    AssocCarrier.forward does), (ii) one unsplit T = 8192 pass. Forward only. Reports the carried path's
+    whole-sequence throughput and the carried-vs-unsplit error on every output and on the final state."""
+    import torch
+    import torch.nn.functional as F
+    from pragnosia_amd import ops  # noqa: F401
+    from pragnosia_amd.assoc import rotate
+    B, H, T, D, W = 2, 12, 8192, 64, 512
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(B, H, T, D, generator=g)
+    k = F.normalize(torch.randn(B, H, T, D, generator=g), dim=-1)
+    v = torch.randn(B, H, T, D, generator=g)
+    la = F.logsigmoid(torch.randn(B, H, T, generator=g) + 4.0)
+    th = torch.rand(H, D // 2, generator=g) * 0.1
+    q, k, v, la, th = (t.to(dev) for t in (q, k, v, la, th))
+    loc = torch.arange(T, device=dev) % W
+    glob = torch.arange(T, device=dev)
+    qw, kw = rotate(q, th, loc).bfloat16(), rotate(k, th, loc).bfloat16()
+    qg, kg = rotate(q, th, glob).bfloat16(), rotate(k, th, glob).bfloat16()
+    vb = v.bfloat16()
+    op = torch.ops.pragnosia
+
+    def carried():
+        S, outs = None, []
+        for s in range(0, T, W):
+            if S is not None:
+                S = op.aspin_rebase(S, th, None, float(W))
+            o, S, _ = op.aspin_chunk(qw[:, :, s:s + W], kw[:, :, s:s + W], vb[:, :, s:s + W], la[:, :, s:s + W],
+                                     S, False)
+            outs.append(o)
+        return torch.cat(outs, 2), S
+
+    with torch.no_grad():
+        for _ in range(3):
+            carried()
+        torch.cuda.synchronize()
+        n = 20
+        t0 = time.perf_counter()
+        for _ in range(n):
+            oc, Sc = carried()
+        torch.cuda.synchronize()
+        t_c = (time.perf_counter() - t0) / n
+        ou, Su, _ = op.aspin_chunk(qg, kg, vb, la, None, False)
+        Su_loc = op.aspin_rebase(Su, th, None, float(T - W))
+    rel = lambda a, b: ((a.float() - b.float()).abs().max() / b.float().abs().max()).item()
+    return {"workload": "aspin carried long context, 16 windows x 512 vs one T8192 pass, B2 H12 D64 (configs[3])",
+            "carried_Mtok_s": round(B * T / t_c / 1e6, 3), "carried_ms": round(t_c * 1e3, 4),
+            "carried_vs_unsplit_rel_err_o": round(rel(oc, ou), 6),
+            "carried_vs_unsplit_rel_err_S": round(rel(Sc, Su_loc), 6)}
+
+
+def decode_bench(n_tokens=1024):
+    """LM(vocab 8192, d 768, 12 layers, 12 heads of 64, ctx 512, aspin), random-init weights
+    N(0, 0.02) (fp32), prefill of 512 random ids, then greedy decode through the graph-captured recurrent step, at
+    batch 1 and batch 64. ms/token = wall time of the decode loop / decode steps."""
+    import torch
+    from pragnosia_amd.decode import GreedyDecoder
+    from pragnosia_amd.model import LM
+    torch.manual_seed(4)
+    m = LM(vocab=8192, d=768, layers=12, mlp_mult=4, ctx=512, mixer="aspin").cuda().eval()
+    n_params = sum(p.numel() for p in m.parameters())
+    weight_bytes = 4 * (n_params - m.p.weight.numel())
+    state_bytes = 12 * 12 * 64 * 64 * 4
+    out = {"workload": "78M-class aspin LM greedy decode (d768 L12 H12x64 V8192 ctx512, fp32), prefill 512 "
+                       "(configs[4])", "params": n_params}
+    g = torch.Generator().manual_seed(4)
+    for B in (1, 64):
+        prompt = torch.randint(0, 8192, (B, 512), generator=g).cuda()
+        dec = GreedyDecoder(m, B, steps_per_graph=8)
+        with torch.no_grad():
+            states, pw, lg = dec.prefill(prompt)
+            dec.start(states, pw, lg, n_tokens)
+            dec.replay(65)
+            torch.cuda.synchronize()
+            dec.start(states, pw, lg, n_tokens)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            dec.replay(n_tokens)
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+        steps = -(-(n_tokens - 1) // dec.K) * dec.K
+        per = dt / steps
+        step_bytes = weight_bytes + 2 * state_bytes * B
+        out[f"bs{B}"] = {"ms_per_step": round(per * 1e3, 4), "tok_s": round(B / per, 1),
+                         "GBs": round(step_bytes / per / 1e9, 1), "hbm_frac": round(step_bytes / per / 1e9 / HBM_PEAK_GBS, 4)}
+    out["ms_per_token_bs1"] = out["bs1"]["ms_per_step"]
+    return out
+
+
 def summarize(r, rule):
     tokens = r["B"] * r["T"]
     dom = (r["names"][1], r["t_bwd"], r["bwd_bytes"], r["bwd_flops"]) if r["t_bwd"] >= r["t_fwd"] else \
@@ -225,6 +317,9 @@ def gpu_bench(args):
             "fwd_bwd_GBs": round((o["fwd_bytes"] + o["bwd_bytes"]) / (o["t_fwd"] + o["t_bwd"]) / 1e9, 1),
             "fwd_bwd_mfma_tflops": round((o["fwd_flops"] + o["bwd_flops"]) / (o["t_fwd"] + o["t_bwd"]) / 1e12, 2)}}
         sec["diag_scan"] = diag_bench(args.steps)
+        sec["carried"] = carried_bench()
+        sec["decode"] = decode_bench()
+        res["decode_ms_per_token_bs1"] = sec["decode"]["ms_per_token_bs1"]
         res["secondary"] = sec
     return res
 

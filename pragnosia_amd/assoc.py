@@ -225,7 +225,12 @@ class AssocCarrier(nn.Module):
             sent = sent if want else None
         self.sent = sent
         o = self.on(o).transpose(1, 2).reshape(B, T, D)
-        out = x + F.linear(o, self.o.weight * torch.sigmoid(self.gate))
+        if _needs_grad(x, o, self.o.weight, self.gate):
+            # gate on the weight, as the reference does for training (it keeps the backward's saved tensor small)
+            out = x + F.linear(o, self.o.weight * torch.sigmoid(self.gate))
+        else:
+            # the same function without materialising a gated d x d weight on every call (decode, inference)
+            out = x + F.linear(o, self.o.weight) * torch.sigmoid(self.gate)
         # the state is now expressed in this call's positions 0..T-1: the next call rebases it by T
         return out, (S, p0 * 0 + T if torch.is_tensor(p0) else T)
 
