@@ -40,6 +40,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="run each hot kernel a fixed number of times (for rocprofv3 counter passes) and exit")
     return ap.parse_args()
 
 
@@ -273,6 +275,22 @@ def decode_bench(n_tokens=1024):
     return out
 
 
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "pmc_traffic_configs.md")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` as measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
+    profiles/pmc_traffic_configs.md (copy-calibrated), or None when the kernel is not in that table."""
+    try:
+        for line in open(TRAFFIC_TABLE):
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 4 and cells[0] == kernel:
+                return int(cells[3])
+    except OSError:
+        return None
+    return None
+
+
 def summarize(r, rule):
     tokens = r["B"] * r["T"]
     dom = (r["names"][1], r["t_bwd"], r["bwd_bytes"], r["bwd_flops"]) if r["t_bwd"] >= r["t_fwd"] else \
@@ -300,7 +318,7 @@ def gpu_bench(args):
         "config": {"workload": f"aspin chunked scan fwd+bwd, {args.rule} rule, B16 T512 H12 D64 chunk64 (configs[2])",
                    "B": r["B"], "T": r["T"], "H": r["H"], "D": r["D"], "chunk": r["C"], "rule": args.rule},
         "roofline": {"bound": "hbm", "kernel": dom[0], "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom[0]),
                      "algorithmic_bytes": dom[2], "avg_launch_us": round(dom[1] * 1e6, 2),
                      "mfma_tflops": round(dom[3] / dom[1] / 1e12, 2),
                      "mfma_frac": round(dom[3] / dom[1] / 1e12 / BF16_PEAK_TFLOPS, 4)},
@@ -361,8 +379,46 @@ def cpu_baseline(args):
                       "median"}
 
 
+def profile_kernels(reps=10):
+    """For counter runs under rocprofv3 (--pmc FETCH_SIZE, then WRITE_SIZE): each hot kernel `reps` times at its
+    configs shape, plus a calibration copy of exactly COPY_BYTES read and COPY_BYTES written (a torch copy_ of a
+    contiguous fp32 tensor), so that the counters' bytes per dispatch can be scaled against a known transfer."""
+    import torch
+    from pragnosia_amd import ops  # noqa: F401
+    dev = torch.device("cuda:0")
+    op = torch.ops.pragnosia
+    src = torch.randn(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    for rule in ("plain", "delta"):
+        x = aspin_inputs(16, 12, 512, 64, 2, rule, dev)
+        for _ in range(reps):
+            if rule == "plain":
+                o, S, sent = op.aspin_chunk(x["q"], x["k"], x["v"], x["la"], None, True)
+                op.aspin_chunk_bwd(x["q"], x["k"], x["v"], x["la"], sent, x["do"], x["dS"])
+            else:
+                o, S, sent, W, X = op.aspin_delta(x["q"], x["k"], x["v"], x["la"], x["beta"], None, True)
+                op.aspin_delta_bwd(x["q"], x["k"], x["v"], x["la"], x["beta"], sent, W, X, x["do"], x["dS"])
+    B, T, D = 16, 512, 768
+    u, lm, an, gy = (torch.randn(B, T, D, device=dev) for _ in range(4))
+    lm = -lm.abs()
+    hr, _, _, hi = op.diag_scan(u, lm, an, None, None)
+    for _ in range(reps):
+        op.diag_scan(u, lm, an, None, None)
+        op.diag_scan_bwd(gy, None, None, lm, an, hr, hi, None, None)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_kernels": reps, "copy_bytes": COPY_BYTES}), flush=True)
+
+
+COPY_BYTES = 256 << 20
+
+
 def main():
     args = parse()
+    if args.profile_kernels:
+        profile_kernels()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the carrier path has no "
               "multi-GPU exchange to measure here.", file=sys.stderr)
