@@ -20,7 +20,7 @@ extern "C" {
 #define PRAGNOSIA_ERR_INVALID_ARGUMENT (-1)
 #define PRAGNOSIA_ERR_UNSUPPORTED (-2)
 
-/* ABI version of this header; bumped on any signature change. */
+/* ABI version of this header (2); bumped on any signature change. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -30,11 +30,12 @@ const char* pragnosia_error_string(int code);
  * Complex diagonal recurrence with per-token lambda (fspin):
  *     h_t = exp(logmag_t + i ang_t) h_{t-1} + u_t,   h_{-1} = h0r + i h0i (zero when h0r/h0i are NULL).
  * Forward: writes hr = Re h and hi = Im h for every t (both (B, T, D) fp32; hr is the output y, hi is saved for
- * the backward). Replaces `_Scan.forward` / `_fwd` of src/scan_kernel.py:24-50, :105-119.
+ * the backward) and, when hr_last/hi_last are non-NULL, the final state (Re h_{T-1}, Im h_{T-1}) as two (B, D) fp32
+ * arrays. Replaces `_Scan.forward` / `_fwd` of src/scan_kernel.py:24-50, :105-119.
  * u, logmag, ang: (B, T, D) fp32. h0r, h0i: (B, D) fp32 or NULL (both or neither). */
 int pragnosia_diag_scan_fwd(const float* u, const float* logmag, const float* ang,
                             const float* h0r, const float* h0i,
-                            float* hr, float* hi,
+                            float* hr, float* hi, float* hr_last, float* hi_last,
                             int64_t B, int64_t T, int64_t D, void* stream);
 
 /* Backward of pragnosia_diag_scan_fwd (the adjoint recurrence run in reverse). Replaces `_Scan.backward` /

@@ -19,7 +19,7 @@ _f32 = ctypes.c_float
 SIGNATURES = {
     "pragnosia_abi_version": [],
     "pragnosia_error_string": [_i32],
-    "pragnosia_diag_scan_fwd": [_p] * 7 + [_i64] * 3 + [_p],
+    "pragnosia_diag_scan_fwd": [_p] * 9 + [_i64] * 3 + [_p],
     "pragnosia_diag_scan_bwd": [_p] * 14 + [_i64] * 3 + [_p],
     "pragnosia_aspin_chunk_fwd": [_p] * 8 + [_i64] * 5 + [_p],
     "pragnosia_aspin_chunk_bwd": [_p] * 12 + [_i64] * 5 + [_p],

@@ -27,6 +27,17 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 
 PGN_DEVICE float pgn_exp(float x) { return __expf(x); }
 
+// sin and cos of x. The hardware sine/cosine (through __sincosf) take the argument in revolutions: scaling x to
+// revolutions in fp32 costs about |x| * 2^-24 rad of absolute angle error, so they are used for |x| < 64 rad (at
+// most ~4e-6 rad; measured 1.3e-6 relative on the diagonal scan's outputs for angles in [-pi, pi]) and the precise
+// library routine beyond.
+PGN_DEVICE void pgn_sincos(float x, float* s, float* c) {
+  if (fabsf(x) < 64.f)
+    __sincosf(x, s, c);
+  else
+    sincosf(x, s, c);
+}
+
 // Round-to-nearest-even fp32 -> bf16 (finite inputs).
 PGN_DEVICE __bf16 pgn_bf16(float x) { return (__bf16)x; }
 PGN_DEVICE float pgn_f32(__bf16 x) { return (float)x; }

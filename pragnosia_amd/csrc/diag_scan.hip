@@ -3,10 +3,11 @@
 //
 // The recurrence composes associatively: a segment of tokens acts on its incoming state as the affine map
 // h -> P h + e, P = prod lambda_t (|P| <= 1), e = the segment's own contribution from zero. One workgroup owns
-// 32 channels of one sequence (a wave = 32 channels x 2 time segments, so every load instruction reads two
-// 128-byte rows of the D-fastest layout) and walks time in blocks of 2 * NW * SEG tokens:
-//   1. each lane loads its segment (SEG tokens of one channel, all loads issued up front), forms lambda in
-//      registers and scans it from zero, giving the segment's map (P, e);
+// CH channels of one sequence (a wave = CH channels x 64/CH time segments; with CH = 64 every load instruction
+// reads one 256-byte row segment of the D-fastest layout) and walks time in blocks of (64/CH) * NW * SEG tokens:
+//   1. each lane takes its segment (SEG tokens of one channel, loaded during the previous block), forms lambda in
+//      registers, issues the loads of its segment in the next block, and scans the current one from zero, giving
+//      the segment's map (P, e);
 //   2. the maps go to LDS; after one barrier every lane folds the maps of the segments before it into the
 //      block's carry-in to get its own incoming state;
 //   3. the lane re-runs its SEG steps from that state out of registers and writes h.
@@ -22,35 +23,50 @@
 
 namespace {
 
-constexpr int kCH = 32;  // channels per workgroup
 
 struct SegMaps {
   float pr, pi, er, ei;
 };
 
-template <int NW, int SEG>
+template <int NW, int SEG, int CH>
 __global__ __launch_bounds__(NW * 64) void diag_fwd_kernel(
     const float* __restrict__ u, const float* __restrict__ lm, const float* __restrict__ an,
     const float* __restrict__ h0r, const float* __restrict__ h0i, float* __restrict__ hr,
-    float* __restrict__ hi, int T, int D, int n_ctile) {
-  constexpr int NSEG = 2 * NW;
+    float* __restrict__ hi, float* __restrict__ hr_last, float* __restrict__ hi_last, int T, int D, int n_ctile) {
+  constexpr int SPW = 64 / CH;  // time segments per wave
+  constexpr int NSEG = SPW * NW;
   constexpr int TB = NSEG * SEG;
-  __shared__ SegMaps maps[2][NSEG][kCH];
-  __shared__ float2 carry[2][kCH];
+  __shared__ SegMaps maps[2][NSEG][CH];
+  __shared__ float2 carry[2][CH];
 
   const int lane = threadIdx.x & 63;
-  const int c = lane & 31;
-  const int seg = 2 * (threadIdx.x >> 6) + (lane >> 5);
+  const int c = lane % CH;
+  const int seg = SPW * (threadIdx.x >> 6) + lane / CH;
   const int b = blockIdx.x / n_ctile;
-  const int d = (blockIdx.x - b * n_ctile) * kCH + c;
+  const int d = (blockIdx.x - b * n_ctile) * CH + c;
   const bool dok = d < D;
   const size_t base = (size_t)b * T * D + (dok ? d : 0);
 
-  if (threadIdx.x < kCH) {
+  if (threadIdx.x < CH) {
     float2 h = make_float2(0.f, 0.f);
     if (h0r != nullptr && dok) h = make_float2(h0r[(size_t)b * D + d], h0i[(size_t)b * D + d]);
     carry[0][c] = h;
   }
+
+  // raw inputs of the next time block, loaded one block ahead so the loads overlap the current block's compute
+  float pu[SEG], pl[SEG], pa[SEG];
+  auto fetch = [&](int tb) {
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+      const int t = tb + seg * SEG + j;
+      const bool ok = dok && t < T;
+      const size_t off = base + (size_t)(ok ? t : 0) * D;
+      pu[j] = ok ? u[off] : 0.f;
+      pl[j] = ok ? lm[off] : 0.f;
+      pa[j] = ok ? an[off] : 0.f;
+    }
+  };
+  fetch(0);
 
   for (int tb = 0, it = 0; tb < T; tb += TB, ++it) {
     const int p = it & 1;
@@ -58,18 +74,14 @@ __global__ __launch_bounds__(NW * 64) void diag_fwd_kernel(
     float xr[SEG], xi[SEG], xu[SEG];
 #pragma unroll
     for (int j = 0; j < SEG; ++j) {
-      const int t = t0 + j;
-      const bool ok = dok && t < T;
-      const size_t off = base + (size_t)(ok ? t : 0) * D;
-      xu[j] = ok ? u[off] : 0.f;
-      const float l = ok ? lm[off] : 0.f;
-      const float a = ok ? an[off] : 0.f;
-      const float m = expf(l);
+      xu[j] = pu[j];
+      const float m = pgn_exp(pl[j]);
       float s, co;
-      sincosf(a, &s, &co);
+      pgn_sincos(pa[j], &s, &co);
       xr[j] = m * co;
       xi[j] = m * s;
     }
+    if (tb + TB < T) fetch(tb + TB);
     // the segment's map from a zero state
     float er = 0.f, ei = 0.f, pr = 1.f, pi = 0.f;
 #pragma unroll
@@ -105,31 +117,36 @@ __global__ __launch_bounds__(NW * 64) void diag_fwd_kernel(
       }
     }
     if (seg == NSEG - 1) carry[p ^ 1][c] = h;
+    if (tb + TB >= T && t0 <= T - 1 && T - 1 < t0 + SEG && dok && hr_last != nullptr) {
+      hr_last[(size_t)b * D + d] = h.x;  // this lane's segment holds token T-1: the final state
+      hi_last[(size_t)b * D + d] = h.y;
+    }
   }
 }
 
-template <int NW, int SEG>
+template <int NW, int SEG, int CH>
 __global__ __launch_bounds__(NW * 64) void diag_bwd_kernel(
     const float* __restrict__ g, const float* __restrict__ glr, const float* __restrict__ gli,
     const float* __restrict__ lm, const float* __restrict__ an, const float* __restrict__ hr,
     const float* __restrict__ hi, const float* __restrict__ h0r, const float* __restrict__ h0i,
     float* __restrict__ du, float* __restrict__ dlm, float* __restrict__ dan, float* __restrict__ dh0r,
     float* __restrict__ dh0i, int T, int D, int n_ctile) {
-  constexpr int NSEG = 2 * NW;
+  constexpr int SPW = 64 / CH;
+  constexpr int NSEG = SPW * NW;
   constexpr int TB = NSEG * SEG;
-  __shared__ SegMaps maps[2][NSEG][kCH];
-  __shared__ float2 carry[2][kCH];
+  __shared__ SegMaps maps[2][NSEG][CH];
+  __shared__ float2 carry[2][CH];
 
   const int lane = threadIdx.x & 63;
-  const int c = lane & 31;
-  const int seg = 2 * (threadIdx.x >> 6) + (lane >> 5);
+  const int c = lane % CH;
+  const int seg = SPW * (threadIdx.x >> 6) + lane / CH;
   const int b = blockIdx.x / n_ctile;
-  const int d = (blockIdx.x - b * n_ctile) * kCH + c;
+  const int d = (blockIdx.x - b * n_ctile) * CH + c;
   const bool dok = d < D;
   const size_t base = (size_t)b * T * D + (dok ? d : 0);
   const size_t bd = (size_t)b * D + (dok ? d : 0);
 
-  if (threadIdx.x < kCH) {
+  if (threadIdx.x < CH) {
     float2 a = make_float2(0.f, 0.f);
     if (dok) {
       if (glr != nullptr) a.x = glr[bd];
@@ -139,25 +156,49 @@ __global__ __launch_bounds__(NW * 64) void diag_bwd_kernel(
   }
 
   const int nblk = (T + TB - 1) / TB;
+  // inputs of the next (earlier) time block, loaded one block ahead: g, logmag, ang and h_{t-1}
+  float pg[SEG], pl[SEG], pa[SEG], phr[SEG], phi[SEG];
+  auto fetch = [&](int blk) {
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+      const int t = blk * TB + seg * SEG + j;
+      const bool ok = dok && t < T;
+      const size_t off = base + (size_t)(ok ? t : 0) * D;
+      pg[j] = ok ? g[off] : 0.f;
+      pl[j] = ok ? lm[off] : 0.f;
+      pa[j] = ok ? an[off] : 0.f;
+      float qr = 0.f, qi = 0.f;
+      if (ok) {
+        if (t > 0) {
+          qr = hr[off - D];
+          qi = hi[off - D];
+        } else if (h0r != nullptr) {
+          qr = h0r[bd];
+          qi = h0i[bd];
+        }
+      }
+      phr[j] = qr;
+      phi[j] = qi;
+    }
+  };
+  fetch(nblk - 1);
   float2 cin = make_float2(0.f, 0.f);
   for (int it = 0; it < nblk; ++it) {
     const int p = it & 1;
     const int t0 = (nblk - 1 - it) * TB + seg * SEG;
-    float xr[SEG], xi[SEG], xg[SEG];  // lambda_t (not conjugated) and g_t
+    float xr[SEG], xi[SEG], xg[SEG], hpr[SEG], hpi[SEG];  // lambda_t (not conjugated), g_t, h_{t-1}
 #pragma unroll
     for (int j = 0; j < SEG; ++j) {
-      const int t = t0 + j;
-      const bool ok = dok && t < T;
-      const size_t off = base + (size_t)(ok ? t : 0) * D;
-      xg[j] = ok ? g[off] : 0.f;
-      const float l = ok ? lm[off] : 0.f;
-      const float a = ok ? an[off] : 0.f;
-      const float m = expf(l);
+      xg[j] = pg[j];
+      hpr[j] = phr[j];
+      hpi[j] = phi[j];
+      const float m = pgn_exp(pl[j]);
       float s, co;
-      sincosf(a, &s, &co);
+      pgn_sincos(pa[j], &s, &co);
       xr[j] = m * co;
       xi[j] = m * s;
     }
+    if (it + 1 < nblk) fetch(nblk - 2 - it);
     // the segment's map on the carry coming from its right: c_out = P c_in + e, where the carry out of a
     // token is conj(lambda_t) a_t and a_t = g_t + (carry in)
     float er = 0.f, ei = 0.f, pr = 1.f, pi = 0.f;
@@ -185,18 +226,8 @@ __global__ __launch_bounds__(NW * 64) void diag_bwd_kernel(
       const int t = t0 + j;
       const bool ok = dok && t < T;
       const float ar = xg[j] + a.x, ai = a.y;
-      float qr = 0.f, qi = 0.f;  // h_{t-1}
-      if (ok) {
-        if (t > 0) {
-          qr = hr[base + (size_t)(t - 1) * D];
-          qi = hi[base + (size_t)(t - 1) * D];
-        } else if (h0r != nullptr) {
-          qr = h0r[bd];
-          qi = h0i[bd];
-        }
-      }
-      const float rr = xr[j] * qr - xi[j] * qi;  // lambda_t h_{t-1}
-      const float ri = xi[j] * qr + xr[j] * qi;
+      const float rr = xr[j] * hpr[j] - xi[j] * hpi[j];  // lambda_t h_{t-1}
+      const float ri = xi[j] * hpr[j] + xr[j] * hpi[j];
       if (ok) {
         const size_t off = base + (size_t)t * D;
         du[off] = ar;
@@ -214,21 +245,21 @@ __global__ __launch_bounds__(NW * 64) void diag_bwd_kernel(
   }
 }
 
-template <int NW, int SEG>
+template <int NW, int SEG, int CH>
 int launch_fwd(const float* u, const float* lm, const float* an, const float* h0r, const float* h0i, float* hr,
-               float* hi, int B, int T, int D, hipStream_t st) {
-  const int nct = (D + kCH - 1) / kCH;
-  hipLaunchKernelGGL((diag_fwd_kernel<NW, SEG>), dim3(B * nct), dim3(NW * 64), 0, st, u, lm, an, h0r, h0i, hr,
-                     hi, T, D, nct);
+               float* hi, float* hrl, float* hil, int B, int T, int D, hipStream_t st) {
+  const int nct = (D + CH - 1) / CH;
+  hipLaunchKernelGGL((diag_fwd_kernel<NW, SEG, CH>), dim3(B * nct), dim3(NW * 64), 0, st, u, lm, an, h0r, h0i, hr,
+                     hi, hrl, hil, T, D, nct);
   PGN_RETURN_LAUNCH();
 }
 
-template <int NW, int SEG>
+template <int NW, int SEG, int CH>
 int launch_bwd(const float* g, const float* glr, const float* gli, const float* lm, const float* an,
                const float* hr, const float* hi, const float* h0r, const float* h0i, float* du, float* dlm,
                float* dan, float* dh0r, float* dh0i, int B, int T, int D, hipStream_t st) {
-  const int nct = (D + kCH - 1) / kCH;
-  hipLaunchKernelGGL((diag_bwd_kernel<NW, SEG>), dim3(B * nct), dim3(NW * 64), 0, st, g, glr, gli, lm, an, hr,
+  const int nct = (D + CH - 1) / CH;
+  hipLaunchKernelGGL((diag_bwd_kernel<NW, SEG, CH>), dim3(B * nct), dim3(NW * 64), 0, st, g, glr, gli, lm, an, hr,
                      hi, h0r, h0i, du, dlm, dan, dh0r, dh0i, T, D, nct);
   PGN_RETURN_LAUNCH();
 }
@@ -237,22 +268,26 @@ bool shape_ok(int64_t B, int64_t T, int64_t D) {
   if (B <= 0 || T < 0 || D <= 0) return false;
   if (B * T * D >= ((int64_t)1 << 40)) return false;
   if (T >= (1 << 30) || D >= (1 << 30)) return false;
-  const int64_t blocks = B * ((D + kCH - 1) / kCH);
+  const int64_t blocks = B * ((D + 31) / 32);
   return blocks < ((int64_t)1 << 31);
 }
 
 }  // namespace
 
 extern "C" int pragnosia_diag_scan_fwd(const float* u, const float* logmag, const float* ang, const float* h0r,
-                                       const float* h0i, float* hr, float* hi, int64_t B, int64_t T, int64_t D,
-                                       void* stream) {
+                                       const float* h0i, float* hr, float* hi, float* hr_last, float* hi_last,
+                                       int64_t B, int64_t T, int64_t D, void* stream) {
   PGN_CHECK_ARG(shape_ok(B, T, D));
   PGN_CHECK_ARG((h0r == nullptr) == (h0i == nullptr));
+  PGN_CHECK_ARG((hr_last == nullptr) == (hi_last == nullptr));
   if (T == 0) return PRAGNOSIA_OK;
   PGN_CHECK_ARG(u && logmag && ang && hr && hi);
   hipStream_t st = (hipStream_t)stream;
-  if (T >= 128) return launch_fwd<8, 8>(u, logmag, ang, h0r, h0i, hr, hi, (int)B, (int)T, (int)D, st);
-  return launch_fwd<2, 8>(u, logmag, ang, h0r, h0i, hr, hi, (int)B, (int)T, (int)D, st);
+  // 16 waves x 64 channels, 4-token segments (64-token time blocks): swept against 4-16 waves, 32/64 channels and
+  // 2-16-token segments at B16 T512 D768; short sequences use 4 waves
+  if (T >= 64)
+    return launch_fwd<16, 4, 64>(u, logmag, ang, h0r, h0i, hr, hi, hr_last, hi_last, (int)B, (int)T, (int)D, st);
+  return launch_fwd<4, 4, 64>(u, logmag, ang, h0r, h0i, hr, hi, hr_last, hi_last, (int)B, (int)T, (int)D, st);
 }
 
 extern "C" int pragnosia_diag_scan_bwd(const float* g, const float* g_last_r, const float* g_last_i,
@@ -265,9 +300,9 @@ extern "C" int pragnosia_diag_scan_bwd(const float* g, const float* g_last_r, co
   hipStream_t st = (hipStream_t)stream;
   if (T == 0) return PRAGNOSIA_ERR_INVALID_ARGUMENT;
   PGN_CHECK_ARG(g && logmag && ang && hr && hi && du && dlogmag && dang);
-  if (T >= 128)
-    return launch_bwd<8, 8>(g, g_last_r, g_last_i, logmag, ang, hr, hi, h0r, h0i, du, dlogmag, dang, dh0r, dh0i,
-                             (int)B, (int)T, (int)D, st);
-  return launch_bwd<2, 8>(g, g_last_r, g_last_i, logmag, ang, hr, hi, h0r, h0i, du, dlogmag, dang, dh0r, dh0i,
-                          (int)B, (int)T, (int)D, st);
+  if (T >= 64)
+    return launch_bwd<16, 4, 64>(g, g_last_r, g_last_i, logmag, ang, hr, hi, h0r, h0i, du, dlogmag, dang, dh0r, dh0i,
+                                 (int)B, (int)T, (int)D, st);
+  return launch_bwd<4, 4, 64>(g, g_last_r, g_last_i, logmag, ang, hr, hi, h0r, h0i, du, dlogmag, dang, dh0r, dh0i,
+                              (int)B, (int)T, (int)D, st);
 }

@@ -47,9 +47,11 @@ def diag_scan(u: Tensor, logmag: Tensor, ang: Tensor, h0r: Optional[Tensor],
     B, T, D = u.shape
     hr = torch.empty(B, T, D, device=u.device, dtype=torch.float32)
     hi = torch.empty_like(hr)
+    hrl = torch.empty(B, D, device=u.device, dtype=torch.float32)
+    hil = torch.empty_like(hrl)
     check(lib().pragnosia_diag_scan_fwd(_ptr(u), _ptr(logmag), _ptr(ang), _ptr(h0r), _ptr(h0i), _ptr(hr), _ptr(hi),
-                                        B, T, D, _stream(u)), "pragnosia_diag_scan_fwd")
-    return hr, hr[:, -1].clone(), hi[:, -1].clone(), hi
+                                        _ptr(hrl), _ptr(hil), B, T, D, _stream(u)), "pragnosia_diag_scan_fwd")
+    return hr, hrl, hil, hi
 
 
 @diag_scan.register_fake

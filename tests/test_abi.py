@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 1
+    assert L.pragnosia_abi_version() == 2
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 
@@ -49,11 +49,11 @@ def test_abi_version_and_error_strings(L):
 def test_arguments_rejected_before_launch(L):
     """Shape errors return PRAGNOSIA_ERR_INVALID_ARGUMENT without touching a device."""
     null = ctypes.c_void_p(0)
-    assert L.pragnosia_diag_scan_fwd(*([null] * 7), 0, 4, 8, null) == -1          # B = 0
-    assert L.pragnosia_diag_scan_fwd(*([null] * 7), 1, 4, -3, null) == -1         # D < 0
+    assert L.pragnosia_diag_scan_fwd(*([null] * 9), 0, 4, 8, null) == -1          # B = 0
+    assert L.pragnosia_diag_scan_fwd(*([null] * 9), 1, 4, -3, null) == -1         # D < 0
     one = ctypes.c_void_p(16)
     # h0r given without h0i
-    assert L.pragnosia_diag_scan_fwd(one, one, one, one, null, one, one, 1, 4, 8, null) == -1
+    assert L.pragnosia_diag_scan_fwd(one, one, one, one, null, one, one, null, null, 1, 4, 8, null) == -1
 
 
 def test_product_never_imports_oracle():
