@@ -113,7 +113,7 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int s = 16 * sb + 4 * g + r;
-        NT[s * NP + t] = (s < t) ? bt * acc[r] * __expf(fminf(Lt - Ls[s], 0.f)) : 0.f;
+        NT[s * NP + t] = bt * acc[r] * masked_decay(Lt - Ls[s], s < t);
       }
     }
   }
@@ -204,20 +204,23 @@ __global__ __launch_bounds__(256) void aspin_delta_fwd(
       const int t = 16 * w + i;
       const bf16x8 qf0 = frag(Qs, t, 0, g), qf1 = frag(Qs, t, 1, g);
       const float Lt = Ls[t];
+      f32x4 pt[4];
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) {  // all score MFMAs first, then the decays
+        pt[sb] = zero4();
+        if (sb <= w) {
+          pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
+          pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
+        }
+      }
 #pragma unroll
       for (int sb = 0; sb < 4; ++sb) {
-        f32x4 pt = zero4();
         if (sb <= w) {
-          pt = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt);
-          pt = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt);
           const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int s = 16 * sb + 4 * g + r;
-            pt[r] = (s <= t) ? pt[r] * __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
-          }
+          for (int r = 0; r < 4; ++r) pt[sb][r] *= masked_decay(Lt - Lsv[r], 16 * sb + 4 * g + r <= t);
         }
-        store_T(As, 16 * w, 16 * sb, g, i, pt);
+        store_T(As, 16 * w, 16 * sb, g, i, pt[sb]);
       }
     }
 
@@ -366,20 +369,23 @@ __global__ __launch_bounds__(256) void aspin_delta_bwd_chain(
       const int t = 16 * w + i;
       const bf16x8 kf0 = frag(Ks, t, 0, g), kf1 = frag(Ks, t, 1, g);
       const float Lt = Ls[t];
+      f32x4 a[4];
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) {  // all score MFMAs first, then the decays
+        a[sb] = zero4();
+        if (sb >= w) {
+          a[sb] = pgn_mfma(frag(Qs, 16 * sb + i, 0, g), kf0, a[sb]);
+          a[sb] = pgn_mfma(frag(Qs, 16 * sb + i, 1, g), kf1, a[sb]);
+        }
+      }
 #pragma unroll
       for (int sb = 0; sb < 4; ++sb) {
-        f32x4 a = zero4();
         if (sb >= w) {
-          a = pgn_mfma(frag(Qs, 16 * sb + i, 0, g), kf0, a);
-          a = pgn_mfma(frag(Qs, 16 * sb + i, 1, g), kf1, a);
           const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int s = 16 * sb + 4 * g + r;
-            a[r] = (s >= t) ? a[r] * __expf(fminf(Lsv[r] - Lt, 0.f)) : 0.f;
-          }
+          for (int r = 0; r < 4; ++r) a[sb][r] *= masked_decay(Lsv[r] - Lt, 16 * sb + 4 * g + r >= t);
         }
-        store_T(AT, 16 * w, 16 * sb, g, i, a);
+        store_T(AT, 16 * w, 16 * sb, g, i, a[sb]);
       }
     }
     // U = K S_c and (Q o eL)^T dO on this wave's columns: neither depends on dS
@@ -572,15 +578,12 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int s = 16 * sb + 4 * g + r;
-          const float dec = (s <= me) ? __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+          const float dec = masked_decay(Lt - Lsv[r], s <= me);
           rowacc += dA[r] * P[r] * dec;
           dPT[sb][r] = dA[r] * dec;
-          if (s < me) {
-            const float M = KK[r] * dec;
-            const float dn = -dN[r];
-            db2 += dn * M;
-            rowacc += bt * dn * M;
-          }
+          const float dnM = -dN[r] * KK[r] * dec * (s < me ? 1.f : 0.f);  // dN M, strictly lower
+          db2 += dnM;
+          rowacc += bt * dnM;
         }
       }
     }
@@ -637,14 +640,12 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * tb + 4 * g + r;
-          const float dec = (t >= me) ? __expf(fminf(Ltv[r] - Lsm, 0.f)) : 0.f;
+          const float dec = masked_decay(Ltv[r] - Lsm, t >= me);
           colacc += dA[r] * P[r] * dec;
           dPt[tb][r] = dA[r] * dec;
-          if (t > me) {
-            const float dkk = -btv[r] * dN[r] * dec;  // dKK[t][s]
-            colacc += dkk * KK[r];
-            Gt[tb][r] = dkk;
-          }
+          const float dkk = -btv[r] * dN[r] * dec * (t > me ? 1.f : 0.f);  // dKK[t][s], strictly lower
+          colacc += dkk * KK[r];
+          Gt[tb][r] = dkk;
         }
       }
       if (tb <= wl) {
@@ -656,7 +657,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * tb + 4 * g + r;
-          if (t < me) Gt[tb][r] += -bsm * dN[r] * __expf(fminf(Lsm - Ltv[r], 0.f));  // dKK[s][t]
+          Gt[tb][r] += -bsm * dN[r] * masked_decay(Lsm - Ltv[r], t < me);  // dKK[s][t]
         }
       }
     }

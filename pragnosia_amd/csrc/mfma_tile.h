@@ -24,9 +24,12 @@ struct WaveIdx {
   int w, l, g, i;
 };
 
+// The wave index is made wave-uniform (an SGPR): conditions on it are then scalar branches. That is required, not
+// an optimisation: MFMA instructions ignore EXEC, so an MFMA under a condition the compiler believes divergent (a
+// lane mask that happens to be empty) would still execute and overwrite its destination.
 PGN_DEVICE WaveIdx wave_idx() {
   const int tid = threadIdx.x;
-  return WaveIdx{tid >> 6, tid & 63, (tid & 63) >> 4, tid & 15};
+  return WaveIdx{__builtin_amdgcn_readfirstlane(tid >> 6), tid & 63, (tid & 63) >> 4, tid & 15};
 }
 
 PGN_DEVICE f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
@@ -96,24 +99,31 @@ PGN_DEVICE bf16x4 zero_bf16x4() {
   return z;
 }
 
-// Load block b of a (rows x 64-wide) region starting at src (row stride ld elements); rows >= nrows read as zero.
+// Load block b of a (rows x 64-wide) region starting at src (row stride ld elements); rows >= nrows (>= 1) read as
+// zero. Rows past the end load row nrows - 1 and are then replaced by zero, so every load is unconditional (a
+// branch per load keeps each load's address and result live across the branch).
 PGN_DEVICE Blk4 load_blk(const __bf16* __restrict__ src, int ld, int nrows, int b) {
   const int r0 = 4 * (b >> 4), c0 = 4 * (b & 15);
   Blk4 x;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    x.r[j] = (r0 + j < nrows) ? *reinterpret_cast<const bf16x4*>(src + (size_t)(r0 + j) * ld + c0) : zero_bf16x4();
+  for (int j = 0; j < 4; ++j) {
+    const bf16x4 v = *reinterpret_cast<const bf16x4*>(src + (size_t)min(r0 + j, nrows - 1) * ld + c0);
+    x.r[j] = (r0 + j < nrows) ? v : zero_bf16x4();
+  }
   return x;
 }
 
-// The same for a region only `ncols` (multiple of 4) wide: block b covers rows 4*(b / (ncols/4)).. .
+// The same for a region only `ncols` (multiple of 4) wide: block b covers rows 4*(b / (ncols/4)).. . Rows past
+// nrows - 1 are outside the blocks any caller passes only when nrows >= 1.
 PGN_DEVICE Blk4 load_blk_w(const __bf16* __restrict__ src, int ld, int nrows, int ncols, int b) {
   const int per_row = ncols >> 2;
   const int r0 = 4 * (b / per_row), c0 = 4 * (b % per_row);
   Blk4 x;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    x.r[j] = (r0 + j < nrows) ? *reinterpret_cast<const bf16x4*>(src + (size_t)(r0 + j) * ld + c0) : zero_bf16x4();
+  for (int j = 0; j < 4; ++j) {
+    const bf16x4 v = *reinterpret_cast<const bf16x4*>(src + (size_t)min(r0 + j, nrows - 1) * ld + c0);
+    x.r[j] = (r0 + j < nrows) ? v : zero_bf16x4();
+  }
   return x;
 }
 
@@ -133,6 +143,10 @@ PGN_DEVICE void put_blk_T(__bf16* tile, const Blk4& x, int r0, int c0) {
     *reinterpret_cast<bf16x4*>(tile + (c0 + j) * kPitch + r0) = col;
   }
 }
+
+// exp(min(x, 0)) where `keep`, else 0, without a branch: the exponent is never positive, so the unmasked value is
+// finite and at most 1 and the mask is a select (a branch per element around the exp serialises the waves).
+PGN_DEVICE float masked_decay(float x, bool keep) { return __expf(fminf(x, 0.f)) * (keep ? 1.f : 0.f); }
 
 // Sum over the 16 lanes of a lane group (same g): butterfly over lane bits 0..3.
 PGN_DEVICE float sum16(float x) {

@@ -16,7 +16,7 @@ def header_functions():
         if fn.endswith(".h"):
             txt = open(os.path.join(ROOT, "include", fn)).read()
             txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-            names += re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(pragnosia_\w+)\s*\(", txt, flags=re.M)
+            names += re.findall(r"^\s*(?:const\s+)?(?:unsigned\s+)?\w+\s*\**\s*(pragnosia_\w+)\s*\(", txt, flags=re.M)
     return names
 
 
@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 2
+    assert L.pragnosia_abi_version() == 5
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 

@@ -19,8 +19,8 @@ def rel(a, b):
 
 @pytest.fixture(scope="module")
 def scan():
-    from pragnosia_amd.assoc import assoc_scan_hip
-    return assoc_scan_hip
+    from pragnosia_amd.assoc import assoc_scan_kernel
+    return assoc_scan_kernel
 
 
 def _unit_inputs(B, H, T, D, seed, s0=True, la_scale=0.05):
@@ -57,6 +57,21 @@ def test_plain_matches_oracle(scan, T, s0):
     e = _check_fwd_bwd(scan, q, k, v, la, S0, seed=T)
     assert e["o"] < TOL_OUT and e["S"] < TOL_OUT, e
     assert max(v_ for n, v_ in e.items() if n.startswith("d")) < TOL_GRAD, e
+
+
+@pytest.mark.parametrize("B,H,T", [(1, 2, 70 * 64 - 17), (8, 16, 256)])
+def test_single_pass_many_chunks(scan, B, H, T):
+    """The single-pass scans with look-back windows longer than one wave (70 chunks per head) and with many heads
+    in flight (128 heads x 4 chunks), forward and backward; then the same call again on recycled workspace."""
+    q, k, v, la, S0 = _unit_inputs(B, H, T, 64, seed=B * T, la_scale=0.01)
+    e = _check_fwd_bwd(scan, q, k, v, la, S0, seed=7)
+    assert e["o"] < TOL_OUT and e["S"] < TOL_OUT, e
+    assert max(v_ for n, v_ in e.items() if n.startswith("d")) < TOL_GRAD, e
+    with torch.no_grad():
+        dev = [t.cuda() for t in (q, k, v, la, S0)]
+        y1, S1, _ = scan(*dev)
+        y2, S2, _ = scan(*dev)
+    assert torch.equal(y1, y2) and torch.equal(S1, S2)
 
 
 def test_cfg0_single_layer(scan):
@@ -126,3 +141,10 @@ def test_unsupported_head_dim_raises(scan):
     q = torch.randn(1, 1, 8, 32, device="cuda")
     with pytest.raises(PragnosiaError):
         scan(q, q, q, torch.zeros(1, 1, 8, device="cuda"))
+
+
+def test_lookback_never_timed_out():
+    """No look-back wait of any single-pass scan run so far in this process ran out of its bound."""
+    from pragnosia_amd._lib import lib
+    torch.cuda.synchronize()
+    assert lib().pragnosia_lookback_timeouts() == 0
