@@ -136,7 +136,7 @@ def aspin_bench(rule, steps, warmup):
         bwd_bytes = 7 * 2 * elem + 2 * sent_n + 8 * ht + 8 * state
         fwd_flops = 4 * D * (C + D) * ht
         bwd_flops = 10 * D * (C + D) * ht
-        names = ("aspin_plain_fwd (single-pass kernel)", "aspin_plain_bwd (state + local kernels)")
+        names = ("aspin_plain_fwd", "aspin_plain_bwd")
     else:
         # forward: q, k, v read; o, W written; X written and read back (bf16 C x C per chunk); la, beta read;
         # S_final, sent written

@@ -20,7 +20,7 @@ extern "C" {
 #define PRAGNOSIA_ERR_INVALID_ARGUMENT (-1)
 #define PRAGNOSIA_ERR_UNSUPPORTED (-2)
 
-/* ABI version of this header (5); bumped on any signature change. */
+/* ABI version of this header (7); bumped on any signature change. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -55,37 +55,19 @@ int pragnosia_diag_scan_bwd(const float* g, const float* g_last_r, const float* 
  * q, k, v: (B, H, T, D) bf16; la: (B, H, T) fp32 (<= 0); S0: (B, H, D, D) fp32, keys on dim 2, or NULL.
  * Writes o: (B, H, T, D) bf16; S_final: (B, H, D, D) fp32; sent (if non-NULL): the state entering every chunk,
  * (B, H, ceil(T/64), D, D) bf16 -- required by the backward. T need not be a multiple of 64.
- * `workspace`: device memory of at least pragnosia_aspin_chunk_fwd_workspace_bytes(...) bytes (per-chunk flags and
- * published states of the single pass), zero-filled before its first use and then kept for later calls; `epoch`:
- * greater than every epoch used before with this workspace, and below 2^56 (the flags of earlier calls then never
- * count, so nothing is cleared between calls). Calls that share a workspace must not overlap (same stream, or
- * ordered). The kernel is persistent: its grid is the number of workgroups the device can hold at once.
  * Replaces `assoc_scan_kernel` and the ops under it (`prefix_scan`, `assoc_out`) of src/assoc_kernel.py:128-323.
  * Returns PRAGNOSIA_ERR_UNSUPPORTED for D != 64 or chunk != 64. */
-int64_t pragnosia_aspin_chunk_fwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk);
 int pragnosia_aspin_chunk_fwd(const void* q, const void* k, const void* v, const float* la, const float* S0,
-                              void* o, float* S_final, void* sent, void* workspace, int64_t workspace_bytes,
-                              uint64_t epoch, int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk,
-                              void* stream);
-
-/* Look-back waits of the single-pass scans that ran out of their bound since the library was loaded (each such
- * wait is a lost publication -- a bug -- and its chunk's result is wrong; the kernel still completes). Synchronises
- * with the device. No counterpart in the reference: a diagnostic for tests. */
-unsigned int pragnosia_lookback_timeouts(void);
-
-/* Bytes of device workspace pragnosia_aspin_chunk_bwd needs at this shape (-1 if the shape is rejected). */
-int64_t pragnosia_aspin_chunk_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk);
+                              void* o, float* S_final, void* sent,
+                              int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
 
 /* Backward of pragnosia_aspin_chunk_fwd. dO: (B, H, T, D) bf16; dS_final: (B, H, D, D) fp32 or NULL (zero);
  * sent: the forward's entering states. Writes dq, dk, dv (bf16, (B, H, T, D)), dla (fp32, (B, H, T)) and, if
- * non-NULL, dS0 (fp32, (B, H, D, D)). `workspace`: caller-allocated device memory of at least
- * pragnosia_aspin_chunk_bwd_workspace_bytes(...) bytes (the per-chunk state gradients, bf16). Replaces the
- * registered backward of the same ops (`assoc_out_bwd`, `prefix_scan_bwd` and the glue of
- * src/assoc_kernel.py:146-299). */
+ * non-NULL, dS0 (fp32, (B, H, D, D)). Replaces the registered backward of the same ops
+ * (`assoc_out_bwd`, `prefix_scan_bwd` and the glue of src/assoc_kernel.py:146-299). */
 int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const void* v, const float* la, const void* sent,
                               const void* dO, const float* dS_final,
                               void* dq, void* dk, void* dv, float* dla, float* dS0,
-                              void* workspace, int64_t workspace_bytes,
                               int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------

@@ -21,11 +21,8 @@ SIGNATURES = {
     "pragnosia_error_string": [_i32],
     "pragnosia_diag_scan_fwd": [_p] * 9 + [_i64] * 3 + [_p],
     "pragnosia_diag_scan_bwd": [_p] * 14 + [_i64] * 3 + [_p],
-    "pragnosia_aspin_chunk_fwd_workspace_bytes": [_i64] * 5,
-    "pragnosia_aspin_chunk_fwd": [_p] * 9 + [_i64, ctypes.c_uint64] + [_i64] * 5 + [_p],
-    "pragnosia_lookback_timeouts": [],
-    "pragnosia_aspin_chunk_bwd_workspace_bytes": [_i64] * 5,
-    "pragnosia_aspin_chunk_bwd": [_p] * 13 + [_i64] * 6 + [_p],
+    "pragnosia_aspin_chunk_fwd": [_p] * 8 + [_i64] * 5 + [_p],
+    "pragnosia_aspin_chunk_bwd": [_p] * 12 + [_i64] * 5 + [_p],
     "pragnosia_aspin_delta_fwd": [_p] * 11 + [_i64] * 5 + [_p],
     "pragnosia_aspin_delta_bwd_workspace_bytes": [_i64] * 5,
     "pragnosia_aspin_delta_bwd": [_p] * 17 + [_i64] * 6 + [_p],
@@ -38,8 +35,7 @@ SIGNATURES = {
 }
 
 # entry points that return a size (int64) rather than a status code
-_RET_I64 = {"pragnosia_aspin_delta_bwd_workspace_bytes", "pragnosia_aspin_prep_theta_partials",
-            "pragnosia_aspin_chunk_bwd_workspace_bytes", "pragnosia_aspin_chunk_fwd_workspace_bytes"}
+_RET_I64 = {"pragnosia_aspin_delta_bwd_workspace_bytes", "pragnosia_aspin_prep_theta_partials"}
 
 _lib = None
 
@@ -60,7 +56,6 @@ def lib():
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = (ctypes.c_char_p if name == "pragnosia_error_string" else
-                          ctypes.c_uint32 if name == "pragnosia_lookback_timeouts" else
                           _i64 if name in _RET_I64 else _i32)
         _lib = L
     return _lib

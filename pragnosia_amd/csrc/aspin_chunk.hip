@@ -3,40 +3,27 @@
 // Per (batch, head), with chunk C = 64 tokens, head dim D = 64, la_t <= 0 the per-token log-decay and, within a
 // chunk, L the inclusive cumulative sum of la, dec[t,s] = exp(L_t - L_s) for s <= t (else 0), eL = exp(L),
 // w = exp(L_C - L), a = exp(L_C):
-//     O       = ((Q K^T) o dec) V + (Q o eL) S_c
+//     O   = ((Q K^T) o dec) V + (Q o eL) S_c
 //     S_{c+1} = a S_c + (K o w)^T V
 // (the reference's `_scan_twopass`, `src/assoc.py:118-165`; its GPU form `src/assoc_kernel.py:47-70,188-202`).
-// Backward, per chunk, with dS_c the gradient on the state LEAVING chunk c, dA = dO V^T, dP = dA o dec,
+//
+// Forward: two workgroups (4 waves each) per (batch, head), each owning 32 of the 64 value columns (the plain rule
+// is independent per value column), walk the chunks in order with their fp32 state columns in registers: wave w
+// holds key rows 16w..16w+15 as accumulator tiles and the state update is an MFMA accumulating onto a*S. Each chunk's
+// Q, K, V tiles are staged in LDS once (K and V also transposed, through a 4x4 register transpose) from registers
+// loaded during the previous chunk's compute, and every contraction reads its operands from LDS, so HBM sees each
+// input once: 8 B per (t, d) element forward (q, k, v read, o written) plus the optional bf16 entering states.
+//
+// The backward walks the chunks in reverse with dS (the gradient on the state leaving the chunk) in registers and
+// the entering states S_c read back from the forward's bf16 copies. Per chunk, with dA = dO V^T, dP = dA o dec,
 // A = (Q K^T) o dec:
-//     dQ = dP K + eL o (dO S_c^T)            dK = dP^T Q + w o (V dS_c^T)
-//     dV = A^T dO + (K o w) dS_c             dS_{c-1} = a dS_c + (Q o eL)^T dO
-//     dL_t = rowsum(dA o A)_t - colsum(dA o A)_t + eL_t q_t.(S_c dO_t) - w_t k_t.(dS_c v_t),
-//     dL_{C-1} += sum_s w_s k_s.(dS_c v_s) + a <S_c, dS_c>,     dla = reverse cumulative sum of dL
-// (equations of `src/assoc_kernel.py:73-116`, `:205-220`, `:279-296`).
-//
-// The only sequential dependency is the state (forward) or state gradient (backward) carried from chunk to chunk,
-// and that recurrence is a scaled add of one 64 x 64 matrix per chunk.
-//
-// Forward: plain_fwd_sp, one persistent single pass. A work item is one (batch-head, chunk); it computes its
-// chunk's state term, publishes it, computes the intra-chunk part of its output, obtains its entering state by
-// look-back over its predecessors' publications (lookback.h), and finishes its output. Every input is read once
-// and the output, the entering states and the final state are written once.
-//
-// Backward: two kernels.
-//   plain_state<true>  one workgroup of SW waves per (batch, head). Wave w takes chunk w of a group of SW chunks,
-//                      stages its X and Y tiles transposed in its own LDS region and computes the chunk's term
-//                      (32 bf16 MFMAs), all chunks of the group at once; then the recurrence runs across the waves
-//                      through one fp32 LDS buffer (one scaled add per chunk, a barrier between chunks), and every
-//                      wave stores the state it read: X = Q, Y = dO, f = eL, gradients dS_c in reverse chunk order
-//                      (bf16, a workspace) and dS0.
-//   plain_bwd_local    one workgroup of 8 waves per (batch-head, chunk): dQ, dK, dV and dla of one chunk from Q, K,
-//                      V, dO, S_c and dS_c. Waves 0-3 own token block wl in the query role (dQ, row sums of
-//                      dA o A, q.(S dO)); waves 4-7 own it in the key role (dV, dK, column sums, k.(dS v), <S, dS>).
-// Every product that has a transposed operand is computed in the orientation whose accumulator is the next
-// product's operand (pgn::pack).
-#include <algorithm>
-
-#include "lookback.h"
+//     dQ = dP K + eL o (dO S_c^T)            dK = dP^T Q + w o (V dS^T)
+//     dV = A^T dO + (K o w) dS               dS_c = a dS + (Q o eL)^T dO
+//     dL_t = rowsum(dA o A)_t - colsum(dA o A)_t + eL_t q_t.(S_c dO_t) - w_t k_t.(dS v_t),
+//     dL_{C-1} += sum_s w_s k_s.(dS v_s) + a <S_c, dS>,     dla = reverse cumulative sum of dL.
+// (equations of `src/assoc_kernel.py:73-116`, `:205-220`, `:279-296`, merged into one pass). Every product that
+// has a transposed operand is computed in the orientation whose accumulator is the next product's operand, so
+// nothing round-trips through LDS except the two copies of dS.
 #include "mfma_tile.h"
 
 using namespace pgn;
@@ -46,397 +33,162 @@ namespace {
 constexpr int C = 64;
 constexpr int DK = 64;
 constexpr int TILE = 64 * kPitch;  // one staged 64 x 64 tile
-constexpr int SW = 8;              // waves (chunks in flight) of the state pass
 
-PGN_DEVICE float incl_scan64(float x, int l) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float y = __shfl_up(x, off);
-    if (l >= off) x += y;
-  }
-  return x;
+constexpr int FBV = 32;         // value columns per forward workgroup
+constexpr int FNB = DK / FBV;   // forward workgroups per (batch, head)
+
+// Forward block -> (batch-head, value block). The FNB workgroups of one head are 8 apart in launch order, and the
+// dispatcher deals workgroups round-robin over the 8 XCDs, so they run on the same XCD and the second one's reads
+// of Q and K hit in that XCD's L2.
+PGN_DEVICE void fwd_block(int& bh, int& jb) {
+  const int x = blockIdx.x;
+  const int grp = x / (8 * FNB), rem = x - grp * (8 * FNB);
+  jb = rem >> 3;
+  bh = grp * 8 + (rem & 7);
 }
 
-PGN_DEVICE float rev_scan64(float x, int l) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float y = __shfl_down(x, off);
-    if (l + off < 64) x += y;
-  }
-  return x;
-}
+__global__ __launch_bounds__(256) void aspin_plain_fwd(const __bf16* __restrict__ q, const __bf16* __restrict__ k,
+                                                       const __bf16* __restrict__ v, const float* __restrict__ la,
+                                                       const float* __restrict__ S0, __bf16* __restrict__ o,
+                                                       float* __restrict__ Sfin, __bf16* __restrict__ sent, int T,
+                                                       int NC, int nbh) {
+  __shared__ __align__(16) __bf16 Qs[TILE], Ks[TILE], KT[TILE], VT[FBV * kPitch], ST[FBV * kPitch];
+  __shared__ __align__(16) float Ls[C], eLs[C], ws[C];
 
-// Per-chunk decay statistics into LDS (one wave, lane = token): L, eL = exp(L), w = exp(L_C - L).
-PGN_DEVICE void chunk_decays(float la_l, int l, float* Ls, float* eLs, float* ws) {
-  const float L = incl_scan64(la_l, l);
-  const float LC = __shfl(L, 63);
-  Ls[l] = L;
-  eLs[l] = __expf(L);
-  ws[l] = __expf(fminf(LC - L, 0.f));
-}
-
-// ------------------------------------------------------------------------------------------------------------------
-// state pass. The chunk terms are computed transposed (M^T = Y^T (X o f)), so a lane's accumulator holds four
-// consecutive columns of one state row: tile tt = 4 db + jt, lane l, element r is entry
-// (16 db + l % 16, 16 jt + 4 (l / 16) + r). The carry buffer holds the state in that order (a wave moves it with
-// 16-byte LDS accesses) and every global access of a state is an 8- or 16-byte row segment.
-constexpr size_t kStateSmem = (size_t)SW * 2 * TILE * sizeof(__bf16) + 16 * 64 * 4 * sizeof(float) +
-                              (size_t)SW * C * sizeof(float) + SW * sizeof(float);
-
-template <bool REV>
-__global__ __launch_bounds__(64 * SW) void plain_state(const __bf16* __restrict__ X, const __bf16* __restrict__ Y,
-                                                       const float* __restrict__ la, const float* __restrict__ init,
-                                                       __bf16* __restrict__ out, float* __restrict__ fin, int T,
-                                                       int NC) {
-  extern __shared__ __align__(16) unsigned char smem[];
+  int bh, jb;
+  fwd_block(bh, jb);
+  if (bh >= nbh) return;
   const WaveIdx x = wave_idx();
-  const int w = x.w, l = x.l, g = x.g, i = x.i;
-  __bf16* XT = reinterpret_cast<__bf16*>(smem) + (size_t)w * 2 * TILE;  // this wave's X^T (d, t)
-  __bf16* YT = XT + TILE;                                                 // this wave's Y^T (j, t)
-  f32x4* CB = reinterpret_cast<f32x4*>(smem + (size_t)SW * 2 * TILE * sizeof(__bf16));
-  float* fw = reinterpret_cast<float*>(CB + 16 * 64);  // [SW][C] per-token scale of each wave's chunk
-  float* aw = fw + SW * C;                             // [SW] chunk decay a_c
-  const int bh = blockIdx.x;
+  const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
+  const int j0 = jb * FBV;  // first value column owned here
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
 
-  // initial carry: S0 (forward) or dS_final (backward), zero when absent; waves split the 16 tiles
-  for (int tt = w; tt < 16; tt += SW) {
-    const int db = tt >> 2, jt = tt & 3;
-    CB[tt * 64 + l] = init ? *reinterpret_cast<const f32x4*>(init + soff + (size_t)(16 * db + i) * DK + 16 * jt + 4 * g)
-                           : zero4();
+  // state rows 16w + 4g + r, columns j0 + 16 jt + i
+  f32x4 S[2];
+#pragma unroll
+  for (int jt = 0; jt < 2; ++jt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) S[jt][r] = S0 ? S0[soff + (16 * w + 4 * g + r) * DK + j0 + 16 * jt + i] : 0.f;
+    store_T(ST, 16 * jt, 16 * w, g, i, S[jt]);
   }
 
-  const int ngroups = (NC + SW - 1) / SW;
-  for (int gi = 0; gi < ngroups; ++gi) {
-    const int n = gi * SW + w;  // position of this wave's chunk in processing order
-    const bool active = n < NC;
-    const int c = REV ? NC - 1 - n : n;
-    Blk4 xb[4], yb[4];
-    float lav = 0.f;
-    if (active) {
-      const int t0 = c * C, nr = min(C, T - t0);
+  // this thread's 4x4 staging blocks: Q, K (64 x 64, all threads), V (64 x 32, threads < 128)
+  const int br = 4 * (tid >> 4), bc = 4 * (tid & 15);
+  const int vr = 4 * (tid >> 3), vc = 4 * (tid & 7);
+  const bool vthr = tid < 128;
+  Blk4 pq = load_blk(q + boff, DK, min(C, T), tid);
+  Blk4 pk = load_blk(k + boff, DK, min(C, T), tid);
+  Blk4 pv;
+  if (vthr) pv = load_blk_w(v + boff + j0, DK, min(C, T), FBV, tid);
+  float pla = (w == 0 && x.l < T) ? la[(size_t)bh * T + x.l] : 0.f;
+
+  const int tq = 16 * w + i;  // this lane's token within the chunk for t-indexed operands
+  for (int c = 0; c < NC; ++c) {
+    const int t0 = c * C;
+    // publish chunk c (prefetched) to LDS
+    put_blk(Qs, pq, br, bc);
+    put_blk(Ks, pk, br, bc);
+    put_blk_T(KT, pk, br, bc);
+    if (vthr) put_blk_T(VT, pv, vr, vc);
+    if (w == 0) {
+      float L = pla;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        xb[b] = load_blk(X + boff + (size_t)t0 * DK, DK, nr, l + 64 * b);
-        yb[b] = load_blk(Y + boff + (size_t)t0 * DK, DK, nr, l + 64 * b);
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(L, off);
+        if (x.l >= off) L += y;
       }
-      lav = l < nr ? la[(size_t)bh * T + t0 + l] : 0.f;
-    }
-    __syncthreads();  // the previous group is done with the LDS tiles and the scale vectors
-    if (active) {
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int blk = l + 64 * b;
-        put_blk_T(XT, xb[b], 4 * (blk >> 4), 4 * (blk & 15));
-        put_blk_T(YT, yb[b], 4 * (blk >> 4), 4 * (blk & 15));
-      }
-      const float L = incl_scan64(lav, l);
       const float LC = __shfl(L, 63);
-      fw[w * C + l] = REV ? __expf(L) : __expf(fminf(LC - L, 0.f));
-      if (l == 0) aw[w] = __expf(LC);
-    }
-    __syncthreads();  // staged tiles and scales visible
-    f32x4 M[16];
-    if (active) {
-      // M^T = Y^T (X o f): rows j (block jt), columns d (block db); contracted over the chunk's tokens
-      const float* f = fw + w * C;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const bf16x8 b0 = frag_scaled_k(XT, 16 * db + i, 0, g, f), b1 = frag_scaled_k(XT, 16 * db + i, 1, g, f);
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-          const f32x4 acc = pgn_mfma(frag(YT, 16 * jt + i, 0, g), b0, zero4());
-          M[4 * db + jt] = pgn_mfma(frag(YT, 16 * jt + i, 1, g), b1, acc);
-        }
-      }
-    }
-    // the recurrence across the group's chunks, in processing order: carry <- a_c carry + M_c
-    bf16x4 Sin[16];  // the carry this chunk saw, rounded for the store
-#pragma unroll 1
-    for (int s = 0; s < SW; ++s) {
-      if (w == s && active) {
-        const float a = aw[w];
-#pragma unroll
-        for (int tt = 0; tt < 16; ++tt) {
-          const f32x4 cur = CB[tt * 64 + l];
-          Sin[tt] = to_bf16x4(cur);
-          CB[tt * 64 + l] = cur * a + M[tt];
-        }
-      }
-      __syncthreads();
-    }
-    if (active) {  // the state this chunk saw: entering state (forward) or leaving gradient (backward), bf16
-      __bf16* dst = out + ((size_t)bh * NC + c) * DK * DK;
-#pragma unroll
-      for (int tt = 0; tt < 16; ++tt)
-        *reinterpret_cast<bf16x4*>(dst + (16 * (tt >> 2) + i) * DK + 16 * (tt & 3) + 4 * g) = Sin[tt];
-    }
-  }
-  // final carry: S_final (forward) or dS0 (backward)
-  if (fin) {
-    for (int tt = w; tt < 16; tt += SW) {
-      *reinterpret_cast<f32x4*>(fin + soff + (size_t)(16 * (tt >> 2) + i) * DK + 16 * (tt & 3) + 4 * g) = CB[tt * 64 + l];
-    }
-  }
-}
-
-// ------------------------------------------------------------------------------------------------------------------
-// Single-pass forward (persistent; look-back scheduling and memory ordering as described in lookback.h). A
-// workgroup of 4 waves per item (batch-head, chunk); wave w owns d block w of the chunk's state term and token block
-// w of its output. The state term is computed transposed, M^T = V^T (K o w), so a lane holds the four state entries
-// (d = 16 w + i, j = 16 jt + 4 g .. + 3) of each value block jt: aggregates and inclusive states are exchanged in
-// that order ([item][w][jt][lane] f32x4, 16 KiB) and `sent` is written as 8-byte row segments.
-//
-// Inputs of the next item are prefetched into registers by waves 1-3 (one tile each: Q, K, V) while the current
-// item computes; wave 0 only prefetches the 64 decays, so its polling loads never wait behind tile loads (the
-// vector memory counter completes in order).
-struct LbPtrs {
-  uint64_t* flags;
-  float* av;
-  f32x4* agg;
-  f32x4* incl;
-};
-
-PGN_DEVICE LbPtrs lb_ptrs(unsigned char* ws, int64_t n) {
-  const LbLayout L = lb_layout(n);
-  LbPtrs P;
-  P.flags = reinterpret_cast<uint64_t*>(ws + L.flags_off);
-  P.av = reinterpret_cast<float*>(ws + L.av_off);
-  P.agg = reinterpret_cast<f32x4*>(ws + L.agg_off);
-  P.incl = reinterpret_cast<f32x4*>(ws + L.incl_off);
-  return P;
-}
-
-// Exchange-order offset (bytes) of lane l's value block jt of wave w within one 16 KiB state.
-PGN_DEVICE int xoff(int w, int jt, int l) { return ((w * 4 + jt) * 64 + l) * 16; }
-
-// The entering value X of scan position `pos` of head bh, in the exchange order of wave w: wait for the block's
-// publications, then run the recurrence from the block's entering value (`init`, fp32 (d, j) row-major or NULL for
-// zero, in the first block; the previous block's inclusive value otherwise) through the aggregates of positions
-// b .. pos-1, loaded two at a time. Item of position p: p * nbh + bh. s_xcc: LDS, kLbGroup + 1 ints.
-PGN_DEVICE void lb_entering(const LbPtrs& P, uint64_t epoch, int pos, int bh, int nbh, int w, int l, int g, int i,
-                            int* s_xcc, const float* __restrict__ init, f32x4 (&X)[4]) {
-  const int b = pos - pos % kLbGroup;
-  const int me = xcc_id();
-  if (pos > 0) {
-    if (w == 0) {
-      int wx = 0;
-      const bool ok = lb_wait_block(pos, l, epoch, [&](int p) { return P.flags + (size_t)p * nbh + bh; }, &wx);
-      if (l <= pos - b) s_xcc[l] = ok ? wx : -1;
+      Ls[x.l] = L;
+      eLs[x.l] = __expf(L);
+      ws[x.l] = __expf(fminf(LC - L, 0.f));
     }
     __syncthreads();
-    if (s_xcc[0] < 0) {  // timed out: count it and continue with a zero state (never hang)
-      if (threadIdx.x == 0) atomicAdd(&g_lookback_timeouts, 1u);
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) X[jt] = zero4();
-      return;
+    // prefetch chunk c + 1 while this one computes
+    if (c + 1 < NC) {
+      const int n0 = t0 + C, nr = min(C, T - n0);
+      pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, tid);
+      pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, tid);
+      if (vthr) pv = load_blk_w(v + boff + (size_t)n0 * DK + j0, DK, nr, FBV, tid);
+      if (w == 0) pla = (n0 + x.l < T) ? la[(size_t)bh * T + n0 + x.l] : 0.f;
     }
-  }
-  if (b > 0) {
-    const bool local = __builtin_amdgcn_readfirstlane(s_xcc[pos - b]) == me;
-    const auto r = lb_rsrc(P.incl + ((size_t)(b - 1) * nbh + bh) * 1024, 16384);
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) X[jt] = lb_load4(r, xoff(w, jt, l), local);
-  } else {
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-      X[jt] = init ? *reinterpret_cast<const f32x4*>(init + (size_t)bh * DK * DK + (16 * w + i) * DK + 16 * jt + 4 * g)
-                   : zero4();
-  }
-  for (int j0 = b; j0 < pos; j0 += 2) {
-    f32x4 buf[2][4];
-    float aj[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int j = min(j0 + u, pos - 1);
-      const size_t it = (size_t)j * nbh + bh;
-      const bool local = __builtin_amdgcn_readfirstlane(s_xcc[j - b]) == me;
-      const auto r = lb_rsrc(P.agg + it * 1024, 16384);
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) buf[u][jt] = lb_load4(r, xoff(w, jt, l), local);
-      aj[u] = __hip_atomic_load(P.av + it, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if (j0 + u < pos) {
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) X[jt] = X[jt] * aj[u] + buf[u][jt];
-      }
-    }
-  }
-}
 
-constexpr size_t kFwdSmem = 5 * TILE * sizeof(__bf16) + 3 * C * sizeof(float) + 16 * sizeof(int);
-
-__global__ __launch_bounds__(256, 2) void plain_fwd_sp(const __bf16* __restrict__ q, const __bf16* __restrict__ k,
-                                                    const __bf16* __restrict__ v, const float* __restrict__ la,
-                                                    const float* __restrict__ S0, __bf16* __restrict__ o,
-                                                    float* __restrict__ S_final, __bf16* __restrict__ sent,
-                                                    unsigned char* ws, uint64_t epoch, int nbh, int T, int NC) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  __bf16* Qs = reinterpret_cast<__bf16*>(smem);
-  __bf16* Ks = Qs + TILE;
-  __bf16* KT = Ks + TILE;
-  __bf16* VT = KT + TILE;
-  __bf16* ST = VT + TILE;
-  float* Ls = reinterpret_cast<float*>(ST + TILE);
-  float* eLs = Ls + C;
-  float* wsc = eLs + C;
-  int* s_xcc = reinterpret_cast<int*>(wsc + C);
-  const WaveIdx x = wave_idx();
-  const int w = x.w, l = x.l, g = x.g, i = x.i, tid = threadIdx.x;
-  const int n = nbh * NC;
-  const LbPtrs P = lb_ptrs(ws, n);
-  const int me = xcc_id();
-
-  // prefetch registers: wave 1 the Q tile, wave 2 the K tile, wave 3 the V tile (four 4 x 4 blocks per lane);
-  // wave 0 the 64 decays
-  Blk4 pre[4];
-  float pre_la = 0.f;
-  auto prefetch = [&](int it) {
-    const int c = it / nbh, bh = it - c * nbh;
-    const int t0 = c * C, nr = min(C, T - t0);
-    const size_t coff = ((size_t)bh * T + t0) * DK;
-    if (w == 0) {
-      pre_la = l < nr ? la[(size_t)bh * T + t0 + l] : 0.f;
-    } else {
-      const __bf16* src = (w == 1 ? q : w == 2 ? k : v) + coff;
+    // (Q K^T)^T tiles (s block sb, t block w), decayed and masked: lane holds column t = tq, rows s.
+    const bf16x8 qf0 = frag(Qs, tq, 0, g), qf1 = frag(Qs, tq, 1, g);
+    const float Lt = Ls[tq];
+    f32x4 pt[4];
 #pragma unroll
-      for (int b4 = 0; b4 < 4; ++b4) pre[b4] = load_blk(src, DK, nr, l + 64 * b4);
-    }
-  };
-  int item = blockIdx.x;
-  if (item < n) prefetch(item);
-
-  for (; item < n; item += gridDim.x) {
-    const int c = item / nbh, bh = item - c * nbh;
-    const int t0 = c * C, nr = min(C, T - t0);
-    const size_t coff = ((size_t)bh * T + t0) * DK;
-    __syncthreads();  // the previous item is done with the LDS tiles and vectors
-    if (w == 0) {
-      chunk_decays(pre_la, l, Ls, eLs, wsc);
-    } else {
+    for (int sb = 0; sb < 4; ++sb) {
+      pt[sb] = zero4();
+      if (sb <= w) {
+        pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
+        pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
+        const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
 #pragma unroll
-      for (int b4 = 0; b4 < 4; ++b4) {
-        const int blk = l + 64 * b4, br = 4 * (blk >> 4), bc = 4 * (blk & 15);
-        if (w == 1) {
-          put_blk(Qs, pre[b4], br, bc);
-        } else if (w == 2) {
-          put_blk(Ks, pre[b4], br, bc);
-          put_blk_T(KT, pre[b4], br, bc);
-        } else {
-          put_blk_T(VT, pre[b4], br, bc);
+        for (int r = 0; r < 4; ++r) {
+          const int s = 16 * sb + 4 * g + r;
+          pt[sb][r] = (s <= tq) ? pt[sb][r] * __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
         }
       }
     }
-    __syncthreads();
+    const bf16x8 af0 = pack(pt[0], pt[1]);
+    const bf16x8 af1 = pack(pt[2], pt[3]);
+    const float eLt = eLs[tq];
+    const bf16x8 qe0 = frag_scaled(Qs, tq, 0, g, eLt);
+    const bf16x8 qe1 = frag_scaled(Qs, tq, 1, g, eLt);
 
-    // this chunk's state term, d block w: M^T tiles (j block jt, d block w) = V^T (K o w)
-    f32x4 M[4];
-    {
-      const bf16x8 b0 = frag_scaled_k(KT, 16 * w + i, 0, g, wsc), b1 = frag_scaled_k(KT, 16 * w + i, 1, g, wsc);
+    // O^T tiles (value block jt, t block w) = V^T A^T + S^T (Q o eL)^T; lane holds token tq, 4 value columns
+    const bool t_ok = t0 + tq < T;
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        M[jt] = pgn_mfma(frag(VT, 16 * jt + i, 0, g), b0, zero4());
-        M[jt] = pgn_mfma(frag(VT, 16 * jt + i, 1, g), b1, M[jt]);
-      }
+    for (int jt = 0; jt < 2; ++jt) {
+      f32x4 acc = zero4();
+      acc = pgn_mfma(frag(VT, 16 * jt + i, 0, g), af0, acc);
+      if (w >= 2) acc = pgn_mfma(frag(VT, 16 * jt + i, 1, g), af1, acc);
+      acc = pgn_mfma(frag(ST, 16 * jt + i, 0, g), qe0, acc);
+      acc = pgn_mfma(frag(ST, 16 * jt + i, 1, g), qe1, acc);
+      if (t_ok)
+        *reinterpret_cast<bf16x4*>(o + boff + (size_t)(t0 + tq) * DK + j0 + 16 * jt + 4 * g) = to_bf16x4(acc);
     }
+
+    // the entering state, bf16, (d, j) layout
+    if (sent) {
+      __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[(16 * w + 4 * g + r) * DK + j0 + 16 * jt + i] = (__bf16)S[jt][r];
+    }
+
+    // S <- a S + (K o w)^T V on this workgroup's columns, rows 16w.. of S
     const float a_c = __expf(Ls[C - 1]);
-    const bool last = c == NC - 1;
-    const bool block_last = c % kLbGroup == kLbGroup - 1;
-    if (!last && !block_last) {  // publish the aggregate for the later chunks of this block
-      const auto r = lb_rsrc(P.agg + (size_t)item * 1024, 16384);
+    const bf16x8 kw0 = frag_scaled_k(KT, 16 * w + i, 0, g, ws);
+    const bf16x8 kw1 = frag_scaled_k(KT, 16 * w + i, 1, g, ws);
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) lb_store4(r, xoff(w, jt, l), M[jt]);
-      if (tid == 0) __hip_atomic_store(P.av + item, a_c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      lb_publish_flag(P.flags + item, lb_flag_word(epoch, me, kFlagAgg));
-    }
-    // the next item's inputs, in flight while this one computes
-    if (item + (int)gridDim.x < n) prefetch(item + gridDim.x);
-
-    // intra-chunk output, token block w: (Q K^T)^T tiles decayed and masked, then O^T = V^T A^T
-    const int t = 16 * w + i;
-    f32x4 acc[4];
-    {
-      const bf16x8 qf0 = frag(Qs, t, 0, g), qf1 = frag(Qs, t, 1, g);
-      f32x4 pt[4];
-#pragma unroll
-      for (int sb = 0; sb < 4; ++sb) {
-        pt[sb] = zero4();
-        if (sb <= w) {
-          pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
-          pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
-        }
-      }
-      const float Lt = Ls[t];
-#pragma unroll
-      for (int sb = 0; sb < 4; ++sb) {
-        if (sb <= w) {
-          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) pt[sb][r] *= masked_decay(Lt - Lsv[r], 16 * sb + 4 * g + r <= t);
-        }
-      }
-      const bf16x8 af0 = pack(pt[0], pt[1]), af1 = pack(pt[2], pt[3]);
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        acc[jt] = pgn_mfma(frag(VT, 16 * jt + i, 0, g), af0, zero4());
-        if (w >= 2) acc[jt] = pgn_mfma(frag(VT, 16 * jt + i, 1, g), af1, acc[jt]);
-      }
-    }
-
-    // the entering state S_c; the leaving state is published (last chunk of a block) or is the final state
-    f32x4 Sx[4];
-    lb_entering(P, epoch, c, bh, nbh, w, l, g, i, s_xcc, S0, Sx);
-    if (last || block_last) {
-      f32x4 Sn[4];
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) Sn[jt] = Sx[jt] * a_c + M[jt];
-      if (!last) {
-        const auto r = lb_rsrc(P.incl + (size_t)item * 1024, 16384);
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) lb_store4(r, xoff(w, jt, l), Sn[jt]);
-        lb_publish_flag(P.flags + item, lb_flag_word(epoch, me, kFlagIncl));
-      } else {
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-          *reinterpret_cast<f32x4*>(S_final + (size_t)bh * DK * DK + (16 * w + i) * DK + 16 * jt + 4 * g) = Sn[jt];
-      }
-    }
-    // S_c: to `sent` (bf16 row segments) and, transposed, to LDS for the inter-chunk product
-    {
-      __bf16* sdst = sent ? sent + ((size_t)bh * NC + c) * DK * DK + (16 * w + i) * DK + 4 * g : nullptr;
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        const bf16x4 sb4 = to_bf16x4(Sx[jt]);
-        if (sdst) *reinterpret_cast<bf16x4*>(sdst + 16 * jt) = sb4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ST[(16 * jt + 4 * g + r) * kPitch + 16 * w + i] = sb4[r];
-      }
+    for (int jt = 0; jt < 2; ++jt) {
+      S[jt] = S[jt] * a_c;
+      S[jt] = pgn_mfma(kw0, frag(VT, 16 * jt + i, 0, g), S[jt]);
+      S[jt] = pgn_mfma(kw1, frag(VT, 16 * jt + i, 1, g), S[jt]);
     }
     __syncthreads();
-    // O^T += S^T (Q o eL)^T, then store: lane holds token t, value columns 16 jt + 4 g ..
-    const float eLt = eLs[t];
-    const bf16x8 qe0 = frag_scaled(Qs, t, 0, g, eLt), qe1 = frag_scaled(Qs, t, 1, g, eLt);
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      acc[jt] = pgn_mfma(frag(ST, 16 * jt + i, 0, g), qe0, acc[jt]);
-      acc[jt] = pgn_mfma(frag(ST, 16 * jt + i, 1, g), qe1, acc[jt]);
-      if (t < nr) *reinterpret_cast<bf16x4*>(o + coff + (size_t)t * DK + 16 * jt + 4 * g) = to_bf16x4(acc[jt]);
-    }
+    for (int jt = 0; jt < 2; ++jt) store_T(ST, 16 * jt, 16 * w, g, i, S[jt]);
   }
+
+#pragma unroll
+  for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Sfin[soff + (16 * w + 4 * g + r) * DK + j0 + 16 * jt + i] = S[jt][r];
 }
 
-// ------------------------------------------------------------------------------------------------------------------
-// backward of one chunk: 8 waves
-constexpr size_t kLocalSmem = 10 * TILE * sizeof(__bf16) + (7 * C + 4) * sizeof(float);
-
-__global__ __launch_bounds__(512) void plain_bwd_local(
+// Backward: 8 waves per (batch, head). Waves 0-3 (group D) own t block wl = w & 3 and compute everything that does
+// not depend on dS: dQ, the row sums of dA o A and q_t.(S_c dO_t). Waves 4-7 (group K) own s block wl and d block wl
+// and carry dS: dV, dK, the column sums of dA o A, k_s.(dS v_s), <S_c, dS> and the dS update. Waves w and w + 4 share
+// a SIMD, and the two groups' MFMA counts per SIMD are within 10% of each other.
+__global__ __launch_bounds__(512) void aspin_plain_bwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
-    const float* __restrict__ la, const __bf16* __restrict__ sent, const __bf16* __restrict__ dSc,
-    const __bf16* __restrict__ dO, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    float* __restrict__ dla, int T, int NC) {
+    const float* __restrict__ la, const __bf16* __restrict__ sent, const __bf16* __restrict__ dO,
+    const float* __restrict__ dSfin, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
+    float* __restrict__ dla, float* __restrict__ dS0, int T, int NC) {
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* Qs = reinterpret_cast<__bf16*>(smem);
   __bf16* QT = Qs + TILE;
@@ -446,283 +198,298 @@ __global__ __launch_bounds__(512) void plain_bwd_local(
   __bf16* Os = Vs + TILE;    // dO
   __bf16* OT = Os + TILE;    // dO^T
   __bf16* Ss = OT + TILE;    // S_c, (d, j)
-  __bf16* dSs = Ss + TILE;   // dS_c, (d, j)
-  __bf16* dST = dSs + TILE;  // dS_c^T, (j, d)
+  __bf16* dSs = Ss + TILE;   // dS, (d, j)
+  __bf16* dST = dSs + TILE;  // dS^T, (j, d)
   float* Ls = reinterpret_cast<float*>(dST + TILE);
   float* eLs = Ls + C;
   float* ws = eLs + C;
-  float* rowM = ws + C;    // row sums of dA o A (query role)
-  float* colM = rowM + C;  // column sums of dA o A (key role)
-  float* qz = colM + C;    // q_t . (S_c dO_t)
-  float* dwv = qz + C;     // k_s . (dS_c v_s)
-  float* sdot = dwv + C;   // per-wave <S_c, dS_c>
+  float* rowM = ws + C;   // row sums of dA o A (group D)
+  float* colM = rowM + C; // column sums of dA o A (group K)
+  float* qz = colM + C;   // q_t . (S_c dO_t)
+  float* dwv = qz + C;    // k_s . (dS v_s)
+  float* sdot = dwv + C;  // per-wave <S_c, dS>
 
   const WaveIdx x = wave_idx();
   const int w = x.w, wl = w & 3, g = x.g, i = x.i, tid = threadIdx.x;
   const bool gk = w >= 4;
-  const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;
-  const int t0 = c * C, nr = min(C, T - t0);
-  const size_t coff = ((size_t)bh * T + t0) * DK;
-  const size_t soff = ((size_t)bh * NC + c) * DK * DK;
-  {
-    const int b = tid & 255;
-    const int br = 4 * (b >> 4), bc = 4 * (b & 15);
-    if (tid < 256) {
-      const Blk4 pq = load_blk(q + coff, DK, nr, b);
-      const Blk4 pv = load_blk(v + coff, DK, nr, b);
-      const Blk4 ps = load_blk(sent + soff, DK, DK, b);
-      const Blk4 pd = load_blk(dSc + soff, DK, DK, b);
-      put_blk(Qs, pq, br, bc);
-      put_blk_T(QT, pq, br, bc);
-      put_blk(Vs, pv, br, bc);
-      put_blk(Ss, ps, br, bc);
-      put_blk(dSs, pd, br, bc);
-      put_blk_T(dST, pd, br, bc);
-    } else {
-      const Blk4 pk = load_blk(k + coff, DK, nr, b);
-      const Blk4 po = load_blk(dO + coff, DK, nr, b);
-      put_blk(Ks, pk, br, bc);
-      put_blk_T(KT, pk, br, bc);
-      put_blk(Os, po, br, bc);
-      put_blk_T(OT, po, br, bc);
-    }
-    if (w == 0) chunk_decays(x.l < nr ? la[(size_t)bh * T + t0 + x.l] : 0.f, x.l, Ls, eLs, ws);
-  }
-  __syncthreads();
+  const int bh = blockIdx.x;
+  const size_t boff = (size_t)bh * T * DK;
+  const size_t soff = (size_t)bh * DK * DK;
 
-  const int me = 16 * wl + i;  // query role: this lane's t; key role: this lane's s
-  const bool row_ok = me < nr;
-  if (!gk) {
-    // ---------------- query role: t = me
-    const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
-    const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
-    f32x4 PT[4], dAT[4];
+  // group K: dS rows 16wl + 4g + r, column 16 jt + i
+  f32x4 dS[4];
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {  // rows s, lane t: P[t][s] and dA[t][s]
-      PT[sb] = zero4();
-      dAT[sb] = zero4();
-      if (sb <= wl) {
-        PT[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, PT[sb]);
-        PT[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, PT[sb]);
-        dAT[sb] = pgn_mfma(frag(Vs, 16 * sb + i, 0, g), of0, dAT[sb]);
-        dAT[sb] = pgn_mfma(frag(Vs, 16 * sb + i, 1, g), of1, dAT[sb]);
-      }
-    }
-    const float Lt = Ls[me];
-    float rowacc = 0.f;
-#pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      if (sb <= wl) {
-        const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float dec = masked_decay(Lt - Lsv[r], 16 * sb + 4 * g + r <= me);
-          rowacc += dAT[sb][r] * (PT[sb][r] * dec);
-          dAT[sb][r] *= dec;  // now dP^T
-        }
-      }
-    }
-    rowacc = sum_groups(rowacc);
-    if (g == 0) rowM[me] = rowacc;
-    const bf16x8 b0 = pack(dAT[0], dAT[1]), b1 = pack(dAT[2], dAT[3]);
-    const float eLt = eLs[me];
-    const __bf16* qrow = Qs + me * kPitch;
-    float qzt = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {  // dQ^T tiles (d block dt, t block wl) = K^T dP^T + eL (S dO^T)
-      f32x4 acc = pgn_mfma(frag(KT, 16 * dt + i, 0, g), b0, zero4());
-      if (wl >= 2) acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), b1, acc);
-      f32x4 Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, zero4());
-      Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
-      const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
-#pragma unroll
-      for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
-      acc = acc + Z * eLt;
-      if (row_ok) *reinterpret_cast<bf16x4*>(dq + coff + (size_t)me * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
-    }
-    qzt = sum_groups(qzt);
-    if (g == 0) qz[me] = qzt;
-  } else {
-    // ---------------- key role: s = me
-    const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
-    const bf16x8 vf0 = frag(Vs, me, 0, g), vf1 = frag(Vs, me, 1, g);
-    f32x4 At[4], dPt[4];
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {  // rows t, lane s: P[t][s] and dA[t][s]
-      At[tb] = zero4();
-      dPt[tb] = zero4();
-      if (tb >= wl) {
-        At[tb] = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, At[tb]);
-        At[tb] = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, At[tb]);
-        dPt[tb] = pgn_mfma(frag(Os, 16 * tb + i, 0, g), vf0, dPt[tb]);
-        dPt[tb] = pgn_mfma(frag(Os, 16 * tb + i, 1, g), vf1, dPt[tb]);
-      }
-    }
-    const float Ls_s = Ls[me];
-    float colacc = 0.f;
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      if (tb >= wl) {
-        const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float dec = masked_decay(Ltv[r] - Ls_s, 16 * tb + 4 * g + r >= me);
-          At[tb][r] *= dec;
-          colacc += dPt[tb][r] * At[tb][r];
-          dPt[tb][r] *= dec;
-        }
-      }
-    }
-    colacc = sum_groups(colacc);
-    if (g == 0) colM[me] = colacc;
-    const bf16x8 A0 = pack(At[0], At[1]), A1 = pack(At[2], At[3]);
-    const bf16x8 dP0 = pack(dPt[0], dPt[1]), dP1 = pack(dPt[2], dPt[3]);
-    const float w_s = ws[me];
-    // dV^T tiles (j block jt, s block wl) = dO^T A + dS^T (K o w)^T
-    const bf16x8 kw0 = frag_scaled(Ks, me, 0, g, w_s), kw1 = frag_scaled(Ks, me, 1, g, w_s);
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      f32x4 acc = zero4();
-      if (wl < 2) acc = pgn_mfma(frag(OT, 16 * jt + i, 0, g), A0, acc);
-      acc = pgn_mfma(frag(OT, 16 * jt + i, 1, g), A1, acc);
-      acc = pgn_mfma(frag(dST, 16 * jt + i, 0, g), kw0, acc);
-      acc = pgn_mfma(frag(dST, 16 * jt + i, 1, g), kw1, acc);
-      if (row_ok) *reinterpret_cast<bf16x4*>(dv + coff + (size_t)me * DK + 16 * jt + 4 * g) = to_bf16x4(acc);
-    }
-    // dK^T tiles (d block dt, s block wl) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
-    const __bf16* krow = Ks + me * kPitch;
-    float dw = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      f32x4 acc = zero4();
-      if (wl < 2) acc = pgn_mfma(frag(QT, 16 * dt + i, 0, g), dP0, acc);
-      acc = pgn_mfma(frag(QT, 16 * dt + i, 1, g), dP1, acc);
-      f32x4 Y = pgn_mfma(frag(dSs, 16 * dt + i, 0, g), vf0, zero4());
-      Y = pgn_mfma(frag(dSs, 16 * dt + i, 1, g), vf1, Y);
-      const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
-      acc = acc + Y * w_s;
-      if (row_ok) *reinterpret_cast<bf16x4*>(dk + coff + (size_t)me * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
-    }
-    dw = sum_groups(dw);
-    if (g == 0) dwv[me] = dw;
-    // <S_c, dS_c> over key rows 16 wl ..
-    float sd = 0.f;
+  for (int jt = 0; jt < 4; ++jt) dS[jt] = zero4();
+  if (gk) {
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = 16 * wl + 4 * g + r;
-        sd += (float)Ss[d * kPitch + 16 * jt + i] * (float)dSs[d * kPitch + 16 * jt + i];
-      }
+      for (int r = 0; r < 4; ++r)
+        dS[jt][r] = dSfin ? dSfin[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] : 0.f;
+      store_T(dST, 16 * jt, 16 * wl, g, i, dS[jt]);
+      store_N(dSs, 16 * wl, 16 * jt, g, i, dS[jt]);
     }
-    sd = wave_sum(sd);
-    if (x.l == 0) sdot[wl] = sd;
   }
-  __syncthreads();
-  if (w == 0) {  // dla for this chunk: the reverse cumulative sum of dL
-    const int t = x.l;
-    const float wdw = ws[t] * dwv[t];
-    float dL = rowM[t] - colM[t] + eLs[t] * qz[t] - wdw;
-    const float tot = wave_sum(wdw);
-    if (t == C - 1) dL += tot + __expf(Ls[C - 1]) * (sdot[0] + sdot[1] + sdot[2] + sdot[3]);
-    dL = rev_scan64(dL, t);
-    if (t < nr) dla[(size_t)bh * T + t0 + t] = dL;
+
+  // staging: threads 0-255 carry Q, V and S_c; threads 256-511 carry K and dO (one 4x4 block of each)
+  const int b = tid & 255;
+  const int br = 4 * (b >> 4), bc = 4 * (b & 15);
+  const bool lo = tid < 256;
+  Blk4 p1, p2, p3;
+  {
+    const int t0 = (NC - 1) * C, nr = min(C, T - t0);
+    if (lo) {
+      p1 = load_blk(q + boff + (size_t)t0 * DK, DK, nr, b);
+      p2 = load_blk(v + boff + (size_t)t0 * DK, DK, nr, b);
+      p3 = load_blk(sent + ((size_t)bh * NC + NC - 1) * DK * DK, DK, DK, b);
+    } else {
+      p1 = load_blk(k + boff + (size_t)t0 * DK, DK, nr, b);
+      p2 = load_blk(dO + boff + (size_t)t0 * DK, DK, nr, b);
+    }
+  }
+  float pla = (w == 0 && (NC - 1) * C + x.l < T) ? la[(size_t)bh * T + (NC - 1) * C + x.l] : 0.f;
+
+  const int me = 16 * wl + i;  // group D: this lane's t; group K: this lane's s
+  for (int cc = NC - 1; cc >= 0; --cc) {
+    const int t0 = cc * C;
+    if (lo) {
+      put_blk(Qs, p1, br, bc);
+      put_blk_T(QT, p1, br, bc);
+      put_blk(Vs, p2, br, bc);
+      put_blk(Ss, p3, br, bc);
+    } else {
+      put_blk(Ks, p1, br, bc);
+      put_blk_T(KT, p1, br, bc);
+      put_blk(Os, p2, br, bc);
+      put_blk_T(OT, p2, br, bc);
+    }
+    if (w == 0) {
+      float L = pla;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(L, off);
+        if (x.l >= off) L += y;
+      }
+      const float LC = __shfl(L, 63);
+      Ls[x.l] = L;
+      eLs[x.l] = __expf(L);
+      ws[x.l] = __expf(fminf(LC - L, 0.f));
+    }
+    __syncthreads();
+    if (cc > 0) {
+      const int n0 = t0 - C;  // full chunk
+      if (lo) {
+        p1 = load_blk(q + boff + (size_t)n0 * DK, DK, C, b);
+        p2 = load_blk(v + boff + (size_t)n0 * DK, DK, C, b);
+        p3 = load_blk(sent + ((size_t)bh * NC + cc - 1) * DK * DK, DK, DK, b);
+      } else {
+        p1 = load_blk(k + boff + (size_t)n0 * DK, DK, C, b);
+        p2 = load_blk(dO + boff + (size_t)n0 * DK, DK, C, b);
+      }
+      if (w == 0) pla = la[(size_t)bh * T + n0 + x.l];
+    }
+    const float a_c = __expf(Ls[C - 1]);
+
+    if (!gk) {
+      // ---------------- group D: t = me
+      const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
+      const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
+      const float Lt = Ls[me];
+      float rowacc = 0.f;
+      f32x4 dPT[4];
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) {
+        dPT[sb] = zero4();
+        if (sb <= wl) {
+          f32x4 PT = zero4(), dAT = zero4();
+          PT = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, PT);
+          PT = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, PT);
+          dAT = pgn_mfma(frag(Vs, 16 * sb + i, 0, g), of0, dAT);
+          dAT = pgn_mfma(frag(Vs, 16 * sb + i, 1, g), of1, dAT);
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int s = 16 * sb + 4 * g + r;
+            const float dec = (s <= me) ? __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+            rowacc += dAT[r] * (PT[r] * dec);
+            dPT[sb][r] = dAT[r] * dec;
+          }
+        }
+      }
+      rowacc = sum_groups(rowacc);
+      if (g == 0) rowM[me] = rowacc;
+      const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
+      const float eLt = eLs[me];
+      const __bf16* qrow = Qs + me * kPitch;
+      const bool t_ok = t0 + me < T;
+      float qzt = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        f32x4 acc = zero4(), Z = zero4();
+        acc = pgn_mfma(frag(KT, 16 * dt + i, 0, g), b0, acc);
+        if (wl >= 2) acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), b1, acc);
+        Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
+        Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
+        const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
+        acc = acc + Z * eLt;
+        if (t_ok) *reinterpret_cast<bf16x4*>(dq + boff + (size_t)(t0 + me) * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
+      }
+      qzt = sum_groups(qzt);
+      if (g == 0) qz[me] = qzt;
+    } else {
+      // ---------------- group K: s = me, d block wl
+      const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
+      const bf16x8 vf0 = frag(Vs, me, 0, g), vf1 = frag(Vs, me, 1, g);
+      const float Ls_s = Ls[me];
+      float colacc = 0.f;
+      f32x4 At[4], dPt[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        At[tb] = zero4();
+        dPt[tb] = zero4();
+        if (tb >= wl) {
+          f32x4 P = zero4(), dA = zero4();
+          P = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, P);
+          P = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, P);
+          dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), vf0, dA);
+          dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), vf1, dA);
+          const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tb + 4 * g + r;
+            const float dec = (t >= me) ? __expf(fminf(Ltv[r] - Ls_s, 0.f)) : 0.f;
+            At[tb][r] = P[r] * dec;
+            dPt[tb][r] = dA[r] * dec;
+            colacc += dA[r] * At[tb][r];
+          }
+        }
+      }
+      colacc = sum_groups(colacc);
+      if (g == 0) colM[me] = colacc;
+      const bf16x8 A0 = pack(At[0], At[1]), A1 = pack(At[2], At[3]);
+      const bf16x8 dP0 = pack(dPt[0], dPt[1]), dP1 = pack(dPt[2], dPt[3]);
+      const float w_s = ws[me];
+      const bool s_ok = t0 + me < T;
+      // dV^T tiles (j block jt, s block wl) = dO^T A + dS^T (K o w)^T
+      const bf16x8 kw0 = frag_scaled(Ks, me, 0, g, w_s), kw1 = frag_scaled(Ks, me, 1, g, w_s);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        f32x4 acc = zero4();
+        if (wl < 2) acc = pgn_mfma(frag(OT, 16 * jt + i, 0, g), A0, acc);
+        acc = pgn_mfma(frag(OT, 16 * jt + i, 1, g), A1, acc);
+        acc = pgn_mfma(frag(dST, 16 * jt + i, 0, g), kw0, acc);
+        acc = pgn_mfma(frag(dST, 16 * jt + i, 1, g), kw1, acc);
+        if (s_ok) *reinterpret_cast<bf16x4*>(dv + boff + (size_t)(t0 + me) * DK + 16 * jt + 4 * g) = to_bf16x4(acc);
+      }
+      // dK^T tiles (d block dt, s block wl) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
+      const __bf16* krow = Ks + me * kPitch;
+      float dw = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        f32x4 acc = zero4(), Y = zero4();
+        if (wl < 2) acc = pgn_mfma(frag(QT, 16 * dt + i, 0, g), dP0, acc);
+        acc = pgn_mfma(frag(QT, 16 * dt + i, 1, g), dP1, acc);
+        Y = pgn_mfma(frag(dSs, 16 * dt + i, 0, g), vf0, Y);
+        Y = pgn_mfma(frag(dSs, 16 * dt + i, 1, g), vf1, Y);
+        const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
+        acc = acc + Y * w_s;
+        if (s_ok) *reinterpret_cast<bf16x4*>(dk + boff + (size_t)(t0 + me) * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
+      }
+      dw = sum_groups(dw);
+      if (g == 0) dwv[me] = dw;
+      // <S_c, dS> over this wave's rows of dS
+      float sd = 0.f;
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * wl + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
+      sd = wave_sum(sd);
+      if (x.l == 0) sdot[wl] = sd;
+      // dS <- a dS + (Q o eL)^T dO, rows 16wl.. of dS
+      const bf16x8 qe0 = frag_scaled_k(QT, 16 * wl + i, 0, g, eLs), qe1 = frag_scaled_k(QT, 16 * wl + i, 1, g, eLs);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        dS[jt] = dS[jt] * a_c;
+        dS[jt] = pgn_mfma(qe0, frag(OT, 16 * jt + i, 0, g), dS[jt]);
+        dS[jt] = pgn_mfma(qe1, frag(OT, 16 * jt + i, 1, g), dS[jt]);
+      }
+    }
+    __syncthreads();
+    if (gk) {
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        store_T(dST, 16 * jt, 16 * wl, g, i, dS[jt]);
+        store_N(dSs, 16 * wl, 16 * jt, g, i, dS[jt]);
+      }
+    } else if (w == 0) {
+      // dla for this chunk: the reverse cumulative sum of dL
+      const int t = x.l;
+      float dL = rowM[t] - colM[t] + eLs[t] * qz[t] - ws[t] * dwv[t];
+      const float wdw = wave_sum(ws[t] * dwv[t]);
+      if (t == C - 1) dL += wdw + a_c * (sdot[0] + sdot[1] + sdot[2] + sdot[3]);
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_down(dL, off);
+        if (t + off < 64) dL += y;
+      }
+      if (t0 + t < T) dla[(size_t)bh * T + t0 + t] = dL;
+    }
+    __syncthreads();
+  }
+  if (gk && dS0) {
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dS0[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] = dS[jt][r];
   }
 }
+
+constexpr size_t kBwdSmem = 10 * TILE * sizeof(__bf16) + (7 * C + 4) * sizeof(float);
 
 bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
   if (B <= 0 || H <= 0 || T <= 0) return false;
-  if (B * H >= ((int64_t)1 << 24) || T >= ((int64_t)1 << 28)) return false;
-  if (B * H * ((T + C - 1) / C) >= ((int64_t)1 << 31)) return false;
+  if (B * H >= ((int64_t)1 << 31) || T >= ((int64_t)1 << 28)) return false;
   return D == DK && Cc == C;
-}
-
-int set_smem(const void* fn, size_t bytes, bool& done) {
-  if (done) return 0;
-  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-  if (e != hipSuccess) return (int)e;
-  done = true;
-  return 0;
 }
 
 }  // namespace
 
-extern "C" int64_t pragnosia_aspin_chunk_fwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D,
-                                                             int64_t chunk) {
-  if (!shape_ok(B, H, T, D, chunk)) return -1;
-  return lb_layout(B * H * ((T + C - 1) / C)).total;
-}
-
-// Resident workgroups of a persistent kernel on the current device (blocks per CU x CUs), cached per kernel.
-static int persistent_grid(const void* fn, int threads, size_t smem, int& cached) {
-  if (cached > 0) return cached;
-  int dev = 0, per_cu = 0;
-  hipDeviceProp_t prop;
-  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return -1;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, smem) != hipSuccess || per_cu < 1)
-    return -1;
-  cached = per_cu * prop.multiProcessorCount;
-  return cached;
-}
-
 extern "C" int pragnosia_aspin_chunk_fwd(const void* q, const void* k, const void* v, const float* la, const float* S0,
-                                         void* o, float* S_final, void* sent, void* workspace,
-                                         int64_t workspace_bytes, uint64_t epoch, int64_t B, int64_t H, int64_t T,
+                                         void* o, float* S_final, void* sent, int64_t B, int64_t H, int64_t T,
                                          int64_t D, int64_t chunk, void* stream) {
   if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
-  PGN_CHECK_ARG(q && k && v && la && o && S_final && workspace);
-  PGN_CHECK_ARG(workspace_bytes >= pragnosia_aspin_chunk_fwd_workspace_bytes(B, H, T, D, chunk));
-  PGN_CHECK_ARG(epoch > 0 && epoch < ((uint64_t)1 << 56));
-  static bool smem_set = false;
-  static int grid_cap = 0;
-  int rc = set_smem((const void*)plain_fwd_sp, kFwdSmem, smem_set);
-  if (rc) return rc;
-  const int cap = persistent_grid((const void*)plain_fwd_sp, 256, kFwdSmem, grid_cap);
-  if (cap <= 0) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(q && k && v && la && o && S_final);
   const int NC = (int)((T + C - 1) / C);
   const int nbh = (int)(B * H);
-  const int64_t n = (int64_t)nbh * NC;
-  const int grid = (int)std::min<int64_t>(n, cap);
-  hipLaunchKernelGGL(plain_fwd_sp, dim3((unsigned)grid), dim3(256), kFwdSmem, (hipStream_t)stream,
-                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, S0, (__bf16*)o, S_final,
-                     (__bf16*)sent, (unsigned char*)workspace, epoch, nbh, (int)T, NC);
+  const unsigned grid = (unsigned)(((nbh + 7) / 8) * 8 * FNB);
+  hipLaunchKernelGGL(aspin_plain_fwd, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const __bf16*)q,
+                     (const __bf16*)k, (const __bf16*)v, la, S0, (__bf16*)o, S_final, (__bf16*)sent, (int)T, NC,
+                     nbh);
   PGN_RETURN_LAUNCH();
-}
-
-extern "C" unsigned int pragnosia_lookback_timeouts(void) { return lb_read_timeouts(); }
-
-extern "C" int64_t pragnosia_aspin_chunk_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D,
-                                                             int64_t chunk) {
-  if (!shape_ok(B, H, T, D, chunk)) return -1;
-  return B * H * ((T + C - 1) / C) * DK * DK * 2;
 }
 
 extern "C" int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const void* v, const float* la,
                                          const void* sent, const void* dO, const float* dS_final, void* dq, void* dk,
-                                         void* dv, float* dla, float* dS0, void* workspace, int64_t workspace_bytes,
-                                         int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream) {
+                                         void* dv, float* dla, float* dS0, int64_t B, int64_t H, int64_t T, int64_t D,
+                                         int64_t chunk, void* stream) {
   if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
-  PGN_CHECK_ARG(q && k && v && la && sent && dO && dq && dk && dv && dla && workspace);
-  PGN_CHECK_ARG(workspace_bytes >= pragnosia_aspin_chunk_bwd_workspace_bytes(B, H, T, D, chunk));
-  static bool state_set = false, local_set = false;
-  int rc = set_smem((const void*)plain_state<true>, kStateSmem, state_set);
-  if (rc) return rc;
-  rc = set_smem((const void*)plain_bwd_local, kLocalSmem, local_set);
-  if (rc) return rc;
+  PGN_CHECK_ARG(q && k && v && la && sent && dO && dq && dk && dv && dla);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)aspin_plain_bwd, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kBwdSmem);
+    if (e != hipSuccess) return (int)e;
+    attr_set = true;
+  }
   const int NC = (int)((T + C - 1) / C);
-  const int nbh = (int)(B * H);
-  hipStream_t st = (hipStream_t)stream;
-  __bf16* dSc = (__bf16*)workspace;
-  hipLaunchKernelGGL(plain_state<true>, dim3((unsigned)nbh), dim3(64 * SW), kStateSmem, st, (const __bf16*)q,
-                     (const __bf16*)dO, la, dS_final, dSc, dS0, (int)T, NC);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(plain_bwd_local, dim3((unsigned)(nbh * NC)), dim3(512), kLocalSmem, st, (const __bf16*)q,
-                     (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent, (const __bf16*)dSc,
-                     (const __bf16*)dO, (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, dla, (int)T, NC);
+  hipLaunchKernelGGL(aspin_plain_bwd, dim3((unsigned)(B * H)), dim3(512), kBwdSmem, (hipStream_t)stream,
+                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent,
+                     (const __bf16*)dO, dS_final, (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, dla, dS0, (int)T, NC);
   PGN_RETURN_LAUNCH();
 }

@@ -24,6 +24,15 @@ struct WaveIdx {
   int w, l, g, i;
 };
 
+// Lane indices recomputed from an opaque copy of the thread index. Persistent kernels call this at the top of
+// every work item: addresses derived from the lane are then recomputed per item (a few ALU operations) instead of
+// being hoisted out of the item loop and held in registers for the kernel's lifetime.
+PGN_DEVICE WaveIdx wave_idx_opaque() {
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  return WaveIdx{__builtin_amdgcn_readfirstlane(tid >> 6), tid & 63, (tid & 63) >> 4, tid & 15};
+}
+
 // The wave index is made wave-uniform (an SGPR): conditions on it are then scalar branches. That is required, not
 // an optimisation: MFMA instructions ignore EXEC, so an MFMA under a condition the compiler believes divergent (a
 // lane mask that happens to be empty) would still execute and overwrite its destination.

@@ -108,33 +108,6 @@ def _diag_backward(ctx, gy, glr, gli, _ghi):
 diag_scan.register_autograd(_diag_backward, setup_context=_diag_setup)
 
 
-_SCAN_WS: dict = {}
-
-
-def _scan_workspace(nbytes: int, like: Tensor, what: str) -> tuple[Tensor, int]:
-    """The persistent workspace of the single-pass scans on `like`'s device and current stream, grown (zero-filled)
-    to at least `nbytes`, and the next epoch for it. One workspace per (device, stream): calls on one stream are
-    ordered, so they may share it; a new, larger one replaces it when a shape needs more (the old one is freed by
-    the caching allocator only after the work queued on the stream)."""
-    if nbytes < 0:
-        raise PragnosiaError(f"{what}: shape {tuple(like.shape)} rejected")
-    stream = torch.cuda.current_stream(like.device)
-    key = (like.device.index, stream.stream_id)
-    ent = _SCAN_WS.get(key)
-    if ent is None or ent[0].numel() < nbytes:
-        ent = [torch.zeros(max(nbytes, 1 << 20), device=like.device, dtype=torch.uint8), 0]
-        _SCAN_WS[key] = ent
-    ent[1] += 1
-    return ent[0], ent[1]
-
-
-def _workspace(nbytes: int, like: Tensor, what: str) -> Tensor:
-    """Device workspace of `nbytes` (uninitialised: the kernels clear what they need) on `like`'s device."""
-    if nbytes < 0:
-        raise PragnosiaError(f"{what}: shape {tuple(like.shape)} rejected")
-    return torch.empty(max(nbytes, 1), device=like.device, dtype=torch.uint8)
-
-
 # ---------------------------------------------------------------------------------------------------------------
 # aspin chunked scan, plain rule: replaces assoc_scan_kernel and its ops, src/assoc_kernel.py:128-323
 CHUNK = 64
@@ -157,10 +130,9 @@ def aspin_chunk(q: Tensor, k: Tensor, v: Tensor, la: Tensor, S0: Optional[Tensor
     S = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
     sent = (torch.empty(B, H, NC, D, D, device=q.device, dtype=torch.bfloat16) if want_sent
             else q.new_empty(0, dtype=torch.bfloat16))
-    ws, epoch = _scan_workspace(lib().pragnosia_aspin_chunk_fwd_workspace_bytes(B, H, T, D, CHUNK), q, "aspin_chunk")
     check(lib().pragnosia_aspin_chunk_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(S0), _ptr(o), _ptr(S),
-                                          _ptr(sent) if want_sent else None, _ptr(ws), ws.numel(), epoch,
-                                          B, H, T, D, CHUNK, _stream(q)), "pragnosia_aspin_chunk_fwd")
+                                          _ptr(sent) if want_sent else None, B, H, T, D, CHUNK, _stream(q)),
+          "pragnosia_aspin_chunk_fwd")
     return o, S, sent
 
 
@@ -182,9 +154,8 @@ def aspin_chunk_bwd(q: Tensor, k: Tensor, v: Tensor, la: Tensor, sent: Tensor, d
     dq, dk, dv = (torch.empty(B, H, T, D, device=q.device, dtype=torch.bfloat16) for _ in range(3))
     dla = torch.empty(B, H, T, device=q.device, dtype=torch.float32)
     dS0 = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
-    ws = _workspace(lib().pragnosia_aspin_chunk_bwd_workspace_bytes(B, H, T, D, CHUNK), q, "aspin_chunk_bwd")
     check(lib().pragnosia_aspin_chunk_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(sent), _ptr(do), _ptr(dS),
-                                          _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla), _ptr(dS0), _ptr(ws), ws.numel(),
+                                          _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla), _ptr(dS0),
                                           B, H, T, D, CHUNK, _stream(q)), "pragnosia_aspin_chunk_bwd")
     return dq, dk, dv, dla, dS0
 

@@ -60,9 +60,9 @@ def test_plain_matches_oracle(scan, T, s0):
 
 
 @pytest.mark.parametrize("B,H,T", [(1, 2, 70 * 64 - 17), (8, 16, 256)])
-def test_single_pass_many_chunks(scan, B, H, T):
-    """The single-pass scans with look-back windows longer than one wave (70 chunks per head) and with many heads
-    in flight (128 heads x 4 chunks), forward and backward; then the same call again on recycled workspace."""
+def test_many_chunks_and_heads(scan, B, H, T):
+    """A long chain (70 chunks per head, ragged end) and many heads in flight (128 heads x 4 chunks), forward and
+    backward; then the same call twice more, which must agree bit for bit (the kernels are deterministic)."""
     q, k, v, la, S0 = _unit_inputs(B, H, T, 64, seed=B * T, la_scale=0.01)
     e = _check_fwd_bwd(scan, q, k, v, la, S0, seed=7)
     assert e["o"] < TOL_OUT and e["S"] < TOL_OUT, e
@@ -142,9 +142,3 @@ def test_unsupported_head_dim_raises(scan):
     with pytest.raises(PragnosiaError):
         scan(q, q, q, torch.zeros(1, 1, 8, device="cuda"))
 
-
-def test_lookback_never_timed_out():
-    """No look-back wait of any single-pass scan run so far in this process ran out of its bound."""
-    from pragnosia_amd._lib import lib
-    torch.cuda.synchronize()
-    assert lib().pragnosia_lookback_timeouts() == 0
