@@ -77,17 +77,36 @@ def aspin_inputs(B, H, T, D, seed, rule, device):
 
 
 def _time_ops(fns, n, stream):
-    """Average seconds per call of each fn, timed back to back with HIP events recorded on `stream` (the stream
-    the ops launch on)."""
+    """Average device seconds per call of each fn. Each fn is captured n times into one HIP graph, and the graph is
+    replayed between two HIP events recorded on `stream`, the stream the replay launches the kernels on, so a
+    kernel shorter than the host's per-call dispatch time is not charged for the gaps between launches. The ops
+    allocate their outputs from the graph's pool and record no memset nodes."""
     import torch
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(fns) + 1)]
-    ev[0].record(stream)
-    for i, fn in enumerate(fns):
-        for _ in range(n):
+    out = []
+    for fn in fns:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
             fn()
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    return [ev[i].elapsed_time(ev[i + 1]) / n * 1e-3 for i in range(len(fns))]
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(n):
+                fn()
+        with torch.cuda.stream(stream):
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 5
+            e0.record(stream)
+            for _ in range(reps):
+                g.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) / (n * reps) * 1e-3)
+        del g
+    return out
 
 
 def aspin_bench(rule, steps, warmup):

@@ -6,11 +6,13 @@ so a state_dict of the product modules in `pragnosia_amd` loads here unchanged. 
 parameters passed in (fp64 for the truth).
 
 Pinning: these are compositions of the pinned scans in `oracle.aspin` / `oracle.diag` with torch built-ins
-(LayerNorm, Linear, RMSNorm, GELU, softplus, sigmoid). The compositions themselves are checked by invariants in
-tests/test_oracle_modules.py: causality, carried windows == one pass (plain rule exactly; across a position restart
-through the rebase), token-at-a-time decode == one pass, forward_carried's last window == the same window after a
-carried prefix. The order of the composition (which norm, which gate, where) has no independent golden vector:
-parity unpinned beyond those invariants.
+(LayerNorm, Linear, RMSNorm, GELU, softplus, sigmoid). The compositions are pinned against the reference's own
+modules by the golden fixtures in tests/golden/modules.npz (the reference's CPU AssocCarrier plain and delta,
+SpinCarrier(rf), LM forward and forward_carried with the aspin and fspin mixers, fp32, seeded parameters; checked in
+tests/test_golden_modules.py to 1e-4), and by invariants in tests/test_oracle_modules.py: causality, carried windows
+== one pass (across a position restart through the rebase), token-at-a-time decode == one pass, forward_carried's
+last window == the same window after a carried prefix. `greedy_decode` composes `lm_forward` calls; it is pinned by
+those invariants only.
 """
 from __future__ import annotations
 

@@ -1,0 +1,74 @@
+"""The HIP modules against the reference's own modules: the fixtures of tests/golden/modules.npz (reference CPU
+modules in fp32, seeded parameters and inputs; see tests/test_golden_modules.py, which pins the oracle to the same
+fixtures at 1e-4). Tolerances: the aspin paths compute the scans on bf16 operands, max relative error <= 2e-2 on
+outputs and carried states (the north star's bound); the fspin paths are fp32 end to end, <= 1e-4."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+G = np.load(os.path.join(HERE, "golden", "modules.npz"))
+
+
+def rel(a, b):
+    a = a.detach().double().cpu()
+    b = torch.as_tensor(np.asarray(b, dtype=np.float64))
+    return ((a - b).abs().max() / b.abs().max()).item()
+
+
+def _params():
+    import sys
+    sys.path.insert(0, os.path.join(HERE, "golden"))
+    import params as P
+    return P
+
+
+@pytest.mark.parametrize("delta", [False, True])
+def test_assoc_carrier_matches_reference(delta):
+    P = _params()
+    from pragnosia_amd.assoc import AssocCarrier
+    a = P.ASSOC
+    m = AssocCarrier(a["d"], heads=a["heads"], delta=delta)
+    P.fill_(m, 10 + delta)
+    m = m.cuda()
+    x, S0 = P.inputs(20 + delta, (a["B"], a["T"], a["d"]), (a["B"], a["heads"], 64, 64))
+    S0 = S0 * 0.2
+    with torch.no_grad():
+        y, (S, p) = m(x.cuda(), (S0.cuda(), a["p0"]))
+    tag = "assoc_delta" if delta else "assoc_plain"
+    assert p == a["T"]
+    assert rel(y - x.cuda(), G[tag + "_y"] - x.numpy()) < 2e-2
+    assert rel(S, G[tag + "_S"]) < 2e-2
+
+
+def test_spin_rf_matches_reference():
+    P = _params()
+    from pragnosia_amd.spin import SpinCarrier
+    s = P.SPIN
+    m = SpinCarrier(s["d"], gated="rf")
+    P.fill_(m, 30)
+    m = m.cuda()
+    x, hr, hi = P.inputs(31, (s["B"], s["T"], s["d"]), (s["B"], s["d"]), (s["B"], s["d"]))
+    with torch.no_grad():
+        y, (hr2, hi2) = m(x.cuda(), (hr.cuda(), hi.cuda()))
+    assert rel(y - x.cuda(), G["spin_y"] - x.numpy()) < 1e-4
+    assert rel(hr2, G["spin_hr"]) < 1e-4 and rel(hi2, G["spin_hi"]) < 1e-4
+
+
+@pytest.mark.parametrize("mixer,tol", [("aspin", 2e-2), ("fspin", 1e-4)])
+def test_lm_matches_reference(mixer, tol):
+    P = _params()
+    from pragnosia_amd.model import LM
+    c = P.LMCFG
+    lm = LM(vocab=c["vocab"], d=c["d"], layers=c["layers"], mlp_mult=c["mlp_mult"], ctx=c["ctx"], mixer=mixer)
+    P.fill_(lm, 40 + len(mixer))
+    lm = lm.cuda().eval()
+    ids = P.ids(41, (c["B"], c["T"]), c["vocab"]).cuda()
+    with torch.no_grad():
+        logits = lm(ids[:, : c["ctx"]])
+        carried = lm.forward_carried(ids, window=c["window"])
+    assert rel(logits, G[f"lm_{mixer}_logits"]) < tol
+    assert rel(carried, G[f"lm_{mixer}_carried"]) < tol
