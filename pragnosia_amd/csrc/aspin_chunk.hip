@@ -181,9 +181,9 @@ __global__ __launch_bounds__(256) void aspin_plain_fwd(const __bf16* __restrict_
 }
 
 // Backward: 8 waves per (batch, head). Waves 0-3 (group D) own t block wl = w & 3 and compute everything that does
-// not depend on dS: dQ, the row sums of dA o A and q_t.(S_c dO_t). Waves 4-7 (group K) own s block wl and d block wl
-// and carry dS: dV, dK, the column sums of dA o A, k_s.(dS v_s), <S_c, dS> and the dS update. Waves w and w + 4 share
-// a SIMD, and the two groups' MFMA counts per SIMD are within 10% of each other.
+// not depend on dS: dQ, the row sums of dA o A, q_t.(S_c dO_t) and this chunk's term (Q o eL)^T dO of the dS update.
+// Waves 4-7 (group K) own s block wl and d block wl and carry dS: dV, dK, the column sums of dA o A, k_s.(dS v_s),
+// <S_c, dS> and dS <- a dS + (Q o eL)^T dO. Waves w and w + 4 share a SIMD; group K's share is the critical path.
 __global__ __launch_bounds__(512) void aspin_plain_bwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const __bf16* __restrict__ sent, const __bf16* __restrict__ dO,
@@ -208,6 +208,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   float* qz = colM + C;   // q_t . (S_c dO_t)
   float* dwv = qz + C;    // k_s . (dS v_s)
   float* sdot = dwv + C;  // per-wave <S_c, dS>
+  f32x4* Mb = reinterpret_cast<f32x4*>(sdot + 4);  // (Q o eL)^T dO in group K's dS order, fp32
 
   const WaveIdx x = wave_idx();
   const int w = x.w, wl = w & 3, g = x.g, i = x.i, tid = threadIdx.x;
@@ -338,6 +339,15 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       }
       qzt = sum_groups(qzt);
       if (g == 0) qz[me] = qzt;
+      // this chunk's term of the state-gradient recurrence, rows 16 wl.. of (Q o eL)^T dO: it does not depend on dS,
+      // so it is computed here, off group K's path, and group K applies it after the barrier
+      const bf16x8 qe0 = frag_scaled_k(QT, 16 * wl + i, 0, g, eLs), qe1 = frag_scaled_k(QT, 16 * wl + i, 1, g, eLs);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        f32x4 m = pgn_mfma(qe0, frag(OT, 16 * jt + i, 0, g), zero4());
+        m = pgn_mfma(qe1, frag(OT, 16 * jt + i, 1, g), m);
+        Mb[(wl * 4 + jt) * 64 + x.l] = m;
+      }
     } else {
       // ---------------- group K: s = me, d block wl
       const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
@@ -409,19 +419,12 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * wl + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
       sd = wave_sum(sd);
       if (x.l == 0) sdot[wl] = sd;
-      // dS <- a dS + (Q o eL)^T dO, rows 16wl.. of dS
-      const bf16x8 qe0 = frag_scaled_k(QT, 16 * wl + i, 0, g, eLs), qe1 = frag_scaled_k(QT, 16 * wl + i, 1, g, eLs);
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        dS[jt] = dS[jt] * a_c;
-        dS[jt] = pgn_mfma(qe0, frag(OT, 16 * jt + i, 0, g), dS[jt]);
-        dS[jt] = pgn_mfma(qe1, frag(OT, 16 * jt + i, 1, g), dS[jt]);
-      }
     }
     __syncthreads();
-    if (gk) {
+    if (gk) {  // dS <- a dS + (Q o eL)^T dO, rows 16wl.. of dS
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
+        dS[jt] = dS[jt] * a_c + Mb[(wl * 4 + jt) * 64 + x.l];
         store_T(dST, 16 * jt, 16 * wl, g, i, dS[jt]);
         store_N(dSs, 16 * wl, 16 * jt, g, i, dS[jt]);
       }
@@ -448,7 +451,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   }
 }
 
-constexpr size_t kBwdSmem = 10 * TILE * sizeof(__bf16) + (7 * C + 4) * sizeof(float);
+constexpr size_t kBwdSmem = 10 * TILE * sizeof(__bf16) + (7 * C + 4) * sizeof(float) + 16 * 64 * sizeof(f32x4);
 
 bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
   if (B <= 0 || H <= 0 || T <= 0) return false;
