@@ -180,10 +180,54 @@ __global__ __launch_bounds__(256) void aspin_plain_fwd(const __bf16* __restrict_
     for (int r = 0; r < 4; ++r) Sfin[soff + (16 * w + 4 * g + r) * DK + j0 + 16 * jt + i] = S[jt][r];
 }
 
-// Backward: 8 waves per (batch, head). Waves 0-3 (group D) own t block wl = w & 3 and compute everything that does
-// not depend on dS: dQ, the row sums of dA o A, q_t.(S_c dO_t) and this chunk's term (Q o eL)^T dO of the dS update.
-// Waves 4-7 (group K) own s block wl and d block wl and carry dS: dV, dK, the column sums of dA o A, k_s.(dS v_s),
-// <S_c, dS> and dS <- a dS + (Q o eL)^T dO. Waves w and w + 4 share a SIMD; group K's share is the critical path.
+// Backward: 8 waves per (batch, head), chunks in reverse. Waves 0-3 (group D) own t block wl = w & 3 and compute
+// everything that does not depend on dS: dQ, the row sums of dA o A, q_t.(S_c dO_t) and this chunk's term
+// (Q o eL)^T dO of the dS update; they also load and stage every input tile, and wave 0 runs the per-chunk scans (L
+// forward, dla in reverse). Waves 4-7 (group K) own s block wl and d block wl and carry dS: dV, dK, the column sums
+// of dA o A, k_s.(dS v_s), <S_c, dS> and dS <- a dS + (Q o eL)^T dO. Group K is the critical path, so it does
+// nothing else: two barriers per chunk, one after the contractions (then group K applies the dS update while group
+// D stages the next chunk's tiles) and one after the staging. The per-chunk vectors (L, e^L, w and the dla partial
+// sums) are double-buffered, so the dla of a chunk is computed by wave 0 during the next chunk's contractions.
+constexpr int kVec = 7 * C + 4;  // one set of per-chunk vectors: L, eL, w, rowM, colM, qz, dwv (C each), sdot (4)
+
+// dla of one chunk from its vector set: dL_t = rowM_t - colM_t + eL_t qz_t - w_t dwv_t, the chunk's last token adds
+// sum_s w_s dwv_s + a <S_c, dS>, and dla is the reverse inclusive cumulative sum of dL. One wave, lane = t.
+PGN_DEVICE void plain_dla(const float* vs, int lane, __amdgpu_buffer_rsrc_t out) {
+  const float* Ls = vs;
+  const float* eLs = vs + C;
+  const float* ws = vs + 2 * C;
+  const float* rowM = vs + 3 * C;
+  const float* colM = vs + 4 * C;
+  const float* qz = vs + 5 * C;
+  const float* dwv = vs + 6 * C;
+  const float* sdot = vs + 7 * C;
+  const int t = lane;
+  const float wd = ws[t] * dwv[t];
+  float dL = rowM[t] - colM[t] + eLs[t] * qz[t] - wd;
+  const float wdw = wave_sum(wd);
+  if (t == C - 1) dL += wdw + __expf(Ls[C - 1]) * (sdot[0] + sdot[1] + sdot[2] + sdot[3]);
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float y = __shfl_down(dL, off);
+    if (t + off < 64) dL += y;
+  }
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, dL), out, 4 * t, 0, 0);
+}
+
+// L (inclusive cumulative sum of the chunk's la, lane = t), e^L and w = exp(L_C - L) into a vector set. One wave.
+PGN_DEVICE void plain_scan(float la_t, int lane, float* vs) {
+  float L = la_t;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float y = __shfl_up(L, off);
+    if (lane >= off) L += y;
+  }
+  const float LC = __shfl(L, 63);
+  vs[lane] = L;
+  vs[C + lane] = __expf(L);
+  vs[2 * C + lane] = __expf(fminf(LC - L, 0.f));
+}
+
 __global__ __launch_bounds__(512) void aspin_plain_bwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const __bf16* __restrict__ sent, const __bf16* __restrict__ dO,
@@ -200,15 +244,8 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   __bf16* Ss = OT + TILE;    // S_c, (d, j)
   __bf16* dSs = Ss + TILE;   // dS, (d, j)
   __bf16* dST = dSs + TILE;  // dS^T, (j, d)
-  float* Ls = reinterpret_cast<float*>(dST + TILE);
-  float* eLs = Ls + C;
-  float* ws = eLs + C;
-  float* rowM = ws + C;   // row sums of dA o A (group D)
-  float* colM = rowM + C; // column sums of dA o A (group K)
-  float* qz = colM + C;   // q_t . (S_c dO_t)
-  float* dwv = qz + C;    // k_s . (dS v_s)
-  float* sdot = dwv + C;  // per-wave <S_c, dS>
-  f32x4* Mb = reinterpret_cast<f32x4*>(sdot + 4);  // (Q o eL)^T dO in group K's dS order, fp32
+  float* vec = reinterpret_cast<float*>(dST + TILE);         // two vector sets, chunk c uses set c & 1
+  f32x4* Mb = reinterpret_cast<f32x4*>(vec + 2 * kVec);      // (Q o eL)^T dO in group K's dS order, fp32
 
   const WaveIdx x = wave_idx();
   const int w = x.w, wl = w & 3, g = x.g, i = x.i, tid = threadIdx.x;
@@ -217,11 +254,12 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
 
-  // group K: dS rows 16wl + 4g + r, column 16 jt + i
-  f32x4 dS[4];
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt) dS[jt] = zero4();
+  const int me = 16 * wl + i;  // group D: this lane's t; group K: this lane's s
+  // The two groups run separate loops (the branch is on a wave-uniform value) that meet at the same barriers: each
+  // loop's registers and memory-counter waits are then its own.
   if (gk) {
+    // ================= group K: dS rows 16wl + 4g + r, column 16 jt + i
+    f32x4 dS[4];
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
@@ -230,126 +268,21 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       store_T(dST, 16 * jt, 16 * wl, g, i, dS[jt]);
       store_N(dSs, 16 * wl, 16 * jt, g, i, dS[jt]);
     }
-  }
-
-  // staging: threads 0-255 carry Q, V and S_c; threads 256-511 carry K and dO (one 4x4 block of each)
-  const int b = tid & 255;
-  const int br = 4 * (b >> 4), bc = 4 * (b & 15);
-  const bool lo = tid < 256;
-  Blk4 p1, p2, p3;
-  {
-    const int t0 = (NC - 1) * C, nr = min(C, T - t0);
-    if (lo) {
-      p1 = load_blk(q + boff + (size_t)t0 * DK, DK, nr, b);
-      p2 = load_blk(v + boff + (size_t)t0 * DK, DK, nr, b);
-      p3 = load_blk(sent + ((size_t)bh * NC + NC - 1) * DK * DK, DK, DK, b);
-    } else {
-      p1 = load_blk(k + boff + (size_t)t0 * DK, DK, nr, b);
-      p2 = load_blk(dO + boff + (size_t)t0 * DK, DK, nr, b);
-    }
-  }
-  float pla = (w == 0 && (NC - 1) * C + x.l < T) ? la[(size_t)bh * T + (NC - 1) * C + x.l] : 0.f;
-
-  const int me = 16 * wl + i;  // group D: this lane's t; group K: this lane's s
-  for (int cc = NC - 1; cc >= 0; --cc) {
-    const int t0 = cc * C;
-    if (lo) {
-      put_blk(Qs, p1, br, bc);
-      put_blk_T(QT, p1, br, bc);
-      put_blk(Vs, p2, br, bc);
-      put_blk(Ss, p3, br, bc);
-    } else {
-      put_blk(Ks, p1, br, bc);
-      put_blk_T(KT, p1, br, bc);
-      put_blk(Os, p2, br, bc);
-      put_blk_T(OT, p2, br, bc);
-    }
-    if (w == 0) {
-      float L = pla;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(L, off);
-        if (x.l >= off) L += y;
-      }
-      const float LC = __shfl(L, 63);
-      Ls[x.l] = L;
-      eLs[x.l] = __expf(L);
-      ws[x.l] = __expf(fminf(LC - L, 0.f));
-    }
     __syncthreads();
-    if (cc > 0) {
-      const int n0 = t0 - C;  // full chunk
-      if (lo) {
-        p1 = load_blk(q + boff + (size_t)n0 * DK, DK, C, b);
-        p2 = load_blk(v + boff + (size_t)n0 * DK, DK, C, b);
-        p3 = load_blk(sent + ((size_t)bh * NC + cc - 1) * DK * DK, DK, DK, b);
-      } else {
-        p1 = load_blk(k + boff + (size_t)n0 * DK, DK, C, b);
-        p2 = load_blk(dO + boff + (size_t)n0 * DK, DK, C, b);
-      }
-      if (w == 0) pla = la[(size_t)bh * T + n0 + x.l];
-    }
-    const float a_c = __expf(Ls[C - 1]);
-
-    if (!gk) {
-      // ---------------- group D: t = me
-      const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
-      const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
-      const float Lt = Ls[me];
-      float rowacc = 0.f;
-      f32x4 dPT[4];
-#pragma unroll
-      for (int sb = 0; sb < 4; ++sb) {
-        dPT[sb] = zero4();
-        if (sb <= wl) {
-          f32x4 PT = zero4(), dAT = zero4();
-          PT = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, PT);
-          PT = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, PT);
-          dAT = pgn_mfma(frag(Vs, 16 * sb + i, 0, g), of0, dAT);
-          dAT = pgn_mfma(frag(Vs, 16 * sb + i, 1, g), of1, dAT);
-          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int s = 16 * sb + 4 * g + r;
-            const float dec = (s <= me) ? __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
-            rowacc += dAT[r] * (PT[r] * dec);
-            dPT[sb][r] = dAT[r] * dec;
-          }
-        }
-      }
-      rowacc = sum_groups(rowacc);
-      if (g == 0) rowM[me] = rowacc;
-      const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
-      const float eLt = eLs[me];
-      const __bf16* qrow = Qs + me * kPitch;
-      const bool t_ok = t0 + me < T;
-      float qzt = 0.f;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        f32x4 acc = zero4(), Z = zero4();
-        acc = pgn_mfma(frag(KT, 16 * dt + i, 0, g), b0, acc);
-        if (wl >= 2) acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), b1, acc);
-        Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
-        Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
-        const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
-        acc = acc + Z * eLt;
-        if (t_ok) *reinterpret_cast<bf16x4*>(dq + boff + (size_t)(t0 + me) * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
-      }
-      qzt = sum_groups(qzt);
-      if (g == 0) qz[me] = qzt;
-      // this chunk's term of the state-gradient recurrence, rows 16 wl.. of (Q o eL)^T dO: it does not depend on dS,
-      // so it is computed here, off group K's path, and group K applies it after the barrier
-      const bf16x8 qe0 = frag_scaled_k(QT, 16 * wl + i, 0, g, eLs), qe1 = frag_scaled_k(QT, 16 * wl + i, 1, g, eLs);
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        f32x4 m = pgn_mfma(qe0, frag(OT, 16 * jt + i, 0, g), zero4());
-        m = pgn_mfma(qe1, frag(OT, 16 * jt + i, 1, g), m);
-        Mb[(wl * 4 + jt) * 64 + x.l] = m;
-      }
-    } else {
-      // ---------------- group K: s = me, d block wl
+    for (int cc = NC - 1; cc >= 0; --cc) {
+      const int t0 = cc * C;
+      const float* vs = vec + (cc & 1) * kVec;
+      const float* Ls = vs;
+      const float* ws = vs + 2 * C;
+      float* colM = const_cast<float*>(vs) + 4 * C;  // column sums of dA o A
+      float* dwv = const_cast<float*>(vs) + 6 * C;   // k_s . (dS v_s)
+      float* sdot = const_cast<float*>(vs) + 7 * C;  // per-wave <S_c, dS>
+      // this chunk's rows of dV and dK: stores to rows past T fall outside the range and are dropped
+      const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
+      const __amdgpu_buffer_rsrc_t dv_out =
+          __builtin_amdgcn_make_buffer_rsrc(dv + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
+      const __amdgpu_buffer_rsrc_t dk_out =
+          __builtin_amdgcn_make_buffer_rsrc(dk + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
       const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
       const bf16x8 vf0 = frag(Vs, me, 0, g), vf1 = frag(Vs, me, 1, g);
       const float Ls_s = Ls[me];
@@ -381,7 +314,6 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       const bf16x8 A0 = pack(At[0], At[1]), A1 = pack(At[2], At[3]);
       const bf16x8 dP0 = pack(dPt[0], dPt[1]), dP1 = pack(dPt[2], dPt[3]);
       const float w_s = ws[me];
-      const bool s_ok = t0 + me < T;
       // dV^T tiles (j block jt, s block wl) = dO^T A + dS^T (K o w)^T
       const bf16x8 kw0 = frag_scaled(Ks, me, 0, g, w_s), kw1 = frag_scaled(Ks, me, 1, g, w_s);
 #pragma unroll
@@ -391,7 +323,8 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         acc = pgn_mfma(frag(OT, 16 * jt + i, 1, g), A1, acc);
         acc = pgn_mfma(frag(dST, 16 * jt + i, 0, g), kw0, acc);
         acc = pgn_mfma(frag(dST, 16 * jt + i, 1, g), kw1, acc);
-        if (s_ok) *reinterpret_cast<bf16x4*>(dv + boff + (size_t)(t0 + me) * DK + 16 * jt + 4 * g) = to_bf16x4(acc);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dv_out,
+                                              (me * DK + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
       }
       // dK^T tiles (d block dt, s block wl) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
       const __bf16* krow = Ks + me * kPitch;
@@ -407,7 +340,8 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 #pragma unroll
         for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
         acc = acc + Y * w_s;
-        if (s_ok) *reinterpret_cast<bf16x4*>(dk + boff + (size_t)(t0 + me) * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dk_out,
+                                              (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
       }
       dw = sum_groups(dw);
       if (g == 0) dwv[me] = dw;
@@ -419,39 +353,144 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * wl + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
       sd = wave_sum(sd);
       if (x.l == 0) sdot[wl] = sd;
-    }
-    __syncthreads();
-    if (gk) {  // dS <- a dS + (Q o eL)^T dO, rows 16wl.. of dS
+      __syncthreads();
+      // dS <- a dS + (Q o eL)^T dO, rows 16wl.. of dS
+      const float a_c = __expf(Ls[C - 1]);
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
         dS[jt] = dS[jt] * a_c + Mb[(wl * 4 + jt) * 64 + x.l];
         store_T(dST, 16 * jt, 16 * wl, g, i, dS[jt]);
         store_N(dSs, 16 * wl, 16 * jt, g, i, dS[jt]);
       }
-    } else if (w == 0) {
-      // dla for this chunk: the reverse cumulative sum of dL
-      const int t = x.l;
-      float dL = rowM[t] - colM[t] + eLs[t] * qz[t] - ws[t] * dwv[t];
-      const float wdw = wave_sum(ws[t] * dwv[t]);
-      if (t == C - 1) dL += wdw + a_c * (sdot[0] + sdot[1] + sdot[2] + sdot[3]);
+      if (cc > 0) __syncthreads();
+    }
+    if (dS0) {
 #pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_down(dL, off);
-        if (t + off < 64) dL += y;
-      }
-      if (t0 + t < T) dla[(size_t)bh * T + t0 + t] = dL;
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dS0[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] = dS[jt][r];
+    }
+  } else {
+    // ================= group D: t = me. Thread tid stages one 4x4 block of each of Q, K, V, dO and S_c.
+    const int b = tid & 255;  // = tid; the mask tells the compiler that every block row is below 64
+    const int br = 4 * (b >> 4), bc = 4 * (b & 15);
+    Blk4 pq, pk, pv, po, ps;
+    float pla = 0.f;
+    auto stage = [&]() {
+      put_blk(Qs, pq, br, bc);
+      put_blk_T(QT, pq, br, bc);
+      put_blk(Ks, pk, br, bc);
+      put_blk_T(KT, pk, br, bc);
+      put_blk(Vs, pv, br, bc);
+      put_blk(Os, po, br, bc);
+      put_blk_T(OT, po, br, bc);
+      put_blk(Ss, ps, br, bc);
+    };
+    {
+      const int t0 = (NC - 1) * C, nr = min(C, T - t0);
+      pq = load_blk(q + boff + (size_t)t0 * DK, DK, nr, b);
+      pk = load_blk(k + boff + (size_t)t0 * DK, DK, nr, b);
+      pv = load_blk(v + boff + (size_t)t0 * DK, DK, nr, b);
+      po = load_blk(dO + boff + (size_t)t0 * DK, DK, nr, b);
+      ps = load_blk(sent + ((size_t)bh * NC + NC - 1) * DK * DK, DK, DK, b);
+      if (w == 0 && t0 + x.l < T) pla = la[(size_t)bh * T + t0 + x.l];
+      stage();
+      if (w == 0) plain_scan(pla, x.l, vec + ((NC - 1) & 1) * kVec);
     }
     __syncthreads();
-  }
-  if (gk && dS0) {
+    for (int cc = NC - 1; cc >= 0; --cc) {
+      const int t0 = cc * C;
+      float* vs = vec + (cc & 1) * kVec;
+      float* vn = vec + ((cc & 1) ^ 1) * kVec;
+      const float* Ls = vs;
+      const float* eLs = vs + C;
+      float* rowM = vs + 3 * C;  // row sums of dA o A
+      float* qz = vs + 5 * C;    // q_t . (S_c dO_t)
+      if (cc > 0) {  // next chunk's tiles, staged after the barrier
+        const int n0 = t0 - C;
+        pq = load_blk(q + boff + (size_t)n0 * DK, DK, C, b);
+        pk = load_blk(k + boff + (size_t)n0 * DK, DK, C, b);
+        pv = load_blk(v + boff + (size_t)n0 * DK, DK, C, b);
+        po = load_blk(dO + boff + (size_t)n0 * DK, DK, C, b);
+        ps = load_blk(sent + ((size_t)bh * NC + cc - 1) * DK * DK, DK, DK, b);
+        if (w == 0) pla = la[(size_t)bh * T + n0 + x.l];
+      }
+      // this chunk's rows of dQ: stores to rows past T fall outside the range and are dropped
+      const __amdgpu_buffer_rsrc_t dq_out = __builtin_amdgcn_make_buffer_rsrc(
+          dq + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
+      const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
+      const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
+      const float Lt = Ls[me];
+      float rowacc = 0.f;
+      f32x4 dPT[4];
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
+      for (int sb = 0; sb < 4; ++sb) {
+        dPT[sb] = zero4();
+        if (sb <= wl) {
+          f32x4 PT = zero4(), dAT = zero4();
+          PT = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, PT);
+          PT = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, PT);
+          dAT = pgn_mfma(frag(Vs, 16 * sb + i, 0, g), of0, dAT);
+          dAT = pgn_mfma(frag(Vs, 16 * sb + i, 1, g), of1, dAT);
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dS0[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] = dS[jt][r];
+          for (int r = 0; r < 4; ++r) {
+            const int s = 16 * sb + 4 * g + r;
+            const float dec = (s <= me) ? __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+            rowacc += dAT[r] * (PT[r] * dec);
+            dPT[sb][r] = dAT[r] * dec;
+          }
+        }
+      }
+      rowacc = sum_groups(rowacc);
+      if (g == 0) rowM[me] = rowacc;
+      const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
+      const float eLt = eLs[me];
+      const __bf16* qrow = Qs + me * kPitch;
+      float qzt = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        f32x4 acc = zero4(), Z = zero4();
+        acc = pgn_mfma(frag(KT, 16 * dt + i, 0, g), b0, acc);
+        if (wl >= 2) acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), b1, acc);
+        Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
+        Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
+        const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
+        acc = acc + Z * eLt;
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dq_out,
+                                              (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+      }
+      qzt = sum_groups(qzt);
+      if (g == 0) qz[me] = qzt;
+      // rows 16 wl.. of (Q o eL)^T dO, applied to dS by group K after the barrier
+      const bf16x8 qe0 = frag_scaled_k(QT, 16 * wl + i, 0, g, eLs), qe1 = frag_scaled_k(QT, 16 * wl + i, 1, g, eLs);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        f32x4 m = pgn_mfma(qe0, frag(OT, 16 * jt + i, 0, g), zero4());
+        m = pgn_mfma(qe1, frag(OT, 16 * jt + i, 1, g), m);
+        Mb[(wl * 4 + jt) * 64 + x.l] = m;
+      }
+      if (w == 0 && cc < NC - 1) {  // the later chunk's dla, from the other vector set
+        const int tn = t0 + C;
+        plain_dla(vn, x.l, __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T + tn, (short)0,
+                                                             4 * min(C, T - tn), 0x00020000));
+      }
+      __syncthreads();
+      if (cc > 0) {
+        stage();
+        if (w == 0) plain_scan(pla, x.l, vn);
+        __syncthreads();
+      }
+    }
+    if (w == 0)  // chunk 0's dla (vector set 0)
+      plain_dla(vec, x.l, __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T, (short)0, 4 * min(C, T),
+                                                            0x00020000));
   }
 }
 
-constexpr size_t kBwdSmem = 10 * TILE * sizeof(__bf16) + (7 * C + 4) * sizeof(float) + 16 * 64 * sizeof(f32x4);
+constexpr size_t kBwdSmem = 10 * TILE * sizeof(__bf16) + 2 * kVec * sizeof(float) + 16 * 64 * sizeof(f32x4);
 
 bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
   if (B <= 0 || H <= 0 || T <= 0) return false;
