@@ -92,13 +92,8 @@ __global__ __launch_bounds__(256) void aspin_plain_fwd(const __bf16* __restrict_
     put_blk_T(KT, pk, br, bc);
     if (vthr) put_blk_T(VT, pv, vr, vc);
     if (w == 0) {
-      float L = pla;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(L, off);
-        if (x.l >= off) L += y;
-      }
-      const float LC = __shfl(L, 63);
+      const float L = wave_prefix_sum(pla, x.l);
+      const float LC = lane_value(L, 63);
       Ls[x.l] = L;
       eLs[x.l] = __expf(L);
       ws[x.l] = __expf(fminf(LC - L, 0.f));
@@ -206,23 +201,14 @@ PGN_DEVICE void plain_dla(const float* vs, int lane, __amdgpu_buffer_rsrc_t out)
   float dL = rowM[t] - colM[t] + eLs[t] * qz[t] - wd;
   const float wdw = wave_sum(wd);
   if (t == C - 1) dL += wdw + __expf(Ls[C - 1]) * (sdot[0] + sdot[1] + sdot[2] + sdot[3]);
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float y = __shfl_down(dL, off);
-    if (t + off < 64) dL += y;
-  }
+  dL = wave_suffix_sum(dL, t);
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, dL), out, 4 * t, 0, 0);
 }
 
 // L (inclusive cumulative sum of the chunk's la, lane = t), e^L and w = exp(L_C - L) into a vector set. One wave.
 PGN_DEVICE void plain_scan(float la_t, int lane, float* vs) {
-  float L = la_t;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float y = __shfl_up(L, off);
-    if (lane >= off) L += y;
-  }
-  const float LC = __shfl(L, 63);
+  const float L = wave_prefix_sum(la_t, lane);
+  const float LC = lane_value(L, 63);
   vs[lane] = L;
   vs[C + lane] = __expf(L);
   vs[2 * C + lane] = __expf(fminf(LC - L, 0.f));

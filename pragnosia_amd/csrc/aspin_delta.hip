@@ -48,28 +48,14 @@ constexpr int DK = 64;
 constexpr int TILE = 64 * kPitch;
 constexpr int NP = C + 4;  // pitch of the fp32 N^T tile
 
-PGN_DEVICE float incl_scan64(float x, int l) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float y = __shfl_up(x, off);
-    if (l >= off) x += y;
-  }
-  return x;
-}
+PGN_DEVICE float incl_scan64(float x, int l) { return wave_prefix_sum(x, l); }
 
-PGN_DEVICE float rev_scan64(float x, int l) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float y = __shfl_down(x, off);
-    if (l + off < 64) x += y;
-  }
-  return x;
-}
+PGN_DEVICE float rev_scan64(float x, int l) { return wave_suffix_sum(x, l); }
 
 // Per-chunk decay statistics into LDS (one wave): L (inclusive cumsum of la), eL = exp(L), w = exp(L_C - L).
 PGN_DEVICE void chunk_decays(float la_l, int l, float* Ls, float* eLs, float* ws) {
   const float L = incl_scan64(la_l, l);
-  const float LC = __shfl(L, 63);
+  const float LC = lane_value(L, 63);
   Ls[l] = L;
   eLs[l] = __expf(L);
   ws[l] = __expf(fminf(LC - L, 0.f));

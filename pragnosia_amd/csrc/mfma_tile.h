@@ -175,4 +175,39 @@ PGN_DEVICE float sum_groups(float x) {
 
 PGN_DEVICE float wave_sum(float x) { return sum_groups(sum16(x)); }
 
+// x moved by a DPP row operation (CTRL), 0 where the source lane falls outside the lane's row of 16.
+template <int CTRL>
+PGN_DEVICE float dpp_row0(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+
+PGN_DEVICE float lane_value(float x, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave (lane `l` = this lane's index): a Hillis-Steele scan inside each
+// row of 16 lanes on DPP row shifts (row_shr 1, 2, 4, 8), then each row adds the totals of the rows before it, read
+// from lanes 15, 31 and 47. Every step is a VALU or lane read: no LDS round trips.
+PGN_DEVICE float wave_prefix_sum(float x, int l) {
+  x += dpp_row0<0x111>(x);
+  x += dpp_row0<0x112>(x);
+  x += dpp_row0<0x114>(x);
+  x += dpp_row0<0x118>(x);
+  const float r0 = lane_value(x, 15), r1 = lane_value(x, 31), r2 = lane_value(x, 47);
+  const int row = l >> 4;
+  return x + ((row >= 1 ? r0 : 0.f) + (row >= 2 ? r1 : 0.f) + (row >= 3 ? r2 : 0.f));
+}
+
+// Inclusive suffix sum (lane l gets the sum over lanes l..63), the mirror image: row_shl shifts, then the totals of
+// the later rows, read from lanes 16, 32 and 48.
+PGN_DEVICE float wave_suffix_sum(float x, int l) {
+  x += dpp_row0<0x101>(x);
+  x += dpp_row0<0x102>(x);
+  x += dpp_row0<0x104>(x);
+  x += dpp_row0<0x108>(x);
+  const float r1 = lane_value(x, 16), r2 = lane_value(x, 32), r3 = lane_value(x, 48);
+  const int row = l >> 4;
+  return x + ((row <= 2 ? r3 : 0.f) + (row <= 1 ? r2 : 0.f) + (row == 0 ? r1 : 0.f));
+}
+
 }  // namespace pgn
