@@ -110,7 +110,8 @@ def _time_ops(fns, n, stream):
 
 
 def aspin_bench(rule, steps, warmup):
-    """The cfg2 step for one write rule: wall-clock throughput over `steps` steps, plus per-op event timings."""
+    """The cfg2 step for one write rule: wall-clock time per step of `steps` steps captured in one HIP graph (and of
+    `steps` eager calls, reported beside it), plus per-op event timings."""
     import torch
     from pragnosia_amd import ops  # noqa: F401
     B, H, T, D, C = 16, 12, 512, 64, 64
@@ -144,7 +145,27 @@ def aspin_bench(rule, steps, warmup):
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
+    eager = (time.perf_counter() - t0) / steps
+    # The same `steps` steps captured into one HIP graph and replayed once: every step runs both kernels over the
+    # full batch, and the timed region is bound by the device rather than by Python's per-op dispatch (which for
+    # this step is comparable to the kernels' own time) or by a per-replay launch cost.
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        step()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(steps):
+            step()
+    graph.replay()  # untimed: first replay
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    graph.replay()
+    torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
+    del graph
     t_fwd, t_bwd = _time_ops([fwd, bwd], max(20, min(steps, 200)), stream)
 
     elem, ht, state, sent_n = B * H * T * D, B * H * T, B * H * D * D, B * H * NC * D * D
@@ -167,7 +188,7 @@ def aspin_bench(rule, steps, warmup):
         fwd_flops = (4 * D * (C + D) + 2 * C * D + 2 * D * D + 2 * C * C) * ht
         bwd_flops = (10 * D * (C + D) + 6 * C * D + 4 * D * D + 4 * C * C) * ht
         names = ("aspin_delta_fwd (inv + fwd kernels)", "aspin_delta_bwd (chain + local kernels)")
-    return dict(B=B, H=H, T=T, D=D, C=C, wall=wall, t_fwd=t_fwd, t_bwd=t_bwd, fwd_bytes=fwd_bytes,
+    return dict(B=B, H=H, T=T, D=D, C=C, wall=wall, eager=eager, t_fwd=t_fwd, t_bwd=t_bwd, fwd_bytes=fwd_bytes,
                 bwd_bytes=bwd_bytes, fwd_flops=fwd_flops, bwd_flops=bwd_flops, names=names)
 
 
@@ -329,6 +350,7 @@ def gpu_bench(args):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(r["wall"] * 1e3, 5),
+        "eager_ms_per_step": round(r["eager"] * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -350,6 +372,7 @@ def gpu_bench(args):
         sec = {f"aspin_{other}": {
             "workload": f"aspin chunked scan fwd+bwd, {other} rule, B16 T512 H12 D64 (configs[2])",
             "Mtok_s": round(ot / o["wall"] / 1e6, 3), "ms_per_step": round(o["wall"] * 1e3, 5),
+            "eager_ms_per_step": round(o["eager"] * 1e3, 5),
             "fwd_us": round(o["t_fwd"] * 1e6, 2), "bwd_us": round(o["t_bwd"] * 1e6, 2),
             "fwd_bwd_GBs": round((o["fwd_bytes"] + o["bwd_bytes"]) / (o["t_fwd"] + o["t_bwd"]) / 1e9, 1),
             "fwd_bwd_mfma_tflops": round((o["fwd_flops"] + o["bwd_flops"]) / (o["t_fwd"] + o["t_bwd"]) / 1e12, 2)}}

@@ -7,12 +7,11 @@
 //     S_{c+1} = a S_c + (K o w)^T V
 // (the reference's `_scan_twopass`, `src/assoc.py:118-165`; its GPU form `src/assoc_kernel.py:47-70,188-202`).
 //
-// Forward: two workgroups (4 waves each) per (batch, head), each owning 32 of the 64 value columns (the plain rule
-// is independent per value column), walk the chunks in order with their fp32 state columns in registers: wave w
-// holds key rows 16w..16w+15 as accumulator tiles and the state update is an MFMA accumulating onto a*S. Each chunk's
-// Q, K, V tiles are staged in LDS once (K and V also transposed, through a 4x4 register transpose) from registers
-// loaded during the previous chunk's compute, and every contraction reads its operands from LDS, so HBM sees each
-// input once: 8 B per (t, d) element forward (q, k, v read, o written) plus the optional bf16 entering states.
+// Forward: one workgroup per (batch, head) walks the chunks in order; eight waves compute (each owns 16 tokens of the
+// chunk and 32 value columns, and holds its 16 x 32 block of the fp32 state as accumulator tiles; the state update
+// is an MFMA accumulating onto a*S) while four more load and stage the next chunk into the other half of a
+// double-buffered LDS. Every contraction reads its operands from LDS, so HBM sees each input once: 8 B per (t, d)
+// element forward (q, k, v read, o written) plus the optional bf16 entering states.
 //
 // The backward walks the chunks in reverse with dS (the gradient on the state leaving the chunk) in registers and
 // the entering states S_c read back from the forward's bf16 copies. Per chunk, with dA = dO V^T, dP = dA o dec,
@@ -34,145 +33,172 @@ constexpr int C = 64;
 constexpr int DK = 64;
 constexpr int TILE = 64 * kPitch;  // one staged 64 x 64 tile
 
-constexpr int FBV = 32;         // value columns per forward workgroup
-constexpr int FNB = DK / FBV;   // forward workgroups per (batch, head)
+// Forward: one workgroup of 12 waves per (batch, head), chunks in order. Waves 0-7 compute: wave w owns t block
+// tb = w & 3 and value columns 32 jh .. 32 jh + 31 (jh = w >> 2), and holds rows 16 tb.. of the fp32 state for those
+// columns as accumulator tiles. Waves 8-11 load: while waves 0-7 compute chunk c from one half of a double-buffered
+// LDS, they stage chunk c + 1 (prefetched into registers during chunk c - 1) into the other half, run its decay scan,
+// issue chunk c + 2's loads and copy chunk c's entering state to `sent`. The state tile S^T the output needs is
+// double-buffered too, so one barrier per chunk orders everything.
+constexpr int kFwdWaves = 12;
+constexpr int kFwdBuf = 4 * TILE * (int)sizeof(__bf16) + 3 * C * (int)sizeof(float);  // Q, K, K^T, V^T, L, eL, w
 
-// Forward block -> (batch-head, value block). The FNB workgroups of one head are 8 apart in launch order, and the
-// dispatcher deals workgroups round-robin over the 8 XCDs, so they run on the same XCD and the second one's reads
-// of Q and K hit in that XCD's L2.
-PGN_DEVICE void fwd_block(int& bh, int& jb) {
-  const int x = blockIdx.x;
-  const int grp = x / (8 * FNB), rem = x - grp * (8 * FNB);
-  jb = rem >> 3;
-  bh = grp * 8 + (rem & 7);
-}
+__global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const float* __restrict__ la, const float* __restrict__ S0, __bf16* __restrict__ o, float* __restrict__ Sfin,
+    __bf16* __restrict__ sent, int T, int NC) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  // buffer set h: Q, K, K^T, V^T tiles and the L, eL, w vectors; then S^T (j, d) for two chunks
+  auto Qb = [&](int h) { return reinterpret_cast<__bf16*>(smem + h * kFwdBuf); };
+  auto Kb = [&](int h) { return Qb(h) + TILE; };
+  auto KTb = [&](int h) { return Qb(h) + 2 * TILE; };
+  auto VTb = [&](int h) { return Qb(h) + 3 * TILE; };
+  auto Vecb = [&](int h) { return reinterpret_cast<float*>(Qb(h) + 4 * TILE); };
+  auto STb = [&](int h) { return reinterpret_cast<__bf16*>(smem + 2 * kFwdBuf) + h * TILE; };
 
-__global__ __launch_bounds__(256) void aspin_plain_fwd(const __bf16* __restrict__ q, const __bf16* __restrict__ k,
-                                                       const __bf16* __restrict__ v, const float* __restrict__ la,
-                                                       const float* __restrict__ S0, __bf16* __restrict__ o,
-                                                       float* __restrict__ Sfin, __bf16* __restrict__ sent, int T,
-                                                       int NC, int nbh) {
-  __shared__ __align__(16) __bf16 Qs[TILE], Ks[TILE], KT[TILE], VT[FBV * kPitch], ST[FBV * kPitch];
-  __shared__ __align__(16) float Ls[C], eLs[C], ws[C];
-
-  int bh, jb;
-  fwd_block(bh, jb);
-  if (bh >= nbh) return;
   const WaveIdx x = wave_idx();
   const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
-  const int j0 = jb * FBV;  // first value column owned here
+  const int bh = blockIdx.x;
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
 
-  // state rows 16w + 4g + r, columns j0 + 16 jt + i
-  f32x4 S[2];
+  if (w < 8) {
+    // ================= compute waves
+    const int tb = w & 3, j0 = 32 * (w >> 2);
+    const int tq = 16 * tb + i;  // this lane's token within the chunk for t-indexed operands
+    // state rows 16 tb + 4g + r, columns j0 + 16 jt + i
+    f32x4 S[2];
 #pragma unroll
-  for (int jt = 0; jt < 2; ++jt) {
+    for (int jt = 0; jt < 2; ++jt) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) S[jt][r] = S0 ? S0[soff + (16 * w + 4 * g + r) * DK + j0 + 16 * jt + i] : 0.f;
-    store_T(ST, 16 * jt, 16 * w, g, i, S[jt]);
-  }
-
-  // this thread's 4x4 staging blocks: Q, K (64 x 64, all threads), V (64 x 32, threads < 128)
-  const int br = 4 * (tid >> 4), bc = 4 * (tid & 15);
-  const int vr = 4 * (tid >> 3), vc = 4 * (tid & 7);
-  const bool vthr = tid < 128;
-  Blk4 pq = load_blk(q + boff, DK, min(C, T), tid);
-  Blk4 pk = load_blk(k + boff, DK, min(C, T), tid);
-  Blk4 pv;
-  if (vthr) pv = load_blk_w(v + boff + j0, DK, min(C, T), FBV, tid);
-  float pla = (w == 0 && x.l < T) ? la[(size_t)bh * T + x.l] : 0.f;
-
-  const int tq = 16 * w + i;  // this lane's token within the chunk for t-indexed operands
-  for (int c = 0; c < NC; ++c) {
-    const int t0 = c * C;
-    // publish chunk c (prefetched) to LDS
-    put_blk(Qs, pq, br, bc);
-    put_blk(Ks, pk, br, bc);
-    put_blk_T(KT, pk, br, bc);
-    if (vthr) put_blk_T(VT, pv, vr, vc);
-    if (w == 0) {
-      const float L = wave_prefix_sum(pla, x.l);
-      const float LC = lane_value(L, 63);
-      Ls[x.l] = L;
-      eLs[x.l] = __expf(L);
-      ws[x.l] = __expf(fminf(LC - L, 0.f));
+      for (int r = 0; r < 4; ++r) S[jt][r] = S0 ? S0[soff + (16 * tb + 4 * g + r) * DK + j0 + 16 * jt + i] : 0.f;
+      store_T(STb(0), j0 + 16 * jt, 16 * tb, g, i, S[jt]);
     }
     __syncthreads();
-    // prefetch chunk c + 1 while this one computes
-    if (c + 1 < NC) {
-      const int n0 = t0 + C, nr = min(C, T - n0);
-      pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, tid);
-      pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, tid);
-      if (vthr) pv = load_blk_w(v + boff + (size_t)n0 * DK + j0, DK, nr, FBV, tid);
-      if (w == 0) pla = (n0 + x.l < T) ? la[(size_t)bh * T + n0 + x.l] : 0.f;
-    }
-
-    // (Q K^T)^T tiles (s block sb, t block w), decayed and masked: lane holds column t = tq, rows s.
-    const bf16x8 qf0 = frag(Qs, tq, 0, g), qf1 = frag(Qs, tq, 1, g);
-    const float Lt = Ls[tq];
-    f32x4 pt[4];
+    for (int c = 0; c < NC; ++c) {
+      const int h = c & 1, t0 = c * C;
+      const __bf16* Qs = Qb(h);
+      const __bf16* Ks = Kb(h);
+      const __bf16* KT = KTb(h);
+      const __bf16* VT = VTb(h);
+      const __bf16* ST = STb(h);
+      const float* Ls = Vecb(h);
+      const float* eLs = Ls + C;
+      const float* ws = Ls + 2 * C;
+      // (Q K^T)^T tiles (s block sb, t block tb), decayed and masked: lane holds column t = tq, rows s.
+      const bf16x8 qf0 = frag(Qs, tq, 0, g), qf1 = frag(Qs, tq, 1, g);
+      const float Lt = Ls[tq];
+      f32x4 pt[4];
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      pt[sb] = zero4();
-      if (sb <= w) {
-        pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
-        pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
-        const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+      for (int sb = 0; sb < 4; ++sb) {
+        pt[sb] = zero4();
+        if (sb <= tb) {
+          pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
+          pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int s = 16 * sb + 4 * g + r;
-          pt[sb][r] = (s <= tq) ? pt[sb][r] * __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+          for (int r = 0; r < 4; ++r) {
+            const int s = 16 * sb + 4 * g + r;
+            pt[sb][r] = (s <= tq) ? pt[sb][r] * __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+          }
         }
       }
-    }
-    const bf16x8 af0 = pack(pt[0], pt[1]);
-    const bf16x8 af1 = pack(pt[2], pt[3]);
-    const float eLt = eLs[tq];
-    const bf16x8 qe0 = frag_scaled(Qs, tq, 0, g, eLt);
-    const bf16x8 qe1 = frag_scaled(Qs, tq, 1, g, eLt);
+      const bf16x8 af0 = pack(pt[0], pt[1]);
+      const bf16x8 af1 = pack(pt[2], pt[3]);
+      const float eLt = eLs[tq];
+      const bf16x8 qe0 = frag_scaled(Qs, tq, 0, g, eLt);
+      const bf16x8 qe1 = frag_scaled(Qs, tq, 1, g, eLt);
 
-    // O^T tiles (value block jt, t block w) = V^T A^T + S^T (Q o eL)^T; lane holds token tq, 4 value columns
-    const bool t_ok = t0 + tq < T;
+      // O^T tiles (value block jt, t block tb) = V^T A^T + S^T (Q o eL)^T; lane holds token tq, 4 value columns.
+      // Rows past T fall outside the store's range and are dropped.
+      const __amdgpu_buffer_rsrc_t o_out = __builtin_amdgcn_make_buffer_rsrc(
+          o + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt) {
-      f32x4 acc = zero4();
-      acc = pgn_mfma(frag(VT, 16 * jt + i, 0, g), af0, acc);
-      if (w >= 2) acc = pgn_mfma(frag(VT, 16 * jt + i, 1, g), af1, acc);
-      acc = pgn_mfma(frag(ST, 16 * jt + i, 0, g), qe0, acc);
-      acc = pgn_mfma(frag(ST, 16 * jt + i, 1, g), qe1, acc);
-      if (t_ok)
-        *reinterpret_cast<bf16x4*>(o + boff + (size_t)(t0 + tq) * DK + j0 + 16 * jt + 4 * g) = to_bf16x4(acc);
-    }
+      for (int jt = 0; jt < 2; ++jt) {
+        const int jr = j0 + 16 * jt + i;
+        f32x4 acc = zero4();
+        acc = pgn_mfma(frag(VT, jr, 0, g), af0, acc);
+        if (tb >= 2) acc = pgn_mfma(frag(VT, jr, 1, g), af1, acc);
+        acc = pgn_mfma(frag(ST, jr, 0, g), qe0, acc);
+        acc = pgn_mfma(frag(ST, jr, 1, g), qe1, acc);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
+                                              (tq * DK + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+      }
 
-    // the entering state, bf16, (d, j) layout
-    if (sent) {
-      __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
+      // S <- a S + (K o w)^T V on rows 16 tb.. and this wave's columns; S^T of the next chunk into the other buffer
+      const float a_c = __expf(Ls[C - 1]);
+      const bf16x8 kw0 = frag_scaled_k(KT, 16 * tb + i, 0, g, ws);
+      const bf16x8 kw1 = frag_scaled_k(KT, 16 * tb + i, 1, g, ws);
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sc[(16 * w + 4 * g + r) * DK + j0 + 16 * jt + i] = (__bf16)S[jt][r];
+      for (int jt = 0; jt < 2; ++jt) {
+        const int jr = j0 + 16 * jt + i;
+        S[jt] = S[jt] * a_c;
+        S[jt] = pgn_mfma(kw0, frag(VT, jr, 0, g), S[jt]);
+        S[jt] = pgn_mfma(kw1, frag(VT, jr, 1, g), S[jt]);
+        store_T(STb(h ^ 1), j0 + 16 * jt, 16 * tb, g, i, S[jt]);
+      }
+      __syncthreads();
     }
-
-    // S <- a S + (K o w)^T V on this workgroup's columns, rows 16w.. of S
-    const float a_c = __expf(Ls[C - 1]);
-    const bf16x8 kw0 = frag_scaled_k(KT, 16 * w + i, 0, g, ws);
-    const bf16x8 kw1 = frag_scaled_k(KT, 16 * w + i, 1, g, ws);
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt) {
-      S[jt] = S[jt] * a_c;
-      S[jt] = pgn_mfma(kw0, frag(VT, 16 * jt + i, 0, g), S[jt]);
-      S[jt] = pgn_mfma(kw1, frag(VT, 16 * jt + i, 1, g), S[jt]);
-    }
+    for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Sfin[soff + (16 * tb + 4 * g + r) * DK + j0 + 16 * jt + i] = S[jt][r];
+  } else {
+    // ================= load waves: thread b carries one 4x4 block of each of Q, K and V
+    const int b = tid & 255;
+    const int br = 4 * (b >> 4), bc = 4 * (b & 15);
+    const bool w0 = w == 8;  // runs the decay scans
+    Blk4 pq, pk, pv;
+    float pla = 0.f;
+    auto load = [&](int cn) {
+      const int n0 = cn * C, nr = min(C, T - n0);
+      pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, b);
+      pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, b);
+      pv = load_blk(v + boff + (size_t)n0 * DK, DK, nr, b);
+      if (w0) pla = (n0 + x.l < T) ? la[(size_t)bh * T + n0 + x.l] : 0.f;
+    };
+    auto stage = [&](int h) {
+      put_blk(Qb(h), pq, br, bc);
+      put_blk(Kb(h), pk, br, bc);
+      put_blk_T(KTb(h), pk, br, bc);
+      put_blk_T(VTb(h), pv, br, bc);
+      if (w0) {
+        const float L = wave_prefix_sum(pla, x.l);
+        const float LC = lane_value(L, 63);
+        float* vs = Vecb(h);
+        vs[x.l] = L;
+        vs[C + x.l] = __expf(L);
+        vs[2 * C + x.l] = __expf(fminf(LC - L, 0.f));
+      }
+    };
+    load(0);
+    stage(0);
+    if (NC > 1) load(1);
     __syncthreads();
+    for (int c = 0; c < NC; ++c) {
+      const int h = c & 1;
+      if (c + 1 < NC) {
+        stage(h ^ 1);
+        if (c + 2 < NC) load(c + 2);
+      }
+      if (sent) {  // chunk c's entering state, bf16 (d, j): a 4x4 block of S^T read and transposed per thread
+        const __bf16* ST = STb(h);
+        Blk4 st;
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt) store_T(ST, 16 * jt, 16 * w, g, i, S[jt]);
+        for (int jj = 0; jj < 4; ++jj) st.r[jj] = *reinterpret_cast<const bf16x4*>(ST + (br + jj) * kPitch + bc);
+        __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) {
+          bf16x4 row;
+          row[0] = st.r[0][dd];
+          row[1] = st.r[1][dd];
+          row[2] = st.r[2][dd];
+          row[3] = st.r[3][dd];
+          *reinterpret_cast<bf16x4*>(sc + (bc + dd) * DK + br) = row;
+        }
+      }
+      __syncthreads();
+    }
   }
-
-#pragma unroll
-  for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Sfin[soff + (16 * w + 4 * g + r) * DK + j0 + 16 * jt + i] = S[jt][r];
 }
 
 // Backward: 8 waves per (batch, head), chunks in reverse. Waves 0-3 (group D) own t block wl = w & 3 and compute
@@ -476,6 +502,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   }
 }
 
+constexpr size_t kFwdSmem = 2 * (size_t)kFwdBuf + 2 * TILE * sizeof(__bf16);
 constexpr size_t kBwdSmem = 10 * TILE * sizeof(__bf16) + 2 * kVec * sizeof(float) + 16 * 64 * sizeof(f32x4);
 
 bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
@@ -492,12 +519,17 @@ extern "C" int pragnosia_aspin_chunk_fwd(const void* q, const void* k, const voi
   if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
   PGN_CHECK_ARG(q && k && v && la && o && S_final);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)aspin_plain_fwd, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kFwdSmem);
+    if (e != hipSuccess) return (int)e;
+    attr_set = true;
+  }
   const int NC = (int)((T + C - 1) / C);
-  const int nbh = (int)(B * H);
-  const unsigned grid = (unsigned)(((nbh + 7) / 8) * 8 * FNB);
-  hipLaunchKernelGGL(aspin_plain_fwd, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const __bf16*)q,
-                     (const __bf16*)k, (const __bf16*)v, la, S0, (__bf16*)o, S_final, (__bf16*)sent, (int)T, NC,
-                     nbh);
+  hipLaunchKernelGGL(aspin_plain_fwd, dim3((unsigned)(B * H)), dim3(kFwdWaves * 64), kFwdSmem, (hipStream_t)stream,
+                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, S0, (__bf16*)o, S_final,
+                     (__bf16*)sent, (int)T, NC);
   PGN_RETURN_LAUNCH();
 }
 
