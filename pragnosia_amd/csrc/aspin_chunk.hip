@@ -201,14 +201,15 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
   }
 }
 
-// Backward: 8 waves per (batch, head), chunks in reverse. Waves 0-3 (group D) own t block wl = w & 3 and compute
-// everything that does not depend on dS: dQ, the row sums of dA o A, q_t.(S_c dO_t) and this chunk's term
-// (Q o eL)^T dO of the dS update; they also load and stage every input tile, and wave 0 runs the per-chunk scans (L
-// forward, dla in reverse). Waves 4-7 (group K) own s block wl and d block wl and carry dS: dV, dK, the column sums
-// of dA o A, k_s.(dS v_s), <S_c, dS> and dS <- a dS + (Q o eL)^T dO. Group K is the critical path, so it does
-// nothing else: two barriers per chunk, one after the contractions (then group K applies the dS update while group
-// D stages the next chunk's tiles) and one after the staging. The per-chunk vectors (L, e^L, w and the dla partial
-// sums) are double-buffered, so the dla of a chunk is computed by wave 0 during the next chunk's contractions.
+// Backward: 8 waves per (batch, head), chunks in reverse, one barrier per chunk. Waves 4-7 (group K) own s block
+// wl = w & 3 and compute dV, dK, the column sums of dA o A and k_s.(dS v_s); they read dS from LDS and do nothing
+// else. Waves 0-3 (group D) own t block wl and compute dQ, the row sums of dA o A, q_t.(S_c dO_t), then carry dS:
+// wave wl holds rows 16 wl.. of dS in fp32 registers, forms <S_c, dS> and dS <- a dS + (Q o eL)^T dO for them and
+// writes the result (bf16, transposed) into the other half of a double-buffered dS^T tile, which group K reads in
+// the next chunk. Group D also stages the next chunk's tiles into the other half of double-buffered input tiles
+// (loaded a chunk earlier still), and its wave 0 runs the per-chunk scans: L for the next chunk and, from the other
+// set of double-buffered per-chunk vectors, the previous (later) chunk's dla. Operands contracted over a tile's row
+// index are read with the LDS transpose read, so each input is staged once, untransposed.
 constexpr int kVec = 7 * C + 4;  // one set of per-chunk vectors: L, eL, w, rowM, colM, qz, dwv (C each), sdot (4)
 
 // dla of one chunk from its vector set: dL_t = rowM_t - colM_t + eL_t qz_t - w_t dwv_t, the chunk's last token adds
@@ -240,55 +241,42 @@ PGN_DEVICE void plain_scan(float la_t, int lane, float* vs) {
   vs[2 * C + lane] = __expf(fminf(LC - L, 0.f));
 }
 
+constexpr int kBwdStage = 5 * TILE;  // Q, K, V, dO, S_c
+
 __global__ __launch_bounds__(512) void aspin_plain_bwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const __bf16* __restrict__ sent, const __bf16* __restrict__ dO,
     const float* __restrict__ dSfin, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
     float* __restrict__ dla, float* __restrict__ dS0, int T, int NC) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __bf16* Qs = reinterpret_cast<__bf16*>(smem);
-  __bf16* QT = Qs + TILE;
-  __bf16* Ks = QT + TILE;
-  __bf16* KT = Ks + TILE;
-  __bf16* Vs = KT + TILE;
-  __bf16* Os = Vs + TILE;    // dO
-  __bf16* OT = Os + TILE;    // dO^T
-  __bf16* Ss = OT + TILE;    // S_c, (d, j)
-  __bf16* dSs = Ss + TILE;   // dS, (d, j)
-  __bf16* dST = dSs + TILE;  // dS^T, (j, d)
-  float* vec = reinterpret_cast<float*>(dST + TILE);         // two vector sets, chunk c uses set c & 1
-  f32x4* Mb = reinterpret_cast<f32x4*>(vec + 2 * kVec);      // (Q o eL)^T dO in group K's dS order, fp32
+  __bf16* stg = reinterpret_cast<__bf16*>(smem);    // two sets of staged tiles, chunk c uses set c & 1
+  __bf16* dSTb = stg + 2 * kBwdStage;                // two dS^T (j, d) tiles: dS leaving chunk c in tile c & 1
+  float* vec = reinterpret_cast<float*>(dSTb + 2 * TILE);  // two vector sets, chunk c uses set c & 1
 
   const WaveIdx x = wave_idx();
   const int w = x.w, wl = w & 3, g = x.g, i = x.i, tid = threadIdx.x;
-  const bool gk = w >= 4;
   const int bh = blockIdx.x;
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
-
   const int me = 16 * wl + i;  // group D: this lane's t; group K: this lane's s
+
   // The two groups run separate loops (the branch is on a wave-uniform value) that meet at the same barriers: each
   // loop's registers and memory-counter waits are then its own.
-  if (gk) {
-    // ================= group K: dS rows 16wl + 4g + r, column 16 jt + i
-    f32x4 dS[4];
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        dS[jt][r] = dSfin ? dSfin[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] : 0.f;
-      store_T(dST, 16 * jt, 16 * wl, g, i, dS[jt]);
-      store_N(dSs, 16 * wl, 16 * jt, g, i, dS[jt]);
-    }
+  if (w >= 4) {
+    // ================= group K: s = me, d block wl
     __syncthreads();
     for (int cc = NC - 1; cc >= 0; --cc) {
-      const int t0 = cc * C;
-      const float* vs = vec + (cc & 1) * kVec;
+      const int t0 = cc * C, h = cc & 1;
+      const __bf16* Qs = stg + h * kBwdStage;
+      const __bf16* Ks = Qs + TILE;
+      const __bf16* Vs = Qs + 2 * TILE;
+      const __bf16* Os = Qs + 3 * TILE;
+      const __bf16* dST = dSTb + h * TILE;
+      float* vs = vec + h * kVec;
       const float* Ls = vs;
       const float* ws = vs + 2 * C;
-      float* colM = const_cast<float*>(vs) + 4 * C;  // column sums of dA o A
-      float* dwv = const_cast<float*>(vs) + 6 * C;   // k_s . (dS v_s)
-      float* sdot = const_cast<float*>(vs) + 7 * C;  // per-wave <S_c, dS>
+      float* colM = vs + 4 * C;  // column sums of dA o A
+      float* dwv = vs + 6 * C;   // k_s . (dS v_s)
       // this chunk's rows of dV and dK: stores to rows past T fall outside the range and are dropped
       const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
       const __amdgpu_buffer_rsrc_t dv_out =
@@ -331,8 +319,8 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
         f32x4 acc = zero4();
-        if (wl < 2) acc = pgn_mfma(frag(OT, 16 * jt + i, 0, g), A0, acc);
-        acc = pgn_mfma(frag(OT, 16 * jt + i, 1, g), A1, acc);
+        if (wl < 2) acc = pgn_mfma(frag_tr(Os, 16 * jt, 0, g, i), A0, acc);
+        acc = pgn_mfma(frag_tr(Os, 16 * jt, 1, g, i), A1, acc);
         acc = pgn_mfma(frag(dST, 16 * jt + i, 0, g), kw0, acc);
         acc = pgn_mfma(frag(dST, 16 * jt + i, 1, g), kw1, acc);
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dv_out,
@@ -344,10 +332,10 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         f32x4 acc = zero4(), Y = zero4();
-        if (wl < 2) acc = pgn_mfma(frag(QT, 16 * dt + i, 0, g), dP0, acc);
-        acc = pgn_mfma(frag(QT, 16 * dt + i, 1, g), dP1, acc);
-        Y = pgn_mfma(frag(dSs, 16 * dt + i, 0, g), vf0, Y);
-        Y = pgn_mfma(frag(dSs, 16 * dt + i, 1, g), vf1, Y);
+        if (wl < 2) acc = pgn_mfma(frag_tr(Qs, 16 * dt, 0, g, i), dP0, acc);
+        acc = pgn_mfma(frag_tr(Qs, 16 * dt, 1, g, i), dP1, acc);
+        Y = pgn_mfma(frag_tr(dST, 16 * dt, 0, g, i), vf0, Y);
+        Y = pgn_mfma(frag_tr(dST, 16 * dt, 1, g, i), vf1, Y);
         const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
 #pragma unroll
         for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
@@ -357,76 +345,58 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       }
       dw = sum_groups(dw);
       if (g == 0) dwv[me] = dw;
-      // <S_c, dS> over this wave's rows of dS
-      float sd = 0.f;
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * wl + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
-      sd = wave_sum(sd);
-      if (x.l == 0) sdot[wl] = sd;
       __syncthreads();
-      // dS <- a dS + (Q o eL)^T dO, rows 16wl.. of dS
-      const float a_c = __expf(Ls[C - 1]);
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        dS[jt] = dS[jt] * a_c + Mb[(wl * 4 + jt) * 64 + x.l];
-        store_T(dST, 16 * jt, 16 * wl, g, i, dS[jt]);
-        store_N(dSs, 16 * wl, 16 * jt, g, i, dS[jt]);
-      }
-      if (cc > 0) __syncthreads();
-    }
-    if (dS0) {
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dS0[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] = dS[jt][r];
     }
   } else {
-    // ================= group D: t = me. Thread tid stages one 4x4 block of each of Q, K, V, dO and S_c.
+    // ================= group D: t = me; dS rows 16 wl + 4g + r, column 16 jt + i
+    f32x4 dS[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        dS[jt][r] = dSfin ? dSfin[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] : 0.f;
+      store_T(dSTb + ((NC - 1) & 1) * TILE, 16 * jt, 16 * wl, g, i, dS[jt]);
+    }
+    // staging: thread b carries one 4x4 block of each of Q, K, V, dO and S_c
     const int b = tid & 255;  // = tid; the mask tells the compiler that every block row is below 64
     const int br = 4 * (b >> 4), bc = 4 * (b & 15);
     Blk4 pq, pk, pv, po, ps;
     float pla = 0.f;
-    auto stage = [&]() {
-      put_blk(Qs, pq, br, bc);
-      put_blk_T(QT, pq, br, bc);
-      put_blk(Ks, pk, br, bc);
-      put_blk_T(KT, pk, br, bc);
-      put_blk(Vs, pv, br, bc);
-      put_blk(Os, po, br, bc);
-      put_blk_T(OT, po, br, bc);
-      put_blk(Ss, ps, br, bc);
+    auto load = [&](int cn) {
+      const int n0 = cn * C, nr = min(C, T - n0);
+      pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, b);
+      pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, b);
+      pv = load_blk(v + boff + (size_t)n0 * DK, DK, nr, b);
+      po = load_blk(dO + boff + (size_t)n0 * DK, DK, nr, b);
+      ps = load_blk(sent + ((size_t)bh * NC + cn) * DK * DK, DK, DK, b);
+      if (w == 0) pla = (n0 + x.l < T) ? la[(size_t)bh * T + n0 + x.l] : 0.f;
     };
-    {
-      const int t0 = (NC - 1) * C, nr = min(C, T - t0);
-      pq = load_blk(q + boff + (size_t)t0 * DK, DK, nr, b);
-      pk = load_blk(k + boff + (size_t)t0 * DK, DK, nr, b);
-      pv = load_blk(v + boff + (size_t)t0 * DK, DK, nr, b);
-      po = load_blk(dO + boff + (size_t)t0 * DK, DK, nr, b);
-      ps = load_blk(sent + ((size_t)bh * NC + NC - 1) * DK * DK, DK, DK, b);
-      if (w == 0 && t0 + x.l < T) pla = la[(size_t)bh * T + t0 + x.l];
-      stage();
-      if (w == 0) plain_scan(pla, x.l, vec + ((NC - 1) & 1) * kVec);
-    }
+    auto stage = [&](int h) {
+      __bf16* Qs = stg + h * kBwdStage;
+      put_blk(Qs, pq, br, bc);
+      put_blk(Qs + TILE, pk, br, bc);
+      put_blk(Qs + 2 * TILE, pv, br, bc);
+      put_blk(Qs + 3 * TILE, po, br, bc);
+      put_blk(Qs + 4 * TILE, ps, br, bc);
+      if (w == 0) plain_scan(pla, x.l, vec + h * kVec);
+    };
+    load(NC - 1);
+    stage((NC - 1) & 1);
+    if (NC > 1) load(NC - 2);
     __syncthreads();
     for (int cc = NC - 1; cc >= 0; --cc) {
-      const int t0 = cc * C;
-      float* vs = vec + (cc & 1) * kVec;
-      float* vn = vec + ((cc & 1) ^ 1) * kVec;
+      const int t0 = cc * C, h = cc & 1;
+      const __bf16* Qs = stg + h * kBwdStage;
+      const __bf16* Ks = Qs + TILE;
+      const __bf16* Vs = Qs + 2 * TILE;
+      const __bf16* Os = Qs + 3 * TILE;
+      const __bf16* Ss = Qs + 4 * TILE;
+      float* vs = vec + h * kVec;
       const float* Ls = vs;
       const float* eLs = vs + C;
       float* rowM = vs + 3 * C;  // row sums of dA o A
       float* qz = vs + 5 * C;    // q_t . (S_c dO_t)
-      if (cc > 0) {  // next chunk's tiles, staged after the barrier
-        const int n0 = t0 - C;
-        pq = load_blk(q + boff + (size_t)n0 * DK, DK, C, b);
-        pk = load_blk(k + boff + (size_t)n0 * DK, DK, C, b);
-        pv = load_blk(v + boff + (size_t)n0 * DK, DK, C, b);
-        po = load_blk(dO + boff + (size_t)n0 * DK, DK, C, b);
-        ps = load_blk(sent + ((size_t)bh * NC + cc - 1) * DK * DK, DK, DK, b);
-        if (w == 0) pla = la[(size_t)bh * T + n0 + x.l];
-      }
+      float* sdot = vs + 7 * C;  // per-wave <S_c, dS>
       // this chunk's rows of dQ: stores to rows past T fall outside the range and are dropped
       const __amdgpu_buffer_rsrc_t dq_out = __builtin_amdgcn_make_buffer_rsrc(
           dq + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
@@ -463,8 +433,8 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         f32x4 acc = zero4(), Z = zero4();
-        acc = pgn_mfma(frag(KT, 16 * dt + i, 0, g), b0, acc);
-        if (wl >= 2) acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), b1, acc);
+        acc = pgn_mfma(frag_tr(Ks, 16 * dt, 0, g, i), b0, acc);
+        if (wl >= 2) acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), b1, acc);
         Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
         Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
         const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
@@ -476,34 +446,51 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       }
       qzt = sum_groups(qzt);
       if (g == 0) qz[me] = qzt;
-      // rows 16 wl.. of (Q o eL)^T dO, applied to dS by group K after the barrier
-      const bf16x8 qe0 = frag_scaled_k(QT, 16 * wl + i, 0, g, eLs), qe1 = frag_scaled_k(QT, 16 * wl + i, 1, g, eLs);
+      // <S_c, dS> over rows 16 wl.. of dS, then dS <- a dS + (Q o eL)^T dO on them, into the other dS^T tile
+      float sd = 0.f;
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * wl + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
+      sd = wave_sum(sd);
+      if (x.l == 0) sdot[wl] = sd;
+      const float a_c = __expf(Ls[C - 1]);
+      const bf16x8 qe0 = frag_tr_scaled_k(Qs, 16 * wl, 0, g, i, eLs);
+      const bf16x8 qe1 = frag_tr_scaled_k(Qs, 16 * wl, 1, g, i, eLs);
+      __bf16* dSTn = dSTb + (h ^ 1) * TILE;
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
-        f32x4 m = pgn_mfma(qe0, frag(OT, 16 * jt + i, 0, g), zero4());
-        m = pgn_mfma(qe1, frag(OT, 16 * jt + i, 1, g), m);
-        Mb[(wl * 4 + jt) * 64 + x.l] = m;
+        f32x4 m = pgn_mfma(qe0, frag_tr(Os, 16 * jt, 0, g, i), zero4());
+        m = pgn_mfma(qe1, frag_tr(Os, 16 * jt, 1, g, i), m);
+        dS[jt] = dS[jt] * a_c + m;
+        store_T(dSTn, 16 * jt, 16 * wl, g, i, dS[jt]);
       }
-      if (w == 0 && cc < NC - 1) {  // the later chunk's dla, from the other vector set
+      if (w == 0 && cc < NC - 1) {  // the later chunk's dla, from the other vector set (before the scan below)
         const int tn = t0 + C;
-        plain_dla(vn, x.l, __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T + tn, (short)0,
-                                                             4 * min(C, T - tn), 0x00020000));
+        plain_dla(vec + (h ^ 1) * kVec, x.l,
+                  __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T + tn, (short)0, 4 * min(C, T - tn),
+                                                    0x00020000));
+      }
+      if (cc > 0) {
+        stage(h ^ 1);
+        if (cc > 1) load(cc - 2);
       }
       __syncthreads();
-      if (cc > 0) {
-        stage();
-        if (w == 0) plain_scan(pla, x.l, vn);
-        __syncthreads();
-      }
     }
     if (w == 0)  // chunk 0's dla (vector set 0)
       plain_dla(vec, x.l, __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T, (short)0, 4 * min(C, T),
                                                             0x00020000));
+    if (dS0) {
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dS0[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] = dS[jt][r];
+    }
   }
 }
 
 constexpr size_t kFwdSmem = 2 * (size_t)kFwdBuf + 2 * TILE * sizeof(__bf16);
-constexpr size_t kBwdSmem = 10 * TILE * sizeof(__bf16) + 2 * kVec * sizeof(float) + 16 * 64 * sizeof(f32x4);
+constexpr size_t kBwdSmem = (2 * kBwdStage + 2 * TILE) * sizeof(__bf16) + 2 * kVec * sizeof(float);
 
 bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
   if (B <= 0 || H <= 0 || T <= 0) return false;

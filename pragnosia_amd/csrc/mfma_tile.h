@@ -83,6 +83,33 @@ PGN_DEVICE bf16x8 frag_scaled_k(const __bf16* tile, int row, int m, int g, const
   return pack(a, b);
 }
 
+// Transposed operand fragments, on gfx950's LDS transpose read (ds_read_b64_tr_b16). Within each group of 16 lanes
+// the instruction hands lane L element L % 4 of the 8 bytes addressed by lanes L / 4, 4 + L / 4, 8 + L / 4 and
+// 12 + L / 4 (in that order). So if lane p of group g addresses row (r0 + 4g + p / 4), columns (n0 + 4 (p % 4)) ..
+// +3 of a row-major tile X, lane i of group g receives X[r0 + 4g + e][n0 + i] for e = 0..3: column n0 + i of X with
+// the contracted index running down X's rows, in this file's k order. frag_tr(X, n0, m, g, i) is therefore the
+// operand frag(X^T, n0 + i, m, g) read straight from X, with no transposed copy of X in LDS.
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+PGN_DEVICE bf16x4 ds_read_tr(const __bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
+}
+
+PGN_DEVICE bf16x8 frag_tr(const __bf16* tile, int n0, int m, int g, int i) {
+  const __bf16* p = tile + (32 * m + 4 * g + (i >> 2)) * kPitch + n0 + 4 * (i & 3);
+  return cat8(ds_read_tr(p), ds_read_tr(p + 16 * kPitch));
+}
+
+// frag_tr scaled per contracted index k by s[k] (fp32 LDS vector), rounded back to bf16.
+PGN_DEVICE bf16x8 frag_tr_scaled_k(const __bf16* tile, int n0, int m, int g, int i, const float* s) {
+  const __bf16* p = tile + (32 * m + 4 * g + (i >> 2)) * kPitch + n0 + 4 * (i & 3);
+  const f32x4 sa = *reinterpret_cast<const f32x4*>(s + 32 * m + 4 * g);
+  const f32x4 sb = *reinterpret_cast<const f32x4*>(s + 32 * m + 16 + 4 * g);
+  f32x4 a = to_f32x4(ds_read_tr(p)) * sa;
+  f32x4 b = to_f32x4(ds_read_tr(p + 16 * kPitch)) * sb;
+  return pack(a, b);
+}
+
 // Store an accumulator tile transposed into an LDS tile: rows 4g..4g+3 of column i land contiguously in row
 // (col0 + i) of `tile`, columns row0 + 4g .. +3 (one 8-byte write).
 PGN_DEVICE void store_T(__bf16* tile, int col0, int row0, int g, int i, f32x4 x) {
