@@ -210,7 +210,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 // (loaded a chunk earlier still), and its wave 0 runs the per-chunk scans: L for the next chunk and, from the other
 // set of double-buffered per-chunk vectors, the previous (later) chunk's dla. Operands contracted over a tile's row
 // index are read with the LDS transpose read, so each input is staged once, untransposed.
-constexpr int kVec = 7 * C + 4;  // one set of per-chunk vectors: L, eL, w, rowM, colM, qz, dwv (C each), sdot (4)
+// one set of per-chunk vectors: L, eL, w, rowM, colM, qz, dwv (C each) and the per-lane partial sums of <S_c, dS>
+// (4 waves x 64 lanes)
+constexpr int kVec = 11 * C;
 
 // dla of one chunk from its vector set: dL_t = rowM_t - colM_t + eL_t qz_t - w_t dwv_t, the chunk's last token adds
 // sum_s w_s dwv_s + a <S_c, dS>, and dla is the reverse inclusive cumulative sum of dL. One wave, lane = t.
@@ -227,7 +229,8 @@ PGN_DEVICE void plain_dla(const float* vs, int lane, __amdgpu_buffer_rsrc_t out)
   const float wd = ws[t] * dwv[t];
   float dL = rowM[t] - colM[t] + eLs[t] * qz[t] - wd;
   const float wdw = wave_sum(wd);
-  if (t == C - 1) dL += wdw + __expf(Ls[C - 1]) * (sdot[0] + sdot[1] + sdot[2] + sdot[3]);
+  const float sd = wave_sum((sdot[t] + sdot[C + t]) + (sdot[2 * C + t] + sdot[3 * C + t]));
+  if (t == C - 1) dL += wdw + __expf(Ls[C - 1]) * sd;
   dL = wave_suffix_sum(dL, t);
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, dL), out, 4 * t, 0, 0);
 }
@@ -263,7 +266,30 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   // The two groups run separate loops (the branch is on a wave-uniform value) that meet at the same barriers: each
   // loop's registers and memory-counter waits are then its own.
   if (w >= 4) {
-    // ================= group K: s = me, d block wl
+    // ================= group K: s = me, d block wl. Waves 6 and 7, whose share of the contractions is the
+    // smallest, also stage the Q and K tiles: thread b2 carries blocks b2 and b2 + 128 of each.
+    const bool kstage = wl >= 2;
+    const int b2 = tid & 127;
+    Blk4 pq0, pq1, pk0, pk1;
+    auto load = [&](int cn) {
+      const int n0 = cn * C, nr = min(C, T - n0);
+      pq0 = load_blk(q + boff + (size_t)n0 * DK, DK, nr, b2);
+      pq1 = load_blk(q + boff + (size_t)n0 * DK, DK, nr, b2 + 128);
+      pk0 = load_blk(k + boff + (size_t)n0 * DK, DK, nr, b2);
+      pk1 = load_blk(k + boff + (size_t)n0 * DK, DK, nr, b2 + 128);
+    };
+    auto stage = [&](int hh) {
+      __bf16* Qs = stg + hh * kBwdStage;
+      put_blk(Qs, pq0, 4 * (b2 >> 4), 4 * (b2 & 15));
+      put_blk(Qs, pq1, 4 * ((b2 + 128) >> 4), 4 * (b2 & 15));
+      put_blk(Qs + TILE, pk0, 4 * (b2 >> 4), 4 * (b2 & 15));
+      put_blk(Qs + TILE, pk1, 4 * ((b2 + 128) >> 4), 4 * (b2 & 15));
+    };
+    if (kstage) {
+      load(NC - 1);
+      stage((NC - 1) & 1);
+      if (NC > 1) load(NC - 2);
+    }
     __syncthreads();
     for (int cc = NC - 1; cc >= 0; --cc) {
       const int t0 = cc * C, h = cc & 1;
@@ -345,6 +371,10 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       }
       dw = sum_groups(dw);
       if (g == 0) dwv[me] = dw;
+      if (kstage && cc > 0) {
+        stage(h ^ 1);
+        if (cc > 1) load(cc - 2);
+      }
       __syncthreads();
     }
   } else {
@@ -357,15 +387,13 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         dS[jt][r] = dSfin ? dSfin[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] : 0.f;
       store_T(dSTb + ((NC - 1) & 1) * TILE, 16 * jt, 16 * wl, g, i, dS[jt]);
     }
-    // staging: thread b carries one 4x4 block of each of Q, K, V, dO and S_c
+    // staging: thread b carries one 4x4 block of each of V, dO and S_c (waves 6 and 7 stage Q and K)
     const int b = tid & 255;  // = tid; the mask tells the compiler that every block row is below 64
     const int br = 4 * (b >> 4), bc = 4 * (b & 15);
-    Blk4 pq, pk, pv, po, ps;
+    Blk4 pv, po, ps;
     float pla = 0.f;
     auto load = [&](int cn) {
       const int n0 = cn * C, nr = min(C, T - n0);
-      pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, b);
-      pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, b);
       pv = load_blk(v + boff + (size_t)n0 * DK, DK, nr, b);
       po = load_blk(dO + boff + (size_t)n0 * DK, DK, nr, b);
       ps = load_blk(sent + ((size_t)bh * NC + cn) * DK * DK, DK, DK, b);
@@ -373,8 +401,6 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
     };
     auto stage = [&](int h) {
       __bf16* Qs = stg + h * kBwdStage;
-      put_blk(Qs, pq, br, bc);
-      put_blk(Qs + TILE, pk, br, bc);
       put_blk(Qs + 2 * TILE, pv, br, bc);
       put_blk(Qs + 3 * TILE, po, br, bc);
       put_blk(Qs + 4 * TILE, ps, br, bc);
@@ -396,7 +422,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       const float* eLs = vs + C;
       float* rowM = vs + 3 * C;  // row sums of dA o A
       float* qz = vs + 5 * C;    // q_t . (S_c dO_t)
-      float* sdot = vs + 7 * C;  // per-wave <S_c, dS>
+      float* sdot = vs + 7 * C;  // per-lane partial sums of <S_c, dS>, summed in the dla
       // this chunk's rows of dQ: stores to rows past T fall outside the range and are dropped
       const __amdgpu_buffer_rsrc_t dq_out = __builtin_amdgcn_make_buffer_rsrc(
           dq + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
@@ -452,8 +478,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * wl + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
-      sd = wave_sum(sd);
-      if (x.l == 0) sdot[wl] = sd;
+      sdot[wl * 64 + x.l] = sd;
       const float a_c = __expf(Ls[C - 1]);
       const bf16x8 qe0 = frag_tr_scaled_k(Qs, 16 * wl, 0, g, i, eLs);
       const bf16x8 qe1 = frag_tr_scaled_k(Qs, 16 * wl, 1, g, i, eLs);
