@@ -23,6 +23,8 @@
 // (equations of `src/assoc_kernel.py:73-116`, `:205-220`, `:279-296`, merged into one pass). Every product that
 // has a transposed operand is computed in the orientation whose accumulator is the next product's operand, so
 // nothing round-trips through LDS except the two copies of dS.
+#include <type_traits>
+
 #include "mfma_tile.h"
 
 using namespace pgn;
@@ -261,7 +263,6 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   const int bh = blockIdx.x;
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
-  const int me = 16 * wl + i;  // group D: this lane's t; group K: this lane's s
 
   // The two groups run separate loops (the branch is on a wave-uniform value) that meet at the same barriers: each
   // loop's registers and memory-counter waits are then its own.
@@ -291,91 +292,101 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       if (NC > 1) load(NC - 2);
     }
     __syncthreads();
-    for (int cc = NC - 1; cc >= 0; --cc) {
-      const int t0 = cc * C, h = cc & 1;
-      const __bf16* Qs = stg + h * kBwdStage;
-      const __bf16* Ks = Qs + TILE;
-      const __bf16* Vs = Qs + 2 * TILE;
-      const __bf16* Os = Qs + 3 * TILE;
-      const __bf16* dST = dSTb + h * TILE;
-      float* vs = vec + h * kVec;
-      const float* Ls = vs;
-      const float* ws = vs + 2 * C;
-      float* colM = vs + 4 * C;  // column sums of dA o A
-      float* dwv = vs + 6 * C;   // k_s . (dS v_s)
-      // this chunk's rows of dV and dK: stores to rows past T fall outside the range and are dropped
-      const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
-      const __amdgpu_buffer_rsrc_t dv_out =
-          __builtin_amdgcn_make_buffer_rsrc(dv + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
-      const __amdgpu_buffer_rsrc_t dk_out =
-          __builtin_amdgcn_make_buffer_rsrc(dk + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
-      const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
-      const bf16x8 vf0 = frag(Vs, me, 0, g), vf1 = frag(Vs, me, 1, g);
-      const float Ls_s = Ls[me];
-      float colacc = 0.f;
-      f32x4 At[4], dPt[4];
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        At[tb] = zero4();
-        dPt[tb] = zero4();
-        if (tb >= wl) {
-          f32x4 P = zero4(), dA = zero4();
-          P = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, P);
-          P = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, P);
-          dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), vf0, dA);
-          dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), vf1, dA);
-          const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = 16 * tb + 4 * g + r;
-            const float dec = (t >= me) ? __expf(fminf(Ltv[r] - Ls_s, 0.f)) : 0.f;
-            At[tb][r] = P[r] * dec;
-            dPt[tb][r] = dA[r] * dec;
-            colacc += dA[r] * At[tb][r];
+    auto kloop = [&](auto wl_c) {
+      constexpr int WL = decltype(wl_c)::value;
+      const int me = 16 * WL + i;
+      for (int cc = NC - 1; cc >= 0; --cc) {
+        const int t0 = cc * C, h = cc & 1;
+        const __bf16* Qs = stg + h * kBwdStage;
+        const __bf16* Ks = Qs + TILE;
+        const __bf16* Vs = Qs + 2 * TILE;
+        const __bf16* Os = Qs + 3 * TILE;
+        const __bf16* dST = dSTb + h * TILE;
+        float* vs = vec + h * kVec;
+        const float* Ls = vs;
+        const float* ws = vs + 2 * C;
+        float* colM = vs + 4 * C;  // column sums of dA o A
+        float* dwv = vs + 6 * C;   // k_s . (dS v_s)
+        // this chunk's rows of dV and dK: stores to rows past T fall outside the range and are dropped
+        const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
+        const __amdgpu_buffer_rsrc_t dv_out =
+            __builtin_amdgcn_make_buffer_rsrc(dv + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t dk_out =
+            __builtin_amdgcn_make_buffer_rsrc(dk + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
+        const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
+        const bf16x8 vf0 = frag(Vs, me, 0, g), vf1 = frag(Vs, me, 1, g);
+        const float Ls_s = Ls[me];
+        float colacc = 0.f;
+        f32x4 At[4], dPt[4];
+  #pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          At[tb] = zero4();
+          dPt[tb] = zero4();
+          if (tb >= WL) {
+            f32x4 P = zero4(), dA = zero4();
+            P = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, P);
+            P = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, P);
+            dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), vf0, dA);
+            dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), vf1, dA);
+            const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = 16 * tb + 4 * g + r;
+              const float dec = (t >= me) ? __expf(fminf(Ltv[r] - Ls_s, 0.f)) : 0.f;
+              At[tb][r] = P[r] * dec;
+              dPt[tb][r] = dA[r] * dec;
+              colacc += dA[r] * At[tb][r];
+            }
           }
         }
+        colacc = sum_groups(colacc);
+        if (g == 0) colM[me] = colacc;
+        const bf16x8 A0 = pack(At[0], At[1]), A1 = pack(At[2], At[3]);
+        const bf16x8 dP0 = pack(dPt[0], dPt[1]), dP1 = pack(dPt[2], dPt[3]);
+        const float w_s = ws[me];
+        // dV^T tiles (j block jt, s block WL) = dO^T A + dS^T (K o w)^T
+        const bf16x8 kw0 = frag_scaled(Ks, me, 0, g, w_s), kw1 = frag_scaled(Ks, me, 1, g, w_s);
+  #pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+          f32x4 acc = zero4();
+          if (WL < 2) acc = pgn_mfma(frag_tr(Os, 16 * jt, 0, g, i), A0, acc);
+          acc = pgn_mfma(frag_tr(Os, 16 * jt, 1, g, i), A1, acc);
+          acc = pgn_mfma(frag(dST, 16 * jt + i, 0, g), kw0, acc);
+          acc = pgn_mfma(frag(dST, 16 * jt + i, 1, g), kw1, acc);
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dv_out,
+                                                (me * DK + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+        }
+        // dK^T tiles (d block dt, s block WL) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
+        const __bf16* krow = Ks + me * kPitch;
+        float dw = 0.f;
+  #pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          f32x4 acc = zero4(), Y = zero4();
+          if (WL < 2) acc = pgn_mfma(frag_tr(Qs, 16 * dt, 0, g, i), dP0, acc);
+          acc = pgn_mfma(frag_tr(Qs, 16 * dt, 1, g, i), dP1, acc);
+          Y = pgn_mfma(frag_tr(dST, 16 * dt, 0, g, i), vf0, Y);
+          Y = pgn_mfma(frag_tr(dST, 16 * dt, 1, g, i), vf1, Y);
+          const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
+          acc = acc + Y * w_s;
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dk_out,
+                                                (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+        }
+        dw = sum_groups(dw);
+        if (g == 0) dwv[me] = dw;
+        if (WL >= 2 && cc > 0) {
+          stage(h ^ 1);
+          if (cc > 1) load(cc - 2);
+        }
+        __syncthreads();
       }
-      colacc = sum_groups(colacc);
-      if (g == 0) colM[me] = colacc;
-      const bf16x8 A0 = pack(At[0], At[1]), A1 = pack(At[2], At[3]);
-      const bf16x8 dP0 = pack(dPt[0], dPt[1]), dP1 = pack(dPt[2], dPt[3]);
-      const float w_s = ws[me];
-      // dV^T tiles (j block jt, s block wl) = dO^T A + dS^T (K o w)^T
-      const bf16x8 kw0 = frag_scaled(Ks, me, 0, g, w_s), kw1 = frag_scaled(Ks, me, 1, g, w_s);
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        f32x4 acc = zero4();
-        if (wl < 2) acc = pgn_mfma(frag_tr(Os, 16 * jt, 0, g, i), A0, acc);
-        acc = pgn_mfma(frag_tr(Os, 16 * jt, 1, g, i), A1, acc);
-        acc = pgn_mfma(frag(dST, 16 * jt + i, 0, g), kw0, acc);
-        acc = pgn_mfma(frag(dST, 16 * jt + i, 1, g), kw1, acc);
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dv_out,
-                                              (me * DK + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
-      }
-      // dK^T tiles (d block dt, s block wl) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
-      const __bf16* krow = Ks + me * kPitch;
-      float dw = 0.f;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        f32x4 acc = zero4(), Y = zero4();
-        if (wl < 2) acc = pgn_mfma(frag_tr(Qs, 16 * dt, 0, g, i), dP0, acc);
-        acc = pgn_mfma(frag_tr(Qs, 16 * dt, 1, g, i), dP1, acc);
-        Y = pgn_mfma(frag_tr(dST, 16 * dt, 0, g, i), vf0, Y);
-        Y = pgn_mfma(frag_tr(dST, 16 * dt, 1, g, i), vf1, Y);
-        const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
-        acc = acc + Y * w_s;
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dk_out,
-                                              (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
-      }
-      dw = sum_groups(dw);
-      if (g == 0) dwv[me] = dw;
-      if (kstage && cc > 0) {
-        stage(h ^ 1);
-        if (cc > 1) load(cc - 2);
-      }
-      __syncthreads();
+    };
+    switch (wl) {  // one instantiation per block index: its block conditions are compile-time constants
+      case 0: kloop(std::integral_constant<int, 0>{}); break;
+      case 1: kloop(std::integral_constant<int, 1>{}); break;
+      case 2: kloop(std::integral_constant<int, 2>{}); break;
+      default: kloop(std::integral_constant<int, 3>{}); break;
     }
   } else {
     // ================= group D: t = me; dS rows 16 wl + 4g + r, column 16 jt + i
@@ -410,97 +421,107 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
     stage((NC - 1) & 1);
     if (NC > 1) load(NC - 2);
     __syncthreads();
-    for (int cc = NC - 1; cc >= 0; --cc) {
-      const int t0 = cc * C, h = cc & 1;
-      const __bf16* Qs = stg + h * kBwdStage;
-      const __bf16* Ks = Qs + TILE;
-      const __bf16* Vs = Qs + 2 * TILE;
-      const __bf16* Os = Qs + 3 * TILE;
-      const __bf16* Ss = Qs + 4 * TILE;
-      float* vs = vec + h * kVec;
-      const float* Ls = vs;
-      const float* eLs = vs + C;
-      float* rowM = vs + 3 * C;  // row sums of dA o A
-      float* qz = vs + 5 * C;    // q_t . (S_c dO_t)
-      float* sdot = vs + 7 * C;  // per-lane partial sums of <S_c, dS>, summed in the dla
-      // this chunk's rows of dQ: stores to rows past T fall outside the range and are dropped
-      const __amdgpu_buffer_rsrc_t dq_out = __builtin_amdgcn_make_buffer_rsrc(
-          dq + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
-      const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
-      const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
-      const float Lt = Ls[me];
-      float rowacc = 0.f;
-      f32x4 dPT[4];
-#pragma unroll
-      for (int sb = 0; sb < 4; ++sb) {
-        dPT[sb] = zero4();
-        if (sb <= wl) {
-          f32x4 PT = zero4(), dAT = zero4();
-          PT = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, PT);
-          PT = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, PT);
-          dAT = pgn_mfma(frag(Vs, 16 * sb + i, 0, g), of0, dAT);
-          dAT = pgn_mfma(frag(Vs, 16 * sb + i, 1, g), of1, dAT);
-          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int s = 16 * sb + 4 * g + r;
-            const float dec = (s <= me) ? __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
-            rowacc += dAT[r] * (PT[r] * dec);
-            dPT[sb][r] = dAT[r] * dec;
+    auto dloop = [&](auto wl_c) {
+      constexpr int WL = decltype(wl_c)::value;
+      const int me = 16 * WL + i;
+      for (int cc = NC - 1; cc >= 0; --cc) {
+        const int t0 = cc * C, h = cc & 1;
+        const __bf16* Qs = stg + h * kBwdStage;
+        const __bf16* Ks = Qs + TILE;
+        const __bf16* Vs = Qs + 2 * TILE;
+        const __bf16* Os = Qs + 3 * TILE;
+        const __bf16* Ss = Qs + 4 * TILE;
+        float* vs = vec + h * kVec;
+        const float* Ls = vs;
+        const float* eLs = vs + C;
+        float* rowM = vs + 3 * C;  // row sums of dA o A
+        float* qz = vs + 5 * C;    // q_t . (S_c dO_t)
+        float* sdot = vs + 7 * C;  // per-lane partial sums of <S_c, dS>, summed in the dla
+        // this chunk's rows of dQ: stores to rows past T fall outside the range and are dropped
+        const __amdgpu_buffer_rsrc_t dq_out = __builtin_amdgcn_make_buffer_rsrc(
+            dq + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
+        const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
+        const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
+        const float Lt = Ls[me];
+        float rowacc = 0.f;
+        f32x4 dPT[4];
+  #pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+          dPT[sb] = zero4();
+          if (sb <= WL) {
+            f32x4 PT = zero4(), dAT = zero4();
+            PT = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, PT);
+            PT = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, PT);
+            dAT = pgn_mfma(frag(Vs, 16 * sb + i, 0, g), of0, dAT);
+            dAT = pgn_mfma(frag(Vs, 16 * sb + i, 1, g), of1, dAT);
+            const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int s = 16 * sb + 4 * g + r;
+              const float dec = (s <= me) ? __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+              rowacc += dAT[r] * (PT[r] * dec);
+              dPT[sb][r] = dAT[r] * dec;
+            }
           }
         }
+        rowacc = sum_groups(rowacc);
+        if (g == 0) rowM[me] = rowacc;
+        const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
+        const float eLt = eLs[me];
+        const __bf16* qrow = Qs + me * kPitch;
+        float qzt = 0.f;
+  #pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          f32x4 acc = zero4(), Z = zero4();
+          acc = pgn_mfma(frag_tr(Ks, 16 * dt, 0, g, i), b0, acc);
+          if (WL >= 2) acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), b1, acc);
+          Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
+          Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
+          const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
+          acc = acc + Z * eLt;
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dq_out,
+                                                (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+        }
+        qzt = sum_groups(qzt);
+        if (g == 0) qz[me] = qzt;
+        // <S_c, dS> over rows 16 WL.. of dS, then dS <- a dS + (Q o eL)^T dO on them, into the other dS^T tile
+        float sd = 0.f;
+  #pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * WL + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
+        sdot[WL * 64 + x.l] = sd;
+        const float a_c = __expf(Ls[C - 1]);
+        const bf16x8 qe0 = frag_tr_scaled_k(Qs, 16 * WL, 0, g, i, eLs);
+        const bf16x8 qe1 = frag_tr_scaled_k(Qs, 16 * WL, 1, g, i, eLs);
+        __bf16* dSTn = dSTb + (h ^ 1) * TILE;
+  #pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+          f32x4 m = pgn_mfma(qe0, frag_tr(Os, 16 * jt, 0, g, i), zero4());
+          m = pgn_mfma(qe1, frag_tr(Os, 16 * jt, 1, g, i), m);
+          dS[jt] = dS[jt] * a_c + m;
+          store_T(dSTn, 16 * jt, 16 * WL, g, i, dS[jt]);
+        }
+        if (w == 0 && cc < NC - 1) {  // the later chunk's dla, from the other vector set (before the scan below)
+          const int tn = t0 + C;
+          plain_dla(vec + (h ^ 1) * kVec, x.l,
+                    __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T + tn, (short)0, 4 * min(C, T - tn),
+                                                      0x00020000));
+        }
+        if (cc > 0) {
+          stage(h ^ 1);
+          if (cc > 1) load(cc - 2);
+        }
+        __syncthreads();
       }
-      rowacc = sum_groups(rowacc);
-      if (g == 0) rowM[me] = rowacc;
-      const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
-      const float eLt = eLs[me];
-      const __bf16* qrow = Qs + me * kPitch;
-      float qzt = 0.f;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        f32x4 acc = zero4(), Z = zero4();
-        acc = pgn_mfma(frag_tr(Ks, 16 * dt, 0, g, i), b0, acc);
-        if (wl >= 2) acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), b1, acc);
-        Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
-        Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
-        const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
-        acc = acc + Z * eLt;
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dq_out,
-                                              (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
-      }
-      qzt = sum_groups(qzt);
-      if (g == 0) qz[me] = qzt;
-      // <S_c, dS> over rows 16 wl.. of dS, then dS <- a dS + (Q o eL)^T dO on them, into the other dS^T tile
-      float sd = 0.f;
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * wl + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
-      sdot[wl * 64 + x.l] = sd;
-      const float a_c = __expf(Ls[C - 1]);
-      const bf16x8 qe0 = frag_tr_scaled_k(Qs, 16 * wl, 0, g, i, eLs);
-      const bf16x8 qe1 = frag_tr_scaled_k(Qs, 16 * wl, 1, g, i, eLs);
-      __bf16* dSTn = dSTb + (h ^ 1) * TILE;
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        f32x4 m = pgn_mfma(qe0, frag_tr(Os, 16 * jt, 0, g, i), zero4());
-        m = pgn_mfma(qe1, frag_tr(Os, 16 * jt, 1, g, i), m);
-        dS[jt] = dS[jt] * a_c + m;
-        store_T(dSTn, 16 * jt, 16 * wl, g, i, dS[jt]);
-      }
-      if (w == 0 && cc < NC - 1) {  // the later chunk's dla, from the other vector set (before the scan below)
-        const int tn = t0 + C;
-        plain_dla(vec + (h ^ 1) * kVec, x.l,
-                  __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T + tn, (short)0, 4 * min(C, T - tn),
-                                                    0x00020000));
-      }
-      if (cc > 0) {
-        stage(h ^ 1);
-        if (cc > 1) load(cc - 2);
-      }
-      __syncthreads();
+    };
+    switch (wl) {  // one instantiation per block index: its block conditions are compile-time constants
+      case 0: dloop(std::integral_constant<int, 0>{}); break;
+      case 1: dloop(std::integral_constant<int, 1>{}); break;
+      case 2: dloop(std::integral_constant<int, 2>{}); break;
+      default: dloop(std::integral_constant<int, 3>{}); break;
     }
     if (w == 0)  // chunk 0's dla (vector set 0)
       plain_dla(vec, x.l, __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T, (short)0, 4 * min(C, T),
