@@ -42,7 +42,7 @@ constexpr int TILE = 64 * kPitch;  // one staged 64 x 64 tile
 // issue chunk c + 2's loads and copy chunk c's entering state to `sent`. The state tile S^T the output needs is
 // double-buffered too, so one barrier per chunk orders everything.
 constexpr int kFwdWaves = 12;
-constexpr int kFwdBuf = 4 * TILE * (int)sizeof(__bf16) + 3 * C * (int)sizeof(float);  // Q, K, K^T, V^T, L, eL, w
+constexpr int kFwdBuf = 3 * TILE * (int)sizeof(__bf16) + 3 * C * (int)sizeof(float);  // Q, K, V, L, eL, w
 
 __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
@@ -52,9 +52,8 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
   // buffer set h: Q, K, K^T, V^T tiles and the L, eL, w vectors; then S^T (j, d) for two chunks
   auto Qb = [&](int h) { return reinterpret_cast<__bf16*>(smem + h * kFwdBuf); };
   auto Kb = [&](int h) { return Qb(h) + TILE; };
-  auto KTb = [&](int h) { return Qb(h) + 2 * TILE; };
-  auto VTb = [&](int h) { return Qb(h) + 3 * TILE; };
-  auto Vecb = [&](int h) { return reinterpret_cast<float*>(Qb(h) + 4 * TILE); };
+  auto Vb = [&](int h) { return Qb(h) + 2 * TILE; };
+  auto Vecb = [&](int h) { return reinterpret_cast<float*>(Qb(h) + 3 * TILE); };
   auto STb = [&](int h) { return reinterpret_cast<__bf16*>(smem + 2 * kFwdBuf) + h * TILE; };
 
   const WaveIdx x = wave_idx();
@@ -66,7 +65,6 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
   if (w < 8) {
     // ================= compute waves
     const int tb = w & 3, j0 = 32 * (w >> 2);
-    const int tq = 16 * tb + i;  // this lane's token within the chunk for t-indexed operands
     // state rows 16 tb + 4g + r, columns j0 + 16 jt + i
     f32x4 S[2];
 #pragma unroll
@@ -76,93 +74,106 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       store_T(STb(0), j0 + 16 * jt, 16 * tb, g, i, S[jt]);
     }
     __syncthreads();
-    for (int c = 0; c < NC; ++c) {
-      const int h = c & 1, t0 = c * C;
-      const __bf16* Qs = Qb(h);
-      const __bf16* Ks = Kb(h);
-      const __bf16* KT = KTb(h);
-      const __bf16* VT = VTb(h);
-      const __bf16* ST = STb(h);
-      const float* Ls = Vecb(h);
-      const float* eLs = Ls + C;
-      const float* ws = Ls + 2 * C;
-      // (Q K^T)^T tiles (s block sb, t block tb), decayed and masked: lane holds column t = tq, rows s.
-      const bf16x8 qf0 = frag(Qs, tq, 0, g), qf1 = frag(Qs, tq, 1, g);
-      const float Lt = Ls[tq];
-      f32x4 pt[4];
-#pragma unroll
-      for (int sb = 0; sb < 4; ++sb) {
-        pt[sb] = zero4();
-        if (sb <= tb) {
-          pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
-          pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
-          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int s = 16 * sb + 4 * g + r;
-            pt[sb][r] = (s <= tq) ? pt[sb][r] * __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+    auto cloop = [&](auto tb_c) {
+      constexpr int TB = decltype(tb_c)::value;
+      const int tq = 16 * TB + i;  // this lane's token within the chunk for t-indexed operands
+      for (int c = 0; c < NC; ++c) {
+        const int h = c & 1, t0 = c * C;
+        const __bf16* Qs = Qb(h);
+        const __bf16* Ks = Kb(h);
+        const __bf16* Vs = Vb(h);
+        const __bf16* ST = STb(h);
+        const float* Ls = Vecb(h);
+        const float* eLs = Ls + C;
+        const float* ws = Ls + 2 * C;
+        // (Q K^T)^T tiles (s block sb, t block TB), decayed and masked: lane holds column t = tq, rows s.
+        const bf16x8 qf0 = frag(Qs, tq, 0, g), qf1 = frag(Qs, tq, 1, g);
+        const float Lt = Ls[tq];
+        f32x4 pt[4];
+  #pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+          pt[sb] = zero4();
+          if (sb <= TB) {
+            pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
+            pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
+            const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int s = 16 * sb + 4 * g + r;
+              pt[sb][r] = (s <= tq) ? pt[sb][r] * __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+            }
           }
         }
-      }
-      const bf16x8 af0 = pack(pt[0], pt[1]);
-      const bf16x8 af1 = pack(pt[2], pt[3]);
-      const float eLt = eLs[tq];
-      const bf16x8 qe0 = frag_scaled(Qs, tq, 0, g, eLt);
-      const bf16x8 qe1 = frag_scaled(Qs, tq, 1, g, eLt);
+        const bf16x8 af0 = pack(pt[0], pt[1]);
+        const bf16x8 af1 = pack(pt[2], pt[3]);
+        const float eLt = eLs[tq];
+        const bf16x8 qe0 = frag_scaled(Qs, tq, 0, g, eLt);
+        const bf16x8 qe1 = frag_scaled(Qs, tq, 1, g, eLt);
 
-      // O^T tiles (value block jt, t block tb) = V^T A^T + S^T (Q o eL)^T; lane holds token tq, 4 value columns.
-      // Rows past T fall outside the store's range and are dropped.
-      const __amdgpu_buffer_rsrc_t o_out = __builtin_amdgcn_make_buffer_rsrc(
-          o + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
-#pragma unroll
-      for (int jt = 0; jt < 2; ++jt) {
-        const int jr = j0 + 16 * jt + i;
-        f32x4 acc = zero4();
-        acc = pgn_mfma(frag(VT, jr, 0, g), af0, acc);
-        if (tb >= 2) acc = pgn_mfma(frag(VT, jr, 1, g), af1, acc);
-        acc = pgn_mfma(frag(ST, jr, 0, g), qe0, acc);
-        acc = pgn_mfma(frag(ST, jr, 1, g), qe1, acc);
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
-                                              (tq * DK + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
-      }
+        // O^T tiles (value block jt, t block TB) = V^T A^T + S^T (Q o eL)^T; lane holds token tq, 4 value columns.
+        // Rows past T fall outside the store's range and are dropped.
+        const __amdgpu_buffer_rsrc_t o_out = __builtin_amdgcn_make_buffer_rsrc(
+            o + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
+  #pragma unroll
+        for (int jt = 0; jt < 2; ++jt) {
+          const int jr = j0 + 16 * jt + i;
+          f32x4 acc = zero4();
+          acc = pgn_mfma(frag_tr(Vs, j0 + 16 * jt, 0, g, i), af0, acc);
+          if (TB >= 2) acc = pgn_mfma(frag_tr(Vs, j0 + 16 * jt, 1, g, i), af1, acc);
+          acc = pgn_mfma(frag(ST, jr, 0, g), qe0, acc);
+          acc = pgn_mfma(frag(ST, jr, 1, g), qe1, acc);
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
+                                                (tq * DK + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+        }
 
-      // S <- a S + (K o w)^T V on rows 16 tb.. and this wave's columns; S^T of the next chunk into the other buffer
-      const float a_c = __expf(Ls[C - 1]);
-      const bf16x8 kw0 = frag_scaled_k(KT, 16 * tb + i, 0, g, ws);
-      const bf16x8 kw1 = frag_scaled_k(KT, 16 * tb + i, 1, g, ws);
-#pragma unroll
-      for (int jt = 0; jt < 2; ++jt) {
-        const int jr = j0 + 16 * jt + i;
-        S[jt] = S[jt] * a_c;
-        S[jt] = pgn_mfma(kw0, frag(VT, jr, 0, g), S[jt]);
-        S[jt] = pgn_mfma(kw1, frag(VT, jr, 1, g), S[jt]);
-        store_T(STb(h ^ 1), j0 + 16 * jt, 16 * tb, g, i, S[jt]);
+        // S <- a S + (K o w)^T V on rows 16 TB.. and this wave's columns; S^T of the next chunk into the other buffer
+        const float a_c = __expf(Ls[C - 1]);
+        const bf16x8 kw0 = frag_tr_scaled_k(Ks, 16 * TB, 0, g, i, ws);
+        const bf16x8 kw1 = frag_tr_scaled_k(Ks, 16 * TB, 1, g, i, ws);
+  #pragma unroll
+        for (int jt = 0; jt < 2; ++jt) {
+          const int jr = j0 + 16 * jt + i;
+          S[jt] = S[jt] * a_c;
+          S[jt] = pgn_mfma(kw0, frag_tr(Vs, j0 + 16 * jt, 0, g, i), S[jt]);
+          S[jt] = pgn_mfma(kw1, frag_tr(Vs, j0 + 16 * jt, 1, g, i), S[jt]);
+          store_T(STb(h ^ 1), j0 + 16 * jt, 16 * TB, g, i, S[jt]);
+        }
+        __syncthreads();
       }
-      __syncthreads();
+    };
+    switch (tb) {  // one instantiation per t block: its block conditions are compile-time constants
+      case 0: cloop(std::integral_constant<int, 0>{}); break;
+      case 1: cloop(std::integral_constant<int, 1>{}); break;
+      case 2: cloop(std::integral_constant<int, 2>{}); break;
+      default: cloop(std::integral_constant<int, 3>{}); break;
     }
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) Sfin[soff + (16 * tb + 4 * g + r) * DK + j0 + 16 * jt + i] = S[jt][r];
   } else {
-    // ================= load waves: thread b carries one 4x4 block of each of Q, K and V
+    // ================= load waves: thread b carries 16-byte row segments b and b + 256 of each of Q, K and V
     const int b = tid & 255;
-    const int br = 4 * (b >> 4), bc = 4 * (b & 15);
     const bool w0 = w == 8;  // runs the decay scans
-    Blk4 pq, pk, pv;
+    bf16x8 sq0, sq1, sk0, sk1, sv0, sv1;
     float pla = 0.f;
     auto load = [&](int cn) {
       const int n0 = cn * C, nr = min(C, T - n0);
-      pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, b);
-      pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, b);
-      pv = load_blk(v + boff + (size_t)n0 * DK, DK, nr, b);
+      sq0 = load_seg(q + boff + (size_t)n0 * DK, nr, b);
+      sq1 = load_seg(q + boff + (size_t)n0 * DK, nr, b + 256);
+      sk0 = load_seg(k + boff + (size_t)n0 * DK, nr, b);
+      sk1 = load_seg(k + boff + (size_t)n0 * DK, nr, b + 256);
+      sv0 = load_seg(v + boff + (size_t)n0 * DK, nr, b);
+      sv1 = load_seg(v + boff + (size_t)n0 * DK, nr, b + 256);
       if (w0) pla = (n0 + x.l < T) ? la[(size_t)bh * T + n0 + x.l] : 0.f;
     };
     auto stage = [&](int h) {
-      put_blk(Qb(h), pq, br, bc);
-      put_blk(Kb(h), pk, br, bc);
-      put_blk_T(KTb(h), pk, br, bc);
-      put_blk_T(VTb(h), pv, br, bc);
+      put_seg(Qb(h), sq0, b);
+      put_seg(Qb(h), sq1, b + 256);
+      put_seg(Kb(h), sk0, b);
+      put_seg(Kb(h), sk1, b + 256);
+      put_seg(Vb(h), sv0, b);
+      put_seg(Vb(h), sv1, b + 256);
       if (w0) {
         const float L = wave_prefix_sum(pla, x.l);
         const float LC = lane_value(L, 63);
@@ -184,6 +195,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       }
       if (sent) {  // chunk c's entering state, bf16 (d, j): a 4x4 block of S^T read and transposed per thread
         const __bf16* ST = STb(h);
+        const int br = 4 * (b >> 4), bc = 4 * (b & 15);
         Blk4 st;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) st.r[jj] = *reinterpret_cast<const bf16x4*>(ST + (br + jj) * kPitch + bc);
@@ -268,23 +280,25 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   // loop's registers and memory-counter waits are then its own.
   if (w >= 4) {
     // ================= group K: s = me, d block wl. Waves 6 and 7, whose share of the contractions is the
-    // smallest, also stage the Q and K tiles: thread b2 carries blocks b2 and b2 + 128 of each.
+    // smallest, also stage the Q and K tiles: thread b2 carries 16-byte row segments b2 + 128 n (n = 0..3) of each.
     const bool kstage = wl >= 2;
     const int b2 = tid & 127;
-    Blk4 pq0, pq1, pk0, pk1;
+    bf16x8 sq[4], sk[4];
     auto load = [&](int cn) {
       const int n0 = cn * C, nr = min(C, T - n0);
-      pq0 = load_blk(q + boff + (size_t)n0 * DK, DK, nr, b2);
-      pq1 = load_blk(q + boff + (size_t)n0 * DK, DK, nr, b2 + 128);
-      pk0 = load_blk(k + boff + (size_t)n0 * DK, DK, nr, b2);
-      pk1 = load_blk(k + boff + (size_t)n0 * DK, DK, nr, b2 + 128);
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        sq[n] = load_seg(q + boff + (size_t)n0 * DK, nr, b2 + 128 * n);
+        sk[n] = load_seg(k + boff + (size_t)n0 * DK, nr, b2 + 128 * n);
+      }
     };
     auto stage = [&](int hh) {
       __bf16* Qs = stg + hh * kBwdStage;
-      put_blk(Qs, pq0, 4 * (b2 >> 4), 4 * (b2 & 15));
-      put_blk(Qs, pq1, 4 * ((b2 + 128) >> 4), 4 * (b2 & 15));
-      put_blk(Qs + TILE, pk0, 4 * (b2 >> 4), 4 * (b2 & 15));
-      put_blk(Qs + TILE, pk1, 4 * ((b2 + 128) >> 4), 4 * (b2 & 15));
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        put_seg(Qs, sq[n], b2 + 128 * n);
+        put_seg(Qs + TILE, sk[n], b2 + 128 * n);
+      }
     };
     if (kstage) {
       load(NC - 1);
@@ -398,23 +412,29 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         dS[jt][r] = dSfin ? dSfin[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] : 0.f;
       store_T(dSTb + ((NC - 1) & 1) * TILE, 16 * jt, 16 * wl, g, i, dS[jt]);
     }
-    // staging: thread b carries one 4x4 block of each of V, dO and S_c (waves 6 and 7 stage Q and K)
-    const int b = tid & 255;  // = tid; the mask tells the compiler that every block row is below 64
-    const int br = 4 * (b >> 4), bc = 4 * (b & 15);
-    Blk4 pv, po, ps;
+    // staging: thread b carries 16-byte row segments b and b + 256 of each of V, dO and S_c (waves 6 and 7 stage
+    // Q and K)
+    const int b = tid & 255;  // = tid; the mask tells the compiler that every segment row is below 64
+    bf16x8 sv0, sv1, so0, so1, ss0, ss1;
     float pla = 0.f;
     auto load = [&](int cn) {
       const int n0 = cn * C, nr = min(C, T - n0);
-      pv = load_blk(v + boff + (size_t)n0 * DK, DK, nr, b);
-      po = load_blk(dO + boff + (size_t)n0 * DK, DK, nr, b);
-      ps = load_blk(sent + ((size_t)bh * NC + cn) * DK * DK, DK, DK, b);
+      sv0 = load_seg(v + boff + (size_t)n0 * DK, nr, b);
+      sv1 = load_seg(v + boff + (size_t)n0 * DK, nr, b + 256);
+      so0 = load_seg(dO + boff + (size_t)n0 * DK, nr, b);
+      so1 = load_seg(dO + boff + (size_t)n0 * DK, nr, b + 256);
+      ss0 = load_seg(sent + ((size_t)bh * NC + cn) * DK * DK, DK, b);
+      ss1 = load_seg(sent + ((size_t)bh * NC + cn) * DK * DK, DK, b + 256);
       if (w == 0) pla = (n0 + x.l < T) ? la[(size_t)bh * T + n0 + x.l] : 0.f;
     };
     auto stage = [&](int h) {
       __bf16* Qs = stg + h * kBwdStage;
-      put_blk(Qs + 2 * TILE, pv, br, bc);
-      put_blk(Qs + 3 * TILE, po, br, bc);
-      put_blk(Qs + 4 * TILE, ps, br, bc);
+      put_seg(Qs + 2 * TILE, sv0, b);
+      put_seg(Qs + 2 * TILE, sv1, b + 256);
+      put_seg(Qs + 3 * TILE, so0, b);
+      put_seg(Qs + 3 * TILE, so1, b + 256);
+      put_seg(Qs + 4 * TILE, ss0, b);
+      put_seg(Qs + 4 * TILE, ss1, b + 256);
       if (w == 0) plain_scan(pla, x.l, vec + h * kVec);
     };
     load(NC - 1);

@@ -180,6 +180,26 @@ PGN_DEVICE void put_blk_T(__bf16* tile, const Blk4& x, int r0, int c0) {
   }
 }
 
+// Staging of row-major 64-column bf16 tiles in 16-byte row segments, for tiles that are only ever read untransposed
+// or through frag_tr: segment e covers row e / 8, columns 8 (e % 8) .. +7, so one 64-lane load reads eight whole
+// 128-byte rows. Rows >= nrows (>= 1) read as zero (the load itself is clamped to row nrows - 1, unconditional).
+PGN_DEVICE bf16x8 load_seg(const __bf16* __restrict__ src, int nrows, int e) {
+  const int r = e >> 3;
+  const bf16x8 v = *reinterpret_cast<const bf16x8*>(src + (size_t)min(r, nrows - 1) * 64 + 8 * (e & 7));
+  if (r < nrows) return v;
+  bf16x8 z;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) z[j] = (__bf16)0.f;
+  return z;
+}
+
+// The segment into an LDS tile (pitch kPitch, so rows are 8-byte aligned: two 8-byte writes).
+PGN_DEVICE void put_seg(__bf16* tile, bf16x8 v, int e) {
+  __bf16* p = tile + (e >> 3) * kPitch + 8 * (e & 7);
+  *reinterpret_cast<bf16x4*>(p) = __builtin_shufflevector(v, v, 0, 1, 2, 3);
+  *reinterpret_cast<bf16x4*>(p + 4) = __builtin_shufflevector(v, v, 4, 5, 6, 7);
+}
+
 // exp(min(x, 0)) where `keep`, else 0, without a branch: the exponent is never positive, so the unmasked value is
 // finite and at most 1 and the mask is a select (a branch per element around the exp serialises the waves).
 PGN_DEVICE float masked_decay(float x, bool keep) { return __expf(fminf(x, 0.f)) * (keep ? 1.f : 0.f); }
