@@ -35,16 +35,16 @@ constexpr int C = 64;
 constexpr int DK = 64;
 constexpr int TILE = 64 * kPitch;  // one staged 64 x 64 tile
 
-// Forward: one workgroup of 12 waves per (batch, head), chunks in order. Waves 0-7 compute: wave w owns t block
-// tb = w & 3 and value columns 32 jh .. 32 jh + 31 (jh = w >> 2), and holds rows 16 tb.. of the fp32 state for those
-// columns as accumulator tiles. Waves 8-11 load: while waves 0-7 compute chunk c from one half of a double-buffered
+// Forward: one workgroup of 12 waves per (batch, head), chunks in order. Waves 0-7 compute: wave w owns a t block tb
+// and value columns 32 jh .. 32 jh + 31 (jh = w >> 2), and holds rows 16 tb.. of the fp32 state for those columns as
+// accumulator tiles. Waves 8-11 load: while waves 0-7 compute chunk c from one half of a double-buffered
 // LDS, they stage chunk c + 1 (prefetched into registers during chunk c - 1) into the other half, run its decay scan,
 // issue chunk c + 2's loads and copy chunk c's entering state to `sent`. The state tile S^T the output needs is
 // double-buffered too, so one barrier per chunk orders everything.
 constexpr int kFwdWaves = 12;
 constexpr int kFwdBuf = 3 * TILE * (int)sizeof(__bf16) + 3 * C * (int)sizeof(float);  // Q, K, V, L, eL, w
 
-__global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
+__global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 3))) void aspin_plain_fwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const float* __restrict__ S0, __bf16* __restrict__ o, float* __restrict__ Sfin,
     __bf16* __restrict__ sent, int T, int NC) {
@@ -64,7 +64,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 
   if (w < 8) {
     // ================= compute waves
-    const int tb = w & 3, j0 = 32 * (w >> 2);
+    // t block: waves w and w + 4 share a SIMD, so the second half takes the blocks in reverse order and each SIMD
+    // gets one heavy (late) and one light (early) t block
+    const int tb = w < 4 ? w : 7 - w, j0 = 32 * (w >> 2);
     // state rows 16 tb + 4g + r, columns j0 + 16 jt + i
     f32x4 S[2];
 #pragma unroll
@@ -86,56 +88,78 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
         const float* Ls = Vecb(h);
         const float* eLs = Ls + C;
         const float* ws = Ls + 2 * C;
-        // (Q K^T)^T tiles (s block sb, t block TB), decayed and masked: lane holds column t = tq, rows s.
+        // Every LDS operand of the chunk is read first, in the order it is consumed: the reads return in order while
+        // the MFMAs below run, instead of each MFMA waiting for a read issued just before it. The value operands serve
+        // both the output (as V^T) and the state update (as V).
         const bf16x8 qf0 = frag(Qs, tq, 0, g), qf1 = frag(Qs, tq, 1, g);
-        const float Lt = Ls[tq];
+        bf16x8 kf[TB + 1][2];
+        f32x4 Lsv[TB + 1];
+#pragma unroll
+        for (int sb = 0; sb <= TB; ++sb) {
+          kf[sb][0] = frag(Ks, 16 * sb + i, 0, g);
+          kf[sb][1] = frag(Ks, 16 * sb + i, 1, g);
+          Lsv[sb] = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+        }
+        const float Lt = Ls[tq], eLt = eLs[tq], LC = Ls[C - 1];
+        bf16x8 vf[2][2], sf[2][2];
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) {
+          vf[jt][0] = frag_tr(Vs, j0 + 16 * jt, 0, g, i);
+          vf[jt][1] = frag_tr(Vs, j0 + 16 * jt, 1, g, i);
+          sf[jt][0] = frag(ST, j0 + 16 * jt + i, 0, g);
+          sf[jt][1] = frag(ST, j0 + 16 * jt + i, 1, g);
+        }
+        const bf16x8 kt0 = frag_tr(Ks, 16 * TB, 0, g, i), kt1 = frag_tr(Ks, 16 * TB, 1, g, i);
+        const f32x4 w00 = *reinterpret_cast<const f32x4*>(ws + 4 * g);
+        const f32x4 w01 = *reinterpret_cast<const f32x4*>(ws + 16 + 4 * g);
+        const f32x4 w10 = *reinterpret_cast<const f32x4*>(ws + 32 + 4 * g);
+        const f32x4 w11 = *reinterpret_cast<const f32x4*>(ws + 48 + 4 * g);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // (Q K^T)^T tiles (s block sb, t block TB), decayed and masked: lane holds column t = tq, rows s.
         f32x4 pt[4];
-  #pragma unroll
+#pragma unroll
         for (int sb = 0; sb < 4; ++sb) {
           pt[sb] = zero4();
           if (sb <= TB) {
-            pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
-            pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
-            const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-  #pragma unroll
+            pt[sb] = pgn_mfma(kf[sb][0], qf0, pt[sb]);
+            pt[sb] = pgn_mfma(kf[sb][1], qf1, pt[sb]);
+#pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int s = 16 * sb + 4 * g + r;
-              pt[sb][r] = (s <= tq) ? pt[sb][r] * __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+              pt[sb][r] = (s <= tq) ? pt[sb][r] * __expf(fminf(Lt - Lsv[sb][r], 0.f)) : 0.f;
             }
           }
         }
         const bf16x8 af0 = pack(pt[0], pt[1]);
         const bf16x8 af1 = pack(pt[2], pt[3]);
-        const float eLt = eLs[tq];
-        const bf16x8 qe0 = frag_scaled(Qs, tq, 0, g, eLt);
-        const bf16x8 qe1 = frag_scaled(Qs, tq, 1, g, eLt);
+        const bf16x8 qe0 = scale_frag(qf0, eLt);
+        const bf16x8 qe1 = scale_frag(qf1, eLt);
 
         // O^T tiles (value block jt, t block TB) = V^T A^T + S^T (Q o eL)^T; lane holds token tq, 4 value columns.
         // Rows past T fall outside the store's range and are dropped.
         const __amdgpu_buffer_rsrc_t o_out = __builtin_amdgcn_make_buffer_rsrc(
             o + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
-  #pragma unroll
+#pragma unroll
         for (int jt = 0; jt < 2; ++jt) {
-          const int jr = j0 + 16 * jt + i;
           f32x4 acc = zero4();
-          acc = pgn_mfma(frag_tr(Vs, j0 + 16 * jt, 0, g, i), af0, acc);
-          if (TB >= 2) acc = pgn_mfma(frag_tr(Vs, j0 + 16 * jt, 1, g, i), af1, acc);
-          acc = pgn_mfma(frag(ST, jr, 0, g), qe0, acc);
-          acc = pgn_mfma(frag(ST, jr, 1, g), qe1, acc);
+          acc = pgn_mfma(vf[jt][0], af0, acc);
+          if (TB >= 2) acc = pgn_mfma(vf[jt][1], af1, acc);
+          acc = pgn_mfma(sf[jt][0], qe0, acc);
+          acc = pgn_mfma(sf[jt][1], qe1, acc);
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
                                                 (tq * DK + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
         }
 
         // S <- a S + (K o w)^T V on rows 16 TB.. and this wave's columns; S^T of the next chunk into the other buffer
-        const float a_c = __expf(Ls[C - 1]);
-        const bf16x8 kw0 = frag_tr_scaled_k(Ks, 16 * TB, 0, g, i, ws);
-        const bf16x8 kw1 = frag_tr_scaled_k(Ks, 16 * TB, 1, g, i, ws);
-  #pragma unroll
+        const float a_c = __expf(LC);
+        const bf16x8 kw0 = scale_frag_k(kt0, w00, w01);
+        const bf16x8 kw1 = scale_frag_k(kt1, w10, w11);
+#pragma unroll
         for (int jt = 0; jt < 2; ++jt) {
-          const int jr = j0 + 16 * jt + i;
           S[jt] = S[jt] * a_c;
-          S[jt] = pgn_mfma(kw0, frag_tr(Vs, j0 + 16 * jt, 0, g, i), S[jt]);
-          S[jt] = pgn_mfma(kw1, frag_tr(Vs, j0 + 16 * jt, 1, g, i), S[jt]);
+          S[jt] = pgn_mfma(kw0, vf[jt][0], S[jt]);
+          S[jt] = pgn_mfma(kw1, vf[jt][1], S[jt]);
           store_T(STb(h ^ 1), j0 + 16 * jt, 16 * TB, g, i, S[jt]);
         }
         __syncthreads();

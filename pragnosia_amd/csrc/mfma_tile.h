@@ -110,6 +110,19 @@ PGN_DEVICE bf16x8 frag_tr_scaled_k(const __bf16* tile, int n0, int m, int g, int
   return pack(a, b);
 }
 
+// A fragment already in registers scaled by one factor, or per contracted index k by (sa, sb) (the factors of its
+// elements 0..3 and 4..7), rounded back to bf16: frag_scaled and frag_tr_scaled_k without the LDS read, so the read
+// can be issued early.
+PGN_DEVICE bf16x8 scale_frag(bf16x8 f, float s) {
+  return pack(to_f32x4(__builtin_shufflevector(f, f, 0, 1, 2, 3)) * s,
+              to_f32x4(__builtin_shufflevector(f, f, 4, 5, 6, 7)) * s);
+}
+
+PGN_DEVICE bf16x8 scale_frag_k(bf16x8 f, f32x4 sa, f32x4 sb) {
+  return pack(to_f32x4(__builtin_shufflevector(f, f, 0, 1, 2, 3)) * sa,
+              to_f32x4(__builtin_shufflevector(f, f, 4, 5, 6, 7)) * sb);
+}
+
 // Store an accumulator tile transposed into an LDS tile: rows 4g..4g+3 of column i land contiguously in row
 // (col0 + i) of `tile`, columns row0 + 4g .. +3 (one 8-byte write).
 PGN_DEVICE void store_T(__bf16* tile, int col0, int row0, int g, int i, f32x4 x) {
