@@ -353,66 +353,102 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             __builtin_amdgcn_make_buffer_rsrc(dk + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
         const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
         const bf16x8 vf0 = frag(Vs, me, 0, g), vf1 = frag(Vs, me, 1, g);
-        const float Ls_s = Ls[me];
-        float colacc = 0.f;
+        const float Ls_s = Ls[me], w_s = ws[me];
+        // The chunk's work as a sequence of steps: the P / dA blocks tb = WL..3, the four dV^T tiles, the four dK^T
+        // tiles. Each step's LDS operands are read one step ahead (behind a scheduling barrier), so the reads
+        // overlap the MFMAs instead of each MFMA waiting on a read issued just before it.
+        constexpr int NA = 4 - WL, NS = NA + 8;
+        StepFrags fr[NS];
+        auto issue = [&](auto s_c) {
+          constexpr int s = decltype(s_c)::value;
+          if constexpr (s < NA) {
+            constexpr int tb = WL + s;
+            fr[s].a = frag(Qs, 16 * tb + i, 0, g);
+            fr[s].b = frag(Qs, 16 * tb + i, 1, g);
+            fr[s].c = frag(Os, 16 * tb + i, 0, g);
+            fr[s].d = frag(Os, 16 * tb + i, 1, g);
+            fr[s].L = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+          } else if constexpr (s < NA + 4) {
+            constexpr int jt = s - NA;
+            if constexpr (WL < 2) fr[s].a = frag_tr(Os, 16 * jt, 0, g, i);
+            fr[s].b = frag_tr(Os, 16 * jt, 1, g, i);
+            fr[s].c = frag(dST, 16 * jt + i, 0, g);
+            fr[s].d = frag(dST, 16 * jt + i, 1, g);
+          } else {
+            constexpr int dt = s - NA - 4;
+            if constexpr (WL < 2) fr[s].a = frag_tr(Qs, 16 * dt, 0, g, i);
+            fr[s].b = frag_tr(Qs, 16 * dt, 1, g, i);
+            fr[s].c = frag_tr(dST, 16 * dt, 0, g, i);
+            fr[s].d = frag_tr(dST, 16 * dt, 1, g, i);
+            fr[s].e = *reinterpret_cast<const bf16x4*>(Ks + me * kPitch + 16 * dt + 4 * g);
+          }
+        };
+        issue(std::integral_constant<int, 0>{});
+        float colacc = 0.f, dw = 0.f;
         f32x4 At[4], dPt[4];
-  #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-          At[tb] = zero4();
-          dPt[tb] = zero4();
-          if (tb >= WL) {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) At[tb] = dPt[tb] = zero4();
+        bf16x8 A0, A1, dP0, dP1, kw0, kw1;
+        static_for<0, NS>([&](auto s_c) {
+          constexpr int s = decltype(s_c)::value;
+          if constexpr (s + 1 < NS) issue(std::integral_constant<int, s + 1>{});
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (s < NA) {
+            // (Q K^T) and dA = dO V^T blocks (t block tb, s block WL), decayed: A, dP, column sums of dA o A
+            constexpr int tb = WL + s;
             f32x4 P = zero4(), dA = zero4();
-            P = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, P);
-            P = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, P);
-            dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), vf0, dA);
-            dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), vf1, dA);
-            const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
-  #pragma unroll
+            P = pgn_mfma(fr[s].a, kf0, P);
+            P = pgn_mfma(fr[s].b, kf1, P);
+            dA = pgn_mfma(fr[s].c, vf0, dA);
+            dA = pgn_mfma(fr[s].d, vf1, dA);
+#pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int t = 16 * tb + 4 * g + r;
-              const float dec = (t >= me) ? __expf(fminf(Ltv[r] - Ls_s, 0.f)) : 0.f;
+              const float dec = (t >= me) ? __expf(fminf(fr[s].L[r] - Ls_s, 0.f)) : 0.f;
               At[tb][r] = P[r] * dec;
               dPt[tb][r] = dA[r] * dec;
               colacc += dA[r] * At[tb][r];
             }
+            if constexpr (s == NA - 1) {
+              colacc = sum_groups(colacc);
+              if (g == 0) colM[me] = colacc;
+              A0 = pack(At[0], At[1]);
+              A1 = pack(At[2], At[3]);
+              dP0 = pack(dPt[0], dPt[1]);
+              dP1 = pack(dPt[2], dPt[3]);
+              kw0 = scale_frag(kf0, w_s);
+              kw1 = scale_frag(kf1, w_s);
+            }
+          } else if constexpr (s < NA + 4) {
+            // dV^T tile (j block jt, s block WL) = dO^T A + dS^T (K o w)^T
+            constexpr int jt = s - NA;
+            f32x4 acc = zero4();
+            if constexpr (WL < 2) acc = pgn_mfma(fr[s].a, A0, acc);
+            acc = pgn_mfma(fr[s].b, A1, acc);
+            acc = pgn_mfma(fr[s].c, kw0, acc);
+            acc = pgn_mfma(fr[s].d, kw1, acc);
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dv_out,
+                                                  (me * DK + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+          } else {
+            // dK^T tile (d block dt, s block WL) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
+            constexpr int dt = s - NA - 4;
+            f32x4 acc = zero4(), Y = zero4();
+            if constexpr (WL < 2) acc = pgn_mfma(fr[s].a, dP0, acc);
+            acc = pgn_mfma(fr[s].b, dP1, acc);
+            Y = pgn_mfma(fr[s].c, vf0, Y);
+            Y = pgn_mfma(fr[s].d, vf1, Y);
+            const f32x4 kk = to_f32x4(fr[s].e);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
+            acc = acc + Y * w_s;
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dk_out,
+                                                  (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+            if constexpr (s == NS - 1) {
+              dw = sum_groups(dw);
+              if (g == 0) dwv[me] = dw;
+            }
           }
-        }
-        colacc = sum_groups(colacc);
-        if (g == 0) colM[me] = colacc;
-        const bf16x8 A0 = pack(At[0], At[1]), A1 = pack(At[2], At[3]);
-        const bf16x8 dP0 = pack(dPt[0], dPt[1]), dP1 = pack(dPt[2], dPt[3]);
-        const float w_s = ws[me];
-        // dV^T tiles (j block jt, s block WL) = dO^T A + dS^T (K o w)^T
-        const bf16x8 kw0 = frag_scaled(Ks, me, 0, g, w_s), kw1 = frag_scaled(Ks, me, 1, g, w_s);
-  #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-          f32x4 acc = zero4();
-          if (WL < 2) acc = pgn_mfma(frag_tr(Os, 16 * jt, 0, g, i), A0, acc);
-          acc = pgn_mfma(frag_tr(Os, 16 * jt, 1, g, i), A1, acc);
-          acc = pgn_mfma(frag(dST, 16 * jt + i, 0, g), kw0, acc);
-          acc = pgn_mfma(frag(dST, 16 * jt + i, 1, g), kw1, acc);
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dv_out,
-                                                (me * DK + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
-        }
-        // dK^T tiles (d block dt, s block WL) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
-        const __bf16* krow = Ks + me * kPitch;
-        float dw = 0.f;
-  #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          f32x4 acc = zero4(), Y = zero4();
-          if (WL < 2) acc = pgn_mfma(frag_tr(Qs, 16 * dt, 0, g, i), dP0, acc);
-          acc = pgn_mfma(frag_tr(Qs, 16 * dt, 1, g, i), dP1, acc);
-          Y = pgn_mfma(frag_tr(dST, 16 * dt, 0, g, i), vf0, Y);
-          Y = pgn_mfma(frag_tr(dST, 16 * dt, 1, g, i), vf1, Y);
-          const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
-  #pragma unroll
-          for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
-          acc = acc + Y * w_s;
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dk_out,
-                                                (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
-        }
-        dw = sum_groups(dw);
-        if (g == 0) dwv[me] = dw;
+        });
         if (WL >= 2 && cc > 0) {
           stage(h ^ 1);
           if (cc > 1) load(cc - 2);
@@ -486,68 +522,114 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             dq + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
         const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
         const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
-        const float Lt = Ls[me];
-        float rowacc = 0.f;
+        const float Lt = Ls[me], eLt = eLs[me], LC = Ls[C - 1];
+        // (Q o eL)^T operand of the dS update: read raw with the last dQ step's operands, scaled after that step
+        bf16x8 qt0, qt1;
+        f32x4 e00, e01, e10, e11;
+        // The chunk's work as a sequence of steps: the P^T / dA^T blocks sb = 0..WL, the four dQ^T tiles, the four
+        // column blocks of the dS update (with <S_c, dS> on the way). Each step's LDS operands are read one step
+        // ahead (behind a scheduling barrier), so the reads overlap the MFMAs.
+        constexpr int NA = WL + 1, NS = NA + 8;
+        StepFrags fr[NS];
+        auto issue = [&](auto s_c) {
+          constexpr int s = decltype(s_c)::value;
+          if constexpr (s < NA) {
+            constexpr int sb = s;
+            fr[s].a = frag(Ks, 16 * sb + i, 0, g);
+            fr[s].b = frag(Ks, 16 * sb + i, 1, g);
+            fr[s].c = frag(Vs, 16 * sb + i, 0, g);
+            fr[s].d = frag(Vs, 16 * sb + i, 1, g);
+            fr[s].L = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+          } else if constexpr (s < NA + 4) {
+            constexpr int dt = s - NA;
+            fr[s].a = frag_tr(Ks, 16 * dt, 0, g, i);
+            if constexpr (WL >= 2) fr[s].b = frag_tr(Ks, 16 * dt, 1, g, i);
+            fr[s].c = frag(Ss, 16 * dt + i, 0, g);
+            fr[s].d = frag(Ss, 16 * dt + i, 1, g);
+            fr[s].e = *reinterpret_cast<const bf16x4*>(Qs + me * kPitch + 16 * dt + 4 * g);
+            if constexpr (dt == 3) {
+              qt0 = frag_tr(Qs, 16 * WL, 0, g, i);
+              qt1 = frag_tr(Qs, 16 * WL, 1, g, i);
+              e00 = *reinterpret_cast<const f32x4*>(eLs + 4 * g);
+              e01 = *reinterpret_cast<const f32x4*>(eLs + 16 + 4 * g);
+              e10 = *reinterpret_cast<const f32x4*>(eLs + 32 + 4 * g);
+              e11 = *reinterpret_cast<const f32x4*>(eLs + 48 + 4 * g);
+            }
+          } else {
+            constexpr int jt = s - NA - 4;
+            fr[s].a = frag_tr(Os, 16 * jt, 0, g, i);
+            fr[s].b = frag_tr(Os, 16 * jt, 1, g, i);
+            // S_c[16 WL + 4g + r][16 jt + i], r = 0..3: the transpose read of Ss at rows 16 WL.., columns 16 jt..
+            fr[s].e = ds_read_tr(Ss + (16 * WL + 4 * g + (i >> 2)) * kPitch + 16 * jt + 4 * (i & 3));
+          }
+        };
+        issue(std::integral_constant<int, 0>{});
+        float rowacc = 0.f, qzt = 0.f, sd = 0.f, a_c = 0.f;
         f32x4 dPT[4];
-  #pragma unroll
-        for (int sb = 0; sb < 4; ++sb) {
-          dPT[sb] = zero4();
-          if (sb <= WL) {
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) dPT[sb] = zero4();
+        bf16x8 b0, b1, qe0, qe1;
+        __bf16* dSTn = dSTb + (h ^ 1) * TILE;
+        static_for<0, NS>([&](auto s_c) {
+          constexpr int s = decltype(s_c)::value;
+          if constexpr (s + 1 < NS) issue(std::integral_constant<int, s + 1>{});
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (s < NA) {
+            // (K Q^T) and dA^T = V dO^T blocks (s block sb, t block WL), decayed: dP^T, row sums of dA o A
+            constexpr int sb = s;
             f32x4 PT = zero4(), dAT = zero4();
-            PT = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, PT);
-            PT = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, PT);
-            dAT = pgn_mfma(frag(Vs, 16 * sb + i, 0, g), of0, dAT);
-            dAT = pgn_mfma(frag(Vs, 16 * sb + i, 1, g), of1, dAT);
-            const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-  #pragma unroll
+            PT = pgn_mfma(fr[s].a, qf0, PT);
+            PT = pgn_mfma(fr[s].b, qf1, PT);
+            dAT = pgn_mfma(fr[s].c, of0, dAT);
+            dAT = pgn_mfma(fr[s].d, of1, dAT);
+#pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int s = 16 * sb + 4 * g + r;
-              const float dec = (s <= me) ? __expf(fminf(Lt - Lsv[r], 0.f)) : 0.f;
+              const int sr = 16 * sb + 4 * g + r;
+              const float dec = (sr <= me) ? __expf(fminf(Lt - fr[s].L[r], 0.f)) : 0.f;
               rowacc += dAT[r] * (PT[r] * dec);
               dPT[sb][r] = dAT[r] * dec;
             }
+            if constexpr (s == NA - 1) {
+              rowacc = sum_groups(rowacc);
+              if (g == 0) rowM[me] = rowacc;
+              b0 = pack(dPT[0], dPT[1]);
+              b1 = pack(dPT[2], dPT[3]);
+            }
+          } else if constexpr (s < NA + 4) {
+            // dQ^T tile (d block dt, t block WL) = K^T dP^T + eL_t (S_c dO_t); q_t.(S_c dO_t) on the way
+            constexpr int dt = s - NA;
+            f32x4 acc = zero4(), Z = zero4();
+            acc = pgn_mfma(fr[s].a, b0, acc);
+            if constexpr (WL >= 2) acc = pgn_mfma(fr[s].b, b1, acc);
+            Z = pgn_mfma(fr[s].c, of0, Z);
+            Z = pgn_mfma(fr[s].d, of1, Z);
+            const f32x4 qq = to_f32x4(fr[s].e);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
+            acc = acc + Z * eLt;
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dq_out,
+                                                  (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+            if constexpr (s == NA + 3) {
+              qzt = sum_groups(qzt);
+              if (g == 0) qz[me] = qzt;
+              a_c = __expf(LC);
+              qe0 = scale_frag_k(qt0, e00, e01);
+              qe1 = scale_frag_k(qt1, e10, e11);
+            }
+          } else {
+            // columns 16 jt.. of rows 16 WL.. of dS: <S_c, dS> with the old values, then dS <- a dS + (Q o eL)^T dO
+            // into the other dS^T tile
+            constexpr int jt = s - NA - 4;
+            const f32x4 sv = to_f32x4(fr[s].e);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sd += sv[r] * dS[jt][r];
+            f32x4 m = pgn_mfma(qe0, fr[s].a, zero4());
+            m = pgn_mfma(qe1, fr[s].b, m);
+            dS[jt] = dS[jt] * a_c + m;
+            store_T(dSTn, 16 * jt, 16 * WL, g, i, dS[jt]);
+            if constexpr (s == NS - 1) sdot[WL * 64 + x.l] = sd;
           }
-        }
-        rowacc = sum_groups(rowacc);
-        if (g == 0) rowM[me] = rowacc;
-        const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
-        const float eLt = eLs[me];
-        const __bf16* qrow = Qs + me * kPitch;
-        float qzt = 0.f;
-  #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          f32x4 acc = zero4(), Z = zero4();
-          acc = pgn_mfma(frag_tr(Ks, 16 * dt, 0, g, i), b0, acc);
-          if (WL >= 2) acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), b1, acc);
-          Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
-          Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
-          const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
-  #pragma unroll
-          for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
-          acc = acc + Z * eLt;
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dq_out,
-                                                (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
-        }
-        qzt = sum_groups(qzt);
-        if (g == 0) qz[me] = qzt;
-        // <S_c, dS> over rows 16 WL.. of dS, then dS <- a dS + (Q o eL)^T dO on them, into the other dS^T tile
-        float sd = 0.f;
-  #pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-  #pragma unroll
-          for (int r = 0; r < 4; ++r) sd += (float)Ss[(16 * WL + 4 * g + r) * kPitch + 16 * jt + i] * dS[jt][r];
-        sdot[WL * 64 + x.l] = sd;
-        const float a_c = __expf(Ls[C - 1]);
-        const bf16x8 qe0 = frag_tr_scaled_k(Qs, 16 * WL, 0, g, i, eLs);
-        const bf16x8 qe1 = frag_tr_scaled_k(Qs, 16 * WL, 1, g, i, eLs);
-        __bf16* dSTn = dSTb + (h ^ 1) * TILE;
-  #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-          f32x4 m = pgn_mfma(qe0, frag_tr(Os, 16 * jt, 0, g, i), zero4());
-          m = pgn_mfma(qe1, frag_tr(Os, 16 * jt, 1, g, i), m);
-          dS[jt] = dS[jt] * a_c + m;
-          store_T(dSTn, 16 * jt, 16 * WL, g, i, dS[jt]);
-        }
+        });
         if (w == 0 && cc < NC - 1) {  // the later chunk's dla, from the other vector set (before the scan below)
           const int tn = t0 + C;
           plain_dla(vec + (h ^ 1) * kVec, x.l,

@@ -10,10 +10,13 @@
 // With it, an accumulator tile pair (rows 0..15 and 16..31 of a 32-row block) IS an operand whose contracted index
 // is the tiles' row index: pack(D_lo, D_hi). Operands read from LDS are two 8-byte loads per lane.
 //
-// LDS tiles are row-major bf16 with a pitch of kPitch = 68 elements (136 bytes, 34 banks): the 16 rows an
-// operand read touches start on 16 distinct even banks, and the transposed 4x4-block writes of the staging below
-// spread over all 64 banks, so both run at (or within one bank of) the 2-pass minimum of a 64-lane 8-byte access.
+// LDS tiles are row-major bf16 with a pitch of kPitch = 68 elements (136 bytes = 34 four-byte banks, 2 mod 32): the
+// 16 rows an operand read touches start on the 16 even banks of 32, so each lane group's 8-byte reads cover every
+// bank once and a 64-lane read runs at its 2-pass minimum (a pitch of 72 measured slower on every kernel). The
+// 16-byte row-segment staging writes spread evenly too (4 passes for 1 KB).
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace pgn {
@@ -42,6 +45,23 @@ PGN_DEVICE WaveIdx wave_idx() {
 }
 
 PGN_DEVICE f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// f(std::integral_constant<int, S>{}) for S = B .. E - 1 in order: a loop whose index is a compile-time constant in
+// the body, for step sequences whose steps differ in kind.
+template <int B, int E, class F>
+PGN_DEVICE void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Registers for one step's LDS operands in a software-pipelined step sequence (fields used as each step needs).
+struct StepFrags {
+  bf16x8 a, b, c, d;
+  f32x4 L;
+  bf16x4 e;
+};
 
 PGN_DEVICE bf16x8 cat8(bf16x4 a, bf16x4 b) { return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7); }
 
