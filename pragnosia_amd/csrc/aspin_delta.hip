@@ -74,11 +74,12 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
   const int l = threadIdx.x, g = l >> 4, i = l & 15;
   const int t0 = c * C, nr = min(C, T - t0);
   const __bf16* kc = k + ((size_t)bh * T + t0) * DK;
-  for (int e = l; e < C * 16; e += 64) {
-    const int r = e >> 4, q4 = (e & 15) * 4;
-    const bf16x4 x = r < nr ? *reinterpret_cast<const bf16x4*>(kc + (size_t)r * DK + q4) : zero_bf16x4();
-    *reinterpret_cast<bf16x4*>(Ks + r * kPitch + q4) = x;
-  }
+  // the chunk's keys: all eight 16-byte segments per lane issued before any is written (one memory round trip)
+  bf16x8 seg[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) seg[n] = load_seg(kc, nr, l + 64 * n);
+#pragma unroll
+  for (int n = 0; n < 8; ++n) put_seg(Ks, seg[n], l + 64 * n);
   const float lav = l < nr ? la[(size_t)bh * T + t0 + l] : 0.f;
   const float bev = l < nr ? be[(size_t)bh * T + t0 + l] : 0.f;
   Ls[l] = incl_scan64(lav, l);
@@ -277,194 +278,238 @@ __global__ __launch_bounds__(256) void aspin_delta_fwd(
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// backward, the sequential part: one workgroup of 4 waves per (batch, head), chunks in reverse
-__global__ __launch_bounds__(256) void aspin_delta_bwd_chain(
+// backward, the sequential part: one workgroup of 8 waves per (batch, head), chunks in reverse. Waves 0-3 carry the
+// chain, wave w owning value columns 16w..16w+15 with its columns of dS in fp32 registers; nothing on the chain is
+// shared between them. Waves 4-7 serve them: per chunk they compute the decayed scores A^T (the only operand the four
+// chain waves share), then stage the next chunk's tiles into the other half of a double-buffered LDS (loaded into
+// registers a chunk earlier still), run its decay scan, and reduce the previous chunk's value-column partial sums
+// into rsum. Two barriers per chunk: A^T ready (the chain waves do their dS-side and dS-free products before it), and
+// the end of the chunk. Operands contracted over a tile's row index use the LDS transpose read.
+constexpr int kChainStage = 6 * TILE;   // Q, K, V, dO, X, S_c
+constexpr int kChainVec = 4 * C + 8 * C;  // L, eL, w, beta; per-wave partial sums of drhs V and drhs U
+
+__global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const float* __restrict__ be, const __bf16* __restrict__ X,
     const __bf16* __restrict__ sent, const __bf16* __restrict__ dO, const float* __restrict__ dSfin,
     __bf16* __restrict__ dv, __bf16* __restrict__ drhs, __bf16* __restrict__ dSc, float* __restrict__ rsum,
     float* __restrict__ dS0, int T, int NC) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __bf16* Qs = reinterpret_cast<__bf16*>(smem);
-  __bf16* QT = Qs + TILE;
-  __bf16* Ks = QT + TILE;
-  __bf16* KT = Ks + TILE;
-  __bf16* VT = KT + TILE;
-  __bf16* OT = VT + TILE;  // dO^T (row j, column t)
-  __bf16* XT = OT + TILE;  // XT[t][s] = X[s][t]
-  __bf16* ST = XT + TILE;  // ST[j][d] = S_c[d][j]
-  __bf16* AT = ST + TILE;  // AT[t][s] = A[s][t]
-  float* Ls = reinterpret_cast<float*>(AT + TILE);
-  float* eLs = Ls + C;
-  float* ws = eLs + C;
-  float* bs = ws + C;
-  float* redV = bs + C;       // [4][C] per-wave partial sums of drhs V
-  float* redU = redV + 4 * C; // [4][C] per-wave partial sums of drhs U
+  __bf16* stg = reinterpret_cast<__bf16*>(smem);          // two sets of staged tiles, chunk c uses set c & 1
+  __bf16* AT = stg + 2 * kChainStage;                       // AT[t][s] = A[s][t]
+  float* vec = reinterpret_cast<float*>(AT + TILE);         // two vector sets, chunk c uses set c & 1
 
   const WaveIdx x = wave_idx();
   const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
   const int bh = blockIdx.x;
-  const int j = 16 * w + i;
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
 
-  f32x4 dS[4];
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) dS[db][r] = dSfin ? dSfin[soff + (size_t)(16 * db + 4 * g + r) * DK + j] : 0.f;
-
-  const int br = 4 * (tid >> 4), bc = 4 * (tid & 15);
-  Blk4 pq, pk, pv, po, px, ps;
-  float pla = 0.f, pbe = 0.f;
-  auto prefetch = [&](int cc) {
-    const int n0 = cc * C, nr = min(C, T - n0);
-    pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, tid);
-    pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, tid);
-    pv = load_blk(v + boff + (size_t)n0 * DK, DK, nr, tid);
-    po = load_blk(dO + boff + (size_t)n0 * DK, DK, nr, tid);
-    px = load_blk(X + ((size_t)bh * NC + cc) * C * C, C, C, tid);
-    ps = load_blk(sent + ((size_t)bh * NC + cc) * DK * DK, DK, DK, tid);
-    if (w == 0) {
-      const bool ok = n0 + x.l < T;
-      pla = ok ? la[(size_t)bh * T + n0 + x.l] : 0.f;
-      pbe = ok ? be[(size_t)bh * T + n0 + x.l] : 0.f;
-    }
-  };
-  prefetch(NC - 1);
-
-  for (int cc = NC - 1; cc >= 0; --cc) {
-    const int t0 = cc * C;
-    put_blk(Qs, pq, br, bc);
-    put_blk_T(QT, pq, br, bc);
-    put_blk(Ks, pk, br, bc);
-    put_blk_T(KT, pk, br, bc);
-    put_blk_T(VT, pv, br, bc);
-    put_blk_T(OT, po, br, bc);
-    put_blk_T(XT, px, br, bc);
-    put_blk_T(ST, ps, br, bc);
-    if (w == 0) {
-      chunk_decays(pla, x.l, Ls, eLs, ws);
-      bs[x.l] = pbe;
-    }
-    __syncthreads();
-    if (cc > 0) prefetch(cc - 1);
-
-    // scores, transposed, for token block w: AT[t][s] = (q_s . k_t) exp(L_s - L_t), s >= t
-    {
-      const int t = 16 * w + i;
-      const bf16x8 kf0 = frag(Ks, t, 0, g), kf1 = frag(Ks, t, 1, g);
-      const float Lt = Ls[t];
-      f32x4 a[4];
-#pragma unroll
-      for (int sb = 0; sb < 4; ++sb) {  // all score MFMAs first, then the decays
-        a[sb] = zero4();
-        if (sb >= w) {
-          a[sb] = pgn_mfma(frag(Qs, 16 * sb + i, 0, g), kf0, a[sb]);
-          a[sb] = pgn_mfma(frag(Qs, 16 * sb + i, 1, g), kf1, a[sb]);
-        }
-      }
-#pragma unroll
-      for (int sb = 0; sb < 4; ++sb) {
-        if (sb >= w) {
-          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) a[sb][r] *= masked_decay(Lsv[r] - Lt, 16 * sb + 4 * g + r >= t);
-        }
-        store_T(AT, 16 * w, 16 * sb, g, i, a[sb]);
-      }
-    }
-    // U = K S_c and (Q o eL)^T dO on this wave's columns: neither depends on dS
-    f32x4 U[4], Yc[4];
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      U[tb] = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), frag(ST, j, 0, g), zero4());
-      U[tb] = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), frag(ST, j, 1, g), U[tb]);
-    }
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      Yc[db] = pgn_mfma(frag_scaled_k(QT, 16 * db + i, 0, g, eLs), frag(OT, j, 0, g), zero4());
-      Yc[db] = pgn_mfma(frag_scaled_k(QT, 16 * db + i, 1, g, eLs), frag(OT, j, 1, g), Yc[db]);
-    }
-    // the gradient on the state leaving this chunk, for the chunk-local kernel
-    {
-      __bf16* dst = dSc + ((size_t)bh * NC + cc) * DK * DK;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * g + r) * DK + j] = (__bf16)dS[db][r];
-    }
-    __syncthreads();  // AT complete
-
-    // dW = A^T dO + w o (K dS)
-    const bf16x8 d01 = pack(dS[0], dS[1]), d23 = pack(dS[2], dS[3]);
-    f32x4 dW[4];
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      f32x4 y = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), d01, zero4());
-      y = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), d23, y);
-      f32x4 acc = zero4();
-      if (tb < 2) acc = pgn_mfma(frag(AT, 16 * tb + i, 0, g), frag(OT, j, 0, g), acc);
-      acc = pgn_mfma(frag(AT, 16 * tb + i, 1, g), frag(OT, j, 1, g), acc);
-      const f32x4 wv = *reinterpret_cast<const f32x4*>(ws + 16 * tb + 4 * g);
-      dW[tb] = acc + wv * y;
-    }
-    // drhs = X^T dW (X^T upper triangular)
-    const bf16x8 w01 = pack(dW[0], dW[1]), w23 = pack(dW[2], dW[3]);
-    f32x4 dR[4], dU[4];
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      f32x4 acc = zero4();
-      if (tb < 2) acc = pgn_mfma(frag(XT, 16 * tb + i, 0, g), w01, acc);
-      acc = pgn_mfma(frag(XT, 16 * tb + i, 1, g), w23, acc);
-      dR[tb] = acc;
-      const f32x4 bv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
-      const f32x4 ev = *reinterpret_cast<const f32x4*>(eLs + 16 * tb + 4 * g);
-      const f32x4 vv = to_f32x4(*reinterpret_cast<const bf16x4*>(VT + j * kPitch + 16 * tb + 4 * g));
-      float pv_[4], pu_[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = t0 + 16 * tb + 4 * g + r;
-        dU[tb][r] = -bv[r] * ev[r] * acc[r];
-        pv_[r] = sum16(acc[r] * vv[r]);
-        pu_[r] = sum16(acc[r] * U[tb][r]);
-        if (t < T) {
-          dv[boff + (size_t)t * DK + j] = (__bf16)(bv[r] * acc[r]);
-          drhs[boff + (size_t)t * DK + j] = (__bf16)acc[r];
-        }
-      }
-      if (i == 0) {
-        *reinterpret_cast<f32x4*>(redV + w * C + 16 * tb + 4 * g) = f32x4{pv_[0], pv_[1], pv_[2], pv_[3]};
-        *reinterpret_cast<f32x4*>(redU + w * C + 16 * tb + 4 * g) = f32x4{pu_[0], pu_[1], pu_[2], pu_[3]};
-      }
-    }
-    // dS_prev = a dS + (Q o eL)^T dO + K^T dU
-    const float a_c = __expf(Ls[C - 1]);
-    const bf16x8 u01 = pack(dU[0], dU[1]), u23 = pack(dU[2], dU[3]);
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      f32x4 acc = dS[db] * a_c + Yc[db];
-      acc = pgn_mfma(frag(KT, 16 * db + i, 0, g), u01, acc);
-      acc = pgn_mfma(frag(KT, 16 * db + i, 1, g), u23, acc);
-      dS[db] = acc;
-    }
-    __syncthreads();  // partial sums complete
-    if (w == 0) {
-      const int t = x.l;
-      const float pv_ = redV[t] + redV[C + t] + redV[2 * C + t] + redV[3 * C + t];
-      const float pu_ = redU[t] + redU[C + t] + redU[2 * C + t] + redU[3 * C + t];
-      if (t0 + t < T) {
-        rsum[((size_t)bh * T + t0 + t) * 2 + 0] = pv_ - eLs[t] * pu_;   // sum_j drhs (V - eL U)
-        rsum[((size_t)bh * T + t0 + t) * 2 + 1] = -bs[t] * pu_;         // d eL from the right-hand side
-      }
-    }
-    __syncthreads();
-  }
-  if (dS0) {
+  if (w < 4) {
+    // ================= chain waves: value columns j = 16w + i; dS rows 16 db + 4g + r
+    const int j = 16 * w + i;
+    f32x4 dS[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dS0[soff + (size_t)(16 * db + 4 * g + r) * DK + j] = dS[db][r];
+      for (int r = 0; r < 4; ++r) dS[db][r] = dSfin ? dSfin[soff + (size_t)(16 * db + 4 * g + r) * DK + j] : 0.f;
+    __syncthreads();
+    for (int cc = NC - 1; cc >= 0; --cc) {
+      const int t0 = cc * C, h = cc & 1;
+      const __bf16* Qs = stg + h * kChainStage;
+      const __bf16* Ks = Qs + TILE;
+      const __bf16* Vs = Qs + 2 * TILE;
+      const __bf16* Os = Qs + 3 * TILE;
+      const __bf16* Xs = Qs + 4 * TILE;
+      const __bf16* Ss = Qs + 5 * TILE;
+      float* vs = vec + h * kChainVec;
+      const float* Ls = vs;
+      const float* eLs = vs + C;
+      const float* ws = vs + 2 * C;
+      const float* bs = vs + 3 * C;
+      float* redV = vs + 4 * C;   // [4][C]
+      float* redU = vs + 8 * C;   // [4][C]
+      // the gradient on the state leaving this chunk, for the chunk-local kernel
+      {
+        __bf16* dst = dSc + ((size_t)bh * NC + cc) * DK * DK;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * g + r) * DK + j] = (__bf16)dS[db][r];
+      }
+      // products that do not need A^T: y = K dS, U = K S_c, Yc = (Q o eL)^T dO, on this wave's columns
+      const bf16x8 d01 = pack(dS[0], dS[1]), d23 = pack(dS[2], dS[3]);
+      const bf16x8 sc0 = frag_tr(Ss, 16 * w, 0, g, i), sc1 = frag_tr(Ss, 16 * w, 1, g, i);  // S_c[d][j]
+      const bf16x8 oc0 = frag_tr(Os, 16 * w, 0, g, i), oc1 = frag_tr(Os, 16 * w, 1, g, i);  // dO[t][j]
+      f32x4 y[4], U[4], Yc[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const bf16x8 k0 = frag(Ks, 16 * tb + i, 0, g), k1 = frag(Ks, 16 * tb + i, 1, g);
+        y[tb] = pgn_mfma(k0, d01, zero4());
+        y[tb] = pgn_mfma(k1, d23, y[tb]);
+        U[tb] = pgn_mfma(k0, sc0, zero4());
+        U[tb] = pgn_mfma(k1, sc1, U[tb]);
+      }
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        Yc[db] = pgn_mfma(frag_tr_scaled_k(Qs, 16 * db, 0, g, i, eLs), oc0, zero4());
+        Yc[db] = pgn_mfma(frag_tr_scaled_k(Qs, 16 * db, 1, g, i, eLs), oc1, Yc[db]);
+      }
+      __syncthreads();  // A^T complete
+
+      // dW = A^T dO + w o (K dS)
+      f32x4 dW[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        f32x4 acc = zero4();
+        if (tb < 2) acc = pgn_mfma(frag(AT, 16 * tb + i, 0, g), oc0, acc);
+        acc = pgn_mfma(frag(AT, 16 * tb + i, 1, g), oc1, acc);
+        const f32x4 wv = *reinterpret_cast<const f32x4*>(ws + 16 * tb + 4 * g);
+        dW[tb] = acc + wv * y[tb];
+      }
+      // drhs = X^T dW (X^T upper triangular); dV = beta drhs; dU = -beta eL drhs; per-row partial sums
+      const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
+      const __amdgpu_buffer_rsrc_t dv_out =
+          __builtin_amdgcn_make_buffer_rsrc(dv + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
+      const __amdgpu_buffer_rsrc_t dr_out =
+          __builtin_amdgcn_make_buffer_rsrc(drhs + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
+      const bf16x8 w01 = pack(dW[0], dW[1]), w23 = pack(dW[2], dW[3]);
+      f32x4 dU[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        f32x4 acc = zero4();
+        if (tb < 2) acc = pgn_mfma(frag_tr(Xs, 16 * tb, 0, g, i), w01, acc);
+        acc = pgn_mfma(frag_tr(Xs, 16 * tb, 1, g, i), w23, acc);
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
+        const f32x4 ev = *reinterpret_cast<const f32x4*>(eLs + 16 * tb + 4 * g);
+        const bf16x4 vv4 = ds_read_tr(Vs + (16 * tb + 4 * g + (i >> 2)) * kPitch + 16 * w + 4 * (i & 3));
+        const f32x4 vv = to_f32x4(vv4);  // V[16 tb + 4g + r][j]
+        float pv_[4], pu_[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tl = 16 * tb + 4 * g + r;
+          dU[tb][r] = -bv[r] * ev[r] * acc[r];
+          pv_[r] = row_total16(acc[r] * vv[r]);
+          pu_[r] = row_total16(acc[r] * U[tb][r]);
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (__bf16)(bv[r] * acc[r])), dv_out,
+                                                (tl * DK + j) * (int)sizeof(__bf16), 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (__bf16)acc[r]), dr_out,
+                                                (tl * DK + j) * (int)sizeof(__bf16), 0, 0);
+        }
+        if (i == 15) {
+          *reinterpret_cast<f32x4*>(redV + w * C + 16 * tb + 4 * g) = f32x4{pv_[0], pv_[1], pv_[2], pv_[3]};
+          *reinterpret_cast<f32x4*>(redU + w * C + 16 * tb + 4 * g) = f32x4{pu_[0], pu_[1], pu_[2], pu_[3]};
+        }
+      }
+      // dS_prev = a dS + (Q o eL)^T dO + K^T dU
+      const float a_c = __expf(Ls[C - 1]);
+      const bf16x8 u01 = pack(dU[0], dU[1]), u23 = pack(dU[2], dU[3]);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        f32x4 acc = dS[db] * a_c + Yc[db];
+        acc = pgn_mfma(frag_tr(Ks, 16 * db, 0, g, i), u01, acc);
+        acc = pgn_mfma(frag_tr(Ks, 16 * db, 1, g, i), u23, acc);
+        dS[db] = acc;
+      }
+      __syncthreads();  // end of the chunk
+    }
+    if (dS0) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dS0[soff + (size_t)(16 * db + 4 * g + r) * DK + j] = dS[db][r];
+    }
+  } else {
+    // ================= service waves: thread b carries 16-byte row segments b and b + 256 of each staged tile
+    const int a = w - 4;       // this wave's t block for the scores
+    const int b = tid & 255;
+    bf16x8 sg[6][2];
+    float pla = 0.f, pbe = 0.f;
+    auto load = [&](int cn) {
+      const int n0 = cn * C, nr = min(C, T - n0);
+      const __bf16* src[6] = {q + boff + (size_t)n0 * DK, k + boff + (size_t)n0 * DK, v + boff + (size_t)n0 * DK,
+                              dO + boff + (size_t)n0 * DK, X + ((size_t)bh * NC + cn) * C * C,
+                              sent + ((size_t)bh * NC + cn) * DK * DK};
+      const int rows[6] = {nr, nr, nr, nr, C, DK};
+#pragma unroll
+      for (int u = 0; u < 6; ++u) {
+        sg[u][0] = load_seg(src[u], rows[u], b);
+        sg[u][1] = load_seg(src[u], rows[u], b + 256);
+      }
+      if (a == 0) {
+        const bool ok = n0 + x.l < T;
+        pla = ok ? la[(size_t)bh * T + n0 + x.l] : 0.f;
+        pbe = ok ? be[(size_t)bh * T + n0 + x.l] : 0.f;
+      }
+    };
+    auto stage = [&](int hh) {
+      __bf16* base = stg + hh * kChainStage;
+#pragma unroll
+      for (int u = 0; u < 6; ++u) {
+        put_seg(base + u * TILE, sg[u][0], b);
+        put_seg(base + u * TILE, sg[u][1], b + 256);
+      }
+      if (a == 0) {
+        float* vs = vec + hh * kChainVec;
+        chunk_decays(pla, x.l, vs, vs + C, vs + 2 * C);
+        vs[3 * C + x.l] = pbe;
+      }
+    };
+    // rsum of a finished chunk from its vector set: sum_j drhs (V - eL U) and -beta sum_j drhs U
+    auto reduce = [&](int cn) {
+      const float* vs = vec + (cn & 1) * kChainVec;
+      const int t = x.l, n0 = cn * C;
+      const float* redV = vs + 4 * C;
+      const float* redU = vs + 8 * C;
+      const float pv_ = redV[t] + redV[C + t] + redV[2 * C + t] + redV[3 * C + t];
+      const float pu_ = redU[t] + redU[C + t] + redU[2 * C + t] + redU[3 * C + t];
+      if (n0 + t < T) {
+        rsum[((size_t)bh * T + n0 + t) * 2 + 0] = pv_ - vs[C + t] * pu_;
+        rsum[((size_t)bh * T + n0 + t) * 2 + 1] = -vs[3 * C + t] * pu_;
+      }
+    };
+    load(NC - 1);
+    stage((NC - 1) & 1);
+    if (NC > 1) load(NC - 2);
+    __syncthreads();
+    for (int cc = NC - 1; cc >= 0; --cc) {
+      const int h = cc & 1;
+      const __bf16* Qs = stg + h * kChainStage;
+      const __bf16* Ks = Qs + TILE;
+      const float* Ls = vec + h * kChainVec;
+      // scores, transposed, for token block a: AT[t][s] = (q_s . k_t) exp(L_s - L_t), s >= t
+      {
+        const int t = 16 * a + i;
+        const bf16x8 kf0 = frag(Ks, t, 0, g), kf1 = frag(Ks, t, 1, g);
+        const float Lt = Ls[t];
+        f32x4 sc[4];
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+          sc[sb] = zero4();
+          if (sb >= a) {
+            sc[sb] = pgn_mfma(frag(Qs, 16 * sb + i, 0, g), kf0, sc[sb]);
+            sc[sb] = pgn_mfma(frag(Qs, 16 * sb + i, 1, g), kf1, sc[sb]);
+          }
+        }
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+          if (sb >= a) {
+            const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[sb][r] *= masked_decay(Lsv[r] - Lt, 16 * sb + 4 * g + r >= t);
+          }
+          store_T(AT, 16 * a, 16 * sb, g, i, sc[sb]);
+        }
+      }
+      __syncthreads();  // A^T complete
+      if (a == 0 && cc < NC - 1) reduce(cc + 1);  // the later chunk's sums, before its vector set is reused below
+      if (cc > 0) {
+        stage(h ^ 1);
+        if (cc > 1) load(cc - 2);
+      }
+      __syncthreads();  // end of the chunk
+    }
+    if (a == 0) reduce(0);
   }
 }
 
@@ -708,7 +753,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
   }
 }
 
-constexpr size_t kChainSmem = 9 * TILE * sizeof(__bf16) + (4 * C + 8 * C) * sizeof(float);
+constexpr size_t kChainSmem = (2 * kChainStage + TILE) * sizeof(__bf16) + 2 * kChainVec * sizeof(float);
 constexpr size_t kLocalSmem = 9 * TILE * sizeof(__bf16) + (9 * C + 4) * sizeof(float);
 
 bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
@@ -779,7 +824,7 @@ extern "C" int pragnosia_aspin_delta_bwd(const void* q, const void* k, const voi
   __bf16* dsc = (__bf16*)(ws + ((B * H * T * DK * 2 + 255) / 256) * 256);
   float* rs = (float*)((unsigned char*)dsc + ((B * H * NC * DK * DK * 2 + 255) / 256) * 256);
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(aspin_delta_bwd_chain, dim3((unsigned)nbh), dim3(256), kChainSmem, st, (const __bf16*)q,
+  hipLaunchKernelGGL(aspin_delta_bwd_chain, dim3((unsigned)nbh), dim3(512), kChainSmem, st, (const __bf16*)q,
                      (const __bf16*)k, (const __bf16*)v, la, beta, (const __bf16*)X, (const __bf16*)sent,
                      (const __bf16*)dO, dS_final, (__bf16*)dv, drhs, dsc, rs, dS0, (int)T, NC);
   hipError_t e = hipGetLastError();

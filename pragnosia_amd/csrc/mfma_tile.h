@@ -265,6 +265,16 @@ PGN_DEVICE float lane_value(float x, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
 }
 
+// Sum over the 16 lanes of each row (lane group): an inclusive scan on DPP row shifts, so lane 15 of each row holds
+// the row's total (the other lanes hold partial sums).
+PGN_DEVICE float row_total16(float x) {
+  x += dpp_row0<0x111>(x);
+  x += dpp_row0<0x112>(x);
+  x += dpp_row0<0x114>(x);
+  x += dpp_row0<0x118>(x);
+  return x;
+}
+
 // Inclusive prefix sum over the 64 lanes of a wave (lane `l` = this lane's index): a Hillis-Steele scan inside each
 // row of 16 lanes on DPP row shifts (row_shr 1, 2, 4, 8), then each row adds the totals of the rows before it, read
 // from lanes 15, 31 and 47. Every step is a VALU or lane read: no LDS round trips.
