@@ -127,154 +127,194 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// forward: one workgroup of 4 waves per (batch, head); wave w owns value columns 16w..16w+15
-__global__ __launch_bounds__(256) void aspin_delta_fwd(
+// forward: one workgroup of 8 waves per (batch, head), chunks in order. Waves 0-3 carry the chain, wave w owning value
+// columns 16w..16w+15 with its columns of the fp32 state in registers (U -> rhs -> W -> S' never leaves them). Waves
+// 4-7 serve them: per chunk they compute the decayed scores A (the one operand the chain waves share), then stage the
+// next chunk's tiles into the other half of a double-buffered LDS and run its decay scan. Two barriers per chunk: A
+// ready (the chain waves form U, rhs and W before it), and the end of the chunk.
+constexpr int kFwdStage = 4 * TILE;    // Q, K, V, X
+constexpr int kFwdVec = 4 * C;         // L, eL, w, beta
+
+__global__ __launch_bounds__(512) void aspin_delta_fwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const float* __restrict__ be, const __bf16* __restrict__ X,
     const float* __restrict__ S0, __bf16* __restrict__ o, __bf16* __restrict__ Wout, float* __restrict__ Sfin,
     __bf16* __restrict__ sent, int T, int NC) {
-  __shared__ __align__(16) __bf16 Qs[TILE], Ks[TILE], KT[TILE], VT[TILE], Xs[TILE], As[TILE];
-  __shared__ __align__(16) float Ls[C], eLs[C], ws[C], bs[C];
+  extern __shared__ __align__(16) unsigned char smem[];
+  __bf16* stg = reinterpret_cast<__bf16*>(smem);          // two sets of staged tiles, chunk c uses set c & 1
+  __bf16* As = stg + 2 * kFwdStage;                        // As[t][s] = A[t][s]
+  float* vec = reinterpret_cast<float*>(As + TILE);        // two vector sets, chunk c uses set c & 1
 
   const WaveIdx x = wave_idx();
   const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
   const int bh = blockIdx.x;
-  const int j = 16 * w + i;  // this lane's value column
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
 
-  // state columns j, key rows 16 db + 4g + r
-  f32x4 S[4];
+  if (w < 4) {
+    // ================= chain waves: value columns j = 16w + i; state rows 16 db + 4g + r
+    const int j = 16 * w + i;
+    f32x4 S[4];
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) S[db][r] = S0 ? S0[soff + (size_t)(16 * db + 4 * g + r) * DK + j] : 0.f;
-
-  const int br = 4 * (tid >> 4), bc = 4 * (tid & 15);
-  Blk4 pq = load_blk(q + boff, DK, min(C, T), tid);
-  Blk4 pk = load_blk(k + boff, DK, min(C, T), tid);
-  Blk4 pv = load_blk(v + boff, DK, min(C, T), tid);
-  Blk4 px = load_blk(X + (size_t)bh * NC * C * C, C, C, tid);
-  float pla = 0.f, pbe = 0.f;
-  if (w == 0 && x.l < T) {
-    pla = la[(size_t)bh * T + x.l];
-    pbe = be[(size_t)bh * T + x.l];
-  }
-
-  for (int c = 0; c < NC; ++c) {
-    const int t0 = c * C;
-    put_blk(Qs, pq, br, bc);
-    put_blk(Ks, pk, br, bc);
-    put_blk_T(KT, pk, br, bc);
-    put_blk_T(VT, pv, br, bc);
-    put_blk(Xs, px, br, bc);
-    if (w == 0) {
-      chunk_decays(pla, x.l, Ls, eLs, ws);
-      bs[x.l] = pbe;
-    }
+      for (int r = 0; r < 4; ++r) S[db][r] = S0 ? S0[soff + (size_t)(16 * db + 4 * g + r) * DK + j] : 0.f;
     __syncthreads();
-    if (c + 1 < NC) {
-      const int n0 = t0 + C, nr = min(C, T - n0);
-      pq = load_blk(q + boff + (size_t)n0 * DK, DK, nr, tid);
-      pk = load_blk(k + boff + (size_t)n0 * DK, DK, nr, tid);
-      pv = load_blk(v + boff + (size_t)n0 * DK, DK, nr, tid);
-      px = load_blk(X + ((size_t)bh * NC + c + 1) * C * C, C, C, tid);
-      if (w == 0) {
+    for (int c = 0; c < NC; ++c) {
+      const int t0 = c * C, h = c & 1;
+      const __bf16* Qs = stg + h * kFwdStage;
+      const __bf16* Ks = Qs + TILE;
+      const __bf16* Vs = Qs + 2 * TILE;
+      const __bf16* Xs = Qs + 3 * TILE;
+      const float* vs = vec + h * kFwdVec;
+      const float* Ls = vs;
+      const float* eLs = vs + C;
+      const float* ws = vs + 2 * C;
+      const float* bs = vs + 3 * C;
+      const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
+      // the entering state, bf16 (d, j)
+      if (sent) {
+        __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[(16 * db + 4 * g + r) * DK + j] = (__bf16)S[db][r];
+      }
+      // U = K S (rows t, this wave's columns); rhs = beta (V - eL U)
+      const bf16x8 s01 = pack(S[0], S[1]), s23 = pack(S[2], S[3]);
+      f32x4 R[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        f32x4 u = zero4();
+        u = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), s01, u);
+        u = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), s23, u);
+        const f32x4 vv = to_f32x4(ds_read_tr(Vs + (16 * tb + 4 * g + (i >> 2)) * kPitch + 16 * w + 4 * (i & 3)));
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
+        const f32x4 ev = *reinterpret_cast<const f32x4*>(eLs + 16 * tb + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) R[tb][r] = bv[r] * (vv[r] - ev[r] * u[r]);
+      }
+      // W = X rhs (X lower triangular); rows past T fall outside the store's range and are dropped
+      const __amdgpu_buffer_rsrc_t w_out =
+          __builtin_amdgcn_make_buffer_rsrc(Wout + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
+      const bf16x8 r01 = pack(R[0], R[1]), r23 = pack(R[2], R[3]);
+      f32x4 Wt[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 0, g), r01, zero4());
+        if (tb >= 2) Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 1, g), r23, Wt[tb]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (__bf16)Wt[tb][r]), w_out,
+                                                ((16 * tb + 4 * g + r) * DK + j) * (int)sizeof(__bf16), 0, 0);
+      }
+      __syncthreads();  // A complete
+
+      // O^T tiles (value rows 16w + 4g + r, token lane 16 tb + i) = W^T A^T + S^T (Q o eL)^T
+      const __amdgpu_buffer_rsrc_t o_out =
+          __builtin_amdgcn_make_buffer_rsrc(o + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
+      const bf16x8 w01 = pack(Wt[0], Wt[1]), w23 = pack(Wt[2], Wt[3]);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int tl = 16 * tb + i;
+        const float eLt = eLs[tl];
+        f32x4 acc = pgn_mfma(w01, frag(As, tl, 0, g), zero4());
+        if (tb >= 2) acc = pgn_mfma(w23, frag(As, tl, 1, g), acc);
+        acc = pgn_mfma(s01, frag_scaled(Qs, tl, 0, g, eLt), acc);
+        acc = pgn_mfma(s23, frag_scaled(Qs, tl, 1, g, eLt), acc);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
+                                              (tl * DK + 16 * w + 4 * g) * (int)sizeof(__bf16), 0, 0);
+      }
+      // S <- a S + (K o w)^T W
+      const float a_c = __expf(Ls[C - 1]);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        S[db] = S[db] * a_c;
+        S[db] = pgn_mfma(frag_tr_scaled_k(Ks, 16 * db, 0, g, i, ws), w01, S[db]);
+        S[db] = pgn_mfma(frag_tr_scaled_k(Ks, 16 * db, 1, g, i, ws), w23, S[db]);
+      }
+      __syncthreads();  // end of the chunk
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Sfin[soff + (size_t)(16 * db + 4 * g + r) * DK + j] = S[db][r];
+  } else {
+    // ================= service waves: thread b carries 16-byte row segments b and b + 256 of each staged tile
+    const int a = w - 4;  // this wave's t block for the scores
+    const int b = tid & 255;
+    bf16x8 sg[4][2];
+    float pla = 0.f, pbe = 0.f;
+    auto load = [&](int cn) {
+      const int n0 = cn * C, nr = min(C, T - n0);
+      const __bf16* src[4] = {q + boff + (size_t)n0 * DK, k + boff + (size_t)n0 * DK, v + boff + (size_t)n0 * DK,
+                              X + ((size_t)bh * NC + cn) * C * C};
+      const int rows[4] = {nr, nr, nr, C};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        sg[u][0] = load_seg(src[u], rows[u], b);
+        sg[u][1] = load_seg(src[u], rows[u], b + 256);
+      }
+      if (a == 0) {
         const bool ok = n0 + x.l < T;
         pla = ok ? la[(size_t)bh * T + n0 + x.l] : 0.f;
         pbe = ok ? be[(size_t)bh * T + n0 + x.l] : 0.f;
       }
-    }
-
-    // decayed scores for token block w: A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, into As (row t)
-    {
-      const int t = 16 * w + i;
-      const bf16x8 qf0 = frag(Qs, t, 0, g), qf1 = frag(Qs, t, 1, g);
-      const float Lt = Ls[t];
-      f32x4 pt[4];
+    };
+    auto stage = [&](int hh) {
+      __bf16* base = stg + hh * kFwdStage;
 #pragma unroll
-      for (int sb = 0; sb < 4; ++sb) {  // all score MFMAs first, then the decays
-        pt[sb] = zero4();
-        if (sb <= w) {
-          pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
-          pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
-        }
+      for (int u = 0; u < 4; ++u) {
+        put_seg(base + u * TILE, sg[u][0], b);
+        put_seg(base + u * TILE, sg[u][1], b + 256);
       }
-#pragma unroll
-      for (int sb = 0; sb < 4; ++sb) {
-        if (sb <= w) {
-          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) pt[sb][r] *= masked_decay(Lt - Lsv[r], 16 * sb + 4 * g + r <= t);
-        }
-        store_T(As, 16 * w, 16 * sb, g, i, pt[sb]);
+      if (a == 0) {
+        float* vs = vec + hh * kFwdVec;
+        chunk_decays(pla, x.l, vs, vs + C, vs + 2 * C);
+        vs[3 * C + x.l] = pbe;
       }
-    }
-
-    // U = K S (rows t, this wave's columns); rhs = beta (V - eL U)
-    const bf16x8 s01 = pack(S[0], S[1]), s23 = pack(S[2], S[3]);
-    f32x4 R[4];
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      f32x4 u = zero4();
-      u = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), s01, u);
-      u = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), s23, u);
-      const f32x4 vv = to_f32x4(*reinterpret_cast<const bf16x4*>(VT + j * kPitch + 16 * tb + 4 * g));
-      const f32x4 bv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
-      const f32x4 ev = *reinterpret_cast<const f32x4*>(eLs + 16 * tb + 4 * g);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) R[tb][r] = bv[r] * (vv[r] - ev[r] * u[r]);
-    }
-    // W = X rhs (X lower triangular)
-    const bf16x8 r01 = pack(R[0], R[1]), r23 = pack(R[2], R[3]);
-    f32x4 Wt[4];
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 0, g), r01, zero4());
-      if (tb >= 2) Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 1, g), r23, Wt[tb]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = t0 + 16 * tb + 4 * g + r;
-        if (t < T) Wout[boff + (size_t)t * DK + j] = (__bf16)Wt[tb][r];
-      }
-    }
-    if (sent) {
-      __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sc[(16 * db + 4 * g + r) * DK + j] = (__bf16)S[db][r];
-    }
-    __syncthreads();  // As complete
-
-    // O^T tiles (value rows 16w + 4g + r, token lane 16 tb + i) = W^T A^T + S^T (Q o eL)^T
-    const bf16x8 w01 = pack(Wt[0], Wt[1]), w23 = pack(Wt[2], Wt[3]);
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      const int tl = 16 * tb + i;
-      const float eLt = eLs[tl];
-      f32x4 acc = pgn_mfma(w01, frag(As, tl, 0, g), zero4());
-      if (tb >= 2) acc = pgn_mfma(w23, frag(As, tl, 1, g), acc);
-      acc = pgn_mfma(s01, frag_scaled(Qs, tl, 0, g, eLt), acc);
-      acc = pgn_mfma(s23, frag_scaled(Qs, tl, 1, g, eLt), acc);
-      if (t0 + tl < T) *reinterpret_cast<bf16x4*>(o + boff + (size_t)(t0 + tl) * DK + 16 * w + 4 * g) = to_bf16x4(acc);
-    }
-
-    // S <- a S + (K o w)^T W
-    const float a_c = __expf(Ls[C - 1]);
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      S[db] = S[db] * a_c;
-      S[db] = pgn_mfma(frag_scaled_k(KT, 16 * db + i, 0, g, ws), w01, S[db]);
-      S[db] = pgn_mfma(frag_scaled_k(KT, 16 * db + i, 1, g, ws), w23, S[db]);
-    }
+    };
+    load(0);
+    stage(0);
+    if (NC > 1) load(1);
     __syncthreads();
+    for (int c = 0; c < NC; ++c) {
+      const int h = c & 1;
+      const __bf16* Qs = stg + h * kFwdStage;
+      const __bf16* Ks = Qs + TILE;
+      const float* Ls = vec + h * kFwdVec;
+      // decayed scores for token block a: A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, into As (row t)
+      {
+        const int t = 16 * a + i;
+        const bf16x8 qf0 = frag(Qs, t, 0, g), qf1 = frag(Qs, t, 1, g);
+        const float Lt = Ls[t];
+        f32x4 pt[4];
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+          pt[sb] = zero4();
+          if (sb <= a) {
+            pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
+            pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
+          }
+        }
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+          if (sb <= a) {
+            const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pt[sb][r] *= masked_decay(Lt - Lsv[r], 16 * sb + 4 * g + r <= t);
+          }
+          store_T(As, 16 * a, 16 * sb, g, i, pt[sb]);
+        }
+      }
+      __syncthreads();  // A complete
+      if (c + 1 < NC) {
+        stage(h ^ 1);
+        if (c + 2 < NC) load(c + 2);
+      }
+      __syncthreads();  // end of the chunk
+    }
   }
-
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Sfin[soff + (size_t)(16 * db + 4 * g + r) * DK + j] = S[db][r];
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -753,6 +793,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
   }
 }
 
+constexpr size_t kFwdSmem = (2 * kFwdStage + TILE) * sizeof(__bf16) + 2 * kFwdVec * sizeof(float);
 constexpr size_t kChainSmem = (2 * kChainStage + TILE) * sizeof(__bf16) + 2 * kChainVec * sizeof(float);
 constexpr size_t kLocalSmem = 9 * TILE * sizeof(__bf16) + (9 * C + 4) * sizeof(float);
 
@@ -795,7 +836,10 @@ extern "C" int pragnosia_aspin_delta_fwd(const void* q, const void* k, const voi
                      (__bf16*)X, (int)T, NC);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(aspin_delta_fwd, dim3((unsigned)nbh), dim3(256), 0, st, (const __bf16*)q, (const __bf16*)k,
+  static bool fwd_set = false;
+  int rc = set_smem((const void*)aspin_delta_fwd, kFwdSmem, fwd_set);
+  if (rc) return rc;
+  hipLaunchKernelGGL(aspin_delta_fwd, dim3((unsigned)nbh), dim3(512), kFwdSmem, st, (const __bf16*)q, (const __bf16*)k,
                      (const __bf16*)v, la, beta, (const __bf16*)X, S0, (__bf16*)o, (__bf16*)W, S_final,
                      (__bf16*)sent, (int)T, NC);
   PGN_RETURN_LAUNCH();
