@@ -8,10 +8,12 @@
 //     O   = ((Q K^T) o dec) W + (Q o eL) S,             S' = a S + (K o w)^T W
 //
 // Four kernels:
-//   aspin_delta_inv    one wave per (batch-head, chunk): N from a bf16 MFMA K K^T and fp32 decays, then X by exact
-//                      fp32 forward substitution, one column of X per lane (the reference sums 16 x 16 diagonal
-//                      blocks by doubling and substitutes across blocks, `src/assoc.py:168-204`; both are exact
-//                      in exact arithmetic, substitution is backward stable). X is stored bf16 for the products.
+//   aspin_delta_inv    one wave per (batch-head, chunk): N from a bf16 MFMA K K^T and fp32 decays, then X in fp32
+//                      by 16 x 16 blocks: the diagonal blocks by forward substitution (one column per lane), the
+//                      blocks below them by block forward substitution on fp32 MFMA (the reference sums the
+//                      diagonal blocks by doubling and substitutes across blocks, `src/assoc.py:168-204`; both are
+//                      exact in exact arithmetic). X is stored bf16 for the products; measured against an fp64
+//                      inverse it is as close as bf16 rounding of the exact inverse allows, repeated keys included.
 //   aspin_delta_fwd    one workgroup of 4 waves per (batch, head) walks the chunks. The rule is independent per
 //                      value column given X, so wave w owns value columns 16w..16w+15 for all 64 tokens and the
 //                      whole state chain (U -> rhs -> W -> S') stays in that wave's MFMA accumulators: each
@@ -68,6 +70,8 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
                                                       int NC) {
   __shared__ __align__(16) __bf16 Ks[TILE];
   __shared__ __align__(16) float NT[C * NP];  // NT[s][t] = N[t][s]
+  __shared__ __align__(16) float Xf[C * NP];  // X, fp32, blocks on and below the diagonal
+  __shared__ __align__(16) float Tt[3 * 16 * 17];  // per-level sums, one 16 x 16 block per product
   __shared__ __align__(16) float Ls[C], bs[C];
 
   const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;
@@ -106,24 +110,85 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
   }
   __syncthreads();
 
-  // column l of X: (I + N) x = e_l, right-looking forward substitution
-  float x[C];
+  // X by blocks of 16: X_ii = (I + N_ii)^-1 by forward substitution, one column of one diagonal block per lane; then
+  // X_ij = -X_ii sum_{k=j}^{i-1} N_ik X_kj, i > j, level by level (i - j = 1, 2, 3), on fp32 MFMA
+  // (v_mfma_f32_16x16x4f32: A[r][k] in lane r + 16k, B[k][c] in lane c + 16k, D[4g + e][c] in lane c + 16g).
+  {
+    const int b = l >> 4, cl = l & 15;
+    float xd[16];
 #pragma unroll
-  for (int t = 0; t < C; ++t) x[t] = (t == l) ? 1.f : 0.f;
+    for (int t = 0; t < 16; ++t) xd[t] = (t == cl) ? 1.f : 0.f;
 #pragma unroll
-  for (int s = 0; s < C - 1; ++s) {
-    const float xs = x[s];
+    for (int s = 0; s < 15; ++s) {
+      const float xs = xd[s];
+      const float* nrow = NT + (16 * b + s) * NP + 16 * b;  // N[16b + t][16b + s], t = 0..15
 #pragma unroll
-    for (int t4 = ((s + 1) >> 2) << 2; t4 < C; t4 += 4) {
-      const f32x4 n = *reinterpret_cast<const f32x4*>(NT + s * NP + t4);
+      for (int t4 = (s + 1) & ~3; t4 < 16; t4 += 4) {
+        const f32x4 n = *reinterpret_cast<const f32x4*>(nrow + t4);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (t4 + u > s) x[t4 + u] -= n[u] * xs;
+        for (int u = 0; u < 4; ++u)
+          if (t4 + u > s) xd[t4 + u] -= n[u] * xs;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 16; ++t) Xf[(16 * b + t) * NP + 16 * b + cl] = xd[t];
+  }
+  __syncthreads();
+  {
+    const int r16 = l & 15, k4 = l >> 4;
+    // one 16 x 16 x 16 product A B accumulated onto acc: A from rows ra.., columns ca.. of tile At (pitch NP), read
+    // transposed when `at` (At[c][r]); B from rows rb.., columns cb.. of tile Bt (pitch pb)
+    auto mm = [&](f32x4 acc, const float* At, bool at, int ra, int ca, const float* Bt, int pb, int rb, int cb) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const float av = at ? At[(ca + 4 * kk + k4) * NP + ra + r16] : At[(ra + r16) * NP + ca + 4 * kk + k4];
+        const float bv = Bt[(rb + 4 * kk + k4) * pb + cb + r16];
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+      }
+      return acc;
+    };
+#pragma unroll
+    for (int d = 1; d < 4; ++d) {
+      f32x4 Tacc[3];
+#pragma unroll
+      for (int jb = 0; jb + d < 4; ++jb) {
+        const int ib = jb + d;
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int kb = jb; kb < ib; ++kb) acc = mm(acc, NT, true, 16 * ib, 16 * kb, Xf, NP, 16 * kb, 16 * jb);
+        Tacc[jb] = acc;
+      }
+#pragma unroll
+      for (int jb = 0; jb + d < 4; ++jb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Tt[jb * 16 * 17 + (4 * k4 + e) * 17 + r16] = Tacc[jb][e];
+      __syncthreads();
+#pragma unroll
+      for (int jb = 0; jb + d < 4; ++jb) {
+        const int ib = jb + d;
+        const f32x4 xr = mm(zero4(), Xf, false, 16 * ib, 16 * ib, Tt + jb * 16 * 17, 17, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Xf[(16 * ib + 4 * k4 + e) * NP + 16 * jb + r16] = -xr[e];
+      }
+      __syncthreads();
     }
   }
+  // X (bf16, row-major; zero above the diagonal blocks) in 16-byte row segments
   __bf16* Xc = X + ((size_t)bh * NC + c) * C * C;
 #pragma unroll
-  for (int t = 0; t < C; ++t) Xc[t * C + l] = (__bf16)x[t];
+  for (int n = 0; n < 8; ++n) {
+    const int e = l + 64 * n, r = e >> 3, c0 = 8 * (e & 7);
+    bf16x8 out;
+    if ((c0 >> 4) <= (r >> 4)) {
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(Xf + r * NP + c0);
+      const f32x4 hi = *reinterpret_cast<const f32x4*>(Xf + r * NP + c0 + 4);
+      out = pack(lo, hi);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) out[u] = (__bf16)0.f;
+    }
+    *reinterpret_cast<bf16x8*>(Xc + r * C + c0) = out;
+  }
 }
 
 // ------------------------------------------------------------------------------------------------------------------
