@@ -629,10 +629,8 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
     float* __restrict__ dbe, int T, int NC) {
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* Qs = reinterpret_cast<__bf16*>(smem);
-  __bf16* QT = Qs + TILE;
-  __bf16* Ks = QT + TILE;
-  __bf16* KT = Ks + TILE;
-  __bf16* Ws = KT + TILE;
+  __bf16* Ks = Qs + TILE;
+  __bf16* Ws = Ks + TILE;
   __bf16* Os = Ws + TILE;   // dO
   __bf16* Ss = Os + TILE;   // S_c (d, j)
   __bf16* dSs = Ss + TILE;  // dS (d, j)
@@ -649,34 +647,21 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
 
   const WaveIdx x = wave_idx();
   const int w = x.w, wl = w & 3, g = x.g, i = x.i, tid = threadIdx.x;
-  const bool gk = w >= 4;
   const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;
   const int t0 = c * C, nr = min(C, T - t0);
   const size_t coff = ((size_t)bh * T + t0) * DK;
   const size_t soff = ((size_t)bh * NC + c) * DK * DK;
 
   {
-    const int b = tid & 255;
-    const int br = 4 * (b >> 4), bc = 4 * (b & 15);
-    if (tid < 256) {
-      const Blk4 a = load_blk(q + coff, DK, nr, b);
-      const Blk4 b2 = load_blk(Win + coff, DK, nr, b);
-      const Blk4 b3 = load_blk(sent + soff, DK, DK, b);
-      const Blk4 b4 = load_blk(drhs + coff, DK, nr, b);
-      put_blk(Qs, a, br, bc);
-      put_blk_T(QT, a, br, bc);
-      put_blk(Ws, b2, br, bc);
-      put_blk(Ss, b3, br, bc);
-      put_blk(Rs, b4, br, bc);
-    } else {
-      const Blk4 a = load_blk(k + coff, DK, nr, b);
-      const Blk4 b2 = load_blk(dO + coff, DK, nr, b);
-      const Blk4 b3 = load_blk(dSc + soff, DK, DK, b);
-      put_blk(Ks, a, br, bc);
-      put_blk_T(KT, a, br, bc);
-      put_blk(Os, b2, br, bc);
-      put_blk(dSs, b3, br, bc);
-    }
+    // every tile staged untransposed, thread tid carrying 16-byte row segment tid of each (operands contracted over
+    // a tile's row index use the LDS transpose read)
+    bf16x8 sg[7];
+    const __bf16* src[7] = {q + coff, k + coff, Win + coff, dO + coff, sent + soff, dSc + soff, drhs + coff};
+    const int rows[7] = {nr, nr, nr, nr, DK, DK, nr};
+#pragma unroll
+    for (int u = 0; u < 7; ++u) sg[u] = load_seg(src[u], rows[u], tid);
+#pragma unroll
+    for (int u = 0; u < 7; ++u) put_seg(Qs + u * TILE, sg[u], tid);
     if (w == 0) {
       const bool ok = x.l < nr;
       const float lav = ok ? la[(size_t)bh * T + t0 + x.l] : 0.f;
@@ -685,159 +670,182 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
     }
   }
   __syncthreads();
-  const int me = 16 * wl + i;
+  auto dpart = [&](auto wl_c) {
+    constexpr int WL = decltype(wl_c)::value;
+    const int me = 16 * WL + i;
+      // ---------------- token block WL in the query role: lane t = me
+      const float Lt = Ls[me], bt = bs[me];
+      const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
+      const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
+      const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
+      const bf16x8 rf0 = frag(Rs, me, 0, g), rf1 = frag(Rs, me, 1, g);
+      float rowacc = 0.f, db2 = 0.f;
+      f32x4 dPT[4];
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) {
+        dPT[sb] = zero4();
+        if (sb <= WL) {
+          // rows s, lane t: P[t][s], dA[t][s], KK[t][s], dN[t][s]
+          f32x4 P = zero4(), dA = zero4(), KK = zero4(), dN = zero4();
+          P = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, P);
+          P = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, P);
+          dA = pgn_mfma(frag(Ws, 16 * sb + i, 0, g), of0, dA);
+          dA = pgn_mfma(frag(Ws, 16 * sb + i, 1, g), of1, dA);
+          KK = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), kf0, KK);
+          KK = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), kf1, KK);
+          dN = pgn_mfma(frag(Ws, 16 * sb + i, 0, g), rf0, dN);
+          dN = pgn_mfma(frag(Ws, 16 * sb + i, 1, g), rf1, dN);
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int s = 16 * sb + 4 * g + r;
+            const float dec = masked_decay(Lt - Lsv[r], s <= me);
+            rowacc += dA[r] * P[r] * dec;
+            dPT[sb][r] = dA[r] * dec;
+            const float dnM = -dN[r] * KK[r] * dec * (s < me ? 1.f : 0.f);  // dN M, strictly lower
+            db2 += dnM;
+            rowacc += bt * dnM;
+          }
+        }
+      }
+      rowacc = sum_groups(rowacc);
+      db2 = sum_groups(db2);
+      const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
+      const float eLt = eLs[me];
+      const __bf16* qrow = Qs + me * kPitch;
+      // rows past the end of a partial chunk fall outside the store's range and are dropped
+      const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(dq + coff, (short)0, nr * DK * (int)sizeof(__bf16),
+                                                                         0x00020000);
+      float qzt = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        f32x4 acc = zero4(), Z = zero4();
+        acc = pgn_mfma(frag_tr(Ks, 16 * dt, 0, g, i), b0, acc);
+        if (WL >= 2) acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), b1, acc);
+        Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
+        Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
+        const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
+        acc = acc + Z * eLt;
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), out,
+                                            (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+      }
+      qzt = sum_groups(qzt);
+      if (g == 0) {
+        rowT[me] = rowacc + eLt * qzt;
+        dbe2[me] = db2;
+      }
 
-  if (!gk) {
-    // ---------------- token block wl in the query role: lane t = me
-    const float Lt = Ls[me], bt = bs[me];
-    const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
-    const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
-    const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
-    const bf16x8 rf0 = frag(Rs, me, 0, g), rf1 = frag(Rs, me, 1, g);
-    float rowacc = 0.f, db2 = 0.f;
-    f32x4 dPT[4];
+  };
+  auto kpart = [&](auto wl_c) {
+    constexpr int WL = decltype(wl_c)::value;
+    const int me = 16 * WL + i;
+      // ---------------- token block WL in the key role: lane s = me
+      const float Lsm = Ls[me], bsm = bs[me], wsm = ws[me], eLsm = eLs[me];
+      const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
+      const bf16x8 wf0 = frag(Ws, me, 0, g), wf1 = frag(Ws, me, 1, g);
+      const bf16x8 rf0 = frag(Rs, me, 0, g), rf1 = frag(Rs, me, 1, g);
+      float colacc = 0.f;
+      f32x4 dPt[4], Gt[4];
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      dPT[sb] = zero4();
-      if (sb <= wl) {
-        // rows s, lane t: P[t][s], dA[t][s], KK[t][s], dN[t][s]
-        f32x4 P = zero4(), dA = zero4(), KK = zero4(), dN = zero4();
-        P = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, P);
-        P = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, P);
-        dA = pgn_mfma(frag(Ws, 16 * sb + i, 0, g), of0, dA);
-        dA = pgn_mfma(frag(Ws, 16 * sb + i, 1, g), of1, dA);
-        KK = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), kf0, KK);
-        KK = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), kf1, KK);
-        dN = pgn_mfma(frag(Ws, 16 * sb + i, 0, g), rf0, dN);
-        dN = pgn_mfma(frag(Ws, 16 * sb + i, 1, g), rf1, dN);
-        const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+      for (int tb = 0; tb < 4; ++tb) {
+        dPt[tb] = zero4();
+        Gt[tb] = zero4();
+        if (tb >= WL) {
+          // rows t, lane s: P[t][s], dA[t][s], KK[t][s], dN[t][s]
+          f32x4 P = zero4(), dA = zero4(), KK = zero4(), dN = zero4();
+          P = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, P);
+          P = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, P);
+          dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), wf0, dA);
+          dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), wf1, dA);
+          KK = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), kf0, KK);
+          KK = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), kf1, KK);
+          dN = pgn_mfma(frag(Rs, 16 * tb + i, 0, g), wf0, dN);
+          dN = pgn_mfma(frag(Rs, 16 * tb + i, 1, g), wf1, dN);
+          const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+          const f32x4 btv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int s = 16 * sb + 4 * g + r;
-          const float dec = masked_decay(Lt - Lsv[r], s <= me);
-          rowacc += dA[r] * P[r] * dec;
-          dPT[sb][r] = dA[r] * dec;
-          const float dnM = -dN[r] * KK[r] * dec * (s < me ? 1.f : 0.f);  // dN M, strictly lower
-          db2 += dnM;
-          rowacc += bt * dnM;
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tb + 4 * g + r;
+            const float dec = masked_decay(Ltv[r] - Lsm, t >= me);
+            colacc += dA[r] * P[r] * dec;
+            dPt[tb][r] = dA[r] * dec;
+            const float dkk = -btv[r] * dN[r] * dec * (t > me ? 1.f : 0.f);  // dKK[t][s], strictly lower
+            colacc += dkk * KK[r];
+            Gt[tb][r] = dkk;
+          }
+        }
+        if (tb <= WL) {
+          // rows t, lane s: dN[s][t] = -sum_j W[t][j] drhs[s][j], for t < s
+          f32x4 dN = zero4();
+          dN = pgn_mfma(frag(Ws, 16 * tb + i, 0, g), rf0, dN);
+          dN = pgn_mfma(frag(Ws, 16 * tb + i, 1, g), rf1, dN);
+          const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tb + 4 * g + r;
+            Gt[tb][r] += -bsm * dN[r] * masked_decay(Lsm - Ltv[r], t < me);  // dKK[s][t]
+          }
         }
       }
-    }
-    rowacc = sum_groups(rowacc);
-    db2 = sum_groups(db2);
-    const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
-    const float eLt = eLs[me];
-    const __bf16* qrow = Qs + me * kPitch;
-    const bool t_ok = me < nr;
-    float qzt = 0.f;
+      colacc = sum_groups(colacc);
+      const bf16x8 p0 = pack(dPt[0], dPt[1]), p1 = pack(dPt[2], dPt[3]);
+      const bf16x8 g0 = pack(Gt[0], Gt[1]), g1 = pack(Gt[2], Gt[3]);
+      const float us = -bsm * eLsm;  // dU[s] = us * drhs[s]
+      const bf16x8 du0 = frag_scaled(Rs, me, 0, g, us), du1 = frag_scaled(Rs, me, 1, g, us);
+      const __bf16* krow = Ks + me * kPitch;
+      // rows past the end of a partial chunk fall outside the store's range and are dropped
+      const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(dk + coff, (short)0, nr * DK * (int)sizeof(__bf16),
+                                                                         0x00020000);
+      float dw = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      f32x4 acc = zero4(), Z = zero4();
-      acc = pgn_mfma(frag(KT, 16 * dt + i, 0, g), b0, acc);
-      if (wl >= 2) acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), b1, acc);
-      Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
-      Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
-      const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
+      for (int dt = 0; dt < 4; ++dt) {
+        f32x4 acc = zero4(), Y = zero4();
+        if (WL < 2) acc = pgn_mfma(frag_tr(Qs, 16 * dt, 0, g, i), p0, acc);
+        acc = pgn_mfma(frag_tr(Qs, 16 * dt, 1, g, i), p1, acc);
+        acc = pgn_mfma(frag_tr(Ks, 16 * dt, 0, g, i), g0, acc);
+        acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), g1, acc);
+        acc = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), du0, acc);
+        acc = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), du1, acc);
+        Y = pgn_mfma(frag(dSs, 16 * dt + i, 0, g), wf0, Y);
+        Y = pgn_mfma(frag(dSs, 16 * dt + i, 1, g), wf1, Y);
+        const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
-      acc = acc + Z * eLt;
-      if (t_ok) *reinterpret_cast<bf16x4*>(dq + coff + (size_t)me * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
-    }
-    qzt = sum_groups(qzt);
-    if (g == 0) {
-      rowT[me] = rowacc + eLt * qzt;
-      dbe2[me] = db2;
-    }
-  } else {
-    // ---------------- token block wl in the key role: lane s = me
-    const float Lsm = Ls[me], bsm = bs[me], wsm = ws[me], eLsm = eLs[me];
-    const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
-    const bf16x8 wf0 = frag(Ws, me, 0, g), wf1 = frag(Ws, me, 1, g);
-    const bf16x8 rf0 = frag(Rs, me, 0, g), rf1 = frag(Rs, me, 1, g);
-    float colacc = 0.f;
-    f32x4 dPt[4], Gt[4];
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      dPt[tb] = zero4();
-      Gt[tb] = zero4();
-      if (tb >= wl) {
-        // rows t, lane s: P[t][s], dA[t][s], KK[t][s], dN[t][s]
-        f32x4 P = zero4(), dA = zero4(), KK = zero4(), dN = zero4();
-        P = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, P);
-        P = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, P);
-        dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), wf0, dA);
-        dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), wf1, dA);
-        KK = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), kf0, KK);
-        KK = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), kf1, KK);
-        dN = pgn_mfma(frag(Rs, 16 * tb + i, 0, g), wf0, dN);
-        dN = pgn_mfma(frag(Rs, 16 * tb + i, 1, g), wf1, dN);
-        const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
-        const f32x4 btv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * tb + 4 * g + r;
-          const float dec = masked_decay(Ltv[r] - Lsm, t >= me);
-          colacc += dA[r] * P[r] * dec;
-          dPt[tb][r] = dA[r] * dec;
-          const float dkk = -btv[r] * dN[r] * dec * (t > me ? 1.f : 0.f);  // dKK[t][s], strictly lower
-          colacc += dkk * KK[r];
-          Gt[tb][r] = dkk;
-        }
+        for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
+        acc = acc + Y * wsm;
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), out,
+                                            (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
       }
-      if (tb <= wl) {
-        // rows t, lane s: dN[s][t] = -sum_j W[t][j] drhs[s][j], for t < s
-        f32x4 dN = zero4();
-        dN = pgn_mfma(frag(Ws, 16 * tb + i, 0, g), rf0, dN);
-        dN = pgn_mfma(frag(Ws, 16 * tb + i, 1, g), rf1, dN);
-        const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * tb + 4 * g + r;
-          Gt[tb][r] += -bsm * dN[r] * masked_decay(Lsm - Ltv[r], t < me);  // dKK[s][t]
-        }
+      dw = sum_groups(dw);
+      if (g == 0) {
+        colS[me] = colacc;
+        dwv[me] = dw;
       }
-    }
-    colacc = sum_groups(colacc);
-    const bf16x8 p0 = pack(dPt[0], dPt[1]), p1 = pack(dPt[2], dPt[3]);
-    const bf16x8 g0 = pack(Gt[0], Gt[1]), g1 = pack(Gt[2], Gt[3]);
-    const float us = -bsm * eLsm;  // dU[s] = us * drhs[s]
-    const bf16x8 du0 = frag_scaled(Rs, me, 0, g, us), du1 = frag_scaled(Rs, me, 1, g, us);
-    const __bf16* krow = Ks + me * kPitch;
-    const bool s_ok = me < nr;
-    float dw = 0.f;
+      // <S_c, dS> over key rows 16 WL ..
+      float sd = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      f32x4 acc = zero4(), Y = zero4();
-      if (wl < 2) acc = pgn_mfma(frag(QT, 16 * dt + i, 0, g), p0, acc);
-      acc = pgn_mfma(frag(QT, 16 * dt + i, 1, g), p1, acc);
-      acc = pgn_mfma(frag(KT, 16 * dt + i, 0, g), g0, acc);
-      acc = pgn_mfma(frag(KT, 16 * dt + i, 1, g), g1, acc);
-      acc = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), du0, acc);
-      acc = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), du1, acc);
-      Y = pgn_mfma(frag(dSs, 16 * dt + i, 0, g), wf0, Y);
-      Y = pgn_mfma(frag(dSs, 16 * dt + i, 1, g), wf1, Y);
-      const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
+      for (int jt = 0; jt < 4; ++jt) {
+        // S_c and dS at rows 16 WL + 4g + r, column 16 jt + i: transpose reads at rows 16 WL.., columns 16 jt..
+        const int off = (16 * WL + 4 * g + (i >> 2)) * kPitch + 16 * jt + 4 * (i & 3);
+        const f32x4 sv = to_f32x4(ds_read_tr(Ss + off)), dv_ = to_f32x4(ds_read_tr(dSs + off));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
-      acc = acc + Y * wsm;
-      if (s_ok) *reinterpret_cast<bf16x4*>(dk + coff + (size_t)me * DK + 16 * dt + 4 * g) = to_bf16x4(acc);
-    }
-    dw = sum_groups(dw);
-    if (g == 0) {
-      colS[me] = colacc;
-      dwv[me] = dw;
-    }
-    // <S_c, dS> over key rows 16 wl ..
-    float sd = 0.f;
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = 16 * wl + 4 * g + r;
-        sd += (float)Ss[d * kPitch + 16 * jt + i] * (float)dSs[d * kPitch + 16 * jt + i];
+        for (int r = 0; r < 4; ++r) sd += sv[r] * dv_[r];
       }
-    sd = wave_sum(sd);
-    if (x.l == 0) sdot[wl] = sd;
+      sd = wave_sum(sd);
+      if (x.l == 0) sdot[WL] = sd;
+  
+  };
+  // one instantiation per (role, block index): block conditions are compile-time constants
+  switch (w) {
+    case 0: dpart(std::integral_constant<int, 0>{}); break;
+    case 1: dpart(std::integral_constant<int, 1>{}); break;
+    case 2: dpart(std::integral_constant<int, 2>{}); break;
+    case 3: dpart(std::integral_constant<int, 3>{}); break;
+    case 4: kpart(std::integral_constant<int, 0>{}); break;
+    case 5: kpart(std::integral_constant<int, 1>{}); break;
+    case 6: kpart(std::integral_constant<int, 2>{}); break;
+    default: kpart(std::integral_constant<int, 3>{}); break;
   }
   __syncthreads();
   if (w == 0) {
@@ -860,7 +868,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
 
 constexpr size_t kFwdSmem = (2 * kFwdStage + TILE) * sizeof(__bf16) + 2 * kFwdVec * sizeof(float);
 constexpr size_t kChainSmem = (2 * kChainStage + TILE) * sizeof(__bf16) + 2 * kChainVec * sizeof(float);
-constexpr size_t kLocalSmem = 9 * TILE * sizeof(__bf16) + (9 * C + 4) * sizeof(float);
+constexpr size_t kLocalSmem = 7 * TILE * sizeof(__bf16) + (9 * C + 4) * sizeof(float);
 
 bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
   if (B <= 0 || H <= 0 || T <= 0) return false;
