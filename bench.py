@@ -339,6 +339,52 @@ def summarize(r, rule):
     return tokens, dom, achieved
 
 
+def lds_contraction_bench():
+    """LDS-resident contraction microbenchmark (csrc/microbench/contract.hip): bf16 MFMA throughput of the scan
+    kernels' operand patterns with every operand on chip, at 8 and 16 waves per CU. Bounds what the contraction phases
+    could reach with no HBM traffic and no chunk chain."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "pragnosia_amd",
+                                   "libpragnosia_microbench.so"))
+    fn = lib.pragnosia_microbench_contract
+    fn.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    stream = torch.cuda.current_stream()
+    iters, waves = 2000, 8
+    names = {0: "registers only", 1: "one LDS operand per MFMA", 2: "LDS operand + accumulator->operand chain"}
+    out = {}
+    for per_cu, nwg in ((8, 256), (16, 512)):
+        buf = torch.empty(nwg * 64 * waves, device="cuda")
+        for var in (0, 1, 2):
+            call = lambda: fn(var, waves, iters, nwg, ctypes.c_void_p(buf.data_ptr()),
+                              ctypes.c_void_p(stream.cuda_stream))
+            assert call() == 0
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(5):
+                call()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) / 5 * 1e-3
+            tfl = nwg * waves * iters * 16 * 16384 / t / 1e12
+            out[f"{names[var]}, {per_cu} waves/CU"] = {"tflops": round(tfl, 1), "frac": round(tfl / BF16_PEAK_TFLOPS, 4)}
+    return out
+
+
+def op_roofline(r):
+    """The whole fwd+bwd op against both rooflines, from the algorithmic bytes and flops over the two kernels' summed
+    durations: the HBM fraction, the bf16 MFMA fraction, and the larger of the two (the op's roofline position)."""
+    t = r["t_fwd"] + r["t_bwd"]
+    gbs = (r["fwd_bytes"] + r["bwd_bytes"]) / t / 1e9
+    tfl = (r["fwd_flops"] + r["bwd_flops"]) / t / 1e12
+    return {"hbm_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_tflops": round(tfl, 2),
+            "mfma_frac": round(tfl / BF16_PEAK_TFLOPS, 4),
+            "achieved_frac": round(max(gbs / HBM_PEAK_GBS, tfl / BF16_PEAK_TFLOPS), 4),
+            "ai_flop_per_byte": round((r["fwd_flops"] + r["bwd_flops"]) / (r["fwd_bytes"] + r["bwd_bytes"]), 1)}
+
+
 def gpu_bench(args):
     r = aspin_bench(args.rule, args.steps, args.warmup)
     tokens, dom, achieved = summarize(r, args.rule)
@@ -364,6 +410,7 @@ def gpu_bench(args):
                      "mfma_tflops": round(dom[3] / dom[1] / 1e12, 2),
                      "mfma_frac": round(dom[3] / dom[1] / 1e12 / BF16_PEAK_TFLOPS, 4)},
         "kernels_us": {r["names"][0]: round(r["t_fwd"] * 1e6, 2), r["names"][1]: round(r["t_bwd"] * 1e6, 2)},
+        "op": op_roofline(r),
     }
     if not args.no_secondary:
         other = "delta" if args.rule == "plain" else "plain"
@@ -375,10 +422,12 @@ def gpu_bench(args):
             "eager_ms_per_step": round(o["eager"] * 1e3, 5),
             "fwd_us": round(o["t_fwd"] * 1e6, 2), "bwd_us": round(o["t_bwd"] * 1e6, 2),
             "fwd_bwd_GBs": round((o["fwd_bytes"] + o["bwd_bytes"]) / (o["t_fwd"] + o["t_bwd"]) / 1e9, 1),
-            "fwd_bwd_mfma_tflops": round((o["fwd_flops"] + o["bwd_flops"]) / (o["t_fwd"] + o["t_bwd"]) / 1e12, 2)}}
+            "fwd_bwd_mfma_tflops": round((o["fwd_flops"] + o["bwd_flops"]) / (o["t_fwd"] + o["t_bwd"]) / 1e12, 2),
+            "op": op_roofline(o)}}
         sec["diag_scan"] = diag_bench(args.steps)
         sec["carried"] = carried_bench()
         sec["decode"] = decode_bench()
+        sec["lds_contraction"] = lds_contraction_bench()
         res["decode_ms_per_token_bs1"] = sec["decode"]["ms_per_token_bs1"]
         res["secondary"] = sec
     return res

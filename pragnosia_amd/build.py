@@ -16,6 +16,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libpragnosia_hip.so")
+# measurement-only kernels (bench.py), kept out of the product library
+MB_CSRC = os.path.join(CSRC, "microbench")
+MB_LIB = os.path.join(HERE, "libpragnosia_microbench.so")
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: packed fp32 forms are never generated (hipcc's host pass warns that the feature is unknown
@@ -31,12 +34,13 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP library cannot be built")
 
 
-def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+def sources(d: str = CSRC):
+    return sorted(os.path.join(d, f) for f in os.listdir(d) if f.endswith(".hip"))
 
 
 def _compile(src: str, verbose: bool) -> str:
-    obj = os.path.join(OBJ, os.path.basename(src)[:-4] + ".o")
+    sub = "mb_" if os.path.dirname(src) == MB_CSRC else ""
+    obj = os.path.join(OBJ, sub + os.path.basename(src)[:-4] + ".o")
     cmd = [hipcc(), *HIPFLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -48,19 +52,25 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compile every csrc/*.hip and link libpragnosia_hip.so. Always recompiles. Returns the library path."""
-    os.makedirs(OBJ, exist_ok=True)
-    srcs = sources()
-    jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
-    with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
-    tmp = LIB + ".tmp"
+def _link(objs, lib: str) -> None:
+    tmp = lib + ".tmp"
     cmd = [hipcc(), "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile every csrc/*.hip and link libpragnosia_hip.so, and csrc/microbench/*.hip into
+    libpragnosia_microbench.so (bench.py's measurement kernels). Always recompiles. Returns the library path."""
+    os.makedirs(OBJ, exist_ok=True)
+    srcs, mb = sources(), sources(MB_CSRC)
+    jobs = jobs or min(len(srcs) + len(mb), max(1, min(8, os.cpu_count() or 1)))
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), srcs + mb))
+    _link(objs[:len(srcs)], LIB)
+    _link(objs[len(srcs):], MB_LIB)
     return LIB
 
 
