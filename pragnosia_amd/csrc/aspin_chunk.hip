@@ -388,7 +388,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         f32x4 At[4], dPt[4];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) At[tb] = dPt[tb] = zero4();
-        bf16x8 A0, A1, dP0, dP1, kw0, kw1;
+        bf16x8 A0, A1, dP0, dP1;
         static_for<0, NS>([&](auto s_c) {
           constexpr int s = decltype(s_c)::value;
           if constexpr (s + 1 < NS) issue(std::integral_constant<int, s + 1>{});
@@ -404,7 +404,9 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int t = 16 * tb + 4 * g + r;
-              const float dec = (t >= me) ? __expf(fminf(fr[s].L[r] - Ls_s, 0.f)) : 0.f;
+              // below the diagonal block every t > s: no mask
+              const float e = __expf(fminf(fr[s].L[r] - Ls_s, 0.f));
+              const float dec = (tb > WL || t >= me) ? e : 0.f;
               At[tb][r] = P[r] * dec;
               dPt[tb][r] = dA[r] * dec;
               colacc += dA[r] * At[tb][r];
@@ -416,17 +418,16 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
               A1 = pack(At[2], At[3]);
               dP0 = pack(dPt[0], dPt[1]);
               dP1 = pack(dPt[2], dPt[3]);
-              kw0 = scale_frag(kf0, w_s);
-              kw1 = scale_frag(kf1, w_s);
             }
           } else if constexpr (s < NA + 4) {
-            // dV^T tile (j block jt, s block WL) = dO^T A + dS^T (K o w)^T
+            // dV^T tile (j block jt, s block WL) = dO^T A + w_s (dS^T K^T): the w_s scaling after the product
             constexpr int jt = s - NA;
-            f32x4 acc = zero4();
+            f32x4 acc = zero4(), acc2 = zero4();
             if constexpr (WL < 2) acc = pgn_mfma(fr[s].a, A0, acc);
             acc = pgn_mfma(fr[s].b, A1, acc);
-            acc = pgn_mfma(fr[s].c, kw0, acc);
-            acc = pgn_mfma(fr[s].d, kw1, acc);
+            acc2 = pgn_mfma(fr[s].c, kf0, acc2);
+            acc2 = pgn_mfma(fr[s].d, kf1, acc2);
+            acc = acc + acc2 * w_s;
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dv_out,
                                                   (me * DK + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
           } else {
@@ -585,7 +586,9 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int sr = 16 * sb + 4 * g + r;
-              const float dec = (sr <= me) ? __expf(fminf(Lt - fr[s].L[r], 0.f)) : 0.f;
+              // left of the diagonal block every s < t: no mask
+              const float e = __expf(fminf(Lt - fr[s].L[r], 0.f));
+              const float dec = (sb < WL || sr <= me) ? e : 0.f;
               rowacc += dAT[r] * (PT[r] * dec);
               dPT[sb][r] = dAT[r] * dec;
             }
