@@ -127,7 +127,10 @@ __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int s = 16 * sb + 4 * g + r;
-              pt[sb][r] = (s <= tq) ? pt[sb][r] * __expf(fminf(Lt - Lsv[sb][r], 0.f)) : 0.f;
+              if (sb < TB)  // left of the diagonal block every s < t, so the exponent is not positive: no mask
+                pt[sb][r] *= exp2_hw(Lt - Lsv[sb][r]);
+              else
+                pt[sb][r] = (s <= tq) ? pt[sb][r] * exp2_hw(fminf(Lt - Lsv[sb][r], 0.f)) : 0.f;
             }
           }
         }
@@ -152,7 +155,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(
         }
 
         // S <- a S + (K o w)^T V on rows 16 TB.. and this wave's columns; S^T of the next chunk into the other buffer
-        const float a_c = __expf(LC);
+        const float a_c = exp2_hw(LC);
         const bf16x8 kw0 = scale_frag_k(kt0, w00, w01);
         const bf16x8 kw1 = scale_frag_k(kt1, w10, w11);
 #pragma unroll
@@ -202,7 +205,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(
         const float L = wave_prefix_sum(pla, x.l);
         const float LC = lane_value(L, 63);
         float* vs = Vecb(h);
-        vs[x.l] = L;
+        vs[x.l] = L * kLog2e;
         vs[C + x.l] = __expf(L);
         vs[2 * C + x.l] = __expf(fminf(LC - L, 0.f));
       }
@@ -268,16 +271,17 @@ PGN_DEVICE void plain_dla(const float* vs, int lane, __amdgpu_buffer_rsrc_t out)
   float dL = rowM[t] - colM[t] + eLs[t] * qz[t] - wd;
   const float wdw = wave_sum(wd);
   const float sd = wave_sum((sdot[t] + sdot[C + t]) + (sdot[2 * C + t] + sdot[3 * C + t]));
-  if (t == C - 1) dL += wdw + __expf(Ls[C - 1]) * sd;
+  if (t == C - 1) dL += wdw + exp2_hw(Ls[C - 1]) * sd;
   dL = wave_suffix_sum(dL, t);
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, dL), out, 4 * t, 0, 0);
 }
 
-// L (inclusive cumulative sum of the chunk's la, lane = t), e^L and w = exp(L_C - L) into a vector set. One wave.
+// L (inclusive cumulative sum of the chunk's la, lane = t, stored in base 2: L log2 e), e^L and w = exp(L_C - L) into a
+// vector set. One wave.
 PGN_DEVICE void plain_scan(float la_t, int lane, float* vs) {
   const float L = wave_prefix_sum(la_t, lane);
   const float LC = lane_value(L, 63);
-  vs[lane] = L;
+  vs[lane] = L * kLog2e;
   vs[C + lane] = __expf(L);
   vs[2 * C + lane] = __expf(fminf(LC - L, 0.f));
 }
@@ -404,9 +408,9 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int t = 16 * tb + 4 * g + r;
-              // below the diagonal block every t > s: no mask
-              const float e = __expf(fminf(fr[s].L[r] - Ls_s, 0.f));
-              const float dec = (tb > WL || t >= me) ? e : 0.f;
+              // below the diagonal block every t > s, so the exponent is not positive: no clamp, no mask
+              const float dec = tb > WL ? exp2_hw(fr[s].L[r] - Ls_s)
+                                        : (t >= me ? exp2_hw(fminf(fr[s].L[r] - Ls_s, 0.f)) : 0.f);
               At[tb][r] = P[r] * dec;
               dPt[tb][r] = dA[r] * dec;
               colacc += dA[r] * At[tb][r];
@@ -586,9 +590,9 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int sr = 16 * sb + 4 * g + r;
-              // left of the diagonal block every s < t: no mask
-              const float e = __expf(fminf(Lt - fr[s].L[r], 0.f));
-              const float dec = (sb < WL || sr <= me) ? e : 0.f;
+              // left of the diagonal block every s < t, so the exponent is not positive: no clamp, no mask
+              const float dec = sb < WL ? exp2_hw(Lt - fr[s].L[r])
+                                        : (sr <= me ? exp2_hw(fminf(Lt - fr[s].L[r], 0.f)) : 0.f);
               rowacc += dAT[r] * (PT[r] * dec);
               dPT[sb][r] = dAT[r] * dec;
             }
@@ -615,7 +619,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             if constexpr (s == NA + 3) {
               qzt = sum_groups(qzt);
               if (g == 0) qz[me] = qzt;
-              a_c = __expf(LC);
+              a_c = exp2_hw(LC);
               qe0 = scale_frag_k(qt0, e00, e01);
               qe1 = scale_frag_k(qt1, e10, e11);
             }

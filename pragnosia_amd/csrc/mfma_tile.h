@@ -46,6 +46,10 @@ PGN_DEVICE WaveIdx wave_idx() {
 
 PGN_DEVICE f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// Decay exponents are kept in base 2 (L log2 e), so exp(L_t - L_s) is one hardware exp2 of a difference.
+constexpr float kLog2e = 1.4426950408889634f;
+PGN_DEVICE float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // f(std::integral_constant<int, S>{}) for S = B .. E - 1 in order: a loop whose index is a compile-time constant in
 // the body, for step sequences whose steps differ in kind.
 template <int B, int E, class F>
