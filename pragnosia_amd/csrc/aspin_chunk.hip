@@ -35,26 +35,32 @@ constexpr int C = 64;
 constexpr int DK = 64;
 constexpr int TILE = 64 * kPitch;  // one staged 64 x 64 tile
 
-// Forward: one workgroup of 12 waves per (batch, head), chunks in order. Waves 0-7 compute: wave w owns a t block tb
-// and value columns 32 jh .. 32 jh + 31 (jh = w >> 2), and holds rows 16 tb.. of the fp32 state for those columns as
-// accumulator tiles. Waves 8-11 load: while waves 0-7 compute chunk c from one half of a double-buffered
-// LDS, they stage chunk c + 1 (prefetched into registers during chunk c - 1) into the other half, run its decay scan,
-// issue chunk c + 2's loads and copy chunk c's entering state to `sent`. The state tile S^T the output needs is
-// double-buffered too, so one barrier per chunk orders everything.
-constexpr int kFwdWaves = 12;
+// Forward: one workgroup of 16 waves per (batch, head), chunks in order, one barrier per chunk, three roles:
+//   output waves (0-7): wave w owns a t block tb and value columns 32 jh .. 32 jh + 31 (jh = w >> 2) and holds its
+//       16 x 32 slice of the fp32 state as MFMA accumulators; per chunk c it forms O^T = V^T A^T + S^T (Q o eL)^T for
+//       its tokens and columns and the state update S <- a S + (K o w)^T V (an MFMA accumulating onto a S), writing
+//       the next chunk's S^T tile into the other half of a double-buffered tile;
+//   score waves (8-11): wave a computes the decayed scores A of chunk c + 1 for t block a, one chunk ahead, into the
+//       other half of a double-buffered A tile (so the output waves never compute them, and never twice);
+//   load waves (12-15): stage chunk c + 2 into a triple-buffered set of Q, K, V tiles (loaded into registers a chunk
+//       earlier still), run its decay scan, issue chunk c + 3's loads and copy chunk c's entering state to `sent`.
+// The t blocks of the two output-wave halves run in opposite orders, so each SIMD gets one early and one late block.
+constexpr int kFwdWaves = 16;
 constexpr int kFwdBuf = 3 * TILE * (int)sizeof(__bf16) + 3 * C * (int)sizeof(float);  // Q, K, V, L, eL, w
 
-__global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 3))) void aspin_plain_fwd(
+__global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const float* __restrict__ S0, __bf16* __restrict__ o, float* __restrict__ Sfin,
     __bf16* __restrict__ sent, int T, int NC) {
   extern __shared__ __align__(16) unsigned char smem[];
-  // buffer set h: Q, K, K^T, V^T tiles and the L, eL, w vectors; then S^T (j, d) for two chunks
+  // input set h (chunk c in set c % 3): Q, K, V tiles and the L (base 2), eL, w vectors; then A (t, s) and S^T (j, d)
+  // tiles for two chunks each (chunk c in c & 1)
   auto Qb = [&](int h) { return reinterpret_cast<__bf16*>(smem + h * kFwdBuf); };
   auto Kb = [&](int h) { return Qb(h) + TILE; };
   auto Vb = [&](int h) { return Qb(h) + 2 * TILE; };
   auto Vecb = [&](int h) { return reinterpret_cast<float*>(Qb(h) + 3 * TILE); };
-  auto STb = [&](int h) { return reinterpret_cast<__bf16*>(smem + 2 * kFwdBuf) + h * TILE; };
+  auto ATb = [&](int h) { return reinterpret_cast<__bf16*>(smem + 3 * kFwdBuf) + h * TILE; };
+  auto STb = [&](int h) { return reinterpret_cast<__bf16*>(smem + 3 * kFwdBuf) + (2 + h) * TILE; };
 
   const WaveIdx x = wave_idx();
   const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
@@ -62,10 +68,46 @@ __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
 
+  // decayed scores A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, of t block a of chunk `cn` (input set hs) into
+  // the A tile `At` (row t), zero above the diagonal block
+  auto scores = [&](auto a_c, int hs, __bf16* At) {
+    constexpr int a = decltype(a_c)::value;
+    const __bf16* Qs = Qb(hs);
+    const __bf16* Ks = Kb(hs);
+    const float* Ls = Vecb(hs);
+    const int tq = 16 * a + i;
+    const bf16x8 qf0 = frag(Qs, tq, 0, g), qf1 = frag(Qs, tq, 1, g);
+    bf16x8 kf[a + 1][2];
+    f32x4 Lsv[a + 1];
+#pragma unroll
+    for (int sb = 0; sb <= a; ++sb) {
+      kf[sb][0] = frag(Ks, 16 * sb + i, 0, g);
+      kf[sb][1] = frag(Ks, 16 * sb + i, 1, g);
+      Lsv[sb] = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+    }
+    const float Lt = Ls[tq];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      f32x4 pt = zero4();
+      if (sb <= a) {
+        pt = pgn_mfma(kf[sb][0], qf0, pt);
+        pt = pgn_mfma(kf[sb][1], qf1, pt);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int s = 16 * sb + 4 * g + r;
+          if (sb < a)  // left of the diagonal block every s < t, so the exponent is not positive: no mask
+            pt[r] *= exp2_hw(Lt - Lsv[sb][r]);
+          else
+            pt[r] = (s <= tq) ? pt[r] * exp2_hw(fminf(Lt - Lsv[sb][r], 0.f)) : 0.f;
+        }
+      }
+      store_T(At, 16 * a, 16 * sb, g, i, pt);
+    }
+  };
+
   if (w < 8) {
-    // ================= compute waves
-    // t block: waves w and w + 4 share a SIMD, so the second half takes the blocks in reverse order and each SIMD
-    // gets one heavy (late) and one light (early) t block
+    // ================= output waves
     const int tb = w < 4 ? w : 7 - w, j0 = 32 * (w >> 2);
     // state rows 16 tb + 4g + r, columns j0 + 16 jt + i
     f32x4 S[2];
@@ -76,31 +118,26 @@ __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(
       store_T(STb(0), j0 + 16 * jt, 16 * tb, g, i, S[jt]);
     }
     __syncthreads();
-    auto cloop = [&](auto tb_c) {
+    __syncthreads();
+    auto oloop = [&](auto tb_c) {
       constexpr int TB = decltype(tb_c)::value;
       const int tq = 16 * TB + i;  // this lane's token within the chunk for t-indexed operands
       for (int c = 0; c < NC; ++c) {
-        const int h = c & 1, t0 = c * C;
-        const __bf16* Qs = Qb(h);
-        const __bf16* Ks = Kb(h);
-        const __bf16* Vs = Vb(h);
-        const __bf16* ST = STb(h);
-        const float* Ls = Vecb(h);
+        const int h3 = c % 3, h2 = c & 1, t0 = c * C;
+        const __bf16* Qs = Qb(h3);
+        const __bf16* Ks = Kb(h3);
+        const __bf16* Vs = Vb(h3);
+        const __bf16* At = ATb(h2);
+        const __bf16* ST = STb(h2);
+        const float* Ls = Vecb(h3);
         const float* eLs = Ls + C;
         const float* ws = Ls + 2 * C;
-        // Every LDS operand of the chunk is read first, in the order it is consumed: the reads return in order while
-        // the MFMAs below run, instead of each MFMA waiting for a read issued just before it. The value operands serve
-        // both the output (as V^T) and the state update (as V).
+        // every LDS operand of the chunk first, in the order consumed; V serves both the output (as V^T) and the
+        // state update (as V)
+        const bf16x8 af0 = frag(At, tq, 0, g);
+        const bf16x8 af1 = TB >= 2 ? frag(At, tq, 1, g) : af0;
         const bf16x8 qf0 = frag(Qs, tq, 0, g), qf1 = frag(Qs, tq, 1, g);
-        bf16x8 kf[TB + 1][2];
-        f32x4 Lsv[TB + 1];
-#pragma unroll
-        for (int sb = 0; sb <= TB; ++sb) {
-          kf[sb][0] = frag(Ks, 16 * sb + i, 0, g);
-          kf[sb][1] = frag(Ks, 16 * sb + i, 1, g);
-          Lsv[sb] = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-        }
-        const float Lt = Ls[tq], eLt = eLs[tq], LC = Ls[C - 1];
+        const float eLt = eLs[tq], LC = Ls[C - 1];
         bf16x8 vf[2][2], sf[2][2];
 #pragma unroll
         for (int jt = 0; jt < 2; ++jt) {
@@ -115,30 +152,8 @@ __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(
         const f32x4 w10 = *reinterpret_cast<const f32x4*>(ws + 32 + 4 * g);
         const f32x4 w11 = *reinterpret_cast<const f32x4*>(ws + 48 + 4 * g);
         __builtin_amdgcn_sched_barrier(0);
-
-        // (Q K^T)^T tiles (s block sb, t block TB), decayed and masked: lane holds column t = tq, rows s.
-        f32x4 pt[4];
-#pragma unroll
-        for (int sb = 0; sb < 4; ++sb) {
-          pt[sb] = zero4();
-          if (sb <= TB) {
-            pt[sb] = pgn_mfma(kf[sb][0], qf0, pt[sb]);
-            pt[sb] = pgn_mfma(kf[sb][1], qf1, pt[sb]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int s = 16 * sb + 4 * g + r;
-              if (sb < TB)  // left of the diagonal block every s < t, so the exponent is not positive: no mask
-                pt[sb][r] *= exp2_hw(Lt - Lsv[sb][r]);
-              else
-                pt[sb][r] = (s <= tq) ? pt[sb][r] * exp2_hw(fminf(Lt - Lsv[sb][r], 0.f)) : 0.f;
-            }
-          }
-        }
-        const bf16x8 af0 = pack(pt[0], pt[1]);
-        const bf16x8 af1 = pack(pt[2], pt[3]);
         const bf16x8 qe0 = scale_frag(qf0, eLt);
         const bf16x8 qe1 = scale_frag(qf1, eLt);
-
         // O^T tiles (value block jt, t block TB) = V^T A^T + S^T (Q o eL)^T; lane holds token tq, 4 value columns.
         // Rows past T fall outside the store's range and are dropped.
         const __amdgpu_buffer_rsrc_t o_out = __builtin_amdgcn_make_buffer_rsrc(
@@ -153,8 +168,15 @@ __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
                                                 (tq * DK + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
         }
-
-        // S <- a S + (K o w)^T V on rows 16 TB.. and this wave's columns; S^T of the next chunk into the other buffer
+        // the entering state, bf16 (d, j), from this wave's state slice
+        if (sent) {
+          __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
+#pragma unroll
+          for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[(16 * TB + 4 * g + r) * DK + j0 + 16 * jt + i] = (__bf16)S[jt][r];
+        }
+        // S <- a S + (K o w)^T V on rows 16 TB.. and this wave's columns; S^T of the next chunk into the other tile
         const float a_c = exp2_hw(LC);
         const bf16x8 kw0 = scale_frag_k(kt0, w00, w01);
         const bf16x8 kw1 = scale_frag_k(kt1, w10, w11);
@@ -163,81 +185,105 @@ __global__ __launch_bounds__(kFwdWaves * 64) __attribute__((amdgpu_waves_per_eu(
           S[jt] = S[jt] * a_c;
           S[jt] = pgn_mfma(kw0, vf[jt][0], S[jt]);
           S[jt] = pgn_mfma(kw1, vf[jt][1], S[jt]);
-          store_T(STb(h ^ 1), j0 + 16 * jt, 16 * TB, g, i, S[jt]);
+          store_T(STb(h2 ^ 1), j0 + 16 * jt, 16 * TB, g, i, S[jt]);
         }
         __syncthreads();
       }
     };
     switch (tb) {  // one instantiation per t block: its block conditions are compile-time constants
-      case 0: cloop(std::integral_constant<int, 0>{}); break;
-      case 1: cloop(std::integral_constant<int, 1>{}); break;
-      case 2: cloop(std::integral_constant<int, 2>{}); break;
-      default: cloop(std::integral_constant<int, 3>{}); break;
+      case 0: oloop(std::integral_constant<int, 0>{}); break;
+      case 1: oloop(std::integral_constant<int, 1>{}); break;
+      case 2: oloop(std::integral_constant<int, 2>{}); break;
+      default: oloop(std::integral_constant<int, 3>{}); break;
     }
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) Sfin[soff + (16 * tb + 4 * g + r) * DK + j0 + 16 * jt + i] = S[jt][r];
-  } else {
-    // ================= load waves: thread b carries 16-byte row segments b and b + 256 of each of Q, K and V
-    const int b = tid & 255;
-    const bool w0 = w == 8;  // runs the decay scans
-    bf16x8 sq0, sq1, sk0, sk1, sv0, sv1;
-    float pla = 0.f;
-    auto load = [&](int cn) {
-      const int n0 = cn * C, nr = min(C, T - n0);
-      sq0 = load_seg(q + boff + (size_t)n0 * DK, nr, b);
-      sq1 = load_seg(q + boff + (size_t)n0 * DK, nr, b + 256);
-      sk0 = load_seg(k + boff + (size_t)n0 * DK, nr, b);
-      sk1 = load_seg(k + boff + (size_t)n0 * DK, nr, b + 256);
-      sv0 = load_seg(v + boff + (size_t)n0 * DK, nr, b);
-      sv1 = load_seg(v + boff + (size_t)n0 * DK, nr, b + 256);
-      if (w0) pla = (n0 + x.l < T) ? la[(size_t)bh * T + n0 + x.l] : 0.f;
+  } else if (w < 12) {
+    // ================= score waves: t block a, one chunk ahead. Wave 8 also runs the decay scans, two chunks ahead
+    // (the load waves stage the same chunk's tiles in the same phase): L (base 2), e^L and w = exp(L_C - L).
+    const bool scan = w == 8;
+    auto la_of = [&](int cn) { return (cn < NC && cn * C + x.l < T) ? la[(size_t)bh * T + cn * C + x.l] : 0.f; };
+    auto run_scan = [&](float la_t, int h) {
+      const float L = wave_prefix_sum(la_t, x.l);
+      const float LC = lane_value(L, 63);
+      float* vs = Vecb(h);
+      vs[x.l] = L * kLog2e;
+      vs[C + x.l] = __expf(L);
+      vs[2 * C + x.l] = __expf(fminf(LC - L, 0.f));
     };
-    auto stage = [&](int h) {
-      put_seg(Qb(h), sq0, b);
-      put_seg(Qb(h), sq1, b + 256);
-      put_seg(Kb(h), sk0, b);
-      put_seg(Kb(h), sk1, b + 256);
-      put_seg(Vb(h), sv0, b);
-      put_seg(Vb(h), sv1, b + 256);
-      if (w0) {
-        const float L = wave_prefix_sum(pla, x.l);
-        const float LC = lane_value(L, 63);
-        float* vs = Vecb(h);
-        vs[x.l] = L * kLog2e;
-        vs[C + x.l] = __expf(L);
-        vs[2 * C + x.l] = __expf(fminf(LC - L, 0.f));
-      }
-    };
-    load(0);
-    stage(0);
-    if (NC > 1) load(1);
-    __syncthreads();
-    for (int c = 0; c < NC; ++c) {
-      const int h = c & 1;
-      if (c + 1 < NC) {
-        stage(h ^ 1);
-        if (c + 2 < NC) load(c + 2);
-      }
-      if (sent) {  // chunk c's entering state, bf16 (d, j): a 4x4 block of S^T read and transposed per thread
-        const __bf16* ST = STb(h);
-        const int br = 4 * (b >> 4), bc = 4 * (b & 15);
-        Blk4 st;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) st.r[jj] = *reinterpret_cast<const bf16x4*>(ST + (br + jj) * kPitch + bc);
-        __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
-#pragma unroll
-        for (int dd = 0; dd < 4; ++dd) {
-          bf16x4 row;
-          row[0] = st.r[0][dd];
-          row[1] = st.r[1][dd];
-          row[2] = st.r[2][dd];
-          row[3] = st.r[3][dd];
-          *reinterpret_cast<bf16x4*>(sc + (bc + dd) * DK + br) = row;
-        }
+    auto sloop = [&](auto a_c) {
+      float pla = 0.f;
+      if (scan) {
+        run_scan(la_of(0), 0);
+        if (NC > 1) run_scan(la_of(1), 1);
+        pla = la_of(2);
       }
       __syncthreads();
+      scores(a_c, 0, ATb(0));
+      __syncthreads();
+      for (int c = 0; c < NC; ++c) {
+        if (c + 1 < NC) scores(a_c, (c + 1) % 3, ATb((c + 1) & 1));
+        if (scan && c + 2 < NC) {
+          run_scan(pla, (c + 2) % 3);
+          pla = la_of(c + 3);
+        }
+        __syncthreads();
+      }
+    };
+    switch (w - 8) {
+      case 0: sloop(std::integral_constant<int, 0>{}); break;
+      case 1: sloop(std::integral_constant<int, 1>{}); break;
+      case 2: sloop(std::integral_constant<int, 2>{}); break;
+      default: sloop(std::integral_constant<int, 3>{}); break;
+    }
+  } else {
+    // ================= load waves: thread b carries 16-byte row segments b and b + 256 of each of Q, K and V.
+    // Two register sets alternate, so a chunk's loads are issued two chunks before it is staged.
+    const int b = tid & 255;
+    struct Regs {
+      bf16x8 q0, q1, k0, k1, v0, v1;
+    };
+    Regs ra, rb;
+    auto load = [&](Regs& r, int cn) {
+      const int n0 = cn * C, nr = min(C, T - n0);
+      r.q0 = load_seg(q + boff + (size_t)n0 * DK, nr, b);
+      r.q1 = load_seg(q + boff + (size_t)n0 * DK, nr, b + 256);
+      r.k0 = load_seg(k + boff + (size_t)n0 * DK, nr, b);
+      r.k1 = load_seg(k + boff + (size_t)n0 * DK, nr, b + 256);
+      r.v0 = load_seg(v + boff + (size_t)n0 * DK, nr, b);
+      r.v1 = load_seg(v + boff + (size_t)n0 * DK, nr, b + 256);
+    };
+    auto stage = [&](const Regs& r, int h) {
+      put_seg(Qb(h), r.q0, b);
+      put_seg(Qb(h), r.q1, b + 256);
+      put_seg(Kb(h), r.k0, b);
+      put_seg(Kb(h), r.k1, b + 256);
+      put_seg(Vb(h), r.v0, b);
+      put_seg(Vb(h), r.v1, b + 256);
+    };
+    load(ra, 0);
+    stage(ra, 0);
+    if (NC > 1) {
+      load(rb, 1);
+      stage(rb, 1);
+      if (NC > 2) load(ra, 2);
+      if (NC > 3) load(rb, 3);
+    }
+    __syncthreads();
+    __syncthreads();
+    // chunk c: stage chunk c + 2 from the set loaded two chunks ago, then reload that set with chunk c + 4
+    auto phase = [&](Regs& r, int c) {
+      if (c + 2 < NC) {
+        stage(r, (c + 2) % 3);
+        if (c + 4 < NC) load(r, c + 4);
+      }
+      __syncthreads();
+    };
+    for (int c = 0; c < NC; c += 2) {
+      phase(ra, c);
+      if (c + 1 < NC) phase(rb, c + 1);
     }
   }
 }
@@ -668,7 +714,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   }
 }
 
-constexpr size_t kFwdSmem = 2 * (size_t)kFwdBuf + 2 * TILE * sizeof(__bf16);
+constexpr size_t kFwdSmem = 3 * (size_t)kFwdBuf + 4 * TILE * sizeof(__bf16);
 constexpr size_t kBwdSmem = (2 * kBwdStage + 2 * TILE) * sizeof(__bf16) + 2 * kVec * sizeof(float);
 
 bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
