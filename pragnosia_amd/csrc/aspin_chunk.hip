@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 
   if (w < 8) {
     // ================= output waves
-    const int tb = w < 4 ? w : 7 - w, j0 = 32 * (w >> 2);
+    const int tb = w < 4 ? 3 - w : w - 4, j0 = 32 * (w >> 2);
     // state rows 16 tb + 4g + r, columns j0 + 16 jt + i
     f32x4 S[2];
 #pragma unroll
