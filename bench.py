@@ -225,9 +225,11 @@ def diag_bench(steps):
 
 def carried_bench():
     """B2 T8192 H12 D64 bf16 inputs, la = logsigmoid(N(4,1)); (i) 16 windows of 512 with the
-    fp32 state carried and rebased by -512 theta between windows (positions restart per window, as
-    AssocCarrier.forward does), (ii) one unsplit T = 8192 pass. Forward only. Reports the carried path's
-    whole-sequence throughput and the carried-vs-unsplit error on every output and on the final state."""
+    fp32 state carried and rebased by -512 theta between windows (positions restart per window, as successive
+    AssocCarrier.forward calls do), in one segment-parallel pass (aspin_chunk_windows); (ii) one unsplit T = 8192
+    pass (aspin_chunk, which takes the segment-parallel forward for these few heads). Forward only; device time per
+    call from graph replays. Also the window-by-window loop (16 x (rebase + aspin_chunk)) the carried path replaces,
+    and the carried-vs-unsplit error on the outputs and on the final state."""
     import torch
     import torch.nn.functional as F
     from pragnosia_amd import ops  # noqa: F401
@@ -248,7 +250,7 @@ def carried_bench():
     vb = v.bfloat16()
     op = torch.ops.pragnosia
 
-    def carried():
+    def loop():
         S, outs = None, []
         for s in range(0, T, W):
             if S is not None:
@@ -258,21 +260,26 @@ def carried_bench():
             outs.append(o)
         return torch.cat(outs, 2), S
 
+    carried = lambda: op.aspin_chunk_windows(qw, kw, vb, la, None, th, W, False)
+    unsplit = lambda: op.aspin_chunk(qg, kg, vb, la, None, False)
+    stream = torch.cuda.current_stream()
     with torch.no_grad():
-        for _ in range(3):
-            carried()
-        torch.cuda.synchronize()
-        n = 20
-        t0 = time.perf_counter()
-        for _ in range(n):
-            oc, Sc = carried()
-        torch.cuda.synchronize()
-        t_c = (time.perf_counter() - t0) / n
-        ou, Su, _ = op.aspin_chunk(qg, kg, vb, la, None, False)
+        t_c, t_u, t_l = _time_ops([carried, unsplit, loop], 10, stream)
+        oc, Sc, _ = carried()
+        ol, Sl = loop()
+        ou, Su, _ = unsplit()
         Su_loc = op.aspin_rebase(Su, th, None, float(T - W))
     rel = lambda a, b: ((a.float() - b.float()).abs().max() / b.float().abs().max()).item()
+    P = ops.seg_chunks(B * H, T // 64, [p for p in range(1, W // 64 + 1) if (W // 64) % p == 0])
+    Pu = ops.seg_chunks(B * H, T // 64, range(1, T // 64 + 1))
     return {"workload": "aspin carried long context, 16 windows x 512 vs one T8192 pass, B2 H12 D64 (configs[3])",
-            "carried_Mtok_s": round(B * T / t_c / 1e6, 3), "carried_ms": round(t_c * 1e3, 4),
+            "carried_Mtok_s": round(B * T / t_c / 1e6, 3), "carried_us": round(t_c * 1e6, 2),
+            "carried_segment_chunks": P,
+            "unsplit_Mtok_s": round(B * T / t_u / 1e6, 3), "unsplit_us": round(t_u * 1e6, 2),
+            "unsplit_segment_chunks": Pu,
+            "window_loop_Mtok_s": round(B * T / t_l / 1e6, 3), "window_loop_us": round(t_l * 1e6, 2),
+            "carried_vs_window_loop_rel_err_o": round(rel(oc, ol), 6),
+            "carried_vs_window_loop_rel_err_S": round(rel(Sc, Sl), 6),
             "carried_vs_unsplit_rel_err_o": round(rel(oc, ou), 6),
             "carried_vs_unsplit_rel_err_S": round(rel(Sc, Su_loc), 6)}
 

@@ -70,6 +70,27 @@ int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const void* v, const
                               void* dq, void* dk, void* dv, float* dla, float* dS0,
                               int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
 
+/* Bytes of device workspace pragnosia_aspin_chunk_fwd_seg needs (-1 if the shape is rejected). */
+int64_t pragnosia_aspin_chunk_fwd_seg_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk,
+                                                      int64_t seg_chunks);
+
+/* The forward of pragnosia_aspin_chunk_fwd, segment-parallel: every head's chunks are split into segments of
+ * `seg_chunks` chunks that run concurrently once their entering states are known (per-segment state sums, a prefix
+ * over segments, then the chunked forward per segment), for few heads over long sequences. Same inputs and
+ * outputs as pragnosia_aspin_chunk_fwd (sent may be NULL).
+ * window = 0: one continuous sequence, the same function as pragnosia_aspin_chunk_fwd.
+ * window > 0 (a multiple of 64 and of 64 * seg_chunks): the sequence is a run of windows of `window` tokens whose
+ * q and k were rotated with positions restarting at 0 in every window; between windows the carried state's key
+ * rows (2i, 2i + 1) are rotated by -window * theta[h, i] (theta: (H, D / 2) fp32). This is what successive calls of
+ * the reference's carrier over consecutive windows compute, each rebasing the state it is handed
+ * (`AssocCarrier.forward`, src/assoc.py:391-405, driven by `LM.forward_carried`, src/model.py:842-864); S_final is
+ * the state after the last window, in that window's positions. S0 is the state entering the first window.
+ * `workspace`: caller-allocated device memory of at least pragnosia_aspin_chunk_fwd_seg_workspace_bytes(...) bytes. */
+int pragnosia_aspin_chunk_fwd_seg(const void* q, const void* k, const void* v, const float* la, const float* S0,
+                                  const float* theta, int64_t window, void* o, float* S_final, void* sent,
+                                  void* workspace, int64_t workspace_bytes, int64_t B, int64_t H, int64_t T,
+                                  int64_t D, int64_t chunk, int64_t seg_chunks, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Associative carrier, DELTA write rule, chunked scan (chunk = 64, head dim D = 64), per (batch, head):
  *     S_t = a_t S_{t-1} + beta_t k_t (v_t - (a_t S_{t-1})^T k_t)^T,   o_t = S_t^T q_t,   a_t = exp(la_t).

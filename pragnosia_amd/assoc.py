@@ -234,6 +234,47 @@ class AssocCarrier(nn.Module):
         # the state is now expressed in this call's positions 0..T-1: the next call rebases it by T
         return out, (S, p0 * 0 + T if torch.is_tensor(p0) else T)
 
+    def forward_windows(self, x, window: int, h0=None, pos0: int = 0):
+        """Consecutive windows of `window` tokens of x (B, T, d), the state carried from each window into the next:
+        the same function as calling `forward` on x[:, s:s + window] for s = 0, window, ... in turn, handing each
+        call the state the previous one returned (`src/model.py:842-864` drives the reference's carrier so). A
+        plain-rule carrier without autograd, with `window` a multiple of 64, runs every window in one pass (the
+        projections over the whole sequence, one segment-parallel scan that rebases the state at window
+        boundaries); otherwise the windows run one call each. Returns (x + gated output, (S, length of the last
+        window)); `sent` is not kept."""
+        B, T, D = x.shape
+        fused = (not self.delta and window % 64 == 0 and T > window and x.is_cuda and self.dk == HEAD_DIM_KERNEL
+                 and not _needs_grad(x, *(h0[:1] if h0 is not None else ()), *self.parameters()))
+        if not fused:
+            outs, st = [], h0
+            for s in range(0, T, window):
+                o, st = self.forward(x[:, s:s + window], st, pos0)
+                outs.append(o)
+            return torch.cat(outs, 1), st
+        if h0 is None:
+            S0, p0 = None, pos0
+        elif len(h0) == 3:
+            raise PragnosiaError("AssocCarrier: a short-convolution cache in the state is not supported")
+        else:
+            S0, p0 = h0
+        z = self.ln(x)
+        qp, kp, vp, gate, la, _ = self._projections(z)
+        p_dev = p0.float().reshape(()) if torch.is_tensor(p0) else None
+        p_host = 0.0 if torch.is_tensor(p0) else float(p0)
+        if S0 is not None and (p_dev is not None or p_host != 0.0):
+            S0 = _op.aspin_rebase(S0, self.theta, p_dev, p_host)
+        pos = _positions(T, x.device, window)
+        wrap = getattr(self, "pos_wrap", None)
+        if wrap:
+            pos = pos % wrap
+        q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
+        o, S, _ = _op.aspin_chunk_windows(q, k, v, la.transpose(1, 2).float(), S0, self.theta, window, False)
+        self.sent = None
+        o = self.on(o.to(qp.dtype)).transpose(1, 2).reshape(B, T, D)
+        out = x + F.linear(o, self.o.weight) * torch.sigmoid(self.gate)
+        last = T - window * ((T - 1) // window)
+        return out, (S, p0 * 0 + last if torch.is_tensor(p0) else last)
+
 
 @contextmanager
 def fused_scan(model):

@@ -51,9 +51,9 @@ constexpr int kFwdBuf = 3 * TILE * (int)sizeof(__bf16) + 3 * C * (int)sizeof(flo
 __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const float* __restrict__ S0, __bf16* __restrict__ o, float* __restrict__ Sfin,
-    __bf16* __restrict__ sent, int T, int NC) {
+    __bf16* __restrict__ sent, int T, int NC, int P) {
   extern __shared__ __align__(16) unsigned char smem[];
-  // input set h (chunk c in set c % 3): Q, K, V tiles and the L (base 2), eL, w vectors; then A (t, s) and S^T (j, d)
+  // input set h (the segment's chunk lc in set lc % 3): Q, K, V tiles and the L (base 2), eL, w vectors; then A (t, s) and S^T (j, d)
   // tiles for two chunks each (chunk c in c & 1)
   auto Qb = [&](int h) { return reinterpret_cast<__bf16*>(smem + h * kFwdBuf); };
   auto Kb = [&](int h) { return Qb(h) + TILE; };
@@ -64,9 +64,13 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 
   const WaveIdx x = wave_idx();
   const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
-  const int bh = blockIdx.x;
+  // workgroup = (batch-head bh, segment sg): chunks c0 .. c0 + n - 1, entering state S0 of this workgroup
+  const int nseg = (NC + P - 1) / P;
+  const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
+  const int c0 = sg * P, n = min(P, NC - c0);
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
+  const size_t s0off = (size_t)blockIdx.x * DK * DK;
 
   // decayed scores A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, of t block a of chunk `cn` (input set hs) into
   // the A tile `At` (row t), zero above the diagonal block
@@ -114,7 +118,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) S[jt][r] = S0 ? S0[soff + (16 * tb + 4 * g + r) * DK + j0 + 16 * jt + i] : 0.f;
+      for (int r = 0; r < 4; ++r) S[jt][r] = S0 ? S0[s0off + (16 * tb + 4 * g + r) * DK + j0 + 16 * jt + i] : 0.f;
       store_T(STb(0), j0 + 16 * jt, 16 * tb, g, i, S[jt]);
     }
     __syncthreads();
@@ -122,8 +126,8 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     auto oloop = [&](auto tb_c) {
       constexpr int TB = decltype(tb_c)::value;
       const int tq = 16 * TB + i;  // this lane's token within the chunk for t-indexed operands
-      for (int c = 0; c < NC; ++c) {
-        const int h3 = c % 3, h2 = c & 1, t0 = c * C;
+      for (int lc = 0; lc < n; ++lc) {
+        const int c = c0 + lc, h3 = lc % 3, h2 = lc & 1, t0 = c * C;
         const __bf16* Qs = Qb(h3);
         const __bf16* Ks = Kb(h3);
         const __bf16* Vs = Vb(h3);
@@ -196,15 +200,20 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       case 2: oloop(std::integral_constant<int, 2>{}); break;
       default: oloop(std::integral_constant<int, 3>{}); break;
     }
+    if (Sfin) {
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt)
+      for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Sfin[soff + (16 * tb + 4 * g + r) * DK + j0 + 16 * jt + i] = S[jt][r];
+        for (int r = 0; r < 4; ++r) Sfin[soff + (16 * tb + 4 * g + r) * DK + j0 + 16 * jt + i] = S[jt][r];
+    }
   } else if (w < 12) {
     // ================= score waves: t block a, one chunk ahead. Wave 8 also runs the decay scans, two chunks ahead
     // (the load waves stage the same chunk's tiles in the same phase): L (base 2), e^L and w = exp(L_C - L).
     const bool scan = w == 8;
-    auto la_of = [&](int cn) { return (cn < NC && cn * C + x.l < T) ? la[(size_t)bh * T + cn * C + x.l] : 0.f; };
+    auto la_of = [&](int ln) {  // the segment's chunk ln
+      const int t = (c0 + ln) * C + x.l;
+      return (ln < n && t < T) ? la[(size_t)bh * T + t] : 0.f;
+    };
     auto run_scan = [&](float la_t, int h) {
       const float L = wave_prefix_sum(la_t, x.l);
       const float LC = lane_value(L, 63);
@@ -217,15 +226,15 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       float pla = 0.f;
       if (scan) {
         run_scan(la_of(0), 0);
-        if (NC > 1) run_scan(la_of(1), 1);
+        if (n > 1) run_scan(la_of(1), 1);
         pla = la_of(2);
       }
       __syncthreads();
       scores(a_c, 0, ATb(0));
       __syncthreads();
-      for (int c = 0; c < NC; ++c) {
-        if (c + 1 < NC) scores(a_c, (c + 1) % 3, ATb((c + 1) & 1));
-        if (scan && c + 2 < NC) {
+      for (int c = 0; c < n; ++c) {
+        if (c + 1 < n) scores(a_c, (c + 1) % 3, ATb((c + 1) & 1));
+        if (scan && c + 2 < n) {
           run_scan(pla, (c + 2) % 3);
           pla = la_of(c + 3);
         }
@@ -246,8 +255,8 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       bf16x8 q0, q1, k0, k1, v0, v1;
     };
     Regs ra, rb;
-    auto load = [&](Regs& r, int cn) {
-      const int n0 = cn * C, nr = min(C, T - n0);
+    auto load = [&](Regs& r, int ln) {  // the segment's chunk ln
+      const int n0 = (c0 + ln) * C, nr = min(C, T - n0);
       r.q0 = load_seg(q + boff + (size_t)n0 * DK, nr, b);
       r.q1 = load_seg(q + boff + (size_t)n0 * DK, nr, b + 256);
       r.k0 = load_seg(k + boff + (size_t)n0 * DK, nr, b);
@@ -265,25 +274,172 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     };
     load(ra, 0);
     stage(ra, 0);
-    if (NC > 1) {
+    if (n > 1) {
       load(rb, 1);
       stage(rb, 1);
-      if (NC > 2) load(ra, 2);
-      if (NC > 3) load(rb, 3);
+      if (n > 2) load(ra, 2);
+      if (n > 3) load(rb, 3);
     }
     __syncthreads();
     __syncthreads();
     // chunk c: stage chunk c + 2 from the set loaded two chunks ago, then reload that set with chunk c + 4
     auto phase = [&](Regs& r, int c) {
-      if (c + 2 < NC) {
+      if (c + 2 < n) {
         stage(r, (c + 2) % 3);
-        if (c + 4 < NC) load(r, c + 4);
+        if (c + 4 < n) load(r, c + 4);
       }
       __syncthreads();
     };
-    for (int c = 0; c < NC; c += 2) {
+    for (int c = 0; c < n; c += 2) {
       phase(ra, c);
-      if (c + 1 < NC) phase(rb, c + 1);
+      if (c + 1 < n) phase(rb, c + 1);
+    }
+  }
+}
+
+// Segment-parallel forward, for few heads over long sequences: the chunks of each head are split into segments of
+// P chunks that run as separate workgroups of the forward above, once each segment's entering state is known. The
+// state a segment leaves is an affine function of the one it enters, S_out = e^{l} S_in + E, with l the segment's
+// total log-decay and E = sum_t exp(L_end - L_t) k_t v_t^T over its tokens (L the cumulative sum of la from the
+// segment's start, so the weight is the decay from token t to the segment's end). Windowed carrying (positions
+// restarting every `window` tokens, the state rebased between windows as successive forward calls do) adds a
+// rotation of the key rows at window boundaries: S_in(next) = R(-window theta) S_out.
+
+// Segment sums: per workgroup (batch-head, segment) E and l. Four waves; wave w owns key rows 16 w.. of E as MFMA
+// accumulators. The segment's chunks are walked from its end, so each chunk's decay to the segment's end is a
+// running sum; K and V are staged through double-buffered LDS, loaded a chunk ahead.
+constexpr int kSumBuf = 2 * TILE * (int)sizeof(__bf16) + C * (int)sizeof(float);  // K, V, w
+
+__global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+                                                          const float* __restrict__ la, float* __restrict__ E,
+                                                          float* __restrict__ lseg, int T, int NC, int P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  auto Kb = [&](int h) { return reinterpret_cast<__bf16*>(smem + h * kSumBuf); };
+  auto Vb = [&](int h) { return Kb(h) + TILE; };
+  auto Wb = [&](int h) { return reinterpret_cast<float*>(Kb(h) + 2 * TILE); };
+  const WaveIdx x = wave_idx();
+  const int w = x.w, g = x.g, i = x.i;
+  const int b = threadIdx.x & 255;
+  const int nseg = (NC + P - 1) / P;
+  const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
+  const int c0 = sg * P, n = min(P, NC - c0);
+  const size_t boff = (size_t)bh * T * DK;
+  bf16x8 k0, k1, v0, v1;
+  float lat = 0.f;
+  auto load = [&](int ln) {  // the segment's chunk ln; rows past T read as zero
+    const int n0 = (c0 + ln) * C, nr = min(C, T - n0);
+    k0 = load_seg(k + boff + (size_t)n0 * DK, nr, b);
+    k1 = load_seg(k + boff + (size_t)n0 * DK, nr, b + 256);
+    v0 = load_seg(v + boff + (size_t)n0 * DK, nr, b);
+    v1 = load_seg(v + boff + (size_t)n0 * DK, nr, b + 256);
+    if (w == 0) lat = x.l < nr ? la[(size_t)bh * T + n0 + x.l] : 0.f;
+  };
+  float after = 0.f;  // wave 0: total log-decay of the segment's chunks after the one being staged
+  auto stage = [&](int h) {
+    put_seg(Kb(h), k0, b);
+    put_seg(Kb(h), k1, b + 256);
+    put_seg(Vb(h), v0, b);
+    put_seg(Vb(h), v1, b + 256);
+    if (w == 0) {
+      const float L = wave_prefix_sum(lat, x.l);
+      const float tot = lane_value(L, 63);
+      Wb(h)[x.l] = __expf(fminf(after + tot - L, 0.f));
+      after += tot;
+    }
+  };
+  f32x4 acc[4];
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) acc[jb] = zero4();
+  load(n - 1);
+  stage(0);
+  if (n > 1) load(n - 2);
+  __syncthreads();
+  for (int it = 0; it < n; ++it) {
+    const int h = it & 1;
+    const __bf16* Ks = Kb(h);
+    const __bf16* Vs = Vb(h);
+    const float* ws = Wb(h);
+    const bf16x8 kt0 = frag_tr(Ks, 16 * w, 0, g, i), kt1 = frag_tr(Ks, 16 * w, 1, g, i);
+    const f32x4 w00 = *reinterpret_cast<const f32x4*>(ws + 4 * g);
+    const f32x4 w01 = *reinterpret_cast<const f32x4*>(ws + 16 + 4 * g);
+    const f32x4 w10 = *reinterpret_cast<const f32x4*>(ws + 32 + 4 * g);
+    const f32x4 w11 = *reinterpret_cast<const f32x4*>(ws + 48 + 4 * g);
+    bf16x8 vf[4][2];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      vf[jb][0] = frag_tr(Vs, 16 * jb, 0, g, i);
+      vf[jb][1] = frag_tr(Vs, 16 * jb, 1, g, i);
+    }
+    const bf16x8 kw0 = scale_frag_k(kt0, w00, w01);
+    const bf16x8 kw1 = scale_frag_k(kt1, w10, w11);
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      acc[jb] = pgn_mfma(kw0, vf[jb][0], acc[jb]);
+      acc[jb] = pgn_mfma(kw1, vf[jb][1], acc[jb]);
+    }
+    if (it + 1 < n) {
+      stage(h ^ 1);
+      if (it + 2 < n) load(n - 3 - it);
+    }
+    __syncthreads();
+  }
+  float* e = E + (size_t)blockIdx.x * DK * DK;
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) e[(16 * w + 4 * g + r) * DK + 16 * jb + i] = acc[jb][r];
+  if (w == 0 && x.l == 0) lseg[blockIdx.x] = after;
+}
+
+// Segment prefix: the state entering each segment, written over that segment's E, and the final state:
+// S_in(0) = S0 (zero if NULL); S_out(g) = e^{l_g} S_in(g) + E_g; S_in(g + 1) = S_out(g), rotated at window boundaries
+// (every `wsegs` segments, when theta is given) by -shift theta[h, i] on key rows (2i, 2i + 1); S_final = S_out(last).
+// Thread = (value column j, key pair ip): 8 workgroups of 256 per head. Each batch of 16 segments is loaded before
+// the recurrence runs over it, so the loads are not serialised behind it.
+__global__ __launch_bounds__(256) void aspin_plain_segprefix(const float* __restrict__ S0,
+                                                             const float* __restrict__ theta, float shift, int wsegs,
+                                                             float* __restrict__ E, const float* __restrict__ lseg,
+                                                             float* __restrict__ Sfin, int H, int nseg) {
+  const int bh = blockIdx.x >> 3, h = bh % H;
+  const int j = threadIdx.x & 63, ip = 4 * (blockIdx.x & 7) + (threadIdx.x >> 6);
+  const int e0 = (2 * ip) * DK + j, e1 = e0 + DK;
+  const size_t soff = (size_t)bh * DK * DK;
+  float s0 = S0 ? S0[soff + e0] : 0.f, s1 = S0 ? S0[soff + e1] : 0.f;
+  float sn = 0.f, cs = 1.f;
+  if (theta) sincosf(-shift * theta[h * (DK / 2) + ip], &sn, &cs);
+  constexpr int kBatch = 16;
+  for (int g0 = 0; g0 < nseg; g0 += kBatch) {
+    float x0[kBatch], x1[kBatch], a[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (g0 + u < nseg) {
+        const size_t off = ((size_t)bh * nseg + g0 + u) * DK * DK;
+        x0[u] = E[off + e0];
+        x1[u] = E[off + e1];
+        a[u] = lseg[(size_t)bh * nseg + g0 + u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int gg = g0 + u;
+      if (gg < nseg) {
+        const size_t off = ((size_t)bh * nseg + gg) * DK * DK;
+        E[off + e0] = s0;
+        E[off + e1] = s1;
+        const float dec = __expf(a[u]);
+        const float t0 = dec * s0 + x0[u], t1 = dec * s1 + x1[u];
+        if (theta && (gg + 1) % wsegs == 0) {
+          s0 = t0 * cs - t1 * sn;
+          s1 = t0 * sn + t1 * cs;
+        } else {
+          s0 = t0;
+          s1 = t1;
+        }
+        if (gg == nseg - 1) {
+          Sfin[soff + e0] = t0;
+          Sfin[soff + e1] = t1;
+        }
+      }
     }
   }
 }
@@ -741,7 +897,61 @@ extern "C" int pragnosia_aspin_chunk_fwd(const void* q, const void* k, const voi
   const int NC = (int)((T + C - 1) / C);
   hipLaunchKernelGGL(aspin_plain_fwd, dim3((unsigned)(B * H)), dim3(kFwdWaves * 64), kFwdSmem, (hipStream_t)stream,
                      (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, S0, (__bf16*)o, S_final,
-                     (__bf16*)sent, (int)T, NC);
+                     (__bf16*)sent, (int)T, NC, NC);
+  PGN_RETURN_LAUNCH();
+}
+
+namespace {
+
+// workspace of the segmented forward: E (fp32 D x D per segment, later the entering states) then l per segment
+int64_t seg_count(int64_t T, int64_t seg_chunks) { return ((T + C - 1) / C + seg_chunks - 1) / seg_chunks; }
+
+int64_t seg_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t seg_chunks) {
+  const int64_t n = B * H * seg_count(T, seg_chunks);
+  return n * DK * DK * (int64_t)sizeof(float) + ((n * (int64_t)sizeof(float) + 255) / 256) * 256;
+}
+
+}  // namespace
+
+extern "C" int64_t pragnosia_aspin_chunk_fwd_seg_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D,
+                                                                 int64_t chunk, int64_t seg_chunks) {
+  if (D != DK || chunk != C || seg_chunks < 1 || !shape_ok(B, H, T, D, chunk)) return -1;
+  return seg_workspace_bytes(B, H, T, seg_chunks);
+}
+
+extern "C" int pragnosia_aspin_chunk_fwd_seg(const void* q, const void* k, const void* v, const float* la,
+                                             const float* S0, const float* theta, int64_t window, void* o,
+                                             float* S_final, void* sent, void* workspace, int64_t workspace_bytes,
+                                             int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk,
+                                             int64_t seg_chunks, void* stream) {
+  if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
+  PGN_CHECK_ARG(q && k && v && la && o && S_final && workspace);
+  PGN_CHECK_ARG(seg_chunks >= 1 && seg_chunks < ((int64_t)1 << 28));
+  PGN_CHECK_ARG(window >= 0);
+  if (window > 0) PGN_CHECK_ARG(theta && window % C == 0 && (window / C) % seg_chunks == 0);
+  PGN_CHECK_ARG(workspace_bytes >= seg_workspace_bytes(B, H, T, seg_chunks));
+  const int64_t nseg = seg_count(T, seg_chunks);
+  PGN_CHECK_ARG(B * H * nseg < ((int64_t)1 << 31));
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)aspin_plain_fwd, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kFwdSmem);
+    if (e != hipSuccess) return (int)e;
+    attr_set = true;
+  }
+  const int NC = (int)((T + C - 1) / C);
+  float* E = (float*)workspace;
+  float* lseg = E + B * H * nseg * DK * DK;
+  const unsigned nblk = (unsigned)(B * H * nseg);
+  hipLaunchKernelGGL(aspin_plain_segsum, dim3(nblk), dim3(256), 2 * kSumBuf, (hipStream_t)stream, (const __bf16*)k,
+                     (const __bf16*)v, la, E, lseg, (int)T, NC, (int)seg_chunks);
+  hipLaunchKernelGGL(aspin_plain_segprefix, dim3((unsigned)(B * H * 8)), dim3(256), 0, (hipStream_t)stream, S0,
+                     window > 0 ? theta : nullptr, (float)window, (int)(window / C / seg_chunks), E, lseg, S_final,
+                     (int)H, (int)nseg);
+  hipLaunchKernelGGL(aspin_plain_fwd, dim3(nblk), dim3(kFwdWaves * 64), kFwdSmem, (hipStream_t)stream,
+                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, E, (__bf16*)o, nullptr,
+                     (__bf16*)sent, (int)T, NC, (int)seg_chunks);
   PGN_RETURN_LAUNCH();
 }
 

@@ -120,16 +120,12 @@ class LM(nn.Module):
     def forward_carried(self, x, window=None):
         """A sequence longer than one window: windows of `window` tokens with every layer's state carried across the
         boundary and position embeddings restarting per window; returns the final window's logits
-        (`src/model.py:842-864`)."""
+        (`src/model.py:842-864`). Computed layer by layer over the whole sequence (the same function as window by
+        window: a layer's windows depend on each other only through its carried state, which each mixer's
+        forward_windows threads through one pass)."""
         window = window or self.ctx
-        states = [None] * self.layers
-        pos = torch.arange(window, device=x.device)
-        logits = None
-        for s in range(0, x.shape[1], window):
-            xw = x[:, s:s + window]
-            h = self._embed(xw, pos[: xw.shape[1]])
-            for i, (mx, mp) in enumerate(zip(self.mix, self.mlp)):
-                h, states[i] = mx(h, states[i])
-                h = mp(h)
-            logits = F.linear(self.n(h), self.e.weight)
-        return logits
+        T = x.shape[1]
+        h = self._embed(x, torch.arange(T, device=x.device) % window)
+        for mx, mp in zip(self.mix, self.mlp):
+            h = mp(mx.forward_windows(h, window)[0])
+        return F.linear(self.n(h[:, window * ((T - 1) // window):]), self.e.weight)

@@ -130,10 +130,83 @@ def aspin_chunk(q: Tensor, k: Tensor, v: Tensor, la: Tensor, S0: Optional[Tensor
     S = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
     sent = (torch.empty(B, H, NC, D, D, device=q.device, dtype=torch.bfloat16) if want_sent
             else q.new_empty(0, dtype=torch.bfloat16))
+    P = seg_chunks(B * H, NC, range(1, NC + 1))
+    if P < NC:
+        _aspin_fwd_seg(q, k, v, la, S0, None, 0, o, S, sent if want_sent else None, P)
+        return o, S, sent
     check(lib().pragnosia_aspin_chunk_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(S0), _ptr(o), _ptr(S),
                                           _ptr(sent) if want_sent else None, B, H, T, D, CHUNK, _stream(q)),
           "pragnosia_aspin_chunk_fwd")
     return o, S, sent
+
+
+COMPUTE_UNITS = 256  # MI355X
+
+
+SEG_MIN_CHUNKS = 2   # shorter segments cost more in start-up than they save (measured)
+SEG_OVERHEAD = 6     # the segment sums and prefix, in chunk steps of the forward (measured)
+
+
+def seg_chunks(heads: int, NC: int, candidates) -> int:
+    """Chunks per segment for the plain forward over `heads` (batch x head) sequences of NC chunks. Segments are
+    sized so that one round of workgroups covers the compute units (several rounds of shorter segments measured
+    slower), at least SEG_MIN_CHUNKS long, and taken only when the walk they save exceeds what they add: the
+    segment sums walk the segment too, plus a fixed overhead. Returns the largest candidate not above that size, or
+    NC (one workgroup per head, no segments)."""
+    nseg = max(1, COMPUTE_UNITS // max(heads, 1))
+    want = max(SEG_MIN_CHUNKS, -(-NC // nseg))
+    fit = [c for c in candidates if c <= want]
+    if not fit:
+        return NC
+    P = max(fit)
+    if -(-NC // P) < 2 or NC <= 2 * P + SEG_OVERHEAD:
+        return NC
+    return P
+
+
+def _aspin_fwd_seg(q, k, v, la, S0, theta, window, o, S, sent, P):
+    B, H, T, D = q.shape
+    nbytes = lib().pragnosia_aspin_chunk_fwd_seg_workspace_bytes(B, H, T, D, CHUNK, P)
+    if nbytes < 0:
+        raise PragnosiaError(f"aspin segmented forward: shape rejected (B={B} H={H} T={T} D={D} segment={P})")
+    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+    check(lib().pragnosia_aspin_chunk_fwd_seg(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(S0), _ptr(theta), window,
+                                              _ptr(o), _ptr(S), _ptr(sent), _ptr(ws), nbytes, B, H, T, D, CHUNK, P,
+                                              _stream(q)), "pragnosia_aspin_chunk_fwd_seg")
+
+
+@torch.library.custom_op("pragnosia::aspin_chunk_windows", mutates_args=())
+def aspin_chunk_windows(q: Tensor, k: Tensor, v: Tensor, la: Tensor, S0: Optional[Tensor], theta: Tensor,
+                        window: int, want_sent: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """Forward only. The plain-rule scan over consecutive windows of `window` tokens (a multiple of 64) whose q and k
+    were rotated with positions restarting at 0 in every window, the state carried across window boundaries and
+    rebased by -window * theta there: what aspin_chunk over each window in turn, with aspin_rebase between, computes
+    (the reference's carried windows, `src/model.py:842-864` over `src/assoc.py:391-405`), as one segment-parallel
+    pass. S0 enters the first window. Returns (o bf16, S after the last window fp32 (in its positions), sent bf16
+    (B, H, NC, 64, 64) or an empty tensor)."""
+    _require_gpu(q, k, v, la, S0, theta)
+    if window <= 0 or window % CHUNK:
+        raise PragnosiaError(f"aspin_chunk_windows: window {window} must be a positive multiple of {CHUNK}")
+    q, k, v, la, S0, theta = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(S0), _f32(theta)
+    B, H, T, D = q.shape
+    NC = (T + CHUNK - 1) // CHUNK
+    o = torch.empty(B, H, T, D, device=q.device, dtype=torch.bfloat16)
+    S = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
+    sent = (torch.empty(B, H, NC, D, D, device=q.device, dtype=torch.bfloat16) if want_sent
+            else q.new_empty(0, dtype=torch.bfloat16))
+    W = window // CHUNK
+    divisors = [p for p in range(1, W + 1) if W % p == 0]
+    P = seg_chunks(B * H, NC, divisors)
+    _aspin_fwd_seg(q, k, v, la, S0, theta, window, o, S, sent if want_sent else None, P if P in divisors else W)
+    return o, S, sent
+
+
+@aspin_chunk_windows.register_fake
+def _(q, k, v, la, S0, theta, window, want_sent):
+    B, H, T, D = q.shape
+    NC = (T + CHUNK - 1) // CHUNK
+    sent = q.new_empty(B, H, NC, D, D, dtype=torch.bfloat16) if want_sent else q.new_empty(0, dtype=torch.bfloat16)
+    return q.new_empty(B, H, T, D, dtype=torch.bfloat16), q.new_empty(B, H, D, D, dtype=torch.float32), sent
 
 
 @aspin_chunk.register_fake

@@ -63,3 +63,9 @@ class SpinCarrier(nn.Module):
         u = self.B(z) * gam * torch.sigmoid(self.Wi(z))
         y, h = scan_hip(u, logmag, ang.expand_as(logmag), h0)
         return x + torch.sigmoid(self.gate) * self.C(y), h
+
+    def forward_windows(self, x, window: int, h0=None):
+        """Consecutive windows of `window` tokens with the state carried from each into the next: nothing in this
+        carrier depends on positions, so that is one continuous scan over the whole sequence. Returns the same as
+        `forward`."""
+        return self.forward(x, h0)
