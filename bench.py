@@ -227,9 +227,10 @@ def carried_bench():
     """B2 T8192 H12 D64 bf16 inputs, la = logsigmoid(N(4,1)); (i) 16 windows of 512 with the
     fp32 state carried and rebased by -512 theta between windows (positions restart per window, as successive
     AssocCarrier.forward calls do), in one segment-parallel pass (aspin_chunk_windows); (ii) one unsplit T = 8192
-    pass (aspin_chunk, which takes the segment-parallel forward for these few heads). Forward only; device time per
-    call from graph replays. Also the window-by-window loop (16 x (rebase + aspin_chunk)) the carried path replaces,
-    and the carried-vs-unsplit error on the outputs and on the final state."""
+    pass (aspin_chunk, which takes the segment-parallel forward for these few heads); device time per call from graph
+    replays. Also the window-by-window loop (16 x (rebase + aspin_chunk)) the carried path replaces, a forward +
+    backward step over the unsplit sequence (segment-parallel, and through the one-workgroup-per-head kernels), and
+    the carried-vs-unsplit error on the outputs and on the final state."""
     import torch
     import torch.nn.functional as F
     from pragnosia_amd import ops  # noqa: F401
@@ -262,9 +263,31 @@ def carried_bench():
 
     carried = lambda: op.aspin_chunk_windows(qw, kw, vb, la, None, th, W, False)
     unsplit = lambda: op.aspin_chunk(qg, kg, vb, la, None, False)
+    # a training step over the long sequence: forward (entering states kept) and backward, segment-parallel, and
+    # the same through the one-workgroup-per-head kernels
+    do = torch.randn(qg.shape, generator=torch.Generator(device=dev).manual_seed(33), device=dev).bfloat16()
+
+    def step():
+        o, S, sent = op.aspin_chunk(qg, kg, vb, la, None, True)
+        return op.aspin_chunk_bwd(qg, kg, vb, la, sent, do, None)
+
+    def step_sequential():
+        from pragnosia_amd._lib import check, lib
+        from pragnosia_amd.ops import _ptr, _stream
+        NC = T // 64
+        o, sent = torch.empty_like(qg), torch.empty(B, H, NC, D, D, device=dev, dtype=torch.bfloat16)
+        S, dS0 = torch.empty(B, H, D, D, device=dev), torch.empty(B, H, D, D, device=dev)
+        dq, dk, dv = torch.empty_like(qg), torch.empty_like(qg), torch.empty_like(qg)
+        dla = torch.empty(B, H, T, device=dev)
+        check(lib().pragnosia_aspin_chunk_fwd(_ptr(qg), _ptr(kg), _ptr(vb), _ptr(la), None, _ptr(o), _ptr(S),
+                                              _ptr(sent), B, H, T, D, 64, _stream(qg)), "fwd")
+        check(lib().pragnosia_aspin_chunk_bwd(_ptr(qg), _ptr(kg), _ptr(vb), _ptr(la), _ptr(sent), _ptr(do), None,
+                                              _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla), _ptr(dS0), B, H, T, D, 64,
+                                              _stream(qg)), "bwd")
+
     stream = torch.cuda.current_stream()
     with torch.no_grad():
-        t_c, t_u, t_l = _time_ops([carried, unsplit, loop], 10, stream)
+        t_c, t_u, t_l, t_s, t_q = _time_ops([carried, unsplit, loop, step, step_sequential], 10, stream)
         oc, Sc, _ = carried()
         ol, Sl = loop()
         ou, Su, _ = unsplit()
@@ -278,6 +301,8 @@ def carried_bench():
             "unsplit_Mtok_s": round(B * T / t_u / 1e6, 3), "unsplit_us": round(t_u * 1e6, 2),
             "unsplit_segment_chunks": Pu,
             "window_loop_Mtok_s": round(B * T / t_l / 1e6, 3), "window_loop_us": round(t_l * 1e6, 2),
+            "long_fwd_bwd_Mtok_s": round(B * T / t_s / 1e6, 3), "long_fwd_bwd_us": round(t_s * 1e6, 2),
+            "long_fwd_bwd_sequential_us": round(t_q * 1e6, 2),
             "carried_vs_window_loop_rel_err_o": round(rel(oc, ol), 6),
             "carried_vs_window_loop_rel_err_S": round(rel(Sc, Sl), 6),
             "carried_vs_unsplit_rel_err_o": round(rel(oc, ou), 6),

@@ -20,7 +20,7 @@ extern "C" {
 #define PRAGNOSIA_ERR_INVALID_ARGUMENT (-1)
 #define PRAGNOSIA_ERR_UNSUPPORTED (-2)
 
-/* ABI version of this header (7); bumped on any signature change. */
+/* ABI version of this header (8); bumped on any signature change. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -70,9 +70,10 @@ int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const void* v, const
                               void* dq, void* dk, void* dv, float* dla, float* dS0,
                               int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
 
-/* Bytes of device workspace pragnosia_aspin_chunk_fwd_seg needs (-1 if the shape is rejected). */
-int64_t pragnosia_aspin_chunk_fwd_seg_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk,
-                                                      int64_t seg_chunks);
+/* Bytes of device workspace pragnosia_aspin_chunk_fwd_seg and pragnosia_aspin_chunk_bwd_seg need (-1 if the shape
+ * is rejected). */
+int64_t pragnosia_aspin_chunk_seg_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk,
+                                                  int64_t seg_chunks);
 
 /* The forward of pragnosia_aspin_chunk_fwd, segment-parallel: every head's chunks are split into segments of
  * `seg_chunks` chunks that run concurrently once their entering states are known (per-segment state sums, a prefix
@@ -85,11 +86,21 @@ int64_t pragnosia_aspin_chunk_fwd_seg_workspace_bytes(int64_t B, int64_t H, int6
  * the reference's carrier over consecutive windows compute, each rebasing the state it is handed
  * (`AssocCarrier.forward`, src/assoc.py:391-405, driven by `LM.forward_carried`, src/model.py:842-864); S_final is
  * the state after the last window, in that window's positions. S0 is the state entering the first window.
- * `workspace`: caller-allocated device memory of at least pragnosia_aspin_chunk_fwd_seg_workspace_bytes(...) bytes. */
+ * `workspace`: caller-allocated device memory of at least pragnosia_aspin_chunk_seg_workspace_bytes(...) bytes. */
 int pragnosia_aspin_chunk_fwd_seg(const void* q, const void* k, const void* v, const float* la, const float* S0,
                                   const float* theta, int64_t window, void* o, float* S_final, void* sent,
                                   void* workspace, int64_t workspace_bytes, int64_t B, int64_t H, int64_t T,
                                   int64_t D, int64_t chunk, int64_t seg_chunks, void* stream);
+
+/* The backward of pragnosia_aspin_chunk_bwd, segment-parallel (segments of `seg_chunks` chunks: per-segment sums of
+ * q and dO, a reverse prefix over segments for the state gradient entering each segment from later ones, then the
+ * chunked backward per segment). Same inputs and outputs as pragnosia_aspin_chunk_bwd (continuous sequences only);
+ * `sent` from either forward. `workspace`: at least pragnosia_aspin_chunk_seg_workspace_bytes(...) bytes.
+ * Replaces the same registered backward (src/assoc_kernel.py:146-299) for few heads over long sequences. */
+int pragnosia_aspin_chunk_bwd_seg(const void* q, const void* k, const void* v, const float* la, const void* sent,
+                                  const void* dO, const float* dS_final, void* dq, void* dk, void* dv, float* dla,
+                                  float* dS0, void* workspace, int64_t workspace_bytes, int64_t B, int64_t H,
+                                  int64_t T, int64_t D, int64_t chunk, int64_t seg_chunks, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Associative carrier, DELTA write rule, chunked scan (chunk = 64, head dim D = 64), per (batch, head):

@@ -23,8 +23,9 @@ SIGNATURES = {
     "pragnosia_diag_scan_bwd": [_p] * 14 + [_i64] * 3 + [_p],
     "pragnosia_aspin_chunk_fwd": [_p] * 8 + [_i64] * 5 + [_p],
     "pragnosia_aspin_chunk_bwd": [_p] * 12 + [_i64] * 5 + [_p],
-    "pragnosia_aspin_chunk_fwd_seg_workspace_bytes": [_i64] * 6,
+    "pragnosia_aspin_chunk_seg_workspace_bytes": [_i64] * 6,
     "pragnosia_aspin_chunk_fwd_seg": [_p] * 6 + [_i64] + [_p] * 4 + [_i64] * 7 + [_p],
+    "pragnosia_aspin_chunk_bwd_seg": [_p] * 13 + [_i64] * 7 + [_p],
     "pragnosia_aspin_delta_fwd": [_p] * 11 + [_i64] * 5 + [_p],
     "pragnosia_aspin_delta_bwd_workspace_bytes": [_i64] * 5,
     "pragnosia_aspin_delta_bwd": [_p] * 17 + [_i64] * 6 + [_p],
@@ -38,7 +39,7 @@ SIGNATURES = {
 
 # entry points that return a size (int64) rather than a status code
 _RET_I64 = {"pragnosia_aspin_delta_bwd_workspace_bytes", "pragnosia_aspin_prep_theta_partials",
-            "pragnosia_aspin_chunk_fwd_seg_workspace_bytes"}
+            "pragnosia_aspin_chunk_seg_workspace_bytes"}
 
 _lib = None
 

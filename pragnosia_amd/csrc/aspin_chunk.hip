@@ -53,8 +53,8 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     const float* __restrict__ la, const float* __restrict__ S0, __bf16* __restrict__ o, float* __restrict__ Sfin,
     __bf16* __restrict__ sent, int T, int NC, int P) {
   extern __shared__ __align__(16) unsigned char smem[];
-  // input set h (the segment's chunk lc in set lc % 3): Q, K, V tiles and the L (base 2), eL, w vectors; then A (t, s) and S^T (j, d)
-  // tiles for two chunks each (chunk c in c & 1)
+  // input set h (the segment's chunk lc in set lc % 3): Q, K, V tiles and the L (base 2), eL, w vectors; then A
+  // (t, s) and S^T (j, d) tiles for two chunks each (chunk lc in lc & 1)
   auto Qb = [&](int h) { return reinterpret_cast<__bf16*>(smem + h * kFwdBuf); };
   auto Kb = [&](int h) { return Qb(h) + TILE; };
   auto Vb = [&](int h) { return Qb(h) + 2 * TILE; };
@@ -305,11 +305,18 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 // restarting every `window` tokens, the state rebased between windows as successive forward calls do) adds a
 // rotation of the key rows at window boundaries: S_in(next) = R(-window theta) S_out.
 
-// Segment sums: per workgroup (batch-head, segment) E and l. Four waves; wave w owns key rows 16 w.. of E as MFMA
-// accumulators. The segment's chunks are walked from its end, so each chunk's decay to the segment's end is a
-// running sum; K and V are staged through double-buffered LDS, loaded a chunk ahead.
-constexpr int kSumBuf = 2 * TILE * (int)sizeof(__bf16) + C * (int)sizeof(float);  // K, V, w
+// The backward splits the same way in reverse. The gradient on the state leaving the chunk before a segment is
+// e^{l} G + F, with G the gradient on the state the segment leaves and F = sum_t exp(L_t) q_t dO_t^T (the decay
+// from the segment's start to t, inclusive), so per-segment sums of q and dO, a reverse prefix over segments, and
+// the backward kernel per segment started from its G give every chunk's state gradient, hence dq, dk, dv and dla.
 
+// Segment sums: per workgroup (batch-head, segment) sum_t w_t x_t y_t^T and l. TO_END (forward): x = k, y = v and
+// w_t = exp(L_end - L_t), the segment's chunks walked from its end so each chunk's decay to the end is a running
+// sum. Otherwise (backward): x = q, y = dO and w_t = exp(L_t), walked from the start. Four waves; wave w owns rows
+// 16 w.. of the sum as MFMA accumulators; x and y are staged through double-buffered LDS, loaded a chunk ahead.
+constexpr int kSumBuf = 2 * TILE * (int)sizeof(__bf16) + C * (int)sizeof(float);  // x, y, w
+
+template <bool TO_END>
 __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restrict__ k, const __bf16* __restrict__ v,
                                                           const float* __restrict__ la, float* __restrict__ E,
                                                           float* __restrict__ lseg, int T, int NC, int P) {
@@ -334,7 +341,9 @@ __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restri
     v1 = load_seg(v + boff + (size_t)n0 * DK, nr, b + 256);
     if (w == 0) lat = x.l < nr ? la[(size_t)bh * T + n0 + x.l] : 0.f;
   };
-  float after = 0.f;  // wave 0: total log-decay of the segment's chunks after the one being staged
+  // wave 0: total log-decay of the segment's chunks already staged (after the next one when walking to the end,
+  // before it when walking from the start)
+  float run = 0.f;
   auto stage = [&](int h) {
     put_seg(Kb(h), k0, b);
     put_seg(Kb(h), k1, b + 256);
@@ -343,16 +352,18 @@ __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restri
     if (w == 0) {
       const float L = wave_prefix_sum(lat, x.l);
       const float tot = lane_value(L, 63);
-      Wb(h)[x.l] = __expf(fminf(after + tot - L, 0.f));
-      after += tot;
+      Wb(h)[x.l] = TO_END ? __expf(fminf(run + tot - L, 0.f)) : __expf(fminf(run + L, 0.f));
+      run += tot;
     }
   };
+  // the segment's chunk walked at step it
+  auto chunk_at = [&](int it) { return TO_END ? n - 1 - it : it; };
   f32x4 acc[4];
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) acc[jb] = zero4();
-  load(n - 1);
+  load(chunk_at(0));
   stage(0);
-  if (n > 1) load(n - 2);
+  if (n > 1) load(chunk_at(1));
   __syncthreads();
   for (int it = 0; it < n; ++it) {
     const int h = it & 1;
@@ -379,7 +390,7 @@ __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restri
     }
     if (it + 1 < n) {
       stage(h ^ 1);
-      if (it + 2 < n) load(n - 3 - it);
+      if (it + 2 < n) load(chunk_at(it + 2));
     }
     __syncthreads();
   }
@@ -388,14 +399,17 @@ __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restri
   for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
     for (int r = 0; r < 4; ++r) e[(16 * w + 4 * g + r) * DK + 16 * jb + i] = acc[jb][r];
-  if (w == 0 && x.l == 0) lseg[blockIdx.x] = after;
+  if (w == 0 && x.l == 0) lseg[blockIdx.x] = run;
 }
 
 // Segment prefix: the state entering each segment, written over that segment's E, and the final state:
 // S_in(0) = S0 (zero if NULL); S_out(g) = e^{l_g} S_in(g) + E_g; S_in(g + 1) = S_out(g), rotated at window boundaries
 // (every `wsegs` segments, when theta is given) by -shift theta[h, i] on key rows (2i, 2i + 1); S_final = S_out(last).
-// Thread = (value column j, key pair ip): 8 workgroups of 256 per head. Each batch of 16 segments is loaded before
-// the recurrence runs over it, so the loads are not serialised behind it.
+// REVERSE (backward): the same recurrence over the segments from the last to the first, S0 the gradient on the final
+// state, writing over each F the gradient on the state the segment leaves and, as "final", the gradient on the
+// initial state (no rotation). Thread = (value column j, key pair ip): 8 workgroups of 256 per head. Each batch of
+// 16 segments is loaded before the recurrence runs over it, so the loads are not serialised behind it.
+template <bool REVERSE>
 __global__ __launch_bounds__(256) void aspin_plain_segprefix(const float* __restrict__ S0,
                                                              const float* __restrict__ theta, float shift, int wsegs,
                                                              float* __restrict__ E, const float* __restrict__ lseg,
@@ -413,29 +427,30 @@ __global__ __launch_bounds__(256) void aspin_plain_segprefix(const float* __rest
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       if (g0 + u < nseg) {
-        const size_t off = ((size_t)bh * nseg + g0 + u) * DK * DK;
+        const int gi = REVERSE ? nseg - 1 - (g0 + u) : g0 + u;
+        const size_t off = ((size_t)bh * nseg + gi) * DK * DK;
         x0[u] = E[off + e0];
         x1[u] = E[off + e1];
-        a[u] = lseg[(size_t)bh * nseg + g0 + u];
+        a[u] = lseg[(size_t)bh * nseg + gi];
       }
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int gg = g0 + u;
       if (gg < nseg) {
-        const size_t off = ((size_t)bh * nseg + gg) * DK * DK;
+        const size_t off = ((size_t)bh * nseg + (REVERSE ? nseg - 1 - gg : gg)) * DK * DK;
         E[off + e0] = s0;
         E[off + e1] = s1;
         const float dec = __expf(a[u]);
         const float t0 = dec * s0 + x0[u], t1 = dec * s1 + x1[u];
-        if (theta && (gg + 1) % wsegs == 0) {
+        if (!REVERSE && theta && (gg + 1) % wsegs == 0) {
           s0 = t0 * cs - t1 * sn;
           s1 = t0 * sn + t1 * cs;
         } else {
           s0 = t0;
           s1 = t1;
         }
-        if (gg == nseg - 1) {
+        if (Sfin && gg == nseg - 1) {
           Sfin[soff + e0] = t0;
           Sfin[soff + e1] = t1;
         }
@@ -494,7 +509,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const __bf16* __restrict__ sent, const __bf16* __restrict__ dO,
     const float* __restrict__ dSfin, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    float* __restrict__ dla, float* __restrict__ dS0, int T, int NC) {
+    float* __restrict__ dla, float* __restrict__ dS0, int T, int NC, int P) {
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* stg = reinterpret_cast<__bf16*>(smem);    // two sets of staged tiles, chunk c uses set c & 1
   __bf16* dSTb = stg + 2 * kBwdStage;                // two dS^T (j, d) tiles: dS leaving chunk c in tile c & 1
@@ -502,9 +517,13 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 
   const WaveIdx x = wave_idx();
   const int w = x.w, wl = w & 3, g = x.g, i = x.i, tid = threadIdx.x;
-  const int bh = blockIdx.x;
+  // workgroup = (batch-head bh, segment sg): chunks c0 .. cl, walked from cl down; dSfin indexed per workgroup
+  const int nseg = (NC + P - 1) / P;
+  const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
+  const int c0 = sg * P, cl = min(c0 + P, NC) - 1;
   const size_t boff = (size_t)bh * T * DK;
   const size_t soff = (size_t)bh * DK * DK;
+  const size_t s0off = (size_t)blockIdx.x * DK * DK;
 
   // The two groups run separate loops (the branch is on a wave-uniform value) that meet at the same barriers: each
   // loop's registers and memory-counter waits are then its own.
@@ -531,15 +550,15 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       }
     };
     if (kstage) {
-      load(NC - 1);
-      stage((NC - 1) & 1);
-      if (NC > 1) load(NC - 2);
+      load(cl);
+      stage(cl & 1);
+      if (cl > c0) load(cl - 1);
     }
     __syncthreads();
     auto kloop = [&](auto wl_c) {
       constexpr int WL = decltype(wl_c)::value;
       const int me = 16 * WL + i;
-      for (int cc = NC - 1; cc >= 0; --cc) {
+      for (int cc = cl; cc >= c0; --cc) {
         const int t0 = cc * C, h = cc & 1;
         const __bf16* Qs = stg + h * kBwdStage;
         const __bf16* Ks = Qs + TILE;
@@ -656,9 +675,9 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             }
           }
         });
-        if (WL >= 2 && cc > 0) {
+        if (WL >= 2 && cc > c0) {
           stage(h ^ 1);
-          if (cc > 1) load(cc - 2);
+          if (cc > c0 + 1) load(cc - 2);
         }
         __syncthreads();
       }
@@ -676,8 +695,8 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
     for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        dS[jt][r] = dSfin ? dSfin[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] : 0.f;
-      store_T(dSTb + ((NC - 1) & 1) * TILE, 16 * jt, 16 * wl, g, i, dS[jt]);
+        dS[jt][r] = dSfin ? dSfin[s0off + (16 * wl + 4 * g + r) * DK + 16 * jt + i] : 0.f;
+      store_T(dSTb + (cl & 1) * TILE, 16 * jt, 16 * wl, g, i, dS[jt]);
     }
     // staging: thread b carries 16-byte row segments b and b + 256 of each of V, dO and S_c (waves 6 and 7 stage
     // Q and K)
@@ -704,14 +723,14 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       put_seg(Qs + 4 * TILE, ss1, b + 256);
       if (w == 0) plain_scan(pla, x.l, vec + h * kVec);
     };
-    load(NC - 1);
-    stage((NC - 1) & 1);
-    if (NC > 1) load(NC - 2);
+    load(cl);
+    stage(cl & 1);
+    if (cl > c0) load(cl - 1);
     __syncthreads();
     auto dloop = [&](auto wl_c) {
       constexpr int WL = decltype(wl_c)::value;
       const int me = 16 * WL + i;
-      for (int cc = NC - 1; cc >= 0; --cc) {
+      for (int cc = cl; cc >= c0; --cc) {
         const int t0 = cc * C, h = cc & 1;
         const __bf16* Qs = stg + h * kBwdStage;
         const __bf16* Ks = Qs + TILE;
@@ -839,15 +858,15 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             if constexpr (s == NS - 1) sdot[WL * 64 + x.l] = sd;
           }
         });
-        if (w == 0 && cc < NC - 1) {  // the later chunk's dla, from the other vector set (before the scan below)
+        if (w == 0 && cc < cl) {  // the later chunk's dla, from the other vector set (before the scan below)
           const int tn = t0 + C;
           plain_dla(vec + (h ^ 1) * kVec, x.l,
                     __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T + tn, (short)0, 4 * min(C, T - tn),
                                                       0x00020000));
         }
-        if (cc > 0) {
+        if (cc > c0) {
           stage(h ^ 1);
-          if (cc > 1) load(cc - 2);
+          if (cc > c0 + 1) load(cc - 2);
         }
         __syncthreads();
       }
@@ -858,9 +877,10 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       case 2: dloop(std::integral_constant<int, 2>{}); break;
       default: dloop(std::integral_constant<int, 3>{}); break;
     }
-    if (w == 0)  // chunk 0's dla (vector set 0)
-      plain_dla(vec, x.l, __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T, (short)0, 4 * min(C, T),
-                                                            0x00020000));
+    if (w == 0)  // the first chunk's dla (its vector set)
+      plain_dla(vec + (c0 & 1) * kVec, x.l,
+                __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T + c0 * C, (short)0, 4 * min(C, T - c0 * C),
+                                                  0x00020000));
     if (dS0) {
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt)
@@ -913,8 +933,8 @@ int64_t seg_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t seg_chunks)
 
 }  // namespace
 
-extern "C" int64_t pragnosia_aspin_chunk_fwd_seg_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D,
-                                                                 int64_t chunk, int64_t seg_chunks) {
+extern "C" int64_t pragnosia_aspin_chunk_seg_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D,
+                                                             int64_t chunk, int64_t seg_chunks) {
   if (D != DK || chunk != C || seg_chunks < 1 || !shape_ok(B, H, T, D, chunk)) return -1;
   return seg_workspace_bytes(B, H, T, seg_chunks);
 }
@@ -944,9 +964,9 @@ extern "C" int pragnosia_aspin_chunk_fwd_seg(const void* q, const void* k, const
   float* E = (float*)workspace;
   float* lseg = E + B * H * nseg * DK * DK;
   const unsigned nblk = (unsigned)(B * H * nseg);
-  hipLaunchKernelGGL(aspin_plain_segsum, dim3(nblk), dim3(256), 2 * kSumBuf, (hipStream_t)stream, (const __bf16*)k,
+  hipLaunchKernelGGL(aspin_plain_segsum<true>, dim3(nblk), dim3(256), 2 * kSumBuf, (hipStream_t)stream, (const __bf16*)k,
                      (const __bf16*)v, la, E, lseg, (int)T, NC, (int)seg_chunks);
-  hipLaunchKernelGGL(aspin_plain_segprefix, dim3((unsigned)(B * H * 8)), dim3(256), 0, (hipStream_t)stream, S0,
+  hipLaunchKernelGGL(aspin_plain_segprefix<false>, dim3((unsigned)(B * H * 8)), dim3(256), 0, (hipStream_t)stream, S0,
                      window > 0 ? theta : nullptr, (float)window, (int)(window / C / seg_chunks), E, lseg, S_final,
                      (int)H, (int)nseg);
   hipLaunchKernelGGL(aspin_plain_fwd, dim3(nblk), dim3(kFwdWaves * 64), kFwdSmem, (hipStream_t)stream,
@@ -972,6 +992,39 @@ extern "C" int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const voi
   const int NC = (int)((T + C - 1) / C);
   hipLaunchKernelGGL(aspin_plain_bwd, dim3((unsigned)(B * H)), dim3(512), kBwdSmem, (hipStream_t)stream,
                      (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent,
-                     (const __bf16*)dO, dS_final, (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, dla, dS0, (int)T, NC);
+                     (const __bf16*)dO, dS_final, (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, dla, dS0, (int)T, NC, NC);
+  PGN_RETURN_LAUNCH();
+}
+
+extern "C" int pragnosia_aspin_chunk_bwd_seg(const void* q, const void* k, const void* v, const float* la,
+                                             const void* sent, const void* dO, const float* dS_final, void* dq,
+                                             void* dk, void* dv, float* dla, float* dS0, void* workspace,
+                                             int64_t workspace_bytes, int64_t B, int64_t H, int64_t T, int64_t D,
+                                             int64_t chunk, int64_t seg_chunks, void* stream) {
+  if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
+  PGN_CHECK_ARG(q && k && v && la && sent && dO && dq && dk && dv && dla && workspace);
+  PGN_CHECK_ARG(seg_chunks >= 1 && seg_chunks < ((int64_t)1 << 28));
+  PGN_CHECK_ARG(workspace_bytes >= seg_workspace_bytes(B, H, T, seg_chunks));
+  const int64_t nseg = seg_count(T, seg_chunks);
+  PGN_CHECK_ARG(B * H * nseg < ((int64_t)1 << 31));
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)aspin_plain_bwd, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kBwdSmem);
+    if (e != hipSuccess) return (int)e;
+    attr_set = true;
+  }
+  const int NC = (int)((T + C - 1) / C);
+  float* F = (float*)workspace;
+  float* lseg = F + B * H * nseg * DK * DK;
+  const unsigned nblk = (unsigned)(B * H * nseg);
+  hipLaunchKernelGGL(aspin_plain_segsum<false>, dim3(nblk), dim3(256), 2 * kSumBuf, (hipStream_t)stream,
+                     (const __bf16*)q, (const __bf16*)dO, la, F, lseg, (int)T, NC, (int)seg_chunks);
+  hipLaunchKernelGGL(aspin_plain_segprefix<true>, dim3((unsigned)(B * H * 8)), dim3(256), 0, (hipStream_t)stream,
+                     dS_final, nullptr, 0.f, 1, F, lseg, dS0, (int)H, (int)nseg);
+  hipLaunchKernelGGL(aspin_plain_bwd, dim3(nblk), dim3(512), kBwdSmem, (hipStream_t)stream, (const __bf16*)q,
+                     (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent, (const __bf16*)dO, F,
+                     (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, dla, nullptr, (int)T, NC, (int)seg_chunks);
   PGN_RETURN_LAUNCH();
 }

@@ -144,35 +144,48 @@ COMPUTE_UNITS = 256  # MI355X
 
 
 SEG_MIN_CHUNKS = 2   # shorter segments cost more in start-up than they save (measured)
-SEG_OVERHEAD = 6     # the segment sums and prefix, in chunk steps of the forward (measured)
+# what the segment sums and prefix add, in chunk steps of the kernel they feed: per chunk summed, and fixed
+# (measured; the backward's chunk step is about twice the forward's, so its sums weigh less)
+SEG_COST = {"fwd": (1.0, 6.0), "bwd": (0.4, 3.0)}
 
 
-def seg_chunks(heads: int, NC: int, candidates) -> int:
-    """Chunks per segment for the plain forward over `heads` (batch x head) sequences of NC chunks. Segments are
-    sized so that one round of workgroups covers the compute units (several rounds of shorter segments measured
-    slower), at least SEG_MIN_CHUNKS long, and taken only when the walk they save exceeds what they add: the
-    segment sums walk the segment too, plus a fixed overhead. Returns the largest candidate not above that size, or
-    NC (one workgroup per head, no segments)."""
+def seg_chunks(heads: int, NC: int, candidates, kind: str = "fwd") -> int:
+    """Chunks per segment for the plain forward (or backward) over `heads` (batch x head) sequences of NC chunks.
+    Segments are sized so that one round of workgroups covers the compute units (several rounds of shorter segments
+    measured slower), at least SEG_MIN_CHUNKS long, and taken only when the walk they save exceeds what the segment
+    sums add. Returns the largest candidate not above that size, or NC (one workgroup per head, no segments)."""
+    per_chunk, fixed = SEG_COST[kind]
     nseg = max(1, COMPUTE_UNITS // max(heads, 1))
     want = max(SEG_MIN_CHUNKS, -(-NC // nseg))
     fit = [c for c in candidates if c <= want]
     if not fit:
         return NC
     P = max(fit)
-    if -(-NC // P) < 2 or NC <= 2 * P + SEG_OVERHEAD:
+    if -(-NC // P) < 2 or NC <= P * (1.0 + per_chunk) + fixed:
         return NC
     return P
 
 
 def _aspin_fwd_seg(q, k, v, la, S0, theta, window, o, S, sent, P):
     B, H, T, D = q.shape
-    nbytes = lib().pragnosia_aspin_chunk_fwd_seg_workspace_bytes(B, H, T, D, CHUNK, P)
+    nbytes = lib().pragnosia_aspin_chunk_seg_workspace_bytes(B, H, T, D, CHUNK, P)
     if nbytes < 0:
         raise PragnosiaError(f"aspin segmented forward: shape rejected (B={B} H={H} T={T} D={D} segment={P})")
     ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
     check(lib().pragnosia_aspin_chunk_fwd_seg(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(S0), _ptr(theta), window,
                                               _ptr(o), _ptr(S), _ptr(sent), _ptr(ws), nbytes, B, H, T, D, CHUNK, P,
                                               _stream(q)), "pragnosia_aspin_chunk_fwd_seg")
+
+
+def _aspin_bwd_seg(q, k, v, la, sent, do, dS, dq, dk, dv, dla, dS0, P):
+    B, H, T, D = q.shape
+    nbytes = lib().pragnosia_aspin_chunk_seg_workspace_bytes(B, H, T, D, CHUNK, P)
+    if nbytes < 0:
+        raise PragnosiaError(f"aspin segmented backward: shape rejected (B={B} H={H} T={T} D={D} segment={P})")
+    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+    check(lib().pragnosia_aspin_chunk_bwd_seg(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(sent), _ptr(do), _ptr(dS),
+                                              _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla), _ptr(dS0), _ptr(ws), nbytes,
+                                              B, H, T, D, CHUNK, P, _stream(q)), "pragnosia_aspin_chunk_bwd_seg")
 
 
 @torch.library.custom_op("pragnosia::aspin_chunk_windows", mutates_args=())
@@ -227,6 +240,11 @@ def aspin_chunk_bwd(q: Tensor, k: Tensor, v: Tensor, la: Tensor, sent: Tensor, d
     dq, dk, dv = (torch.empty(B, H, T, D, device=q.device, dtype=torch.bfloat16) for _ in range(3))
     dla = torch.empty(B, H, T, device=q.device, dtype=torch.float32)
     dS0 = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
+    NC = (T + CHUNK - 1) // CHUNK
+    P = seg_chunks(B * H, NC, range(1, NC + 1), "bwd")
+    if P < NC:
+        _aspin_bwd_seg(q, k, v, la, sent, do, dS, dq, dk, dv, dla, dS0, P)
+        return dq, dk, dv, dla, dS0
     check(lib().pragnosia_aspin_chunk_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(sent), _ptr(do), _ptr(dS),
                                           _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla), _ptr(dS0),
                                           B, H, T, D, CHUNK, _stream(q)), "pragnosia_aspin_chunk_bwd")

@@ -60,10 +60,10 @@ def test_segmented_forward_arguments(L):
     """The segmented forward's workspace query and its host-side rejections (no device is touched)."""
     null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
     # B2 H12 T8192: 128 chunks in 16 segments of 8 -> 384 segments of 64 x 64 fp32 plus 384 log-decays
-    assert L.pragnosia_aspin_chunk_fwd_seg_workspace_bytes(2, 12, 8192, 64, 64, 8) == 384 * 16384 + 1536
-    assert L.pragnosia_aspin_chunk_fwd_seg_workspace_bytes(2, 12, 8192, 64, 64, 0) == -1
-    assert L.pragnosia_aspin_chunk_fwd_seg_workspace_bytes(2, 12, 8192, 128, 64, 8) == -1
-    ws = L.pragnosia_aspin_chunk_fwd_seg_workspace_bytes(1, 1, 1000, 64, 64, 3)
+    assert L.pragnosia_aspin_chunk_seg_workspace_bytes(2, 12, 8192, 64, 64, 8) == 384 * 16384 + 1536
+    assert L.pragnosia_aspin_chunk_seg_workspace_bytes(2, 12, 8192, 64, 64, 0) == -1
+    assert L.pragnosia_aspin_chunk_seg_workspace_bytes(2, 12, 8192, 128, 64, 8) == -1
+    ws = L.pragnosia_aspin_chunk_seg_workspace_bytes(1, 1, 1000, 64, 64, 3)
     assert ws == 6 * 16384 + 256
     args = lambda th, win, wsb, sc: (one, one, one, one, null, th, win, one, one, null, one, wsb, 1, 1, 1000, 64, 64,
                                      sc, null)
@@ -73,6 +73,11 @@ def test_segmented_forward_arguments(L):
     assert L.pragnosia_aspin_chunk_fwd_seg(*args(one, 100, ws, 3)) == -1          # window not a multiple of 64
     assert L.pragnosia_aspin_chunk_fwd_seg(*args(one, 128, ws, 3)) == -1          # window not whole segments
     assert L.pragnosia_aspin_chunk_fwd_seg(*args(one, -64, ws, 3)) == -1
+    bargs = lambda wsb, sc: ([one] * 11 + [null, one], wsb, 1, 1, 1000, 64, 64, sc, null)
+    flat = lambda a: (*a[0], *a[1:])
+    assert L.pragnosia_aspin_chunk_bwd_seg(*flat(bargs(ws - 1, 3))) == -1           # workspace too small
+    assert L.pragnosia_aspin_chunk_bwd_seg(*flat(bargs(ws, 0))) == -1               # empty segments
+    assert L.pragnosia_aspin_chunk_bwd_seg(*([one] * 13), ws, 1, 1, 1000, 128, 64, 3, null) == -2   # head dim
 
 
 def test_product_never_imports_oracle():

@@ -124,6 +124,51 @@ def test_policy_routes_few_heads_to_segments():
         assert rel(a.grad, b.grad) < 5e-2
 
 
+def _bwd(q, k, v, la, sent, do, dS, P):
+    """The backward through the C ABI: sequential kernel (P = None) or segments of P chunks."""
+    from pragnosia_amd import ops
+    from pragnosia_amd._lib import check, lib
+    from pragnosia_amd.ops import _ptr, _stream
+    B, H, T, D = q.shape
+    dq, dk, dv = (torch.empty(B, H, T, D, device="cuda", dtype=torch.bfloat16) for _ in range(3))
+    dla = torch.empty(B, H, T, device="cuda")
+    dS0 = torch.empty(B, H, D, D, device="cuda")
+    if P is None:
+        check(lib().pragnosia_aspin_chunk_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(sent), _ptr(do), _ptr(dS),
+                                              _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla), _ptr(dS0), B, H, T, D, 64,
+                                              _stream(q)), "pragnosia_aspin_chunk_bwd")
+    else:
+        ops._aspin_bwd_seg(q, k, v, la, sent, do, dS, dq, dk, dv, dla, dS0, P)
+    return dq, dk, dv, dla, dS0
+
+
+@pytest.mark.parametrize("B,H,T,P", [(1, 2, 70 * 64 - 17, 8), (1, 2, 70 * 64 - 17, 1), (2, 3, 333, 2),
+                                     (1, 1, 64 * 9, 4), (3, 1, 64 * 9, 9), (1, 2, 40, 1)])
+def test_segmented_backward_matches_oracle_and_sequential(B, H, T, P):
+    """Every gradient (q, k, v, la, S0) of the segmented backward, with and without an upstream gradient on the
+    final state, against the fp64 oracle's autograd and against the sequential backward on the same saved states."""
+    for with_dS in (True, False):
+        q, k, v, la, S0 = _inputs(B, H, T, seed=3 * T + P + with_dS)
+        g = torch.Generator().manual_seed(T + P)
+        wo = torch.randn(q.shape, generator=g)
+        wS = torch.randn(B, H, 64, 64, generator=g) if with_dS else None
+        r = [t.double().requires_grad_(True) for t in (q.bfloat16(), k.bfloat16(), v.bfloat16(), la, S0)]
+        yr, Sr = O.assoc_scan(*r, chunk=64)
+        ((yr * wo.double()).sum() + ((Sr * wS.double()).sum() if with_dS else 0)).backward()
+        with torch.no_grad():
+            dev = [t.cuda().bfloat16().contiguous() for t in (q, k, v)] + [la.cuda(), S0.cuda()]
+            _, _, sent = _sequential_forward(q, k, v, la, S0)
+            do = wo.cuda().bfloat16().contiguous()
+            dS = wS.cuda() if with_dS else None
+            seg = _bwd(*dev[:4], sent, do, dS, P)
+            seq = _bwd(*dev[:4], sent, do, dS, None)
+        errs = {}
+        for n, a, b, c in zip(("dq", "dk", "dv", "dla", "dS0"), seg, seq, r):
+            errs[n] = rel(a, c.grad)
+            errs[n + "_vs_seq"] = rel(a, b)
+        assert max(errs.values()) < 5e-2, errs
+
+
 def _window_loop_oracle(q, k, v, la, S0, theta, W):
     """The reference's carried windows on the oracle: one two-pass scan per window, the state rebased by -W theta
     between windows (q and k already rotated with positions restarting per window)."""

@@ -25,3 +25,12 @@ def test_few_heads_over_many_chunks_split():
 def test_single_chunk_and_single_candidate():
     assert seg_chunks(1, 1, [1]) == 1
     assert seg_chunks(4, 3, []) == 3
+
+
+def test_backward_splits_sooner():
+    # the backward's chunk step is heavier, so 96 heads of 16 chunks split for it (measured 41.8 -> 36.8 us) but
+    # not for the forward (22.6 us sequential vs 26 segmented); 128 heads of 8 chunks split for neither
+    assert seg_chunks(96, 16, range(1, 17), "bwd") == 8
+    assert seg_chunks(96, 16, range(1, 17), "fwd") == 16
+    assert seg_chunks(128, 8, range(1, 9), "bwd") == 8
+    assert seg_chunks(192, 8, range(1, 9), "bwd") == 8
