@@ -309,6 +309,66 @@ def carried_bench():
             "carried_vs_unsplit_rel_err_S": round(rel(Sc, Su_loc), 6)}
 
 
+def carrier_layer_bench(steps=20):
+    """The carrier layer around the scan at configs[2]'s shape: AssocCarrier(768) (12 heads of 64, plain rule) forward
+    + backward on x (B16, T512, 768) under bf16 autocast, fp32 parameters: LayerNorm, the q/k/v and gate
+    projections, the decay, prep, the chunked scan, the output epilogue and the gated o-projection with its
+    residual. Reported eagerly (host dispatch included) and as HIP-graph replays of the whole step (device time),
+    with the output epilogue fused (this build) and as the reference's torch composition."""
+    import torch
+    from pragnosia_amd import assoc
+    torch.manual_seed(7)
+    B, T, d = 16, 512, 768
+    m = assoc.AssocCarrier(d).cuda()
+    x = torch.randn(B, T, d, device="cuda", requires_grad=True)
+    gy = torch.randn(B, T, d, device="cuda")
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y, _ = m(x)
+        y.backward(gy)
+
+    out = {"workload": "AssocCarrier(768) layer fwd+bwd, B16 T512, bf16 autocast (configs[2] shape)"}
+    prev = assoc.FUSED_EPILOGUE
+    try:
+        for name, fused in (("fused_epilogue", True), ("torch_epilogue", False)):
+            assoc.FUSED_EPILOGUE = fused
+            for p in list(m.parameters()) + [x]:
+                p.grad = None
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    step()
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            eager = (time.perf_counter() - t0) / steps
+            for p in list(m.parameters()) + [x]:
+                p.grad = None
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step()
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            dev = e0.elapsed_time(e1) / steps * 1e-3
+            out[name] = {"graph_ms_per_step": round(dev * 1e3, 4), "graph_Mtok_s": round(B * T / dev / 1e6, 3),
+                         "eager_ms_per_step": round(eager * 1e3, 4)}
+            del g
+    finally:
+        assoc.FUSED_EPILOGUE = prev
+    return out
+
+
 def decode_bench(n_tokens=1024):
     """LM(vocab 8192, d 768, 12 layers, 12 heads of 64, ctx 512, aspin), random-init weights
     N(0, 0.02) (fp32), prefill of 512 random ids, then greedy decode through the graph-captured recurrent step, at
@@ -458,6 +518,7 @@ def gpu_bench(args):
             "op": op_roofline(o)}}
         sec["diag_scan"] = diag_bench(args.steps)
         sec["carried"] = carried_bench()
+        sec["carrier_layer"] = carrier_layer_bench()
         sec["decode"] = decode_bench()
         sec["lds_contraction"] = lds_contraction_bench()
         res["decode_ms_per_token_bs1"] = sec["decode"]["ms_per_token_bs1"]

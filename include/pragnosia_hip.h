@@ -102,6 +102,23 @@ int pragnosia_aspin_chunk_bwd_seg(const void* q, const void* k, const void* v, c
                                   float* dS0, void* workspace, int64_t workspace_bytes, int64_t B, int64_t H,
                                   int64_t T, int64_t D, int64_t chunk, int64_t seg_chunks, void* stream);
 
+/* The carrier's output epilogue (head dim D = 64): per (batch, head, token) row x of the scan output o
+ * ((B, H, T, D) bf16), r = 1 / sqrt(mean(x^2) + eps) and y[b, t, h D + d] = (x_d r) w_d, rounded once to y's dtype
+ * (bf16 if y_bf16, else fp32) and written token-major, (B, T, H D); r is written to rstd ((B, H, T) fp32) for the
+ * backward. weight: (D) fp32. Replaces `self.on(o).transpose(1, 2).reshape(B, T, D)` of src/assoc.py:505
+ * (nn.RMSNorm(dk) with eps=None, i.e. fp32 epsilon, computed in fp32). */
+int pragnosia_aspin_out_fwd(const void* o, const float* weight, float eps, void* y, int y_bf16, float* rstd,
+                            int64_t B, int64_t H, int64_t T, int64_t D, void* stream);
+
+/* Rows of 64 fp32 partial weight gradients pragnosia_aspin_out_bwd writes (-1 if the shape is rejected). */
+int64_t pragnosia_aspin_out_weight_partials(int64_t B, int64_t H, int64_t T);
+
+/* Backward of pragnosia_aspin_out_fwd: gy (B, T, H D), bf16 if gy_bf16 else fp32; o, weight, rstd as the forward.
+ * Writes dO ((B, H, T, D) bf16, the scan's output gradient) and dw_partials (pragnosia_aspin_out_weight_partials(...)
+ * rows of D fp32; the weight gradient is their sum over rows). Replaces the autograd backward of the same lines. */
+int pragnosia_aspin_out_bwd(const void* gy, int gy_bf16, const void* o, const float* weight, const float* rstd,
+                            void* dO, float* dw_partials, int64_t B, int64_t H, int64_t T, int64_t D, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Associative carrier, DELTA write rule, chunked scan (chunk = 64, head dim D = 64), per (batch, head):
  *     S_t = a_t S_{t-1} + beta_t k_t (v_t - (a_t S_{t-1})^T k_t)^T,   o_t = S_t^T q_t,   a_t = exp(la_t).

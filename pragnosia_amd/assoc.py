@@ -19,7 +19,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import ops  # noqa: F401  (registers torch.ops.pragnosia.*)
+from . import ops as _op_mod  # registers torch.ops.pragnosia.*
 from ._lib import PragnosiaError
 
 _op = torch.ops.pragnosia
@@ -29,6 +29,9 @@ _op = torch.ops.pragnosia
 # kernel runs without writing them). FUSED_PROJ: one GEMM for the delta carrier's five input projections.
 FUSED_SCAN = False
 FUSED_PROJ = False
+# This build's own switch: the per-head RMSNorm and the transpose after the scan as one kernel each way (True), or
+# the torch composition the reference uses (nn.RMSNorm, transpose, reshape; kept for comparison)
+FUSED_EPILOGUE = True
 
 HEAD_DIM_KERNEL = 64
 _POS_CACHE: dict = {}
@@ -181,6 +184,16 @@ class AssocCarrier(nn.Module):
                 bt = bt.clamp(min=0.75)
         return qo.view(B, T, self.h, self.dk), kp, vo.view(B, T, self.h, self.dk), gate, la, bt
 
+    def _epilogue(self, o, dtype):
+        """`self.on(o.to(dtype)).transpose(1, 2).reshape(B, T, D)` (`src/assoc.py:500-505`) for the scan's bf16 output
+        o (B, H, T, dk): one kernel each way (per-head RMSNorm in fp32, rounded once to `dtype`, written token-major)."""
+        B, H, T, Dk = o.shape
+        if (FUSED_EPILOGUE and dtype in (torch.bfloat16, torch.float32) and self.on.weight is not None
+                and Dk == HEAD_DIM_KERNEL):
+            eps = self.on.eps if self.on.eps is not None else _op_mod.RMS_EPS
+            return _op.aspin_out(o, self.on.weight, eps, dtype == torch.bfloat16)[0]
+        return self.on(o.to(dtype)).transpose(1, 2).reshape(B, T, H * Dk)
+
     def forward(self, x, h0=None, pos0: int = 0):
         """x (B, T, d); h0 = (S (B, H, dk, dk) fp32, p0) from a previous call, or None. Returns
         (x + gated output, (S, p0 + T)); positions restart at 0 every call and the carried state is rebased by -p0."""
@@ -221,10 +234,9 @@ class AssocCarrier(nn.Module):
                                                    bt.transpose(1, 2).float(), S0, want)
             else:
                 o, S, sent = _op.aspin_chunk(q, k, v, la.transpose(1, 2).float(), S0, want)
-            o = o.to(qp.dtype)
             sent = sent if want else None
         self.sent = sent
-        o = self.on(o).transpose(1, 2).reshape(B, T, D)
+        o = self.on(o).transpose(1, 2).reshape(B, T, D) if decode else self._epilogue(o, qp.dtype)
         if _needs_grad(x, o, self.o.weight, self.gate):
             # gate on the weight, as the reference does for training (it keeps the backward's saved tensor small)
             out = x + F.linear(o, self.o.weight * torch.sigmoid(self.gate))
@@ -270,7 +282,7 @@ class AssocCarrier(nn.Module):
         q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
         o, S, _ = _op.aspin_chunk_windows(q, k, v, la.transpose(1, 2).float(), S0, self.theta, window, False)
         self.sent = None
-        o = self.on(o.to(qp.dtype)).transpose(1, 2).reshape(B, T, D)
+        o = self._epilogue(o, qp.dtype)
         out = x + F.linear(o, self.o.weight) * torch.sigmoid(self.gate)
         last = T - window * ((T - 1) // window)
         return out, (S, p0 * 0 + last if torch.is_tensor(p0) else last)

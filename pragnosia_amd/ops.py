@@ -109,6 +109,68 @@ diag_scan.register_autograd(_diag_backward, setup_context=_diag_setup)
 
 
 # ---------------------------------------------------------------------------------------------------------------
+# the carrier's output epilogue: replaces `self.on(o).transpose(1, 2).reshape(B, T, D)`, src/assoc.py:505
+RMS_EPS = torch.finfo(torch.float32).eps  # nn.RMSNorm(eps=None) computes in fp32 with fp32's epsilon
+
+
+@torch.library.custom_op("pragnosia::aspin_out", mutates_args=())
+def aspin_out(o: Tensor, weight: Tensor, eps: float, out_bf16: bool) -> tuple[Tensor, Tensor]:
+    """Per-head RMSNorm of the scan output o (B, H, T, 64) (cast to bf16) with `weight` (64,), written token-major
+    as (B, T, H * 64) in bf16 (out_bf16) or fp32. Returns (y, rstd (B, H, T) fp32, saved for the backward)."""
+    _require_gpu(o, weight)
+    o, weight = _bf16(o), _f32(weight)
+    B, H, T, D = o.shape
+    y = torch.empty(B, T, H * D, device=o.device, dtype=torch.bfloat16 if out_bf16 else torch.float32)
+    rstd = torch.empty(B, H, T, device=o.device, dtype=torch.float32)
+    check(lib().pragnosia_aspin_out_fwd(_ptr(o), _ptr(weight), float(eps), _ptr(y), int(out_bf16), _ptr(rstd),
+                                        B, H, T, D, _stream(o)), "pragnosia_aspin_out_fwd")
+    return y, rstd
+
+
+@aspin_out.register_fake
+def _(o, weight, eps, out_bf16):
+    B, H, T, D = o.shape
+    return (o.new_empty(B, T, H * D, dtype=torch.bfloat16 if out_bf16 else torch.float32),
+            o.new_empty(B, H, T, dtype=torch.float32))
+
+
+@torch.library.custom_op("pragnosia::aspin_out_bwd", mutates_args=())
+def aspin_out_bwd(gy: Tensor, o: Tensor, weight: Tensor, rstd: Tensor) -> tuple[Tensor, Tensor]:
+    """Backward of aspin_out. gy (B, T, H * 64) bf16 or fp32. Returns (dO (B, H, T, 64) bf16, dweight (64,) fp32)."""
+    _require_gpu(gy, o, weight, rstd)
+    gy = gy.contiguous() if gy.dtype in (torch.bfloat16, torch.float32) else gy.float().contiguous()
+    o, weight, rstd = _bf16(o), _f32(weight), _f32(rstd)
+    B, H, T, D = o.shape
+    dO = torch.empty(B, H, T, D, device=o.device, dtype=torch.bfloat16)
+    n = lib().pragnosia_aspin_out_weight_partials(B, H, T)
+    part = torch.empty(n, D, device=o.device, dtype=torch.float32)
+    check(lib().pragnosia_aspin_out_bwd(_ptr(gy), int(gy.dtype == torch.bfloat16), _ptr(o), _ptr(weight), _ptr(rstd),
+                                        _ptr(dO), _ptr(part), B, H, T, D, _stream(o)), "pragnosia_aspin_out_bwd")
+    return dO, part.sum(0)
+
+
+@aspin_out_bwd.register_fake
+def _(gy, o, weight, rstd):
+    return o.new_empty(o.shape, dtype=torch.bfloat16), o.new_empty(o.shape[-1], dtype=torch.float32)
+
+
+def _out_setup(ctx, inputs, output):
+    o, weight, eps, out_bf16 = inputs
+    _, rstd = output
+    ctx.save_for_backward(o, weight, rstd)
+    ctx.mark_non_differentiable(rstd)
+
+
+def _out_backward(ctx, gy, _grstd):
+    o, weight, rstd = ctx.saved_tensors
+    dO, dw = aspin_out_bwd(gy, o, weight, rstd)
+    return dO.to(o.dtype), dw.to(weight.dtype), None, None
+
+
+aspin_out.register_autograd(_out_backward, setup_context=_out_setup)
+
+
+# ---------------------------------------------------------------------------------------------------------------
 # aspin chunked scan, plain rule: replaces assoc_scan_kernel and its ops, src/assoc_kernel.py:128-323
 CHUNK = 64
 
