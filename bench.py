@@ -314,7 +314,8 @@ def carrier_layer_bench(steps=20):
     + backward on x (B16, T512, 768) under bf16 autocast, fp32 parameters: LayerNorm, the q/k/v and gate
     projections, the decay, prep, the chunked scan, the output epilogue and the gated o-projection with its
     residual. Reported eagerly (host dispatch included) and as HIP-graph replays of the whole step (device time),
-    with the output epilogue fused (this build) and as the reference's torch composition."""
+    with this build's fused plumbing (one projection GEMM feeding one prep kernel, fused output epilogue) and as the
+    reference's torch composition around the same scan kernels."""
     import torch
     from pragnosia_amd import assoc
     torch.manual_seed(7)
@@ -329,10 +330,10 @@ def carrier_layer_bench(steps=20):
         y.backward(gy)
 
     out = {"workload": "AssocCarrier(768) layer fwd+bwd, B16 T512, bf16 autocast (configs[2] shape)"}
-    prev = assoc.FUSED_EPILOGUE
+    prev = assoc.FUSED_PLUMBING
     try:
-        for name, fused in (("fused_epilogue", True), ("torch_epilogue", False)):
-            assoc.FUSED_EPILOGUE = fused
+        for name, fused in (("fused_plumbing", True), ("torch_plumbing", False)):
+            assoc.FUSED_PLUMBING = fused
             for p in list(m.parameters()) + [x]:
                 p.grad = None
             side = torch.cuda.Stream()
@@ -365,7 +366,7 @@ def carrier_layer_bench(steps=20):
                          "eager_ms_per_step": round(eager * 1e3, 4)}
             del g
     finally:
-        assoc.FUSED_EPILOGUE = prev
+        assoc.FUSED_PLUMBING = prev
     return out
 
 

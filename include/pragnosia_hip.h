@@ -150,24 +150,54 @@ int pragnosia_aspin_delta_bwd(const void* q, const void* k, const void* v, const
  * The plumbing between the carrier's projections and the scan (head dim D = 64): per (b, t, h) row, unit-normalise
  * q, k, v (x / max(|x|, 1e-12)), scale k by sigmoid(gate) when `gate` is non-NULL (plain rule), rotate q and k on
  * interleaved channel pairs (2i, 2i+1) by pos[t] * theta[h, i], cast to bf16 and transpose to the scan layout.
- * qp, kp, vp: (B, T, H, D), fp32 (in_bf16 = 0) or bf16 (in_bf16 = 1); gate: (B, T, H) fp32 or NULL; theta: (H, D/2)
- * fp32; pos: (T,) int64. Writes q, k, v: (B, H, T, D) bf16. Replaces `prep_kernel` / `_prep_fwd` of
- * src/assoc_kernel.py:740-769, :828-891 (torch form src/assoc.py:453-460). */
+ * qp, kp, vp: (B, T, H, D) with consecutive tokens `in_stride` elements apart (H * D when dense; larger when they are
+ * column slices of one wider row, e.g. one GEMM's output holding all projections), fp32 (in_bf16 = 0) or bf16
+ * (in_bf16 = 1); gate: (B, T, H) fp32 or NULL; theta: (H, D/2) fp32; pos: (T,) int64. Writes q, k, v: (B, H, T, D)
+ * bf16. Replaces `prep_kernel` / `_prep_fwd` of src/assoc_kernel.py:740-769, :828-891 (torch form
+ * src/assoc.py:453-460). */
 int pragnosia_aspin_prep_fwd(const void* qp, const void* kp, const void* vp, const float* gate, const float* theta,
                              const int64_t* pos, void* q, void* k, void* v, int64_t B, int64_t T, int64_t H,
-                             int64_t D, int in_bf16, void* stream);
+                             int64_t D, int64_t in_stride, int in_bf16, void* stream);
 
 /* Rows of the theta-gradient partial buffer of pragnosia_aspin_prep_bwd: (rows, H, D/2) fp32, summed by the caller. */
 int64_t pragnosia_aspin_prep_theta_partials(int64_t B, int64_t T);
 
 /* Backward of pragnosia_aspin_prep_fwd: from dq, dk, dv ((B, H, T, D) bf16) writes dqp, dkp, dvp in the projections'
- * layout and dtype, dgate ((B, T, H) fp32, required iff gate is non-NULL) and dtheta_partial
+ * layout, stride and dtype, dgate ((B, T, H) fp32, required iff gate is non-NULL) and dtheta_partial
  * ((pragnosia_aspin_prep_theta_partials(B, T), H, D/2) fp32; theta's gradient is its sum over the first dim).
  * Replaces `_prep_bwd` of src/assoc_kernel.py:772-822, :848-885. */
 int pragnosia_aspin_prep_bwd(const void* qp, const void* kp, const void* vp, const float* gate, const float* theta,
                              const int64_t* pos, const void* dq, const void* dk, const void* dv, void* dqp,
                              void* dkp, void* dvp, float* dgate, float* dtheta_partial, int64_t B, int64_t T,
-                             int64_t H, int64_t D, int in_bf16, void* stream);
+                             int64_t H, int64_t D, int64_t in_stride, int in_bf16, void* stream);
+
+/* The same plumbing fed by ONE GEMM's output P (B, T, stride) (fp32, or bf16 if in_bf16) holding, per token, the q,
+ * k and v projections in columns [0, H D), [H D, 2 H D), [2 H D, 3 H D), the decay logits (before bias) in columns
+ * [la_col, la_col + H) and, when gate_col >= 0, the write-gate logits (before bias) in [gate_col, gate_col + H).
+ * Besides q, k, v (as pragnosia_aspin_prep_fwd, gate = sigmoid(logit + gate_bias[h])), writes the decay in the scan's
+ * layout, la (B, H, T) fp32: la = -softplus(logit + la_bias[h]) exp(A[h]), floored at la_floor[h] when la_floor is
+ * non-NULL. la_bias, A, la_floor, gate_bias: (H) fp32 (gate_bias may be NULL: no bias). Replaces the carrier's
+ * separate q/k/v/gate projections' consumers: `logalpha` (src/assoc.py:355-359), the write gate
+ * (src/assoc.py:458-459) and `prep_kernel` (src/assoc_kernel.py:740-769), with the transpose of la for the scan. */
+int pragnosia_aspin_prep_proj_fwd(const void* P, int64_t stride, int64_t la_col, int64_t gate_col,
+                                  const float* la_bias, const float* A, const float* la_floor,
+                                  const float* gate_bias, const float* theta, const int64_t* pos, void* q, void* k,
+                                  void* v, float* la, int64_t B, int64_t T, int64_t H, int64_t D, int in_bf16,
+                                  void* stream);
+
+/* Rows of 3 fp32 per-head partial sums pragnosia_aspin_prep_proj_bwd writes (-1 if the shape is rejected). */
+int64_t pragnosia_aspin_prep_proj_partials(int64_t B, int64_t T, int64_t H);
+
+/* Backward of pragnosia_aspin_prep_proj_fwd: from dq, dk, dv ((B, H, T, D) bf16) and dla ((B, H, T) fp32) writes the
+ * q, k, v, decay and gate columns of dP (P's layout, stride and dtype; other columns untouched), theta's partials
+ * (as pragnosia_aspin_prep_bwd) and `part`: pragnosia_aspin_prep_proj_partials(B, T, H) rows, row (b H + h) ntb + j
+ * holding (d gate_bias[h], d la_bias[h], dA[h]) partial sums (ntb = ceil(T / 64)); the caller sums them per head. */
+int pragnosia_aspin_prep_proj_bwd(const void* P, int64_t stride, int64_t la_col, int64_t gate_col,
+                                  const float* la_bias, const float* A, const float* la_floor,
+                                  const float* gate_bias, const float* theta, const int64_t* pos, const void* dq,
+                                  const void* dk, const void* dv, const float* dla, void* dP, float* dtheta_partial,
+                                  float* part, int64_t B, int64_t T, int64_t H, int64_t D, int in_bf16,
+                                  void* stream);
 
 /* The carried-state rebase of src/assoc.py:399-402: S (B, H, D, D) fp32 with keys on dim 2; key rows (2i, 2i+1) are
  * rotated by -p0 * theta[h, i], p0 = *p0_dev when p0_dev is non-NULL (a device fp32 scalar, as the graphed decode

@@ -29,9 +29,12 @@ _op = torch.ops.pragnosia
 # kernel runs without writing them). FUSED_PROJ: one GEMM for the delta carrier's five input projections.
 FUSED_SCAN = False
 FUSED_PROJ = False
-# This build's own switch: the per-head RMSNorm and the transpose after the scan as one kernel each way (True), or
-# the torch composition the reference uses (nn.RMSNorm, transpose, reshape; kept for comparison)
-FUSED_EPILOGUE = True
+# This build's own switch for the plumbing around the plain-rule scan. True: one GEMM for the q, k, v, decay and
+# write-gate projections, one kernel from its output to the scan's inputs (normalise, gate, rotate, decay, cast,
+# transpose), and the per-head RMSNorm and transpose after the scan as one kernel, each with its own backward.
+# False: the torch composition the reference uses (separate projections, elementwise decay and gate, nn.RMSNorm,
+# transposes), kept for comparison.
+FUSED_PLUMBING = True
 
 HEAD_DIM_KERNEL = 64
 _POS_CACHE: dict = {}
@@ -184,11 +187,30 @@ class AssocCarrier(nn.Module):
                 bt = bt.clamp(min=0.75)
         return qo.view(B, T, self.h, self.dk), kp, vo.view(B, T, self.h, self.dk), gate, la, bt
 
+    def _scan_inputs(self, z, pos):
+        """The scan's inputs from the normalised layer input z (B, T, d): q, k, v (B, H, T, dk) bf16, la and beta
+        (B, H, T) fp32 (beta None for the plain rule), and the projections' dtype. With FUSED_PLUMBING (plain rule,
+        no key_topk): one GEMM for the q, k, v, decay and write-gate projections and one kernel from its output;
+        otherwise the reference's composition: separate projections, elementwise decay and gate, prep."""
+        if FUSED_PLUMBING and not self.delta and not self.key_topk and self.dk == HEAD_DIM_KERNEL:
+            gated = not self.write_all
+            W = torch.cat([self.q.weight, self.k.weight, self.v.weight, self.wa.weight] +
+                          ([self.wi.weight] if gated else []))
+            P = F.linear(z, W)
+            q, k, v, la = _op.aspin_prep_proj(P, self.h, self.wa.bias, self.A,
+                                              self.la_floor if self.hl_floor else None,
+                                              self.wi.bias if gated else None, self.theta, pos)
+            return q, k, v, la, None, P.dtype
+        qp, kp, vp, gate, la, bt = self._projections(z)
+        q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
+        bt = None if bt is None else bt.transpose(1, 2).float()
+        return q, k, v, la.transpose(1, 2).float(), bt, qp.dtype
+
     def _epilogue(self, o, dtype):
         """`self.on(o.to(dtype)).transpose(1, 2).reshape(B, T, D)` (`src/assoc.py:500-505`) for the scan's bf16 output
         o (B, H, T, dk): one kernel each way (per-head RMSNorm in fp32, rounded once to `dtype`, written token-major)."""
         B, H, T, Dk = o.shape
-        if (FUSED_EPILOGUE and dtype in (torch.bfloat16, torch.float32) and self.on.weight is not None
+        if (FUSED_PLUMBING and dtype in (torch.bfloat16, torch.float32) and self.on.weight is not None
                 and Dk == HEAD_DIM_KERNEL):
             eps = self.on.eps if self.on.eps is not None else _op_mod.RMS_EPS
             return _op.aspin_out(o, self.on.weight, eps, dtype == torch.bfloat16)[0]
@@ -209,11 +231,11 @@ class AssocCarrier(nn.Module):
         else:
             S0, p0 = h0
         z = self.ln(x)
-        qp, kp, vp, gate, la, bt = self._projections(z)
         p_dev = p0.float().reshape(()) if torch.is_tensor(p0) else None
         p_host = 0.0 if torch.is_tensor(p0) else float(p0)
         decode = T == 1 and not _needs_grad(x, S0, *self.parameters())
         if decode:
+            qp, kp, vp, gate, la, bt = self._projections(z)
             S_prev = S0 if S0 is not None else torch.zeros(B, self.h, self.dk, self.dk, device=x.device)
             S, o = _op.aspin_decode_step(S_prev, qp.reshape(B, self.h, self.dk), kp.reshape(B, self.h, self.dk),
                                          vp.reshape(B, self.h, self.dk),
@@ -226,17 +248,16 @@ class AssocCarrier(nn.Module):
             if S0 is not None and (p_dev is not None or p_host != 0.0):
                 S0 = _op.aspin_rebase(S0, self.theta, p_dev, p_host)
             pos = _positions(T, x.device, getattr(self, "pos_wrap", None))
-            q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
+            q, k, v, la, bt, dtype = self._scan_inputs(z, pos)
             want = bool(self.need_sent or not (FUSED_SCAN and self.delta) or
                         _needs_grad(x, S0, *self.parameters()))
             if self.delta:
-                o, S, sent, _, _ = _op.aspin_delta(q, k, v, la.transpose(1, 2).float(),
-                                                   bt.transpose(1, 2).float(), S0, want)
+                o, S, sent, _, _ = _op.aspin_delta(q, k, v, la, bt, S0, want)
             else:
-                o, S, sent = _op.aspin_chunk(q, k, v, la.transpose(1, 2).float(), S0, want)
+                o, S, sent = _op.aspin_chunk(q, k, v, la, S0, want)
             sent = sent if want else None
         self.sent = sent
-        o = self.on(o).transpose(1, 2).reshape(B, T, D) if decode else self._epilogue(o, qp.dtype)
+        o = self.on(o).transpose(1, 2).reshape(B, T, D) if decode else self._epilogue(o, dtype)
         if _needs_grad(x, o, self.o.weight, self.gate):
             # gate on the weight, as the reference does for training (it keeps the backward's saved tensor small)
             out = x + F.linear(o, self.o.weight * torch.sigmoid(self.gate))
@@ -270,7 +291,6 @@ class AssocCarrier(nn.Module):
         else:
             S0, p0 = h0
         z = self.ln(x)
-        qp, kp, vp, gate, la, _ = self._projections(z)
         p_dev = p0.float().reshape(()) if torch.is_tensor(p0) else None
         p_host = 0.0 if torch.is_tensor(p0) else float(p0)
         if S0 is not None and (p_dev is not None or p_host != 0.0):
@@ -279,10 +299,10 @@ class AssocCarrier(nn.Module):
         wrap = getattr(self, "pos_wrap", None)
         if wrap:
             pos = pos % wrap
-        q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
-        o, S, _ = _op.aspin_chunk_windows(q, k, v, la.transpose(1, 2).float(), S0, self.theta, window, False)
+        q, k, v, la, _, dtype = self._scan_inputs(z, pos)
+        o, S, _ = _op.aspin_chunk_windows(q, k, v, la, S0, self.theta, window, False)
         self.sent = None
-        o = self._epilogue(o, qp.dtype)
+        o = self._epilogue(o, dtype)
         out = x + F.linear(o, self.o.weight) * torch.sigmoid(self.gate)
         last = T - window * ((T - 1) // window)
         return out, (S, p0 * 0 + last if torch.is_tensor(p0) else last)

@@ -11,7 +11,9 @@
 // (batch, 64-token block) that the caller reduces.
 //
 // One workgroup of 256 threads per (batch, head, 64-token block): 32 threads per row (one channel pair each), 8 rows
-// per pass, 8 passes. Row loads are 128 or 256 contiguous bytes; normalisation is a 32-lane butterfly.
+// per pass, 8 passes. Row loads are 128 or 256 contiguous bytes; normalisation is a 32-lane butterfly. The projections
+// (and their gradients) may be column slices of one wider row per token (`in_stride` elements apart), such as one
+// GEMM's output holding q, k, v and the gate logits side by side.
 //
 // rebase: S (B, H, Dk, Dv) with keys on dim 2; key rows (2i, 2i+1) are rotated by -p0 * theta[h, i] (the state written
 // at positions up to p0 - 1, re-expressed for a window whose positions restart at 0: `src/assoc.py:399-402`).
@@ -59,22 +61,42 @@ PGN_DEVICE float sum32(float x) {
 
 PGN_DEVICE float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
 
+// softplus with torch's default threshold: x above 20 passes through
+PGN_DEVICE float softplusf_(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+
+// The decay and write gate taken from columns of the projections' rows (a single GEMM's output): per (b, t, h) the
+// decay logit at acol[row + h] and the gate logit at gcol[row + h] (row = (b T + t) * S), each plus its bias.
+// la = -softplus(logit + abias[h]) exp(A[h]), floored at floor[h] when given (`src/assoc.py:355-359`); the gate is
+// sigmoid(logit + gbias[h]) (`src/assoc.py:458-459`).
+template <typename In>
+struct Cols {
+  const In* acol;       // decay logits, or NULL (then no la)
+  const float* abias;   // (H)
+  const float* A;       // (H) log-timescales
+  const float* floor;   // (H) or NULL
+  const In* gcol;       // gate logits, or NULL (then the separate fp32 gate, if any)
+  const float* gbias;   // (H) or NULL
+};
+
 template <typename In>
 __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const In* __restrict__ kp,
                                                 const In* __restrict__ vp, const float* __restrict__ gl,
                                                 const float* __restrict__ theta, const int64_t* __restrict__ pos,
                                                 __bf16* __restrict__ q, __bf16* __restrict__ k,
-                                                __bf16* __restrict__ v, int T, int H, int ntb) {
+                                                __bf16* __restrict__ v, int T, int H, int ntb, int64_t S,
+                                                Cols<In> cols, float* __restrict__ la) {
   const int blk = blockIdx.x;
   const int bh = blk / ntb, tb = blk - bh * ntb;
   const int b = bh / H, h = bh - b * H;
   const int i = threadIdx.x & 31, rs = threadIdx.x >> 5;
   const float th = theta[h * (D / 2) + i];
+  const float eA = cols.acol ? __expf(cols.A[h]) : 0.f;
 #pragma unroll 2
   for (int p = 0; p < TB / ROWS; ++p) {
     const int t = tb * TB + p * ROWS + rs;
     if (t >= T) break;
-    const size_t in = (((size_t)b * T + t) * H + h) * D + 2 * i;
+    const size_t row = ((size_t)b * T + t) * S;
+    const size_t in = row + h * D + 2 * i;
     const size_t out = ((size_t)bh * T + t) * D + 2 * i;
     const float2 xq = ld2<In>(qp + in), xk = ld2<In>(kp + in), xv = ld2<In>(vp + in);
     const float nq = sum32(xq.x * xq.x + xq.y * xq.y);
@@ -83,7 +105,15 @@ __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const
     const float iq = 1.f / fmaxf(sqrtf(nq), 1e-12f);
     float ik = 1.f / fmaxf(sqrtf(nk), 1e-12f);
     const float iv = 1.f / fmaxf(sqrtf(nv), 1e-12f);
-    if (gl) ik *= sigmoidf_(gl[((size_t)b * T + t) * H + h]);
+    if (cols.gcol)
+      ik *= sigmoidf_((float)cols.gcol[row + h] + (cols.gbias ? cols.gbias[h] : 0.f));
+    else if (gl)
+      ik *= sigmoidf_(gl[((size_t)b * T + t) * H + h]);
+    if (cols.acol && i == 0) {
+      float l = -softplusf_((float)cols.acol[row + h] + cols.abias[h]) * eA;
+      if (cols.floor) l = fmaxf(l, cols.floor[h]);
+      la[(size_t)bh * T + t] = l;
+    }
     float s, c;
     sincosf((float)pos[t] * th, &s, &c);
     st2<__bf16>(q + out, (xq.x * c - xq.y * s) * iq, (xq.x * s + xq.y * c) * iq);
@@ -92,23 +122,40 @@ __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const
   }
 }
 
+// With columns (cols.acol / cols.gcol), the decay and gate gradients go to the same rows of the projections'
+// gradient (dcol = the gradient buffer, same layout and stride): dlogit_a = dla mask (-exp(A)) sigmoid(logit_a + b)
+// (mask: the floor not active), dlogit_g = dsig sig (1 - sig); and one partial per workgroup of the three per-head
+// sums (d gbias, d abias, dA = sum dla mask la) to part[blk * 3 ..].
 template <typename In>
 __global__ __launch_bounds__(256) void prep_bwd(
     const In* __restrict__ qp, const In* __restrict__ kp, const In* __restrict__ vp, const float* __restrict__ gl,
     const float* __restrict__ theta, const int64_t* __restrict__ pos, const __bf16* __restrict__ dq,
     const __bf16* __restrict__ dk, const __bf16* __restrict__ dv, In* __restrict__ dqp, In* __restrict__ dkp,
-    In* __restrict__ dvp, float* __restrict__ dgl, float* __restrict__ dth, int T, int H, int ntb) {
+    In* __restrict__ dvp, float* __restrict__ dgl, float* __restrict__ dth, int T, int H, int ntb, int64_t S,
+    Cols<In> cols, const float* __restrict__ dla, In* __restrict__ dcol, float* __restrict__ part) {
   __shared__ float red[ROWS][D / 2];
+  __shared__ float red3[ROWS][3];
   const int blk = blockIdx.x;
   const int bh = blk / ntb, tb = blk - bh * ntb;
   const int b = bh / H, h = bh - b * H;
   const int i = threadIdx.x & 31, rs = threadIdx.x >> 5;
   const float th = theta[h * (D / 2) + i];
-  float dth_acc = 0.f;
+  const float eA = cols.acol ? __expf(cols.A[h]) : 0.f;
+  float dth_acc = 0.f, dgb = 0.f, dab = 0.f, dA = 0.f;
   for (int p = 0; p < TB / ROWS; ++p) {
     const int t = tb * TB + p * ROWS + rs;
     if (t >= T) break;
-    const size_t in = (((size_t)b * T + t) * H + h) * D + 2 * i;
+    const size_t row = ((size_t)b * T + t) * S;
+    const size_t in = row + h * D + 2 * i;
+    if (cols.acol && i == 0) {
+      const float x = (float)cols.acol[row + h] + cols.abias[h];
+      const float l = -softplusf_(x) * eA;
+      const float g = (cols.floor && l < cols.floor[h]) ? 0.f : dla[(size_t)bh * T + t];
+      const float dx = -g * eA * sigmoidf_(x);
+      dcol[row + (cols.acol - qp) + h] = (In)dx;
+      dab += dx;
+      dA += g * l;
+    }
     const size_t out = ((size_t)bh * T + t) * D + 2 * i;
     const float pt = (float)pos[t];
     float s, c;
@@ -130,10 +177,19 @@ __global__ __launch_bounds__(256) void prep_bwd(
       const float inv = 1.f / fmaxf(sqrtf(sum32(x.x * x.x + x.y * x.y)), 1e-12f);
       const float u1 = x.x * inv, u2 = x.y * inv;
       const float r1 = u1 * c - u2 * s, r2 = u1 * s + u2 * c;
-      if (gl) {
-        const float sg = sigmoidf_(gl[((size_t)b * T + t) * H + h]);
+      if (cols.gcol || gl) {
+        const float sg = cols.gcol ? sigmoidf_((float)cols.gcol[row + h] + (cols.gbias ? cols.gbias[h] : 0.f))
+                                   : sigmoidf_(gl[((size_t)b * T + t) * H + h]);
         const float dsg = sum32(gk.x * r1 + gk.y * r2);
-        if (i == 0) dgl[((size_t)b * T + t) * H + h] = dsg * sg * (1.f - sg);
+        if (i == 0) {
+          const float dlg = dsg * sg * (1.f - sg);
+          if (cols.gcol) {
+            dcol[row + (cols.gcol - qp) + h] = (In)dlg;
+            dgb += dlg;
+          } else {
+            dgl[((size_t)b * T + t) * H + h] = dlg;
+          }
+        }
         gk.x *= sg;
         gk.y *= sg;
       }
@@ -153,12 +209,23 @@ __global__ __launch_bounds__(256) void prep_bwd(
     dth_acc += dang * pt;
   }
   red[rs][i] = dth_acc;
+  if (i == 0) {
+    red3[rs][0] = dgb;
+    red3[rs][1] = dab;
+    red3[rs][2] = dA;
+  }
   __syncthreads();
   if (threadIdx.x < D / 2) {
     float a = 0.f;
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) a += red[r][threadIdx.x];
     dth[(((size_t)b * ntb + tb) * H + h) * (D / 2) + threadIdx.x] = a;
+  }
+  if (part && threadIdx.x < 3) {
+    float a = 0.f;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) a += red3[r][threadIdx.x];
+    part[(size_t)blk * 3 + threadIdx.x] = a;
   }
 }
 
@@ -226,19 +293,22 @@ bool shape_ok(int64_t B, int64_t T, int64_t H) {
 
 extern "C" int pragnosia_aspin_prep_fwd(const void* qp, const void* kp, const void* vp, const float* gate,
                                         const float* theta, const int64_t* pos, void* q, void* k, void* v,
-                                        int64_t B, int64_t T, int64_t H, int64_t Dh, int in_bf16, void* stream) {
+                                        int64_t B, int64_t T, int64_t H, int64_t Dh, int64_t in_stride, int in_bf16,
+                                        void* stream) {
   if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, T, H));
-  PGN_CHECK_ARG(qp && kp && vp && theta && pos && q && k && v);
+  PGN_CHECK_ARG(qp && kp && vp && theta && pos && q && k && v && in_stride >= H * D);
   const int ntb = (int)((T + TB - 1) / TB);
   const dim3 grid((unsigned)(B * H * ntb));
   hipStream_t st = (hipStream_t)stream;
   if (in_bf16)
     hipLaunchKernelGGL(prep_fwd<__bf16>, grid, dim3(256), 0, st, (const __bf16*)qp, (const __bf16*)kp,
-                       (const __bf16*)vp, gate, theta, pos, (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb);
+                       (const __bf16*)vp, gate, theta, pos, (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb,
+                       in_stride, Cols<__bf16>{}, nullptr);
   else
     hipLaunchKernelGGL(prep_fwd<float>, grid, dim3(256), 0, st, (const float*)qp, (const float*)kp,
-                       (const float*)vp, gate, theta, pos, (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb);
+                       (const float*)vp, gate, theta, pos, (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb,
+                       in_stride, Cols<float>{}, nullptr);
   PGN_RETURN_LAUNCH();
 }
 
@@ -248,10 +318,11 @@ extern "C" int pragnosia_aspin_prep_bwd(const void* qp, const void* kp, const vo
                                         const float* theta, const int64_t* pos, const void* dq, const void* dk,
                                         const void* dv, void* dqp, void* dkp, void* dvp, float* dgate,
                                         float* dtheta_partial, int64_t B, int64_t T, int64_t H, int64_t Dh,
-                                        int in_bf16, void* stream) {
+                                        int64_t in_stride, int in_bf16, void* stream) {
   if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, T, H));
   PGN_CHECK_ARG(qp && kp && vp && theta && pos && dq && dk && dv && dqp && dkp && dvp && dtheta_partial);
+  PGN_CHECK_ARG(in_stride >= H * D);
   PGN_CHECK_ARG(gate == nullptr || dgate != nullptr);
   const int ntb = (int)((T + TB - 1) / TB);
   const dim3 grid((unsigned)(B * H * ntb));
@@ -259,11 +330,96 @@ extern "C" int pragnosia_aspin_prep_bwd(const void* qp, const void* kp, const vo
   if (in_bf16)
     hipLaunchKernelGGL(prep_bwd<__bf16>, grid, dim3(256), 0, st, (const __bf16*)qp, (const __bf16*)kp,
                        (const __bf16*)vp, gate, theta, pos, (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv,
-                       (__bf16*)dqp, (__bf16*)dkp, (__bf16*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb);
+                       (__bf16*)dqp, (__bf16*)dkp, (__bf16*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb,
+                       in_stride, Cols<__bf16>{}, nullptr, nullptr, nullptr);
   else
     hipLaunchKernelGGL(prep_bwd<float>, grid, dim3(256), 0, st, (const float*)qp, (const float*)kp,
                        (const float*)vp, gate, theta, pos, (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv,
-                       (float*)dqp, (float*)dkp, (float*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb);
+                       (float*)dqp, (float*)dkp, (float*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb, in_stride,
+                       Cols<float>{}, nullptr, nullptr, nullptr);
+  PGN_RETURN_LAUNCH();
+}
+
+namespace {
+
+bool proj_cols_ok(int64_t H, int64_t stride, int64_t la_col, int64_t gate_col) {
+  const int64_t hd = H * D;
+  if (la_col < 3 * hd || la_col + H > stride) return false;
+  if (gate_col >= 0 && (gate_col < 3 * hd || gate_col + H > stride || (gate_col < la_col + H && la_col < gate_col + H)))
+    return false;
+  return stride >= 3 * hd;
+}
+
+template <typename In>
+Cols<In> proj_cols(const void* P, int64_t la_col, int64_t gate_col, const float* la_bias, const float* A,
+                   const float* la_floor, const float* gate_bias) {
+  const In* base = (const In*)P;
+  return Cols<In>{base + la_col, la_bias, A, la_floor, gate_col >= 0 ? base + gate_col : nullptr, gate_bias};
+}
+
+}  // namespace
+
+extern "C" int pragnosia_aspin_prep_proj_fwd(const void* P, int64_t stride, int64_t la_col, int64_t gate_col,
+                                             const float* la_bias, const float* A, const float* la_floor,
+                                             const float* gate_bias, const float* theta, const int64_t* pos, void* q,
+                                             void* k, void* v, float* la, int64_t B, int64_t T, int64_t H,
+                                             int64_t Dh, int in_bf16, void* stream) {
+  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(shape_ok(B, T, H));
+  PGN_CHECK_ARG(P && la_bias && A && theta && pos && q && k && v && la);
+  PGN_CHECK_ARG(proj_cols_ok(H, stride, la_col, gate_col));
+  const int ntb = (int)((T + TB - 1) / TB);
+  const dim3 grid((unsigned)(B * H * ntb));
+  const int64_t hd = H * D;
+  hipStream_t st = (hipStream_t)stream;
+  if (in_bf16) {
+    const __bf16* p = (const __bf16*)P;
+    hipLaunchKernelGGL(prep_fwd<__bf16>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
+                       (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb, stride,
+                       proj_cols<__bf16>(P, la_col, gate_col, la_bias, A, la_floor, gate_bias), la);
+  } else {
+    const float* p = (const float*)P;
+    hipLaunchKernelGGL(prep_fwd<float>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
+                       (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb, stride,
+                       proj_cols<float>(P, la_col, gate_col, la_bias, A, la_floor, gate_bias), la);
+  }
+  PGN_RETURN_LAUNCH();
+}
+
+extern "C" int64_t pragnosia_aspin_prep_proj_partials(int64_t B, int64_t T, int64_t H) {
+  if (!shape_ok(B, T, H)) return -1;
+  return B * H * ((T + TB - 1) / TB);
+}
+
+extern "C" int pragnosia_aspin_prep_proj_bwd(const void* P, int64_t stride, int64_t la_col, int64_t gate_col,
+                                             const float* la_bias, const float* A, const float* la_floor,
+                                             const float* gate_bias, const float* theta, const int64_t* pos,
+                                             const void* dq, const void* dk, const void* dv, const float* dla,
+                                             void* dP, float* dtheta_partial, float* part, int64_t B, int64_t T,
+                                             int64_t H, int64_t Dh, int in_bf16, void* stream) {
+  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(shape_ok(B, T, H));
+  PGN_CHECK_ARG(P && la_bias && A && theta && pos && dq && dk && dv && dla && dP && dtheta_partial && part);
+  PGN_CHECK_ARG(proj_cols_ok(H, stride, la_col, gate_col) && P != dP);
+  const int ntb = (int)((T + TB - 1) / TB);
+  const dim3 grid((unsigned)(B * H * ntb));
+  const int64_t hd = H * D;
+  hipStream_t st = (hipStream_t)stream;
+  if (in_bf16) {
+    const __bf16* p = (const __bf16*)P;
+    __bf16* d = (__bf16*)dP;
+    hipLaunchKernelGGL(prep_bwd<__bf16>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
+                       (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv, d, d + hd, d + 2 * hd, nullptr,
+                       dtheta_partial, (int)T, (int)H, ntb, stride,
+                       proj_cols<__bf16>(P, la_col, gate_col, la_bias, A, la_floor, gate_bias), dla, d, part);
+  } else {
+    const float* p = (const float*)P;
+    float* d = (float*)dP;
+    hipLaunchKernelGGL(prep_bwd<float>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
+                       (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv, d, d + hd, d + 2 * hd, nullptr,
+                       dtheta_partial, (int)T, (int)H, ntb, stride,
+                       proj_cols<float>(P, la_col, gate_col, la_bias, A, la_floor, gate_bias), dla, d, part);
+  }
   PGN_RETURN_LAUNCH();
 }
 
