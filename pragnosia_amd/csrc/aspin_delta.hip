@@ -65,46 +65,65 @@ PGN_DEVICE void chunk_decays(float la_l, int l, float* Ls, float* eLs, float* ws
 
 // ------------------------------------------------------------------------------------------------------------------
 // X = (I + N)^-1, one wave per (batch-head, chunk)
+// N^T and X are kept as their ten 16 x 16 blocks on and below the diagonal (block (tb, sb), sb <= tb, at index
+// tb (tb + 1) / 2 + sb, unpadded rows so the substitution reads four entries at once): 24 KB of LDS per chunk, so
+// six chunks (one round of the grid at cfg2) are resident per compute unit. The keys are read from global memory
+// straight into MFMA operand registers.
+constexpr int BP = 16;                 // row pitch of a 16 x 16 fp32 block
+constexpr int BLK = 16 * BP;
+PGN_DEVICE int blk(int tb, int sb) { return (tb * (tb + 1) / 2 + sb) * BLK; }
+
+// the MFMA operand of one key row from global memory: row[32 m + 4 g .. + 3] and row[32 m + 16 + 4 g .. + 3]
+PGN_DEVICE bf16x8 gfrag(const __bf16* row, int m, int g, bool valid) {
+  bf16x4 lo, hi;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) lo[u] = hi[u] = (__bf16)0.f;
+  if (valid) {
+    lo = *reinterpret_cast<const bf16x4*>(row + 32 * m + 4 * g);
+    hi = *reinterpret_cast<const bf16x4*>(row + 32 * m + 16 + 4 * g);
+  }
+  return cat8(lo, hi);
+}
+
 __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__ k, const float* __restrict__ la,
                                                       const float* __restrict__ be, __bf16* __restrict__ X, int T,
                                                       int NC) {
-  __shared__ __align__(16) __bf16 Ks[TILE];
-  __shared__ __align__(16) float NT[C * NP];  // NT[s][t] = N[t][s]
-  __shared__ __align__(16) float Xf[C * NP];  // X, fp32, blocks on and below the diagonal
-  __shared__ __align__(16) float Tt[3 * 16 * 17];  // per-level sums, one 16 x 16 block per product
+  __shared__ __align__(16) float NT[10 * BLK];  // N^T blocks: NT(tb, sb)[s' * BP + t'] = N[16 tb + t'][16 sb + s']
+  __shared__ __align__(16) float Xf[10 * BLK];  // X blocks: Xf(ib, jb)[r * BP + c] = X[16 ib + r][16 jb + c]
+  __shared__ __align__(16) float Tt[3 * BLK];   // per-level sums, one block per product
   __shared__ __align__(16) float Ls[C], bs[C];
 
   const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;
   const int l = threadIdx.x, g = l >> 4, i = l & 15;
   const int t0 = c * C, nr = min(C, T - t0);
   const __bf16* kc = k + ((size_t)bh * T + t0) * DK;
-  // the chunk's keys: all eight 16-byte segments per lane issued before any is written (one memory round trip)
-  bf16x8 seg[8];
+  // this lane's operand rows i, 16 + i, 32 + i, 48 + i (both halves of the contraction), all loads issued at once
+  bf16x8 kf[4][2];
 #pragma unroll
-  for (int n = 0; n < 8; ++n) seg[n] = load_seg(kc, nr, l + 64 * n);
+  for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-  for (int n = 0; n < 8; ++n) put_seg(Ks, seg[n], l + 64 * n);
+    for (int m = 0; m < 2; ++m) kf[rb][m] = gfrag(kc + (size_t)(16 * rb + i) * DK, m, g, 16 * rb + i < nr);
   const float lav = l < nr ? la[(size_t)bh * T + t0 + l] : 0.f;
   const float bev = l < nr ? be[(size_t)bh * T + t0 + l] : 0.f;
   Ls[l] = incl_scan64(lav, l);
   bs[l] = bev;
   __syncthreads();
 
-  // N^T tiles: accumulator rows s (block sb), lane t (block tb), for sb <= tb
+  // N^T blocks: accumulator rows s (block sb), lane t (block tb), for sb <= tb
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int t = 16 * tb + i;
     const float Lt = Ls[t], bt = bs[t];
-    const bf16x8 kt0 = frag(Ks, t, 0, g), kt1 = frag(Ks, t, 1, g);
 #pragma unroll
     for (int sb = 0; sb <= tb; ++sb) {
       f32x4 acc = zero4();
-      acc = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), kt0, acc);
-      acc = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), kt1, acc);
+      acc = pgn_mfma(kf[sb][0], kf[tb][0], acc);
+      acc = pgn_mfma(kf[sb][1], kf[tb][1], acc);
+      float* nb = NT + blk(tb, sb);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int s = 16 * sb + 4 * g + r;
-        NT[s * NP + t] = bt * acc[r] * masked_decay(Lt - Ls[s], s < t);
+        nb[(4 * g + r) * BP + i] = bt * acc[r] * masked_decay(Lt - Ls[s], s < t);
       }
     }
   }
@@ -115,35 +134,36 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
   // (v_mfma_f32_16x16x4f32: A[r][k] in lane r + 16k, B[k][c] in lane c + 16k, D[4g + e][c] in lane c + 16g).
   {
     const int b = l >> 4, cl = l & 15;
+    const float* nd = NT + blk(b, b);
     float xd[16];
 #pragma unroll
     for (int t = 0; t < 16; ++t) xd[t] = (t == cl) ? 1.f : 0.f;
 #pragma unroll
     for (int s = 0; s < 15; ++s) {
       const float xs = xd[s];
-      const float* nrow = NT + (16 * b + s) * NP + 16 * b;  // N[16b + t][16b + s], t = 0..15
 #pragma unroll
       for (int t4 = (s + 1) & ~3; t4 < 16; t4 += 4) {
-        const f32x4 n = *reinterpret_cast<const f32x4*>(nrow + t4);
+        const f32x4 n = *reinterpret_cast<const f32x4*>(nd + s * BP + t4);  // N[16b + t][16b + s], t = t4..
 #pragma unroll
         for (int u = 0; u < 4; ++u)
           if (t4 + u > s) xd[t4 + u] -= n[u] * xs;
       }
     }
+    float* xb = Xf + blk(b, b);
 #pragma unroll
-    for (int t = 0; t < 16; ++t) Xf[(16 * b + t) * NP + 16 * b + cl] = xd[t];
+    for (int t = 0; t < 16; ++t) xb[t * BP + cl] = xd[t];
   }
   __syncthreads();
   {
     const int r16 = l & 15, k4 = l >> 4;
-    // one 16 x 16 x 16 product A B accumulated onto acc: A from rows ra.., columns ca.. of tile At (pitch NP), read
-    // transposed when `at` (At[c][r]); B from rows rb.., columns cb.. of tile Bt (pitch pb)
-    auto mm = [&](f32x4 acc, const float* At, bool at, int ra, int ca, const float* Bt, int pb, int rb, int cb) {
+    // one 16 x 16 x 16 product A B accumulated onto acc: A the block at `Ab`, read transposed when `at`
+    // (A[r][k] = Ab[k * BP + r]); B the block at `Bb` (B[k][c] = Bb[k * BP + c])
+    auto mm = [&](f32x4 acc, const float* Ab, bool at, const float* Bb) {
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const float av = at ? At[(ca + 4 * kk + k4) * NP + ra + r16] : At[(ra + r16) * NP + ca + 4 * kk + k4];
-        const float bv = Bt[(rb + 4 * kk + k4) * pb + cb + r16];
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+        const int kx = 4 * kk + k4;
+        const float av = at ? Ab[kx * BP + r16] : Ab[r16 * BP + kx];
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, Bb[kx * BP + r16], acc, 0, 0, 0);
       }
       return acc;
     };
@@ -154,21 +174,23 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
       for (int jb = 0; jb + d < 4; ++jb) {
         const int ib = jb + d;
         f32x4 acc = zero4();
+        // N_ik = (N^T block (ib, kb)) transposed
 #pragma unroll
-        for (int kb = jb; kb < ib; ++kb) acc = mm(acc, NT, true, 16 * ib, 16 * kb, Xf, NP, 16 * kb, 16 * jb);
+        for (int kb = jb; kb < ib; ++kb) acc = mm(acc, NT + blk(ib, kb), true, Xf + blk(kb, jb));
         Tacc[jb] = acc;
       }
 #pragma unroll
       for (int jb = 0; jb + d < 4; ++jb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) Tt[jb * 16 * 17 + (4 * k4 + e) * 17 + r16] = Tacc[jb][e];
+        for (int e = 0; e < 4; ++e) Tt[jb * BLK + (4 * k4 + e) * BP + r16] = Tacc[jb][e];
       __syncthreads();
 #pragma unroll
       for (int jb = 0; jb + d < 4; ++jb) {
         const int ib = jb + d;
-        const f32x4 xr = mm(zero4(), Xf, false, 16 * ib, 16 * ib, Tt + jb * 16 * 17, 17, 0, 0);
+        const f32x4 xr = mm(zero4(), Xf + blk(ib, ib), false, Tt + jb * BLK);
+        float* xo = Xf + blk(ib, jb);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) Xf[(16 * ib + 4 * k4 + e) * NP + 16 * jb + r16] = -xr[e];
+        for (int e = 0; e < 4; ++e) xo[(4 * k4 + e) * BP + r16] = -xr[e];
       }
       __syncthreads();
     }
@@ -178,11 +200,12 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
     const int e = l + 64 * n, r = e >> 3, c0 = 8 * (e & 7);
+    const int rb = r >> 4, cb = c0 >> 4;
     bf16x8 out;
-    if ((c0 >> 4) <= (r >> 4)) {
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(Xf + r * NP + c0);
-      const f32x4 hi = *reinterpret_cast<const f32x4*>(Xf + r * NP + c0 + 4);
-      out = pack(lo, hi);
+    if (cb <= rb) {
+      const float* xb = Xf + blk(rb, cb) + (r & 15) * BP + (c0 & 15);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) out[u] = (__bf16)xb[u];
     } else {
 #pragma unroll
       for (int u = 0; u < 8; ++u) out[u] = (__bf16)0.f;
