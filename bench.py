@@ -309,18 +309,18 @@ def carried_bench():
             "carried_vs_unsplit_rel_err_S": round(rel(Sc, Su_loc), 6)}
 
 
-def carrier_layer_bench(steps=20):
-    """The carrier layer around the scan at configs[2]'s shape: AssocCarrier(768) (12 heads of 64, plain rule) forward
-    + backward on x (B16, T512, 768) under bf16 autocast, fp32 parameters: LayerNorm, the q/k/v and gate
-    projections, the decay, prep, the chunked scan, the output epilogue and the gated o-projection with its
-    residual. Reported eagerly (host dispatch included) and as HIP-graph replays of the whole step (device time),
-    with this build's fused plumbing (one projection GEMM feeding one prep kernel, fused output epilogue) and as the
-    reference's torch composition around the same scan kernels."""
+def carrier_layer_bench(steps=20, delta=False):
+    """The carrier layer around the scan at configs[2]'s shape: AssocCarrier(768) (12 heads of 64; plain rule, or the
+    delta rule) forward + backward on x (B16, T512, 768) under bf16 autocast, fp32 parameters: LayerNorm, the q/k/v
+    and gate (or write-strength) projections, the decay, prep, the chunked scan, the output epilogue and the gated
+    o-projection with its residual. Reported eagerly (host dispatch included) and as HIP-graph replays of the whole
+    step (device time), with this build's fused plumbing (one projection GEMM feeding one prep kernel, fused output
+    epilogue) and as the reference's torch composition around the same scan kernels."""
     import torch
     from pragnosia_amd import assoc
     torch.manual_seed(7)
     B, T, d = 16, 512, 768
-    m = assoc.AssocCarrier(d).cuda()
+    m = assoc.AssocCarrier(d, delta=delta).cuda()
     x = torch.randn(B, T, d, device="cuda", requires_grad=True)
     gy = torch.randn(B, T, d, device="cuda")
 
@@ -329,7 +329,8 @@ def carrier_layer_bench(steps=20):
             y, _ = m(x)
         y.backward(gy)
 
-    out = {"workload": "AssocCarrier(768) layer fwd+bwd, B16 T512, bf16 autocast (configs[2] shape)"}
+    out = {"workload": f"AssocCarrier(768{', delta=True' if delta else ''}) layer fwd+bwd, B16 T512, bf16 autocast "
+                       "(configs[2] shape)"}
     prev = assoc.FUSED_PLUMBING
     try:
         for name, fused in (("fused_plumbing", True), ("torch_plumbing", False)):
@@ -520,6 +521,7 @@ def gpu_bench(args):
         sec["diag_scan"] = diag_bench(args.steps)
         sec["carried"] = carried_bench()
         sec["carrier_layer"] = carrier_layer_bench()
+        sec["carrier_layer_delta"] = carrier_layer_bench(delta=True)
         sec["decode"] = decode_bench()
         sec["lds_contraction"] = lds_contraction_bench()
         res["decode_ms_per_token_bs1"] = sec["decode"]["ms_per_token_bs1"]

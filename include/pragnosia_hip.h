@@ -173,31 +173,37 @@ int pragnosia_aspin_prep_bwd(const void* qp, const void* kp, const void* vp, con
 
 /* The same plumbing fed by ONE GEMM's output P (B, T, stride) (fp32, or bf16 if in_bf16) holding, per token, the q,
  * k and v projections in columns [0, H D), [H D, 2 H D), [2 H D, 3 H D), the decay logits (before bias) in columns
- * [la_col, la_col + H) and, when gate_col >= 0, the write-gate logits (before bias) in [gate_col, gate_col + H).
+ * [la_col, la_col + H) and at most one of: the plain rule's write-gate logits in [gate_col, gate_col + H)
+ * (gate_col >= 0), or the delta rule's write-strength logits in [beta_col, beta_col + H) (beta_col >= 0); -1 = absent.
  * Besides q, k, v (as pragnosia_aspin_prep_fwd, gate = sigmoid(logit + gate_bias[h])), writes the decay in the scan's
  * layout, la (B, H, T) fp32: la = -softplus(logit + la_bias[h]) exp(A[h]), floored at la_floor[h] when la_floor is
- * non-NULL. la_bias, A, la_floor, gate_bias: (H) fp32 (gate_bias may be NULL: no bias). Replaces the carrier's
- * separate q/k/v/gate projections' consumers: `logalpha` (src/assoc.py:355-359), the write gate
- * (src/assoc.py:458-459) and `prep_kernel` (src/assoc_kernel.py:740-769), with the transpose of la for the scan. */
-int pragnosia_aspin_prep_proj_fwd(const void* P, int64_t stride, int64_t la_col, int64_t gate_col,
+ * non-NULL, and with beta_col >= 0 the strength beta (B, H, T) fp32 = max(sigmoid(logit + beta_bias[h]), beta_min).
+ * la_bias, A, la_floor, gate_bias, beta_bias: (H) fp32 (the biases may be NULL: none). Replaces the carrier's
+ * separate projections' consumers: `logalpha` (src/assoc.py:355-359), the write gate (src/assoc.py:458-459), beta
+ * (src/assoc.py:468, the write_all floor 0.75 included) and `prep_kernel` (src/assoc_kernel.py:740-769), with the
+ * transposes of la and beta for the scan. */
+int pragnosia_aspin_prep_proj_fwd(const void* P, int64_t stride, int64_t la_col, int64_t gate_col, int64_t beta_col,
                                   const float* la_bias, const float* A, const float* la_floor,
-                                  const float* gate_bias, const float* theta, const int64_t* pos, void* q, void* k,
-                                  void* v, float* la, int64_t B, int64_t T, int64_t H, int64_t D, int in_bf16,
+                                  const float* gate_bias, const float* beta_bias, float beta_min,
+                                  const float* theta, const int64_t* pos, void* q, void* k, void* v, float* la,
+                                  float* beta, int64_t B, int64_t T, int64_t H, int64_t D, int in_bf16,
                                   void* stream);
 
 /* Rows of 3 fp32 per-head partial sums pragnosia_aspin_prep_proj_bwd writes (-1 if the shape is rejected). */
 int64_t pragnosia_aspin_prep_proj_partials(int64_t B, int64_t T, int64_t H);
 
-/* Backward of pragnosia_aspin_prep_proj_fwd: from dq, dk, dv ((B, H, T, D) bf16) and dla ((B, H, T) fp32) writes the
- * q, k, v, decay and gate columns of dP (P's layout, stride and dtype; other columns untouched), theta's partials
- * (as pragnosia_aspin_prep_bwd) and `part`: pragnosia_aspin_prep_proj_partials(B, T, H) rows, row (b H + h) ntb + j
- * holding (d gate_bias[h], d la_bias[h], dA[h]) partial sums (ntb = ceil(T / 64)); the caller sums them per head. */
-int pragnosia_aspin_prep_proj_bwd(const void* P, int64_t stride, int64_t la_col, int64_t gate_col,
+/* Backward of pragnosia_aspin_prep_proj_fwd: from dq, dk, dv ((B, H, T, D) bf16), dla and (with beta_col >= 0) dbeta
+ * ((B, H, T) fp32) writes the q, k, v, decay and gate or strength columns of dP (P's layout, stride and dtype; other
+ * columns untouched), theta's partials (as pragnosia_aspin_prep_bwd) and `part`:
+ * pragnosia_aspin_prep_proj_partials(B, T, H) rows, row (b H + h) ntb + j holding (d gate_bias[h] or
+ * d beta_bias[h], d la_bias[h], dA[h]) partial sums (ntb = ceil(T / 64)); the caller sums them per head. */
+int pragnosia_aspin_prep_proj_bwd(const void* P, int64_t stride, int64_t la_col, int64_t gate_col, int64_t beta_col,
                                   const float* la_bias, const float* A, const float* la_floor,
-                                  const float* gate_bias, const float* theta, const int64_t* pos, const void* dq,
-                                  const void* dk, const void* dv, const float* dla, void* dP, float* dtheta_partial,
-                                  float* part, int64_t B, int64_t T, int64_t H, int64_t D, int in_bf16,
-                                  void* stream);
+                                  const float* gate_bias, const float* beta_bias, float beta_min,
+                                  const float* theta, const int64_t* pos, const void* dq, const void* dk,
+                                  const void* dv, const float* dla, const float* dbeta, void* dP,
+                                  float* dtheta_partial, float* part, int64_t B, int64_t T, int64_t H, int64_t D,
+                                  int in_bf16, void* stream);
 
 /* The carried-state rebase of src/assoc.py:399-402: S (B, H, D, D) fp32 with keys on dim 2; key rows (2i, 2i+1) are
  * rotated by -p0 * theta[h, i], p0 = *p0_dev when p0_dev is non-NULL (a device fp32 scalar, as the graphed decode

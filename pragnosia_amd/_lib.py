@@ -35,9 +35,9 @@ SIGNATURES = {
     "pragnosia_aspin_prep_fwd": [_p] * 9 + [_i64] * 5 + [_i32, _p],
     "pragnosia_aspin_prep_theta_partials": [_i64] * 2,
     "pragnosia_aspin_prep_bwd": [_p] * 14 + [_i64] * 5 + [_i32, _p],
-    "pragnosia_aspin_prep_proj_fwd": [_p, _i64, _i64, _i64] + [_p] * 10 + [_i64] * 4 + [_i32, _p],
+    "pragnosia_aspin_prep_proj_fwd": [_p] + [_i64] * 4 + [_p] * 5 + [_f32] + [_p] * 7 + [_i64] * 4 + [_i32, _p],
     "pragnosia_aspin_prep_proj_partials": [_i64] * 3,
-    "pragnosia_aspin_prep_proj_bwd": [_p, _i64, _i64, _i64] + [_p] * 13 + [_i64] * 4 + [_i32, _p],
+    "pragnosia_aspin_prep_proj_bwd": [_p] + [_i64] * 4 + [_p] * 5 + [_f32] + [_p] * 10 + [_i64] * 4 + [_i32, _p],
     "pragnosia_aspin_rebase_fwd": [_p] * 3 + [_f32, _p] + [_i64] * 3 + [_p],
     "pragnosia_aspin_rebase_bwd": [_p] * 3 + [_f32] + [_p] * 3 + [_i64] * 3 + [_p],
     "pragnosia_aspin_decode_step": [_p] * 10 + [_f32, _p] + [_i64] * 3 + [_p],

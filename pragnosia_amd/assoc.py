@@ -189,18 +189,21 @@ class AssocCarrier(nn.Module):
 
     def _scan_inputs(self, z, pos):
         """The scan's inputs from the normalised layer input z (B, T, d): q, k, v (B, H, T, dk) bf16, la and beta
-        (B, H, T) fp32 (beta None for the plain rule), and the projections' dtype. With FUSED_PLUMBING (plain rule,
-        no key_topk): one GEMM for the q, k, v, decay and write-gate projections and one kernel from its output;
-        otherwise the reference's composition: separate projections, elementwise decay and gate, prep."""
-        if FUSED_PLUMBING and not self.delta and not self.key_topk and self.dk == HEAD_DIM_KERNEL:
-            gated = not self.write_all
-            W = torch.cat([self.q.weight, self.k.weight, self.v.weight, self.wa.weight] +
-                          ([self.wi.weight] if gated else []))
+        (B, H, T) fp32 (beta None for the plain rule), and the projections' dtype. With FUSED_PLUMBING (no key_topk,
+        no beta_scale): one GEMM for the q, k, v, decay and write-gate (plain) or write-strength (delta) projections
+        and one kernel from its output; otherwise the reference's composition: separate projections (one GEMM under
+        FUSED_PROJ), elementwise decay, gate and strength, prep."""
+        if (FUSED_PLUMBING and not self.key_topk and self.dk == HEAD_DIM_KERNEL
+                and getattr(self, "beta_scale", None) is None):
+            gated = not (self.delta or self.write_all)
+            extra = [self.wi.weight] if gated else ([self.wb.weight] if self.delta else [])
+            W = torch.cat([self.q.weight, self.k.weight, self.v.weight, self.wa.weight] + extra)
             P = F.linear(z, W)
-            q, k, v, la = _op.aspin_prep_proj(P, self.h, self.wa.bias, self.A,
-                                              self.la_floor if self.hl_floor else None,
-                                              self.wi.bias if gated else None, self.theta, pos)
-            return q, k, v, la, None, P.dtype
+            q, k, v, la, beta = _op.aspin_prep_proj(
+                P, self.h, self.wa.bias, self.A, self.la_floor if self.hl_floor else None,
+                self.wi.bias if gated else None, self.wb.bias if self.delta else None,
+                0.75 if (self.delta and self.write_all) else 0.0, gated, self.theta, pos)
+            return q, k, v, la, (beta if self.delta else None), P.dtype
         qp, kp, vp, gate, la, bt = self._projections(z)
         q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
         bt = None if bt is None else bt.transpose(1, 2).float()

@@ -64,10 +64,12 @@ PGN_DEVICE float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
 // softplus with torch's default threshold: x above 20 passes through
 PGN_DEVICE float softplusf_(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
-// The decay and write gate taken from columns of the projections' rows (a single GEMM's output): per (b, t, h) the
-// decay logit at acol[row + h] and the gate logit at gcol[row + h] (row = (b T + t) * S), each plus its bias.
-// la = -softplus(logit + abias[h]) exp(A[h]), floored at floor[h] when given (`src/assoc.py:355-359`); the gate is
-// sigmoid(logit + gbias[h]) (`src/assoc.py:458-459`).
+// The decay, write gate and write strength taken from columns of the projections' rows (a single GEMM's output):
+// per (b, t, h) the decay logit at acol[row + h], the gate logit at gcol[row + h] and the strength logit at
+// bcol[row + h] (row = (b T + t) * S), each plus its bias. la = -softplus(logit + abias[h]) exp(A[h]), floored at
+// floor[h] when given (`src/assoc.py:355-359`); the gate is sigmoid(logit + gbias[h]) (`src/assoc.py:458-459`); the
+// delta rule's strength is beta = max(sigmoid(logit + bbias[h]), bmin) (`src/assoc.py:468`, bmin = 0.75 with
+// write_all, else 0: no floor).
 template <typename In>
 struct Cols {
   const In* acol;       // decay logits, or NULL (then no la)
@@ -76,6 +78,9 @@ struct Cols {
   const float* floor;   // (H) or NULL
   const In* gcol;       // gate logits, or NULL (then the separate fp32 gate, if any)
   const float* gbias;   // (H) or NULL
+  const In* bcol;       // write-strength logits, or NULL (then no beta)
+  const float* bbias;   // (H) or NULL
+  float bmin;
 };
 
 template <typename In>
@@ -84,7 +89,8 @@ __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const
                                                 const float* __restrict__ theta, const int64_t* __restrict__ pos,
                                                 __bf16* __restrict__ q, __bf16* __restrict__ k,
                                                 __bf16* __restrict__ v, int T, int H, int ntb, int64_t S,
-                                                Cols<In> cols, float* __restrict__ la) {
+                                                Cols<In> cols, float* __restrict__ la,
+                                                float* __restrict__ beta) {
   const int blk = blockIdx.x;
   const int bh = blk / ntb, tb = blk - bh * ntb;
   const int b = bh / H, h = bh - b * H;
@@ -114,6 +120,9 @@ __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const
       if (cols.floor) l = fmaxf(l, cols.floor[h]);
       la[(size_t)bh * T + t] = l;
     }
+    if (cols.bcol && i == 0)
+      beta[(size_t)bh * T + t] =
+          fmaxf(sigmoidf_((float)cols.bcol[row + h] + (cols.bbias ? cols.bbias[h] : 0.f)), cols.bmin);
     float s, c;
     sincosf((float)pos[t] * th, &s, &c);
     st2<__bf16>(q + out, (xq.x * c - xq.y * s) * iq, (xq.x * s + xq.y * c) * iq);
@@ -122,17 +131,19 @@ __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const
   }
 }
 
-// With columns (cols.acol / cols.gcol), the decay and gate gradients go to the same rows of the projections'
-// gradient (dcol = the gradient buffer, same layout and stride): dlogit_a = dla mask (-exp(A)) sigmoid(logit_a + b)
-// (mask: the floor not active), dlogit_g = dsig sig (1 - sig); and one partial per workgroup of the three per-head
-// sums (d gbias, d abias, dA = sum dla mask la) to part[blk * 3 ..].
+// With columns (cols.acol / cols.gcol / cols.bcol), the decay, gate and strength gradients go to the same rows of the
+// projections' gradient (dcol = the gradient buffer, same layout and stride): dlogit_a = dla mask (-exp(A))
+// sigmoid(logit_a + b) (mask: the floor not active), dlogit_g = dsig sig (1 - sig), dlogit_b = dbeta mask sig (1 -
+// sig) (mask: bmin not active); and one partial per workgroup of the three per-head sums (d gbias or d bbias,
+// d abias, dA = sum dla mask la) to part[blk * 3 ..].
 template <typename In>
 __global__ __launch_bounds__(256) void prep_bwd(
     const In* __restrict__ qp, const In* __restrict__ kp, const In* __restrict__ vp, const float* __restrict__ gl,
     const float* __restrict__ theta, const int64_t* __restrict__ pos, const __bf16* __restrict__ dq,
     const __bf16* __restrict__ dk, const __bf16* __restrict__ dv, In* __restrict__ dqp, In* __restrict__ dkp,
     In* __restrict__ dvp, float* __restrict__ dgl, float* __restrict__ dth, int T, int H, int ntb, int64_t S,
-    Cols<In> cols, const float* __restrict__ dla, In* __restrict__ dcol, float* __restrict__ part) {
+    Cols<In> cols, const float* __restrict__ dla, const float* __restrict__ dbeta, In* __restrict__ dcol,
+    float* __restrict__ part) {
   __shared__ float red[ROWS][D / 2];
   __shared__ float red3[ROWS][3];
   const int blk = blockIdx.x;
@@ -155,6 +166,12 @@ __global__ __launch_bounds__(256) void prep_bwd(
       dcol[row + (cols.acol - qp) + h] = (In)dx;
       dab += dx;
       dA += g * l;
+    }
+    if (cols.bcol && i == 0) {
+      const float sb = sigmoidf_((float)cols.bcol[row + h] + (cols.bbias ? cols.bbias[h] : 0.f));
+      const float db = sb < cols.bmin ? 0.f : dbeta[(size_t)bh * T + t] * sb * (1.f - sb);
+      dcol[row + (cols.bcol - qp) + h] = (In)db;
+      dgb += db;
     }
     const size_t out = ((size_t)bh * T + t) * D + 2 * i;
     const float pt = (float)pos[t];
@@ -304,11 +321,11 @@ extern "C" int pragnosia_aspin_prep_fwd(const void* qp, const void* kp, const vo
   if (in_bf16)
     hipLaunchKernelGGL(prep_fwd<__bf16>, grid, dim3(256), 0, st, (const __bf16*)qp, (const __bf16*)kp,
                        (const __bf16*)vp, gate, theta, pos, (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb,
-                       in_stride, Cols<__bf16>{}, nullptr);
+                       in_stride, Cols<__bf16>{}, nullptr, nullptr);
   else
     hipLaunchKernelGGL(prep_fwd<float>, grid, dim3(256), 0, st, (const float*)qp, (const float*)kp,
                        (const float*)vp, gate, theta, pos, (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb,
-                       in_stride, Cols<float>{}, nullptr);
+                       in_stride, Cols<float>{}, nullptr, nullptr);
   PGN_RETURN_LAUNCH();
 }
 
@@ -331,43 +348,49 @@ extern "C" int pragnosia_aspin_prep_bwd(const void* qp, const void* kp, const vo
     hipLaunchKernelGGL(prep_bwd<__bf16>, grid, dim3(256), 0, st, (const __bf16*)qp, (const __bf16*)kp,
                        (const __bf16*)vp, gate, theta, pos, (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv,
                        (__bf16*)dqp, (__bf16*)dkp, (__bf16*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb,
-                       in_stride, Cols<__bf16>{}, nullptr, nullptr, nullptr);
+                       in_stride, Cols<__bf16>{}, nullptr, nullptr, nullptr, nullptr);
   else
     hipLaunchKernelGGL(prep_bwd<float>, grid, dim3(256), 0, st, (const float*)qp, (const float*)kp,
                        (const float*)vp, gate, theta, pos, (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv,
                        (float*)dqp, (float*)dkp, (float*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb, in_stride,
-                       Cols<float>{}, nullptr, nullptr, nullptr);
+                       Cols<float>{}, nullptr, nullptr, nullptr, nullptr);
   PGN_RETURN_LAUNCH();
 }
 
 namespace {
 
-bool proj_cols_ok(int64_t H, int64_t stride, int64_t la_col, int64_t gate_col) {
+// the H-column groups at la_col (required), gate_col and beta_col (each optional: -1) lie past q, k, v, inside the
+// row, and do not overlap; a row has a gate or a strength, not both
+bool proj_cols_ok(int64_t H, int64_t stride, int64_t la_col, int64_t gate_col, int64_t beta_col) {
   const int64_t hd = H * D;
-  if (la_col < 3 * hd || la_col + H > stride) return false;
-  if (gate_col >= 0 && (gate_col < 3 * hd || gate_col + H > stride || (gate_col < la_col + H && la_col < gate_col + H)))
-    return false;
-  return stride >= 3 * hd;
+  if (stride < 3 * hd || la_col < 3 * hd || la_col + H > stride) return false;
+  if (gate_col >= 0 && beta_col >= 0) return false;
+  const int64_t x = gate_col >= 0 ? gate_col : beta_col;
+  if (x >= 0 && (x < 3 * hd || x + H > stride || (x < la_col + H && la_col < x + H))) return false;
+  return true;
 }
 
 template <typename In>
-Cols<In> proj_cols(const void* P, int64_t la_col, int64_t gate_col, const float* la_bias, const float* A,
-                   const float* la_floor, const float* gate_bias) {
+Cols<In> proj_cols(const void* P, int64_t la_col, int64_t gate_col, int64_t beta_col, const float* la_bias,
+                   const float* A, const float* la_floor, const float* gate_bias, const float* beta_bias,
+                   float beta_min) {
   const In* base = (const In*)P;
-  return Cols<In>{base + la_col, la_bias, A, la_floor, gate_col >= 0 ? base + gate_col : nullptr, gate_bias};
+  return Cols<In>{base + la_col, la_bias, A, la_floor, gate_col >= 0 ? base + gate_col : nullptr, gate_bias,
+                  beta_col >= 0 ? base + beta_col : nullptr, beta_bias, beta_min};
 }
 
 }  // namespace
 
 extern "C" int pragnosia_aspin_prep_proj_fwd(const void* P, int64_t stride, int64_t la_col, int64_t gate_col,
-                                             const float* la_bias, const float* A, const float* la_floor,
-                                             const float* gate_bias, const float* theta, const int64_t* pos, void* q,
-                                             void* k, void* v, float* la, int64_t B, int64_t T, int64_t H,
-                                             int64_t Dh, int in_bf16, void* stream) {
+                                             int64_t beta_col, const float* la_bias, const float* A,
+                                             const float* la_floor, const float* gate_bias, const float* beta_bias,
+                                             float beta_min, const float* theta, const int64_t* pos, void* q,
+                                             void* k, void* v, float* la, float* beta, int64_t B, int64_t T,
+                                             int64_t H, int64_t Dh, int in_bf16, void* stream) {
   if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, T, H));
-  PGN_CHECK_ARG(P && la_bias && A && theta && pos && q && k && v && la);
-  PGN_CHECK_ARG(proj_cols_ok(H, stride, la_col, gate_col));
+  PGN_CHECK_ARG(P && la_bias && A && theta && pos && q && k && v && la && (beta_col < 0 || beta));
+  PGN_CHECK_ARG(proj_cols_ok(H, stride, la_col, gate_col, beta_col));
   const int ntb = (int)((T + TB - 1) / TB);
   const dim3 grid((unsigned)(B * H * ntb));
   const int64_t hd = H * D;
@@ -376,12 +399,16 @@ extern "C" int pragnosia_aspin_prep_proj_fwd(const void* P, int64_t stride, int6
     const __bf16* p = (const __bf16*)P;
     hipLaunchKernelGGL(prep_fwd<__bf16>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
                        (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb, stride,
-                       proj_cols<__bf16>(P, la_col, gate_col, la_bias, A, la_floor, gate_bias), la);
+                       proj_cols<__bf16>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias, beta_bias,
+                                         beta_min),
+                       la, beta);
   } else {
     const float* p = (const float*)P;
     hipLaunchKernelGGL(prep_fwd<float>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
                        (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb, stride,
-                       proj_cols<float>(P, la_col, gate_col, la_bias, A, la_floor, gate_bias), la);
+                       proj_cols<float>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias, beta_bias,
+                                        beta_min),
+                       la, beta);
   }
   PGN_RETURN_LAUNCH();
 }
@@ -392,15 +419,18 @@ extern "C" int64_t pragnosia_aspin_prep_proj_partials(int64_t B, int64_t T, int6
 }
 
 extern "C" int pragnosia_aspin_prep_proj_bwd(const void* P, int64_t stride, int64_t la_col, int64_t gate_col,
-                                             const float* la_bias, const float* A, const float* la_floor,
-                                             const float* gate_bias, const float* theta, const int64_t* pos,
+                                             int64_t beta_col, const float* la_bias, const float* A,
+                                             const float* la_floor, const float* gate_bias, const float* beta_bias,
+                                             float beta_min, const float* theta, const int64_t* pos,
                                              const void* dq, const void* dk, const void* dv, const float* dla,
-                                             void* dP, float* dtheta_partial, float* part, int64_t B, int64_t T,
-                                             int64_t H, int64_t Dh, int in_bf16, void* stream) {
+                                             const float* dbeta, void* dP, float* dtheta_partial, float* part,
+                                             int64_t B, int64_t T, int64_t H, int64_t Dh, int in_bf16,
+                                             void* stream) {
   if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, T, H));
   PGN_CHECK_ARG(P && la_bias && A && theta && pos && dq && dk && dv && dla && dP && dtheta_partial && part);
-  PGN_CHECK_ARG(proj_cols_ok(H, stride, la_col, gate_col) && P != dP);
+  PGN_CHECK_ARG(beta_col < 0 || dbeta);
+  PGN_CHECK_ARG(proj_cols_ok(H, stride, la_col, gate_col, beta_col) && P != dP);
   const int ntb = (int)((T + TB - 1) / TB);
   const dim3 grid((unsigned)(B * H * ntb));
   const int64_t hd = H * D;
@@ -411,14 +441,18 @@ extern "C" int pragnosia_aspin_prep_proj_bwd(const void* P, int64_t stride, int6
     hipLaunchKernelGGL(prep_bwd<__bf16>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
                        (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv, d, d + hd, d + 2 * hd, nullptr,
                        dtheta_partial, (int)T, (int)H, ntb, stride,
-                       proj_cols<__bf16>(P, la_col, gate_col, la_bias, A, la_floor, gate_bias), dla, d, part);
+                       proj_cols<__bf16>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias, beta_bias,
+                                         beta_min),
+                       dla, dbeta, d, part);
   } else {
     const float* p = (const float*)P;
     float* d = (float*)dP;
     hipLaunchKernelGGL(prep_bwd<float>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
                        (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv, d, d + hd, d + 2 * hd, nullptr,
                        dtheta_partial, (int)T, (int)H, ntb, stride,
-                       proj_cols<float>(P, la_col, gate_col, la_bias, A, la_floor, gate_bias), dla, d, part);
+                       proj_cols<float>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias, beta_bias,
+                                        beta_min),
+                       dla, dbeta, d, part);
   }
   PGN_RETURN_LAUNCH();
 }

@@ -508,89 +508,118 @@ def _prep_backward(ctx, dq, dk, dv):
 aspin_prep.register_autograd(_prep_backward, setup_context=_prep_setup)
 
 
+def _proj_cols(H: int, gated: bool, has_beta: bool) -> tuple[int, int, int]:
+    """Column offsets (decay, gate, strength; -1 = absent) in the projection GEMM's output rows."""
+    base = 3 * H * 64
+    return base, (base + H if gated else -1), (base + H if has_beta else -1)
+
+
 @torch.library.custom_op("pragnosia::aspin_prep_proj", mutates_args=())
 def aspin_prep_proj(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Optional[Tensor],
-                    gate_bias: Optional[Tensor], theta: Tensor, pos: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """The carrier's inputs to the scan from ONE GEMM's output P (B, T, 3 H 64 + H [+ H]) (fp32 or bf16): q, k, v
-    projections in the first 3 H 64 columns, then the decay logits, then (when gate_bias is given) the write-gate
-    logits, all before their biases. Returns bf16 q, k, v (B, H, T, 64) (normalised, k gated, q and k rotated by
-    pos * theta) and la (B, H, T) fp32 = -softplus(logit + la_bias) exp(A), floored at la_floor when given."""
-    _require_gpu(P, la_bias, A, la_floor, gate_bias, theta, pos)
+                    gate_bias: Optional[Tensor], beta_bias: Optional[Tensor], beta_min: float, gated: bool,
+                    theta: Tensor, pos: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The carrier's inputs to the scan from ONE GEMM's output P (B, T, 3 H 64 + 2 H) (fp32 or bf16): the q, k, v
+    projections in the first 3 H 64 columns, then the decay logits, then either the plain rule's write-gate logits
+    (gated) or the delta rule's write-strength logits (beta_bias given, or beta_min > 0), all before their biases.
+    Returns bf16 q, k, v (B, H, T, 64) (normalised, k gated, q and k rotated by pos * theta), la (B, H, T) fp32 =
+    -softplus(logit + la_bias) exp(A) (floored at la_floor when given) and beta (B, H, T) fp32 =
+    max(sigmoid(logit + beta_bias), beta_min) for the delta rule (else an empty tensor)."""
+    _require_gpu(P, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos)
     P = _proj(P)
-    la_bias, A, la_floor, gate_bias, theta = _f32(la_bias), _f32(A), _f32(la_floor), _f32(gate_bias), _f32(theta)
+    la_bias, A, la_floor, theta = _f32(la_bias), _f32(A), _f32(la_floor), _f32(theta)
+    gate_bias, beta_bias = _f32(gate_bias), _f32(beta_bias)
     pos = pos.to(torch.int64).contiguous()
     B, T, W = P.shape
     D = 64
+    has_beta = not gated and W > 3 * H * D + H
     q, k, v = (torch.empty(B, H, T, D, device=P.device, dtype=torch.bfloat16) for _ in range(3))
     la = torch.empty(B, H, T, device=P.device, dtype=torch.float32)
-    gcol = 3 * H * D + H if gate_bias is not None else -1
-    check(lib().pragnosia_aspin_prep_proj_fwd(_ptr(P), W, 3 * H * D, gcol, _ptr(la_bias), _ptr(A), _ptr(la_floor),
-                                              _ptr(gate_bias), _ptr(theta), _ptr(pos), _ptr(q), _ptr(k), _ptr(v),
-                                              _ptr(la), B, T, H, D, int(P.dtype == torch.bfloat16), _stream(P)),
+    beta = (torch.empty(B, H, T, device=P.device, dtype=torch.float32) if has_beta
+            else P.new_empty(0, dtype=torch.float32))
+    acol, gcol, bcol = _proj_cols(H, gated, has_beta)
+    check(lib().pragnosia_aspin_prep_proj_fwd(_ptr(P), W, acol, gcol, bcol, _ptr(la_bias), _ptr(A), _ptr(la_floor),
+                                              _ptr(gate_bias), _ptr(beta_bias), float(beta_min), _ptr(theta),
+                                              _ptr(pos), _ptr(q), _ptr(k), _ptr(v), _ptr(la),
+                                              _ptr(beta) if has_beta else None, B, T, H, D,
+                                              int(P.dtype == torch.bfloat16), _stream(P)),
           "pragnosia_aspin_prep_proj_fwd")
-    return q, k, v, la
+    return q, k, v, la, beta
 
 
 @aspin_prep_proj.register_fake
-def _(P, H, la_bias, A, la_floor, gate_bias, theta, pos):
-    B, T, _ = P.shape
+def _(P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, pos):
+    B, T, W = P.shape
     b = lambda: P.new_empty(B, H, T, 64, dtype=torch.bfloat16)
-    return b(), b(), b(), P.new_empty(B, H, T, dtype=torch.float32)
+    has_beta = not gated and W > 3 * H * 64 + H
+    beta = P.new_empty(B, H, T, dtype=torch.float32) if has_beta else P.new_empty(0, dtype=torch.float32)
+    return b(), b(), b(), P.new_empty(B, H, T, dtype=torch.float32), beta
 
 
 @torch.library.custom_op("pragnosia::aspin_prep_proj_bwd", mutates_args=())
 def aspin_prep_proj_bwd(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Optional[Tensor],
-                        gate_bias: Optional[Tensor], theta: Tensor, pos: Tensor, dq: Tensor, dk: Tensor, dv: Tensor,
-                        dla: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Backward of aspin_prep_proj. Returns (dP in P's dtype and layout, d la_bias, dA, d gate_bias (empty when no
-    gate), dtheta), the per-head sums reduced from the kernel's partials."""
-    _require_gpu(P, dq, dk, dv, dla)
+                        gate_bias: Optional[Tensor], beta_bias: Optional[Tensor], beta_min: float, gated: bool,
+                        theta: Tensor, pos: Tensor, dq: Tensor, dk: Tensor, dv: Tensor, dla: Tensor,
+                        dbeta: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Backward of aspin_prep_proj. Returns (dP in P's dtype and layout, d la_bias, dA, d gate_bias or d beta_bias
+    (the one in use; empty when neither), dtheta), the per-head sums reduced from the kernel's partials."""
+    _require_gpu(P, dq, dk, dv, dla, dbeta)
     P = _proj(P)
-    la_bias, A, la_floor, gate_bias, theta = _f32(la_bias), _f32(A), _f32(la_floor), _f32(gate_bias), _f32(theta)
+    la_bias, A, la_floor, theta = _f32(la_bias), _f32(A), _f32(la_floor), _f32(theta)
+    gate_bias, beta_bias = _f32(gate_bias), _f32(beta_bias)
     pos = pos.to(torch.int64).contiguous()
     dq, dk, dv, dla = _bf16(dq), _bf16(dk), _bf16(dv), _f32(dla)
     B, T, W = P.shape
     D = 64
+    has_beta = not gated and W > 3 * H * D + H
+    if has_beta:
+        dbeta = torch.zeros(B, H, T, device=P.device) if dbeta is None else _f32(dbeta)
     dP = torch.empty_like(P)
-    if W > 3 * H * D + (2 if gate_bias is not None else 1) * H:
+    if W > 3 * H * D + (2 if (gated or has_beta) else 1) * H:
         dP.zero_()  # columns the kernel does not write
     rows = lib().pragnosia_aspin_prep_theta_partials(B, T)
     dth = torch.empty(rows, H, D // 2, device=P.device, dtype=torch.float32)
     part = torch.empty(lib().pragnosia_aspin_prep_proj_partials(B, T, H), 3, device=P.device, dtype=torch.float32)
-    gcol = 3 * H * D + H if gate_bias is not None else -1
-    check(lib().pragnosia_aspin_prep_proj_bwd(_ptr(P), W, 3 * H * D, gcol, _ptr(la_bias), _ptr(A), _ptr(la_floor),
-                                              _ptr(gate_bias), _ptr(theta), _ptr(pos), _ptr(dq), _ptr(dk), _ptr(dv),
-                                              _ptr(dla), _ptr(dP), _ptr(dth), _ptr(part), B, T, H, D,
-                                              int(P.dtype == torch.bfloat16), _stream(P)),
+    acol, gcol, bcol = _proj_cols(H, gated, has_beta)
+    check(lib().pragnosia_aspin_prep_proj_bwd(_ptr(P), W, acol, gcol, bcol, _ptr(la_bias), _ptr(A), _ptr(la_floor),
+                                              _ptr(gate_bias), _ptr(beta_bias), float(beta_min), _ptr(theta),
+                                              _ptr(pos), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla),
+                                              _ptr(dbeta) if has_beta else None, _ptr(dP), _ptr(dth), _ptr(part),
+                                              B, T, H, D, int(P.dtype == torch.bfloat16), _stream(P)),
           "pragnosia_aspin_prep_proj_bwd")
     sums = part.view(B, H, -1, 3).sum((0, 2))
-    dgb = sums[:, 0].clone() if gate_bias is not None else P.new_empty(0, dtype=torch.float32)
-    return dP, sums[:, 1].clone(), sums[:, 2].clone(), dgb, dth.sum(0)
+    dxb = sums[:, 0].clone() if (gated or has_beta) else P.new_empty(0, dtype=torch.float32)
+    return dP, sums[:, 1].clone(), sums[:, 2].clone(), dxb, dth.sum(0)
 
 
 @aspin_prep_proj_bwd.register_fake
-def _(P, H, la_bias, A, la_floor, gate_bias, theta, pos, dq, dk, dv, dla):
+def _(P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, pos, dq, dk, dv, dla, dbeta):
     f = lambda *s: P.new_empty(*s, dtype=torch.float32)
-    return (torch.empty_like(P), f(H), f(H), f(H) if gate_bias is not None else f(0), f(H, 32))
+    has_beta = not gated and P.shape[-1] > 3 * H * 64 + H
+    return (torch.empty_like(P), f(H), f(H), f(H) if (gated or has_beta) else f(0), f(H, 32))
 
 
 def _prep_proj_setup(ctx, inputs, output):
-    P, H, la_bias, A, la_floor, gate_bias, theta, pos = inputs
-    ctx.H = H
-    ctx.dtypes = (P.dtype, la_bias.dtype, A.dtype, None if gate_bias is None else gate_bias.dtype, theta.dtype)
-    ctx.save_for_backward(P, la_bias, A, la_floor, gate_bias, theta, pos)
+    P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, pos = inputs
+    ctx.H, ctx.beta_min, ctx.gated = H, beta_min, gated
+    ctx.bias_dtype = (gate_bias if gated else beta_bias)
+    ctx.bias_dtype = None if ctx.bias_dtype is None else ctx.bias_dtype.dtype
+    ctx.dtypes = (P.dtype, la_bias.dtype, A.dtype, theta.dtype)
+    ctx.save_for_backward(P, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos)
+    ctx.mark_non_differentiable(*[t for t in output[4:] if t.numel() == 0])
 
 
-def _prep_proj_backward(ctx, dq, dk, dv, dla):
-    P, la_bias, A, la_floor, gate_bias, theta, pos = ctx.saved_tensors
+def _prep_proj_backward(ctx, dq, dk, dv, dla, dbeta):
+    P, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos = ctx.saved_tensors
     B, T, _ = P.shape
     zb = lambda t: torch.zeros(B, ctx.H, T, 64, device=P.device, dtype=torch.bfloat16) if t is None else t
     dla = torch.zeros(B, ctx.H, T, device=P.device) if dla is None else dla
-    dP, dlb, dA, dgb, dth = aspin_prep_proj_bwd(P, ctx.H, la_bias, A, la_floor, gate_bias, theta, pos, zb(dq), zb(dk),
-                                                zb(dv), dla)
+    dP, dlb, dA, dxb, dth = aspin_prep_proj_bwd(P, ctx.H, la_bias, A, la_floor, gate_bias, beta_bias, ctx.beta_min,
+                                                ctx.gated, theta, pos, zb(dq), zb(dk), zb(dv), dla,
+                                                dbeta if (dbeta is not None and dbeta.numel()) else None)
     dt = ctx.dtypes
-    return (dP.to(dt[0]), None, dlb.to(dt[1]), dA.to(dt[2]), None, (dgb.to(dt[3]) if gate_bias is not None else None),
-            dth.to(dt[4]), None)
+    dgb = dxb.to(ctx.bias_dtype) if (ctx.gated and gate_bias is not None) else None
+    dbb = dxb.to(ctx.bias_dtype) if (not ctx.gated and beta_bias is not None) else None
+    return (dP.to(dt[0]), None, dlb.to(dt[1]), dA.to(dt[2]), None, dgb, dbb, None, None, dth.to(dt[3]), None)
 
 
 aspin_prep_proj.register_autograd(_prep_proj_backward, setup_context=_prep_proj_setup)

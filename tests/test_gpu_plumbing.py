@@ -39,7 +39,7 @@ def test_prep_proj_matches_composition(gated, floor, dtype):
     Pd, lbd, Ad, fld, gbd, thd = ins
     if fld is not None:
         fld.requires_grad_(False)
-    q, k, v, la = op.aspin_prep_proj(Pd, H, lbd, Ad, fld, gbd, thd, pos.cuda())
+    q, k, v, la, _ = op.aspin_prep_proj(Pd, H, lbd, Ad, fld, gbd, None, 0.0, gated, thd, pos.cuda())
     gq, gk, gv, gl = (torch.randn(t.shape, generator=g) for t in (q, k, v, la))
     ((q.float() * gq.cuda()).sum() + (k.float() * gk.cuda()).sum() + (v.float() * gv.cuda()).sum()
      + (la * gl.cuda()).sum()).backward()
@@ -65,14 +65,52 @@ def test_prep_proj_matches_composition(gated, floor, dtype):
         assert rel(a.grad, b.grad) < gtol
 
 
-@pytest.mark.parametrize("autocast", [False, True])
-@pytest.mark.parametrize("write_all,hl_floor", [(False, False), (True, True)])
-def test_module_fused_plumbing_equals_composition(autocast, write_all, hl_floor):
+@pytest.mark.parametrize("write_all", [False, True])
+def test_prep_proj_write_strength_matches_composition(write_all):
+    """The delta rule's columns: beta = max(sigmoid(logit + b), 0.75 under write_all) alongside the decay, with
+    its gradient into the same buffer."""
+    import pragnosia_amd.ops  # noqa: F401
+    op = torch.ops.pragnosia
+    g = torch.Generator().manual_seed(20 + write_all)
+    B, T, H = 2, 130, 2
+    d = 64 * H
+    P = torch.randn(B, T, 3 * d + 2 * H, generator=g) * 0.7
+    la_b, A, bb = torch.randn(H, generator=g), torch.randn(H, generator=g) - 2.0, torch.randn(H, generator=g)
+    th = torch.rand(H, 32, generator=g) * 0.1
+    pos = torch.arange(T).cuda()
+    bmin = 0.75 if write_all else 0.0
+    Pd, lbd, Ad, bbd, thd = (t.cuda().requires_grad_(True) for t in (P, la_b, A, bb, th))
+    q, k, v, la, beta = op.aspin_prep_proj(Pd, H, lbd, Ad, None, None, bbd, bmin, False, thd, pos)
+    ws = [torch.randn(t.shape, generator=g).cuda() for t in (q, k, v, la, beta)]
+    sum(((t.float() * w).sum() for t, w in zip((q, k, v, la, beta), ws))).backward()
+    Pr, lbr, Ar, bbr, thr = (t.cuda().requires_grad_(True) for t in (P, la_b, A, bb, th))
+    qp, kp, vp = (Pr[..., i * d:(i + 1) * d].reshape(B, T, H, 64) for i in range(3))
+    q2, k2, v2 = op.aspin_prep(qp, kp, vp, None, thr, pos)
+    la2 = (-F.softplus(Pr[..., 3 * d:3 * d + H] + lbr) * torch.exp(Ar)).transpose(1, 2)
+    b2 = torch.sigmoid(Pr[..., 3 * d + H:] + bbr)
+    if write_all:
+        b2 = b2.clamp(min=0.75)
+    b2 = b2.transpose(1, 2)
+    sum(((t.float() * w).sum() for t, w in zip((q2, k2, v2, la2, b2), ws))).backward()
+    for a, b in ((q, q2), (k, k2), (v, v2)):
+        assert rel(a, b) < 2 ** -8
+    assert rel(la, la2) < 1e-5 and rel(beta, b2) < 1e-5
+    for a, b in ((Pd, Pr), (lbd, lbr), (Ad, Ar), (bbd, bbr), (thd, thr)):
+        assert rel(a.grad, b.grad) < 1e-3
+
+
+@pytest.mark.parametrize("delta,write_all,hl_floor", [(False, False, False), (False, True, True),
+                                                      (True, False, False), (True, True, True)])
+def test_module_fused_plumbing_equals_composition(delta, write_all, hl_floor):
     """AssocCarrier forward and backward (every parameter's gradient, the input's, the carried state's) with the
-    fused plumbing and with the reference's composition, from the same parameters."""
+    fused plumbing and with the reference's composition, from the same parameters. In fp32 the two agree within the
+    bf16 bounds (q, k, v and o pass through bf16 on both, rounded differently). Under bf16 autocast both move away
+    from the fp32 run by bf16 arithmetic (the weight gradients of the small decay and strength projections most:
+    measured 8% on wa.weight for both, 4% vs 22% on wb.weight); the fused path must stay within the bf16 bounds of
+    the fp32 run or, where the composition itself does not, no further than 1.25 times the composition's distance."""
     from pragnosia_amd import assoc
     torch.manual_seed(11)
-    m = assoc.AssocCarrier(256, write_all=write_all, hl_floor=hl_floor).cuda()
+    m = assoc.AssocCarrier(256, delta=delta, write_all=write_all, hl_floor=hl_floor).cuda()
     with torch.no_grad():
         for p in m.parameters():
             p.add_(torch.randn_like(p) * 0.05)
@@ -84,20 +122,22 @@ def test_module_fused_plumbing_equals_composition(autocast, write_all, hl_floor)
     prev = assoc.FUSED_PLUMBING
     try:
         for fused in (True, False):
-            assoc.FUSED_PLUMBING = fused
-            m.zero_grad(set_to_none=True)
-            xi, Si = x.clone().requires_grad_(True), S0.clone().requires_grad_(True)
-            with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
-                y, (S, _) = m(xi, (Si, 17))
-            ((y.float() * gy).sum() + (S * gS).sum()).backward()
-            res[fused] = (y.detach(), S.detach(), xi.grad, Si.grad,
-                          {n: p.grad.clone() for n, p in m.named_parameters() if p.grad is not None})
+            for autocast in (False, True):
+                assoc.FUSED_PLUMBING = fused
+                m.zero_grad(set_to_none=True)
+                xi, Si = x.clone().requires_grad_(True), S0.clone().requires_grad_(True)
+                with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+                    y, (S, _) = m(xi, (Si, 17))
+                ((y.float() * gy).sum() + (S * gS).sum()).backward()
+                out = {"y": y.detach() - x, "S": S.detach(), "dx": xi.grad, "dS0": Si.grad}
+                out.update({n: p.grad.clone() for n, p in m.named_parameters() if p.grad is not None})
+                res[(fused, autocast)] = out
     finally:
         assoc.FUSED_PLUMBING = prev
-    a, b = res[True], res[False]
-    otol, gtol = 2e-2, 5e-2  # both sides cast q, k, v and o to bf16: their roundings differ, and that propagates
-    assert rel(a[0] - x, b[0] - x) < otol and rel(a[1], b[1]) < otol
-    assert rel(a[2], b[2]) < gtol and rel(a[3], b[3]) < gtol
-    assert set(a[4]) == set(b[4])
-    for n in a[4]:
-        assert rel(a[4][n], b[4][n]) < gtol, n
+    ref = res[(True, False)]
+    tol = lambda n: 2e-2 if n in ("y", "S") else 5e-2
+    assert set(res[(False, False)]) == set(ref) == set(res[(True, True)])
+    for n in ref:
+        assert rel(res[(False, False)][n], ref[n]) < tol(n), n
+        e_fused, e_comp = rel(res[(True, True)][n], ref[n]), rel(res[(False, True)][n], ref[n])
+        assert e_fused < max(tol(n), 1.25 * e_comp), (n, e_fused, e_comp)
