@@ -412,15 +412,18 @@ def decode_bench(n_tokens=1024):
 TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "pmc_traffic_configs.md")
 
 
-def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` as measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
-    profiles/pmc_traffic_configs.md (copy-calibrated), or None when the kernel is not in that table."""
+def measured_traffic(kernel, launch="configs[2]"):
+    """HBM bytes per launch of `kernel` at the named launch as measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes recorded in profiles/pmc_traffic_configs.md (copy-calibrated), or None when the table has no such row."""
     try:
+        col = None
         for line in open(TRAFFIC_TABLE):
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
-            if len(cells) >= 4 and cells[0] == kernel:
-                return int(cells[3])
-    except OSError:
+            if col is None and "traffic_bytes (calibrated)" in cells:
+                col = cells.index("traffic_bytes (calibrated)")
+            elif col is not None and len(cells) > col and cells[0] == kernel and launch in cells[1]:
+                return int(cells[col])
+    except (OSError, ValueError):
         return None
     return None
 
@@ -594,6 +597,27 @@ def profile_kernels(reps=10):
     for _ in range(reps):
         op.diag_scan(u, lm, an, None, None)
         op.diag_scan_bwd(gy, None, None, lm, an, hr, hi, None, None)
+    # the segment-parallel forward and backward at configs[3]'s unsplit shape (B2 H12 T8192)
+    x = aspin_inputs(2, 12, 8192, 64, 3, "plain", dev)
+    for _ in range(reps):
+        o, S, sent = op.aspin_chunk(x["q"], x["k"], x["v"], x["la"], None, True)
+        op.aspin_chunk_bwd(x["q"], x["k"], x["v"], x["la"], sent, x["do"], x["dS"])
+    # the carrier's plumbing at configs[2]'s shape: the prep from one projection GEMM's bf16 output (q, k, v, decay and
+    # gate columns) and the output epilogue, each way
+    H = 12
+    g = torch.Generator(device=dev).manual_seed(5)
+    P = torch.randn(16, 512, 3 * H * 64 + 2 * H, device=dev, generator=g).bfloat16()
+    lb, A, gb = (torch.randn(H, device=dev, generator=g) for _ in range(3))
+    th = torch.rand(H, 32, device=dev, generator=g) * 0.1
+    pos = torch.arange(512, device=dev)
+    o = x_o = torch.randn(16, H, 512, 64, device=dev, generator=g).bfloat16()
+    w = torch.randn(64, device=dev, generator=g)
+    gyo = torch.randn(16, 512, H * 64, device=dev, generator=g).bfloat16()
+    for _ in range(reps):
+        q, k, v, la, _ = op.aspin_prep_proj(P, H, lb, A, None, gb, None, 0.0, True, th, pos)
+        op.aspin_prep_proj_bwd(P, H, lb, A, None, gb, None, 0.0, True, th, pos, q, k, v, la, None)
+        y, rstd = op.aspin_out(x_o, w, ops.RMS_EPS, True)
+        op.aspin_out_bwd(gyo, o, w, rstd)
     torch.cuda.synchronize()
     print(json.dumps({"profile_kernels": reps, "copy_bytes": COPY_BYTES}), flush=True)
 
