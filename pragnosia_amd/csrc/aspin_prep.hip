@@ -10,8 +10,9 @@
 // writing the projections' gradients in THEIR layout, the gate's per (b, t, h), and theta's as one partial sum per
 // (batch, 64-token block) that the caller reduces.
 //
-// One workgroup of 256 threads per (batch, head, 64-token block): 32 threads per row (one channel pair each), 8 rows
-// per pass, 8 passes. Row loads are 128 or 256 contiguous bytes; normalisation is a 32-lane butterfly. The projections
+// One workgroup of 256 threads per (batch, head, 64-token block): 8 threads per row (eight channels, four rotation
+// pairs each, one 16-byte access per tensor for bf16), 32 rows per pass, 2 passes; the norms are 8-lane
+// butterflies. The projections
 // (and their gradients) may be column slices of one wider row per token (`in_stride` elements apart), such as one
 // GEMM's output holding q, k, v and the gate logits side by side.
 //
@@ -23,41 +24,6 @@ namespace {
 
 constexpr int D = 64;
 constexpr int TB = 64;    // tokens per workgroup
-constexpr int ROWS = 8;   // rows per pass
-
-template <typename In>
-PGN_DEVICE float2 ld2(const In* p);
-template <>
-PGN_DEVICE float2 ld2<float>(const float* p) { return *reinterpret_cast<const float2*>(p); }
-template <>
-PGN_DEVICE float2 ld2<__bf16>(const __bf16* p) {
-  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-  const bf16x2 x = *reinterpret_cast<const bf16x2*>(p);
-  return make_float2((float)x[0], (float)x[1]);
-}
-
-template <typename Out>
-PGN_DEVICE void st2(Out* p, float a, float b);
-template <>
-PGN_DEVICE void st2<float>(float* p, float a, float b) { *reinterpret_cast<float2*>(p) = make_float2(a, b); }
-template <>
-PGN_DEVICE void st2<__bf16>(__bf16* p, float a, float b) {
-  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-  bf16x2 x;
-  x[0] = (__bf16)a;
-  x[1] = (__bf16)b;
-  *reinterpret_cast<bf16x2*>(p) = x;
-}
-
-// sum over the 32 lanes that share a row (lane bits 0..4)
-PGN_DEVICE float sum32(float x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 4);
-  x += __shfl_xor(x, 8);
-  x += __shfl_xor(x, 16);
-  return x;
-}
 
 PGN_DEVICE float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
 
@@ -83,6 +49,59 @@ struct Cols {
   float bmin;
 };
 
+// 8 consecutive channels of one row: one 16-byte access (bf16) or two (fp32)
+template <typename T_>
+PGN_DEVICE void ld8(const T_* p, float* x);
+template <>
+PGN_DEVICE void ld8<float>(const float* p, float* x) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = a[e];
+    x[4 + e] = b[e];
+  }
+}
+template <>
+PGN_DEVICE void ld8<__bf16>(const __bf16* p, float* x) {
+  const bf16x8 a = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = (float)a[e];
+}
+template <typename T_>
+PGN_DEVICE void st8(T_* p, const float* x);
+template <>
+PGN_DEVICE void st8<float>(float* p, const float* x) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+  *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
+}
+template <>
+PGN_DEVICE void st8<__bf16>(__bf16* p, const float* x) {
+  bf16x8 a;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = (__bf16)x[e];
+  *reinterpret_cast<bf16x8*>(p) = a;
+}
+
+// sum over the 8 lanes that share a row (lane bits 0..2)
+PGN_DEVICE float sum8(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  return x;
+}
+
+PGN_DEVICE float inv_norm8(const float* x) {
+  float n = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) n += x[e] * x[e];
+  return 1.f / fmaxf(sqrtf(sum8(n)), 1e-12f);
+}
+
+// Thread = (row slot rs = tid / 8, channel group j = tid % 8): channels 8 j .. 8 j + 7 of one row, i.e. the
+// interleaved pairs 4 j .. 4 j + 3; 32 rows per pass, two passes per 64-token block.
+constexpr int LANES = 8;
+constexpr int SLOTS = 256 / LANES;
+
 template <typename In>
 __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const In* __restrict__ kp,
                                                 const In* __restrict__ vp, const float* __restrict__ gl,
@@ -94,40 +113,53 @@ __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const
   const int blk = blockIdx.x;
   const int bh = blk / ntb, tb = blk - bh * ntb;
   const int b = bh / H, h = bh - b * H;
-  const int i = threadIdx.x & 31, rs = threadIdx.x >> 5;
-  const float th = theta[h * (D / 2) + i];
+  const int j = threadIdx.x & (LANES - 1), rs = threadIdx.x / LANES;
+  float th[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) th[u] = theta[h * (D / 2) + 4 * j + u];
   const float eA = cols.acol ? __expf(cols.A[h]) : 0.f;
-#pragma unroll 2
-  for (int p = 0; p < TB / ROWS; ++p) {
-    const int t = tb * TB + p * ROWS + rs;
+#pragma unroll
+  for (int p = 0; p < TB / SLOTS; ++p) {
+    const int t = tb * TB + p * SLOTS + rs;
     if (t >= T) break;
     const size_t row = ((size_t)b * T + t) * S;
-    const size_t in = row + h * D + 2 * i;
-    const size_t out = ((size_t)bh * T + t) * D + 2 * i;
-    const float2 xq = ld2<In>(qp + in), xk = ld2<In>(kp + in), xv = ld2<In>(vp + in);
-    const float nq = sum32(xq.x * xq.x + xq.y * xq.y);
-    const float nk = sum32(xk.x * xk.x + xk.y * xk.y);
-    const float nv = sum32(xv.x * xv.x + xv.y * xv.y);
-    const float iq = 1.f / fmaxf(sqrtf(nq), 1e-12f);
-    float ik = 1.f / fmaxf(sqrtf(nk), 1e-12f);
-    const float iv = 1.f / fmaxf(sqrtf(nv), 1e-12f);
+    const size_t in = row + h * D + 8 * j;
+    const size_t out = ((size_t)bh * T + t) * D + 8 * j;
+    float xq[8], xk[8], xv[8];
+    ld8<In>(qp + in, xq);
+    ld8<In>(kp + in, xk);
+    ld8<In>(vp + in, xv);
+    const float iq = inv_norm8(xq), iv = inv_norm8(xv);
+    float ik = inv_norm8(xk);
     if (cols.gcol)
       ik *= sigmoidf_((float)cols.gcol[row + h] + (cols.gbias ? cols.gbias[h] : 0.f));
     else if (gl)
       ik *= sigmoidf_(gl[((size_t)b * T + t) * H + h]);
-    if (cols.acol && i == 0) {
+    if (cols.acol && j == 0) {
       float l = -softplusf_((float)cols.acol[row + h] + cols.abias[h]) * eA;
       if (cols.floor) l = fmaxf(l, cols.floor[h]);
       la[(size_t)bh * T + t] = l;
     }
-    if (cols.bcol && i == 0)
+    if (cols.bcol && j == 0)
       beta[(size_t)bh * T + t] =
           fmaxf(sigmoidf_((float)cols.bcol[row + h] + (cols.bbias ? cols.bbias[h] : 0.f)), cols.bmin);
-    float s, c;
-    sincosf((float)pos[t] * th, &s, &c);
-    st2<__bf16>(q + out, (xq.x * c - xq.y * s) * iq, (xq.x * s + xq.y * c) * iq);
-    st2<__bf16>(k + out, (xk.x * c - xk.y * s) * ik, (xk.x * s + xk.y * c) * ik);
-    st2<__bf16>(v + out, xv.x * iv, xv.y * iv);
+    const float pt = (float)pos[t];
+    float oq[8], ok[8], ov[8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float sn, cs;
+      sincosf(pt * th[u], &sn, &cs);
+      const float q1 = xq[2 * u], q2 = xq[2 * u + 1], k1 = xk[2 * u], k2 = xk[2 * u + 1];
+      oq[2 * u] = (q1 * cs - q2 * sn) * iq;
+      oq[2 * u + 1] = (q1 * sn + q2 * cs) * iq;
+      ok[2 * u] = (k1 * cs - k2 * sn) * ik;
+      ok[2 * u + 1] = (k1 * sn + k2 * cs) * ik;
+      ov[2 * u] = xv[2 * u] * iv;
+      ov[2 * u + 1] = xv[2 * u + 1] * iv;
+    }
+    st8<__bf16>(q + out, oq);
+    st8<__bf16>(k + out, ok);
+    st8<__bf16>(v + out, ov);
   }
 }
 
@@ -144,21 +176,24 @@ __global__ __launch_bounds__(256) void prep_bwd(
     In* __restrict__ dvp, float* __restrict__ dgl, float* __restrict__ dth, int T, int H, int ntb, int64_t S,
     Cols<In> cols, const float* __restrict__ dla, const float* __restrict__ dbeta, In* __restrict__ dcol,
     float* __restrict__ part) {
-  __shared__ float red[ROWS][D / 2];
-  __shared__ float red3[ROWS][3];
+  __shared__ float red[SLOTS][D / 2];
+  __shared__ float red3[SLOTS][3];
   const int blk = blockIdx.x;
   const int bh = blk / ntb, tb = blk - bh * ntb;
   const int b = bh / H, h = bh - b * H;
-  const int i = threadIdx.x & 31, rs = threadIdx.x >> 5;
-  const float th = theta[h * (D / 2) + i];
+  const int j = threadIdx.x & (LANES - 1), rs = threadIdx.x / LANES;
+  float th[4], dth_acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < 4; ++u) th[u] = theta[h * (D / 2) + 4 * j + u];
   const float eA = cols.acol ? __expf(cols.A[h]) : 0.f;
-  float dth_acc = 0.f, dgb = 0.f, dab = 0.f, dA = 0.f;
-  for (int p = 0; p < TB / ROWS; ++p) {
-    const int t = tb * TB + p * ROWS + rs;
+  float dgb = 0.f, dab = 0.f, dA = 0.f;
+#pragma unroll
+  for (int p = 0; p < TB / SLOTS; ++p) {
+    const int t = tb * TB + p * SLOTS + rs;
     if (t >= T) break;
     const size_t row = ((size_t)b * T + t) * S;
-    const size_t in = row + h * D + 2 * i;
-    if (cols.acol && i == 0) {
+    const size_t in = row + h * D + 8 * j;
+    if (cols.acol && j == 0) {
       const float x = (float)cols.acol[row + h] + cols.abias[h];
       const float l = -softplusf_(x) * eA;
       const float g = (cols.floor && l < cols.floor[h]) ? 0.f : dla[(size_t)bh * T + t];
@@ -167,38 +202,56 @@ __global__ __launch_bounds__(256) void prep_bwd(
       dab += dx;
       dA += g * l;
     }
-    if (cols.bcol && i == 0) {
+    if (cols.bcol && j == 0) {
       const float sb = sigmoidf_((float)cols.bcol[row + h] + (cols.bbias ? cols.bbias[h] : 0.f));
       const float db = sb < cols.bmin ? 0.f : dbeta[(size_t)bh * T + t] * sb * (1.f - sb);
       dcol[row + (cols.bcol - qp) + h] = (In)db;
       dgb += db;
     }
-    const size_t out = ((size_t)bh * T + t) * D + 2 * i;
+    const size_t out = ((size_t)bh * T + t) * D + 8 * j;
     const float pt = (float)pos[t];
-    float s, c;
-    sincosf(pt * th, &s, &c);
-    float dang = 0.f;
+    float sn[4], cs[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) sincosf(pt * th[u], &sn[u], &cs[u]);
+    float dang[4] = {0.f, 0.f, 0.f, 0.f};
     {  // q: normalise, rotate
-      const float2 x = ld2<In>(qp + in);
-      const float2 gq = ld2<__bf16>(dq + out);
-      const float inv = 1.f / fmaxf(sqrtf(sum32(x.x * x.x + x.y * x.y)), 1e-12f);
-      const float u1 = x.x * inv, u2 = x.y * inv;
-      dang += gq.y * (u1 * c - u2 * s) - gq.x * (u1 * s + u2 * c);
-      const float du1 = gq.x * c + gq.y * s, du2 = gq.y * c - gq.x * s;
-      const float dot = sum32(u1 * du1 + u2 * du2);
-      st2<In>(dqp + in, (du1 - u1 * dot) * inv, (du2 - u2 * dot) * inv);
+      float x[8], g[8], du[8], o[8];
+      ld8<In>(qp + in, x);
+      ld8<__bf16>(dq + out, g);
+      const float inv = inv_norm8(x);
+      float dot = 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float u1 = x[2 * u] * inv, u2 = x[2 * u + 1] * inv, g1 = g[2 * u], g2 = g[2 * u + 1];
+        dang[u] += g2 * (u1 * cs[u] - u2 * sn[u]) - g1 * (u1 * sn[u] + u2 * cs[u]);
+        du[2 * u] = g1 * cs[u] + g2 * sn[u];
+        du[2 * u + 1] = g2 * cs[u] - g1 * sn[u];
+        dot += u1 * du[2 * u] + u2 * du[2 * u + 1];
+      }
+      dot = sum8(dot);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (du[e] - x[e] * inv * dot) * inv;
+      st8<In>(dqp + in, o);
     }
     {  // k: normalise, gate, rotate
-      const float2 x = ld2<In>(kp + in);
-      float2 gk = ld2<__bf16>(dk + out);
-      const float inv = 1.f / fmaxf(sqrtf(sum32(x.x * x.x + x.y * x.y)), 1e-12f);
-      const float u1 = x.x * inv, u2 = x.y * inv;
-      const float r1 = u1 * c - u2 * s, r2 = u1 * s + u2 * c;
+      float x[8], g[8], du[8], o[8], r[8];
+      ld8<In>(kp + in, x);
+      ld8<__bf16>(dk + out, g);
+      const float inv = inv_norm8(x);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float u1 = x[2 * u] * inv, u2 = x[2 * u + 1] * inv;
+        r[2 * u] = u1 * cs[u] - u2 * sn[u];
+        r[2 * u + 1] = u1 * sn[u] + u2 * cs[u];
+      }
       if (cols.gcol || gl) {
         const float sg = cols.gcol ? sigmoidf_((float)cols.gcol[row + h] + (cols.gbias ? cols.gbias[h] : 0.f))
                                    : sigmoidf_(gl[((size_t)b * T + t) * H + h]);
-        const float dsg = sum32(gk.x * r1 + gk.y * r2);
-        if (i == 0) {
+        float dsg = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dsg += g[e] * r[e];
+        dsg = sum8(dsg);
+        if (j == 0) {
           const float dlg = dsg * sg * (1.f - sg);
           if (cols.gcol) {
             dcol[row + (cols.gcol - qp) + h] = (In)dlg;
@@ -207,26 +260,42 @@ __global__ __launch_bounds__(256) void prep_bwd(
             dgl[((size_t)b * T + t) * H + h] = dlg;
           }
         }
-        gk.x *= sg;
-        gk.y *= sg;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[e] *= sg;
       }
-      dang += gk.y * r1 - gk.x * r2;
-      const float du1 = gk.x * c + gk.y * s, du2 = gk.y * c - gk.x * s;
-      const float dot = sum32(u1 * du1 + u2 * du2);
-      st2<In>(dkp + in, (du1 - u1 * dot) * inv, (du2 - u2 * dot) * inv);
+      float dot = 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float g1 = g[2 * u], g2 = g[2 * u + 1];
+        dang[u] += g2 * r[2 * u] - g1 * r[2 * u + 1];
+        du[2 * u] = g1 * cs[u] + g2 * sn[u];
+        du[2 * u + 1] = g2 * cs[u] - g1 * sn[u];
+        dot += x[2 * u] * inv * du[2 * u] + x[2 * u + 1] * inv * du[2 * u + 1];
+      }
+      dot = sum8(dot);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (du[e] - x[e] * inv * dot) * inv;
+      st8<In>(dkp + in, o);
     }
     {  // v: normalise
-      const float2 x = ld2<In>(vp + in);
-      const float2 gv = ld2<__bf16>(dv + out);
-      const float inv = 1.f / fmaxf(sqrtf(sum32(x.x * x.x + x.y * x.y)), 1e-12f);
-      const float u1 = x.x * inv, u2 = x.y * inv;
-      const float dot = sum32(u1 * gv.x + u2 * gv.y);
-      st2<In>(dvp + in, (gv.x - u1 * dot) * inv, (gv.y - u2 * dot) * inv);
+      float x[8], g[8], o[8];
+      ld8<In>(vp + in, x);
+      ld8<__bf16>(dv + out, g);
+      const float inv = inv_norm8(x);
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot += x[e] * inv * g[e];
+      dot = sum8(dot);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (g[e] - x[e] * inv * dot) * inv;
+      st8<In>(dvp + in, o);
     }
-    dth_acc += dang * pt;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dth_acc[u] += dang[u] * pt;
   }
-  red[rs][i] = dth_acc;
-  if (i == 0) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) red[rs][4 * j + u] = dth_acc[u];
+  if (j == 0) {
     red3[rs][0] = dgb;
     red3[rs][1] = dab;
     red3[rs][2] = dA;
@@ -235,13 +304,13 @@ __global__ __launch_bounds__(256) void prep_bwd(
   if (threadIdx.x < D / 2) {
     float a = 0.f;
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) a += red[r][threadIdx.x];
+    for (int r = 0; r < SLOTS; ++r) a += red[r][threadIdx.x];
     dth[(((size_t)b * ntb + tb) * H + h) * (D / 2) + threadIdx.x] = a;
   }
   if (part && threadIdx.x < 3) {
     float a = 0.f;
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) a += red3[r][threadIdx.x];
+    for (int r = 0; r < SLOTS; ++r) a += red3[r][threadIdx.x];
     part[(size_t)blk * 3 + threadIdx.x] = a;
   }
 }
