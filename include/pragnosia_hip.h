@@ -228,6 +228,34 @@ int pragnosia_aspin_decode_step(const float* S, float* S_out, const float* qp, c
                                 const float* p0_dev, float p0, float* o, int64_t B, int64_t H, int64_t D,
                                 void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * The carrier LM's single-token decode step, fused (all fp32, as the reference decodes).
+ *
+ * The carrier's recurrent step reading its inputs from ONE projection GEMV's output P (B, np): per sequence b,
+ * P[b] = [qp (H D) | kp (H D) | vp (H D) | ... ] with the decay logits (before bias) at columns la_col + h and either
+ * the write-gate logits (gate_col >= 0, plain rule) or the write-strength logits (beta_col >= 0, delta rule) at
+ * their columns (the other -1). Forms la = -softplus(logit + la_bias[h]) exp(A[h]) (floored at la_floor[h] when
+ * non-NULL), the gate logit + gate_bias[h], beta = max(sigmoid(logit + beta_bias[h]), beta_min), then runs the step of
+ * pragnosia_aspin_decode_step (S_out may equal S: in place) and writes the output per-head RMS-normalised and
+ * token-major: o[b][h D + j] = (o_j r) on_weight[j], r = 1 / sqrt(mean_j o_j^2 + on_eps). Replaces, inside the
+ * reference's graphed decode (src/bench.py:241-317), the T = 1 path of `AssocCarrier.forward` from its projections
+ * to `self.on(o).transpose(1, 2).reshape(B, T, D)` (src/assoc.py:384-505). */
+int pragnosia_aspin_decode_proj(const float* S, float* S_out, const float* P, int64_t np, int64_t la_col,
+                                int64_t gate_col, int64_t beta_col, const float* la_bias, const float* A,
+                                const float* la_floor, const float* gate_bias, const float* beta_bias, float beta_min,
+                                const float* theta, const float* p0_dev, float p0, const float* on_weight,
+                                float on_eps, float* o, int64_t B, int64_t H, int64_t D, void* stream);
+
+/* One dense layer of the decode step over B sequences: y (B, N) = act(scale * (W z) + bias) + resid, with W (N, K)
+ * row-major, z = LayerNorm(x) with ln_weight / ln_bias (may be NULL) / ln_eps when ln_weight is non-NULL (K <= 1024),
+ * else z = x (B, K); scale a device scalar or NULL (1); bias (N) or NULL; act 0 = identity, 1 = GELU (erf form);
+ * resid (B, N) or NULL. y must not alias x or resid. Replaces the LayerNorm + nn.Linear (+ GELU, + residual) calls of
+ * the carrier's projections and gated output projection, the MLP (src/model.py:552-560) and the tied head during
+ * decoding. */
+int pragnosia_decode_gemv(const float* x, int64_t B, int64_t K, const float* ln_weight, const float* ln_bias,
+                          float ln_eps, const float* W, int64_t N, const float* bias, const float* scale, int act,
+                          const float* resid, float* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,30 +20,79 @@ namespace {
 
 constexpr int D = 64;
 
-__global__ __launch_bounds__(256) void aspin_decode(const float* __restrict__ S, float* __restrict__ Sout,
-                                                    const float* __restrict__ qp, const float* __restrict__ kp,
-                                                    const float* __restrict__ vp, const float* __restrict__ gl,
-                                                    const float* __restrict__ la, const float* __restrict__ beta,
+// Where the step reads its inputs: separate (B, H, 64) projections and (B, H) gate / log-decay / strength arrays, or
+// (FROM_P) one projection GEMV's output row per sequence, P[b] = [q (H 64) | k | v | decay logits (H) | gate or
+// strength logits (H)], with the decay and the gate or strength formed here from their logits and biases as the
+// chunked path's prep does: la = -softplus(logit + la_b) exp(A) (floored), gate logit + gate_b, beta =
+// max(sigmoid(logit + beta_b), beta_min).
+struct StepIn {
+  const float* qp;
+  const float* kp;
+  const float* vp;
+  const float* gl;
+  const float* la;
+  const float* beta;
+  // FROM_P
+  const float* P;
+  int np;                 // row length of P
+  int la_col, gate_col, beta_col;  // -1: absent
+  const float* la_b;
+  const float* A;
+  const float* floor;
+  const float* gate_b;
+  const float* beta_b;
+  float beta_min;
+};
+
+PGN_DEVICE float softplus_(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+
+// With `on` (the per-head RMSNorm weight), the output is written normalised and token-major, o[b][h 64 + j] =
+// (o_j r) on_j with r = 1 / sqrt(mean_j o_j^2 + eps) (nn.RMSNorm(dk), eps=None: fp32 epsilon; `src/assoc.py:505`);
+// else o (B, H, 64) as computed.
+template <bool FROM_P>
+__global__ __launch_bounds__(256) void aspin_decode(const float* __restrict__ S, float* __restrict__ Sout, StepIn in,
                                                     const float* __restrict__ theta, const float* __restrict__ p0d,
-                                                    float p0h, float* __restrict__ o, int H) {
+                                                    float p0h, const float* __restrict__ on, float on_eps,
+                                                    float* __restrict__ o, int H) {
   __shared__ float qs[D], ks[D], vs[D];
   __shared__ float red[4][D];
-  const int bh = blockIdx.x, h = bh % H;
+  const int bh = blockIdx.x, h = bh % H, b = bh / H;
   const int tid = threadIdx.x, j = tid & 63, rg = tid >> 6;
   const size_t voff = (size_t)bh * D;
+  const float* prow = FROM_P ? in.P + (size_t)b * in.np : nullptr;
 
+  float la_v, gl_v = 0.f, be_v = 0.f;
+  bool has_g, has_b;
+  if constexpr (FROM_P) {
+    la_v = -softplus_(prow[in.la_col + h] + in.la_b[h]) * __expf(in.A[h]);
+    if (in.floor) la_v = fmaxf(la_v, in.floor[h]);
+    has_g = in.gate_col >= 0;
+    has_b = in.beta_col >= 0;
+    if (has_g) gl_v = prow[in.gate_col + h] + (in.gate_b ? in.gate_b[h] : 0.f);
+    if (has_b) be_v = fmaxf(1.f / (1.f + __expf(-(prow[in.beta_col + h] + (in.beta_b ? in.beta_b[h] : 0.f)))),
+                            in.beta_min);
+  } else {
+    la_v = in.la[bh];
+    has_g = in.gl != nullptr;
+    has_b = in.beta != nullptr;
+    if (has_g) gl_v = in.gl[bh];
+    if (has_b) be_v = in.beta[bh];
+  }
   if (rg < 3) {
-    const float* src = rg == 0 ? qp : (rg == 1 ? kp : vp);
-    const float x = src[voff + j];
+    float x;
+    if constexpr (FROM_P)
+      x = prow[rg * H * D + h * D + j];
+    else
+      x = (rg == 0 ? in.qp : (rg == 1 ? in.kp : in.vp))[voff + j];
     float n = x * x;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) n += __shfl_xor(n, off);
     float inv = 1.f / fmaxf(sqrtf(n), 1e-12f);
-    if (rg == 1 && gl) inv *= 1.f / (1.f + __expf(-gl[bh]));
+    if (rg == 1 && has_g) inv *= 1.f / (1.f + __expf(-gl_v));
     (rg == 0 ? qs : (rg == 1 ? ks : vs))[j] = x * inv;
   }
   const float p0 = p0d ? *p0d : p0h;
-  const float a = __expf(la[bh]);
+  const float a = __expf(la_v);
   const float* Sbh = S + (size_t)bh * D * D;
   float x[16];
 #pragma unroll
@@ -58,14 +107,14 @@ __global__ __launch_bounds__(256) void aspin_decode(const float* __restrict__ S,
   }
   __syncthreads();
   float wv = vs[j];
-  if (beta) {
+  if (has_b) {
     float r_ = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) r_ += ks[16 * rg + r] * x[r];
     red[rg][j] = r_;
     __syncthreads();
     const float rd = red[0][j] + red[1][j] + red[2][j] + red[3][j];
-    wv = beta[bh] * (wv - rd);
+    wv = be_v * (wv - rd);
     __syncthreads();
   }
   float y = 0.f;
@@ -79,7 +128,18 @@ __global__ __launch_bounds__(256) void aspin_decode(const float* __restrict__ S,
 #pragma unroll
   for (int r = 0; r < 16; ++r) Sob[(16 * rg + r) * D + j] = x[r];
   __syncthreads();
-  if (rg == 0) o[voff + j] = red[0][j] + red[1][j] + red[2][j] + red[3][j];
+  if (rg == 0) {
+    const float ov = red[0][j] + red[1][j] + red[2][j] + red[3][j];
+    if (on) {
+      float ss = ov * ov;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
+      const float rr = 1.f / sqrtf(ss * (1.f / D) + on_eps);
+      o[(size_t)b * H * D + h * D + j] = (ov * rr) * on[j];
+    } else {
+      o[voff + j] = ov;
+    }
+  }
 }
 
 }  // namespace
@@ -92,7 +152,42 @@ extern "C" int pragnosia_aspin_decode_step(const float* S, float* S_out, const f
   PGN_CHECK_ARG(B > 0 && H > 0 && B * H < ((int64_t)1 << 31));
   PGN_CHECK_ARG(S && S_out && qp && kp && vp && la && theta && o);
   PGN_CHECK_ARG(!(gate && beta));
-  hipLaunchKernelGGL(aspin_decode, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, S_out, qp, kp, vp,
-                     gate, la, beta, theta, p0_dev, p0, o, (int)H);
+  StepIn in{};
+  in.qp = qp;
+  in.kp = kp;
+  in.vp = vp;
+  in.gl = gate;
+  in.la = la;
+  in.beta = beta;
+  hipLaunchKernelGGL(aspin_decode<false>, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, S_out, in,
+                     theta, p0_dev, p0, nullptr, 0.f, o, (int)H);
+  PGN_RETURN_LAUNCH();
+}
+
+extern "C" int pragnosia_aspin_decode_proj(const float* S, float* S_out, const float* P, int64_t np, int64_t la_col,
+                                           int64_t gate_col, int64_t beta_col, const float* la_bias, const float* A,
+                                           const float* la_floor, const float* gate_bias, const float* beta_bias,
+                                           float beta_min, const float* theta, const float* p0_dev, float p0,
+                                           const float* on_weight, float on_eps, float* o, int64_t B, int64_t H,
+                                           int64_t Dh, void* stream) {
+  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(B > 0 && H > 0 && B * H < ((int64_t)1 << 31));
+  PGN_CHECK_ARG(S && S_out && P && la_bias && A && theta && o);
+  PGN_CHECK_ARG(!(gate_col >= 0 && beta_col >= 0));
+  PGN_CHECK_ARG(la_col >= 3 * H * D && la_col + H <= np && gate_col + H <= np && beta_col + H <= np);
+  StepIn in{};
+  in.P = P;
+  in.np = (int)np;
+  in.la_col = (int)la_col;
+  in.gate_col = (int)gate_col;
+  in.beta_col = (int)beta_col;
+  in.la_b = la_bias;
+  in.A = A;
+  in.floor = la_floor;
+  in.gate_b = gate_bias;
+  in.beta_b = beta_bias;
+  in.beta_min = beta_min;
+  hipLaunchKernelGGL(aspin_decode<true>, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, S_out, in,
+                     theta, p0_dev, p0, on_weight, on_eps, o, (int)H);
   PGN_RETURN_LAUNCH();
 }

@@ -1,0 +1,165 @@
+// The dense layers of the carrier LM's single-token decode step, batched over B sequences, fp32 (the reference
+// decodes in fp32 without autocast): y = act(scale * (W z) + bias) + resid, with z = LayerNorm(x) (weight, bias,
+// eps) or z = x, act = identity or GELU (erf form), all optional parts NULL. One call per dense layer of the step:
+// the carrier's input projections (LayerNorm + one concatenated projection), its gated output projection with the
+// residual, the MLP's first layer (LayerNorm + bias + GELU) and second (bias + residual), and the tied head
+// (LayerNorm). Replaces the torch calls of `src/model.py:552-560` and `src/assoc.py:384-512` inside the graphed
+// decode of `src/bench.py:241-317`, one kernel each instead of three to six.
+//
+// At decode batch sizes the weight read is the whole cost (each weight read once per step), so a workgroup owns a
+// few output rows and all B sequences: thread (r, l) reads 16-byte pieces 4 l + 4 LANES i of weight row r (a row
+// is read by LANES consecutive lanes, 16 * LANES contiguous bytes per instruction), twelve pieces at a time held in
+// registers (all issued before the first is used), and accumulates 8 sequences at a time; the LayerNorm'd inputs of
+// those 8 sequences sit in LDS. The first weight pieces are loaded before the LayerNorm, whose row is held in
+// registers (one read of x). Each group of 8 sequences is its own row of workgroups (the weight is then read once
+// from HBM and again from the last-level cache). LANES = 64 for narrow outputs (more workgroups) or long rows, 16
+// otherwise.
+#include <algorithm>
+
+#include "common.h"
+
+namespace {
+
+constexpr int BT = 8;            // sequences per pass
+constexpr int LNMAX = 1024;      // LayerNorm'd inputs are staged in LDS for K <= LNMAX
+
+PGN_DEVICE float gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
+
+template <int LANES>
+__global__ __launch_bounds__(256) void gemv(const float* __restrict__ x, int B, int K, const float* __restrict__ lnw,
+                                            const float* __restrict__ lnb, float eps, const float* __restrict__ W,
+                                            int N, const float* __restrict__ bias,
+                                            const float* __restrict__ scale, int act,
+                                            const float* __restrict__ resid, float* __restrict__ y) {
+  constexpr int ROWS = 256 / LANES;
+  constexpr int NW = 12;                 // 16-byte weight pieces per thread held in registers per K chunk
+  constexpr int KC = NW * 4 * LANES;     // K chunk
+  constexpr int LV = LNMAX / 128;        // 16-byte pieces of one LayerNorm row per lane (32 lanes a row)
+  __shared__ __align__(16) float zs[BT * LNMAX];  // the LayerNorm'd inputs of one pass
+  const int tid = threadIdx.x, r = tid / LANES, l = tid % LANES;
+  const int n = blockIdx.x * ROWS + r;
+  const bool ln = lnw != nullptr;
+  const float* wr = W + (size_t)min(n, N - 1) * K;
+  f32x4 w4[NW];
+  auto load_w = [&](int kc) {
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const int k = kc + 4 * l + 4 * LANES * u;
+      w4[u] = k < K ? *reinterpret_cast<const f32x4*>(wr + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  // the first chunk's weights are in flight while the LayerNorm below runs
+  load_w(0);
+  const float sc = scale ? *scale : 1.f;
+  for (int b0 = blockIdx.y * BT; b0 < B; b0 += BT * gridDim.y) {
+    const int nb = min(BT, B - b0);
+    if (ln) {
+      // row rr of the pass by 32 lanes, held in registers: mean, then the variance about it, then z into LDS
+      __syncthreads();
+      const int rr = tid / 32, ll = tid % 32;
+      if (rr < nb) {
+        const float* xr = x + (size_t)(b0 + rr) * K;
+        f32x4 xv[LV];
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < LV; ++i) {
+          const int k = 4 * ll + 128 * i;
+          xv[i] = k < K ? *reinterpret_cast<const f32x4*>(xr + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+          s += (xv[i][0] + xv[i][1]) + (xv[i][2] + xv[i][3]);
+        }
+        for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 32);
+        const float mean = s / K;
+        float s2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < LV; ++i) {
+          if (4 * ll + 128 * i < K) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float d = xv[i][e] - mean;
+              s2 += d * d;
+            }
+          }
+        }
+        for (int o = 16; o > 0; o >>= 1) s2 += __shfl_xor(s2, o, 32);
+        const float rs = 1.f / sqrtf(s2 / K + eps);
+#pragma unroll
+        for (int i = 0; i < LV; ++i) {
+          const int k = 4 * ll + 128 * i;
+          if (k < K) {
+            const f32x4 g = *reinterpret_cast<const f32x4*>(lnw + k);
+            const f32x4 c = lnb ? *reinterpret_cast<const f32x4*>(lnb + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+            f32x4 z;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) z[e] = (xv[i][e] - mean) * rs * g[e] + c[e];
+            *reinterpret_cast<f32x4*>(zs + rr * K + k) = z;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    float acc[BT];
+#pragma unroll
+    for (int b = 0; b < BT; ++b) acc[b] = 0.f;
+    for (int kc = 0; kc < K; kc += KC) {
+      if (kc > 0 || b0 != (int)blockIdx.y * BT) load_w(kc);
+#pragma unroll
+      for (int b = 0; b < BT; ++b) {
+        if (b < nb) {
+          const float* zr = ln ? zs + b * K : x + (size_t)(b0 + b) * K;
+          float a = 0.f;
+#pragma unroll
+          for (int u = 0; u < NW; ++u) {
+            const int k = kc + 4 * l + 4 * LANES * u;
+            if (k < K) {
+              const f32x4 z4 = *reinterpret_cast<const f32x4*>(zr + k);
+              a += w4[u][0] * z4[0] + w4[u][1] * z4[1] + w4[u][2] * z4[2] + w4[u][3] * z4[3];
+            }
+          }
+          acc[b] += a;
+        }
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+      float v = acc[b];
+      for (int o = LANES / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LANES);
+      acc[b] = v;
+    }
+    if (l == 0 && n < N) {
+#pragma unroll
+      for (int b = 0; b < BT; ++b) {
+        if (b < nb) {
+          float v = sc * acc[b] + (bias ? bias[n] : 0.f);
+          if (act == 1) v = gelu_erf(v);
+          const size_t off = (size_t)(b0 + b) * N + n;
+          if (resid) v += resid[off];
+          y[off] = v;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int pragnosia_decode_gemv(const float* x, int64_t B, int64_t K, const float* ln_weight,
+                                     const float* ln_bias, float ln_eps, const float* W, int64_t N,
+                                     const float* bias, const float* scale, int act, const float* resid, float* y,
+                                     void* stream) {
+  PGN_CHECK_ARG(x && W && y && B > 0 && K > 0 && N > 0 && K % 4 == 0);
+  PGN_CHECK_ARG(B * N < ((int64_t)1 << 31) && B * K < ((int64_t)1 << 31));
+  PGN_CHECK_ARG(act == 0 || act == 1);
+  PGN_CHECK_ARG(ln_weight == nullptr || K <= LNMAX);
+  PGN_CHECK_ARG(y != x && (resid == nullptr || resid != y));
+  PGN_CHECK_ARG(((uintptr_t)x | (uintptr_t)W | (uintptr_t)ln_weight | (uintptr_t)ln_bias) % 16 == 0);
+  hipStream_t st = (hipStream_t)stream;
+  const unsigned tiles = (unsigned)std::min<int64_t>((B + BT - 1) / BT, 65535);  // one workgroup row per 8 sequences
+  if (N < 2048 || K > 768) {  // 64 lanes a row: more workgroups for narrow outputs, fewer chunks for long rows
+    hipLaunchKernelGGL(gemv<64>, dim3((unsigned)((N + 3) / 4), tiles), dim3(256), 0, st, x, (int)B, (int)K, ln_weight,
+                       ln_bias, ln_eps, W, (int)N, bias, scale, act, resid, y);
+  } else {
+    hipLaunchKernelGGL(gemv<16>, dim3((unsigned)((N + 15) / 16), tiles), dim3(256), 0, st, x, (int)B, (int)K, ln_weight,
+                       ln_bias, ln_eps, W, (int)N, bias, scale, act, resid, y);
+  }
+  PGN_RETURN_LAUNCH();
+}

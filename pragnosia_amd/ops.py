@@ -705,3 +705,57 @@ def aspin_decode_step(S: Tensor, qp: Tensor, kp: Tensor, vp: Tensor, gate: Optio
 def _(S, qp, kp, vp, gate, la, beta, theta, p0_dev, p0):
     B, H, D, _ = S.shape
     return torch.empty_like(S, dtype=torch.float32), S.new_empty(B, H, D, dtype=torch.float32)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the fused decode step's kernels: replace the torch calls of one LM layer's T = 1 step inside the graphed decode
+@torch.library.custom_op("pragnosia::decode_gemv", mutates_args=())
+def decode_gemv(x: Tensor, W: Tensor, ln_weight: Optional[Tensor], ln_bias: Optional[Tensor], ln_eps: float,
+                bias: Optional[Tensor], scale: Optional[Tensor], act: int, resid: Optional[Tensor]) -> Tensor:
+    """y (B, N) = act(scale * (W LayerNorm(x)) + bias) + resid for x (B, K), W (N, K), all fp32; LayerNorm only when
+    ln_weight is given; act 0 identity, 1 GELU (erf form); scale a device scalar. Not differentiable."""
+    _require_gpu(x, W, ln_weight, ln_bias, bias, scale, resid)
+    x, W = _f32(x), _f32(W)
+    ln_weight, ln_bias, bias, scale, resid = _f32(ln_weight), _f32(ln_bias), _f32(bias), _f32(scale), _f32(resid)
+    B, K = x.shape
+    N = W.shape[0]
+    y = torch.empty(B, N, device=x.device, dtype=torch.float32)
+    check(lib().pragnosia_decode_gemv(_ptr(x), B, K, _ptr(ln_weight), _ptr(ln_bias), float(ln_eps), _ptr(W), N,
+                                      _ptr(bias), _ptr(scale), int(act), _ptr(resid), _ptr(y), _stream(x)),
+          "pragnosia_decode_gemv")
+    return y
+
+
+@decode_gemv.register_fake
+def _(x, W, ln_weight, ln_bias, ln_eps, bias, scale, act, resid):
+    return x.new_empty(x.shape[0], W.shape[0], dtype=torch.float32)
+
+
+@torch.library.custom_op("pragnosia::aspin_decode_proj_", mutates_args=("S",))
+def aspin_decode_proj_(S: Tensor, P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Optional[Tensor],
+                       gate_bias: Optional[Tensor], beta_bias: Optional[Tensor], beta_min: float, gated: bool,
+                       theta: Tensor, p0_dev: Optional[Tensor], p0: float, on_weight: Tensor,
+                       on_eps: float) -> Tensor:
+    """The carrier's recurrent step from one projection GEMV's output P (B, 3 H 64 + H [+ H]) (q, k, v, decay
+    logits, then the write-gate (gated) or write-strength logits), updating the carried state S (B, H, 64, 64) fp32 in
+    place. Returns the output RMS-normalised per head with on_weight and token-major, (B, H * 64) fp32."""
+    _require_gpu(S, P, la_bias, A, theta, on_weight)
+    if not (S.is_contiguous() and S.dtype == torch.float32):
+        raise PragnosiaError("aspin_decode_proj_: the state must be a contiguous fp32 tensor (it is updated in place)")
+    P, la_bias, A, la_floor, theta = _f32(P), _f32(la_bias), _f32(A), _f32(la_floor), _f32(theta)
+    gate_bias, beta_bias, p0_dev, on_weight = _f32(gate_bias), _f32(beta_bias), _f32(p0_dev), _f32(on_weight)
+    B, np_ = P.shape
+    D = 64
+    has_beta = not gated and np_ > 3 * H * D + H
+    acol, gcol, bcol = _proj_cols(H, gated, has_beta)
+    o = torch.empty(B, H * D, device=P.device, dtype=torch.float32)
+    check(lib().pragnosia_aspin_decode_proj(_ptr(S), _ptr(S), _ptr(P), np_, acol, gcol, bcol, _ptr(la_bias), _ptr(A),
+                                            _ptr(la_floor), _ptr(gate_bias), _ptr(beta_bias), float(beta_min),
+                                            _ptr(theta), _ptr(p0_dev), float(p0), _ptr(on_weight), float(on_eps),
+                                            _ptr(o), B, H, D, _stream(P)), "pragnosia_aspin_decode_proj")
+    return o
+
+
+@aspin_decode_proj_.register_fake
+def _(S, P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, p0_dev, p0, on_weight, on_eps):
+    return P.new_empty(P.shape[0], H * 64, dtype=torch.float32)

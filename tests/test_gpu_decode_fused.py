@@ -1,0 +1,111 @@
+"""GPU parity of the fused decode step: the batched dense-layer kernel (pragnosia_decode_gemv) against torch's
+LayerNorm + Linear (+ GELU, + residual), the step kernel reading one projection GEMV's output
+(pragnosia_aspin_decode_proj) against the module's own T = 1 path, and whole greedy generations of the fused graphed
+decoder against the unfused one and the eager loop.
+
+Everything is fp32, as the reference decodes. Tolerances: max relative error max|x - ref| / max|ref| <= 1e-5 for a
+dense layer (fp32 sums in another order) and 1e-4 for a whole carrier layer step; generated tokens must be equal."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+
+def rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).abs().max() / (b.abs().max() + 1e-30)).item()
+
+
+@pytest.mark.parametrize("B", [1, 5, 13, 64])
+@pytest.mark.parametrize("K,N,ln,act,res", [(768, 2328, True, 0, False), (768, 768, False, 0, True),
+                                            (768, 3072, True, 1, False), (3072, 768, False, 0, True),
+                                            (128, 8192, True, 0, False), (1000, 300, True, 1, True),
+                                            (4100, 200, False, 0, False)])
+def test_decode_gemv_matches_torch(B, K, N, ln, act, res):
+    import pragnosia_amd.ops  # noqa: F401
+    g = torch.Generator(device="cuda").manual_seed(B + K + N)
+    x = torch.randn(B, K, device="cuda", generator=g)
+    W = torch.randn(N, K, device="cuda", generator=g) * 0.05
+    lw, lb = torch.randn(K, device="cuda", generator=g), torch.randn(K, device="cuda", generator=g)
+    bias = torch.randn(N, device="cuda", generator=g) if act else None
+    scale = torch.rand(1, device="cuda", generator=g) if res else None
+    resid = torch.randn(B, N, device="cuda", generator=g) if res else None
+    y = torch.ops.pragnosia.decode_gemv(x, W, lw if ln else None, lb if ln else None, 1e-5, bias, scale, act, resid)
+    xd, Wd = x.double(), W.double()
+    z = F.layer_norm(xd, (K,), lw.double(), lb.double(), 1e-5) if ln else xd
+    r = z @ Wd.t()
+    if scale is not None:
+        r = r * scale.double()
+    if bias is not None:
+        r = r + bias.double()
+    if act == 1:
+        r = F.gelu(r)
+    if resid is not None:
+        r = r + resid.double()
+    assert rel(y, r) < 1e-5
+
+
+@pytest.mark.parametrize("delta,write_all,hl_floor", [(False, False, False), (False, True, True),
+                                                      (True, False, False), (True, True, True)])
+def test_decode_proj_matches_module_step(delta, write_all, hl_floor):
+    """One carrier step through the projection GEMV + the fused step kernel against the module's T = 1 path (its
+    projections, aspin_decode_step, nn.RMSNorm), from a rebased carried state, twice in a row (in-place state)."""
+    from pragnosia_amd.assoc import AssocCarrier
+    op = torch.ops.pragnosia
+    torch.manual_seed(3)
+    m = AssocCarrier(256, delta=delta, write_all=write_all, hl_floor=hl_floor).cuda().eval()
+    with torch.no_grad():
+        for p in m.parameters():
+            p.add_(torch.randn_like(p) * 0.05)
+        B = 3
+        S = torch.randn(B, 4, 64, 64, device="cuda") * 0.1
+        S_f = S.clone()
+        p0 = torch.tensor([7.0], device="cuda")
+        gated = not (delta or write_all)
+        extra = [m.wi.weight] if gated else ([m.wb.weight] if delta else [])
+        W = torch.cat([m.q.weight, m.k.weight, m.v.weight, m.wa.weight] + extra)
+        st = (S, 7)
+        for step in range(2):
+            x = torch.randn(B, 1, 256, device="cuda")
+            y_mod, st = m(x, st)
+            P = op.decode_gemv(x.reshape(B, 256), W, m.ln.weight, m.ln.bias, m.ln.eps, None, None, 0, None)
+            o = op.aspin_decode_proj_(S_f, P, 4, m.wa.bias, m.A, m.la_floor if hl_floor else None,
+                                      m.wi.bias if gated else None, m.wb.bias if delta else None,
+                                      0.75 if (delta and write_all) else 0.0, gated, m.theta, p0, 0.0, m.on.weight,
+                                      torch.finfo(torch.float32).eps)
+            y_f = op.decode_gemv(o, m.o.weight, None, None, 0.0, None, torch.sigmoid(m.gate).reshape(1), 0,
+                                 x.reshape(B, 256))
+            p0.fill_(1.0)
+            assert rel(y_f - x.reshape(B, 256), y_mod.reshape(B, 256) - x.reshape(B, 256)) < 1e-4, step
+            assert rel(S_f, st[0]) < 1e-4, step
+
+
+@pytest.mark.parametrize("mixer", ["aspin", "dspin"])
+@pytest.mark.parametrize("B", [1, 3])
+def test_fused_graphed_decode_equals_unfused_and_eager(mixer, B):
+    from pragnosia_amd.decode import GreedyDecoder, greedy_eager
+    from pragnosia_amd.model import LM
+    torch.manual_seed(50 + B)
+    m = LM(vocab=300, d=128, layers=2, mlp_mult=2, ctx=64, mixer=mixer).cuda().eval()
+    with torch.no_grad():
+        for mx in m.mix:
+            for p in mx.parameters():
+                p.add_(torch.randn_like(p) * 0.05)
+        m.e.weight.mul_(20)
+    g = torch.Generator().manual_seed(51)
+    prompt = torch.randint(0, 300, (B, 100), generator=g).cuda()
+    n = 25
+    fused = GreedyDecoder(m, B, steps_per_graph=4)
+    assert fused.fused
+    plain = GreedyDecoder(m, B, steps_per_graph=4, fused=False)
+    t_f = fused.generate(prompt, n)
+    t_p = plain.generate(prompt, n)
+    t_e, _ = greedy_eager(m, prompt, n)
+    assert torch.equal(t_f.cpu(), t_p.cpu()) and torch.equal(t_f.cpu(), t_e.cpu())
+    # a second generation through the same captured graph, after a parameter change the copied weights must follow
+    with torch.no_grad():
+        m.mix[0].q.weight.mul_(1.5)
+    t_f2 = fused.generate(prompt[:, :70], n)
+    t_e2, _ = greedy_eager(m, prompt[:, :70], n)
+    assert torch.equal(t_f2.cpu(), t_e2.cpu())
