@@ -42,6 +42,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile-kernels", action="store_true",
                     help="run each hot kernel a fixed number of times (for rocprofv3 counter passes) and exit")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the configs[4] decode measurement (batch 1 and 64), print its JSON and exit")
     return ap.parse_args()
 
 
@@ -629,6 +631,9 @@ def main():
     args = parse()
     if args.profile_kernels:
         profile_kernels()
+        return
+    if args.decode_only:
+        print(json.dumps(decode_bench()), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the carrier path has no "
