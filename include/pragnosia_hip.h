@@ -123,7 +123,8 @@ int pragnosia_aspin_out_bwd(const void* gy, int gy_bf16, const void* o, const fl
  * Associative carrier, DELTA write rule, chunked scan (chunk = 64, head dim D = 64), per (batch, head):
  *     S_t = a_t S_{t-1} + beta_t k_t (v_t - (a_t S_{t-1})^T k_t)^T,   o_t = S_t^T q_t,   a_t = exp(la_t).
  * Layouts as pragnosia_aspin_chunk_fwd; beta: (B, H, T) fp32 in (0, 1). Writes o (bf16), S_final (fp32), sent
- * (bf16 entering states, required by the backward; may be NULL when no backward follows), and the two saved
+ * (bf16 entering states, each chunk's transposed: sent[b, h, c, j, d] = S[d, j]; required by the backward; may be
+ * NULL when no backward follows), and the two saved
  * intermediates of the backward: W, the residuals actually written, (B, H, T, D) bf16, and X, the per-chunk
  * inverse (I + diag(beta) strictly_lower((K K^T) o dec))^-1, (B, H, ceil(T/64), 64, 64) bf16, computed in fp32.
  * Replaces `delta_scan_kernel` and the ops under it (`delta_inv`, `delta_loop_fwd`, `assoc_out`) of

@@ -82,6 +82,7 @@ def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = Fa
         o, S, sent = _op.aspin_chunk(q, k, v, logalpha.float(), S0, want)
     else:
         o, S, sent, _, _ = _op.aspin_delta(q, k, v, logalpha.float(), beta.float(), S0, want)
+        sent = sent.transpose(-1, -2) if need_sent else sent  # the op stores each state transposed
     o = o.to(q.dtype) if q.dtype != torch.bfloat16 else o
     if need_sent:
         return o, S, sent
@@ -256,6 +257,7 @@ class AssocCarrier(nn.Module):
                         _needs_grad(x, S0, *self.parameters()))
             if self.delta:
                 o, S, sent, _, _ = _op.aspin_delta(q, k, v, la, bt, S0, want)
+                sent = sent.transpose(-1, -2) if want else sent  # the op stores each state transposed
             else:
                 o, S, sent = _op.aspin_chunk(q, k, v, la, S0, want)
             sent = sent if want else None

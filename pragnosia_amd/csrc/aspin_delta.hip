@@ -18,8 +18,9 @@
 //                      value column given X, so wave w owns value columns 16w..16w+15 for all 64 tokens and the
 //                      whole state chain (U -> rhs -> W -> S') stays in that wave's MFMA accumulators: each
 //                      product's accumulator is the next product's operand, with no LDS round trip and no barrier
-//                      on the chain. Writes o, the residuals W and the entering states (both bf16) for the
-//                      backward, and the final fp32 state.
+//                      on the chain. Writes o, the residuals W and the entering states (both bf16; each entering
+//                      state transposed, (j, d), so a lane's four consecutive key rows are one 8-byte store) for
+//                      the backward, and the final fp32 state.
 //   aspin_delta_bwd_chain   one workgroup of 4 waves per (batch, head), chunks in reverse, wave w owning value
 //                      columns 16w.. again. Carries dS (gradient on the state leaving the chunk) in registers:
 //                          dW = A^T dO + w o (K dS),  drhs = X^T dW,  dU = -beta eL o drhs,
@@ -260,13 +261,11 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
       const float* ws = vs + 2 * C;
       const float* bs = vs + 3 * C;
       const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
-      // the entering state, bf16 (d, j)
+      // the entering state, bf16, transposed: row j holds key rows d contiguously
       if (sent) {
-        __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
+        __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK + (size_t)j * DK + 4 * g;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sc[(16 * db + 4 * g + r) * DK + j] = (__bf16)S[db][r];
+        for (int db = 0; db < 4; ++db) *reinterpret_cast<bf16x4*>(sc + 16 * db) = to_bf16x4(S[db]);
       }
       // U = K S (rows t, this wave's columns); rhs = beta (V - eL U)
       const bf16x8 s01 = pack(S[0], S[1]), s23 = pack(S[2], S[3]);
@@ -291,35 +290,41 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
       for (int tb = 0; tb < 4; ++tb) {
         Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 0, g), r01, zero4());
         if (tb >= 2) Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 1, g), r23, Wt[tb]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (__bf16)Wt[tb][r]), w_out,
-                                                ((16 * tb + 4 * g + r) * DK + j) * (int)sizeof(__bf16), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, quad_rows(Wt[tb], i)), w_out,
+                                              ((16 * tb + 4 * g + (i & 3)) * DK + 16 * w + 4 * (i >> 2)) *
+                                                  (int)sizeof(__bf16), 0, 0);
       }
       __syncthreads();  // A complete
 
-      // O^T tiles (value rows 16w + 4g + r, token lane 16 tb + i) = W^T A^T + S^T (Q o eL)^T
+      // O^T tiles (value rows 16w + 4g + r, token lane 16 tb + i) = W^T A^T + eL_t (S^T Q^T): the decay of the
+      // state read is one factor per output column, applied to the accumulator rather than to the Q operand
       const __amdgpu_buffer_rsrc_t o_out =
           __builtin_amdgcn_make_buffer_rsrc(o + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
       const bf16x8 w01 = pack(Wt[0], Wt[1]), w23 = pack(Wt[2], Wt[3]);
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
         const int tl = 16 * tb + i;
-        const float eLt = eLs[tl];
         f32x4 acc = pgn_mfma(w01, frag(As, tl, 0, g), zero4());
         if (tb >= 2) acc = pgn_mfma(w23, frag(As, tl, 1, g), acc);
-        acc = pgn_mfma(s01, frag_scaled(Qs, tl, 0, g, eLt), acc);
-        acc = pgn_mfma(s23, frag_scaled(Qs, tl, 1, g, eLt), acc);
+        f32x4 qs = pgn_mfma(s01, frag(Qs, tl, 0, g), zero4());
+        qs = pgn_mfma(s23, frag(Qs, tl, 1, g), qs);
+        acc += eLs[tl] * qs;
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
                                               (tl * DK + 16 * w + 4 * g) * (int)sizeof(__bf16), 0, 0);
       }
-      // S <- a S + (K o w)^T W
+      // S <- a S + K^T (w o W): the per-token weight w_t scales W's fp32 rows before they are rounded, so K enters
+      // the product as it is staged
       const float a_c = __expf(Ls[C - 1]);
+      bf16x8 ww[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+        ww[m] = pack(Wt[2 * m] * *reinterpret_cast<const f32x4*>(ws + 32 * m + 4 * g),
+                     Wt[2 * m + 1] * *reinterpret_cast<const f32x4*>(ws + 32 * m + 16 + 4 * g));
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         S[db] = S[db] * a_c;
-        S[db] = pgn_mfma(frag_tr_scaled_k(Ks, 16 * db, 0, g, i, ws), w01, S[db]);
-        S[db] = pgn_mfma(frag_tr_scaled_k(Ks, 16 * db, 1, g, i, ws), w23, S[db]);
+        S[db] = pgn_mfma(frag_tr(Ks, 16 * db, 0, g, i), ww[0], S[db]);
+        S[db] = pgn_mfma(frag_tr(Ks, 16 * db, 1, g, i), ww[1], S[db]);
       }
       __syncthreads();  // end of the chunk
     }
@@ -467,7 +472,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
       }
       // products that do not need A^T: y = K dS, U = K S_c, Yc = (Q o eL)^T dO, on this wave's columns
       const bf16x8 d01 = pack(dS[0], dS[1]), d23 = pack(dS[2], dS[3]);
-      const bf16x8 sc0 = frag_tr(Ss, 16 * w, 0, g, i), sc1 = frag_tr(Ss, 16 * w, 1, g, i);  // S_c[d][j]
+      const bf16x8 sc0 = frag(Ss, 16 * w + i, 0, g), sc1 = frag(Ss, 16 * w + i, 1, g);  // S_c[d][j], staged (j, d)
       const bf16x8 oc0 = frag_tr(Os, 16 * w, 0, g, i), oc1 = frag_tr(Os, 16 * w, 1, g, i);  // dO[t][j]
       f32x4 y[4], U[4], Yc[4];
 #pragma unroll
@@ -655,7 +660,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
   __bf16* Ks = Qs + TILE;
   __bf16* Ws = Ks + TILE;
   __bf16* Os = Ws + TILE;   // dO
-  __bf16* Ss = Os + TILE;   // S_c (d, j)
+  __bf16* Ss = Os + TILE;   // S_c transposed, (j, d)
   __bf16* dSs = Ss + TILE;  // dS (d, j)
   __bf16* Rs = dSs + TILE;  // drhs (t, j)
   float* Ls = reinterpret_cast<float*>(Rs + TILE);
@@ -745,8 +750,8 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
         f32x4 acc = zero4(), Z = zero4();
         acc = pgn_mfma(frag_tr(Ks, 16 * dt, 0, g, i), b0, acc);
         if (WL >= 2) acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), b1, acc);
-        Z = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), of0, Z);
-        Z = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), of1, Z);
+        Z = pgn_mfma(frag_tr(Ss, 16 * dt, 0, g, i), of0, Z);
+        Z = pgn_mfma(frag_tr(Ss, 16 * dt, 1, g, i), of1, Z);
         const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
 #pragma unroll
         for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
@@ -829,8 +834,8 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
         acc = pgn_mfma(frag_tr(Qs, 16 * dt, 1, g, i), p1, acc);
         acc = pgn_mfma(frag_tr(Ks, 16 * dt, 0, g, i), g0, acc);
         acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), g1, acc);
-        acc = pgn_mfma(frag(Ss, 16 * dt + i, 0, g), du0, acc);
-        acc = pgn_mfma(frag(Ss, 16 * dt + i, 1, g), du1, acc);
+        acc = pgn_mfma(frag_tr(Ss, 16 * dt, 0, g, i), du0, acc);
+        acc = pgn_mfma(frag_tr(Ss, 16 * dt, 1, g, i), du1, acc);
         Y = pgn_mfma(frag(dSs, 16 * dt + i, 0, g), wf0, Y);
         Y = pgn_mfma(frag(dSs, 16 * dt + i, 1, g), wf1, Y);
         const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
@@ -849,9 +854,11 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
       float sd = 0.f;
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
-        // S_c and dS at rows 16 WL + 4g + r, column 16 jt + i: transpose reads at rows 16 WL.., columns 16 jt..
+        // S_c and dS at rows 16 WL + 4g + r, column 16 jt + i: dS by a transpose read at rows 16 WL.., columns
+        // 16 jt..; S_c (staged transposed) by a plain read of row 16 jt + i
         const int off = (16 * WL + 4 * g + (i >> 2)) * kPitch + 16 * jt + 4 * (i & 3);
-        const f32x4 sv = to_f32x4(ds_read_tr(Ss + off)), dv_ = to_f32x4(ds_read_tr(dSs + off));
+        const f32x4 sv = to_f32x4(*reinterpret_cast<const bf16x4*>(Ss + (16 * jt + i) * kPitch + 16 * WL + 4 * g));
+        const f32x4 dv_ = to_f32x4(ds_read_tr(dSs + off));
 #pragma unroll
         for (int r = 0; r < 4; ++r) sd += sv[r] * dv_[r];
       }

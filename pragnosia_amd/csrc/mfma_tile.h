@@ -84,6 +84,30 @@ PGN_DEVICE bf16x4 to_bf16x4(f32x4 x) {
   return r;
 }
 
+// A 16 x 16 accumulator tile (lane (i, g) holds rows 4g..4g+3 of column i) rounded to bf16 and transposed within
+// each quad of lanes (i = 4m..4m+3) by two DPP exchanges (the off-diagonal 2 x 2 blocks between lanes p and p^2,
+// then 16-bit halves between lanes p and p^1), so that lane (i, g) ends holding row 4g + (i & 3), columns
+// 4 (i >> 2) .. +3 of the tile: one 8-byte row-major store per lane instead of four 2-byte ones. All 64 lanes must
+// be active.
+PGN_DEVICE bf16x4 quad_rows(f32x4 x, int i) {
+  const int p = i & 3;
+  const i32x2 v = __builtin_bit_cast(i32x2, to_bf16x4(x));
+  unsigned d0 = (unsigned)v[0], d1 = (unsigned)v[1];  // rows (0, 1) and (2, 3) of this lane's column
+  const unsigned send = (p & 2) ? d0 : d1;
+  const unsigned recv = (unsigned)__builtin_amdgcn_update_dpp(0, (int)send, 0x4E, 0xf, 0xf, false);  // [2,3,0,1]
+  if (p & 2) d0 = recv; else d1 = recv;
+  const unsigned o0 = (unsigned)__builtin_amdgcn_update_dpp(0, (int)d0, 0xB1, 0xf, 0xf, false);  // [1,0,3,2]
+  const unsigned o1 = (unsigned)__builtin_amdgcn_update_dpp(0, (int)d1, 0xB1, 0xf, 0xf, false);
+  if (p & 1) {
+    d0 = (o0 >> 16) | (d0 & 0xffff0000u);
+    d1 = (o1 >> 16) | (d1 & 0xffff0000u);
+  } else {
+    d0 = (d0 & 0xffffu) | (o0 << 16);
+    d1 = (d1 & 0xffffu) | (o1 << 16);
+  }
+  return __builtin_bit_cast(bf16x4, i32x2{(int)d0, (int)d1});
+}
+
 PGN_DEVICE f32x4 to_f32x4(bf16x4 x) { return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]}; }
 
 // Operand from an accumulator tile pair (contracted index = the tiles' row index).

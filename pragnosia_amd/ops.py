@@ -349,7 +349,8 @@ def aspin_delta(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor, S0: O
                 want_sent: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Delta-rule chunked scan. q, k, v (B, H, T, 64) (cast to bf16), la and beta (B, H, T) fp32, S0 (B, H, 64, 64)
     fp32 or None. Returns (o bf16, S_final fp32, sent bf16 (B, H, NC, 64, 64) or empty, W bf16 (B, H, T, 64),
-    X bf16 (B, H, NC, 64, 64)); W and X are the intermediates the backward reads (not differentiable)."""
+    X bf16 (B, H, NC, 64, 64)); W and X are the intermediates the backward reads (not differentiable). Each entering
+    state in sent is stored transposed (sent[..., c, j, d] = S_c[d, j]); `.transpose(-1, -2)` gives the states."""
     _require_gpu(q, k, v, la, beta, S0)
     q, k, v, la, beta, S0 = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(beta), _f32(S0)
     B, H, T, D = q.shape

@@ -84,7 +84,7 @@ def test_delta_intermediates(delta):
     Xr = O.delta_inverse(kc, bc, dec)
     assert rel(X.float(), Xr) < 1e-2
     assert rel(W.float(), Wr) < TOL_OUT
-    assert rel(sent.float(), Sent) < TOL_OUT
+    assert rel(sent.transpose(-1, -2).float(), Sent) < TOL_OUT  # stored transposed per chunk
     N = bc.unsqueeze(-1) * torch.tril((kc @ kc.transpose(-1, -2)) * dec, -1)
     eye = torch.eye(64, dtype=torch.float64)
     assert ((X.double().cpu() @ (eye + N)) - eye).abs().max() < 2e-2
