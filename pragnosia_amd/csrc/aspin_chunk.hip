@@ -156,10 +156,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
         const f32x4 w10 = *reinterpret_cast<const f32x4*>(ws + 32 + 4 * g);
         const f32x4 w11 = *reinterpret_cast<const f32x4*>(ws + 48 + 4 * g);
         __builtin_amdgcn_sched_barrier(0);
-        const bf16x8 qe0 = scale_frag(qf0, eLt);
-        const bf16x8 qe1 = scale_frag(qf1, eLt);
-        // O^T tiles (value block jt, t block TB) = V^T A^T + S^T (Q o eL)^T; lane holds token tq, 4 value columns.
-        // Rows past T fall outside the store's range and are dropped.
+        // O^T tiles (value block jt, t block TB) = V^T A^T + eL_t (S^T Q^T); lane holds token tq, 4 value columns,
+        // so the state read's decay is one factor on the accumulator. Rows past T fall outside the store's range
+        // and are dropped.
         const __amdgpu_buffer_rsrc_t o_out = __builtin_amdgcn_make_buffer_rsrc(
             o + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
 #pragma unroll
@@ -167,8 +166,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
           f32x4 acc = zero4();
           acc = pgn_mfma(vf[jt][0], af0, acc);
           if (TB >= 2) acc = pgn_mfma(vf[jt][1], af1, acc);
-          acc = pgn_mfma(sf[jt][0], qe0, acc);
-          acc = pgn_mfma(sf[jt][1], qe1, acc);
+          f32x4 qs = pgn_mfma(sf[jt][0], qf0, zero4());
+          qs = pgn_mfma(sf[jt][1], qf1, qs);
+          acc += eLt * qs;
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
                                                 (tq * DK + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
         }

@@ -24,9 +24,11 @@
 //   aspin_delta_bwd_chain   one workgroup of 4 waves per (batch, head), chunks in reverse, wave w owning value
 //                      columns 16w.. again. Carries dS (gradient on the state leaving the chunk) in registers:
 //                          dW = A^T dO + w o (K dS),  drhs = X^T dW,  dU = -beta eL o drhs,
-//                          dS_prev = a dS + (Q o eL)^T dO + K^T dU,   dV = beta o drhs,
-//                      and writes drhs, the per-chunk dS (bf16) and the row sums over value columns that the decay
+//                          dS_prev = a dS + (Q o eL)^T dO + K^T dU,
+//                      and writes drhs, the per-chunk dS (bf16, transposed) and the row sums over value columns that the decay
 //                      and beta gradients need: sum_j drhs (V - eL U) and -beta sum_j drhs U.
+//                      dV = beta o drhs is written by the local kernel from the stored drhs (coalesced, off the
+//                      chain).
 //   aspin_delta_bwd_local   one workgroup of 8 waves per (batch-head, chunk), fully parallel: everything that is
 //                      local to a chunk once drhs and dS are known. With dN = -drhs W^T (the gradient through
 //                      W = X rhs, since dX = dW rhs^T and dN = -X^T dX X^T), dKK = diag(beta) dN o dec (strictly
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const float* __restrict__ be, const __bf16* __restrict__ X,
     const __bf16* __restrict__ sent, const __bf16* __restrict__ dO, const float* __restrict__ dSfin,
-    __bf16* __restrict__ dv, __bf16* __restrict__ drhs, __bf16* __restrict__ dSc, float* __restrict__ rsum,
+    __bf16* __restrict__ drhs, __bf16* __restrict__ dSc, float* __restrict__ rsum,
     float* __restrict__ dS0, int T, int NC) {
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* stg = reinterpret_cast<__bf16*>(smem);          // two sets of staged tiles, chunk c uses set c & 1
@@ -462,13 +464,12 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
       const float* bs = vs + 3 * C;
       float* redV = vs + 4 * C;   // [4][C]
       float* redU = vs + 8 * C;   // [4][C]
-      // the gradient on the state leaving this chunk, for the chunk-local kernel
+      // the gradient on the state leaving this chunk, for the chunk-local kernel, transposed ((j, d): a lane's four
+      // consecutive key rows are one 8-byte store)
       {
-        __bf16* dst = dSc + ((size_t)bh * NC + cc) * DK * DK;
+        __bf16* dst = dSc + ((size_t)bh * NC + cc) * DK * DK + (size_t)j * DK + 4 * g;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * g + r) * DK + j] = (__bf16)dS[db][r];
+        for (int db = 0; db < 4; ++db) *reinterpret_cast<bf16x4*>(dst + 16 * db) = to_bf16x4(dS[db]);
       }
       // products that do not need A^T: y = K dS, U = K S_c, Yc = (Q o eL)^T dO, on this wave's columns
       const bf16x8 d01 = pack(dS[0], dS[1]), d23 = pack(dS[2], dS[3]);
@@ -483,10 +484,15 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
         U[tb] = pgn_mfma(k0, sc0, zero4());
         U[tb] = pgn_mfma(k1, sc1, U[tb]);
       }
+      // the per-token factor eL_t on the dO operand, shared by the four key blocks, rather than on each Q^T block
+      const bf16x8 oe0 = scale_frag_k(oc0, *reinterpret_cast<const f32x4*>(eLs + 4 * g),
+                                      *reinterpret_cast<const f32x4*>(eLs + 16 + 4 * g));
+      const bf16x8 oe1 = scale_frag_k(oc1, *reinterpret_cast<const f32x4*>(eLs + 32 + 4 * g),
+                                      *reinterpret_cast<const f32x4*>(eLs + 48 + 4 * g));
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        Yc[db] = pgn_mfma(frag_tr_scaled_k(Qs, 16 * db, 0, g, i, eLs), oc0, zero4());
-        Yc[db] = pgn_mfma(frag_tr_scaled_k(Qs, 16 * db, 1, g, i, eLs), oc1, Yc[db]);
+        Yc[db] = pgn_mfma(frag_tr(Qs, 16 * db, 0, g, i), oe0, zero4());
+        Yc[db] = pgn_mfma(frag_tr(Qs, 16 * db, 1, g, i), oe1, Yc[db]);
       }
       __syncthreads();  // A^T complete
 
@@ -500,10 +506,9 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
         const f32x4 wv = *reinterpret_cast<const f32x4*>(ws + 16 * tb + 4 * g);
         dW[tb] = acc + wv * y[tb];
       }
-      // drhs = X^T dW (X^T upper triangular); dV = beta drhs; dU = -beta eL drhs; per-row partial sums
+      // drhs = X^T dW (X^T upper triangular); dU = -beta eL drhs; per-row partial sums (dV = beta drhs is written
+      // by the chunk-local kernel from the stored drhs)
       const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
-      const __amdgpu_buffer_rsrc_t dv_out =
-          __builtin_amdgcn_make_buffer_rsrc(dv + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
       const __amdgpu_buffer_rsrc_t dr_out =
           __builtin_amdgcn_make_buffer_rsrc(drhs + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
       const bf16x8 w01 = pack(dW[0], dW[1]), w23 = pack(dW[2], dW[3]);
@@ -517,22 +522,18 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
         const f32x4 ev = *reinterpret_cast<const f32x4*>(eLs + 16 * tb + 4 * g);
         const bf16x4 vv4 = ds_read_tr(Vs + (16 * tb + 4 * g + (i >> 2)) * kPitch + 16 * w + 4 * (i & 3));
         const f32x4 vv = to_f32x4(vv4);  // V[16 tb + 4g + r][j]
-        float pv_[4], pu_[4];
+        float pr[8];  // per token row 4g + r: drhs V and drhs U, summed over this wave's 16 columns below
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tl = 16 * tb + 4 * g + r;
           dU[tb][r] = -bv[r] * ev[r] * acc[r];
-          pv_[r] = row_total16(acc[r] * vv[r]);
-          pu_[r] = row_total16(acc[r] * U[tb][r]);
-          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (__bf16)(bv[r] * acc[r])), dv_out,
-                                                (tl * DK + j) * (int)sizeof(__bf16), 0, 0);
+          pr[r] = acc[r] * vv[r];
+          pr[4 + r] = acc[r] * U[tb][r];
           __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (__bf16)acc[r]), dr_out,
                                                 (tl * DK + j) * (int)sizeof(__bf16), 0, 0);
         }
-        if (i == 15) {
-          *reinterpret_cast<f32x4*>(redV + w * C + 16 * tb + 4 * g) = f32x4{pv_[0], pv_[1], pv_[2], pv_[3]};
-          *reinterpret_cast<f32x4*>(redU + w * C + 16 * tb + 4 * g) = f32x4{pu_[0], pu_[1], pu_[2], pu_[3]};
-        }
+        const float tot = row_totals16x8(pr, i);  // lane i: the total of pr[(i >> 1) & 7]
+        if (!(i & 1)) ((i & 8) ? redU : redV)[w * C + 16 * tb + 4 * g + ((i >> 1) & 3)] = tot;
       }
       // dS_prev = a dS + (Q o eL)^T dO + K^T dU
       const float a_c = __expf(Ls[C - 1]);
@@ -653,15 +654,15 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const float* __restrict__ la,
     const float* __restrict__ be, const __bf16* __restrict__ Win, const __bf16* __restrict__ sent,
     const __bf16* __restrict__ dO, const __bf16* __restrict__ drhs, const __bf16* __restrict__ dSc,
-    const float* __restrict__ rsum, __bf16* __restrict__ dq, __bf16* __restrict__ dk, float* __restrict__ dla,
-    float* __restrict__ dbe, int T, int NC) {
+    const float* __restrict__ rsum, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
+    float* __restrict__ dla, float* __restrict__ dbe, int T, int NC) {
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* Qs = reinterpret_cast<__bf16*>(smem);
   __bf16* Ks = Qs + TILE;
   __bf16* Ws = Ks + TILE;
   __bf16* Os = Ws + TILE;   // dO
   __bf16* Ss = Os + TILE;   // S_c transposed, (j, d)
-  __bf16* dSs = Ss + TILE;  // dS (d, j)
+  __bf16* dSs = Ss + TILE;  // dS transposed, (j, d)
   __bf16* Rs = dSs + TILE;  // drhs (t, j)
   float* Ls = reinterpret_cast<float*>(Rs + TILE);
   float* eLs = Ls + C;
@@ -690,6 +691,17 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
     for (int u = 0; u < 7; ++u) sg[u] = load_seg(src[u], rows[u], tid);
 #pragma unroll
     for (int u = 0; u < 7; ++u) put_seg(Qs + u * TILE, sg[u], tid);
+    {
+      // dV = beta drhs, row segment tid (the chain kernel rounds drhs to bf16 once; dV rounds its product again)
+      const int r = tid >> 3;
+      if (r < nr) {
+        const float bt = be[(size_t)bh * T + t0 + r];
+        bf16x8 dvs;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dvs[e] = (__bf16)(bt * (float)sg[6][e]);
+        *reinterpret_cast<bf16x8*>(dv + coff + (size_t)r * DK + 8 * (tid & 7)) = dvs;
+      }
+    }
     if (w == 0) {
       const bool ok = x.l < nr;
       const float lav = ok ? la[(size_t)bh * T + t0 + x.l] : 0.f;
@@ -836,8 +848,8 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
         acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), g1, acc);
         acc = pgn_mfma(frag_tr(Ss, 16 * dt, 0, g, i), du0, acc);
         acc = pgn_mfma(frag_tr(Ss, 16 * dt, 1, g, i), du1, acc);
-        Y = pgn_mfma(frag(dSs, 16 * dt + i, 0, g), wf0, Y);
-        Y = pgn_mfma(frag(dSs, 16 * dt + i, 1, g), wf1, Y);
+        Y = pgn_mfma(frag_tr(dSs, 16 * dt, 0, g, i), wf0, Y);
+        Y = pgn_mfma(frag_tr(dSs, 16 * dt, 1, g, i), wf1, Y);
         const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
 #pragma unroll
         for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
@@ -854,11 +866,11 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
       float sd = 0.f;
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
-        // S_c and dS at rows 16 WL + 4g + r, column 16 jt + i: dS by a transpose read at rows 16 WL.., columns
-        // 16 jt..; S_c (staged transposed) by a plain read of row 16 jt + i
-        const int off = (16 * WL + 4 * g + (i >> 2)) * kPitch + 16 * jt + 4 * (i & 3);
-        const f32x4 sv = to_f32x4(*reinterpret_cast<const bf16x4*>(Ss + (16 * jt + i) * kPitch + 16 * WL + 4 * g));
-        const f32x4 dv_ = to_f32x4(ds_read_tr(dSs + off));
+        // S_c and dS at key rows 16 WL + 4g + r, column 16 jt + i: both staged transposed, so a plain read of row
+        // 16 jt + i
+        const int off = (16 * jt + i) * kPitch + 16 * WL + 4 * g;
+        const f32x4 sv = to_f32x4(*reinterpret_cast<const bf16x4*>(Ss + off));
+        const f32x4 dv_ = to_f32x4(*reinterpret_cast<const bf16x4*>(dSs + off));
 #pragma unroll
         for (int r = 0; r < 4; ++r) sd += sv[r] * dv_[r];
       }
@@ -973,11 +985,12 @@ extern "C" int pragnosia_aspin_delta_bwd(const void* q, const void* k, const voi
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(aspin_delta_bwd_chain, dim3((unsigned)nbh), dim3(512), kChainSmem, st, (const __bf16*)q,
                      (const __bf16*)k, (const __bf16*)v, la, beta, (const __bf16*)X, (const __bf16*)sent,
-                     (const __bf16*)dO, dS_final, (__bf16*)dv, drhs, dsc, rs, dS0, (int)T, NC);
+                     (const __bf16*)dO, dS_final, drhs, dsc, rs, dS0, (int)T, NC);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL(aspin_delta_bwd_local, dim3((unsigned)(nbh * NC)), dim3(512), kLocalSmem, st,
                      (const __bf16*)q, (const __bf16*)k, la, beta, (const __bf16*)W, (const __bf16*)sent,
-                     (const __bf16*)dO, drhs, dsc, rs, (__bf16*)dq, (__bf16*)dk, dla, dbeta, (int)T, NC);
+                     (const __bf16*)dO, drhs, dsc, rs, (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, dla, dbeta, (int)T,
+                     NC);
   PGN_RETURN_LAUNCH();
 }

@@ -303,6 +303,30 @@ PGN_DEVICE float row_total16(float x) {
   return x;
 }
 
+// Eight sums over the 16 lanes of each row at once: a butterfly that halves the values a lane carries at each step
+// (partners at lane distance xor 15, 7, 2, then 1, by DPP row_mirror, row_half_mirror and quad_perm), 15 exchanges
+// instead of 8 separate reductions. Lane i of each row ends holding the row's total of a[(i >> 1) & 7].
+PGN_DEVICE float row_totals16x8(const float (&a)[8], int i) {
+  auto xch = [](float x, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl)::value,
+                                                                 0xf, 0xf, false));
+  };
+  using mirror = std::integral_constant<int, 0x140>;
+  using half_mirror = std::integral_constant<int, 0x141>;
+  using swap2 = std::integral_constant<int, 0x4E>;
+  using swap1 = std::integral_constant<int, 0xB1>;
+  const bool b3 = i & 8, b2 = i & 4, b1 = i & 2;
+  float s4[4], s2[2];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)  // keep a[4 b3 + u], add the partner's copy of it
+    s4[u] = (b3 ? a[4 + u] : a[u]) + xch(b3 ? a[u] : a[4 + u], mirror{});
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    s2[u] = (b2 ? s4[2 + u] : s4[u]) + xch(b2 ? s4[u] : s4[2 + u], half_mirror{});
+  const float s1 = (b1 ? s2[1] : s2[0]) + xch(b1 ? s2[0] : s2[1], swap2{});
+  return s1 + xch(s1, swap1{});
+}
+
 // Inclusive prefix sum over the 64 lanes of a wave (lane `l` = this lane's index): a Hillis-Steele scan inside each
 // row of 16 lanes on DPP row shifts (row_shr 1, 2, 4, 8), then each row adds the totals of the rows before it, read
 // from lanes 15, 31 and 47. Every step is a VALU or lane read: no LDS round trips.
