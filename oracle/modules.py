@@ -88,7 +88,7 @@ def spin_rf(sd, x, h0=None, gate_c=8.0, nu_min=1e-3):
 
 def _mixer(sd, prefix, mixer, heads, x, st):
     sub = {k[len(prefix):]: v for k, v in sd.items() if k.startswith(prefix)}
-    if mixer in ("aspin", "dspin"):
+    if mixer in ("aspin", "dspin", "hspin"):  # hspin: AssocCarrier(d, head_dim=128), `src/model.py:650`
         return assoc_carrier(sub, x, st, heads=heads, delta=(mixer == "dspin"))
     if mixer == "fspin":
         return spin_rf(sub, x, st)

@@ -50,6 +50,58 @@ def rotate(x, theta, pos):
     return torch.stack((even * c - odd * s, even * s + odd * c), dim=-1).flatten(-2)
 
 
+HEAD_DIM_WIDE = 128
+
+
+def _plain_scan_wide(q, k, v, la, S0, want):
+    """The plain rule at head dim 128 (the reference's `hspin` carrier, `src/model.py:650`) on the 64 x 64 kernels.
+    The state's key halves evolve independently (S_t = a_t S_{t-1} + k_t v_t^T, row block by row block) and the read
+    o_t = S_t^T q_t sums over them, so with q = (q1, q2), k = (k1, k2), v = (v1, v2) in halves of 64,
+        o[..., half vh] = scan(q1, k1, v_vh) + scan(q2, k2, v_vh),   S[half kh, half vh] = final state of
+        scan(q_kh, k_kh, v_vh),
+    four 64 x 64 scans per head in one launch over 4 H heads; autograd sums the gradients of the copies. Each half of
+    q, k and v is read twice and o written twice: about twice the bytes of a 128-wide kernel. Returns
+    (o bf16 (B, H, T, 128), S_final fp32, sent (B, H, NC, 128, 128) bf16 or empty)."""
+    B, H, T, D = q.shape
+    h = D // 2
+    q1, q2, k1, k2, v1, v2 = q[..., :h], q[..., h:], k[..., :h], k[..., h:], v[..., :h], v[..., h:]
+    # sub-scan order per head: (kh, vh) = (0, 0), (0, 1), (1, 0), (1, 1)
+    qq = torch.stack([q1, q1, q2, q2], 2).reshape(B, 4 * H, T, h)
+    kk = torch.stack([k1, k1, k2, k2], 2).reshape(B, 4 * H, T, h)
+    vv = torch.stack([v1, v2, v1, v2], 2).reshape(B, 4 * H, T, h)
+    ll = la.repeat_interleave(4, dim=1)
+    S04 = None if S0 is None else S0.reshape(B, H, 2, h, 2, h).permute(0, 1, 2, 4, 3, 5).reshape(B, 4 * H, h, h)
+    o4, S4, sent4 = _op.aspin_chunk(qq, kk, vv, ll, S04, want)
+    o4 = o4.reshape(B, H, 2, 2, T, h).float()
+    o = (o4[:, :, 0] + o4[:, :, 1]).permute(0, 1, 3, 2, 4).reshape(B, H, T, D).to(torch.bfloat16)
+    S = S4.reshape(B, H, 2, 2, h, h).permute(0, 1, 2, 4, 3, 5).reshape(B, H, D, D)
+    if want:
+        NC = sent4.shape[2]
+        sent = sent4.reshape(B, H, 2, 2, NC, h, h).permute(0, 1, 4, 2, 5, 3, 6).reshape(B, H, NC, D, D)
+    else:
+        sent = sent4
+    return o, S, sent
+
+
+def _prep_wide(qp, kp, vp, gate, theta, pos, dtype=torch.bfloat16):
+    """The prep for heads the prep kernel does not take (128 wide), as torch on the GPU: unit-normalise q, k, v per
+    head (eps 1e-12), scale k by sigmoid(gate) (plain rule), rotate q and k at `pos`, transpose to (B, H, T, dk) and
+    round to `dtype` (`src/assoc.py:453-460`)."""
+    q, k, v = (F.normalize(t.transpose(1, 2).float(), dim=-1, eps=1e-12) for t in (qp, kp, vp))
+    if gate is not None:
+        k = k * torch.sigmoid(gate.float()).transpose(1, 2).unsqueeze(-1)
+    th = theta.float()
+    return rotate(q, th, pos).to(dtype), rotate(k, th, pos).to(dtype), v.to(dtype)
+
+
+def _rebase_wide(S, theta, p_dev, p_host):
+    """Key rows (2i, 2i+1) of S rotated by -p0 theta[h, i] (`src/assoc.py:399-402`) as torch on the GPU, for heads
+    the rebase kernel does not take; p0 the device scalar p_dev when given, else p_host."""
+    Dv = S.shape[-1]
+    p = p_dev.float() if p_dev is not None else torch.tensor(p_host, device=S.device, dtype=torch.float32)
+    return rotate(S.transpose(-1, -2), theta.float(), (-p).expand(Dv)).transpose(-1, -2).contiguous()
+
+
 def _positions(T, device, wrap=None):
     key = (T, str(device), wrap)
     pos = _POS_CACHE.get(key)
@@ -74,11 +126,15 @@ def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = Fa
     of 64 whatever `chunk` says: the result does not depend on the chunk size (the reference's own test), so the
     argument is accepted for signature compatibility, as are `recompute` and `mm` (operands are bf16, accumulation
     and state fp32). Returns (o in q's dtype, S_final fp32), plus the bf16 entering states when need_sent."""
-    if q.shape[-1] != HEAD_DIM_KERNEL:
-        raise PragnosiaError(f"assoc_scan: head dim {q.shape[-1]} is not supported by the HIP kernels (64 only)")
+    wide = q.shape[-1] == HEAD_DIM_WIDE and beta is None
+    if q.shape[-1] != HEAD_DIM_KERNEL and not wide:
+        raise PragnosiaError(f"assoc_scan: head dim {q.shape[-1]} is not supported by the HIP kernels (64; 128 for "
+                             "the plain rule)")
     want = bool(need_sent or _needs_grad(q, k, v, logalpha, S0, beta))
     S0 = None if S0 is None else S0.float()
-    if beta is None:
+    if wide:
+        o, S, sent = _plain_scan_wide(q.bfloat16(), k.bfloat16(), v.bfloat16(), logalpha.float(), S0, want)
+    elif beta is None:
         o, S, sent = _op.aspin_chunk(q, k, v, logalpha.float(), S0, want)
     else:
         o, S, sent, _, _ = _op.aspin_delta(q, k, v, logalpha.float(), beta.float(), S0, want)
@@ -206,7 +262,10 @@ class AssocCarrier(nn.Module):
                 0.75 if (self.delta and self.write_all) else 0.0, gated, self.theta, pos)
             return q, k, v, la, (beta if self.delta else None), P.dtype
         qp, kp, vp, gate, la, bt = self._projections(z)
-        q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
+        if self.dk == HEAD_DIM_KERNEL:
+            q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
+        else:
+            q, k, v = _prep_wide(qp, kp, vp, gate, self.theta, pos)
         bt = None if bt is None else bt.transpose(1, 2).float()
         return q, k, v, la.transpose(1, 2).float(), bt, qp.dtype
 
@@ -223,8 +282,10 @@ class AssocCarrier(nn.Module):
     def forward(self, x, h0=None, pos0: int = 0):
         """x (B, T, d); h0 = (S (B, H, dk, dk) fp32, p0) from a previous call, or None. Returns
         (x + gated output, (S, p0 + T)); positions restart at 0 every call and the carried state is rebased by -p0."""
-        if self.dk != HEAD_DIM_KERNEL:
-            raise PragnosiaError(f"AssocCarrier: head dim {self.dk} is not supported by the HIP kernels (64 only)")
+        wide = self.dk == HEAD_DIM_WIDE and not self.delta
+        if self.dk != HEAD_DIM_KERNEL and not wide:
+            raise PragnosiaError(f"AssocCarrier: head dim {self.dk} is not supported by the HIP kernels (64; 128 for "
+                                 "the plain rule)")
         if not x.is_cuda:
             raise PragnosiaError("AssocCarrier runs on a ROCm GPU only; there is no CPU path")
         B, T, D = x.shape
@@ -238,7 +299,17 @@ class AssocCarrier(nn.Module):
         p_dev = p0.float().reshape(()) if torch.is_tensor(p0) else None
         p_host = 0.0 if torch.is_tensor(p0) else float(p0)
         decode = T == 1 and not _needs_grad(x, S0, *self.parameters())
-        if decode:
+        if decode and wide:
+            # the reference's T = 1 step (`src/assoc.py:411`, torch there too), fp32: rebase, write, read
+            qp, kp, vp, gate, la, _ = self._projections(z)
+            q, k, v = _prep_wide(qp, kp, vp, gate, self.theta, torch.zeros(1, dtype=torch.long, device=x.device),
+                                 torch.float32)
+            S_prev = (torch.zeros(B, self.h, self.dk, self.dk, device=x.device) if S0 is None
+                      else _rebase_wide(S0.float(), self.theta, p_dev, p_host))
+            S = torch.exp(la.float()).transpose(1, 2).unsqueeze(-1) * S_prev + k.transpose(-1, -2) @ v
+            o = (q @ S).to(qp.dtype)
+            sent = None
+        elif decode:
             qp, kp, vp, gate, la, bt = self._projections(z)
             S_prev = S0 if S0 is not None else torch.zeros(B, self.h, self.dk, self.dk, device=x.device)
             S, o = _op.aspin_decode_step(S_prev, qp.reshape(B, self.h, self.dk), kp.reshape(B, self.h, self.dk),
@@ -250,7 +321,8 @@ class AssocCarrier(nn.Module):
             sent = None
         else:
             if S0 is not None and (p_dev is not None or p_host != 0.0):
-                S0 = _op.aspin_rebase(S0, self.theta, p_dev, p_host)
+                S0 = (_rebase_wide(S0.float(), self.theta, p_dev, p_host) if wide
+                      else _op.aspin_rebase(S0, self.theta, p_dev, p_host))
             pos = _positions(T, x.device, getattr(self, "pos_wrap", None))
             q, k, v, la, bt, dtype = self._scan_inputs(z, pos)
             want = bool(self.need_sent or not (FUSED_SCAN and self.delta) or
@@ -258,6 +330,8 @@ class AssocCarrier(nn.Module):
             if self.delta:
                 o, S, sent, _, _ = _op.aspin_delta(q, k, v, la, bt, S0, want)
                 sent = sent.transpose(-1, -2) if want else sent  # the op stores each state transposed
+            elif wide:
+                o, S, sent = _plain_scan_wide(q, k, v, la, S0, want)
             else:
                 o, S, sent = _op.aspin_chunk(q, k, v, la, S0, want)
             sent = sent if want else None

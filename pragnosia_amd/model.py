@@ -5,6 +5,7 @@ Constructor arguments, module names and initialisation follow the reference (`sr
 
     "aspin"  AssocCarrier(d)               plain write rule, 64-dim heads
     "dspin"  AssocCarrier(d, delta=True)   delta write rule
+    "hspin"  AssocCarrier(d, head_dim=128) plain write rule, 128-dim heads (four 64 x 64 scans per head)
     "fspin"  SpinCarrier(d, gated="rf")    forget-gated complex diagonal carrier
 
 The mixers run on the HIP kernels; embeddings, LayerNorms, the MLPs and the tied head are torch. Attention and the
@@ -24,6 +25,7 @@ from .spin import SpinCarrier
 MIXERS = {
     "aspin": lambda d: AssocCarrier(d),
     "dspin": lambda d: AssocCarrier(d, delta=True),
+    "hspin": lambda d: AssocCarrier(d, head_dim=128),
     "fspin": lambda d: SpinCarrier(d, gated="rf"),
 }
 

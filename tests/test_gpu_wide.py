@@ -1,0 +1,123 @@
+"""GPU parity of the plain rule at head dim 128 (the reference's `hspin` carrier, `src/model.py:650`), which runs as
+four 64 x 64 kernel scans per head (key half x value half) summed: the scan against the fp64 oracle's chunked scan,
+forward (o, final state, entering states) and backward; AssocCarrier(d, head_dim=128) forward and backward and its
+T = 1 step against the oracle's module; an LM with 128-dim heads, forward_carried and graphed greedy decode.
+
+Tolerances as for the 64-dim paths: bf16 operands, max relative error max|x - ref| / max|ref| <= 2e-2 on outputs and
+states, 5e-2 on gradients; the T = 1 step is fp32 throughout (1e-4)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import aspin as OA
+from oracle import modules as M
+from test_gpu_modules import TOL_GRAD, TOL_OUT, _block_errors, _randomise, _sd64, rel
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("T,s0", [(200, True), (64, False), (1, True)])
+def test_wide_plain_scan_matches_oracle(T, s0):
+    from pragnosia_amd.assoc import assoc_scan
+    g = torch.Generator().manual_seed(T)
+    B, H, D = 2, 3, 128
+    q = F.normalize(torch.randn(B, H, T, D, generator=g), dim=-1).bfloat16()
+    k = F.normalize(torch.randn(B, H, T, D, generator=g), dim=-1).bfloat16()
+    v = torch.randn(B, H, T, D, generator=g).bfloat16()
+    la = F.logsigmoid(torch.randn(B, H, T, generator=g) + 3)
+    S0 = torch.randn(B, H, D, D, generator=g) * 0.2 if s0 else None
+    wo, wS = torch.randn(B, H, T, D, generator=g), torch.randn(B, H, D, D, generator=g)
+    ref = [t.double().requires_grad_(True) for t in (q, k, v, la)] + [S0.double().requires_grad_(True) if s0 else None]
+    o_r, S_r, sent_r = OA.scan_twopass(*ref[:4], ref[4] if s0 else torch.zeros(B, H, D, D, dtype=torch.float64), 64)
+    ((o_r * wo.double()).sum() + (S_r * wS.double()).sum()).backward()
+    dev = [t.cuda().requires_grad_(True) for t in (q, k, v, la)] + [S0.cuda().requires_grad_(True) if s0 else None]
+    o, S, sent = assoc_scan(*dev, need_sent=True)
+    assert o.shape == (B, H, T, D) and S.shape == (B, H, D, D) and sent.shape == sent_r.shape
+    ((o.float() * wo.cuda()).sum() + (S * wS.cuda()).sum()).backward()
+    assert rel(o, o_r) < TOL_OUT and rel(S, S_r) < TOL_OUT and rel(sent.float(), sent_r) < TOL_OUT
+    for a, b in zip(dev, ref):
+        if a is not None:
+            assert rel(a.grad, b.grad) < TOL_GRAD
+
+
+def test_wide_carrier_forward_backward():
+    from pragnosia_amd.assoc import AssocCarrier
+    torch.manual_seed(60)
+    g = torch.Generator().manual_seed(60)
+    mod = AssocCarrier(256, head_dim=128)
+    assert mod.h == 2 and mod.dk == 128
+    _randomise(mod, g)
+    mod = mod.cuda()
+    x = torch.randn(2, 150, 256, generator=g)
+    S0 = torch.randn(2, 2, 128, 128, generator=g) * 0.2
+    wo = torch.randn(2, 150, 256, generator=g)
+    wS = torch.randn(2, 2, 128, 128, generator=g)
+    sd = {k: v.clone().requires_grad_(v.is_floating_point()) for k, v in _sd64(mod).items()}
+    xr, S0r = x.double().requires_grad_(True), S0.double().requires_grad_(True)
+    yr, (Sr, Tr) = M.assoc_carrier(sd, xr, (S0r, 77), heads=2)
+    ((yr - xr) * wo.double()).sum().add((Sr * wS.double()).sum()).backward()
+    xk, S0k = x.cuda().requires_grad_(True), S0.cuda().requires_grad_(True)
+    yk, (Sk, Tk) = mod(xk, (S0k, 77))
+    assert Tk == Tr == 150
+    ((yk - xk) * wo.cuda()).sum().add((Sk * wS.cuda()).sum()).backward()
+    assert rel(yk - xk, yr - xr) < TOL_OUT and rel(Sk, Sr) < TOL_OUT
+    assert rel(xk.grad, xr.grad) < TOL_GRAD and rel(S0k.grad, S0r.grad) < TOL_GRAD
+    for blk, e in _block_errors(mod, sd).items():
+        assert e < TOL_GRAD, (blk, e)
+
+
+def test_wide_carrier_decode_step_and_delta_rejected():
+    """T = 1 without autograd: rebase by p0 (host int and device scalar), normalise, gate, write, read, in fp32,
+    against the oracle's T = 1 call. The delta rule at head dim 128 has no kernel yet and says so."""
+    from pragnosia_amd._lib import PragnosiaError
+    from pragnosia_amd.assoc import AssocCarrier
+    torch.manual_seed(61)
+    g = torch.Generator().manual_seed(61)
+    mod = AssocCarrier(256, head_dim=128)
+    _randomise(mod, g)
+    mod = mod.cuda()
+    sd = _sd64(mod)
+    x = torch.randn(3, 1, 256, generator=g)
+    S0 = torch.randn(3, 2, 128, 128, generator=g) * 0.2
+    yr, (Sr, _) = M.assoc_carrier(sd, x.double(), (S0.double(), 33), heads=2)
+    with torch.no_grad():
+        yk, (Sk, Tk) = mod(x.cuda(), (S0.cuda(), 33))
+        yd, (Sd, Td) = mod(x.cuda(), (S0.cuda(), torch.tensor(33.0, device="cuda")))
+    assert Tk == 1 and float(Td) == 1.0
+    assert rel(yk - x.cuda(), yr - x.double()) < 1e-4 and rel(Sk, Sr) < 1e-4
+    assert rel(yd, yk) < 1e-6 and rel(Sd, Sk) < 1e-6
+    with pytest.raises(PragnosiaError, match="head dim 128"):
+        AssocCarrier(256, delta=True, head_dim=128).cuda()(x.cuda())
+
+
+def _lm_wide(seed):
+    from pragnosia_amd.model import LM
+    torch.manual_seed(seed)
+    m = LM(vocab=300, d=256, layers=2, ctx=64, mixer="hspin")
+    g = torch.Generator().manual_seed(seed)
+    for mx in m.mix:
+        _randomise(mx, g)
+    with torch.no_grad():
+        m.e.weight.mul_(20)
+    return m.cuda().eval()
+
+
+def test_wide_lm_forward_carried_and_graphed_decode():
+    from pragnosia_amd.decode import GreedyDecoder, greedy_eager
+    m = _lm_wide(62)
+    sd = _sd64(m)
+    g = torch.Generator().manual_seed(62)
+    ids = torch.randint(0, 300, (2, 200), generator=g)
+    with torch.no_grad():
+        f = m(ids[:, :64].cuda())
+        c = m.forward_carried(ids.cuda(), window=64)
+    assert rel(f, M.lm_forward(sd, ids[:, :64], layers=2, mixer="hspin", heads=2)) < TOL_OUT
+    assert rel(c, M.lm_forward_carried(sd, ids, 64, layers=2, mixer="hspin", heads=2)) < TOL_OUT
+    prompt = ids[:, :100]
+    dec = GreedyDecoder(m, 2, steps_per_graph=4)
+    assert not dec.fused
+    toks_g = dec.generate(prompt.cuda(), 13)
+    toks_e, lgs_e = greedy_eager(m, prompt.cuda(), 13)
+    assert torch.equal(toks_g.cpu(), toks_e.cpu())
+    _, lgs_r = M.greedy_decode(sd, prompt, 13, layers=2, mixer="hspin", heads=2, forced=toks_e.cpu())
+    assert rel(lgs_e, lgs_r) < TOL_OUT
