@@ -611,29 +611,27 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
       const __bf16* Qs = stg + h * kChainStage;
       const __bf16* Ks = Qs + TILE;
       const float* Ls = vec + h * kChainVec;
-      // scores, transposed, for token block a: AT[t][s] = (q_s . k_t) exp(L_s - L_t), s >= t
+      // scores, transposed: AT[t][s] = (q_s . k_t) exp(L_s - L_t), s >= t, zero below. Wave a owns token block a's
+      // blocks (a, sb >= a) and zeros (a, sb < a); waves 6 and 7 also take (0, 2) and (0, 3), so the ten nonzero
+      // blocks split 2, 3, 3, 2 instead of 4, 3, 2, 1 (wave 4 also reduces the previous chunk's sums)
       {
+        auto score = [&](int ta, int sb, bf16x8 kf0, bf16x8 kf1, float Lt) {
+          f32x4 sc = pgn_mfma(frag(Qs, 16 * sb + i, 0, g), kf0, zero4());
+          sc = pgn_mfma(frag(Qs, 16 * sb + i, 1, g), kf1, sc);
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[r] *= masked_decay(Lsv[r] - Lt, 16 * sb + 4 * g + r >= 16 * ta + i);
+          store_T(AT, 16 * ta, 16 * sb, g, i, sc);
+        };
         const int t = 16 * a + i;
         const bf16x8 kf0 = frag(Ks, t, 0, g), kf1 = frag(Ks, t, 1, g);
         const float Lt = Ls[t];
-        f32x4 sc[4];
-#pragma unroll
+        const int last = a == 0 ? 1 : 3;
         for (int sb = 0; sb < 4; ++sb) {
-          sc[sb] = zero4();
-          if (sb >= a) {
-            sc[sb] = pgn_mfma(frag(Qs, 16 * sb + i, 0, g), kf0, sc[sb]);
-            sc[sb] = pgn_mfma(frag(Qs, 16 * sb + i, 1, g), kf1, sc[sb]);
-          }
+          if (sb < a) store_T(AT, 16 * a, 16 * sb, g, i, zero4());
+          else if (sb <= last) score(a, sb, kf0, kf1, Lt);
         }
-#pragma unroll
-        for (int sb = 0; sb < 4; ++sb) {
-          if (sb >= a) {
-            const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sc[sb][r] *= masked_decay(Lsv[r] - Lt, 16 * sb + 4 * g + r >= t);
-          }
-          store_T(AT, 16 * a, 16 * sb, g, i, sc[sb]);
-        }
+        if (a >= 2) score(0, a, frag(Ks, i, 0, g), frag(Ks, i, 1, g), Ls[i]);
       }
       __syncthreads();  // A^T complete
       if (a == 0 && cc < NC - 1) reduce(cc + 1);  // the later chunk's sums, before its vector set is reused below
