@@ -12,8 +12,9 @@ For an LM of associative carriers (aspin or dspin, LayerNorm) the step is fused:
 projection kernel (q, k, v, decay and gate or strength in one concatenated weight), one recurrent-step kernel that
 forms the decay, gate or strength itself and writes the per-head RMS-normalised output, one kernel for the gated
 output projection with the residual, and two for the MLP (LayerNorm + first layer + GELU; second layer + residual):
-five kernels a layer instead of about twenty-five, the same fp32 arithmetic. Other mixers run the modules' own T = 1
-path. The concatenated weights are copied from the parameters at every `start`, so the graph always sees the
+five kernels a layer instead of about twenty-five, the same fp32 arithmetic. Above GEMV_MAX_BATCH sequences the dense
+layers run as torch's LayerNorm and GEMMs (matrix cores) and the carrier step stays fused. Other mixers run the
+modules' own T = 1 path. The concatenated weights are copied from the parameters at every `start`, so the graph always sees the
 current parameters.
 """
 from __future__ import annotations
@@ -24,10 +25,11 @@ import torch.nn.functional as F
 from .assoc import AssocCarrier
 
 
-# The fused step's dense kernels read each weight once per step and serve up to this many sequences well; beyond it
-# the per-layer torch GEMMs (matrix cores) are faster: measured on the 12-layer d768 LM, 0.63 vs 1.45 ms a step at
-# batch 1, 1.51 vs 1.57 at 32, 2.52 vs 1.57 at 64.
-FUSED_MAX_BATCH = 32
+# The fused step's dense layers run as the batched GEMV kernel (each weight read once a step) up to this many
+# sequences; beyond it as torch GEMMs (matrix cores), the carrier step still fused. Measured on the 12-layer d768 LM,
+# ms a step (GEMV / torch GEMMs, both with the fused step): batch 1 0.45 / 0.77, 4 0.71 / 0.75, 8 1.06 / 0.76,
+# 32 1.18 / 0.85, 64 2.05 / 0.83; the unfused step with torch GEMMs: 1.45-1.57.
+GEMV_MAX_BATCH = 4
 
 
 def fused_decode_ok(model) -> bool:
@@ -50,7 +52,7 @@ class GreedyDecoder:
         self.B = batch
         self.K = steps_per_graph
         self.graph = None
-        self.fused = (fused_decode_ok(model) and batch <= FUSED_MAX_BATCH) if fused is None else fused
+        self.fused = fused_decode_ok(model) if fused is None else fused
         if self.fused and not fused_decode_ok(model):
             raise ValueError("GreedyDecoder: this model's decode step cannot run fused")
 
@@ -117,23 +119,38 @@ class GreedyDecoder:
                 dst[0].copy_(w)
                 dst[1].copy_(g)
 
+    def _dense(self, x, W, ln, bias=None, scale=None, act=0, resid=None):
+        """act(scale * (W LayerNorm(x)) + bias) + resid: the batched GEMV kernel up to GEMV_MAX_BATCH sequences,
+        else torch's LayerNorm and GEMM (matrix cores) with the same epilogue."""
+        if self.B <= GEMV_MAX_BATCH:
+            return torch.ops.pragnosia.decode_gemv(x, W, None if ln is None else ln.weight,
+                                                   None if ln is None else ln.bias, 0.0 if ln is None else ln.eps,
+                                                   bias, scale, act, resid)
+        z = x if ln is None else F.layer_norm(x, (x.shape[-1],), ln.weight, ln.bias, ln.eps)
+        y = F.linear(z, W, bias)
+        if act == 1:
+            y = F.gelu(y)
+        if scale is not None:
+            return torch.addcmul(resid, y, scale) if resid is not None else y * scale
+        return y + resid if resid is not None else y
+
     def _one_step_fused(self):
         m, op = self.m, torch.ops.pragnosia
         h = (m.e(self.tok) + m.p(self.pos)).reshape(self.B, -1)
         for i, (mx, mp) in enumerate(zip(m.mix, m.mlp)):
             gated = not (mx.delta or mx.write_all)
-            P = op.decode_gemv(h, self.wcat[i], mx.ln.weight, mx.ln.bias, mx.ln.eps, None, None, 0, None)
+            P = self._dense(h, self.wcat[i], mx.ln)
             o = op.aspin_decode_proj_(self.st[i][0], P, mx.h, mx.wa.bias, mx.A,
                                       mx.la_floor if mx.hl_floor else None, mx.wi.bias if gated else None,
                                       mx.wb.bias if mx.delta else None, 0.75 if (mx.delta and mx.write_all) else 0.0,
                                       gated, mx.theta, self.p0s[i:i + 1], 0.0, mx.on.weight,
                                       mx.on.eps if mx.on.eps is not None else torch.finfo(torch.float32).eps)
-            x1 = op.decode_gemv(o, mx.o.weight, None, None, 0.0, None, self.sig[i], 0, h)
-            hm = op.decode_gemv(x1, mp.a.weight, mp.n.weight, mp.n.bias, mp.n.eps, mp.a.bias, None, 1, None)
-            h = op.decode_gemv(hm, mp.b.weight, None, None, 0.0, mp.b.bias, None, 0, x1)
+            x1 = self._dense(o, mx.o.weight, None, scale=self.sig[i], resid=h)
+            hm = self._dense(x1, mp.a.weight, mp.n, bias=mp.a.bias, act=1)
+            h = self._dense(hm, mp.b.weight, None, bias=mp.b.bias, resid=x1)
         self.p0s.fill_(1.0)  # every state is now in the positions of a one-token call
         self.pos.copy_((self.pos + 1) % m.ctx)
-        lg = op.decode_gemv(h, m.e.weight, m.n.weight, m.n.bias, m.n.eps, None, None, 0, None)
+        lg = self._dense(h, m.e.weight, m.n)
         nxt = lg.argmax(-1)
         self.out.index_copy_(0, self.ctr, nxt.view(1, -1))
         self.ctr.add_(1)

@@ -82,7 +82,7 @@ def test_decode_proj_matches_module_step(delta, write_all, hl_floor):
 
 
 @pytest.mark.parametrize("mixer", ["aspin", "dspin"])
-@pytest.mark.parametrize("B", [1, 3])
+@pytest.mark.parametrize("B", [1, 3, 40])  # 1, 3: GEMV dense layers; 40: torch GEMMs around the fused step
 def test_fused_graphed_decode_equals_unfused_and_eager(mixer, B):
     from pragnosia_amd.decode import GreedyDecoder, greedy_eager
     from pragnosia_amd.model import LM
