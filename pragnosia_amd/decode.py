@@ -102,22 +102,25 @@ class GreedyDecoder:
         self.tok.copy_(nxt.view(-1, 1))
 
     def _fused_weights(self):
-        """Per layer: the concatenated input projection (q, k, v, decay, then the gate or strength) and the output
-        gate sigmoid(g) as a device scalar, written into the same buffers every time (the graph reads them)."""
+        """Per layer: the concatenated input projection (q, k, v, decay, then the gate or strength), the output gate
+        sigmoid(g) as a device scalar and the output projection pre-scaled by it (for the GEMM form), written into
+        the same buffers every time (the graph reads them)."""
         m = self.m
         fresh = []
         for mx in m.mix:
             gated = not (mx.delta or mx.write_all)
             extra = [mx.wi.weight] if gated else ([mx.wb.weight] if mx.delta else [])
-            fresh.append((torch.cat([mx.q.weight, mx.k.weight, mx.v.weight, mx.wa.weight] + extra).float(),
-                          torch.sigmoid(mx.gate.detach().float()).reshape(1)))
+            sig = torch.sigmoid(mx.gate.detach().float()).reshape(1)
+            fresh.append((torch.cat([mx.q.weight, mx.k.weight, mx.v.weight, mx.wa.weight] + extra).float(), sig,
+                          mx.o.weight.detach().float() * sig))
         if getattr(self, "wcat", None) is None:
-            self.wcat = [w.contiguous() for w, _ in fresh]
-            self.sig = [g.contiguous() for _, g in fresh]
+            self.wcat = [w.contiguous() for w, _, _ in fresh]
+            self.sig = [g.contiguous() for _, g, _ in fresh]
+            self.wos = [wo.contiguous() for _, _, wo in fresh]
         else:
-            for dst, (w, g) in zip(zip(self.wcat, self.sig), fresh):
-                dst[0].copy_(w)
-                dst[1].copy_(g)
+            for dst, src in zip(zip(self.wcat, self.sig, self.wos), fresh):
+                for d, t in zip(dst, src):
+                    d.copy_(t)
 
     def _dense(self, x, W, ln, bias=None, scale=None, act=0, resid=None):
         """act(scale * (W LayerNorm(x)) + bias) + resid: the batched GEMV kernel up to GEMV_MAX_BATCH sequences,
@@ -145,7 +148,10 @@ class GreedyDecoder:
                                       mx.wb.bias if mx.delta else None, 0.75 if (mx.delta and mx.write_all) else 0.0,
                                       gated, mx.theta, self.p0s[i:i + 1], 0.0, mx.on.weight,
                                       mx.on.eps if mx.on.eps is not None else torch.finfo(torch.float32).eps)
-            x1 = self._dense(o, mx.o.weight, None, scale=self.sig[i], resid=h)
+            if self.B <= GEMV_MAX_BATCH:
+                x1 = self._dense(o, mx.o.weight, None, scale=self.sig[i], resid=h)
+            else:  # h + o (sigmoid(g) W_o)^T in one GEMM
+                x1 = torch.addmm(h, o, self.wos[i].t())
             hm = self._dense(x1, mp.a.weight, mp.n, bias=mp.a.bias, act=1)
             h = self._dense(hm, mp.b.weight, None, bias=mp.b.bias, resid=x1)
         self.p0s.fill_(1.0)  # every state is now in the positions of a one-token call
