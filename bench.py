@@ -225,6 +225,47 @@ def diag_bench(steps):
             "hbm_frac": round((fb + bb) / (t_fwd + t_bwd) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def wide_bench(steps=30):
+    """The plain rule at head dim 128 (the reference's `hspin` carrier) at configs[2]'s width: B16 T512, d 768 as 6
+    heads of 128, bf16 q/k/v; one forward + backward through `assoc_scan` (four 64 x 64 kernel scans per head and the
+    copies around them), one step captured in a HIP graph (forward and autograd backward) and replayed `steps` times
+    between HIP events, beside the 64-dim path at the same width timed the same way."""
+    import torch
+    import torch.nn.functional as F
+    from pragnosia_amd.assoc import assoc_scan
+    g = torch.Generator().manual_seed(9)
+    out = {"workload": "plain rule fwd+bwd at head dim 128 vs 64, B16 T512 d768 (configs[2] width), graph-replayed"}
+    for H, D in ((6, 128), (12, 64)):
+        q = F.normalize(torch.randn(16, H, 512, D, generator=g), dim=-1).bfloat16().cuda().requires_grad_(True)
+        k = F.normalize(torch.randn(16, H, 512, D, generator=g), dim=-1).bfloat16().cuda().requires_grad_(True)
+        v = torch.randn(16, H, 512, D, generator=g).bfloat16().cuda().requires_grad_(True)
+        la = F.logsigmoid(torch.randn(16, H, 512, generator=g) + 3).cuda().requires_grad_(True)
+        do = torch.randn(16, H, 512, D, generator=g).bfloat16().cuda()
+
+        def step():
+            o, _ = assoc_scan(q, k, v, la)
+            torch.autograd.backward([o], [do])
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        out[f"head_dim_{D}"] = {"ms_per_step": round(ms, 4), "Mtok_s": round(16 * 512 / ms / 1e3, 2)}
+    return out
+
+
 def carried_bench():
     """B2 T8192 H12 D64 bf16 inputs, la = logsigmoid(N(4,1)); (i) 16 windows of 512 with the
     fp32 state carried and rebased by -512 theta between windows (positions restart per window, as successive
@@ -528,6 +569,7 @@ def gpu_bench(args):
         sec["carrier_layer"] = carrier_layer_bench()
         sec["carrier_layer_delta"] = carrier_layer_bench(delta=True)
         sec["decode"] = decode_bench()
+        sec["head_dim_128"] = wide_bench()
         sec["lds_contraction"] = lds_contraction_bench()
         res["decode_ms_per_token_bs1"] = sec["decode"]["ms_per_token_bs1"]
         res["secondary"] = sec
