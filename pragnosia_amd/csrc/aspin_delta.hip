@@ -70,23 +70,12 @@ PGN_DEVICE void chunk_decays(float la_l, int l, float* Ls, float* eLs, float* ws
 // X = (I + N)^-1, one wave per (batch-head, chunk)
 // N^T and X are kept as their ten 16 x 16 blocks on and below the diagonal (block (tb, sb), sb <= tb, at index
 // tb (tb + 1) / 2 + sb, unpadded rows so the substitution reads four entries at once): 24 KB of LDS per chunk, so
-// six chunks (one round of the grid at cfg2) are resident per compute unit. The keys are read from global memory
-// straight into MFMA operand registers.
+// six chunks (one round of the grid at cfg2) are resident per compute unit. The keys are loaded in 16-byte row
+// segments into the X block area (unused until N is formed) and read from there as MFMA operands.
 constexpr int BP = 16;                 // row pitch of a 16 x 16 fp32 block
 constexpr int BLK = 16 * BP;
 PGN_DEVICE int blk(int tb, int sb) { return (tb * (tb + 1) / 2 + sb) * BLK; }
 
-// the MFMA operand of one key row from global memory: row[32 m + 4 g .. + 3] and row[32 m + 16 + 4 g .. + 3]
-PGN_DEVICE bf16x8 gfrag(const __bf16* row, int m, int g, bool valid) {
-  bf16x4 lo, hi;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) lo[u] = hi[u] = (__bf16)0.f;
-  if (valid) {
-    lo = *reinterpret_cast<const bf16x4*>(row + 32 * m + 4 * g);
-    hi = *reinterpret_cast<const bf16x4*>(row + 32 * m + 16 + 4 * g);
-  }
-  return cat8(lo, hi);
-}
 
 __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__ k, const float* __restrict__ la,
                                                       const float* __restrict__ be, __bf16* __restrict__ X, int T,
@@ -100,17 +89,27 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
   const int l = threadIdx.x, g = l >> 4, i = l & 15;
   const int t0 = c * C, nr = min(C, T - t0);
   const __bf16* kc = k + ((size_t)bh * T + t0) * DK;
-  // this lane's operand rows i, 16 + i, 32 + i, 48 + i (both halves of the contraction), all loads issued at once
-  bf16x8 kf[4][2];
+  // the keys in 16-byte row segments (eight contiguous 1 KB loads per wave, rows past T as zeros), staged in the X
+  // block area, which nothing uses before N is formed; then this lane's operand rows i, 16 + i, 32 + i, 48 + i
+  __bf16* Kst = reinterpret_cast<__bf16*>(Xf);
+  static_assert(64 * kPitch * sizeof(__bf16) <= sizeof(Xf), "the key tile fits the X block area");
+  {
+    bf16x8 seg[8];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+    for (int n = 0; n < 8; ++n) seg[n] = load_seg(kc, nr, l + 64 * n);
 #pragma unroll
-    for (int m = 0; m < 2; ++m) kf[rb][m] = gfrag(kc + (size_t)(16 * rb + i) * DK, m, g, 16 * rb + i < nr);
+    for (int n = 0; n < 8; ++n) put_seg(Kst, seg[n], l + 64 * n);
+  }
   const float lav = l < nr ? la[(size_t)bh * T + t0 + l] : 0.f;
   const float bev = l < nr ? be[(size_t)bh * T + t0 + l] : 0.f;
   Ls[l] = incl_scan64(lav, l);
   bs[l] = bev;
   __syncthreads();
+  bf16x8 kf[4][2];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int m = 0; m < 2; ++m) kf[rb][m] = frag(Kst, 16 * rb + i, m, g);
 
   // N^T blocks: accumulator rows s (block sb), lane t (block tb), for sb <= tb
 #pragma unroll
