@@ -32,7 +32,8 @@ const char* pragnosia_error_string(int code);
  * Forward: writes hr = Re h and hi = Im h for every t (both (B, T, D) fp32; hr is the output y, hi is saved for
  * the backward) and, when hr_last/hi_last are non-NULL, the final state (Re h_{T-1}, Im h_{T-1}) as two (B, D) fp32
  * arrays. Replaces `_Scan.forward` / `_fwd` of src/scan_kernel.py:24-50, :105-119.
- * u, logmag, ang: (B, T, D) fp32. h0r, h0i: (B, D) fp32 or NULL (both or neither). */
+ * u, logmag, ang: (B, T, D) fp32. h0r, h0i: (B, D) fp32 or NULL (both or neither). T = 0 is allowed: the final
+ * state is then h0 (zero when NULL), as the reference's scan returns it. */
 int pragnosia_diag_scan_fwd(const float* u, const float* logmag, const float* ang,
                             const float* h0r, const float* h0i,
                             float* hr, float* hi, float* hr_last, float* hi_last,
@@ -42,7 +43,8 @@ int pragnosia_diag_scan_fwd(const float* u, const float* logmag, const float* an
  * `_bwd` of src/scan_kernel.py:53-99, :121-140, including the folding of the final-state gradients:
  * g_last_r adds to g at t = T-1 and g_last_i seeds the imaginary adjoint (either may be NULL = zero).
  * g, hr, hi, logmag, ang: (B, T, D) fp32; du, dlogmag, dang: (B, T, D) fp32 outputs.
- * h0r/h0i: the forward's initial state or NULL; dh0r/dh0i: (B, D) outputs or NULL (written only if non-NULL). */
+ * h0r/h0i: the forward's initial state or NULL; dh0r/dh0i: (B, D) outputs or NULL (written only if non-NULL).
+ * T = 0: dh0 = the final state's gradient (g_last_r, g_last_i). */
 int pragnosia_diag_scan_bwd(const float* g, const float* g_last_r, const float* g_last_i,
                             const float* logmag, const float* ang, const float* hr, const float* hi,
                             const float* h0r, const float* h0i,

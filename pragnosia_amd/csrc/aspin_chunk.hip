@@ -907,12 +907,9 @@ extern "C" int pragnosia_aspin_chunk_fwd(const void* q, const void* k, const voi
   if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
   PGN_CHECK_ARG(q && k && v && la && o && S_final);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)aspin_plain_fwd, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kFwdSmem);
+  {
+    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_fwd, kFwdSmem);
     if (e != hipSuccess) return (int)e;
-    attr_set = true;
   }
   const int NC = (int)((T + C - 1) / C);
   hipLaunchKernelGGL(aspin_plain_fwd, dim3((unsigned)(B * H)), dim3(kFwdWaves * 64), kFwdSmem, (hipStream_t)stream,
@@ -953,12 +950,9 @@ extern "C" int pragnosia_aspin_chunk_fwd_seg(const void* q, const void* k, const
   PGN_CHECK_ARG(workspace_bytes >= seg_workspace_bytes(B, H, T, seg_chunks));
   const int64_t nseg = seg_count(T, seg_chunks);
   PGN_CHECK_ARG(B * H * nseg < ((int64_t)1 << 31));
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)aspin_plain_fwd, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kFwdSmem);
+  {
+    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_fwd, kFwdSmem);
     if (e != hipSuccess) return (int)e;
-    attr_set = true;
   }
   const int NC = (int)((T + C - 1) / C);
   float* E = (float*)workspace;
@@ -982,12 +976,9 @@ extern "C" int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const voi
   if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
   PGN_CHECK_ARG(q && k && v && la && sent && dO && dq && dk && dv && dla);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)aspin_plain_bwd, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kBwdSmem);
+  {
+    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_bwd, kBwdSmem);
     if (e != hipSuccess) return (int)e;
-    attr_set = true;
   }
   const int NC = (int)((T + C - 1) / C);
   hipLaunchKernelGGL(aspin_plain_bwd, dim3((unsigned)(B * H)), dim3(512), kBwdSmem, (hipStream_t)stream,
@@ -1008,12 +999,9 @@ extern "C" int pragnosia_aspin_chunk_bwd_seg(const void* q, const void* k, const
   PGN_CHECK_ARG(workspace_bytes >= seg_workspace_bytes(B, H, T, seg_chunks));
   const int64_t nseg = seg_count(T, seg_chunks);
   PGN_CHECK_ARG(B * H * nseg < ((int64_t)1 << 31));
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)aspin_plain_bwd, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kBwdSmem);
+  {
+    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_bwd, kBwdSmem);
     if (e != hipSuccess) return (int)e;
-    attr_set = true;
   }
   const int NC = (int)((T + C - 1) / C);
   float* F = (float*)workspace;

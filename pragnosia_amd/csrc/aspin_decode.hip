@@ -48,9 +48,10 @@ PGN_DEVICE float softplus_(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
 // With `on` (the per-head RMSNorm weight), the output is written normalised and token-major, o[b][h 64 + j] =
 // (o_j r) on_j with r = 1 / sqrt(mean_j o_j^2 + eps) (nn.RMSNorm(dk), eps=None: fp32 epsilon; `src/assoc.py:505`);
-// else o (B, H, 64) as computed.
+// else o (B, H, 64) as computed. S and Sout may be the same array (the in-place update of the graphed decode), so
+// neither is declared __restrict__: every element is read into registers before the thread that owns it stores it.
 template <bool FROM_P>
-__global__ __launch_bounds__(256) void aspin_decode(const float* __restrict__ S, float* __restrict__ Sout, StepIn in,
+__global__ __launch_bounds__(256) void aspin_decode(const float* S, float* Sout, StepIn in,
                                                     const float* __restrict__ theta, const float* __restrict__ p0d,
                                                     float p0h, const float* __restrict__ on, float on_eps,
                                                     float* __restrict__ o, int H) {

@@ -14,15 +14,16 @@
 //                      diagonal blocks by doubling and substitutes across blocks, `src/assoc.py:168-204`; both are
 //                      exact in exact arithmetic). X is stored bf16 for the products; measured against an fp64
 //                      inverse it is as close as bf16 rounding of the exact inverse allows, repeated keys included.
-//   aspin_delta_fwd    one workgroup of 4 waves per (batch, head) walks the chunks. The rule is independent per
-//                      value column given X, so wave w owns value columns 16w..16w+15 for all 64 tokens and the
-//                      whole state chain (U -> rhs -> W -> S') stays in that wave's MFMA accumulators: each
+//   aspin_delta_fwd    one workgroup of 8 waves per (batch, head) walks the chunks: 4 chain waves and 4 service
+//                      waves (decayed scores, staging of the next chunk, its decay scan). The rule is independent
+//                      per value column given X, so chain wave w owns value columns 16w..16w+15 for all 64 tokens
+//                      and the whole state chain (U -> rhs -> W -> S') stays in that wave's MFMA accumulators: each
 //                      product's accumulator is the next product's operand, with no LDS round trip and no barrier
 //                      on the chain. Writes o, the residuals W and the entering states (both bf16; each entering
 //                      state transposed, (j, d), so a lane's four consecutive key rows are one 8-byte store) for
 //                      the backward, and the final fp32 state.
-//   aspin_delta_bwd_chain   one workgroup of 4 waves per (batch, head), chunks in reverse, wave w owning value
-//                      columns 16w.. again. Carries dS (gradient on the state leaving the chunk) in registers:
+//   aspin_delta_bwd_chain   one workgroup of 8 waves per (batch, head), chunks in reverse: 4 chain waves, chain
+//                      wave w owning value columns 16w.. again, and 4 service waves. Carries dS (gradient on the state leaving the chunk) in registers:
 //                          dW = A^T dO + w o (K dS),  drhs = X^T dW,  dU = -beta eL o drhs,
 //                          dS_prev = a dS + (Q o eL)^T dO + K^T dU,
 //                      and writes drhs, the per-chunk dS (bf16, transposed) and the row sums over value columns that the decay
@@ -916,13 +917,7 @@ bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
   return D == DK && Cc == C;
 }
 
-int set_smem(const void* fn, size_t bytes, bool& done) {
-  if (done) return 0;
-  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-  if (e != hipSuccess) return (int)e;
-  done = true;
-  return 0;
-}
+int set_smem(const void* fn, size_t bytes) { return (int)pgn_lds_limit(fn, bytes); }
 
 }  // namespace
 
@@ -948,8 +943,7 @@ extern "C" int pragnosia_aspin_delta_fwd(const void* q, const void* k, const voi
                      (__bf16*)X, (int)T, NC);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  static bool fwd_set = false;
-  int rc = set_smem((const void*)aspin_delta_fwd, kFwdSmem, fwd_set);
+  int rc = set_smem((const void*)aspin_delta_fwd, kFwdSmem);
   if (rc) return rc;
   hipLaunchKernelGGL(aspin_delta_fwd, dim3((unsigned)nbh), dim3(512), kFwdSmem, st, (const __bf16*)q, (const __bf16*)k,
                      (const __bf16*)v, la, beta, (const __bf16*)X, S0, (__bf16*)o, (__bf16*)W, S_final,
@@ -968,10 +962,9 @@ extern "C" int pragnosia_aspin_delta_bwd(const void* q, const void* k, const voi
   PGN_CHECK_ARG(q && k && v && la && beta && sent && W && X && dO && dq && dk && dv && dla && dbeta && workspace);
   const int64_t need = pragnosia_aspin_delta_bwd_workspace_bytes(B, H, T, D, chunk);
   PGN_CHECK_ARG(workspace_bytes >= need);
-  static bool chain_set = false, local_set = false;
-  int rc = set_smem((const void*)aspin_delta_bwd_chain, kChainSmem, chain_set);
+  int rc = set_smem((const void*)aspin_delta_bwd_chain, kChainSmem);
   if (rc) return rc;
-  rc = set_smem((const void*)aspin_delta_bwd_local, kLocalSmem, local_set);
+  rc = set_smem((const void*)aspin_delta_bwd_local, kLocalSmem);
   if (rc) return rc;
   const int NC = (int)((T + C - 1) / C);
   const int nbh = (int)(B * H);

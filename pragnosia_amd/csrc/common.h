@@ -5,7 +5,26 @@
 #include <hip/hip_bf16.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <set>
+#include <utility>
+
 #include "../../include/pragnosia_hip.h"
+
+// Raise a kernel's dynamic LDS limit to `bytes` on the current device, once per (kernel, device). Safe to call from
+// several host threads at once (the entry points promise that calls on distinct streams are independent).
+inline hipError_t pgn_lds_limit(const void* fn, size_t bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({fn, dev})) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e == hipSuccess) done.insert({fn, dev});
+  return e;
+}
 
 #define PGN_DEVICE __device__ __forceinline__
 

@@ -245,6 +245,24 @@ __global__ __launch_bounds__(NW * 64) void diag_bwd_kernel(
   }
 }
 
+// The empty sequence (T = 0): the final state is the initial one, so the forward writes (x_r, x_i) = h0 (zero when
+// h0 is absent) and the backward passes the final state's gradient through to h0's, (x_r, x_i) = (g_last_r,
+// g_last_i) (zero when absent). n = B D elements.
+__global__ __launch_bounds__(256) void diag_empty_kernel(const float* ar, const float* ai, float* xr, float* xi,
+                                                         int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) {
+    xr[i] = ar != nullptr ? ar[i] : 0.f;
+    xi[i] = ai != nullptr ? ai[i] : 0.f;
+  }
+}
+
+int launch_empty(const float* ar, const float* ai, float* xr, float* xi, int64_t n, hipStream_t st) {
+  if (xr == nullptr) return PRAGNOSIA_OK;
+  hipLaunchKernelGGL(diag_empty_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, ar, ai, xr, xi, n);
+  PGN_RETURN_LAUNCH();
+}
+
 template <int NW, int SEG, int CH>
 int launch_fwd(const float* u, const float* lm, const float* an, const float* h0r, const float* h0i, float* hr,
                float* hi, float* hrl, float* hil, int B, int T, int D, hipStream_t st) {
@@ -280,9 +298,9 @@ extern "C" int pragnosia_diag_scan_fwd(const float* u, const float* logmag, cons
   PGN_CHECK_ARG(shape_ok(B, T, D));
   PGN_CHECK_ARG((h0r == nullptr) == (h0i == nullptr));
   PGN_CHECK_ARG((hr_last == nullptr) == (hi_last == nullptr));
-  if (T == 0) return PRAGNOSIA_OK;
-  PGN_CHECK_ARG(u && logmag && ang && hr && hi);
   hipStream_t st = (hipStream_t)stream;
+  if (T == 0) return launch_empty(h0r, h0i, hr_last, hi_last, B * D, st);
+  PGN_CHECK_ARG(u && logmag && ang && hr && hi);
   // 16 waves x 64 channels, 4-token segments (64-token time blocks): swept against 4-16 waves, 32/64 channels and
   // 2-16-token segments at B16 T512 D768; short sequences use 4 waves
   if (T >= 64)
@@ -298,7 +316,7 @@ extern "C" int pragnosia_diag_scan_bwd(const float* g, const float* g_last_r, co
   PGN_CHECK_ARG((h0r == nullptr) == (h0i == nullptr));
   PGN_CHECK_ARG((dh0r == nullptr) == (dh0i == nullptr));
   hipStream_t st = (hipStream_t)stream;
-  if (T == 0) return PRAGNOSIA_ERR_INVALID_ARGUMENT;
+  if (T == 0) return launch_empty(g_last_r, g_last_i, dh0r, dh0i, B * D, st);
   PGN_CHECK_ARG(g && logmag && ang && hr && hi && du && dlogmag && dang);
   if (T >= 64)
     return launch_bwd<16, 4, 64>(g, g_last_r, g_last_i, logmag, ang, hr, hi, h0r, h0i, du, dlogmag, dang, dh0r, dh0i,

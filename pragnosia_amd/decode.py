@@ -219,14 +219,15 @@ class GreedyDecoder:
 
 
 @torch.no_grad()
-def greedy_eager(model, prompt, n):
+def greedy_eager(model, prompt, n, forced=None):
     """The same generation without a graph, one eager step per token (the reference's generate() with temp 0).
-    Returns (tokens (B, n), logits of every step (B, n, V))."""
+    `forced` (B, n) replaces each argmax by the given token (teacher forcing), so the logits of another run's tokens
+    can be compared step by step. Returns (tokens (B, n), logits of every step (B, n, V))."""
     dec = GreedyDecoder(model, prompt.shape[0])
     states, pw, lg = dec.prefill(prompt)
     toks, lgs = [], []
-    for _ in range(n):
-        nxt = lg.argmax(-1)
+    for step in range(n):
+        nxt = lg.argmax(-1) if forced is None else forced[:, step]
         toks.append(nxt)
         lgs.append(lg)
         h = model.e(nxt[:, None]) + model.p(torch.full((1,), pw, device=prompt.device, dtype=torch.long))

@@ -35,6 +35,25 @@ def _f32(t: Optional[Tensor]) -> Optional[Tensor]:
     return None if t is None else t.to(torch.float32).contiguous()
 
 
+def _expect(op: str, dev, **shapes) -> None:
+    """Reject, before anything is launched, an argument whose shape differs from the one the kernels assume or that
+    lives on another device than `dev`: the C ABI takes raw pointers and sizes, so a mismatch there would read or
+    write past a buffer instead of raising. `shapes` maps an argument name to (tensor or None, expected shape), a
+    shape entry None matching any size; a shape of () for a scalar accepts any one-element tensor."""
+    for name, (t, shape) in shapes.items():
+        if t is None:
+            continue
+        if shape == ():
+            ok = t.numel() == 1
+        else:
+            ok = t.dim() == len(shape) and all(s is None or t.shape[i] == s for i, s in enumerate(shape))
+        if not ok:
+            want = "one element" if shape == () else str(tuple("*" if s is None else s for s in shape))
+            raise PragnosiaError(f"{op}: {name} has shape {tuple(t.shape)}, expected {want}")
+        if t.device != dev:
+            raise PragnosiaError(f"{op}: {name} is on {t.device}, expected {dev}")
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # complex diagonal scan (fspin): replaces src/scan_kernel.py:105-148
 @torch.library.custom_op("pragnosia::diag_scan", mutates_args=())
@@ -43,8 +62,12 @@ def diag_scan(u: Tensor, logmag: Tensor, ang: Tensor, h0r: Optional[Tensor],
     """h_t = exp(logmag_t + i ang_t) h_{t-1} + u_t over (B, T, D) fp32. Returns (Re h, Re h_last, Im h_last, Im h);
     the last output is the saved imaginary part for the backward (not differentiable)."""
     _require_gpu(u, logmag, ang, h0r, h0i)
-    u, logmag, ang, h0r, h0i = _f32(u), _f32(logmag), _f32(ang), _f32(h0r), _f32(h0i)
+    if u.dim() != 3 or (h0r is None) != (h0i is None):
+        raise PragnosiaError("diag_scan: u must be (B, T, D), and h0r and h0i given together")
     B, T, D = u.shape
+    _expect("diag_scan", u.device, logmag=(logmag, (B, T, D)), ang=(ang, (B, T, D)), h0r=(h0r, (B, D)),
+            h0i=(h0i, (B, D)))
+    u, logmag, ang, h0r, h0i = _f32(u), _f32(logmag), _f32(ang), _f32(h0r), _f32(h0i)
     hr = torch.empty(B, T, D, device=u.device, dtype=torch.float32)
     hi = torch.empty_like(hr)
     hrl = torch.empty(B, D, device=u.device, dtype=torch.float32)
@@ -67,9 +90,14 @@ def diag_scan_bwd(g: Tensor, g_last_r: Optional[Tensor], g_last_i: Optional[Tens
                   h0i: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """The adjoint recurrence. Returns (du, dlogmag, dang, dh0r, dh0i); dh0r/dh0i are empty when h0 was None."""
     _require_gpu(g, logmag, ang, hr, hi)
+    if g.dim() != 3 or (h0r is None) != (h0i is None):
+        raise PragnosiaError("diag_scan_bwd: g must be (B, T, D), and h0r and h0i given together")
+    B, T, D = g.shape
+    _expect("diag_scan_bwd", g.device, g_last_r=(g_last_r, (B, D)), g_last_i=(g_last_i, (B, D)),
+            logmag=(logmag, (B, T, D)), ang=(ang, (B, T, D)), hr=(hr, (B, T, D)), hi=(hi, (B, T, D)),
+            h0r=(h0r, (B, D)), h0i=(h0i, (B, D)))
     g, g_last_r, g_last_i = _f32(g), _f32(g_last_r), _f32(g_last_i)
     logmag, ang, hr, hi, h0r, h0i = _f32(logmag), _f32(ang), _f32(hr), _f32(hi), _f32(h0r), _f32(h0i)
-    B, T, D = g.shape
     du, dlm, dan = (torch.empty(B, T, D, device=g.device, dtype=torch.float32) for _ in range(3))
     has = h0r is not None
     dh0r = torch.empty(B, D, device=g.device) if has else g.new_empty(0)
@@ -118,6 +146,7 @@ def aspin_out(o: Tensor, weight: Tensor, eps: float, out_bf16: bool) -> tuple[Te
     """Per-head RMSNorm of the scan output o (B, H, T, 64) (cast to bf16) with `weight` (64,), written token-major
     as (B, T, H * 64) in bf16 (out_bf16) or fp32. Returns (y, rstd (B, H, T) fp32, saved for the backward)."""
     _require_gpu(o, weight)
+    _expect("aspin_out", o.device, o=(o, (None, None, None, 64)), weight=(weight, (64,)))
     o, weight = _bf16(o), _f32(weight)
     B, H, T, D = o.shape
     y = torch.empty(B, T, H * D, device=o.device, dtype=torch.bfloat16 if out_bf16 else torch.float32)
@@ -138,9 +167,11 @@ def _(o, weight, eps, out_bf16):
 def aspin_out_bwd(gy: Tensor, o: Tensor, weight: Tensor, rstd: Tensor) -> tuple[Tensor, Tensor]:
     """Backward of aspin_out. gy (B, T, H * 64) bf16 or fp32. Returns (dO (B, H, T, 64) bf16, dweight (64,) fp32)."""
     _require_gpu(gy, o, weight, rstd)
+    _expect("aspin_out_bwd", o.device, o=(o, (None, None, None, 64)), weight=(weight, (64,)))
+    B, H, T, D = o.shape
+    _expect("aspin_out_bwd", o.device, gy=(gy, (B, T, H * D)), rstd=(rstd, (B, H, T)))
     gy = gy.contiguous() if gy.dtype in (torch.bfloat16, torch.float32) else gy.float().contiguous()
     o, weight, rstd = _bf16(o), _f32(weight), _f32(rstd)
-    B, H, T, D = o.shape
     dO = torch.empty(B, H, T, D, device=o.device, dtype=torch.bfloat16)
     n = lib().pragnosia_aspin_out_weight_partials(B, H, T)
     part = torch.empty(n, D, device=o.device, dtype=torch.float32)
@@ -179,12 +210,21 @@ def _bf16(t: Tensor) -> Tensor:
     return t.to(torch.bfloat16).contiguous()
 
 
+def _expect_scan(op: str, q: Tensor, k, v, la, beta=None, S0=None, theta=None) -> None:
+    """q, k, v (B, H, T, 64); la and beta (B, H, T); S0 (B, H, 64, 64); theta (H, 32); all on q's device."""
+    _expect(op, q.device, q=(q, (None, None, None, 64)))
+    B, H, T, D = q.shape
+    _expect(op, q.device, k=(k, (B, H, T, D)), v=(v, (B, H, T, D)), la=(la, (B, H, T)), beta=(beta, (B, H, T)),
+            S0=(S0, (B, H, D, D)), theta=(theta, (H, D // 2)))
+
+
 @torch.library.custom_op("pragnosia::aspin_chunk", mutates_args=())
 def aspin_chunk(q: Tensor, k: Tensor, v: Tensor, la: Tensor, S0: Optional[Tensor],
                 want_sent: bool) -> tuple[Tensor, Tensor, Tensor]:
     """Plain-rule chunked scan. q, k, v (B, H, T, 64) (cast to bf16), la (B, H, T) fp32, S0 (B, H, 64, 64) fp32 or
     None. Returns (o bf16, S_final fp32, sent bf16 (B, H, NC, 64, 64), or an empty tensor if not wanted)."""
     _require_gpu(q, k, v, la, S0)
+    _expect_scan("aspin_chunk", q, k, v, la, S0=S0)
     q, k, v, la, S0 = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(S0)
     B, H, T, D = q.shape
     NC = (T + CHUNK - 1) // CHUNK
@@ -260,6 +300,7 @@ def aspin_chunk_windows(q: Tensor, k: Tensor, v: Tensor, la: Tensor, S0: Optiona
     pass. S0 enters the first window. Returns (o bf16, S after the last window fp32 (in its positions), sent bf16
     (B, H, NC, 64, 64) or an empty tensor)."""
     _require_gpu(q, k, v, la, S0, theta)
+    _expect_scan("aspin_chunk_windows", q, k, v, la, S0=S0, theta=theta)
     if window <= 0 or window % CHUNK:
         raise PragnosiaError(f"aspin_chunk_windows: window {window} must be a positive multiple of {CHUNK}")
     q, k, v, la, S0, theta = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(S0), _f32(theta)
@@ -297,8 +338,11 @@ def aspin_chunk_bwd(q: Tensor, k: Tensor, v: Tensor, la: Tensor, sent: Tensor, d
                     dS: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Backward of aspin_chunk. Returns (dq, dk, dv bf16, dla fp32, dS0 fp32)."""
     _require_gpu(q, k, v, la, sent, do, dS)
-    q, k, v, la, sent, do, dS = _bf16(q), _bf16(k), _bf16(v), _f32(la), _bf16(sent), _bf16(do), _f32(dS)
+    _expect_scan("aspin_chunk_bwd", q, k, v, la)
     B, H, T, D = q.shape
+    _expect("aspin_chunk_bwd", q.device, sent=(sent, (B, H, (T + CHUNK - 1) // CHUNK, D, D)), do=(do, (B, H, T, D)),
+            dS=(dS, (B, H, D, D)))
+    q, k, v, la, sent, do, dS = _bf16(q), _bf16(k), _bf16(v), _f32(la), _bf16(sent), _bf16(do), _f32(dS)
     dq, dk, dv = (torch.empty(B, H, T, D, device=q.device, dtype=torch.bfloat16) for _ in range(3))
     dla = torch.empty(B, H, T, device=q.device, dtype=torch.float32)
     dS0 = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
@@ -352,6 +396,7 @@ def aspin_delta(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor, S0: O
     X bf16 (B, H, NC, 64, 64)); W and X are the intermediates the backward reads (not differentiable). Each entering
     state in sent is stored transposed (sent[..., c, j, d] = S_c[d, j]); `.transpose(-1, -2)` gives the states."""
     _require_gpu(q, k, v, la, beta, S0)
+    _expect_scan("aspin_delta", q, k, v, la, beta=beta, S0=S0)
     q, k, v, la, beta, S0 = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(beta), _f32(S0)
     B, H, T, D = q.shape
     NC = (T + CHUNK - 1) // CHUNK
@@ -382,6 +427,11 @@ def aspin_delta_bwd(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor, s
                     do: Tensor, dS: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Backward of aspin_delta. Returns (dq, dk, dv bf16, dla fp32, dbeta fp32, dS0 fp32)."""
     _require_gpu(q, k, v, la, beta, sent, W, X, do, dS)
+    _expect_scan("aspin_delta_bwd", q, k, v, la, beta=beta)
+    B, H, T, D = q.shape
+    NC = (T + CHUNK - 1) // CHUNK
+    _expect("aspin_delta_bwd", q.device, sent=(sent, (B, H, NC, D, D)), W=(W, (B, H, T, D)),
+            X=(X, (B, H, NC, CHUNK, CHUNK)), do=(do, (B, H, T, D)), dS=(dS, (B, H, D, D)))
     q, k, v, la, beta = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(beta)
     sent, W, X, do, dS = _bf16(sent), _bf16(W), _bf16(X), _bf16(do), _f32(dS)
     B, H, T, D = q.shape
@@ -438,12 +488,21 @@ def _proj(t: Tensor) -> Tensor:
     return t.contiguous()
 
 
+def _expect_prep(op: str, qp: Tensor, kp, vp, gate, theta, pos) -> None:
+    """qp, kp, vp (B, T, H, 64); gate (B, T, H); theta (H, 32); pos (T,); all on qp's device."""
+    _expect(op, qp.device, qp=(qp, (None, None, None, 64)))
+    B, T, H, D = qp.shape
+    _expect(op, qp.device, kp=(kp, (B, T, H, D)), vp=(vp, (B, T, H, D)), gate=(gate, (B, T, H)),
+            theta=(theta, (H, D // 2)), pos=(pos, (T,)))
+
+
 @torch.library.custom_op("pragnosia::aspin_prep", mutates_args=())
 def aspin_prep(qp: Tensor, kp: Tensor, vp: Tensor, gate: Optional[Tensor], theta: Tensor,
                pos: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     """qp, kp, vp (B, T, H, 64) fp32 or bf16 projections; gate (B, T, H) logits or None; theta (H, 32); pos (T,)
     int64. Returns bf16 q, k, v in (B, H, T, 64)."""
     _require_gpu(qp, kp, vp, gate, theta, pos)
+    _expect_prep("aspin_prep", qp, kp, vp, gate, theta, pos)
     qp, kp, vp = _proj(qp), _proj(kp).to(qp.dtype), _proj(vp).to(qp.dtype)
     gate, theta, pos = _f32(gate), _f32(theta), pos.to(torch.int64).contiguous()
     B, T, H, D = qp.shape
@@ -465,6 +524,9 @@ def aspin_prep_bwd(qp: Tensor, kp: Tensor, vp: Tensor, gate: Optional[Tensor], t
                    dq: Tensor, dk: Tensor, dv: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Returns (dqp, dkp, dvp in the projections' dtype, dgate fp32 (B, T, H) or empty, dtheta fp32 (H, 32))."""
     _require_gpu(qp, kp, vp, gate, theta, pos, dq, dk, dv)
+    _expect_prep("aspin_prep_bwd", qp, kp, vp, gate, theta, pos)
+    B, T, H, D = qp.shape
+    _expect("aspin_prep_bwd", qp.device, dq=(dq, (B, H, T, D)), dk=(dk, (B, H, T, D)), dv=(dv, (B, H, T, D)))
     qp, kp, vp = _proj(qp), _proj(kp).to(qp.dtype), _proj(vp).to(qp.dtype)
     gate, theta, pos = _f32(gate), _f32(theta), pos.to(torch.int64).contiguous()
     dq, dk, dv = _bf16(dq), _bf16(dk), _bf16(dv)
@@ -515,6 +577,19 @@ def _proj_cols(H: int, gated: bool, has_beta: bool) -> tuple[int, int, int]:
     return base, (base + H if gated else -1), (base + H if has_beta else -1)
 
 
+def _expect_proj(op: str, P: Tensor, H: int, gated: bool, la_bias, A, la_floor, gate_bias, beta_bias, theta,
+                 pos=None) -> None:
+    """P (B, T, W) (or (B, W) for the decode step) with W at least the columns the kernels read; the per-head
+    vectors (H,); theta (H, 32); pos (T,); all on P's device."""
+    if H <= 0 or P.dim() not in (2, 3) or P.shape[-1] < 3 * H * 64 + (2 if gated else 1) * H:
+        raise PragnosiaError(f"{op}: P has shape {tuple(P.shape)}, expected (B, [T,] >= {3 * H * 64 + H}) columns "
+                             f"for {H} heads")
+    _expect(op, P.device, la_bias=(la_bias, (H,)), A=(A, (H,)), la_floor=(la_floor, (H,)),
+            gate_bias=(gate_bias, (H,)), beta_bias=(beta_bias, (H,)), theta=(theta, (H, 32)))
+    if pos is not None:
+        _expect(op, P.device, pos=(pos, (P.shape[1] if P.dim() == 3 else None,)))
+
+
 @torch.library.custom_op("pragnosia::aspin_prep_proj", mutates_args=())
 def aspin_prep_proj(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Optional[Tensor],
                     gate_bias: Optional[Tensor], beta_bias: Optional[Tensor], beta_min: float, gated: bool,
@@ -526,6 +601,9 @@ def aspin_prep_proj(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Opt
     -softplus(logit + la_bias) exp(A) (floored at la_floor when given) and beta (B, H, T) fp32 =
     max(sigmoid(logit + beta_bias), beta_min) for the delta rule (else an empty tensor)."""
     _require_gpu(P, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos)
+    _expect_proj("aspin_prep_proj", P, H, gated, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos)
+    if P.dim() != 3:
+        raise PragnosiaError(f"aspin_prep_proj: P must be (B, T, W), got {tuple(P.shape)}")
     P = _proj(P)
     la_bias, A, la_floor, theta = _f32(la_bias), _f32(A), _f32(la_floor), _f32(theta)
     gate_bias, beta_bias = _f32(gate_bias), _f32(beta_bias)
@@ -564,6 +642,12 @@ def aspin_prep_proj_bwd(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor:
     """Backward of aspin_prep_proj. Returns (dP in P's dtype and layout, d la_bias, dA, d gate_bias or d beta_bias
     (the one in use; empty when neither), dtheta), the per-head sums reduced from the kernel's partials."""
     _require_gpu(P, dq, dk, dv, dla, dbeta)
+    _expect_proj("aspin_prep_proj_bwd", P, H, gated, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos)
+    if P.dim() != 3:
+        raise PragnosiaError(f"aspin_prep_proj_bwd: P must be (B, T, W), got {tuple(P.shape)}")
+    _expect("aspin_prep_proj_bwd", P.device, dq=(dq, (P.shape[0], H, P.shape[1], 64)),
+            dk=(dk, (P.shape[0], H, P.shape[1], 64)), dv=(dv, (P.shape[0], H, P.shape[1], 64)),
+            dla=(dla, (P.shape[0], H, P.shape[1])), dbeta=(dbeta, (P.shape[0], H, P.shape[1])))
     P = _proj(P)
     la_bias, A, la_floor, theta = _f32(la_bias), _f32(A), _f32(la_floor), _f32(theta)
     gate_bias, beta_bias = _f32(gate_bias), _f32(beta_bias)
@@ -633,6 +717,8 @@ def aspin_rebase(S: Tensor, theta: Tensor, p0_dev: Optional[Tensor], p0: float) 
     """Key rows (2i, 2i+1) of S (B, H, 64, 64) rotated by -p0 * theta[h, i]; p0 from the device scalar p0_dev when
     given, else the float p0."""
     _require_gpu(S, theta, p0_dev)
+    _expect("aspin_rebase", S.device, S=(S, (None, None, 64, 64)))
+    _expect("aspin_rebase", S.device, theta=(theta, (S.shape[1], 32)), p0_dev=(p0_dev, ()))
     S, theta, p0_dev = _f32(S), _f32(theta), _f32(p0_dev)
     B, H, D, _ = S.shape
     out = torch.empty_like(S)
@@ -650,6 +736,8 @@ def _(S, theta, p0_dev, p0):
 def aspin_rebase_bwd(S: Tensor, theta: Tensor, p0_dev: Optional[Tensor], p0: float,
                      g: Tensor) -> tuple[Tensor, Tensor]:
     _require_gpu(S, theta, p0_dev, g)
+    _expect("aspin_rebase_bwd", S.device, S=(S, (None, None, 64, 64)))
+    _expect("aspin_rebase_bwd", S.device, theta=(theta, (S.shape[1], 32)), p0_dev=(p0_dev, ()), g=(g, tuple(S.shape)))
     S, theta, p0_dev, g = _f32(S), _f32(theta), _f32(p0_dev), _f32(g)
     B, H, D, _ = S.shape
     dS = torch.empty_like(S)
@@ -691,6 +779,11 @@ def aspin_decode_step(S: Tensor, qp: Tensor, kp: Tensor, vp: Tensor, gate: Optio
     logits (plain rule) or None; la (B, H) log-decay; beta (B, H) write strength (delta rule) or None; theta (H, 32).
     Returns (S_new fp32, o (B, H, 64) fp32). Not differentiable (decode runs without autograd)."""
     _require_gpu(S, qp, kp, vp, gate, la, beta, theta, p0_dev)
+    _expect("aspin_decode_step", S.device, S=(S, (None, None, 64, 64)))
+    B_, H_ = S.shape[0], S.shape[1]
+    _expect("aspin_decode_step", S.device, qp=(qp, (B_, H_, 64)), kp=(kp, (B_, H_, 64)), vp=(vp, (B_, H_, 64)),
+            gate=(gate, (B_, H_)), la=(la, (B_, H_)), beta=(beta, (B_, H_)), theta=(theta, (H_, 32)),
+            p0_dev=(p0_dev, ()))
     S, qp, kp, vp, gate = _f32(S), _f32(qp), _f32(kp), _f32(vp), _f32(gate)
     la, beta, theta, p0_dev = _f32(la), _f32(beta), _f32(theta), _f32(p0_dev)
     B, H, D, _ = S.shape
@@ -716,6 +809,11 @@ def decode_gemv(x: Tensor, W: Tensor, ln_weight: Optional[Tensor], ln_bias: Opti
     """y (B, N) = act(scale * (W LayerNorm(x)) + bias) + resid for x (B, K), W (N, K), all fp32; LayerNorm only when
     ln_weight is given; act 0 identity, 1 GELU (erf form); scale a device scalar. Not differentiable."""
     _require_gpu(x, W, ln_weight, ln_bias, bias, scale, resid)
+    if x.dim() != 2 or W.dim() != 2 or W.shape[1] != x.shape[1]:
+        raise PragnosiaError(f"decode_gemv: x {tuple(x.shape)} and W {tuple(W.shape)} must be (B, K) and (N, K)")
+    B_, K_, N_ = x.shape[0], x.shape[1], W.shape[0]
+    _expect("decode_gemv", x.device, W=(W, (N_, K_)), ln_weight=(ln_weight, (K_,)), ln_bias=(ln_bias, (K_,)),
+            bias=(bias, (N_,)), scale=(scale, ()), resid=(resid, (B_, N_)))
     x, W = _f32(x), _f32(W)
     ln_weight, ln_bias, bias, scale, resid = _f32(ln_weight), _f32(ln_bias), _f32(bias), _f32(scale), _f32(resid)
     B, K = x.shape
@@ -743,6 +841,11 @@ def aspin_decode_proj_(S: Tensor, P: Tensor, H: int, la_bias: Tensor, A: Tensor,
     _require_gpu(S, P, la_bias, A, theta, on_weight)
     if not (S.is_contiguous() and S.dtype == torch.float32):
         raise PragnosiaError("aspin_decode_proj_: the state must be a contiguous fp32 tensor (it is updated in place)")
+    if P.dim() != 2:
+        raise PragnosiaError(f"aspin_decode_proj_: P must be (B, W), got {tuple(P.shape)}")
+    _expect_proj("aspin_decode_proj_", P, H, gated, la_bias, A, la_floor, gate_bias, beta_bias, theta)
+    _expect("aspin_decode_proj_", P.device, S=(S, (P.shape[0], H, 64, 64)), p0_dev=(p0_dev, ()),
+            on_weight=(on_weight, (64,)))
     P, la_bias, A, la_floor, theta = _f32(P), _f32(la_bias), _f32(A), _f32(la_floor), _f32(theta)
     gate_bias, beta_bias, p0_dev, on_weight = _f32(gate_bias), _f32(beta_bias), _f32(p0_dev), _f32(on_weight)
     B, np_ = P.shape

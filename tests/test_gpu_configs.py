@@ -57,11 +57,62 @@ def test_cfg3_carried_windows_equal_unsplit_pass():
     assert torch.isfinite(S).all()
 
 
-def test_cfg4_decode_matches_oracle():
+def test_cfg3_one_pass_windows_full_size():
+    """configs[3] through the path `LM.forward_carried` and bench.py time: `aspin_chunk_windows`, the 16 windows of
+    512 carried in ONE segment-parallel pass (state rebased by -512 theta at every window boundary inside the
+    kernels). Against (i) the window-by-window loop on the GPU (aspin_chunk + aspin_rebase per window) and (ii) the
+    CPU oracle's window loop (`oracle.aspin.assoc_scan` per window, `oracle.aspin.rebase` between), outputs and the
+    final state, on the same bf16 inputs."""
+    from pragnosia_amd import ops  # noqa: F401
+    from pragnosia_amd.assoc import rotate
+    B, H, T, D, W = 2, 12, 8192, 64, 512
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(B, H, T, D, generator=g)
+    k = F.normalize(torch.randn(B, H, T, D, generator=g), dim=-1)
+    v = torch.randn(B, H, T, D, generator=g)
+    la = F.logsigmoid(torch.randn(B, H, T, generator=g) + 4.0)
+    th = torch.rand(H, D // 2, generator=g) * 0.1
+    op = torch.ops.pragnosia
+    qd, kd, vd, lad, thd = (t.cuda() for t in (q, k, v, la, th))
+    loc = torch.arange(T, device="cuda") % W
+    qw, kw, vb = rotate(qd, thd, loc).bfloat16(), rotate(kd, thd, loc).bfloat16(), vd.bfloat16()
+    with torch.no_grad():
+        o1, S1, _ = op.aspin_chunk_windows(qw, kw, vb, lad, None, thd, W, False)
+        S, outs = None, []
+        for s in range(0, T, W):
+            if S is not None:
+                S = op.aspin_rebase(S, thd, None, float(W))
+            o, S, _ = op.aspin_chunk(qw[:, :, s:s + W], kw[:, :, s:s + W], vb[:, :, s:s + W], lad[:, :, s:s + W],
+                                     S, False)
+            outs.append(o)
+        oloop = torch.cat(outs, 2)
+    torch.cuda.synchronize()
+    assert rel(o1, oloop) < TOL and rel(S1, S) < TOL
+    qc, kc, vc = qw.float().cpu(), kw.float().cpu(), vb.float().cpu()
+    Sr, outs = None, []
+    for s in range(0, T, W):
+        if Sr is not None:
+            Sr = OA.rebase(Sr, th, float(W))
+        o, Sr = OA.assoc_scan(qc[:, :, s:s + W], kc[:, :, s:s + W], vc[:, :, s:s + W], la[:, :, s:s + W], Sr, chunk=64)
+        outs.append(o)
+    o_r = torch.cat(outs, 2)
+    assert rel(o1, o_r) < TOL and rel(S1, Sr) < TOL
+    print(f"cfg3 one pass vs loop {rel(o1, oloop):.2e}, vs oracle out {rel(o1, o_r):.2e} state {rel(S1, Sr):.2e}")
+
+
+@pytest.mark.parametrize("batch", [1, 64])
+def test_cfg4_decode_matches_oracle(batch):
     """LM(vocab 8192, d 768, 12 layers, 12 heads of 64, ctx 512, aspin), weights N(0, 0.02), a 512-token
-    prefill then greedy decode through the captured graph. The graphed tokens equal the eager loop's, and the
-    eager loop's logits equal the fp32 oracle's teacher-forced decode on the same tokens."""
-    from pragnosia_amd.decode import GreedyDecoder, greedy_eager
+    prefill then 520 greedy steps through the captured graph, at batch 1 (the GEMV dense layers) and batch 64 (torch
+    GEMM dense layers around the fused carrier step, the branch above GEMV_MAX_BATCH). The prefill fills one window,
+    so the first step starts a new window with every state rebased by 512, and the position index wraps mod 512 at
+    step 512: both happen inside the run.
+    (i) The eager loop teacher-forced with the graphed tokens gives logits whose argmax is the graphed token at every
+    step whose top-2 logit gap exceeds 1e-4 (closer calls may flip on fp32 rounding between the two step
+    implementations; at most 0.5% of them are allowed to be such near-ties).
+    (ii) Those eager logits equal the CPU oracle's teacher-forced decode (`oracle.modules.greedy_decode`, pinned
+    against forward_carried across window boundaries and the wrap) at every step, for sequences 0 and batch - 1."""
+    from pragnosia_amd.decode import GEMV_MAX_BATCH, GreedyDecoder, greedy_eager
     from pragnosia_amd.model import LM
     torch.manual_seed(4)
     m = LM(vocab=8192, d=768, layers=12, mlp_mult=4, ctx=512, mixer="aspin")
@@ -69,11 +120,19 @@ def test_cfg4_decode_matches_oracle():
     sd = {k_: v_.detach().clone() for k_, v_ in m.state_dict().items()}
     m = m.cuda().eval()
     g = torch.Generator().manual_seed(4)
-    prompt = torch.randint(0, 8192, (1, 512), generator=g)
-    n = 6
-    dec = GreedyDecoder(m, 1, steps_per_graph=4)
+    prompt = torch.randint(0, 8192, (batch, 512), generator=g)
+    n = 520
+    dec = GreedyDecoder(m, batch, steps_per_graph=8)
+    assert dec.fused and (batch > GEMV_MAX_BATCH) == (batch == 64)
     toks_g = dec.generate(prompt.cuda(), n)
-    toks_e, lgs_e = greedy_eager(m, prompt.cuda(), n)
-    assert torch.equal(toks_g.cpu(), toks_e.cpu())
-    _, lgs_r = M.greedy_decode(sd, prompt, n, layers=12, mixer="aspin", heads=12, forced=toks_e.cpu())
-    assert rel(lgs_e, lgs_r) < TOL
+    _, lgs_e = greedy_eager(m, prompt.cuda(), n, forced=toks_g)
+    top2 = lgs_e.topk(2, dim=-1).values
+    decided = (top2[..., 0] - top2[..., 1]) > 1e-4
+    agree = lgs_e.argmax(-1) == toks_g
+    assert bool(agree[decided].all()), int((~agree & decided).sum())
+    assert float(decided.float().mean()) > 0.995
+    rows = [0] if batch == 1 else [0, batch - 1]
+    _, lgs_r = M.greedy_decode(sd, prompt[rows], n, layers=12, mixer="aspin", heads=12, forced=toks_g[rows].cpu())
+    err = rel(lgs_e[rows], lgs_r)
+    print(f"cfg4 batch {batch}: {n} steps, near-ties {int((~decided).sum())}, logits vs oracle {err:.2e}")
+    assert err < TOL

@@ -127,3 +127,20 @@ def test_large_angles(scan):
     assert rel(y32, y64) < TOL
     for mine, ref in zip(a32, a64):
         assert rel(mine.grad, ref.grad) < TOL
+
+
+def test_empty_sequence_returns_h0_and_passes_its_gradient(scan):
+    """T = 0: the final state is the initial one (zero without h0), as the reference's scan returns it, and the
+    gradient on the final state is the gradient on h0."""
+    B, D = 3, 40
+    g = torch.Generator().manual_seed(11)
+    h0r, h0i = (torch.randn(B, D, generator=g).cuda().requires_grad_(True) for _ in range(2))
+    u, lm, an = (torch.zeros(B, 0, D, device="cuda", requires_grad=True) for _ in range(3))
+    y, (hr, hi) = scan(u, lm, an, (h0r, h0i))
+    assert y.shape == (B, 0, D) and torch.equal(hr, h0r) and torch.equal(hi, h0i)
+    wr, wi = (torch.randn(B, D, generator=g).cuda() for _ in range(2))
+    ((hr * wr).sum() + (hi * wi).sum()).backward()
+    assert torch.equal(h0r.grad, wr) and torch.equal(h0i.grad, wi)
+    with torch.no_grad():
+        _, (zr, zi) = scan(u, lm, an)
+    assert not zr.any() and not zi.any()

@@ -155,3 +155,54 @@ def test_greedy_decode_logits_equal_one_pass_forward(mixer):
     # teacher forcing with the greedy tokens reproduces the greedy run
     toks2, lgs2 = M.greedy_decode(sd, prompt, 6, layers=2, mixer=mixer, heads=2, forced=toks)
     assert torch.equal(toks, toks2) and (lgs - lgs2).abs().max() == 0
+
+
+@pytest.mark.parametrize("mixer", ["aspin", "dspin", "fspin"])
+@pytest.mark.parametrize("plen", [8, 13])
+def test_greedy_decode_across_windows_and_position_wrap(mixer, plen):
+    """The regime of configs[4] (a prefill of exactly ctx tokens, then many more steps than ctx): each decode step's
+    logits equal `lm_forward_carried` of the prompt plus the tokens so far, in windows of ctx (`src/model.py:
+    842-864`), itself pinned against the reference's own forward_carried by the golden fixtures. A prompt of exactly
+    ctx (8) and one that is not a multiple of it (13), and 20 steps, so the decode crosses two window boundaries and
+    the position table wraps mid-decode. The two sides share no code path for the decode bookkeeping: greedy_decode
+    carries T = 1 calls with the state rebased by 1 and the position index (P + i) mod ctx (`src/bench.py:203-236`,
+    `:281-288`), forward_carried restarts positions per window and rebases by the window's length. A wrong wrap, a
+    rebase by the wrong length or a state not carried past the boundary moves the logits by 1e-3 or more."""
+    ctx, n = 8, 20
+    g = torch.Generator().manual_seed(7)
+    sd = lm_sd(50, 16, 2, ctx, mixer, 2, g)
+    prompt = torch.randint(0, 50, (2, plen), generator=g)
+    toks, lgs = M.greedy_decode(sd, prompt, n, layers=2, mixer=mixer, heads=2)
+    assert (plen + n) // ctx >= 2
+    for i in range(n):
+        seq = torch.cat([prompt, toks[:, :i]], 1)
+        ref = M.lm_forward_carried(sd, seq, ctx, layers=2, mixer=mixer, heads=2)[:, -1]
+        assert (lgs[:, i] - ref).abs().max() < 1e-9, (i, (lgs[:, i] - ref).abs().max())
+
+
+def test_greedy_decode_pin_is_observable(monkeypatch):
+    """The pin above can fail: planted in the oracle's decode, a position index off by one (the table rolled) or a
+    carrier that skips the rebase of its state on T = 1 calls each move the logits, after the first step, by far more
+    than the 1e-9 tolerance."""
+    ctx = 8
+    g = torch.Generator().manual_seed(8)
+    sd = lm_sd(50, 16, 2, ctx, "aspin", 2, g)
+    prompt = torch.randint(0, 50, (1, ctx), generator=g)
+    toks, lgs = M.greedy_decode(sd, prompt, 12, layers=2, mixer="aspin", heads=2)
+    ref = torch.stack([M.lm_forward_carried(sd, torch.cat([prompt, toks[:, :i]], 1), ctx, layers=2, mixer="aspin",
+                                            heads=2)[:, -1] for i in range(12)], 1)
+    assert (lgs - ref).abs().max() < 1e-9
+    sd_bad = dict(sd)
+    sd_bad["p.weight"] = torch.roll(sd["p.weight"], 1, 0)
+    _, lgs_bad = M.greedy_decode(sd_bad, prompt, 12, layers=2, mixer="aspin", heads=2, forced=toks)
+    assert (lgs_bad[:, 1:] - ref[:, 1:]).abs().max() > 1e-3
+    real = M.assoc_carrier
+
+    def no_rebase(sd_, x, h0=None, pos0=0, **kw):
+        if h0 is not None and x.shape[1] == 1:
+            h0 = (h0[0], 0)
+        return real(sd_, x, h0, pos0, **kw)
+
+    monkeypatch.setattr(M, "assoc_carrier", no_rebase)
+    _, lgs_bad = M.greedy_decode(sd, prompt, 12, layers=2, mixer="aspin", heads=2, forced=toks)
+    assert (lgs_bad[:, 1:] - ref[:, 1:]).abs().max() > 1e-3
