@@ -19,8 +19,12 @@ extern "C" {
 #define PRAGNOSIA_OK 0
 #define PRAGNOSIA_ERR_INVALID_ARGUMENT (-1)
 #define PRAGNOSIA_ERR_UNSUPPORTED (-2)
+#define PRAGNOSIA_ERR_TOO_LARGE (-3)
 
-/* ABI version of this header (8); bumped on any signature change. */
+/* Bytes of device scratch the allocation-free entry point pragnosia_aspin_chunk_fwd_seg_noalloc holds per GPU. */
+#define PRAGNOSIA_SEG_SCRATCH_BYTES (32u << 20)
+
+/* ABI version of this header (9); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -93,6 +97,21 @@ int pragnosia_aspin_chunk_fwd_seg(const void* q, const void* k, const void* v, c
                                   const float* theta, int64_t window, void* o, float* S_final, void* sent,
                                   void* workspace, int64_t workspace_bytes, int64_t B, int64_t H, int64_t T,
                                   int64_t D, int64_t chunk, int64_t seg_chunks, void* stream);
+
+/* pragnosia_aspin_chunk_fwd_seg without a workspace argument: the same kernels and the same results, their workspace
+ * taken from a fixed array of PRAGNOSIA_SEG_SCRATCH_BYTES of device memory that the library holds on every GPU it
+ * runs on until the process ends. It allocates nothing (no hipMalloc, no hipFree, no allocating library call) and
+ * writes no memset, so it suits callers that cannot allocate: code under HIP graph capture, serving loops that
+ * prefill long contexts, harnesses that forbid allocation. Returns PRAGNOSIA_ERR_TOO_LARGE when the shape needs more
+ * than the array holds (pragnosia_aspin_chunk_seg_workspace_bytes(...) > PRAGNOSIA_SEG_SCRATCH_BYTES; e.g. B2 H12
+ * T8192 in segments of 8 chunks needs 6 MiB). Every call on one GPU shares that GPU's array: calls that overlap in
+ * time on one GPU (concurrent streams, or threads) race and must be serialised by the caller. Nothing in the array
+ * needs to start at zero (every byte read is written first by the same call).
+ * This entry point has no counterpart in the reference; it exists for the callers above. */
+int pragnosia_aspin_chunk_fwd_seg_noalloc(const void* q, const void* k, const void* v, const float* la,
+                                          const float* S0, const float* theta, int64_t window, void* o,
+                                          float* S_final, void* sent, int64_t B, int64_t H, int64_t T, int64_t D,
+                                          int64_t chunk, int64_t seg_chunks, void* stream);
 
 /* The backward of pragnosia_aspin_chunk_bwd, segment-parallel (segments of `seg_chunks` chunks: per-segment sums of
  * q and dO, a reverse prefix over segments for the state gradient entering each segment from later ones, then the

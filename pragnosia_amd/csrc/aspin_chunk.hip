@@ -936,20 +936,23 @@ extern "C" int64_t pragnosia_aspin_chunk_seg_workspace_bytes(int64_t B, int64_t 
   return seg_workspace_bytes(B, H, T, seg_chunks);
 }
 
-extern "C" int pragnosia_aspin_chunk_fwd_seg(const void* q, const void* k, const void* v, const float* la,
-                                             const float* S0, const float* theta, int64_t window, void* o,
-                                             float* S_final, void* sent, void* workspace, int64_t workspace_bytes,
-                                             int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk,
-                                             int64_t seg_chunks, void* stream) {
-  if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
-  PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
-  PGN_CHECK_ARG(q && k && v && la && o && S_final && workspace);
-  PGN_CHECK_ARG(seg_chunks >= 1 && seg_chunks < ((int64_t)1 << 28));
-  PGN_CHECK_ARG(window >= 0);
-  if (window > 0) PGN_CHECK_ARG(theta && window % C == 0 && (window / C) % seg_chunks == 0);
-  PGN_CHECK_ARG(workspace_bytes >= seg_workspace_bytes(B, H, T, seg_chunks));
+namespace {
+
+// Host-side checks of the segmented forward's arguments other than its workspace.
+bool fwd_seg_args_ok(const void* q, const void* k, const void* v, const float* la, const float* theta,
+                     int64_t window, void* o, float* S_final, int64_t B, int64_t H, int64_t T, int64_t D,
+                     int64_t chunk, int64_t seg_chunks) {
+  if (!shape_ok(B, H, T, D, chunk) || !(q && k && v && la && o && S_final)) return false;
+  if (seg_chunks < 1 || seg_chunks >= ((int64_t)1 << 28) || window < 0) return false;
+  if (window > 0 && !(theta && window % C == 0 && (window / C) % seg_chunks == 0)) return false;
+  return B * H * seg_count(T, seg_chunks) < ((int64_t)1 << 31);
+}
+
+// The segmented forward's three launches on a workspace of at least seg_workspace_bytes(...) bytes.
+int launch_fwd_seg(const void* q, const void* k, const void* v, const float* la, const float* S0, const float* theta,
+                   int64_t window, void* o, float* S_final, void* sent, void* workspace, int64_t B, int64_t H,
+                   int64_t T, int64_t seg_chunks, void* stream) {
   const int64_t nseg = seg_count(T, seg_chunks);
-  PGN_CHECK_ARG(B * H * nseg < ((int64_t)1 << 31));
   {
     const hipError_t e = pgn_lds_limit((const void*)aspin_plain_fwd, kFwdSmem);
     if (e != hipSuccess) return (int)e;
@@ -967,6 +970,63 @@ extern "C" int pragnosia_aspin_chunk_fwd_seg(const void* q, const void* k, const
                      (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, E, (__bf16*)o, nullptr,
                      (__bf16*)sent, (int)T, NC, (int)seg_chunks);
   PGN_RETURN_LAUNCH();
+}
+
+}  // namespace
+
+extern "C" int pragnosia_aspin_chunk_fwd_seg(const void* q, const void* k, const void* v, const float* la,
+                                             const float* S0, const float* theta, int64_t window, void* o,
+                                             float* S_final, void* sent, void* workspace, int64_t workspace_bytes,
+                                             int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk,
+                                             int64_t seg_chunks, void* stream) {
+  if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(fwd_seg_args_ok(q, k, v, la, theta, window, o, S_final, B, H, T, D, chunk, seg_chunks));
+  PGN_CHECK_ARG(workspace && workspace_bytes >= seg_workspace_bytes(B, H, T, seg_chunks));
+  return launch_fwd_seg(q, k, v, la, S0, theta, window, o, S_final, sent, workspace, B, H, T, seg_chunks, stream);
+}
+
+// The allocation-free variant's workspace: one array per GPU, in the library's own device memory, held until the
+// process ends. Host code never passes the array's name to a kernel (on the host it is only a stand-in for the
+// symbol); the device address comes from hipGetSymbolAddress, once per device with that device current.
+static __device__ __align__(256) unsigned char scratch[PRAGNOSIA_SEG_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};  // device address of `scratch` per device ordinal
+
+// The current device's address of `scratch`, looked up on the first call on that device.
+hipError_t scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int pragnosia_aspin_chunk_fwd_seg_noalloc(const void* q, const void* k, const void* v, const float* la,
+                                                     const float* S0, const float* theta, int64_t window, void* o,
+                                                     float* S_final, void* sent, int64_t B, int64_t H, int64_t T,
+                                                     int64_t D, int64_t chunk, int64_t seg_chunks, void* stream) {
+  if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(fwd_seg_args_ok(q, k, v, la, theta, window, o, S_final, B, H, T, D, chunk, seg_chunks));
+  if (seg_workspace_bytes(B, H, T, seg_chunks) > (int64_t)PRAGNOSIA_SEG_SCRATCH_BYTES) return PRAGNOSIA_ERR_TOO_LARGE;
+  void* ws = nullptr;
+  const hipError_t e = scratch_address(&ws);
+  if (e != hipSuccess) return (int)e;
+  // every byte the launches read from the workspace is written by them first (each segment's full sum and decay,
+  // then its entering state), so nothing left by an earlier call needs clearing
+  return launch_fwd_seg(q, k, v, la, S0, theta, window, o, S_final, sent, ws, B, H, T, seg_chunks, stream);
 }
 
 extern "C" int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const void* v, const float* la,

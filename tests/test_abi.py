@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 8
+    assert L.pragnosia_abi_version() == 9
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 
@@ -87,3 +87,15 @@ def test_product_never_imports_oracle():
             if f.endswith(".py"):
                 src = open(os.path.join(dp, f)).read()
                 assert not re.search(r"^\s*(from|import)\s+oracle\b", src, flags=re.M), f
+
+
+def test_noalloc_limit_checked_on_host(L):
+    """The allocation-free windowed forward refuses, on the host, a shape whose workspace exceeds the fixed scratch
+    array (PRAGNOSIA_ERR_TOO_LARGE), and takes the other argument checks of the workspace entry point."""
+    null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    assert L.pragnosia_aspin_chunk_seg_workspace_bytes(64, 64, 65536, 64, 64, 4) > 32 << 20
+    args = lambda B, H, T, win, sc, th: (one, one, one, one, null, th, win, one, one, null, B, H, T, 64, 64, sc, null)
+    assert L.pragnosia_aspin_chunk_fwd_seg_noalloc(*args(64, 64, 65536, 0, 4, null)) == -3
+    assert L.pragnosia_aspin_chunk_fwd_seg_noalloc(*args(1, 1, 1000, 0, 0, null)) == -1      # empty segments
+    assert L.pragnosia_aspin_chunk_fwd_seg_noalloc(*args(1, 1, 1000, 192, 3, null)) == -1    # window without theta
+    assert L.pragnosia_error_string(-3).startswith(b"shape needs more scratch")
