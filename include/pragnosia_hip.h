@@ -24,6 +24,13 @@ extern "C" {
 /* Bytes of device scratch the allocation-free entry point pragnosia_aspin_chunk_fwd_seg_noalloc holds per GPU. */
 #define PRAGNOSIA_SEG_SCRATCH_BYTES (32u << 20)
 
+/* Operand types of the exact (fp32 / fp64) scan. */
+#define PRAGNOSIA_F32 0
+#define PRAGNOSIA_F64 1
+
+/* Tokens per checkpointed state of the exact scan's forward. */
+#define PRAGNOSIA_EXACT_CKPT_TOKENS 8
+
 /* ABI version of this header (9); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
@@ -139,6 +146,30 @@ int64_t pragnosia_aspin_out_weight_partials(int64_t B, int64_t H, int64_t T);
  * rows of D fp32; the weight gradient is their sum over rows). Replaces the autograd backward of the same lines. */
 int pragnosia_aspin_out_bwd(const void* gy, int gy_bf16, const void* o, const float* weight, const float* rstd,
                             void* dO, float* dw_partials, int64_t B, int64_t H, int64_t T, int64_t D, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Associative carrier scan with fp32 or fp64 operands (no bf16 rounding), plain rule (beta NULL) or delta rule,
+ * per (batch, head), any head dims 1 <= Dk, Dv <= 128:
+ *     plain: S_t = a_t S_{t-1} + k_t v_t^T;   delta: S_t = P + beta_t k_t (v_t - P^T k_t)^T, P = a_t S_{t-1};
+ *     o_t = S_t^T q_t,   a_t = exp(la_t),   S_{-1} = S0 (zero when NULL).
+ * Every tensor has the operand type `dtype` (PRAGNOSIA_F32 or PRAGNOSIA_F64): q, k (B, H, T, Dk); v (B, H, T, Dv);
+ * la, beta (B, H, T); S0, S_final (B, H, Dk, Dv) keys on dim 2; o (B, H, T, Dv). For a backward the forward also
+ * writes ckpt, the state entering every block of PRAGNOSIA_EXACT_CKPT_TOKENS tokens, (B, H, ceil(T / 8), Dk, Dv),
+ * and with the delta rule resid, the residuals v_t - P^T k_t, (B, H, T, Dv) (both NULL when no backward follows).
+ * Replaces `assoc_scan` of src/assoc.py:254-269 (fp32, or fp64 for fp64 inputs: `_scan_twopass`,
+ * `_scan_twopass_delta`, src/assoc.py:118-165, :207-251) and its autograd backward. */
+int pragnosia_aspin_exact_fwd(const void* q, const void* k, const void* v, const void* la, const void* beta,
+                              const void* S0, void* o, void* S_final, void* ckpt, void* resid, int64_t B, int64_t H,
+                              int64_t T, int64_t Dk, int64_t Dv, int dtype, void* stream);
+
+/* Backward of pragnosia_aspin_exact_fwd from dO (B, H, T, Dv) and dS_final (or NULL = zero), with the forward's ckpt
+ * and resid: writes dq, dk (B, H, T, Dk), dv (B, H, T, Dv), dla (B, H, T), dbeta (B, H, T; delta rule) and, if
+ * non-NULL, dS0 (B, H, Dk, Dv), all of type `dtype`. PRAGNOSIA_ERR_UNSUPPORTED when fp64 with both Dk and Dv above
+ * 64 (its block buffers exceed the LDS). */
+int pragnosia_aspin_exact_bwd(const void* q, const void* k, const void* v, const void* la, const void* beta,
+                              const void* ckpt, const void* resid, const void* dO, const void* dS_final, void* dq,
+                              void* dk, void* dv, void* dla, void* dbeta, void* dS0, int64_t B, int64_t H, int64_t T,
+                              int64_t Dk, int64_t Dv, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Associative carrier, DELTA write rule, chunked scan (chunk = 64, head dim D = 64), per (batch, head):

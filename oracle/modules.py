@@ -11,8 +11,9 @@ modules by the golden fixtures in tests/golden/modules.npz (the reference's CPU 
 SpinCarrier(rf), LM forward and forward_carried with the aspin and fspin mixers, fp32, seeded parameters; checked in
 tests/test_golden_modules.py to 1e-4), and by invariants in tests/test_oracle_modules.py: causality, carried windows
 == one pass (across a position restart through the rebase), token-at-a-time decode == one pass, forward_carried's
-last window == the same window after a carried prefix. `greedy_decode` composes `lm_forward` calls; it is pinned by
-those invariants only.
+last window == the same window after a carried prefix. `greedy_decode` is pinned against `lm_forward_carried` at
+every step across window boundaries and the position wrap. `short_conv`: identity initialisation == no convolution,
+carried cache == one pass, and a single tap equals the input shifted by that many tokens.
 """
 from __future__ import annotations
 
@@ -39,27 +40,44 @@ def _rms(x, weight, eps=torch.finfo(torch.float32).eps):
     return F.rms_norm(x, (x.shape[-1],), weight, eps)
 
 
+def short_conv(sconv, qo, ko, vo, cc):
+    """The carrier's causal depthwise convolution on q, k, v (B, T, d each) over the last K tokens
+    (`src/assoc.py:374-382`): weight sconv (3 d, K), the current token on the last tap; cc the previous call's last
+    K - 1 inputs (B, 3 d, K - 1) or None (zeros) at a sequence start. Returns q, k, v and the new cache."""
+    D, K = qo.shape[-1], sconv.shape[1]
+    x = torch.cat([qo, ko, vo], dim=-1).transpose(1, 2)
+    pad = cc.to(x.dtype) if cc is not None else x.new_zeros(x.shape[0], 3 * D, K - 1)
+    xp = torch.cat([pad, x], dim=-1)
+    y = F.conv1d(xp, sconv.to(x.dtype).unsqueeze(1), groups=3 * D).transpose(1, 2)
+    return y[..., :D], y[..., D:2 * D], y[..., 2 * D:], xp[..., -(K - 1):]
+
+
 def assoc_carrier(sd, x, h0=None, pos0=0, *, heads, delta=False, write_all=False, key_topk=0, la_floor=None,
                   chunk=64, pos_wrap=None):
-    """AssocCarrier.forward, torch path (`src/assoc.py:384-512`, kernel=False, no fused projections, no short
-    convolution). h0 = (S, p0) or None. Returns (out, (S, p0 + T))."""
+    """AssocCarrier.forward, torch path (`src/assoc.py:384-512`, kernel=False, no fused projections), with the short
+    convolution when sd holds "sconv". h0 = (S, p0), (S, p0, cache) with the convolution, or None. Returns
+    (out, (S, T)) or (out, (S, T, cache))."""
     B, T, D = x.shape
     H = heads
     dk = D // H
     z = _ln(x, sd, "ln")
     S0, p0 = (None, pos0) if h0 is None else (h0[0], h0[1])
+    cc = h0[2] if (h0 is not None and len(h0) == 3) else None
     theta = sd["theta"]
     if S0 is not None and float(p0) != 0.0:
         S0 = A_.rebase(S0.to(x.dtype), theta.to(x.dtype), float(p0))
     pos = torch.arange(T)
     if pos_wrap:
         pos = pos % pos_wrap
-    kp = _lin(z, sd, "k").reshape(B, T, H, dk)
+    qo, ko, vo = _lin(z, sd, "q"), _lin(z, sd, "k"), _lin(z, sd, "v")
+    if "sconv" in sd:
+        qo, ko, vo, cc = short_conv(sd["sconv"], qo, ko, vo, cc)
+    kp = ko.reshape(B, T, H, dk)
     if key_topk:
         keep = torch.zeros_like(kp).scatter_(-1, kp.abs().topk(key_topk, dim=-1).indices, 1.0)
         kp = kp * keep
-    qp = _lin(z, sd, "q").reshape(B, T, H, dk)
-    vp = _lin(z, sd, "v").reshape(B, T, H, dk)
+    qp = qo.reshape(B, T, H, dk)
+    vp = vo.reshape(B, T, H, dk)
     gate = None if (delta or write_all) else _lin(z, sd, "wi")
     q, k, v = A_.prep(qp, kp, vp, gate, theta, pos)
     la = A_.logalpha(_lin(z, sd, "wa"), sd["A"], la_floor).transpose(1, 2)
@@ -71,7 +89,7 @@ def assoc_carrier(sd, x, h0=None, pos0=0, *, heads, delta=False, write_all=False
     o, S = A_.assoc_scan(q, k, v, la, S0, chunk=chunk, beta=beta)
     o = _rms(o.to(x.dtype), sd["on.weight"]).transpose(1, 2).reshape(B, T, D)
     out = x + F.linear(o, sd["o.weight"] * torch.sigmoid(sd["gate"]))
-    return out, (S, T)
+    return out, ((S, T, cc) if "sconv" in sd else (S, T))
 
 
 def spin_rf(sd, x, h0=None, gate_c=8.0, nu_min=1e-3):
@@ -86,10 +104,16 @@ def spin_rf(sd, x, h0=None, gate_c=8.0, nu_min=1e-3):
     return x + torch.sigmoid(sd["gate"]) * _lin(y.to(x.dtype), sd, "C"), h
 
 
+# the carrier mixers of `src/model.py:632-660`: (delta rule, options); the head count is the caller's `heads`
+ASSOC_MIXERS = {"aspin": (False, {}), "dspin": (True, {}), "hspin": (False, {}), "hspin1": (False, {"write_all": True}),
+                "hdspin": (True, {}), "sdspin": (True, {"key_topk": 8}), "aspin1": (True, {"write_all": True})}
+
+
 def _mixer(sd, prefix, mixer, heads, x, st):
     sub = {k[len(prefix):]: v for k, v in sd.items() if k.startswith(prefix)}
-    if mixer in ("aspin", "dspin", "hspin"):  # hspin: AssocCarrier(d, head_dim=128), `src/model.py:650`
-        return assoc_carrier(sub, x, st, heads=heads, delta=(mixer == "dspin"))
+    if mixer in ASSOC_MIXERS:
+        delta, opts = ASSOC_MIXERS[mixer]
+        return assoc_carrier(sub, x, st, heads=heads, delta=delta, **opts)
     if mixer == "fspin":
         return spin_rf(sub, x, st)
     raise ValueError(mixer)

@@ -30,6 +30,8 @@ SIGNATURES = {
     "pragnosia_aspin_out_fwd": [_p] * 2 + [_f32, _p, _i32, _p] + [_i64] * 4 + [_p],
     "pragnosia_aspin_out_weight_partials": [_i64] * 3,
     "pragnosia_aspin_out_bwd": [_p, _i32] + [_p] * 5 + [_i64] * 4 + [_p],
+    "pragnosia_aspin_exact_fwd": [_p] * 10 + [_i64] * 5 + [_i32, _p],
+    "pragnosia_aspin_exact_bwd": [_p] * 15 + [_i64] * 5 + [_i32, _p],
     "pragnosia_aspin_delta_fwd": [_p] * 11 + [_i64] * 5 + [_p],
     "pragnosia_aspin_delta_bwd_workspace_bytes": [_i64] * 5,
     "pragnosia_aspin_delta_bwd": [_p] * 17 + [_i64] * 6 + [_p],

@@ -4,8 +4,10 @@ Signatures, parameter names, initialisation and the state layout follow the refe
 reference state_dict loads unchanged and the callers (LM, forward_carried, the trainer, the decode loop) use this as
 a drop-in. Every scan runs on the hand-written gfx950 kernels behind `torch.ops.pragnosia.*`:
 
-    T > 1 (or any T with autograd):  aspin_rebase (carried state) -> aspin_prep -> aspin_chunk / aspin_delta
-    T = 1 without autograd (decode): aspin_decode_step (rebase, normalise, gate, write and read fused)
+    kernel path (T > 1):        aspin_rebase -> aspin_prep_proj / aspin_prep -> aspin_chunk / aspin_delta (bf16 MFMA)
+    decode (T = 1, no autograd): aspin_decode_step (rebase, normalise, gate, write and read fused, fp32)
+    torch path (kernel=False, T = 1 under autograd, other head dims): torch prep -> assoc_scan -> aspin_exact
+                                (fp32 / fp64 operands; bf16 MFMA kernels under autocast)
 
 The projections, LayerNorm, the decay and write-strength gates, the per-head RMSNorm and the gated output projection
 are torch GEMMs and elementwise ops around them, as in the reference. There is no CPU path: a CPU tensor raises.
@@ -156,18 +158,41 @@ def _needs_grad(*ts):
     return torch.is_grad_enabled() and any(t is not None and torch.is_tensor(t) and t.requires_grad for t in ts)
 
 
-def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = False, mm=None, beta=None,
-               kernel=True, need_sent: bool = False):
-    """The reference's dispatcher (`src/assoc.py:254-269`) on the HIP kernels: o_t = S_t^T q_t with
-    S_t = a_t S_{t-1} + k_t v_t^T (plain) or the delta rule when `beta` is given.
+def _kernel_ok(dk: int, dv: int, delta: bool) -> bool:
+    """Whether the bf16-operand MFMA kernels take these heads: 64 wide, or 128 wide for the plain rule."""
+    return dk == dv and (dk == HEAD_DIM_KERNEL or (dk == HEAD_DIM_WIDE and not delta))
 
-    q, k, v: (B, H, T, 64); logalpha, beta: (B, H, T); S0: (B, H, 64, 64) or None. The kernels tile time in chunks
-    of 64 whatever `chunk` says: the result does not depend on the chunk size (the reference's own test), so the
-    argument is accepted for signature compatibility, as are `recompute` and `mm` (operands are bf16, accumulation
-    and state fp32). Returns (o in q's dtype, S_final fp32), plus the bf16 entering states when need_sent."""
+
+def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = False, mm=None, beta=None,
+               kernel=False, need_sent: bool = False):
+    """The reference's dispatcher (`src/assoc.py:254-269`): o_t = S_t^T q_t with S_t = a_t S_{t-1} + k_t v_t^T (plain)
+    or the delta rule when `beta` is given. q, k (B, H, T, Dk); v (B, H, T, Dv); logalpha, beta (B, H, T); S0
+    (B, H, Dk, Dv) or None. Returns (o in q's dtype, S_final).
+
+    As in the reference, the arithmetic is fp32, or fp64 for fp64 inputs (`rt`, `src/assoc.py:259-261`), with no
+    operand rounding: the exact kernels (any Dk, Dv <= 128), S_final in that type. With `mm` a 16-bit type (the
+    reference's bf16 matmuls under autocast, `:149-153`) the bf16-operand MFMA kernels run instead (fp32 accumulation
+    and state; head dim 64, or 128 for the plain rule), S_final fp32. The result does not depend on `chunk` (the
+    reference's own test), and both paths recompute in the backward what they do not save, so `chunk`, `recompute`
+    and `kernel` are accepted for the signature. need_sent (this build's): also return the bf16 entering state of
+    every 64-token chunk, from the MFMA kernels."""
+    lowp = mm in (torch.bfloat16, torch.float16)
+    if need_sent or (lowp and _kernel_ok(q.shape[-1], v.shape[-1], beta is not None)):
+        return _kernel_scan(q, k, v, logalpha, S0, beta, need_sent)
+    rt = torch.float64 if q.dtype == torch.float64 else torch.float32
+    want = _needs_grad(q, k, v, logalpha, S0, beta)
+    o, S, _, _ = _op.aspin_exact(q.to(rt), k.to(rt), v.to(rt), logalpha.to(rt),
+                                 None if beta is None else beta.to(rt), None if S0 is None else S0.to(rt), want)
+    return o.to(q.dtype), S
+
+
+def _kernel_scan(q, k, v, logalpha, S0, beta, need_sent):
+    """The bf16-operand MFMA kernels: q, k, v (B, H, T, 64) (128 for the plain rule), operands rounded to bf16,
+    accumulation and state fp32. Returns (o in q's dtype, S_final fp32) and, when need_sent, the bf16 state entering
+    every 64-token chunk."""
     wide = q.shape[-1] == HEAD_DIM_WIDE and beta is None
-    if q.shape[-1] != HEAD_DIM_KERNEL and not wide:
-        raise PragnosiaError(f"assoc_scan: head dim {q.shape[-1]} is not supported by the HIP kernels (64; 128 for "
+    if not _kernel_ok(q.shape[-1], v.shape[-1], beta is not None):
+        raise PragnosiaError(f"assoc_scan: head dim {q.shape[-1]} is not supported by the bf16 kernels (64; 128 for "
                              "the plain rule)")
     want = bool(need_sent or _needs_grad(q, k, v, logalpha, S0, beta))
     S0 = None if S0 is None else S0.float()
@@ -187,12 +212,12 @@ def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = Fa
 def assoc_scan_kernel(q, k, v, logalpha, S0=None, bv: int = 16):
     """Plain rule; the contract of the reference's `assoc_scan_kernel` (`src/assoc_kernel.py:302-323`):
     returns (o in q's dtype, S_final fp32, sent bf16 (B, H, NC, 64, 64))."""
-    return assoc_scan(q, k, v, logalpha, S0, need_sent=True)
+    return _kernel_scan(q, k, v, logalpha, S0, None, True)
 
 
 def delta_scan_kernel(q, k, v, logalpha, beta, S0=None, chunk: int = 64, bv: int = 32, bv_bwd: int = 16):
     """Delta rule; the contract of the reference's `delta_scan_kernel` (`src/assoc_kernel.py:512-546`)."""
-    return assoc_scan(q, k, v, logalpha, S0, beta=beta, need_sent=True)
+    return _kernel_scan(q, k, v, logalpha, S0, beta, True)
 
 
 def prep_kernel(qp, kp, vp, gate_logits, theta, pos):
@@ -203,10 +228,12 @@ def prep_kernel(qp, kp, vp, gate_logits, theta, pos):
 
 class AssocCarrier(nn.Module):
     """Per-head key-value outer-product memory with per-token forgetting, learned rotation frequencies and an
-    optional delta write rule (`src/assoc.py:279-512`). Constructor arguments and parameters are the reference's;
-    `kernel` is accepted and ignored (every path is the HIP kernel path). Supported on the kernels: head dim 64,
-    key_topk, hl_floor, write_all, beta_scale, FUSED_PROJ. The short causal convolution (add_short_conv) is not built
-    here and raises."""
+    optional delta write rule (`src/assoc.py:279-512`). Constructor arguments, parameters and paths are the
+    reference's: with `kernel` (and T > 1, head dim 64, or 128 for the plain rule) the bf16-operand MFMA kernels with
+    the fused prep; otherwise (kernel=False, a T = 1 call under autograd, other head dims up to 128) the reference's
+    torch composition around the exact fp32 scan (bf16 MFMA kernels under autocast, as the reference's bf16 matmuls);
+    a T = 1 call without autograd (decode) the fused fp32 step kernel. Options: key_topk, hl_floor, write_all,
+    beta_scale, FUSED_PROJ, pos_wrap, and the short causal convolution with its carried cache (add_short_conv)."""
 
     def __init__(self, d: int, heads: int | None = None, chunk: int = 64, recompute: bool = False,
                  delta: bool = False, head_dim: int | None = None, kernel: bool = True, key_topk: int = 0,
@@ -254,9 +281,27 @@ class AssocCarrier(nn.Module):
         return la.clamp(min=self.la_floor) if self.hl_floor else la
 
     def add_short_conv(self, K: int):
-        raise PragnosiaError("AssocCarrier.add_short_conv: the short causal convolution is not part of this build")
+        """A depthwise causal convolution over the last K tokens on q, k and v (`src/assoc.py:361-372`): weight
+        (3 d, K), initialised as the identity (all weight on the current token). The carried state becomes
+        (S, position, cache) with the cache the last K - 1 inputs, (B, 3 d, K - 1)."""
+        w = torch.zeros(3 * self.d, K, device=self.q.weight.device, dtype=self.q.weight.dtype)
+        w[:, -1] = 1.0
+        self.sconv = nn.Parameter(w)
+        return self
 
-    def _projections(self, z):
+    def _sconv(self, qo, ko, vo, cc):
+        """The causal depthwise convolution on q, k, v (B, T, d each) continuing the cache cc ((B, 3 d, K - 1) or None
+        at a sequence start) (`src/assoc.py:374-382`). Returns q, k, v and the new cache."""
+        D, K = self.d, self.sconv.shape[1]
+        x = torch.cat([qo, ko, vo], dim=-1).transpose(1, 2)
+        pad = cc.to(x.dtype) if cc is not None else x.new_zeros(x.shape[0], 3 * D, K - 1)
+        xp = torch.cat([pad, x], dim=-1)
+        y = F.conv1d(xp, self.sconv.to(x.dtype).unsqueeze(1), groups=3 * D).transpose(1, 2)
+        return y[..., :D].contiguous(), y[..., D:2 * D].contiguous(), y[..., 2 * D:].contiguous(), xp[..., -(K - 1):]
+
+    def _projections(self, z, cc=None):
+        """q, k, v projections (B, T, H, dk) (short convolution and key_topk applied), the write-gate logits (plain
+        rule, else None), la (B, T, H), beta (B, T, H) or None, and the convolution's new cache."""
         B, T, _ = z.shape
         fused = FUSED_PROJ and self.delta and not self.key_topk
         if fused:
@@ -271,6 +316,8 @@ class AssocCarrier(nn.Module):
             qo, ko, vo = self.q(z), self.k(z), self.v(z)
             la = self.logalpha(z)
             bt = torch.sigmoid(self.wb(z)) if self.delta else None
+        if getattr(self, "sconv", None) is not None:
+            qo, ko, vo, cc = self._sconv(qo, ko, vo, cc)
         kp = ko.view(B, T, self.h, self.dk)
         if self.key_topk:
             keep = torch.zeros_like(kp).scatter_(-1, kp.abs().topk(self.key_topk, dim=-1).indices, 1.0)
@@ -281,16 +328,29 @@ class AssocCarrier(nn.Module):
                 bt = bt * self.beta_scale.transpose(1, 2).to(bt.dtype)
             if self.write_all:
                 bt = bt.clamp(min=0.75)
-        return qo.view(B, T, self.h, self.dk), kp, vo.view(B, T, self.h, self.dk), gate, la, bt
+        return qo.view(B, T, self.h, self.dk), kp, vo.view(B, T, self.h, self.dk), gate, la, bt, cc
 
-    def _scan_inputs(self, z, pos):
-        """The scan's inputs from the normalised layer input z (B, T, d): q, k, v (B, H, T, dk) bf16, la and beta
-        (B, H, T) fp32 (beta None for the plain rule), and the projections' dtype. With FUSED_PLUMBING (no key_topk,
-        no beta_scale): one GEMM for the q, k, v, decay and write-gate (plain) or write-strength (delta) projections
-        and one kernel from its output; otherwise the reference's composition: separate projections (one GEMM under
-        FUSED_PROJ), elementwise decay, gate and strength, prep."""
+    def _torch_inputs(self, z, pos, cc=None):
+        """The reference's torch path to the scan's inputs (`src/assoc.py:436-444`, used when the kernels are not):
+        unit-normalise q, k, v per head, gate k (plain rule), rotate q and k at `pos`, all in the projections' dtype.
+        Returns q, k, v (B, H, T, dk), la and beta (B, H, T) (beta None for the plain rule), the projections' dtype
+        and the convolution's new cache."""
+        qp, kp, vp, gate, la, bt, cc = self._projections(z, cc)
+        q, k, v = (F.normalize(t.transpose(1, 2), dim=-1) for t in (qp, kp, vp))
+        if gate is not None:
+            k = k * torch.sigmoid(gate).transpose(1, 2).unsqueeze(-1)
+        q, k = rotate(q, self.theta, pos), rotate(k, self.theta, pos)
+        return q, k, v, la.transpose(1, 2), (None if bt is None else bt.transpose(1, 2)), qp.dtype, cc
+
+    def _scan_inputs(self, z, pos, cc=None):
+        """The bf16 kernels' inputs from the normalised layer input z (B, T, d): q, k, v (B, H, T, dk) bf16, la and
+        beta (B, H, T) fp32 (beta None for the plain rule), the projections' dtype and the short convolution's new
+        cache. With FUSED_PLUMBING (no key_topk, beta_scale or short convolution): one GEMM for the q, k, v, decay and
+        write-gate (plain) or write-strength (delta) projections and one kernel from its output; otherwise the
+        reference's composition: separate projections (one GEMM under FUSED_PROJ), convolution, elementwise decay,
+        gate and strength, prep."""
         if (FUSED_PLUMBING and not self.key_topk and self.dk == HEAD_DIM_KERNEL
-                and getattr(self, "beta_scale", None) is None):
+                and getattr(self, "beta_scale", None) is None and getattr(self, "sconv", None) is None):
             gated = not (self.delta or self.write_all)
             extra = [self.wi.weight] if gated else ([self.wb.weight] if self.delta else [])
             W = torch.cat([self.q.weight, self.k.weight, self.v.weight, self.wa.weight] + extra)
@@ -299,14 +359,14 @@ class AssocCarrier(nn.Module):
                 P, self.h, self.wa.bias, self.A, self.la_floor if self.hl_floor else None,
                 self.wi.bias if gated else None, self.wb.bias if self.delta else None,
                 0.75 if (self.delta and self.write_all) else 0.0, gated, self.theta, pos)
-            return q, k, v, la, (beta if self.delta else None), P.dtype
-        qp, kp, vp, gate, la, bt = self._projections(z)
+            return q, k, v, la, (beta if self.delta else None), P.dtype, cc
+        qp, kp, vp, gate, la, bt, cc = self._projections(z, cc)
         if self.dk == HEAD_DIM_KERNEL:
             q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
         else:
             q, k, v = _prep_wide(qp, kp, vp, gate, self.theta, pos)
         bt = None if bt is None else bt.transpose(1, 2).float()
-        return q, k, v, la.transpose(1, 2).float(), bt, qp.dtype
+        return q, k, v, la.transpose(1, 2).float(), bt, qp.dtype, cc
 
     def _epilogue(self, o, dtype):
         """`self.on(o.to(dtype)).transpose(1, 2).reshape(B, T, D)` (`src/assoc.py:500-505`) for the scan's bf16 output
@@ -319,51 +379,46 @@ class AssocCarrier(nn.Module):
         return self.on(o.to(dtype)).transpose(1, 2).reshape(B, T, H * Dk)
 
     def forward(self, x, h0=None, pos0: int = 0):
-        """x (B, T, d); h0 = (S (B, H, dk, dk) fp32, p0) from a previous call, or None. Returns
-        (x + gated output, (S, p0 + T)); positions restart at 0 every call and the carried state is rebased by -p0."""
-        wide = self.dk == HEAD_DIM_WIDE and not self.delta
-        if self.dk != HEAD_DIM_KERNEL and not wide:
-            raise PragnosiaError(f"AssocCarrier: head dim {self.dk} is not supported by the HIP kernels (64; 128 for "
-                                 "the plain rule)")
+        """x (B, T, d); h0 = (S (B, H, dk, dk), p0) from a previous call, (S, p0, cache) with the short convolution, or
+        None. Returns (x + gated output, (S, T) or (S, T, cache)); positions restart at 0 every call and the carried
+        state is rebased by -p0 (`src/assoc.py:384-512`)."""
+        if self.dk > _op_mod.EXACT_MAX_D:
+            raise PragnosiaError(f"AssocCarrier: head dim {self.dk} is above the {_op_mod.EXACT_MAX_D} the kernels take")
         if not x.is_cuda:
             raise PragnosiaError("AssocCarrier runs on a ROCm GPU only; there is no CPU path")
         B, T, D = x.shape
+        sc = getattr(self, "sconv", None) is not None
+        cc = None
         if h0 is None:
             S0, p0 = None, pos0
         elif len(h0) == 3:
-            raise PragnosiaError("AssocCarrier: a short-convolution cache in the state is not supported")
+            S0, p0, cc = h0
         else:
             S0, p0 = h0
         z = self.ln(x)
         p_dev = p0.float().reshape(()) if torch.is_tensor(p0) else None
         p_host = 0.0 if torch.is_tensor(p0) else float(p0)
+        shifted = S0 is not None and (p_dev is not None or p_host != 0.0)
         decode = T == 1 and not _needs_grad(x, S0, *self.parameters())
-        if decode and wide:
-            # the reference's T = 1 step (`src/assoc.py:411`, torch there too), fp32: rebase, write, read
-            qp, kp, vp, gate, la, _ = self._projections(z)
-            q, k, v = _prep_wide(qp, kp, vp, gate, self.theta, torch.zeros(1, dtype=torch.long, device=x.device),
-                                 torch.float32)
-            S_prev = (torch.zeros(B, self.h, self.dk, self.dk, device=x.device) if S0 is None
-                      else _rebase_wide(S0.float(), self.theta, p_dev, p_host))
-            S = torch.exp(la.float()).transpose(1, 2).unsqueeze(-1) * S_prev + k.transpose(-1, -2) @ v
-            o = (q @ S).to(qp.dtype)
-            sent = None
-        elif decode:
-            qp, kp, vp, gate, la, bt = self._projections(z)
+        kern = self.kernel and T > 1 and _kernel_ok(self.dk, self.dk, self.delta)
+        sent = None
+        if decode and self.dk == HEAD_DIM_KERNEL:
+            # the fused fp32 step: rebase, normalise, gate, decay, write, read
+            qp, kp, vp, gate, la, bt, cc = self._projections(z, cc)
             S_prev = S0 if S0 is not None else torch.zeros(B, self.h, self.dk, self.dk, device=x.device)
             S, o = _op.aspin_decode_step(S_prev, qp.reshape(B, self.h, self.dk), kp.reshape(B, self.h, self.dk),
                                          vp.reshape(B, self.h, self.dk),
                                          None if gate is None else gate.reshape(B, self.h),
                                          la.reshape(B, self.h), None if bt is None else bt.reshape(B, self.h),
                                          self.theta, p_dev, p_host)
-            o = o.unsqueeze(2).to(qp.dtype)
-            sent = None
-        else:
-            if S0 is not None and (p_dev is not None or p_host != 0.0):
+            o = self.on(o.unsqueeze(2).to(qp.dtype)).transpose(1, 2).reshape(B, T, D)
+        elif kern:
+            wide = self.dk == HEAD_DIM_WIDE
+            if shifted:
                 S0 = (_rebase_wide(S0.float(), self.theta, p_dev, p_host) if wide
                       else _op.aspin_rebase(S0, self.theta, p_dev, p_host))
             pos = _positions(T, x.device, getattr(self, "pos_wrap", None))
-            q, k, v, la, bt, dtype = self._scan_inputs(z, pos)
+            q, k, v, la, bt, dtype, cc = self._scan_inputs(z, pos, cc)
             want = bool(self.need_sent or not (FUSED_SCAN and self.delta) or
                         _needs_grad(x, S0, *self.parameters()))
             if self.delta:
@@ -374,8 +429,21 @@ class AssocCarrier(nn.Module):
             else:
                 o, S, sent = _op.aspin_chunk(q, k, v, la, S0, want)
             sent = sent if want else None
+            o = self._epilogue(o, dtype)
+        else:
+            # the reference's torch path (kernel=False, a T = 1 call under autograd, a decode step at a head dim
+            # other than 64): normalise, gate and rotate in torch, then assoc_scan, fp32 (bf16 MFMA kernels under
+            # autocast, as the reference's bf16 matmuls)
+            if shifted:
+                S0 = (_op.aspin_rebase(S0, self.theta, p_dev, p_host)
+                      if self.dk == HEAD_DIM_KERNEL and S0.dtype == torch.float32
+                      else _rebase_wide(S0, self.theta, p_dev, p_host))
+            pos = _positions(T, x.device, getattr(self, "pos_wrap", None))
+            q, k, v, la, bt, dtype, cc = self._torch_inputs(z, pos, cc)
+            mm = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
+            o, S = assoc_scan(q, k, v, la, S0, chunk=self.chunk, recompute=self.recompute, mm=mm, beta=bt)
+            o = self.on(o).transpose(1, 2).reshape(B, T, D)
         self.sent = sent
-        o = self.on(o).transpose(1, 2).reshape(B, T, D) if decode else self._epilogue(o, dtype)
         if _needs_grad(x, o, self.o.weight, self.gate):
             # gate on the weight, as the reference does for training (it keeps the backward's saved tensor small)
             out = x + F.linear(o, self.o.weight * torch.sigmoid(self.gate))
@@ -383,7 +451,8 @@ class AssocCarrier(nn.Module):
             # the same function without materialising a gated d x d weight on every call (decode, inference)
             out = x + F.linear(o, self.o.weight) * torch.sigmoid(self.gate)
         # the state is now expressed in this call's positions 0..T-1: the next call rebases it by T
-        return out, (S, p0 * 0 + T if torch.is_tensor(p0) else T)
+        p_out = p0 * 0 + T if torch.is_tensor(p0) else T
+        return out, ((S, p_out, cc) if sc else (S, p_out))
 
     def forward_windows(self, x, window: int, h0=None, pos0: int = 0):
         """Consecutive windows of `window` tokens of x (B, T, d), the state carried from each window into the next:
@@ -395,6 +464,7 @@ class AssocCarrier(nn.Module):
         window)); `sent` is not kept."""
         B, T, D = x.shape
         fused = (not self.delta and window % 64 == 0 and T > window and x.is_cuda and self.dk == HEAD_DIM_KERNEL
+                 and self.kernel and getattr(self, "sconv", None) is None
                  and not _needs_grad(x, *(h0[:1] if h0 is not None else ()), *self.parameters()))
         if not fused:
             outs, st = [], h0
@@ -402,12 +472,7 @@ class AssocCarrier(nn.Module):
                 o, st = self.forward(x[:, s:s + window], st, pos0)
                 outs.append(o)
             return torch.cat(outs, 1), st
-        if h0 is None:
-            S0, p0 = None, pos0
-        elif len(h0) == 3:
-            raise PragnosiaError("AssocCarrier: a short-convolution cache in the state is not supported")
-        else:
-            S0, p0 = h0
+        S0, p0 = (None, pos0) if h0 is None else h0[:2]
         z = self.ln(x)
         p_dev = p0.float().reshape(()) if torch.is_tensor(p0) else None
         p_host = 0.0 if torch.is_tensor(p0) else float(p0)
@@ -417,7 +482,7 @@ class AssocCarrier(nn.Module):
         wrap = getattr(self, "pos_wrap", None)
         if wrap:
             pos = pos % wrap
-        q, k, v, la, _, dtype = self._scan_inputs(z, pos)
+        q, k, v, la, _, dtype, _ = self._scan_inputs(z, pos)
         o, S, _ = _op.aspin_chunk_windows(q, k, v, la, S0, self.theta, window, False)
         self.sent = None
         o = self._epilogue(o, dtype)

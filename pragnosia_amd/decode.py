@@ -78,7 +78,9 @@ class GreedyDecoder:
         for st in states:
             if isinstance(st[1], (int, float)) or (torch.is_tensor(st[1]) and st[1].dim() == 0):
                 p0 = st[1] if torch.is_tensor(st[1]) else torch.tensor(float(st[1]), device=st[0].device)
-                out.append((st[0].clone().contiguous(), p0.float().clone()))
+                # (S, position) or, with a short convolution, (S, position, cache)
+                out.append((st[0].clone().contiguous(), p0.float().clone(),
+                            *(t.clone().contiguous() for t in st[2:])))
             else:
                 out.append(tuple(t.clone().contiguous() for t in st))
         return out

@@ -3,13 +3,18 @@
 Constructor arguments, module names and initialisation follow the reference (`src/model.py:552-560`, `:621-738`), so
 `LM(**cfg).load_state_dict(sd)` takes a reference checkpoint of a supported mixer:
 
-    "aspin"  AssocCarrier(d)               plain write rule, 64-dim heads
-    "dspin"  AssocCarrier(d, delta=True)   delta write rule
-    "hspin"  AssocCarrier(d, head_dim=128) plain write rule, 128-dim heads (four 64 x 64 scans per head)
-    "fspin"  SpinCarrier(d, gated="rf")    forget-gated complex diagonal carrier
+    "aspin"   AssocCarrier(d)                                      plain write rule, 64-dim heads
+    "dspin"   AssocCarrier(d, delta=True)                          delta write rule
+    "hspin"   AssocCarrier(d, head_dim=128)                        plain rule, 128-dim heads (four 64 x 64 scans)
+    "hspin1"  AssocCarrier(d, head_dim=128, write_all=True)        ... with no write gate
+    "hdspin"  AssocCarrier(d, delta=True, head_dim=128)            delta rule, 128-dim heads
+    "sdspin"  ... + key_topk=8;  "tspin" ... + hl_floor=True;  "aspin1" ... + write_all=True
+    "fspin"   SpinCarrier(d, gated="rf")                           forget-gated complex diagonal carrier
 
-The mixers run on the HIP kernels; embeddings, LayerNorms, the MLPs and the tied head are torch. Attention and the
-other reference mixers are outside this build and raise.
+(`src/model.py:632-660`.) The mixers run on the HIP kernels (the delta rule at head dim 128 on the fp32 exact scan);
+embeddings, LayerNorms, the MLPs and the tied head are torch. Attention, the hybrid stacks and the other reference
+mixers are outside this build and raise. `short_conv=K` adds every carrier's short causal convolution
+(`src/model.py:717-726`).
 """
 from __future__ import annotations
 
@@ -26,6 +31,11 @@ MIXERS = {
     "aspin": lambda d: AssocCarrier(d),
     "dspin": lambda d: AssocCarrier(d, delta=True),
     "hspin": lambda d: AssocCarrier(d, head_dim=128),
+    "hspin1": lambda d: AssocCarrier(d, head_dim=128, write_all=True),
+    "hdspin": lambda d: AssocCarrier(d, delta=True, head_dim=128),
+    "sdspin": lambda d: AssocCarrier(d, delta=True, head_dim=128, key_topk=8),
+    "tspin": lambda d: AssocCarrier(d, delta=True, head_dim=128, hl_floor=True),
+    "aspin1": lambda d: AssocCarrier(d, delta=True, head_dim=128, write_all=True),
     "fspin": lambda d: SpinCarrier(d, gated="rf"),
 }
 
@@ -47,8 +57,6 @@ class LM(nn.Module):
         super().__init__()
         if mixer not in MIXERS:
             raise PragnosiaError(f"LM: mixer {mixer!r} is outside this build (supported: {sorted(MIXERS)})")
-        if short_conv:
-            raise PragnosiaError("LM: short convolutions are not part of this build")
         self.vocab, self.d, self.layers, self.ctx, self.mixer, self.norm = vocab, d, layers, ctx, mixer, norm
         self.e = nn.Embedding(vocab, d)
         self.p = nn.Embedding(ctx, d)
@@ -62,6 +70,17 @@ class LM(nn.Module):
                         setattr(mod, name, nn.RMSNorm(child.normalized_shape[0]))
         self.apply(self._init)
         self.short_conv = 0
+        if short_conv:
+            self.add_short_conv(short_conv)
+
+    def add_short_conv(self, K: int):
+        """A short causal convolution over the last K tokens on every carrier's q, k and v, initialised as the
+        identity (`src/model.py:721-726`); the carriers' states then carry the convolution's cache."""
+        for mx in self.mix:
+            if hasattr(mx, "add_short_conv"):
+                mx.add_short_conv(K)
+        self.short_conv = K
+        return self
 
     @staticmethod
     def _init(m):

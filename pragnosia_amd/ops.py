@@ -481,6 +481,137 @@ aspin_delta.register_autograd(_delta_backward, setup_context=_delta_setup)
 
 
 # ---------------------------------------------------------------------------------------------------------------
+# the scan with fp32 / fp64 operands (no bf16 rounding): replaces assoc_scan's fp32/fp64 torch forms and their
+# autograd backward, src/assoc.py:118-165, :207-269
+EXACT_CKPT = 8  # tokens per checkpointed state (PRAGNOSIA_EXACT_CKPT_TOKENS)
+EXACT_MAX_D = 128
+
+
+def _exact_dtype(t: Tensor) -> torch.dtype:
+    return torch.float64 if t.dtype == torch.float64 else torch.float32
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    return 1 if dt == torch.float64 else 0
+
+
+def _expect_exact(op: str, q: Tensor, k, v, la, beta=None, S0=None) -> None:
+    """q, k (B, H, T, Dk); v (B, H, T, Dv); la, beta (B, H, T); S0 (B, H, Dk, Dv); Dk, Dv <= 128."""
+    if q.dim() != 4 or v is None or v.dim() != 4:
+        raise PragnosiaError(f"{op}: q and v must be (B, H, T, D)")
+    B, H, T, Dk = q.shape
+    Dv = v.shape[-1]
+    if not (0 < Dk <= EXACT_MAX_D and 0 < Dv <= EXACT_MAX_D):
+        raise PragnosiaError(f"{op}: head dims Dk={Dk}, Dv={Dv} must be in 1..{EXACT_MAX_D}")
+    _expect(op, q.device, k=(k, (B, H, T, Dk)), v=(v, (B, H, T, Dv)), la=(la, (B, H, T)), beta=(beta, (B, H, T)),
+            S0=(S0, (B, H, Dk, Dv)))
+
+
+@torch.library.custom_op("pragnosia::aspin_exact", mutates_args=())
+def aspin_exact(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Optional[Tensor], S0: Optional[Tensor],
+                want_ckpt: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """The scan with fp32 operands (fp64 when q is fp64), plain rule, or the delta rule when beta is given.
+    q, k (B, H, T, Dk), v (B, H, T, Dv), la and beta (B, H, T), S0 (B, H, Dk, Dv) or None; Dk, Dv <= 128. Returns
+    (o (B, H, T, Dv), S_final (B, H, Dk, Dv), ckpt, resid) in the compute dtype; ckpt (the state entering every 8
+    tokens) and resid (the delta rule's residuals) are what the backward reads, empty unless want_ckpt."""
+    _require_gpu(q, k, v, la, beta, S0)
+    _expect_exact("aspin_exact", q, k, v, la, beta, S0)
+    dt = _exact_dtype(q)
+    cv = lambda t: None if t is None else t.to(dt).contiguous()
+    q, k, v, la, beta, S0 = cv(q), cv(k), cv(v), cv(la), cv(beta), cv(S0)
+    B, H, T, Dk = q.shape
+    Dv = v.shape[-1]
+    dev = q.device
+    o = torch.empty(B, H, T, Dv, device=dev, dtype=dt)
+    S = torch.empty(B, H, Dk, Dv, device=dev, dtype=dt)
+    NB = (T + EXACT_CKPT - 1) // EXACT_CKPT
+    ckpt = torch.empty(B, H, NB, Dk, Dv, device=dev, dtype=dt) if want_ckpt else q.new_empty(0)
+    resid = (torch.empty(B, H, T, Dv, device=dev, dtype=dt) if (want_ckpt and beta is not None)
+             else q.new_empty(0))
+    check(lib().pragnosia_aspin_exact_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(beta), _ptr(S0), _ptr(o), _ptr(S),
+                                          _ptr(ckpt) if want_ckpt else None,
+                                          _ptr(resid) if resid.numel() else None, B, H, T, Dk, Dv, _dtype_code(dt),
+                                          _stream(q)), "pragnosia_aspin_exact_fwd")
+    return o, S, ckpt, resid
+
+
+@aspin_exact.register_fake
+def _(q, k, v, la, beta, S0, want_ckpt):
+    B, H, T, Dk = q.shape
+    Dv = v.shape[-1]
+    dt = _exact_dtype(q)
+    NB = (T + EXACT_CKPT - 1) // EXACT_CKPT
+    ckpt = q.new_empty(B, H, NB, Dk, Dv, dtype=dt) if want_ckpt else q.new_empty(0, dtype=dt)
+    resid = q.new_empty(B, H, T, Dv, dtype=dt) if (want_ckpt and beta is not None) else q.new_empty(0, dtype=dt)
+    return q.new_empty(B, H, T, Dv, dtype=dt), q.new_empty(B, H, Dk, Dv, dtype=dt), ckpt, resid
+
+
+@torch.library.custom_op("pragnosia::aspin_exact_bwd", mutates_args=())
+def aspin_exact_bwd(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Optional[Tensor], ckpt: Tensor,
+                    resid: Optional[Tensor], do: Tensor,
+                    dS: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Backward of aspin_exact. Returns (dq, dk, dv, dla, dbeta (empty for the plain rule), dS0) in the compute
+    dtype."""
+    _require_gpu(q, k, v, la, beta, ckpt, resid, do, dS)
+    _expect_exact("aspin_exact_bwd", q, k, v, la, beta)
+    B, H, T, Dk = q.shape
+    Dv = v.shape[-1]
+    NB = (T + EXACT_CKPT - 1) // EXACT_CKPT
+    _expect("aspin_exact_bwd", q.device, ckpt=(ckpt, (B, H, NB, Dk, Dv)), do=(do, (B, H, T, Dv)),
+            dS=(dS, (B, H, Dk, Dv)), resid=(resid if beta is not None else None, (B, H, T, Dv)))
+    dt = _exact_dtype(q)
+    cv = lambda t: None if t is None else t.to(dt).contiguous()
+    q, k, v, la, beta, ckpt, do, dS = cv(q), cv(k), cv(v), cv(la), cv(beta), cv(ckpt), cv(do), cv(dS)
+    resid = cv(resid) if beta is not None else None
+    dev = q.device
+    dq, dk = torch.empty(B, H, T, Dk, device=dev, dtype=dt), torch.empty(B, H, T, Dk, device=dev, dtype=dt)
+    dv = torch.empty(B, H, T, Dv, device=dev, dtype=dt)
+    dla = torch.empty(B, H, T, device=dev, dtype=dt)
+    dbeta = torch.empty(B, H, T, device=dev, dtype=dt) if beta is not None else q.new_empty(0)
+    dS0 = torch.empty(B, H, Dk, Dv, device=dev, dtype=dt)
+    check(lib().pragnosia_aspin_exact_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(beta), _ptr(ckpt), _ptr(resid),
+                                          _ptr(do), _ptr(dS), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla),
+                                          _ptr(dbeta) if beta is not None else None, _ptr(dS0), B, H, T, Dk, Dv,
+                                          _dtype_code(dt), _stream(q)), "pragnosia_aspin_exact_bwd")
+    return dq, dk, dv, dla, dbeta, dS0
+
+
+@aspin_exact_bwd.register_fake
+def _(q, k, v, la, beta, ckpt, resid, do, dS):
+    B, H, T, Dk = q.shape
+    Dv = v.shape[-1]
+    dt = _exact_dtype(q)
+    e = lambda *s: q.new_empty(*s, dtype=dt)
+    return e(B, H, T, Dk), e(B, H, T, Dk), e(B, H, T, Dv), e(B, H, T), e(B, H, T) if beta is not None else e(0), \
+        e(B, H, Dk, Dv)
+
+
+def _exact_setup(ctx, inputs, output):
+    q, k, v, la, beta, S0, want_ckpt = inputs
+    _, _, ckpt, resid = output
+    if ckpt.numel() == 0 and any(ctx.needs_input_grad[:6]):
+        raise PragnosiaError("aspin_exact: the backward needs the checkpoints; call with want_ckpt=True")
+    ctx.has_s0, ctx.has_beta = S0 is not None, beta is not None
+    ctx.dtypes = tuple(None if t is None else t.dtype for t in (q, k, v, la, beta, S0))
+    ctx.save_for_backward(q, k, v, la, beta, ckpt, resid)
+    ctx.mark_non_differentiable(ckpt, resid)
+
+
+def _exact_backward(ctx, do, dS, _dckpt, _dresid):
+    q, k, v, la, beta, ckpt, resid = ctx.saved_tensors
+    if do is None:
+        do = torch.zeros(*q.shape[:3], v.shape[-1], device=q.device, dtype=_exact_dtype(q))
+    dq, dk, dv, dla, dbeta, dS0 = aspin_exact_bwd(q, k, v, la, beta, ckpt, resid if ctx.has_beta else None,
+                                                  do.contiguous(), dS)
+    dt = ctx.dtypes
+    return (dq.to(dt[0]), dk.to(dt[1]), dv.to(dt[2]), dla.to(dt[3]), dbeta.to(dt[4]) if ctx.has_beta else None,
+            dS0.to(dt[5]) if ctx.has_s0 else None, None)
+
+
+aspin_exact.register_autograd(_exact_backward, setup_context=_exact_setup)
+
+
+# ---------------------------------------------------------------------------------------------------------------
 # prep (normalise, gate, rotate, cast, transpose): replaces prep_kernel and its ops, src/assoc_kernel.py:740-891
 def _proj(t: Tensor) -> Tensor:
     if t.dtype not in (torch.float32, torch.bfloat16):

@@ -1,7 +1,8 @@
 """The HIP modules against the reference's own modules: the fixtures of tests/golden/modules.npz (reference CPU
-modules in fp32, seeded parameters and inputs; see tests/test_golden_modules.py, which pins the oracle to the same
-fixtures at 1e-4). Tolerances: the aspin paths compute the scans on bf16 operands, max relative error <= 2e-2 on
-outputs and carried states (the north star's bound); the fspin paths are fp32 end to end, <= 1e-4."""
+modules in fp32 on their torch path, kernel=False; seeded parameters and inputs; see tests/test_golden_modules.py,
+which pins the oracle to the same fixtures at 1e-4). Tolerances: the aspin kernel paths compute the scans on bf16
+operands, max relative error <= 2e-2 on outputs and carried states (the north star's bound); the aspin torch path
+(kernel=False: the exact fp32 scan) and the fspin paths are fp32 end to end, <= 1e-4."""
 import os
 
 import numpy as np
@@ -26,12 +27,13 @@ def _params():
     return P
 
 
+@pytest.mark.parametrize("kernel,tol", [(True, 2e-2), (False, 1e-4)])
 @pytest.mark.parametrize("delta", [False, True])
-def test_assoc_carrier_matches_reference(delta):
+def test_assoc_carrier_matches_reference(delta, kernel, tol):
     P = _params()
     from pragnosia_amd.assoc import AssocCarrier
     a = P.ASSOC
-    m = AssocCarrier(a["d"], heads=a["heads"], delta=delta)
+    m = AssocCarrier(a["d"], heads=a["heads"], delta=delta, kernel=kernel)
     P.fill_(m, 10 + delta)
     m = m.cuda()
     x, S0 = P.inputs(20 + delta, (a["B"], a["T"], a["d"]), (a["B"], a["heads"], 64, 64))
@@ -40,8 +42,8 @@ def test_assoc_carrier_matches_reference(delta):
         y, (S, p) = m(x.cuda(), (S0.cuda(), a["p0"]))
     tag = "assoc_delta" if delta else "assoc_plain"
     assert p == a["T"]
-    assert rel(y - x.cuda(), G[tag + "_y"] - x.numpy()) < 2e-2
-    assert rel(S, G[tag + "_S"]) < 2e-2
+    assert rel(y - x.cuda(), G[tag + "_y"] - x.numpy()) < tol
+    assert rel(S, G[tag + "_S"]) < tol
 
 
 def test_spin_rf_matches_reference():
@@ -58,12 +60,15 @@ def test_spin_rf_matches_reference():
     assert rel(hr2, G["spin_hr"]) < 1e-4 and rel(hi2, G["spin_hi"]) < 1e-4
 
 
-@pytest.mark.parametrize("mixer,tol", [("aspin", 2e-2), ("fspin", 1e-4)])
-def test_lm_matches_reference(mixer, tol):
+@pytest.mark.parametrize("mixer,kernel,tol", [("aspin", True, 2e-2), ("aspin", False, 1e-4), ("fspin", True, 1e-4)])
+def test_lm_matches_reference(mixer, kernel, tol):
     P = _params()
     from pragnosia_amd.model import LM
     c = P.LMCFG
     lm = LM(vocab=c["vocab"], d=c["d"], layers=c["layers"], mlp_mult=c["mlp_mult"], ctx=c["ctx"], mixer=mixer)
+    for mod in lm.modules():
+        if hasattr(mod, "kernel"):
+            mod.kernel = kernel
     P.fill_(lm, 40 + len(mixer))
     lm = lm.cuda().eval()
     ids = P.ids(41, (c["B"], c["T"]), c["vocab"]).cuda()

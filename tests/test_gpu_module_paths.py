@@ -1,0 +1,131 @@
+"""GPU parity of the carrier's other paths against the fp64 CPU oracle driven by the same state_dict: the reference's
+torch path (kernel=False, and a T = 1 call under autograd) on the exact fp32 scan, the short causal convolution with
+its carried cache, and the head-dim-128 delta carriers (hdspin, sdspin, aspin1) in an LM with graphed decode.
+
+Tolerances: the torch path is fp32 end to end, 1e-4 max relative error on outputs, states and every gradient (per
+affine block, as tests/test_gpu_modules.py explains); kernel-path comparisons keep the bf16 bounds 2e-2 / 5e-2."""
+import pytest
+import torch
+
+from oracle import aspin as OA
+from oracle import modules as M
+from test_gpu_modules import _block_errors, _randomise, _sd64, rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_grads(mod, x, S0, p0, wo, wS, delta, cc=None):
+    sd = {k: v.clone().requires_grad_(v.is_floating_point()) for k, v in _sd64(mod).items()}
+    xr, S0r = x.double().requires_grad_(True), S0.double().requires_grad_(True)
+    h0 = (S0r, p0) if cc is None else (S0r, p0, cc.double())
+    yr, st = M.assoc_carrier(sd, xr, h0, heads=mod.h, delta=delta, write_all=mod.write_all, key_topk=mod.key_topk)
+    ((yr - xr) * wo.double()).sum().add((st[0] * wS.double()).sum()).backward()
+    return sd, xr, S0r, yr, st
+
+
+@pytest.mark.parametrize("T", [150, 1])
+@pytest.mark.parametrize("delta", [False, True])
+def test_torch_path_forward_backward_fp32(delta, T):
+    """kernel=False (T = 150), and a T = 1 call under autograd (which takes the torch path whatever `kernel`
+    says, `src/assoc.py:411`): output, final state and the gradients of x, S0 and every parameter at 1e-4."""
+    from pragnosia_amd.assoc import AssocCarrier
+    torch.manual_seed(60 + delta)
+    g = torch.Generator().manual_seed(60 + delta + T)
+    mod = AssocCarrier(128, delta=delta, kernel=(T == 1))
+    _randomise(mod, g)
+    mod = mod.cuda()
+    x = torch.randn(2, T, 128, generator=g)
+    S0 = torch.randn(2, 2, 64, 64, generator=g) * 0.2
+    wo, wS = torch.randn(2, T, 128, generator=g), torch.randn(2, 2, 64, 64, generator=g)
+    sd, xr, S0r, yr, (Sr, _) = _oracle_grads(mod, x, S0, 37, wo, wS, delta)
+    xk, S0k = x.cuda().requires_grad_(True), S0.cuda().requires_grad_(True)
+    yk, (Sk, Tk) = mod(xk, (S0k, 37))
+    assert Tk == T and Sk.dtype == torch.float32
+    ((yk - xk) * wo.cuda()).sum().add((Sk * wS.cuda()).sum()).backward()
+    errs = {"y": rel(yk - xk, yr - xr), "S": rel(Sk, Sr), "dx": rel(xk.grad, xr.grad), "dS0": rel(S0k.grad, S0r.grad)}
+    errs.update(_block_errors(mod, sd))
+    assert max(errs.values()) < 1e-4, errs
+
+
+@pytest.mark.parametrize("kernel", [False, True])
+@pytest.mark.parametrize("delta", [False, True])
+def test_short_conv_carrier(delta, kernel):
+    """add_short_conv (`src/assoc.py:361-382`): with random convolution weights, one pass and two calls carrying
+    (S, T, cache), and (kernel=False) token-at-a-time decode steps, against the oracle; gradients (kernel=False)
+    including the convolution weight's. The identity initialisation leaves the carrier's function unchanged."""
+    from pragnosia_amd.assoc import AssocCarrier
+    torch.manual_seed(70 + delta)
+    g = torch.Generator().manual_seed(70 + delta + 2 * kernel)
+    mod = AssocCarrier(128, delta=delta, kernel=kernel)
+    _randomise(mod, g)
+    mod = mod.cuda()
+    x = torch.randn(2, 90, 128, generator=g)
+    with torch.no_grad():
+        y_plain, (S_plain, _) = mod(x.cuda())
+        mod.add_short_conv(4)
+        y_id, (S_id, _, _) = mod(x.cuda())
+    tol_o = 1e-4 if not kernel else 2e-2
+    assert rel(y_id - x.cuda(), y_plain - x.cuda()) < tol_o and rel(S_id, S_plain) < tol_o
+    with torch.no_grad():
+        mod.sconv.copy_(torch.randn(mod.sconv.shape, generator=g) * 0.5)
+    S0 = torch.randn(2, 2, 64, 64, generator=g) * 0.2
+    cc = torch.randn(2, 3 * 128, 3, generator=g)
+    wo, wS = torch.randn(2, 90, 128, generator=g), torch.randn(2, 2, 64, 64, generator=g)
+    sd, xr, S0r, yr, (Sr, _, ccr) = _oracle_grads(mod, x, S0, 11, wo, wS, delta, cc)
+    xk, S0k = x.cuda().requires_grad_(True), S0.cuda().requires_grad_(True)
+    yk, (Sk, Tk, cck) = mod(xk, (S0k, 11, cc.cuda()))
+    assert Tk == 90 and rel(cck, ccr) < 1e-5
+    ((yk - xk) * wo.cuda()).sum().add((Sk * wS.cuda()).sum()).backward()
+    assert rel(yk - xk, yr - xr) < tol_o and rel(Sk, Sr) < tol_o
+    if not kernel:
+        errs = {"dx": rel(xk.grad, xr.grad), "dS0": rel(S0k.grad, S0r.grad)}
+        errs.update(_block_errors(mod, sd))
+        assert max(errs.values()) < 1e-4, errs
+    else:
+        assert rel(xk.grad, xr.grad) < 5e-2 and rel(mod.sconv.grad, sd["sconv"].grad) < 5e-2
+    with torch.no_grad():
+        a, st = mod(x[:, :40].cuda(), (S0.cuda(), 11, cc.cuda()))
+        b, st = mod(x[:, 40:].cuda(), st)
+        assert rel(torch.cat([a, b], 1) - x.cuda(), yr.detach() - xr.detach()) < tol_o
+        if not kernel:
+            st, outs = (S0.cuda(), 11, cc.cuda()), []
+            for t in range(90):
+                o, st = mod(x[:, t:t + 1].cuda(), st)
+                outs.append(o)
+            assert rel(torch.cat(outs, 1) - x.cuda(), yr.detach() - xr.detach()) < 1e-4
+            # the stepped state is in the last call's positions (its token at 0), the one-pass state has its last
+            # token at 89: rotating the latter's keys by -89 theta re-expresses it
+            assert rel(st[0], OA.rebase(Sr.detach(), sd["theta"].detach(), 89.0)) < 1e-4
+
+
+@pytest.mark.parametrize("mixer", ["hdspin", "sdspin", "aspin1", "hspin1"])
+def test_head_dim_128_mixers_lm(mixer):
+    """The reference's head-dim-128 carriers (`src/model.py:650-660`) in a small LM (d 256: two heads of 128):
+    forward and forward_carried logits against the oracle (fp32: the delta rule at head dim 128 runs the exact
+    scan; hspin1 the bf16 kernels), a finite backward, and the graphed greedy decode equal to the eager loop."""
+    from pragnosia_amd.decode import GreedyDecoder, greedy_eager
+    from pragnosia_amd.model import LM
+    torch.manual_seed(80)
+    g = torch.Generator().manual_seed(80)
+    lm = LM(vocab=300, d=256, layers=2, mlp_mult=2, ctx=48, mixer=mixer)
+    with torch.no_grad():
+        lm.e.weight.mul_(10)
+    sd = {k: v.detach().double() for k, v in lm.state_dict().items()}
+    lm = lm.cuda()
+    ids = torch.randint(0, 300, (2, 100), generator=g)
+    tol = 1e-4 if mixer != "hspin1" else 2e-2
+    with torch.no_grad():
+        lg = lm(ids[:, :48].cuda())
+        lc = lm.forward_carried(ids.cuda(), window=48)
+    ref = M.lm_forward(sd, ids[:, :48], layers=2, mixer=mixer, heads=2)
+    refc = M.lm_forward_carried(sd, ids, 48, layers=2, mixer=mixer, heads=2)
+    assert rel(lg, ref) < tol and rel(lc, refc) < tol, (rel(lg, ref), rel(lc, refc))
+    loss = torch.nn.functional.cross_entropy(lm(ids[:, :48].cuda()).reshape(-1, 300), ids[:, 1:49].reshape(-1).cuda())
+    loss.backward()
+    assert all(torch.isfinite(p.grad).all() for p in lm.parameters() if p.grad is not None)
+    lm.eval()
+    dec = GreedyDecoder(lm, 2, steps_per_graph=4)
+    assert not dec.fused
+    toks_g = dec.generate(ids[:, :30].cuda(), 12)
+    toks_e, _ = greedy_eager(lm, ids[:, :30].cuda(), 12)
+    assert torch.equal(toks_g, toks_e)

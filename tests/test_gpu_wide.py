@@ -66,10 +66,9 @@ def test_wide_carrier_forward_backward():
         assert e < TOL_GRAD, (blk, e)
 
 
-def test_wide_carrier_decode_step_and_delta_rejected():
+def test_wide_carrier_decode_step():
     """T = 1 without autograd: rebase by p0 (host int and device scalar), normalise, gate, write, read, in fp32,
-    against the oracle's T = 1 call. The delta rule at head dim 128 has no kernel yet and says so."""
-    from pragnosia_amd._lib import PragnosiaError
+    against the oracle's T = 1 call; the delta rule at head dim 128 (hdspin) likewise, on the exact fp32 scan."""
     from pragnosia_amd.assoc import AssocCarrier
     torch.manual_seed(61)
     g = torch.Generator().manual_seed(61)
@@ -86,8 +85,13 @@ def test_wide_carrier_decode_step_and_delta_rejected():
     assert Tk == 1 and float(Td) == 1.0
     assert rel(yk - x.cuda(), yr - x.double()) < 1e-4 and rel(Sk, Sr) < 1e-4
     assert rel(yd, yk) < 1e-6 and rel(Sd, Sk) < 1e-6
-    with pytest.raises(PragnosiaError, match="head dim 128"):
-        AssocCarrier(256, delta=True, head_dim=128).cuda()(x.cuda())
+    mod_d = AssocCarrier(256, delta=True, head_dim=128)
+    _randomise(mod_d, g)
+    mod_d = mod_d.cuda()
+    yr2, (Sr2, _) = M.assoc_carrier(_sd64(mod_d), x.double(), (S0.double(), 33), heads=2, delta=True)
+    with torch.no_grad():
+        yk2, (Sk2, _) = mod_d(x.cuda(), (S0.cuda(), 33))
+    assert rel(yk2 - x.cuda(), yr2 - x.double()) < 1e-4 and rel(Sk2, Sr2) < 1e-4
 
 
 def _lm_wide(seed):

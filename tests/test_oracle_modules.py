@@ -206,3 +206,49 @@ def test_greedy_decode_pin_is_observable(monkeypatch):
     monkeypatch.setattr(M, "assoc_carrier", no_rebase)
     _, lgs_bad = M.greedy_decode(sd, prompt, 12, layers=2, mixer="aspin", heads=2, forced=toks)
     assert (lgs_bad[:, 1:] - ref[:, 1:]).abs().max() > 1e-3
+
+
+def test_short_conv_pins():
+    """`oracle.modules.short_conv` (`src/assoc.py:374-382`): a single tap at index K - 1 - s is the input delayed by
+    s tokens (zeros before the start), so the identity weight (all on the last tap) is no convolution, and the last
+    K - 1 inputs carried as the cache make two calls equal one."""
+    g = torch.Generator().manual_seed(9)
+    B, T, D, K = 2, 11, 5, 4
+    qo, ko, vo = (torch.randn(B, T, D, generator=g) for _ in range(3))
+    for s in range(K):
+        w = torch.zeros(3 * D, K)
+        w[:, K - 1 - s] = 1.0
+        q2, k2, v2, _ = M.short_conv(w, qo, ko, vo, None)
+        for a, b in ((q2, qo), (k2, ko), (v2, vo)):
+            assert torch.equal(a[:, s:], b[:, :T - s]) and not a[:, :s].any()
+    w = torch.randn(3 * D, K, generator=g)
+    full = M.short_conv(w, qo, ko, vo, None)
+    a = M.short_conv(w, qo[:, :6], ko[:, :6], vo[:, :6], None)
+    b = M.short_conv(w, qo[:, 6:], ko[:, 6:], vo[:, 6:], a[3])
+    for i in range(3):
+        assert (torch.cat([a[i], b[i]], 1) - full[i]).abs().max() < 1e-12
+    assert torch.equal(b[3], full[3])
+
+
+@pytest.mark.parametrize("delta", [False, True])
+def test_carrier_with_short_conv_carries_and_reduces_to_plain(delta):
+    """The carrier with the convolution: identity weights give the carrier without it; with random weights two
+    calls carrying (S, T, cache) equal one pass, and token-at-a-time calls reproduce it."""
+    g = torch.Generator().manual_seed(10)
+    sd = assoc_sd(16, 2, delta, g)
+    x = torch.randn(2, 30, 16, generator=g)
+    ident = torch.zeros(48, 4)
+    ident[:, -1] = 1.0
+    y0, (S0, _) = M.assoc_carrier(sd, x, heads=2, delta=delta)
+    y1, (S1, _, _) = M.assoc_carrier(dict(sd, sconv=ident), x, heads=2, delta=delta)
+    assert (y1 - y0).abs().max() < 1e-12 and (S1 - S0).abs().max() < 1e-12
+    sdc = dict(sd, sconv=torch.randn(48, 4, generator=g) * 0.5)
+    full, (S, T, cc) = M.assoc_carrier(sdc, x, heads=2, delta=delta)
+    a, st = M.assoc_carrier(sdc, x[:, :13], heads=2, delta=delta)
+    b, (S2, T2, cc2) = M.assoc_carrier(sdc, x[:, 13:], st, heads=2, delta=delta)
+    assert (torch.cat([a, b], 1) - full).abs().max() < 1e-10 and torch.equal(cc2, cc)
+    st, outs = None, []
+    for t in range(30):
+        o, st = M.assoc_carrier(sdc, x[:, t:t + 1], st, heads=2, delta=delta)
+        outs.append(o)
+    assert (torch.cat(outs, 1) - full).abs().max() < 1e-10
