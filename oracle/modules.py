@@ -53,7 +53,7 @@ def short_conv(sconv, qo, ko, vo, cc):
 
 
 def assoc_carrier(sd, x, h0=None, pos0=0, *, heads, delta=False, write_all=False, key_topk=0, la_floor=None,
-                  chunk=64, pos_wrap=None):
+                  chunk=64, pos_wrap=None, beta_scale=None):
     """AssocCarrier.forward, torch path (`src/assoc.py:384-512`, kernel=False, no fused projections), with the short
     convolution when sd holds "sconv". h0 = (S, p0), (S, p0, cache) with the convolution, or None. Returns
     (out, (S, T)) or (out, (S, T, cache))."""
@@ -84,6 +84,8 @@ def assoc_carrier(sd, x, h0=None, pos0=0, *, heads, delta=False, write_all=False
     beta = None
     if delta:
         beta = torch.sigmoid(_lin(z, sd, "wb")).transpose(1, 2)
+        if beta_scale is not None:  # a diagnostic multiplier on the write strength, (B, H, T) (`src/assoc.py:469-472`)
+            beta = beta * beta_scale.to(beta.dtype)
         if write_all:
             beta = beta.clamp(min=0.75)
     o, S = A_.assoc_scan(q, k, v, la, S0, chunk=chunk, beta=beta)

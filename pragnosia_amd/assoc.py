@@ -144,6 +144,9 @@ def _rebase_wide(S, theta, p_dev, p_host):
 
 
 def _positions(T, device, wrap=None):
+    if torch.compiler.is_compiling():  # traced code builds the tensor in the graph rather than caching it
+        pos = torch.arange(T, device=device, dtype=torch.int64)
+        return pos % wrap if wrap else pos
     key = (T, str(device), wrap)
     pos = _POS_CACHE.get(key)
     if pos is None:
@@ -277,7 +280,7 @@ class AssocCarrier(nn.Module):
     def logalpha(self, z):
         """la = -softplus(W_a z + b) exp(A_h) <= 0 per (b, t, h), floored per head when hl_floor
         (`src/assoc.py:355-359`)."""
-        la = -F.softplus(self.wa(z)) * torch.exp(self.A)
+        la = -F.softplus(_op_mod.linear(z, self.wa)) * torch.exp(self.A)
         return la.clamp(min=self.la_floor) if self.hl_floor else la
 
     def add_short_conv(self, K: int):
@@ -315,14 +318,14 @@ class AssocCarrier(nn.Module):
         else:
             qo, ko, vo = self.q(z), self.k(z), self.v(z)
             la = self.logalpha(z)
-            bt = torch.sigmoid(self.wb(z)) if self.delta else None
+            bt = torch.sigmoid(_op_mod.linear(z, self.wb)) if self.delta else None
         if getattr(self, "sconv", None) is not None:
             qo, ko, vo, cc = self._sconv(qo, ko, vo, cc)
         kp = ko.view(B, T, self.h, self.dk)
         if self.key_topk:
             keep = torch.zeros_like(kp).scatter_(-1, kp.abs().topk(self.key_topk, dim=-1).indices, 1.0)
             kp = kp * keep
-        gate = None if (self.delta or self.write_all) else self.wi(z)
+        gate = None if (self.delta or self.write_all) else _op_mod.linear(z, self.wi)
         if bt is not None:
             if getattr(self, "beta_scale", None) is not None:
                 bt = bt * self.beta_scale.transpose(1, 2).to(bt.dtype)

@@ -25,6 +25,7 @@ import torch.utils.checkpoint
 
 from ._lib import PragnosiaError
 from .assoc import AssocCarrier
+from .ops import linear
 from .spin import SpinCarrier
 
 MIXERS = {
@@ -48,7 +49,8 @@ class MLP(nn.Module):
         self.b = nn.Linear(mult * d, d)
 
     def forward(self, x):
-        return x + self.b(F.gelu(self.a(self.n(x))))
+        # the biases' gradients as GEMMs, so a captured training step records no memset (ops.linear)
+        return x + linear(F.gelu(linear(self.n(x), self.a)), self.b)
 
 
 class LM(nn.Module):

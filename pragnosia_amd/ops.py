@@ -11,6 +11,7 @@ import ctypes
 from typing import Optional
 
 import torch
+import torch.nn.functional as F
 from torch import Tensor
 
 from ._lib import PragnosiaError, check, lib
@@ -33,6 +34,47 @@ def _require_gpu(*ts: Optional[Tensor]) -> None:
 
 def _f32(t: Optional[Tensor]) -> Optional[Tensor]:
     return None if t is None else t.to(torch.float32).contiguous()
+
+
+def colsum(x: Tensor) -> Tensor:
+    """Sum over the first dimension, as a GEMM against a ones vector. torch's column sum over many rows is a
+    multi-block reduction that zeroes its semaphores with a memset, and memset nodes captured in a HIP graph have
+    given wrong results on replays after the first on this ROCm stack; a GEMM records none. Same function, the terms
+    summed in another order."""
+    rows = x.shape[0]
+    x2 = x.reshape(rows, -1)
+    return (torch.ones(1, rows, device=x.device, dtype=x2.dtype) @ x2).reshape(x.shape[1:])
+
+
+class _Linear(torch.autograd.Function):
+    """F.linear(x, W, b) with its bias gradient formed by `colsum` (a GEMM) instead of torch's column sum, so a
+    backward captured in a HIP graph records no memset node; the other gradients are the usual two GEMMs. Runs in the
+    autocast dtype like F.linear."""
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda")
+    def forward(ctx, x, W, b):
+        ctx.save_for_backward(x, W)
+        ctx.b_dtype = None if b is None else b.dtype
+        return F.linear(x, W, b)
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, g):
+        x, W = ctx.saved_tensors
+        g2 = g.reshape(-1, g.shape[-1])
+        cdt = g2.dtype
+        gx = (g2 @ W.to(cdt)).reshape(x.shape).to(x.dtype) if ctx.needs_input_grad[0] else None
+        gW = (g2.t() @ x.reshape(-1, x.shape[-1]).to(cdt)).to(W.dtype) if ctx.needs_input_grad[1] else None
+        gb = colsum(g2).to(ctx.b_dtype) if (ctx.b_dtype is not None and ctx.needs_input_grad[2]) else None
+        return gx, gW, gb
+
+
+def linear(x: Tensor, mod) -> Tensor:
+    """`mod(x)` for an nn.Linear `mod`, with a graph-capturable bias gradient (see _Linear)."""
+    if mod.bias is None or not torch.is_grad_enabled():
+        return F.linear(x, mod.weight, mod.bias)
+    return _Linear.apply(x, mod.weight, mod.bias)
 
 
 def _expect(op: str, dev, **shapes) -> None:
@@ -177,7 +219,7 @@ def aspin_out_bwd(gy: Tensor, o: Tensor, weight: Tensor, rstd: Tensor) -> tuple[
     part = torch.empty(n, D, device=o.device, dtype=torch.float32)
     check(lib().pragnosia_aspin_out_bwd(_ptr(gy), int(gy.dtype == torch.bfloat16), _ptr(o), _ptr(weight), _ptr(rstd),
                                         _ptr(dO), _ptr(part), B, H, T, D, _stream(o)), "pragnosia_aspin_out_bwd")
-    return dO, part.sum(0)
+    return dO, colsum(part)
 
 
 @aspin_out_bwd.register_fake
@@ -670,7 +712,7 @@ def aspin_prep_bwd(qp: Tensor, kp: Tensor, vp: Tensor, gate: Optional[Tensor], t
                                          _ptr(dk), _ptr(dv), _ptr(dqp), _ptr(dkp), _ptr(dvp),
                                          _ptr(dgate) if gate is not None else None, _ptr(dth), B, T, H, D, H * D,
                                          int(qp.dtype == torch.bfloat16), _stream(qp)), "pragnosia_aspin_prep_bwd")
-    return dqp, dkp, dvp, dgate, dth.sum(0)
+    return dqp, dkp, dvp, dgate, colsum(dth)
 
 
 @aspin_prep_bwd.register_fake
@@ -802,9 +844,9 @@ def aspin_prep_proj_bwd(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor:
                                               _ptr(dbeta) if has_beta else None, _ptr(dP), _ptr(dth), _ptr(part),
                                               B, T, H, D, int(P.dtype == torch.bfloat16), _stream(P)),
           "pragnosia_aspin_prep_proj_bwd")
-    sums = part.view(B, H, -1, 3).sum((0, 2))
+    sums = colsum(part.view(B, H, -1, 3).transpose(1, 2).reshape(-1, H, 3))
     dxb = sums[:, 0].clone() if (gated or has_beta) else P.new_empty(0, dtype=torch.float32)
-    return dP, sums[:, 1].clone(), sums[:, 2].clone(), dxb, dth.sum(0)
+    return dP, sums[:, 1].clone(), sums[:, 2].clone(), dxb, colsum(dth)
 
 
 @aspin_prep_proj_bwd.register_fake
@@ -875,7 +917,7 @@ def aspin_rebase_bwd(S: Tensor, theta: Tensor, p0_dev: Optional[Tensor], p0: flo
     dth = torch.empty(B, H, D // 2, device=S.device, dtype=torch.float32)
     check(lib().pragnosia_aspin_rebase_bwd(_ptr(S), _ptr(theta), _ptr(p0_dev), float(p0), _ptr(g), _ptr(dS),
                                            _ptr(dth), B, H, D, _stream(S)), "pragnosia_aspin_rebase_bwd")
-    return dS, dth.sum(0)
+    return dS, colsum(dth)
 
 
 @aspin_rebase_bwd.register_fake

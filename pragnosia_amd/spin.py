@@ -11,6 +11,7 @@ import torch
 import torch.nn as nn
 
 from ._lib import PragnosiaError
+from .ops import linear
 from .scan import scan_hip
 
 
@@ -57,10 +58,10 @@ class SpinCarrier(nn.Module):
         z = self.ln(x)
         mag, ang = self.lam()
         # per-token log-magnitude <= 0: the recurrence gate scales the channel's timescale
-        logmag = -self.gate_c * torch.sigmoid(self.Wr(z)) * (-torch.log(mag))
+        logmag = -self.gate_c * torch.sigmoid(linear(z, self.Wr)) * (-torch.log(mag))
         # per-token input normalisation sqrt(1 - |lambda_t|^2), its argument clamped to bound the derivative
         gam = torch.sqrt((1.0 - torch.exp(2.0 * logmag)).clamp_min(1e-6))
-        u = self.B(z) * gam * torch.sigmoid(self.Wi(z))
+        u = self.B(z) * gam * torch.sigmoid(linear(z, self.Wi))
         y, h = scan_hip(u, logmag, ang.expand_as(logmag), h0)
         return x + torch.sigmoid(self.gate) * self.C(y), h
 

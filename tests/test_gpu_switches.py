@@ -1,0 +1,102 @@
+"""The carrier's module switches against the fp64 oracle on the same state_dict: `fused_scan` (no entering states
+kept, `src/assoc.py:518-532`), `FUSED_PROJ` (one GEMM for the delta carrier's five projections, `:272-276`,
+`:415-427`), `key_topk` (`:438-442`), `pos_wrap` (`:406-410`), `beta_scale` (`:469-472`) and `hl_floor` (`:355-359`).
+
+Tolerances: kernel path (bf16 operands) 2e-2 on outputs and states, 5e-2 on gradients; torch path (kernel=False,
+fp32) 1e-4."""
+import math
+
+import pytest
+import torch
+
+from oracle import modules as M
+from test_gpu_modules import _block_errors, _randomise, _sd64, rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _carrier(seed, **kw):
+    from pragnosia_amd.assoc import AssocCarrier
+    torch.manual_seed(seed)
+    g = torch.Generator().manual_seed(seed)
+    mod = AssocCarrier(128, **kw)
+    _randomise(mod, g)
+    return mod.cuda(), g
+
+
+@pytest.mark.parametrize("delta", [False, True])
+def test_fused_scan_context(delta):
+    """Inside fused_scan the carriers keep no entering states (their `sent` is None) and their outputs are
+    unchanged; on exit the previous setting returns."""
+    from pragnosia_amd import assoc as A
+    from pragnosia_amd.model import LM
+    torch.manual_seed(100)
+    lm = LM(vocab=300, d=128, layers=2, ctx=64, mixer="dspin" if delta else "aspin").cuda()
+    ids = torch.randint(0, 300, (2, 64), device="cuda")
+    with torch.no_grad():
+        ref = lm(ids)
+        assert all(mx.sent is not None for mx in lm.mix)
+        with A.fused_scan(lm):
+            assert A.FUSED_SCAN and all(not mx.need_sent for mx in lm.mix)
+            got = lm(ids)
+            assert all(mx.sent is None for mx in lm.mix) or not delta
+        assert not A.FUSED_SCAN and all(mx.need_sent for mx in lm.mix)
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("kernel", [True, False])
+def test_fused_proj_delta(kernel, monkeypatch):
+    """FUSED_PROJ (with this build's own fused plumbing off, so the reference's composition runs): one GEMM for q,
+    k, v, the decay and the write strength; output, state and gradients against the oracle."""
+    from pragnosia_amd import assoc as A
+    monkeypatch.setattr(A, "FUSED_PROJ", True)
+    monkeypatch.setattr(A, "FUSED_PLUMBING", False)
+    mod, g = _carrier(110 + kernel, delta=True, kernel=kernel)
+    _check(mod, g, delta=True, tol=(2e-2, 5e-2) if kernel else (1e-4, 1e-4))
+
+
+def _check(mod, g, delta, tol, T=100, p0=21, **oracle_kw):
+    x = torch.randn(2, T, 128, generator=g)
+    S0 = torch.randn(2, mod.h, 64, 64, generator=g) * 0.2
+    wo, wS = torch.randn(2, T, 128, generator=g), torch.randn(2, mod.h, 64, 64, generator=g)
+    sd = {k: v.clone().requires_grad_(v.is_floating_point()) for k, v in _sd64(mod).items()}
+    xr, S0r = x.double().requires_grad_(True), S0.double().requires_grad_(True)
+    yr, (Sr, _) = M.assoc_carrier(sd, xr, (S0r, p0), heads=mod.h, delta=delta, key_topk=mod.key_topk,
+                                  write_all=mod.write_all, **oracle_kw)
+    ((yr - xr) * wo.double()).sum().add((Sr * wS.double()).sum()).backward()
+    xk, S0k = x.cuda().requires_grad_(True), S0.cuda().requires_grad_(True)
+    yk, (Sk, _) = mod(xk, (S0k, p0))
+    ((yk - xk) * wo.cuda()).sum().add((Sk * wS.cuda()).sum()).backward()
+    t_out, t_grad = tol
+    assert rel(yk - xk, yr - xr) < t_out and rel(Sk, Sr) < t_out
+    assert rel(xk.grad, xr.grad) < t_grad and rel(S0k.grad, S0r.grad) < t_grad
+    for blk, e in _block_errors(mod, sd).items():
+        assert e < t_grad, (blk, e)
+
+
+@pytest.mark.parametrize("kernel", [True, False])
+@pytest.mark.parametrize("delta", [False, True])
+def test_key_topk(delta, kernel):
+    """Sparse keys: only the key_topk largest coordinates of each projected key survive (straight-through)."""
+    mod, g = _carrier(120 + delta + 2 * kernel, delta=delta, key_topk=8, kernel=kernel)
+    _check(mod, g, delta, (2e-2, 5e-2) if kernel else (1e-4, 1e-4))
+
+
+@pytest.mark.parametrize("kernel", [True, False])
+def test_pos_wrap(kernel):
+    """Rotation positions modulo pos_wrap (T = 100 > pos_wrap = 32): the plain carrier against the oracle."""
+    mod, g = _carrier(130 + kernel, kernel=kernel)
+    mod.pos_wrap = 32
+    _check(mod, g, False, (2e-2, 5e-2) if kernel else (1e-4, 1e-4), pos_wrap=32)
+
+
+@pytest.mark.parametrize("kernel", [True, False])
+def test_beta_scale_and_hl_floor(kernel):
+    """The delta carrier with a per-token write-strength multiplier (beta_scale, (B, H, T)) and the half-life floor
+    under each head's decay."""
+    mod, g = _carrier(140 + kernel, delta=True, hl_floor=True, kernel=kernel)
+    bs = torch.rand(2, mod.h, 100, generator=g)
+    mod.beta_scale = bs.cuda()
+    floor = (-math.log(2.0) / torch.logspace(math.log10(8.0), math.log10(131072.0), mod.h)).double()
+    assert torch.allclose(mod.la_floor.cpu().double(), floor)
+    _check(mod, g, True, (2e-2, 5e-2) if kernel else (1e-4, 1e-4), la_floor=floor, beta_scale=bs.double())
