@@ -290,7 +290,9 @@ int pragnosia_aspin_decode_step(const float* S, float* S_out, const float* qp, c
  * their columns (the other -1). Forms la = -softplus(logit + la_bias[h]) exp(A[h]) (floored at la_floor[h] when
  * non-NULL), the gate logit + gate_bias[h], beta = max(sigmoid(logit + beta_bias[h]), beta_min), then runs the step of
  * pragnosia_aspin_decode_step (S_out may equal S: in place) and writes the output per-head RMS-normalised and
- * token-major: o[b][h D + j] = (o_j r) on_weight[j], r = 1 / sqrt(mean_j o_j^2 + on_eps). Replaces, inside the
+ * token-major: o[b][h D + j] = (o_j r) on_weight[j], r = 1 / sqrt(mean_j o_j^2 + on_eps); with on_weight NULL the
+ * output is written raw, o[b][h D + j] = o_j (four workgroups per head; the consumer applies the RMSNorm, e.g.
+ * pragnosia_decode_gemv_rms). Replaces, inside the
  * reference's graphed decode (src/bench.py:241-317), the T = 1 path of `AssocCarrier.forward` from its projections
  * to `self.on(o).transpose(1, 2).reshape(B, T, D)` (src/assoc.py:384-505). */
 int pragnosia_aspin_decode_proj(const float* S, float* S_out, const float* P, int64_t np, int64_t la_col,
@@ -308,6 +310,15 @@ int pragnosia_aspin_decode_proj(const float* S, float* S_out, const float* P, in
 int pragnosia_decode_gemv(const float* x, int64_t B, int64_t K, const float* ln_weight, const float* ln_bias,
                           float ln_eps, const float* W, int64_t N, const float* bias, const float* scale, int act,
                           const float* resid, float* y, void* stream);
+
+/* pragnosia_decode_gemv with the carrier's per-head RMSNorm on its input instead of a LayerNorm: z[b][h 64 + j] =
+ * x[b][h 64 + j] r_{b,h} rms_weight[j], r = 1 / sqrt(mean_j x[b][h 64 + j]^2 + rms_eps), then y = act(scale (W z) +
+ * bias) + resid. For B <= 4 and K a multiple of 256 up to 1024 (PRAGNOSIA_ERR_UNSUPPORTED otherwise). Replaces
+ * `self.on(o)` and the gated o-projection with the residual of the carrier's T = 1 step (src/assoc.py:505-511),
+ * reading the raw output of pragnosia_aspin_decode_proj (on_weight NULL). */
+int pragnosia_decode_gemv_rms(const float* x, int64_t B, int64_t K, const float* rms_weight, float rms_eps,
+                              const float* W, int64_t N, const float* bias, const float* scale, int act,
+                              const float* resid, float* y, void* stream);
 
 #ifdef __cplusplus
 }

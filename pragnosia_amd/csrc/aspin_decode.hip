@@ -143,6 +143,91 @@ __global__ __launch_bounds__(256) void aspin_decode(const float* S, float* Sout,
   }
 }
 
+// The same step from one projection output P (FROM_P inputs), split four ways per head over value columns for
+// latency: workgroup (b, h, quarter) owns value columns 16 quarter .. 16 quarter + 15, thread (jj, rg) column
+// 16 quarter + jj and key rows 4 rg .. 4 rg + 3 (two rotation pairs). Every global load (the projections, the state
+// slice, theta, p0, the gate parameters) is issued at the start; the key-row reductions (the delta read and the
+// output) go through LDS. The output is written raw, token-major o[b][h 64 + j] (the per-head RMSNorm is applied by
+// the consumer, pragnosia_decode_gemv_rms). Four times the workgroups of aspin_decode, and no dependent load chain.
+__global__ __launch_bounds__(256) void aspin_decode_split(const float* S, float* Sout, StepIn in,
+                                                          const float* __restrict__ theta,
+                                                          const float* __restrict__ p0d, float p0h,
+                                                          float* __restrict__ o, int H) {
+  __shared__ float qs[D], ks[D], vs[D];
+  __shared__ float red[16][17];
+  const int bhq = blockIdx.x, qtr = bhq & 3, bh = bhq >> 2, h = bh % H, b = bh / H;
+  const int tid = threadIdx.x, jj = tid & 15, rg = tid >> 4;
+  const int j = 16 * qtr + jj;
+  const float* prow = in.P + (size_t)b * in.np;
+  // independent loads first
+  const float* Sbh = S + (size_t)bh * D * D;
+  float x[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) x[r] = Sbh[(4 * rg + r) * D + j];
+  const float th0 = theta[h * (D / 2) + 2 * rg], th1 = theta[h * (D / 2) + 2 * rg + 1];
+  const float p0 = p0d ? *p0d : p0h;
+  const float la_logit = prow[in.la_col + h], la_b = in.la_b[h], Ah = in.A[h];
+  const float fl = in.floor ? in.floor[h] : -INFINITY;
+  const bool has_g = in.gate_col >= 0, has_b = in.beta_col >= 0;
+  const float gl = has_g ? prow[in.gate_col + h] + (in.gate_b ? in.gate_b[h] : 0.f) : 0.f;
+  const float bl = has_b ? prow[in.beta_col + h] + (in.beta_b ? in.beta_b[h] : 0.f) : 0.f;
+  float xin = 0.f;
+  if (tid < 3 * D) xin = prow[(tid >> 6) * H * D + h * D + (tid & 63)];
+  // q, k, v unit-normalised (k also gated) by waves 0, 1, 2
+  if (tid < 3 * D) {
+    float n = xin * xin;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) n += __shfl_xor(n, off);
+    float inv = 1.f / fmaxf(sqrtf(n), 1e-12f);
+    if (tid >= D && tid < 2 * D && has_g) inv *= 1.f / (1.f + __expf(-gl));
+    (tid < D ? qs : (tid < 2 * D ? ks : vs))[tid & 63] = xin * inv;
+  }
+  const float la_v = fmaxf(-softplus_(la_logit + la_b) * __expf(Ah), fl);
+  const float a = __expf(la_v);
+  const float be_v = has_b ? fmaxf(1.f / (1.f + __expf(-bl)), in.beta_min) : 0.f;
+  {
+    float s0, c0, s1, c1;
+    sincosf(-p0 * th0, &s0, &c0);
+    sincosf(-p0 * th1, &s1, &c1);
+    const float e0 = x[0], f0 = x[1], e1 = x[2], f1 = x[3];
+    x[0] = a * (e0 * c0 - f0 * s0);
+    x[1] = a * (e0 * s0 + f0 * c0);
+    x[2] = a * (e1 * c1 - f1 * s1);
+    x[3] = a * (e1 * s1 + f1 * c1);
+  }
+  __syncthreads();
+  float wv = vs[j];
+  if (has_b) {
+    float r_ = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) r_ += ks[4 * rg + r] * x[r];
+    red[rg][jj] = r_;
+    __syncthreads();
+    float rd = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) rd += red[g][jj];
+    wv = be_v * (wv - rd);
+    __syncthreads();
+  }
+  float y = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    x[r] += ks[4 * rg + r] * wv;
+    y += x[r] * qs[4 * rg + r];
+  }
+  red[rg][jj] = y;
+  float* Sob = Sout + (size_t)bh * D * D;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) Sob[(4 * rg + r) * D + j] = x[r];
+  __syncthreads();
+  if (rg == 0) {
+    float ov = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) ov += red[g][jj];
+    o[(size_t)b * H * D + h * D + j] = ov;
+  }
+}
+
 }  // namespace
 
 extern "C" int pragnosia_aspin_decode_step(const float* S, float* S_out, const float* qp, const float* kp,
@@ -188,7 +273,12 @@ extern "C" int pragnosia_aspin_decode_proj(const float* S, float* S_out, const f
   in.gate_b = gate_bias;
   in.beta_b = beta_bias;
   in.beta_min = beta_min;
-  hipLaunchKernelGGL(aspin_decode<true>, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, S_out, in,
-                     theta, p0_dev, p0, on_weight, on_eps, o, (int)H);
+  PGN_CHECK_ARG(B * H * 4 < ((int64_t)1 << 31));
+  if (on_weight == nullptr)  // raw output: four workgroups per head
+    hipLaunchKernelGGL(aspin_decode_split, dim3((unsigned)(B * H * 4)), dim3(256), 0, (hipStream_t)stream, S, S_out,
+                       in, theta, p0_dev, p0, o, (int)H);
+  else
+    hipLaunchKernelGGL(aspin_decode<true>, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, S_out, in,
+                       theta, p0_dev, p0, on_weight, on_eps, o, (int)H);
   PGN_RETURN_LAUNCH();
 }

@@ -6,8 +6,9 @@
 // (LayerNorm). Replaces the torch calls of `src/model.py:552-560` and `src/assoc.py:384-512` inside the graphed
 // decode of `src/bench.py:241-317`, one kernel each instead of three to six.
 //
-// At decode batch sizes the weight read is the whole cost (each weight read once per step), so a workgroup owns a
-// few output rows and all B sequences: thread (r, l) reads 16-byte pieces 4 l + 4 LANES i of weight row r (a row
+// At decode batch sizes the weight read is the whole cost (each weight read once per step). Up to 4 sequences (and K
+// a multiple of 256) the one-wave kernel gemv_wave below runs; beyond, a workgroup owns a few output rows and all B
+// sequences: thread (r, l) reads 16-byte pieces 4 l + 4 LANES i of weight row r (a row
 // is read by LANES consecutive lanes, 16 * LANES contiguous bytes per instruction), twelve pieces at a time held in
 // registers (all issued before the first is used), and accumulates 8 sequences at a time; the LayerNorm'd inputs of
 // those 8 sequences sit in LDS. The first weight pieces are loaded before the LayerNorm, whose row is held in
@@ -140,6 +141,207 @@ __global__ __launch_bounds__(256) void gemv(const float* __restrict__ x, int B, 
   }
 }
 
+// Sum over the 64 lanes of a wave of NV values per lane (NV a power of two <= 16): the lanes exchange halves, so the
+// sums take 6 + NV - 1 exchanges instead of 6 NV. Lane l ends with the sum of value l >> (6 - log2 NV) in v[0].
+template <int NV>
+PGN_DEVICE void wave_sum_many(float (&v)[NV], int l) {
+  int len = NV;
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    if (len > 1) {
+      const int half = len / 2;
+      const bool hi = (l & s) != 0;
+#pragma unroll
+      for (int m = 0; m < half; ++m) {
+        const float send = hi ? v[m] : v[m + half];
+        const float keep = hi ? v[m + half] : v[m];
+        v[m] = keep + __shfl_xor(send, s);
+      }
+      len = half;
+    } else {
+      v[0] += __shfl_xor(v[0], s);
+    }
+  }
+}
+
+template <int NV>
+constexpr int log2_of() { return NV == 1 ? 0 : NV == 2 ? 1 : NV == 4 ? 2 : NV == 8 ? 3 : 4; }
+
+// The decode GEMV for B <= 4 sequences and K = 256 KV: one wave per RPW output rows (a one-wave workgroup, so
+// hundreds to thousands of them cover the chip and one round of loads covers the whole weight). Lane l reads the
+// 16-byte pieces 4 l + 256 u of each of its rows, so one load instruction reads 1 KiB contiguous; all RPW KV pieces
+// are issued before the inputs are read. The input is used as is (MODE 0), LayerNorm'd (MODE 1: the wave computes
+// the LayerNorm of every input row itself, the row in registers, two wave reductions), or RMS-normalised per group
+// of 64 channels (MODE 2: the carrier's per-head RMSNorm; a group's 64 channels sit on 16 consecutive lanes of one
+// piece, so its sum of squares is a four-step exchange). No LDS, no barrier. NB = 1 (B = 1) or 4 (B <= 4, rows past
+// B masked).
+template <int RPW, int NB, int KV, int MODE>
+__global__ __launch_bounds__(64) void gemv_wave(const float* __restrict__ x, int B, const float* __restrict__ lnw,
+                                                const float* __restrict__ lnb, float eps, const float* __restrict__ W,
+                                                int N, const float* __restrict__ bias,
+                                                const float* __restrict__ scale, int act,
+                                                const float* __restrict__ resid, float* __restrict__ y) {
+  constexpr int K = 256 * KV;
+  const int l = threadIdx.x;
+  const int n0 = blockIdx.x * RPW;
+  f32x4 w[RPW][KV];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const float* wr = W + (size_t)min(n0 + r, N - 1) * K + 4 * l;
+#pragma unroll
+    for (int u = 0; u < KV; ++u) w[r][u] = *reinterpret_cast<const f32x4*>(wr + 256 * u);
+  }
+  float acc[RPW * NB];
+#pragma unroll
+  for (int m = 0; m < RPW * NB; ++m) acc[m] = 0.f;
+  if constexpr (MODE != 0) {
+    f32x4 z[NB][KV];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int u = 0; u < KV; ++u)
+        z[b][u] = b < B ? *reinterpret_cast<const f32x4*>(x + (size_t)b * K + 4 * l + 256 * u)
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (MODE == 1) {
+      f32x4 g[KV], c[KV];
+#pragma unroll
+      for (int u = 0; u < KV; ++u) {
+        g[u] = *reinterpret_cast<const f32x4*>(lnw + 4 * l + 256 * u);
+        c[u] = lnb ? *reinterpret_cast<const f32x4*>(lnb + 4 * l + 256 * u) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        float s = 0.f;
+#pragma unroll
+        for (int u = 0; u < KV; ++u) s += (z[b][u][0] + z[b][u][1]) + (z[b][u][2] + z[b][u][3]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+        const float mean = s * (1.f / K);
+        float s2 = 0.f;
+#pragma unroll
+        for (int u = 0; u < KV; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float d = z[b][u][e] - mean;
+            s2 += d * d;
+          }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s2 += __shfl_xor(s2, o);
+        const float rs = 1.f / sqrtf(s2 * (1.f / K) + eps);
+#pragma unroll
+        for (int u = 0; u < KV; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) z[b][u][e] = (z[b][u][e] - mean) * rs * g[u][e] + c[u][e];
+      }
+    } else {
+      // channels 4 (l mod 16) .. + 3 of a 64-channel group: the group weight piece is the same for every u
+      const f32x4 g = *reinterpret_cast<const f32x4*>(lnw + 4 * (l & 15));
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int u = 0; u < KV; ++u) {
+          float s = (z[b][u][0] * z[b][u][0] + z[b][u][1] * z[b][u][1]) +
+                    (z[b][u][2] * z[b][u][2] + z[b][u][3] * z[b][u][3]);
+#pragma unroll
+          for (int o = 1; o < 16; o <<= 1) s += __shfl_xor(s, o);
+          const float rs = 1.f / sqrtf(s * (1.f / 64) + eps);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) z[b][u][e] = (z[b][u][e] * rs) * g[e];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int u = 0; u < KV; ++u)
+          acc[r * NB + b] += w[r][u][0] * z[b][u][0] + w[r][u][1] * z[b][u][1] + w[r][u][2] * z[b][u][2] +
+                             w[r][u][3] * z[b][u][3];
+  } else {
+#pragma unroll
+    for (int u = 0; u < KV; ++u)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const f32x4 z = b < B ? *reinterpret_cast<const f32x4*>(x + (size_t)b * K + 4 * l + 256 * u)
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+          acc[r * NB + b] += w[r][u][0] * z[0] + w[r][u][1] * z[1] + w[r][u][2] * z[2] + w[r][u][3] * z[3];
+      }
+  }
+  constexpr int NV = RPW * NB;
+  wave_sum_many<NV>(acc, l);
+  constexpr int sh = 6 - log2_of<NV>();
+  if ((l & ((1 << sh) - 1)) == 0) {
+    const int m = l >> sh, r = m / NB, b = m % NB;
+    const int n = n0 + r;
+    if (n < N && b < B) {
+      float v = (scale ? *scale : 1.f) * acc[0] + (bias ? bias[n] : 0.f);
+      if (act == 1) v = gelu_erf(v);
+      const size_t off = (size_t)b * N + n;
+      if (resid) v += resid[off];
+      y[off] = v;
+    }
+  }
+}
+
+template <int RPW, int NB, int KV, int MODE>
+int launch_wave(const float* x, int B, const float* lnw, const float* lnb, float eps, const float* W, int N,
+                const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
+  hipLaunchKernelGGL((gemv_wave<RPW, NB, KV, MODE>), dim3((unsigned)((N + RPW - 1) / RPW)), dim3(64), 0, st, x, B,
+                     lnw, lnb, eps, W, N, bias, scale, act, resid, y);
+  PGN_RETURN_LAUNCH();
+}
+
+template <int RPW, int NB, int MODE>
+int dispatch_kv(int KV, const float* x, int B, const float* lnw, const float* lnb, float eps, const float* W, int N,
+                const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
+#define PGN_KV(V) return launch_wave<RPW, NB, V, MODE>(x, B, lnw, lnb, eps, W, N, bias, scale, act, resid, y, st)
+  if constexpr (MODE != 0) {
+    switch (KV) {
+      case 1: PGN_KV(1);
+      case 2: PGN_KV(2);
+      case 3: PGN_KV(3);
+      default: PGN_KV(4);
+    }
+  } else {
+    switch (KV) {
+      case 1: PGN_KV(1);
+      case 2: PGN_KV(2);
+      case 3: PGN_KV(3);
+      case 4: PGN_KV(4);
+      case 8: PGN_KV(8);
+      case 12: PGN_KV(12);
+      default: PGN_KV(16);
+    }
+  }
+#undef PGN_KV
+}
+
+template <int RPW, int MODE>
+int dispatch_nb(int KV, const float* x, int B, const float* lnw, const float* lnb, float eps, const float* W, int N,
+                const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
+  return B == 1 ? dispatch_kv<RPW, 1, MODE>(KV, x, B, lnw, lnb, eps, W, N, bias, scale, act, resid, y, st)
+                : dispatch_kv<RPW, 4, MODE>(KV, x, B, lnw, lnb, eps, W, N, bias, scale, act, resid, y, st);
+}
+
+template <int MODE>
+int dispatch_rpw(int KV, const float* x, int B, const float* lnw, const float* lnb, float eps, const float* W,
+                 int N, const float* bias, const float* scale, int act, const float* resid, float* y,
+                 hipStream_t st) {
+  // at least ~1000 one-wave workgroups where the rows allow (four per compute unit), up to 4 rows a wave
+  if (N <= 1024) return dispatch_nb<1, MODE>(KV, x, B, lnw, lnb, eps, W, N, bias, scale, act, resid, y, st);
+  if (N <= 4096) return dispatch_nb<2, MODE>(KV, x, B, lnw, lnb, eps, W, N, bias, scale, act, resid, y, st);
+  return dispatch_nb<4, MODE>(KV, x, B, lnw, lnb, eps, W, N, bias, scale, act, resid, y, st);
+}
+
+bool wave_shape_ok(int64_t B, int64_t K, bool ln) {
+  if (B > 4 || K % 256) return false;
+  const int64_t KV = K / 256;
+  if (ln) return KV >= 1 && KV <= 4;
+  return (KV >= 1 && KV <= 4) || KV == 8 || KV == 12 || KV == 16;
+}
+
 }  // namespace
 
 extern "C" int pragnosia_decode_gemv(const float* x, int64_t B, int64_t K, const float* ln_weight,
@@ -153,6 +355,12 @@ extern "C" int pragnosia_decode_gemv(const float* x, int64_t B, int64_t K, const
   PGN_CHECK_ARG(y != x && (resid == nullptr || resid != y));
   PGN_CHECK_ARG(((uintptr_t)x | (uintptr_t)W | (uintptr_t)ln_weight | (uintptr_t)ln_bias) % 16 == 0);
   hipStream_t st = (hipStream_t)stream;
+  const bool ln = ln_weight != nullptr;
+  if (wave_shape_ok(B, K, ln))
+    return ln ? dispatch_rpw<1>((int)(K / 256), x, (int)B, ln_weight, ln_bias, ln_eps, W, (int)N, bias, scale, act,
+                                resid, y, st)
+              : dispatch_rpw<0>((int)(K / 256), x, (int)B, ln_weight, ln_bias, ln_eps, W, (int)N, bias, scale, act,
+                                resid, y, st);
   const unsigned tiles = (unsigned)std::min<int64_t>((B + BT - 1) / BT, 65535);  // one workgroup row per 8 sequences
   if (N < 2048 || K > 768) {  // 64 lanes a row: more workgroups for narrow outputs, fewer chunks for long rows
     hipLaunchKernelGGL(gemv<64>, dim3((unsigned)((N + 3) / 4), tiles), dim3(256), 0, st, x, (int)B, (int)K, ln_weight,
@@ -162,4 +370,17 @@ extern "C" int pragnosia_decode_gemv(const float* x, int64_t B, int64_t K, const
                        ln_bias, ln_eps, W, (int)N, bias, scale, act, resid, y);
   }
   PGN_RETURN_LAUNCH();
+}
+
+extern "C" int pragnosia_decode_gemv_rms(const float* x, int64_t B, int64_t K, const float* rms_weight, float rms_eps,
+                                         const float* W, int64_t N, const float* bias, const float* scale, int act,
+                                         const float* resid, float* y, void* stream) {
+  PGN_CHECK_ARG(x && W && y && rms_weight && B > 0 && K > 0 && N > 0);
+  PGN_CHECK_ARG(B * N < ((int64_t)1 << 31) && B * K < ((int64_t)1 << 31));
+  PGN_CHECK_ARG(act == 0 || act == 1);
+  PGN_CHECK_ARG(y != x && (resid == nullptr || resid != y));
+  PGN_CHECK_ARG(((uintptr_t)x | (uintptr_t)W | (uintptr_t)rms_weight) % 16 == 0);
+  if (!wave_shape_ok(B, K, true)) return PRAGNOSIA_ERR_UNSUPPORTED;
+  return dispatch_rpw<2>((int)(K / 256), x, (int)B, rms_weight, nullptr, rms_eps, W, (int)N, bias, scale, act, resid,
+                         y, (hipStream_t)stream);
 }

@@ -26,9 +26,10 @@ from .assoc import AssocCarrier
 
 
 # The fused step's dense layers run as the batched GEMV kernel (each weight read once a step) up to this many
-# sequences; beyond it as torch GEMMs (matrix cores), the carrier step still fused. Measured on the 12-layer d768 LM,
-# ms a step (GEMV / torch GEMMs, both with the fused step): batch 1 0.45 / 0.77, 4 0.71 / 0.75, 8 1.06 / 0.76,
-# 32 1.18 / 0.85, 64 2.05 / 0.83; the unfused step with torch GEMMs: 1.45-1.57.
+# sequences; beyond it as torch GEMMs (matrix cores), the carrier step still fused. Measured on the 12-layer d768 LM
+# with the earlier 256-thread GEMV, ms a step (GEMV / torch GEMMs, both with the fused step): batch 1 0.45 / 0.77,
+# 4 0.71 / 0.75, 8 1.06 / 0.76, 32 1.18 / 0.85, 64 2.05 / 0.83; the unfused step with torch GEMMs: 1.45-1.57. The
+# one-wave GEMV (up to 4 sequences) and the split carrier step bring batch 1 to 0.31.
 GEMV_MAX_BATCH = 4
 
 
@@ -142,15 +143,21 @@ class GreedyDecoder:
     def _one_step_fused(self):
         m, op = self.m, torch.ops.pragnosia
         h = (m.e(self.tok) + m.p(self.pos)).reshape(self.B, -1)
+        # at small batches the per-head RMSNorm moves into the o-projection's GEMV, so the carrier step can run four
+        # workgroups per head (decode_gemv_rms needs d a multiple of 256, at most 1024)
+        rms_in_gemv = self.B <= GEMV_MAX_BATCH and m.d % 256 == 0 and m.d <= 1024
         for i, (mx, mp) in enumerate(zip(m.mix, m.mlp)):
             gated = not (mx.delta or mx.write_all)
             P = self._dense(h, self.wcat[i], mx.ln)
+            on_eps = mx.on.eps if mx.on.eps is not None else torch.finfo(torch.float32).eps
             o = op.aspin_decode_proj_(self.st[i][0], P, mx.h, mx.wa.bias, mx.A,
                                       mx.la_floor if mx.hl_floor else None, mx.wi.bias if gated else None,
                                       mx.wb.bias if mx.delta else None, 0.75 if (mx.delta and mx.write_all) else 0.0,
-                                      gated, mx.theta, self.p0s[i:i + 1], 0.0, mx.on.weight,
-                                      mx.on.eps if mx.on.eps is not None else torch.finfo(torch.float32).eps)
-            if self.B <= GEMV_MAX_BATCH:
+                                      gated, mx.theta, self.p0s[i:i + 1], 0.0,
+                                      None if rms_in_gemv else mx.on.weight, on_eps)
+            if rms_in_gemv:
+                x1 = op.decode_gemv_rms(o, mx.o.weight, mx.on.weight, on_eps, None, self.sig[i], 0, h)
+            elif self.B <= GEMV_MAX_BATCH:
                 x1 = self._dense(o, mx.o.weight, None, scale=self.sig[i], resid=h)
             else:  # h + o (sigmoid(g) W_o)^T in one GEMM
                 x1 = torch.addmm(h, o, self.wos[i].t())

@@ -1003,14 +1003,41 @@ def _(x, W, ln_weight, ln_bias, ln_eps, bias, scale, act, resid):
     return x.new_empty(x.shape[0], W.shape[0], dtype=torch.float32)
 
 
+@torch.library.custom_op("pragnosia::decode_gemv_rms", mutates_args=())
+def decode_gemv_rms(x: Tensor, W: Tensor, rms_weight: Tensor, rms_eps: float, bias: Optional[Tensor],
+                    scale: Optional[Tensor], act: int, resid: Optional[Tensor]) -> Tensor:
+    """y (B, N) = act(scale * (W z) + bias) + resid with z the per-64-channel-group RMSNorm of x (B, K) with
+    rms_weight (64,): the carrier's per-head RMSNorm and gated o-projection of one decode step, for B <= 4 and K a
+    multiple of 256 up to 1024. All fp32. Not differentiable."""
+    _require_gpu(x, W, rms_weight, bias, scale, resid)
+    if x.dim() != 2 or W.dim() != 2 or W.shape[1] != x.shape[1]:
+        raise PragnosiaError(f"decode_gemv_rms: x {tuple(x.shape)} and W {tuple(W.shape)} must be (B, K) and (N, K)")
+    B_, K_, N_ = x.shape[0], x.shape[1], W.shape[0]
+    _expect("decode_gemv_rms", x.device, W=(W, (N_, K_)), rms_weight=(rms_weight, (64,)), bias=(bias, (N_,)),
+            scale=(scale, ()), resid=(resid, (B_, N_)))
+    x, W, rms_weight = _f32(x), _f32(W), _f32(rms_weight)
+    bias, scale, resid = _f32(bias), _f32(scale), _f32(resid)
+    y = torch.empty(B_, N_, device=x.device, dtype=torch.float32)
+    check(lib().pragnosia_decode_gemv_rms(_ptr(x), B_, K_, _ptr(rms_weight), float(rms_eps), _ptr(W), N_, _ptr(bias),
+                                          _ptr(scale), int(act), _ptr(resid), _ptr(y), _stream(x)),
+          "pragnosia_decode_gemv_rms")
+    return y
+
+
+@decode_gemv_rms.register_fake
+def _(x, W, rms_weight, rms_eps, bias, scale, act, resid):
+    return x.new_empty(x.shape[0], W.shape[0], dtype=torch.float32)
+
+
 @torch.library.custom_op("pragnosia::aspin_decode_proj_", mutates_args=("S",))
 def aspin_decode_proj_(S: Tensor, P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Optional[Tensor],
                        gate_bias: Optional[Tensor], beta_bias: Optional[Tensor], beta_min: float, gated: bool,
-                       theta: Tensor, p0_dev: Optional[Tensor], p0: float, on_weight: Tensor,
+                       theta: Tensor, p0_dev: Optional[Tensor], p0: float, on_weight: Optional[Tensor],
                        on_eps: float) -> Tensor:
     """The carrier's recurrent step from one projection GEMV's output P (B, 3 H 64 + H [+ H]) (q, k, v, decay
     logits, then the write-gate (gated) or write-strength logits), updating the carried state S (B, H, 64, 64) fp32 in
-    place. Returns the output RMS-normalised per head with on_weight and token-major, (B, H * 64) fp32."""
+    place. Returns the output token-major, (B, H * 64) fp32: RMS-normalised per head with on_weight, or raw when
+    on_weight is None (four workgroups per head; decode_gemv_rms then applies the RMSNorm)."""
     _require_gpu(S, P, la_bias, A, theta, on_weight)
     if not (S.is_contiguous() and S.dtype == torch.float32):
         raise PragnosiaError("aspin_decode_proj_: the state must be a contiguous fp32 tensor (it is updated in place)")

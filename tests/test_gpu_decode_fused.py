@@ -17,11 +17,13 @@ def rel(a, b):
     return ((a - b).abs().max() / (b.abs().max() + 1e-30)).item()
 
 
-@pytest.mark.parametrize("B", [1, 5, 13, 64])
+@pytest.mark.parametrize("B", [1, 2, 3, 4, 5, 13, 64])
 @pytest.mark.parametrize("K,N,ln,act,res", [(768, 2328, True, 0, False), (768, 768, False, 0, True),
                                             (768, 3072, True, 1, False), (3072, 768, False, 0, True),
                                             (128, 8192, True, 0, False), (1000, 300, True, 1, True),
-                                            (4100, 200, False, 0, False)])
+                                            (4100, 200, False, 0, False), (768, 8192, True, 0, False),
+                                            (512, 1025, True, 1, True), (1024, 4097, True, 0, False),
+                                            (2048, 300, False, 1, True), (4096, 5000, False, 0, True)])
 def test_decode_gemv_matches_torch(B, K, N, ln, act, res):
     import pragnosia_amd.ops  # noqa: F401
     g = torch.Generator(device="cuda").manual_seed(B + K + N)
@@ -60,7 +62,7 @@ def test_decode_proj_matches_module_step(delta, write_all, hl_floor):
             p.add_(torch.randn_like(p) * 0.05)
         B = 3
         S = torch.randn(B, 4, 64, 64, device="cuda") * 0.1
-        S_f = S.clone()
+        S_f, S_r = S.clone(), S.clone()
         p0 = torch.tensor([7.0], device="cuda")
         gated = not (delta or write_all)
         extra = [m.wi.weight] if gated else ([m.wb.weight] if delta else [])
@@ -76,18 +78,52 @@ def test_decode_proj_matches_module_step(delta, write_all, hl_floor):
                                       torch.finfo(torch.float32).eps)
             y_f = op.decode_gemv(o, m.o.weight, None, None, 0.0, None, torch.sigmoid(m.gate).reshape(1), 0,
                                  x.reshape(B, 256))
+            # the raw output (four workgroups per head) with the RMSNorm in the o-projection's GEMV
+            o_r = op.aspin_decode_proj_(S_r, P, 4, m.wa.bias, m.A, m.la_floor if hl_floor else None,
+                                        m.wi.bias if gated else None, m.wb.bias if delta else None,
+                                        0.75 if (delta and write_all) else 0.0, gated, m.theta, p0, 0.0, None,
+                                        torch.finfo(torch.float32).eps)
+            y_r = op.decode_gemv_rms(o_r, m.o.weight, m.on.weight, torch.finfo(torch.float32).eps, None,
+                                     torch.sigmoid(m.gate).reshape(1), 0, x.reshape(B, 256))
             p0.fill_(1.0)
             assert rel(y_f - x.reshape(B, 256), y_mod.reshape(B, 256) - x.reshape(B, 256)) < 1e-4, step
             assert rel(S_f, st[0]) < 1e-4, step
+            assert rel(y_r - x.reshape(B, 256), y_mod.reshape(B, 256) - x.reshape(B, 256)) < 1e-4, step
+            assert rel(S_r, st[0]) < 1e-4, step
 
 
+@pytest.mark.parametrize("B", [1, 3, 4])
+@pytest.mark.parametrize("K,N,bias,act", [(768, 768, False, 0), (512, 300, True, 1), (1024, 1500, True, 0)])
+def test_decode_gemv_rms_matches_torch(B, K, N, bias, act):
+    """The o-projection GEMV with the carrier's per-head (64-channel) RMSNorm on its input, against fp64 torch."""
+    import pragnosia_amd.ops  # noqa: F401
+    g = torch.Generator(device="cuda").manual_seed(B + K + N)
+    x = torch.randn(B, K, device="cuda", generator=g)
+    W = torch.randn(N, K, device="cuda", generator=g) * 0.05
+    w64 = 1 + 0.1 * torch.randn(64, device="cuda", generator=g)
+    b = torch.randn(N, device="cuda", generator=g) if bias else None
+    scale = torch.rand(1, device="cuda", generator=g)
+    resid = torch.randn(B, N, device="cuda", generator=g)
+    eps = torch.finfo(torch.float32).eps
+    y = torch.ops.pragnosia.decode_gemv_rms(x, W, w64, eps, b, scale, act, resid)
+    z = F.rms_norm(x.double().view(B, K // 64, 64), (64,), w64.double(), eps).view(B, K)
+    r = (z @ W.double().t()) * scale.double()
+    if b is not None:
+        r = r + b.double()
+    if act == 1:
+        r = F.gelu(r)
+    r = r + resid.double()
+    assert rel(y, r) < 1e-5
+
+
+@pytest.mark.parametrize("d", [128, 256])  # 256: the per-head RMSNorm runs inside the o-projection's GEMV
 @pytest.mark.parametrize("mixer", ["aspin", "dspin"])
 @pytest.mark.parametrize("B", [1, 3, 40])  # 1, 3: GEMV dense layers; 40: torch GEMMs around the fused step
-def test_fused_graphed_decode_equals_unfused_and_eager(mixer, B):
+def test_fused_graphed_decode_equals_unfused_and_eager(mixer, B, d):
     from pragnosia_amd.decode import GreedyDecoder, greedy_eager
     from pragnosia_amd.model import LM
     torch.manual_seed(50 + B)
-    m = LM(vocab=300, d=128, layers=2, mlp_mult=2, ctx=64, mixer=mixer).cuda().eval()
+    m = LM(vocab=300, d=d, layers=2, mlp_mult=2, ctx=64, mixer=mixer).cuda().eval()
     with torch.no_grad():
         for mx in m.mix:
             for p in mx.parameters():

@@ -80,6 +80,9 @@ def _samples():
         ("decode_gemv", (x, r(50, 96), 1 + 0.1 * r(96), r(96), 1e-5, r(50), r(1), 1, r(3, 50))),
         ("aspin_decode_proj_", (r(B, H, D, D), r(B, 3 * H * D + 2 * H), H, r(H), r(H), None, r(H), None, 0.0, True,
                                 th, torch.tensor(1.0, device=dev), 0.0, 1 + 0.1 * r(64), 1e-6)),
+        ("aspin_decode_proj_", (r(B, H, D, D), r(B, 3 * H * D + 2 * H), H, r(H), r(H), None, r(H), None, 0.0, True,
+                                th, torch.tensor(1.0, device=dev), 0.0, None, 1e-6)),
+        ("decode_gemv_rms", (r(3, 256), r(50, 256), 1 + 0.1 * r(64), 1e-6, r(50), r(1), 1, r(3, 50))),
     ]
 
 
