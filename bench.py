@@ -179,19 +179,66 @@ def aspin_bench(rule, steps, warmup):
         fwd_flops = 4 * D * (C + D) * ht
         bwd_flops = 10 * D * (C + D) * ht
         names = ("aspin_plain_fwd", "aspin_plain_bwd")
+        impl_fwd, impl_bwd = fwd_bytes, bwd_bytes
     else:
-        # forward: q, k, v read; o, W written; X written and read back (bf16 C x C per chunk); la, beta read;
-        # S_final, sent written
+        # the minimal I/O of the delta rule (the algorithmic bytes): forward q, k, v, la, beta read, o written, the
+        # final state and the bf16 entering states written; backward q, k, v, dO, la, beta and the entering states
+        # read, dq, dk, dv, dla, dbeta written, dS_final read, dS0 written
+        fwd_bytes = 4 * 2 * elem + 8 * ht + 4 * state + 2 * sent_n
+        bwd_bytes = 7 * 2 * elem + 2 * sent_n + 16 * ht + 8 * state
+        # what this implementation moves besides: X (bf16 C x C per chunk) written and read back in the forward and
+        # read again in the backward, W written and read back, the chain/local hand-off (drhs and per-chunk dS,
+        # bf16) written once and read once, and the entering states read twice in the backward
         x_n = B * H * NC * C * C
-        fwd_bytes = 5 * 2 * elem + 2 * 2 * x_n + 8 * ht + 4 * state + 2 * sent_n
-        # backward: q, k, v, dO, W, X, sent read; dq, dk, dv written; la, beta read, dla, dbeta written; the
-        # chain/local hand-off (drhs and per-chunk dS, bf16) written once and read once
-        bwd_bytes = 7 * 2 * elem + 2 * x_n + 2 * sent_n + 16 * ht + 8 * state + 2 * (2 * elem + 2 * sent_n)
+        impl_fwd = fwd_bytes + 2 * 2 * x_n + 2 * elem
+        impl_bwd = bwd_bytes + 2 * x_n + 2 * elem + 2 * sent_n + 2 * (2 * elem + 2 * sent_n)
         fwd_flops = (4 * D * (C + D) + 2 * C * D + 2 * D * D + 2 * C * C) * ht
         bwd_flops = (10 * D * (C + D) + 6 * C * D + 4 * D * D + 4 * C * C) * ht
         names = ("aspin_delta_fwd (inv + fwd kernels)", "aspin_delta_bwd (chain + local kernels)")
+    cold = _rotating_bwd(rule, stream, x)
     return dict(B=B, H=H, T=T, D=D, C=C, wall=wall, eager=eager, t_fwd=t_fwd, t_bwd=t_bwd, fwd_bytes=fwd_bytes,
-                bwd_bytes=bwd_bytes, fwd_flops=fwd_flops, bwd_flops=bwd_flops, names=names)
+                bwd_bytes=bwd_bytes, impl_fwd_bytes=impl_fwd, impl_bwd_bytes=impl_bwd, fwd_flops=fwd_flops,
+                bwd_flops=bwd_flops, names=names, cold=cold)
+
+
+ROTATE_SETS = 8
+
+
+def _rotating_bwd(rule, stream, bwd_args):
+    """The backward (and forward) kernels timed over ROTATE_SETS different input sets in turn, each set the full
+    cfg2 inputs plus the forward's saved tensors (~63 MB for the plain rule), ~500 MB in all, twice the 256 MB
+    last-level cache: no launch finds its inputs in that cache from an earlier one. Returns the average launch times
+    (us) of the forward and backward under rotation."""
+    import torch
+    op = torch.ops.pragnosia
+    sets = []
+    for i in range(ROTATE_SETS):
+        x = {n: (None if t is None else t.clone()) for n, t in bwd_args.items()}
+        with torch.no_grad():
+            sv = (op.aspin_chunk(x["q"], x["k"], x["v"], x["la"], None, True) if rule == "plain" else
+                  op.aspin_delta(x["q"], x["k"], x["v"], x["la"], x["beta"], None, True))
+        sets.append((x, sv))
+    it = {"f": 0, "b": 0}
+
+    def fwd_cycle():
+        x, _ = sets[it["f"] % ROTATE_SETS]
+        it["f"] += 1
+        return (op.aspin_chunk(x["q"], x["k"], x["v"], x["la"], None, True) if rule == "plain" else
+                op.aspin_delta(x["q"], x["k"], x["v"], x["la"], x["beta"], None, True))
+
+    def bwd_cycle():
+        x, sv = sets[it["b"] % ROTATE_SETS]
+        it["b"] += 1
+        if rule == "plain":
+            return op.aspin_chunk_bwd(x["q"], x["k"], x["v"], x["la"], sv[2], x["do"], x["dS"])
+        return op.aspin_delta_bwd(x["q"], x["k"], x["v"], x["la"], x["beta"], sv[2], sv[3], sv[4], x["do"], x["dS"])
+
+    t_f, t_b = _time_ops([fwd_cycle, bwd_cycle], 8 * ROTATE_SETS, stream)
+    footprint = sum(t.numel() * t.element_size() for x, sv in sets for t in list(x.values()) + list(sv)
+                    if t is not None)
+    del sets
+    return {"sets": ROTATE_SETS, "input_footprint_MB": round(footprint / 1e6, 1), "fwd_us": round(t_f * 1e6, 2),
+            "bwd_us": round(t_b * 1e6, 2)}
 
 
 def diag_bench(steps):
@@ -519,10 +566,17 @@ def op_roofline(r):
     t = r["t_fwd"] + r["t_bwd"]
     gbs = (r["fwd_bytes"] + r["bwd_bytes"]) / t / 1e9
     tfl = (r["fwd_flops"] + r["bwd_flops"]) / t / 1e12
+    impl = r["impl_fwd_bytes"] + r["impl_bwd_bytes"]
+    tc = (r["cold"]["fwd_us"] + r["cold"]["bwd_us"]) * 1e-6
     return {"hbm_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_tflops": round(tfl, 2),
             "mfma_frac": round(tfl / BF16_PEAK_TFLOPS, 4),
             "achieved_frac": round(max(gbs / HBM_PEAK_GBS, tfl / BF16_PEAK_TFLOPS), 4),
-            "ai_flop_per_byte": round((r["fwd_flops"] + r["bwd_flops"]) / (r["fwd_bytes"] + r["bwd_bytes"]), 1)}
+            "ai_flop_per_byte": round((r["fwd_flops"] + r["bwd_flops"]) / (r["fwd_bytes"] + r["bwd_bytes"]), 1),
+            # this implementation's bytes (its own intermediates included) against the algorithmic ones
+            "impl_bytes_ratio": round(impl / (r["fwd_bytes"] + r["bwd_bytes"]), 3),
+            "impl_GBs": round(impl / t / 1e9, 1),
+            # the same kernels with every launch's inputs out of the last-level cache (rotating input sets)
+            "cold": dict(r["cold"], hbm_frac=round((r["fwd_bytes"] + r["bwd_bytes"]) / tc / 1e9 / HBM_PEAK_GBS, 4))}
 
 
 def gpu_bench(args):
@@ -548,7 +602,10 @@ def gpu_bench(args):
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom[0]),
                      "algorithmic_bytes": dom[2], "avg_launch_us": round(dom[1] * 1e6, 2),
                      "mfma_tflops": round(dom[3] / dom[1] / 1e12, 2),
-                     "mfma_frac": round(dom[3] / dom[1] / 1e12 / BF16_PEAK_TFLOPS, 4)},
+                     "mfma_frac": round(dom[3] / dom[1] / 1e12 / BF16_PEAK_TFLOPS, 4),
+                     "cold_avg_launch_us": r["cold"]["bwd_us" if dom[0] == r["names"][1] else "fwd_us"],
+                     "cold_frac": round(dom[2] / (r["cold"]["bwd_us" if dom[0] == r["names"][1] else "fwd_us"] * 1e-6)
+                                        / 1e9 / HBM_PEAK_GBS, 4)},
         "kernels_us": {r["names"][0]: round(r["t_fwd"] * 1e6, 2), r["names"][1]: round(r["t_bwd"] * 1e6, 2)},
         "op": op_roofline(r),
     }
@@ -611,6 +668,90 @@ def cpu_baseline(args):
             "sample": f"CPU oracle ({args.rule} rule, two-pass fp32 restatement of {form}, autograd backward), "
                       f"B=1 x T512 H12 D64 per iteration, {len(times)} iterations (~{args.cpu_seconds:.0f} s), "
                       "median"}
+
+
+def _host_cpu():
+    """The host CPU's model name (from /proc/cpuinfo) and logical core count."""
+    name = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": name, "logical_cores": os.cpu_count()}
+
+
+def _median_rate(fn, seconds, units):
+    for _ in range(2):
+        fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return units / med, med, len(times)
+
+
+def cpu_baselines_more(args, seconds=5.0):
+    """The CPU oracle on the other workloads, each on a bounded sample of its config (about `seconds` each): the
+    delta rule of configs[2] (two-pass fp32 with the chunk inverse, autograd backward), the diagonal scan of
+    configs[1] (`scan_gated`, chunk 16, autograd backward, the reference's CPU path `src/spin.py:181-215`), and the
+    eager fp32 decode of configs[4] (the oracle's T = 1 steps through the 12-layer d768 LM)."""
+    import torch
+    from oracle import aspin as O
+    from oracle import diag as OD
+    from oracle import modules as OM
+    out = {"host_cpu": _host_cpu(), "threads": torch.get_num_threads()}
+    B, H, T, D = 1, 12, 512, 64
+    x = aspin_inputs(B, H, T, D, 2, "delta", "cpu")
+    S0 = torch.zeros(B, H, D, D)
+
+    def delta_it():
+        a = [x[n].clone().requires_grad_(True) for n in ("q", "k", "v", "la", "beta")]
+        o, S, _, _ = O.scan_twopass_delta(*a, S0, 64, None)
+        ((o * x["do"]).sum() + (S * x["dS"]).sum()).backward()
+
+    rate, med, n = _median_rate(delta_it, seconds, B * T)
+    out["aspin_delta_cfg2"] = {"value": round(rate / 1e6, 5), "unit": "Mtok/s", "kind": "port",
+                               "sample": f"B=1 x T512 H12 D64, fwd + autograd bwd, {n} iterations, median"}
+    g = torch.Generator().manual_seed(1)
+    Tb, Db = 512, 768
+    u = torch.randn(1, Tb, Db, generator=g)
+    lm = torch.nn.functional.logsigmoid(torch.randn(1, Tb, Db, generator=g) + 4.0)
+    an = torch.rand(1, Tb, Db, generator=g) - 0.5
+    gy = torch.randn(1, Tb, Db, generator=g)
+
+    def diag_it():
+        a = [t.clone().requires_grad_(True) for t in (u, lm, an)]
+        y, (hr, hi) = OD.scan_gated(*a, None, 16)
+        (y * gy).sum().add(hr.sum() + hi.sum()).backward()
+
+    rate, med, n = _median_rate(diag_it, seconds, Tb)
+    out["diag_scan_cfg1"] = {"value": round(rate / 1e6, 5), "unit": "Mtok/s", "kind": "port",
+                             "sample": f"B=1 x T512 D768 (one of 16 sequences), scan_gated chunk 16 fwd + autograd "
+                                       f"bwd, {n} iterations, median; GPU reference point: configs[1] B16"}
+    from pragnosia_amd.model import LM
+    torch.manual_seed(4)
+    sd = {k: v.detach() for k, v in LM(vocab=8192, d=768, layers=12, mlp_mult=4, ctx=512,
+                                         mixer="aspin").state_dict().items()}
+    prompt = torch.randint(0, 8192, (1, 16), generator=g)
+    steps = 8
+
+    def decode_it():
+        with torch.inference_mode():
+            OM.greedy_decode(sd, prompt, steps, layers=12, mixer="aspin", heads=12)
+
+    rate, med, n = _median_rate(decode_it, seconds, 1)
+    # the prefill of 16 tokens is part of each timed run; it is charged to the decode steps (an upper bound)
+    out["decode_cfg4_bs1"] = {"value": round(med / steps * 1e3, 3), "unit": "ms/token", "kind": "port",
+                              "sample": f"92M LM, prefill 16 + {steps} greedy T=1 steps at batch 1, fp32, oracle "
+                                        f"(torch CPU) path, {n} runs, median, prefill charged to the steps"}
+    return out
 
 
 def profile_kernels(reps=10):
@@ -684,6 +825,9 @@ def main():
     res = gpu_bench(args)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(args)
+        res["cpu_baseline"]["host_cpu"] = _host_cpu()
+        if not args.no_secondary:
+            res["cpu_baselines_more"] = cpu_baselines_more(args)
     print(json.dumps(res), flush=True)
 
 
