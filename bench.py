@@ -274,9 +274,10 @@ def diag_bench(steps):
 
 def wide_bench(steps=30):
     """The plain rule at head dim 128 (the reference's `hspin` carrier) at configs[2]'s width: B16 T512, d 768 as 6
-    heads of 128, bf16 q/k/v; one forward + backward through `assoc_scan` (four 64 x 64 kernel scans per head and the
-    copies around them), one step captured in a HIP graph (forward and autograd backward) and replayed `steps` times
-    between HIP events, beside the 64-dim path at the same width timed the same way."""
+    heads of 128, bf16 q/k/v; one forward + backward through `assoc_scan` with bf16 matmuls (mm=bf16, the kernel
+    path: four 64 x 64 scans per head reading the halves in place, and the sums of their partial outputs), one step
+    captured in a HIP graph (forward and autograd backward) and replayed `steps` times between HIP events, beside the
+    64-dim path at the same width timed the same way."""
     import torch
     import torch.nn.functional as F
     from pragnosia_amd.assoc import assoc_scan
@@ -290,7 +291,7 @@ def wide_bench(steps=30):
         do = torch.randn(16, H, 512, D, generator=g).bfloat16().cuda()
 
         def step():
-            o, _ = assoc_scan(q, k, v, la)
+            o, _ = assoc_scan(q, k, v, la, mm=torch.bfloat16)
             torch.autograd.backward([o], [do])
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())

@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (9); bumped on any change of the entry points. */
+/* ABI version of this header (10); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -129,6 +129,29 @@ int pragnosia_aspin_chunk_bwd_seg(const void* q, const void* k, const void* v, c
                                   const void* dO, const float* dS_final, void* dq, void* dk, void* dv, float* dla,
                                   float* dS0, void* workspace, int64_t workspace_bytes, int64_t B, int64_t H,
                                   int64_t T, int64_t D, int64_t chunk, int64_t seg_chunks, void* stream);
+
+/* The plain rule at head dim D = 128 (the reference's assoc_scan_kernel at D = 128, src/assoc_kernel.py:21,302-323,
+ * which the carrier takes for 128-wide heads, src/assoc.py:411, and its registered backward, :146-299). The state's
+ * key rows evolve independently and o_t = S_t^T q_t sums over them, so each head runs as four 64 x 64 scans, one per
+ * (key half kh, value half vh) block of its state, reading q and k at columns 64 kh and v and dO at columns 64 vh of
+ * the 128-wide rows (no copies); o, dv (summed over key halves) and dq, dk (over value halves) are written as two
+ * bf16 partials each, the second into the workspace, and added (fp32 sum rounded once to bf16) by one more kernel.
+ * q, k, v, dO: (B, H, T, 128) bf16; la, dla: (B, H, T) fp32; S0, S_final, dS_final, dS0: (B, H, 128, 128) fp32
+ * (S0, dS_final, dS0 may be NULL); sent: the entering states per scan, (B, H, 4, NC, 64, 64) bf16 (scan 2 kh + vh
+ * holds block rows 64 kh.., columns 64 vh..; NC = ceil(T / 64)), written by the forward when not NULL and read by the
+ * backward. seg_chunks: the segment length of the segment-parallel passes (as pragnosia_aspin_chunk_fwd_seg, no
+ * windows); at least NC runs one workgroup per scan. `workspace`: caller-allocated device memory of at least
+ * pragnosia_aspin_chunk_wide_workspace_bytes(..., backward) bytes. */
+int64_t pragnosia_aspin_chunk_wide_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk,
+                                                   int64_t seg_chunks, int32_t backward);
+int pragnosia_aspin_chunk_fwd_wide(const void* q, const void* k, const void* v, const float* la, const float* S0,
+                                   void* o, float* S_final, void* sent, void* workspace, int64_t workspace_bytes,
+                                   int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, int64_t seg_chunks,
+                                   void* stream);
+int pragnosia_aspin_chunk_bwd_wide(const void* q, const void* k, const void* v, const float* la, const void* sent,
+                                   const void* dO, const float* dS_final, void* dq, void* dk, void* dv, float* dla,
+                                   float* dS0, void* workspace, int64_t workspace_bytes, int64_t B, int64_t H,
+                                   int64_t T, int64_t D, int64_t chunk, int64_t seg_chunks, void* stream);
 
 /* The carrier's output epilogue (head dim D = 64): per (batch, head, token) row x of the scan output o
  * ((B, H, T, D) bf16), r = 1 / sqrt(mean(x^2) + eps) and y[b, t, h D + d] = (x_d r) w_d, rounded once to y's dtype

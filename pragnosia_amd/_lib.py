@@ -27,6 +27,9 @@ SIGNATURES = {
     "pragnosia_aspin_chunk_fwd_seg": [_p] * 6 + [_i64] + [_p] * 4 + [_i64] * 7 + [_p],
     "pragnosia_aspin_chunk_bwd_seg": [_p] * 13 + [_i64] * 7 + [_p],
     "pragnosia_aspin_chunk_fwd_seg_noalloc": [_p] * 6 + [_i64] + [_p] * 3 + [_i64] * 6 + [_p],
+    "pragnosia_aspin_chunk_wide_workspace_bytes": [_i64] * 6 + [_i32],
+    "pragnosia_aspin_chunk_fwd_wide": [_p] * 9 + [_i64] * 7 + [_p],
+    "pragnosia_aspin_chunk_bwd_wide": [_p] * 13 + [_i64] * 7 + [_p],
     "pragnosia_aspin_out_fwd": [_p] * 2 + [_f32, _p, _i32, _p] + [_i64] * 4 + [_p],
     "pragnosia_aspin_out_weight_partials": [_i64] * 3,
     "pragnosia_aspin_out_bwd": [_p, _i32] + [_p] * 5 + [_i64] * 4 + [_p],
@@ -53,7 +56,7 @@ SIGNATURES = {
 # entry points that return a size (int64) rather than a status code
 _RET_I64 = {"pragnosia_aspin_delta_bwd_workspace_bytes", "pragnosia_aspin_prep_theta_partials",
             "pragnosia_aspin_chunk_seg_workspace_bytes", "pragnosia_aspin_out_weight_partials",
-            "pragnosia_aspin_prep_proj_partials"}
+            "pragnosia_aspin_prep_proj_partials", "pragnosia_aspin_chunk_wide_workspace_bytes"}
 
 _lib = None
 

@@ -55,73 +55,16 @@ def rotate(x, theta, pos):
 HEAD_DIM_WIDE = 128
 
 
-def _split4(x, B, H, T, h, v_order):
-    """(B, H, T, 2h) -> (B, 4H, T, h): per head the halves in the sub-scan order (kh, vh) = (0,0), (0,1), (1,0),
-    (1,1): q and k by key half (x1, x1, x2, x2), v and dO by value half (x1, x2, x1, x2). One copy."""
-    xh = x.reshape(B, H, T, 2, h).transpose(2, 3)  # (B, H, 2, T, h), a view
-    x4 = xh.repeat(1, 1, 2, 1, 1) if v_order else xh.repeat_interleave(2, dim=2)
-    return x4.reshape(B, 4 * H, T, h)
-
-
-def _join4(x4, B, H, T, h, over_v):
-    """The gradient of _split4: (B, 4H, T, h) -> (B, H, T, 2h), summing the two copies of each half (over the value
-    half for q and k, over the key half for v), written straight into the interleaved layout: one kernel. (Also the
-    forward's output sum, over the key half.) Not differentiable."""
-    x = x4.reshape(B, H, 2, 2, T, h)
-    a, b = (x[:, :, :, 0], x[:, :, :, 1]) if over_v else (x[:, :, 0], x[:, :, 1])
-    out = torch.empty(B, H, T, 2 * h, device=x4.device, dtype=x4.dtype)
-    # a bf16 add rounds the fp32 sum of its operands once
-    torch.add(a, b, out=out.view(B, H, T, 2, h).transpose(2, 3))
-    return out
-
-
-class _WideScan(torch.autograd.Function):
-    """The four 64 x 64 sub-scans of `_plain_scan_wide` with their input copies and output sums written out for both
-    directions, so the backward is one kernel call plus one reduction per gradient."""
-
-    @staticmethod
-    def forward(ctx, q, k, v, la, S0, need_sent):
-        B, H, T, D = q.shape
-        h = D // 2
-        q4, k4, v4 = _split4(q, B, H, T, h, False), _split4(k, B, H, T, h, False), _split4(v, B, H, T, h, True)
-        la4 = la.repeat_interleave(4, dim=1)
-        S04 = None if S0 is None else S0.reshape(B, H, 2, h, 2, h).permute(0, 1, 2, 4, 3, 5).reshape(B, 4 * H, h, h)
-        o4, S4, sent4 = _op.aspin_chunk(q4, k4, v4, la4, S04, True)
-        ctx.save_for_backward(q4, k4, v4, la4, sent4)
-        ctx.has_s0, ctx.dims = S0 is not None, (B, H, T, h)
-        o = _join4(o4, B, H, T, h, False)
-        S = S4.reshape(B, H, 2, 2, h, h).permute(0, 1, 2, 4, 3, 5).reshape(B, H, D, D)
-        NC = sent4.shape[2]
-        sent = (sent4.reshape(B, H, 2, 2, NC, h, h).permute(0, 1, 4, 2, 5, 3, 6).reshape(B, H, NC, D, D)
-                if need_sent else sent4.new_empty(0))
-        ctx.mark_non_differentiable(sent)
-        return o, S, sent
-
-    @staticmethod
-    def backward(ctx, do, dS, _dsent):
-        q4, k4, v4, la4, sent4 = ctx.saved_tensors
-        B, H, T, h = ctx.dims
-        do = torch.zeros(B, H, T, 2 * h, device=q4.device, dtype=torch.bfloat16) if do is None else do.bfloat16()
-        do4 = _split4(do, B, H, T, h, True)  # dO_4(kh, vh) = dO[.., vh]
-        dS4 = None if dS is None else dS.reshape(B, H, 2, h, 2, h).permute(0, 1, 2, 4, 3, 5).reshape(B, 4 * H, h, h)
-        dq4, dk4, dv4, dla4, dS04 = _op.aspin_chunk_bwd(q4, k4, v4, la4, sent4, do4, dS4)
-        dq, dk, dv = _join4(dq4, B, H, T, h, True), _join4(dk4, B, H, T, h, True), _join4(dv4, B, H, T, h, False)
-        dla = dla4.reshape(B, H, 4, T).sum(2)
-        dS0 = (dS04.reshape(B, H, 2, 2, h, h).permute(0, 1, 2, 4, 3, 5).reshape(B, H, 2 * h, 2 * h)
-               if ctx.has_s0 else None)
-        return dq, dk, dv, dla, dS0, None
-
-
 def _plain_scan_wide(q, k, v, la, S0, want):
-    """The plain rule at head dim 128 (the reference's `hspin` carrier, `src/model.py:650`) on the 64 x 64 kernels.
-    The state's key halves evolve independently (S_t = a_t S_{t-1} + k_t v_t^T, row block by row block) and the read
-    o_t = S_t^T q_t sums over them, so with q = (q1, q2), k = (k1, k2), v = (v1, v2) in halves of 64,
+    """The plain rule at head dim 128 (the reference's `hspin` carrier, `src/model.py:650`, on its kernel path,
+    `src/assoc.py:411`). The state's key rows evolve independently and o_t = S_t^T q_t sums over them, so with q = (q1,
+    q2), k = (k1, k2), v = (v1, v2) in halves of 64,
         o[..., half vh] = scan(q1, k1, v_vh) + scan(q2, k2, v_vh),   S[half kh, half vh] = final state of
-        scan(q_kh, k_kh, v_vh),
-    four 64 x 64 scans per head in one launch over 4 H heads (`_WideScan`). Each half of q, k and v is copied and read
-    twice and o written twice: a drop-in, slower than a 128-wide kernel would be. Returns
-    (o bf16 (B, H, T, 128), S_final fp32, sent (B, H, NC, 128, 128) bf16, or empty when not `want`)."""
-    return _WideScan.apply(q.bfloat16(), k.bfloat16(), v.bfloat16(), la.float(), S0, want)
+        scan(q_kh, k_kh, v_vh):
+    four 64 x 64 scans per head in one launch over 4 H scans that read the halves in place (`aspin_chunk_wide`).
+    Returns (o bf16 (B, H, T, 128), S_final fp32, sent per scan (B, H, 4, NC, 64, 64) bf16, or empty when not
+    `want`; `ops.wide_sent` gives the whole states)."""
+    return _op.aspin_chunk_wide(q, k, v, la.float(), S0, want)
 
 
 def _prep_wide(qp, kp, vp, gate, theta, pos, dtype=torch.bfloat16):
@@ -200,7 +143,8 @@ def _kernel_scan(q, k, v, logalpha, S0, beta, need_sent):
     want = bool(need_sent or _needs_grad(q, k, v, logalpha, S0, beta))
     S0 = None if S0 is None else S0.float()
     if wide:
-        o, S, sent = _plain_scan_wide(q.bfloat16(), k.bfloat16(), v.bfloat16(), logalpha.float(), S0, want)
+        o, S, sent = _plain_scan_wide(q, k, v, logalpha, S0, want)
+        sent = _op_mod.wide_sent(sent) if need_sent else sent
     elif beta is None:
         o, S, sent = _op.aspin_chunk(q, k, v, logalpha.float(), S0, want)
     else:
@@ -273,6 +217,21 @@ class AssocCarrier(nn.Module):
         self.on = nn.RMSNorm(self.dk)
         self.gate = nn.Parameter(torch.zeros(()))
         self.sent = None
+
+    @property
+    def sent(self):
+        """The bf16 state entering every 64-token chunk of the last kernel-path call, (B, H, NC, dk, dk), or None (the
+        reference's `self.sent`, `src/assoc.py:349,510`, which its retrieval layers read). The 128-wide scan keeps it
+        per 64 x 64 block; it is assembled on first read."""
+        s = self.__dict__.get("_sent")
+        if s is not None and s.dim() == 6:
+            s = _op_mod.wide_sent(s)
+            self.__dict__["_sent"] = s
+        return s
+
+    @sent.setter
+    def sent(self, value):
+        self.__dict__["_sent"] = value
 
     def spectral_parameters(self):
         return [self.A, self.theta, self.gate]

@@ -35,6 +35,30 @@ constexpr int C = 64;
 constexpr int DK = 64;
 constexpr int TILE = 64 * kPitch;  // one staged 64 x 64 tile
 
+// Where the scan of workgroup head index bh finds its rows. Narrow heads (64 wide): scan bh is head bh, rows of 64.
+// Wide heads (128 wide, plain rule): scan bh = 4 hw + 2 kh + vh runs the 64 x 64 block (key half kh, value half vh)
+// of head hw's 128 x 128 state. The plain rule's state rows evolve independently (S_t = a_t S_{t-1} + k_t v_t^T row
+// by row) and o_t = S_t^T q_t sums over key rows, so the block's scan is an ordinary 64 x 64 scan of q, k at columns
+// 64 kh and v, dO at columns 64 vh of rows of 128, and o (dv) of head hw is the sum of its two key halves' outputs,
+// dq and dk the sums over the two value halves. Such a sum has two slots, the caller's tensor (slot 0) and a
+// workspace tensor of the same layout (slot 1): o and dv go to slot kh at columns 64 vh, dq and dk to slot vh at
+// columns 64 kh. States (S0, S_final, dS_final, dS0) are the caller's (B, H, 128, 128) arrays: block (kh, vh) at rows
+// 64 kh, columns 64 vh. The entering states `sent` stay per scan, (B, 4H, NC, 64, 64).
+template <bool WIDE>
+struct HeadRows {
+  static constexpr int ld = WIDE ? 128 : 64;  // row pitch of token-major operands and of states
+  int hw, kh, vh;
+  PGN_DEVICE explicit HeadRows(int bh)
+      : hw(WIDE ? bh >> 2 : bh), kh(WIDE ? (bh >> 1) & 1 : 0), vh(WIDE ? bh & 1 : 0) {}
+  PGN_DEVICE size_t keys(int T) const { return (size_t)hw * T * ld + 64 * kh; }  // q, k, dq, dk
+  PGN_DEVICE size_t vals(int T) const { return (size_t)hw * T * ld + 64 * vh; }  // v, dO, o, dv
+  PGN_DEVICE size_t state() const { return (size_t)hw * ld * ld + (size_t)64 * kh * ld + 64 * vh; }
+  template <class Ptr>
+  PGN_DEVICE Ptr slot(Ptr s0, Ptr s1, int which) const {
+    return (WIDE && which) ? s1 : s0;
+  }
+};
+
 // Forward: one workgroup of 16 waves per (batch, head), chunks in order, one barrier per chunk, three roles:
 //   output waves (0-7): wave w owns a t block tb and value columns 32 jh .. 32 jh + 31 (jh = w >> 2) and holds its
 //       16 x 32 slice of the fp32 state as MFMA accumulators; per chunk c it forms O^T = V^T A^T + S^T (Q o eL)^T for
@@ -48,10 +72,14 @@ constexpr int TILE = 64 * kPitch;  // one staged 64 x 64 tile
 constexpr int kFwdWaves = 16;
 constexpr int kFwdBuf = 3 * TILE * (int)sizeof(__bf16) + 3 * C * (int)sizeof(float);  // Q, K, V, L, eL, w
 
+// S0 is the caller's entering state (head layout, read when there is one segment per head); Sws, when given instead,
+// holds each workgroup's entering state (64 x 64 per workgroup, the segmented forward's workspace).
+template <bool WIDE>
 __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
-    const float* __restrict__ la, const float* __restrict__ S0, __bf16* __restrict__ o, float* __restrict__ Sfin,
-    __bf16* __restrict__ sent, int T, int NC, int P) {
+    const float* __restrict__ la, const float* __restrict__ S0, const float* __restrict__ Sws,
+    __bf16* __restrict__ o, __bf16* __restrict__ o1, float* __restrict__ Sfin, __bf16* __restrict__ sent, int T,
+    int NC, int P) {
   extern __shared__ __align__(16) unsigned char smem[];
   // input set h (the segment's chunk lc in set lc % 3): Q, K, V tiles and the L (base 2), eL, w vectors; then A
   // (t, s) and S^T (j, d) tiles for two chunks each (chunk lc in lc & 1)
@@ -68,9 +96,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
   const int nseg = (NC + P - 1) / P;
   const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
   const int c0 = sg * P, n = min(P, NC - c0);
-  const size_t boff = (size_t)bh * T * DK;
-  const size_t soff = (size_t)bh * DK * DK;
-  const size_t s0off = (size_t)blockIdx.x * DK * DK;
+  const HeadRows<WIDE> R(bh);
+  constexpr int ld = HeadRows<WIDE>::ld;
+  const size_t koff = R.keys(T), voff = R.vals(T);
 
   // decayed scores A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, of t block a of chunk `cn` (input set hs) into
   // the A tile `At` (row t), zero above the diagonal block
@@ -115,12 +143,15 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     const int tb = w < 4 ? 3 - w : w - 4, j0 = 32 * (w >> 2);
     // state rows 16 tb + 4g + r, columns j0 + 16 jt + i
     f32x4 S[2];
+    const float* s0p = Sws ? Sws + (size_t)blockIdx.x * DK * DK : (S0 ? S0 + R.state() : nullptr);
+    const int s0ld = Sws ? DK : ld;
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) S[jt][r] = S0 ? S0[s0off + (16 * tb + 4 * g + r) * DK + j0 + 16 * jt + i] : 0.f;
+      for (int r = 0; r < 4; ++r) S[jt][r] = s0p ? s0p[(16 * tb + 4 * g + r) * s0ld + j0 + 16 * jt + i] : 0.f;
       store_T(STb(0), j0 + 16 * jt, 16 * tb, g, i, S[jt]);
     }
+    __bf16* const obase = R.slot(o, o1, R.kh) + voff;
     __syncthreads();
     __syncthreads();
     auto oloop = [&](auto tb_c) {
@@ -160,7 +191,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
         // so the state read's decay is one factor on the accumulator. Rows past T fall outside the store's range
         // and are dropped.
         const __amdgpu_buffer_rsrc_t o_out = __builtin_amdgcn_make_buffer_rsrc(
-            o + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
+            obase + (size_t)t0 * ld, (short)0, min(C, T - t0) * ld * (int)sizeof(__bf16), 0x00020000);
 #pragma unroll
         for (int jt = 0; jt < 2; ++jt) {
           f32x4 acc = zero4();
@@ -170,7 +201,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
           qs = pgn_mfma(sf[jt][1], qf1, qs);
           acc += eLt * qs;
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
-                                                (tq * DK + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+                                                (tq * ld + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
         }
         // the entering state, bf16 (d, j), from this wave's state slice
         if (sent) {
@@ -204,7 +235,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Sfin[soff + (16 * tb + 4 * g + r) * DK + j0 + 16 * jt + i] = S[jt][r];
+        for (int r = 0; r < 4; ++r) Sfin[R.state() + (16 * tb + 4 * g + r) * ld + j0 + 16 * jt + i] = S[jt][r];
     }
   } else if (w < 12) {
     // ================= score waves: t block a, one chunk ahead. Wave 8 also runs the decay scans, two chunks ahead
@@ -212,7 +243,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     const bool scan = w == 8;
     auto la_of = [&](int ln) {  // the segment's chunk ln
       const int t = (c0 + ln) * C + x.l;
-      return (ln < n && t < T) ? la[(size_t)bh * T + t] : 0.f;
+      return (ln < n && t < T) ? la[(size_t)R.hw * T + t] : 0.f;
     };
     auto run_scan = [&](float la_t, int h) {
       const float L = wave_prefix_sum(la_t, x.l);
@@ -257,12 +288,12 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     Regs ra, rb;
     auto load = [&](Regs& r, int ln) {  // the segment's chunk ln
       const int n0 = (c0 + ln) * C, nr = min(C, T - n0);
-      r.q0 = load_seg(q + boff + (size_t)n0 * DK, nr, b);
-      r.q1 = load_seg(q + boff + (size_t)n0 * DK, nr, b + 256);
-      r.k0 = load_seg(k + boff + (size_t)n0 * DK, nr, b);
-      r.k1 = load_seg(k + boff + (size_t)n0 * DK, nr, b + 256);
-      r.v0 = load_seg(v + boff + (size_t)n0 * DK, nr, b);
-      r.v1 = load_seg(v + boff + (size_t)n0 * DK, nr, b + 256);
+      r.q0 = load_seg(q + koff + (size_t)n0 * ld, nr, b, ld);
+      r.q1 = load_seg(q + koff + (size_t)n0 * ld, nr, b + 256, ld);
+      r.k0 = load_seg(k + koff + (size_t)n0 * ld, nr, b, ld);
+      r.k1 = load_seg(k + koff + (size_t)n0 * ld, nr, b + 256, ld);
+      r.v0 = load_seg(v + voff + (size_t)n0 * ld, nr, b, ld);
+      r.v1 = load_seg(v + voff + (size_t)n0 * ld, nr, b + 256, ld);
     };
     auto stage = [&](const Regs& r, int h) {
       put_seg(Qb(h), r.q0, b);
@@ -316,7 +347,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 // 16 w.. of the sum as MFMA accumulators; x and y are staged through double-buffered LDS, loaded a chunk ahead.
 constexpr int kSumBuf = 2 * TILE * (int)sizeof(__bf16) + C * (int)sizeof(float);  // x, y, w
 
-template <bool TO_END>
+template <bool TO_END, bool WIDE>
 __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restrict__ k, const __bf16* __restrict__ v,
                                                           const float* __restrict__ la, float* __restrict__ E,
                                                           float* __restrict__ lseg, int T, int NC, int P) {
@@ -330,16 +361,19 @@ __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restri
   const int nseg = (NC + P - 1) / P;
   const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
   const int c0 = sg * P, n = min(P, NC - c0);
-  const size_t boff = (size_t)bh * T * DK;
+  // x (k, or q) at the scan's key columns, y (v, or dO) at its value columns
+  const HeadRows<WIDE> R(bh);
+  constexpr int ld = HeadRows<WIDE>::ld;
+  const size_t koff = R.keys(T), voff = R.vals(T);
   bf16x8 k0, k1, v0, v1;
   float lat = 0.f;
   auto load = [&](int ln) {  // the segment's chunk ln; rows past T read as zero
     const int n0 = (c0 + ln) * C, nr = min(C, T - n0);
-    k0 = load_seg(k + boff + (size_t)n0 * DK, nr, b);
-    k1 = load_seg(k + boff + (size_t)n0 * DK, nr, b + 256);
-    v0 = load_seg(v + boff + (size_t)n0 * DK, nr, b);
-    v1 = load_seg(v + boff + (size_t)n0 * DK, nr, b + 256);
-    if (w == 0) lat = x.l < nr ? la[(size_t)bh * T + n0 + x.l] : 0.f;
+    k0 = load_seg(k + koff + (size_t)n0 * ld, nr, b, ld);
+    k1 = load_seg(k + koff + (size_t)n0 * ld, nr, b + 256, ld);
+    v0 = load_seg(v + voff + (size_t)n0 * ld, nr, b, ld);
+    v1 = load_seg(v + voff + (size_t)n0 * ld, nr, b + 256, ld);
+    if (w == 0) lat = x.l < nr ? la[(size_t)R.hw * T + n0 + x.l] : 0.f;
   };
   // wave 0: total log-decay of the segment's chunks already staged (after the next one when walking to the end,
   // before it when walking from the start)
@@ -408,8 +442,9 @@ __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restri
 // REVERSE (backward): the same recurrence over the segments from the last to the first, S0 the gradient on the final
 // state, writing over each F the gradient on the state the segment leaves and, as "final", the gradient on the
 // initial state (no rotation). Thread = (value column j, key pair ip): 8 workgroups of 256 per head. Each batch of
-// 16 segments is loaded before the recurrence runs over it, so the loads are not serialised behind it.
-template <bool REVERSE>
+// 16 segments is loaded before the recurrence runs over it, so the loads are not serialised behind it. S0 and Sfin
+// are in the caller's head layout (HeadRows), E per (scan, segment) 64 x 64. Windows (theta) are for narrow heads.
+template <bool REVERSE, bool WIDE>
 __global__ __launch_bounds__(256) void aspin_plain_segprefix(const float* __restrict__ S0,
                                                              const float* __restrict__ theta, float shift, int wsegs,
                                                              float* __restrict__ E, const float* __restrict__ lseg,
@@ -417,8 +452,10 @@ __global__ __launch_bounds__(256) void aspin_plain_segprefix(const float* __rest
   const int bh = blockIdx.x >> 3, h = bh % H;
   const int j = threadIdx.x & 63, ip = 4 * (blockIdx.x & 7) + (threadIdx.x >> 6);
   const int e0 = (2 * ip) * DK + j, e1 = e0 + DK;
-  const size_t soff = (size_t)bh * DK * DK;
-  float s0 = S0 ? S0[soff + e0] : 0.f, s1 = S0 ? S0[soff + e1] : 0.f;
+  const HeadRows<WIDE> R(bh);
+  constexpr int ld = HeadRows<WIDE>::ld;
+  const size_t u0 = R.state() + (2 * ip) * ld + j, u1 = u0 + ld;
+  float s0 = S0 ? S0[u0] : 0.f, s1 = S0 ? S0[u1] : 0.f;
   float sn = 0.f, cs = 1.f;
   if (theta) sincosf(-shift * theta[h * (DK / 2) + ip], &sn, &cs);
   constexpr int kBatch = 16;
@@ -451,8 +488,8 @@ __global__ __launch_bounds__(256) void aspin_plain_segprefix(const float* __rest
           s1 = t1;
         }
         if (Sfin && gg == nseg - 1) {
-          Sfin[soff + e0] = t0;
-          Sfin[soff + e1] = t1;
+          Sfin[u0] = t0;
+          Sfin[u1] = t1;
         }
       }
     }
@@ -505,11 +542,17 @@ PGN_DEVICE void plain_scan(float la_t, int lane, float* vs) {
 
 constexpr int kBwdStage = 5 * TILE;  // Q, K, V, dO, S_c
 
+// dSfin is the caller's gradient on the final state (head layout, read when there is one segment per head); dSws,
+// when given instead, holds the gradient on the state each workgroup's segment leaves (64 x 64 per workgroup, the
+// segmented backward's workspace). Wide heads: dla of scan 4 hw + s goes to dla (s = 0) or to dla1 slot s - 1.
+template <bool WIDE>
 __global__ __launch_bounds__(512) void aspin_plain_bwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const __bf16* __restrict__ sent, const __bf16* __restrict__ dO,
-    const float* __restrict__ dSfin, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    float* __restrict__ dla, float* __restrict__ dS0, int T, int NC, int P) {
+    const float* __restrict__ dSfin, const float* __restrict__ dSws, __bf16* __restrict__ dq,
+    __bf16* __restrict__ dq1, __bf16* __restrict__ dk, __bf16* __restrict__ dk1, __bf16* __restrict__ dv,
+    __bf16* __restrict__ dv1, float* __restrict__ dla, float* __restrict__ dla1, float* __restrict__ dS0, int T,
+    int NC, int P) {
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* stg = reinterpret_cast<__bf16*>(smem);    // two sets of staged tiles, chunk c uses set c & 1
   __bf16* dSTb = stg + 2 * kBwdStage;                // two dS^T (j, d) tiles: dS leaving chunk c in tile c & 1
@@ -521,9 +564,11 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   const int nseg = (NC + P - 1) / P;
   const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
   const int c0 = sg * P, cl = min(c0 + P, NC) - 1;
-  const size_t boff = (size_t)bh * T * DK;
-  const size_t soff = (size_t)bh * DK * DK;
-  const size_t s0off = (size_t)blockIdx.x * DK * DK;
+  const HeadRows<WIDE> R(bh);
+  constexpr int ld = HeadRows<WIDE>::ld;
+  const size_t koff = R.keys(T), voff = R.vals(T);
+  const int nwide = (int)(gridDim.x / nseg) >> 2;  // wide heads in the launch
+  float* const dlar = (WIDE && (bh & 3)) ? dla1 + ((size_t)((bh & 3) - 1) * nwide + R.hw) * T : dla + (size_t)R.hw * T;
 
   // The two groups run separate loops (the branch is on a wave-uniform value) that meet at the same barriers: each
   // loop's registers and memory-counter waits are then its own.
@@ -537,8 +582,8 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       const int n0 = cn * C, nr = min(C, T - n0);
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        sq[n] = load_seg(q + boff + (size_t)n0 * DK, nr, b2 + 128 * n);
-        sk[n] = load_seg(k + boff + (size_t)n0 * DK, nr, b2 + 128 * n);
+        sq[n] = load_seg(q + koff + (size_t)n0 * ld, nr, b2 + 128 * n, ld);
+        sk[n] = load_seg(k + koff + (size_t)n0 * ld, nr, b2 + 128 * n, ld);
       }
     };
     auto stage = [&](int hh) {
@@ -571,11 +616,11 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         float* colM = vs + 4 * C;  // column sums of dA o A
         float* dwv = vs + 6 * C;   // k_s . (dS v_s)
         // this chunk's rows of dV and dK: stores to rows past T fall outside the range and are dropped
-        const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
-        const __amdgpu_buffer_rsrc_t dv_out =
-            __builtin_amdgcn_make_buffer_rsrc(dv + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
-        const __amdgpu_buffer_rsrc_t dk_out =
-            __builtin_amdgcn_make_buffer_rsrc(dk + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
+        const int out_bytes = min(C, T - t0) * ld * (int)sizeof(__bf16);
+        const __amdgpu_buffer_rsrc_t dv_out = __builtin_amdgcn_make_buffer_rsrc(
+            R.slot(dv, dv1, R.kh) + voff + (size_t)t0 * ld, (short)0, out_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t dk_out = __builtin_amdgcn_make_buffer_rsrc(
+            R.slot(dk, dk1, R.vh) + koff + (size_t)t0 * ld, (short)0, out_bytes, 0x00020000);
         const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
         const bf16x8 vf0 = frag(Vs, me, 0, g), vf1 = frag(Vs, me, 1, g);
         const float Ls_s = Ls[me], w_s = ws[me];
@@ -654,7 +699,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             acc2 = pgn_mfma(fr[s].d, kf1, acc2);
             acc = acc + acc2 * w_s;
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dv_out,
-                                                  (me * DK + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+                                                  (me * ld + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
           } else {
             // dK^T tile (d block dt, s block WL) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
             constexpr int dt = s - NA - 4;
@@ -668,7 +713,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
             acc = acc + Y * w_s;
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dk_out,
-                                                  (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+                                                  (me * ld + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
             if constexpr (s == NS - 1) {
               dw = sum_groups(dw);
               if (g == 0) dwv[me] = dw;
@@ -691,11 +736,12 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   } else {
     // ================= group D: t = me; dS rows 16 wl + 4g + r, column 16 jt + i
     f32x4 dS[4];
+    const float* dsp = dSws ? dSws + (size_t)blockIdx.x * DK * DK : (dSfin ? dSfin + R.state() : nullptr);
+    const int dsld = dSws ? DK : ld;
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        dS[jt][r] = dSfin ? dSfin[s0off + (16 * wl + 4 * g + r) * DK + 16 * jt + i] : 0.f;
+      for (int r = 0; r < 4; ++r) dS[jt][r] = dsp ? dsp[(16 * wl + 4 * g + r) * dsld + 16 * jt + i] : 0.f;
       store_T(dSTb + (cl & 1) * TILE, 16 * jt, 16 * wl, g, i, dS[jt]);
     }
     // staging: thread b carries 16-byte row segments b and b + 256 of each of V, dO and S_c (waves 6 and 7 stage
@@ -705,13 +751,13 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
     float pla = 0.f;
     auto load = [&](int cn) {
       const int n0 = cn * C, nr = min(C, T - n0);
-      sv0 = load_seg(v + boff + (size_t)n0 * DK, nr, b);
-      sv1 = load_seg(v + boff + (size_t)n0 * DK, nr, b + 256);
-      so0 = load_seg(dO + boff + (size_t)n0 * DK, nr, b);
-      so1 = load_seg(dO + boff + (size_t)n0 * DK, nr, b + 256);
+      sv0 = load_seg(v + voff + (size_t)n0 * ld, nr, b, ld);
+      sv1 = load_seg(v + voff + (size_t)n0 * ld, nr, b + 256, ld);
+      so0 = load_seg(dO + voff + (size_t)n0 * ld, nr, b, ld);
+      so1 = load_seg(dO + voff + (size_t)n0 * ld, nr, b + 256, ld);
       ss0 = load_seg(sent + ((size_t)bh * NC + cn) * DK * DK, DK, b);
       ss1 = load_seg(sent + ((size_t)bh * NC + cn) * DK * DK, DK, b + 256);
-      if (w == 0) pla = (n0 + x.l < T) ? la[(size_t)bh * T + n0 + x.l] : 0.f;
+      if (w == 0) pla = (n0 + x.l < T) ? la[(size_t)R.hw * T + n0 + x.l] : 0.f;
     };
     auto stage = [&](int h) {
       __bf16* Qs = stg + h * kBwdStage;
@@ -744,8 +790,9 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         float* qz = vs + 5 * C;    // q_t . (S_c dO_t)
         float* sdot = vs + 7 * C;  // per-lane partial sums of <S_c, dS>, summed in the dla
         // this chunk's rows of dQ: stores to rows past T fall outside the range and are dropped
-        const __amdgpu_buffer_rsrc_t dq_out = __builtin_amdgcn_make_buffer_rsrc(
-            dq + boff + (size_t)t0 * DK, (short)0, min(C, T - t0) * DK * (int)sizeof(__bf16), 0x00020000);
+        const __amdgpu_buffer_rsrc_t dq_out =
+            __builtin_amdgcn_make_buffer_rsrc(R.slot(dq, dq1, R.vh) + koff + (size_t)t0 * ld, (short)0,
+                                              min(C, T - t0) * ld * (int)sizeof(__bf16), 0x00020000);
         const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
         const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
         const float Lt = Ls[me], eLt = eLs[me], LC = Ls[C - 1];
@@ -836,7 +883,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
             acc = acc + Z * eLt;
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dq_out,
-                                                  (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+                                                  (me * ld + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
             if constexpr (s == NA + 3) {
               qzt = sum_groups(qzt);
               if (g == 0) qz[me] = qzt;
@@ -861,8 +908,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         if (w == 0 && cc < cl) {  // the later chunk's dla, from the other vector set (before the scan below)
           const int tn = t0 + C;
           plain_dla(vec + (h ^ 1) * kVec, x.l,
-                    __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T + tn, (short)0, 4 * min(C, T - tn),
-                                                      0x00020000));
+                    __builtin_amdgcn_make_buffer_rsrc(dlar + tn, (short)0, 4 * min(C, T - tn), 0x00020000));
         }
         if (cc > c0) {
           stage(h ^ 1);
@@ -879,13 +925,12 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
     }
     if (w == 0)  // the first chunk's dla (its vector set)
       plain_dla(vec + (c0 & 1) * kVec, x.l,
-                __builtin_amdgcn_make_buffer_rsrc(dla + (size_t)bh * T + c0 * C, (short)0, 4 * min(C, T - c0 * C),
-                                                  0x00020000));
+                __builtin_amdgcn_make_buffer_rsrc(dlar + c0 * C, (short)0, 4 * min(C, T - c0 * C), 0x00020000));
     if (dS0) {
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dS0[soff + (16 * wl + 4 * g + r) * DK + 16 * jt + i] = dS[jt][r];
+        for (int r = 0; r < 4; ++r) dS0[R.state() + (16 * wl + 4 * g + r) * ld + 16 * jt + i] = dS[jt][r];
     }
   }
 }
@@ -899,6 +944,144 @@ bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
   return D == DK && Cc == C;
 }
 
+// Heads of 128 (four scans each): the scan count and the slot sum's thread count (16 per row of 128) stay in range.
+bool wide_shape_ok(int64_t B, int64_t H, int64_t T) {
+  if (B <= 0 || H <= 0 || T <= 0) return false;
+  if (4 * B * H >= ((int64_t)1 << 31) || T >= ((int64_t)1 << 28)) return false;
+  return B * H * T < ((int64_t)1 << 27);
+}
+
+int64_t seg_count(int64_t T, int64_t seg_chunks) { return ((T + C - 1) / C + seg_chunks - 1) / seg_chunks; }
+
+int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
+
+// workspace of the segmented passes over `scans` 64 x 64 scans: E (F in the backward; fp32 64 x 64 per segment,
+// later the state entering it) then the segment's total log-decay l
+int64_t seg_bytes(int64_t scans, int64_t T, int64_t seg_chunks) {
+  const int64_t n = scans * seg_count(T, seg_chunks);
+  return n * DK * DK * (int64_t)sizeof(float) + align256(n * (int64_t)sizeof(float));
+}
+
+// The plain forward over `scans` scans (B H narrow heads, 4 B H wide): one workgroup per scan when seg_chunks covers
+// the sequence, else the segmented forward's three launches on `ws` (seg_bytes(scans, T, seg_chunks) bytes). theta,
+// window: the carried windows (narrow heads only; H indexes theta).
+template <bool WIDE>
+int launch_fwd(const void* q, const void* k, const void* v, const float* la, const float* S0, const float* theta,
+               int64_t window, void* o, void* o1, float* S_final, void* sent, void* ws, int64_t scans, int64_t H,
+               int64_t T, int64_t seg_chunks, hipStream_t stream) {
+  {
+    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_fwd<WIDE>, kFwdSmem);
+    if (e != hipSuccess) return (int)e;
+  }
+  const int NC = (int)((T + C - 1) / C);
+  if (seg_chunks >= NC) {
+    hipLaunchKernelGGL(aspin_plain_fwd<WIDE>, dim3((unsigned)scans), dim3(kFwdWaves * 64), kFwdSmem, stream,
+                       (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, S0, nullptr, (__bf16*)o,
+                       (__bf16*)o1, S_final, (__bf16*)sent, (int)T, NC, NC);
+    PGN_RETURN_LAUNCH();
+  }
+  const int64_t nseg = seg_count(T, seg_chunks);
+  float* E = (float*)ws;
+  float* lseg = E + scans * nseg * DK * DK;
+  const unsigned nblk = (unsigned)(scans * nseg);
+  hipLaunchKernelGGL((aspin_plain_segsum<true, WIDE>), dim3(nblk), dim3(256), 2 * kSumBuf, stream, (const __bf16*)k,
+                     (const __bf16*)v, la, E, lseg, (int)T, NC, (int)seg_chunks);
+  hipLaunchKernelGGL((aspin_plain_segprefix<false, WIDE>), dim3((unsigned)(scans * 8)), dim3(256), 0, stream, S0,
+                     window > 0 ? theta : nullptr, (float)window, window > 0 ? (int)(window / C / seg_chunks) : 1, E,
+                     lseg, S_final, (int)H, (int)nseg);
+  hipLaunchKernelGGL(aspin_plain_fwd<WIDE>, dim3(nblk), dim3(kFwdWaves * 64), kFwdSmem, stream, (const __bf16*)q,
+                     (const __bf16*)k, (const __bf16*)v, la, nullptr, E, (__bf16*)o, (__bf16*)o1, nullptr,
+                     (__bf16*)sent, (int)T, NC, (int)seg_chunks);
+  PGN_RETURN_LAUNCH();
+}
+
+// The plain backward over `scans` scans, one workgroup per scan or segmented as the forward.
+template <bool WIDE>
+int launch_bwd(const void* q, const void* k, const void* v, const float* la, const void* sent, const void* dO,
+               const float* dS_final, void* dq, void* dq1, void* dk, void* dk1, void* dv, void* dv1, float* dla,
+               float* dla1, float* dS0, void* ws, int64_t scans, int64_t T, int64_t seg_chunks, hipStream_t stream) {
+  {
+    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_bwd<WIDE>, kBwdSmem);
+    if (e != hipSuccess) return (int)e;
+  }
+  const int NC = (int)((T + C - 1) / C);
+  if (seg_chunks >= NC) {
+    hipLaunchKernelGGL(aspin_plain_bwd<WIDE>, dim3((unsigned)scans), dim3(512), kBwdSmem, stream, (const __bf16*)q,
+                       (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent, (const __bf16*)dO, dS_final,
+                       nullptr, (__bf16*)dq, (__bf16*)dq1, (__bf16*)dk, (__bf16*)dk1, (__bf16*)dv, (__bf16*)dv1, dla,
+                       dla1, dS0, (int)T, NC, NC);
+    PGN_RETURN_LAUNCH();
+  }
+  const int64_t nseg = seg_count(T, seg_chunks);
+  float* F = (float*)ws;
+  float* lseg = F + scans * nseg * DK * DK;
+  const unsigned nblk = (unsigned)(scans * nseg);
+  hipLaunchKernelGGL((aspin_plain_segsum<false, WIDE>), dim3(nblk), dim3(256), 2 * kSumBuf, stream, (const __bf16*)q,
+                     (const __bf16*)dO, la, F, lseg, (int)T, NC, (int)seg_chunks);
+  hipLaunchKernelGGL((aspin_plain_segprefix<true, WIDE>), dim3((unsigned)(scans * 8)), dim3(256), 0, stream, dS_final,
+                     nullptr, 0.f, 1, F, lseg, dS0, 1, (int)nseg);
+  hipLaunchKernelGGL(aspin_plain_bwd<WIDE>, dim3(nblk), dim3(512), kBwdSmem, stream, (const __bf16*)q,
+                     (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent, (const __bf16*)dO, nullptr, F,
+                     (__bf16*)dq, (__bf16*)dq1, (__bf16*)dk, (__bf16*)dk1, (__bf16*)dv, (__bf16*)dv1, dla, dla1,
+                     nullptr, (int)T, NC, (int)seg_chunks);
+  PGN_RETURN_LAUNCH();
+}
+
+// The slot sums of the wide entry points: for each bf16 pair p with x[p] set, x[p][i] <- x[p][i] + y[p][i] over n
+// elements (the fp32 sum of the two bf16 values rounded once to bf16, as a bf16 tensor add rounds), and, when dla is
+// set, dla[i] <- ((dla[i] + w[i]) + w[m + i]) + w[2 m + i] over m fp32 elements. Thread u covers elements
+// 8u .. 8u + 7 of every pair (n % 8 == 0) and fp32 element u (m <= n / 8).
+struct JoinArgs {
+  __bf16* x[3];
+  const __bf16* y[3];
+  float* dla;
+  const float* w;
+  int64_t n, m;
+};
+
+__global__ __launch_bounds__(256) void aspin_wide_join(JoinArgs a) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (8 * u < a.n) {
+    bf16x8 xs[3], ys[3];
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+      if (a.x[p]) {
+        xs[p] = *reinterpret_cast<const bf16x8*>(a.x[p] + 8 * u);
+        ys[p] = *reinterpret_cast<const bf16x8*>(a.y[p] + 8 * u);
+      }
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+      if (a.x[p]) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xs[p][j] = pgn_bf16(pgn_f32(xs[p][j]) + pgn_f32(ys[p][j]));
+        *reinterpret_cast<bf16x8*>(a.x[p] + 8 * u) = xs[p];
+      }
+  }
+  if (a.dla && u < a.m) a.dla[u] = ((a.dla[u] + a.w[u]) + a.w[a.m + u]) + a.w[2 * a.m + u];
+}
+
+int launch_join(const JoinArgs& a, hipStream_t stream) {
+  const int64_t units = a.n / 8;
+  hipLaunchKernelGGL(aspin_wide_join, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, stream, a);
+  PGN_RETURN_LAUNCH();
+}
+
+// workspace of the wide entry points: the slot-1 outputs (o; or dq, dk, dv and three dla slots), then the segmented
+// passes' workspace when seg_chunks does not cover the sequence
+int64_t wide_slot_bytes(int64_t B, int64_t H, int64_t T) { return align256(B * H * T * 2 * DK * (int64_t)sizeof(__bf16)); }
+
+int64_t wide_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t seg_chunks, bool backward) {
+  const int64_t slot = wide_slot_bytes(B, H, T);
+  int64_t n = backward ? 3 * slot + align256(3 * B * H * T * (int64_t)sizeof(float)) : slot;
+  if (seg_chunks < (T + C - 1) / C) n += seg_bytes(4 * B * H, T, seg_chunks);
+  return n;
+}
+
+bool wide_args_ok(int64_t B, int64_t H, int64_t T, int64_t seg_chunks) {
+  return wide_shape_ok(B, H, T) && seg_chunks >= 1 && seg_chunks < ((int64_t)1 << 28) &&
+         4 * B * H * seg_count(T, seg_chunks) < ((int64_t)1 << 31);
+}
+
 }  // namespace
 
 extern "C" int pragnosia_aspin_chunk_fwd(const void* q, const void* k, const void* v, const float* la, const float* S0,
@@ -907,33 +1090,14 @@ extern "C" int pragnosia_aspin_chunk_fwd(const void* q, const void* k, const voi
   if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
   PGN_CHECK_ARG(q && k && v && la && o && S_final);
-  {
-    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_fwd, kFwdSmem);
-    if (e != hipSuccess) return (int)e;
-  }
-  const int NC = (int)((T + C - 1) / C);
-  hipLaunchKernelGGL(aspin_plain_fwd, dim3((unsigned)(B * H)), dim3(kFwdWaves * 64), kFwdSmem, (hipStream_t)stream,
-                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, S0, (__bf16*)o, S_final,
-                     (__bf16*)sent, (int)T, NC, NC);
-  PGN_RETURN_LAUNCH();
+  return launch_fwd<false>(q, k, v, la, S0, nullptr, 0, o, nullptr, S_final, sent, nullptr, B * H, H, T,
+                           (T + C - 1) / C, (hipStream_t)stream);
 }
-
-namespace {
-
-// workspace of the segmented forward: E (fp32 D x D per segment, later the entering states) then l per segment
-int64_t seg_count(int64_t T, int64_t seg_chunks) { return ((T + C - 1) / C + seg_chunks - 1) / seg_chunks; }
-
-int64_t seg_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t seg_chunks) {
-  const int64_t n = B * H * seg_count(T, seg_chunks);
-  return n * DK * DK * (int64_t)sizeof(float) + ((n * (int64_t)sizeof(float) + 255) / 256) * 256;
-}
-
-}  // namespace
 
 extern "C" int64_t pragnosia_aspin_chunk_seg_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D,
                                                              int64_t chunk, int64_t seg_chunks) {
   if (D != DK || chunk != C || seg_chunks < 1 || !shape_ok(B, H, T, D, chunk)) return -1;
-  return seg_workspace_bytes(B, H, T, seg_chunks);
+  return seg_bytes(B * H, T, seg_chunks);
 }
 
 namespace {
@@ -948,28 +1112,13 @@ bool fwd_seg_args_ok(const void* q, const void* k, const void* v, const float* l
   return B * H * seg_count(T, seg_chunks) < ((int64_t)1 << 31);
 }
 
-// The segmented forward's three launches on a workspace of at least seg_workspace_bytes(...) bytes.
+// The segmented forward's three launches on a workspace of at least seg_bytes(B H, T, seg_chunks) bytes (seg_chunks
+// at least the sequence's chunk count: one workgroup per head, the workspace unused).
 int launch_fwd_seg(const void* q, const void* k, const void* v, const float* la, const float* S0, const float* theta,
                    int64_t window, void* o, float* S_final, void* sent, void* workspace, int64_t B, int64_t H,
                    int64_t T, int64_t seg_chunks, void* stream) {
-  const int64_t nseg = seg_count(T, seg_chunks);
-  {
-    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_fwd, kFwdSmem);
-    if (e != hipSuccess) return (int)e;
-  }
-  const int NC = (int)((T + C - 1) / C);
-  float* E = (float*)workspace;
-  float* lseg = E + B * H * nseg * DK * DK;
-  const unsigned nblk = (unsigned)(B * H * nseg);
-  hipLaunchKernelGGL(aspin_plain_segsum<true>, dim3(nblk), dim3(256), 2 * kSumBuf, (hipStream_t)stream, (const __bf16*)k,
-                     (const __bf16*)v, la, E, lseg, (int)T, NC, (int)seg_chunks);
-  hipLaunchKernelGGL(aspin_plain_segprefix<false>, dim3((unsigned)(B * H * 8)), dim3(256), 0, (hipStream_t)stream, S0,
-                     window > 0 ? theta : nullptr, (float)window, (int)(window / C / seg_chunks), E, lseg, S_final,
-                     (int)H, (int)nseg);
-  hipLaunchKernelGGL(aspin_plain_fwd, dim3(nblk), dim3(kFwdWaves * 64), kFwdSmem, (hipStream_t)stream,
-                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, E, (__bf16*)o, nullptr,
-                     (__bf16*)sent, (int)T, NC, (int)seg_chunks);
-  PGN_RETURN_LAUNCH();
+  return launch_fwd<false>(q, k, v, la, S0, theta, window, o, nullptr, S_final, sent, workspace, B * H, H, T,
+                           seg_chunks, (hipStream_t)stream);
 }
 
 }  // namespace
@@ -981,7 +1130,7 @@ extern "C" int pragnosia_aspin_chunk_fwd_seg(const void* q, const void* k, const
                                              int64_t seg_chunks, void* stream) {
   if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(fwd_seg_args_ok(q, k, v, la, theta, window, o, S_final, B, H, T, D, chunk, seg_chunks));
-  PGN_CHECK_ARG(workspace && workspace_bytes >= seg_workspace_bytes(B, H, T, seg_chunks));
+  PGN_CHECK_ARG(workspace && workspace_bytes >= seg_bytes(B * H, T, seg_chunks));
   return launch_fwd_seg(q, k, v, la, S0, theta, window, o, S_final, sent, workspace, B, H, T, seg_chunks, stream);
 }
 
@@ -1020,7 +1169,7 @@ extern "C" int pragnosia_aspin_chunk_fwd_seg_noalloc(const void* q, const void* 
                                                      int64_t D, int64_t chunk, int64_t seg_chunks, void* stream) {
   if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(fwd_seg_args_ok(q, k, v, la, theta, window, o, S_final, B, H, T, D, chunk, seg_chunks));
-  if (seg_workspace_bytes(B, H, T, seg_chunks) > (int64_t)PRAGNOSIA_SEG_SCRATCH_BYTES) return PRAGNOSIA_ERR_TOO_LARGE;
+  if (seg_bytes(B * H, T, seg_chunks) > (int64_t)PRAGNOSIA_SEG_SCRATCH_BYTES) return PRAGNOSIA_ERR_TOO_LARGE;
   void* ws = nullptr;
   const hipError_t e = scratch_address(&ws);
   if (e != hipSuccess) return (int)e;
@@ -1036,15 +1185,8 @@ extern "C" int pragnosia_aspin_chunk_bwd(const void* q, const void* k, const voi
   if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
   PGN_CHECK_ARG(q && k && v && la && sent && dO && dq && dk && dv && dla);
-  {
-    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_bwd, kBwdSmem);
-    if (e != hipSuccess) return (int)e;
-  }
-  const int NC = (int)((T + C - 1) / C);
-  hipLaunchKernelGGL(aspin_plain_bwd, dim3((unsigned)(B * H)), dim3(512), kBwdSmem, (hipStream_t)stream,
-                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent,
-                     (const __bf16*)dO, dS_final, (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, dla, dS0, (int)T, NC, NC);
-  PGN_RETURN_LAUNCH();
+  return launch_bwd<false>(q, k, v, la, sent, dO, dS_final, dq, nullptr, dk, nullptr, dv, nullptr, dla, nullptr, dS0,
+                           nullptr, B * H, T, (T + C - 1) / C, (hipStream_t)stream);
 }
 
 extern "C" int pragnosia_aspin_chunk_bwd_seg(const void* q, const void* k, const void* v, const float* la,
@@ -1056,23 +1198,65 @@ extern "C" int pragnosia_aspin_chunk_bwd_seg(const void* q, const void* k, const
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
   PGN_CHECK_ARG(q && k && v && la && sent && dO && dq && dk && dv && dla && workspace);
   PGN_CHECK_ARG(seg_chunks >= 1 && seg_chunks < ((int64_t)1 << 28));
-  PGN_CHECK_ARG(workspace_bytes >= seg_workspace_bytes(B, H, T, seg_chunks));
-  const int64_t nseg = seg_count(T, seg_chunks);
-  PGN_CHECK_ARG(B * H * nseg < ((int64_t)1 << 31));
-  {
-    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_bwd, kBwdSmem);
-    if (e != hipSuccess) return (int)e;
-  }
-  const int NC = (int)((T + C - 1) / C);
-  float* F = (float*)workspace;
-  float* lseg = F + B * H * nseg * DK * DK;
-  const unsigned nblk = (unsigned)(B * H * nseg);
-  hipLaunchKernelGGL(aspin_plain_segsum<false>, dim3(nblk), dim3(256), 2 * kSumBuf, (hipStream_t)stream,
-                     (const __bf16*)q, (const __bf16*)dO, la, F, lseg, (int)T, NC, (int)seg_chunks);
-  hipLaunchKernelGGL(aspin_plain_segprefix<true>, dim3((unsigned)(B * H * 8)), dim3(256), 0, (hipStream_t)stream,
-                     dS_final, nullptr, 0.f, 1, F, lseg, dS0, (int)H, (int)nseg);
-  hipLaunchKernelGGL(aspin_plain_bwd, dim3(nblk), dim3(512), kBwdSmem, (hipStream_t)stream, (const __bf16*)q,
-                     (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent, (const __bf16*)dO, F,
-                     (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, dla, nullptr, (int)T, NC, (int)seg_chunks);
-  PGN_RETURN_LAUNCH();
+  PGN_CHECK_ARG(workspace_bytes >= seg_bytes(B * H, T, seg_chunks));
+  PGN_CHECK_ARG(B * H * seg_count(T, seg_chunks) < ((int64_t)1 << 31));
+  return launch_bwd<false>(q, k, v, la, sent, dO, dS_final, dq, nullptr, dk, nullptr, dv, nullptr, dla, nullptr, dS0,
+                           workspace, B * H, T, seg_chunks, (hipStream_t)stream);
+}
+
+extern "C" int64_t pragnosia_aspin_chunk_wide_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D,
+                                                              int64_t chunk, int64_t seg_chunks, int32_t backward) {
+  if (D != 2 * DK || chunk != C || !wide_args_ok(B, H, T, seg_chunks)) return -1;
+  return wide_workspace_bytes(B, H, T, seg_chunks, backward != 0);
+}
+
+extern "C" int pragnosia_aspin_chunk_fwd_wide(const void* q, const void* k, const void* v, const float* la,
+                                              const float* S0, void* o, float* S_final, void* sent, void* workspace,
+                                              int64_t workspace_bytes, int64_t B, int64_t H, int64_t T, int64_t D,
+                                              int64_t chunk, int64_t seg_chunks, void* stream) {
+  if (D != 2 * DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(wide_args_ok(B, H, T, seg_chunks));
+  PGN_CHECK_ARG(q && k && v && la && o && S_final && workspace);
+  PGN_CHECK_ARG(workspace_bytes >= wide_workspace_bytes(B, H, T, seg_chunks, false));
+  char* ws = (char*)workspace;
+  void* o1 = ws;
+  const int rc = launch_fwd<true>(q, k, v, la, S0, nullptr, 0, o, o1, S_final, sent, ws + wide_slot_bytes(B, H, T),
+                                  4 * B * H, 4 * H, T, seg_chunks, (hipStream_t)stream);
+  if (rc != PRAGNOSIA_OK) return rc;
+  JoinArgs a = {};
+  a.x[0] = (__bf16*)o;
+  a.y[0] = (const __bf16*)o1;
+  a.n = B * H * T * 2 * DK;
+  return launch_join(a, (hipStream_t)stream);
+}
+
+extern "C" int pragnosia_aspin_chunk_bwd_wide(const void* q, const void* k, const void* v, const float* la,
+                                              const void* sent, const void* dO, const float* dS_final, void* dq,
+                                              void* dk, void* dv, float* dla, float* dS0, void* workspace,
+                                              int64_t workspace_bytes, int64_t B, int64_t H, int64_t T, int64_t D,
+                                              int64_t chunk, int64_t seg_chunks, void* stream) {
+  if (D != 2 * DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(wide_args_ok(B, H, T, seg_chunks));
+  PGN_CHECK_ARG(q && k && v && la && sent && dO && dq && dk && dv && dla && workspace);
+  PGN_CHECK_ARG(workspace_bytes >= wide_workspace_bytes(B, H, T, seg_chunks, true));
+  char* ws = (char*)workspace;
+  const int64_t slot = wide_slot_bytes(B, H, T);
+  void *dq1 = ws, *dk1 = ws + slot, *dv1 = ws + 2 * slot;
+  float* dla1 = (float*)(ws + 3 * slot);
+  void* segws = ws + 3 * slot + align256(3 * B * H * T * (int64_t)sizeof(float));
+  const int rc = launch_bwd<true>(q, k, v, la, sent, dO, dS_final, dq, dq1, dk, dk1, dv, dv1, dla, dla1, dS0, segws,
+                                  4 * B * H, T, seg_chunks, (hipStream_t)stream);
+  if (rc != PRAGNOSIA_OK) return rc;
+  JoinArgs a = {};
+  a.x[0] = (__bf16*)dq;
+  a.y[0] = (const __bf16*)dq1;
+  a.x[1] = (__bf16*)dk;
+  a.y[1] = (const __bf16*)dk1;
+  a.x[2] = (__bf16*)dv;
+  a.y[2] = (const __bf16*)dv1;
+  a.dla = dla;
+  a.w = dla1;
+  a.n = B * H * T * 2 * DK;
+  a.m = B * H * T;
+  return launch_join(a, (hipStream_t)stream);
 }

@@ -244,9 +244,10 @@ PGN_DEVICE void put_blk_T(__bf16* tile, const Blk4& x, int r0, int c0) {
 // Staging of row-major 64-column bf16 tiles in 16-byte row segments, for tiles that are only ever read untransposed
 // or through frag_tr: segment e covers row e / 8, columns 8 (e % 8) .. +7, so one 64-lane load reads eight whole
 // 128-byte rows. Rows >= nrows (>= 1) read as zero (the load itself is clamped to row nrows - 1, unconditional).
-PGN_DEVICE bf16x8 load_seg(const __bf16* __restrict__ src, int nrows, int e) {
+// `ld` is the source's row pitch in elements (64 for a dense tile; 128 for one half of rows of 128).
+PGN_DEVICE bf16x8 load_seg(const __bf16* __restrict__ src, int nrows, int e, int ld = 64) {
   const int r = e >> 3;
-  const bf16x8 v = *reinterpret_cast<const bf16x8*>(src + (size_t)min(r, nrows - 1) * 64 + 8 * (e & 7));
+  const bf16x8 v = *reinterpret_cast<const bf16x8*>(src + (size_t)min(r, nrows - 1) * ld + 8 * (e & 7));
   if (r < nrows) return v;
   bf16x8 z;
 #pragma unroll

@@ -429,6 +429,107 @@ aspin_chunk.register_autograd(_aspin_backward, setup_context=_aspin_setup)
 
 
 # ---------------------------------------------------------------------------------------------------------------
+# the plain rule at head dim 128: assoc_scan_kernel at D = 128 (src/assoc_kernel.py:21,302-323) and its backward
+HEAD_DIM_WIDE = 128
+
+
+def _expect_wide(op: str, q: Tensor, k, v, la) -> None:
+    _expect(op, q.device, q=(q, (None, None, None, HEAD_DIM_WIDE)))
+    B, H, T, D = q.shape
+    _expect(op, q.device, k=(k, (B, H, T, D)), v=(v, (B, H, T, D)), la=(la, (B, H, T)))
+
+
+def _wide_workspace(op: str, B: int, H: int, T: int, P: int, backward: bool, dev) -> Tensor:
+    nbytes = lib().pragnosia_aspin_chunk_wide_workspace_bytes(B, H, T, HEAD_DIM_WIDE, CHUNK, P, int(backward))
+    if nbytes < 0:
+        raise PragnosiaError(f"{op}: shape rejected (B={B} H={H} T={T} segment={P})")
+    return torch.empty(nbytes, device=dev, dtype=torch.uint8)
+
+
+@torch.library.custom_op("pragnosia::aspin_chunk_wide", mutates_args=())
+def aspin_chunk_wide(q: Tensor, k: Tensor, v: Tensor, la: Tensor, S0: Optional[Tensor],
+                     want_sent: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """Plain-rule chunked scan at head dim 128, as four 64 x 64 scans per head (key half x value half) that read
+    the 128-wide rows in place. q, k, v (B, H, T, 128) (cast to bf16), la (B, H, T) fp32, S0 (B, H, 128, 128) fp32 or
+    None. Returns (o bf16 (B, H, T, 128), S_final fp32 (B, H, 128, 128), sent bf16 (B, H, 4, NC, 64, 64): the state
+    entering every chunk per scan, scan 2 kh + vh holding block (rows 64 kh.., columns 64 vh..); or an empty tensor
+    if not wanted). `wide_sent` turns sent into (B, H, NC, 128, 128)."""
+    _require_gpu(q, k, v, la, S0)
+    _expect_wide("aspin_chunk_wide", q, k, v, la)
+    B, H, T, D = q.shape
+    _expect("aspin_chunk_wide", q.device, S0=(S0, (B, H, D, D)))
+    q, k, v, la, S0 = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(S0)
+    NC = (T + CHUNK - 1) // CHUNK
+    o = torch.empty(B, H, T, D, device=q.device, dtype=torch.bfloat16)
+    S = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
+    sent = (torch.empty(B, H, 4, NC, CHUNK, CHUNK, device=q.device, dtype=torch.bfloat16) if want_sent
+            else q.new_empty(0, dtype=torch.bfloat16))
+    P = seg_chunks(4 * B * H, NC, range(1, NC + 1))
+    ws = _wide_workspace("aspin_chunk_wide", B, H, T, P, False, q.device)
+    check(lib().pragnosia_aspin_chunk_fwd_wide(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(S0), _ptr(o), _ptr(S),
+                                               _ptr(sent) if want_sent else None, _ptr(ws), ws.numel(),
+                                               B, H, T, D, CHUNK, P, _stream(q)), "pragnosia_aspin_chunk_fwd_wide")
+    return o, S, sent
+
+
+@aspin_chunk_wide.register_fake
+def _(q, k, v, la, S0, want_sent):
+    B, H, T, D = q.shape
+    NC = (T + CHUNK - 1) // CHUNK
+    sent = (q.new_empty(B, H, 4, NC, CHUNK, CHUNK, dtype=torch.bfloat16) if want_sent
+            else q.new_empty(0, dtype=torch.bfloat16))
+    return q.new_empty(B, H, T, D, dtype=torch.bfloat16), q.new_empty(B, H, D, D, dtype=torch.float32), sent
+
+
+def wide_sent(sent: Tensor) -> Tensor:
+    """aspin_chunk_wide's per-scan entering states (B, H, 4, NC, 64, 64) as whole states (B, H, NC, 128, 128)."""
+    B, H, _, NC, h, _ = sent.shape
+    return sent.view(B, H, 2, 2, NC, h, h).permute(0, 1, 4, 2, 5, 3, 6).reshape(B, H, NC, 2 * h, 2 * h)
+
+
+@torch.library.custom_op("pragnosia::aspin_chunk_wide_bwd", mutates_args=())
+def aspin_chunk_wide_bwd(q: Tensor, k: Tensor, v: Tensor, la: Tensor, sent: Tensor, do: Tensor,
+                         dS: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Backward of aspin_chunk_wide. Returns (dq, dk, dv bf16, dla fp32, dS0 fp32)."""
+    _require_gpu(q, k, v, la, sent, do, dS)
+    _expect_wide("aspin_chunk_wide_bwd", q, k, v, la)
+    B, H, T, D = q.shape
+    NC = (T + CHUNK - 1) // CHUNK
+    _expect("aspin_chunk_wide_bwd", q.device, sent=(sent, (B, H, 4, NC, CHUNK, CHUNK)), do=(do, (B, H, T, D)),
+            dS=(dS, (B, H, D, D)))
+    q, k, v, la, sent, do, dS = _bf16(q), _bf16(k), _bf16(v), _f32(la), _bf16(sent), _bf16(do), _f32(dS)
+    dq, dk, dv = (torch.empty(B, H, T, D, device=q.device, dtype=torch.bfloat16) for _ in range(3))
+    dla = torch.empty(B, H, T, device=q.device, dtype=torch.float32)
+    dS0 = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
+    P = seg_chunks(4 * B * H, NC, range(1, NC + 1), "bwd")
+    ws = _wide_workspace("aspin_chunk_wide_bwd", B, H, T, P, True, q.device)
+    check(lib().pragnosia_aspin_chunk_bwd_wide(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(sent), _ptr(do), _ptr(dS),
+                                               _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla), _ptr(dS0), _ptr(ws),
+                                               ws.numel(), B, H, T, D, CHUNK, P, _stream(q)),
+          "pragnosia_aspin_chunk_bwd_wide")
+    return dq, dk, dv, dla, dS0
+
+
+@aspin_chunk_wide_bwd.register_fake
+def _(q, k, v, la, sent, do, dS):
+    B, H, T, D = q.shape
+    b = lambda *s: q.new_empty(*s, dtype=torch.bfloat16)
+    f = lambda *s: q.new_empty(*s, dtype=torch.float32)
+    return b(B, H, T, D), b(B, H, T, D), b(B, H, T, D), f(B, H, T), f(B, H, D, D)
+
+
+def _wide_backward(ctx, do, dS, _dsent):
+    q, k, v, la, sent = ctx.saved_tensors
+    if do is None:
+        do = torch.zeros(q.shape, device=q.device, dtype=torch.bfloat16)
+    dq, dk, dv, dla, dS0 = aspin_chunk_wide_bwd(q, k, v, la, sent, do.contiguous(), dS)
+    return dq, dk, dv, dla, (dS0 if ctx.has_s0 else None), None
+
+
+aspin_chunk_wide.register_autograd(_wide_backward, setup_context=_aspin_setup)
+
+
+# ---------------------------------------------------------------------------------------------------------------
 # aspin chunked scan, delta rule: replaces delta_scan_kernel and its ops, src/assoc_kernel.py:332-704
 @torch.library.custom_op("pragnosia::aspin_delta", mutates_args=())
 def aspin_delta(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor, S0: Optional[Tensor],

@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 9
+    assert L.pragnosia_abi_version() == 10
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 
@@ -78,6 +78,31 @@ def test_segmented_forward_arguments(L):
     assert L.pragnosia_aspin_chunk_bwd_seg(*flat(bargs(ws - 1, 3))) == -1           # workspace too small
     assert L.pragnosia_aspin_chunk_bwd_seg(*flat(bargs(ws, 0))) == -1               # empty segments
     assert L.pragnosia_aspin_chunk_bwd_seg(*([one] * 13), ws, 1, 1, 1000, 128, 64, 3, null) == -2   # head dim
+
+
+def test_wide_arguments(L):
+    """The head-dim-128 entry points' workspace query (one bf16 partial of o forward; partials of dq, dk, dv and
+    three dla slots backward; plus the segmented passes' workspace over 4 B H scans) and host-side rejections."""
+    null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    q = L.pragnosia_aspin_chunk_wide_workspace_bytes
+    slot = 2 * 3 * 1000 * 128 * 2                          # B2 H3 T1000: 1,536,000 bytes, a multiple of 256
+    dla = (3 * 2 * 3 * 1000 * 4 + 255) // 256 * 256
+    assert q(2, 3, 1000, 128, 64, 16, 0) == slot           # 16 chunks: one workgroup per scan
+    assert q(2, 3, 1000, 128, 64, 99, 1) == 3 * slot + dla
+    seg = 24 * 6 * 16384 + 768                             # 24 scans x 6 segments of 3 chunks, fp32 64 x 64 each
+    assert q(2, 3, 1000, 128, 64, 3, 0) == slot + seg
+    assert q(2, 3, 1000, 128, 64, 3, 1) == 3 * slot + dla + seg
+    assert q(2, 3, 1000, 64, 64, 16, 0) == -1 and q(2, 3, 1000, 128, 64, 0, 0) == -1 and q(0, 3, 1000, 128, 64, 16, 0) == -1
+    ws = q(1, 1, 1000, 128, 64, 3, 0)
+    fargs = lambda wsb, D, w: (one, one, one, one, null, one, one, null, w, wsb, 1, 1, 1000, D, 64, 3, null)
+    assert L.pragnosia_aspin_chunk_fwd_wide(*fargs(ws - 1, 128, one)) == -1      # workspace too small
+    assert L.pragnosia_aspin_chunk_fwd_wide(*fargs(ws, 128, null)) == -1         # no workspace
+    assert L.pragnosia_aspin_chunk_fwd_wide(*fargs(ws, 64, one)) == -2           # head dim
+    wb = q(1, 1, 1000, 128, 64, 3, 1)
+    bargs = lambda wsb, sent: (one, one, one, one, sent, one, null, one, one, one, one, null, one, wsb, 1, 1, 1000,
+                               128, 64, 3, null)
+    assert L.pragnosia_aspin_chunk_bwd_wide(*bargs(wb - 1, one)) == -1
+    assert L.pragnosia_aspin_chunk_bwd_wide(*bargs(wb, null)) == -1              # the backward needs sent
 
 
 def test_product_never_imports_oracle():

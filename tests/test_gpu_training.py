@@ -50,7 +50,15 @@ def _samples():
     with torch.no_grad():
         _, rstd = op.aspin_out(ob, wrms, 1e-6, True)
     x = r(3, 96)
+    qw, kw, vw = (F.normalize(r(B, 1, T, 128), dim=-1).bfloat16().requires_grad_(True) for _ in range(3))
+    law = F.logsigmoid(r(B, 1, T) + 3).requires_grad_(True)
+    S0w = (r(B, 1, 128, 128) * 0.1).requires_grad_(True)
+    with torch.no_grad():
+        _, _, sentw = op.aspin_chunk_wide(qw, kw, vw, law, S0w, True)
     return [
+        ("aspin_chunk_wide", (qw, kw, vw, law, S0w, True)),
+        ("aspin_chunk_wide_bwd", (qw.detach(), kw.detach(), vw.detach(), law.detach(), sentw,
+                                  r(B, 1, T, 128).bfloat16(), r(B, 1, 128, 128))),
         ("diag_scan", (u, lm_, an, h0r, h0i)),
         ("diag_scan_bwd", (r(B, T, 40), r(B, 40), r(B, 40), lm_.detach(), an.detach(), hr, hi, h0r.detach(),
                            h0i.detach())),

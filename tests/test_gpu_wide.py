@@ -5,6 +5,8 @@ T = 1 step against the oracle's module; an LM with 128-dim heads, forward_carrie
 
 Tolerances as for the 64-dim paths: bf16 operands, max relative error max|x - ref| / max|ref| <= 2e-2 on outputs and
 states, 5e-2 on gradients; the T = 1 step is fp32 throughout (1e-4)."""
+import ctypes
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -38,6 +40,89 @@ def test_wide_plain_scan_matches_oracle(T, s0):
     for a, b in zip(dev, ref):
         if a is not None:
             assert rel(a.grad, b.grad) < TOL_GRAD
+
+
+def _wide_inputs(B, H, T, seed):
+    g = torch.Generator().manual_seed(seed)
+    D = 128
+    q = F.normalize(torch.randn(B, H, T, D, generator=g), dim=-1).bfloat16()
+    k = F.normalize(torch.randn(B, H, T, D, generator=g), dim=-1).bfloat16()
+    v = torch.randn(B, H, T, D, generator=g).bfloat16()
+    la = F.logsigmoid(torch.randn(B, H, T, generator=g) + 3)
+    S0 = torch.randn(B, H, D, D, generator=g) * 0.2
+    wo, wS = torch.randn(B, H, T, D, generator=g), torch.randn(B, H, D, D, generator=g)
+    return q, k, v, la, S0, wo, wS
+
+
+def test_wide_plain_scan_segmented_matches_oracle():
+    """Few heads over a long sequence (B1 H1 T1000: 4 scans) take the segment-parallel passes in both directions;
+    forward and backward against the fp64 oracle."""
+    from pragnosia_amd import ops
+    from pragnosia_amd.assoc import assoc_scan
+    B, H, T = 1, 1, 1000
+    NC = (T + 63) // 64
+    assert ops.seg_chunks(4 * B * H, NC, range(1, NC + 1)) < NC
+    assert ops.seg_chunks(4 * B * H, NC, range(1, NC + 1), "bwd") < NC
+    q, k, v, la, S0, wo, wS = _wide_inputs(B, H, T, 70)
+    ref = [t.double().requires_grad_(True) for t in (q, k, v, la, S0)]
+    o_r, S_r, _ = OA.scan_twopass(*ref, 64)
+    ((o_r * wo.double()).sum() + (S_r * wS.double()).sum()).backward()
+    dev = [t.cuda().requires_grad_(True) for t in (q, k, v, la, S0)]
+    o, S = assoc_scan(*dev)
+    ((o.float() * wo.cuda()).sum() + (S * wS.cuda()).sum()).backward()
+    assert rel(o, o_r) < TOL_OUT and rel(S, S_r) < TOL_OUT
+    for a, b in zip(dev, ref):
+        assert rel(a.grad, b.grad) < TOL_GRAD
+
+
+def test_wide_abi_segment_lengths_agree():
+    """The C ABI at head dim 128 over segment lengths 1, 3 (ragged: 11 chunks) and whole (one workgroup per scan):
+    the segmented forward and backward agree with the one-pass result, which matches the oracle; sent is the same
+    in every case (each chunk's entering state is the one-pass scan's up to fp32 summation order)."""
+    from pragnosia_amd import ops
+    from pragnosia_amd._lib import lib
+    L = lib()
+    B, H, T, D = 2, 1, 700, 128
+    NC = 11
+    q, k, v, la, S0, wo, wS = _wide_inputs(B, H, T, 71)
+    ref = [t.double().requires_grad_(True) for t in (q, k, v, la, S0)]
+    o_r, S_r, _ = OA.scan_twopass(*ref, 64)
+    ((o_r * wo.double()).sum() + (S_r * wS.double()).sum()).backward()
+    q, k, v, la, S0 = (t.cuda().contiguous() for t in (q, k, v, la, S0))
+    do = wo.bfloat16().cuda()
+    dS = wS.cuda()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = {}
+    for seg in (NC, 3, 1):
+        o = torch.empty(B, H, T, D, device="cuda", dtype=torch.bfloat16)
+        S = torch.empty(B, H, D, D, device="cuda")
+        sent = torch.empty(B, H, 4, NC, 64, 64, device="cuda", dtype=torch.bfloat16)
+        ws = torch.empty(L.pragnosia_aspin_chunk_wide_workspace_bytes(B, H, T, D, 64, seg, 0), device="cuda",
+                         dtype=torch.uint8)
+        print(f"wide fwd B{B} H{H} T{T} seg {seg}", flush=True)
+        assert L.pragnosia_aspin_chunk_fwd_wide(P(q), P(k), P(v), P(la), P(S0), P(o), P(S), P(sent), P(ws),
+                                                ws.numel(), B, H, T, D, 64, seg, s) == 0
+        dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+        dla = torch.empty_like(la)
+        dS0 = torch.empty_like(S0)
+        wb = torch.empty(L.pragnosia_aspin_chunk_wide_workspace_bytes(B, H, T, D, 64, seg, 1), device="cuda",
+                         dtype=torch.uint8)
+        print(f"wide bwd B{B} H{H} T{T} seg {seg}", flush=True)
+        assert L.pragnosia_aspin_chunk_bwd_wide(P(q), P(k), P(v), P(la), P(sent), P(do), P(dS), P(dq), P(dk), P(dv),
+                                                P(dla), P(dS0), P(wb), wb.numel(), B, H, T, D, 64, seg, s) == 0
+        torch.cuda.synchronize()
+        res[seg] = (o, S, sent, dq, dk, dv, dla, dS0)
+    o, S, sent, dq, dk, dv, dla, dS0 = res[NC]
+    assert rel(o, o_r) < TOL_OUT and rel(S, S_r) < TOL_OUT
+    for a, b in zip((dq, dk, dv, dla, dS0), ref):
+        assert rel(a, b.grad) < TOL_GRAD
+    for seg in (3, 1):
+        for a, b in zip(res[seg], res[NC]):
+            assert rel(a.float(), b.float()) < 1e-2, seg
+    # the whole states assembled from the per-scan blocks, against the oracle's entering states
+    _, _, sent_r = OA.scan_twopass(*(t.detach() for t in ref), 64)
+    assert rel(ops.wide_sent(res[NC][2]).float(), sent_r) < TOL_OUT
 
 
 def test_wide_carrier_forward_backward():
