@@ -160,6 +160,7 @@ def _(g, g_last_r, g_last_i, logmag, ang, hr, hi, h0r, h0i):
 
 
 def _diag_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
     u, logmag, ang, h0r, h0i = inputs
     hr, _, _, hi = output
     ctx.has_h0 = h0r is not None
@@ -228,6 +229,7 @@ def _(gy, o, weight, rstd):
 
 
 def _out_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
     o, weight, eps, out_bf16 = inputs
     _, rstd = output
     ctx.save_for_backward(o, weight, rstd)
@@ -236,6 +238,8 @@ def _out_setup(ctx, inputs, output):
 
 def _out_backward(ctx, gy, _grstd):
     o, weight, rstd = ctx.saved_tensors
+    if gy is None:
+        return None, None, None, None
     dO, dw = aspin_out_bwd(gy, o, weight, rstd)
     return dO.to(o.dtype), dw.to(weight.dtype), None, None
 
@@ -408,6 +412,7 @@ def _(q, k, v, la, sent, do, dS):
 
 
 def _aspin_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
     q, k, v, la, S0, want_sent = inputs
     _, _, sent = output
     if sent.numel() == 0 and any(ctx.needs_input_grad[:5]):
@@ -603,6 +608,7 @@ def _(q, k, v, la, beta, sent, W, X, do, dS):
 
 
 def _delta_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
     q, k, v, la, beta, S0, want_sent = inputs
     _, _, sent, W, X = output
     if sent.numel() == 0 and any(ctx.needs_input_grad[:6]):
@@ -730,6 +736,7 @@ def _(q, k, v, la, beta, ckpt, resid, do, dS):
 
 
 def _exact_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
     q, k, v, la, beta, S0, want_ckpt = inputs
     _, _, ckpt, resid = output
     if ckpt.numel() == 0 and any(ctx.needs_input_grad[:6]):
@@ -825,6 +832,7 @@ def _(qp, kp, vp, gate, theta, pos, dq, dk, dv):
 
 
 def _prep_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
     qp, kp, vp, gate, theta, pos = inputs
     ctx.has_gate = gate is not None
     ctx.dtypes = (qp.dtype, kp.dtype, vp.dtype, None if gate is None else gate.dtype, theta.dtype)
@@ -958,6 +966,7 @@ def _(P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, 
 
 
 def _prep_proj_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
     P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, pos = inputs
     ctx.H, ctx.beta_min, ctx.gated = H, beta_min, gated
     ctx.bias_dtype = (gate_bias if gated else beta_bias)

@@ -132,7 +132,7 @@ def test_rebase_kernel_and_gradient():
     out = torch.ops.pragnosia.aspin_rebase(Sk, thk, None, 300.0)
     (out * w.cuda()).sum().backward()
     assert rel(out, OA.rebase(S.double(), th.double(), 300.0)) < 1e-4
-    assert rel(Sk.grad, Sr.grad) < 1e-4 and rel(thk.grad, thr.grad) < 1e-3
+    assert rel(Sk.grad, Sr.grad) < 1e-4 and rel(thk.grad, thr.grad) < 1e-4
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -179,8 +179,9 @@ def test_spin_rf_forward_backward():
     ((yk - xk) * w.cuda()).sum().add(hk[0].sum() + 2 * hk[1].sum()).backward()
     assert rel(yk - xk, yr - xr) < 1e-4 and rel(hk[0], hr[0]) < 1e-4 and rel(hk[1], hr[1]) < 1e-4
     assert rel(xk.grad, xr.grad) < 1e-4
+    # parameter gradients are sums over B T tokens (the scalar gate's of mixed signs): measured <= 3e-5
     for name, p in mod.named_parameters():
-        assert rel(p.grad, sd[name].grad) < 1e-3, name
+        assert rel(p.grad, sd[name].grad) < 1e-4, name
 
 
 def _lm(mixer, seed):
