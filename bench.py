@@ -44,6 +44,9 @@ def parse():
                     help="run each hot kernel a fixed number of times (for rocprofv3 counter passes) and exit")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the configs[4] decode measurement (batch 1 and 64), print its JSON and exit")
+    ap.add_argument("--phase-rates", action="store_true",
+                    help="measure the MFMA rate inside the scan kernels' per-chunk phases from the instrumented "
+                         "build (libpragnosia_stamps.so), print its JSON and exit")
     return ap.parse_args()
 
 
@@ -810,6 +813,145 @@ def profile_kernels(reps=10):
 
 COPY_BYTES = 256 << 20
 
+# MFMAs (16x16x32 bf16, 16384 flops each) per 64-token chunk of one workgroup, counted from the kernels' code.
+# Plain forward: output waves 88 (per t block TB and value half: O^T = V^T A^T + S^T (Q o eL)^T, 3 or 4 a column
+# tile (2 A operands from TB 2 on), 2 column tiles, and the state update 2 x 2), score waves 20 (2 per s block at or
+# below the diagonal). Plain backward: group K 152 (P and dA 4 per block WL..3, then 4 dV^T and 4 dK^T tiles of 3 or
+# 4), group D 128 (P^T and dA^T 4 per block 0..WL, 4 dQ^T tiles of 3 or 4, the dS update 4 x 2). Delta forward
+# chain: 4 chain waves x 36 (U = K S 8, W = X rhs 6, O 14, state update 8) and the scores 20. Delta backward chain:
+# 4 chain waves x 44 (K dS 8, K S_c 8, (Q o eL)^T dO 8, dW 6, drhs 6, dS update 8) and the transposed scores 20.
+PHASE_MFMAS = {"plain_fwd": {"output": 88, "score": 20}, "plain_bwd": 280, "delta_fwd": 164, "delta_bwd_chain": 196}
+MFMA_FLOPS = 16 * 16 * 32 * 2
+
+
+def _rel32(x, ref):
+    """uint32 clock readings relative to ref, as signed int64 (differences within a kernel never wrap twice)."""
+    import numpy as np
+    d = (x.astype(np.int64) - ref.astype(np.int64)) % (1 << 32)
+    return np.where(d >= (1 << 31), d - (1 << 32), d)
+
+
+def _phase_stats(buf, nwg, nw, NC, waves_of, flops_of):
+    """Per-chunk phase windows from one stamp buffer ((workgroups, waves, 4 + 2 NC) uint32; entries 0-3 the clocks
+    at the role's start and the kernel's end, then each chunk's phase start and end): the shader clock's rate from
+    the 100 MHz clock beside it, each chunk's window (earliest start to latest end over waves_of(c)), and the MFMA
+    rate over the windows against the per-CU share of the bf16 peak."""
+    import numpy as np
+    s = buf.cpu().numpy().view(np.uint32).reshape(nwg, nw, 4 + 2 * NC)
+    mt_b, rt_b, mt_e, rt_e = (s[:, :, j].astype(np.int64) for j in range(4))
+    clk = float(np.median(((mt_e - mt_b) % (1 << 32)) / ((rt_e - rt_b) % (1 << 32)))) * 1e8
+    ref = s[:, :1, 0]
+    start, end = _rel32(s[:, :, 4::2], ref[..., None]), _rel32(s[:, :, 5::2], ref[..., None])
+    life = (_rel32(s[:, :, 2], ref).max(1) - _rel32(s[:, :, 0], ref).min(1)).astype(np.float64)
+    win = np.stack([(end[:, waves_of(c), c].max(1) - start[:, waves_of(c), c].min(1)).astype(np.float64)
+                    for c in range(NC)], 1)
+    fl = np.array([flops_of(c) for c in range(NC)], dtype=np.float64)
+    rate = fl.sum() * nwg / (win.sum() / clk)
+    peak_cu = BF16_PEAK_TFLOPS * 1e12 / 256
+    return {"shader_clock_GHz": round(clk / 1e9, 3),
+            "phase_us_median": round(float(np.median(win)) / clk * 1e6, 3),
+            "phase_TFLOPs_per_CU": round(rate / 1e12, 3),
+            "phase_frac_of_peak": round(rate / peak_cu, 4),
+            "phase_share_of_workgroup_life": round(float(win.sum(1).mean() / life.mean()), 4)}, fl.sum() * nwg
+
+
+def phase_rates(reps=50):
+    """MFMA rate inside the scan kernels' per-chunk phases at configs[2] (B16 T512 H12 D64), from the instrumented
+    build (libpragnosia_stamps.so: the same kernels, every wave writing its shader clock where its role's branch
+    starts, at the start and end of each chunk's phase, and at the kernel's end). A chunk's phase on a workgroup runs
+    from the earliest phase start to the latest phase end over the waves that contract in that barrier interval
+    (plain forward: the 8 output waves on chunk c and the 4 score waves on chunk c + 1; plain backward and the delta
+    chain kernels: all 8 waves), so it covers the operand reads, the MFMAs, the result stores and, in the delta
+    chain, its mid-chunk barrier. Rate = the chunk's MFMA flops (counted from the code, PHASE_MFMAS) / its window,
+    per CU, against the per-CU share of the dense bf16 peak (2.5 PFLOP/s / 256 CUs). The shader clock's rate comes
+    from the 100 MHz clock read beside it. Also reported: the share of each workgroup's lifetime spent in phases,
+    and the stamped entry points' times against the product library's (the stamps' own cost)."""
+    import ctypes
+    import torch
+    from pragnosia_amd._lib import SIGNATURES, lib as product_lib
+    dev = torch.device("cuda:0")
+    st = ctypes.CDLL(os.path.join(ROOT, "pragnosia_amd", "libpragnosia_stamps.so"))
+    libs = {"stamped": st, "product": product_lib()}
+    names = ("pragnosia_aspin_chunk_fwd", "pragnosia_aspin_chunk_bwd", "pragnosia_aspin_delta_fwd",
+             "pragnosia_aspin_delta_bwd")
+    for L in libs.values():
+        for name in names:
+            getattr(L, name).argtypes = SIGNATURES[name]
+            getattr(L, name).restype = ctypes.c_int
+    for unit in ("chunk", "delta"):
+        getattr(st, "pragnosia_stamps_set_" + unit).argtypes = [ctypes.c_void_p]
+        getattr(st, "pragnosia_stamps_set_" + unit).restype = ctypes.c_int
+    B, H, T, D = 16, 12, 512, 64
+    NC, nwg = T // 64, B * H
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    xp = aspin_inputs(B, H, T, D, 0, "plain", dev)
+    xd = aspin_inputs(B, H, T, D, 0, "delta", dev)
+    e = lambda *shape, dt=torch.float32: torch.empty(*shape, device=dev, dtype=dt)
+    bf = torch.bfloat16
+    o, dq, dk, dv, W = (e(B, H, T, D, dt=bf) for _ in range(5))
+    S, dS0 = e(B, H, D, D), e(B, H, D, D)
+    sent, X = e(B, H, NC, D, D, dt=bf), e(B, H, NC, 64, 64, dt=bf)
+    dla, dbeta = e(B, H, T), e(B, H, T)
+    wsb = product_lib().pragnosia_aspin_delta_bwd_workspace_bytes(B, H, T, D, 64)
+    ws = e(wsb, dt=torch.uint8)
+    run = {
+        "plain_fwd": lambda L: L.pragnosia_aspin_chunk_fwd(
+            P(xp["q"]), P(xp["k"]), P(xp["v"]), P(xp["la"]), None, P(o), P(S), P(sent), B, H, T, D, 64, sp),
+        "plain_bwd": lambda L: L.pragnosia_aspin_chunk_bwd(
+            P(xp["q"]), P(xp["k"]), P(xp["v"]), P(xp["la"]), P(sent), P(xp["do"]), P(xp["dS"]), P(dq), P(dk),
+            P(dv), P(dla), P(dS0), B, H, T, D, 64, sp),
+        "delta_fwd": lambda L: L.pragnosia_aspin_delta_fwd(
+            P(xd["q"]), P(xd["k"]), P(xd["v"]), P(xd["la"]), P(xd["beta"]), None, P(o), P(S), P(sent), P(W), P(X),
+            B, H, T, D, 64, sp),
+        "delta_bwd_chain": lambda L: L.pragnosia_aspin_delta_bwd(
+            P(xd["q"]), P(xd["k"]), P(xd["v"]), P(xd["la"]), P(xd["beta"]), P(sent), P(W), P(X), P(xd["do"]),
+            P(xd["dS"]), P(dq), P(dk), P(dv), P(dla), P(dbeta), P(dS0), P(ws), wsb, B, H, T, D, 64, sp)}
+    unit = {"plain_fwd": "chunk", "plain_bwd": "chunk", "delta_fwd": "delta", "delta_bwd_chain": "delta"}
+    waves = {"plain_fwd": 16, "plain_bwd": 8, "delta_fwd": 8, "delta_bwd_chain": 8}
+    pf = PHASE_MFMAS["plain_fwd"]
+    waves_of = {"plain_fwd": lambda c: list(range(8)) + (list(range(8, 12)) if c + 1 < NC else []),
+                "plain_bwd": lambda c: list(range(8)), "delta_fwd": lambda c: list(range(8)),
+                "delta_bwd_chain": lambda c: list(range(8))}
+    flops_of = {"plain_fwd": lambda c: (pf["output"] + (pf["score"] if c + 1 < NC else 0)) * MFMA_FLOPS,
+                "plain_bwd": lambda c: PHASE_MFMAS["plain_bwd"] * MFMA_FLOPS,
+                "delta_fwd": lambda c: PHASE_MFMAS["delta_fwd"] * MFMA_FLOPS,
+                "delta_bwd_chain": lambda c: PHASE_MFMAS["delta_bwd_chain"] * MFMA_FLOPS}
+
+    def timed(fn, L):
+        for _ in range(5):
+            assert fn(L) == 0
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn(L)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    out = {"workload": "plain and delta chunked scans, B16 T512 H12 D64 bf16 (configs[2]), phase stamps"}
+    for kern in ("plain_fwd", "plain_bwd", "delta_fwd", "delta_bwd_chain"):
+        setter = getattr(st, "pragnosia_stamps_set_" + unit[kern])
+        buf = torch.zeros(nwg * waves[kern] * (4 + 2 * NC), device=dev, dtype=torch.int32)
+        if kern == "delta_bwd_chain":  # its inputs: the forward's entering states, W and X
+            assert run["delta_fwd"](libs["product"]) == 0
+        assert setter(None) == 0
+        t = {"product_us": timed(run[kern], libs["product"]), "stamped_off_us": timed(run[kern], st)}
+        assert setter(P(buf)) == 0
+        t["stamped_on_us"] = timed(run[kern], st)
+        torch.cuda.synchronize()
+        assert setter(None) == 0
+        stats, total_flops = _phase_stats(buf, nwg, waves[kern], NC, waves_of[kern], flops_of[kern])
+        stats["mfma_per_chunk"] = (pf["output"] + pf["score"]) if kern == "plain_fwd" else PHASE_MFMAS[kern]
+        if kern.startswith("plain"):  # one kernel per entry point: the kernel's whole-run rate
+            stats["kernel_TFLOPs"] = round(total_flops / (t["product_us"] * 1e-6) / 1e12, 1)
+            stats["kernel_frac_of_peak"] = round(total_flops / (t["product_us"] * 1e-6) /
+                                                 (BF16_PEAK_TFLOPS * 1e12), 4)
+        out[kern] = {**stats, **{k_ + ("" if kern.startswith("plain") else "_entry_point"): round(v_, 2)
+                                 for k_, v_ in t.items()}}
+    return out
+
 
 def main():
     args = parse()
@@ -818,6 +960,9 @@ def main():
         return
     if args.decode_only:
         print(json.dumps(decode_bench()), flush=True)
+        return
+    if args.phase_rates:
+        print(json.dumps(phase_rates()), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the carrier path has no "

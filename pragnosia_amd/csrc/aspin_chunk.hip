@@ -29,6 +29,8 @@
 
 using namespace pgn;
 
+PGN_STAMP_UNIT(chunk)
+
 namespace {
 
 constexpr int C = 64;
@@ -92,6 +94,10 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 
   const WaveIdx x = wave_idx();
   const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
+  // instrumented build: per wave, clocks where its role's branch starts (entries 0, 1) and at the kernel's end (2, 3),
+  // then the start and end of its phase in barrier interval lc (4 + 2 lc, 5 + 2 lc)
+#define FWD_STAMP(k) \
+  PGN_STAMP((blockIdx.x * kFwdWaves + __builtin_amdgcn_readfirstlane(w)) * (4 + 2 * NC) + (k))
   // workgroup = (batch-head bh, segment sg): chunks c0 .. c0 + n - 1, entering state S0 of this workgroup
   const int nseg = (NC + P - 1) / P;
   const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
@@ -102,8 +108,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 
   // decayed scores A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, of t block a of chunk `cn` (input set hs) into
   // the A tile `At` (row t), zero above the diagonal block
-  auto scores = [&](auto a_c, int hs, __bf16* At) {
+  auto scores = [&](auto a_c, int hs, __bf16* At, int stamp) {
     constexpr int a = decltype(a_c)::value;
+    if (stamp >= 0) FWD_STAMP(stamp);
     const __bf16* Qs = Qb(hs);
     const __bf16* Ks = Kb(hs);
     const float* Ls = Vecb(hs);
@@ -136,10 +143,12 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       }
       store_T(At, 16 * a, 16 * sb, g, i, pt);
     }
+    if (stamp >= 0) FWD_STAMP(stamp + 1);
   };
 
   if (w < 8) {
     // ================= output waves
+    PGN_STAMP_CLOCKS((blockIdx.x * kFwdWaves + __builtin_amdgcn_readfirstlane(w)) * (4 + 2 * NC));
     const int tb = w < 4 ? 3 - w : w - 4, j0 = 32 * (w >> 2);
     // state rows 16 tb + 4g + r, columns j0 + 16 jt + i
     f32x4 S[2];
@@ -159,6 +168,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       const int tq = 16 * TB + i;  // this lane's token within the chunk for t-indexed operands
       for (int lc = 0; lc < n; ++lc) {
         const int c = c0 + lc, h3 = lc % 3, h2 = lc & 1, t0 = c * C;
+        FWD_STAMP(4 + 2 * lc);  // the chunk's phase: operand reads, contractions, result stores
         const __bf16* Qs = Qb(h3);
         const __bf16* Ks = Kb(h3);
         const __bf16* Vs = Vb(h3);
@@ -222,6 +232,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
           S[jt] = pgn_mfma(kw1, vf[jt][1], S[jt]);
           store_T(STb(h2 ^ 1), j0 + 16 * jt, 16 * TB, g, i, S[jt]);
         }
+        FWD_STAMP(5 + 2 * lc);
         __syncthreads();
       }
     };
@@ -238,6 +249,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
         for (int r = 0; r < 4; ++r) Sfin[R.state() + (16 * tb + 4 * g + r) * ld + j0 + 16 * jt + i] = S[jt][r];
     }
   } else if (w < 12) {
+    PGN_STAMP_CLOCKS((blockIdx.x * kFwdWaves + __builtin_amdgcn_readfirstlane(w)) * (4 + 2 * NC));
     // ================= score waves: t block a, one chunk ahead. Wave 8 also runs the decay scans, two chunks ahead
     // (the load waves stage the same chunk's tiles in the same phase): L (base 2), e^L and w = exp(L_C - L).
     const bool scan = w == 8;
@@ -261,10 +273,10 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
         pla = la_of(2);
       }
       __syncthreads();
-      scores(a_c, 0, ATb(0));
+      scores(a_c, 0, ATb(0), -1);
       __syncthreads();
       for (int c = 0; c < n; ++c) {
-        if (c + 1 < n) scores(a_c, (c + 1) % 3, ATb((c + 1) & 1));
+        if (c + 1 < n) scores(a_c, (c + 1) % 3, ATb((c + 1) & 1), 4 + 2 * c);
         if (scan && c + 2 < n) {
           run_scan(pla, (c + 2) % 3);
           pla = la_of(c + 3);
@@ -279,6 +291,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       default: sloop(std::integral_constant<int, 3>{}); break;
     }
   } else {
+    PGN_STAMP_CLOCKS((blockIdx.x * kFwdWaves + __builtin_amdgcn_readfirstlane(w)) * (4 + 2 * NC));
     // ================= load waves: thread b carries 16-byte row segments b and b + 256 of each of Q, K and V.
     // Two register sets alternate, so a chunk's loads are issued two chunks before it is staged.
     const int b = tid & 255;
@@ -326,6 +339,8 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       if (c + 1 < n) phase(rb, c + 1);
     }
   }
+  PGN_STAMP_CLOCKS((blockIdx.x * kFwdWaves + __builtin_amdgcn_readfirstlane(w)) * (4 + 2 * NC) + 2);
+#undef FWD_STAMP
 }
 
 // Segment-parallel forward, for few heads over long sequences: the chunks of each head are split into segments of
@@ -560,6 +575,9 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 
   const WaveIdx x = wave_idx();
   const int w = x.w, wl = w & 3, g = x.g, i = x.i, tid = threadIdx.x;
+  // instrumented build: per wave, clocks where its group's branch starts (entries 0, 1) and at the kernel's end (2, 3),
+  // then the start and end of its phase for chunk cc (4 + 2 cc, 5 + 2 cc)
+#define BWD_STAMP(k) PGN_STAMP((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(w)) * (4 + 2 * NC) + (k))
   // workgroup = (batch-head bh, segment sg): chunks c0 .. cl, walked from cl down; dSfin indexed per workgroup
   const int nseg = (NC + P - 1) / P;
   const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
@@ -573,6 +591,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   // The two groups run separate loops (the branch is on a wave-uniform value) that meet at the same barriers: each
   // loop's registers and memory-counter waits are then its own.
   if (w >= 4) {
+    PGN_STAMP_CLOCKS((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(w)) * (4 + 2 * NC));
     // ================= group K: s = me, d block wl. Waves 6 and 7, whose share of the contractions is the
     // smallest, also stage the Q and K tiles: thread b2 carries 16-byte row segments b2 + 128 n (n = 0..3) of each.
     const bool kstage = wl >= 2;
@@ -604,6 +623,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       constexpr int WL = decltype(wl_c)::value;
       const int me = 16 * WL + i;
       for (int cc = cl; cc >= c0; --cc) {
+        BWD_STAMP(4 + 2 * cc);  // the chunk's phase: operand reads, contractions, result stores
         const int t0 = cc * C, h = cc & 1;
         const __bf16* Qs = stg + h * kBwdStage;
         const __bf16* Ks = Qs + TILE;
@@ -720,6 +740,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             }
           }
         });
+        BWD_STAMP(5 + 2 * cc);
         if (WL >= 2 && cc > c0) {
           stage(h ^ 1);
           if (cc > c0 + 1) load(cc - 2);
@@ -734,6 +755,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       default: kloop(std::integral_constant<int, 3>{}); break;
     }
   } else {
+    PGN_STAMP_CLOCKS((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(w)) * (4 + 2 * NC));
     // ================= group D: t = me; dS rows 16 wl + 4g + r, column 16 jt + i
     f32x4 dS[4];
     const float* dsp = dSws ? dSws + (size_t)blockIdx.x * DK * DK : (dSfin ? dSfin + R.state() : nullptr);
@@ -777,6 +799,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       constexpr int WL = decltype(wl_c)::value;
       const int me = 16 * WL + i;
       for (int cc = cl; cc >= c0; --cc) {
+        BWD_STAMP(4 + 2 * cc);  // the chunk's phase: operand reads, contractions, result stores
         const int t0 = cc * C, h = cc & 1;
         const __bf16* Qs = stg + h * kBwdStage;
         const __bf16* Ks = Qs + TILE;
@@ -905,6 +928,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             if constexpr (s == NS - 1) sdot[WL * 64 + x.l] = sd;
           }
         });
+        BWD_STAMP(5 + 2 * cc);
         if (w == 0 && cc < cl) {  // the later chunk's dla, from the other vector set (before the scan below)
           const int tn = t0 + C;
           plain_dla(vec + (h ^ 1) * kVec, x.l,
@@ -933,6 +957,8 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         for (int r = 0; r < 4; ++r) dS0[R.state() + (16 * wl + 4 * g + r) * ld + 16 * jt + i] = dS[jt][r];
     }
   }
+  PGN_STAMP_CLOCKS((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(w)) * (4 + 2 * NC) + 2);
+#undef BWD_STAMP
 }
 
 constexpr size_t kFwdSmem = 3 * (size_t)kFwdBuf + 4 * TILE * sizeof(__bf16);

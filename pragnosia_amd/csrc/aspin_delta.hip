@@ -47,6 +47,8 @@
 
 using namespace pgn;
 
+PGN_STAMP_UNIT(delta)
+
 namespace {
 
 constexpr int C = 64;
@@ -234,6 +236,11 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* stg = reinterpret_cast<__bf16*>(smem);          // two sets of staged tiles, chunk c uses set c & 1
   __bf16* As = stg + 2 * kFwdStage;                        // As[t][s] = A[t][s]
+  // instrumented build: per wave, clocks where its role's branch starts (entries 0, 1) and at the kernel's end (2, 3),
+  // then the start and end of its phase for chunk c (4 + 2 c, 5 + 2 c)
+#define DF_STAMP(k) PGN_STAMP((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (4 + 2 * NC) + (k))
+#define DF_CLOCKS(k) \
+  PGN_STAMP_CLOCKS((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (4 + 2 * NC) + (k))
   float* vec = reinterpret_cast<float*>(As + TILE);        // two vector sets, chunk c uses set c & 1
 
   const WaveIdx x = wave_idx();
@@ -244,6 +251,7 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
 
   if (w < 4) {
     // ================= chain waves: value columns j = 16w + i; state rows 16 db + 4g + r
+    DF_CLOCKS(0);
     const int j = 16 * w + i;
     f32x4 S[4];
 #pragma unroll
@@ -252,6 +260,7 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
       for (int r = 0; r < 4; ++r) S[db][r] = S0 ? S0[soff + (size_t)(16 * db + 4 * g + r) * DK + j] : 0.f;
     __syncthreads();
     for (int c = 0; c < NC; ++c) {
+      DF_STAMP(4 + 2 * c);  // the chunk's phase: operand reads, contractions, result stores (across the A barrier)
       const int t0 = c * C, h = c & 1;
       const __bf16* Qs = stg + h * kFwdStage;
       const __bf16* Ks = Qs + TILE;
@@ -328,6 +337,7 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
         S[db] = pgn_mfma(frag_tr(Ks, 16 * db, 0, g, i), ww[0], S[db]);
         S[db] = pgn_mfma(frag_tr(Ks, 16 * db, 1, g, i), ww[1], S[db]);
       }
+      DF_STAMP(5 + 2 * c);
       __syncthreads();  // end of the chunk
     }
 #pragma unroll
@@ -336,6 +346,7 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
       for (int r = 0; r < 4; ++r) Sfin[soff + (size_t)(16 * db + 4 * g + r) * DK + j] = S[db][r];
   } else {
     // ================= service waves: thread b carries 16-byte row segments b and b + 256 of each staged tile
+    DF_CLOCKS(0);
     const int a = w - 4;  // this wave's t block for the scores
     const int b = tid & 255;
     bf16x8 sg[4][2];
@@ -379,6 +390,7 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
       const __bf16* Ks = Qs + TILE;
       const float* Ls = vec + h * kFwdVec;
       // decayed scores for token block a: A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, into As (row t)
+      DF_STAMP(4 + 2 * c);
       {
         const int t = 16 * a + i;
         const bf16x8 qf0 = frag(Qs, t, 0, g), qf1 = frag(Qs, t, 1, g);
@@ -402,6 +414,7 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
           store_T(As, 16 * a, 16 * sb, g, i, pt[sb]);
         }
       }
+      DF_STAMP(5 + 2 * c);
       __syncthreads();  // A complete
       if (c + 1 < NC) {
         stage(h ^ 1);
@@ -410,6 +423,9 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
       __syncthreads();  // end of the chunk
     }
   }
+  DF_CLOCKS(2);
+#undef DF_STAMP
+#undef DF_CLOCKS
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -432,6 +448,11 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* stg = reinterpret_cast<__bf16*>(smem);          // two sets of staged tiles, chunk c uses set c & 1
   __bf16* AT = stg + 2 * kChainStage;                       // AT[t][s] = A[s][t]
+  // instrumented build: per wave, clocks where its role's branch starts (entries 0, 1) and at the kernel's end (2, 3),
+  // then the start and end of its phase for chunk cc (4 + 2 cc, 5 + 2 cc)
+#define DB_STAMP(k) PGN_STAMP((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (4 + 2 * NC) + (k))
+#define DB_CLOCKS(k) \
+  PGN_STAMP_CLOCKS((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (4 + 2 * NC) + (k))
   float* vec = reinterpret_cast<float*>(AT + TILE);         // two vector sets, chunk c uses set c & 1
 
   const WaveIdx x = wave_idx();
@@ -442,6 +463,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
 
   if (w < 4) {
     // ================= chain waves: value columns j = 16w + i; dS rows 16 db + 4g + r
+    DB_CLOCKS(0);
     const int j = 16 * w + i;
     f32x4 dS[4];
 #pragma unroll
@@ -450,6 +472,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
       for (int r = 0; r < 4; ++r) dS[db][r] = dSfin ? dSfin[soff + (size_t)(16 * db + 4 * g + r) * DK + j] : 0.f;
     __syncthreads();
     for (int cc = NC - 1; cc >= 0; --cc) {
+      DB_STAMP(4 + 2 * cc);  // the chunk's phase: operand reads, contractions, result stores (across the A^T barrier)
       const int t0 = cc * C, h = cc & 1;
       const __bf16* Qs = stg + h * kChainStage;
       const __bf16* Ks = Qs + TILE;
@@ -545,6 +568,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
         acc = pgn_mfma(frag_tr(Ks, 16 * db, 1, g, i), u23, acc);
         dS[db] = acc;
       }
+      DB_STAMP(5 + 2 * cc);
       __syncthreads();  // end of the chunk
     }
     if (dS0) {
@@ -555,6 +579,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
     }
   } else {
     // ================= service waves: thread b carries 16-byte row segments b and b + 256 of each staged tile
+    DB_CLOCKS(0);
     const int a = w - 4;       // this wave's t block for the scores
     const int b = tid & 255;
     bf16x8 sg[6][2];
@@ -614,6 +639,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
       // scores, transposed: AT[t][s] = (q_s . k_t) exp(L_s - L_t), s >= t, zero below. Wave a owns token block a's
       // blocks (a, sb >= a) and zeros (a, sb < a); waves 6 and 7 also take (0, 2) and (0, 3), so the ten nonzero
       // blocks split 2, 3, 3, 2 instead of 4, 3, 2, 1 (wave 4 also reduces the previous chunk's sums)
+      DB_STAMP(4 + 2 * cc);
       {
         auto score = [&](int ta, int sb, bf16x8 kf0, bf16x8 kf1, float Lt) {
           f32x4 sc = pgn_mfma(frag(Qs, 16 * sb + i, 0, g), kf0, zero4());
@@ -633,6 +659,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
         }
         if (a >= 2) score(0, a, frag(Ks, i, 0, g), frag(Ks, i, 1, g), Ls[i]);
       }
+      DB_STAMP(5 + 2 * cc);
       __syncthreads();  // A^T complete
       if (a == 0 && cc < NC - 1) reduce(cc + 1);  // the later chunk's sums, before its vector set is reused below
       if (cc > 0) {
@@ -643,6 +670,9 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
     }
     if (a == 0) reduce(0);
   }
+  DB_CLOCKS(2);
+#undef DB_STAMP
+#undef DB_CLOCKS
 }
 
 // ------------------------------------------------------------------------------------------------------------------

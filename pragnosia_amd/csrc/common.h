@@ -28,6 +28,41 @@ inline hipError_t pgn_lds_limit(const void* fn, size_t bytes) {
 
 #define PGN_DEVICE __device__ __forceinline__
 
+// Phase stamps, for the instrumented build only (compiled with -DPRAGNOSIA_PHASE_STAMPS into a separate library; the
+// product library has none). A translation unit declares its stamp buffer with PGN_STAMP_UNIT(name), which also
+// exports `pragnosia_stamps_set_<name>(void* buffer)` to set it (NULL: no stamps). PGN_STAMP(i) has the wave write
+// the low 32 bits of the shader clock (s_memtime) to entry i of the buffer (32-bit entries: differences over a
+// kernel's duration do not wrap); PGN_STAMP_CLOCKS(i) writes the shader clock and the constant 100 MHz clock
+// (s_memrealtime) to entries i and i + 1, from which the shader clock's rate follows. `i` is wave-uniform: every
+// lane stores the same (scalar) value to the same entry, so no branch splits the kernel's scheduled blocks.
+#ifdef PRAGNOSIA_PHASE_STAMPS
+// The buffer pointer lives in constant memory (one scalar load, hoisted out of the kernels' loops) and points to
+// global memory (plain global stores: no wait on the kernel's outstanding loads, stores or LDS traffic).
+typedef __attribute__((address_space(1))) unsigned int pgn_stamp_t;
+#define PGN_STAMP_UNIT(name)                                                                        \
+  static __constant__ pgn_stamp_t* pgn_stamps;                                                      \
+  extern "C" int pragnosia_stamps_set_##name(void* buffer) {                                        \
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(pgn_stamps), &buffer, sizeof(buffer));                 \
+  }
+#define PGN_STAMP(i)                                                                                \
+  do {                                                                                              \
+    pgn_stamp_t* const pgn_b_ = pgn_stamps;                                                         \
+    if (pgn_b_ != nullptr) pgn_b_[(i)] = (unsigned int)__builtin_amdgcn_s_memtime();                \
+  } while (0)
+#define PGN_STAMP_CLOCKS(i)                                                                         \
+  do {                                                                                              \
+    pgn_stamp_t* const pgn_b_ = pgn_stamps;                                                         \
+    if (pgn_b_ != nullptr) {                                                                        \
+      pgn_b_[(i)] = (unsigned int)__builtin_amdgcn_s_memtime();                                     \
+      pgn_b_[(i) + 1] = (unsigned int)__builtin_amdgcn_s_memrealtime();                             \
+    }                                                                                               \
+  } while (0)
+#else
+#define PGN_STAMP_UNIT(name)
+#define PGN_STAMP(i) ((void)0)
+#define PGN_STAMP_CLOCKS(i) ((void)0)
+#endif
+
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
