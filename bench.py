@@ -276,44 +276,49 @@ def diag_bench(steps):
 
 
 def wide_bench(steps=30):
-    """The plain rule at head dim 128 (the reference's `hspin` carrier) at configs[2]'s width: B16 T512, d 768 as 6
-    heads of 128, bf16 q/k/v; one forward + backward through `assoc_scan` with bf16 matmuls (mm=bf16, the kernel
-    path: four 64 x 64 scans per head reading the halves in place, and the sums of their partial outputs), one step
-    captured in a HIP graph (forward and autograd backward) and replayed `steps` times between HIP events, beside the
-    64-dim path at the same width timed the same way."""
+    """Head dim 128 (the reference's `hspin` / `hdspin` carriers) at configs[2]'s width: B16 T512, d 768 as 6 heads
+    of 128, bf16 q/k/v; one forward + backward through `assoc_scan` with bf16 matmuls (mm=bf16, the kernel path: for
+    the plain rule four 64 x 64 scans per head reading the halves in place and the sums of their partial outputs, for
+    the delta rule two 128 x 64 scans per head over its value halves), one step captured in a HIP graph (forward and
+    autograd backward, leaf-gradient accumulation included) and replayed `steps` times between HIP events, beside
+    the 64-dim path at the same width timed the same way."""
     import torch
     import torch.nn.functional as F
     from pragnosia_amd.assoc import assoc_scan
     g = torch.Generator().manual_seed(9)
-    out = {"workload": "plain rule fwd+bwd at head dim 128 vs 64, B16 T512 d768 (configs[2] width), graph-replayed"}
-    for H, D in ((6, 128), (12, 64)):
-        q = F.normalize(torch.randn(16, H, 512, D, generator=g), dim=-1).bfloat16().cuda().requires_grad_(True)
-        k = F.normalize(torch.randn(16, H, 512, D, generator=g), dim=-1).bfloat16().cuda().requires_grad_(True)
-        v = torch.randn(16, H, 512, D, generator=g).bfloat16().cuda().requires_grad_(True)
-        la = F.logsigmoid(torch.randn(16, H, 512, generator=g) + 3).cuda().requires_grad_(True)
-        do = torch.randn(16, H, 512, D, generator=g).bfloat16().cuda()
+    out = {"workload": "plain and delta rule fwd+bwd at head dim 128 vs 64, B16 T512 d768 (configs[2] width), "
+                       "graph-replayed"}
+    for rule in ("plain", "delta"):
+        for H, D in ((6, 128), (12, 64)):
+            q = F.normalize(torch.randn(16, H, 512, D, generator=g), dim=-1).bfloat16().cuda().requires_grad_(True)
+            k = F.normalize(torch.randn(16, H, 512, D, generator=g), dim=-1).bfloat16().cuda().requires_grad_(True)
+            v = torch.randn(16, H, 512, D, generator=g).bfloat16().cuda().requires_grad_(True)
+            la = F.logsigmoid(torch.randn(16, H, 512, generator=g) + 3).cuda().requires_grad_(True)
+            be = (torch.sigmoid(torch.randn(16, H, 512, generator=g)).cuda().requires_grad_(True)
+                  if rule == "delta" else None)
+            do = torch.randn(16, H, 512, D, generator=g).bfloat16().cuda()
 
-        def step():
-            o, _ = assoc_scan(q, k, v, la, mm=torch.bfloat16)
-            torch.autograd.backward([o], [do])
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for _ in range(3):
+            def step():
+                o, _ = assoc_scan(q, k, v, la, mm=torch.bfloat16, beta=be)
+                torch.autograd.backward([o], [do])
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    step()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
                 step()
-        torch.cuda.current_stream().wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            step()
-        torch.cuda.synchronize()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0.record()
-        for _ in range(steps):
-            graph.replay()
-        t1.record()
-        torch.cuda.synchronize()
-        ms = t0.elapsed_time(t1) / steps
-        out[f"head_dim_{D}"] = {"ms_per_step": round(ms, 4), "Mtok_s": round(16 * 512 / ms / 1e3, 2)}
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(steps):
+                graph.replay()
+            t1.record()
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / steps
+            out[f"{rule}_head_dim_{D}"] = {"ms_per_step": round(ms, 4), "Mtok_s": round(16 * 512 / ms / 1e3, 2)}
     return out
 
 

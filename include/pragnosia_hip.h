@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (10); bumped on any change of the entry points. */
+/* ABI version of this header (11); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -195,15 +195,18 @@ int pragnosia_aspin_exact_bwd(const void* q, const void* k, const void* v, const
                               int64_t Dk, int64_t Dv, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
- * Associative carrier, DELTA write rule, chunked scan (chunk = 64, head dim D = 64), per (batch, head):
+ * Associative carrier, DELTA write rule, chunked scan (chunk = 64, head dim D = 64 or 128), per (batch, head):
  *     S_t = a_t S_{t-1} + beta_t k_t (v_t - (a_t S_{t-1})^T k_t)^T,   o_t = S_t^T q_t,   a_t = exp(la_t).
- * Layouts as pragnosia_aspin_chunk_fwd; beta: (B, H, T) fp32 in (0, 1). Writes o (bf16), S_final (fp32), sent
- * (bf16 entering states, each chunk's transposed: sent[b, h, c, j, d] = S[d, j]; required by the backward; may be
- * NULL when no backward follows), and the two saved
- * intermediates of the backward: W, the residuals actually written, (B, H, T, D) bf16, and X, the per-chunk
- * inverse (I + diag(beta) strictly_lower((K K^T) o dec))^-1, (B, H, ceil(T/64), 64, 64) bf16, computed in fp32.
+ * Layouts as pragnosia_aspin_chunk_fwd (q, k, v, o (B, H, T, D); S0, S_final (B, H, D, D)); beta: (B, H, T) fp32 in
+ * (0, 1). Writes o (bf16), S_final (fp32), sent (bf16 entering states, each chunk's transposed: sent[b, h, c, j, d] =
+ * S[d, j], (B, H, ceil(T/64), D, D); required by the backward; may be NULL when no backward follows), and the two
+ * saved intermediates of the backward: W, the residuals actually written, (B, H, T, D) bf16, and X, the per-chunk
+ * inverse (I + diag(beta) strictly_lower((K K^T) o dec))^-1, (B, H, ceil(T/64), 64, 64) bf16, computed in fp32. At
+ * D = 128 the rule is independent per value column once X is known, so each head runs as two scans over its value
+ * halves, each carrying a 128 x 64 state slice and sharing X.
  * Replaces `delta_scan_kernel` and the ops under it (`delta_inv`, `delta_loop_fwd`, `assoc_out`) of
- * src/assoc_kernel.py:332-386, :512-704; the rule is `_scan_twopass_delta` of src/assoc.py:207-251. */
+ * src/assoc_kernel.py:332-386, :512-704 (head dims 64 and 128, src/assoc_kernel.py:21); the rule is
+ * `_scan_twopass_delta` of src/assoc.py:207-251. */
 int pragnosia_aspin_delta_fwd(const void* q, const void* k, const void* v, const float* la, const float* beta,
                               const float* S0, void* o, float* S_final, void* sent, void* W, void* X,
                               int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
@@ -213,7 +216,8 @@ int64_t pragnosia_aspin_delta_bwd_workspace_bytes(int64_t B, int64_t H, int64_t 
 
 /* Backward of pragnosia_aspin_delta_fwd. dO (B, H, T, D) bf16; dS_final fp32 or NULL (zero). Writes dq, dk, dv
  * (bf16), dla and dbeta (fp32, (B, H, T)) and, if non-NULL, dS0 (fp32). `workspace` is caller-allocated device
- * memory of at least pragnosia_aspin_delta_bwd_workspace_bytes(...) bytes (no alignment beyond 256 B needed).
+ * memory of at least pragnosia_aspin_delta_bwd_workspace_bytes(...) bytes (no alignment beyond 256 B needed); at
+ * D = 128 it also holds the second value-half scan's parts of dq, dk, dla and dbeta, which one more kernel adds.
  * Replaces the registered backward of `delta_loop_fwd`, `delta_inv` and `assoc_out`
  * (`_delta_loop_bwd`, `_inv_bwd`, `_bwd_chunk` of src/assoc_kernel.py:73-116, :389-509, :625-704). */
 int pragnosia_aspin_delta_bwd(const void* q, const void* k, const void* v, const float* la, const float* beta,

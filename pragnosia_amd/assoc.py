@@ -105,8 +105,8 @@ def _needs_grad(*ts):
 
 
 def _kernel_ok(dk: int, dv: int, delta: bool) -> bool:
-    """Whether the bf16-operand MFMA kernels take these heads: 64 wide, or 128 wide for the plain rule."""
-    return dk == dv and (dk == HEAD_DIM_KERNEL or (dk == HEAD_DIM_WIDE and not delta))
+    """Whether the bf16-operand MFMA kernels take these heads: 64 or 128 wide, either rule."""
+    return dk == dv and dk in (HEAD_DIM_KERNEL, HEAD_DIM_WIDE)
 
 
 def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = False, mm=None, beta=None,
@@ -118,7 +118,7 @@ def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = Fa
     As in the reference, the arithmetic is fp32, or fp64 for fp64 inputs (`rt`, `src/assoc.py:259-261`), with no
     operand rounding: the exact kernels (any Dk, Dv <= 128), S_final in that type. With `mm` a 16-bit type (the
     reference's bf16 matmuls under autocast, `:149-153`) the bf16-operand MFMA kernels run instead (fp32 accumulation
-    and state; head dim 64, or 128 for the plain rule), S_final fp32. The result does not depend on `chunk` (the
+    and state; head dim 64 or 128), S_final fp32. The result does not depend on `chunk` (the
     reference's own test), and both paths recompute in the backward what they do not save, so `chunk`, `recompute`
     and `kernel` are accepted for the signature. need_sent (this build's): also return the bf16 entering state of
     every 64-token chunk, from the MFMA kernels."""
@@ -133,13 +133,12 @@ def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = Fa
 
 
 def _kernel_scan(q, k, v, logalpha, S0, beta, need_sent):
-    """The bf16-operand MFMA kernels: q, k, v (B, H, T, 64) (128 for the plain rule), operands rounded to bf16,
+    """The bf16-operand MFMA kernels: q, k, v (B, H, T, 64 or 128), operands rounded to bf16,
     accumulation and state fp32. Returns (o in q's dtype, S_final fp32) and, when need_sent, the bf16 state entering
     every 64-token chunk."""
     wide = q.shape[-1] == HEAD_DIM_WIDE and beta is None
     if not _kernel_ok(q.shape[-1], v.shape[-1], beta is not None):
-        raise PragnosiaError(f"assoc_scan: head dim {q.shape[-1]} is not supported by the bf16 kernels (64; 128 for "
-                             "the plain rule)")
+        raise PragnosiaError(f"assoc_scan: head dim {q.shape[-1]} is not supported by the bf16 kernels (64 or 128)")
     want = bool(need_sent or _needs_grad(q, k, v, logalpha, S0, beta))
     S0 = None if S0 is None else S0.float()
     if wide:
@@ -176,7 +175,7 @@ def prep_kernel(qp, kp, vp, gate_logits, theta, pos):
 class AssocCarrier(nn.Module):
     """Per-head key-value outer-product memory with per-token forgetting, learned rotation frequencies and an
     optional delta write rule (`src/assoc.py:279-512`). Constructor arguments, parameters and paths are the
-    reference's: with `kernel` (and T > 1, head dim 64, or 128 for the plain rule) the bf16-operand MFMA kernels with
+    reference's: with `kernel` (and T > 1, head dim 64 or 128) the bf16-operand MFMA kernels with
     the fused prep; otherwise (kernel=False, a T = 1 call under autograd, other head dims up to 128) the reference's
     torch composition around the exact fp32 scan (bf16 MFMA kernels under autocast, as the reference's bf16 matmuls);
     a T = 1 call without autograd (decode) the fused fp32 step kernel. Options: key_topk, hl_floor, write_all,

@@ -56,6 +56,34 @@ constexpr int DK = 64;
 constexpr int TILE = 64 * kPitch;
 constexpr int NP = C + 4;  // pitch of the fp32 N^T tile
 
+// Where the delta scan of workgroup index bh finds its rows. KH = 1 (64-wide heads): scan bh is head bh. KH = 2
+// (128-wide heads): given X (which depends on the keys, decays and write strengths only) the rule is independent per
+// value column, so head hw runs as two scans bh = 2 hw + vh over value columns 64 vh .. 64 vh + 63, each carrying
+// the full 128-key state slice (128 x 64). Every (T, .) operand has rows of DKEY elements: q and k are read whole
+// (KH 64-wide halves; LDS tiles are 64 wide, so a 128-wide operand is staged as two tiles), v, dO, o, W, drhs and dv
+// at columns 64 vh. X is per (head, chunk), shared by both scans. States (S0, S_final, dS_final, dS0; (B, H, DKEY,
+// DKEY) fp32, key rows) are read and written at columns 64 vh; the entering states and per-chunk state gradients,
+// stored transposed ((value j, key d), (B, H, NC, DKEY, DKEY) bf16), at rows 64 vh. dq, dk, dla and dbeta of a
+// 128-wide head sum over its two scans: scan vh writes slot vh (the caller's tensor, or a workspace tensor of the
+// same layout), and a last kernel adds the slots.
+template <int KH>
+struct DeltaRows {
+  static constexpr int DKEY = 64 * KH;
+  int hw, vh;
+  PGN_DEVICE explicit DeltaRows(int bh) : hw(KH == 2 ? bh >> 1 : bh), vh(KH == 2 ? bh & 1 : 0) {}
+  PGN_DEVICE size_t rows(int T) const { return (size_t)hw * T * DKEY; }    // q, k, dq, dk
+  PGN_DEVICE size_t vals(int T) const { return rows(T) + 64 * vh; }        // v, dO, o, W, drhs, dv
+  PGN_DEVICE size_t state() const { return (size_t)hw * DKEY * DKEY + 64 * vh; }
+  PGN_DEVICE size_t stateT(int NC, int c) const {
+    return ((size_t)hw * NC + c) * DKEY * DKEY + (size_t)64 * vh * DKEY;
+  }
+  PGN_DEVICE size_t tok(int T) const { return (size_t)hw * T; }            // la, beta, dla, dbeta
+  template <class Ptr>
+  PGN_DEVICE Ptr slot(Ptr s0, Ptr s1) const {
+    return (KH == 2 && vh) ? s1 : s0;
+  }
+};
+
 PGN_DEVICE float incl_scan64(float x, int l) { return wave_prefix_sum(x, l); }
 
 PGN_DEVICE float rev_scan64(float x, int l) { return wave_suffix_sum(x, l); }
@@ -73,46 +101,52 @@ PGN_DEVICE void chunk_decays(float la_l, int l, float* Ls, float* eLs, float* ws
 // X = (I + N)^-1, one wave per (batch-head, chunk)
 // N^T and X are kept as their ten 16 x 16 blocks on and below the diagonal (block (tb, sb), sb <= tb, at index
 // tb (tb + 1) / 2 + sb, unpadded rows so the substitution reads four entries at once): 24 KB of LDS per chunk, so
-// six chunks (one round of the grid at cfg2) are resident per compute unit. The keys are loaded in 16-byte row
-// segments into the X block area (unused until N is formed) and read from there as MFMA operands.
+// six chunks (one round of the grid at cfg2) are resident per compute unit. The keys (KH 64-wide tiles) are loaded in
+// 16-byte row segments into the N and X block areas (unused until N is formed) and read from there as MFMA operands.
 constexpr int BP = 16;                 // row pitch of a 16 x 16 fp32 block
 constexpr int BLK = 16 * BP;
 PGN_DEVICE int blk(int tb, int sb) { return (tb * (tb + 1) / 2 + sb) * BLK; }
 
 
+template <int KH>
 __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__ k, const float* __restrict__ la,
                                                       const float* __restrict__ be, __bf16* __restrict__ X, int T,
                                                       int NC) {
-  __shared__ __align__(16) float NT[10 * BLK];  // N^T blocks: NT(tb, sb)[s' * BP + t'] = N[16 tb + t'][16 sb + s']
-  __shared__ __align__(16) float Xf[10 * BLK];  // X blocks: Xf(ib, jb)[r * BP + c] = X[16 ib + r][16 jb + c]
+  constexpr int DKEY = 64 * KH;
+  __shared__ __align__(16) float NX[20 * BLK];
+  float* const NT = NX;             // N^T blocks: NT(tb, sb)[s' * BP + t'] = N[16 tb + t'][16 sb + s']
+  float* const Xf = NX + 10 * BLK;  // X blocks: Xf(ib, jb)[r * BP + c] = X[16 ib + r][16 jb + c]
   __shared__ __align__(16) float Tt[3 * BLK];   // per-level sums, one block per product
   __shared__ __align__(16) float Ls[C], bs[C];
 
-  const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;
+  const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;  // head (not scan), chunk
   const int l = threadIdx.x, g = l >> 4, i = l & 15;
   const int t0 = c * C, nr = min(C, T - t0);
-  const __bf16* kc = k + ((size_t)bh * T + t0) * DK;
-  // the keys in 16-byte row segments (eight contiguous 1 KB loads per wave, rows past T as zeros), staged in the X
-  // block area, which nothing uses before N is formed; then this lane's operand rows i, 16 + i, 32 + i, 48 + i
-  __bf16* Kst = reinterpret_cast<__bf16*>(Xf);
-  static_assert(64 * kPitch * sizeof(__bf16) <= sizeof(Xf), "the key tile fits the X block area");
-  {
+  const __bf16* kc = k + ((size_t)bh * T + t0) * DKEY;
+  // the keys in 16-byte row segments (eight contiguous 1 KB loads per wave and half, rows past T as zeros), staged
+  // in the N and X block areas, which nothing uses before N is formed; then this lane's operand rows i, 16 + i,
+  // 32 + i, 48 + i
+  __bf16* Kst = reinterpret_cast<__bf16*>(NX);
+  static_assert(KH * TILE * sizeof(__bf16) <= sizeof(NX), "the key tiles fit the N and X block areas");
+#pragma unroll
+  for (int h = 0; h < KH; ++h) {
     bf16x8 seg[8];
 #pragma unroll
-    for (int n = 0; n < 8; ++n) seg[n] = load_seg(kc, nr, l + 64 * n);
+    for (int n = 0; n < 8; ++n) seg[n] = load_seg(kc + 64 * h, nr, l + 64 * n, DKEY);
 #pragma unroll
-    for (int n = 0; n < 8; ++n) put_seg(Kst, seg[n], l + 64 * n);
+    for (int n = 0; n < 8; ++n) put_seg(Kst + h * TILE, seg[n], l + 64 * n);
   }
   const float lav = l < nr ? la[(size_t)bh * T + t0 + l] : 0.f;
   const float bev = l < nr ? be[(size_t)bh * T + t0 + l] : 0.f;
   Ls[l] = incl_scan64(lav, l);
   bs[l] = bev;
   __syncthreads();
-  bf16x8 kf[4][2];
+  bf16x8 kf[4][2 * KH];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-    for (int m = 0; m < 2; ++m) kf[rb][m] = frag(Kst, 16 * rb + i, m, g);
+    for (int m = 0; m < 2 * KH; ++m) kf[rb][m] = frag(Kst + (m >> 1) * TILE, 16 * rb + i, m & 1, g);
+  __syncthreads();  // every key operand is in registers before N overwrites the staged keys
 
   // N^T blocks: accumulator rows s (block sb), lane t (block tb), for sb <= tb
 #pragma unroll
@@ -122,8 +156,8 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
 #pragma unroll
     for (int sb = 0; sb <= tb; ++sb) {
       f32x4 acc = zero4();
-      acc = pgn_mfma(kf[sb][0], kf[tb][0], acc);
-      acc = pgn_mfma(kf[sb][1], kf[tb][1], acc);
+#pragma unroll
+      for (int m = 0; m < 2 * KH; ++m) acc = pgn_mfma(kf[sb][m], kf[tb][m], acc);
       float* nb = NT + blk(tb, sb);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -220,89 +254,96 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// forward: one workgroup of 8 waves per (batch, head), chunks in order. Waves 0-3 carry the chain, wave w owning value
-// columns 16w..16w+15 with its columns of the fp32 state in registers (U -> rhs -> W -> S' never leaves them). Waves
+// forward: one workgroup of 8 waves per scan (a 64-wide head, or one value half of a 128-wide one), chunks in order.
+// Waves 0-3 carry the chain, wave w owning value columns 16w..16w+15 with its columns of the fp32 state (all key
+// rows) in registers (U -> rhs -> W -> S' never leaves them). Waves
 // 4-7 serve them: per chunk they compute the decayed scores A (the one operand the chain waves share), then stage the
 // next chunk's tiles into the other half of a double-buffered LDS and run its decay scan. Two barriers per chunk: A
 // ready (the chain waves form U, rhs and W before it), and the end of the chunk.
-constexpr int kFwdStage = 4 * TILE;    // Q, K, V, X
+// Per chunk: Q and K (KH tiles each), V, X; L, eL, w, beta.
+template <int KH>
+constexpr int fwd_stage() { return (2 * KH + 2) * TILE; }
 constexpr int kFwdVec = 4 * C;         // L, eL, w, beta
 
+template <int KH>
 __global__ __launch_bounds__(512) void aspin_delta_fwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const float* __restrict__ be, const __bf16* __restrict__ X,
     const float* __restrict__ S0, __bf16* __restrict__ o, __bf16* __restrict__ Wout, float* __restrict__ Sfin,
     __bf16* __restrict__ sent, int T, int NC) {
+  constexpr int DKEY = 64 * KH;
+  constexpr int kStage = fwd_stage<KH>();
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* stg = reinterpret_cast<__bf16*>(smem);          // two sets of staged tiles, chunk c uses set c & 1
-  __bf16* As = stg + 2 * kFwdStage;                        // As[t][s] = A[t][s]
+  __bf16* As = stg + 2 * kStage;                           // As[t][s] = A[t][s]
+  float* vec = reinterpret_cast<float*>(As + TILE);        // two vector sets, chunk c uses set c & 1
   // instrumented build: per wave, clocks where its role's branch starts (entries 0, 1) and at the kernel's end (2, 3),
   // then the start and end of its phase for chunk c (4 + 2 c, 5 + 2 c)
 #define DF_STAMP(k) PGN_STAMP((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (4 + 2 * NC) + (k))
 #define DF_CLOCKS(k) \
   PGN_STAMP_CLOCKS((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (4 + 2 * NC) + (k))
-  float* vec = reinterpret_cast<float*>(As + TILE);        // two vector sets, chunk c uses set c & 1
 
   const WaveIdx x = wave_idx();
   const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
-  const int bh = blockIdx.x;
-  const size_t boff = (size_t)bh * T * DK;
-  const size_t soff = (size_t)bh * DK * DK;
+  const DeltaRows<KH> R(blockIdx.x);
+  const size_t voff = R.vals(T);
 
   if (w < 4) {
     // ================= chain waves: value columns j = 16w + i; state rows 16 db + 4g + r
     DF_CLOCKS(0);
     const int j = 16 * w + i;
-    f32x4 S[4];
+    f32x4 S[4 * KH];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4 * KH; ++db)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) S[db][r] = S0 ? S0[soff + (size_t)(16 * db + 4 * g + r) * DK + j] : 0.f;
+      for (int r = 0; r < 4; ++r) S[db][r] = S0 ? S0[R.state() + (size_t)(16 * db + 4 * g + r) * DKEY + j] : 0.f;
     __syncthreads();
     for (int c = 0; c < NC; ++c) {
       DF_STAMP(4 + 2 * c);  // the chunk's phase: operand reads, contractions, result stores (across the A barrier)
       const int t0 = c * C, h = c & 1;
-      const __bf16* Qs = stg + h * kFwdStage;
-      const __bf16* Ks = Qs + TILE;
-      const __bf16* Vs = Qs + 2 * TILE;
-      const __bf16* Xs = Qs + 3 * TILE;
+      const __bf16* Qs = stg + h * kStage;  // KH tiles: key columns 64 n .. of tile n
+      const __bf16* Ks = Qs + KH * TILE;
+      const __bf16* Vs = Qs + 2 * KH * TILE;
+      const __bf16* Xs = Vs + TILE;
       const float* vs = vec + h * kFwdVec;
       const float* Ls = vs;
       const float* eLs = vs + C;
       const float* ws = vs + 2 * C;
       const float* bs = vs + 3 * C;
-      const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
+      const int out_bytes = min(C, T - t0) * DKEY * (int)sizeof(__bf16);
       // the entering state, bf16, transposed: row j holds key rows d contiguously
       if (sent) {
-        __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK + (size_t)j * DK + 4 * g;
+        __bf16* sc = sent + R.stateT(NC, c) + (size_t)j * DKEY + 4 * g;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) *reinterpret_cast<bf16x4*>(sc + 16 * db) = to_bf16x4(S[db]);
+        for (int db = 0; db < 4 * KH; ++db) *reinterpret_cast<bf16x4*>(sc + 16 * db) = to_bf16x4(S[db]);
       }
       // U = K S (rows t, this wave's columns); rhs = beta (V - eL U)
-      const bf16x8 s01 = pack(S[0], S[1]), s23 = pack(S[2], S[3]);
-      f32x4 R[4];
+      bf16x8 sp[2 * KH];  // the state as operands: key rows 32 m .. 32 m + 31
+#pragma unroll
+      for (int m = 0; m < 2 * KH; ++m) sp[m] = pack(S[2 * m], S[2 * m + 1]);
+      f32x4 R4[4];
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
         f32x4 u = zero4();
-        u = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), s01, u);
-        u = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), s23, u);
+#pragma unroll
+        for (int m = 0; m < 2 * KH; ++m) u = pgn_mfma(frag(Ks + (m >> 1) * TILE, 16 * tb + i, m & 1, g), sp[m], u);
         const f32x4 vv = to_f32x4(ds_read_tr(Vs + (16 * tb + 4 * g + (i >> 2)) * kPitch + 16 * w + 4 * (i & 3)));
         const f32x4 bv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
         const f32x4 ev = *reinterpret_cast<const f32x4*>(eLs + 16 * tb + 4 * g);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) R[tb][r] = bv[r] * (vv[r] - ev[r] * u[r]);
+        for (int r = 0; r < 4; ++r) R4[tb][r] = bv[r] * (vv[r] - ev[r] * u[r]);
       }
       // W = X rhs (X lower triangular); rows past T fall outside the store's range and are dropped
       const __amdgpu_buffer_rsrc_t w_out =
-          __builtin_amdgcn_make_buffer_rsrc(Wout + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
-      const bf16x8 r01 = pack(R[0], R[1]), r23 = pack(R[2], R[3]);
+          __builtin_amdgcn_make_buffer_rsrc(Wout + voff + (size_t)t0 * DKEY, (short)0, out_bytes, 0x00020000);
+      const bf16x8 r01 = pack(R4[0], R4[1]), r23 = pack(R4[2], R4[3]);
       f32x4 Wt[4];
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
         Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 0, g), r01, zero4());
         if (tb >= 2) Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 1, g), r23, Wt[tb]);
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, quad_rows(Wt[tb], i)), w_out,
-                                              ((16 * tb + 4 * g + (i & 3)) * DK + 16 * w + 4 * (i >> 2)) *
+                                              ((16 * tb + 4 * g + (i & 3)) * DKEY + 16 * w + 4 * (i >> 2)) *
                                                   (int)sizeof(__bf16), 0, 0);
       }
       __syncthreads();  // A complete
@@ -310,18 +351,19 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
       // O^T tiles (value rows 16w + 4g + r, token lane 16 tb + i) = W^T A^T + eL_t (S^T Q^T): the decay of the
       // state read is one factor per output column, applied to the accumulator rather than to the Q operand
       const __amdgpu_buffer_rsrc_t o_out =
-          __builtin_amdgcn_make_buffer_rsrc(o + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
+          __builtin_amdgcn_make_buffer_rsrc(o + voff + (size_t)t0 * DKEY, (short)0, out_bytes, 0x00020000);
       const bf16x8 w01 = pack(Wt[0], Wt[1]), w23 = pack(Wt[2], Wt[3]);
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
         const int tl = 16 * tb + i;
         f32x4 acc = pgn_mfma(w01, frag(As, tl, 0, g), zero4());
         if (tb >= 2) acc = pgn_mfma(w23, frag(As, tl, 1, g), acc);
-        f32x4 qs = pgn_mfma(s01, frag(Qs, tl, 0, g), zero4());
-        qs = pgn_mfma(s23, frag(Qs, tl, 1, g), qs);
+        f32x4 qs = zero4();
+#pragma unroll
+        for (int m = 0; m < 2 * KH; ++m) qs = pgn_mfma(sp[m], frag(Qs + (m >> 1) * TILE, tl, m & 1, g), qs);
         acc += eLs[tl] * qs;
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
-                                              (tl * DK + 16 * w + 4 * g) * (int)sizeof(__bf16), 0, 0);
+                                              (tl * DKEY + 16 * w + 4 * g) * (int)sizeof(__bf16), 0, 0);
       }
       // S <- a S + K^T (w o W): the per-token weight w_t scales W's fp32 rows before they are rounded, so K enters
       // the product as it is staged
@@ -332,45 +374,49 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
         ww[m] = pack(Wt[2 * m] * *reinterpret_cast<const f32x4*>(ws + 32 * m + 4 * g),
                      Wt[2 * m + 1] * *reinterpret_cast<const f32x4*>(ws + 32 * m + 16 + 4 * g));
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
+      for (int db = 0; db < 4 * KH; ++db) {
+        const __bf16* Kh = Ks + (db >> 2) * TILE;
         S[db] = S[db] * a_c;
-        S[db] = pgn_mfma(frag_tr(Ks, 16 * db, 0, g, i), ww[0], S[db]);
-        S[db] = pgn_mfma(frag_tr(Ks, 16 * db, 1, g, i), ww[1], S[db]);
+        S[db] = pgn_mfma(frag_tr(Kh, 16 * (db & 3), 0, g, i), ww[0], S[db]);
+        S[db] = pgn_mfma(frag_tr(Kh, 16 * (db & 3), 1, g, i), ww[1], S[db]);
       }
       DF_STAMP(5 + 2 * c);
       __syncthreads();  // end of the chunk
     }
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4 * KH; ++db)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Sfin[soff + (size_t)(16 * db + 4 * g + r) * DK + j] = S[db][r];
+      for (int r = 0; r < 4; ++r) Sfin[R.state() + (size_t)(16 * db + 4 * g + r) * DKEY + j] = S[db][r];
   } else {
     // ================= service waves: thread b carries 16-byte row segments b and b + 256 of each staged tile
     DF_CLOCKS(0);
     const int a = w - 4;  // this wave's t block for the scores
     const int b = tid & 255;
-    bf16x8 sg[4][2];
+    constexpr int NT = 2 * KH + 2;  // tiles per chunk: Q halves, K halves, V, X
+    bf16x8 sg[NT][2];
     float pla = 0.f, pbe = 0.f;
     auto load = [&](int cn) {
       const int n0 = cn * C, nr = min(C, T - n0);
-      const __bf16* src[4] = {q + boff + (size_t)n0 * DK, k + boff + (size_t)n0 * DK, v + boff + (size_t)n0 * DK,
-                              X + ((size_t)bh * NC + cn) * C * C};
-      const int rows[4] = {nr, nr, nr, C};
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        sg[u][0] = load_seg(src[u], rows[u], b);
-        sg[u][1] = load_seg(src[u], rows[u], b + 256);
+      for (int u = 0; u < NT; ++u) {
+        const __bf16* src = u < KH ? q + R.rows(T) + (size_t)n0 * DKEY + 64 * u
+                          : u < 2 * KH ? k + R.rows(T) + (size_t)n0 * DKEY + 64 * (u - KH)
+                          : u == 2 * KH ? v + voff + (size_t)n0 * DKEY
+                                        : X + ((size_t)R.hw * NC + cn) * C * C;
+        const int rows = u == NT - 1 ? C : nr, ld = u == NT - 1 ? C : DKEY;
+        sg[u][0] = load_seg(src, rows, b, ld);
+        sg[u][1] = load_seg(src, rows, b + 256, ld);
       }
       if (a == 0) {
         const bool ok = n0 + x.l < T;
-        pla = ok ? la[(size_t)bh * T + n0 + x.l] : 0.f;
-        pbe = ok ? be[(size_t)bh * T + n0 + x.l] : 0.f;
+        pla = ok ? la[R.tok(T) + n0 + x.l] : 0.f;
+        pbe = ok ? be[R.tok(T) + n0 + x.l] : 0.f;
       }
     };
     auto stage = [&](int hh) {
-      __bf16* base = stg + hh * kFwdStage;
+      __bf16* base = stg + hh * kStage;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < NT; ++u) {
         put_seg(base + u * TILE, sg[u][0], b);
         put_seg(base + u * TILE, sg[u][1], b + 256);
       }
@@ -386,22 +432,25 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
     __syncthreads();
     for (int c = 0; c < NC; ++c) {
       const int h = c & 1;
-      const __bf16* Qs = stg + h * kFwdStage;
-      const __bf16* Ks = Qs + TILE;
+      const __bf16* Qs = stg + h * kStage;
+      const __bf16* Ks = Qs + KH * TILE;
       const float* Ls = vec + h * kFwdVec;
       // decayed scores for token block a: A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, into As (row t)
       DF_STAMP(4 + 2 * c);
       {
         const int t = 16 * a + i;
-        const bf16x8 qf0 = frag(Qs, t, 0, g), qf1 = frag(Qs, t, 1, g);
+        bf16x8 qf[2 * KH];
+#pragma unroll
+        for (int m = 0; m < 2 * KH; ++m) qf[m] = frag(Qs + (m >> 1) * TILE, t, m & 1, g);
         const float Lt = Ls[t];
         f32x4 pt[4];
 #pragma unroll
         for (int sb = 0; sb < 4; ++sb) {
           pt[sb] = zero4();
           if (sb <= a) {
-            pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, pt[sb]);
-            pt[sb] = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, pt[sb]);
+#pragma unroll
+            for (int m = 0; m < 2 * KH; ++m)
+              pt[sb] = pgn_mfma(frag(Ks + (m >> 1) * TILE, 16 * sb + i, m & 1, g), qf[m], pt[sb]);
           }
         }
 #pragma unroll
@@ -429,57 +478,66 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// backward, the sequential part: one workgroup of 8 waves per (batch, head), chunks in reverse. Waves 0-3 carry the
-// chain, wave w owning value columns 16w..16w+15 with its columns of dS in fp32 registers; nothing on the chain is
-// shared between them. Waves 4-7 serve them: per chunk they compute the decayed scores A^T (the only operand the four
-// chain waves share), then stage the next chunk's tiles into the other half of a double-buffered LDS (loaded into
-// registers a chunk earlier still), run its decay scan, and reduce the previous chunk's value-column partial sums
-// into rsum. Two barriers per chunk: A^T ready (the chain waves do their dS-side and dS-free products before it), and
-// the end of the chunk. Operands contracted over a tile's row index use the LDS transpose read.
-constexpr int kChainStage = 6 * TILE;   // Q, K, V, dO, X, S_c
+// backward, the sequential part: one workgroup of 8 waves per scan (a 64-wide head, or one value half of a 128-wide
+// one), chunks in reverse. Waves 0-3 carry the chain, wave w owning value columns 16w..16w+15 with its columns of dS
+// (all key rows) in fp32 registers; nothing on the chain is shared between them. Waves 4-7 serve them: per chunk they
+// compute the decayed scores A^T (the only operand the four chain waves share), then stage the next chunk's tiles
+// (loaded into registers a chunk earlier still), run its decay scan, and reduce the previous chunk's value-column
+// partial sums into rsum. Two barriers per chunk: A^T ready (the chain waves do their dS-side and dS-free products
+// before it), and the end of the chunk. Operands contracted over a tile's row index use the LDS transpose read.
+// LDS per chunk: Q (KH tiles), S_c transposed (KH tiles: value rows j, key columns 64 n .. of tile n) and dO, read
+// only before the A^T barrier, in one copy that the service waves restage for the next chunk after that barrier; K
+// (KH tiles), V and X, read after it too, double-buffered.
+template <int KH>
+constexpr int chain_single() { return (2 * KH + 1) * TILE; }
+template <int KH>
+constexpr int chain_double() { return (KH + 2) * TILE; }
 constexpr int kChainVec = 4 * C + 8 * C;  // L, eL, w, beta; per-wave partial sums of drhs V and drhs U
 
+template <int KH>
 __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const float* __restrict__ be, const __bf16* __restrict__ X,
     const __bf16* __restrict__ sent, const __bf16* __restrict__ dO, const float* __restrict__ dSfin,
     __bf16* __restrict__ drhs, __bf16* __restrict__ dSc, float* __restrict__ rsum,
     float* __restrict__ dS0, int T, int NC) {
+  constexpr int DKEY = 64 * KH;
+  constexpr int kSingle = chain_single<KH>(), kDouble = chain_double<KH>();
   extern __shared__ __align__(16) unsigned char smem[];
-  __bf16* stg = reinterpret_cast<__bf16*>(smem);          // two sets of staged tiles, chunk c uses set c & 1
-  __bf16* AT = stg + 2 * kChainStage;                       // AT[t][s] = A[s][t]
+  __bf16* sgl = reinterpret_cast<__bf16*>(smem);          // Q, S_c, dO of the current chunk
+  __bf16* dbl = sgl + kSingle;                             // two sets of K, V, X: chunk c uses set c & 1
+  __bf16* AT = dbl + 2 * kDouble;                          // AT[t][s] = A[s][t]
+  float* vec = reinterpret_cast<float*>(AT + TILE);        // two vector sets, chunk c uses set c & 1
   // instrumented build: per wave, clocks where its role's branch starts (entries 0, 1) and at the kernel's end (2, 3),
   // then the start and end of its phase for chunk cc (4 + 2 cc, 5 + 2 cc)
 #define DB_STAMP(k) PGN_STAMP((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (4 + 2 * NC) + (k))
 #define DB_CLOCKS(k) \
   PGN_STAMP_CLOCKS((blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (4 + 2 * NC) + (k))
-  float* vec = reinterpret_cast<float*>(AT + TILE);         // two vector sets, chunk c uses set c & 1
 
   const WaveIdx x = wave_idx();
   const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
-  const int bh = blockIdx.x;
-  const size_t boff = (size_t)bh * T * DK;
-  const size_t soff = (size_t)bh * DK * DK;
+  const DeltaRows<KH> R(blockIdx.x);
+  const __bf16* Qs = sgl;
+  const __bf16* Ss = sgl + KH * TILE;
+  const __bf16* Os = sgl + 2 * KH * TILE;
 
   if (w < 4) {
     // ================= chain waves: value columns j = 16w + i; dS rows 16 db + 4g + r
     DB_CLOCKS(0);
     const int j = 16 * w + i;
-    f32x4 dS[4];
+    f32x4 dS[4 * KH];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4 * KH; ++db)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dS[db][r] = dSfin ? dSfin[soff + (size_t)(16 * db + 4 * g + r) * DK + j] : 0.f;
+      for (int r = 0; r < 4; ++r)
+        dS[db][r] = dSfin ? dSfin[R.state() + (size_t)(16 * db + 4 * g + r) * DKEY + j] : 0.f;
     __syncthreads();
     for (int cc = NC - 1; cc >= 0; --cc) {
       DB_STAMP(4 + 2 * cc);  // the chunk's phase: operand reads, contractions, result stores (across the A^T barrier)
       const int t0 = cc * C, h = cc & 1;
-      const __bf16* Qs = stg + h * kChainStage;
-      const __bf16* Ks = Qs + TILE;
-      const __bf16* Vs = Qs + 2 * TILE;
-      const __bf16* Os = Qs + 3 * TILE;
-      const __bf16* Xs = Qs + 4 * TILE;
-      const __bf16* Ss = Qs + 5 * TILE;
+      const __bf16* Ks = dbl + h * kDouble;
+      const __bf16* Vs = Ks + KH * TILE;
+      const __bf16* Xs = Vs + TILE;
       float* vs = vec + h * kChainVec;
       const float* Ls = vs;
       const float* eLs = vs + C;
@@ -490,34 +548,42 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
       // the gradient on the state leaving this chunk, for the chunk-local kernel, transposed ((j, d): a lane's four
       // consecutive key rows are one 8-byte store)
       {
-        __bf16* dst = dSc + ((size_t)bh * NC + cc) * DK * DK + (size_t)j * DK + 4 * g;
+        __bf16* dst = dSc + R.stateT(NC, cc) + (size_t)j * DKEY + 4 * g;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) *reinterpret_cast<bf16x4*>(dst + 16 * db) = to_bf16x4(dS[db]);
+        for (int db = 0; db < 4 * KH; ++db) *reinterpret_cast<bf16x4*>(dst + 16 * db) = to_bf16x4(dS[db]);
       }
       // products that do not need A^T: y = K dS, U = K S_c, Yc = (Q o eL)^T dO, on this wave's columns
-      const bf16x8 d01 = pack(dS[0], dS[1]), d23 = pack(dS[2], dS[3]);
-      const bf16x8 sc0 = frag(Ss, 16 * w + i, 0, g), sc1 = frag(Ss, 16 * w + i, 1, g);  // S_c[d][j], staged (j, d)
+      bf16x8 dp[2 * KH], scf[2 * KH];
+#pragma unroll
+      for (int m = 0; m < 2 * KH; ++m) {
+        dp[m] = pack(dS[2 * m], dS[2 * m + 1]);
+        scf[m] = frag(Ss + (m >> 1) * TILE, 16 * w + i, m & 1, g);  // S_c[d][j], staged (j, d)
+      }
       const bf16x8 oc0 = frag_tr(Os, 16 * w, 0, g, i), oc1 = frag_tr(Os, 16 * w, 1, g, i);  // dO[t][j]
-      f32x4 y[4], U[4], Yc[4];
+      f32x4 y[4], U[4], Yc[4 * KH];
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
-        const bf16x8 k0 = frag(Ks, 16 * tb + i, 0, g), k1 = frag(Ks, 16 * tb + i, 1, g);
-        y[tb] = pgn_mfma(k0, d01, zero4());
-        y[tb] = pgn_mfma(k1, d23, y[tb]);
-        U[tb] = pgn_mfma(k0, sc0, zero4());
-        U[tb] = pgn_mfma(k1, sc1, U[tb]);
+        y[tb] = zero4();
+        U[tb] = zero4();
+#pragma unroll
+        for (int m = 0; m < 2 * KH; ++m) {
+          const bf16x8 kk = frag(Ks + (m >> 1) * TILE, 16 * tb + i, m & 1, g);
+          y[tb] = pgn_mfma(kk, dp[m], y[tb]);
+          U[tb] = pgn_mfma(kk, scf[m], U[tb]);
+        }
       }
-      // the per-token factor eL_t on the dO operand, shared by the four key blocks, rather than on each Q^T block
+      // the per-token factor eL_t on the dO operand, shared by the key blocks, rather than on each Q^T block
       const bf16x8 oe0 = scale_frag_k(oc0, *reinterpret_cast<const f32x4*>(eLs + 4 * g),
                                       *reinterpret_cast<const f32x4*>(eLs + 16 + 4 * g));
       const bf16x8 oe1 = scale_frag_k(oc1, *reinterpret_cast<const f32x4*>(eLs + 32 + 4 * g),
                                       *reinterpret_cast<const f32x4*>(eLs + 48 + 4 * g));
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        Yc[db] = pgn_mfma(frag_tr(Qs, 16 * db, 0, g, i), oe0, zero4());
-        Yc[db] = pgn_mfma(frag_tr(Qs, 16 * db, 1, g, i), oe1, Yc[db]);
+      for (int db = 0; db < 4 * KH; ++db) {
+        const __bf16* Qh = Qs + (db >> 2) * TILE;
+        Yc[db] = pgn_mfma(frag_tr(Qh, 16 * (db & 3), 0, g, i), oe0, zero4());
+        Yc[db] = pgn_mfma(frag_tr(Qh, 16 * (db & 3), 1, g, i), oe1, Yc[db]);
       }
-      __syncthreads();  // A^T complete
+      __syncthreads();  // A^T complete (and Q, S_c, dO no longer read: the service waves restage them)
 
       // dW = A^T dO + w o (K dS)
       f32x4 dW[4];
@@ -531,9 +597,9 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
       }
       // drhs = X^T dW (X^T upper triangular); dU = -beta eL drhs; per-row partial sums (dV = beta drhs is written
       // by the chunk-local kernel from the stored drhs)
-      const int out_bytes = min(C, T - t0) * DK * (int)sizeof(__bf16);
-      const __amdgpu_buffer_rsrc_t dr_out =
-          __builtin_amdgcn_make_buffer_rsrc(drhs + boff + (size_t)t0 * DK, (short)0, out_bytes, 0x00020000);
+      const int out_bytes = min(C, T - t0) * DKEY * (int)sizeof(__bf16);
+      const __amdgpu_buffer_rsrc_t dr_out = __builtin_amdgcn_make_buffer_rsrc(
+          drhs + R.vals(T) + (size_t)t0 * DKEY, (short)0, out_bytes, 0x00020000);
       const bf16x8 w01 = pack(dW[0], dW[1]), w23 = pack(dW[2], dW[3]);
       f32x4 dU[4];
 #pragma unroll
@@ -553,7 +619,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
           pr[r] = acc[r] * vv[r];
           pr[4 + r] = acc[r] * U[tb][r];
           __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (__bf16)acc[r]), dr_out,
-                                                (tl * DK + j) * (int)sizeof(__bf16), 0, 0);
+                                                (tl * DKEY + j) * (int)sizeof(__bf16), 0, 0);
         }
         const float tot = row_totals16x8(pr, i);  // lane i: the total of pr[(i >> 1) & 7]
         if (!(i & 1)) ((i & 8) ? redU : redV)[w * C + 16 * tb + 4 * g + ((i >> 1) & 3)] = tot;
@@ -562,10 +628,11 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
       const float a_c = __expf(Ls[C - 1]);
       const bf16x8 u01 = pack(dU[0], dU[1]), u23 = pack(dU[2], dU[3]);
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
+      for (int db = 0; db < 4 * KH; ++db) {
+        const __bf16* Kh = Ks + (db >> 2) * TILE;
         f32x4 acc = dS[db] * a_c + Yc[db];
-        acc = pgn_mfma(frag_tr(Ks, 16 * db, 0, g, i), u01, acc);
-        acc = pgn_mfma(frag_tr(Ks, 16 * db, 1, g, i), u23, acc);
+        acc = pgn_mfma(frag_tr(Kh, 16 * (db & 3), 0, g, i), u01, acc);
+        acc = pgn_mfma(frag_tr(Kh, 16 * (db & 3), 1, g, i), u23, acc);
         dS[db] = acc;
       }
       DB_STAMP(5 + 2 * cc);
@@ -573,40 +640,56 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
     }
     if (dS0) {
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < 4 * KH; ++db)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dS0[soff + (size_t)(16 * db + 4 * g + r) * DK + j] = dS[db][r];
+        for (int r = 0; r < 4; ++r) dS0[R.state() + (size_t)(16 * db + 4 * g + r) * DKEY + j] = dS[db][r];
     }
   } else {
-    // ================= service waves: thread b carries 16-byte row segments b and b + 256 of each staged tile
+    // ================= service waves: thread b carries 16-byte row segments b and b + 256 of each staged tile:
+    // Q halves, S_c halves, dO (the single copy), then K halves, V, X (the double-buffered set)
     DB_CLOCKS(0);
     const int a = w - 4;       // this wave's t block for the scores
     const int b = tid & 255;
-    bf16x8 sg[6][2];
+    constexpr int NS = 2 * KH + 1, ND = KH + 2;
+    bf16x8 sg[NS + ND][2];
     float pla = 0.f, pbe = 0.f;
     auto load = [&](int cn) {
       const int n0 = cn * C, nr = min(C, T - n0);
-      const __bf16* src[6] = {q + boff + (size_t)n0 * DK, k + boff + (size_t)n0 * DK, v + boff + (size_t)n0 * DK,
-                              dO + boff + (size_t)n0 * DK, X + ((size_t)bh * NC + cn) * C * C,
-                              sent + ((size_t)bh * NC + cn) * DK * DK};
-      const int rows[6] = {nr, nr, nr, nr, C, DK};
 #pragma unroll
-      for (int u = 0; u < 6; ++u) {
-        sg[u][0] = load_seg(src[u], rows[u], b);
-        sg[u][1] = load_seg(src[u], rows[u], b + 256);
+      for (int u = 0; u < NS + ND; ++u) {
+        const __bf16* src;
+        int rows = nr, ld = DKEY;
+        if (u < KH) {
+          src = q + R.rows(T) + (size_t)n0 * DKEY + 64 * u;
+        } else if (u < 2 * KH) {
+          src = sent + R.stateT(NC, cn) + 64 * (u - KH);
+          rows = DK;
+        } else if (u == 2 * KH) {
+          src = dO + R.vals(T) + (size_t)n0 * DKEY;
+        } else if (u < NS + KH) {
+          src = k + R.rows(T) + (size_t)n0 * DKEY + 64 * (u - NS);
+        } else if (u == NS + KH) {
+          src = v + R.vals(T) + (size_t)n0 * DKEY;
+        } else {
+          src = X + ((size_t)R.hw * NC + cn) * C * C;
+          rows = C;
+          ld = C;
+        }
+        sg[u][0] = load_seg(src, rows, b, ld);
+        sg[u][1] = load_seg(src, rows, b + 256, ld);
       }
       if (a == 0) {
         const bool ok = n0 + x.l < T;
-        pla = ok ? la[(size_t)bh * T + n0 + x.l] : 0.f;
-        pbe = ok ? be[(size_t)bh * T + n0 + x.l] : 0.f;
+        pla = ok ? la[R.tok(T) + n0 + x.l] : 0.f;
+        pbe = ok ? be[R.tok(T) + n0 + x.l] : 0.f;
       }
     };
     auto stage = [&](int hh) {
-      __bf16* base = stg + hh * kChainStage;
 #pragma unroll
-      for (int u = 0; u < 6; ++u) {
-        put_seg(base + u * TILE, sg[u][0], b);
-        put_seg(base + u * TILE, sg[u][1], b + 256);
+      for (int u = 0; u < NS + ND; ++u) {
+        __bf16* dst = u < NS ? sgl + u * TILE : dbl + hh * kDouble + (u - NS) * TILE;
+        put_seg(dst, sg[u][0], b);
+        put_seg(dst, sg[u][1], b + 256);
       }
       if (a == 0) {
         float* vs = vec + hh * kChainVec;
@@ -614,7 +697,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
         vs[3 * C + x.l] = pbe;
       }
     };
-    // rsum of a finished chunk from its vector set: sum_j drhs (V - eL U) and -beta sum_j drhs U
+    // rsum of a finished chunk from its vector set: sum_j drhs (V - eL U) and -beta sum_j drhs U (per scan)
     auto reduce = [&](int cn) {
       const float* vs = vec + (cn & 1) * kChainVec;
       const int t = x.l, n0 = cn * C;
@@ -623,8 +706,8 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
       const float pv_ = redV[t] + redV[C + t] + redV[2 * C + t] + redV[3 * C + t];
       const float pu_ = redU[t] + redU[C + t] + redU[2 * C + t] + redU[3 * C + t];
       if (n0 + t < T) {
-        rsum[((size_t)bh * T + n0 + t) * 2 + 0] = pv_ - vs[C + t] * pu_;
-        rsum[((size_t)bh * T + n0 + t) * 2 + 1] = -vs[3 * C + t] * pu_;
+        rsum[((size_t)blockIdx.x * T + n0 + t) * 2 + 0] = pv_ - vs[C + t] * pu_;
+        rsum[((size_t)blockIdx.x * T + n0 + t) * 2 + 1] = -vs[3 * C + t] * pu_;
       }
     };
     load(NC - 1);
@@ -633,31 +716,38 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
     __syncthreads();
     for (int cc = NC - 1; cc >= 0; --cc) {
       const int h = cc & 1;
-      const __bf16* Qs = stg + h * kChainStage;
-      const __bf16* Ks = Qs + TILE;
+      const __bf16* Ks = dbl + h * kDouble;
       const float* Ls = vec + h * kChainVec;
       // scores, transposed: AT[t][s] = (q_s . k_t) exp(L_s - L_t), s >= t, zero below. Wave a owns token block a's
       // blocks (a, sb >= a) and zeros (a, sb < a); waves 6 and 7 also take (0, 2) and (0, 3), so the ten nonzero
       // blocks split 2, 3, 3, 2 instead of 4, 3, 2, 1 (wave 4 also reduces the previous chunk's sums)
       DB_STAMP(4 + 2 * cc);
       {
-        auto score = [&](int ta, int sb, bf16x8 kf0, bf16x8 kf1, float Lt) {
-          f32x4 sc = pgn_mfma(frag(Qs, 16 * sb + i, 0, g), kf0, zero4());
-          sc = pgn_mfma(frag(Qs, 16 * sb + i, 1, g), kf1, sc);
+        auto score = [&](int ta, int sb, const bf16x8* kf, float Lt) {
+          f32x4 sc = zero4();
+#pragma unroll
+          for (int m = 0; m < 2 * KH; ++m) sc = pgn_mfma(frag(Qs + (m >> 1) * TILE, 16 * sb + i, m & 1, g), kf[m], sc);
           const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
 #pragma unroll
           for (int r = 0; r < 4; ++r) sc[r] *= masked_decay(Lsv[r] - Lt, 16 * sb + 4 * g + r >= 16 * ta + i);
           store_T(AT, 16 * ta, 16 * sb, g, i, sc);
         };
         const int t = 16 * a + i;
-        const bf16x8 kf0 = frag(Ks, t, 0, g), kf1 = frag(Ks, t, 1, g);
+        bf16x8 kf[2 * KH];
+#pragma unroll
+        for (int m = 0; m < 2 * KH; ++m) kf[m] = frag(Ks + (m >> 1) * TILE, t, m & 1, g);
         const float Lt = Ls[t];
         const int last = a == 0 ? 1 : 3;
         for (int sb = 0; sb < 4; ++sb) {
           if (sb < a) store_T(AT, 16 * a, 16 * sb, g, i, zero4());
-          else if (sb <= last) score(a, sb, kf0, kf1, Lt);
+          else if (sb <= last) score(a, sb, kf, Lt);
         }
-        if (a >= 2) score(0, a, frag(Ks, i, 0, g), frag(Ks, i, 1, g), Ls[i]);
+        if (a >= 2) {
+          bf16x8 kf0[2 * KH];
+#pragma unroll
+          for (int m = 0; m < 2 * KH; ++m) kf0[m] = frag(Ks + (m >> 1) * TILE, i, m & 1, g);
+          score(0, a, kf0, Ls[i]);
+        }
       }
       DB_STAMP(5 + 2 * cc);
       __syncthreads();  // A^T complete
@@ -676,22 +766,29 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// backward, the chunk-local part: one workgroup of 8 waves per (batch-head, chunk). Waves 0-3 own token block
-// t = 16w.. (dQ, row sums), waves 4-7 own token block s = 16(w-4).. in the key role (dK, column sums).
+// backward, the chunk-local part: one workgroup of 8 waves per (scan, chunk). Waves 0-3 own token block
+// t = 16w.. (dQ, row sums), waves 4-7 own token block s = 16(w-4).. in the key role (dK, column sums). Staged:
+// Q and K (KH tiles each), W, dO, S_c and dS transposed (KH tiles each: value rows j, key columns), drhs.
+template <int KH>
+constexpr int local_tiles() { return 4 * KH + 3; }
+
+template <int KH>
 __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const float* __restrict__ la,
     const float* __restrict__ be, const __bf16* __restrict__ Win, const __bf16* __restrict__ sent,
     const __bf16* __restrict__ dO, const __bf16* __restrict__ drhs, const __bf16* __restrict__ dSc,
-    const float* __restrict__ rsum, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    float* __restrict__ dla, float* __restrict__ dbe, int T, int NC) {
+    const float* __restrict__ rsum, __bf16* __restrict__ dq, __bf16* __restrict__ dq1, __bf16* __restrict__ dk,
+    __bf16* __restrict__ dk1, __bf16* __restrict__ dv, float* __restrict__ dla, float* __restrict__ dla1,
+    float* __restrict__ dbe, float* __restrict__ dbe1, int T, int NC) {
+  constexpr int DKEY = 64 * KH;
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* Qs = reinterpret_cast<__bf16*>(smem);
-  __bf16* Ks = Qs + TILE;
-  __bf16* Ws = Ks + TILE;
-  __bf16* Os = Ws + TILE;   // dO
-  __bf16* Ss = Os + TILE;   // S_c transposed, (j, d)
-  __bf16* dSs = Ss + TILE;  // dS transposed, (j, d)
-  __bf16* Rs = dSs + TILE;  // drhs (t, j)
+  __bf16* Ks = Qs + KH * TILE;
+  __bf16* Ws = Ks + KH * TILE;
+  __bf16* Os = Ws + TILE;        // dO
+  __bf16* Ss = Os + TILE;        // S_c transposed, (j, d)
+  __bf16* dSs = Ss + KH * TILE;  // dS transposed, (j, d)
+  __bf16* Rs = dSs + KH * TILE;  // drhs (t, j)
   float* Ls = reinterpret_cast<float*>(Rs + TILE);
   float* eLs = Ls + C;
   float* ws = eLs + C;
@@ -703,38 +800,50 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
   float* sdot = dwv + C;    // per-wave <S, dS>
 
   const WaveIdx x = wave_idx();
-  const int w = x.w, wl = w & 3, g = x.g, i = x.i, tid = threadIdx.x;
-  const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;
+  const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
+  const int sc = blockIdx.x / NC, c = blockIdx.x - sc * NC;
+  const DeltaRows<KH> R(sc);
   const int t0 = c * C, nr = min(C, T - t0);
-  const size_t coff = ((size_t)bh * T + t0) * DK;
-  const size_t soff = ((size_t)bh * NC + c) * DK * DK;
+  const size_t roff = R.rows(T) + (size_t)t0 * DKEY;  // the chunk's q, k, dq, dk rows
+  const size_t voff = R.vals(T) + (size_t)t0 * DKEY;  // the chunk's W, dO, drhs, dv rows
+  const size_t toff = R.stateT(NC, c);                // this scan's rows of the transposed states
 
   {
     // every tile staged untransposed, thread tid carrying 16-byte row segment tid of each (operands contracted over
     // a tile's row index use the LDS transpose read)
-    bf16x8 sg[7];
-    const __bf16* src[7] = {q + coff, k + coff, Win + coff, dO + coff, sent + soff, dSc + soff, drhs + coff};
-    const int rows[7] = {nr, nr, nr, nr, DK, DK, nr};
+    constexpr int NT = local_tiles<KH>();
+    bf16x8 sg[NT];
 #pragma unroll
-    for (int u = 0; u < 7; ++u) sg[u] = load_seg(src[u], rows[u], tid);
+    for (int u = 0; u < NT; ++u) {
+      const __bf16* src;
+      int rows = nr;
+      if (u < KH) src = q + roff + 64 * u;
+      else if (u < 2 * KH) src = k + roff + 64 * (u - KH);
+      else if (u == 2 * KH) src = Win + voff;
+      else if (u == 2 * KH + 1) src = dO + voff;
+      else if (u < 3 * KH + 2) { src = sent + toff + 64 * (u - 2 * KH - 2); rows = DK; }
+      else if (u < 4 * KH + 2) { src = dSc + toff + 64 * (u - 3 * KH - 2); rows = DK; }
+      else src = drhs + voff;
+      sg[u] = load_seg(src, rows, tid, DKEY);
+    }
 #pragma unroll
-    for (int u = 0; u < 7; ++u) put_seg(Qs + u * TILE, sg[u], tid);
+    for (int u = 0; u < NT; ++u) put_seg(Qs + u * TILE, sg[u], tid);
     {
       // dV = beta drhs, row segment tid (the chain kernel rounds drhs to bf16 once; dV rounds its product again)
       const int r = tid >> 3;
       if (r < nr) {
-        const float bt = be[(size_t)bh * T + t0 + r];
+        const float bt = be[R.tok(T) + t0 + r];
         bf16x8 dvs;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dvs[e] = (__bf16)(bt * (float)sg[6][e]);
-        *reinterpret_cast<bf16x8*>(dv + coff + (size_t)r * DK + 8 * (tid & 7)) = dvs;
+        for (int e = 0; e < 8; ++e) dvs[e] = (__bf16)(bt * (float)sg[NT - 1][e]);
+        *reinterpret_cast<bf16x8*>(dv + voff + (size_t)r * DKEY + 8 * (tid & 7)) = dvs;
       }
     }
     if (w == 0) {
       const bool ok = x.l < nr;
-      const float lav = ok ? la[(size_t)bh * T + t0 + x.l] : 0.f;
+      const float lav = ok ? la[R.tok(T) + t0 + x.l] : 0.f;
       chunk_decays(lav, x.l, Ls, eLs, ws);
-      bs[x.l] = ok ? be[(size_t)bh * T + t0 + x.l] : 0.f;
+      bs[x.l] = ok ? be[R.tok(T) + t0 + x.l] : 0.f;
     }
   }
   __syncthreads();
@@ -743,9 +852,13 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
     const int me = 16 * WL + i;
       // ---------------- token block WL in the query role: lane t = me
       const float Lt = Ls[me], bt = bs[me];
-      const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
+      bf16x8 qf[2 * KH], kf[2 * KH];
+#pragma unroll
+      for (int m = 0; m < 2 * KH; ++m) {
+        qf[m] = frag(Qs + (m >> 1) * TILE, me, m & 1, g);
+        kf[m] = frag(Ks + (m >> 1) * TILE, me, m & 1, g);
+      }
       const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
-      const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
       const bf16x8 rf0 = frag(Rs, me, 0, g), rf1 = frag(Rs, me, 1, g);
       float rowacc = 0.f, db2 = 0.f;
       f32x4 dPT[4];
@@ -755,12 +868,14 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
         if (sb <= WL) {
           // rows s, lane t: P[t][s], dA[t][s], KK[t][s], dN[t][s]
           f32x4 P = zero4(), dA = zero4(), KK = zero4(), dN = zero4();
-          P = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), qf0, P);
-          P = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), qf1, P);
+#pragma unroll
+          for (int m = 0; m < 2 * KH; ++m) {
+            const bf16x8 ks = frag(Ks + (m >> 1) * TILE, 16 * sb + i, m & 1, g);
+            P = pgn_mfma(ks, qf[m], P);
+            KK = pgn_mfma(ks, kf[m], KK);
+          }
           dA = pgn_mfma(frag(Ws, 16 * sb + i, 0, g), of0, dA);
           dA = pgn_mfma(frag(Ws, 16 * sb + i, 1, g), of1, dA);
-          KK = pgn_mfma(frag(Ks, 16 * sb + i, 0, g), kf0, KK);
-          KK = pgn_mfma(frag(Ks, 16 * sb + i, 1, g), kf1, KK);
           dN = pgn_mfma(frag(Ws, 16 * sb + i, 0, g), rf0, dN);
           dN = pgn_mfma(frag(Ws, 16 * sb + i, 1, g), rf1, dN);
           const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
@@ -780,38 +895,42 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
       db2 = sum_groups(db2);
       const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
       const float eLt = eLs[me];
-      const __bf16* qrow = Qs + me * kPitch;
       // rows past the end of a partial chunk fall outside the store's range and are dropped
-      const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(dq + coff, (short)0, nr * DK * (int)sizeof(__bf16),
-                                                                         0x00020000);
+      const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+          R.slot(dq, dq1) + roff, (short)0, nr * DKEY * (int)sizeof(__bf16), 0x00020000);
       float qzt = 0.f;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
+      for (int dt = 0; dt < 4 * KH; ++dt) {
+        const int n0 = 16 * (dt & 3);
+        const __bf16* Kh = Ks + (dt >> 2) * TILE;
+        const __bf16* Sh = Ss + (dt >> 2) * TILE;
         f32x4 acc = zero4(), Z = zero4();
-        acc = pgn_mfma(frag_tr(Ks, 16 * dt, 0, g, i), b0, acc);
-        if (WL >= 2) acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), b1, acc);
-        Z = pgn_mfma(frag_tr(Ss, 16 * dt, 0, g, i), of0, Z);
-        Z = pgn_mfma(frag_tr(Ss, 16 * dt, 1, g, i), of1, Z);
-        const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(qrow + 16 * dt + 4 * g));
+        acc = pgn_mfma(frag_tr(Kh, n0, 0, g, i), b0, acc);
+        if (WL >= 2) acc = pgn_mfma(frag_tr(Kh, n0, 1, g, i), b1, acc);
+        Z = pgn_mfma(frag_tr(Sh, n0, 0, g, i), of0, Z);
+        Z = pgn_mfma(frag_tr(Sh, n0, 1, g, i), of1, Z);
+        const f32x4 qq =
+            to_f32x4(*reinterpret_cast<const bf16x4*>(Qs + (dt >> 2) * TILE + me * kPitch + n0 + 4 * g));
 #pragma unroll
         for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
         acc = acc + Z * eLt;
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), out,
-                                            (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+                                              (me * DKEY + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
       }
       qzt = sum_groups(qzt);
       if (g == 0) {
         rowT[me] = rowacc + eLt * qzt;
         dbe2[me] = db2;
       }
-
   };
   auto kpart = [&](auto wl_c) {
     constexpr int WL = decltype(wl_c)::value;
     const int me = 16 * WL + i;
       // ---------------- token block WL in the key role: lane s = me
       const float Lsm = Ls[me], bsm = bs[me], wsm = ws[me], eLsm = eLs[me];
-      const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
+      bf16x8 kf[2 * KH];
+#pragma unroll
+      for (int m = 0; m < 2 * KH; ++m) kf[m] = frag(Ks + (m >> 1) * TILE, me, m & 1, g);
       const bf16x8 wf0 = frag(Ws, me, 0, g), wf1 = frag(Ws, me, 1, g);
       const bf16x8 rf0 = frag(Rs, me, 0, g), rf1 = frag(Rs, me, 1, g);
       float colacc = 0.f;
@@ -823,12 +942,13 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
         if (tb >= WL) {
           // rows t, lane s: P[t][s], dA[t][s], KK[t][s], dN[t][s]
           f32x4 P = zero4(), dA = zero4(), KK = zero4(), dN = zero4();
-          P = pgn_mfma(frag(Qs, 16 * tb + i, 0, g), kf0, P);
-          P = pgn_mfma(frag(Qs, 16 * tb + i, 1, g), kf1, P);
+#pragma unroll
+          for (int m = 0; m < 2 * KH; ++m) {
+            P = pgn_mfma(frag(Qs + (m >> 1) * TILE, 16 * tb + i, m & 1, g), kf[m], P);
+            KK = pgn_mfma(frag(Ks + (m >> 1) * TILE, 16 * tb + i, m & 1, g), kf[m], KK);
+          }
           dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), wf0, dA);
           dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), wf1, dA);
-          KK = pgn_mfma(frag(Ks, 16 * tb + i, 0, g), kf0, KK);
-          KK = pgn_mfma(frag(Ks, 16 * tb + i, 1, g), kf1, KK);
           dN = pgn_mfma(frag(Rs, 16 * tb + i, 0, g), wf0, dN);
           dN = pgn_mfma(frag(Rs, 16 * tb + i, 1, g), wf1, dN);
           const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
@@ -862,49 +982,54 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
       const bf16x8 g0 = pack(Gt[0], Gt[1]), g1 = pack(Gt[2], Gt[3]);
       const float us = -bsm * eLsm;  // dU[s] = us * drhs[s]
       const bf16x8 du0 = frag_scaled(Rs, me, 0, g, us), du1 = frag_scaled(Rs, me, 1, g, us);
-      const __bf16* krow = Ks + me * kPitch;
       // rows past the end of a partial chunk fall outside the store's range and are dropped
-      const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(dk + coff, (short)0, nr * DK * (int)sizeof(__bf16),
-                                                                         0x00020000);
+      const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+          R.slot(dk, dk1) + roff, (short)0, nr * DKEY * (int)sizeof(__bf16), 0x00020000);
       float dw = 0.f;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
+      for (int dt = 0; dt < 4 * KH; ++dt) {
+        const int n0 = 16 * (dt & 3);
+        const __bf16* Qh = Qs + (dt >> 2) * TILE;
+        const __bf16* Kh = Ks + (dt >> 2) * TILE;
+        const __bf16* Sh = Ss + (dt >> 2) * TILE;
+        const __bf16* dSh = dSs + (dt >> 2) * TILE;
         f32x4 acc = zero4(), Y = zero4();
-        if (WL < 2) acc = pgn_mfma(frag_tr(Qs, 16 * dt, 0, g, i), p0, acc);
-        acc = pgn_mfma(frag_tr(Qs, 16 * dt, 1, g, i), p1, acc);
-        acc = pgn_mfma(frag_tr(Ks, 16 * dt, 0, g, i), g0, acc);
-        acc = pgn_mfma(frag_tr(Ks, 16 * dt, 1, g, i), g1, acc);
-        acc = pgn_mfma(frag_tr(Ss, 16 * dt, 0, g, i), du0, acc);
-        acc = pgn_mfma(frag_tr(Ss, 16 * dt, 1, g, i), du1, acc);
-        Y = pgn_mfma(frag_tr(dSs, 16 * dt, 0, g, i), wf0, Y);
-        Y = pgn_mfma(frag_tr(dSs, 16 * dt, 1, g, i), wf1, Y);
-        const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(krow + 16 * dt + 4 * g));
+        if (WL < 2) acc = pgn_mfma(frag_tr(Qh, n0, 0, g, i), p0, acc);
+        acc = pgn_mfma(frag_tr(Qh, n0, 1, g, i), p1, acc);
+        acc = pgn_mfma(frag_tr(Kh, n0, 0, g, i), g0, acc);
+        acc = pgn_mfma(frag_tr(Kh, n0, 1, g, i), g1, acc);
+        acc = pgn_mfma(frag_tr(Sh, n0, 0, g, i), du0, acc);
+        acc = pgn_mfma(frag_tr(Sh, n0, 1, g, i), du1, acc);
+        Y = pgn_mfma(frag_tr(dSh, n0, 0, g, i), wf0, Y);
+        Y = pgn_mfma(frag_tr(dSh, n0, 1, g, i), wf1, Y);
+        const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(Kh + me * kPitch + n0 + 4 * g));
 #pragma unroll
         for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
         acc = acc + Y * wsm;
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), out,
-                                            (me * DK + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+                                              (me * DKEY + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
       }
       dw = sum_groups(dw);
       if (g == 0) {
         colS[me] = colacc;
         dwv[me] = dw;
       }
-      // <S_c, dS> over key rows 16 WL ..
+      // <S_c, dS> over key rows 16 WL .. of each 64-wide key tile
       float sd = 0.f;
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        // S_c and dS at key rows 16 WL + 4g + r, column 16 jt + i: both staged transposed, so a plain read of row
-        // 16 jt + i
-        const int off = (16 * jt + i) * kPitch + 16 * WL + 4 * g;
-        const f32x4 sv = to_f32x4(*reinterpret_cast<const bf16x4*>(Ss + off));
-        const f32x4 dv_ = to_f32x4(*reinterpret_cast<const bf16x4*>(dSs + off));
+      for (int hh = 0; hh < KH; ++hh)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sd += sv[r] * dv_[r];
-      }
+        for (int jt = 0; jt < 4; ++jt) {
+          // S_c and dS at key rows 64 hh + 16 WL + 4g + r, column 16 jt + i: both staged transposed, so a plain read
+          // of row 16 jt + i
+          const int off = hh * TILE + (16 * jt + i) * kPitch + 16 * WL + 4 * g;
+          const f32x4 sv = to_f32x4(*reinterpret_cast<const bf16x4*>(Ss + off));
+          const f32x4 dv_ = to_f32x4(*reinterpret_cast<const bf16x4*>(dSs + off));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sd += sv[r] * dv_[r];
+        }
       sd = wave_sum(sd);
       if (x.l == 0) sdot[WL] = sd;
-  
   };
   // one instantiation per (role, block index): block conditions are compile-time constants
   switch (w) {
@@ -921,8 +1046,8 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
   if (w == 0) {
     const int t = x.l;
     const bool ok = t < nr;
-    const size_t ti = (size_t)bh * T + t0 + t;
-    const float r0 = ok ? rsum[ti * 2 + 0] : 0.f, r1 = ok ? rsum[ti * 2 + 1] : 0.f;
+    const size_t ri = (size_t)sc * T + t0 + t;  // this scan's rsum entry
+    const float r0 = ok ? rsum[ri * 2 + 0] : 0.f, r1 = ok ? rsum[ri * 2 + 1] : 0.f;
     const float wdw = ws[t] * dwv[t];
     float dL = rowT[t] - colS[t] + eLs[t] * r1 - wdw;
     const float tot = wave_sum(wdw);
@@ -930,55 +1055,180 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
     if (t == C - 1) dL += tot + a_c * (sdot[0] + sdot[1] + sdot[2] + sdot[3]);
     dL = rev_scan64(dL, t);
     if (ok) {
-      dla[ti] = dL;
-      dbe[ti] = r0 + dbe2[t];
+      const size_t ti = R.tok(T) + t0 + t;
+      R.slot(dla, dla1)[ti] = dL;
+      R.slot(dbe, dbe1)[ti] = r0 + dbe2[t];
     }
   }
 }
 
-constexpr size_t kFwdSmem = (2 * kFwdStage + TILE) * sizeof(__bf16) + 2 * kFwdVec * sizeof(float);
-constexpr size_t kChainSmem = (2 * kChainStage + TILE) * sizeof(__bf16) + 2 * kChainVec * sizeof(float);
-constexpr size_t kLocalSmem = 7 * TILE * sizeof(__bf16) + (9 * C + 4) * sizeof(float);
+// The slot sums of the 128-wide backward: x[p][i] <- x[p][i] + y[p][i] for the bf16 pairs (dq, dk; the fp32 sum of
+// two bf16 values rounded once, as a bf16 tensor add rounds) over n elements (n % 8 == 0), and f[p][i] <- f[p][i] +
+// e[p][i] for the fp32 pairs (dla, dbeta) over m elements (m <= n / 8). Thread u covers elements 8u .. 8u + 7 of
+// each bf16 pair and element u of each fp32 pair.
+struct DeltaJoin {
+  __bf16* x[2];
+  const __bf16* y[2];
+  float* f[2];
+  const float* e[2];
+  int64_t n, m;
+};
 
+__global__ __launch_bounds__(256) void aspin_delta_join(DeltaJoin a) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (8 * u < a.n) {
+    bf16x8 xs[2], ys[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      xs[p] = *reinterpret_cast<const bf16x8*>(a.x[p] + 8 * u);
+      ys[p] = *reinterpret_cast<const bf16x8*>(a.y[p] + 8 * u);
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xs[p][j] = pgn_bf16(pgn_f32(xs[p][j]) + pgn_f32(ys[p][j]));
+      *reinterpret_cast<bf16x8*>(a.x[p] + 8 * u) = xs[p];
+    }
+  }
+  if (u < a.m) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) a.f[p][u] += a.e[p][u];
+  }
+}
+
+template <int KH>
+constexpr size_t fwd_smem() {
+  return (2 * fwd_stage<KH>() + TILE) * sizeof(__bf16) + 2 * kFwdVec * sizeof(float);
+}
+template <int KH>
+constexpr size_t chain_smem() {
+  return (chain_single<KH>() + 2 * chain_double<KH>() + TILE) * sizeof(__bf16) + 2 * kChainVec * sizeof(float);
+}
+template <int KH>
+constexpr size_t local_smem() {
+  return local_tiles<KH>() * TILE * sizeof(__bf16) + (9 * C + 4) * sizeof(float);
+}
+
+// Head dim D = 64 or 128 (KH = D / 64 key tiles; a 128-wide head runs as two scans).
 bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
   if (B <= 0 || H <= 0 || T <= 0) return false;
-  if (B * H >= ((int64_t)1 << 24) || T >= ((int64_t)1 << 28)) return false;
-  if (B * H * ((T + C - 1) / C) >= ((int64_t)1 << 31)) return false;
-  return D == DK && Cc == C;
+  if (B * H >= ((int64_t)1 << 23) || T >= ((int64_t)1 << 28)) return false;
+  if (2 * B * H * ((T + C - 1) / C) >= ((int64_t)1 << 31)) return false;
+  if (B * H * T * D >= ((int64_t)1 << 34)) return false;
+  return (D == DK || D == 2 * DK) && Cc == C;
 }
 
 int set_smem(const void* fn, size_t bytes) { return (int)pgn_lds_limit(fn, bytes); }
+
+int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
+
+// The backward's workspace: drhs (B, H, T, D) bf16, the per-chunk state gradients (B, H, NC, D, D) bf16 and the
+// per-scan row sums (B H D / 64 scans, T, 2) fp32; at D = 128 then the second slots of dq and dk ((B, H, T, D) bf16)
+// and of dla and dbeta ((B, H, T) fp32).
+struct BwdWorkspace {
+  int64_t drhs, dsc, rsum, dq1, dk1, dla1, dbe1, total;
+  BwdWorkspace(int64_t B, int64_t H, int64_t T, int64_t D) {
+    const int64_t NC = (T + C - 1) / C, KH = D / DK;
+    drhs = 0;
+    dsc = align256(B * H * T * D * 2);
+    rsum = dsc + align256(B * H * NC * D * D * 2);
+    const int64_t rs = B * H * KH * T * 2 * 4;
+    if (KH == 1) {
+      dq1 = dk1 = dla1 = dbe1 = -1;
+      total = rsum + rs;
+      return;
+    }
+    dq1 = rsum + align256(rs);
+    dk1 = dq1 + align256(B * H * T * D * 2);
+    dla1 = dk1 + align256(B * H * T * D * 2);
+    dbe1 = dla1 + align256(B * H * T * 4);
+    total = dbe1 + B * H * T * 4;
+  }
+};
+
+template <int KH>
+int delta_fwd(const void* q, const void* k, const void* v, const float* la, const float* beta, const float* S0,
+              void* o, float* S_final, void* sent, void* W, void* X, int64_t B, int64_t H, int64_t T,
+              hipStream_t st) {
+  const int NC = (int)((T + C - 1) / C);
+  const int heads = (int)(B * H);
+  hipLaunchKernelGGL(aspin_delta_inv<KH>, dim3((unsigned)(heads * NC)), dim3(64), 0, st, (const __bf16*)k, la, beta,
+                     (__bf16*)X, (int)T, NC);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  const int rc = set_smem((const void*)aspin_delta_fwd<KH>, fwd_smem<KH>());
+  if (rc) return rc;
+  hipLaunchKernelGGL(aspin_delta_fwd<KH>, dim3((unsigned)(heads * KH)), dim3(512), fwd_smem<KH>(), st,
+                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, beta, (const __bf16*)X, S0,
+                     (__bf16*)o, (__bf16*)W, S_final, (__bf16*)sent, (int)T, NC);
+  PGN_RETURN_LAUNCH();
+}
+
+template <int KH>
+int delta_bwd(const void* q, const void* k, const void* v, const float* la, const float* beta, const void* sent,
+              const void* W, const void* X, const void* dO, const float* dS_final, void* dq, void* dk, void* dv,
+              float* dla, float* dbeta, float* dS0, void* workspace, int64_t B, int64_t H, int64_t T,
+              hipStream_t st) {
+  int rc = set_smem((const void*)aspin_delta_bwd_chain<KH>, chain_smem<KH>());
+  if (rc) return rc;
+  rc = set_smem((const void*)aspin_delta_bwd_local<KH>, local_smem<KH>());
+  if (rc) return rc;
+  const int NC = (int)((T + C - 1) / C);
+  const int scans = (int)(B * H * KH);
+  const BwdWorkspace L(B, H, T, 64 * KH);
+  unsigned char* ws = (unsigned char*)workspace;
+  __bf16* drhs = (__bf16*)(ws + L.drhs);
+  __bf16* dsc = (__bf16*)(ws + L.dsc);
+  float* rs = (float*)(ws + L.rsum);
+  __bf16* dq1 = KH == 2 ? (__bf16*)(ws + L.dq1) : nullptr;
+  __bf16* dk1 = KH == 2 ? (__bf16*)(ws + L.dk1) : nullptr;
+  float* dla1 = KH == 2 ? (float*)(ws + L.dla1) : nullptr;
+  float* dbe1 = KH == 2 ? (float*)(ws + L.dbe1) : nullptr;
+  hipLaunchKernelGGL(aspin_delta_bwd_chain<KH>, dim3((unsigned)scans), dim3(512), chain_smem<KH>(), st,
+                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, beta, (const __bf16*)X,
+                     (const __bf16*)sent, (const __bf16*)dO, dS_final, drhs, dsc, rs, dS0, (int)T, NC);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(aspin_delta_bwd_local<KH>, dim3((unsigned)(scans * NC)), dim3(512), local_smem<KH>(), st,
+                     (const __bf16*)q, (const __bf16*)k, la, beta, (const __bf16*)W, (const __bf16*)sent,
+                     (const __bf16*)dO, drhs, dsc, rs, (__bf16*)dq, dq1, (__bf16*)dk, dk1, (__bf16*)dv, dla, dla1,
+                     dbeta, dbe1, (int)T, NC);
+  if (KH == 1) PGN_RETURN_LAUNCH();
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  DeltaJoin j = {};
+  j.x[0] = (__bf16*)dq;
+  j.y[0] = dq1;
+  j.x[1] = (__bf16*)dk;
+  j.y[1] = dk1;
+  j.f[0] = dla;
+  j.e[0] = dla1;
+  j.f[1] = dbeta;
+  j.e[1] = dbe1;
+  j.n = B * H * T * 64 * KH;
+  j.m = B * H * T;
+  hipLaunchKernelGGL(aspin_delta_join, dim3((unsigned)((j.n / 8 + 255) / 256)), dim3(256), 0, st, j);
+  PGN_RETURN_LAUNCH();
+}
 
 }  // namespace
 
 extern "C" int64_t pragnosia_aspin_delta_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D,
                                                              int64_t chunk) {
   if (!shape_ok(B, H, T, D, chunk)) return -1;
-  const int64_t NC = (T + C - 1) / C;
-  const int64_t drhs = B * H * T * DK * 2, dsc = B * H * NC * DK * DK * 2, rs = B * H * T * 2 * 4;
-  return ((drhs + 255) / 256) * 256 + ((dsc + 255) / 256) * 256 + rs;
+  return BwdWorkspace(B, H, T, D).total;
 }
 
 extern "C" int pragnosia_aspin_delta_fwd(const void* q, const void* k, const void* v, const float* la,
                                          const float* beta, const float* S0, void* o, float* S_final, void* sent,
                                          void* W, void* X, int64_t B, int64_t H, int64_t T, int64_t D,
                                          int64_t chunk, void* stream) {
-  if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
+  if ((D != DK && D != 2 * DK) || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
   PGN_CHECK_ARG(q && k && v && la && beta && o && S_final && W && X);
-  const int NC = (int)((T + C - 1) / C);
-  const int nbh = (int)(B * H);
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(aspin_delta_inv, dim3((unsigned)(nbh * NC)), dim3(64), 0, st, (const __bf16*)k, la, beta,
-                     (__bf16*)X, (int)T, NC);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  int rc = set_smem((const void*)aspin_delta_fwd, kFwdSmem);
-  if (rc) return rc;
-  hipLaunchKernelGGL(aspin_delta_fwd, dim3((unsigned)nbh), dim3(512), kFwdSmem, st, (const __bf16*)q, (const __bf16*)k,
-                     (const __bf16*)v, la, beta, (const __bf16*)X, S0, (__bf16*)o, (__bf16*)W, S_final,
-                     (__bf16*)sent, (int)T, NC);
-  PGN_RETURN_LAUNCH();
+  return D == DK ? delta_fwd<1>(q, k, v, la, beta, S0, o, S_final, sent, W, X, B, H, T, st)
+                 : delta_fwd<2>(q, k, v, la, beta, S0, o, S_final, sent, W, X, B, H, T, st);
 }
 
 extern "C" int pragnosia_aspin_delta_bwd(const void* q, const void* k, const void* v, const float* la,
@@ -987,30 +1237,13 @@ extern "C" int pragnosia_aspin_delta_bwd(const void* q, const void* k, const voi
                                          float* dla, float* dbeta, float* dS0, void* workspace,
                                          int64_t workspace_bytes, int64_t B, int64_t H, int64_t T, int64_t D,
                                          int64_t chunk, void* stream) {
-  if (D != DK || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
+  if ((D != DK && D != 2 * DK) || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
   PGN_CHECK_ARG(q && k && v && la && beta && sent && W && X && dO && dq && dk && dv && dla && dbeta && workspace);
-  const int64_t need = pragnosia_aspin_delta_bwd_workspace_bytes(B, H, T, D, chunk);
-  PGN_CHECK_ARG(workspace_bytes >= need);
-  int rc = set_smem((const void*)aspin_delta_bwd_chain, kChainSmem);
-  if (rc) return rc;
-  rc = set_smem((const void*)aspin_delta_bwd_local, kLocalSmem);
-  if (rc) return rc;
-  const int NC = (int)((T + C - 1) / C);
-  const int nbh = (int)(B * H);
-  unsigned char* ws = (unsigned char*)workspace;
-  __bf16* drhs = (__bf16*)ws;
-  __bf16* dsc = (__bf16*)(ws + ((B * H * T * DK * 2 + 255) / 256) * 256);
-  float* rs = (float*)((unsigned char*)dsc + ((B * H * NC * DK * DK * 2 + 255) / 256) * 256);
+  PGN_CHECK_ARG(workspace_bytes >= BwdWorkspace(B, H, T, D).total);
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(aspin_delta_bwd_chain, dim3((unsigned)nbh), dim3(512), kChainSmem, st, (const __bf16*)q,
-                     (const __bf16*)k, (const __bf16*)v, la, beta, (const __bf16*)X, (const __bf16*)sent,
-                     (const __bf16*)dO, dS_final, drhs, dsc, rs, dS0, (int)T, NC);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(aspin_delta_bwd_local, dim3((unsigned)(nbh * NC)), dim3(512), kLocalSmem, st,
-                     (const __bf16*)q, (const __bf16*)k, la, beta, (const __bf16*)W, (const __bf16*)sent,
-                     (const __bf16*)dO, drhs, dsc, rs, (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, dla, dbeta, (int)T,
-                     NC);
-  PGN_RETURN_LAUNCH();
+  return D == DK ? delta_bwd<1>(q, k, v, la, beta, sent, W, X, dO, dS_final, dq, dk, dv, dla, dbeta, dS0, workspace,
+                                B, H, T, st)
+                 : delta_bwd<2>(q, k, v, la, beta, sent, W, X, dO, dS_final, dq, dk, dv, dla, dbeta, dS0, workspace,
+                                B, H, T, st);
 }

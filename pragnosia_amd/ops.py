@@ -256,9 +256,13 @@ def _bf16(t: Tensor) -> Tensor:
     return t.to(torch.bfloat16).contiguous()
 
 
-def _expect_scan(op: str, q: Tensor, k, v, la, beta=None, S0=None, theta=None) -> None:
-    """q, k, v (B, H, T, 64); la and beta (B, H, T); S0 (B, H, 64, 64); theta (H, 32); all on q's device."""
-    _expect(op, q.device, q=(q, (None, None, None, 64)))
+def _expect_scan(op: str, q: Tensor, k, v, la, beta=None, S0=None, theta=None, widths=(64,)) -> None:
+    """q, k, v (B, H, T, D) with D in `widths`; la and beta (B, H, T); S0 (B, H, D, D); theta (H, D / 2); all on q's
+    device."""
+    if q.dim() == 4 and q.shape[-1] in widths:
+        _expect(op, q.device, q=(q, (None, None, None, q.shape[-1])))
+    else:
+        _expect(op, q.device, q=(q, (None, None, None, widths[0])))
     B, H, T, D = q.shape
     _expect(op, q.device, k=(k, (B, H, T, D)), v=(v, (B, H, T, D)), la=(la, (B, H, T)), beta=(beta, (B, H, T)),
             S0=(S0, (B, H, D, D)), theta=(theta, (H, D // 2)))
@@ -539,12 +543,14 @@ aspin_chunk_wide.register_autograd(_wide_backward, setup_context=_aspin_setup)
 @torch.library.custom_op("pragnosia::aspin_delta", mutates_args=())
 def aspin_delta(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor, S0: Optional[Tensor],
                 want_sent: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Delta-rule chunked scan. q, k, v (B, H, T, 64) (cast to bf16), la and beta (B, H, T) fp32, S0 (B, H, 64, 64)
-    fp32 or None. Returns (o bf16, S_final fp32, sent bf16 (B, H, NC, 64, 64) or empty, W bf16 (B, H, T, 64),
+    """Delta-rule chunked scan. q, k, v (B, H, T, D), D = 64 or 128 (cast to bf16), la and beta (B, H, T) fp32, S0
+    (B, H, D, D) fp32 or None. Returns (o bf16, S_final fp32, sent bf16 (B, H, NC, D, D) or empty, W bf16 (B, H, T, D),
     X bf16 (B, H, NC, 64, 64)); W and X are the intermediates the backward reads (not differentiable). Each entering
-    state in sent is stored transposed (sent[..., c, j, d] = S_c[d, j]); `.transpose(-1, -2)` gives the states."""
+    state in sent is stored transposed (sent[..., c, j, d] = S_c[d, j]); `.transpose(-1, -2)` gives the states.
+    D = 128 runs each head as two scans over its value halves (the rule is independent per value column given X),
+    sharing X."""
     _require_gpu(q, k, v, la, beta, S0)
-    _expect_scan("aspin_delta", q, k, v, la, beta=beta, S0=S0)
+    _expect_scan("aspin_delta", q, k, v, la, beta=beta, S0=S0, widths=(64, 128))
     q, k, v, la, beta, S0 = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(beta), _f32(S0)
     B, H, T, D = q.shape
     NC = (T + CHUNK - 1) // CHUNK
@@ -575,7 +581,7 @@ def aspin_delta_bwd(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor, s
                     do: Tensor, dS: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Backward of aspin_delta. Returns (dq, dk, dv bf16, dla fp32, dbeta fp32, dS0 fp32)."""
     _require_gpu(q, k, v, la, beta, sent, W, X, do, dS)
-    _expect_scan("aspin_delta_bwd", q, k, v, la, beta=beta)
+    _expect_scan("aspin_delta_bwd", q, k, v, la, beta=beta, widths=(64, 128))
     B, H, T, D = q.shape
     NC = (T + CHUNK - 1) // CHUNK
     _expect("aspin_delta_bwd", q.device, sent=(sent, (B, H, NC, D, D)), W=(W, (B, H, T, D)),

@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 10
+    assert L.pragnosia_abi_version() == 11
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 
@@ -103,6 +103,20 @@ def test_wide_arguments(L):
                                128, 64, 3, null)
     assert L.pragnosia_aspin_chunk_bwd_wide(*bargs(wb - 1, one)) == -1
     assert L.pragnosia_aspin_chunk_bwd_wide(*bargs(wb, null)) == -1              # the backward needs sent
+
+
+def test_delta_workspace_both_widths(L):
+    """The delta backward's workspace: drhs, the per-chunk state gradients and the per-scan row sums; at head dim 128
+    also the second slots of dq, dk, dla and dbeta (each head runs as two value-half scans whose parts are summed)."""
+    q = L.pragnosia_aspin_delta_bwd_workspace_bytes
+    # B2 H3 T100 (2 chunks), D 64: drhs 76800 + state gradients 98304 + row sums 4800
+    assert q(2, 3, 100, 64, 64) == 76800 + 98304 + 4800
+    # D 128: drhs 153600 + state gradients 393216 + row sums 9600 (to 9728) + dq, dk 153600 each + dla 2400 (to
+    # 2560) + dbeta 2400
+    assert q(2, 3, 100, 128, 64) == 153600 + 393216 + 9728 + 2 * 153600 + 2560 + 2400
+    assert q(2, 3, 100, 96, 64) == -1 and q(2, 3, 100, 128, 32) == -1
+    null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    assert L.pragnosia_aspin_delta_fwd(*([one] * 5), null, *([one] * 5), 1, 1, 100, 96, 64, null) == -2
 
 
 def test_product_never_imports_oracle():

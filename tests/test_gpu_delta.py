@@ -157,3 +157,68 @@ def test_delta_carried_windows_equal_one_pass(delta):
         a, Sa, *_ = delta(*(t[:, :, :130] for t in dev[:5]), dev[5], False)
         b, Sb, *_ = delta(*(t[:, :, 130:] for t in dev[:5]), Sa, False)
     assert rel(torch.cat([a, b], 2), y) < TOL_OUT and rel(Sb, S) < TOL_OUT
+
+
+# ---- head dim 128 (the reference's hdspin / sdspin / tspin / aspin1 carriers, `src/model.py:651-660`): each head runs
+# as two scans over its value halves sharing X; dq, dk, dla and dbeta are the sums of the two scans' parts.
+@pytest.mark.parametrize("T,s0", [(64, False), (200, True), (1, True), (130, True)])
+def test_delta_128_matches_oracle(delta, T, s0):
+    q, k, v, la, be, S0 = _inputs(2, 2, T, 128, seed=300 + T, s0=s0)
+    print(f"delta 128: T {T} s0 {s0}", flush=True)
+    _assert(_check(delta, q, k, v, la, be, S0, seed=300 + T))
+
+
+def test_delta_128_intermediates(delta):
+    """At head dim 128: X (shared by the head's two value-half scans) against the oracle's inverse and X (I + N) = I;
+    W and the entering states (stored transposed per chunk) against the oracle's."""
+    q, k, v, la, be, S0 = _inputs(1, 2, 200, 128, seed=41)
+    with torch.no_grad():
+        _, _, Sent, Wr = O.scan_twopass_delta(*(t.double() for t in (q, k, v, la, be, S0)), 64)
+        o, S, sent, W, X = delta(*(t.cuda() for t in (q, k, v, la, be, S0)), True)
+    (qc, kc, vc), lc, (bc,), NC = O._chunk_views([q.double(), k.double(), v.double()], la.double(), 64,
+                                                  extra=(be.double(),))
+    dec, _, _, _ = O._decays(lc)
+    Xr = O.delta_inverse(kc, bc, dec)
+    assert X.shape == (1, 2, NC, 64, 64) and sent.shape == (1, 2, NC, 128, 128) and W.shape == (1, 2, 200, 128)
+    assert rel(X.float(), Xr) < 1e-2
+    assert rel(W.float(), Wr) < TOL_OUT
+    assert rel(sent.transpose(-1, -2).float(), Sent) < TOL_OUT
+    N = bc.unsqueeze(-1) * torch.tril((kc @ kc.transpose(-1, -2)) * dec, -1)
+    eye = torch.eye(64, dtype=torch.float64)
+    assert ((X.double().cpu() @ (eye + N)) - eye).abs().max() < 2e-2
+
+
+def test_delta_128_known_answer(delta):
+    """The reference's overwrite test (`tests/test_assoc.py:118-130`) at head dim 128, with the key in the second key
+    half and the values in the second value half: the second write replaces the first."""
+    B, H, T, D = 1, 1, 2, 128
+    k = torch.zeros(B, H, T, D)
+    k[..., 100] = 1.0
+    v = torch.zeros(B, H, T, D)
+    v[0, 0, 0, 70] = 1.0
+    v[0, 0, 1, 71] = 1.0
+    la = torch.zeros(B, H, T)
+    be = torch.ones(B, H, T)
+    with torch.no_grad():
+        o, S, _, _, _ = delta(k.cuda(), k.cuda(), v.cuda(), la.cuda(), be.cuda(), None, False)
+    assert torch.allclose(o[0, 0, 1].float().cpu(), v[0, 0, 1], atol=1e-3)
+    assert torch.allclose(S[0, 0, 100].cpu(), v[0, 0, 1], atol=1e-3)
+    assert S[0, 0].abs().sum().item() == pytest.approx(1.0, abs=1e-3)
+
+
+def test_delta_128_long_sequence(delta):
+    """B2 H3 T512 at head dim 128 with S0, forward and backward against the fp32 oracle (fp64 at this size is slow
+    on the host)."""
+    q, k, v, la, be, S0 = _inputs(2, 3, 512, 128, seed=51)
+    g = torch.Generator().manual_seed(52)
+    do = torch.randn(q.shape, generator=g)
+    dSf = torch.randn(2, 3, 128, 128, generator=g)
+    r = [t.clone().requires_grad_(True) for t in (q, k, v, la, be, S0)]
+    yr, Sr, _, _ = O.scan_twopass_delta(*r, 64)
+    ((yr * do).sum() + (Sr * dSf).sum()).backward()
+    kk = [t.cuda().requires_grad_(True) for t in (q, k, v, la, be, S0)]
+    yk, Sk, _, _, _ = delta(*kk, True)
+    ((yk.float() * do.cuda()).sum() + (Sk * dSf.cuda()).sum()).backward()
+    assert rel(yk, yr) < TOL_OUT and rel(Sk, Sr) < TOL_OUT
+    for a, b in zip(kk, r):
+        assert rel(a.grad, b.grad) < TOL_GRAD

@@ -101,8 +101,8 @@ def test_short_conv_carrier(delta, kernel):
 @pytest.mark.parametrize("mixer", ["hdspin", "sdspin", "aspin1", "hspin1"])
 def test_head_dim_128_mixers_lm(mixer):
     """The reference's head-dim-128 carriers (`src/model.py:650-660`) in a small LM (d 256: two heads of 128):
-    forward and forward_carried logits against the oracle (fp32: the delta rule at head dim 128 runs the exact
-    scan; hspin1 the bf16 kernels), a finite backward, and the graphed greedy decode equal to the eager loop."""
+    forward and forward_carried logits against the oracle (the bf16 MFMA kernels for both rules: bf16 tolerance),
+    a finite backward, and the graphed greedy decode equal to the eager loop."""
     from pragnosia_amd.decode import GreedyDecoder, greedy_eager
     from pragnosia_amd.model import LM
     torch.manual_seed(80)
@@ -113,7 +113,11 @@ def test_head_dim_128_mixers_lm(mixer):
     sd = {k: v.detach().double() for k, v in lm.state_dict().items()}
     lm = lm.cuda()
     ids = torch.randint(0, 300, (2, 100), generator=g)
-    tol = 1e-4 if mixer != "hspin1" else 2e-2
+    # sdspin keeps 8 of each key's 128 coordinates: keys within a chunk overlap, the delta rule's chunk inverse is
+    # ill-conditioned and amplifies the bf16 operand rounding (as in test_delta_repeated_keys_bounded). Measured on
+    # this LM over three seeds: 3.0-4.3e-2 at head dim 128 and 1.9-3.9e-2 with the same top-8 keys on 64-wide heads,
+    # against 1.4e-3-9.2e-3 without top-k at either width and 5e-7 on the exact fp32 scan.
+    tol = 5e-2 if mixer == "sdspin" else 2e-2
     with torch.no_grad():
         lg = lm(ids[:, :48].cuda())
         lc = lm.forward_carried(ids.cuda(), window=48)

@@ -53,9 +53,14 @@ def _samples():
     qw, kw, vw = (F.normalize(r(B, 1, T, 128), dim=-1).bfloat16().requires_grad_(True) for _ in range(3))
     law = F.logsigmoid(r(B, 1, T) + 3).requires_grad_(True)
     S0w = (r(B, 1, 128, 128) * 0.1).requires_grad_(True)
+    bew = torch.sigmoid(r(B, 1, T)).requires_grad_(True)
     with torch.no_grad():
         _, _, sentw = op.aspin_chunk_wide(qw, kw, vw, law, S0w, True)
+        _, _, sentdw, Ww, Xw = op.aspin_delta(qw, kw, vw, law, bew, S0w, True)
     return [
+        ("aspin_delta", (qw, kw, vw, law, bew, S0w, True)),
+        ("aspin_delta_bwd", (qw.detach(), kw.detach(), vw.detach(), law.detach(), bew.detach(), sentdw, Ww, Xw,
+                             r(B, 1, T, 128).bfloat16(), r(B, 1, 128, 128))),
         ("aspin_chunk_wide", (qw, kw, vw, law, S0w, True)),
         ("aspin_chunk_wide_bwd", (qw.detach(), kw.detach(), vw.detach(), law.detach(), sentw,
                                   r(B, 1, T, 128).bfloat16(), r(B, 1, 128, 128))),
