@@ -936,6 +936,27 @@ def phase_rates(reps=50):
         return e0.elapsed_time(e1) / reps * 1e3
 
     out = {"workload": "plain and delta chunked scans, B16 T512 H12 D64 bf16 (configs[2]), phase stamps"}
+    # the delta inverse (one wave per (batch-head, chunk)): its phases from the unit's second stamp buffer
+    import numpy as np
+    st.pragnosia_stamps_set_delta_aux.argtypes = [ctypes.c_void_p]
+    st.pragnosia_stamps_set_delta_aux.restype = ctypes.c_int
+    ninv = nwg * NC
+    ibuf = torch.zeros(ninv * 8, device=dev, dtype=torch.int32)
+    assert st.pragnosia_stamps_set_delta_aux(P(ibuf)) == 0
+    for _ in range(3):
+        assert run["delta_fwd"](st) == 0
+    torch.cuda.synchronize()
+    assert st.pragnosia_stamps_set_delta_aux(None) == 0
+    si = ibuf.cpu().numpy().view(np.uint32).reshape(ninv, 8)
+    clk = float(np.median(((si[:, 6].astype(np.int64) - si[:, 0]) % (1 << 32)) /
+                          ((si[:, 7].astype(np.int64) - si[:, 1]) % (1 << 32)))) * 1e8
+    # differences within a wave only (the shader clocks of different XCDs are not synchronised)
+    t = _rel32(si[:, [0, 2, 3, 4, 5, 6]], si[:, :1]).astype(np.float64) / clk * 1e6  # us from the wave's start
+    names = ("staging: keys, decays, strengths", "N", "diagonal blocks", "block levels", "store X")
+    out["delta_inverse_phases"] = {
+        "waves": ninv, "shader_clock_GHz": round(clk / 1e9, 3),
+        "median_us": {n: round(float(np.median(t[:, j + 1] - t[:, j])), 3) for j, n in enumerate(names)},
+        "wave_total_median_us": round(float(np.median(t[:, 5] - t[:, 0])), 3)}
     for kern in ("plain_fwd", "plain_bwd", "delta_fwd", "delta_bwd_chain"):
         setter = getattr(st, "pragnosia_stamps_set_" + unit[kern])
         buf = torch.zeros(nwg * waves[kern] * (4 + 2 * NC), device=dev, dtype=torch.int32)

@@ -121,6 +121,9 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
 
   const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;  // head (not scan), chunk
   const int l = threadIdx.x, g = l >> 4, i = l & 15;
+  // instrumented build (second buffer): per chunk, clocks at the start (entries 0, 1), the end of the key staging (2),
+  // of N (3), of the diagonal blocks (4), of the block levels (5), and clocks after the store (6, 7)
+  PGN_STAMP_CLOCKS_AUX(blockIdx.x * 8);
   const int t0 = c * C, nr = min(C, T - t0);
   const __bf16* kc = k + ((size_t)bh * T + t0) * DKEY;
   // the keys in 16-byte row segments (eight contiguous 1 KB loads per wave and half, rows past T as zeros), staged
@@ -141,6 +144,7 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
   Ls[l] = incl_scan64(lav, l);
   bs[l] = bev;
   __syncthreads();
+  PGN_STAMP_AUX(blockIdx.x * 8 + 2);
   bf16x8 kf[4][2 * KH];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb)
@@ -167,6 +171,7 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
     }
   }
   __syncthreads();
+  PGN_STAMP_AUX(blockIdx.x * 8 + 3);
 
   // X by blocks of 16: X_ii = (I + N_ii)^-1 by forward substitution, one column of one diagonal block per lane; then
   // X_ij = -X_ii sum_{k=j}^{i-1} N_ik X_kj, i > j, level by level (i - j = 1, 2, 3), on fp32 MFMA
@@ -193,6 +198,7 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
     for (int t = 0; t < 16; ++t) xb[t * BP + cl] = xd[t];
   }
   __syncthreads();
+  PGN_STAMP_AUX(blockIdx.x * 8 + 4);
   {
     const int r16 = l & 15, k4 = l >> 4;
     // one 16 x 16 x 16 product A B accumulated onto acc: A the block at `Ab`, read transposed when `at`
@@ -234,6 +240,7 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
       __syncthreads();
     }
   }
+  PGN_STAMP_AUX(blockIdx.x * 8 + 5);
   // X (bf16, row-major; zero above the diagonal blocks) in 16-byte row segments
   __bf16* Xc = X + ((size_t)bh * NC + c) * C * C;
 #pragma unroll
@@ -251,6 +258,7 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
     }
     *reinterpret_cast<bf16x8*>(Xc + r * C + c0) = out;
   }
+  PGN_STAMP_CLOCKS_AUX(blockIdx.x * 8 + 6);
 }
 
 // ------------------------------------------------------------------------------------------------------------------

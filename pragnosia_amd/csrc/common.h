@@ -41,8 +41,12 @@ inline hipError_t pgn_lds_limit(const void* fn, size_t bytes) {
 typedef __attribute__((address_space(1))) unsigned int pgn_stamp_t;
 #define PGN_STAMP_UNIT(name)                                                                        \
   static __constant__ pgn_stamp_t* pgn_stamps;                                                      \
+  static __constant__ pgn_stamp_t* pgn_stamps_aux;                                                  \
   extern "C" int pragnosia_stamps_set_##name(void* buffer) {                                        \
     return (int)hipMemcpyToSymbol(HIP_SYMBOL(pgn_stamps), &buffer, sizeof(buffer));                 \
+  }                                                                                                 \
+  extern "C" int pragnosia_stamps_set_##name##_aux(void* buffer) {                                  \
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(pgn_stamps_aux), &buffer, sizeof(buffer));             \
   }
 #define PGN_STAMP(i)                                                                                \
   do {                                                                                              \
@@ -57,10 +61,27 @@ typedef __attribute__((address_space(1))) unsigned int pgn_stamp_t;
       pgn_b_[(i) + 1] = (unsigned int)__builtin_amdgcn_s_memrealtime();                             \
     }                                                                                               \
   } while (0)
+// The second buffer of a unit (`pragnosia_stamps_set_<name>_aux`), for a kernel launched beside the one stamping the
+// first: the shader clock to entry i (PGN_STAMP_AUX), or the shader and 100 MHz clocks to i, i + 1.
+#define PGN_STAMP_AUX(i)                                                                            \
+  do {                                                                                              \
+    pgn_stamp_t* const pgn_b_ = pgn_stamps_aux;                                                     \
+    if (pgn_b_ != nullptr) pgn_b_[(i)] = (unsigned int)__builtin_amdgcn_s_memtime();                \
+  } while (0)
+#define PGN_STAMP_CLOCKS_AUX(i)                                                                     \
+  do {                                                                                              \
+    pgn_stamp_t* const pgn_b_ = pgn_stamps_aux;                                                     \
+    if (pgn_b_ != nullptr) {                                                                        \
+      pgn_b_[(i)] = (unsigned int)__builtin_amdgcn_s_memtime();                                     \
+      pgn_b_[(i) + 1] = (unsigned int)__builtin_amdgcn_s_memrealtime();                             \
+    }                                                                                               \
+  } while (0)
 #else
 #define PGN_STAMP_UNIT(name)
 #define PGN_STAMP(i) ((void)0)
 #define PGN_STAMP_CLOCKS(i) ((void)0)
+#define PGN_STAMP_AUX(i) ((void)0)
+#define PGN_STAMP_CLOCKS_AUX(i) ((void)0)
 #endif
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;

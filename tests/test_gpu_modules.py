@@ -156,8 +156,18 @@ def test_prep_kernel_forward_backward(dtype):
     sum((o.float() * wi.cuda()).sum() for o, wi in zip(kouts, w)).backward()
     for o, r in zip(kouts, outs):
         assert rel(o, r) < 1e-2
+    # the op's outputs are the bf16 operands of the scan, and their gradients arrive rounded to bf16 (2^-9 per
+    # element): against the exact fp64 gradients that costs 1.4-3.2e-3 (measured over three seeds), so fp32 inputs are
+    # held to 5e-3 there, and the kernel itself to the fp32 bound against the same fp64 composition fed the
+    # bf16-rounded upstream gradients (measured <= 1.3e-5)
     for a, b in zip(k_in, ref_in):
-        assert rel(a.grad, b.grad) < (5e-2 if dtype == torch.bfloat16 else 1e-2)
+        assert rel(a.grad, b.grad) < (5e-2 if dtype == torch.bfloat16 else 5e-3)
+    if dtype == torch.float32:
+        ref2 = [t.double().requires_grad_(True) for t in (qp, kp, vp, gate, th)]
+        outs2 = OA.prep(*ref2[:4], ref2[4], pos)
+        sum((o * wi.bfloat16().double()).sum() for o, wi in zip(outs2, w)).backward()
+        for a, b in zip(k_in, ref2):
+            assert rel(a.grad, b.grad) < 1e-4
 
 
 def test_spin_rf_forward_backward():
