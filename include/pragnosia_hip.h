@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (11); bumped on any change of the entry points. */
+/* ABI version of this header (12); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -160,6 +160,32 @@ int pragnosia_aspin_chunk_bwd_wide(const void* q, const void* k, const void* v, 
  * (nn.RMSNorm(dk) with eps=None, i.e. fp32 epsilon, computed in fp32). */
 int pragnosia_aspin_out_fwd(const void* o, const float* weight, float eps, void* y, int y_bf16, float* rstd,
                             int64_t B, int64_t H, int64_t T, int64_t D, void* stream);
+
+/* LayerNorm over the last dimension (D a multiple of 256, at most 2048; rows = the product of the leading dims),
+ * fp32 statistics: mu = mean(x), var = mean((x - mu)^2), y = (x - mu) / sqrt(var + eps) * weight + bias, written as
+ * bf16 when y_bf16 (the dtype the matmul after it computes in under autocast) or fp32; mean and rstd ((rows) fp32)
+ * are kept for the backward. x, weight, bias fp32. Replaces `self.ln(x)` of the carrier (`nn.LayerNorm(d)`,
+ * src/assoc.py:323,388) and of the MLP (src/model.py:555) with the cast to bf16 that autocast's matmul applies to
+ * its fp32 output. PRAGNOSIA_ERR_UNSUPPORTED for other D. */
+int pragnosia_layer_norm_fwd(const float* x, const float* weight, const float* bias, float eps, void* y, int y_bf16,
+                             float* mean, float* rstd, int64_t rows, int64_t D, void* stream);
+
+/* Rows of D fp32 partial sums pragnosia_layer_norm_bwd writes for each of dweight and dbias (-1 if rejected). */
+int64_t pragnosia_layer_norm_partials(int64_t rows, int64_t D);
+
+/* Backward of pragnosia_layer_norm_fwd from dy ((rows, D), bf16 when dy_bf16, else fp32): dx (rows, D) fp32 and the
+ * weight and bias gradients as partial rows (pragnosia_layer_norm_partials(rows, D) rows of D fp32 each; the
+ * gradients are their sums over rows). Replaces the autograd backward of the same lines. */
+int pragnosia_layer_norm_bwd(const void* dy, int dy_bf16, const float* x, const float* weight, const float* mean,
+                             const float* rstd, float* dx, float* dw_partials, float* db_partials, int64_t rows,
+                             int64_t D, void* stream);
+
+/* Column sums of a row-major fp32 matrix x (rows, cols): out[c] = sum over r of x[r][c], in an order fixed by the
+ * shape (deterministic). Sums the per-workgroup partial rows of the parameter gradients above (LayerNorm weight and
+ * bias, the RMSNorm weight, the rotation frequencies, the decay and gate biases), the reduction the reference's
+ * autograd applies to a broadcast parameter's gradient (e.g. the bias of nn.LayerNorm, src/assoc.py:388). Records no
+ * memset, so a captured backward can hold it. */
+int pragnosia_colsum_f32(const float* x, int64_t rows, int64_t cols, float* out, void* stream);
 
 /* Rows of 64 fp32 partial weight gradients pragnosia_aspin_out_bwd writes (-1 if the shape is rejected). */
 int64_t pragnosia_aspin_out_weight_partials(int64_t B, int64_t H, int64_t T);

@@ -31,6 +31,10 @@ SIGNATURES = {
     "pragnosia_aspin_chunk_fwd_wide": [_p] * 9 + [_i64] * 7 + [_p],
     "pragnosia_aspin_chunk_bwd_wide": [_p] * 13 + [_i64] * 7 + [_p],
     "pragnosia_aspin_out_fwd": [_p] * 2 + [_f32, _p, _i32, _p] + [_i64] * 4 + [_p],
+    "pragnosia_layer_norm_fwd": [_p] * 3 + [_f32, _p, _i32, _p, _p, _i64, _i64, _p],
+    "pragnosia_layer_norm_partials": [_i64] * 2,
+    "pragnosia_layer_norm_bwd": [_p, _i32] + [_p] * 7 + [_i64, _i64, _p],
+    "pragnosia_colsum_f32": [_p, _i64, _i64, _p, _p],
     "pragnosia_aspin_out_weight_partials": [_i64] * 3,
     "pragnosia_aspin_out_bwd": [_p, _i32] + [_p] * 5 + [_i64] * 4 + [_p],
     "pragnosia_aspin_exact_fwd": [_p] * 10 + [_i64] * 5 + [_i32, _p],
@@ -56,7 +60,8 @@ SIGNATURES = {
 # entry points that return a size (int64) rather than a status code
 _RET_I64 = {"pragnosia_aspin_delta_bwd_workspace_bytes", "pragnosia_aspin_prep_theta_partials",
             "pragnosia_aspin_chunk_seg_workspace_bytes", "pragnosia_aspin_out_weight_partials",
-            "pragnosia_aspin_prep_proj_partials", "pragnosia_aspin_chunk_wide_workspace_bytes"}
+            "pragnosia_aspin_prep_proj_partials", "pragnosia_aspin_chunk_wide_workspace_bytes",
+            "pragnosia_layer_norm_partials"}
 
 _lib = None
 

@@ -329,6 +329,11 @@ class AssocCarrier(nn.Module):
         bt = None if bt is None else bt.transpose(1, 2).float()
         return q, k, v, la.transpose(1, 2).float(), bt, qp.dtype, cc
 
+    def _norm_in(self, x):
+        """`self.ln(x)` (`src/assoc.py:388`); with FUSED_PLUMBING one kernel each way that writes the result in the
+        dtype the projections compute in."""
+        return _op_mod.layer_norm(x, self.ln) if FUSED_PLUMBING else self.ln(x)
+
     def _epilogue(self, o, dtype):
         """`self.on(o.to(dtype)).transpose(1, 2).reshape(B, T, D)` (`src/assoc.py:500-505`) for the scan's bf16 output
         o (B, H, T, dk): one kernel each way (per-head RMSNorm in fp32, rounded once to `dtype`, written token-major)."""
@@ -356,7 +361,7 @@ class AssocCarrier(nn.Module):
             S0, p0, cc = h0
         else:
             S0, p0 = h0
-        z = self.ln(x)
+        z = self._norm_in(x)
         p_dev = p0.float().reshape(()) if torch.is_tensor(p0) else None
         p_host = 0.0 if torch.is_tensor(p0) else float(p0)
         shifted = S0 is not None and (p_dev is not None or p_host != 0.0)
@@ -434,7 +439,7 @@ class AssocCarrier(nn.Module):
                 outs.append(o)
             return torch.cat(outs, 1), st
         S0, p0 = (None, pos0) if h0 is None else h0[:2]
-        z = self.ln(x)
+        z = self._norm_in(x)
         p_dev = p0.float().reshape(()) if torch.is_tensor(p0) else None
         p_host = 0.0 if torch.is_tensor(p0) else float(p0)
         if S0 is not None and (p_dev is not None or p_host != 0.0):

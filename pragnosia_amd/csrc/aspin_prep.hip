@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const
 // projections' gradient (dcol = the gradient buffer, same layout and stride): dlogit_a = dla mask (-exp(A))
 // sigmoid(logit_a + b) (mask: the floor not active), dlogit_g = dsig sig (1 - sig), dlogit_b = dbeta mask sig (1 -
 // sig) (mask: bmin not active); and one partial per workgroup of the three per-head sums (d gbias or d bbias,
-// d abias, dA = sum dla mask la) to part[blk * 3 ..].
+// d abias, dA = sum dla mask la) to part, laid out (B, T blocks, H, 3) like the theta partials.
 template <typename In>
 __global__ __launch_bounds__(256) void prep_bwd(
     const In* __restrict__ qp, const In* __restrict__ kp, const In* __restrict__ vp, const float* __restrict__ gl,
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256) void prep_bwd(
     float a = 0.f;
 #pragma unroll
     for (int r = 0; r < SLOTS; ++r) a += red3[r][threadIdx.x];
-    part[(size_t)blk * 3 + threadIdx.x] = a;
+    part[(((size_t)b * ntb + tb) * H + h) * 3 + threadIdx.x] = a;
   }
 }
 

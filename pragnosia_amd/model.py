@@ -25,7 +25,7 @@ import torch.utils.checkpoint
 
 from ._lib import PragnosiaError
 from .assoc import AssocCarrier
-from .ops import linear
+from .ops import layer_norm, linear
 from .spin import SpinCarrier
 
 MIXERS = {
@@ -49,8 +49,9 @@ class MLP(nn.Module):
         self.b = nn.Linear(mult * d, d)
 
     def forward(self, x):
-        # the biases' gradients as GEMMs, so a captured training step records no memset (ops.linear)
-        return x + linear(F.gelu(linear(self.n(x), self.a)), self.b)
+        # the biases' gradients as GEMMs, so a captured training step records no memset (ops.linear); the norm on
+        # its kernel, in the dtype the first matmul computes in (ops.layer_norm)
+        return x + linear(F.gelu(linear(layer_norm(x, self.n), self.a)), self.b)
 
 
 class LM(nn.Module):

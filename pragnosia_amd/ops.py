@@ -36,13 +36,21 @@ def _f32(t: Optional[Tensor]) -> Optional[Tensor]:
     return None if t is None else t.to(torch.float32).contiguous()
 
 
+COLSUM_MAX_ROWS = 4096  # above this many rows the GEMM form (more workgroups per column) is the faster one
+
+
 def colsum(x: Tensor) -> Tensor:
-    """Sum over the first dimension, as a GEMM against a ones vector. torch's column sum over many rows is a
-    multi-block reduction that zeroes its semaphores with a memset, and memset nodes captured in a HIP graph have
-    given wrong results on replays after the first on this ROCm stack; a GEMM records none. Same function, the terms
-    summed in another order."""
+    """Sum over the first dimension. torch's column sum over many rows is a multi-block reduction that zeroes its
+    semaphores with a memset, and memset nodes captured in a HIP graph have given wrong results on replays after the
+    first on this ROCm stack. A contiguous fp32 GPU tensor of at most COLSUM_MAX_ROWS rows (the kernels' partial
+    rows) is summed by `pragnosia_colsum_f32` (one launch, a fixed order); anything else as a GEMM against a ones
+    vector. Neither records a memset. Same function, the terms summed in another order."""
     rows = x.shape[0]
     x2 = x.reshape(rows, -1)
+    if x2.is_cuda and x2.dtype == torch.float32 and x2.is_contiguous() and 0 < rows <= COLSUM_MAX_ROWS and x2.numel():
+        out = torch.empty(x2.shape[1], device=x.device, dtype=torch.float32)
+        check(lib().pragnosia_colsum_f32(_ptr(x2), rows, x2.shape[1], _ptr(out), _stream(x2)), "pragnosia_colsum_f32")
+        return out.reshape(x.shape[1:])
     return (torch.ones(1, rows, device=x.device, dtype=x2.dtype) @ x2).reshape(x.shape[1:])
 
 
@@ -245,6 +253,111 @@ def _out_backward(ctx, gy, _grstd):
 
 
 aspin_out.register_autograd(_out_backward, setup_context=_out_setup)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# LayerNorm before the carrier's projections and the MLP: replaces nn.LayerNorm(d) (src/assoc.py:323,388;
+# src/model.py:555) together with autocast's cast of its fp32 output to bf16 for the matmul after it
+LN_MAX_D = 2048
+
+
+def ln_supported(x: Tensor, mod) -> bool:
+    """Whether the LayerNorm kernels take `mod(x)`: fp32 x on the GPU, the last dim a multiple of 256 up to 2048,
+    an affine nn.LayerNorm over that dim."""
+    D = x.shape[-1]
+    return (x.is_cuda and x.dtype == torch.float32 and D % 256 == 0 and D <= LN_MAX_D and x.numel() > 0
+            and isinstance(mod, torch.nn.LayerNorm) and tuple(mod.normalized_shape) == (D,)
+            and mod.weight is not None and mod.bias is not None
+            and mod.weight.dtype == torch.float32 and mod.bias.dtype == torch.float32)
+
+
+@torch.library.custom_op("pragnosia::layer_norm", mutates_args=())
+def layer_norm_op(x: Tensor, weight: Tensor, bias: Tensor, eps: float,
+                  out_bf16: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """LayerNorm of x (..., D) fp32 over its last dim with fp32 statistics. Returns (y (..., D), bf16 if out_bf16 else
+    fp32; mean and rstd (rows,) fp32, kept for the backward)."""
+    _require_gpu(x, weight, bias)
+    D = x.shape[-1]
+    _expect("layer_norm", x.device, weight=(weight, (D,)), bias=(bias, (D,)))
+    if x.dtype != torch.float32 or weight.dtype != torch.float32 or bias.dtype != torch.float32:
+        raise PragnosiaError("layer_norm: x, weight and bias must be fp32")
+    x = x.contiguous()
+    rows = x.numel() // D
+    y = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16 if out_bf16 else torch.float32)
+    mean = torch.empty(rows, device=x.device, dtype=torch.float32)
+    rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
+    check(lib().pragnosia_layer_norm_fwd(_ptr(x), _ptr(weight.contiguous()), _ptr(bias.contiguous()), float(eps),
+                                         _ptr(y), int(out_bf16), _ptr(mean), _ptr(rstd), rows, D, _stream(x)),
+          "pragnosia_layer_norm_fwd")
+    return y, mean, rstd
+
+
+@layer_norm_op.register_fake
+def _(x, weight, bias, eps, out_bf16):
+    rows = x.numel() // x.shape[-1]
+    return (x.new_empty(x.shape, dtype=torch.bfloat16 if out_bf16 else torch.float32),
+            x.new_empty(rows, dtype=torch.float32), x.new_empty(rows, dtype=torch.float32))
+
+
+@torch.library.custom_op("pragnosia::layer_norm_bwd", mutates_args=())
+def layer_norm_bwd(dy: Tensor, x: Tensor, weight: Tensor, mean: Tensor,
+                   rstd: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Backward of layer_norm from dy (bf16 or fp32, x's shape). Returns (dx fp32, dweight fp32, dbias fp32)."""
+    _require_gpu(dy, x, weight, mean, rstd)
+    D = x.shape[-1]
+    rows = x.numel() // D
+    _expect("layer_norm_bwd", x.device, dy=(dy, tuple(x.shape)), weight=(weight, (D,)), mean=(mean, (rows,)),
+            rstd=(rstd, (rows,)))
+    if dy.dtype not in (torch.bfloat16, torch.float32):
+        dy = dy.float()
+    dy, x = dy.contiguous(), x.contiguous()
+    P = lib().pragnosia_layer_norm_partials(rows, D)
+    if P < 0:
+        raise PragnosiaError(f"layer_norm_bwd: shape {tuple(x.shape)} rejected")
+    dx = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    dwp = torch.empty(P, D, device=x.device, dtype=torch.float32)
+    dbp = torch.empty(P, D, device=x.device, dtype=torch.float32)
+    check(lib().pragnosia_layer_norm_bwd(_ptr(dy), int(dy.dtype == torch.bfloat16), _ptr(x), _ptr(weight.contiguous()),
+                                         _ptr(mean), _ptr(rstd), _ptr(dx), _ptr(dwp), _ptr(dbp), rows, D, _stream(x)),
+          "pragnosia_layer_norm_bwd")
+    with torch.autocast("cuda", enabled=False):  # the partial rows summed in fp32
+        return dx, colsum(dwp), colsum(dbp)
+
+
+@layer_norm_bwd.register_fake
+def _(dy, x, weight, mean, rstd):
+    D = x.shape[-1]
+    return (x.new_empty(x.shape, dtype=torch.float32), x.new_empty(D, dtype=torch.float32),
+            x.new_empty(D, dtype=torch.float32))
+
+
+def _ln_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
+    x, weight, bias, eps, out_bf16 = inputs
+    _, mean, rstd = output
+    ctx.save_for_backward(x, weight, mean, rstd)
+    ctx.mark_non_differentiable(mean, rstd)
+
+
+def _ln_backward(ctx, dy, _dmean, _drstd):
+    if dy is None:
+        return None, None, None, None, None
+    x, weight, mean, rstd = ctx.saved_tensors
+    dx, dw, db = layer_norm_bwd(dy, x, weight, mean, rstd)
+    return dx, dw, db, None, None
+
+
+layer_norm_op.register_autograd(_ln_backward, setup_context=_ln_setup)
+
+
+def layer_norm(x: Tensor, mod) -> Tensor:
+    """`mod(x)` for an nn.LayerNorm `mod` feeding a matmul: on the LayerNorm kernels when they take the shape
+    (ln_supported), with the output in bf16 under bf16 autocast (the dtype that matmul computes in, so its own cast
+    is skipped) and fp32 otherwise; `mod(x)` itself elsewhere."""
+    if not ln_supported(x, mod):
+        return mod(x)
+    bf16 = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
+    return layer_norm_op(x, mod.weight, mod.bias, float(mod.eps), bf16)[0]
 
 
 # ---------------------------------------------------------------------------------------------------------------
@@ -959,7 +1072,7 @@ def aspin_prep_proj_bwd(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor:
                                               _ptr(dbeta) if has_beta else None, _ptr(dP), _ptr(dth), _ptr(part),
                                               B, T, H, D, int(P.dtype == torch.bfloat16), _stream(P)),
           "pragnosia_aspin_prep_proj_bwd")
-    sums = colsum(part.view(B, H, -1, 3).transpose(1, 2).reshape(-1, H, 3))
+    sums = colsum(part.view(-1, H, 3))  # partials laid out (B, T blocks, H, 3)
     dxb = sums[:, 0].clone() if (gated or has_beta) else P.new_empty(0, dtype=torch.float32)
     return dP, sums[:, 1].clone(), sums[:, 2].clone(), dxb, colsum(dth)
 

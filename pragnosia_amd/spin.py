@@ -11,7 +11,7 @@ import torch
 import torch.nn as nn
 
 from ._lib import PragnosiaError
-from .ops import linear
+from .ops import layer_norm, linear
 from .scan import scan_hip
 
 
@@ -55,7 +55,7 @@ class SpinCarrier(nn.Module):
                                  "kernels; the FFT carrier is outside it")
         if not x.is_cuda:
             raise PragnosiaError("SpinCarrier runs on a ROCm GPU only; there is no CPU path")
-        z = self.ln(x)
+        z = layer_norm(x, self.ln)  # self.ln(x), in the dtype the projections compute in
         mag, ang = self.lam()
         # per-token log-magnitude <= 0: the recurrence gate scales the channel's timescale
         logmag = -self.gate_c * torch.sigmoid(linear(z, self.Wr)) * (-torch.log(mag))

@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 11
+    assert L.pragnosia_abi_version() == 12
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 
@@ -117,6 +117,16 @@ def test_delta_workspace_both_widths(L):
     assert q(2, 3, 100, 96, 64) == -1 and q(2, 3, 100, 128, 32) == -1
     null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
     assert L.pragnosia_aspin_delta_fwd(*([one] * 5), null, *([one] * 5), 1, 1, 100, 96, 64, null) == -2
+
+
+def test_colsum_arguments_rejected(L):
+    null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    assert L.pragnosia_colsum_f32(one, 0, 8, one, null) == -1
+    assert L.pragnosia_colsum_f32(one, 8, 0, one, null) == -1
+    assert L.pragnosia_colsum_f32(null, 8, 8, one, null) == -1
+    assert L.pragnosia_layer_norm_partials(8192, 768) == 512      # 8 waves of 2 rows per partial row
+    assert L.pragnosia_layer_norm_partials(100, 2048) == 13       # 8 waves of 1 row
+    assert L.pragnosia_layer_norm_partials(100, 96) == -1
 
 
 def test_product_never_imports_oracle():

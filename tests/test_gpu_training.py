@@ -57,7 +57,14 @@ def _samples():
     with torch.no_grad():
         _, _, sentw = op.aspin_chunk_wide(qw, kw, vw, law, S0w, True)
         _, _, sentdw, Ww, Xw = op.aspin_delta(qw, kw, vw, law, bew, S0w, True)
+    xl = r(3, 40, 768, grad=True)
+    wl, bl = (1 + 0.1 * r(768)).requires_grad_(True), (0.1 * r(768)).requires_grad_(True)
+    with torch.no_grad():
+        _, ml, rl = op.layer_norm(xl, wl, bl, 1e-5, True)
     return [
+        ("layer_norm", (xl, wl, bl, 1e-5, True)),
+        ("layer_norm", (xl, wl, bl, 1e-5, False)),
+        ("layer_norm_bwd", (r(3, 40, 768).bfloat16(), xl.detach(), wl.detach(), ml, rl)),
         ("aspin_delta", (qw, kw, vw, law, bew, S0w, True)),
         ("aspin_delta_bwd", (qw.detach(), kw.detach(), vw.detach(), law.detach(), bew.detach(), sentdw, Ww, Xw,
                              r(B, 1, T, 128).bfloat16(), r(B, 1, 128, 128))),
