@@ -26,9 +26,11 @@ from ._lib import PragnosiaError
 
 _op = torch.ops.pragnosia
 
-# Module switches kept from the reference (`src/assoc.py:272-276`). FUSED_SCAN: skip the per-chunk entering states
-# when no later layer reads them (the reference switched to a third-party fused kernel there; here the same delta
-# kernel runs without writing them). FUSED_PROJ: one GEMM for the delta carrier's five input projections.
+# Module switches kept from the reference (`src/assoc.py:272-276`). FUSED_SCAN: delta carriers whose per-chunk
+# entering states no later layer reads keep nothing from forward to backward but the scan's inputs (the reference
+# switched to a third-party fused kernel there, which keeps the state on chip and recomputes chunk states in the
+# backward; here `aspin_delta_fused` runs the same delta kernels and recomputes X, W and the entering states in its
+# backward). FUSED_PROJ: one GEMM for the delta carrier's five input projections.
 FUSED_SCAN = False
 FUSED_PROJ = False
 # This build's own switch for the plumbing around the plain-rule scan. True: one GEMM for the q, k, v, decay and
@@ -385,9 +387,14 @@ class AssocCarrier(nn.Module):
                       else _op.aspin_rebase(S0, self.theta, p_dev, p_host))
             pos = _positions(T, x.device, getattr(self, "pos_wrap", None))
             q, k, v, la, bt, dtype, cc = self._scan_inputs(z, pos, cc)
+            fused = FUSED_SCAN and self.delta and not self.need_sent
             want = bool(self.need_sent or not (FUSED_SCAN and self.delta) or
                         _needs_grad(x, S0, *self.parameters()))
-            if self.delta:
+            if fused:
+                # nothing kept for the backward but the scan's inputs: it recomputes X, W and the entering states
+                o, S = _op.aspin_delta_fused(q, k, v, la, bt, S0)
+                sent = None
+            elif self.delta:
                 o, S, sent, _, _ = _op.aspin_delta(q, k, v, la, bt, S0, want)
                 sent = sent.transpose(-1, -2) if want else sent  # the op stores each state transposed
             elif wide:

@@ -748,6 +748,46 @@ def _delta_backward(ctx, do, dS, _dsent, _dW, _dX):
 aspin_delta.register_autograd(_delta_backward, setup_context=_delta_setup)
 
 
+@torch.library.custom_op("pragnosia::aspin_delta_fused", mutates_args=())
+def aspin_delta_fused(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor,
+                      S0: Optional[Tensor]) -> tuple[Tensor, Tensor]:
+    """The delta-rule scan keeping nothing for its backward but its inputs: (o bf16, S_final fp32). The state lives in
+    the chain waves' registers; X, W and the per-chunk entering states exist only within the call (W and X in
+    temporaries freed on return, the entering states not written). Its backward recomputes them with the same
+    kernels, so they are bit-identical to what the forward formed and so are the gradients, then runs the
+    stored-state backward. This is the trait of the third-party fused kernel the reference's FUSED_SCAN switches to
+    (`src/assoc.py:481-492`: state on chip, chunk states recomputed in the backward instead of written per chunk and
+    read back): the activation memory kept from forward to backward drops by 2 B/elem of W, 2 B per entering-state
+    element and 2 B per X element, for one more inverse and forward pass in the backward."""
+    o, S, _, _, _ = aspin_delta(q, k, v, la, beta, S0, False)
+    return o, S
+
+
+@aspin_delta_fused.register_fake
+def _(q, k, v, la, beta, S0):
+    B, H, T, D = q.shape
+    return q.new_empty(B, H, T, D, dtype=torch.bfloat16), q.new_empty(B, H, D, D, dtype=torch.float32)
+
+
+def _delta_fused_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
+    q, k, v, la, beta, S0 = inputs
+    ctx.has_s0 = S0 is not None
+    ctx.save_for_backward(q, k, v, la, beta, S0)
+
+
+def _delta_fused_backward(ctx, do, dS):
+    q, k, v, la, beta, S0 = ctx.saved_tensors
+    _, _, sent, W, X = aspin_delta(q, k, v, la, beta, S0, True)  # the forward's intermediates, recomputed
+    if do is None:
+        do = torch.zeros(q.shape, device=q.device, dtype=torch.bfloat16)
+    dq, dk, dv, dla, dbeta, dS0 = aspin_delta_bwd(q, k, v, la, beta, sent, W, X, do.contiguous(), dS)
+    return dq, dk, dv, dla, dbeta, (dS0 if ctx.has_s0 else None)
+
+
+aspin_delta_fused.register_autograd(_delta_fused_backward, setup_context=_delta_fused_setup)
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # the scan with fp32 / fp64 operands (no bf16 rounding): replaces assoc_scan's fp32/fp64 torch forms and their
 # autograd backward, src/assoc.py:118-165, :207-269

@@ -1,5 +1,5 @@
 """The carrier's module switches against the fp64 oracle on the same state_dict: `fused_scan` (no entering states
-kept, `src/assoc.py:518-532`), `FUSED_PROJ` (one GEMM for the delta carrier's five projections, `:272-276`,
+kept, `src/assoc.py:518-532`; under autograd the delta carriers recompute them in the backward, `:481-492`), `FUSED_PROJ` (one GEMM for the delta carrier's five projections, `:272-276`,
 `:415-427`), `key_topk` (`:438-442`), `pos_wrap` (`:406-410`), `beta_scale` (`:469-472`) and `hl_floor` (`:355-359`).
 
 Tolerances: kernel path (bf16 operands) 2e-2 on outputs and states, 5e-2 on gradients; torch path (kernel=False,
@@ -42,6 +42,71 @@ def test_fused_scan_context(delta):
             assert all(mx.sent is None for mx in lm.mix) or not delta
         assert not A.FUSED_SCAN and all(mx.need_sent for mx in lm.mix)
     assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_delta_fused_recomputes_in_backward(D):
+    """`aspin_delta_fused` (the FUSED_SCAN training path) equals the stored-state op bit for bit, outputs and every
+    gradient (its backward recomputes X, W and the entering states with the same kernels), and what it keeps for the
+    backward is its inputs: the saved bytes drop by exactly the entering states, W and X, less the S0 it keeps."""
+    import torch.nn.functional as F
+    from pragnosia_amd import ops  # noqa: F401
+    op = torch.ops.pragnosia
+    g = torch.Generator().manual_seed(5 + D)
+    B, H, T = 2, 3, 200
+    q = F.normalize(torch.randn(B, H, T, D, generator=g), dim=-1).bfloat16().cuda()
+    k = F.normalize(torch.randn(B, H, T, D, generator=g), dim=-1).bfloat16().cuda()
+    v = torch.randn(B, H, T, D, generator=g).bfloat16().cuda()
+    la = (-0.1 * torch.rand(B, H, T, generator=g)).cuda()
+    beta = (0.2 + 0.6 * torch.rand(B, H, T, generator=g)).cuda()
+    S0 = (0.1 * torch.randn(B, H, D, D, generator=g)).cuda()
+    do = torch.randn(B, H, T, D, generator=g).bfloat16().cuda()
+    dS = torch.randn(B, H, D, D, generator=g).cuda()
+
+    def run(fused):
+        ins = [t.clone().requires_grad_(True) for t in (q, k, v, la, beta, S0)]
+        saved = []
+
+        def pack(t):
+            saved.append(t.numel() * t.element_size())
+            return t
+        with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+            o, S = op.aspin_delta_fused(*ins) if fused else op.aspin_delta(*ins, True)[:2]
+        torch.autograd.backward([o, S], [do, dS])
+        return o, S, [t.grad for t in ins], sum(saved)
+    o1, S1, g1, b1 = run(False)
+    o2, S2, g2, b2 = run(True)
+    assert torch.equal(o1, o2) and torch.equal(S1, S2)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+    NC = (T + 63) // 64
+    assert b1 - b2 == 2 * (B * H * NC * D * D + B * H * T * D + B * H * NC * 64 * 64) - 4 * B * H * D * D
+
+
+def test_fused_scan_training_step():
+    """A training step of a delta LM inside fused_scan: the carriers keep no entering states, and the loss and every
+    parameter gradient equal the stored-state path's bit for bit."""
+    from pragnosia_amd import assoc as A
+    from pragnosia_amd.model import LM
+    torch.manual_seed(101)
+    lm = LM(vocab=300, d=128, layers=2, ctx=160, mixer="dspin").cuda()
+    ids = torch.randint(0, 300, (2, 160), device="cuda")
+
+    def step():
+        lm.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            logits = lm(ids)
+        loss = torch.nn.functional.cross_entropy(logits.float().reshape(-1, 300), ids.reshape(-1))
+        loss.backward()
+        return loss.detach(), [None if p.grad is None else p.grad.clone() for p in lm.parameters()]
+    ref_loss, ref_grads = step()
+    with A.fused_scan(lm):
+        loss, grads = step()
+        assert all(mx.sent is None for mx in lm.mix)
+    assert torch.equal(loss, ref_loss)
+    assert sum(a is not None for a in grads) > 10
+    for a, b in zip(grads, ref_grads):
+        assert (a is None and b is None) or torch.equal(a, b)
 
 
 @pytest.mark.parametrize("kernel", [True, False])

@@ -66,6 +66,7 @@ def _samples():
         ("layer_norm", (xl, wl, bl, 1e-5, False)),
         ("layer_norm_bwd", (r(3, 40, 768).bfloat16(), xl.detach(), wl.detach(), ml, rl)),
         ("aspin_delta", (qw, kw, vw, law, bew, S0w, True)),
+        ("aspin_delta_fused", (qw, kw, vw, law, bew, S0w)),
         ("aspin_delta_bwd", (qw.detach(), kw.detach(), vw.detach(), law.detach(), bew.detach(), sentdw, Ww, Xw,
                              r(B, 1, T, 128).bfloat16(), r(B, 1, 128, 128))),
         ("aspin_chunk_wide", (qw, kw, vw, law, S0w, True)),
