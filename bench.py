@@ -442,6 +442,8 @@ def carrier_layer_bench(steps=20, delta=False):
                 for _ in range(3):
                     step()
             torch.cuda.current_stream().wait_stream(side)
+            for _ in range(2):
+                step()  # the caching allocator keeps blocks per stream: the timed stream's own, allocated untimed
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             for _ in range(steps):

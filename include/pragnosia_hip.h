@@ -187,6 +187,19 @@ int pragnosia_layer_norm_bwd(const void* dy, int dy_bf16, const float* x, const 
  * memset, so a captured backward can hold it. */
 int pragnosia_colsum_f32(const float* x, int64_t rows, int64_t cols, float* out, void* stream);
 
+/* Bytes of workspace pragnosia_wgrad_bf16 needs for (M, N, K) (0: none; -1 if the shape is rejected). */
+int64_t pragnosia_wgrad_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/* The weight gradient of a linear layer over its token rows: C (M x N fp32, row pitch ldc) = A^T B, or C += A^T B
+ * when accumulate, with A (K x M) and B (K x N) bf16, row-major with row pitches lda, ldb (K = tokens; A the output
+ * gradient, B the layer input). M and N multiples of 8, lda and ldb multiples of 8, ldc of 4, pointers 16-byte
+ * aligned. K is split over workgroups whose fp32 partials (in the caller's workspace) are summed in a fixed order,
+ * so the result is deterministic. Replaces the weight-gradient GEMM autograd forms for the F.linear / nn.Linear
+ * calls around the carrier (src/assoc.py:384-512: the q/k/v/decay/gate projections and the gated o-projection) and
+ * the MLP (src/model.py:552-560), there a bf16 GEMM cast to the fp32 parameter. */
+int pragnosia_wgrad_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, float* C, int64_t ldc, int accumulate,
+                         void* workspace, int64_t workspace_bytes, int64_t M, int64_t N, int64_t K, void* stream);
+
 /* Rows of 64 fp32 partial weight gradients pragnosia_aspin_out_bwd writes (-1 if the shape is rejected). */
 int64_t pragnosia_aspin_out_weight_partials(int64_t B, int64_t H, int64_t T);
 

@@ -35,6 +35,8 @@ SIGNATURES = {
     "pragnosia_layer_norm_partials": [_i64] * 2,
     "pragnosia_layer_norm_bwd": [_p, _i32] + [_p] * 7 + [_i64, _i64, _p],
     "pragnosia_colsum_f32": [_p, _i64, _i64, _p, _p],
+    "pragnosia_wgrad_workspace_bytes": [_i64] * 3,
+    "pragnosia_wgrad_bf16": [_p, _i64, _p, _i64, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _p],
     "pragnosia_aspin_out_weight_partials": [_i64] * 3,
     "pragnosia_aspin_out_bwd": [_p, _i32] + [_p] * 5 + [_i64] * 4 + [_p],
     "pragnosia_aspin_exact_fwd": [_p] * 10 + [_i64] * 5 + [_i32, _p],
@@ -61,7 +63,7 @@ SIGNATURES = {
 _RET_I64 = {"pragnosia_aspin_delta_bwd_workspace_bytes", "pragnosia_aspin_prep_theta_partials",
             "pragnosia_aspin_chunk_seg_workspace_bytes", "pragnosia_aspin_out_weight_partials",
             "pragnosia_aspin_prep_proj_partials", "pragnosia_aspin_chunk_wide_workspace_bytes",
-            "pragnosia_layer_norm_partials"}
+            "pragnosia_layer_norm_partials", "pragnosia_wgrad_workspace_bytes"}
 
 _lib = None
 

@@ -317,7 +317,7 @@ class AssocCarrier(nn.Module):
             gated = not (self.delta or self.write_all)
             extra = [self.wi.weight] if gated else ([self.wb.weight] if self.delta else [])
             W = torch.cat([self.q.weight, self.k.weight, self.v.weight, self.wa.weight] + extra)
-            P = F.linear(z, W)
+            P = _op_mod.linear_w(z, W)
             q, k, v, la, beta = _op.aspin_prep_proj(
                 P, self.h, self.wa.bias, self.A, self.la_floor if self.hl_floor else None,
                 self.wi.bias if gated else None, self.wb.bias if self.delta else None,
@@ -419,7 +419,8 @@ class AssocCarrier(nn.Module):
         self.sent = sent
         if _needs_grad(x, o, self.o.weight, self.gate):
             # gate on the weight, as the reference does for training (it keeps the backward's saved tensor small)
-            out = x + F.linear(o, self.o.weight * torch.sigmoid(self.gate))
+            Wg = self.o.weight * torch.sigmoid(self.gate)
+            out = x + (_op_mod.linear_w(o, Wg) if FUSED_PLUMBING else F.linear(o, Wg))
         else:
             # the same function without materialising a gated d x d weight on every call (decode, inference)
             out = x + F.linear(o, self.o.weight) * torch.sigmoid(self.gate)

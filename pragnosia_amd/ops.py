@@ -54,35 +54,84 @@ def colsum(x: Tensor) -> Tensor:
     return (torch.ones(1, rows, device=x.device, dtype=x2.dtype) @ x2).reshape(x.shape[1:])
 
 
+@torch.library.custom_op("pragnosia::wgrad", mutates_args=())
+def wgrad(dy: Tensor, x: Tensor) -> Tensor:
+    """The weight gradient of y = x Wᵀ over token rows, dy (K, M) and x (K, N) bf16 → dW = dyᵀ x (M, N) fp32: the
+    split-K MFMA kernel `pragnosia_wgrad_bf16`, the fp32 accumulator being the result (autograd's form is a bf16 GEMM
+    whose result is cast to the fp32 parameter). M and N multiples of 8."""
+    _require_gpu(dy, x)
+    if dy.dim() != 2 or x.dim() != 2 or dy.shape[0] != x.shape[0]:
+        raise PragnosiaError(f"wgrad: dy (K, M) and x (K, N) expected, got {tuple(dy.shape)} and {tuple(x.shape)}")
+    _expect("wgrad", dy.device, x=(x, (dy.shape[0], None)))
+    dy, x = _bf16(dy), _bf16(x)
+    K, M = dy.shape
+    N = x.shape[1]
+    nbytes = lib().pragnosia_wgrad_workspace_bytes(M, N, K)
+    if nbytes < 0:
+        raise PragnosiaError(f"wgrad: shape M={M} N={N} K={K} rejected (M and N must be multiples of 8)")
+    out = torch.empty(M, N, device=dy.device, dtype=torch.float32)
+    ws = torch.empty(nbytes, device=dy.device, dtype=torch.uint8) if nbytes else None
+    check(lib().pragnosia_wgrad_bf16(_ptr(dy), M, _ptr(x), N, _ptr(out), N, 0, _ptr(ws), nbytes, M, N, K,
+                                     _stream(dy)), "pragnosia_wgrad_bf16")
+    return out
+
+
+@wgrad.register_fake
+def _(dy, x):
+    return dy.new_empty(dy.shape[1], x.shape[1], dtype=torch.float32)
+
+
+def weight_grad(g2: Tensor, x2: Tensor) -> Tensor:
+    """g2ᵀ x2 over token rows (the weight gradient of F.linear): `wgrad` in fp32 for bf16 GPU operands whose widths
+    are multiples of 8 (autocast's case), a matmul in the operands' dtype otherwise."""
+    if (g2.is_cuda and g2.dtype == torch.bfloat16 and x2.dtype == torch.bfloat16 and g2.shape[0] > 0
+            and g2.shape[1] % 8 == 0 and x2.shape[1] % 8 == 0):
+        return wgrad(g2, x2)
+    return g2.t() @ x2
+
+
 class _Linear(torch.autograd.Function):
-    """F.linear(x, W, b) with its bias gradient formed by `colsum` (a GEMM) instead of torch's column sum, so a
-    backward captured in a HIP graph records no memset node; the other gradients are the usual two GEMMs. Runs in the
-    autocast dtype like F.linear."""
+    """F.linear(x, W, b) whose backward forms the weight gradient with `weight_grad` (the split-K kernel under bf16
+    autocast) and the bias gradient with `colsum` instead of torch's column sum, so a backward captured in a HIP graph
+    records no memset node; the input gradient is the usual GEMM. Runs in the autocast dtype like F.linear."""
 
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
     def forward(ctx, x, W, b):
-        ctx.save_for_backward(x, W)
+        # under autocast the operands are cast once here, as F.linear would, and the casts are what the backward
+        # reads (no second cast of W there)
+        ctx.dtypes = (x.dtype, W.dtype)  # the gradients' dtypes
         ctx.b_dtype = None if b is None else b.dtype
+        if torch.is_autocast_enabled("cuda") and x.is_cuda:
+            dt = torch.get_autocast_dtype("cuda")
+            x, W, b = x.to(dt), W.to(dt), (None if b is None else b.to(dt))
+        ctx.save_for_backward(x, W)
         return F.linear(x, W, b)
 
     @staticmethod
     @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, g):
         x, W = ctx.saved_tensors
+        x_dtype, W_dtype = ctx.dtypes
         g2 = g.reshape(-1, g.shape[-1])
         cdt = g2.dtype
-        gx = (g2 @ W.to(cdt)).reshape(x.shape).to(x.dtype) if ctx.needs_input_grad[0] else None
-        gW = (g2.t() @ x.reshape(-1, x.shape[-1]).to(cdt)).to(W.dtype) if ctx.needs_input_grad[1] else None
+        gx = (g2 @ W.to(cdt)).reshape(x.shape).to(x_dtype) if ctx.needs_input_grad[0] else None
+        gW = weight_grad(g2, x.reshape(-1, x.shape[-1]).to(cdt)).to(W_dtype) if ctx.needs_input_grad[1] else None
         gb = colsum(g2).to(ctx.b_dtype) if (ctx.b_dtype is not None and ctx.needs_input_grad[2]) else None
         return gx, gW, gb
 
 
 def linear(x: Tensor, mod) -> Tensor:
-    """`mod(x)` for an nn.Linear `mod`, with a graph-capturable bias gradient (see _Linear)."""
-    if mod.bias is None or not torch.is_grad_enabled():
-        return F.linear(x, mod.weight, mod.bias)
-    return _Linear.apply(x, mod.weight, mod.bias)
+    """`mod(x)` for an nn.Linear `mod`, with the split-K weight gradient and a graph-capturable bias gradient (see
+    _Linear)."""
+    return linear_w(x, mod.weight, mod.bias)
+
+
+def linear_w(x: Tensor, W: Tensor, b: Optional[Tensor] = None) -> Tensor:
+    """F.linear(x, W, b), under autograd through _Linear."""
+    if not torch.is_grad_enabled():
+        return F.linear(x, W, b)
+    return _Linear.apply(x, W, b)
 
 
 def _expect(op: str, dev, **shapes) -> None:

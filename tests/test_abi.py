@@ -129,6 +129,24 @@ def test_colsum_arguments_rejected(L):
     assert L.pragnosia_layer_norm_partials(100, 96) == -1
 
 
+def test_wgrad_workspace_and_rejections(L):
+    """The split count targets ~512 workgroups of 128 x 128 tiles (at most 16 splits, whole 64-row steps each): the
+    workspace holds one fp32 (M, N) partial per split, none for a single split."""
+    q = L.pragnosia_wgrad_workspace_bytes
+    assert q(768, 768, 8192) == 13 * 768 * 768 * 4       # 36 tiles -> 14 splits of 10 steps -> 13 ranges
+    assert q(2328, 768, 8192) == 4 * 2328 * 768 * 4      # 114 tiles -> 4 splits
+    assert q(4096, 4096, 64) == 0                        # one step: no split
+    assert q(12, 8, 64) == -1 and q(8, 12, 64) == -1 and q(8, 8, 0) == -1
+    null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    args = lambda lda, ldb, ldc, wsb, M, N, K: (one, lda, one, ldb, one, ldc, 0, one, wsb, M, N, K, null)
+    assert L.pragnosia_wgrad_bf16(*args(768, 768, 768, q(768, 768, 8192) - 1, 768, 768, 8192)) == -1
+    assert L.pragnosia_wgrad_bf16(*args(760, 768, 768, q(768, 768, 8192), 768, 768, 8192)) == -1   # lda < M
+    assert L.pragnosia_wgrad_bf16(*args(772, 768, 768, q(768, 768, 8192), 768, 768, 8192)) == -1   # lda % 8
+    mis = ctypes.c_void_p(24)
+    assert L.pragnosia_wgrad_bf16(mis, 768, one, 768, one, 768, 0, one, 0, 768, 768, 12, null) == -1  # misaligned
+    assert L.pragnosia_wgrad_bf16(*args(24, 16, 16, 0, 20, 16, 64)) == -1                          # M % 8
+
+
 def test_product_never_imports_oracle():
     pkg = os.path.join(ROOT, "pragnosia_amd")
     for dp, _, files in os.walk(pkg):

@@ -62,6 +62,7 @@ def _samples():
     with torch.no_grad():
         _, ml, rl = op.layer_norm(xl, wl, bl, 1e-5, True)
     return [
+        ("wgrad", (r(200, 24).bfloat16(), r(200, 40).bfloat16())),
         ("layer_norm", (xl, wl, bl, 1e-5, True)),
         ("layer_norm", (xl, wl, bl, 1e-5, False)),
         ("layer_norm_bwd", (r(3, 40, 768).bfloat16(), xl.detach(), wl.detach(), ml, rl)),
