@@ -408,6 +408,65 @@ def carried_bench():
             "carried_vs_unsplit_rel_err_S": round(rel(Sc, Su_loc), 6)}
 
 
+def lm_train_bench(mixer="aspin", updates=4, micro_per_update=4):
+    """Whole-model training at the reference's own context configuration (`PROGRESS.md:428`: 78M, d704, 12 layers,
+    mlp 4, ctx 2048, micro-batch 4, 32k tokens per update; 351 ktok/s plain and 335 delta on an H100 NVL): each
+    micro-step is the trainer's (`src/train.py:494-517`: bf16 autocast trunk, the chunked tied-head loss, backward,
+    gradients accumulated) captured in one HIP graph, and every `micro_per_update` micro-steps one fused AdamW update
+    and a gradient reset run eagerly. Random-init weights, synthetic token ids. Reported: tokens/s over whole updates
+    and the micro-step's own time."""
+    import torch
+    from pragnosia_amd.model import LM
+    torch.manual_seed(11)
+    B, T, V = 4, 2048, 8192
+    m = LM(vocab=V, d=704, layers=12, mlp_mult=4, ctx=T, mixer=mixer).cuda()
+    opt = torch.optim.AdamW(m.parameters(), lr=1e-4, fused=True)
+    for p in m.parameters():
+        p.grad = torch.zeros_like(p)
+    xs = torch.randint(0, V, (B, T + 1), device="cuda")
+
+    def micro():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            h = m.trunk(xs[:, :T])
+        m.loss(h.float(), xs[:, 1:T + 1]).backward()
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            micro()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        micro()
+    opt.step()
+    opt.zero_grad(set_to_none=False)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(updates):
+        for _ in range(micro_per_update):
+            xs.random_(0, V)
+            graph.replay()
+        opt.step()
+        opt.zero_grad(set_to_none=False)
+    e1.record()
+    torch.cuda.synchronize()
+    per_update = e0.elapsed_time(e1) / updates * 1e-3
+    e0.record()
+    for _ in range(micro_per_update):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    micro_s = e0.elapsed_time(e1) / micro_per_update * 1e-3
+    n = sum(p.numel() for p in m.parameters())
+    return {"workload": f"LM({mixer}, d704 L12 mlp4 V8192 ctx2048) training, micro-batch 4, {micro_per_update} "
+                        f"micro-steps ({micro_per_update * B * T} tokens) per fused AdamW update, bf16 autocast, "
+                        "micro-step graph-captured", "params": n,
+            "ktok_s": round(micro_per_update * B * T / per_update / 1e3, 1),
+            "micro_step_ms": round(micro_s * 1e3, 3)}
+
+
 def carrier_layer_bench(steps=20, delta=False):
     """The carrier layer around the scan at configs[2]'s shape: AssocCarrier(768) (12 heads of 64; plain rule, or the
     delta rule) forward + backward on x (B16, T512, 768) under bf16 autocast, fp32 parameters: LayerNorm, the q/k/v
@@ -636,6 +695,8 @@ def gpu_bench(args):
         sec["carried"] = carried_bench()
         sec["carrier_layer"] = carrier_layer_bench()
         sec["carrier_layer_delta"] = carrier_layer_bench(delta=True)
+        sec["lm_train"] = {"plain": lm_train_bench("aspin"), "delta": lm_train_bench("dspin"),
+                           "reference_h100_nvl_ktok_s": {"plain": 351, "delta": 335}}
         sec["decode"] = decode_bench()
         sec["head_dim_128"] = wide_bench()
         sec["lds_contraction"] = lds_contraction_bench()

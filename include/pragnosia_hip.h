@@ -161,7 +161,7 @@ int pragnosia_aspin_chunk_bwd_wide(const void* q, const void* k, const void* v, 
 int pragnosia_aspin_out_fwd(const void* o, const float* weight, float eps, void* y, int y_bf16, float* rstd,
                             int64_t B, int64_t H, int64_t T, int64_t D, void* stream);
 
-/* LayerNorm over the last dimension (D a multiple of 256, at most 2048; rows = the product of the leading dims),
+/* LayerNorm over the last dimension (D a multiple of 4, at most 2048; rows = the product of the leading dims),
  * fp32 statistics: mu = mean(x), var = mean((x - mu)^2), y = (x - mu) / sqrt(var + eps) * weight + bias, written as
  * bf16 when y_bf16 (the dtype the matmul after it computes in under autocast) or fp32; mean and rstd ((rows) fp32)
  * are kept for the backward. x, weight, bias fp32. Replaces `self.ln(x)` of the carrier (`nn.LayerNorm(d)`,

@@ -131,7 +131,11 @@ class LM(nn.Module):
         n = hf.shape[0]
 
         def piece(hc, yc, E):
-            return F.cross_entropy(F.linear(hc, E).float(), yc, reduction="sum")
+            # the logits as the reference forms them (`src/model.py:563-567`): bf16 under autocast on the GPU,
+            # the cross-entropy in fp32
+            with torch.autocast("cuda", dtype=torch.bfloat16, enabled=hc.is_cuda):
+                lg = F.linear(hc, E)
+            return F.cross_entropy(lg.float(), yc, reduction="sum")
 
         total = 0.0
         for i in range(chunks):

@@ -311,10 +311,10 @@ LN_MAX_D = 2048
 
 
 def ln_supported(x: Tensor, mod) -> bool:
-    """Whether the LayerNorm kernels take `mod(x)`: fp32 x on the GPU, the last dim a multiple of 256 up to 2048,
-    an affine nn.LayerNorm over that dim."""
+    """Whether the LayerNorm kernels take `mod(x)`: fp32 x on the GPU, the last dim a multiple of 4 up to 2048, an
+    affine nn.LayerNorm over that dim."""
     D = x.shape[-1]
-    return (x.is_cuda and x.dtype == torch.float32 and D % 256 == 0 and D <= LN_MAX_D and x.numel() > 0
+    return (x.is_cuda and x.dtype == torch.float32 and D % 4 == 0 and D <= LN_MAX_D and x.numel() > 0
             and isinstance(mod, torch.nn.LayerNorm) and tuple(mod.normalized_shape) == (D,)
             and mod.weight is not None and mod.bias is not None
             and mod.weight.dtype == torch.float32 and mod.bias.dtype == torch.float32)

@@ -126,7 +126,8 @@ def test_colsum_arguments_rejected(L):
     assert L.pragnosia_colsum_f32(null, 8, 8, one, null) == -1
     assert L.pragnosia_layer_norm_partials(8192, 768) == 512      # 8 waves of 2 rows per partial row
     assert L.pragnosia_layer_norm_partials(100, 2048) == 13       # 8 waves of 1 row
-    assert L.pragnosia_layer_norm_partials(100, 96) == -1
+    assert L.pragnosia_layer_norm_partials(100, 704) == 7        # 3 blocks of 256: 8 waves of 2 rows
+    assert L.pragnosia_layer_norm_partials(100, 90) == -1 and L.pragnosia_layer_norm_partials(100, 2052) == -1
 
 
 def test_wgrad_workspace_and_rejections(L):

@@ -26,7 +26,8 @@ def _inputs(shape, seed):
     return x, w, b, dy
 
 
-@pytest.mark.parametrize("shape", [(3, 200, 768), (1000, 256), (7, 2048), (1, 1, 1024), (5, 512), (33, 1280)])
+@pytest.mark.parametrize("shape", [(3, 200, 768), (1000, 256), (7, 2048), (1, 1, 1024), (5, 512), (33, 1280),
+                                   (4, 257, 704), (9, 100), (50, 68), (6, 2044)])
 @pytest.mark.parametrize("dy_bf16", [False, True])
 def test_layer_norm_forward_backward(shape, dy_bf16):
     from pragnosia_amd import ops  # noqa: F401
@@ -57,7 +58,7 @@ def test_layer_norm_bf16_output():
 
 def test_layer_norm_helper_dtype_and_fallback():
     """The module helper: fp32 output without autocast, bf16 under bf16 autocast (the dtype of the matmul after it),
-    and nn.LayerNorm itself for a shape the kernels do not take (D = 96)."""
+    and nn.LayerNorm itself for a shape the kernels do not take (D = 90, not a multiple of 4)."""
     from pragnosia_amd.ops import layer_norm
     torch.manual_seed(3)
     mod = torch.nn.LayerNorm(768).cuda()
@@ -66,8 +67,8 @@ def test_layer_norm_helper_dtype_and_fallback():
     with torch.autocast("cuda", dtype=torch.bfloat16):
         yb = layer_norm(x, mod)
     assert yb.dtype == torch.bfloat16 and rel(yb.float(), mod(x)) < 2 ** -8
-    small = torch.nn.LayerNorm(96).cuda()
-    xs = torch.randn(3, 96, device="cuda")
+    small = torch.nn.LayerNorm(90).cuda()
+    xs = torch.randn(3, 90, device="cuda")
     assert torch.equal(layer_norm(xs, small), small(xs))
 
 
