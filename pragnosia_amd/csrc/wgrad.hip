@@ -13,9 +13,9 @@
 // tiles (v_mfma_f32_16x16x32_bf16). K advances 64 rows a step: the step's A and B rows (64 x 128 each, untransposed,
 // 16-byte row segments, four per thread per operand) are staged into double-buffered LDS tiles (pitch 68) and read as
 // operands contracted over the tile's row index with the LDS transpose read. Global loads run kDepth - 1 steps ahead
-// in a ring of register sets (the loop unrolled by kDepth so each set is fixed registers): one step's products are
-// far shorter than a load's latency, and with a single step of lead each step waited out a whole load (measured
-// ~2 us a step). One barrier per step.
+// in a ring of kDepth - 1 register sets (the loop unrolled by the ring's size so each set is fixed registers): one
+// step's products are far shorter than a load's latency, and with a single step of lead each step waited out a
+// whole load (measured ~2 us a step). One barrier per step.
 #include <algorithm>
 
 #include "mfma_tile.h"
@@ -30,7 +30,7 @@ constexpr int kSetTiles = 4;           // A halves (m 0..63, 64..127), B halves
 constexpr int kTargetGroups = 512;     // two per compute unit
 constexpr int kMaxSplits = 16;
 constexpr int kXcds = 8;            // XCDs of an MI355X, taking workgroups in turn
-constexpr int kDepth = 3;          // register sets: loads issued kDepth - 1 steps ahead
+constexpr int kDepth = 3;          // pipeline depth: loads issued kDepth - 1 steps ahead of their step
 
 struct Split {
   int S;        // number of K ranges
@@ -83,9 +83,11 @@ __global__ __launch_bounds__(256) void wgrad_tiles(const __bf16* __restrict__ A,
   const int steps = (int)((k_end - k_begin + KS - 1) / KS);
   float* const dst = out + split * split_stride;
 
-  // Register set j holds the segments of the steps s with s % kDepth == j, loaded kDepth - 1 steps before they are
-  // staged, so kDepth - 1 steps of products cover each load's latency.
-  bf16x8 ra[kDepth][4], rb[kDepth][4];
+  // A ring of kRing = kDepth - 1 register sets: set j holds the segments of the steps s with s % kRing == j, loaded
+  // kRing steps before they are staged, so kRing steps of products cover each load's latency (while step s is
+  // contracted, steps s + 1 .. s + kRing are in flight; step s itself was staged before it started).
+  constexpr int kRing = kDepth - 1;
+  bf16x8 ra[kRing][4], rb[kRing][4];
   const __amdgpu_buffer_rsrc_t a_rows = rows_rsrc(A, lda, k_begin, k_end);
   const __amdgpu_buffer_rsrc_t b_rows = rows_rsrc(B, ldb, k_begin, k_end);
   // Segment u of thread tid: 64-column half u >> 1, row (tid >> 3) + 32 (u & 1) of the step, segment tid & 7 of that
@@ -120,20 +122,21 @@ __global__ __launch_bounds__(256) void wgrad_tiles(const __bf16* __restrict__ A,
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = zero4();
 
-  // prologue: steps 0 .. kDepth - 2 in flight, step 0 staged. The steps run in whole rounds of kDepth (a step past
-  // the split's rows loads zeros through the buffer range check and adds nothing), so every step of the loop body
-  // is unconditional and the ring's registers are defined on every path.
-  const int rounds = (steps + kDepth - 1) / kDepth;
-  static_for<0, kDepth - 1>([&](auto j_c) { load(j_c, decltype(j_c)::value); });
+  // prologue: steps 0 .. kRing - 1 in flight, step 0 staged. The steps run in whole rounds of kRing (a step past the
+  // split's rows loads zeros through the buffer range check and adds nothing), so every step of the loop body is
+  // unconditional and the ring's registers are defined on every path.
+  const int rounds = (steps + kRing - 1) / kRing;
+  static_for<0, kRing>([&](auto j_c) { load(j_c, decltype(j_c)::value); });
   stage(std::integral_constant<int, 0>{}, 0);
   __syncthreads();
-  // step s: load step s + kDepth - 1 into the set step s - 1 used, contract step s from LDS set s & 1, stage step
-  // s + 1 into the other LDS set (its last reader finished before the previous barrier), barrier
+  // step s: load step s + kRing into the set step s occupied (staged before step s began), contract step s from LDS
+  // set s & 1, stage step s + 1 into the other LDS set (its last reader finished before the previous barrier),
+  // barrier
   for (int rd = 0; rd < rounds; ++rd) {
-    static_for<0, kDepth>([&](auto j_c) {
+    static_for<0, kRing>([&](auto j_c) {
       constexpr int j = decltype(j_c)::value;
-      const int s = rd * kDepth + j;
-      load(std::integral_constant<int, (j + kDepth - 1) % kDepth>{}, s + kDepth - 1);
+      const int s = rd * kRing + j;
+      load(j_c, s + kRing);
       __builtin_amdgcn_sched_barrier(0);  // the loads issue before this step's products, not after them
       const __bf16* t = lds + (s & 1) * kSetTiles * TILE;
       const __bf16* At = t + wm * TILE;
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(256) void wgrad_tiles(const __bf16* __restrict__ A,
 #pragma unroll
           for (int b = 0; b < 4; ++b) acc[a][b] = pgn_mfma(fb[b], fa[a], acc[a][b]);
       }
-      stage(std::integral_constant<int, (j + 1) % kDepth>{}, (s + 1) & 1);
+      stage(std::integral_constant<int, (j + 1) % kRing>{}, (s + 1) & 1);
       __syncthreads();
     });
   }
