@@ -44,6 +44,10 @@ def parse():
                     help="run each hot kernel a fixed number of times (for rocprofv3 counter passes) and exit")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the configs[4] decode measurement (batch 1 and 64), print its JSON and exit")
+    ap.add_argument("--profile-workload", choices=("layer", "layer_delta", "lm", "lm_delta", "wgrad"),
+                    help="run one workload a fixed number of times for a tracer (rocprofv3 --kernel-trace or "
+                         "--pmc) and exit: the carrier layer step (graph replays), the LM training micro-step "
+                         "(graph replays), or the weight-gradient kernel at the layer's two shapes")
     ap.add_argument("--phase-rates", action="store_true",
                     help="measure the MFMA rate inside the scan kernels' per-chunk phases from the instrumented "
                          "build (libpragnosia_stamps.so), print its JSON and exit")
@@ -826,6 +830,61 @@ def cpu_baselines_more(args, seconds=5.0):
     return out
 
 
+def profile_workload(name, reps=10):
+    """The workloads behind the layer, LM and weight-gradient traces in profiles/: `reps` graph replays of the
+    carrier layer step (AssocCarrier(768), B16 T512, bf16 autocast, fused plumbing) or of the LM training micro-step
+    (d704 L12 mlp4 ctx2048 micro-batch 4, as lm_train_bench), after three eager warm-up steps on a side stream; or
+    `reps` calls of the weight-gradient kernel at 8192 x 2328 x 768 and 8192 x 768 x 768."""
+    import torch
+    from pragnosia_amd import assoc, ops
+    torch.manual_seed(7)
+    if name == "wgrad":
+        for M in (2328, 768):
+            A = torch.randn(8192, M, device="cuda").bfloat16()
+            Bm = torch.randn(8192, 768, device="cuda").bfloat16()
+            for _ in range(reps):
+                ops.wgrad(A, Bm)
+        torch.cuda.synchronize()
+        return
+    if name.startswith("layer"):
+        m = assoc.AssocCarrier(768, delta=name == "layer_delta").cuda()
+        x = torch.randn(16, 512, 768, device="cuda", requires_grad=True)
+        gy = torch.randn(16, 512, 768, device="cuda")
+
+        def step():
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                y, _ = m(x)
+            y.backward(gy)
+        params = list(m.parameters()) + [x]
+    else:
+        from pragnosia_amd.model import LM
+        m = LM(vocab=8192, d=704, layers=12, mlp_mult=4, ctx=2048, mixer="dspin" if name == "lm_delta" else "aspin")
+        m = m.cuda()
+        xs = torch.randint(0, 8192, (4, 2049), device="cuda")
+
+        def step():
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                h = m.trunk(xs[:, :2048])
+            m.loss(h, xs[:, 1:]).backward()
+        params = list(m.parameters())
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    for p in params:
+        # as carrier_layer_bench (gradients assigned by the captured step) and lm_train_bench (accumulated into
+        # allocated gradients over the micro-steps of an update)
+        p.grad = torch.zeros_like(p) if name.startswith("lm") else None
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+
+
 def profile_kernels(reps=10):
     """For counter runs under rocprofv3 (--pmc FETCH_SIZE, then WRITE_SIZE): each hot kernel `reps` times at its
     configs shape, plus a calibration copy of exactly COPY_BYTES read and COPY_BYTES written (a torch copy_ of a
@@ -1052,6 +1111,9 @@ def main():
         return
     if args.phase_rates:
         print(json.dumps(phase_rates()), flush=True)
+        return
+    if args.profile_workload:
+        profile_workload(args.profile_workload)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the carrier path has no "

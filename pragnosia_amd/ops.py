@@ -102,7 +102,9 @@ class _Linear(torch.autograd.Function):
         # reads (no second cast of W there)
         ctx.dtypes = (x.dtype, W.dtype)  # the gradients' dtypes
         ctx.b_dtype = None if b is None else b.dtype
-        if torch.is_autocast_enabled("cuda") and x.is_cuda:
+        low = (torch.float32, torch.float16, torch.bfloat16)  # the dtypes autocast casts (fp64 stays as it is)
+        if (torch.is_autocast_enabled("cuda") and x.is_cuda and x.dtype in low and W.dtype in low
+                and (b is None or b.dtype in low)):
             dt = torch.get_autocast_dtype("cuda")
             x, W, b = x.to(dt), W.to(dt), (None if b is None else b.to(dt))
         ctx.save_for_backward(x, W)
