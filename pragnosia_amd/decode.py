@@ -13,8 +13,8 @@ projection kernel (q, k, v, decay and gate or strength in one concatenated weigh
 forms the decay, gate or strength itself and writes the per-head RMS-normalised output, one kernel for the gated
 output projection with the residual, and two for the MLP (LayerNorm + first layer + GELU; second layer + residual):
 five kernels a layer instead of about twenty-five, the same fp32 arithmetic. Above GEMV_MAX_BATCH sequences the dense
-layers run as torch's LayerNorm and GEMMs (matrix cores) and the carrier step stays fused. Other mixers run the
-modules' own T = 1 path. The concatenated weights are copied from the parameters at every `start`, so the graph always sees the
+layers run as the LayerNorm kernel and torch's GEMMs (matrix cores) and the carrier step stays fused. Other mixers
+run the modules' own T = 1 path. The concatenated weights are copied from the parameters at every `start`, so the graph always sees the
 current parameters.
 """
 from __future__ import annotations
@@ -23,6 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from .assoc import AssocCarrier
+from .ops import ln_supported
 
 
 # The fused step's dense layers run as the batched GEMV kernel (each weight read once a step) up to this many
@@ -127,12 +128,17 @@ class GreedyDecoder:
 
     def _dense(self, x, W, ln, bias=None, scale=None, act=0, resid=None):
         """act(scale * (W LayerNorm(x)) + bias) + resid: the batched GEMV kernel up to GEMV_MAX_BATCH sequences,
-        else torch's LayerNorm and GEMM (matrix cores) with the same epilogue."""
+        else the LayerNorm kernel and torch's GEMM (matrix cores) with the same epilogue."""
         if self.B <= GEMV_MAX_BATCH:
             return torch.ops.pragnosia.decode_gemv(x, W, None if ln is None else ln.weight,
                                                    None if ln is None else ln.bias, 0.0 if ln is None else ln.eps,
                                                    bias, scale, act, resid)
-        z = x if ln is None else F.layer_norm(x, (x.shape[-1],), ln.weight, ln.bias, ln.eps)
+        if ln is None:
+            z = x
+        elif ln_supported(x, ln):
+            z = torch.ops.pragnosia.layer_norm(x, ln.weight, ln.bias, ln.eps, False)[0]  # the LayerNorm kernel
+        else:
+            z = F.layer_norm(x, (x.shape[-1],), ln.weight, ln.bias, ln.eps)
         y = F.linear(z, W, bias)
         if act == 1:
             y = F.gelu(y)
