@@ -338,7 +338,8 @@ class AssocCarrier(nn.Module):
 
     def _epilogue(self, o, dtype):
         """`self.on(o.to(dtype)).transpose(1, 2).reshape(B, T, D)` (`src/assoc.py:500-505`) for the scan's bf16 output
-        o (B, H, T, dk): one kernel each way (per-head RMSNorm in fp32, rounded once to `dtype`, written token-major)."""
+        o (B, H, T, dk): one kernel each way (per-head RMSNorm in fp32, rounded once to `dtype`, written
+        token-major)."""
         B, H, T, Dk = o.shape
         if (FUSED_PLUMBING and dtype in (torch.bfloat16, torch.float32) and self.on.weight is not None
                 and Dk == HEAD_DIM_KERNEL):
@@ -351,7 +352,8 @@ class AssocCarrier(nn.Module):
         None. Returns (x + gated output, (S, T) or (S, T, cache)); positions restart at 0 every call and the carried
         state is rebased by -p0 (`src/assoc.py:384-512`)."""
         if self.dk > _op_mod.EXACT_MAX_D:
-            raise PragnosiaError(f"AssocCarrier: head dim {self.dk} is above the {_op_mod.EXACT_MAX_D} the kernels take")
+            raise PragnosiaError(f"AssocCarrier: head dim {self.dk} is above the {_op_mod.EXACT_MAX_D} the kernels "
+                                 "take")
         if not x.is_cuda:
             raise PragnosiaError("AssocCarrier runs on a ROCm GPU only; there is no CPU path")
         B, T, D = x.shape

@@ -14,8 +14,8 @@ forms the decay, gate or strength itself and writes the per-head RMS-normalised 
 output projection with the residual, and two for the MLP (LayerNorm + first layer + GELU; second layer + residual):
 five kernels a layer instead of about twenty-five, the same fp32 arithmetic. Above GEMV_MAX_BATCH sequences the dense
 layers run as the LayerNorm kernel and torch's GEMMs (matrix cores) and the carrier step stays fused. Other mixers
-run the modules' own T = 1 path. The concatenated weights are copied from the parameters at every `start`, so the graph always sees the
-current parameters.
+run the modules' own T = 1 path. The concatenated weights are copied from the parameters at every `start`, so the
+graph always sees the current parameters.
 """
 from __future__ import annotations
 
