@@ -27,7 +27,7 @@ def _inputs(shape, seed):
 
 
 @pytest.mark.parametrize("shape", [(3, 200, 768), (1000, 256), (7, 2048), (1, 1, 1024), (5, 512), (33, 1280),
-                                   (4, 257, 704), (9, 100), (50, 68), (6, 2044)])
+                                   (4, 257, 704), (9, 100), (50, 68), (6, 2044), (37, 4)])
 @pytest.mark.parametrize("dy_bf16", [False, True])
 def test_layer_norm_forward_backward(shape, dy_bf16):
     from pragnosia_amd import ops  # noqa: F401
