@@ -45,19 +45,30 @@ constexpr int TILE = 64 * kPitch;  // one staged 64 x 64 tile
 // dq and dk the sums over the two value halves. Such a sum has two slots, the caller's tensor (slot 0) and a
 // workspace tensor of the same layout (slot 1): o and dv go to slot kh at columns 64 vh, dq and dk to slot vh at
 // columns 64 kh. States (S0, S_final, dS_final, dS0) are the caller's (B, H, 128, 128) arrays: block (kh, vh) at rows
-// 64 kh, columns 64 vh. The entering states `sent` stay per scan, (B, 4H, NC, 64, 64).
-template <bool WIDE>
+// 64 kh, columns 64 vh. The entering states `sent` stay per scan, (B, 4H, NC, 64, 64), at scan index 4 hw + 2 kh + vh.
+//
+// PASS (wide heads, one workgroup per scan): 0 runs all four scans of a head in one launch, the sums through the
+// slots above. 1 and 2 are two launches of two scans per head: launch p = PASS - 1 runs (kh, vh) = (j, j ^ p) at
+// workgroup index 2 hw + j, so within a launch no two scans write the same block of o, dq, dk or dv, and the second
+// launch adds its outputs to the first's (read, add in fp32, round once), so those sums need no slot and no extra
+// pass over the tensors. dla (four terms) keeps two slots there, by kh.
+template <bool WIDE, int PASS = 0>
 struct HeadRows {
+  static_assert(PASS == 0 || WIDE, "two-launch passes are for wide heads");
   static constexpr int ld = WIDE ? 128 : 64;  // row pitch of token-major operands and of states
-  int hw, kh, vh;
+  static constexpr bool kAccumulate = PASS == 2;
+  int hw, kh, vh, scan;
   PGN_DEVICE explicit HeadRows(int bh)
-      : hw(WIDE ? bh >> 2 : bh), kh(WIDE ? (bh >> 1) & 1 : 0), vh(WIDE ? bh & 1 : 0) {}
+      : hw(!WIDE ? bh : PASS ? bh >> 1 : bh >> 2),
+        kh(!WIDE ? 0 : PASS ? bh & 1 : (bh >> 1) & 1),
+        vh(!WIDE ? 0 : PASS ? (bh & 1) ^ (PASS - 1) : bh & 1),
+        scan(!WIDE ? bh : 4 * hw + 2 * kh + vh) {}
   PGN_DEVICE size_t keys(int T) const { return (size_t)hw * T * ld + 64 * kh; }  // q, k, dq, dk
   PGN_DEVICE size_t vals(int T) const { return (size_t)hw * T * ld + 64 * vh; }  // v, dO, o, dv
   PGN_DEVICE size_t state() const { return (size_t)hw * ld * ld + (size_t)64 * kh * ld + 64 * vh; }
   template <class Ptr>
   PGN_DEVICE Ptr slot(Ptr s0, Ptr s1, int which) const {
-    return (WIDE && which) ? s1 : s0;
+    return (WIDE && PASS == 0 && which) ? s1 : s0;
   }
 };
 
@@ -76,7 +87,7 @@ constexpr int kFwdBuf = 3 * TILE * (int)sizeof(__bf16) + 3 * C * (int)sizeof(flo
 
 // S0 is the caller's entering state (head layout, read when there is one segment per head); Sws, when given instead,
 // holds each workgroup's entering state (64 x 64 per workgroup, the segmented forward's workspace).
-template <bool WIDE>
+template <bool WIDE, int PASS>
 __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const float* __restrict__ S0, const float* __restrict__ Sws,
@@ -102,8 +113,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
   const int nseg = (NC + P - 1) / P;
   const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
   const int c0 = sg * P, n = min(P, NC - c0);
-  const HeadRows<WIDE> R(bh);
-  constexpr int ld = HeadRows<WIDE>::ld;
+  using Rows = HeadRows<WIDE, PASS>;
+  const Rows R(bh);
+  constexpr int ld = Rows::ld;
   const size_t koff = R.keys(T), voff = R.vals(T);
 
   // decayed scores A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, of t block a of chunk `cn` (input set hs) into
@@ -161,11 +173,25 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       store_T(STb(0), j0 + 16 * jt, 16 * tb, g, i, S[jt]);
     }
     __bf16* const obase = R.slot(o, o1, R.kh) + voff;
+    // rows past T fall outside the range of a chunk's o rows: stores to them are dropped, loads read zero
+    auto o_rows = [&](int c) {
+      const int t0 = c * C;
+      return __builtin_amdgcn_make_buffer_rsrc(obase + (size_t)t0 * ld, (short)0,
+                                               min(C, T - t0) * ld * (int)sizeof(__bf16), 0x00020000);
+    };
     __syncthreads();
     __syncthreads();
     auto oloop = [&](auto tb_c) {
       constexpr int TB = decltype(tb_c)::value;
       const int tq = 16 * TB + i;  // this lane's token within the chunk for t-indexed operands
+      // accumulating pass: the first launch's o at this lane's outputs, loaded a chunk ahead
+      i32x2 opart[2];
+      auto load_opart = [&](int c) {
+        const __amdgpu_buffer_rsrc_t r = o_rows(c);
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) opart[jt] = load_part4(r, (tq * ld + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16));
+      };
+      if constexpr (Rows::kAccumulate) load_opart(c0);
       for (int lc = 0; lc < n; ++lc) {
         const int c = c0 + lc, h3 = lc % 3, h2 = lc & 1, t0 = c * C;
         FWD_STAMP(4 + 2 * lc);  // the chunk's phase: operand reads, contractions, result stores
@@ -200,8 +226,7 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
         // O^T tiles (value block jt, t block TB) = V^T A^T + eL_t (S^T Q^T); lane holds token tq, 4 value columns,
         // so the state read's decay is one factor on the accumulator. Rows past T fall outside the store's range
         // and are dropped.
-        const __amdgpu_buffer_rsrc_t o_out = __builtin_amdgcn_make_buffer_rsrc(
-            obase + (size_t)t0 * ld, (short)0, min(C, T - t0) * ld * (int)sizeof(__bf16), 0x00020000);
+        const __amdgpu_buffer_rsrc_t o_out = o_rows(c);
 #pragma unroll
         for (int jt = 0; jt < 2; ++jt) {
           f32x4 acc = zero4();
@@ -210,12 +235,14 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
           f32x4 qs = pgn_mfma(sf[jt][0], qf0, zero4());
           qs = pgn_mfma(sf[jt][1], qf1, qs);
           acc += eLt * qs;
+          if constexpr (Rows::kAccumulate) acc += part4(opart[jt]);  // added last: the load is waited for here
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
                                                 (tq * ld + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
         }
+        if constexpr (Rows::kAccumulate) load_opart(c0 + min(lc + 1, n - 1));  // unconditional: exact counter waits
         // the entering state, bf16 (d, j), from this wave's state slice
         if (sent) {
-          __bf16* sc = sent + ((size_t)bh * NC + c) * DK * DK;
+          __bf16* sc = sent + ((size_t)R.scan * NC + c) * DK * DK;
 #pragma unroll
           for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
@@ -525,8 +552,9 @@ __global__ __launch_bounds__(256) void aspin_plain_segprefix(const float* __rest
 constexpr int kVec = 11 * C;
 
 // dla of one chunk from its vector set: dL_t = rowM_t - colM_t + eL_t qz_t - w_t dwv_t, the chunk's last token adds
-// sum_s w_s dwv_s + a <S_c, dS>, and dla is the reverse inclusive cumulative sum of dL. One wave, lane = t.
-PGN_DEVICE void plain_dla(const float* vs, int lane, __amdgpu_buffer_rsrc_t out) {
+// sum_s w_s dwv_s + a <S_c, dS>, and dla is the reverse inclusive cumulative sum of dL (plus `part`, lane t's partial
+// from an earlier launch, when accumulating). One wave, lane = t.
+PGN_DEVICE void plain_dla(const float* vs, int lane, __amdgpu_buffer_rsrc_t out, float part = 0.f) {
   const float* Ls = vs;
   const float* eLs = vs + C;
   const float* ws = vs + 2 * C;
@@ -541,7 +569,7 @@ PGN_DEVICE void plain_dla(const float* vs, int lane, __amdgpu_buffer_rsrc_t out)
   const float wdw = wave_sum(wd);
   const float sd = wave_sum((sdot[t] + sdot[C + t]) + (sdot[2 * C + t] + sdot[3 * C + t]));
   if (t == C - 1) dL += wdw + exp2_hw(Ls[C - 1]) * sd;
-  dL = wave_suffix_sum(dL, t);
+  dL = wave_suffix_sum(dL, t) + part;
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, dL), out, 4 * t, 0, 0);
 }
 
@@ -560,7 +588,7 @@ constexpr int kBwdStage = 5 * TILE;  // Q, K, V, dO, S_c
 // dSfin is the caller's gradient on the final state (head layout, read when there is one segment per head); dSws,
 // when given instead, holds the gradient on the state each workgroup's segment leaves (64 x 64 per workgroup, the
 // segmented backward's workspace). Wide heads: dla of scan 4 hw + s goes to dla (s = 0) or to dla1 slot s - 1.
-template <bool WIDE>
+template <bool WIDE, int PASS>
 __global__ __launch_bounds__(512) void aspin_plain_bwd(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const __bf16* __restrict__ sent, const __bf16* __restrict__ dO,
@@ -582,11 +610,19 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   const int nseg = (NC + P - 1) / P;
   const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
   const int c0 = sg * P, cl = min(c0 + P, NC) - 1;
-  const HeadRows<WIDE> R(bh);
-  constexpr int ld = HeadRows<WIDE>::ld;
+  using Rows = HeadRows<WIDE, PASS>;
+  const Rows R(bh);
+  constexpr int ld = Rows::ld;
   const size_t koff = R.keys(T), voff = R.vals(T);
-  const int nwide = (int)(gridDim.x / nseg) >> 2;  // wide heads in the launch
-  float* const dlar = (WIDE && (bh & 3)) ? dla1 + ((size_t)((bh & 3) - 1) * nwide + R.hw) * T : dla + (size_t)R.hw * T;
+  // dla slots: narrow heads one; wide heads in one launch four (slot s = bh & 3: dla, then dla1 s - 1 of nwide heads
+  // each); in two launches two (slot kh)
+  float* dlar = dla + (size_t)R.hw * T;
+  if constexpr (WIDE && PASS == 0) {
+    const int nwide = (int)(gridDim.x / nseg) >> 2;  // wide heads in the launch
+    if (bh & 3) dlar = dla1 + ((size_t)((bh & 3) - 1) * nwide + R.hw) * T;
+  } else if constexpr (WIDE) {
+    if (R.kh) dlar = dla1 + (size_t)R.hw * T;
+  }
 
   // The two groups run separate loops (the branch is on a wave-uniform value) that meet at the same barriers: each
   // loop's registers and memory-counter waits are then its own.
@@ -613,11 +649,38 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         put_seg(Qs + TILE, sk[n], b2 + 128 * n);
       }
     };
+    // this chunk's rows of dV and dK: stores to rows past T fall outside the range and are dropped (loads read zero)
+    auto out_rows = [&](__bf16* base, int cc) {
+      const int t0 = cc * C;
+      return __builtin_amdgcn_make_buffer_rsrc(base + (size_t)t0 * ld, (short)0,
+                                               min(C, T - t0) * ld * (int)sizeof(__bf16), 0x00020000);
+    };
+    __bf16* const dv_base = R.slot(dv, dv1, R.kh) + voff;
+    __bf16* const dk_base = R.slot(dk, dk1, R.vh) + koff;
+    // accumulating pass: the first launch's dV and dK at this lane's outputs (s = 16 wl + i), loaded a chunk ahead.
+    // Issued in the order the loop issues them, before the next chunk's staging loads, so that the loop's memory
+    // counter waits for them stay exact on its first iteration too.
+    const int me_k = 16 * wl + i;
+    i32x2 dvp[4], dkp[4];
+    auto load_dvp = [&](int cc) {
+      const __amdgpu_buffer_rsrc_t r = out_rows(dv_base, cc);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) dvp[jt] = load_part4(r, (me_k * ld + 16 * jt + 4 * g) * (int)sizeof(__bf16));
+    };
+    auto load_dkp = [&](int cc) {
+      const __amdgpu_buffer_rsrc_t r = out_rows(dk_base, cc);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) dkp[dt] = load_part4(r, (me_k * ld + 16 * dt + 4 * g) * (int)sizeof(__bf16));
+    };
     if (kstage) {
       load(cl);
       stage(cl & 1);
-      if (cl > c0) load(cl - 1);
     }
+    if constexpr (Rows::kAccumulate) {
+      load_dvp(cl);
+      load_dkp(cl);
+    }
+    if (kstage) load(max(cl - 1, c0));
     __syncthreads();
     auto kloop = [&](auto wl_c) {
       constexpr int WL = decltype(wl_c)::value;
@@ -635,12 +698,9 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         const float* ws = vs + 2 * C;
         float* colM = vs + 4 * C;  // column sums of dA o A
         float* dwv = vs + 6 * C;   // k_s . (dS v_s)
-        // this chunk's rows of dV and dK: stores to rows past T fall outside the range and are dropped
-        const int out_bytes = min(C, T - t0) * ld * (int)sizeof(__bf16);
-        const __amdgpu_buffer_rsrc_t dv_out = __builtin_amdgcn_make_buffer_rsrc(
-            R.slot(dv, dv1, R.kh) + voff + (size_t)t0 * ld, (short)0, out_bytes, 0x00020000);
-        const __amdgpu_buffer_rsrc_t dk_out = __builtin_amdgcn_make_buffer_rsrc(
-            R.slot(dk, dk1, R.vh) + koff + (size_t)t0 * ld, (short)0, out_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t dv_out = out_rows(dv_base, cc);
+        const __amdgpu_buffer_rsrc_t dk_out = out_rows(dk_base, cc);
+        const int cn = max(cc - 1, c0);  // the next chunk walked (unconditional loads: exact counter waits)
         const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
         const bf16x8 vf0 = frag(Vs, me, 0, g), vf1 = frag(Vs, me, 1, g);
         const float Ls_s = Ls[me], w_s = ws[me];
@@ -718,8 +778,10 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
             acc2 = pgn_mfma(fr[s].c, kf0, acc2);
             acc2 = pgn_mfma(fr[s].d, kf1, acc2);
             acc = acc + acc2 * w_s;
+            if constexpr (Rows::kAccumulate) acc += part4(dvp[jt]);  // added last: the load is waited for here
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dv_out,
                                                   (me * ld + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+            if constexpr (Rows::kAccumulate && jt == 3) load_dvp(cn);
           } else {
             // dK^T tile (d block dt, s block WL) = Q^T dP + w_s (dS V^T); k_s.(dS v_s) on the way
             constexpr int dt = s - NA - 4;
@@ -732,18 +794,21 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 #pragma unroll
             for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
             acc = acc + Y * w_s;
+            if constexpr (Rows::kAccumulate) acc += part4(dkp[dt]);
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dk_out,
                                                   (me * ld + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
             if constexpr (s == NS - 1) {
               dw = sum_groups(dw);
               if (g == 0) dwv[me] = dw;
+              if constexpr (Rows::kAccumulate) load_dkp(cn);
             }
           }
         });
         BWD_STAMP(5 + 2 * cc);
-        if (WL >= 2 && cc > c0) {
-          stage(h ^ 1);
-          if (cc > c0 + 1) load(cc - 2);
+        if constexpr (WL >= 2) {
+          if (cc > c0) stage(h ^ 1);
+          // unconditional (the last ones re-read a staged chunk, unused), so the loops' counter waits stay exact
+          load(max(cc - 2, c0));
         }
         __syncthreads();
       }
@@ -777,8 +842,8 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       sv1 = load_seg(v + voff + (size_t)n0 * ld, nr, b + 256, ld);
       so0 = load_seg(dO + voff + (size_t)n0 * ld, nr, b, ld);
       so1 = load_seg(dO + voff + (size_t)n0 * ld, nr, b + 256, ld);
-      ss0 = load_seg(sent + ((size_t)bh * NC + cn) * DK * DK, DK, b);
-      ss1 = load_seg(sent + ((size_t)bh * NC + cn) * DK * DK, DK, b + 256);
+      ss0 = load_seg(sent + ((size_t)R.scan * NC + cn) * DK * DK, DK, b);
+      ss1 = load_seg(sent + ((size_t)R.scan * NC + cn) * DK * DK, DK, b + 256);
       if (w == 0) pla = (n0 + x.l < T) ? la[(size_t)R.hw * T + n0 + x.l] : 0.f;
     };
     auto stage = [&](int h) {
@@ -791,14 +856,42 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       put_seg(Qs + 4 * TILE, ss1, b + 256);
       if (w == 0) plain_scan(pla, x.l, vec + h * kVec);
     };
+    // accumulating pass: the first launch's dQ at this lane's outputs (t = 16 wl + i), loaded a chunk ahead and
+    // issued, as in the loop, before the next chunk's staging loads (exact counter waits from the first iteration)
+    __bf16* const dq_base = R.slot(dq, dq1, R.vh) + koff;
+    auto dq_rows = [&](int cc) {
+      const int t0 = cc * C;
+      return __builtin_amdgcn_make_buffer_rsrc(dq_base + (size_t)t0 * ld, (short)0,
+                                               min(C, T - t0) * ld * (int)sizeof(__bf16), 0x00020000);
+    };
+    const int me_d = 16 * wl + i;
+    i32x2 dqp[4];
+    auto load_dqp = [&](int cc) {
+      const __amdgpu_buffer_rsrc_t r = dq_rows(cc);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) dqp[dt] = load_part4(r, (me_d * ld + 16 * dt + 4 * g) * (int)sizeof(__bf16));
+    };
     load(cl);
     stage(cl & 1);
-    if (cl > c0) load(cl - 1);
+    if constexpr (Rows::kAccumulate) load_dqp(cl);
+    load(max(cl - 1, c0));
     __syncthreads();
+    // this chunk's dla: stores to rows past T fall outside the range and are dropped (loads read zero)
+    auto dla_rows = [&](int cc) {
+      const int t0 = cc * C;
+      return __builtin_amdgcn_make_buffer_rsrc(dlar + t0, (short)0, 4 * min(C, T - t0), 0x00020000);
+    };
+    // accumulating pass, wave 0: the first launch's dla of the chunk whose dla is pending
+    float dlap = 0.f;
     auto dloop = [&](auto wl_c) {
       constexpr int WL = decltype(wl_c)::value;
       const int me = 16 * WL + i;
       for (int cc = cl; cc >= c0; --cc) {
+        // wave 0: this chunk's dla partial, used when its dla is written after the next chunk's phase
+        float dlap_next = 0.f;
+        if constexpr (Rows::kAccumulate && WL == 0)
+          dlap_next = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(dla_rows(cc), 4 * x.l, 0, 0));
         BWD_STAMP(4 + 2 * cc);  // the chunk's phase: operand reads, contractions, result stores
         const int t0 = cc * C, h = cc & 1;
         const __bf16* Qs = stg + h * kBwdStage;
@@ -812,10 +905,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         float* rowM = vs + 3 * C;  // row sums of dA o A
         float* qz = vs + 5 * C;    // q_t . (S_c dO_t)
         float* sdot = vs + 7 * C;  // per-lane partial sums of <S_c, dS>, summed in the dla
-        // this chunk's rows of dQ: stores to rows past T fall outside the range and are dropped
-        const __amdgpu_buffer_rsrc_t dq_out =
-            __builtin_amdgcn_make_buffer_rsrc(R.slot(dq, dq1, R.vh) + koff + (size_t)t0 * ld, (short)0,
-                                              min(C, T - t0) * ld * (int)sizeof(__bf16), 0x00020000);
+        const __amdgpu_buffer_rsrc_t dq_out = dq_rows(cc);
         const bf16x8 qf0 = frag(Qs, me, 0, g), qf1 = frag(Qs, me, 1, g);
         const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
         const float Lt = Ls[me], eLt = eLs[me], LC = Ls[C - 1];
@@ -905,9 +995,11 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
 #pragma unroll
             for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
             acc = acc + Z * eLt;
+            if constexpr (Rows::kAccumulate) acc += part4(dqp[dt]);
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), dq_out,
                                                   (me * ld + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
             if constexpr (s == NA + 3) {
+              if constexpr (Rows::kAccumulate) load_dqp(max(cc - 1, c0));  // unconditional: exact counter waits
               qzt = sum_groups(qzt);
               if (g == 0) qz[me] = qzt;
               a_c = exp2_hw(LC);
@@ -929,15 +1021,11 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
           }
         });
         BWD_STAMP(5 + 2 * cc);
-        if (w == 0 && cc < cl) {  // the later chunk's dla, from the other vector set (before the scan below)
-          const int tn = t0 + C;
-          plain_dla(vec + (h ^ 1) * kVec, x.l,
-                    __builtin_amdgcn_make_buffer_rsrc(dlar + tn, (short)0, 4 * min(C, T - tn), 0x00020000));
-        }
-        if (cc > c0) {
-          stage(h ^ 1);
-          if (cc > c0 + 1) load(cc - 2);
-        }
+        if (w == 0 && cc < cl)  // the later chunk's dla, from the other vector set (before the scan below)
+          plain_dla(vec + (h ^ 1) * kVec, x.l, dla_rows(cc + 1), dlap);
+        dlap = dlap_next;
+        if (cc > c0) stage(h ^ 1);
+        load(max(cc - 2, c0));  // unconditional (the last ones re-read a staged chunk, unused): exact counter waits
         __syncthreads();
       }
     };
@@ -948,8 +1036,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       default: dloop(std::integral_constant<int, 3>{}); break;
     }
     if (w == 0)  // the first chunk's dla (its vector set)
-      plain_dla(vec + (c0 & 1) * kVec, x.l,
-                __builtin_amdgcn_make_buffer_rsrc(dlar + c0 * C, (short)0, 4 * min(C, T - c0 * C), 0x00020000));
+      plain_dla(vec + (c0 & 1) * kVec, x.l, dla_rows(c0), dlap);
     if (dS0) {
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt)
@@ -988,24 +1075,25 @@ int64_t seg_bytes(int64_t scans, int64_t T, int64_t seg_chunks) {
   return n * DK * DK * (int64_t)sizeof(float) + align256(n * (int64_t)sizeof(float));
 }
 
-// The plain forward over `scans` scans (B H narrow heads, 4 B H wide): one workgroup per scan when seg_chunks covers
-// the sequence, else the segmented forward's three launches on `ws` (seg_bytes(scans, T, seg_chunks) bytes). theta,
-// window: the carried windows (narrow heads only; H indexes theta).
-template <bool WIDE>
+// The plain forward over `scans` scans (B H narrow heads; wide: 4 B H at PASS 0, 2 B H at PASS 1, 2): one workgroup
+// per scan when seg_chunks covers the sequence, else (PASS 0) the segmented forward's three launches on `ws`
+// (seg_bytes(scans, T, seg_chunks) bytes). theta, window: the carried windows (narrow heads only; H indexes theta).
+template <bool WIDE, int PASS = 0>
 int launch_fwd(const void* q, const void* k, const void* v, const float* la, const float* S0, const float* theta,
                int64_t window, void* o, void* o1, float* S_final, void* sent, void* ws, int64_t scans, int64_t H,
                int64_t T, int64_t seg_chunks, hipStream_t stream) {
   {
-    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_fwd<WIDE>, kFwdSmem);
+    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_fwd<WIDE, PASS>, kFwdSmem);
     if (e != hipSuccess) return (int)e;
   }
   const int NC = (int)((T + C - 1) / C);
   if (seg_chunks >= NC) {
-    hipLaunchKernelGGL(aspin_plain_fwd<WIDE>, dim3((unsigned)scans), dim3(kFwdWaves * 64), kFwdSmem, stream,
+    hipLaunchKernelGGL((aspin_plain_fwd<WIDE, PASS>), dim3((unsigned)scans), dim3(kFwdWaves * 64), kFwdSmem, stream,
                        (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, S0, nullptr, (__bf16*)o,
                        (__bf16*)o1, S_final, (__bf16*)sent, (int)T, NC, NC);
     PGN_RETURN_LAUNCH();
   }
+  if constexpr (PASS != 0) return PRAGNOSIA_ERR_INVALID_ARGUMENT;  // the two-launch passes are unsegmented
   const int64_t nseg = seg_count(T, seg_chunks);
   float* E = (float*)ws;
   float* lseg = E + scans * nseg * DK * DK;
@@ -1015,29 +1103,30 @@ int launch_fwd(const void* q, const void* k, const void* v, const float* la, con
   hipLaunchKernelGGL((aspin_plain_segprefix<false, WIDE>), dim3((unsigned)(scans * 8)), dim3(256), 0, stream, S0,
                      window > 0 ? theta : nullptr, (float)window, window > 0 ? (int)(window / C / seg_chunks) : 1, E,
                      lseg, S_final, (int)H, (int)nseg);
-  hipLaunchKernelGGL(aspin_plain_fwd<WIDE>, dim3(nblk), dim3(kFwdWaves * 64), kFwdSmem, stream, (const __bf16*)q,
+  hipLaunchKernelGGL((aspin_plain_fwd<WIDE, 0>), dim3(nblk), dim3(kFwdWaves * 64), kFwdSmem, stream, (const __bf16*)q,
                      (const __bf16*)k, (const __bf16*)v, la, nullptr, E, (__bf16*)o, (__bf16*)o1, nullptr,
                      (__bf16*)sent, (int)T, NC, (int)seg_chunks);
   PGN_RETURN_LAUNCH();
 }
 
-// The plain backward over `scans` scans, one workgroup per scan or segmented as the forward.
-template <bool WIDE>
+// The plain backward over `scans` scans, one workgroup per scan or (PASS 0) segmented as the forward.
+template <bool WIDE, int PASS = 0>
 int launch_bwd(const void* q, const void* k, const void* v, const float* la, const void* sent, const void* dO,
                const float* dS_final, void* dq, void* dq1, void* dk, void* dk1, void* dv, void* dv1, float* dla,
                float* dla1, float* dS0, void* ws, int64_t scans, int64_t T, int64_t seg_chunks, hipStream_t stream) {
   {
-    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_bwd<WIDE>, kBwdSmem);
+    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_bwd<WIDE, PASS>, kBwdSmem);
     if (e != hipSuccess) return (int)e;
   }
   const int NC = (int)((T + C - 1) / C);
   if (seg_chunks >= NC) {
-    hipLaunchKernelGGL(aspin_plain_bwd<WIDE>, dim3((unsigned)scans), dim3(512), kBwdSmem, stream, (const __bf16*)q,
+    hipLaunchKernelGGL((aspin_plain_bwd<WIDE, PASS>), dim3((unsigned)scans), dim3(512), kBwdSmem, stream, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent, (const __bf16*)dO, dS_final,
                        nullptr, (__bf16*)dq, (__bf16*)dq1, (__bf16*)dk, (__bf16*)dk1, (__bf16*)dv, (__bf16*)dv1, dla,
                        dla1, dS0, (int)T, NC, NC);
     PGN_RETURN_LAUNCH();
   }
+  if constexpr (PASS != 0) return PRAGNOSIA_ERR_INVALID_ARGUMENT;  // the two-launch passes are unsegmented
   const int64_t nseg = seg_count(T, seg_chunks);
   float* F = (float*)ws;
   float* lseg = F + scans * nseg * DK * DK;
@@ -1046,7 +1135,7 @@ int launch_bwd(const void* q, const void* k, const void* v, const float* la, con
                      (const __bf16*)dO, la, F, lseg, (int)T, NC, (int)seg_chunks);
   hipLaunchKernelGGL((aspin_plain_segprefix<true, WIDE>), dim3((unsigned)(scans * 8)), dim3(256), 0, stream, dS_final,
                      nullptr, 0.f, 1, F, lseg, dS0, 1, (int)nseg);
-  hipLaunchKernelGGL(aspin_plain_bwd<WIDE>, dim3(nblk), dim3(512), kBwdSmem, stream, (const __bf16*)q,
+  hipLaunchKernelGGL((aspin_plain_bwd<WIDE, 0>), dim3(nblk), dim3(512), kBwdSmem, stream, (const __bf16*)q,
                      (const __bf16*)k, (const __bf16*)v, la, (const __bf16*)sent, (const __bf16*)dO, nullptr, F,
                      (__bf16*)dq, (__bf16*)dq1, (__bf16*)dk, (__bf16*)dk1, (__bf16*)dv, (__bf16*)dv1, dla, dla1,
                      nullptr, (int)T, NC, (int)seg_chunks);
@@ -1055,14 +1144,15 @@ int launch_bwd(const void* q, const void* k, const void* v, const float* la, con
 
 // The slot sums of the wide entry points: for each bf16 pair p with x[p] set, x[p][i] <- x[p][i] + y[p][i] over n
 // elements (the fp32 sum of the two bf16 values rounded once to bf16, as a bf16 tensor add rounds), and, when dla is
-// set, dla[i] <- ((dla[i] + w[i]) + w[m + i]) + w[2 m + i] over m fp32 elements. Thread u covers elements
-// 8u .. 8u + 7 of every pair (n % 8 == 0) and fp32 element u (m <= n / 8).
+// set, dla[i] <- (dla[i] + w[i]) + w[m + i] ... over the nw slots of w (m fp32 elements each). Thread u covers
+// elements 8u .. 8u + 7 of every pair (n % 8 == 0) and fp32 element u (m <= n / 8).
 struct JoinArgs {
   __bf16* x[3];
   const __bf16* y[3];
   float* dla;
   const float* w;
   int64_t n, m;
+  int nw;
 };
 
 __global__ __launch_bounds__(256) void aspin_wide_join(JoinArgs a) {
@@ -1083,11 +1173,15 @@ __global__ __launch_bounds__(256) void aspin_wide_join(JoinArgs a) {
         *reinterpret_cast<bf16x8*>(a.x[p] + 8 * u) = xs[p];
       }
   }
-  if (a.dla && u < a.m) a.dla[u] = ((a.dla[u] + a.w[u]) + a.w[a.m + u]) + a.w[2 * a.m + u];
+  if (a.dla && u < a.m) {
+    float d = a.dla[u];
+    for (int j = 0; j < a.nw; ++j) d += a.w[j * a.m + u];
+    a.dla[u] = d;
+  }
 }
 
 int launch_join(const JoinArgs& a, hipStream_t stream) {
-  const int64_t units = a.n / 8;
+  const int64_t units = std::max(a.n / 8, a.m);
   hipLaunchKernelGGL(aspin_wide_join, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, stream, a);
   PGN_RETURN_LAUNCH();
 }
@@ -1245,6 +1339,14 @@ extern "C" int pragnosia_aspin_chunk_fwd_wide(const void* q, const void* k, cons
   PGN_CHECK_ARG(q && k && v && la && o && S_final && workspace);
   PGN_CHECK_ARG(workspace_bytes >= wide_workspace_bytes(B, H, T, seg_chunks, false));
   char* ws = (char*)workspace;
+  if (seg_chunks >= (T + C - 1) / C) {
+    // two launches of two scans per head, the second adding its o to the first's
+    int rc = launch_fwd<true, 1>(q, k, v, la, S0, nullptr, 0, o, nullptr, S_final, sent, nullptr, 2 * B * H, 4 * H, T,
+                                 seg_chunks, (hipStream_t)stream);
+    if (rc != PRAGNOSIA_OK) return rc;
+    return launch_fwd<true, 2>(q, k, v, la, S0, nullptr, 0, o, nullptr, S_final, sent, nullptr, 2 * B * H, 4 * H, T,
+                               seg_chunks, (hipStream_t)stream);
+  }
   void* o1 = ws;
   const int rc = launch_fwd<true>(q, k, v, la, S0, nullptr, 0, o, o1, S_final, sent, ws + wide_slot_bytes(B, H, T),
                                   4 * B * H, 4 * H, T, seg_chunks, (hipStream_t)stream);
@@ -1269,6 +1371,21 @@ extern "C" int pragnosia_aspin_chunk_bwd_wide(const void* q, const void* k, cons
   const int64_t slot = wide_slot_bytes(B, H, T);
   void *dq1 = ws, *dk1 = ws + slot, *dv1 = ws + 2 * slot;
   float* dla1 = (float*)(ws + 3 * slot);
+  if (seg_chunks >= (T + C - 1) / C) {
+    // two launches of two scans per head, the second adding its dq, dk, dv to the first's; dla from two slots
+    int rc = launch_bwd<true, 1>(q, k, v, la, sent, dO, dS_final, dq, nullptr, dk, nullptr, dv, nullptr, dla, dla1,
+                                 dS0, nullptr, 2 * B * H, T, seg_chunks, (hipStream_t)stream);
+    if (rc != PRAGNOSIA_OK) return rc;
+    rc = launch_bwd<true, 2>(q, k, v, la, sent, dO, dS_final, dq, nullptr, dk, nullptr, dv, nullptr, dla, dla1, dS0,
+                             nullptr, 2 * B * H, T, seg_chunks, (hipStream_t)stream);
+    if (rc != PRAGNOSIA_OK) return rc;
+    JoinArgs a = {};
+    a.dla = dla;
+    a.w = dla1;
+    a.m = B * H * T;
+    a.nw = 1;
+    return launch_join(a, (hipStream_t)stream);
+  }
   void* segws = ws + 3 * slot + align256(3 * B * H * T * (int64_t)sizeof(float));
   const int rc = launch_bwd<true>(q, k, v, la, sent, dO, dS_final, dq, dq1, dk, dk1, dv, dv1, dla, dla1, dS0, segws,
                                   4 * B * H, T, seg_chunks, (hipStream_t)stream);
@@ -1284,5 +1401,6 @@ extern "C" int pragnosia_aspin_chunk_bwd_wide(const void* q, const void* k, cons
   a.w = dla1;
   a.n = B * H * T * 2 * DK;
   a.m = B * H * T;
+  a.nw = 3;
   return launch_join(a, (hipStream_t)stream);
 }

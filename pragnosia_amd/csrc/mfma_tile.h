@@ -243,17 +243,23 @@ PGN_DEVICE void put_blk_T(__bf16* tile, const Blk4& x, int r0, int c0) {
 
 // Staging of row-major 64-column bf16 tiles in 16-byte row segments, for tiles that are only ever read untransposed
 // or through frag_tr: segment e covers row e / 8, columns 8 (e % 8) .. +7, so one 64-lane load reads eight whole
-// 128-byte rows. Rows >= nrows (>= 1) read as zero (the load itself is clamped to row nrows - 1, unconditional).
-// `ld` is the source's row pitch in elements (64 for a dense tile; 128 for one half of rows of 128).
+// 128-byte rows. Rows >= nrows (0 <= nrows <= 64) read as zero: the load goes through a buffer resource whose range
+// ends after row nrows - 1, so it needs no branch (with a select on the row instead, the compiler sinks each load
+// into a branch, and the memory-counter waits of the loops around it turn conservative). `ld` is the source's row
+// pitch in elements (64 for a dense tile; 128 for one half of rows of 128).
 PGN_DEVICE bf16x8 load_seg(const __bf16* __restrict__ src, int nrows, int e, int ld = 64) {
-  const int r = e >> 3;
-  const bf16x8 v = *reinterpret_cast<const bf16x8*>(src + (size_t)min(r, nrows - 1) * ld + 8 * (e & 7));
-  if (r < nrows) return v;
-  bf16x8 z;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) z[j] = (__bf16)0.f;
-  return z;
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(src), (short)0,
+                                                                     nrows * ld * (int)sizeof(__bf16), 0x00020000);
+  return __builtin_bit_cast(
+      bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, ((e >> 3) * ld + 8 * (e & 7)) * (int)sizeof(__bf16), 0, 0));
 }
+
+// Four bf16 at byte offset `off` of a range-checked buffer (zero past the range), kept packed until used: the partial
+// result that an accumulating store adds to (part4 widens it to fp32).
+PGN_DEVICE i32x2 load_part4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+PGN_DEVICE f32x4 part4(i32x2 v) { return to_f32x4(__builtin_bit_cast(bf16x4, v)); }
 
 // The segment into an LDS tile (pitch kPitch, so rows are 8-byte aligned: two 8-byte writes).
 PGN_DEVICE void put_seg(__bf16* tile, bf16x8 v, int e) {
