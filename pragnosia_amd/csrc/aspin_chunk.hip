@@ -680,7 +680,6 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       load_dvp(cl);
       load_dkp(cl);
     }
-    if (kstage) load(max(cl - 1, c0));
     __syncthreads();
     auto kloop = [&](auto wl_c) {
       constexpr int WL = decltype(wl_c)::value;
@@ -701,6 +700,10 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         const __amdgpu_buffer_rsrc_t dv_out = out_rows(dv_base, cc);
         const __amdgpu_buffer_rsrc_t dk_out = out_rows(dk_base, cc);
         const int cn = max(cc - 1, c0);  // the next chunk walked (unconditional loads: exact counter waits)
+        // the next chunk's Q and K, staged after this chunk's phase: loaded and staged within one iteration, so no
+        // loaded register is carried around the loop (a carried one is copied at the loop's end, which waits for
+        // the load)
+        if constexpr (WL >= 2) load(cn);
         const bf16x8 kf0 = frag(Ks, me, 0, g), kf1 = frag(Ks, me, 1, g);
         const bf16x8 vf0 = frag(Vs, me, 0, g), vf1 = frag(Vs, me, 1, g);
         const float Ls_s = Ls[me], w_s = ws[me];
@@ -807,8 +810,6 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         BWD_STAMP(5 + 2 * cc);
         if constexpr (WL >= 2) {
           if (cc > c0) stage(h ^ 1);
-          // unconditional (the last ones re-read a staged chunk, unused), so the loops' counter waits stay exact
-          load(max(cc - 2, c0));
         }
         __syncthreads();
       }
@@ -874,7 +875,6 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
     load(cl);
     stage(cl & 1);
     if constexpr (Rows::kAccumulate) load_dqp(cl);
-    load(max(cl - 1, c0));
     __syncthreads();
     // this chunk's dla: stores to rows past T fall outside the range and are dropped (loads read zero)
     auto dla_rows = [&](int cc) {
@@ -887,6 +887,10 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       constexpr int WL = decltype(wl_c)::value;
       const int me = 16 * WL + i;
       for (int cc = cl; cc >= c0; --cc) {
+        // the next chunk's V, dO and S_c, staged after this chunk's phase: loaded and staged within one iteration,
+        // so no loaded register is carried around the loop (a carried one is copied at the loop's end, which waits
+        // for the load). Unconditional: the last iteration re-reads this chunk, unused.
+        load(max(cc - 1, c0));
         // wave 0: this chunk's dla partial, used when its dla is written after the next chunk's phase
         float dlap_next = 0.f;
         if constexpr (Rows::kAccumulate && WL == 0)
@@ -1025,7 +1029,6 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
           plain_dla(vec + (h ^ 1) * kVec, x.l, dla_rows(cc + 1), dlap);
         dlap = dlap_next;
         if (cc > c0) stage(h ^ 1);
-        load(max(cc - 2, c0));  // unconditional (the last ones re-read a staged chunk, unused): exact counter waits
         __syncthreads();
       }
     };
