@@ -280,9 +280,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     // ================= score waves: t block a, one chunk ahead. Wave 8 also runs the decay scans, two chunks ahead
     // (the load waves stage the same chunk's tiles in the same phase): L (base 2), e^L and w = exp(L_C - L).
     const bool scan = w == 8;
-    auto la_of = [&](int ln) {  // the segment's chunk ln
-      const int t = (c0 + ln) * C + x.l;
-      return (ln < n && t < T) ? la[(size_t)R.hw * T + t] : 0.f;
+    auto la_of = [&](int ln) {  // the segment's chunk ln (zero past the segment or T): a load with no branch
+      const int n0 = (c0 + ln) * C;
+      return load_f32_lane(la + (size_t)R.hw * T + n0, ln < n ? min(C, T - n0) : 0, x.l);
     };
     auto run_scan = [&](float la_t, int h) {
       const float L = wave_prefix_sum(la_t, x.l);
@@ -293,21 +293,19 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       vs[2 * C + x.l] = __expf(fminf(LC - L, 0.f));
     };
     auto sloop = [&](auto a_c) {
-      float pla = 0.f;
       if (scan) {
         run_scan(la_of(0), 0);
         if (n > 1) run_scan(la_of(1), 1);
-        pla = la_of(2);
       }
       __syncthreads();
       scores(a_c, 0, ATb(0), -1);
       __syncthreads();
       for (int c = 0; c < n; ++c) {
+        // chunk c + 2's decays, loaded before this phase's scores and used after them: not carried around the
+        // loop (a carried load result is copied at the loop's end, which waits for the load)
+        const float la_t = la_of(c + 2);
         if (c + 1 < n) scores(a_c, (c + 1) % 3, ATb((c + 1) & 1), 4 + 2 * c);
-        if (scan && c + 2 < n) {
-          run_scan(pla, (c + 2) % 3);
-          pla = la_of(c + 3);
-        }
+        if (scan && c + 2 < n) run_scan(la_t, (c + 2) % 3);
         __syncthreads();
       }
     };
@@ -343,22 +341,21 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
       put_seg(Vb(h), r.v0, b);
       put_seg(Vb(h), r.v1, b + 256);
     };
+    // Every load is unconditional (chunk indices clamped to the segment's last chunk; the extra loads re-read it,
+    // unused), so the compiler counts the loads in flight exactly and the wait before staging a set covers that set
+    // only, not the other one issued a chunk later.
     load(ra, 0);
     stage(ra, 0);
-    if (n > 1) {
-      load(rb, 1);
-      stage(rb, 1);
-      if (n > 2) load(ra, 2);
-      if (n > 3) load(rb, 3);
-    }
+    load(rb, min(1, n - 1));
+    if (n > 1) stage(rb, 1);
+    load(ra, min(2, n - 1));
+    load(rb, min(3, n - 1));
     __syncthreads();
     __syncthreads();
     // chunk c: stage chunk c + 2 from the set loaded two chunks ago, then reload that set with chunk c + 4
     auto phase = [&](Regs& r, int c) {
-      if (c + 2 < n) {
-        stage(r, (c + 2) % 3);
-        if (c + 4 < n) load(r, c + 4);
-      }
+      if (c + 2 < n) stage(r, (c + 2) % 3);
+      load(r, min(c + 4, n - 1));
       __syncthreads();
     };
     for (int c = 0; c < n; c += 2) {
@@ -415,7 +412,7 @@ __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restri
     k1 = load_seg(k + koff + (size_t)n0 * ld, nr, b + 256, ld);
     v0 = load_seg(v + voff + (size_t)n0 * ld, nr, b, ld);
     v1 = load_seg(v + voff + (size_t)n0 * ld, nr, b + 256, ld);
-    if (w == 0) lat = x.l < nr ? la[(size_t)R.hw * T + n0 + x.l] : 0.f;
+    lat = load_f32_lane(la + (size_t)R.hw * T + n0, nr, x.l);  // every wave (wave 0 uses it): no branch
   };
   // wave 0: total log-decay of the segment's chunks already staged (after the next one when walking to the end,
   // before it when walking from the start)
@@ -439,7 +436,7 @@ __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restri
   for (int jb = 0; jb < 4; ++jb) acc[jb] = zero4();
   load(chunk_at(0));
   stage(0);
-  if (n > 1) load(chunk_at(1));
+  load(chunk_at(min(1, n - 1)));  // unconditional (clamped; an extra load re-reads a chunk, unused)
   __syncthreads();
   for (int it = 0; it < n; ++it) {
     const int h = it & 1;
@@ -464,10 +461,8 @@ __global__ __launch_bounds__(256) void aspin_plain_segsum(const __bf16* __restri
       acc[jb] = pgn_mfma(kw0, vf[jb][0], acc[jb]);
       acc[jb] = pgn_mfma(kw1, vf[jb][1], acc[jb]);
     }
-    if (it + 1 < n) {
-      stage(h ^ 1);
-      if (it + 2 < n) load(chunk_at(it + 2));
-    }
+    if (it + 1 < n) stage(h ^ 1);
+    load(chunk_at(min(it + 2, n - 1)));
     __syncthreads();
   }
   float* e = E + (size_t)blockIdx.x * DK * DK;
@@ -845,7 +840,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       so1 = load_seg(dO + voff + (size_t)n0 * ld, nr, b + 256, ld);
       ss0 = load_seg(sent + ((size_t)R.scan * NC + cn) * DK * DK, DK, b);
       ss1 = load_seg(sent + ((size_t)R.scan * NC + cn) * DK * DK, DK, b + 256);
-      if (w == 0) pla = (n0 + x.l < T) ? la[(size_t)R.hw * T + n0 + x.l] : 0.f;
+      pla = load_f32_lane(la + (size_t)R.hw * T + n0, nr, x.l);  // every wave (wave 0 uses it): no branch
     };
     auto stage = [&](int h) {
       __bf16* Qs = stg + h * kBwdStage;

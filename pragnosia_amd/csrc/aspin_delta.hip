@@ -415,11 +415,9 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
         sg[u][0] = load_seg(src, rows, b, ld);
         sg[u][1] = load_seg(src, rows, b + 256, ld);
       }
-      if (a == 0) {
-        const bool ok = n0 + x.l < T;
-        pla = ok ? la[R.tok(T) + n0 + x.l] : 0.f;
-        pbe = ok ? be[R.tok(T) + n0 + x.l] : 0.f;
-      }
+      // every service wave loads them (wave 4 uses them): no branch around a load
+      pla = load_f32_lane(la + R.tok(T) + n0, nr, x.l);
+      pbe = load_f32_lane(be + R.tok(T) + n0, nr, x.l);
     };
     auto stage = [&](int hh) {
       __bf16* base = stg + hh * kStage;
@@ -436,7 +434,7 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
     };
     load(0);
     stage(0);
-    if (NC > 1) load(1);
+    load(min(1, NC - 1));
     __syncthreads();
     for (int c = 0; c < NC; ++c) {
       const int h = c & 1;
@@ -473,10 +471,10 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
       }
       DF_STAMP(5 + 2 * c);
       __syncthreads();  // A complete
-      if (c + 1 < NC) {
-        stage(h ^ 1);
-        if (c + 2 < NC) load(c + 2);
-      }
+      // the next chunk's tiles (loaded a chunk ago), then the loads of the one after (unconditional: the last ones
+      // re-read the last chunk, unused)
+      if (c + 1 < NC) stage(h ^ 1);
+      load(min(c + 2, NC - 1));
       __syncthreads();  // end of the chunk
     }
   }
@@ -686,11 +684,9 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
         sg[u][0] = load_seg(src, rows, b, ld);
         sg[u][1] = load_seg(src, rows, b + 256, ld);
       }
-      if (a == 0) {
-        const bool ok = n0 + x.l < T;
-        pla = ok ? la[R.tok(T) + n0 + x.l] : 0.f;
-        pbe = ok ? be[R.tok(T) + n0 + x.l] : 0.f;
-      }
+      // every service wave loads them (wave 4 uses them): no branch around a load
+      pla = load_f32_lane(la + R.tok(T) + n0, nr, x.l);
+      pbe = load_f32_lane(be + R.tok(T) + n0, nr, x.l);
     };
     auto stage = [&](int hh) {
 #pragma unroll
@@ -720,7 +716,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
     };
     load(NC - 1);
     stage((NC - 1) & 1);
-    if (NC > 1) load(NC - 2);
+    load(max(NC - 2, 0));
     __syncthreads();
     for (int cc = NC - 1; cc >= 0; --cc) {
       const int h = cc & 1;
@@ -760,10 +756,10 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
       DB_STAMP(5 + 2 * cc);
       __syncthreads();  // A^T complete
       if (a == 0 && cc < NC - 1) reduce(cc + 1);  // the later chunk's sums, before its vector set is reused below
-      if (cc > 0) {
-        stage(h ^ 1);
-        if (cc > 1) load(cc - 2);
-      }
+      // the next chunk's tiles (loaded a chunk ago), then the loads of the one after (unconditional: the last ones
+      // re-read the first chunk, unused)
+      if (cc > 0) stage(h ^ 1);
+      load(max(cc - 2, 0));
       __syncthreads();  // end of the chunk
     }
     if (a == 0) reduce(0);

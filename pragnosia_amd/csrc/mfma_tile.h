@@ -254,6 +254,14 @@ PGN_DEVICE bf16x8 load_seg(const __bf16* __restrict__ src, int nrows, int e, int
       bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, ((e >> 3) * ld + 8 * (e & 7)) * (int)sizeof(__bf16), 0, 0));
 }
 
+// Element `lane` of an fp32 vector of n elements (0 <= n <= 64; zero at and past n) through a range-checked buffer:
+// no select on the lane, so the load is not sunk into a branch.
+PGN_DEVICE float load_f32_lane(const float* p, int n, int lane) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), (short)0, n * (int)sizeof(float), 0x00020000);
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, lane * (int)sizeof(float), 0, 0));
+}
+
 // Four bf16 at byte offset `off` of a range-checked buffer (zero past the range), kept packed until used: the partial
 // result that an accumulating store adds to (part4 widens it to fp32).
 PGN_DEVICE i32x2 load_part4(__amdgpu_buffer_rsrc_t r, int off) {
