@@ -166,12 +166,14 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     f32x4 S[2];
     const float* s0p = Sws ? Sws + (size_t)blockIdx.x * DK * DK : (S0 ? S0 + R.state() : nullptr);
     const int s0ld = Sws ? DK : ld;
+    // every load first (an empty view when there is no entering state: zeros, no branch), then the LDS writes
+    const __amdgpu_buffer_rsrc_t s0v = f32_view(s0p, DK * s0ld);
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt) {
+    for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) S[jt][r] = s0p ? s0p[(16 * tb + 4 * g + r) * s0ld + j0 + 16 * jt + i] : 0.f;
-      store_T(STb(0), j0 + 16 * jt, 16 * tb, g, i, S[jt]);
-    }
+      for (int r = 0; r < 4; ++r) S[jt][r] = load_f32(s0v, (16 * tb + 4 * g + r) * s0ld + j0 + 16 * jt + i);
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt) store_T(STb(0), j0 + 16 * jt, 16 * tb, g, i, S[jt]);
     __bf16* const obase = R.slot(o, o1, R.kh) + voff;
     // rows past T fall outside the range of a chunk's o rows: stores to them are dropped, loads read zero
     auto o_rows = [&](int c) {
@@ -345,9 +347,9 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
     // unused), so the compiler counts the loads in flight exactly and the wait before staging a set covers that set
     // only, not the other one issued a chunk later.
     load(ra, 0);
+    load(rb, min(1, n - 1));  // both chunks' loads in flight together
     stage(ra, 0);
-    load(rb, min(1, n - 1));
-    if (n > 1) stage(rb, 1);
+    stage(rb, 1);  // unconditional (with one chunk, a copy of it into a set nothing reads): the loads stay issued above
     load(ra, min(2, n - 1));
     load(rb, min(3, n - 1));
     __syncthreads();
@@ -821,12 +823,6 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
     f32x4 dS[4];
     const float* dsp = dSws ? dSws + (size_t)blockIdx.x * DK * DK : (dSfin ? dSfin + R.state() : nullptr);
     const int dsld = dSws ? DK : ld;
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dS[jt][r] = dsp ? dsp[(16 * wl + 4 * g + r) * dsld + 16 * jt + i] : 0.f;
-      store_T(dSTb + (cl & 1) * TILE, 16 * jt, 16 * wl, g, i, dS[jt]);
-    }
     // staging: thread b carries 16-byte row segments b and b + 256 of each of V, dO and S_c (waves 6 and 7 stage
     // Q and K)
     const int b = tid & 255;  // = tid; the mask tells the compiler that every segment row is below 64
@@ -850,7 +846,8 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       put_seg(Qs + 3 * TILE, so1, b + 256);
       put_seg(Qs + 4 * TILE, ss0, b);
       put_seg(Qs + 4 * TILE, ss1, b + 256);
-      if (w == 0) plain_scan(pla, x.l, vec + h * kVec);
+      const float la_t = pin_use(pla);  // (the staging loads have landed by here)
+      if (w == 0) plain_scan(la_t, x.l, vec + h * kVec);
     };
     // accumulating pass: the first launch's dQ at this lane's outputs (t = 16 wl + i), loaded a chunk ahead and
     // issued, as in the loop, before the next chunk's staging loads (exact counter waits from the first iteration)
@@ -868,6 +865,17 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       for (int dt = 0; dt < 4; ++dt) dqp[dt] = load_part4(r, (me_d * ld + 16 * dt + 4 * g) * (int)sizeof(__bf16));
     };
     load(cl);
+    {
+      // the gradient on the state the workgroup's chunks leave, 16 values a lane, loaded after the first chunk's
+      // staging loads so that the two round trips overlap (an empty view when there is none: zeros, no branch)
+      const __amdgpu_buffer_rsrc_t dsv = f32_view(dsp, DK * dsld);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dS[jt][r] = load_f32(dsv, (16 * wl + 4 * g + r) * dsld + 16 * jt + i);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) store_T(dSTb + (cl & 1) * TILE, 16 * jt, 16 * wl, g, i, dS[jt]);
+    }
     stage(cl & 1);
     if constexpr (Rows::kAccumulate) load_dqp(cl);
     __syncthreads();

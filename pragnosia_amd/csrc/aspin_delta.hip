@@ -301,10 +301,14 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
     DF_CLOCKS(0);
     const int j = 16 * w + i;
     f32x4 S[4 * KH];
+    {
+      // all loads at once (an empty view when there is no entering state: zeros, no branch per element)
+      const __amdgpu_buffer_rsrc_t sv = f32_view(S0 ? S0 + R.state() : nullptr, DKEY * DKEY);
 #pragma unroll
-    for (int db = 0; db < 4 * KH; ++db)
+      for (int db = 0; db < 4 * KH; ++db)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) S[db][r] = S0 ? S0[R.state() + (size_t)(16 * db + 4 * g + r) * DKEY + j] : 0.f;
+        for (int r = 0; r < 4; ++r) S[db][r] = load_f32(sv, (16 * db + 4 * g + r) * DKEY + j);
+    }
     __syncthreads();
     for (int c = 0; c < NC; ++c) {
       DF_STAMP(4 + 2 * c);  // the chunk's phase: operand reads, contractions, result stores (across the A barrier)
@@ -532,11 +536,14 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
     DB_CLOCKS(0);
     const int j = 16 * w + i;
     f32x4 dS[4 * KH];
+    {
+      // all loads at once (an empty view when there is no final-state gradient: zeros, no branch per element)
+      const __amdgpu_buffer_rsrc_t dv = f32_view(dSfin ? dSfin + R.state() : nullptr, DKEY * DKEY);
 #pragma unroll
-    for (int db = 0; db < 4 * KH; ++db)
+      for (int db = 0; db < 4 * KH; ++db)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        dS[db][r] = dSfin ? dSfin[R.state() + (size_t)(16 * db + 4 * g + r) * DKEY + j] : 0.f;
+        for (int r = 0; r < 4; ++r) dS[db][r] = load_f32(dv, (16 * db + 4 * g + r) * DKEY + j);
+    }
     __syncthreads();
     for (int cc = NC - 1; cc >= 0; --cc) {
       DB_STAMP(4 + 2 * cc);  // the chunk's phase: operand reads, contractions, result stores (across the A^T barrier)

@@ -254,6 +254,24 @@ PGN_DEVICE bf16x8 load_seg(const __bf16* __restrict__ src, int nrows, int e, int
       bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, ((e >> 3) * ld + 8 * (e & 7)) * (int)sizeof(__bf16), 0, 0));
 }
 
+// The value, used outside any branch: a load whose only use sits inside a branch is sunk into that branch by the
+// compiler (issued there, just before the use, so its latency is exposed); passing it through this where the value
+// is needed anyway keeps the load at its place in the code. Emits no instruction.
+PGN_DEVICE float pin_use(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// A range-checked view of n fp32 elements at p (an empty one when p is null): a load past the range, or from an empty
+// view, reads zero with no branch, so a kernel can issue such loads unconditionally, all before it uses any.
+PGN_DEVICE __amdgpu_buffer_rsrc_t f32_view(const float* p, int n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), (short)0, p ? n * (int)sizeof(float) : 0,
+                                           0x00020000);
+}
+PGN_DEVICE float load_f32(__amdgpu_buffer_rsrc_t r, int i) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, i * (int)sizeof(float), 0, 0));
+}
+
 // Element `lane` of an fp32 vector of n elements (0 <= n <= 64; zero at and past n) through a range-checked buffer:
 // no select on the lane, so the load is not sunk into a branch.
 PGN_DEVICE float load_f32_lane(const float* p, int n, int lane) {
