@@ -159,6 +159,21 @@ __global__ __launch_bounds__(256) void wgrad_tiles(const __bf16* __restrict__ A,
     });
   }
 
+  if (accumulate) {
+    // every earlier value is read before any store, from a clamped (always valid) address with no branch, and
+    // dropped outside the matrix (a read-add-write per element, behind a bounds branch, waits for each load in turn)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int64_t m = m_base + 64 * wm + 16 * a + i;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int64_t n = n_base + 64 * wn + 16 * b + 4 * g;
+        const float4 o = *reinterpret_cast<const float4*>(dst + std::min(m, M - 1) * ldo + std::min(n, N - 4));
+        const float keep = (m < M && n < N) ? 1.f : 0.f;
+        acc[a][b] += f32x4{o.x, o.y, o.z, o.w} * keep;
+      }
+    }
+  }
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     const int64_t m = m_base + 64 * wm + 16 * a + i;
@@ -167,16 +182,8 @@ __global__ __launch_bounds__(256) void wgrad_tiles(const __bf16* __restrict__ A,
     for (int b = 0; b < 4; ++b) {
       const int64_t n = n_base + 64 * wn + 16 * b + 4 * g;
       if (n >= N) continue;
-      float4* p = reinterpret_cast<float4*>(dst + m * ldo + n);
-      float4 v = make_float4(acc[a][b][0], acc[a][b][1], acc[a][b][2], acc[a][b][3]);
-      if (accumulate) {
-        const float4 o = *p;
-        v.x += o.x;
-        v.y += o.y;
-        v.z += o.z;
-        v.w += o.w;
-      }
-      *p = v;
+      *reinterpret_cast<float4*>(dst + m * ldo + n) =
+          make_float4(acc[a][b][0], acc[a][b][1], acc[a][b][2], acc[a][b][3]);
     }
   }
 }
