@@ -445,32 +445,42 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
       const __bf16* Qs = stg + h * kStage;
       const __bf16* Ks = Qs + KH * TILE;
       const float* Ls = vec + h * kFwdVec;
-      // decayed scores for token block a: A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, into As (row t)
+      // decayed scores A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, into As (row t). The ten nonzero 16 x 16
+      // blocks split 2, 3, 3, 2 over the four waves (wave a takes row block a's, and row block 3's first two go to
+      // waves 0 and 1), so the last row block's four do not hold up the A barrier the chain waves wait at; each wave
+      // zeroes its row block above the diagonal.
       DF_STAMP(4 + 2 * c);
       {
-        const int t = 16 * a + i;
-        bf16x8 qf[2 * KH];
+        auto block = [&](int tb, int sb) {
+          const int t = 16 * tb + i;
+          f32x4 pt = zero4();
 #pragma unroll
-        for (int m = 0; m < 2 * KH; ++m) qf[m] = frag(Qs + (m >> 1) * TILE, t, m & 1, g);
-        const float Lt = Ls[t];
-        f32x4 pt[4];
+          for (int m = 0; m < 2 * KH; ++m)
+            pt = pgn_mfma(frag(Ks + (m >> 1) * TILE, 16 * sb + i, m & 1, g), frag(Qs + (m >> 1) * TILE, t, m & 1, g),
+                          pt);
+          const float Lt = Ls[t];
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
 #pragma unroll
-        for (int sb = 0; sb < 4; ++sb) {
-          pt[sb] = zero4();
-          if (sb <= a) {
+          for (int r = 0; r < 4; ++r) pt[r] *= masked_decay(Lt - Lsv[r], 16 * sb + 4 * g + r <= t);
+          store_T(As, 16 * tb, 16 * sb, g, i, pt);
+        };
 #pragma unroll
-            for (int m = 0; m < 2 * KH; ++m)
-              pt[sb] = pgn_mfma(frag(Ks + (m >> 1) * TILE, 16 * sb + i, m & 1, g), qf[m], pt[sb]);
-          }
-        }
-#pragma unroll
-        for (int sb = 0; sb < 4; ++sb) {
-          if (sb <= a) {
-            const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) pt[sb][r] *= masked_decay(Lt - Lsv[r], 16 * sb + 4 * g + r <= t);
-          }
-          store_T(As, 16 * a, 16 * sb, g, i, pt[sb]);
+        for (int sb = 1; sb < 4; ++sb)
+          if (sb > a) store_T(As, 16 * a, 16 * sb, g, i, zero4());
+        if (a == 0) {
+          block(0, 0);
+          block(3, 0);
+        } else if (a == 1) {
+          block(1, 0);
+          block(1, 1);
+          block(3, 1);
+        } else if (a == 2) {
+          block(2, 0);
+          block(2, 1);
+          block(2, 2);
+        } else {
+          block(3, 2);
+          block(3, 3);
         }
       }
       DF_STAMP(5 + 2 * c);
