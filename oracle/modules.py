@@ -107,8 +107,11 @@ def spin_rf(sd, x, h0=None, gate_c=8.0, nu_min=1e-3):
 
 
 # the carrier mixers of `src/model.py:632-660`: (delta rule, options); the head count is the caller's `heads`
+# `src/model.py:632-660`: the rule and options of each carrier mixer (its head count is the caller's `heads`: wspin
+# and xspin four, w2spin two)
 ASSOC_MIXERS = {"aspin": (False, {}), "dspin": (True, {}), "hspin": (False, {}), "hspin1": (False, {"write_all": True}),
-                "hdspin": (True, {}), "sdspin": (True, {"key_topk": 8}), "aspin1": (True, {"write_all": True})}
+                "hdspin": (True, {}), "sdspin": (True, {"key_topk": 8}), "aspin1": (True, {"write_all": True}),
+                "wspin": (False, {}), "w2spin": (False, {}), "xspin": (True, {})}
 
 
 def _mixer(sd, prefix, mixer, heads, x, st):

@@ -129,9 +129,43 @@ def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = Fa
         return _kernel_scan(q, k, v, logalpha, S0, beta, need_sent)
     rt = torch.float64 if q.dtype == torch.float64 else torch.float32
     want = _needs_grad(q, k, v, logalpha, S0, beta)
-    o, S, _, _ = _op.aspin_exact(q.to(rt), k.to(rt), v.to(rt), logalpha.to(rt),
-                                 None if beta is None else beta.to(rt), None if S0 is None else S0.to(rt), want)
+    cv = lambda t: None if t is None else t.to(rt)
+    o, S = _exact_scan(cv(q), cv(k), cv(v), cv(logalpha), cv(beta), cv(S0), want)
     return o.to(q.dtype), S
+
+
+def _dim_blocks(n: int, cap: int) -> list[tuple[int, int]]:
+    """[start, end) ranges splitting n into the fewest near-equal blocks of at most cap."""
+    nb = (n + cap - 1) // cap
+    edges = [round(i * n / nb) for i in range(nb + 1)]
+    return list(zip(edges[:-1], edges[1:]))
+
+
+def _exact_scan(q, k, v, logalpha, beta, S0, want):
+    """The exact scan (`ops.aspin_exact`) at any head dims for the plain rule: its state's key rows evolve
+    independently and the read sums over them, so with keys and values split into blocks of at most EXACT_MAX_D,
+    o[.., vb] = sum over key blocks kb of scan(q[.., kb], k[.., kb], v[.., vb]) and S[kb, vb] is that scan's state
+    (the reference's wide carriers, `src/model.py:636-643`: four or two heads of 176-384). The delta rule couples all
+    key rows in every write (r = v - P^T k), so it takes head dims up to EXACT_MAX_D only."""
+    Dk, Dv = q.shape[-1], v.shape[-1]
+    cap = _op_mod.EXACT_MAX_D
+    if Dk <= cap and Dv <= cap:
+        o, S, _, _ = _op.aspin_exact(q, k, v, logalpha, beta, S0, want)
+        return o, S
+    if beta is not None:
+        raise PragnosiaError(f"assoc_scan: the delta rule takes head dims up to {cap} (got {Dk} x {Dv}): its state "
+                             "does not split into key blocks")
+    outs, cols = [], []
+    for v0, v1 in _dim_blocks(Dv, cap):
+        o_vb, rows = None, []
+        for k0, k1 in _dim_blocks(Dk, cap):
+            S0b = None if S0 is None else S0[..., k0:k1, v0:v1]
+            o_b, S_b, _, _ = _op.aspin_exact(q[..., k0:k1], k[..., k0:k1], v[..., v0:v1], logalpha, None, S0b, want)
+            o_vb = o_b if o_vb is None else o_vb + o_b
+            rows.append(S_b)
+        outs.append(o_vb)
+        cols.append(torch.cat(rows, dim=-2))
+    return torch.cat(outs, dim=-1), torch.cat(cols, dim=-1)
 
 
 def _kernel_scan(q, k, v, logalpha, S0, beta, need_sent):
@@ -178,8 +212,8 @@ class AssocCarrier(nn.Module):
     """Per-head key-value outer-product memory with per-token forgetting, learned rotation frequencies and an
     optional delta write rule (`src/assoc.py:279-512`). Constructor arguments, parameters and paths are the
     reference's: with `kernel` (and T > 1, head dim 64 or 128) the bf16-operand MFMA kernels with
-    the fused prep; otherwise (kernel=False, a T = 1 call under autograd, other head dims up to 128) the reference's
-    torch composition around the exact fp32 scan (bf16 MFMA kernels under autocast, as the reference's bf16 matmuls);
+    the fused prep; otherwise (kernel=False, a T = 1 call under autograd, other head dims: any width for the plain
+    rule, up to 128 for the delta rule) the reference's torch composition around the exact fp32 scan (bf16 MFMA kernels under autocast, as the reference's bf16 matmuls);
     a T = 1 call without autograd (decode) the fused fp32 step kernel. Options: key_topk, hl_floor, write_all,
     beta_scale, FUSED_PROJ, pos_wrap, and the short causal convolution with its carried cache (add_short_conv)."""
 
@@ -351,9 +385,9 @@ class AssocCarrier(nn.Module):
         """x (B, T, d); h0 = (S (B, H, dk, dk), p0) from a previous call, (S, p0, cache) with the short convolution, or
         None. Returns (x + gated output, (S, T) or (S, T, cache)); positions restart at 0 every call and the carried
         state is rebased by -p0 (`src/assoc.py:384-512`)."""
-        if self.dk > _op_mod.EXACT_MAX_D:
-            raise PragnosiaError(f"AssocCarrier: head dim {self.dk} is above the {_op_mod.EXACT_MAX_D} the kernels "
-                                 "take")
+        if self.delta and self.dk > _op_mod.EXACT_MAX_D:
+            raise PragnosiaError(f"AssocCarrier: the delta rule takes head dims up to {_op_mod.EXACT_MAX_D} (got "
+                                 f"{self.dk})")
         if not x.is_cuda:
             raise PragnosiaError("AssocCarrier runs on a ROCm GPU only; there is no CPU path")
         B, T, D = x.shape

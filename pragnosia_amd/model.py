@@ -9,11 +9,15 @@ Constructor arguments, module names and initialisation follow the reference (`sr
     "hspin1"  AssocCarrier(d, head_dim=128, write_all=True)        ... with no write gate
     "hdspin"  AssocCarrier(d, delta=True, head_dim=128)            delta rule, 128-dim heads
     "sdspin"  ... + key_topk=8;  "tspin" ... + hl_floor=True;  "aspin1" ... + write_all=True
+    "wspin"   AssocCarrier(d, heads=4)                             plain rule, four wide heads (d / 4)
+    "w2spin"  AssocCarrier(d, heads=2)                             plain rule, two wide heads (d / 2)
+    "xspin"   AssocCarrier(d, delta=True, heads=4)                 delta rule, four heads (up to 128 wide: d <= 512)
     "fspin"   SpinCarrier(d, gated="rf")                           forget-gated complex diagonal carrier
 
-(`src/model.py:632-660`.) The mixers run on the HIP kernels (the delta rule at head dim 128 on the fp32 exact scan);
-embeddings, LayerNorms, the MLPs and the tied head are torch. Attention, the hybrid stacks and the other reference
-mixers are outside this build and raise. `short_conv=K` adds every carrier's short causal convolution
+(`src/model.py:632-660`.) The mixers run on the HIP kernels: heads of 64 and 128 on the bf16 MFMA scans, other head
+widths on the exact fp32 scan (the plain rule in key and value blocks of at most 128, so any width; the delta rule up
+to 128). Embeddings, LayerNorms, the MLPs and the tied head are torch. Attention, the hybrid stacks and the other
+reference mixers are outside this build and raise. `short_conv=K` adds every carrier's short causal convolution
 (`src/model.py:717-726`).
 """
 from __future__ import annotations
@@ -37,6 +41,9 @@ MIXERS = {
     "sdspin": lambda d: AssocCarrier(d, delta=True, head_dim=128, key_topk=8),
     "tspin": lambda d: AssocCarrier(d, delta=True, head_dim=128, hl_floor=True),
     "aspin1": lambda d: AssocCarrier(d, delta=True, head_dim=128, write_all=True),
+    "wspin": lambda d: AssocCarrier(d, heads=4),
+    "w2spin": lambda d: AssocCarrier(d, heads=2),
+    "xspin": lambda d: AssocCarrier(d, delta=True, heads=4),
     "fspin": lambda d: SpinCarrier(d, gated="rf"),
 }
 

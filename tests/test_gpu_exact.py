@@ -129,6 +129,24 @@ def test_fp32_matches_oracle(scan, delta, B, H, T, Dk, Dv, s0):
     assert max(e.values()) < 1e-4, e
 
 
+@pytest.mark.parametrize("B,H,T,Dk,Dv", [(1, 2, 77, 176, 176), (1, 1, 40, 384, 200)])
+def test_fp32_wide_heads_plain(scan, B, H, T, Dk, Dv):
+    """Head dims above 128, plain rule (the reference's wspin / w2spin: four or two heads of 176-384): the exact scan
+    over key and value blocks of at most 128, outputs, final state and every gradient within 1e-4 of the fp64
+    oracle."""
+    e = _check_fp32(scan, *_fp32_case(B, H, T, Dk, Dv, False, seed=T + Dk, s0=True))
+    assert max(e.values()) < 1e-4, e
+
+
+def test_fp32_wide_heads_delta_rejected(scan):
+    """The delta rule couples every key row in each write, so head dims above 128 are refused with an error (before
+    any launch) rather than split."""
+    from pragnosia_amd._lib import PragnosiaError
+    q, k, v, la, be, S0, _, _ = _fp32_case(1, 1, 20, 176, 176, True, seed=5)
+    with pytest.raises(PragnosiaError):
+        scan(q.cuda(), k.cuda(), v.cuda(), la.cuda(), S0.cuda(), beta=be.cuda())
+
+
 def test_cfg0_fp32(scan):
     """BASELINE configs[0], the reference's CPU-runnable case, at its fp32 bound: B1 H4 T256 D64; q, k, v ~ N(0,1),
     k L2-normalised; la = logsigmoid(N(3,1)); theta ~ U(0, 0.1) rotating q and k at positions 0..255; S0 = 0.

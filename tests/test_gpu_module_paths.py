@@ -98,6 +98,40 @@ def test_short_conv_carrier(delta, kernel):
             assert rel(st[0], OA.rebase(Sr.detach(), sd["theta"].detach(), 89.0)) < 1e-4
 
 
+@pytest.mark.parametrize("mixer,d,heads", [("wspin", 704, 4), ("w2spin", 352, 2), ("xspin", 256, 4)])
+def test_wide_head_mixers_lm(mixer, d, heads):
+    """The reference's few-wide-heads carriers (`src/model.py:636-643`) in a small LM: wspin at d 704 (four heads of
+    176) and w2spin at d 352 (two of 176) on the exact fp32 scan in key and value blocks of at most 128; xspin (the
+    delta rule, four heads) at d 256, where its heads are 64 wide. Logits of forward and forward_carried against the
+    oracle (fp32 exact path: 1e-4; xspin on the bf16 kernels: 2e-2), a finite backward, and the graphed greedy decode
+    equal to the eager loop."""
+    from pragnosia_amd.decode import GreedyDecoder, greedy_eager
+    from pragnosia_amd.model import LM
+    torch.manual_seed(81)
+    g = torch.Generator().manual_seed(81)
+    lm = LM(vocab=300, d=d, layers=2, mlp_mult=2, ctx=48, mixer=mixer)
+    with torch.no_grad():
+        lm.e.weight.mul_(10)
+    sd = {k: v.detach().double() for k, v in lm.state_dict().items()}
+    lm = lm.cuda()
+    ids = torch.randint(0, 300, (2, 100), generator=g)
+    tol = 2e-2 if mixer == "xspin" else 1e-4
+    with torch.no_grad():
+        lg = lm(ids[:, :48].cuda())
+        lc = lm.forward_carried(ids.cuda(), window=48)
+    ref = M.lm_forward(sd, ids[:, :48], layers=2, mixer=mixer, heads=heads)
+    refc = M.lm_forward_carried(sd, ids, 48, layers=2, mixer=mixer, heads=heads)
+    assert rel(lg, ref) < tol and rel(lc, refc) < tol, (rel(lg, ref), rel(lc, refc))
+    loss = torch.nn.functional.cross_entropy(lm(ids[:, :48].cuda()).reshape(-1, 300), ids[:, 1:49].reshape(-1).cuda())
+    loss.backward()
+    assert all(torch.isfinite(p.grad).all() for p in lm.parameters() if p.grad is not None)
+    lm.eval()
+    dec = GreedyDecoder(lm, 2, steps_per_graph=4)
+    toks_g = dec.generate(ids[:, :30].cuda(), 12)
+    toks_e, _ = greedy_eager(lm, ids[:, :30].cuda(), 12)
+    assert torch.equal(toks_g, toks_e)
+
+
 @pytest.mark.parametrize("mixer", ["hdspin", "sdspin", "aspin1", "hspin1"])
 def test_head_dim_128_mixers_lm(mixer):
     """The reference's head-dim-128 carriers (`src/model.py:650-660`) in a small LM (d 256: two heads of 128):
