@@ -211,7 +211,7 @@ int pragnosia_aspin_out_bwd(const void* gy, int gy_bf16, const void* o, const fl
 
 /* ---------------------------------------------------------------------------------------------------------
  * Associative carrier scan with fp32 or fp64 operands (no bf16 rounding), plain rule (beta NULL) or delta rule,
- * per (batch, head), any head dims 1 <= Dk, Dv <= 128:
+ * per (batch, head), head dims 1 <= Dk <= 384, 1 <= Dv <= 128:
  *     plain: S_t = a_t S_{t-1} + k_t v_t^T;   delta: S_t = P + beta_t k_t (v_t - P^T k_t)^T, P = a_t S_{t-1};
  *     o_t = S_t^T q_t,   a_t = exp(la_t),   S_{-1} = S0 (zero when NULL).
  * Every tensor has the operand type `dtype` (PRAGNOSIA_F32 or PRAGNOSIA_F64): q, k (B, H, T, Dk); v (B, H, T, Dv);
@@ -226,8 +226,9 @@ int pragnosia_aspin_exact_fwd(const void* q, const void* k, const void* v, const
 
 /* Backward of pragnosia_aspin_exact_fwd from dO (B, H, T, Dv) and dS_final (or NULL = zero), with the forward's ckpt
  * and resid: writes dq, dk (B, H, T, Dk), dv (B, H, T, Dv), dla (B, H, T), dbeta (B, H, T; delta rule) and, if
- * non-NULL, dS0 (B, H, Dk, Dv), all of type `dtype`. PRAGNOSIA_ERR_UNSUPPORTED when fp64 with both Dk and Dv above
- * 64 (its block buffers exceed the LDS). */
+ * non-NULL, dS0 (B, H, Dk, Dv), all of type `dtype`. PRAGNOSIA_ERR_UNSUPPORTED when its block buffers exceed the
+ * 160 KiB of LDS: they grow with Dk times Dv (fp32 fits Dv 128 up to Dk 128, 80 up to 384; fp64 112 up to 128, 80 up
+ * to 192, 32 up to 384). Value columns are independent recurrences: a caller splits wider ones into blocks. */
 int pragnosia_aspin_exact_bwd(const void* q, const void* k, const void* v, const void* la, const void* beta,
                               const void* ckpt, const void* resid, const void* dO, const void* dS_final, void* dq,
                               void* dk, void* dv, void* dla, void* dbeta, void* dS0, int64_t B, int64_t H, int64_t T,

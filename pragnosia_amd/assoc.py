@@ -118,7 +118,8 @@ def assoc_scan(q, k, v, logalpha, S0=None, chunk: int = 64, recompute: bool = Fa
     (B, H, Dk, Dv) or None. Returns (o in q's dtype, S_final).
 
     As in the reference, the arithmetic is fp32, or fp64 for fp64 inputs (`rt`, `src/assoc.py:259-261`), with no
-    operand rounding: the exact kernels (any Dk, Dv <= 128), S_final in that type. With `mm` a 16-bit type (the
+    operand rounding: the exact kernels (any head dims for the plain rule, keys up to 384 for the delta rule; wide heads
+    run in blocks), S_final in that type. With `mm` a 16-bit type (the
     reference's bf16 matmuls under autocast, `:149-153`) the bf16-operand MFMA kernels run instead (fp32 accumulation
     and state; head dim 64 or 128), S_final fp32. The result does not depend on `chunk` (the
     reference's own test), and both paths recompute in the backward what they do not save, so `chunk`, `recompute`
@@ -142,29 +143,32 @@ def _dim_blocks(n: int, cap: int) -> list[tuple[int, int]]:
 
 
 def _exact_scan(q, k, v, logalpha, beta, S0, want):
-    """The exact scan (`ops.aspin_exact`) at any head dims for the plain rule: its state's key rows evolve
-    independently and the read sums over them, so with keys and values split into blocks of at most EXACT_MAX_D,
-    o[.., vb] = sum over key blocks kb of scan(q[.., kb], k[.., kb], v[.., vb]) and S[kb, vb] is that scan's state
-    (the reference's wide carriers, `src/model.py:636-643`: four or two heads of 176-384). The delta rule couples all
-    key rows in every write (r = v - P^T k), so it takes head dims up to EXACT_MAX_D only."""
+    """The exact scan (`ops.aspin_exact`) at the reference's wide head dims (`src/model.py:636-643`: four or two
+    heads of 176-384). Value columns never mix (each is its own recurrence over the key rows), so every rule splits
+    them into blocks that fit one launch's LDS (`exact_value_cap`). The plain rule's key rows evolve independently
+    too and its read sums over them: with keys in blocks of at most 128, o[.., vb] = sum over key blocks kb of
+    scan(q[.., kb], k[.., kb], v[.., vb]) and S[kb, vb] is that scan's state. The delta rule couples all key rows in
+    every write (r = v - P^T k), so its keys stay in one launch, up to EXACT_MAX_DK = 384."""
     Dk, Dv = q.shape[-1], v.shape[-1]
-    cap = _op_mod.EXACT_MAX_D
-    if Dk <= cap and Dv <= cap:
+    dt = torch.float64 if q.dtype == torch.float64 else torch.float32
+    if beta is not None and Dk > _op_mod.EXACT_MAX_DK:
+        raise PragnosiaError(f"assoc_scan: the delta rule takes key dims up to {_op_mod.EXACT_MAX_DK} (got {Dk}): "
+                             "its state does not split into key blocks")
+    kblocks = [(0, Dk)] if beta is not None else _dim_blocks(Dk, 128)
+    vcap = min(_op_mod.exact_value_cap(k1 - k0, dt, bool(want)) for k0, k1 in kblocks)
+    if len(kblocks) == 1 and Dv <= vcap:
         o, S, _, _ = _op.aspin_exact(q, k, v, logalpha, beta, S0, want)
         return o, S
-    if beta is not None:
-        raise PragnosiaError(f"assoc_scan: the delta rule takes head dims up to {cap} (got {Dk} x {Dv}): its state "
-                             "does not split into key blocks")
     outs, cols = [], []
-    for v0, v1 in _dim_blocks(Dv, cap):
+    for v0, v1 in _dim_blocks(Dv, vcap):
         o_vb, rows = None, []
-        for k0, k1 in _dim_blocks(Dk, cap):
+        for k0, k1 in kblocks:
             S0b = None if S0 is None else S0[..., k0:k1, v0:v1]
-            o_b, S_b, _, _ = _op.aspin_exact(q[..., k0:k1], k[..., k0:k1], v[..., v0:v1], logalpha, None, S0b, want)
+            o_b, S_b, _, _ = _op.aspin_exact(q[..., k0:k1], k[..., k0:k1], v[..., v0:v1], logalpha, beta, S0b, want)
             o_vb = o_b if o_vb is None else o_vb + o_b
             rows.append(S_b)
         outs.append(o_vb)
-        cols.append(torch.cat(rows, dim=-2))
+        cols.append(rows[0] if len(rows) == 1 else torch.cat(rows, dim=-2))
     return torch.cat(outs, dim=-1), torch.cat(cols, dim=-1)
 
 
@@ -213,7 +217,7 @@ class AssocCarrier(nn.Module):
     optional delta write rule (`src/assoc.py:279-512`). Constructor arguments, parameters and paths are the
     reference's: with `kernel` (and T > 1, head dim 64 or 128) the bf16-operand MFMA kernels with
     the fused prep; otherwise (kernel=False, a T = 1 call under autograd, other head dims: any width for the plain
-    rule, up to 128 for the delta rule) the reference's torch composition around the exact fp32 scan (bf16 MFMA kernels under autocast, as the reference's bf16 matmuls);
+    rule, up to 384 for the delta rule) the reference's torch composition around the exact fp32 scan (bf16 MFMA kernels under autocast, as the reference's bf16 matmuls);
     a T = 1 call without autograd (decode) the fused fp32 step kernel. Options: key_topk, hl_floor, write_all,
     beta_scale, FUSED_PROJ, pos_wrap, and the short causal convolution with its carried cache (add_short_conv)."""
 
@@ -385,8 +389,8 @@ class AssocCarrier(nn.Module):
         """x (B, T, d); h0 = (S (B, H, dk, dk), p0) from a previous call, (S, p0, cache) with the short convolution, or
         None. Returns (x + gated output, (S, T) or (S, T, cache)); positions restart at 0 every call and the carried
         state is rebased by -p0 (`src/assoc.py:384-512`)."""
-        if self.delta and self.dk > _op_mod.EXACT_MAX_D:
-            raise PragnosiaError(f"AssocCarrier: the delta rule takes head dims up to {_op_mod.EXACT_MAX_D} (got "
+        if self.delta and self.dk > _op_mod.EXACT_MAX_DK:
+            raise PragnosiaError(f"AssocCarrier: the delta rule takes head dims up to {_op_mod.EXACT_MAX_DK} (got "
                                  f"{self.dk})")
         if not x.is_cuda:
             raise PragnosiaError("AssocCarrier runs on a ROCm GPU only; there is no CPU path")

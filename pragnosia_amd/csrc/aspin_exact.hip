@@ -1,5 +1,5 @@
 // The associative carrier's scan with fp32 or fp64 operands (the exact path): plain and delta write rules, forward
-// and backward, any head dims Dk, Dv <= 128.
+// and backward, any head dims Dk <= 384, Dv <= 128.
 //
 // The reference's `assoc_scan` (src/assoc.py:254-269) computes in fp32, or in fp64 for fp64 inputs, through the
 // chunked two-pass forms `_scan_twopass` / `_scan_twopass_delta` (src/assoc.py:118-165, :207-251), whose tests hold
@@ -14,9 +14,11 @@
 //
 // Layout of the work: one workgroup per (batch, head), ceil(Dv / 16) waves. Lane l of wave w owns value column
 // j = 16 w + (l & 15) and the R key rows g R .. g R + R - 1 of that column (g = l >> 4, R = the smallest of 2, 4, 8,
-// 16, 32 with 4 R >= Dk), so the state lives in registers, the update is R fused multiply-adds per lane and a read
-// over the key rows is R products plus a two-step exchange across the four row groups of the wave. Inputs are staged
-// through LDS a block of CK = 8 tokens at a time.
+// 16, 32, 48, 96 with 4 R >= Dk), so the state lives in registers (the larger R spill part of it to scratch), the
+// update is R fused multiply-adds per lane and a read over the key rows is R products plus a two-step exchange across
+// the four row groups of the wave. Inputs are staged through LDS a block of CK = 8 tokens at a time. The backward's
+// LDS grows with R times the number of waves, so wide keys take fewer value columns per launch (the entry points
+// return PRAGNOSIA_ERR_UNSUPPORTED past 160 KiB; the caller splits the value columns, which are independent).
 //
 // Forward writes o, the final state, and for a backward the state entering every block of CK tokens (`ckpt`,
 // (B, H, ceil(T / CK), Dk, Dv)) and, for the delta rule, the residual r_t ((B, H, T, Dv)), so that re-running the
@@ -35,7 +37,8 @@
 namespace {
 
 constexpr int CK = PRAGNOSIA_EXACT_CKPT_TOKENS;
-constexpr int kMaxD = 128;
+constexpr int kMaxDk = 384;  // key rows: R up to 96 a lane (four row groups)
+constexpr int kMaxDv = 128;  // value columns: one a lane, up to eight waves
 
 PGN_DEVICE float exp_(float x) { return expf(x); }
 PGN_DEVICE double exp_(double x) { return exp(x); }
@@ -321,7 +324,9 @@ __global__ __launch_bounds__(512) void aspin_exact_bwd(
   }
 }
 
-int rows_per_lane(int64_t Dk) { return Dk <= 8 ? 2 : Dk <= 16 ? 4 : Dk <= 32 ? 8 : Dk <= 64 ? 16 : 32; }
+int rows_per_lane(int64_t Dk) {
+  return Dk <= 8 ? 2 : Dk <= 16 ? 4 : Dk <= 32 ? 8 : Dk <= 64 ? 16 : Dk <= 128 ? 32 : Dk <= 192 ? 48 : 96;
+}
 
 template <typename real>
 size_t fwd_lds(int R, int NW) {
@@ -336,9 +341,9 @@ size_t bwd_lds(int R, int NW) {
 constexpr size_t kMaxLds = 160 * 1024;
 
 bool exact_shape_ok(int64_t B, int64_t H, int64_t T, int64_t Dk, int64_t Dv) {
-  if (B <= 0 || H <= 0 || T <= 0 || Dk <= 0 || Dv <= 0 || Dk > kMaxD || Dv > kMaxD) return false;
+  if (B <= 0 || H <= 0 || T <= 0 || Dk <= 0 || Dv <= 0 || Dk > kMaxDk || Dv > kMaxDv) return false;
   if (B * H >= ((int64_t)1 << 31) || T >= ((int64_t)1 << 28)) return false;
-  return B * H * T * kMaxD < ((int64_t)1 << 46);
+  return B * H * T * kMaxDk < ((int64_t)1 << 46);
 }
 
 template <typename real, bool DELTA, int R>
@@ -347,6 +352,7 @@ int launch_fwd(const void* q, const void* k, const void* v, const void* la, cons
                hipStream_t st) {
   const int NW = (int)((Dv + 15) / 16);
   const size_t lds = fwd_lds<real>(R, NW);
+  if (lds > kMaxLds) return PRAGNOSIA_ERR_UNSUPPORTED;
   const void* fn = (const void*)aspin_exact_fwd<real, R, DELTA>;
   const hipError_t e = pgn_lds_limit(fn, lds);
   if (e != hipSuccess) return (int)e;
@@ -382,7 +388,9 @@ int dispatch_fwd(int R, const void* q, const void* k, const void* v, const void*
     case 4: return launch_fwd<real, DELTA, 4>(q, k, v, la, beta, S0, o, Sfin, ckpt, resid, B, H, T, Dk, Dv, st);
     case 8: return launch_fwd<real, DELTA, 8>(q, k, v, la, beta, S0, o, Sfin, ckpt, resid, B, H, T, Dk, Dv, st);
     case 16: return launch_fwd<real, DELTA, 16>(q, k, v, la, beta, S0, o, Sfin, ckpt, resid, B, H, T, Dk, Dv, st);
-    default: return launch_fwd<real, DELTA, 32>(q, k, v, la, beta, S0, o, Sfin, ckpt, resid, B, H, T, Dk, Dv, st);
+    case 32: return launch_fwd<real, DELTA, 32>(q, k, v, la, beta, S0, o, Sfin, ckpt, resid, B, H, T, Dk, Dv, st);
+    case 48: return launch_fwd<real, DELTA, 48>(q, k, v, la, beta, S0, o, Sfin, ckpt, resid, B, H, T, Dk, Dv, st);
+    default: return launch_fwd<real, DELTA, 96>(q, k, v, la, beta, S0, o, Sfin, ckpt, resid, B, H, T, Dk, Dv, st);
   }
 }
 
@@ -399,7 +407,9 @@ int dispatch_bwd(int R, const void* q, const void* k, const void* v, const void*
     case 4: PGN_EXACT_BWD(4);
     case 8: PGN_EXACT_BWD(8);
     case 16: PGN_EXACT_BWD(16);
-    default: PGN_EXACT_BWD(32);
+    case 32: PGN_EXACT_BWD(32);
+    case 48: PGN_EXACT_BWD(48);
+    default: PGN_EXACT_BWD(96);
   }
 #undef PGN_EXACT_BWD
 }

@@ -11,7 +11,7 @@ Constructor arguments, module names and initialisation follow the reference (`sr
     "sdspin"  ... + key_topk=8;  "tspin" ... + hl_floor=True;  "aspin1" ... + write_all=True
     "wspin"   AssocCarrier(d, heads=4)                             plain rule, four wide heads (d / 4)
     "w2spin"  AssocCarrier(d, heads=2)                             plain rule, two wide heads (d / 2)
-    "xspin"   AssocCarrier(d, delta=True, heads=4)                 delta rule, four heads (up to 128 wide: d <= 512)
+    "xspin"   AssocCarrier(d, delta=True, heads=4)                 delta rule, four heads (up to 384 wide)
     "fspin"   SpinCarrier(d, gated="rf")                           forget-gated complex diagonal carrier
 
 (`src/model.py:632-660`.) The mixers run on the HIP kernels: heads of 64 and 128 on the bf16 MFMA scans, other head

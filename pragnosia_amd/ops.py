@@ -843,7 +843,32 @@ aspin_delta_fused.register_autograd(_delta_fused_backward, setup_context=_delta_
 # the scan with fp32 / fp64 operands (no bf16 rounding): replaces assoc_scan's fp32/fp64 torch forms and their
 # autograd backward, src/assoc.py:118-165, :207-269
 EXACT_CKPT = 8  # tokens per checkpointed state (PRAGNOSIA_EXACT_CKPT_TOKENS)
-EXACT_MAX_D = 128
+EXACT_MAX_DK = 384  # key rows (kMaxDk)
+EXACT_MAX_DV = 128  # value columns (kMaxDv)
+EXACT_MAX_LDS = 160 * 1024
+
+
+def exact_rows_per_lane(Dk: int) -> int:
+    """Key rows each lane holds in the exact scan (rows_per_lane): the smallest of 2 .. 96 with 4 R >= Dk."""
+    for r in (2, 4, 8, 16, 32, 48, 96):
+        if 4 * r >= Dk:
+            return r
+    raise PragnosiaError(f"exact scan: Dk={Dk} exceeds {EXACT_MAX_DK}")
+
+
+def exact_value_cap(Dk: int, dtype: torch.dtype, backward: bool) -> int:
+    """The most value columns one exact-scan launch takes at key width Dk: a multiple of 16 (one wave each) whose
+    LDS (fwd_lds / bwd_lds of the kernel) fits 160 KiB."""
+    R, es = exact_rows_per_lane(Dk), (8 if dtype == torch.float64 else 4)
+    for nw in range(EXACT_MAX_DV // 16, 0, -1):
+        if backward:
+            n = 2 * EXACT_CKPT * 4 * R + 3 * EXACT_CKPT * 16 * nw + 2 * EXACT_CKPT + 2 * nw * EXACT_CKPT * 4 * R \
+                + 2 * nw * EXACT_CKPT
+        else:
+            n = 2 * EXACT_CKPT * 4 * R + EXACT_CKPT * 16 * nw + 2 * EXACT_CKPT
+        if n * es <= EXACT_MAX_LDS:
+            return 16 * nw
+    raise PragnosiaError(f"exact scan: no value block fits the LDS at Dk={Dk}")
 
 
 def _exact_dtype(t: Tensor) -> torch.dtype:
@@ -855,13 +880,13 @@ def _dtype_code(dt: torch.dtype) -> int:
 
 
 def _expect_exact(op: str, q: Tensor, k, v, la, beta=None, S0=None) -> None:
-    """q, k (B, H, T, Dk); v (B, H, T, Dv); la, beta (B, H, T); S0 (B, H, Dk, Dv); Dk, Dv <= 128."""
+    """q, k (B, H, T, Dk); v (B, H, T, Dv); la, beta (B, H, T); S0 (B, H, Dk, Dv); Dk <= 384, Dv <= 128."""
     if q.dim() != 4 or v is None or v.dim() != 4:
         raise PragnosiaError(f"{op}: q and v must be (B, H, T, D)")
     B, H, T, Dk = q.shape
     Dv = v.shape[-1]
-    if not (0 < Dk <= EXACT_MAX_D and 0 < Dv <= EXACT_MAX_D):
-        raise PragnosiaError(f"{op}: head dims Dk={Dk}, Dv={Dv} must be in 1..{EXACT_MAX_D}")
+    if not (0 < Dk <= EXACT_MAX_DK and 0 < Dv <= EXACT_MAX_DV):
+        raise PragnosiaError(f"{op}: head dims Dk={Dk}, Dv={Dv} must be in 1..{EXACT_MAX_DK} x 1..{EXACT_MAX_DV}")
     _expect(op, q.device, k=(k, (B, H, T, Dk)), v=(v, (B, H, T, Dv)), la=(la, (B, H, T)), beta=(beta, (B, H, T)),
             S0=(S0, (B, H, Dk, Dv)))
 
@@ -870,7 +895,8 @@ def _expect_exact(op: str, q: Tensor, k, v, la, beta=None, S0=None) -> None:
 def aspin_exact(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Optional[Tensor], S0: Optional[Tensor],
                 want_ckpt: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """The scan with fp32 operands (fp64 when q is fp64), plain rule, or the delta rule when beta is given.
-    q, k (B, H, T, Dk), v (B, H, T, Dv), la and beta (B, H, T), S0 (B, H, Dk, Dv) or None; Dk, Dv <= 128. Returns
+    q, k (B, H, T, Dk), v (B, H, T, Dv), la and beta (B, H, T), S0 (B, H, Dk, Dv) or None; Dk <= 384, Dv <= 128
+    (wide keys take fewer value columns: exact_value_cap; the library refuses what does not fit its LDS). Returns
     (o (B, H, T, Dv), S_final (B, H, Dk, Dv), ckpt, resid) in the compute dtype; ckpt (the state entering every 8
     tokens) and resid (the delta rule's residuals) are what the backward reads, empty unless want_ckpt."""
     _require_gpu(q, k, v, la, beta, S0)

@@ -138,11 +138,38 @@ def test_fp32_wide_heads_plain(scan, B, H, T, Dk, Dv):
     assert max(e.values()) < 1e-4, e
 
 
-def test_fp32_wide_heads_delta_rejected(scan):
-    """The delta rule couples every key row in each write, so head dims above 128 are refused with an error (before
-    any launch) rather than split."""
+@pytest.mark.parametrize("B,H,T,Dk,Dv", [(1, 2, 45, 176, 176), (1, 1, 30, 384, 72), (2, 1, 17, 300, 40)])
+def test_fp32_wide_heads_delta(scan, B, H, T, Dk, Dv):
+    """Key dims above 128, delta rule (the reference's xspin at d 704-768: four heads of 176-192; and up to 384): the
+    keys stay in one launch (48 or 96 rows a lane), the value columns split into blocks that fit the backward's LDS;
+    outputs, final state and every gradient within 1e-4 of the fp64 oracle."""
+    e = _check_fp32(scan, *_fp32_case(B, H, T, Dk, Dv, True, seed=T + Dk, s0=True))
+    assert max(e.values()) < 1e-4, e
+
+
+@pytest.mark.parametrize("delta,Dk,Dv", [(False, 128, 128), (True, 192, 96)])
+def test_fp64_wide_value_blocks(scan, delta, Dk, Dv):
+    """fp64 at widths whose backward does not fit one launch's LDS (128 x 128 plain, 192 keys with the delta rule):
+    split into value blocks, forward, state and gradients within 1e-10 of the fp64 oracle."""
+    q, k, v, la, be, S0, wo, wS = (None if t is None else t.double()
+                                   for t in _fp32_case(1, 2, 37, Dk, Dv, delta, seed=Dk + Dv, s0=True))
+    ins = [q, k, v, la] + ([be] if delta else []) + [S0]
+    r = [t.clone().requires_grad_(True) for t in ins]
+    yr, Sr = O.assoc_scan(r[0], r[1], r[2], r[3], r[-1], chunk=16, beta=r[4] if delta else None)
+    ((yr * wo).sum() + (Sr * wS).sum()).backward()
+    d = [t.cuda().requires_grad_(True) for t in ins]
+    yk, Sk = scan(d[0], d[1], d[2], d[3], d[-1], beta=d[4] if delta else None)
+    assert yk.dtype == torch.float64
+    ((yk * wo.cuda()).sum() + (Sk * wS.cuda()).sum()).backward()
+    errs = [rel(yk, yr), rel(Sk, Sr)] + [rel(a.grad, b.grad) for a, b in zip(d, r)]
+    assert max(errs) < 1e-10, errs
+
+
+def test_delta_keys_above_384_rejected(scan):
+    """The delta rule couples every key row in each write, so its keys do not split: key dims above 384 are refused
+    with an error before any launch."""
     from pragnosia_amd._lib import PragnosiaError
-    q, k, v, la, be, S0, _, _ = _fp32_case(1, 1, 20, 176, 176, True, seed=5)
+    q, k, v, la, be, S0, _, _ = _fp32_case(1, 1, 12, 400, 32, True, seed=5)
     with pytest.raises(PragnosiaError):
         scan(q.cuda(), k.cuda(), v.cuda(), la.cuda(), S0.cuda(), beta=be.cuda())
 
