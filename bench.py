@@ -1058,7 +1058,8 @@ def phase_rates(reps=50):
         return e0.elapsed_time(e1) / reps * 1e3
 
     out = {"workload": "plain and delta chunked scans, B16 T512 H12 D64 bf16 (configs[2]), phase stamps"}
-    # the delta inverse (one wave per (batch-head, chunk)): its phases from the unit's second stamp buffer
+    # the delta inverse (one workgroup of four waves per (batch-head, chunk)): its phases from the unit's second stamp
+    # buffer, as wave 0 passes them
     import numpy as np
     st.pragnosia_stamps_set_delta_aux.argtypes = [ctypes.c_void_p]
     st.pragnosia_stamps_set_delta_aux.restype = ctypes.c_int
@@ -1076,7 +1077,7 @@ def phase_rates(reps=50):
     t = _rel32(si[:, [0, 2, 3, 4, 5, 6]], si[:, :1]).astype(np.float64) / clk * 1e6  # us from the wave's start
     names = ("staging: keys, decays, strengths", "N", "diagonal blocks", "block levels", "store X")
     out["delta_inverse_phases"] = {
-        "waves": ninv, "shader_clock_GHz": round(clk / 1e9, 3),
+        "workgroups": ninv, "shader_clock_GHz": round(clk / 1e9, 3),
         "median_us": {n: round(float(np.median(t[:, j + 1] - t[:, j])), 3) for j, n in enumerate(names)},
         "wave_total_median_us": round(float(np.median(t[:, 5] - t[:, 0])), 3)}
     for kern in ("plain_fwd", "plain_bwd", "delta_fwd", "delta_bwd_chain"):

@@ -8,7 +8,7 @@
 //     O   = ((Q K^T) o dec) W + (Q o eL) S,             S' = a S + (K o w)^T W
 //
 // Four kernels:
-//   aspin_delta_inv    one wave per (batch-head, chunk): N from a bf16 MFMA K K^T and fp32 decays, then X in fp32
+//   aspin_delta_inv    four waves per (batch-head, chunk): N from a bf16 MFMA K K^T and fp32 decays, then X in fp32
 //                      by 16 x 16 blocks: the diagonal blocks by forward substitution (one column per lane), the
 //                      blocks below them by block forward substitution on fp32 MFMA (the reference sums the
 //                      diagonal blocks by doubling and substitutes across blocks, `src/assoc.py:168-204`; both are
@@ -98,20 +98,26 @@ PGN_DEVICE void chunk_decays(float la_l, int l, float* Ls, float* eLs, float* ws
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// X = (I + N)^-1, one wave per (batch-head, chunk)
+// X = (I + N)^-1, one workgroup of four waves per (batch-head, chunk)
 // N^T and X are kept as their ten 16 x 16 blocks on and below the diagonal (block (tb, sb), sb <= tb, at index
 // tb (tb + 1) / 2 + sb, unpadded rows so the substitution reads four entries at once): 24 KB of LDS per chunk, so
-// six chunks (one round of the grid at cfg2) are resident per compute unit. The keys (KH 64-wide tiles) are loaded in
-// 16-byte row segments into the N and X block areas (unused until N is formed) and read from there as MFMA operands.
+// six chunks (one round of the grid at cfg2, 24 waves) are resident per compute unit. The keys (KH 64-wide tiles) are
+// loaded in 16-byte row segments into the N and X block areas (unused until N is formed) and read from there as MFMA
+// operands. The waves share the independent work of each phase: the ten N blocks (three, three, two, two), the
+// products of each block level (one per wave), the staging and the store; the four diagonal blocks' substitutions
+// are wave 0's (one column per lane). Each block is computed exactly as by one wave, so X does not depend on the split.
 constexpr int BP = 16;                 // row pitch of a 16 x 16 fp32 block
 constexpr int BLK = 16 * BP;
 PGN_DEVICE int blk(int tb, int sb) { return (tb * (tb + 1) / 2 + sb) * BLK; }
 
+// the N blocks (tb, sb) of wave w, -1 past its share
+__constant__ const signed char kInvNT[4][3] = {{3, 3, 0}, {3, 1, 1}, {3, 2, -1}, {2, 2, -1}};
+__constant__ const signed char kInvNS[4][3] = {{0, 3, 0}, {1, 0, 1}, {2, 0, -1}, {1, 2, -1}};
 
 template <int KH>
-__global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__ k, const float* __restrict__ la,
-                                                      const float* __restrict__ be, __bf16* __restrict__ X, int T,
-                                                      int NC) {
+__global__ __launch_bounds__(256) void aspin_delta_inv(const __bf16* __restrict__ k, const float* __restrict__ la,
+                                                       const float* __restrict__ be, __bf16* __restrict__ X, int T,
+                                                       int NC) {
   constexpr int DKEY = 64 * KH;
   __shared__ __align__(16) float NX[20 * BLK];
   float* const NT = NX;             // N^T blocks: NT(tb, sb)[s' * BP + t'] = N[16 tb + t'][16 sb + s']
@@ -120,63 +126,73 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
   __shared__ __align__(16) float Ls[C], bs[C];
 
   const int bh = blockIdx.x / NC, c = blockIdx.x - bh * NC;  // head (not scan), chunk
-  const int l = threadIdx.x, g = l >> 4, i = l & 15;
-  // instrumented build (second buffer): per chunk, clocks at the start (entries 0, 1), the end of the key staging (2),
-  // of N (3), of the diagonal blocks (4), of the block levels (5), and clocks after the store (6, 7)
-  PGN_STAMP_CLOCKS_AUX(blockIdx.x * 8);
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, g = l >> 4, i = l & 15;
+  // instrumented build (second buffer): per chunk, wave 0's clocks at the start (entries 0, 1), the end of the key
+  // staging (2), of N (3), of the diagonal blocks (4), of the block levels (5), and clocks after the store (6, 7)
+  if (w == 0) PGN_STAMP_CLOCKS_AUX(blockIdx.x * 8);
   const int t0 = c * C, nr = min(C, T - t0);
   const __bf16* kc = k + ((size_t)bh * T + t0) * DKEY;
-  // the keys in 16-byte row segments (eight contiguous 1 KB loads per wave and half, rows past T as zeros), staged
-  // in the N and X block areas, which nothing uses before N is formed; then this lane's operand rows i, 16 + i,
-  // 32 + i, 48 + i
+  // the keys in 16-byte row segments (two per thread and tile, rows past T as zeros), staged in the N and X block
+  // areas, which nothing uses before N is formed
   __bf16* Kst = reinterpret_cast<__bf16*>(NX);
   static_assert(KH * TILE * sizeof(__bf16) <= sizeof(NX), "the key tiles fit the N and X block areas");
+  {
+    bf16x8 seg[2 * KH];
 #pragma unroll
-  for (int h = 0; h < KH; ++h) {
-    bf16x8 seg[8];
+    for (int n = 0; n < 2 * KH; ++n) seg[n] = load_seg(kc + 64 * (n >> 1), nr, tid + 256 * (n & 1), DKEY);
 #pragma unroll
-    for (int n = 0; n < 8; ++n) seg[n] = load_seg(kc + 64 * h, nr, l + 64 * n, DKEY);
-#pragma unroll
-    for (int n = 0; n < 8; ++n) put_seg(Kst + h * TILE, seg[n], l + 64 * n);
+    for (int n = 0; n < 2 * KH; ++n) put_seg(Kst + (n >> 1) * TILE, seg[n], tid + 256 * (n & 1));
   }
-  const float lav = l < nr ? la[(size_t)bh * T + t0 + l] : 0.f;
-  const float bev = l < nr ? be[(size_t)bh * T + t0 + l] : 0.f;
-  Ls[l] = incl_scan64(lav, l);
-  bs[l] = bev;
+  if (w == 0) {
+    const float lav = l < nr ? la[(size_t)bh * T + t0 + l] : 0.f;
+    const float bev = l < nr ? be[(size_t)bh * T + t0 + l] : 0.f;
+    Ls[l] = incl_scan64(lav, l);
+    bs[l] = bev;
+  }
   __syncthreads();
-  PGN_STAMP_AUX(blockIdx.x * 8 + 2);
-  bf16x8 kf[4][2 * KH];
-#pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-    for (int m = 0; m < 2 * KH; ++m) kf[rb][m] = frag(Kst + (m >> 1) * TILE, 16 * rb + i, m & 1, g);
-  __syncthreads();  // every key operand is in registers before N overwrites the staged keys
+  if (w == 0) PGN_STAMP_AUX(blockIdx.x * 8 + 2);
 
-  // N^T blocks: accumulator rows s (block sb), lane t (block tb), for sb <= tb
+  // N^T blocks: accumulator rows s (block sb), lane t (block tb), for sb <= tb; formed in registers, written once
+  // every wave has read its key operands (N overwrites the staged keys)
+  f32x4 nv[3];
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int t = 16 * tb + i;
-    const float Lt = Ls[t], bt = bs[t];
-#pragma unroll
-    for (int sb = 0; sb <= tb; ++sb) {
+  for (int n = 0; n < 3; ++n) {
+    const int tb = kInvNT[w][n], sb = kInvNS[w][n];
+    nv[n] = zero4();
+    if (tb >= 0) {
       f32x4 acc = zero4();
 #pragma unroll
-      for (int m = 0; m < 2 * KH; ++m) acc = pgn_mfma(kf[sb][m], kf[tb][m], acc);
-      float* nb = NT + blk(tb, sb);
+      for (int m = 0; m < 2 * KH; ++m)
+        acc = pgn_mfma(frag(Kst + (m >> 1) * TILE, 16 * sb + i, m & 1, g),
+                       frag(Kst + (m >> 1) * TILE, 16 * tb + i, m & 1, g), acc);
+      const int t = 16 * tb + i;
+      const float Lt = Ls[t], bt = bs[t];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int s = 16 * sb + 4 * g + r;
-        nb[(4 * g + r) * BP + i] = bt * acc[r] * masked_decay(Lt - Ls[s], s < t);
+        nv[n][r] = bt * acc[r] * masked_decay(Lt - Ls[s], s < t);
       }
     }
   }
   __syncthreads();
-  PGN_STAMP_AUX(blockIdx.x * 8 + 3);
+#pragma unroll
+  for (int n = 0; n < 3; ++n) {
+    const int tb = kInvNT[w][n], sb = kInvNS[w][n];
+    if (tb >= 0) {
+      float* nb = NT + blk(tb, sb);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) nb[(4 * g + r) * BP + i] = nv[n][r];
+    }
+  }
+  __syncthreads();
+  if (w == 0) PGN_STAMP_AUX(blockIdx.x * 8 + 3);
 
-  // X by blocks of 16: X_ii = (I + N_ii)^-1 by forward substitution, one column of one diagonal block per lane; then
-  // X_ij = -X_ii sum_{k=j}^{i-1} N_ik X_kj, i > j, level by level (i - j = 1, 2, 3), on fp32 MFMA
-  // (v_mfma_f32_16x16x4f32: A[r][k] in lane r + 16k, B[k][c] in lane c + 16k, D[4g + e][c] in lane c + 16g).
-  {
+  // X by blocks of 16: X_ii = (I + N_ii)^-1 by forward substitution, one column of one diagonal block per lane of
+  // wave 0; then X_ij = -X_ii sum_{k=j}^{i-1} N_ik X_kj, i > j, level by level (i - j = 1, 2, 3), product j on wave
+  // j, on fp32 MFMA (v_mfma_f32_16x16x4f32: A[r][k] in lane r + 16k, B[k][c] in lane c + 16k, D[4g + e][c] in lane
+  // c + 16g).
+  if (w == 0) {
     const int b = l >> 4, cl = l & 15;
     const float* nd = NT + blk(b, b);
     float xd[16];
@@ -198,7 +214,7 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
     for (int t = 0; t < 16; ++t) xb[t * BP + cl] = xd[t];
   }
   __syncthreads();
-  PGN_STAMP_AUX(blockIdx.x * 8 + 4);
+  if (w == 0) PGN_STAMP_AUX(blockIdx.x * 8 + 4);
   {
     const int r16 = l & 15, k4 = l >> 4;
     // one 16 x 16 x 16 product A B accumulated onto acc: A the block at `Ab`, read transposed when `at`
@@ -212,26 +228,20 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
       }
       return acc;
     };
+    const int jb = w;
 #pragma unroll
     for (int d = 1; d < 4; ++d) {
-      f32x4 Tacc[3];
-#pragma unroll
-      for (int jb = 0; jb + d < 4; ++jb) {
-        const int ib = jb + d;
+      const int ib = jb + d;
+      if (ib < 4) {
         f32x4 acc = zero4();
-        // N_ik = (N^T block (ib, kb)) transposed
+        // N_ik = (N^T block (ib, kb)) transposed, kb = jb .. ib - 1
 #pragma unroll
-        for (int kb = jb; kb < ib; ++kb) acc = mm(acc, NT + blk(ib, kb), true, Xf + blk(kb, jb));
-        Tacc[jb] = acc;
+        for (int u = 0; u < d; ++u) acc = mm(acc, NT + blk(ib, jb + u), true, Xf + blk(jb + u, jb));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Tt[jb * BLK + (4 * k4 + e) * BP + r16] = acc[e];
       }
-#pragma unroll
-      for (int jb = 0; jb + d < 4; ++jb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) Tt[jb * BLK + (4 * k4 + e) * BP + r16] = Tacc[jb][e];
       __syncthreads();
-#pragma unroll
-      for (int jb = 0; jb + d < 4; ++jb) {
-        const int ib = jb + d;
+      if (ib < 4) {
         const f32x4 xr = mm(zero4(), Xf + blk(ib, ib), false, Tt + jb * BLK);
         float* xo = Xf + blk(ib, jb);
 #pragma unroll
@@ -240,12 +250,12 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
       __syncthreads();
     }
   }
-  PGN_STAMP_AUX(blockIdx.x * 8 + 5);
-  // X (bf16, row-major; zero above the diagonal blocks) in 16-byte row segments
+  if (w == 0) PGN_STAMP_AUX(blockIdx.x * 8 + 5);
+  // X (bf16, row-major; zero above the diagonal blocks) in 16-byte row segments, two per thread
   __bf16* Xc = X + ((size_t)bh * NC + c) * C * C;
 #pragma unroll
-  for (int n = 0; n < 8; ++n) {
-    const int e = l + 64 * n, r = e >> 3, c0 = 8 * (e & 7);
+  for (int n = 0; n < 2; ++n) {
+    const int e = tid + 256 * n, r = e >> 3, c0 = 8 * (e & 7);
     const int rb = r >> 4, cb = c0 >> 4;
     bf16x8 out;
     if (cb <= rb) {
@@ -258,7 +268,7 @@ __global__ __launch_bounds__(64) void aspin_delta_inv(const __bf16* __restrict__
     }
     *reinterpret_cast<bf16x8*>(Xc + r * C + c0) = out;
   }
-  PGN_STAMP_CLOCKS_AUX(blockIdx.x * 8 + 6);
+  if (w == 0) PGN_STAMP_CLOCKS_AUX(blockIdx.x * 8 + 6);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -828,6 +838,11 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
   const size_t roff = R.rows(T) + (size_t)t0 * DKEY;  // the chunk's q, k, dq, dk rows
   const size_t voff = R.vals(T) + (size_t)t0 * DKEY;  // the chunk's W, dO, drhs, dv rows
   const size_t toff = R.stateT(NC, c);                // this scan's rows of the transposed states
+  // instrumented build: 40 entries per workgroup, per wave its entry (0-7), tiles in LDS (8-15), past the barrier
+  // (16-23) and end (24-31); wave 0's shader and 100 MHz clocks at entry (32, 33) and end (34, 35)
+#define DL_STAMP(k) PGN_STAMP_AUX(blockIdx.x * 40 + (k) + w)
+  DL_STAMP(0);
+  if (w == 0) PGN_STAMP_CLOCKS_AUX(blockIdx.x * 40 + 32);
 
   {
     // every tile staged untransposed, thread tid carrying 16-byte row segment tid of each (operands contracted over
@@ -849,6 +864,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
     }
 #pragma unroll
     for (int u = 0; u < NT; ++u) put_seg(Qs + u * TILE, sg[u], tid);
+    DL_STAMP(8);
     {
       // dV = beta drhs, row segment tid (the chain kernel rounds drhs to bf16 once; dV rounds its product again)
       const int r = tid >> 3;
@@ -868,6 +884,7 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
     }
   }
   __syncthreads();
+  DL_STAMP(16);
   auto dpart = [&](auto wl_c) {
     constexpr int WL = decltype(wl_c)::value;
     const int me = 16 * WL + i;
@@ -1081,6 +1098,9 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
       R.slot(dbe, dbe1)[ti] = r0 + dbe2[t];
     }
   }
+  DL_STAMP(24);
+  if (w == 0) PGN_STAMP_CLOCKS_AUX(blockIdx.x * 40 + 34);
+#undef DL_STAMP
 }
 
 // The slot sums of the 128-wide backward: x[p][i] <- x[p][i] + y[p][i] for the bf16 pairs (dq, dk; the fp32 sum of
@@ -1173,7 +1193,7 @@ int delta_fwd(const void* q, const void* k, const void* v, const float* la, cons
               hipStream_t st) {
   const int NC = (int)((T + C - 1) / C);
   const int heads = (int)(B * H);
-  hipLaunchKernelGGL(aspin_delta_inv<KH>, dim3((unsigned)(heads * NC)), dim3(64), 0, st, (const __bf16*)k, la, beta,
+  hipLaunchKernelGGL(aspin_delta_inv<KH>, dim3((unsigned)(heads * NC)), dim3(256), 0, st, (const __bf16*)k, la, beta,
                      (__bf16*)X, (int)T, NC);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
