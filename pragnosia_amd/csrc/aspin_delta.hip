@@ -104,11 +104,23 @@ PGN_DEVICE void chunk_decays(float la_l, int l, float* Ls, float* eLs, float* ws
 // six chunks (one round of the grid at cfg2, 24 waves) are resident per compute unit. The keys (KH 64-wide tiles) are
 // loaded in 16-byte row segments into the N and X block areas (unused until N is formed) and read from there as MFMA
 // operands. The waves share the independent work of each phase: the ten N blocks (three, three, two, two), the
-// products of each block level (one per wave), the staging and the store; the four diagonal blocks' substitutions
-// are wave 0's (one column per lane). Each block is computed exactly as by one wave, so X does not depend on the split.
+// products of each block level (one per wave), the four diagonal blocks' substitutions (one per wave, four lanes per
+// column), the staging and the store. Each entry is computed by the same operations in the same order as by one wave,
+// so X does not depend on the split.
 constexpr int BP = 16;                 // row pitch of a 16 x 16 fp32 block
 constexpr int BLK = 16 * BP;
 PGN_DEVICE int blk(int tb, int sb) { return (tb * (tb + 1) / 2 + sb) * BLK; }
+
+// x of lane q of each group of four lanes, in all four (q a compile-time constant once the caller's loop unrolls)
+PGN_DEVICE float quad_bcast(float x, int q) {
+  const int v = __builtin_bit_cast(int, x);
+  switch (q) {
+    case 0: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x00, 0xf, 0xf, false));
+    case 1: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x55, 0xf, 0xf, false));
+    case 2: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0xAA, 0xf, 0xf, false));
+    default: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0xFF, 0xf, 0xf, false));
+  }
+}
 
 // the N blocks (tb, sb) of wave w, -1 past its share
 __constant__ const signed char kInvNT[4][3] = {{3, 3, 0}, {3, 1, 1}, {3, 2, -1}, {2, 2, -1}};
@@ -188,30 +200,46 @@ __global__ __launch_bounds__(256) void aspin_delta_inv(const __bf16* __restrict_
   __syncthreads();
   if (w == 0) PGN_STAMP_AUX(blockIdx.x * 8 + 3);
 
-  // X by blocks of 16: X_ii = (I + N_ii)^-1 by forward substitution, one column of one diagonal block per lane of
-  // wave 0; then X_ij = -X_ii sum_{k=j}^{i-1} N_ik X_kj, i > j, level by level (i - j = 1, 2, 3), product j on wave
-  // j, on fp32 MFMA (v_mfma_f32_16x16x4f32: A[r][k] in lane r + 16k, B[k][c] in lane c + 16k, D[4g + e][c] in lane
-  // c + 16g).
-  if (w == 0) {
-    const int b = l >> 4, cl = l & 15;
-    const float* nd = NT + blk(b, b);
-    float xd[16];
+  // X by blocks of 16: X_ii = (I + N_ii)^-1 by forward substitution, diagonal block i on wave i; then
+  // X_ij = -X_ii sum_{k=j}^{i-1} N_ik X_kj, i > j, level by level (i - j = 1, 2, 3), product j on wave j, on fp32
+  // MFMA (v_mfma_f32_16x16x4f32: A[r][k] in lane r + 16k, B[k][c] in lane c + 16k, D[4g + e][c] in lane c + 16g).
+  {
+    // diagonal block b = w, column cl = l / 4 on four lanes, lane q = l % 4 holding rows t = 4 m + q; row s's value,
+    // final after step s - 1, reaches the column's four lanes by a quad broadcast (DPP) before step s
+    const int cl = l >> 2, q = l & 3;
+    const float* nd = NT + blk(w, w);
+    float xr[4];
 #pragma unroll
-    for (int t = 0; t < 16; ++t) xd[t] = (t == cl) ? 1.f : 0.f;
+    for (int m = 0; m < 4; ++m) xr[m] = (4 * m + q == cl) ? 1.f : 0.f;
+    // N[16w + t][16w + s] for the lane's rows and the four steps of a group, read a group ahead and unconditionally
+    // (the row condition selects the updated value, not the read, so the reads are not sunk into it)
+    float nb[2][4][4];
+    auto read_group = [&](int k, float (&dst)[4][4]) {
 #pragma unroll
-    for (int s = 0; s < 15; ++s) {
-      const float xs = xd[s];
+      for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int t4 = (s + 1) & ~3; t4 < 16; t4 += 4) {
-        const f32x4 n = *reinterpret_cast<const f32x4*>(nd + s * BP + t4);  // N[16b + t][16b + s], t = t4..
+        for (int m = 0; m < 4; ++m) dst[u][m] = (4 * k + u < 15) ? nd[(4 * k + u) * BP + 4 * m + q] : 0.f;
+    };
+    read_group(0, nb[0]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (t4 + u > s) xd[t4 + u] -= n[u] * xs;
+    for (int k = 0; k < 4; ++k) {
+      if (k < 3) read_group(k + 1, nb[(k + 1) & 1]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = 4 * k + u;
+        if (s < 15) {
+          const float xs = quad_bcast(xr[s >> 2], s & 3);
+#pragma unroll
+          for (int m = (s + 1) >> 2; m < 4; ++m) {
+            const float upd = xr[m] - nb[k & 1][u][m] * xs;
+            xr[m] = (4 * m + q > s) ? upd : xr[m];
+          }
+        }
       }
     }
-    float* xb = Xf + blk(b, b);
+    float* xb = Xf + blk(w, w);
 #pragma unroll
-    for (int t = 0; t < 16; ++t) xb[t * BP + cl] = xd[t];
+    for (int m = 0; m < 4; ++m) xb[(4 * m + q) * BP + cl] = xr[m];
   }
   __syncthreads();
   if (w == 0) PGN_STAMP_AUX(blockIdx.x * 8 + 4);
