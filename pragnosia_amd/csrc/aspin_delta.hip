@@ -153,14 +153,15 @@ __global__ __launch_bounds__(256) void aspin_delta_inv(const __bf16* __restrict_
     bf16x8 seg[2 * KH];
 #pragma unroll
     for (int n = 0; n < 2 * KH; ++n) seg[n] = load_seg(kc + 64 * (n >> 1), nr, tid + 256 * (n & 1), DKEY);
+    // this lane's decay and strength, issued with the keys (range-checked: zero past T, no branch)
+    const float lav = load_f32_lane(la + (size_t)bh * T + t0, nr, l);
+    const float bev = load_f32_lane(be + (size_t)bh * T + t0, nr, l);
 #pragma unroll
     for (int n = 0; n < 2 * KH; ++n) put_seg(Kst + (n >> 1) * TILE, seg[n], tid + 256 * (n & 1));
-  }
-  if (w == 0) {
-    const float lav = l < nr ? la[(size_t)bh * T + t0 + l] : 0.f;
-    const float bev = l < nr ? be[(size_t)bh * T + t0 + l] : 0.f;
-    Ls[l] = incl_scan64(lav, l);
-    bs[l] = bev;
+    if (w == 0) {
+      Ls[l] = incl_scan64(lav, l);
+      bs[l] = bev;
+    }
   }
   __syncthreads();
   if (w == 0) PGN_STAMP_AUX(blockIdx.x * 8 + 2);
@@ -872,6 +873,10 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
   DL_STAMP(0);
   if (w == 0) PGN_STAMP_CLOCKS_AUX(blockIdx.x * 40 + 32);
 
+  // the chunk's per-token vectors, issued right after the tiles and range-checked (zero past the chunk's end, no
+  // branch), so no wave waits on a global load after a barrier: this thread's dV row strength, and this lane's decay,
+  // strength and rsum pair (the decay scan and the final dla on wave 0)
+  float bt_row, lav, bev, r0, r1;
   {
     // every tile staged untransposed, thread tid carrying 16-byte row segment tid of each (operands contracted over
     // a tile's row index use the LDS transpose read)
@@ -890,25 +895,32 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
       else src = drhs + voff;
       sg[u] = load_seg(src, rows, tid, DKEY);
     }
+    {
+      const __amdgpu_buffer_rsrc_t bv = f32_view(be + R.tok(T) + t0, nr);
+      const __amdgpu_buffer_rsrc_t rv = f32_view(rsum + ((size_t)sc * T + t0) * 2, 2 * nr);
+      bt_row = load_f32(bv, tid >> 3);
+      lav = load_f32(f32_view(la + R.tok(T) + t0, nr), x.l);
+      bev = load_f32(bv, x.l);
+      r0 = load_f32(rv, 2 * x.l);
+      r1 = load_f32(rv, 2 * x.l + 1);
+    }
 #pragma unroll
     for (int u = 0; u < NT; ++u) put_seg(Qs + u * TILE, sg[u], tid);
     DL_STAMP(8);
     {
-      // dV = beta drhs, row segment tid (the chain kernel rounds drhs to bf16 once; dV rounds its product again)
-      const int r = tid >> 3;
-      if (r < nr) {
-        const float bt = be[R.tok(T) + t0 + r];
-        bf16x8 dvs;
+      // dV = beta drhs, row segment tid (the chain kernel rounds drhs to bf16 once; dV rounds its product again);
+      // rows past the end of a partial chunk fall outside the store's range and are dropped
+      bf16x8 dvs;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dvs[e] = (__bf16)(bt * (float)sg[NT - 1][e]);
-        *reinterpret_cast<bf16x8*>(dv + voff + (size_t)r * DKEY + 8 * (tid & 7)) = dvs;
-      }
+      for (int e = 0; e < 8; ++e) dvs[e] = (__bf16)(bt_row * (float)sg[NT - 1][e]);
+      const __amdgpu_buffer_rsrc_t dv_out = __builtin_amdgcn_make_buffer_rsrc(
+          dv + voff, (short)0, nr * DKEY * (int)sizeof(__bf16), 0x00020000);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, dvs), dv_out,
+                                             ((tid >> 3) * DKEY + 8 * (tid & 7)) * (int)sizeof(__bf16), 0, 0);
     }
     if (w == 0) {
-      const bool ok = x.l < nr;
-      const float lav = ok ? la[R.tok(T) + t0 + x.l] : 0.f;
       chunk_decays(lav, x.l, Ls, eLs, ws);
-      bs[x.l] = ok ? be[R.tok(T) + t0 + x.l] : 0.f;
+      bs[x.l] = bev;
     }
   }
   __syncthreads();
@@ -1112,8 +1124,6 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
   if (w == 0) {
     const int t = x.l;
     const bool ok = t < nr;
-    const size_t ri = (size_t)sc * T + t0 + t;  // this scan's rsum entry
-    const float r0 = ok ? rsum[ri * 2 + 0] : 0.f, r1 = ok ? rsum[ri * 2 + 1] : 0.f;
     const float wdw = ws[t] * dwv[t];
     float dL = rowT[t] - colS[t] + eLs[t] * r1 - wdw;
     const float tot = wave_sum(wdw);
