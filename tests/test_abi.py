@@ -167,3 +167,23 @@ def test_noalloc_limit_checked_on_host(L):
     assert L.pragnosia_aspin_chunk_fwd_seg_noalloc(*args(1, 1, 1000, 0, 0, null)) == -1      # empty segments
     assert L.pragnosia_aspin_chunk_fwd_seg_noalloc(*args(1, 1, 1000, 192, 3, null)) == -1    # window without theta
     assert L.pragnosia_error_string(-3).startswith(b"shape needs more scratch")
+
+
+def test_exact_value_blocks_past_the_lds_refused_on_host(L):
+    """The exact scan's backward refuses, before any launch, a value width one wave past the widest block that
+    `ops.exact_value_cap` gives (its block buffers would exceed the 160 KiB of LDS: PRAGNOSIA_ERR_UNSUPPORTED), at
+    the key widths and operand types where that block is narrower than 128; with the GPU test that runs the cap
+    itself, this pins the host-side mirror of the kernel's LDS formula."""
+    import torch
+    from pragnosia_amd.ops import exact_value_cap
+    null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    checked = 0
+    for dk in (128, 176, 192, 300, 384):
+        for dt, code in ((torch.float32, 0), (torch.float64, 1)):
+            cap = exact_value_cap(dk, dt, True)
+            if cap >= 128:
+                continue
+            args = [one] * 4 + [null, one, null, one, null] + [one] * 4 + [null, null] + [1, 1, 16, dk, cap + 16, code, null]
+            assert L.pragnosia_aspin_exact_bwd(*args) == -2, (dk, dt, cap)
+            checked += 1
+    assert checked >= 5

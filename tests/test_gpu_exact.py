@@ -216,3 +216,23 @@ def test_repeated_calls_are_deterministic(scan):
     y1, S1 = scan(*dev[:4], dev[5], beta=dev[4])
     y2, S2 = scan(*dev[:4], dev[5], beta=dev[4])
     assert torch.equal(y1, y2) and torch.equal(S1, S2)
+
+
+@pytest.mark.parametrize("Dk,dtype", [(384, torch.float32), (128, torch.float64), (192, torch.float64),
+                                      (384, torch.float64)])
+def test_value_cap_is_the_library_limit(Dk, dtype):
+    """`ops.exact_value_cap` is the library's own limit: one launch at exactly that many value columns runs forward
+    and backward (delta rule, finite results), and one wave more is refused by the backward."""
+    from pragnosia_amd import ops
+    from pragnosia_amd._lib import PragnosiaError
+    cap = ops.exact_value_cap(Dk, dtype, True)
+    assert cap < 128
+    q, k, v, la, be, S0, _, _ = _fp32_case(1, 1, 20, Dk, cap + 16, True, seed=Dk)
+    dev = lambda t: t.to(dtype).cuda()
+    q, k, la, be = dev(q), dev(k), dev(la), dev(be)
+    o, S, ckpt, resid = ops.aspin_exact(q, k, dev(v[..., :cap]), la, be, None, True)
+    g = ops.aspin_exact_bwd(q, k, dev(v[..., :cap]), la, be, ckpt, resid, torch.ones_like(o), None)
+    assert all(torch.isfinite(t).all() for t in (o, S) + tuple(g))
+    o2, S2, ckpt2, resid2 = ops.aspin_exact(q, k, dev(v), la, be, None, True)
+    with pytest.raises(PragnosiaError):
+        ops.aspin_exact_bwd(q, k, dev(v), la, be, ckpt2, resid2, torch.ones_like(o2), None)
