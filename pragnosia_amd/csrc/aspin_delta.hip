@@ -683,8 +683,10 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_chain(
           __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (__bf16)acc[r]), dr_out,
                                                 (tl * DKEY + j) * (int)sizeof(__bf16), 0, 0);
         }
-        const float tot = row_totals16x8(pr, i);  // lane i: the total of pr[(i >> 1) & 7]
-        if (!(i & 1)) ((i & 8) ? redU : redV)[w * C + 16 * tb + 4 * g + ((i >> 1) & 3)] = tot;
+        // lane i: the total of pr[(i >> 1) & 7], equal in lanes i and i ^ 1 (the last butterfly step adds the same
+        // two values in either order), so both write it: no branch splits the chunk's scheduling region
+        const float tot = row_totals16x8(pr, i);
+        ((i & 8) ? redU : redV)[w * C + 16 * tb + 4 * g + ((i >> 1) & 3)] = tot;
       }
       // dS_prev = a dS + (Q o eL)^T dO + K^T dU
       const float a_c = __expf(Ls[C - 1]);
