@@ -61,6 +61,16 @@ __global__ __launch_bounds__(256) void aspin_decode(const float* S, float* Sout,
   const int tid = threadIdx.x, j = tid & 63, rg = tid >> 6;
   const size_t voff = (size_t)bh * D;
   const float* prow = FROM_P ? in.P + (size_t)b * in.np : nullptr;
+  // the state slice, the rotation frequencies and p0 first: nothing below depends on them until the rotation, so
+  // their latency overlaps the projections' loads and the normalisation
+  const float* Sbh = S + (size_t)bh * D * D;
+  float x[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) x[r] = Sbh[(16 * rg + r) * D + j];
+  float thv[8];
+#pragma unroll
+  for (int pr = 0; pr < 8; ++pr) thv[pr] = theta[h * (D / 2) + 8 * rg + pr];
+  const float p0 = p0d ? *p0d : p0h;
 
   float la_v, gl_v = 0.f, be_v = 0.f;
   bool has_g, has_b;
@@ -92,16 +102,11 @@ __global__ __launch_bounds__(256) void aspin_decode(const float* S, float* Sout,
     if (rg == 1 && has_g) inv *= 1.f / (1.f + __expf(-gl_v));
     (rg == 0 ? qs : (rg == 1 ? ks : vs))[j] = x * inv;
   }
-  const float p0 = p0d ? *p0d : p0h;
   const float a = __expf(la_v);
-  const float* Sbh = S + (size_t)bh * D * D;
-  float x[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) x[r] = Sbh[(16 * rg + r) * D + j];
 #pragma unroll
   for (int pr = 0; pr < 8; ++pr) {
     float s, c;
-    sincosf(-p0 * theta[h * (D / 2) + 8 * rg + pr], &s, &c);
+    sincosf(-p0 * thv[pr], &s, &c);
     const float e = x[2 * pr], f = x[2 * pr + 1];
     x[2 * pr] = a * (e * c - f * s);
     x[2 * pr + 1] = a * (e * s + f * c);
