@@ -815,18 +815,23 @@ def cpu_baselines_more(args, seconds=5.0):
     torch.manual_seed(4)
     sd = {k: v.detach() for k, v in LM(vocab=8192, d=768, layers=12, mlp_mult=4, ctx=512,
                                          mixer="aspin").state_dict().items()}
-    prompt = torch.randint(0, 8192, (1, 16), generator=g)
-    steps = 8
+    prompt = torch.randint(0, 8192, (1, 64), generator=g)
+    n1, n2 = 8, 72
 
-    def decode_it():
+    def decode_run(steps):
         with torch.inference_mode():
+            t0 = time.perf_counter()
             OM.greedy_decode(sd, prompt, steps, layers=12, mixer="aspin", heads=12)
+            return time.perf_counter() - t0
 
-    rate, med, n = _median_rate(decode_it, seconds, 1)
-    # the prefill of 16 tokens is part of each timed run; it is charged to the decode steps (an upper bound)
-    out["decode_cfg4_bs1"] = {"value": round(med / steps * 1e3, 3), "unit": "ms/token", "kind": "port",
-                              "sample": f"92M LM, prefill 16 + {steps} greedy T=1 steps at batch 1, fp32, oracle "
-                                        f"(torch CPU) path, {n} runs, median, prefill charged to the steps"}
+    decode_run(n1)
+    t1 = sorted(decode_run(n1) for _ in range(3))[1]
+    t2 = sorted(decode_run(n2) for _ in range(3))[1]
+    # the same prefill in both runs: the difference of the medians is the cost of n2 - n1 steps, prefill excluded
+    out["decode_cfg4_bs1"] = {"value": round((t2 - t1) / (n2 - n1) * 1e3, 3), "unit": "ms/token", "kind": "port",
+                              "sample": f"92M LM at batch 1, fp32, oracle (torch CPU) T=1 steps: median time of "
+                                        f"prefill 64 + {n2} greedy steps minus that of prefill 64 + {n1} steps, "
+                                        f"over {n2 - n1} steps (3 runs each)"}
     return out
 
 

@@ -242,8 +242,10 @@ extern "C" int pragnosia_wgrad_bf16(const void* A, int64_t lda, const void* B, i
   PGN_CHECK_ARG(lda >= M && ldb >= N && ldc >= N && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0);
   PGN_CHECK_ARG(((uintptr_t)A % 16) == 0 && ((uintptr_t)B % 16) == 0 && ((uintptr_t)C % 16) == 0);
   const Split sp = choose_split(M, N, K);
-  // each split's rows are addressed through a buffer resource with 32-bit byte offsets
-  PGN_CHECK_ARG(sp.len * std::max(lda, ldb) * (int64_t)sizeof(uint16_t) < ((int64_t)1 << 31));
+  // each split's rows are addressed through a buffer resource with 32-bit byte offsets: the largest offset a load
+  // forms is at row len + 3 KS (the ring's look-ahead past the rounded-up last step), columns up to max(M, N) + 128
+  PGN_CHECK_ARG(((sp.len + 3 * KS) * std::max(lda, ldb) + std::max(M, N) + 128) * (int64_t)sizeof(uint16_t) <
+                ((int64_t)1 << 31));
   const int64_t need = partial_bytes(M, N, K);
   PGN_CHECK_ARG(workspace_bytes >= need && (need == 0 || (workspace && ((uintptr_t)workspace % 16) == 0)));
   hipStream_t st = (hipStream_t)stream;

@@ -49,10 +49,16 @@ def fused_decode_ok(model) -> bool:
 
 
 class GreedyDecoder:
-    def __init__(self, model, batch: int, steps_per_graph: int = 8, fused: bool | None = None):
+    def __init__(self, model, batch: int, steps_per_graph: int = 8, fused: bool | None = None,
+                 record_logits: bool = False):
+        """record_logits: the captured step also writes each step's logits (fp32) into a device buffer of
+        (n + steps_per_graph, batch, vocab), read with `logits(n)`; for checking the graphed path itself against a
+        reference decode, at the cost of one (batch, vocab) copy a step."""
         self.m = model
         self.B = batch
         self.K = steps_per_graph
+        self.record = record_logits
+        self.lgs = None
         self.graph = None
         self.fused = fused_decode_ok(model) if fused is None else fused
         if self.fused and not fused_decode_ok(model):
@@ -101,6 +107,8 @@ class GreedyDecoder:
         self.pos.copy_((self.pos + 1) % m.ctx)
         lg = F.linear(m.n(h), m.e.weight)[:, -1]
         nxt = lg.argmax(-1)
+        if self.lgs is not None:
+            self.lgs.index_copy_(0, self.ctr, lg.float().view(1, self.B, -1))
         self.out.index_copy_(0, self.ctr, nxt.view(1, -1))
         self.ctr.add_(1)
         self.tok.copy_(nxt.view(-1, 1))
@@ -173,6 +181,8 @@ class GreedyDecoder:
         self.pos.copy_((self.pos + 1) % m.ctx)
         lg = self._dense(h, m.e.weight, m.n)
         nxt = lg.argmax(-1)
+        if self.lgs is not None:
+            self.lgs.index_copy_(0, self.ctr, lg.float().view(1, self.B, -1))
         self.out.index_copy_(0, self.ctr, nxt.view(1, -1))
         self.ctr.add_(1)
         self.tok.copy_(nxt.view(-1, 1))
@@ -187,6 +197,8 @@ class GreedyDecoder:
         self.pos = torch.zeros(1, dtype=torch.long, device=dev)
         self.out = torch.zeros(n_max + self.K, self.B, dtype=torch.long, device=dev)
         self.ctr = torch.zeros(1, dtype=torch.long, device=dev)
+        if self.record:
+            self.lgs = torch.zeros(n_max + self.K, self.B, self.m.e.weight.shape[0], dtype=torch.float32, device=dev)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         step = self._one_step_fused if self.fused else self._one_step
@@ -215,6 +227,9 @@ class GreedyDecoder:
         first = lg.argmax(-1)
         self.out.zero_()
         self.out[0].copy_(first)
+        if self.lgs is not None:
+            self.lgs.zero_()
+            self.lgs[0].copy_(lg.float())
         self.ctr.fill_(1)
         self.tok.copy_(first.view(-1, 1))
 
@@ -223,6 +238,13 @@ class GreedyDecoder:
         """Run ceil((n - 1) / steps_per_graph) graph replays (the first token came from the prefill's logits)."""
         for _ in range(-(-(n - 1) // self.K)):
             self.graph.replay()
+
+    def logits(self, n):
+        """With record_logits: the logits each of the last run's first n tokens was chosen from, (batch, n, vocab)
+        (step 0's are the prefill's)."""
+        if self.lgs is None:
+            raise ValueError("GreedyDecoder: constructed without record_logits")
+        return self.lgs[:n].transpose(0, 1)
 
     @torch.no_grad()
     def generate(self, prompt, n):

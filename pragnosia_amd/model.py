@@ -15,8 +15,8 @@ Constructor arguments, module names and initialisation follow the reference (`sr
     "fspin"   SpinCarrier(d, gated="rf")                           forget-gated complex diagonal carrier
 
 (`src/model.py:632-660`.) The mixers run on the HIP kernels: heads of 64 and 128 on the bf16 MFMA scans, other head
-widths on the exact fp32 scan (the plain rule in key and value blocks of at most 128, so any width; the delta rule up
-to 128). Embeddings, LayerNorms, the MLPs and the tied head are torch. Attention, the hybrid stacks and the other
+widths on the exact fp32 scan (the plain rule at any width, in key blocks of at most 128; the delta rule with keys up
+to 384; value columns split to fit the LDS). Embeddings, LayerNorms, the MLPs and the tied head are torch. Attention, the hybrid stacks and the other
 reference mixers are outside this build and raise. `short_conv=K` adds every carrier's short causal convolution
 (`src/model.py:717-726`).
 """

@@ -64,6 +64,44 @@ def main(ref: str) -> None:
     np.savez_compressed(os.path.join(HERE, "modules.npz"), **out)
     for k, v in out.items():
         print(k, v.shape, float(np.abs(v).max()))
+    options(AssocCarrier, LM)
+
+
+def options(AssocCarrier, LM) -> None:
+    """tests/golden/options.npz: the carrier's options (key_topk, hl_floor, write_all, pos_wrap, beta_scale, head
+    dim 128, alone or combined as the mixers combine them), each with a carried state at a position offset: the
+    output, the final state and the input gradient under a seeded upstream gradient (the reference's fp32 autograd
+    through its torch path); and the dspin LM's forward and forward_carried."""
+    out = {}
+    o = P.OPT
+    for name, c in P.OPTIONS.items():
+        m = AssocCarrier(c["d"], heads=c["heads"], delta=c["delta"], kernel=False, **c["ctor"])
+        P.fill_(m, P.option_seed(name))
+        x, S0, gy, bs = P.option_inputs(name)
+        if "pos_wrap" in c.get("attrs", {}):
+            m.pos_wrap = c["attrs"]["pos_wrap"]
+        if bs is not None:
+            m.beta_scale = bs
+        x = x.clone().requires_grad_(True)
+        y, (S, p) = m(x, (S0, o["p0"]))
+        assert p == o["T"]
+        (y * gy).sum().backward()
+        out[name + "_y"], out[name + "_S"], out[name + "_dx"] = y.detach().numpy(), S.detach().numpy(), x.grad.numpy()
+    c = P.LMCFG
+    torch.manual_seed(0)
+    lm = LM(vocab=c["vocab"], d=c["d"], layers=c["layers"], mlp_mult=c["mlp_mult"], ctx=c["ctx"], mixer="dspin")
+    for mod in lm.modules():
+        if hasattr(mod, "kernel"):
+            mod.kernel = False
+    P.fill_(lm, 45)
+    ids = P.ids(41, (c["B"], c["T"]), c["vocab"])
+    with torch.no_grad():
+        out["lm_dspin_logits"] = lm(ids[:, : c["ctx"]]).numpy()
+        out["lm_dspin_carried"] = lm.forward_carried(ids, window=c["window"]).numpy()
+    out = {k: v.astype(np.float32) for k, v in out.items()}
+    np.savez_compressed(os.path.join(HERE, "options.npz"), **out)
+    for k, v in out.items():
+        print(k, v.shape, float(np.abs(v).max()))
 
 
 if __name__ == "__main__":

@@ -146,6 +146,8 @@ def test_wgrad_workspace_and_rejections(L):
     mis = ctypes.c_void_p(24)
     assert L.pragnosia_wgrad_bf16(mis, 768, one, 768, one, 768, 0, one, 0, 768, 768, 12, null) == -1  # misaligned
     assert L.pragnosia_wgrad_bf16(*args(24, 16, 16, 0, 20, 16, 64)) == -1                          # M % 8
+    # a row pitch whose largest look-ahead offset (row len + 3 * 64) passes 2^31 bytes is refused
+    assert L.pragnosia_wgrad_bf16(*args(8_000_000, 8, 8, 0, 8, 8, 64)) == -1
 
 
 def test_product_never_imports_oracle():

@@ -77,3 +77,63 @@ def test_lm_matches_reference(mixer):
     carried = M.lm_forward_carried(sd, ids, c["window"], layers=c["layers"], mixer=mixer, heads=heads)
     assert rel(logits, G[f"lm_{mixer}_logits"]) < TOL
     assert rel(carried, G[f"lm_{mixer}_carried"]) < TOL
+
+
+OPT = np.load(os.path.join(HERE, "golden", "options.npz"))
+
+
+def option_case(name, build):
+    """(module built by `build(ctor kwargs)` and filled, x, S0, gy, beta_scale, la_floor, pos_wrap) for an option
+    case of tests/golden/options.npz."""
+    P = _params()
+    c = P.OPTIONS[name]
+    m = build(c)
+    P.fill_(m, P.option_seed(name))
+    x, S0, gy, bs = P.option_inputs(name)
+    return m, c, x, S0, gy, bs, P.option_la_floor(name), c.get("attrs", {}).get("pos_wrap")
+
+
+@pytest.mark.parametrize("name", list(_params().OPTIONS))
+def test_assoc_options_match_reference(name):
+    """The carrier's options (key_topk, hl_floor, write_all, pos_wrap, beta_scale, head dim 128, and the sparse wide
+    delta carrier) against the reference's own module: output, final state, and the input gradient under a seeded
+    upstream gradient (the reference's fp32 autograd), the oracle in fp64 autograd."""
+    from pragnosia_amd.assoc import AssocCarrier
+    m, c, x, S0, gy, bs, floor, wrap = option_case(
+        name, lambda c: AssocCarrier(c["d"], heads=c["heads"], delta=c["delta"], **c["ctor"]))
+    xd = x.double().requires_grad_(True)
+    y, (S, p) = M.assoc_carrier(_sd(m), xd, (S0.double(), _params().OPT["p0"]), heads=c["heads"], delta=c["delta"],
+                                write_all=c["ctor"].get("write_all", False), key_topk=c["ctor"].get("key_topk", 0),
+                                la_floor=floor, pos_wrap=wrap, beta_scale=None if bs is None else bs.double())
+    (y * gy.double()).sum().backward()
+    assert p == _params().OPT["T"]
+    assert rel(y - xd, OPT[name + "_y"] - x.numpy()) < TOL
+    assert rel(S, OPT[name + "_S"]) < TOL
+    assert rel(xd.grad - gy.double(), OPT[name + "_dx"] - gy.numpy()) < TOL
+
+
+def test_option_fixtures_exercise_their_branches():
+    """Each option changes the reference's output (so its fixture pins the branch, not the default path): the oracle
+    with the option switched off misses the fixture by far more than the tolerance."""
+    from pragnosia_amd.assoc import AssocCarrier
+    for name in ("topk", "hlfloor", "writeall", "poswrap", "delta_betascale", "delta_writeall"):
+        m, c, x, S0, gy, bs, floor, wrap = option_case(
+            name, lambda c: AssocCarrier(c["d"], heads=c["heads"], delta=c["delta"], **c["ctor"]))
+        y, _ = M.assoc_carrier(_sd(m), x.double(), (S0.double(), _params().OPT["p0"]), heads=c["heads"],
+                               delta=c["delta"])
+        assert rel(y - x.double(), OPT[name + "_y"] - x.numpy()) > 100 * TOL, name
+
+
+def test_lm_dspin_matches_reference():
+    """The delta-rule LM (mixer "dspin"): forward and forward_carried logits."""
+    P = _params()
+    from pragnosia_amd.model import LM
+    c = P.LMCFG
+    lm = LM(vocab=c["vocab"], d=c["d"], layers=c["layers"], mlp_mult=c["mlp_mult"], ctx=c["ctx"], mixer="dspin")
+    P.fill_(lm, 45)
+    ids = P.ids(41, (c["B"], c["T"]), c["vocab"])
+    sd = _sd(lm)
+    logits = M.lm_forward(sd, ids[:, : c["ctx"]], layers=c["layers"], mixer="dspin", heads=c["d"] // 64)
+    carried = M.lm_forward_carried(sd, ids, c["window"], layers=c["layers"], mixer="dspin", heads=c["d"] // 64)
+    assert rel(logits, OPT["lm_dspin_logits"]) < TOL
+    assert rel(carried, OPT["lm_dspin_carried"]) < TOL

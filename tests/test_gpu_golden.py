@@ -77,3 +77,54 @@ def test_lm_matches_reference(mixer, kernel, tol):
         carried = lm.forward_carried(ids, window=c["window"])
     assert rel(logits, G[f"lm_{mixer}_logits"]) < tol
     assert rel(carried, G[f"lm_{mixer}_carried"]) < tol
+
+
+OPT = np.load(os.path.join(HERE, "golden", "options.npz"))
+
+
+@pytest.mark.parametrize("kernel", [True, False])
+@pytest.mark.parametrize("name", list(_params().OPTIONS))
+def test_assoc_options_match_reference(name, kernel):
+    """The carrier's options against the reference's own module (tests/golden/options.npz; the oracle is held to the
+    same fixtures at 1e-4 in tests/test_golden_modules.py): output, final state and the input gradient under a seeded
+    upstream gradient. Kernel path (bf16 scan operands): 2e-2 on outputs and states, 5e-2 on the gradient; exact
+    path (kernel=False, fp32 scan): 1e-4."""
+    P = _params()
+    from pragnosia_amd.assoc import AssocCarrier
+    c = P.OPTIONS[name]
+    m = AssocCarrier(c["d"], heads=c["heads"], delta=c["delta"], kernel=kernel, **c["ctor"])
+    P.fill_(m, P.option_seed(name))
+    m = m.cuda()
+    x, S0, gy, bs = P.option_inputs(name)
+    if "pos_wrap" in c.get("attrs", {}):
+        m.pos_wrap = c["attrs"]["pos_wrap"]
+    if bs is not None:
+        m.beta_scale = bs.cuda()
+    xc = x.cuda().requires_grad_(True)
+    y, (S, p) = m(xc, (S0.cuda(), P.OPT["p0"]))
+    (y * gy.cuda()).sum().backward()
+    tol, gtol = (2e-2, 5e-2) if kernel else (1e-4, 1e-4)
+    assert p == P.OPT["T"]
+    assert rel(y - xc, OPT[name + "_y"] - x.numpy()) < tol
+    assert rel(S, OPT[name + "_S"]) < tol
+    assert rel(xc.grad - gy.cuda(), OPT[name + "_dx"] - gy.numpy()) < gtol
+
+
+@pytest.mark.parametrize("kernel,tol", [(True, 2e-2), (False, 1e-4)])
+def test_lm_dspin_matches_reference(kernel, tol):
+    """The delta-rule LM (mixer "dspin"): forward and forward_carried logits against the reference's."""
+    P = _params()
+    from pragnosia_amd.model import LM
+    c = P.LMCFG
+    lm = LM(vocab=c["vocab"], d=c["d"], layers=c["layers"], mlp_mult=c["mlp_mult"], ctx=c["ctx"], mixer="dspin")
+    for mod in lm.modules():
+        if hasattr(mod, "kernel"):
+            mod.kernel = kernel
+    P.fill_(lm, 45)
+    lm = lm.cuda().eval()
+    ids = P.ids(41, (c["B"], c["T"]), c["vocab"]).cuda()
+    with torch.no_grad():
+        logits = lm(ids[:, : c["ctx"]])
+        carried = lm.forward_carried(ids, window=c["window"])
+    assert rel(logits, OPT["lm_dspin_logits"]) < tol
+    assert rel(carried, OPT["lm_dspin_carried"]) < tol
