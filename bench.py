@@ -186,6 +186,7 @@ def aspin_bench(rule, steps, warmup):
         fwd_flops = 4 * D * (C + D) * ht
         bwd_flops = 10 * D * (C + D) * ht
         names = ("aspin_plain_fwd", "aspin_plain_bwd")
+        counted = names
         impl_fwd, impl_bwd = fwd_bytes, bwd_bytes
     else:
         # the minimal I/O of the delta rule (the algorithmic bytes): forward q, k, v, la, beta read, o written, the
@@ -193,19 +194,21 @@ def aspin_bench(rule, steps, warmup):
         # read, dq, dk, dv, dla, dbeta written, dS_final read, dS0 written
         fwd_bytes = 4 * 2 * elem + 8 * ht + 4 * state + 2 * sent_n
         bwd_bytes = 7 * 2 * elem + 2 * sent_n + 16 * ht + 8 * state
-        # what this implementation moves besides: X (bf16 C x C per chunk) written and read back in the forward and
-        # read again in the backward, W written and read back, the chain/local hand-off (drhs and per-chunk dS,
-        # bf16) written once and read once, and the entering states read twice in the backward
+        # what this implementation moves besides: in the forward (one kernel, the inverses formed on chip) the keys
+        # read a second time by the inverse waves, X (bf16 C x C per chunk) and W written for the backward; in the
+        # backward X read, W read, the chain/local hand-off (drhs and per-chunk dS, bf16) written once and read once,
+        # and the entering states read a second time
         x_n = B * H * NC * C * C
-        impl_fwd = fwd_bytes + 2 * 2 * x_n + 2 * elem
+        impl_fwd = fwd_bytes + 2 * elem + 2 * x_n + 2 * elem
         impl_bwd = bwd_bytes + 2 * x_n + 2 * elem + 2 * sent_n + 2 * (2 * elem + 2 * sent_n)
         fwd_flops = (4 * D * (C + D) + 2 * C * D + 2 * D * D + 2 * C * C) * ht
         bwd_flops = (10 * D * (C + D) + 6 * C * D + 4 * D * D + 4 * C * C) * ht
-        names = ("aspin_delta_fwd (inv + fwd kernels)", "aspin_delta_bwd (chain + local kernels)")
+        names = ("aspin_delta_fwd_inv (one kernel, inverses on chip)", "aspin_delta_bwd (chain + local kernels)")
+        counted = ("aspin_delta_fwd_inv", "aspin_delta_bwd_chain", "aspin_delta_bwd_local")
     cold = _rotating_bwd(rule, stream, x)
     return dict(B=B, H=H, T=T, D=D, C=C, wall=wall, eager=eager, t_fwd=t_fwd, t_bwd=t_bwd, fwd_bytes=fwd_bytes,
                 bwd_bytes=bwd_bytes, impl_fwd_bytes=impl_fwd, impl_bwd_bytes=impl_bwd, fwd_flops=fwd_flops,
-                bwd_flops=bwd_flops, names=names, cold=cold)
+                bwd_flops=bwd_flops, names=names, counted=counted, cold=cold)
 
 
 ROTATE_SETS = 8
@@ -634,6 +637,15 @@ def lds_contraction_bench():
     return out
 
 
+def counter_ratio(r):
+    """HBM bytes the rocprofv3 counters measured for the op's kernels at configs[2], summed, over its algorithmic
+    bytes; None when any of them has no row in the traffic table."""
+    got = [measured_traffic(k) for k in r["counted"]]
+    if any(v is None for v in got):
+        return None
+    return round(sum(got) / (r["fwd_bytes"] + r["bwd_bytes"]), 3)
+
+
 def op_roofline(r):
     """The whole fwd+bwd op against both rooflines, from the algorithmic bytes and flops over the two kernels' summed
     durations: the HBM fraction, the bf16 MFMA fraction, and the larger of the two (the op's roofline position)."""
@@ -646,8 +658,11 @@ def op_roofline(r):
             "mfma_frac": round(tfl / BF16_PEAK_TFLOPS, 4),
             "achieved_frac": round(max(gbs / HBM_PEAK_GBS, tfl / BF16_PEAK_TFLOPS), 4),
             "ai_flop_per_byte": round((r["fwd_flops"] + r["bwd_flops"]) / (r["fwd_bytes"] + r["bwd_bytes"]), 1),
-            # this implementation's bytes (its own intermediates included) against the algorithmic ones
+            # this implementation's bytes (its own intermediates included) against the algorithmic ones: from the
+            # formula above, and as the FETCH_SIZE / WRITE_SIZE counters measured them for the same kernels
+            # (profiles/pmc_traffic_configs.md; null when a kernel has no row there)
             "impl_bytes_ratio": round(impl / (r["fwd_bytes"] + r["bwd_bytes"]), 3),
+            "counter_bytes_ratio": counter_ratio(r),
             "impl_GBs": round(impl / t / 1e9, 1),
             # the same kernels with every launch's inputs out of the last-level cache (rotating input sets)
             "cold": dict(r["cold"], hbm_frac=round((r["fwd_bytes"] + r["bwd_bytes"]) / tc / 1e9 / HBM_PEAK_GBS, 4))}
@@ -950,7 +965,8 @@ COPY_BYTES = 256 << 20
 # tile (2 A operands from TB 2 on), 2 column tiles, and the state update 2 x 2), score waves 20 (2 per s block at or
 # below the diagonal). Plain backward: group K 152 (P and dA 4 per block WL..3, then 4 dV^T and 4 dK^T tiles of 3 or
 # 4), group D 128 (P^T and dA^T 4 per block 0..WL, 4 dQ^T tiles of 3 or 4, the dS update 4 x 2). Delta forward
-# chain: 4 chain waves x 36 (U = K S 8, W = X rhs 6, O 14, state update 8) and the scores 20. Delta backward chain:
+# chain: 4 chain waves x 36 (U = K S 8, W = X rhs 6, O 14, state update 8) and the scores 20 (the inverse waves' bf16
+# products, 20 a chunk, run in other phases and are not counted). Delta backward chain:
 # 4 chain waves x 44 (K dS 8, K S_c 8, (Q o eL)^T dO 8, dW 6, drhs 6, dS update 8) and the transposed scores 20.
 PHASE_MFMAS = {"plain_fwd": {"output": 88, "score": 20}, "plain_bwd": 280, "delta_fwd": 164, "delta_bwd_chain": 196}
 MFMA_FLOPS = 16 * 16 * 32 * 2
@@ -1063,28 +1079,31 @@ def phase_rates(reps=50):
         return e0.elapsed_time(e1) / reps * 1e3
 
     out = {"workload": "plain and delta chunked scans, B16 T512 H12 D64 bf16 (configs[2]), phase stamps"}
-    # the delta inverse (one workgroup of four waves per (batch-head, chunk)): its phases from the unit's second stamp
-    # buffer, as wave 0 passes them
+    # the delta inverse at head dim 64 (formed on chip by the forward's three inverse waves, one chunk each over three
+    # iterations in six phases): each phase's duration from the unit's second stamp buffer, 16 entries per (head,
+    # chunk): clocks at the inverse's start (0, 1), each phase's start and end (2 + 2p, 3 + 2p), clocks at its end
+    # (14, 15); the span from start to end includes the barriers between the phases
     import numpy as np
     st.pragnosia_stamps_set_delta_aux.argtypes = [ctypes.c_void_p]
     st.pragnosia_stamps_set_delta_aux.restype = ctypes.c_int
     ninv = nwg * NC
-    ibuf = torch.zeros(ninv * 8, device=dev, dtype=torch.int32)
+    ibuf = torch.zeros(ninv * 16, device=dev, dtype=torch.int32)
     assert st.pragnosia_stamps_set_delta_aux(P(ibuf)) == 0
     for _ in range(3):
         assert run["delta_fwd"](st) == 0
     torch.cuda.synchronize()
     assert st.pragnosia_stamps_set_delta_aux(None) == 0
-    si = ibuf.cpu().numpy().view(np.uint32).reshape(ninv, 8)
-    clk = float(np.median(((si[:, 6].astype(np.int64) - si[:, 0]) % (1 << 32)) /
-                          ((si[:, 7].astype(np.int64) - si[:, 1]) % (1 << 32)))) * 1e8
+    si = ibuf.cpu().numpy().view(np.uint32).reshape(ninv, 16)
+    clk = float(np.median(((si[:, 14].astype(np.int64) - si[:, 0]) % (1 << 32)) /
+                          ((si[:, 15].astype(np.int64) - si[:, 1]) % (1 << 32)))) * 1e8
     # differences within a wave only (the shader clocks of different XCDs are not synchronised)
-    t = _rel32(si[:, [0, 2, 3, 4, 5, 6]], si[:, :1]).astype(np.float64) / clk * 1e6  # us from the wave's start
-    names = ("staging: keys, decays, strengths", "N", "diagonal blocks", "block levels", "store X")
+    t = _rel32(si, si[:, :1]).astype(np.float64) / clk * 1e6  # us from the inverse's start
+    names = ("keys staged, decay scan, N blocks", "diagonal blocks", "level 1", "level 2", "level 3",
+             "store X, next keys' loads")
     out["delta_inverse_phases"] = {
-        "workgroups": ninv, "shader_clock_GHz": round(clk / 1e9, 3),
-        "median_us": {n: round(float(np.median(t[:, j + 1] - t[:, j])), 3) for j, n in enumerate(names)},
-        "wave_total_median_us": round(float(np.median(t[:, 5] - t[:, 0])), 3)}
+        "chunks": ninv, "shader_clock_GHz": round(clk / 1e9, 3),
+        "median_us": {n: round(float(np.median(t[:, 3 + 2 * j] - t[:, 2 + 2 * j])), 3) for j, n in enumerate(names)},
+        "span_median_us": round(float(np.median(t[:, 14])), 3)}
     for kern in ("plain_fwd", "plain_bwd", "delta_fwd", "delta_bwd_chain"):
         setter = getattr(st, "pragnosia_stamps_set_" + unit[kern])
         buf = torch.zeros(nwg * waves[kern] * (4 + 2 * NC), device=dev, dtype=torch.int32)

@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (12); bumped on any change of the entry points. */
+/* ABI version of this header (13); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -242,7 +242,10 @@ int pragnosia_aspin_exact_bwd(const void* q, const void* k, const void* v, const
  * S[d, j], (B, H, ceil(T/64), D, D); required by the backward; may be NULL when no backward follows), and the two
  * saved intermediates of the backward: W, the residuals actually written, (B, H, T, D) bf16, and X, the per-chunk
  * inverse (I + diag(beta) strictly_lower((K K^T) o dec))^-1, (B, H, ceil(T/64), 64, 64) bf16, computed in fp32. At
- * D = 128 the rule is independent per value column once X is known, so each head runs as two scans over its value
+ * D = 64 the forward is one kernel that forms each chunk's inverse on chip, and o, W, sent and X are each written only
+ * when non-NULL (S_final always): with only o the call keeps nothing for a backward, with no o it is the state pass
+ * that a backward recomputing the intermediates runs (the output products skipped). At D = 128 o, W and X are
+ * required; the rule is independent per value column once X is known, so each head runs as two scans over its value
  * halves, each carrying a 128 x 64 state slice and sharing X.
  * Replaces `delta_scan_kernel` and the ops under it (`delta_inv`, `delta_loop_fwd`, `assoc_out`) of
  * src/assoc_kernel.py:332-386, :512-704 (head dims 64 and 128, src/assoc_kernel.py:21); the rule is

@@ -537,6 +537,467 @@ __global__ __launch_bounds__(512) void aspin_delta_fwd(
 }
 
 // ------------------------------------------------------------------------------------------------------------------
+// forward with the chunk inverses formed on chip (64-wide heads): aspin_delta_fwd's chain and service waves plus
+// kNIW = 3 inverse waves, one workgroup of 11 waves per (batch, head), so a forward is one launch and X need not pass
+// through memory. Inverse wave iw (waves 8..10) forms X for the chunks iw, iw + 3, iw + 6, ..., each over the three
+// iterations before the chain reaches it, with the one-wave form of aspin_delta_inv's algorithm (N blocks from a bf16
+// MFMA K K^T and fp32 decays, the diagonal blocks by substitution, one column per lane, the blocks below by block
+// forward substitution on fp32 MFMA; every entry by the same operations in the same order as aspin_delta_inv, so X is
+// bit-identical to its), in six phases, one per barrier interval: keys staged (loaded an iteration earlier), decay
+// scan and the ten N blocks; the four diagonal blocks; the three block levels; X into the chunk's X tile (the chain is
+// done with the tile's previous chunk by then) and, when asked for, to memory, then the next chunk's loads. The first
+// kNIW iterations run before the chain's first chunk (the service waves stage chunk 0 meanwhile). The outputs o, W,
+// sent and X are each written only when the caller passes a buffer; without o, the chain waves skip the output
+// products and the service waves the scores (the state pass a recomputing backward needs).
+constexpr int kNIW = 3;                         // inverse waves; a chunk's inverse spans kNIW iterations
+constexpr int kIBS = 16 * 16 + 4;               // floats per 16 x 16 block (16-byte pad: blocks start on other banks)
+constexpr int kInvScratch = 23 * kIBS + 2 * C;  // floats per inverse wave: N^T (10 blocks), X (10), level sums (3), L, beta
+PGN_DEVICE int iblk(int tb, int sb) { return (tb * (tb + 1) / 2 + sb) * kIBS; }
+// dynamic LDS: the staged tiles, the scores and the per-token vectors; the inverse waves' scratch is a static array of
+// its own (so the compiler knows their accesses never alias the tiles' and can issue them ahead)
+constexpr size_t fwd_inv_smem() { return (2 * 4 * TILE + TILE) * sizeof(__bf16) + 2 * kFwdVec * sizeof(float); }
+static_assert(fwd_inv_smem() + kNIW * kInvScratch * sizeof(float) <= 160 * 1024, "the forward's LDS fits a CU");
+
+__global__ __launch_bounds__(64 * (8 + kNIW)) void aspin_delta_fwd_inv(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const float* __restrict__ la, const float* __restrict__ be, const float* __restrict__ S0, __bf16* __restrict__ o,
+    __bf16* __restrict__ Wout, float* __restrict__ Sfin, __bf16* __restrict__ sent, __bf16* __restrict__ Xout, int T,
+    int NC) {
+  constexpr int KH = 1, DKEY = 64;
+  constexpr int kStage = 4 * TILE;  // Q, K, V, X
+  extern __shared__ __align__(16) unsigned char smem[];
+  __bf16* stg = reinterpret_cast<__bf16*>(smem);           // two sets of staged tiles, chunk c uses set c & 1
+  __bf16* As = stg + 2 * kStage;                            // As[t][s] = A[t][s]
+  float* vec = reinterpret_cast<float*>(As + TILE);         // two vector sets, chunk c uses set c & 1
+  __shared__ __align__(16) float inv[kNIW * kInvScratch];  // the inverse waves' scratch
+
+  const WaveIdx x = wave_idx();
+  const int w = x.w, tid = threadIdx.x;
+  const DeltaRows<KH> R(blockIdx.x);
+  const size_t voff = R.vals(T);
+  // instrumented build: as aspin_delta_fwd's, for the chain and service waves (first buffer: per wave, clocks where
+  // its role's branch starts (entries 0, 1) and at the kernel's end (2, 3), then the start and end of its phase for
+  // chunk c (4 + 2 c, 5 + 2 c)); the inverse waves write the second buffer, per (head, chunk) 16 entries: clocks at
+  // the inverse's start (0, 1), the start and end of phase p (2 + 2p, 3 + 2p), clocks at its end (14, 15)
+#define DF_STAMP(k) PGN_STAMP((blockIdx.x * 8 + w) * (4 + 2 * NC) + (k))
+#define DF_CLOCKS(k) PGN_STAMP_CLOCKS((blockIdx.x * 8 + w) * (4 + 2 * NC) + (k))
+#define DI_STAMP(cn, k) PGN_STAMP_AUX(((int)blockIdx.x * NC + (cn)) * 16 + (k))
+#define DI_CLOCKS(cn, k) PGN_STAMP_CLOCKS_AUX(((int)blockIdx.x * NC + (cn)) * 16 + (k))
+
+  if (w < 4) {
+    // ================= chain waves: value columns j = 16w + i; state rows 16 db + 4g + r
+    DF_CLOCKS(0);
+    f32x4 S[4];
+    {
+      const int g = x.g, j = 16 * w + x.i;
+      const __amdgpu_buffer_rsrc_t sv = f32_view(S0 ? S0 + R.state() : nullptr, DKEY * DKEY);
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[db][r] = load_f32(sv, (16 * db + 4 * g + r) * DKEY + j);
+    }
+    for (int it = 0; it < 2 * kNIW; ++it) __syncthreads();  // the kNIW iterations that form X_0
+    for (int c = 0; c < NC; ++c) {
+      // lane indices recomputed per chunk from an opaque copy of the thread index (loop-invariant LDS addresses
+      // hoisted out of the chunk loop would each hold a register)
+      const WaveIdx xo = wave_idx_opaque();
+      const int g = xo.g, i = xo.i, j = 16 * w + i;
+      const int t0 = c * C, h = c & 1;
+      const __bf16* Qs = stg + h * kStage;
+      const __bf16* Ks = Qs + TILE;
+      const __bf16* Vs = Qs + 2 * TILE;
+      const __bf16* Xs = Qs + 3 * TILE;
+      const float* vs = vec + h * kFwdVec;
+      const float* Ls = vs;
+      const float* eLs = vs + C;
+      const float* ws = vs + 2 * C;
+      const float* bs = vs + 3 * C;
+      const int out_bytes = min(C, T - t0) * DKEY * (int)sizeof(__bf16);
+      DF_STAMP(4 + 2 * c);  // the chunk's phase: operand reads, contractions, result stores (across the A barrier)
+      if (sent) {
+        __bf16* sc = sent + R.stateT(NC, c) + (size_t)j * DKEY + 4 * g;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) *reinterpret_cast<bf16x4*>(sc + 16 * db) = to_bf16x4(S[db]);
+      }
+      // U = K S (rows t, this wave's columns); rhs = beta (V - eL U)
+      bf16x8 sp[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) sp[m] = pack(S[2 * m], S[2 * m + 1]);
+      f32x4 R4[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        f32x4 u = zero4();
+#pragma unroll
+        for (int m = 0; m < 2; ++m) u = pgn_mfma(frag(Ks, 16 * tb + i, m, g), sp[m], u);
+        const f32x4 vv = to_f32x4(ds_read_tr(Vs + (16 * tb + 4 * g + (i >> 2)) * kPitch + 16 * w + 4 * (i & 3)));
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
+        const f32x4 ev = *reinterpret_cast<const f32x4*>(eLs + 16 * tb + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) R4[tb][r] = bv[r] * (vv[r] - ev[r] * u[r]);
+      }
+      // W = X rhs; stored when asked for (no W buffer: an empty range, the stores dropped)
+      const __amdgpu_buffer_rsrc_t w_out = __builtin_amdgcn_make_buffer_rsrc(
+          Wout ? Wout + voff + (size_t)t0 * DKEY : nullptr, (short)0, Wout ? out_bytes : 0, 0x00020000);
+      const bf16x8 r01 = pack(R4[0], R4[1]), r23 = pack(R4[2], R4[3]);
+      f32x4 Wt[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 0, g), r01, zero4());
+        if (tb >= 2) Wt[tb] = pgn_mfma(frag(Xs, 16 * tb + i, 1, g), r23, Wt[tb]);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, quad_rows(Wt[tb], i)), w_out,
+                                              ((16 * tb + 4 * g + (i & 3)) * DKEY + 16 * w + 4 * (i >> 2)) *
+                                                  (int)sizeof(__bf16), 0, 0);
+      }
+      __syncthreads();  // A complete
+      if (o) {
+        // O^T tiles (value rows 16w + 4g + r, token lane 16 tb + i) = W^T A^T + eL_t (S^T Q^T)
+        const __amdgpu_buffer_rsrc_t o_out =
+            __builtin_amdgcn_make_buffer_rsrc(o + voff + (size_t)t0 * DKEY, (short)0, out_bytes, 0x00020000);
+        const bf16x8 w01 = pack(Wt[0], Wt[1]), w23 = pack(Wt[2], Wt[3]);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          const int tl = 16 * tb + i;
+          f32x4 acc = pgn_mfma(w01, frag(As, tl, 0, g), zero4());
+          if (tb >= 2) acc = pgn_mfma(w23, frag(As, tl, 1, g), acc);
+          f32x4 qs = zero4();
+#pragma unroll
+          for (int m = 0; m < 2; ++m) qs = pgn_mfma(sp[m], frag(Qs, tl, m, g), qs);
+          acc += eLs[tl] * qs;
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), o_out,
+                                                (tl * DKEY + 16 * w + 4 * g) * (int)sizeof(__bf16), 0, 0);
+        }
+      }
+      // S <- a S + K^T (w o W)
+      const float a_c = __expf(Ls[C - 1]);
+      bf16x8 ww[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+        ww[m] = pack(Wt[2 * m] * *reinterpret_cast<const f32x4*>(ws + 32 * m + 4 * g),
+                     Wt[2 * m + 1] * *reinterpret_cast<const f32x4*>(ws + 32 * m + 16 + 4 * g));
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        S[db] = S[db] * a_c;
+        S[db] = pgn_mfma(frag_tr(Ks, 16 * db, 0, g, i), ww[0], S[db]);
+        S[db] = pgn_mfma(frag_tr(Ks, 16 * db, 1, g, i), ww[1], S[db]);
+      }
+      DF_STAMP(5 + 2 * c);
+      __syncthreads();  // end of the chunk
+    }
+    {
+      const int g = x.g, j = 16 * w + x.i;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Sfin[R.state() + (size_t)(16 * db + 4 * g + r) * DKEY + j] = S[db][r];
+    }
+  } else if (w < 8) {
+    // ================= service waves: thread b carries 16-byte row segments b and b + 256 of Q, K and V
+    const int a = w - 4;  // this wave's t block for the scores
+    const int b = tid & 255;
+    DF_CLOCKS(0);
+    bf16x8 sg[3][2];
+    float pla = 0.f, pbe = 0.f;
+    auto load = [&](int cn) {
+      const int n0 = cn * C, nr = min(C, T - n0);
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        const __bf16* src = u == 0 ? q + R.rows(T) + (size_t)n0 * DKEY
+                          : u == 1 ? k + R.rows(T) + (size_t)n0 * DKEY
+                                   : v + voff + (size_t)n0 * DKEY;
+        sg[u][0] = load_seg(src, nr, b);
+        sg[u][1] = load_seg(src, nr, b + 256);
+      }
+      pla = load_f32_lane(la + R.tok(T) + n0, nr, x.l);
+      pbe = load_f32_lane(be + R.tok(T) + n0, nr, x.l);
+    };
+    auto stage = [&](int hh) {
+      __bf16* base = stg + hh * kStage;
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        put_seg(base + u * TILE, sg[u][0], b);
+        put_seg(base + u * TILE, sg[u][1], b + 256);
+      }
+      if (a == 0) {
+        float* vs = vec + hh * kFwdVec;
+        chunk_decays(pla, x.l, vs, vs + C, vs + 2 * C);
+        vs[3 * C + x.l] = pbe;
+      }
+    };
+    load(0);
+    for (int it = 0; it < 2 * kNIW - 2; ++it) __syncthreads();  // the kNIW iterations that form X_0
+    stage(0);
+    __syncthreads();
+    load(min(1, NC - 1));
+    __syncthreads();
+    for (int c = 0; c < NC; ++c) {
+      const WaveIdx xo = wave_idx_opaque();
+      const int g = xo.g, i = xo.i;
+      const int h = c & 1;
+      const __bf16* Qs = stg + h * kStage;
+      const __bf16* Ks = Qs + TILE;
+      const float* Ls = vec + h * kFwdVec;
+      DF_STAMP(4 + 2 * c);
+      if (o) {
+        // decayed scores A[t][s] = (q_t . k_s) exp(L_t - L_s), s <= t, into As (row t); the ten nonzero blocks split
+        // 2, 3, 3, 2 over the four waves, each wave zeroing its row block above the diagonal
+        auto block = [&](int tb, int sb) {
+          const int t = 16 * tb + i;
+          f32x4 pt = zero4();
+#pragma unroll
+          for (int m = 0; m < 2; ++m) pt = pgn_mfma(frag(Ks, 16 * sb + i, m, g), frag(Qs, t, m, g), pt);
+          const float Lt = Ls[t];
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pt[r] *= masked_decay(Lt - Lsv[r], 16 * sb + 4 * g + r <= t);
+          store_T(As, 16 * tb, 16 * sb, g, i, pt);
+        };
+#pragma unroll
+        for (int sb = 1; sb < 4; ++sb)
+          if (sb > a) store_T(As, 16 * a, 16 * sb, g, i, zero4());
+        if (a == 0) {
+          block(0, 0);
+          block(3, 0);
+        } else if (a == 1) {
+          block(1, 0);
+          block(1, 1);
+          block(3, 1);
+        } else if (a == 2) {
+          block(2, 0);
+          block(2, 1);
+          block(2, 2);
+        } else {
+          block(3, 2);
+          block(3, 3);
+        }
+      }
+      DF_STAMP(5 + 2 * c);
+      __syncthreads();  // A complete
+      if (c + 1 < NC) stage(h ^ 1);
+      load(min(c + 2, NC - 1));  // unconditional (the last ones re-read the last chunk, unused)
+      __syncthreads();  // end of the chunk
+    }
+  } else {
+    // ================= inverse waves: chunk cn is formed by wave cn % kNIW over iterations cn - kNIW .. cn - 1, in
+    // phases 0 .. 2 kNIW - 1 (two per iteration, before and after the A barrier): 0 keys staged, decay scan, N blocks;
+    // 1 the diagonal blocks; 2, 3, 4 the three block levels; 5 X into the chunk's X tile (and to memory), then the
+    // loads of the wave's next chunk
+    static_assert(kNIW == 3, "six phases over three iterations");
+    const int iw = w - 8;
+    // the inverse waves issue first when their SIMD has a choice: the chain and service waves leave gaps that they
+    // fill, and an iteration lasts as long as the slowest phase
+    __builtin_amdgcn_s_setprio(2);
+    float* NT = inv + iw * kInvScratch;  // N^T blocks: NT(tb, sb)[s' * BP + t'] = N[16 tb + t'][16 sb + s']
+    float* Xf = NT + 10 * kIBS;          // X blocks: Xf(ib, jb)[r * BP + c] = X[16 ib + r][16 jb + c]
+    float* Tt = Xf + 10 * kIBS;          // per-level sums, one block per product
+    float* Li = Tt + 3 * kIBS;
+    float* bi = Li + C;
+    __bf16* Kst = reinterpret_cast<__bf16*>(Xf);  // the keys, staged in the X block area until N is formed
+    static_assert(TILE * sizeof(__bf16) <= 10 * kIBS * sizeof(float), "the key tile fits the X block area");
+    bf16x8 seg[8];
+    float lav = 0.f, bev = 0.f;
+    auto iload = [&](int cn) {  // keys in 16-byte row segments (rows past T as zeros), decays and strengths
+      const int t0 = cn * C, nr = min(C, T - t0);
+      const __bf16* kc = k + R.rows(T) + (size_t)t0 * DKEY;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) seg[n] = load_seg(kc, nr, x.l + 64 * n);
+      lav = load_f32_lane(la + R.tok(T) + t0, nr, x.l);
+      bev = load_f32_lane(be + R.tok(T) + t0, nr, x.l);
+    };
+    // Each phase reads what it needs into registers before it writes anything: its LDS writes could alias its
+    // reads (one scratch array), so the compiler would otherwise issue each read only after the writes before it.
+    auto phase_n = [&]() {  // keys staged, decay scan, the N^T blocks
+      const WaveIdx xo = wave_idx_opaque();
+      const int l = xo.l, g = xo.g, i = xo.i;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) put_seg(Kst, seg[n], l + 64 * n);
+      Li[l] = incl_scan64(lav, l);
+      bi[l] = bev;
+      bf16x8 kf[4][2];
+      float Lt[4], bt[4];
+      f32x4 Lsv[4];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m) kf[rb][m] = frag(Kst, 16 * rb + i, m, g);
+        Lt[rb] = Li[16 * rb + i];
+        bt[rb] = bi[16 * rb + i];
+        Lsv[rb] = *reinterpret_cast<const f32x4*>(Li + 16 * rb + 4 * g);
+      }
+      f32x4 nv[10];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int t = 16 * tb + i;
+#pragma unroll
+        for (int sb = 0; sb <= tb; ++sb) {
+          f32x4 acc = zero4();
+          acc = pgn_mfma(kf[sb][0], kf[tb][0], acc);
+          acc = pgn_mfma(kf[sb][1], kf[tb][1], acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int s = 16 * sb + 4 * g + r;
+            nv[tb * (tb + 1) / 2 + sb][r] = bt[tb] * acc[r] * masked_decay(Lt[tb] - Lsv[sb][r], s < t);
+          }
+        }
+      }
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int sb = 0; sb <= tb; ++sb) {
+          float* nb = NT + iblk(tb, sb);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) nb[(4 * g + r) * BP + i] = nv[tb * (tb + 1) / 2 + sb][r];
+        }
+    };
+    // X_ii = (I + N_ii)^-1 by forward substitution, one column of one diagonal block per lane (the keys in the X
+    // block area are dead once N is formed)
+    auto phase_diag = [&]() {
+      const WaveIdx xo = wave_idx_opaque();
+      const int bb = xo.l >> 4, cl = xo.l & 15;
+      const float* nd = NT + iblk(bb, bb);
+      float xd[16];
+#pragma unroll
+      for (int t = 0; t < 16; ++t) xd[t] = (t == cl) ? 1.f : 0.f;
+#pragma unroll
+      for (int s = 0; s < 15; ++s) {
+        const float xs = xd[s];
+#pragma unroll
+        for (int t4 = (s + 1) & ~3; t4 < 16; t4 += 4) {
+          const f32x4 n = *reinterpret_cast<const f32x4*>(nd + s * BP + t4);  // N[16b + t][16b + s], t = t4..
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (t4 + u > s) xd[t4 + u] -= n[u] * xs;
+        }
+      }
+      float* xb = Xf + iblk(bb, bb);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) xb[t * BP + cl] = xd[t];
+    };
+    // level d: X_ij = -X_ii sum_{k=j}^{i-1} N_ik X_kj for i - j = d, on fp32 MFMA (v_mfma_f32_16x16x4f32: A[r][k] in
+    // lane r + 16k, B[k][c] in lane c + 16k, D[4g + e][c] in lane c + 16g)
+    auto phase_level = [&](int d) {
+      const WaveIdx xo = wave_idx_opaque();
+      const int r16 = xo.l & 15, k4 = xo.l >> 4;
+      // one 16 x 16 x 16 product's operands, A[r][k] and B[k][c] for this lane's k = 4 kk + k4 (A read transposed
+      // when `at`: A[r][k] = Ab[k * BP + r]), and the product accumulated onto acc
+      struct Ops {
+        float a[4], b[4];
+      };
+      auto rd = [&](const float* Ab, bool at, const float* Bb) {
+        Ops o_;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int kx = 4 * kk + k4;
+          o_.a[kk] = at ? Ab[kx * BP + r16] : Ab[r16 * BP + kx];
+          o_.b[kk] = Bb[kx * BP + r16];
+        }
+        return o_;
+      };
+      auto mm = [&](f32x4 acc, const Ops& o_) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(o_.a[kk], o_.b[kk], acc, 0, 0, 0);
+        return acc;
+      };
+      // T_j = sum_{k=j}^{i-1} N_ik X_kj (at most three products a level, three terms each: d = 1 has 3 x 1, d = 2
+      // 2 x 2, d = 3 1 x 3); all operands read first
+      Ops to[3][3];
+#pragma unroll
+      for (int jb = 0; jb < 3; ++jb)
+#pragma unroll
+        for (int u = 0; u < 3; ++u)
+          if (jb + d < 4 && u < d) to[jb][u] = rd(NT + iblk(jb + d, jb + u), true, Xf + iblk(jb + u, jb));
+      f32x4 Tacc[3];
+#pragma unroll
+      for (int jb = 0; jb < 3; ++jb) {
+        if (jb + d < 4) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int u = 0; u < 3; ++u)
+            if (u < d) acc = mm(acc, to[jb][u]);
+          Tacc[jb] = acc;
+        }
+      }
+#pragma unroll
+      for (int jb = 0; jb < 3; ++jb)
+        if (jb + d < 4)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) Tt[jb * kIBS + (4 * k4 + e) * BP + r16] = Tacc[jb][e];
+      // X_ij = -X_ii T_j
+      Ops xo2[3];
+#pragma unroll
+      for (int jb = 0; jb < 3; ++jb)
+        if (jb + d < 4) xo2[jb] = rd(Xf + iblk(jb + d, jb + d), false, Tt + jb * kIBS);
+#pragma unroll
+      for (int jb = 0; jb < 3; ++jb) {
+        if (jb + d < 4) {
+          const f32x4 xr = mm(zero4(), xo2[jb]);
+          float* xo_ = Xf + iblk(jb + d, jb);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xo_[(4 * k4 + e) * BP + r16] = -xr[e];
+        }
+      }
+    };
+    // X (bf16, row-major; zero above the diagonal blocks) into chunk cn's X tile and, when asked for, to memory, in
+    // 16-byte row segments (every lane reads a block, those above the diagonal selected away: no divergent branch)
+    auto phase_store = [&](int cn) {
+      const WaveIdx xo = wave_idx_opaque();
+      const int l = xo.l;
+      __bf16* Xs = stg + (cn & 1) * kStage + 3 * TILE;
+      __bf16* Xg = Xout ? Xout + ((size_t)R.hw * NC + cn) * C * C : nullptr;
+      f32x4 xv[8][2];
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const int e = l + 64 * n, r = e >> 3, c0 = 8 * (e & 7);
+        const int rb = r >> 4, cb = c0 >> 4;
+        const float* xb = Xf + iblk(rb, cb <= rb ? cb : 0) + (r & 15) * BP + (c0 & 15);
+        xv[n][0] = *reinterpret_cast<const f32x4*>(xb);
+        xv[n][1] = *reinterpret_cast<const f32x4*>(xb + 4);
+      }
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const int e = l + 64 * n, r = e >> 3, c0 = 8 * (e & 7);
+        const bool keep = (c0 >> 4) <= (r >> 4);
+        bf16x8 out;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          out[u] = (__bf16)(keep ? xv[n][0][u] : 0.f);
+          out[4 + u] = (__bf16)(keep ? xv[n][1][u] : 0.f);
+        }
+        put_seg(Xs, out, e);
+        if (Xg) *reinterpret_cast<bf16x8*>(Xg + r * C + c0) = out;
+      }
+    };
+    auto phase = [&](int ph, int cn) {
+      if (ph == 0) DI_CLOCKS(cn, 0);
+      DI_STAMP(cn, 2 + 2 * ph);
+      if (ph == 0) phase_n();
+      else if (ph == 1) phase_diag();
+      else if (ph < 5) phase_level(ph - 1);
+      else {
+        phase_store(cn);
+        if (cn + kNIW < NC) iload(cn + kNIW);
+      }
+      DI_STAMP(cn, 3 + 2 * ph);
+      if (ph == 5) DI_CLOCKS(cn, 14);
+    };
+    if (iw < NC) iload(iw);
+    for (int it = -kNIW; it < NC; ++it) {
+      const int cn = it + 1 + ((iw - it - 1) % kNIW + kNIW) % kNIW;  // this wave's chunk: cn = iw mod kNIW
+      const int ph = 2 * (it - (cn - kNIW));
+      const bool mine = cn >= 0 && cn < NC;
+      if (mine) phase(ph, cn);
+      __syncthreads();  // A complete
+      if (mine) phase(ph + 1, cn);
+      __syncthreads();  // end of the chunk
+    }
+  }
+  if (w < 8) DF_CLOCKS(2);
+#undef DF_STAMP
+#undef DF_CLOCKS
+#undef DI_STAMP
+#undef DI_CLOCKS
+}
+
+// ------------------------------------------------------------------------------------------------------------------
 // backward, the sequential part: one workgroup of 8 waves per scan (a 64-wide head, or one value half of a 128-wide
 // one), chunks in reverse. Waves 0-3 carry the chain, wave w owning value columns 16w..16w+15 with its columns of dS
 // (all key rows) in fp32 registers; nothing on the chain is shared between them. Waves 4-7 serve them: per chunk they
@@ -1233,6 +1694,14 @@ int delta_fwd(const void* q, const void* k, const void* v, const float* la, cons
               hipStream_t st) {
   const int NC = (int)((T + C - 1) / C);
   const int heads = (int)(B * H);
+  if constexpr (KH == 1) {  // one launch: the inverses formed on chip
+    const int rc = set_smem((const void*)aspin_delta_fwd_inv, fwd_inv_smem());
+    if (rc) return rc;
+    hipLaunchKernelGGL(aspin_delta_fwd_inv, dim3((unsigned)heads), dim3(64 * (8 + kNIW)), fwd_inv_smem(), st, (const __bf16*)q,
+                       (const __bf16*)k, (const __bf16*)v, la, beta, S0, (__bf16*)o, (__bf16*)W, S_final,
+                       (__bf16*)sent, (__bf16*)X, (int)T, NC);
+    PGN_RETURN_LAUNCH();
+  }
   hipLaunchKernelGGL(aspin_delta_inv<KH>, dim3((unsigned)(heads * NC)), dim3(256), 0, st, (const __bf16*)k, la, beta,
                      (__bf16*)X, (int)T, NC);
   hipError_t e = hipGetLastError();
@@ -1306,7 +1775,9 @@ extern "C" int pragnosia_aspin_delta_fwd(const void* q, const void* k, const voi
                                          int64_t chunk, void* stream) {
   if ((D != DK && D != 2 * DK) || chunk != C) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, H, T, D, chunk));
-  PGN_CHECK_ARG(q && k && v && la && beta && o && S_final && W && X);
+  PGN_CHECK_ARG(q && k && v && la && beta && S_final);
+  // at D = 128 every output is written (the backward reads W and X); at D = 64 each only when given
+  PGN_CHECK_ARG(D == DK || (o && W && X));
   hipStream_t st = (hipStream_t)stream;
   return D == DK ? delta_fwd<1>(q, k, v, la, beta, S0, o, S_final, sent, W, X, B, H, T, st)
                  : delta_fwd<2>(q, k, v, la, beta, S0, o, S_final, sent, W, X, B, H, T, st);

@@ -799,18 +799,47 @@ def _delta_backward(ctx, do, dS, _dsent, _dW, _dX):
 aspin_delta.register_autograd(_delta_backward, setup_context=_delta_setup)
 
 
+def _delta_pass(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor, S0: Optional[Tensor], want_o: bool,
+                want_saved: bool) -> tuple[Optional[Tensor], Tensor, Optional[Tensor], Optional[Tensor],
+                                            Optional[Tensor]]:
+    """One 64-wide delta forward through the C ABI writing only what is asked for: o when want_o; the entering
+    states, W and X when want_saved (the state pass of a recomputing backward, want_o False, skips the output
+    products). Returns (o, S_final, sent, W, X), None for what was not written. Inputs already cast."""
+    B, H, T, D = q.shape
+    NC = (T + CHUNK - 1) // CHUNK
+    dev = q.device
+    o = torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16) if want_o else None
+    S = torch.empty(B, H, D, D, device=dev, dtype=torch.float32)
+    sent = W = X = None
+    if want_saved:
+        sent = torch.empty(B, H, NC, D, D, device=dev, dtype=torch.bfloat16)
+        W = torch.empty(B, H, T, D, device=dev, dtype=torch.bfloat16)
+        X = torch.empty(B, H, NC, CHUNK, CHUNK, device=dev, dtype=torch.bfloat16)
+    check(lib().pragnosia_aspin_delta_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(la), _ptr(beta), _ptr(S0), _ptr(o),
+                                          _ptr(S), _ptr(sent), _ptr(W), _ptr(X), B, H, T, D, CHUNK, _stream(q)),
+          "pragnosia_aspin_delta_fwd")
+    return o, S, sent, W, X
+
+
 @torch.library.custom_op("pragnosia::aspin_delta_fused", mutates_args=())
 def aspin_delta_fused(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tensor,
                       S0: Optional[Tensor]) -> tuple[Tensor, Tensor]:
-    """The delta-rule scan keeping nothing for its backward but its inputs: (o bf16, S_final fp32). The state lives in
-    the chain waves' registers; X, W and the per-chunk entering states exist only within the call (W and X in
-    temporaries freed on return, the entering states not written). Its backward recomputes them with the same
-    kernels, so they are bit-identical to what the forward formed and so are the gradients, then runs the
-    stored-state backward. This is the trait of the third-party fused kernel the reference's FUSED_SCAN switches to
-    (`src/assoc.py:481-492`: state on chip, chunk states recomputed in the backward instead of written per chunk and
-    read back): the activation memory kept from forward to backward drops by 2 B/elem of W, 2 B per entering-state
-    element and 2 B per X element, for one more inverse and forward pass in the backward."""
-    o, S, _, _, _ = aspin_delta(q, k, v, la, beta, S0, False)
+    """The delta-rule scan keeping nothing for its backward but its inputs: (o bf16, S_final fp32). At head dim 64
+    the forward is one kernel that forms each chunk's inverse X on chip and writes only o and S_final: X, W and the
+    per-chunk entering states never reach memory. Its backward first runs the state pass of the same kernel (no
+    output products), which writes the entering states, W and X (the same operations on the same inputs, so
+    bit-identical to what the forward formed), then the stored-state backward. At head dim 128, X, W and o come from
+    the two-kernel forward into temporaries freed on return. This is the trait of the third-party fused kernel the
+    reference's FUSED_SCAN switches to (`src/assoc.py:481-492`: state on chip, chunk states recomputed in the backward
+    instead of written per chunk and read back): the activation memory kept from forward to backward drops by 2 B/elem
+    of W, 2 B per entering-state element and 2 B per X element, for one more forward pass in the backward."""
+    _require_gpu(q, k, v, la, beta, S0)
+    _expect_scan("aspin_delta_fused", q, k, v, la, beta=beta, S0=S0, widths=(64, 128))
+    if q.shape[-1] == 128:
+        o, S, _, _, _ = aspin_delta(q, k, v, la, beta, S0, False)
+        return o, S
+    q, k, v, la, beta, S0 = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(beta), _f32(S0)
+    o, S, _, _, _ = _delta_pass(q, k, v, la, beta, S0, True, False)
     return o, S
 
 
@@ -829,7 +858,10 @@ def _delta_fused_setup(ctx, inputs, output):
 
 def _delta_fused_backward(ctx, do, dS):
     q, k, v, la, beta, S0 = ctx.saved_tensors
-    _, _, sent, W, X = aspin_delta(q, k, v, la, beta, S0, True)  # the forward's intermediates, recomputed
+    if q.shape[-1] == 128:
+        _, _, sent, W, X = aspin_delta(q, k, v, la, beta, S0, True)  # the forward's intermediates, recomputed
+    else:  # the state pass: entering states, W and X, no output
+        _, _, sent, W, X = _delta_pass(_bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(beta), _f32(S0), False, True)
     if do is None:
         do = torch.zeros(q.shape, device=q.device, dtype=torch.bfloat16)
     dq, dk, dv, dla, dbeta, dS0 = aspin_delta_bwd(q, k, v, la, beta, sent, W, X, do.contiguous(), dS)

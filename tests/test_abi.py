@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 12
+    assert L.pragnosia_abi_version() == 13
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 
@@ -117,6 +117,9 @@ def test_delta_workspace_both_widths(L):
     assert q(2, 3, 100, 96, 64) == -1 and q(2, 3, 100, 128, 32) == -1
     null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
     assert L.pragnosia_aspin_delta_fwd(*([one] * 5), null, *([one] * 5), 1, 1, 100, 96, 64, null) == -2
+    # at head dim 128 o, W and X are required (its backward reads W and X); at 64 each is optional
+    fwd = lambda o, W, X, D: L.pragnosia_aspin_delta_fwd(*([one] * 5), null, o, one, null, W, X, 1, 1, 100, D, 64, null)
+    assert fwd(one, null, one, 128) == -1 and fwd(one, one, null, 128) == -1 and fwd(null, one, one, 128) == -1
 
 
 def test_colsum_arguments_rejected(L):

@@ -126,6 +126,43 @@ def test_cfg2_full_shape_delta(delta):
         assert rel(a.grad, b.grad) < TOL_GRAD
 
 
+def _fused(*a):
+    """aspin_delta_fused (the FUSED_SCAN path: nothing kept but the inputs; at head dim 64 a forward that writes only o
+    and S_final, X formed on chip) in aspin_delta's calling convention."""
+    o, S = torch.ops.pragnosia.aspin_delta_fused(*a[:6])
+    return o, S, None, None, None
+
+
+def test_cfg2_full_shape_delta_fused():
+    """The FUSED_SCAN path at BASELINE configs[2]'s full shape with an entering state: outputs, the final state and all
+    six gradients (q, k, v, la, beta, S0) against the oracle in fp32 (as test_cfg2_full_shape_delta)."""
+    from pragnosia_amd import ops  # noqa: F401
+    B, H, T, D = 16, 12, 512, 64
+    q, k, v, la, be, S0 = _inputs(B, H, T, D, seed=3, s0=True)
+    g = torch.Generator().manual_seed(23)
+    do = torch.randn(B, H, T, D, generator=g)
+    dSf = torch.randn(B, H, D, D, generator=g)
+    r = [t.clone().requires_grad_(True) for t in (q, k, v, la, be, S0)]
+    yr, Sr, _, _ = O.scan_twopass_delta(*r, 64)
+    ((yr * do).sum() + (Sr * dSf).sum()).backward()
+    kk = [t.cuda().requires_grad_(True) for t in (q, k, v, la, be, S0)]
+    yk, Sk, _, _, _ = _fused(*kk)
+    ((yk.float() * do.cuda()).sum() + (Sk * dSf.cuda()).sum()).backward()
+    assert rel(yk, yr) < TOL_OUT and rel(Sk, Sr) < TOL_OUT
+    for n, a, b in zip(("q", "k", "v", "la", "beta", "S0"), kk, r):
+        assert rel(a.grad, b.grad) < TOL_GRAD, n
+
+
+@pytest.mark.parametrize("D,T", [(64, 333), (64, 1), (128, 200), (128, 64)])
+def test_delta_fused_matches_oracle(D, T):
+    """The FUSED_SCAN path against the fp64 oracle, with an entering state and a final-state gradient, at head dims
+    64 and 128, ragged and one-token sequences."""
+    from pragnosia_amd import ops  # noqa: F401
+    q, k, v, la, be, S0 = _inputs(2, 3, T, D, seed=500 + D + T, s0=True)
+    print(f"delta fused: D {D} T {T}", flush=True)
+    _assert(_check(_fused, q, k, v, la, be, S0, seed=500 + T))
+
+
 def test_delta_repeated_keys_bounded(delta):
     """256 writes of nearly the same key at beta near 1 with no forgetting (the case that breaks a bf16 or tf32
     inverse, `src/assoc_kernel.py:577-582`): the state stays finite and bounded, and matches the fp64 oracle within
