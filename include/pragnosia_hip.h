@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (13); bumped on any change of the entry points. */
+/* ABI version of this header (14); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -389,6 +389,24 @@ int pragnosia_decode_gemv(const float* x, int64_t B, int64_t K, const float* ln_
 int pragnosia_decode_gemv_rms(const float* x, int64_t B, int64_t K, const float* rms_weight, float rms_eps,
                               const float* W, int64_t N, const float* bias, const float* scale, int act,
                               const float* resid, float* y, void* stream);
+
+/* The dense layers of the decode step on the fp32 matrix cores, for batches past the GEMV's (any B; 16 rows a
+ * workgroup): y (B, N) = act(scale * (W z) + bias) + resid, with z = x (mode 0); z = (x - mean) / sqrt(var + eps) over
+ * each row (mode 1: a LayerNorm whose weight is folded into W's columns, W[n][k] ln_weight[k], and whose bias into
+ * `bias` as W ln_bias; csum (N) = the row sums of the folded W, required); or z = x / sqrt(mean of squares + eps) over
+ * each 64-channel group (mode 2, K a multiple of 64 up to 1024: the carrier's per-head RMSNorm, its weight folded into
+ * W's columns, W[n][k] rms_weight[k mod 64]). scale a device scalar or NULL, bias (N) or NULL, act 0 identity / 1 GELU
+ * (erf form), resid (B, N) or NULL. W (N, K) is given tiled: Wt[((t (K / 16) + s) 64 + l) 4 + e] = W[16 t + l % 16][16
+ * s + 4 (l / 16) + e], zero for columns past N, so Wt holds ceil(N / 16) 16 K floats. K a multiple of 16; y must not
+ * alias x or resid. Deterministic; no workspace. pragnosia_decode_gemm_waves gives the waves a workgroup runs for (K,
+ * mode), -1 where the kernel does not cover it (the call then returns PRAGNOSIA_ERR_UNSUPPORTED). Replaces the
+ * LayerNorm + nn.Linear (+ GELU, + residual) calls of the carrier's projections, its RMSNorm and gated output
+ * projection, the MLP (src/model.py:552-560) and the tied head in the reference's batched graphed decode
+ * (src/bench.py:241-317), as pragnosia_decode_gemv does for B <= 4. */
+int pragnosia_decode_gemm_waves(int64_t K, int mode);
+int pragnosia_decode_gemm(const float* x, int64_t B, int64_t K, int mode, const float* csum, float eps,
+                          const float* Wt, int64_t N, const float* bias, const float* scale, int act,
+                          const float* resid, float* y, void* stream);
 
 #ifdef __cplusplus
 }

@@ -104,6 +104,9 @@ typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 
 PGN_DEVICE float pgn_exp(float x) { return __expf(x); }
 
+// GELU, erf form (torch's default F.gelu): 0.5 x (1 + erf(x / sqrt 2)).
+PGN_DEVICE float pgn_gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
+
 // sin and cos of x. The hardware sine/cosine (through __sincosf) take the argument in revolutions: scaling x to
 // revolutions in fp32 costs about |x| * 2^-24 rad of absolute angle error, so they are used for |x| < 64 rad (at
 // most ~4e-6 rad; measured 1.3e-6 relative on the diagonal scan's outputs for angles in [-pi, pi]) and the precise

@@ -1,0 +1,263 @@
+// The dense layers of the carrier LM's decode step for batches past the one-wave GEMV (5 sequences and more), fp32
+// on the matrix cores (v_mfma_f32_16x16x4f32): y = act(scale * (W z) + bias) + resid with z the row standardised,
+// (x - mean) / sqrt(var + eps) (MODE 1: a LayerNorm whose weight the caller folds into W's columns and whose bias
+// into `bias` as W ln_bias), the per-64-channel-group RMS scaling x / sqrt(mean x^2 + eps) (MODE 2: the carrier's
+// per-head RMSNorm of its raw step output, its weight folded into W's columns) or x (MODE 0). Replaces, inside the
+// graphed decode of `src/bench.py:241-317`, the LayerNorm + nn.Linear (+ GELU, + residual) calls of
+// `src/model.py:552-560` and `src/assoc.py:384-512`, one kernel per dense layer, as decode_gemv.hip does for at most
+// 4 sequences.
+//
+// At 64 sequences every weight element is used 64 times a step (32 flop per byte read), so the fp32 matrix-core rate
+// matters as much as HBM, and at these sizes a workgroup's own latency (its loads, then its products, then its
+// reduction) sets the kernel's time. Work split: a workgroup owns 16 output columns (one column tile) of 16 rows (one
+// row block), all of K: its KW waves (at most 16) split K into 16-wide steps, S consecutive steps a chunk and C chunks
+// a wave. So a layer at 64 rows is 4 x ceil(N / 16) workgroups; those of one column tile are numbered 8 apart, so
+// they run on one XCD (workgroup i goes to XCD i mod 8) and read the tile's weight from one L2. A wave issues its
+// first chunk's loads before any product and each next chunk's loads before the current chunk's products (register
+// double buffering): S weight pieces, each one contiguous 1 KiB, and S input pieces. The weight (N, K) comes
+// pre-tiled: Wt[((t KS + s) 64 + l) 4 + e] = W[16 t + l % 16][16 s + 4 (l / 16) + e] for column tile t, 16-wide step
+// s (KS = K / 16 of them), lane l and entry e, zero for columns past N (tiled once by the caller; ops.decode_gemm_tile).
+// MODE 1 needs the row's moments only in the epilogue: the products run on x - x0 (x0 the row's first entry, so the
+// subtraction of mean(x - x0) csum below cancels no more than the row's spread; csum[n] = sum_k W[n][k]) while each
+// wave forms, per chunk, the mean and the sum of squared deviations of its entries (exact two-pass in registers) and
+// merges them (Chan, Golub and LeVeque's pairwise update); the waves' pairs meet in the epilogue, in wave order, with
+// the products' partials. MODE 2 (S = 4, C = 1) has each wave own one 64-channel group, so the group's sum of squares
+// is a two-step lane exchange before its products. The wave partials are summed through LDS in wave order:
+// deterministic, no atomics, nothing shared between workgroups, no workspace.
+//
+// Operand layout of v_mfma_f32_16x16x4f32: A[r][k] in lane r + 16 k, B[k][c] in lane c + 16 k, D[4 g + e][c] in
+// lane c + 16 g, e = 0..3. A lane holds four consecutive K entries of a row (one 16-byte piece): product e of a
+// 16-wide step contracts entry e of every lane's piece, i.e. k = 16 s + 4 (l / 16) + e; the weight pieces are tiled
+// with the same pairing, so every k is contracted exactly once.
+#include "common.h"
+
+namespace {
+
+constexpr int MAXW = 16;  // waves per workgroup
+
+template <int S, int C, int MODE>
+__global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ x, int B, int K,
+                                                      const float* __restrict__ csum, float eps,
+                                                      const float* __restrict__ Wt, int N, int NT, int ZB,
+                                                      const float* __restrict__ bias,
+                                                      const float* __restrict__ scale, int act,
+                                                      const float* __restrict__ resid, float* __restrict__ y) {
+  static_assert(MODE != 2 || C == 1, "the RMS mode holds one 64-channel group per wave");
+  __shared__ __align__(16) float red[MAXW * 256];
+  __shared__ float2 stat[MAXW][16];
+  const int KW = blockDim.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, r16 = l & 15, k4 = l >> 4;
+  // workgroup i -> (column tile, row block): the ZB row blocks of a tile are 8 apart (one XCD)
+  const int i = blockIdx.x;
+  const int nt = (i / (8 * ZB)) * 8 + (i & 7), zb = (i >> 3) % ZB;
+  if (nt >= NT) return;  // padding workgroups of the last group of 8 tiles
+  const int KS = K >> 4;
+  const int s0 = w * S * C;  // the wave's first 16-wide step
+  const int row = 16 * zb + r16;
+  const bool live = row < B;
+  const float* xrow = x + (size_t)min(row, B - 1) * K;
+  const float* xr = xrow + 16 * s0 + 4 * k4;
+  const float* wp = Wt + ((size_t)nt * KS + s0) * 256 + 4 * l;
+
+  f32x4 wv[2][S], z[2][S];
+  auto load = [&](int c, int b) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      wv[b][s] = *reinterpret_cast<const f32x4*>(wp + 256 * (c * S + s));
+      const f32x4 v = *reinterpret_cast<const f32x4*>(xr + 16 * (c * S + s));
+      z[b][s] = live ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  // LayerNorm mode: the products run on the row shifted by its first entry, x - x0 (the shift keeps the products'
+  // cancellation against mean * csum at the size of the row's spread); the row's moments are formed beside them
+  const float x0 = MODE == 1 && live ? xrow[0] : 0.f;
+  load(0, 0);
+  float mw = 0.f, m2w = 0.f;  // this wave's mean and sum of squared deviations of the row (LayerNorm mode)
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    if (c + 1 < C) load(c + 1, (c + 1) & 1);
+    const int b = c & 1;
+    if constexpr (MODE == 1) {
+      // the chunk's 16 S entries of the row (the lane's 4 S and those of lanes l ^ 16, l ^ 32, l ^ 48): their mean
+      // and sum of squared deviations, merged into the wave's by the pairwise update (equal counts per chunk)
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) z[b][s][e] -= x0;
+      float a = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) a += (z[b][s][0] + z[b][s][1]) + (z[b][s][2] + z[b][s][3]);
+      a += __shfl_xor(a, 16);
+      a += __shfl_xor(a, 32);
+      const float mc = a * (1.f / (16 * S));
+      float q = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float d = z[b][s][e] - mc;
+          q += d * d;
+        }
+      q += __shfl_xor(q, 16);
+      q += __shfl_xor(q, 32);
+      if (c == 0) {
+        mw = mc;
+        m2w = q;
+      } else {  // merge n = 16 S c entries (mw, m2w) with 16 S new ones (mc, q)
+        const float d = mc - mw, f = 1.f / (c + 1);
+        mw += d * f;
+        m2w += q + d * d * (16.f * S) * c * f;
+      }
+    } else if constexpr (MODE == 2) {
+      // one 64-channel group per wave (S = 4): r = 1 / sqrt(mean of squares + eps) scales the group
+      static_assert(S == 4, "the RMS mode runs one 64-channel group per wave");
+      float a = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a += z[b][s][e] * z[b][s][e];
+      a += __shfl_xor(a, 16);
+      a += __shfl_xor(a, 32);
+      const float r = 1.f / sqrtf(a * (1.f / 64) + eps);
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) z[b][s][e] *= r;
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(z[b][s][e], wv[b][s][e], acc, 0, 0, 0);
+  }
+
+  // wave partials (and the LayerNorm moments) through LDS; output v = 16 i + c (row i, column c of the block) sits
+  // in lane c + 16 (i / 4), entry i % 4
+  *reinterpret_cast<f32x4*>(red + w * 256 + 4 * l) = acc;
+  if (MODE == 1 && k4 == 0) stat[w][r16] = float2{mw, m2w};
+  __syncthreads();
+  for (int v = threadIdx.x; v < 256; v += blockDim.x) {  // a workgroup of fewer than 4 waves takes two rounds
+    const int ri = v >> 4, cc = v & 15;
+    const int src = 4 * (cc + 16 * (ri >> 2)) + (ri & 3);
+    float t = 0.f;
+    for (int u = 0; u < KW; ++u) t += red[u * 256 + src];
+    const int orow = 16 * zb + ri, col = 16 * nt + cc;
+    if (orow < B && col < N) {
+      if constexpr (MODE == 1) {
+        // the row's mean (of x - x0) and variance from the waves' pairs in wave order (equal counts); the products
+        // of x - x0 minus (mean of x - x0) csum are the products of x - mean
+        const float n_w = 16.f * S * C;
+        float mean = 0.f;
+        for (int u = 0; u < KW; ++u) mean += stat[u][ri].x;
+        mean /= KW;
+        float m2 = 0.f;
+        for (int u = 0; u < KW; ++u) {
+          const float2 p = stat[u][ri];
+          const float d = p.x - mean;
+          m2 += p.y + n_w * d * d;
+        }
+        t = (t - mean * csum[col]) * (1.f / sqrtf(m2 / K + eps));
+      }
+      float r = (scale ? *scale : 1.f) * t + (bias ? bias[col] : 0.f);
+      if (act == 1) r = pgn_gelu_erf(r);
+      const size_t off = (size_t)orow * N + col;
+      if (resid) r += resid[off];
+      y[off] = r;
+    }
+  }
+}
+
+struct Plan {
+  int S = 0, C = 0, KW = 0;
+};
+
+// The launch shape for (K, mode); false when the kernel does not cover it.
+bool make_plan(int64_t K, int mode, Plan& p) {
+  if (K <= 0 || K % 16) return false;
+  const int64_t KS = K / 16;
+  if (mode == 2) {  // one 64-channel group per wave
+    if (K % 64 || K / 64 > MAXW) return false;
+    p = Plan{4, 1, (int)(K / 64)};
+    return true;
+  }
+  int S = 1;
+  for (int s : {6, 4, 3, 2})
+    if (KS % s == 0) {
+      S = s;
+      break;
+    }
+  const int64_t R = KS / S;  // chunks to spread over waves
+  for (int64_t cap : {8, MAXW})
+    for (int c : {1, 2, 4})
+      if (R % c == 0 && R / c <= cap) {
+        p = Plan{S, c, (int)(R / c)};
+        return true;
+      }
+  return false;
+}
+
+template <int S, int C, int MODE>
+int launch(const Plan& p, const float* x, int B, int K, const float* csum, float eps, const float* Wt, int N,
+           const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
+  const int NT = (N + 15) / 16, ZB = (B + 15) / 16;
+  const int64_t groups = (NT + 7) / 8;  // tiles in groups of 8, each group's ZB row blocks together
+  hipLaunchKernelGGL((decode_gemm_k<S, C, MODE>), dim3((unsigned)(groups * 8 * ZB)), dim3((unsigned)(64 * p.KW)), 0,
+                     st, x, B, K, csum, eps, Wt, N, NT, ZB, bias, scale, act, resid, y);
+  PGN_RETURN_LAUNCH();
+}
+
+template <int C, int MODE>
+int dispatch_s(const Plan& p, const float* x, int B, int K, const float* csum, float eps, const float* Wt, int N,
+               const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
+#define PGN_S(V) return launch<V, C, MODE>(p, x, B, K, csum, eps, Wt, N, bias, scale, act, resid, y, st)
+  if constexpr (MODE == 2) {
+    PGN_S(4);
+  } else {
+    switch (p.S) {
+      case 1: PGN_S(1);
+      case 2: PGN_S(2);
+      case 3: PGN_S(3);
+      case 4: PGN_S(4);
+      default: PGN_S(6);
+    }
+  }
+#undef PGN_S
+}
+
+}  // namespace
+
+extern "C" int pragnosia_decode_gemm_waves(int64_t K, int mode) {
+  Plan p;
+  if (mode < 0 || mode > 2 || !make_plan(K, mode, p)) return -1;
+  return p.KW;
+}
+
+template <int MODE>
+int dispatch_c(const Plan& p, const float* x, int B, int K, const float* csum, float eps, const float* Wt, int N,
+               const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
+  switch (p.C) {
+    case 1: return dispatch_s<1, MODE>(p, x, B, K, csum, eps, Wt, N, bias, scale, act, resid, y, st);
+    case 2: return dispatch_s<2, MODE>(p, x, B, K, csum, eps, Wt, N, bias, scale, act, resid, y, st);
+    default: return dispatch_s<4, MODE>(p, x, B, K, csum, eps, Wt, N, bias, scale, act, resid, y, st);
+  }
+}
+
+extern "C" int pragnosia_decode_gemm(const float* x, int64_t B, int64_t K, int mode, const float* csum, float eps,
+                                     const float* Wt, int64_t N, const float* bias, const float* scale, int act,
+                                     const float* resid, float* y, void* stream) {
+  PGN_CHECK_ARG(x && Wt && y && B > 0 && K > 0 && N > 0);
+  PGN_CHECK_ARG(mode >= 0 && mode <= 2 && (mode != 1 || csum != nullptr));
+  PGN_CHECK_ARG(B * N < ((int64_t)1 << 31) && B * K < ((int64_t)1 << 31) &&
+                ((N + 15) / 16) * 16 * K < ((int64_t)1 << 31) && ((N + 127) / 128) * 8 * ((B + 15) / 16) < (1 << 30));
+  PGN_CHECK_ARG(act == 0 || act == 1);
+  PGN_CHECK_ARG(y != x && (resid == nullptr || resid != y));
+  PGN_CHECK_ARG(((uintptr_t)x | (uintptr_t)Wt) % 16 == 0);
+  Plan p;
+  if (!make_plan(K, mode, p)) return PRAGNOSIA_ERR_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  const int b = (int)B, k = (int)K, n = (int)N;
+  if (mode == 1) return dispatch_c<1>(p, x, b, k, csum, eps, Wt, n, bias, scale, act, resid, y, st);
+  if (mode == 2) return dispatch_s<1, 2>(p, x, b, k, nullptr, eps, Wt, n, bias, scale, act, resid, y, st);
+  return dispatch_c<0>(p, x, b, k, nullptr, eps, Wt, n, bias, scale, act, resid, y, st);
+}

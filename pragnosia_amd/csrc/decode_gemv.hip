@@ -24,8 +24,6 @@ namespace {
 constexpr int BT = 8;            // sequences per pass
 constexpr int LNMAX = 1024;      // LayerNorm'd inputs are staged in LDS for K <= LNMAX
 
-PGN_DEVICE float gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
-
 template <int LANES>
 __global__ __launch_bounds__(256) void gemv(const float* __restrict__ x, int B, int K, const float* __restrict__ lnw,
                                             const float* __restrict__ lnb, float eps, const float* __restrict__ W,
@@ -131,7 +129,7 @@ __global__ __launch_bounds__(256) void gemv(const float* __restrict__ x, int B, 
       for (int b = 0; b < BT; ++b) {
         if (b < nb) {
           float v = sc * acc[b] + (bias ? bias[n] : 0.f);
-          if (act == 1) v = gelu_erf(v);
+          if (act == 1) v = pgn_gelu_erf(v);
           const size_t off = (size_t)(b0 + b) * N + n;
           if (resid) v += resid[off];
           y[off] = v;
@@ -277,7 +275,7 @@ __global__ __launch_bounds__(64) void gemv_wave(const float* __restrict__ x, int
     const int n = n0 + r;
     if (n < N && b < B) {
       float v = (scale ? *scale : 1.f) * acc[0] + (bias ? bias[n] : 0.f);
-      if (act == 1) v = gelu_erf(v);
+      if (act == 1) v = pgn_gelu_erf(v);
       const size_t off = (size_t)b * N + n;
       if (resid) v += resid[off];
       y[off] = v;

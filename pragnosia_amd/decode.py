@@ -13,7 +13,8 @@ projection kernel (q, k, v, decay and gate or strength in one concatenated weigh
 forms the decay, gate or strength itself and writes the per-head RMS-normalised output, one kernel for the gated
 output projection with the residual, and two for the MLP (LayerNorm + first layer + GELU; second layer + residual):
 five kernels a layer instead of about twenty-five, the same fp32 arithmetic. Above GEMV_MAX_BATCH sequences the dense
-layers run as the LayerNorm kernel and torch's GEMMs (matrix cores) and the carrier step stays fused. Other mixers
+layers run on the fp32 matrix cores (decode_gemm, the norms, biases, GELU and residuals inside), still five kernels
+a layer (LayerNorm kernel and torch GEMMs where a width is not covered). Other mixers
 run the modules' own T = 1 path. The concatenated weights are copied from the parameters at every `start`, so the
 graph always sees the current parameters.
 """
@@ -23,14 +24,16 @@ import torch
 import torch.nn.functional as F
 
 from .assoc import AssocCarrier
-from .ops import ln_supported
+from .ops import decode_gemm_ln, decode_gemm_ok, decode_gemm_tile, ln_supported
 
 
 # The fused step's dense layers run as the batched GEMV kernel (each weight read once a step) up to this many
-# sequences; beyond it as torch GEMMs (matrix cores), the carrier step still fused. Measured on the 12-layer d768 LM
-# with the earlier 256-thread GEMV, ms a step (GEMV / torch GEMMs, both with the fused step): batch 1 0.45 / 0.77,
-# 4 0.71 / 0.75, 8 1.06 / 0.76, 32 1.18 / 0.85, 64 2.05 / 0.83; the unfused step with torch GEMMs: 1.45-1.57. The
-# one-wave GEMV (up to 4 sequences) and the split carrier step bring batch 1 to 0.31.
+# sequences; beyond it on the fp32 matrix cores (decode_gemm: the LayerNorm, the per-head RMSNorm, the bias, GELU and
+# the residual inside, weights tiled and the norms' weights folded in once per `start`), the carrier step fused and
+# split four workgroups a head. Measured on the 12-layer d768 LM with the earlier 256-thread GEMV, ms a step (GEMV /
+# torch GEMMs, both with the fused step): batch 1 0.45 / 0.77, 4 0.71 / 0.75, 8 1.06 / 0.76, 32 1.18 / 0.85, 64 2.05
+# / 0.83; the unfused step with torch GEMMs: 1.45-1.57. The one-wave GEMV (up to 4 sequences) and the split carrier
+# step bring batch 1 to 0.31.
 GEMV_MAX_BATCH = 4
 
 
@@ -113,26 +116,47 @@ class GreedyDecoder:
         self.ctr.add_(1)
         self.tok.copy_(nxt.view(-1, 1))
 
+    def _gemm_ok(self) -> bool:
+        """Whether the dense layers run on decode_gemm: past the GEMV's batch sizes, every layer's input width covered
+        (the LayerNorm'd d-wide inputs, the per-head RMSNorm'd carrier output, the MLP's hidden width)."""
+        m = self.m
+        if self.B <= GEMV_MAX_BATCH:
+            return False
+        hid = m.mlp[0].a.weight.shape[0]
+        return decode_gemm_ok(m.d, 1) and decode_gemm_ok(m.d, 2) and decode_gemm_ok(hid, 0)
+
     def _fused_weights(self):
         """Per layer: the concatenated input projection (q, k, v, decay, then the gate or strength), the output gate
         sigmoid(g) as a device scalar and the output projection pre-scaled by it (for the GEMM form), written into
-        the same buffers every time (the graph reads them)."""
+        the same buffers every time (the graph reads them). On the decode_gemm path, instead of the GEMM form: each
+        dense layer's weight tiled, its input LayerNorm's (or the carrier's RMSNorm's) weight folded into the tiled
+        columns, the LayerNorm's bias into the layer's bias, with the folded weights' row sums."""
         m = self.m
         fresh = []
-        for mx in m.mix:
+        for mx, mp in zip(m.mix, m.mlp):
             gated = not (mx.delta or mx.write_all)
             extra = [mx.wi.weight] if gated else ([mx.wb.weight] if mx.delta else [])
             sig = torch.sigmoid(mx.gate.detach().float()).reshape(1)
-            fresh.append((torch.cat([mx.q.weight, mx.k.weight, mx.v.weight, mx.wa.weight] + extra).float(), sig,
-                          mx.o.weight.detach().float() * sig))
-        if getattr(self, "wcat", None) is None:
-            self.wcat = [w.contiguous() for w, _, _ in fresh]
-            self.sig = [g.contiguous() for _, g, _ in fresh]
-            self.wos = [wo.contiguous() for _, _, wo in fresh]
+            wcat = torch.cat([mx.q.weight, mx.k.weight, mx.v.weight, mx.wa.weight] + extra).detach().float()
+            if self.gemm:
+                tp, cp, bp = decode_gemm_ln(wcat, mx.ln.weight, mx.ln.bias, None)
+                ta, ca, ba = decode_gemm_ln(mp.a.weight, mp.n.weight, mp.n.bias, mp.a.bias)
+                fresh.append((tp, cp, bp, sig, decode_gemm_tile(mx.o.weight, mx.on.weight), ta, ca, ba,
+                              decode_gemm_tile(mp.b.weight)))
+            else:
+                fresh.append((wcat, sig, mx.o.weight.detach().float() * sig))
+        if self.gemm:
+            fresh.append(decode_gemm_ln(m.e.weight, m.n.weight, m.n.bias, None))
+        if getattr(self, "wbuf", None) is None:
+            self.wbuf = [tuple(t.contiguous() for t in f) for f in fresh]
         else:
-            for dst, src in zip(zip(self.wcat, self.sig, self.wos), fresh):
+            for dst, src in zip(self.wbuf, fresh):
                 for d, t in zip(dst, src):
                     d.copy_(t)
+        if not self.gemm:
+            self.wcat = [f[0] for f in self.wbuf]
+            self.sig = [f[1] for f in self.wbuf]
+            self.wos = [f[2] for f in self.wbuf]
 
     def _dense(self, x, W, ln, bias=None, scale=None, act=0, resid=None):
         """act(scale * (W LayerNorm(x)) + bias) + resid: the batched GEMV kernel up to GEMV_MAX_BATCH sequences,
@@ -153,6 +177,35 @@ class GreedyDecoder:
         if scale is not None:
             return torch.addcmul(resid, y, scale) if resid is not None else y * scale
         return y + resid if resid is not None else y
+
+    def _one_step_gemm(self):
+        """The fused step past GEMV batch sizes: five kernels a layer, all on the fp32 matrix cores but the carrier
+        step (LayerNorm + projection; the step, split four workgroups a head, raw output; per-head RMSNorm + gated
+        o-projection + residual; LayerNorm + MLP in + GELU; MLP out + residual), then LayerNorm + head and argmax."""
+        m, op = self.m, torch.ops.pragnosia
+        h = (m.e(self.tok) + m.p(self.pos)).reshape(self.B, -1)
+        for i, (mx, mp) in enumerate(zip(m.mix, m.mlp)):
+            gated = not (mx.delta or mx.write_all)
+            tp, cp, bp, sig, to, ta, ca, ba, tb = self.wbuf[i]
+            P = op.decode_gemm(h, tp, cp.shape[0], 1, cp, mx.ln.eps, bp, None, 0, None)
+            on_eps = mx.on.eps if mx.on.eps is not None else torch.finfo(torch.float32).eps
+            o = op.aspin_decode_proj_(self.st[i][0], P, mx.h, mx.wa.bias, mx.A,
+                                      mx.la_floor if mx.hl_floor else None, mx.wi.bias if gated else None,
+                                      mx.wb.bias if mx.delta else None, 0.75 if (mx.delta and mx.write_all) else 0.0,
+                                      gated, mx.theta, self.p0s[i:i + 1], 0.0, None, on_eps)
+            x1 = op.decode_gemm(o, to, m.d, 2, None, on_eps, None, sig, 0, h)
+            hm = op.decode_gemm(x1, ta, ca.shape[0], 1, ca, mp.n.eps, ba, None, 1, None)
+            h = op.decode_gemm(hm, tb, m.d, 0, None, 0.0, mp.b.bias, None, 0, x1)
+        self.p0s.fill_(1.0)  # every state is now in the positions of a one-token call
+        self.pos.copy_((self.pos + 1) % m.ctx)
+        th, ch, bh = self.wbuf[-1]
+        lg = op.decode_gemm(h, th, ch.shape[0], 1, ch, m.n.eps, bh, None, 0, None)
+        nxt = lg.argmax(-1)
+        if self.lgs is not None:
+            self.lgs.index_copy_(0, self.ctr, lg.float().view(1, self.B, -1))
+        self.out.index_copy_(0, self.ctr, nxt.view(1, -1))
+        self.ctr.add_(1)
+        self.tok.copy_(nxt.view(-1, 1))
 
     def _one_step_fused(self):
         m, op = self.m, torch.ops.pragnosia
@@ -191,6 +244,7 @@ class GreedyDecoder:
         dev = self.m.e.weight.device
         self.st = self._static_states(states)
         if self.fused:
+            self.gemm = self._gemm_ok()
             self._fused_weights()
             self.p0s = torch.stack([st[1].reshape(()) for st in self.st]).float().contiguous()
         self.tok = torch.zeros(self.B, 1, dtype=torch.long, device=dev)
@@ -201,7 +255,7 @@ class GreedyDecoder:
             self.lgs = torch.zeros(n_max + self.K, self.B, self.m.e.weight.shape[0], dtype=torch.float32, device=dev)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
-        step = self._one_step_fused if self.fused else self._one_step
+        step = (self._one_step if not self.fused else self._one_step_gemm if self.gemm else self._one_step_fused)
         with torch.cuda.stream(side):
             for _ in range(2):
                 step()

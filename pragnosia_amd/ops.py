@@ -1407,6 +1407,73 @@ def _(x, W, rms_weight, rms_eps, bias, scale, act, resid):
     return x.new_empty(x.shape[0], W.shape[0], dtype=torch.float32)
 
 
+def decode_gemm_tile(W: Tensor, col_scale: Optional[Tensor] = None) -> Tensor:
+    """The tiled copy of a dense layer's weight W (N, K) fp32 that `decode_gemm` reads (K a multiple of 16), its
+    columns scaled by col_scale when given (a normalisation's weight folded in: (K,), or (64,) repeated over the
+    64-channel groups), flat: Wt[((t KS + s) 64 + l) 4 + e] = W[16 t + l % 16][16 s + 4 (l / 16) + e] for column tile
+    t, 16-wide step s of KS = K / 16, lane l, entry e; columns past N padded with zeros. So each wave's weight piece
+    of a step is one contiguous 1 KiB read, laid out as the fp32 matrix cores take their operand."""
+    N, K = W.shape
+    if K % 16:
+        raise PragnosiaError(f"decode_gemm_tile: K = {K} is not a multiple of 16")
+    Wp = W.detach().to(torch.float32)
+    if col_scale is not None:
+        cs = col_scale.detach().to(torch.float32)
+        Wp = Wp * (cs.repeat(K // cs.numel()) if cs.numel() != K else cs)
+    NT = (N + 15) // 16
+    if NT * 16 != N:
+        Wp = torch.cat([Wp, Wp.new_zeros(NT * 16 - N, K)])
+    return Wp.reshape(NT, 16, K // 16, 4, 4).permute(0, 2, 3, 1, 4).contiguous().reshape(-1)
+
+
+def decode_gemm_ln(W: Tensor, ln_weight: Tensor, ln_bias: Optional[Tensor], bias: Optional[Tensor],
+                   scale: Optional[Tensor] = None) -> tuple[Tensor, Tensor, Tensor]:
+    """A LayerNorm + linear layer folded for `decode_gemm` mode 1: (the tiled W diag(ln_weight), the row sums of that
+    fp32 product (summed in fp64), bias + scale W ln_bias (in fp64)). Then decode_gemm(x, Wt, N, 1, csum, eps, bias',
+    scale, ...) = scale (W LayerNorm(x)) + bias. With a scale, the folded bias holds its value at fold time."""
+    Wf = W.detach().to(torch.float32) * ln_weight.detach().to(torch.float32)
+    csum = Wf.double().sum(1).float()
+    b = torch.zeros(W.shape[0], device=W.device, dtype=torch.float64) if bias is None else bias.detach().double()
+    if ln_bias is not None:
+        wb = W.detach().double() @ ln_bias.detach().double()
+        b = b + (wb if scale is None else scale.detach().double() * wb)
+    return decode_gemm_tile(Wf), csum, b.float()
+
+
+def decode_gemm_ok(K: int, mode: int) -> bool:
+    """Whether `decode_gemm` covers a dense layer of input width K in this mode."""
+    return lib().pragnosia_decode_gemm_waves(K, mode) > 0
+
+
+@torch.library.custom_op("pragnosia::decode_gemm", mutates_args=())
+def decode_gemm(x: Tensor, Wt: Tensor, N: int, mode: int, csum: Optional[Tensor], eps: float,
+                bias: Optional[Tensor], scale: Optional[Tensor], act: int, resid: Optional[Tensor]) -> Tensor:
+    """y (B, N) = act(scale * (W z) + bias) + resid on the fp32 matrix cores, W given tiled (`decode_gemm_tile`), with
+    z = x (mode 0), the row standardised (mode 1: a LayerNorm folded by `decode_gemm_ln`, csum its row sums) or each
+    64-channel group RMS-scaled (mode 2: the RMSNorm's weight folded into the tiled W). The dense layers of the decode
+    step past GEMV batch sizes. Not differentiable."""
+    _require_gpu(x, Wt, csum, bias, scale, resid)
+    if x.dim() != 2:
+        raise PragnosiaError(f"decode_gemm: x must be (B, K), got {tuple(x.shape)}")
+    B_, K_ = x.shape
+    if K_ % 16 or Wt.numel() != ((N + 15) // 16) * 16 * K_:
+        raise PragnosiaError(f"decode_gemm: tiled weight of {Wt.numel()} values does not fit N {N} and K {K_}")
+    if (mode == 1) != (csum is not None):
+        raise PragnosiaError("decode_gemm: mode 1 takes the folded weight's row sums, the other modes none")
+    _expect("decode_gemm", x.device, csum=(csum, (N,)), bias=(bias, (N,)), scale=(scale, ()), resid=(resid, (B_, N)))
+    x, Wt, csum, bias, scale, resid = _f32(x), _f32(Wt), _f32(csum), _f32(bias), _f32(scale), _f32(resid)
+    y = torch.empty(B_, N, device=x.device, dtype=torch.float32)
+    check(lib().pragnosia_decode_gemm(_ptr(x), B_, K_, int(mode), _ptr(csum), float(eps), _ptr(Wt), N, _ptr(bias),
+                                      _ptr(scale), int(act), _ptr(resid), _ptr(y), _stream(x)),
+          "pragnosia_decode_gemm")
+    return y
+
+
+@decode_gemm.register_fake
+def _(x, Wt, N, mode, csum, eps, bias, scale, act, resid):
+    return x.new_empty(x.shape[0], N, dtype=torch.float32)
+
+
 @torch.library.custom_op("pragnosia::aspin_decode_proj_", mutates_args=("S",))
 def aspin_decode_proj_(S: Tensor, P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Optional[Tensor],
                        gate_bias: Optional[Tensor], beta_bias: Optional[Tensor], beta_min: float, gated: bool,

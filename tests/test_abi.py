@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 13
+    assert L.pragnosia_abi_version() == 14
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 
@@ -151,6 +151,22 @@ def test_wgrad_workspace_and_rejections(L):
     assert L.pragnosia_wgrad_bf16(*args(24, 16, 16, 0, 20, 16, 64)) == -1                          # M % 8
     # a row pitch whose largest look-ahead offset (row len + 3 * 64) passes 2^31 bytes is refused
     assert L.pragnosia_wgrad_bf16(*args(8_000_000, 8, 8, 0, 8, 8, 64)) == -1
+
+
+def test_decode_gemm_plans_and_rejections(L):
+    """The decode GEMM's plan (waves a workgroup per input width and mode) and its host-side rejections."""
+    q = L.pragnosia_decode_gemm_waves
+    assert q(768, 1) == 8 and q(768, 0) == 8 and q(3072, 0) == 8     # 8 waves of 6 steps; 3072: 4 chunks each
+    assert q(768, 2) == 12 and q(1024, 2) == 16 and q(1088, 2) == -1   # one 64-channel group a wave
+    assert q(3072, 1) == 8 and q(4096, 1) == 16 and q(128, 0) == 2
+    assert q(760, 0) == -1 and q(96, 2) == -1 and q(0, 0) == -1 and q(768, 3) == -1
+    null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    call = lambda B, K, mode, cs, x=one: L.pragnosia_decode_gemm(x, B, K, mode, cs, 1e-5, one, 768, null, null, 0,
+                                                                null, ctypes.c_void_p(32), null)
+    assert call(64, 768, 1, null) == -1                                # LayerNorm without the row sums
+    assert call(64, 1088, 2, null) == -2                               # not covered
+    assert call(0, 768, 0, null) == -1
+    assert call(64, 768, 0, null, ctypes.c_void_p(24)) == -1           # misaligned input
 
 
 def test_product_never_imports_oracle():

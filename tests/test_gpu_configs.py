@@ -104,7 +104,7 @@ def test_cfg3_one_pass_windows_full_size():
 def test_cfg4_decode_matches_oracle(batch):
     """LM(vocab 8192, d 768, 12 layers, 12 heads of 64, ctx 512, aspin), weights N(0, 0.02), a 512-token
     prefill then all 1,024 greedy steps through the captured graph, at batch 1 (the GEMV dense layers) and batch 64
-    (torch GEMM dense layers around the fused carrier step, the branch above GEMV_MAX_BATCH). The prefill fills one
+    (the dense layers on the fp32 matrix cores, decode_gemm, the branch above GEMV_MAX_BATCH). The prefill fills one
     window, so the first step starts a new window with every state rebased by 512, and the position index wraps mod
     512 at step 512: both happen inside the run. The graph records the logits of every step (record_logits).
     (i) Every graphed token is the argmax of the graphed step's own logits.
@@ -126,6 +126,7 @@ def test_cfg4_decode_matches_oracle(batch):
     dec = GreedyDecoder(m, batch, steps_per_graph=8, record_logits=True)
     assert dec.fused and (batch > GEMV_MAX_BATCH) == (batch == 64)
     toks_g = dec.generate(prompt.cuda(), n)
+    assert dec.gemm == (batch == 64)
     lgs_g = dec.logits(n)
     assert bool((lgs_g.argmax(-1) == toks_g).all())
     rows = [0] if batch == 1 else [0, batch - 1]

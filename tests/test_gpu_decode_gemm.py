@@ -1,0 +1,155 @@
+"""GPU parity of the decode step's dense layers on the fp32 matrix cores (pragnosia_decode_gemm, the batches past the
+one-wave GEMV) against fp64 torch: LayerNorm + Linear (+ bias, GELU, residual), the per-head RMSNorm + gated output
+projection, and the long-row layer whose waves each run several chunks of K.
+
+Everything is fp32, as the reference decodes. Tolerance: max relative error max|y - ref| / max|ref| <= 1e-5 (fp32
+sums in another order). Results must be bit-identical from call to call, and a captured graph must replay correctly
+with new inputs."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+
+def rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).abs().max() / (b.abs().max() + 1e-30)).item()
+
+
+def reference(x, W, mode, nw, nb, eps, bias, scale, act, resid):
+    xd, Wd = x.double(), W.double()
+    B, K = x.shape
+    if mode == 1:
+        z = F.layer_norm(xd, (K,), nw.double(), None if nb is None else nb.double(), eps)
+    elif mode == 2:
+        z = F.rms_norm(xd.view(B, K // 64, 64), (64,), nw.double(), eps).view(B, K)
+    else:
+        z = xd
+    r = z @ Wd.t()
+    if scale is not None:
+        r = r * scale.double()
+    if bias is not None:
+        r = r + bias.double()
+    if act == 1:
+        r = F.gelu(r)
+    if resid is not None:
+        r = r + resid.double()
+    return r
+
+
+def inputs(B, K, N, mode, act, res, seed, mean=0.0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(B, K, device="cuda", generator=g) + mean
+    W = torch.randn(N, K, device="cuda", generator=g) * 0.05
+    nw = (1 + 0.1 * torch.randn(64 if mode == 2 else K, device="cuda", generator=g)) if mode else None
+    nb = torch.randn(K, device="cuda", generator=g) if mode == 1 else None
+    bias = torch.randn(N, device="cuda", generator=g) if act else None
+    scale = torch.rand(1, device="cuda", generator=g) if res else None
+    resid = torch.randn(B, N, device="cuda", generator=g) if res else None
+    return x, W, nw, nb, bias, scale, resid
+
+
+def run(x, W, mode, nw, nb, eps, bias, scale, act, resid):
+    """The layer through decode_gemm: mode 1 folds the LayerNorm's weight and bias (decode_gemm_ln), mode 2 the
+    RMSNorm's weight into the tiled weight's columns."""
+    from pragnosia_amd import ops
+    N = W.shape[0]
+    if mode == 1:
+        Wt, csum, b = ops.decode_gemm_ln(W, nw, nb, bias, scale)
+        return torch.ops.pragnosia.decode_gemm(x, Wt, N, 1, csum, eps, b, scale, act, resid)
+    Wt = ops.decode_gemm_tile(W, nw if mode == 2 else None)
+    return torch.ops.pragnosia.decode_gemm(x, Wt, N, mode, None, eps, bias, scale, act, resid)
+
+
+SHAPES = [(768, 2328, 1, 0, False),   # the carrier's projections (LayerNorm)
+          (768, 768, 2, 0, True),     # RMSNorm + gated o-projection + residual (12 waves, one head each)
+          (768, 3072, 1, 1, False),   # MLP in: LayerNorm + bias + GELU
+          (3072, 768, 0, 0, True),    # MLP out: bias-free here, residual; 4 chunks a wave
+          (768, 8192, 1, 0, False),   # the tied head
+          (256, 200, 1, 1, True),     # a ragged column tile, small K
+          (128, 1000, 0, 1, False),   # fewer than four waves
+          (512, 300, 2, 1, True),     # RMS over 8 groups
+          (1024, 640, 1, 0, False),   # LayerNorm over 16 waves of 4 steps
+          (3072, 520, 1, 0, True),    # LayerNorm moments merged over 4 chunks a wave
+          (4096, 520, 0, 0, True)]    # 16 waves of 4 chunks of 4 steps
+
+
+@pytest.mark.parametrize("B", [5, 13, 32, 64, 100])
+@pytest.mark.parametrize("K,N,mode,act,res", SHAPES)
+def test_decode_gemm_matches_torch(B, K, N, mode, act, res):
+    x, W, nw, nb, bias, scale, resid = inputs(B, K, N, mode, act, res, B + K + N + mode)
+    eps = 1e-5 if mode == 1 else torch.finfo(torch.float32).eps
+    y = run(x, W, mode, nw, nb, eps, bias, scale, act, resid)
+    r = reference(x, W, mode, nw, nb, eps, bias, scale, act, resid)
+    assert rel(y, r) < 1e-5, (B, K, N, mode)
+    assert torch.equal(y, run(x, W, mode, nw, nb, eps, bias, scale, act, resid))
+
+
+@pytest.mark.parametrize("mean,spread", [(40.0, 1.0), (0.0, 1e-3), (-300.0, 20.0)])
+def test_layer_norm_with_offset_rows(mean, spread):
+    """LayerNorm input rows far from zero or of small spread: the moments are exact two-pass ones merged pairwise and
+    the products run on the row shifted by its first entry, so neither cancels."""
+    B, K, N = 64, 768, 2328
+    x, W, nw, nb, _, _, _ = inputs(B, K, N, 1, 0, False, 7)
+    x = x * spread + mean
+    y = run(x, W, 1, nw, nb, 1e-5, None, None, 0, None)
+    assert rel(y, reference(x, W, 1, nw, nb, 1e-5, None, None, 0, None)) < 1e-5
+
+
+def test_tile_layout():
+    """decode_gemm_tile against the layout stated in the header, element by element on a small weight."""
+    from pragnosia_amd import ops
+    N, K = 21, 32
+    W = torch.arange(N * K, dtype=torch.float32).reshape(N, K)
+    Wt = ops.decode_gemm_tile(W)
+    assert Wt.numel() == 32 * K
+    KS = K // 16
+    for t in range(2):
+        for s in range(KS):
+            for lane in range(64):
+                for e in range(4):
+                    n, k = 16 * t + lane % 16, 16 * s + 4 * (lane // 16) + e
+                    want = W[n, k].item() if n < N else 0.0
+                    assert Wt[((t * KS + s) * 64 + lane) * 4 + e].item() == want
+
+
+def test_graph_replay_with_new_inputs():
+    """Three dependent layers (each mode) captured into one graph and replayed with new inputs copied into the captured
+    buffers, eager work and synchronisations between replays: every replay equals the eager calls bit for bit."""
+    from pragnosia_amd import ops
+    op = torch.ops.pragnosia
+    B, d = 64, 768
+    g = torch.Generator(device="cuda").manual_seed(11)
+    W1 = torch.randn(3072, d, device="cuda", generator=g) * 0.05
+    W2 = torch.randn(d, 3072, device="cuda", generator=g) * 0.05
+    W3 = torch.randn(d, d, device="cuda", generator=g) * 0.05
+    lw, lb = 1 + 0.1 * torch.randn(d, device="cuda", generator=g), torch.randn(d, device="cuda", generator=g)
+    w64 = 1 + 0.1 * torch.randn(64, device="cuda", generator=g)
+    b1 = torch.randn(3072, device="cuda", generator=g)
+    sc = torch.rand(1, device="cuda", generator=g)
+    T1, c1, b1f = ops.decode_gemm_ln(W1, lw, lb, b1)
+    T2, T3 = ops.decode_gemm_tile(W2), ops.decode_gemm_tile(W3, w64)
+    x = torch.randn(B, d, device="cuda", generator=g)
+    eps = torch.finfo(torch.float32).eps
+
+    def chain(x):
+        h = op.decode_gemm(x, T1, 3072, 1, c1, 1e-5, b1f, None, 1, None)
+        y = op.decode_gemm(h, T2, d, 0, None, 0.0, None, None, 0, x)
+        return op.decode_gemm(y, T3, d, 2, None, eps, None, sc, 0, y)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        chain(x)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = chain(x)
+    for rep in range(4):
+        x.copy_(torch.randn(B, d, device="cuda", generator=g))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = chain(x.clone())
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
