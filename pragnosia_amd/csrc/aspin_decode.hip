@@ -157,10 +157,14 @@ __global__ __launch_bounds__(256) void aspin_decode(const float* S, float* Sout,
 __global__ __launch_bounds__(256) void aspin_decode_split(const float* S, float* Sout, StepIn in,
                                                           const float* __restrict__ theta,
                                                           const float* __restrict__ p0d, float p0h,
-                                                          float* __restrict__ o, int H) {
+                                                          float* __restrict__ o, int H, int nbh) {
   __shared__ float qs[D], ks[D], vs[D];
   __shared__ float red[16][17];
-  const int bhq = blockIdx.x, qtr = bhq & 3, bh = bhq >> 2, h = bh % H, b = bh / H;
+  // workgroup i -> (head bh, quarter): the four quarters of a head are 8 apart, so they run on one XCD (workgroup i
+  // goes to XCD i mod 8) and the 128-byte lines of the state rows they share are fetched into one L2 only
+  const int i = blockIdx.x, qtr = (i >> 3) & 3, bh = (i >> 5) * 8 + (i & 7);
+  if (bh >= nbh) return;  // padding of the last group of 8 heads
+  const int h = bh % H, b = bh / H;
   const int tid = threadIdx.x, jj = tid & 15, rg = tid >> 4;
   const int j = 16 * qtr + jj;
   const float* prow = in.P + (size_t)b * in.np;
@@ -280,8 +284,8 @@ extern "C" int pragnosia_aspin_decode_proj(const float* S, float* S_out, const f
   in.beta_min = beta_min;
   PGN_CHECK_ARG(B * H * 4 < ((int64_t)1 << 31));
   if (on_weight == nullptr)  // raw output: four workgroups per head
-    hipLaunchKernelGGL(aspin_decode_split, dim3((unsigned)(B * H * 4)), dim3(256), 0, (hipStream_t)stream, S, S_out,
-                       in, theta, p0_dev, p0, o, (int)H);
+    hipLaunchKernelGGL(aspin_decode_split, dim3((unsigned)((B * H + 7) / 8 * 32)), dim3(256), 0, (hipStream_t)stream,
+                       S, S_out, in, theta, p0_dev, p0, o, (int)H, (int)(B * H));
   else
     hipLaunchKernelGGL(aspin_decode<true>, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, S_out, in,
                        theta, p0_dev, p0, on_weight, on_eps, o, (int)H);
