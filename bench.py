@@ -391,9 +391,27 @@ def carried_bench():
                                               _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla), _ptr(dS0), B, H, T, D, 64,
                                               _stream(qg)), "bwd")
 
+    # the delta rule over the same windows (beta = sigmoid(N(0, 1))): every window at once from its affine state map,
+    # and the window-by-window loop it replaces
+    be = torch.sigmoid(torch.randn(B, H, T, generator=g)).to(dev)
+
+    def loop_delta():
+        S, outs = None, []
+        for s in range(0, T, W):
+            if S is not None:
+                S = op.aspin_rebase(S, th, None, float(W))
+            o, S, _, _, _ = op.aspin_delta(qw[:, :, s:s + W], kw[:, :, s:s + W], vb[:, :, s:s + W], la[:, :, s:s + W],
+                                           be[:, :, s:s + W], S, False)
+            outs.append(o)
+        return torch.cat(outs, 2), S
+
+    carried_delta = lambda: op.aspin_delta_windows(qw, kw, vb, la, be, None, th, W)
     stream = torch.cuda.current_stream()
     with torch.no_grad():
-        t_c, t_u, t_l, t_s, t_q = _time_ops([carried, unsplit, loop, step, step_sequential], 10, stream)
+        t_c, t_u, t_l, t_s, t_q, t_cd, t_ld = _time_ops([carried, unsplit, loop, step, step_sequential, carried_delta,
+                                                         loop_delta], 10, stream)
+        ocd, Scd = carried_delta()
+        old, Sld = loop_delta()
         oc, Sc, _ = carried()
         ol, Sl = loop()
         ou, Su, _ = unsplit()
@@ -412,7 +430,11 @@ def carried_bench():
             "carried_vs_window_loop_rel_err_o": round(rel(oc, ol), 6),
             "carried_vs_window_loop_rel_err_S": round(rel(Sc, Sl), 6),
             "carried_vs_unsplit_rel_err_o": round(rel(oc, ou), 6),
-            "carried_vs_unsplit_rel_err_S": round(rel(Sc, Su_loc), 6)}
+            "carried_vs_unsplit_rel_err_S": round(rel(Sc, Su_loc), 6),
+            "delta": {"carried_Mtok_s": round(B * T / t_cd / 1e6, 3), "carried_us": round(t_cd * 1e6, 2),
+                      "window_loop_Mtok_s": round(B * T / t_ld / 1e6, 3), "window_loop_us": round(t_ld * 1e6, 2),
+                      "carried_vs_window_loop_rel_err_o": round(rel(ocd, old), 6),
+                      "carried_vs_window_loop_rel_err_S": round(rel(Scd, Sld), 6)}}
 
 
 def lm_train_bench(mixer="aspin", updates=4, micro_per_update=4):

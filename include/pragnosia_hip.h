@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (14); bumped on any change of the entry points. */
+/* ABI version of this header (15); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -268,6 +268,18 @@ int pragnosia_aspin_delta_bwd(const void* q, const void* k, const void* v, const
                               const float* dS_final, void* dq, void* dk, void* dv, float* dla, float* dbeta,
                               float* dS0, void* workspace, int64_t workspace_bytes,
                               int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk, void* stream);
+
+/* The carried windows of the delta rule in one pass (with pragnosia_aspin_delta_fwd over all windows at once): the
+ * entering state of every window from the windows' affine maps. A window maps its entering state as S_out = M S_in + R
+ * (keys on rows; M acts on the key rows, the same for every value column): R = its final state from a zero entering
+ * state, M = its final state from the identity with zero values. Between windows the state is rebased by -shift theta
+ * (key-row pairs (2i, 2i+1) rotated by -shift theta[h][i]): S_in[0] = S0, S_in[w + 1] = Rot(M[w] S_in[w] + R[w]).
+ * M, R, S_in: (BH, NW, 64, 64) fp32 (BH = B H, window w of sequence bh at index bh NW + w); S0: (BH, 64, 64) fp32 or
+ * NULL (zero); theta (H, 32) fp32, head h = bh mod H. fp32 throughout. Replaces the window-by-window loop of
+ * `LM.forward_carried` (src/model.py:842-864) over the carried-state rebase (src/assoc.py:391-405) for delta
+ * carriers. */
+int pragnosia_aspin_delta_window_prefix(const float* M, const float* R, const float* S0, const float* theta,
+                                        float shift, float* S_in, int64_t BH, int64_t H, int64_t NW, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * The plumbing between the carrier's projections and the scan (head dim D = 64): per (b, t, h) row, unit-normalise

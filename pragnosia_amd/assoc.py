@@ -472,12 +472,13 @@ class AssocCarrier(nn.Module):
         """Consecutive windows of `window` tokens of x (B, T, d), the state carried from each window into the next:
         the same function as calling `forward` on x[:, s:s + window] for s = 0, window, ... in turn, handing each
         call the state the previous one returned (`src/model.py:842-864` drives the reference's carrier so). A
-        plain-rule carrier without autograd, with `window` a multiple of 64, runs every window in one pass (the
-        projections over the whole sequence, one segment-parallel scan that rebases the state at window
-        boundaries); otherwise the windows run one call each. Returns (x + gated output, (S, length of the last
-        window)); `sent` is not kept."""
+        carrier without autograd, with `window` a multiple of 64, runs every window in one pass: the projections over
+        the whole sequence, then for the plain rule one segment-parallel scan that rebases the state at window
+        boundaries, for the delta rule every window at once from its affine state map (`ops.aspin_delta_windows`);
+        otherwise the windows run one call each. Returns (x + gated output, (S, length of the last window)); `sent`
+        is not kept."""
         B, T, D = x.shape
-        fused = (not self.delta and window % 64 == 0 and T > window and x.is_cuda and self.dk == HEAD_DIM_KERNEL
+        fused = (window % 64 == 0 and T > window and x.is_cuda and self.dk == HEAD_DIM_KERNEL
                  and self.kernel and getattr(self, "sconv", None) is None
                  and not _needs_grad(x, *(h0[:1] if h0 is not None else ()), *self.parameters()))
         if not fused:
@@ -496,8 +497,11 @@ class AssocCarrier(nn.Module):
         wrap = getattr(self, "pos_wrap", None)
         if wrap:
             pos = pos % wrap
-        q, k, v, la, _, dtype, _ = self._scan_inputs(z, pos)
-        o, S, _ = _op.aspin_chunk_windows(q, k, v, la, S0, self.theta, window, False)
+        q, k, v, la, bt, dtype, _ = self._scan_inputs(z, pos)
+        if self.delta:
+            o, S = _op.aspin_delta_windows(q, k, v, la, bt, S0, self.theta, window)
+        else:
+            o, S, _ = _op.aspin_chunk_windows(q, k, v, la, S0, self.theta, window, False)
         self.sent = None
         o = self._epilogue(o, dtype)
         out = x + F.linear(o, self.o.weight) * torch.sigmoid(self.gate)

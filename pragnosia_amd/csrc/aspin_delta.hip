@@ -1660,6 +1660,70 @@ bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
   return (D == DK || D == 2 * DK) && Cc == C;
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// Carried windows of the delta rule in one pass: the entering state of every window from the windows' affine maps.
+// Given X (keys, decays and strengths only) the rule is independent per value column and linear in the state, so a
+// window maps its entering state affinely, S_out = M S_in + R, with M (64 x 64) acting on the key rows, the same for
+// every value column: R is the window's final state from a zero entering state, M its final state from the identity
+// with zero values (both from the forward's state pass, all windows at once). Successive windows restart their
+// positions, so the state is rebased between them by -shift theta (key-row pairs rotated, `src/assoc.py:399-402`):
+//     S_in[0] = S0,   S_in[w + 1] = Rot(M[w] S_in[w] + R[w]).
+// One workgroup of 256 threads per (batch, head) walks the windows, fp32 throughout: thread (value column j, row
+// group rg) forms rows 16 rg .. 16 rg + 15 of column j over the 64 keys, M's rows read from LDS (the 64 lanes of a
+// wave read the same entries: broadcasts), then rotates its row pairs and writes S_in[w + 1] to memory and to LDS.
+// M, R, S_in: (BH, NW, 64, 64) fp32; S0: (BH, 64, 64) fp32 or NULL (zero).
+__global__ __launch_bounds__(256) void delta_window_prefix(const float* __restrict__ M, const float* __restrict__ R,
+                                                           const float* __restrict__ S0,
+                                                           const float* __restrict__ theta, float shift,
+                                                           float* __restrict__ Sin, int H, int NW) {
+  __shared__ float Ss[64][65];
+  __shared__ __align__(16) float Ms[64 * 64];
+  const int bh = blockIdx.x, h = bh % H;
+  const int tid = threadIdx.x, j = tid & 63, rg = tid >> 6;
+  float sn[8], cs[8];
+#pragma unroll
+  for (int pr = 0; pr < 8; ++pr) sincosf(-shift * theta[h * 32 + 8 * rg + pr], &sn[pr], &cs[pr]);
+  const size_t base = (size_t)bh * NW * 4096;
+  float x[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    x[r] = S0 ? S0[(size_t)bh * 4096 + (16 * rg + r) * 64 + j] : 0.f;
+    Ss[16 * rg + r][j] = x[r];
+    Sin[base + (16 * rg + r) * 64 + j] = x[r];
+  }
+  for (int w = 0; w + 1 < NW; ++w) {
+    const float* Mw = M + base + (size_t)w * 4096;
+    const float* Rw = R + base + (size_t)w * 4096;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = Rw[(16 * rg + r) * 64 + j];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      *reinterpret_cast<f32x4*>(Ms + 4 * (tid + 256 * u)) = *reinterpret_cast<const f32x4*>(Mw + 4 * (tid + 256 * u));
+    __syncthreads();  // M[w] staged; S_in[w] (written at the end of the previous window) visible
+    for (int k4 = 0; k4 < 64; k4 += 4) {
+      const float s0 = Ss[k4][j], s1 = Ss[k4 + 1][j], s2 = Ss[k4 + 2][j], s3 = Ss[k4 + 3][j];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const f32x4 m = *reinterpret_cast<const f32x4*>(Ms + (16 * rg + r) * 64 + k4);
+        x[r] += m[0] * s0 + m[1] * s1 + m[2] * s2 + m[3] * s3;
+      }
+    }
+    __syncthreads();  // every read of S_in[w] and M[w] done before they are overwritten
+#pragma unroll
+    for (int pr = 0; pr < 8; ++pr) {
+      const float a = x[2 * pr], b = x[2 * pr + 1];
+      x[2 * pr] = a * cs[pr] - b * sn[pr];
+      x[2 * pr + 1] = a * sn[pr] + b * cs[pr];
+    }
+    float* dst = Sin + base + (size_t)(w + 1) * 4096;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      Ss[16 * rg + r][j] = x[r];
+      dst[(16 * rg + r) * 64 + j] = x[r];
+    }
+  }
+}
+
 int set_smem(const void* fn, size_t bytes) { return (int)pgn_lds_limit(fn, bytes); }
 
 int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
@@ -1798,4 +1862,15 @@ extern "C" int pragnosia_aspin_delta_bwd(const void* q, const void* k, const voi
                                 B, H, T, st)
                  : delta_bwd<2>(q, k, v, la, beta, sent, W, X, dO, dS_final, dq, dk, dv, dla, dbeta, dS0, workspace,
                                 B, H, T, st);
+}
+
+extern "C" int pragnosia_aspin_delta_window_prefix(const float* M, const float* R, const float* S0, const float* theta,
+                                                   float shift, float* S_in, int64_t BH, int64_t H, int64_t NW,
+                                                   void* stream) {
+  PGN_CHECK_ARG(M && R && theta && S_in && BH > 0 && H > 0 && NW > 0 && BH % H == 0);
+  PGN_CHECK_ARG(BH < ((int64_t)1 << 31) && BH * NW < ((int64_t)1 << 40));
+  PGN_CHECK_ARG(((uintptr_t)M | (uintptr_t)R) % 16 == 0);
+  hipLaunchKernelGGL(delta_window_prefix, dim3((unsigned)BH), dim3(256), 0, (hipStream_t)stream, M, R, S0, theta,
+                     shift, S_in, (int)H, (int)NW);
+  PGN_RETURN_LAUNCH();
 }

@@ -9,3 +9,6 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X) and the built HIP library")
+    # registers the torch.ops.pragnosia namespace for every test module, whichever subset runs (the library itself
+    # loads on the first call)
+    import pragnosia_amd.ops  # noqa: F401

@@ -211,11 +211,13 @@ def test_windows_match_window_loop(B, H, T, W):
     assert sent.shape[2] == (T + 63) // 64 and torch.isfinite(sent.float()).all()
 
 
-def test_windows_carrier_module_matches_window_calls():
-    """AssocCarrier.forward_windows (one pass) against calling forward on each window with the carried state."""
+@pytest.mark.parametrize("delta", [False, True])
+def test_windows_carrier_module_matches_window_calls(delta):
+    """AssocCarrier.forward_windows (one pass; the delta rule from the windows' affine state maps, its ragged last
+    window zero-padded) against calling forward on each window with the carried state."""
     from pragnosia_amd.assoc import AssocCarrier
     torch.manual_seed(12)
-    m = AssocCarrier(128).cuda().eval()
+    m = AssocCarrier(128, delta=delta).cuda().eval()
     with torch.no_grad():
         for p in m.parameters():
             p.add_(torch.randn_like(p) * 0.05)

@@ -100,6 +100,54 @@ def test_cfg3_one_pass_windows_full_size():
     print(f"cfg3 one pass vs loop {rel(o1, oloop):.2e}, vs oracle out {rel(o1, o_r):.2e} state {rel(S1, Sr):.2e}")
 
 
+def test_cfg3_delta_windows_full_size():
+    """configs[3]'s shape with the delta write rule (beta = sigmoid(N(0, 1)) per token and head): the 16 windows of 512
+    through `aspin_delta_windows` (every window at once from its affine state map: two state passes, the prefix of
+    the maps with the -512 theta rebase, one output pass) against (i) the window-by-window loop on the GPU
+    (aspin_delta + aspin_rebase per window) and (ii) the CPU oracle's window loop (`oracle.aspin.assoc_scan` with
+    beta per window, `oracle.aspin.rebase` between), outputs and the final state, on the same bf16 inputs; also with
+    an entering state."""
+    from pragnosia_amd import ops  # noqa: F401
+    from pragnosia_amd.assoc import rotate
+    B, H, T, D, W = 2, 12, 8192, 64, 512
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(B, H, T, D, generator=g)
+    k = F.normalize(torch.randn(B, H, T, D, generator=g), dim=-1)
+    v = torch.randn(B, H, T, D, generator=g)
+    la = F.logsigmoid(torch.randn(B, H, T, generator=g) + 4.0)
+    be = torch.sigmoid(torch.randn(B, H, T, generator=g))
+    th = torch.rand(H, D // 2, generator=g) * 0.1
+    S0 = torch.randn(B, H, D, D, generator=g) * 0.1
+    op = torch.ops.pragnosia
+    qd, kd, vd, lad, bed, thd, S0d = (t.cuda() for t in (q, k, v, la, be, th, S0))
+    loc = torch.arange(T, device="cuda") % W
+    qw, kw, vb = rotate(qd, thd, loc).bfloat16(), rotate(kd, thd, loc).bfloat16(), vd.bfloat16()
+    qc, kc, vc = qw.float().cpu(), kw.float().cpu(), vb.float().cpu()
+    for s0 in (None, S0d):
+        with torch.no_grad():
+            o1, S1 = op.aspin_delta_windows(qw, kw, vb, lad, bed, s0, thd, W)
+            S, outs = s0, []
+            for s in range(0, T, W):
+                if s:
+                    S = op.aspin_rebase(S, thd, None, float(W))
+                o, S, _, _, _ = op.aspin_delta(qw[:, :, s:s + W], kw[:, :, s:s + W], vb[:, :, s:s + W],
+                                               lad[:, :, s:s + W], bed[:, :, s:s + W], S, False)
+                outs.append(o)
+            oloop = torch.cat(outs, 2)
+        torch.cuda.synchronize()
+        e_loop = (rel(o1, oloop), rel(S1, S))
+        Sr, outs = (None if s0 is None else S0.double()), []
+        for s in range(0, T, W):
+            if s:
+                Sr = OA.rebase(Sr, th.double(), float(W))
+            o, Sr = OA.assoc_scan(qc[:, :, s:s + W].double(), kc[:, :, s:s + W].double(), vc[:, :, s:s + W].double(),
+                                  la[:, :, s:s + W].double(), Sr, chunk=64, beta=be[:, :, s:s + W].double())
+            outs.append(o)
+        e_ref = (rel(o1, torch.cat(outs, 2)), rel(S1, Sr))
+        print(f"cfg3 delta one pass (S0 {'given' if s0 is not None else 'none'}): vs loop {e_loop}, vs oracle {e_ref}")
+        assert max(e_loop + e_ref) < TOL
+
+
 @pytest.mark.parametrize("batch", [1, 64])
 def test_cfg4_decode_matches_oracle(batch):
     """LM(vocab 8192, d 768, 12 layers, 12 heads of 64, ctx 512, aspin), weights N(0, 0.02), a 512-token
