@@ -69,20 +69,10 @@ def _plain_scan_wide(q, k, v, la, S0, want):
     return _op.aspin_chunk_wide(q, k, v, la.float(), S0, want)
 
 
-def _prep_wide(qp, kp, vp, gate, theta, pos, dtype=torch.bfloat16):
-    """The prep for heads the prep kernel does not take (128 wide), as torch on the GPU: unit-normalise q, k, v per
-    head (eps 1e-12), scale k by sigmoid(gate) (plain rule), rotate q and k at `pos`, transpose to (B, H, T, dk) and
-    round to `dtype` (`src/assoc.py:453-460`)."""
-    q, k, v = (F.normalize(t.transpose(1, 2).float(), dim=-1, eps=1e-12) for t in (qp, kp, vp))
-    if gate is not None:
-        k = k * torch.sigmoid(gate.float()).transpose(1, 2).unsqueeze(-1)
-    th = theta.float()
-    return rotate(q, th, pos).to(dtype), rotate(k, th, pos).to(dtype), v.to(dtype)
-
-
 def _rebase_wide(S, theta, p_dev, p_host):
-    """Key rows (2i, 2i+1) of S rotated by -p0 theta[h, i] (`src/assoc.py:399-402`) as torch on the GPU, for heads
-    the rebase kernel does not take; p0 the device scalar p_dev when given, else p_host."""
+    """Key rows (2i, 2i+1) of S rotated by -p0 theta[h, i] (`src/assoc.py:399-402`) as torch on the GPU, for states
+    the rebase kernel does not take (heads other than 64 and 128 wide, fp64); p0 the device scalar p_dev when given,
+    else p_host."""
     Dv = S.shape[-1]
     p = p_dev.float() if p_dev is not None else torch.tensor(p_host, device=S.device, dtype=torch.float32)
     return rotate(S.transpose(-1, -2), theta.float(), (-p).expand(Dv)).transpose(-1, -2).contiguous()
@@ -350,7 +340,7 @@ class AssocCarrier(nn.Module):
         write-gate (plain) or write-strength (delta) projections and one kernel from its output; otherwise the
         reference's composition: separate projections (one GEMM under FUSED_PROJ), convolution, elementwise decay,
         gate and strength, prep."""
-        if (FUSED_PLUMBING and not self.key_topk and self.dk == HEAD_DIM_KERNEL
+        if (FUSED_PLUMBING and not self.key_topk and self.dk in (HEAD_DIM_KERNEL, HEAD_DIM_WIDE)
                 and getattr(self, "beta_scale", None) is None and getattr(self, "sconv", None) is None):
             gated = not (self.delta or self.write_all)
             extra = [self.wi.weight] if gated else ([self.wb.weight] if self.delta else [])
@@ -359,13 +349,10 @@ class AssocCarrier(nn.Module):
             q, k, v, la, beta = _op.aspin_prep_proj(
                 P, self.h, self.wa.bias, self.A, self.la_floor if self.hl_floor else None,
                 self.wi.bias if gated else None, self.wb.bias if self.delta else None,
-                0.75 if (self.delta and self.write_all) else 0.0, gated, self.theta, pos)
+                0.75 if (self.delta and self.write_all) else 0.0, gated, self.theta, pos, self.dk)
             return q, k, v, la, (beta if self.delta else None), P.dtype, cc
         qp, kp, vp, gate, la, bt, cc = self._projections(z, cc)
-        if self.dk == HEAD_DIM_KERNEL:
-            q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
-        else:
-            q, k, v = _prep_wide(qp, kp, vp, gate, self.theta, pos)
+        q, k, v = _op.aspin_prep(qp, kp, vp, gate, self.theta, pos)
         bt = None if bt is None else bt.transpose(1, 2).float()
         return q, k, v, la.transpose(1, 2).float(), bt, qp.dtype, cc
 
@@ -380,7 +367,7 @@ class AssocCarrier(nn.Module):
         token-major)."""
         B, H, T, Dk = o.shape
         if (FUSED_PLUMBING and dtype in (torch.bfloat16, torch.float32) and self.on.weight is not None
-                and Dk == HEAD_DIM_KERNEL):
+                and Dk in (HEAD_DIM_KERNEL, HEAD_DIM_WIDE)):
             eps = self.on.eps if self.on.eps is not None else _op_mod.RMS_EPS
             return _op.aspin_out(o, self.on.weight, eps, dtype == torch.bfloat16)[0]
         return self.on(o.to(dtype)).transpose(1, 2).reshape(B, T, H * Dk)
@@ -423,8 +410,7 @@ class AssocCarrier(nn.Module):
         elif kern:
             wide = self.dk == HEAD_DIM_WIDE
             if shifted:
-                S0 = (_rebase_wide(S0.float(), self.theta, p_dev, p_host) if wide
-                      else _op.aspin_rebase(S0, self.theta, p_dev, p_host))
+                S0 = _op.aspin_rebase(S0, self.theta, p_dev, p_host)
             pos = _positions(T, x.device, getattr(self, "pos_wrap", None))
             q, k, v, la, bt, dtype, cc = self._scan_inputs(z, pos, cc)
             fused = FUSED_SCAN and self.delta and not self.need_sent
@@ -449,7 +435,7 @@ class AssocCarrier(nn.Module):
             # autocast, as the reference's bf16 matmuls)
             if shifted:
                 S0 = (_op.aspin_rebase(S0, self.theta, p_dev, p_host)
-                      if self.dk == HEAD_DIM_KERNEL and S0.dtype == torch.float32
+                      if self.dk in (HEAD_DIM_KERNEL, HEAD_DIM_WIDE) and S0.dtype == torch.float32
                       else _rebase_wide(S0, self.theta, p_dev, p_host))
             pos = _positions(T, x.device, getattr(self, "pos_wrap", None))
             q, k, v, la, bt, dtype, cc = self._torch_inputs(z, pos, cc)

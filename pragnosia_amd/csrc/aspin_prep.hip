@@ -1,6 +1,6 @@
 // The plumbing between the carrier's projections and the scan, and the carried-state rebase.
 //
-// prep: per (batch, token, head) row of 64 channels: q, k, v are unit-normalised (x / max(|x|, 1e-12)), k is
+// prep: per (batch, token, head) row of D = 64 or 128 channels: q, k, v are unit-normalised (x / max(|x|, 1e-12)), k is
 // scaled by the write gate sigmoid(g) (plain rule; no gate for the delta rule), q and k are rotated by the angle
 // pos_t * theta[h, i] on interleaved channel pairs (2i, 2i+1), and the three results are cast to bf16 and written in
 // the scan's (B, H, T, D) layout from the projections' (B, T, H, D) layout (the reference's `_prep_fwd`,
@@ -10,19 +10,18 @@
 // writing the projections' gradients in THEIR layout, the gate's per (b, t, h), and theta's as one partial sum per
 // (batch, 64-token block) that the caller reduces.
 //
-// One workgroup of 256 threads per (batch, head, 64-token block): 8 threads per row (eight channels, four rotation
-// pairs each, one 16-byte access per tensor for bf16), 32 rows per pass, 2 passes; the norms are 8-lane
-// butterflies. The projections
+// One workgroup of 256 threads per (batch, head, 64-token block): D / 8 threads per row (eight channels, four rotation
+// pairs each, one 16-byte access per tensor for bf16), 2048 / D rows per pass; the norms are D / 8-lane butterflies.
+// The projections
 // (and their gradients) may be column slices of one wider row per token (`in_stride` elements apart), such as one
 // GEMM's output holding q, k, v and the gate logits side by side.
 //
-// rebase: S (B, H, Dk, Dv) with keys on dim 2; key rows (2i, 2i+1) are rotated by -p0 * theta[h, i] (the state written
+// rebase: S (B, H, D, D) with keys on dim 2; key rows (2i, 2i+1) are rotated by -p0 * theta[h, i] (the state written
 // at positions up to p0 - 1, re-expressed for a window whose positions restart at 0: `src/assoc.py:399-402`).
 #include "common.h"
 
 namespace {
 
-constexpr int D = 64;
 constexpr int TB = 64;    // tokens per workgroup
 
 PGN_DEVICE float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
@@ -82,27 +81,31 @@ PGN_DEVICE void st8<__bf16>(__bf16* p, const float* x) {
   *reinterpret_cast<bf16x8*>(p) = a;
 }
 
-// sum over the 8 lanes that share a row (lane bits 0..2)
-PGN_DEVICE float sum8(float x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 4);
+// sum over the L lanes that share a row (lane bits 0 .. log2 L - 1)
+template <int L>
+PGN_DEVICE float sum_row(float x) {
+#pragma unroll
+  for (int o = 1; o < L; o <<= 1) x += __shfl_xor(x, o);
   return x;
 }
 
+template <int L>
 PGN_DEVICE float inv_norm8(const float* x) {
   float n = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) n += x[e] * x[e];
-  return 1.f / fmaxf(sqrtf(sum8(n)), 1e-12f);
+  return 1.f / fmaxf(sqrtf(sum_row<L>(n)), 1e-12f);
 }
 
-// Thread = (row slot rs = tid / 8, channel group j = tid % 8): channels 8 j .. 8 j + 7 of one row, i.e. the
-// interleaved pairs 4 j .. 4 j + 3; 32 rows per pass, two passes per 64-token block.
-constexpr int LANES = 8;
-constexpr int SLOTS = 256 / LANES;
+// Thread = (row slot rs = tid / LANES, channel group j = tid % LANES): channels 8 j .. 8 j + 7 of one row, i.e. the
+// interleaved pairs 4 j .. 4 j + 3; LANES = D / 8 threads a row, SLOTS rows per pass.
+template <int D>
+struct RowSplit {
+  static constexpr int LANES = D / 8;
+  static constexpr int SLOTS = 256 / LANES;
+};
 
-template <typename In>
+template <typename In, int D>
 __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const In* __restrict__ kp,
                                                 const In* __restrict__ vp, const float* __restrict__ gl,
                                                 const float* __restrict__ theta, const int64_t* __restrict__ pos,
@@ -110,6 +113,7 @@ __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const
                                                 __bf16* __restrict__ v, int T, int H, int ntb, int64_t S,
                                                 Cols<In> cols, float* __restrict__ la,
                                                 float* __restrict__ beta) {
+  constexpr int LANES = RowSplit<D>::LANES, SLOTS = RowSplit<D>::SLOTS;
   const int blk = blockIdx.x;
   const int bh = blk / ntb, tb = blk - bh * ntb;
   const int b = bh / H, h = bh - b * H;
@@ -129,8 +133,8 @@ __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const
     ld8<In>(qp + in, xq);
     ld8<In>(kp + in, xk);
     ld8<In>(vp + in, xv);
-    const float iq = inv_norm8(xq), iv = inv_norm8(xv);
-    float ik = inv_norm8(xk);
+    const float iq = inv_norm8<LANES>(xq), iv = inv_norm8<LANES>(xv);
+    float ik = inv_norm8<LANES>(xk);
     if (cols.gcol)
       ik *= sigmoidf_((float)cols.gcol[row + h] + (cols.gbias ? cols.gbias[h] : 0.f));
     else if (gl)
@@ -168,7 +172,7 @@ __global__ __launch_bounds__(256) void prep_fwd(const In* __restrict__ qp, const
 // sigmoid(logit_a + b) (mask: the floor not active), dlogit_g = dsig sig (1 - sig), dlogit_b = dbeta mask sig (1 -
 // sig) (mask: bmin not active); and one partial per workgroup of the three per-head sums (d gbias or d bbias,
 // d abias, dA = sum dla mask la) to part, laid out (B, T blocks, H, 3) like the theta partials.
-template <typename In>
+template <typename In, int D>
 __global__ __launch_bounds__(256) void prep_bwd(
     const In* __restrict__ qp, const In* __restrict__ kp, const In* __restrict__ vp, const float* __restrict__ gl,
     const float* __restrict__ theta, const int64_t* __restrict__ pos, const __bf16* __restrict__ dq,
@@ -176,6 +180,7 @@ __global__ __launch_bounds__(256) void prep_bwd(
     In* __restrict__ dvp, float* __restrict__ dgl, float* __restrict__ dth, int T, int H, int ntb, int64_t S,
     Cols<In> cols, const float* __restrict__ dla, const float* __restrict__ dbeta, In* __restrict__ dcol,
     float* __restrict__ part) {
+  constexpr int LANES = RowSplit<D>::LANES, SLOTS = RowSplit<D>::SLOTS;
   __shared__ float red[SLOTS][D / 2];
   __shared__ float red3[SLOTS][3];
   const int blk = blockIdx.x;
@@ -218,7 +223,7 @@ __global__ __launch_bounds__(256) void prep_bwd(
       float x[8], g[8], du[8], o[8];
       ld8<In>(qp + in, x);
       ld8<__bf16>(dq + out, g);
-      const float inv = inv_norm8(x);
+      const float inv = inv_norm8<LANES>(x);
       float dot = 0.f;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -228,7 +233,7 @@ __global__ __launch_bounds__(256) void prep_bwd(
         du[2 * u + 1] = g2 * cs[u] - g1 * sn[u];
         dot += u1 * du[2 * u] + u2 * du[2 * u + 1];
       }
-      dot = sum8(dot);
+      dot = sum_row<LANES>(dot);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (du[e] - x[e] * inv * dot) * inv;
       st8<In>(dqp + in, o);
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(256) void prep_bwd(
       float x[8], g[8], du[8], o[8], r[8];
       ld8<In>(kp + in, x);
       ld8<__bf16>(dk + out, g);
-      const float inv = inv_norm8(x);
+      const float inv = inv_norm8<LANES>(x);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float u1 = x[2 * u] * inv, u2 = x[2 * u + 1] * inv;
@@ -250,7 +255,7 @@ __global__ __launch_bounds__(256) void prep_bwd(
         float dsg = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) dsg += g[e] * r[e];
-        dsg = sum8(dsg);
+        dsg = sum_row<LANES>(dsg);
         if (j == 0) {
           const float dlg = dsg * sg * (1.f - sg);
           if (cols.gcol) {
@@ -272,7 +277,7 @@ __global__ __launch_bounds__(256) void prep_bwd(
         du[2 * u + 1] = g2 * cs[u] - g1 * sn[u];
         dot += x[2 * u] * inv * du[2 * u] + x[2 * u + 1] * inv * du[2 * u + 1];
       }
-      dot = sum8(dot);
+      dot = sum_row<LANES>(dot);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (du[e] - x[e] * inv * dot) * inv;
       st8<In>(dkp + in, o);
@@ -281,11 +286,11 @@ __global__ __launch_bounds__(256) void prep_bwd(
       float x[8], g[8], o[8];
       ld8<In>(vp + in, x);
       ld8<__bf16>(dv + out, g);
-      const float inv = inv_norm8(x);
+      const float inv = inv_norm8<LANES>(x);
       float dot = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) dot += x[e] * inv * g[e];
-      dot = sum8(dot);
+      dot = sum_row<LANES>(dot);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (g[e] - x[e] * inv * dot) * inv;
       st8<In>(dvp + in, o);
@@ -315,56 +320,72 @@ __global__ __launch_bounds__(256) void prep_bwd(
   }
 }
 
-// rebase: one workgroup of 256 threads per (batch, head); thread = (value column j, group of 16 key rows)
+// rebase: one workgroup of 256 threads per (batch, head); thread = (value column j of each 64-column half, group rg
+// of D / 4 key rows, i.e. D / 8 rotation pairs)
+template <int D>
 __global__ __launch_bounds__(256) void rebase_fwd(const float* __restrict__ S, const float* __restrict__ theta,
                                                   const float* __restrict__ p0d, float p0h, float* __restrict__ So,
                                                   int H) {
+  constexpr int NP = D / 8;  // rotation pairs per thread
   const int bh = blockIdx.x, h = bh % H;
   const int j = threadIdx.x & 63, rg = threadIdx.x >> 6;
   const float p0 = p0d ? *p0d : p0h;
   const float* src = S + (size_t)bh * D * D;
   float* dst = So + (size_t)bh * D * D;
-  float x[16];
+  float sn[NP], cs[NP];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) x[r] = src[(16 * rg + r) * D + j];
+  for (int pr = 0; pr < NP; ++pr) sincosf(-p0 * theta[h * (D / 2) + NP * rg + pr], &sn[pr], &cs[pr]);
 #pragma unroll
-  for (int pr = 0; pr < 8; ++pr) {
-    const int ip = 8 * rg + pr;
-    float s, c;
-    sincosf(-p0 * theta[h * (D / 2) + ip], &s, &c);
-    const float a = x[2 * pr], bb = x[2 * pr + 1];
-    dst[(2 * ip) * D + j] = a * c - bb * s;
-    dst[(2 * ip + 1) * D + j] = a * s + bb * c;
+  for (int ch = 0; ch < D / 64; ++ch) {
+    const int col = 64 * ch + j;
+    float x[2 * NP];
+#pragma unroll
+    for (int r = 0; r < 2 * NP; ++r) x[r] = src[(2 * NP * rg + r) * D + col];
+#pragma unroll
+    for (int pr = 0; pr < NP; ++pr) {
+      const int ip = NP * rg + pr;
+      const float a = x[2 * pr], bb = x[2 * pr + 1];
+      dst[(2 * ip) * D + col] = a * cs[pr] - bb * sn[pr];
+      dst[(2 * ip + 1) * D + col] = a * sn[pr] + bb * cs[pr];
+    }
   }
 }
 
 // backward of rebase: dS = R^T g; d(angle) = g2 r1 - g1 r2 summed over value columns, times -p0 for theta
+template <int D>
 __global__ __launch_bounds__(256) void rebase_bwd(const float* __restrict__ S, const float* __restrict__ theta,
                                                   const float* __restrict__ p0d, float p0h,
                                                   const float* __restrict__ g, float* __restrict__ dS,
                                                   float* __restrict__ dth, int H) {
-  __shared__ float red[4][64][9];
+  constexpr int NP = D / 8;
+  __shared__ float red[4][64][NP + 1];
   const int bh = blockIdx.x, h = bh % H;
   const int j = threadIdx.x & 63, rg = threadIdx.x >> 6;
   const float p0 = p0d ? *p0d : p0h;
   const size_t off = (size_t)bh * D * D;
 #pragma unroll
-  for (int pr = 0; pr < 8; ++pr) {
-    const int ip = 8 * rg + pr;
+  for (int pr = 0; pr < NP; ++pr) {
+    const int ip = NP * rg + pr;
     float s, c;
     sincosf(-p0 * theta[h * (D / 2) + ip], &s, &c);
-    const float a = S[off + (2 * ip) * D + j], bb = S[off + (2 * ip + 1) * D + j];
-    const float g1 = g[off + (2 * ip) * D + j], g2 = g[off + (2 * ip + 1) * D + j];
-    const float r1 = a * c - bb * s, r2 = a * s + bb * c;
-    if (dS) {
-      dS[off + (2 * ip) * D + j] = g1 * c + g2 * s;
-      dS[off + (2 * ip + 1) * D + j] = g2 * c - g1 * s;
+    float acc = 0.f;
+#pragma unroll
+    for (int ch = 0; ch < D / 64; ++ch) {
+      const int col = 64 * ch + j;
+      const float a = S[off + (2 * ip) * D + col], bb = S[off + (2 * ip + 1) * D + col];
+      const float g1 = g[off + (2 * ip) * D + col], g2 = g[off + (2 * ip + 1) * D + col];
+      const float r1 = a * c - bb * s, r2 = a * s + bb * c;
+      if (dS) {
+        dS[off + (2 * ip) * D + col] = g1 * c + g2 * s;
+        dS[off + (2 * ip + 1) * D + col] = g2 * c - g1 * s;
+      }
+      acc += g2 * r1 - g1 * r2;
     }
-    red[rg][j][pr] = (g2 * r1 - g1 * r2) * (-p0);
+    red[rg][j][pr] = acc * (-p0);
   }
   __syncthreads();
   if (dth && threadIdx.x < D / 2) {
-    const int ip = threadIdx.x, rgi = ip >> 3, pr = ip & 7;
+    const int ip = threadIdx.x, rgi = ip / NP, pr = ip % NP;
     float acc = 0.f;
     for (int jj = 0; jj < 64; ++jj) acc += red[rgi][jj][pr];
     dth[(size_t)bh * (D / 2) + ip] = acc;
@@ -377,24 +398,70 @@ bool shape_ok(int64_t B, int64_t T, int64_t H) {
 
 }  // namespace
 
+namespace {
+
+bool width_ok(int64_t Dh) { return Dh == 64 || Dh == 128; }
+
+// the launches at head width D (64 or 128), input type In
+template <typename In, int D>
+void launch_prep_fwd(dim3 grid, hipStream_t st, const In* qp, const In* kp, const In* vp, const float* gate,
+                     const float* theta, const int64_t* pos, void* q, void* k, void* v, int T, int H, int ntb,
+                     int64_t stride, Cols<In> cols, float* la, float* beta) {
+  hipLaunchKernelGGL((prep_fwd<In, D>), grid, dim3(256), 0, st, qp, kp, vp, gate, theta, pos, (__bf16*)q, (__bf16*)k,
+                     (__bf16*)v, T, H, ntb, stride, cols, la, beta);
+}
+
+template <typename In, int D>
+void launch_prep_bwd(dim3 grid, hipStream_t st, const In* qp, const In* kp, const In* vp, const float* gate,
+                     const float* theta, const int64_t* pos, const void* dq, const void* dk, const void* dv, In* dqp,
+                     In* dkp, In* dvp, float* dgate, float* dth, int T, int H, int ntb, int64_t stride, Cols<In> cols,
+                     const float* dla, const float* dbeta, In* dcol, float* part) {
+  hipLaunchKernelGGL((prep_bwd<In, D>), grid, dim3(256), 0, st, qp, kp, vp, gate, theta, pos, (const __bf16*)dq,
+                     (const __bf16*)dk, (const __bf16*)dv, dqp, dkp, dvp, dgate, dth, T, H, ntb, stride, cols, dla,
+                     dbeta, dcol, part);
+}
+
+template <typename In>
+void prep_fwd_any(int64_t Dh, dim3 grid, hipStream_t st, const In* qp, const In* kp, const In* vp, const float* gate,
+                  const float* theta, const int64_t* pos, void* q, void* k, void* v, int T, int H, int ntb,
+                  int64_t stride, Cols<In> cols, float* la, float* beta) {
+  if (Dh == 64)
+    launch_prep_fwd<In, 64>(grid, st, qp, kp, vp, gate, theta, pos, q, k, v, T, H, ntb, stride, cols, la, beta);
+  else
+    launch_prep_fwd<In, 128>(grid, st, qp, kp, vp, gate, theta, pos, q, k, v, T, H, ntb, stride, cols, la, beta);
+}
+
+template <typename In>
+void prep_bwd_any(int64_t Dh, dim3 grid, hipStream_t st, const In* qp, const In* kp, const In* vp, const float* gate,
+                  const float* theta, const int64_t* pos, const void* dq, const void* dk, const void* dv, In* dqp,
+                  In* dkp, In* dvp, float* dgate, float* dth, int T, int H, int ntb, int64_t stride, Cols<In> cols,
+                  const float* dla, const float* dbeta, In* dcol, float* part) {
+  if (Dh == 64)
+    launch_prep_bwd<In, 64>(grid, st, qp, kp, vp, gate, theta, pos, dq, dk, dv, dqp, dkp, dvp, dgate, dth, T, H, ntb,
+                            stride, cols, dla, dbeta, dcol, part);
+  else
+    launch_prep_bwd<In, 128>(grid, st, qp, kp, vp, gate, theta, pos, dq, dk, dv, dqp, dkp, dvp, dgate, dth, T, H,
+                             ntb, stride, cols, dla, dbeta, dcol, part);
+}
+
+}  // namespace
+
 extern "C" int pragnosia_aspin_prep_fwd(const void* qp, const void* kp, const void* vp, const float* gate,
                                         const float* theta, const int64_t* pos, void* q, void* k, void* v,
                                         int64_t B, int64_t T, int64_t H, int64_t Dh, int64_t in_stride, int in_bf16,
                                         void* stream) {
-  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  if (!width_ok(Dh)) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, T, H));
-  PGN_CHECK_ARG(qp && kp && vp && theta && pos && q && k && v && in_stride >= H * D);
+  PGN_CHECK_ARG(qp && kp && vp && theta && pos && q && k && v && in_stride >= H * Dh);
   const int ntb = (int)((T + TB - 1) / TB);
   const dim3 grid((unsigned)(B * H * ntb));
   hipStream_t st = (hipStream_t)stream;
   if (in_bf16)
-    hipLaunchKernelGGL(prep_fwd<__bf16>, grid, dim3(256), 0, st, (const __bf16*)qp, (const __bf16*)kp,
-                       (const __bf16*)vp, gate, theta, pos, (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb,
-                       in_stride, Cols<__bf16>{}, nullptr, nullptr);
+    prep_fwd_any<__bf16>(Dh, grid, st, (const __bf16*)qp, (const __bf16*)kp, (const __bf16*)vp, gate, theta, pos, q, k,
+                         v, (int)T, (int)H, ntb, in_stride, Cols<__bf16>{}, nullptr, nullptr);
   else
-    hipLaunchKernelGGL(prep_fwd<float>, grid, dim3(256), 0, st, (const float*)qp, (const float*)kp,
-                       (const float*)vp, gate, theta, pos, (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb,
-                       in_stride, Cols<float>{}, nullptr, nullptr);
+    prep_fwd_any<float>(Dh, grid, st, (const float*)qp, (const float*)kp, (const float*)vp, gate, theta, pos, q, k, v,
+                        (int)T, (int)H, ntb, in_stride, Cols<float>{}, nullptr, nullptr);
   PGN_RETURN_LAUNCH();
 }
 
@@ -405,24 +472,22 @@ extern "C" int pragnosia_aspin_prep_bwd(const void* qp, const void* kp, const vo
                                         const void* dv, void* dqp, void* dkp, void* dvp, float* dgate,
                                         float* dtheta_partial, int64_t B, int64_t T, int64_t H, int64_t Dh,
                                         int64_t in_stride, int in_bf16, void* stream) {
-  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  if (!width_ok(Dh)) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, T, H));
   PGN_CHECK_ARG(qp && kp && vp && theta && pos && dq && dk && dv && dqp && dkp && dvp && dtheta_partial);
-  PGN_CHECK_ARG(in_stride >= H * D);
+  PGN_CHECK_ARG(in_stride >= H * Dh);
   PGN_CHECK_ARG(gate == nullptr || dgate != nullptr);
   const int ntb = (int)((T + TB - 1) / TB);
   const dim3 grid((unsigned)(B * H * ntb));
   hipStream_t st = (hipStream_t)stream;
   if (in_bf16)
-    hipLaunchKernelGGL(prep_bwd<__bf16>, grid, dim3(256), 0, st, (const __bf16*)qp, (const __bf16*)kp,
-                       (const __bf16*)vp, gate, theta, pos, (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv,
-                       (__bf16*)dqp, (__bf16*)dkp, (__bf16*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb,
-                       in_stride, Cols<__bf16>{}, nullptr, nullptr, nullptr, nullptr);
+    prep_bwd_any<__bf16>(Dh, grid, st, (const __bf16*)qp, (const __bf16*)kp, (const __bf16*)vp, gate, theta, pos, dq,
+                         dk, dv, (__bf16*)dqp, (__bf16*)dkp, (__bf16*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb,
+                         in_stride, Cols<__bf16>{}, nullptr, nullptr, nullptr, nullptr);
   else
-    hipLaunchKernelGGL(prep_bwd<float>, grid, dim3(256), 0, st, (const float*)qp, (const float*)kp,
-                       (const float*)vp, gate, theta, pos, (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv,
-                       (float*)dqp, (float*)dkp, (float*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb, in_stride,
-                       Cols<float>{}, nullptr, nullptr, nullptr, nullptr);
+    prep_bwd_any<float>(Dh, grid, st, (const float*)qp, (const float*)kp, (const float*)vp, gate, theta, pos, dq, dk,
+                        dv, (float*)dqp, (float*)dkp, (float*)dvp, dgate, dtheta_partial, (int)T, (int)H, ntb,
+                        in_stride, Cols<float>{}, nullptr, nullptr, nullptr, nullptr);
   PGN_RETURN_LAUNCH();
 }
 
@@ -430,8 +495,8 @@ namespace {
 
 // the H-column groups at la_col (required), gate_col and beta_col (each optional: -1) lie past q, k, v, inside the
 // row, and do not overlap; a row has a gate or a strength, not both
-bool proj_cols_ok(int64_t H, int64_t stride, int64_t la_col, int64_t gate_col, int64_t beta_col) {
-  const int64_t hd = H * D;
+bool proj_cols_ok(int64_t H, int64_t Dh, int64_t stride, int64_t la_col, int64_t gate_col, int64_t beta_col) {
+  const int64_t hd = H * Dh;
   if (stride < 3 * hd || la_col < 3 * hd || la_col + H > stride) return false;
   if (gate_col >= 0 && beta_col >= 0) return false;
   const int64_t x = gate_col >= 0 ? gate_col : beta_col;
@@ -456,28 +521,26 @@ extern "C" int pragnosia_aspin_prep_proj_fwd(const void* P, int64_t stride, int6
                                              float beta_min, const float* theta, const int64_t* pos, void* q,
                                              void* k, void* v, float* la, float* beta, int64_t B, int64_t T,
                                              int64_t H, int64_t Dh, int in_bf16, void* stream) {
-  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  if (!width_ok(Dh)) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, T, H));
   PGN_CHECK_ARG(P && la_bias && A && theta && pos && q && k && v && la && (beta_col < 0 || beta));
-  PGN_CHECK_ARG(proj_cols_ok(H, stride, la_col, gate_col, beta_col));
+  PGN_CHECK_ARG(proj_cols_ok(H, Dh, stride, la_col, gate_col, beta_col));
   const int ntb = (int)((T + TB - 1) / TB);
   const dim3 grid((unsigned)(B * H * ntb));
-  const int64_t hd = H * D;
+  const int64_t hd = H * Dh;
   hipStream_t st = (hipStream_t)stream;
   if (in_bf16) {
     const __bf16* p = (const __bf16*)P;
-    hipLaunchKernelGGL(prep_fwd<__bf16>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
-                       (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb, stride,
-                       proj_cols<__bf16>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias, beta_bias,
-                                         beta_min),
-                       la, beta);
+    prep_fwd_any<__bf16>(Dh, grid, st, p, p + hd, p + 2 * hd, nullptr, theta, pos, q, k, v, (int)T, (int)H, ntb,
+                         stride, proj_cols<__bf16>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias,
+                                                   beta_bias, beta_min),
+                         la, beta);
   } else {
     const float* p = (const float*)P;
-    hipLaunchKernelGGL(prep_fwd<float>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
-                       (__bf16*)q, (__bf16*)k, (__bf16*)v, (int)T, (int)H, ntb, stride,
-                       proj_cols<float>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias, beta_bias,
-                                        beta_min),
-                       la, beta);
+    prep_fwd_any<float>(Dh, grid, st, p, p + hd, p + 2 * hd, nullptr, theta, pos, q, k, v, (int)T, (int)H, ntb,
+                        stride, proj_cols<float>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias,
+                                                 beta_bias, beta_min),
+                        la, beta);
   }
   PGN_RETURN_LAUNCH();
 }
@@ -495,54 +558,61 @@ extern "C" int pragnosia_aspin_prep_proj_bwd(const void* P, int64_t stride, int6
                                              const float* dbeta, void* dP, float* dtheta_partial, float* part,
                                              int64_t B, int64_t T, int64_t H, int64_t Dh, int in_bf16,
                                              void* stream) {
-  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  if (!width_ok(Dh)) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(shape_ok(B, T, H));
   PGN_CHECK_ARG(P && la_bias && A && theta && pos && dq && dk && dv && dla && dP && dtheta_partial && part);
   PGN_CHECK_ARG(beta_col < 0 || dbeta);
-  PGN_CHECK_ARG(proj_cols_ok(H, stride, la_col, gate_col, beta_col) && P != dP);
+  PGN_CHECK_ARG(proj_cols_ok(H, Dh, stride, la_col, gate_col, beta_col) && P != dP);
   const int ntb = (int)((T + TB - 1) / TB);
   const dim3 grid((unsigned)(B * H * ntb));
-  const int64_t hd = H * D;
+  const int64_t hd = H * Dh;
   hipStream_t st = (hipStream_t)stream;
   if (in_bf16) {
     const __bf16* p = (const __bf16*)P;
     __bf16* d = (__bf16*)dP;
-    hipLaunchKernelGGL(prep_bwd<__bf16>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
-                       (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv, d, d + hd, d + 2 * hd, nullptr,
-                       dtheta_partial, (int)T, (int)H, ntb, stride,
-                       proj_cols<__bf16>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias, beta_bias,
-                                         beta_min),
-                       dla, dbeta, d, part);
+    prep_bwd_any<__bf16>(Dh, grid, st, p, p + hd, p + 2 * hd, nullptr, theta, pos, dq, dk, dv, d, d + hd, d + 2 * hd,
+                         nullptr, dtheta_partial, (int)T, (int)H, ntb, stride,
+                         proj_cols<__bf16>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias, beta_bias,
+                                           beta_min),
+                         dla, dbeta, d, part);
   } else {
     const float* p = (const float*)P;
     float* d = (float*)dP;
-    hipLaunchKernelGGL(prep_bwd<float>, grid, dim3(256), 0, st, p, p + hd, p + 2 * hd, nullptr, theta, pos,
-                       (const __bf16*)dq, (const __bf16*)dk, (const __bf16*)dv, d, d + hd, d + 2 * hd, nullptr,
-                       dtheta_partial, (int)T, (int)H, ntb, stride,
-                       proj_cols<float>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias, beta_bias,
-                                        beta_min),
-                       dla, dbeta, d, part);
+    prep_bwd_any<float>(Dh, grid, st, p, p + hd, p + 2 * hd, nullptr, theta, pos, dq, dk, dv, d, d + hd, d + 2 * hd,
+                        nullptr, dtheta_partial, (int)T, (int)H, ntb, stride,
+                        proj_cols<float>(P, la_col, gate_col, beta_col, la_bias, A, la_floor, gate_bias, beta_bias,
+                                         beta_min),
+                        dla, dbeta, d, part);
   }
   PGN_RETURN_LAUNCH();
 }
 
 extern "C" int pragnosia_aspin_rebase_fwd(const float* S, const float* theta, const float* p0_dev, float p0,
                                           float* S_out, int64_t B, int64_t H, int64_t Dh, void* stream) {
-  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  if (!width_ok(Dh)) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(B > 0 && H > 0 && B * H < ((int64_t)1 << 31));
   PGN_CHECK_ARG(S && theta && S_out && S != S_out);
-  hipLaunchKernelGGL(rebase_fwd, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, theta, p0_dev, p0,
-                     S_out, (int)H);
+  hipStream_t st = (hipStream_t)stream;
+  if (Dh == 64)
+    hipLaunchKernelGGL(rebase_fwd<64>, dim3((unsigned)(B * H)), dim3(256), 0, st, S, theta, p0_dev, p0, S_out, (int)H);
+  else
+    hipLaunchKernelGGL(rebase_fwd<128>, dim3((unsigned)(B * H)), dim3(256), 0, st, S, theta, p0_dev, p0, S_out,
+                       (int)H);
   PGN_RETURN_LAUNCH();
 }
 
 extern "C" int pragnosia_aspin_rebase_bwd(const float* S, const float* theta, const float* p0_dev, float p0,
                                           const float* dS_out, float* dS, float* dtheta_partial, int64_t B,
                                           int64_t H, int64_t Dh, void* stream) {
-  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  if (!width_ok(Dh)) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(B > 0 && H > 0 && B * H < ((int64_t)1 << 31));
   PGN_CHECK_ARG(S && theta && dS_out);
-  hipLaunchKernelGGL(rebase_bwd, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, theta, p0_dev, p0,
-                     dS_out, dS, dtheta_partial, (int)H);
+  hipStream_t st = (hipStream_t)stream;
+  if (Dh == 64)
+    hipLaunchKernelGGL(rebase_bwd<64>, dim3((unsigned)(B * H)), dim3(256), 0, st, S, theta, p0_dev, p0, dS_out, dS,
+                       dtheta_partial, (int)H);
+  else
+    hipLaunchKernelGGL(rebase_bwd<128>, dim3((unsigned)(B * H)), dim3(256), 0, st, S, theta, p0_dev, p0, dS_out, dS,
+                       dtheta_partial, (int)H);
   PGN_RETURN_LAUNCH();
 }

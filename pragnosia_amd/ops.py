@@ -245,10 +245,12 @@ RMS_EPS = torch.finfo(torch.float32).eps  # nn.RMSNorm(eps=None) computes in fp3
 
 @torch.library.custom_op("pragnosia::aspin_out", mutates_args=())
 def aspin_out(o: Tensor, weight: Tensor, eps: float, out_bf16: bool) -> tuple[Tensor, Tensor]:
-    """Per-head RMSNorm of the scan output o (B, H, T, 64) (cast to bf16) with `weight` (64,), written token-major
-    as (B, T, H * 64) in bf16 (out_bf16) or fp32. Returns (y, rstd (B, H, T) fp32, saved for the backward)."""
+    """Per-head RMSNorm of the scan output o (B, H, T, D), D = 64 or 128 (cast to bf16), with `weight` (D,), written
+    token-major as (B, T, H * D) in bf16 (out_bf16) or fp32. Returns (y, rstd (B, H, T) fp32, saved for the
+    backward)."""
     _require_gpu(o, weight)
-    _expect("aspin_out", o.device, o=(o, (None, None, None, 64)), weight=(weight, (64,)))
+    Dw = o.shape[-1] if o.dim() == 4 and o.shape[-1] in (64, 128) else 64
+    _expect("aspin_out", o.device, o=(o, (None, None, None, Dw)), weight=(weight, (Dw,)))
     o, weight = _bf16(o), _f32(weight)
     B, H, T, D = o.shape
     y = torch.empty(B, T, H * D, device=o.device, dtype=torch.bfloat16 if out_bf16 else torch.float32)
@@ -267,9 +269,10 @@ def _(o, weight, eps, out_bf16):
 
 @torch.library.custom_op("pragnosia::aspin_out_bwd", mutates_args=())
 def aspin_out_bwd(gy: Tensor, o: Tensor, weight: Tensor, rstd: Tensor) -> tuple[Tensor, Tensor]:
-    """Backward of aspin_out. gy (B, T, H * 64) bf16 or fp32. Returns (dO (B, H, T, 64) bf16, dweight (64,) fp32)."""
+    """Backward of aspin_out. gy (B, T, H * D) bf16 or fp32. Returns (dO (B, H, T, D) bf16, dweight (D,) fp32)."""
     _require_gpu(gy, o, weight, rstd)
-    _expect("aspin_out_bwd", o.device, o=(o, (None, None, None, 64)), weight=(weight, (64,)))
+    Dw = o.shape[-1] if o.dim() == 4 and o.shape[-1] in (64, 128) else 64
+    _expect("aspin_out_bwd", o.device, o=(o, (None, None, None, Dw)), weight=(weight, (Dw,)))
     B, H, T, D = o.shape
     _expect("aspin_out_bwd", o.device, gy=(gy, (B, T, H * D)), rstd=(rstd, (B, H, T)))
     gy = gy.contiguous() if gy.dtype in (torch.bfloat16, torch.float32) else gy.float().contiguous()
@@ -1082,8 +1085,9 @@ def _proj(t: Tensor) -> Tensor:
 
 
 def _expect_prep(op: str, qp: Tensor, kp, vp, gate, theta, pos) -> None:
-    """qp, kp, vp (B, T, H, 64); gate (B, T, H); theta (H, 32); pos (T,); all on qp's device."""
-    _expect(op, qp.device, qp=(qp, (None, None, None, 64)))
+    """qp, kp, vp (B, T, H, D), D = 64 or 128; gate (B, T, H); theta (H, D / 2); pos (T,); all on qp's device."""
+    Dw = qp.shape[-1] if qp.dim() == 4 and qp.shape[-1] in (64, 128) else 64
+    _expect(op, qp.device, qp=(qp, (None, None, None, Dw)))
     B, T, H, D = qp.shape
     _expect(op, qp.device, kp=(kp, (B, T, H, D)), vp=(vp, (B, T, H, D)), gate=(gate, (B, T, H)),
             theta=(theta, (H, D // 2)), pos=(pos, (T,)))
@@ -1092,8 +1096,8 @@ def _expect_prep(op: str, qp: Tensor, kp, vp, gate, theta, pos) -> None:
 @torch.library.custom_op("pragnosia::aspin_prep", mutates_args=())
 def aspin_prep(qp: Tensor, kp: Tensor, vp: Tensor, gate: Optional[Tensor], theta: Tensor,
                pos: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-    """qp, kp, vp (B, T, H, 64) fp32 or bf16 projections; gate (B, T, H) logits or None; theta (H, 32); pos (T,)
-    int64. Returns bf16 q, k, v in (B, H, T, 64)."""
+    """qp, kp, vp (B, T, H, D) fp32 or bf16 projections, D = 64 or 128; gate (B, T, H) logits or None; theta
+    (H, D / 2); pos (T,) int64. Returns bf16 q, k, v in (B, H, T, D)."""
     _require_gpu(qp, kp, vp, gate, theta, pos)
     _expect_prep("aspin_prep", qp, kp, vp, gate, theta, pos)
     qp, kp, vp = _proj(qp), _proj(kp).to(qp.dtype), _proj(vp).to(qp.dtype)
@@ -1115,7 +1119,7 @@ def _(qp, kp, vp, gate, theta, pos):
 @torch.library.custom_op("pragnosia::aspin_prep_bwd", mutates_args=())
 def aspin_prep_bwd(qp: Tensor, kp: Tensor, vp: Tensor, gate: Optional[Tensor], theta: Tensor, pos: Tensor,
                    dq: Tensor, dk: Tensor, dv: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Returns (dqp, dkp, dvp in the projections' dtype, dgate fp32 (B, T, H) or empty, dtheta fp32 (H, 32))."""
+    """Returns (dqp, dkp, dvp in the projections' dtype, dgate fp32 (B, T, H) or empty, dtheta fp32 (H, D / 2))."""
     _require_gpu(qp, kp, vp, gate, theta, pos, dq, dk, dv)
     _expect_prep("aspin_prep_bwd", qp, kp, vp, gate, theta, pos)
     B, T, H, D = qp.shape
@@ -1165,21 +1169,23 @@ def _prep_backward(ctx, dq, dk, dv):
 aspin_prep.register_autograd(_prep_backward, setup_context=_prep_setup)
 
 
-def _proj_cols(H: int, gated: bool, has_beta: bool) -> tuple[int, int, int]:
+def _proj_cols(H: int, gated: bool, has_beta: bool, D: int = 64) -> tuple[int, int, int]:
     """Column offsets (decay, gate, strength; -1 = absent) in the projection GEMM's output rows."""
-    base = 3 * H * 64
+    base = 3 * H * D
     return base, (base + H if gated else -1), (base + H if has_beta else -1)
 
 
 def _expect_proj(op: str, P: Tensor, H: int, gated: bool, la_bias, A, la_floor, gate_bias, beta_bias, theta,
-                 pos=None) -> None:
+                 pos=None, D: int = 64) -> None:
     """P (B, T, W) (or (B, W) for the decode step) with W at least the columns the kernels read; the per-head
-    vectors (H,); theta (H, 32); pos (T,); all on P's device."""
-    if H <= 0 or P.dim() not in (2, 3) or P.shape[-1] < 3 * H * 64 + (2 if gated else 1) * H:
-        raise PragnosiaError(f"{op}: P has shape {tuple(P.shape)}, expected (B, [T,] >= {3 * H * 64 + H}) columns "
-                             f"for {H} heads")
+    vectors (H,); theta (H, D / 2); pos (T,); all on P's device. D = 64 or 128."""
+    if D not in (64, 128):
+        raise PragnosiaError(f"{op}: head dim {D} (the prep kernels take 64 and 128)")
+    if H <= 0 or P.dim() not in (2, 3) or P.shape[-1] < 3 * H * D + (2 if gated else 1) * H:
+        raise PragnosiaError(f"{op}: P has shape {tuple(P.shape)}, expected (B, [T,] >= {3 * H * D + H}) columns "
+                             f"for {H} heads of {D}")
     _expect(op, P.device, la_bias=(la_bias, (H,)), A=(A, (H,)), la_floor=(la_floor, (H,)),
-            gate_bias=(gate_bias, (H,)), beta_bias=(beta_bias, (H,)), theta=(theta, (H, 32)))
+            gate_bias=(gate_bias, (H,)), beta_bias=(beta_bias, (H,)), theta=(theta, (H, D // 2)))
     if pos is not None:
         _expect(op, P.device, pos=(pos, (P.shape[1] if P.dim() == 3 else None,)))
 
@@ -1187,15 +1193,15 @@ def _expect_proj(op: str, P: Tensor, H: int, gated: bool, la_bias, A, la_floor, 
 @torch.library.custom_op("pragnosia::aspin_prep_proj", mutates_args=())
 def aspin_prep_proj(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Optional[Tensor],
                     gate_bias: Optional[Tensor], beta_bias: Optional[Tensor], beta_min: float, gated: bool,
-                    theta: Tensor, pos: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """The carrier's inputs to the scan from ONE GEMM's output P (B, T, 3 H 64 + 2 H) (fp32 or bf16): the q, k, v
-    projections in the first 3 H 64 columns, then the decay logits, then either the plain rule's write-gate logits
-    (gated) or the delta rule's write-strength logits (beta_bias given, or beta_min > 0), all before their biases.
-    Returns bf16 q, k, v (B, H, T, 64) (normalised, k gated, q and k rotated by pos * theta), la (B, H, T) fp32 =
-    -softplus(logit + la_bias) exp(A) (floored at la_floor when given) and beta (B, H, T) fp32 =
+                    theta: Tensor, pos: Tensor, D: int = 64) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The carrier's inputs to the scan from ONE GEMM's output P (B, T, 3 H D + 2 H) (fp32 or bf16), head dim D = 64
+    or 128: the q, k, v projections in the first 3 H D columns, then the decay logits, then either the plain rule's
+    write-gate logits (gated) or the delta rule's write-strength logits (beta_bias given, or beta_min > 0), all before
+    their biases. Returns bf16 q, k, v (B, H, T, D) (normalised, k gated, q and k rotated by pos * theta), la (B, H,
+    T) fp32 = -softplus(logit + la_bias) exp(A) (floored at la_floor when given) and beta (B, H, T) fp32 =
     max(sigmoid(logit + beta_bias), beta_min) for the delta rule (else an empty tensor)."""
     _require_gpu(P, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos)
-    _expect_proj("aspin_prep_proj", P, H, gated, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos)
+    _expect_proj("aspin_prep_proj", P, H, gated, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos, D)
     if P.dim() != 3:
         raise PragnosiaError(f"aspin_prep_proj: P must be (B, T, W), got {tuple(P.shape)}")
     P = _proj(P)
@@ -1203,13 +1209,12 @@ def aspin_prep_proj(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Opt
     gate_bias, beta_bias = _f32(gate_bias), _f32(beta_bias)
     pos = pos.to(torch.int64).contiguous()
     B, T, W = P.shape
-    D = 64
     has_beta = not gated and W > 3 * H * D + H
     q, k, v = (torch.empty(B, H, T, D, device=P.device, dtype=torch.bfloat16) for _ in range(3))
     la = torch.empty(B, H, T, device=P.device, dtype=torch.float32)
     beta = (torch.empty(B, H, T, device=P.device, dtype=torch.float32) if has_beta
             else P.new_empty(0, dtype=torch.float32))
-    acol, gcol, bcol = _proj_cols(H, gated, has_beta)
+    acol, gcol, bcol = _proj_cols(H, gated, has_beta, D)
     check(lib().pragnosia_aspin_prep_proj_fwd(_ptr(P), W, acol, gcol, bcol, _ptr(la_bias), _ptr(A), _ptr(la_floor),
                                               _ptr(gate_bias), _ptr(beta_bias), float(beta_min), _ptr(theta),
                                               _ptr(pos), _ptr(q), _ptr(k), _ptr(v), _ptr(la),
@@ -1220,10 +1225,10 @@ def aspin_prep_proj(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Opt
 
 
 @aspin_prep_proj.register_fake
-def _(P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, pos):
+def _(P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, pos, D=64):
     B, T, W = P.shape
-    b = lambda: P.new_empty(B, H, T, 64, dtype=torch.bfloat16)
-    has_beta = not gated and W > 3 * H * 64 + H
+    b = lambda: P.new_empty(B, H, T, D, dtype=torch.bfloat16)
+    has_beta = not gated and W > 3 * H * D + H
     beta = P.new_empty(B, H, T, dtype=torch.float32) if has_beta else P.new_empty(0, dtype=torch.float32)
     return b(), b(), b(), P.new_empty(B, H, T, dtype=torch.float32), beta
 
@@ -1232,15 +1237,15 @@ def _(P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, 
 def aspin_prep_proj_bwd(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Optional[Tensor],
                         gate_bias: Optional[Tensor], beta_bias: Optional[Tensor], beta_min: float, gated: bool,
                         theta: Tensor, pos: Tensor, dq: Tensor, dk: Tensor, dv: Tensor, dla: Tensor,
-                        dbeta: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+                        dbeta: Optional[Tensor], D: int = 64) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Backward of aspin_prep_proj. Returns (dP in P's dtype and layout, d la_bias, dA, d gate_bias or d beta_bias
     (the one in use; empty when neither), dtheta), the per-head sums reduced from the kernel's partials."""
     _require_gpu(P, dq, dk, dv, dla, dbeta)
-    _expect_proj("aspin_prep_proj_bwd", P, H, gated, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos)
+    _expect_proj("aspin_prep_proj_bwd", P, H, gated, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos, D)
     if P.dim() != 3:
         raise PragnosiaError(f"aspin_prep_proj_bwd: P must be (B, T, W), got {tuple(P.shape)}")
-    _expect("aspin_prep_proj_bwd", P.device, dq=(dq, (P.shape[0], H, P.shape[1], 64)),
-            dk=(dk, (P.shape[0], H, P.shape[1], 64)), dv=(dv, (P.shape[0], H, P.shape[1], 64)),
+    _expect("aspin_prep_proj_bwd", P.device, dq=(dq, (P.shape[0], H, P.shape[1], D)),
+            dk=(dk, (P.shape[0], H, P.shape[1], D)), dv=(dv, (P.shape[0], H, P.shape[1], D)),
             dla=(dla, (P.shape[0], H, P.shape[1])), dbeta=(dbeta, (P.shape[0], H, P.shape[1])))
     P = _proj(P)
     la_bias, A, la_floor, theta = _f32(la_bias), _f32(A), _f32(la_floor), _f32(theta)
@@ -1248,7 +1253,6 @@ def aspin_prep_proj_bwd(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor:
     pos = pos.to(torch.int64).contiguous()
     dq, dk, dv, dla = _bf16(dq), _bf16(dk), _bf16(dv), _f32(dla)
     B, T, W = P.shape
-    D = 64
     has_beta = not gated and W > 3 * H * D + H
     if has_beta:
         dbeta = torch.zeros(B, H, T, device=P.device) if dbeta is None else _f32(dbeta)
@@ -1258,7 +1262,7 @@ def aspin_prep_proj_bwd(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor:
     rows = lib().pragnosia_aspin_prep_theta_partials(B, T)
     dth = torch.empty(rows, H, D // 2, device=P.device, dtype=torch.float32)
     part = torch.empty(lib().pragnosia_aspin_prep_proj_partials(B, T, H), 3, device=P.device, dtype=torch.float32)
-    acol, gcol, bcol = _proj_cols(H, gated, has_beta)
+    acol, gcol, bcol = _proj_cols(H, gated, has_beta, D)
     check(lib().pragnosia_aspin_prep_proj_bwd(_ptr(P), W, acol, gcol, bcol, _ptr(la_bias), _ptr(A), _ptr(la_floor),
                                               _ptr(gate_bias), _ptr(beta_bias), float(beta_min), _ptr(theta),
                                               _ptr(pos), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dla),
@@ -1271,16 +1275,16 @@ def aspin_prep_proj_bwd(P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor:
 
 
 @aspin_prep_proj_bwd.register_fake
-def _(P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, pos, dq, dk, dv, dla, dbeta):
+def _(P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, pos, dq, dk, dv, dla, dbeta, D=64):
     f = lambda *s: P.new_empty(*s, dtype=torch.float32)
-    has_beta = not gated and P.shape[-1] > 3 * H * 64 + H
-    return (torch.empty_like(P), f(H), f(H), f(H) if (gated or has_beta) else f(0), f(H, 32))
+    has_beta = not gated and P.shape[-1] > 3 * H * D + H
+    return (torch.empty_like(P), f(H), f(H), f(H) if (gated or has_beta) else f(0), f(H, D // 2))
 
 
 def _prep_proj_setup(ctx, inputs, output):
     ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
-    P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, pos = inputs
-    ctx.H, ctx.beta_min, ctx.gated = H, beta_min, gated
+    P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, pos, D = inputs
+    ctx.H, ctx.beta_min, ctx.gated, ctx.D = H, beta_min, gated, D
     ctx.bias_dtype = (gate_bias if gated else beta_bias)
     ctx.bias_dtype = None if ctx.bias_dtype is None else ctx.bias_dtype.dtype
     ctx.dtypes = (P.dtype, la_bias.dtype, A.dtype, theta.dtype)
@@ -1291,15 +1295,15 @@ def _prep_proj_setup(ctx, inputs, output):
 def _prep_proj_backward(ctx, dq, dk, dv, dla, dbeta):
     P, la_bias, A, la_floor, gate_bias, beta_bias, theta, pos = ctx.saved_tensors
     B, T, _ = P.shape
-    zb = lambda t: torch.zeros(B, ctx.H, T, 64, device=P.device, dtype=torch.bfloat16) if t is None else t
+    zb = lambda t: torch.zeros(B, ctx.H, T, ctx.D, device=P.device, dtype=torch.bfloat16) if t is None else t
     dla = torch.zeros(B, ctx.H, T, device=P.device) if dla is None else dla
     dP, dlb, dA, dxb, dth = aspin_prep_proj_bwd(P, ctx.H, la_bias, A, la_floor, gate_bias, beta_bias, ctx.beta_min,
                                                 ctx.gated, theta, pos, zb(dq), zb(dk), zb(dv), dla,
-                                                dbeta if (dbeta is not None and dbeta.numel()) else None)
+                                                dbeta if (dbeta is not None and dbeta.numel()) else None, ctx.D)
     dt = ctx.dtypes
     dgb = dxb.to(ctx.bias_dtype) if (ctx.gated and gate_bias is not None) else None
     dbb = dxb.to(ctx.bias_dtype) if (not ctx.gated and beta_bias is not None) else None
-    return (dP.to(dt[0]), None, dlb.to(dt[1]), dA.to(dt[2]), None, dgb, dbb, None, None, dth.to(dt[3]), None)
+    return (dP.to(dt[0]), None, dlb.to(dt[1]), dA.to(dt[2]), None, dgb, dbb, None, None, dth.to(dt[3]), None, None)
 
 
 aspin_prep_proj.register_autograd(_prep_proj_backward, setup_context=_prep_proj_setup)
@@ -1309,11 +1313,12 @@ aspin_prep_proj.register_autograd(_prep_proj_backward, setup_context=_prep_proj_
 # carried-state rebase: replaces the rotate() of S0's key rows at src/assoc.py:399-402
 @torch.library.custom_op("pragnosia::aspin_rebase", mutates_args=())
 def aspin_rebase(S: Tensor, theta: Tensor, p0_dev: Optional[Tensor], p0: float) -> Tensor:
-    """Key rows (2i, 2i+1) of S (B, H, 64, 64) rotated by -p0 * theta[h, i]; p0 from the device scalar p0_dev when
-    given, else the float p0."""
+    """Key rows (2i, 2i+1) of S (B, H, D, D), D = 64 or 128, rotated by -p0 * theta[h, i]; p0 from the device scalar
+    p0_dev when given, else the float p0."""
     _require_gpu(S, theta, p0_dev)
-    _expect("aspin_rebase", S.device, S=(S, (None, None, 64, 64)))
-    _expect("aspin_rebase", S.device, theta=(theta, (S.shape[1], 32)), p0_dev=(p0_dev, ()))
+    Dw = S.shape[-1] if S.dim() == 4 and S.shape[-1] in (64, 128) else 64
+    _expect("aspin_rebase", S.device, S=(S, (None, None, Dw, Dw)))
+    _expect("aspin_rebase", S.device, theta=(theta, (S.shape[1], Dw // 2)), p0_dev=(p0_dev, ()))
     S, theta, p0_dev = _f32(S), _f32(theta), _f32(p0_dev)
     B, H, D, _ = S.shape
     out = torch.empty_like(S)
@@ -1331,8 +1336,10 @@ def _(S, theta, p0_dev, p0):
 def aspin_rebase_bwd(S: Tensor, theta: Tensor, p0_dev: Optional[Tensor], p0: float,
                      g: Tensor) -> tuple[Tensor, Tensor]:
     _require_gpu(S, theta, p0_dev, g)
-    _expect("aspin_rebase_bwd", S.device, S=(S, (None, None, 64, 64)))
-    _expect("aspin_rebase_bwd", S.device, theta=(theta, (S.shape[1], 32)), p0_dev=(p0_dev, ()), g=(g, tuple(S.shape)))
+    Dw = S.shape[-1] if S.dim() == 4 and S.shape[-1] in (64, 128) else 64
+    _expect("aspin_rebase_bwd", S.device, S=(S, (None, None, Dw, Dw)))
+    _expect("aspin_rebase_bwd", S.device, theta=(theta, (S.shape[1], Dw // 2)), p0_dev=(p0_dev, ()),
+            g=(g, tuple(S.shape)))
     S, theta, p0_dev, g = _f32(S), _f32(theta), _f32(p0_dev), _f32(g)
     B, H, D, _ = S.shape
     dS = torch.empty_like(S)

@@ -24,18 +24,20 @@ def _ref(o, w):
     return (x * r * w.double()).transpose(1, 2).reshape(B, T, H * D)
 
 
-@pytest.mark.parametrize("B,H,T,scale", [(2, 3, 333, 1.0), (1, 12, 64, 1e-3), (3, 2, 1, 10.0), (2, 12, 512, 0.05)])
+@pytest.mark.parametrize("B,H,T,scale,D", [(2, 3, 333, 1.0, 64), (1, 12, 64, 1e-3, 64), (3, 2, 1, 10.0, 64),
+                                           (2, 12, 512, 0.05, 64), (2, 3, 333, 1.0, 128), (2, 6, 512, 0.05, 128),
+                                           (1, 2, 7, 10.0, 128)])
 @pytest.mark.parametrize("out_bf16", [True, False])
-def test_epilogue_forward_and_backward_match_fp64(B, H, T, scale, out_bf16):
+def test_epilogue_forward_and_backward_match_fp64(B, H, T, scale, D, out_bf16):
     import pragnosia_amd.ops  # noqa: F401
     g = torch.Generator().manual_seed(B * T + H)
-    o = (torch.randn(B, H, T, 64, generator=g) * scale).bfloat16()
-    w = torch.randn(64, generator=g)
-    gy = torch.randn(B, T, H * 64, generator=g)
+    o = (torch.randn(B, H, T, D, generator=g) * scale).bfloat16()
+    w = torch.randn(D, generator=g)
+    gy = torch.randn(B, T, H * D, generator=g)
     od = o.cuda().requires_grad_(True)
     wd = w.cuda().requires_grad_(True)
     y, rstd = torch.ops.pragnosia.aspin_out(od, wd, EPS, out_bf16)
-    assert y.dtype == (torch.bfloat16 if out_bf16 else torch.float32) and y.shape == (B, T, H * 64)
+    assert y.dtype == (torch.bfloat16 if out_bf16 else torch.float32) and y.shape == (B, T, H * D)
     gyd = gy.cuda().to(y.dtype)
     (y.float() * gyd.float()).sum().backward()
     orr = o.double().requires_grad_(True)

@@ -119,13 +119,15 @@ def test_assoc_carrier_decode_step(delta):
     assert torch.equal(Sk, Sd) and torch.equal(yk, yd)
 
 
-def test_rebase_kernel_and_gradient():
-    """The rebase kernel against the oracle's rotation of the key rows, and its backward against autograd."""
+@pytest.mark.parametrize("D", [64, 128])
+def test_rebase_kernel_and_gradient(D):
+    """The rebase kernel against the oracle's rotation of the key rows, and its backward against autograd, at head
+    dims 64 and 128."""
     from pragnosia_amd import ops  # noqa: F401
     g = torch.Generator().manual_seed(3)
-    S = torch.randn(2, 3, 64, 64, generator=g)
-    th = torch.rand(3, 32, generator=g) * 0.1
-    w = torch.randn(2, 3, 64, 64, generator=g)
+    S = torch.randn(2, 3, D, D, generator=g)
+    th = torch.rand(3, D // 2, generator=g) * 0.1
+    w = torch.randn(2, 3, D, D, generator=g)
     Sr, thr = S.double().requires_grad_(True), th.double().requires_grad_(True)
     (OA.rebase(Sr, thr, 300.0) * w.double()).sum().backward()
     Sk, thk = S.cuda().requires_grad_(True), th.cuda().requires_grad_(True)
@@ -135,13 +137,15 @@ def test_rebase_kernel_and_gradient():
     assert rel(Sk.grad, Sr.grad) < 1e-4 and rel(thk.grad, thr.grad) < 1e-4
 
 
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_prep_kernel_forward_backward(dtype):
+def test_prep_kernel_forward_backward(dtype, D):
     """The fused prep against the oracle's normalise/gate/rotate (`tests/test_assoc.py:187-212` of the reference:
-    prep kernel vs torch at position offsets up to 4096), with gradients of the projections, gate and theta."""
+    prep kernel vs torch at position offsets up to 4096), with gradients of the projections, gate and theta, at head
+    dims 64 and 128."""
     from pragnosia_amd import ops  # noqa: F401
     g = torch.Generator().manual_seed(5)
-    B, T, H, D = 2, 200, 3, 64
+    B, T, H = 2, 200, 3
     qp, kp, vp = (torch.randn(B, T, H, D, generator=g).to(dtype).float() for _ in range(3))
     gate = torch.randn(B, T, H, generator=g)
     th = torch.rand(H, D // 2, generator=g) * 0.1

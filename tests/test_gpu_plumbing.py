@@ -19,27 +19,28 @@ def rel(a, b):
     return ((a - b).abs().max() / (b.abs().max() + 1e-30)).item()
 
 
-@pytest.mark.parametrize("gated,floor,dtype", [(True, False, torch.float32), (True, True, torch.float32),
-                                               (False, False, torch.float32), (True, True, torch.bfloat16)])
-def test_prep_proj_matches_composition(gated, floor, dtype):
+@pytest.mark.parametrize("gated,floor,dtype,D", [(True, False, torch.float32, 64), (True, True, torch.float32, 64),
+                                                 (False, False, torch.float32, 64), (True, True, torch.bfloat16, 64),
+                                                 (True, True, torch.float32, 128), (True, False, torch.bfloat16, 128)])
+def test_prep_proj_matches_composition(gated, floor, dtype, D):
     import pragnosia_amd.ops  # noqa: F401
     op = torch.ops.pragnosia
     g = torch.Generator().manual_seed(int(gated) + 2 * int(floor) + 4 * (dtype == torch.bfloat16))
     B, T, H = 2, 150, 3
-    d = 64 * H
+    d = D * H
     W = 3 * d + H + (H if gated else 0)
     P = (torch.randn(B, T, W, generator=g) * 0.5).to(dtype)
     la_b, A = torch.randn(H, generator=g), torch.randn(H, generator=g) - 2.0
     fl = -torch.rand(H, generator=g) * 0.05 if floor else None
     gb = torch.randn(H, generator=g) if gated else None
-    th = torch.rand(H, 32, generator=g) * 0.1
+    th = torch.rand(H, D // 2, generator=g) * 0.1
     pos = torch.arange(T)
     dev = lambda t: None if t is None else t.cuda().requires_grad_(t.is_floating_point())
     ins = [dev(t) for t in (P, la_b, A, fl, gb, th)]
     Pd, lbd, Ad, fld, gbd, thd = ins
     if fld is not None:
         fld.requires_grad_(False)
-    q, k, v, la, _ = op.aspin_prep_proj(Pd, H, lbd, Ad, fld, gbd, None, 0.0, gated, thd, pos.cuda())
+    q, k, v, la, _ = op.aspin_prep_proj(Pd, H, lbd, Ad, fld, gbd, None, 0.0, gated, thd, pos.cuda(), D)
     gq, gk, gv, gl = (torch.randn(t.shape, generator=g) for t in (q, k, v, la))
     ((q.float() * gq.cuda()).sum() + (k.float() * gk.cuda()).sum() + (v.float() * gv.cuda()).sum()
      + (la * gl.cuda()).sum()).backward()
@@ -47,7 +48,7 @@ def test_prep_proj_matches_composition(gated, floor, dtype):
     ref = [None if t is None else t.detach().cuda().requires_grad_(t.is_floating_point() and t is not fl)
            for t in (P, la_b, A, fl, gb, th)]
     Pr, lbr, Ar, flr, gbr, thr = ref
-    qp, kp, vp = (Pr[..., i * d:(i + 1) * d].reshape(B, T, H, 64) for i in range(3))
+    qp, kp, vp = (Pr[..., i * d:(i + 1) * d].reshape(B, T, H, D) for i in range(3))
     lar = -F.softplus(Pr[..., 3 * d:3 * d + H].float() + lbr) * torch.exp(Ar)
     if flr is not None:
         lar = lar.clamp(min=flr)
@@ -99,25 +100,26 @@ def test_prep_proj_write_strength_matches_composition(write_all):
         assert rel(a.grad, b.grad) < 1e-3
 
 
-@pytest.mark.parametrize("delta,write_all,hl_floor", [(False, False, False), (False, True, True),
-                                                      (True, False, False), (True, True, True)])
-def test_module_fused_plumbing_equals_composition(delta, write_all, hl_floor):
+@pytest.mark.parametrize("delta,write_all,hl_floor,dk", [(False, False, False, 64), (False, True, True, 64),
+                                                         (True, False, False, 64), (True, True, True, 64),
+                                                         (False, False, False, 128), (True, False, True, 128)])
+def test_module_fused_plumbing_equals_composition(delta, write_all, hl_floor, dk):
     """AssocCarrier forward and backward (every parameter's gradient, the input's, the carried state's) with the
-    fused plumbing and with the reference's composition, from the same parameters. In fp32 the two agree within the
+    fused plumbing and with the reference's composition, from the same parameters, at head dims 64 and 128. In fp32 the two agree within the
     bf16 bounds (q, k, v and o pass through bf16 on both, rounded differently). Under bf16 autocast both move away
     from the fp32 run by bf16 arithmetic (the weight gradients of the small decay and strength projections most:
     measured 8% on wa.weight for both, 4% vs 22% on wb.weight); the fused path must stay within the bf16 bounds of
     the fp32 run or, where the composition itself does not, no further than 1.25 times the composition's distance."""
     from pragnosia_amd import assoc
     torch.manual_seed(11)
-    m = assoc.AssocCarrier(256, delta=delta, write_all=write_all, hl_floor=hl_floor).cuda()
+    m = assoc.AssocCarrier(256, delta=delta, write_all=write_all, hl_floor=hl_floor, head_dim=dk).cuda()
     with torch.no_grad():
         for p in m.parameters():
             p.add_(torch.randn_like(p) * 0.05)
     x = torch.randn(2, 300, 256, device="cuda")
-    S0 = torch.randn(2, 4, 64, 64, device="cuda") * 0.1
+    S0 = torch.randn(2, 256 // dk, dk, dk, device="cuda") * 0.1
     gy = torch.randn(2, 300, 256, device="cuda")
-    gS = torch.randn(2, 4, 64, 64, device="cuda")
+    gS = torch.randn(2, 256 // dk, dk, dk, device="cuda")
     res = {}
     prev = assoc.FUSED_PLUMBING
     try:
