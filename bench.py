@@ -948,6 +948,14 @@ def profile_kernels(reps=10):
             else:
                 o, S, sent, W, X = op.aspin_delta(x["q"], x["k"], x["v"], x["la"], x["beta"], None, True)
                 op.aspin_delta_bwd(x["q"], x["k"], x["v"], x["la"], x["beta"], sent, W, X, x["do"], x["dS"])
+        if rule == "delta":
+            # the same forward kernel writing only o and the final state (the recomputing path's forward), then its
+            # state pass (entering states, W and X; no output products), each `reps` times after the stored form's
+            args = [x["q"].bfloat16(), x["k"].bfloat16(), x["v"].bfloat16(), x["la"].float(), x["beta"].float(), None]
+            for _ in range(reps):
+                ops._delta_pass(*args, True, False)
+            for _ in range(reps):
+                ops._delta_pass(*args, False, True)
     B, T, D = 16, 512, 768
     u, lm, an, gy = (torch.randn(B, T, D, device=dev) for _ in range(4))
     lm = -lm.abs()
