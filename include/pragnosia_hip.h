@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (15); bumped on any change of the entry points. */
+/* ABI version of this header (16); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -401,6 +401,20 @@ int pragnosia_decode_gemv(const float* x, int64_t B, int64_t K, const float* ln_
 int pragnosia_decode_gemv_rms(const float* x, int64_t B, int64_t K, const float* rms_weight, float rms_eps,
                               const float* W, int64_t N, const float* bias, const float* scale, int act,
                               const float* resid, float* y, void* stream);
+
+/* The end of one greedy decode step for B sequences, in one launch: tok = argmax over logits (B, V) fp32 per row
+ * (the first index among equal maxima, NaN above every number, as torch.argmax), out[c][b] = tok and tok_out[b] = tok
+ * with c = *ctr_in (out (n_rows, B) int64, the row skipped when c >= n_rows), h (B, d) = emb[tok] + pemb[p] fp32 with
+ * p = (*pos_in + 1) mod ctx (emb (V, d), pemb (ctx, d): the tied token embedding and the position table), then
+ * *pos_out = p, *ctr_out = c + 1, p0s[0 .. L-1] = 1 (the carried states' position offsets after a one-token call), and
+ * with logits_rec non-NULL (n_rows, B, V) fp32 the logits copied to row c. The counter and position are read from one
+ * int64 and written to another (ctr_in != ctr_out, pos_in != pos_out; the caller alternates them step to step).
+ * Replaces the per-token tail of the reference's graphed generate (`src/bench.py:241-317`: argmax, append, position
+ * advance modulo ctx, the next input's embedding sum of `src/model.py:822-826`). */
+int pragnosia_decode_tail(const float* logits, int64_t B, int64_t V, const float* emb, const float* pemb, int64_t d,
+                          int64_t ctx, const int64_t* ctr_in, int64_t* ctr_out, const int64_t* pos_in,
+                          int64_t* pos_out, int64_t* out, int64_t n_rows, int64_t* tok, float* h, float* p0s,
+                          int64_t L, float* logits_rec, void* stream);
 
 /* The dense layers of the decode step on the fp32 matrix cores, for batches past the GEMV's (any B; 16 rows a
  * workgroup): y (B, N) = act(scale * (W z) + bias) + resid, with z = x (mode 0); z = (x - mean) / sqrt(var + eps) over

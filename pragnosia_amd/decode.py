@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from .assoc import AssocCarrier
-from .ops import decode_gemm_ln, decode_gemm_ok, decode_gemm_tile, ln_supported
+from .ops import decode_gemm_ln, decode_gemm_ok, decode_gemm_tile, decode_tail, ln_supported
 
 
 # The fused step's dense layers run as the batched GEMV kernel (each weight read once a step) up to this many
@@ -66,6 +66,9 @@ class GreedyDecoder:
         self.fused = fused_decode_ok(model) if fused is None else fused
         if self.fused and not fused_decode_ok(model):
             raise ValueError("GreedyDecoder: this model's decode step cannot run fused")
+        if self.fused and steps_per_graph % 2:
+            raise ValueError("GreedyDecoder: the fused step captures an even number of steps per graph (its tail "
+                             "alternates two counter slots)")
 
     @torch.no_grad()
     def prefill(self, ids):
@@ -96,7 +99,7 @@ class GreedyDecoder:
                 out.append(tuple(t.clone().contiguous() for t in st))
         return out
 
-    def _one_step(self):
+    def _one_step(self, par=0):
         m = self.m
         h = m.e(self.tok) + m.p(self.pos)
         for i, (mx, mp) in enumerate(zip(m.mix, m.mlp)):
@@ -178,12 +181,12 @@ class GreedyDecoder:
             return torch.addcmul(resid, y, scale) if resid is not None else y * scale
         return y + resid if resid is not None else y
 
-    def _one_step_gemm(self):
+    def _one_step_gemm(self, par=0):
         """The fused step past GEMV batch sizes: five kernels a layer, all on the fp32 matrix cores but the carrier
         step (LayerNorm + projection; the step, split four workgroups a head, raw output; per-head RMSNorm + gated
         o-projection + residual; LayerNorm + MLP in + GELU; MLP out + residual), then LayerNorm + head and argmax."""
         m, op = self.m, torch.ops.pragnosia
-        h = (m.e(self.tok) + m.p(self.pos)).reshape(self.B, -1)
+        h = self.h
         for i, (mx, mp) in enumerate(zip(m.mix, m.mlp)):
             gated = not (mx.delta or mx.write_all)
             tp, cp, bp, sig, to, ta, ca, ba, tb = self.wbuf[i]
@@ -196,20 +199,22 @@ class GreedyDecoder:
             x1 = op.decode_gemm(o, to, m.d, 2, None, on_eps, None, sig, 0, h)
             hm = op.decode_gemm(x1, ta, ca.shape[0], 1, ca, mp.n.eps, ba, None, 1, None)
             h = op.decode_gemm(hm, tb, m.d, 0, None, 0.0, mp.b.bias, None, 0, x1)
-        self.p0s.fill_(1.0)  # every state is now in the positions of a one-token call
-        self.pos.copy_((self.pos + 1) % m.ctx)
         th, ch, bh = self.wbuf[-1]
-        lg = op.decode_gemm(h, th, ch.shape[0], 1, ch, m.n.eps, bh, None, 0, None)
-        nxt = lg.argmax(-1)
-        if self.lgs is not None:
-            self.lgs.index_copy_(0, self.ctr, lg.float().view(1, self.B, -1))
-        self.out.index_copy_(0, self.ctr, nxt.view(1, -1))
-        self.ctr.add_(1)
-        self.tok.copy_(nxt.view(-1, 1))
+        self._tail(op.decode_gemm(h, th, ch.shape[0], 1, ch, m.n.eps, bh, None, 0, None), par)
 
-    def _one_step_fused(self):
+    def _tail(self, lg, par):
+        """The step's end in one kernel (decode_tail): argmax, the token written to the output row and the token
+        buffer, the position advanced, the next step's input embedding into `self.h`, every carried state's position
+        offset reset to 1 (one-token calls from here on), the logits recorded when asked. The row counter and the
+        position alternate between two int64 slots (read slot `par`, write the other), so a captured graph of an even
+        number of steps replays where the last replay ended."""
+        m = self.m
+        decode_tail(lg, m.e.weight, m.p.weight, self.ctrb[par], self.ctrb[1 - par], self.posb[par],
+                    self.posb[1 - par], self.out, self.tok, self.h, self.p0s, self.lgs)
+
+    def _one_step_fused(self, par=0):
         m, op = self.m, torch.ops.pragnosia
-        h = (m.e(self.tok) + m.p(self.pos)).reshape(self.B, -1)
+        h = self.h
         # at small batches the per-head RMSNorm moves into the o-projection's GEMV, so the carrier step can run four
         # workgroups per head (decode_gemv_rms needs d a multiple of 256, at most 1024)
         rms_in_gemv = self.B <= GEMV_MAX_BATCH and m.d % 256 == 0 and m.d <= 1024
@@ -230,15 +235,7 @@ class GreedyDecoder:
                 x1 = torch.addmm(h, o, self.wos[i].t())
             hm = self._dense(x1, mp.a.weight, mp.n, bias=mp.a.bias, act=1)
             h = self._dense(hm, mp.b.weight, None, bias=mp.b.bias, resid=x1)
-        self.p0s.fill_(1.0)  # every state is now in the positions of a one-token call
-        self.pos.copy_((self.pos + 1) % m.ctx)
-        lg = self._dense(h, m.e.weight, m.n)
-        nxt = lg.argmax(-1)
-        if self.lgs is not None:
-            self.lgs.index_copy_(0, self.ctr, lg.float().view(1, self.B, -1))
-        self.out.index_copy_(0, self.ctr, nxt.view(1, -1))
-        self.ctr.add_(1)
-        self.tok.copy_(nxt.view(-1, 1))
+        self._tail(self._dense(h, m.e.weight, m.n), par)
 
     def _capture(self, states, n_max):
         dev = self.m.e.weight.device
@@ -251,19 +248,23 @@ class GreedyDecoder:
         self.pos = torch.zeros(1, dtype=torch.long, device=dev)
         self.out = torch.zeros(n_max + self.K, self.B, dtype=torch.long, device=dev)
         self.ctr = torch.zeros(1, dtype=torch.long, device=dev)
+        if self.fused:  # the fused step's input and the tail kernel's alternating counter and position slots
+            self.h = torch.zeros(self.B, self.m.d, device=dev)
+            self.ctrb = torch.zeros(2, dtype=torch.long, device=dev)
+            self.posb = torch.zeros(2, dtype=torch.long, device=dev)
         if self.record:
             self.lgs = torch.zeros(n_max + self.K, self.B, self.m.e.weight.shape[0], dtype=torch.float32, device=dev)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         step = (self._one_step if not self.fused else self._one_step_gemm if self.gemm else self._one_step_fused)
         with torch.cuda.stream(side):
-            for _ in range(2):
-                step()
+            for i in range(2):
+                step(i % 2)
         torch.cuda.current_stream().wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            for _ in range(self.K):
-                step()
+            for i in range(self.K):
+                step(i % 2)
         self.n_max = n_max
 
     @torch.no_grad()
@@ -286,6 +287,10 @@ class GreedyDecoder:
             self.lgs[0].copy_(lg.float())
         self.ctr.fill_(1)
         self.tok.copy_(first.view(-1, 1))
+        if self.fused:
+            self.ctrb.fill_(1)
+            self.posb.fill_(pw)
+            self.h.copy_((self.m.e(self.tok) + self.m.p(self.pos)).reshape(self.B, -1))
 
     @torch.no_grad()
     def replay(self, n):

@@ -1525,6 +1525,32 @@ def _(x, Wt, N, mode, csum, eps, bias, scale, act, resid):
     return x.new_empty(x.shape[0], N, dtype=torch.float32)
 
 
+def decode_tail(logits: Tensor, emb: Tensor, pemb: Tensor, ctr_in: Tensor, ctr_out: Tensor, pos_in: Tensor,
+                pos_out: Tensor, out: Tensor, tok: Tensor, h: Tensor, p0s: Optional[Tensor],
+                logits_rec: Optional[Tensor]) -> None:
+    """The end of one graphed greedy decode step, in place (`pragnosia_decode_tail`): tok = argmax of logits (B, V)
+    per row (torch.argmax's rule), out[*ctr_in] = tok, h = emb[tok] + pemb[(*pos_in + 1) mod ctx], *pos_out and
+    *ctr_out advanced, p0s set to 1, and the logits copied to logits_rec[*ctr_in] when given. ctr and pos are int64
+    device scalars, each read from one and written to another. All on one device, fp32 / int64 contiguous."""
+    _require_gpu(logits, emb, pemb, ctr_in, ctr_out, pos_in, pos_out, out, tok, h, p0s, logits_rec)
+    B, V = logits.shape
+    d = emb.shape[1]
+    ok = (logits.dtype == torch.float32 and logits.is_contiguous() and emb.shape[0] == V and pemb.shape[1] == d
+          and out.dtype == torch.int64 and out.dim() == 2 and out.shape[1] == B and tok.numel() == B
+          and tok.dtype == torch.int64 and h.shape == (B, d) and h.dtype == torch.float32
+          and all(t.dtype == torch.int64 and t.numel() == 1 for t in (ctr_in, ctr_out, pos_in, pos_out))
+          and all(t.is_contiguous() for t in (emb, pemb, out, tok, h))
+          and (logits_rec is None or (logits_rec.shape == (out.shape[0], B, V) and logits_rec.is_contiguous()
+                                      and logits_rec.dtype == torch.float32))
+          and (p0s is None or (p0s.dtype == torch.float32 and p0s.is_contiguous())))
+    if not ok or emb.dtype != torch.float32 or pemb.dtype != torch.float32:
+        raise PragnosiaError("decode_tail: buffers do not have the documented shapes, dtypes or layout")
+    check(lib().pragnosia_decode_tail(_ptr(logits), B, V, _ptr(emb), _ptr(pemb), d, pemb.shape[0], _ptr(ctr_in),
+                                      _ptr(ctr_out), _ptr(pos_in), _ptr(pos_out), _ptr(out), out.shape[0], _ptr(tok),
+                                      _ptr(h), _ptr(p0s), 0 if p0s is None else p0s.numel(), _ptr(logits_rec),
+                                      _stream(logits)), "pragnosia_decode_tail")
+
+
 @torch.library.custom_op("pragnosia::aspin_decode_proj_", mutates_args=("S",))
 def aspin_decode_proj_(S: Tensor, P: Tensor, H: int, la_bias: Tensor, A: Tensor, la_floor: Optional[Tensor],
                        gate_bias: Optional[Tensor], beta_bias: Optional[Tensor], beta_min: float, gated: bool,
