@@ -145,3 +145,39 @@ def test_fused_graphed_decode_equals_unfused_and_eager(mixer, B, d):
     t_f2 = fused.generate(prompt[:, :70], n)
     t_e2, _ = greedy_eager(m, prompt[:, :70], n)
     assert torch.equal(t_f2.cpu(), t_e2.cpu())
+
+
+@pytest.mark.parametrize("B,V", [(1, 8192), (3, 1000), (64, 8192)])
+def test_decode_tail_matches_torch(B, V):
+    """The step tail kernel against torch: argmax with ties (the first index of the maximum), a NaN row (NaN above
+    every number, as torch.argmax), the output row and token buffer, the next input embedding at the advanced and
+    wrapped position, the counter and position written to their other slots, p0 reset, the recorded logits."""
+    from pragnosia_amd.ops import decode_tail
+    g = torch.Generator(device="cuda").manual_seed(B + V)
+    d, ctx, n_rows, L = 96, 7, 5, 12
+    lg = torch.randn(B, V, device="cuda", generator=g)
+    lg[0, 10] = lg[0, 700] = lg[0].max() + 1.0  # a tie: index 10 must win
+    if B > 1:
+        lg[1, 333] = float("nan")
+        lg[1, 900] = float("nan")
+    emb = torch.randn(V, d, device="cuda", generator=g)
+    pemb = torch.randn(ctx, d, device="cuda", generator=g)
+    ctr = torch.tensor([3, -1], device="cuda")
+    pos = torch.tensor([6, -1], device="cuda")
+    out = torch.zeros(n_rows, B, dtype=torch.long, device="cuda")
+    tok = torch.zeros(B, 1, dtype=torch.long, device="cuda")
+    h = torch.zeros(B, d, device="cuda")
+    p0s = torch.zeros(L, device="cuda")
+    rec = torch.zeros(n_rows, B, V, device="cuda")
+    decode_tail(lg, emb, pemb, ctr[0], ctr[1], pos[0], pos[1], out, tok, h, p0s, rec)
+    want = lg.argmax(-1)
+    assert torch.equal(tok.view(-1), want) and torch.equal(out[3], want)
+    assert int(want[0]) == 10 and (B == 1 or int(want[1]) == 333)
+    assert int(ctr[1]) == 4 and int(pos[1]) == 0 and int(ctr[0]) == 3 and int(pos[0]) == 6
+    assert torch.equal(h, emb[want] + pemb[0])
+    assert bool((p0s == 1).all()) and int(out[[0, 1, 2, 4]].abs().sum()) == 0
+    assert torch.allclose(rec[3], lg, rtol=0, atol=0, equal_nan=True)  # the NaN row copied as is
+    # the counter past the buffer's rows: nothing is written there
+    ctr[0] = n_rows
+    decode_tail(lg, emb, pemb, ctr[0], ctr[1], pos[1], pos[0], out, tok, h, None, None)
+    assert int(ctr[1]) == n_rows + 1 and int(pos[0]) == 1 and torch.equal(out[3], want)
