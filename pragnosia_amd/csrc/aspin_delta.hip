@@ -697,10 +697,13 @@ __global__ __launch_bounds__(64 * (8 + kNIW)) void aspin_delta_fwd_inv(
     DF_CLOCKS(0);
     bf16x8 sg[3][2];
     float pla = 0.f, pbe = 0.f;
+    // without o (the state pass) nothing reads Q: its tile is neither loaded nor staged
+    const int u0 = o ? 0 : 1;
     auto load = [&](int cn) {
       const int n0 = cn * C, nr = min(C, T - n0);
 #pragma unroll
       for (int u = 0; u < 3; ++u) {
+        if (u < u0) continue;
         const __bf16* src = u == 0 ? q + R.rows(T) + (size_t)n0 * DKEY
                           : u == 1 ? k + R.rows(T) + (size_t)n0 * DKEY
                                    : v + voff + (size_t)n0 * DKEY;
@@ -714,6 +717,7 @@ __global__ __launch_bounds__(64 * (8 + kNIW)) void aspin_delta_fwd_inv(
       __bf16* base = stg + hh * kStage;
 #pragma unroll
       for (int u = 0; u < 3; ++u) {
+        if (u < u0) continue;
         put_seg(base + u * TILE, sg[u][0], b);
         put_seg(base + u * TILE, sg[u][1], b + 256);
       }
