@@ -105,6 +105,9 @@ def _samples():
         ("aspin_decode_proj_", (r(B, H, D, D), r(B, 3 * H * D + 2 * H), H, r(H), r(H), None, r(H), None, 0.0, True,
                                 th, torch.tensor(1.0, device=dev), 0.0, None, 1e-6)),
         ("decode_gemv_rms", (r(3, 256), r(50, 256), 1 + 0.1 * r(64), 1e-6, r(50), r(1), 1, r(3, 50))),
+        ("decode_gemm", (r(20, 256), r(64 * 256), 50, 1, r(50), 1e-5, r(50), None, 1, r(20, 50))),
+        ("decode_gemm", (r(20, 256), r(64 * 256), 50, 2, None, 1e-6, None, r(1), 0, None)),
+        ("aspin_delta_windows", (q.detach(), k.detach(), v.detach(), la.detach(), be.detach(), S0.detach(), th, 64)),
     ]
 
 
