@@ -194,12 +194,13 @@ def aspin_bench(rule, steps, warmup):
         # read, dq, dk, dv, dla, dbeta written, dS_final read, dS0 written
         fwd_bytes = 4 * 2 * elem + 8 * ht + 4 * state + 2 * sent_n
         bwd_bytes = 7 * 2 * elem + 2 * sent_n + 16 * ht + 8 * state
-        # what this implementation moves besides: in the forward (one kernel, the inverses formed on chip) the keys
-        # read a second time by the inverse waves, X (bf16 C x C per chunk) and W written for the backward; in the
-        # backward X read, W read, the chain/local hand-off (drhs and per-chunk dS, bf16) written once and read once,
-        # and the entering states read a second time
+        # what this implementation moves besides, as a formula (the counter-measured bytes, where the traffic table
+        # has them, replace it in op_roofline): in the forward (one kernel, the inverses formed on chip; the inverse
+        # waves' key reads hit L2) X (bf16 C x C per chunk) and W written for the backward; in the backward X read,
+        # W read, the chain/local hand-off (drhs and per-chunk dS, bf16) written once and read once, and the entering
+        # states read a second time (the two backward kernels also both read q, k and dO, which the counters include)
         x_n = B * H * NC * C * C
-        impl_fwd = fwd_bytes + 2 * elem + 2 * x_n + 2 * elem
+        impl_fwd = fwd_bytes + 2 * x_n + 2 * elem
         impl_bwd = bwd_bytes + 2 * x_n + 2 * elem + 2 * sent_n + 2 * (2 * elem + 2 * sent_n)
         fwd_flops = (4 * D * (C + D) + 2 * C * D + 2 * D * D + 2 * C * C) * ht
         bwd_flops = (10 * D * (C + D) + 6 * C * D + 4 * D * D + 4 * C * C) * ht
@@ -674,17 +675,19 @@ def op_roofline(r):
     t = r["t_fwd"] + r["t_bwd"]
     gbs = (r["fwd_bytes"] + r["bwd_bytes"]) / t / 1e9
     tfl = (r["fwd_flops"] + r["bwd_flops"]) / t / 1e12
-    impl = r["impl_fwd_bytes"] + r["impl_bwd_bytes"]
+    measured = counter_ratio(r)
+    impl = (measured * (r["fwd_bytes"] + r["bwd_bytes"]) if measured is not None
+            else r["impl_fwd_bytes"] + r["impl_bwd_bytes"])
     tc = (r["cold"]["fwd_us"] + r["cold"]["bwd_us"]) * 1e-6
     return {"hbm_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_tflops": round(tfl, 2),
             "mfma_frac": round(tfl / BF16_PEAK_TFLOPS, 4),
             "achieved_frac": round(max(gbs / HBM_PEAK_GBS, tfl / BF16_PEAK_TFLOPS), 4),
             "ai_flop_per_byte": round((r["fwd_flops"] + r["bwd_flops"]) / (r["fwd_bytes"] + r["bwd_bytes"]), 1),
-            # this implementation's bytes (its own intermediates included) against the algorithmic ones: from the
-            # formula above, and as the FETCH_SIZE / WRITE_SIZE counters measured them for the same kernels
-            # (profiles/pmc_traffic_configs.md; null when a kernel has no row there)
+            # this implementation's bytes (its own intermediates included) against the algorithmic ones: as the
+            # FETCH_SIZE / WRITE_SIZE counters measured them for the same kernels (profiles/pmc_traffic_configs.md),
+            # or from the formula in aspin_bench when a kernel has no row there (then counter_bytes_ratio is null)
             "impl_bytes_ratio": round(impl / (r["fwd_bytes"] + r["bwd_bytes"]), 3),
-            "counter_bytes_ratio": counter_ratio(r),
+            "counter_bytes_ratio": measured,
             "impl_GBs": round(impl / t / 1e9, 1),
             # the same kernels with every launch's inputs out of the last-level cache (rotating input sets)
             "cold": dict(r["cold"], hbm_frac=round((r["fwd_bytes"] + r["bwd_bytes"]) / tc / 1e9 / HBM_PEAK_GBS, 4))}
