@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (16); bumped on any change of the entry points. */
+/* ABI version of this header (17); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -373,10 +373,10 @@ int pragnosia_aspin_decode_step(const float* S, float* S_out, const float* qp, c
  * non-NULL), the gate logit + gate_bias[h], beta = max(sigmoid(logit + beta_bias[h]), beta_min), then runs the step of
  * pragnosia_aspin_decode_step (S_out may equal S: in place) and writes the output per-head RMS-normalised and
  * token-major: o[b][h D + j] = (o_j r) on_weight[j], r = 1 / sqrt(mean_j o_j^2 + on_eps); with on_weight NULL the
- * output is written raw, o[b][h D + j] = o_j (four workgroups per head; the consumer applies the RMSNorm, e.g.
- * pragnosia_decode_gemv_rms). Replaces, inside the
- * reference's graphed decode (src/bench.py:241-317), the T = 1 path of `AssocCarrier.forward` from its projections
- * to `self.on(o).transpose(1, 2).reshape(B, T, D)` (src/assoc.py:384-505). */
+ * output is written raw, o[b][h D + j] = o_j (D / 16 workgroups per head; the consumer applies the RMSNorm, e.g.
+ * pragnosia_decode_gemv_rms). D = 64, or 128 with on_weight NULL (PRAGNOSIA_ERR_UNSUPPORTED otherwise). Replaces,
+ * inside the reference's graphed decode (src/bench.py:241-317), the T = 1 path of `AssocCarrier.forward` from its
+ * projections to `self.on(o).transpose(1, 2).reshape(B, T, D)` (src/assoc.py:384-505). */
 int pragnosia_aspin_decode_proj(const float* S, float* S_out, const float* P, int64_t np, int64_t la_col,
                                 int64_t gate_col, int64_t beta_col, const float* la_bias, const float* A,
                                 const float* la_floor, const float* gate_bias, const float* beta_bias, float beta_min,
@@ -393,13 +393,14 @@ int pragnosia_decode_gemv(const float* x, int64_t B, int64_t K, const float* ln_
                           float ln_eps, const float* W, int64_t N, const float* bias, const float* scale, int act,
                           const float* resid, float* y, void* stream);
 
-/* pragnosia_decode_gemv with the carrier's per-head RMSNorm on its input instead of a LayerNorm: z[b][h 64 + j] =
- * x[b][h 64 + j] r_{b,h} rms_weight[j], r = 1 / sqrt(mean_j x[b][h 64 + j]^2 + rms_eps), then y = act(scale (W z) +
- * bias) + resid. For B <= 4 and K a multiple of 256 up to 1024 (PRAGNOSIA_ERR_UNSUPPORTED otherwise). Replaces
- * `self.on(o)` and the gated o-projection with the residual of the carrier's T = 1 step (src/assoc.py:505-511),
- * reading the raw output of pragnosia_aspin_decode_proj (on_weight NULL). */
-int pragnosia_decode_gemv_rms(const float* x, int64_t B, int64_t K, const float* rms_weight, float rms_eps,
-                              const float* W, int64_t N, const float* bias, const float* scale, int act,
+/* pragnosia_decode_gemv with the carrier's per-head RMSNorm on its input instead of a LayerNorm, over heads of
+ * group = 64 or 128 channels: z[b][h G + j] = x[b][h G + j] r_{b,h} rms_weight[j], r = 1 / sqrt(mean_j x[b][h G + j]^2
+ * + rms_eps), then y = act(scale (W z) + bias) + resid. For B <= 4 and K a multiple of 256 up to 1024
+ * (PRAGNOSIA_ERR_UNSUPPORTED otherwise). Replaces `self.on(o)` and the gated o-projection with the residual of the
+ * carrier's T = 1 step (src/assoc.py:505-511), reading the raw output of pragnosia_aspin_decode_proj (on_weight
+ * NULL). */
+int pragnosia_decode_gemv_rms(const float* x, int64_t B, int64_t K, const float* rms_weight, int64_t group,
+                              float rms_eps, const float* W, int64_t N, const float* bias, const float* scale, int act,
                               const float* resid, float* y, void* stream);
 
 /* The end of one greedy decode step for B sequences, in one launch: tok = argmax over logits (B, V) fp32 per row
@@ -420,8 +421,8 @@ int pragnosia_decode_tail(const float* logits, int64_t B, int64_t V, const float
  * workgroup): y (B, N) = act(scale * (W z) + bias) + resid, with z = x (mode 0); z = (x - mean) / sqrt(var + eps) over
  * each row (mode 1: a LayerNorm whose weight is folded into W's columns, W[n][k] ln_weight[k], and whose bias into
  * `bias` as W ln_bias; csum (N) = the row sums of the folded W, required); or z = x / sqrt(mean of squares + eps) over
- * each 64-channel group (mode 2, K a multiple of 64 up to 1024: the carrier's per-head RMSNorm, its weight folded into
- * W's columns, W[n][k] rms_weight[k mod 64]). scale a device scalar or NULL, bias (N) or NULL, act 0 identity / 1 GELU
+ * each 64-channel group (mode 2, K a multiple of 64 up to 1024) or each 128-channel group (mode 3, K a multiple of
+ * 128 up to 2048): the carrier's per-head RMSNorm, its weight folded into W's columns, W[n][k] rms_weight[k mod G]). scale a device scalar or NULL, bias (N) or NULL, act 0 identity / 1 GELU
  * (erf form), resid (B, N) or NULL. W (N, K) is given tiled: Wt[((t (K / 16) + s) 64 + l) 4 + e] = W[16 t + l % 16][16
  * s + 4 (l / 16) + e], zero for columns past N, so Wt holds ceil(N / 16) 16 K floats. K a multiple of 16; y must not
  * alias x or resid. Deterministic; no workspace. pragnosia_decode_gemm_waves gives the waves a workgroup runs for (K,

@@ -148,68 +148,78 @@ __global__ __launch_bounds__(256) void aspin_decode(const float* S, float* Sout,
   }
 }
 
-// The same step from one projection output P (FROM_P inputs), split four ways per head over value columns for
-// latency: workgroup (b, h, quarter) owns value columns 16 quarter .. 16 quarter + 15, thread (jj, rg) column
-// 16 quarter + jj and key rows 4 rg .. 4 rg + 3 (two rotation pairs). Every global load (the projections, the state
-// slice, theta, p0, the gate parameters) is issued at the start; the key-row reductions (the delta read and the
-// output) go through LDS. The output is written raw, token-major o[b][h 64 + j] (the per-head RMSNorm is applied by
-// the consumer, pragnosia_decode_gemv_rms). Four times the workgroups of aspin_decode, and no dependent load chain.
+// The step for D = 64 or 128 with the work of a head split over D / 16 workgroups (for latency: a one-token step is
+// short, and D / 16 workgroups per head fill the chip at small batches): workgroup (b, h, part) owns value columns
+// 16 part .. 16 part + 15, thread (jj, rg) column 16 part + jj and key rows (D / 16) rg .. (D / 16) rg + D / 16 - 1
+// (D / 32 rotation pairs). Every global load (the projections, the state slice, theta, p0, the gate parameters) is
+// issued at the start; the key-row reductions (the delta read and the output) go through LDS. The output is written
+// raw, token-major o[b][h D + j] (the per-head RMSNorm is applied by the consumer, pragnosia_decode_gemv_rms or
+// pragnosia_decode_gemm). A head's parts are numbered 8 apart, so they run on one XCD (workgroup i goes to XCD i mod
+// 8) and the 128-byte lines of the state rows they share are fetched into one L2 only.
+template <int DH>
 __global__ __launch_bounds__(256) void aspin_decode_split(const float* S, float* Sout, StepIn in,
                                                           const float* __restrict__ theta,
                                                           const float* __restrict__ p0d, float p0h,
                                                           float* __restrict__ o, int H, int nbh) {
-  __shared__ float qs[D], ks[D], vs[D];
+  constexpr int NP = DH / 16;  // parts per head (workgroups of 16 value columns)
+  constexpr int RT = DH / 16;  // key rows per thread
+  __shared__ float qs[DH], ks[DH], vs[DH];
   __shared__ float red[16][17];
-  // workgroup i -> (head bh, quarter): the four quarters of a head are 8 apart, so they run on one XCD (workgroup i
-  // goes to XCD i mod 8) and the 128-byte lines of the state rows they share are fetched into one L2 only
-  const int i = blockIdx.x, qtr = (i >> 3) & 3, bh = (i >> 5) * 8 + (i & 7);
+  const int i = blockIdx.x, part = (i >> 3) % NP, bh = (i / (8 * NP)) * 8 + (i & 7);
   if (bh >= nbh) return;  // padding of the last group of 8 heads
   const int h = bh % H, b = bh / H;
   const int tid = threadIdx.x, jj = tid & 15, rg = tid >> 4;
-  const int j = 16 * qtr + jj;
+  const int j = 16 * part + jj;
   const float* prow = in.P + (size_t)b * in.np;
   // independent loads first
-  const float* Sbh = S + (size_t)bh * D * D;
-  float x[4];
+  const float* Sbh = S + (size_t)bh * DH * DH;
+  float x[RT];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) x[r] = Sbh[(4 * rg + r) * D + j];
-  const float th0 = theta[h * (D / 2) + 2 * rg], th1 = theta[h * (D / 2) + 2 * rg + 1];
+  for (int r = 0; r < RT; ++r) x[r] = Sbh[(RT * rg + r) * DH + j];
+  float th[RT / 2];
+#pragma unroll
+  for (int pr = 0; pr < RT / 2; ++pr) th[pr] = theta[h * (DH / 2) + (RT / 2) * rg + pr];
   const float p0 = p0d ? *p0d : p0h;
   const float la_logit = prow[in.la_col + h], la_b = in.la_b[h], Ah = in.A[h];
   const float fl = in.floor ? in.floor[h] : -INFINITY;
   const bool has_g = in.gate_col >= 0, has_b = in.beta_col >= 0;
   const float gl = has_g ? prow[in.gate_col + h] + (in.gate_b ? in.gate_b[h] : 0.f) : 0.f;
   const float bl = has_b ? prow[in.beta_col + h] + (in.beta_b ? in.beta_b[h] : 0.f) : 0.f;
-  float xin = 0.f;
-  if (tid < 3 * D) xin = prow[(tid >> 6) * H * D + h * D + (tid & 63)];
-  // q, k, v unit-normalised (k also gated) by waves 0, 1, 2
-  if (tid < 3 * D) {
-    float n = xin * xin;
+  // q, k, v unit-normalised (k also gated) by waves 0, 1, 2, D / 64 channels a lane
+  constexpr int CL = DH / 64;
+  float xin[CL];
+  if (tid < 3 * 64) {
+    const int vec = tid >> 6, l = tid & 63;
+#pragma unroll
+    for (int e = 0; e < CL; ++e) xin[e] = prow[vec * H * DH + h * DH + 64 * e + l];
+    float n = 0.f;
+#pragma unroll
+    for (int e = 0; e < CL; ++e) n += xin[e] * xin[e];
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) n += __shfl_xor(n, off);
     float inv = 1.f / fmaxf(sqrtf(n), 1e-12f);
-    if (tid >= D && tid < 2 * D && has_g) inv *= 1.f / (1.f + __expf(-gl));
-    (tid < D ? qs : (tid < 2 * D ? ks : vs))[tid & 63] = xin * inv;
+    if (vec == 1 && has_g) inv *= 1.f / (1.f + __expf(-gl));
+    float* dst = vec == 0 ? qs : (vec == 1 ? ks : vs);
+#pragma unroll
+    for (int e = 0; e < CL; ++e) dst[64 * e + l] = xin[e] * inv;
   }
   const float la_v = fmaxf(-softplus_(la_logit + la_b) * __expf(Ah), fl);
   const float a = __expf(la_v);
   const float be_v = has_b ? fmaxf(1.f / (1.f + __expf(-bl)), in.beta_min) : 0.f;
-  {
-    float s0, c0, s1, c1;
-    sincosf(-p0 * th0, &s0, &c0);
-    sincosf(-p0 * th1, &s1, &c1);
-    const float e0 = x[0], f0 = x[1], e1 = x[2], f1 = x[3];
-    x[0] = a * (e0 * c0 - f0 * s0);
-    x[1] = a * (e0 * s0 + f0 * c0);
-    x[2] = a * (e1 * c1 - f1 * s1);
-    x[3] = a * (e1 * s1 + f1 * c1);
+#pragma unroll
+  for (int pr = 0; pr < RT / 2; ++pr) {
+    float sn, cs;
+    sincosf(-p0 * th[pr], &sn, &cs);
+    const float e0 = x[2 * pr], f0 = x[2 * pr + 1];
+    x[2 * pr] = a * (e0 * cs - f0 * sn);
+    x[2 * pr + 1] = a * (e0 * sn + f0 * cs);
   }
   __syncthreads();
   float wv = vs[j];
   if (has_b) {
     float r_ = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) r_ += ks[4 * rg + r] * x[r];
+    for (int r = 0; r < RT; ++r) r_ += ks[RT * rg + r] * x[r];
     red[rg][jj] = r_;
     __syncthreads();
     float rd = 0.f;
@@ -220,20 +230,20 @@ __global__ __launch_bounds__(256) void aspin_decode_split(const float* S, float*
   }
   float y = 0.f;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    x[r] += ks[4 * rg + r] * wv;
-    y += x[r] * qs[4 * rg + r];
+  for (int r = 0; r < RT; ++r) {
+    x[r] += ks[RT * rg + r] * wv;
+    y += x[r] * qs[RT * rg + r];
   }
   red[rg][jj] = y;
-  float* Sob = Sout + (size_t)bh * D * D;
+  float* Sob = Sout + (size_t)bh * DH * DH;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) Sob[(4 * rg + r) * D + j] = x[r];
+  for (int r = 0; r < RT; ++r) Sob[(RT * rg + r) * DH + j] = x[r];
   __syncthreads();
   if (rg == 0) {
     float ov = 0.f;
 #pragma unroll
     for (int g = 0; g < 16; ++g) ov += red[g][jj];
-    o[(size_t)b * H * D + h * D + j] = ov;
+    o[(size_t)b * H * DH + h * DH + j] = ov;
   }
 }
 
@@ -265,11 +275,12 @@ extern "C" int pragnosia_aspin_decode_proj(const float* S, float* S_out, const f
                                            float beta_min, const float* theta, const float* p0_dev, float p0,
                                            const float* on_weight, float on_eps, float* o, int64_t B, int64_t H,
                                            int64_t Dh, void* stream) {
-  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  // 64-wide heads with or without the fused RMSNorm; 128-wide heads with the raw output only
+  if (!(Dh == D || (Dh == 2 * D && on_weight == nullptr))) return PRAGNOSIA_ERR_UNSUPPORTED;
   PGN_CHECK_ARG(B > 0 && H > 0 && B * H < ((int64_t)1 << 31));
   PGN_CHECK_ARG(S && S_out && P && la_bias && A && theta && o);
   PGN_CHECK_ARG(!(gate_col >= 0 && beta_col >= 0));
-  PGN_CHECK_ARG(la_col >= 3 * H * D && la_col + H <= np && gate_col + H <= np && beta_col + H <= np);
+  PGN_CHECK_ARG(la_col >= 3 * H * Dh && la_col + H <= np && gate_col + H <= np && beta_col + H <= np);
   StepIn in{};
   in.P = P;
   in.np = (int)np;
@@ -282,11 +293,15 @@ extern "C" int pragnosia_aspin_decode_proj(const float* S, float* S_out, const f
   in.gate_b = gate_bias;
   in.beta_b = beta_bias;
   in.beta_min = beta_min;
-  PGN_CHECK_ARG(B * H * 4 < ((int64_t)1 << 31));
-  if (on_weight == nullptr)  // raw output: four workgroups per head
-    hipLaunchKernelGGL(aspin_decode_split, dim3((unsigned)((B * H + 7) / 8 * 32)), dim3(256), 0, (hipStream_t)stream,
-                       S, S_out, in, theta, p0_dev, p0, o, (int)H, (int)(B * H));
-  else
+  PGN_CHECK_ARG(B * H * 8 < ((int64_t)1 << 31));
+  if (on_weight == nullptr) {  // raw output: Dh / 16 workgroups per head
+    if (Dh == D)
+      hipLaunchKernelGGL(aspin_decode_split<64>, dim3((unsigned)((B * H + 7) / 8 * 32)), dim3(256), 0,
+                         (hipStream_t)stream, S, S_out, in, theta, p0_dev, p0, o, (int)H, (int)(B * H));
+    else
+      hipLaunchKernelGGL(aspin_decode_split<128>, dim3((unsigned)((B * H + 7) / 8 * 64)), dim3(256), 0,
+                         (hipStream_t)stream, S, S_out, in, theta, p0_dev, p0, o, (int)H, (int)(B * H));
+  } else
     hipLaunchKernelGGL(aspin_decode<true>, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, S_out, in,
                        theta, p0_dev, p0, on_weight, on_eps, o, (int)H);
   PGN_RETURN_LAUNCH();

@@ -1,11 +1,11 @@
 // The dense layers of the carrier LM's decode step for batches past the one-wave GEMV (5 sequences and more), fp32
 // on the matrix cores (v_mfma_f32_16x16x4f32): y = act(scale * (W z) + bias) + resid with z the row standardised,
 // (x - mean) / sqrt(var + eps) (MODE 1: a LayerNorm whose weight the caller folds into W's columns and whose bias
-// into `bias` as W ln_bias), the per-64-channel-group RMS scaling x / sqrt(mean x^2 + eps) (MODE 2: the carrier's
-// per-head RMSNorm of its raw step output, its weight folded into W's columns) or x (MODE 0). Replaces, inside the
-// graphed decode of `src/bench.py:241-317`, the LayerNorm + nn.Linear (+ GELU, + residual) calls of
-// `src/model.py:552-560` and `src/assoc.py:384-512`, one kernel per dense layer, as decode_gemv.hip does for at most
-// 4 sequences.
+// into `bias` as W ln_bias), the per-group RMS scaling x / sqrt(mean x^2 + eps) over groups of 64 or 128 channels
+// (MODE 2, mode 2 or 3 at the boundary: the carrier's per-head RMSNorm of its raw step output, its weight folded into
+// W's columns) or x (MODE 0). Replaces, inside the graphed decode of `src/bench.py:241-317`, the LayerNorm +
+// nn.Linear (+ GELU, + residual) calls of `src/model.py:552-560` and `src/assoc.py:384-512`, one kernel per dense
+// layer, as decode_gemv.hip does for at most 4 sequences.
 //
 // At 64 sequences every weight element is used 64 times a step (32 flop per byte read), so the fp32 matrix-core rate
 // matters as much as HBM, and at these sizes a workgroup's own latency (its loads, then its products, then its
@@ -21,9 +21,9 @@
 // subtraction of mean(x - x0) csum below cancels no more than the row's spread; csum[n] = sum_k W[n][k]) while each
 // wave forms, per chunk, the mean and the sum of squared deviations of its entries (exact two-pass in registers) and
 // merges them (Chan, Golub and LeVeque's pairwise update); the waves' pairs meet in the epilogue, in wave order, with
-// the products' partials. MODE 2 (S = 4, C = 1) has each wave own one 64-channel group, so the group's sum of squares
-// is a two-step lane exchange before its products. The wave partials are summed through LDS in wave order:
-// deterministic, no atomics, nothing shared between workgroups, no workspace.
+// the products' partials. MODE 2 (S = 4 or 8, C = 1) has each wave own one group of 16 S channels, so the group's
+// sum of squares is a two-step lane exchange before its products. The wave partials are summed through LDS in wave
+// order: deterministic, no atomics, nothing shared between workgroups, no workspace.
 //
 // Operand layout of v_mfma_f32_16x16x4f32: A[r][k] in lane r + 16 k, B[k][c] in lane c + 16 k, D[4 g + e][c] in
 // lane c + 16 g, e = 0..3. A lane holds four consecutive K entries of a row (one 16-byte piece): product e of a
@@ -42,7 +42,7 @@ __global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ 
                                                       const float* __restrict__ bias,
                                                       const float* __restrict__ scale, int act,
                                                       const float* __restrict__ resid, float* __restrict__ y) {
-  static_assert(MODE != 2 || C == 1, "the RMS mode holds one 64-channel group per wave");
+  static_assert(MODE != 2 || C == 1, "the RMS mode holds one channel group per wave");
   __shared__ __align__(16) float red[MAXW * 256];
   __shared__ float2 stat[MAXW][16];
   const int KW = blockDim.x >> 6;
@@ -111,8 +111,8 @@ __global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ 
         m2w += q + d * d * (16.f * S) * c * f;
       }
     } else if constexpr (MODE == 2) {
-      // one 64-channel group per wave (S = 4): r = 1 / sqrt(mean of squares + eps) scales the group
-      static_assert(S == 4, "the RMS mode runs one 64-channel group per wave");
+      // one group of 16 S channels per wave (S = 4 or 8): r = 1 / sqrt(mean of squares + eps) scales the group
+      static_assert(S == 4 || S == 8, "the RMS mode runs one 64- or 128-channel group per wave");
       float a = 0.f;
 #pragma unroll
       for (int s = 0; s < S; ++s)
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ 
         for (int e = 0; e < 4; ++e) a += z[b][s][e] * z[b][s][e];
       a += __shfl_xor(a, 16);
       a += __shfl_xor(a, 32);
-      const float r = 1.f / sqrtf(a * (1.f / 64) + eps);
+      const float r = 1.f / sqrtf(a * (1.f / (16 * S)) + eps);
 #pragma unroll
       for (int s = 0; s < S; ++s)
 #pragma unroll
@@ -176,9 +176,10 @@ struct Plan {
 bool make_plan(int64_t K, int mode, Plan& p) {
   if (K <= 0 || K % 16) return false;
   const int64_t KS = K / 16;
-  if (mode == 2) {  // one 64-channel group per wave
-    if (K % 64 || K / 64 > MAXW) return false;
-    p = Plan{4, 1, (int)(K / 64)};
+  if (mode == 2 || mode == 3) {  // one 64- or 128-channel group per wave
+    const int G = mode == 2 ? 64 : 128;
+    if (K % G || K / G > MAXW) return false;
+    p = Plan{G / 16, 1, (int)(K / G)};
     return true;
   }
   int S = 1;
@@ -212,6 +213,7 @@ int dispatch_s(const Plan& p, const float* x, int B, int K, const float* csum, f
                const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
 #define PGN_S(V) return launch<V, C, MODE>(p, x, B, K, csum, eps, Wt, N, bias, scale, act, resid, y, st)
   if constexpr (MODE == 2) {
+    if (p.S == 8) PGN_S(8);
     PGN_S(4);
   } else {
     switch (p.S) {
@@ -229,7 +231,7 @@ int dispatch_s(const Plan& p, const float* x, int B, int K, const float* csum, f
 
 extern "C" int pragnosia_decode_gemm_waves(int64_t K, int mode) {
   Plan p;
-  if (mode < 0 || mode > 2 || !make_plan(K, mode, p)) return -1;
+  if (mode < 0 || mode > 3 || !make_plan(K, mode, p)) return -1;
   return p.KW;
 }
 
@@ -247,7 +249,7 @@ extern "C" int pragnosia_decode_gemm(const float* x, int64_t B, int64_t K, int m
                                      const float* Wt, int64_t N, const float* bias, const float* scale, int act,
                                      const float* resid, float* y, void* stream) {
   PGN_CHECK_ARG(x && Wt && y && B > 0 && K > 0 && N > 0);
-  PGN_CHECK_ARG(mode >= 0 && mode <= 2 && (mode != 1 || csum != nullptr));
+  PGN_CHECK_ARG(mode >= 0 && mode <= 3 && (mode != 1 || csum != nullptr));
   PGN_CHECK_ARG(B * N < ((int64_t)1 << 31) && B * K < ((int64_t)1 << 31) &&
                 ((N + 15) / 16) * 16 * K < ((int64_t)1 << 31) && ((N + 127) / 128) * 8 * ((B + 15) / 16) < (1 << 30));
   PGN_CHECK_ARG(act == 0 || act == 1);
@@ -258,6 +260,6 @@ extern "C" int pragnosia_decode_gemm(const float* x, int64_t B, int64_t K, int m
   hipStream_t st = (hipStream_t)stream;
   const int b = (int)B, k = (int)K, n = (int)N;
   if (mode == 1) return dispatch_c<1>(p, x, b, k, csum, eps, Wt, n, bias, scale, act, resid, y, st);
-  if (mode == 2) return dispatch_s<1, 2>(p, x, b, k, nullptr, eps, Wt, n, bias, scale, act, resid, y, st);
+  if (mode >= 2) return dispatch_s<1, 2>(p, x, b, k, nullptr, eps, Wt, n, bias, scale, act, resid, y, st);
   return dispatch_c<0>(p, x, b, k, nullptr, eps, Wt, n, bias, scale, act, resid, y, st);
 }

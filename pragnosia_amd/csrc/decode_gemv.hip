@@ -170,8 +170,8 @@ constexpr int log2_of() { return NV == 1 ? 0 : NV == 2 ? 1 : NV == 4 ? 2 : NV ==
 // 16-byte pieces 4 l + 256 u of each of its rows, so one load instruction reads 1 KiB contiguous; all RPW KV pieces
 // are issued before the inputs are read. The input is used as is (MODE 0), LayerNorm'd (MODE 1: the wave computes
 // the LayerNorm of every input row itself, the row in registers, two wave reductions), or RMS-normalised per group
-// of 64 channels (MODE 2: the carrier's per-head RMSNorm; a group's 64 channels sit on 16 consecutive lanes of one
-// piece, so its sum of squares is a four-step exchange). No LDS, no barrier. NB = 1 (B = 1) or 4 (B <= 4, rows past
+// of 64 or 128 channels (MODE 2 or 3: the carrier's per-head RMSNorm; a group's channels sit on 16 or 32 consecutive
+// lanes of one piece, so its sum of squares is a four- or five-step exchange). No LDS, no barrier. NB = 1 (B = 1) or 4 (B <= 4, rows past
 // B masked).
 template <int RPW, int NB, int KV, int MODE>
 __global__ __launch_bounds__(64) void gemv_wave(const float* __restrict__ x, int B, const float* __restrict__ lnw,
@@ -232,8 +232,9 @@ __global__ __launch_bounds__(64) void gemv_wave(const float* __restrict__ x, int
           for (int e = 0; e < 4; ++e) z[b][u][e] = (z[b][u][e] - mean) * rs * g[u][e] + c[u][e];
       }
     } else {
-      // channels 4 (l mod 16) .. + 3 of a 64-channel group: the group weight piece is the same for every u
-      const f32x4 g = *reinterpret_cast<const f32x4*>(lnw + 4 * (l & 15));
+      // channels 4 (l mod GL) .. + 3 of a G-channel group: the group weight piece is the same for every u
+      constexpr int G = MODE == 3 ? 128 : 64, GL = G / 4;
+      const f32x4 g = *reinterpret_cast<const f32x4*>(lnw + 4 * (l & (GL - 1)));
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -241,8 +242,8 @@ __global__ __launch_bounds__(64) void gemv_wave(const float* __restrict__ x, int
           float s = (z[b][u][0] * z[b][u][0] + z[b][u][1] * z[b][u][1]) +
                     (z[b][u][2] * z[b][u][2] + z[b][u][3] * z[b][u][3]);
 #pragma unroll
-          for (int o = 1; o < 16; o <<= 1) s += __shfl_xor(s, o);
-          const float rs = 1.f / sqrtf(s * (1.f / 64) + eps);
+          for (int o = 1; o < GL; o <<= 1) s += __shfl_xor(s, o);
+          const float rs = 1.f / sqrtf(s * (1.f / G) + eps);
 #pragma unroll
           for (int e = 0; e < 4; ++e) z[b][u][e] = (z[b][u][e] * rs) * g[e];
         }
@@ -370,15 +371,18 @@ extern "C" int pragnosia_decode_gemv(const float* x, int64_t B, int64_t K, const
   PGN_RETURN_LAUNCH();
 }
 
-extern "C" int pragnosia_decode_gemv_rms(const float* x, int64_t B, int64_t K, const float* rms_weight, float rms_eps,
-                                         const float* W, int64_t N, const float* bias, const float* scale, int act,
-                                         const float* resid, float* y, void* stream) {
-  PGN_CHECK_ARG(x && W && y && rms_weight && B > 0 && K > 0 && N > 0);
+extern "C" int pragnosia_decode_gemv_rms(const float* x, int64_t B, int64_t K, const float* rms_weight, int64_t group,
+                                         float rms_eps, const float* W, int64_t N, const float* bias,
+                                         const float* scale, int act, const float* resid, float* y, void* stream) {
+  PGN_CHECK_ARG(x && W && y && rms_weight && B > 0 && K > 0 && N > 0 && (group == 64 || group == 128));
   PGN_CHECK_ARG(B * N < ((int64_t)1 << 31) && B * K < ((int64_t)1 << 31));
   PGN_CHECK_ARG(act == 0 || act == 1);
   PGN_CHECK_ARG(y != x && (resid == nullptr || resid != y));
   PGN_CHECK_ARG(((uintptr_t)x | (uintptr_t)W | (uintptr_t)rms_weight) % 16 == 0);
   if (!wave_shape_ok(B, K, true)) return PRAGNOSIA_ERR_UNSUPPORTED;
+  if (group == 128)
+    return dispatch_rpw<3>((int)(K / 256), x, (int)B, rms_weight, nullptr, rms_eps, W, (int)N, bias, scale, act,
+                           resid, y, (hipStream_t)stream);
   return dispatch_rpw<2>((int)(K / 256), x, (int)B, rms_weight, nullptr, rms_eps, W, (int)N, bias, scale, act, resid,
                          y, (hipStream_t)stream);
 }

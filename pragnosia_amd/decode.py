@@ -37,18 +37,38 @@ from .ops import decode_gemm_ln, decode_gemm_ok, decode_gemm_tile, decode_tail, 
 GEMV_MAX_BATCH = 4
 
 
-def fused_decode_ok(model) -> bool:
-    """Whether `model`'s decode step can run fused: every mixer an AssocCarrier with 64-dim heads and no key_topk,
-    beta_scale or short convolution, LayerNorms throughout and the standard MLP."""
+def _rms_gemv_ok(K: int) -> bool:
+    """Whether decode_gemv_rms covers the carrier output of width K (B <= GEMV_MAX_BATCH)."""
+    return K % 256 == 0 and K <= 1024
+
+
+def fused_decode_ok(model, batch: int = 1) -> bool:
+    """Whether `model`'s decode step can run fused at this batch size: every mixer an AssocCarrier with 64- or
+    128-dim heads and no key_topk, beta_scale or short convolution, LayerNorms throughout and the standard MLP. The
+    128-dim step writes its output raw, so its per-head RMSNorm must fit the consumer: the o-projection's GEMV up to
+    GEMV_MAX_BATCH sequences, decode_gemm's 128-channel RMS mode past it."""
     import torch.nn as nn
     if not (isinstance(model.n, nn.LayerNorm) and getattr(model, "short_conv", 0) == 0):
         return False
     for mx, mp in zip(model.mix, model.mlp):
-        if not (isinstance(mx, AssocCarrier) and mx.dk == 64 and not mx.key_topk
+        if not (isinstance(mx, AssocCarrier) and mx.dk in (64, 128) and not mx.key_topk
                 and getattr(mx, "beta_scale", None) is None and isinstance(mx.ln, nn.LayerNorm)
                 and mx.on.weight is not None and isinstance(mp.n, nn.LayerNorm)):
             return False
+        if mx.dk == 128:
+            K = mx.h * mx.dk
+            if not (_rms_gemv_ok(K) if batch <= GEMV_MAX_BATCH else _gemm_layers_ok(model)):
+                return False
     return True
+
+
+def _gemm_layers_ok(model) -> bool:
+    """Whether decode_gemm covers every dense layer's input width of `model`'s step (the LayerNorm'd d-wide inputs,
+    the per-head RMSNorm'd carrier outputs, the MLP's hidden width)."""
+    hid = model.mlp[0].a.weight.shape[0]
+    if not (decode_gemm_ok(model.d, 1) and decode_gemm_ok(hid, 0)):
+        return False
+    return all(decode_gemm_ok(mx.h * mx.dk, 2 if mx.dk == 64 else 3) for mx in model.mix)
 
 
 class GreedyDecoder:
@@ -63,8 +83,8 @@ class GreedyDecoder:
         self.record = record_logits
         self.lgs = None
         self.graph = None
-        self.fused = fused_decode_ok(model) if fused is None else fused
-        if self.fused and not fused_decode_ok(model):
+        self.fused = fused_decode_ok(model, batch) if fused is None else fused
+        if self.fused and not fused_decode_ok(model, batch):
             raise ValueError("GreedyDecoder: this model's decode step cannot run fused")
         if self.fused and steps_per_graph % 2:
             raise ValueError("GreedyDecoder: the fused step captures an even number of steps per graph (its tail "
@@ -120,13 +140,9 @@ class GreedyDecoder:
         self.tok.copy_(nxt.view(-1, 1))
 
     def _gemm_ok(self) -> bool:
-        """Whether the dense layers run on decode_gemm: past the GEMV's batch sizes, every layer's input width covered
-        (the LayerNorm'd d-wide inputs, the per-head RMSNorm'd carrier output, the MLP's hidden width)."""
-        m = self.m
-        if self.B <= GEMV_MAX_BATCH:
-            return False
-        hid = m.mlp[0].a.weight.shape[0]
-        return decode_gemm_ok(m.d, 1) and decode_gemm_ok(m.d, 2) and decode_gemm_ok(hid, 0)
+        """Whether the dense layers run on decode_gemm: past the GEMV's batch sizes, every layer's input width
+        covered."""
+        return self.B > GEMV_MAX_BATCH and _gemm_layers_ok(self.m)
 
     def _fused_weights(self):
         """Per layer: the concatenated input projection (q, k, v, decay, then the gate or strength), the output gate
@@ -183,8 +199,9 @@ class GreedyDecoder:
 
     def _one_step_gemm(self, par=0):
         """The fused step past GEMV batch sizes: five kernels a layer, all on the fp32 matrix cores but the carrier
-        step (LayerNorm + projection; the step, split four workgroups a head, raw output; per-head RMSNorm + gated
-        o-projection + residual; LayerNorm + MLP in + GELU; MLP out + residual), then LayerNorm + head and argmax."""
+        step (LayerNorm + projection; the step, split dk / 16 workgroups a head, raw output; per-head RMSNorm + gated
+        o-projection + residual; LayerNorm + MLP in + GELU; MLP out + residual), then LayerNorm + head and the step's
+        tail (argmax, next input)."""
         m, op = self.m, torch.ops.pragnosia
         h = self.h
         for i, (mx, mp) in enumerate(zip(m.mix, m.mlp)):
@@ -196,7 +213,7 @@ class GreedyDecoder:
                                       mx.la_floor if mx.hl_floor else None, mx.wi.bias if gated else None,
                                       mx.wb.bias if mx.delta else None, 0.75 if (mx.delta and mx.write_all) else 0.0,
                                       gated, mx.theta, self.p0s[i:i + 1], 0.0, None, on_eps)
-            x1 = op.decode_gemm(o, to, m.d, 2, None, on_eps, None, sig, 0, h)
+            x1 = op.decode_gemm(o, to, m.d, 2 if mx.dk == 64 else 3, None, on_eps, None, sig, 0, h)
             hm = op.decode_gemm(x1, ta, ca.shape[0], 1, ca, mp.n.eps, ba, None, 1, None)
             h = op.decode_gemm(hm, tb, m.d, 0, None, 0.0, mp.b.bias, None, 0, x1)
         th, ch, bh = self.wbuf[-1]
@@ -215,10 +232,10 @@ class GreedyDecoder:
     def _one_step_fused(self, par=0):
         m, op = self.m, torch.ops.pragnosia
         h = self.h
-        # at small batches the per-head RMSNorm moves into the o-projection's GEMV, so the carrier step can run four
-        # workgroups per head (decode_gemv_rms needs d a multiple of 256, at most 1024)
-        rms_in_gemv = self.B <= GEMV_MAX_BATCH and m.d % 256 == 0 and m.d <= 1024
         for i, (mx, mp) in enumerate(zip(m.mix, m.mlp)):
+            # at small batches the per-head RMSNorm moves into the o-projection's GEMV, so the carrier step can run
+            # dk / 16 workgroups per head (always so for 128-dim heads, whose step writes only the raw output)
+            rms_in_gemv = self.B <= GEMV_MAX_BATCH and _rms_gemv_ok(mx.h * mx.dk)
             gated = not (mx.delta or mx.write_all)
             P = self._dense(h, self.wcat[i], mx.ln)
             on_eps = mx.on.eps if mx.on.eps is not None else torch.finfo(torch.float32).eps

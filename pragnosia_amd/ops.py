@@ -1435,20 +1435,23 @@ def _(x, W, ln_weight, ln_bias, ln_eps, bias, scale, act, resid):
 @torch.library.custom_op("pragnosia::decode_gemv_rms", mutates_args=())
 def decode_gemv_rms(x: Tensor, W: Tensor, rms_weight: Tensor, rms_eps: float, bias: Optional[Tensor],
                     scale: Optional[Tensor], act: int, resid: Optional[Tensor]) -> Tensor:
-    """y (B, N) = act(scale * (W z) + bias) + resid with z the per-64-channel-group RMSNorm of x (B, K) with
-    rms_weight (64,): the carrier's per-head RMSNorm and gated o-projection of one decode step, for B <= 4 and K a
-    multiple of 256 up to 1024. All fp32. Not differentiable."""
+    """y (B, N) = act(scale * (W z) + bias) + resid with z the per-head RMSNorm of x (B, K) with rms_weight (G,),
+    heads of G = 64 or 128 channels: the carrier's per-head RMSNorm and gated o-projection of one decode step, for
+    B <= 4 and K a multiple of 256 up to 1024. All fp32. Not differentiable."""
     _require_gpu(x, W, rms_weight, bias, scale, resid)
     if x.dim() != 2 or W.dim() != 2 or W.shape[1] != x.shape[1]:
         raise PragnosiaError(f"decode_gemv_rms: x {tuple(x.shape)} and W {tuple(W.shape)} must be (B, K) and (N, K)")
     B_, K_, N_ = x.shape[0], x.shape[1], W.shape[0]
-    _expect("decode_gemv_rms", x.device, W=(W, (N_, K_)), rms_weight=(rms_weight, (64,)), bias=(bias, (N_,)),
+    G = rms_weight.numel()
+    if G not in (64, 128) or K_ % G:
+        raise PragnosiaError(f"decode_gemv_rms: RMSNorm weight of {G} channels over rows of {K_} (heads of 64 or 128)")
+    _expect("decode_gemv_rms", x.device, W=(W, (N_, K_)), rms_weight=(rms_weight, (G,)), bias=(bias, (N_,)),
             scale=(scale, ()), resid=(resid, (B_, N_)))
     x, W, rms_weight = _f32(x), _f32(W), _f32(rms_weight)
     bias, scale, resid = _f32(bias), _f32(scale), _f32(resid)
     y = torch.empty(B_, N_, device=x.device, dtype=torch.float32)
-    check(lib().pragnosia_decode_gemv_rms(_ptr(x), B_, K_, _ptr(rms_weight), float(rms_eps), _ptr(W), N_, _ptr(bias),
-                                          _ptr(scale), int(act), _ptr(resid), _ptr(y), _stream(x)),
+    check(lib().pragnosia_decode_gemv_rms(_ptr(x), B_, K_, _ptr(rms_weight), G, float(rms_eps), _ptr(W), N_,
+                                          _ptr(bias), _ptr(scale), int(act), _ptr(resid), _ptr(y), _stream(x)),
           "pragnosia_decode_gemv_rms")
     return y
 
@@ -1460,8 +1463,8 @@ def _(x, W, rms_weight, rms_eps, bias, scale, act, resid):
 
 def decode_gemm_tile(W: Tensor, col_scale: Optional[Tensor] = None) -> Tensor:
     """The tiled copy of a dense layer's weight W (N, K) fp32 that `decode_gemm` reads (K a multiple of 16), its
-    columns scaled by col_scale when given (a normalisation's weight folded in: (K,), or (64,) repeated over the
-    64-channel groups), flat: Wt[((t KS + s) 64 + l) 4 + e] = W[16 t + l % 16][16 s + 4 (l / 16) + e] for column tile
+    columns scaled by col_scale when given (a normalisation's weight folded in: (K,), or (G,) repeated over the
+    G-channel groups), flat: Wt[((t KS + s) 64 + l) 4 + e] = W[16 t + l % 16][16 s + 4 (l / 16) + e] for column tile
     t, 16-wide step s of KS = K / 16, lane l, entry e; columns past N padded with zeros. So each wave's weight piece
     of a step is one contiguous 1 KiB read, laid out as the fp32 matrix cores take their operand."""
     N, K = W.shape
@@ -1501,8 +1504,8 @@ def decode_gemm(x: Tensor, Wt: Tensor, N: int, mode: int, csum: Optional[Tensor]
                 bias: Optional[Tensor], scale: Optional[Tensor], act: int, resid: Optional[Tensor]) -> Tensor:
     """y (B, N) = act(scale * (W z) + bias) + resid on the fp32 matrix cores, W given tiled (`decode_gemm_tile`), with
     z = x (mode 0), the row standardised (mode 1: a LayerNorm folded by `decode_gemm_ln`, csum its row sums) or each
-    64-channel group RMS-scaled (mode 2: the RMSNorm's weight folded into the tiled W). The dense layers of the decode
-    step past GEMV batch sizes. Not differentiable."""
+    64-channel (mode 2) or 128-channel (mode 3) group RMS-scaled (the RMSNorm's weight folded into the tiled W). The
+    dense layers of the decode step past GEMV batch sizes. Not differentiable."""
     _require_gpu(x, Wt, csum, bias, scale, resid)
     if x.dim() != 2:
         raise PragnosiaError(f"decode_gemm: x must be (B, K), got {tuple(x.shape)}")
@@ -1556,24 +1559,27 @@ def aspin_decode_proj_(S: Tensor, P: Tensor, H: int, la_bias: Tensor, A: Tensor,
                        gate_bias: Optional[Tensor], beta_bias: Optional[Tensor], beta_min: float, gated: bool,
                        theta: Tensor, p0_dev: Optional[Tensor], p0: float, on_weight: Optional[Tensor],
                        on_eps: float) -> Tensor:
-    """The carrier's recurrent step from one projection GEMV's output P (B, 3 H 64 + H [+ H]) (q, k, v, decay
-    logits, then the write-gate (gated) or write-strength logits), updating the carried state S (B, H, 64, 64) fp32 in
-    place. Returns the output token-major, (B, H * 64) fp32: RMS-normalised per head with on_weight, or raw when
-    on_weight is None (four workgroups per head; decode_gemv_rms then applies the RMSNorm)."""
+    """The carrier's recurrent step from one projection GEMV's output P (B, 3 H D + H [+ H]) (q, k, v, decay
+    logits, then the write-gate (gated) or write-strength logits), updating the carried state S (B, H, D, D) fp32 in
+    place. Returns the output token-major, (B, H * D) fp32: RMS-normalised per head with on_weight (D = 64), or raw
+    when on_weight is None (D = 64 or 128, D / 16 workgroups per head; decode_gemv_rms or decode_gemm then applies
+    the RMSNorm)."""
     _require_gpu(S, P, la_bias, A, theta, on_weight)
     if not (S.is_contiguous() and S.dtype == torch.float32):
         raise PragnosiaError("aspin_decode_proj_: the state must be a contiguous fp32 tensor (it is updated in place)")
     if P.dim() != 2:
         raise PragnosiaError(f"aspin_decode_proj_: P must be (B, W), got {tuple(P.shape)}")
-    _expect_proj("aspin_decode_proj_", P, H, gated, la_bias, A, la_floor, gate_bias, beta_bias, theta)
-    _expect("aspin_decode_proj_", P.device, S=(S, (P.shape[0], H, 64, 64)), p0_dev=(p0_dev, ()),
+    D = S.shape[-1] if S.dim() == 4 else 64
+    if D not in (64, 128) or (D == 128 and on_weight is not None):
+        raise PragnosiaError(f"aspin_decode_proj_: heads of {D} (64, or 128 with the raw output)")
+    _expect_proj("aspin_decode_proj_", P, H, gated, la_bias, A, la_floor, gate_bias, beta_bias, theta, D=D)
+    _expect("aspin_decode_proj_", P.device, S=(S, (P.shape[0], H, D, D)), p0_dev=(p0_dev, ()),
             on_weight=(on_weight, (64,)))
     P, la_bias, A, la_floor, theta = _f32(P), _f32(la_bias), _f32(A), _f32(la_floor), _f32(theta)
     gate_bias, beta_bias, p0_dev, on_weight = _f32(gate_bias), _f32(beta_bias), _f32(p0_dev), _f32(on_weight)
     B, np_ = P.shape
-    D = 64
     has_beta = not gated and np_ > 3 * H * D + H
-    acol, gcol, bcol = _proj_cols(H, gated, has_beta)
+    acol, gcol, bcol = _proj_cols(H, gated, has_beta, D)
     o = torch.empty(B, H * D, device=P.device, dtype=torch.float32)
     check(lib().pragnosia_aspin_decode_proj(_ptr(S), _ptr(S), _ptr(P), np_, acol, gcol, bcol, _ptr(la_bias), _ptr(A),
                                             _ptr(la_floor), _ptr(gate_bias), _ptr(beta_bias), float(beta_min),
@@ -1584,4 +1590,4 @@ def aspin_decode_proj_(S: Tensor, P: Tensor, H: int, la_bias: Tensor, A: Tensor,
 
 @aspin_decode_proj_.register_fake
 def _(S, P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, p0_dev, p0, on_weight, on_eps):
-    return P.new_empty(P.shape[0], H * 64, dtype=torch.float32)
+    return P.new_empty(P.shape[0], H * S.shape[-1], dtype=torch.float32)

@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 16
+    assert L.pragnosia_abi_version() == 17
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 
@@ -159,7 +159,8 @@ def test_decode_gemm_plans_and_rejections(L):
     assert q(768, 1) == 8 and q(768, 0) == 8 and q(3072, 0) == 8     # 8 waves of 6 steps; 3072: 4 chunks each
     assert q(768, 2) == 12 and q(1024, 2) == 16 and q(1088, 2) == -1   # one 64-channel group a wave
     assert q(3072, 1) == 8 and q(4096, 1) == 16 and q(128, 0) == 2
-    assert q(760, 0) == -1 and q(96, 2) == -1 and q(0, 0) == -1 and q(768, 3) == -1
+    assert q(768, 3) == 6 and q(2048, 3) == 16 and q(2176, 3) == -1 and q(704, 3) == -1  # one 128-group a wave
+    assert q(760, 0) == -1 and q(96, 2) == -1 and q(0, 0) == -1 and q(768, 4) == -1
     null, one = ctypes.c_void_p(0), ctypes.c_void_p(16)
     call = lambda B, K, mode, cs, x=one: L.pragnosia_decode_gemm(x, B, K, mode, cs, 1e-5, one, 768, null, null, 0,
                                                                 null, ctypes.c_void_p(32), null)
@@ -167,6 +168,9 @@ def test_decode_gemm_plans_and_rejections(L):
     assert call(64, 1088, 2, null) == -2                               # not covered
     assert call(0, 768, 0, null) == -1
     assert call(64, 768, 0, null, ctypes.c_void_p(24)) == -1           # misaligned input
+    rms = lambda G: L.pragnosia_decode_gemv_rms(one, 2, 768, one, G, 1e-6, one, 768, null, null, 0, null,
+                                               ctypes.c_void_p(32), null)
+    assert rms(96) == -1 and rms(0) == -1                              # heads of 64 or 128 only
 
 
 def test_product_never_imports_oracle():

@@ -92,21 +92,64 @@ def test_decode_proj_matches_module_step(delta, write_all, hl_floor):
             assert rel(S_r, st[0]) < 1e-4, step
 
 
+@pytest.mark.parametrize("delta,write_all", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("B", [2, 40])  # the GEMV consumer (B <= 4) and decode_gemm's (past it)
+def test_decode_proj_wide_matches_module_step(delta, write_all, B):
+    """The 128-dim step (raw output, eight workgroups per head) with its RMSNorm in the consumer (the o-projection's
+    GEMV, or decode_gemm's 128-channel RMS mode with the weight folded in) against the module's own T = 1 path
+    (its projections, the torch step at 128, nn.RMSNorm), from a rebased carried state, twice in a row."""
+    from pragnosia_amd import ops
+    from pragnosia_amd.assoc import AssocCarrier
+    op = torch.ops.pragnosia
+    torch.manual_seed(5)
+    d = 512
+    m = AssocCarrier(d, delta=delta, write_all=write_all, head_dim=128).cuda().eval()
+    with torch.no_grad():
+        for p in m.parameters():
+            p.add_(torch.randn_like(p) * 0.05)
+        H = m.h
+        S = torch.randn(B, H, 128, 128, device="cuda") * 0.1
+        S_f = S.clone()
+        p0 = torch.tensor([7.0], device="cuda")
+        gated = not (delta or write_all)
+        extra = [m.wi.weight] if gated else ([m.wb.weight] if delta else [])
+        W = torch.cat([m.q.weight, m.k.weight, m.v.weight, m.wa.weight] + extra)
+        eps = torch.finfo(torch.float32).eps
+        sig = torch.sigmoid(m.gate).reshape(1)
+        Wt = ops.decode_gemm_tile(m.o.weight, m.on.weight)
+        st = (S, 7)
+        for step in range(2):
+            x = torch.randn(B, 1, d, device="cuda")
+            y_mod, st = m(x, st)
+            P = F.linear(F.layer_norm(x.reshape(B, d), (d,), m.ln.weight, m.ln.bias, m.ln.eps), W)
+            o = op.aspin_decode_proj_(S_f, P, H, m.wa.bias, m.A, None, m.wi.bias if gated else None,
+                                      m.wb.bias if delta else None, 0.75 if (delta and write_all) else 0.0, gated,
+                                      m.theta, p0, 0.0, None, eps)
+            if B <= 4:
+                y = op.decode_gemv_rms(o, m.o.weight, m.on.weight, eps, None, sig, 0, x.reshape(B, d))
+            else:
+                y = op.decode_gemm(o, Wt, d, 3, None, eps, None, sig, 0, x.reshape(B, d))
+            p0.fill_(1.0)
+            assert rel(y - x.reshape(B, d), y_mod.reshape(B, d) - x.reshape(B, d)) < 1e-4, step
+            assert rel(S_f, st[0]) < 1e-4, step
+
+
 @pytest.mark.parametrize("B", [1, 3, 4])
+@pytest.mark.parametrize("G", [64, 128])
 @pytest.mark.parametrize("K,N,bias,act", [(768, 768, False, 0), (512, 300, True, 1), (1024, 1500, True, 0)])
-def test_decode_gemv_rms_matches_torch(B, K, N, bias, act):
+def test_decode_gemv_rms_matches_torch(B, K, N, bias, act, G):
     """The o-projection GEMV with the carrier's per-head (64-channel) RMSNorm on its input, against fp64 torch."""
     import pragnosia_amd.ops  # noqa: F401
     g = torch.Generator(device="cuda").manual_seed(B + K + N)
     x = torch.randn(B, K, device="cuda", generator=g)
     W = torch.randn(N, K, device="cuda", generator=g) * 0.05
-    w64 = 1 + 0.1 * torch.randn(64, device="cuda", generator=g)
+    w64 = 1 + 0.1 * torch.randn(G, device="cuda", generator=g)
     b = torch.randn(N, device="cuda", generator=g) if bias else None
     scale = torch.rand(1, device="cuda", generator=g)
     resid = torch.randn(B, N, device="cuda", generator=g)
     eps = torch.finfo(torch.float32).eps
     y = torch.ops.pragnosia.decode_gemv_rms(x, W, w64, eps, b, scale, act, resid)
-    z = F.rms_norm(x.double().view(B, K // 64, 64), (64,), w64.double(), eps).view(B, K)
+    z = F.rms_norm(x.double().view(B, K // G, G), (G,), w64.double(), eps).view(B, K)
     r = (z @ W.double().t()) * scale.double()
     if b is not None:
         r = r + b.double()
@@ -116,10 +159,12 @@ def test_decode_gemv_rms_matches_torch(B, K, N, bias, act):
     assert rel(y, r) < 1e-5
 
 
-@pytest.mark.parametrize("d", [128, 256])  # 256: the per-head RMSNorm runs inside the o-projection's GEMV
-@pytest.mark.parametrize("mixer", ["aspin", "dspin"])
-@pytest.mark.parametrize("B", [1, 3, 40])  # 1, 3: GEMV dense layers; 40: torch GEMMs around the fused step
+@pytest.mark.parametrize("d,mixer", [(128, "aspin"), (128, "dspin"), (256, "aspin"), (256, "dspin"),
+                                     (256, "hspin"), (256, "hdspin"), (512, "hspin1")])
+@pytest.mark.parametrize("B", [1, 3, 40])  # 1, 3: GEMV dense layers; 40: decode_gemm or torch GEMMs
 def test_fused_graphed_decode_equals_unfused_and_eager(mixer, B, d):
+    """d 256 and 64-dim heads: the per-head RMSNorm inside the o-projection's GEMV at B <= 4; 128-dim heads (hspin,
+    hdspin, hspin1): the raw-output step with the RMSNorm in the GEMV or in decode_gemm's 128-channel mode."""
     from pragnosia_amd.decode import GreedyDecoder, greedy_eager
     from pragnosia_amd.model import LM
     torch.manual_seed(50 + B)

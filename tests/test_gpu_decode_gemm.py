@@ -22,8 +22,9 @@ def reference(x, W, mode, nw, nb, eps, bias, scale, act, resid):
     B, K = x.shape
     if mode == 1:
         z = F.layer_norm(xd, (K,), nw.double(), None if nb is None else nb.double(), eps)
-    elif mode == 2:
-        z = F.rms_norm(xd.view(B, K // 64, 64), (64,), nw.double(), eps).view(B, K)
+    elif mode in (2, 3):
+        G = 64 if mode == 2 else 128
+        z = F.rms_norm(xd.view(B, K // G, G), (G,), nw.double(), eps).view(B, K)
     else:
         z = xd
     r = z @ Wd.t()
@@ -42,7 +43,7 @@ def inputs(B, K, N, mode, act, res, seed, mean=0.0):
     g = torch.Generator(device="cuda").manual_seed(seed)
     x = torch.randn(B, K, device="cuda", generator=g) + mean
     W = torch.randn(N, K, device="cuda", generator=g) * 0.05
-    nw = (1 + 0.1 * torch.randn(64 if mode == 2 else K, device="cuda", generator=g)) if mode else None
+    nw = (1 + 0.1 * torch.randn({2: 64, 3: 128}.get(mode, K), device="cuda", generator=g)) if mode else None
     nb = torch.randn(K, device="cuda", generator=g) if mode == 1 else None
     bias = torch.randn(N, device="cuda", generator=g) if act else None
     scale = torch.rand(1, device="cuda", generator=g) if res else None
@@ -51,14 +52,14 @@ def inputs(B, K, N, mode, act, res, seed, mean=0.0):
 
 
 def run(x, W, mode, nw, nb, eps, bias, scale, act, resid):
-    """The layer through decode_gemm: mode 1 folds the LayerNorm's weight and bias (decode_gemm_ln), mode 2 the
-    RMSNorm's weight into the tiled weight's columns."""
+    """The layer through decode_gemm: mode 1 folds the LayerNorm's weight and bias (decode_gemm_ln), modes 2 and 3
+    the RMSNorm's weight into the tiled weight's columns."""
     from pragnosia_amd import ops
     N = W.shape[0]
     if mode == 1:
         Wt, csum, b = ops.decode_gemm_ln(W, nw, nb, bias, scale)
         return torch.ops.pragnosia.decode_gemm(x, Wt, N, 1, csum, eps, b, scale, act, resid)
-    Wt = ops.decode_gemm_tile(W, nw if mode == 2 else None)
+    Wt = ops.decode_gemm_tile(W, nw if mode in (2, 3) else None)
     return torch.ops.pragnosia.decode_gemm(x, Wt, N, mode, None, eps, bias, scale, act, resid)
 
 
@@ -70,6 +71,8 @@ SHAPES = [(768, 2328, 1, 0, False),   # the carrier's projections (LayerNorm)
           (256, 200, 1, 1, True),     # a ragged column tile, small K
           (128, 1000, 0, 1, False),   # fewer than four waves
           (512, 300, 2, 1, True),     # RMS over 8 groups
+          (768, 768, 3, 0, True),     # 128-dim heads: RMSNorm over 6 groups of 128 + gated o-projection
+          (2048, 300, 3, 1, True),    # 16 groups of 128
           (1024, 640, 1, 0, False),   # LayerNorm over 16 waves of 4 steps
           (3072, 520, 1, 0, True),    # LayerNorm moments merged over 4 chunks a wave
           (4096, 520, 0, 0, True)]    # 16 waves of 4 chunks of 4 steps

@@ -204,9 +204,10 @@ def test_wide_lm_forward_carried_and_graphed_decode():
     assert rel(c, M.lm_forward_carried(sd, ids, 64, layers=2, mixer="hspin", heads=2)) < TOL_OUT
     prompt = ids[:, :100]
     dec = GreedyDecoder(m, 2, steps_per_graph=4)
-    assert not dec.fused
+    assert dec.fused  # the raw-output step at 128, the RMSNorm in the o-projection's GEMV
     toks_g = dec.generate(prompt.cuda(), 13)
+    toks_u = GreedyDecoder(m, 2, steps_per_graph=4, fused=False).generate(prompt.cuda(), 13)
     toks_e, lgs_e = greedy_eager(m, prompt.cuda(), 13)
-    assert torch.equal(toks_g.cpu(), toks_e.cpu())
+    assert torch.equal(toks_g.cpu(), toks_e.cpu()) and torch.equal(toks_u.cpu(), toks_e.cpu())
     _, lgs_r = M.greedy_decode(sd, prompt, 13, layers=2, mixer="hspin", heads=2, forced=toks_e.cpu())
     assert rel(lgs_e, lgs_r) < TOL_OUT
