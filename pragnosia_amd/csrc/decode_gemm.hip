@@ -188,13 +188,13 @@ bool make_plan(int64_t K, int mode, Plan& p) {
       S = s;
       break;
     }
-  const int64_t R = KS / S;  // chunks to spread over waves
-  for (int64_t cap : {8, MAXW})
-    for (int c : {1, 2, 4})
-      if (R % c == 0 && R / c <= cap) {
-        p = Plan{S, c, (int)(R / c)};
-        return true;
-      }
+  const int64_t R = KS / S;  // chunks to spread over waves: as many waves as allowed, each as few chunks (at 64 rows
+                             // and K 3072, 16 waves of 2 chunks took the step 0.608 -> 0.602 ms against 8 of 4)
+  for (int c : {1, 2, 4})
+    if (R % c == 0 && R / c <= MAXW) {
+      p = Plan{S, c, (int)(R / c)};
+      return true;
+    }
   return false;
 }
 

@@ -66,7 +66,7 @@ def run(x, W, mode, nw, nb, eps, bias, scale, act, resid):
 SHAPES = [(768, 2328, 1, 0, False),   # the carrier's projections (LayerNorm)
           (768, 768, 2, 0, True),     # RMSNorm + gated o-projection + residual (12 waves, one head each)
           (768, 3072, 1, 1, False),   # MLP in: LayerNorm + bias + GELU
-          (3072, 768, 0, 0, True),    # MLP out: bias-free here, residual; 4 chunks a wave
+          (3072, 768, 0, 0, True),    # MLP out: bias-free here, residual; 2 chunks a wave
           (768, 8192, 1, 0, False),   # the tied head
           (256, 200, 1, 1, True),     # a ragged column tile, small K
           (128, 1000, 0, 1, False),   # fewer than four waves
@@ -74,7 +74,8 @@ SHAPES = [(768, 2328, 1, 0, False),   # the carrier's projections (LayerNorm)
           (768, 768, 3, 0, True),     # 128-dim heads: RMSNorm over 6 groups of 128 + gated o-projection
           (2048, 300, 3, 1, True),    # 16 groups of 128
           (1024, 640, 1, 0, False),   # LayerNorm over 16 waves of 4 steps
-          (3072, 520, 1, 0, True),    # LayerNorm moments merged over 4 chunks a wave
+          (3072, 520, 1, 0, True),    # LayerNorm moments merged over 2 chunks a wave
+          (4096, 300, 1, 1, True),    # ... and over 4 chunks a wave
           (4096, 520, 0, 0, True)]    # 16 waves of 4 chunks of 4 steps
 
 
