@@ -44,10 +44,11 @@ def parse():
                     help="run each hot kernel a fixed number of times (for rocprofv3 counter passes) and exit")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the configs[4] decode measurement (batch 1 and 64), print its JSON and exit")
-    ap.add_argument("--profile-workload", choices=("layer", "layer_delta", "lm", "lm_delta", "wgrad"),
+    ap.add_argument("--profile-workload", choices=("layer", "layer_delta", "lm", "lm_delta", "wgrad", "head128"),
                     help="run one workload a fixed number of times for a tracer (rocprofv3 --kernel-trace or "
                          "--pmc) and exit: the carrier layer step (graph replays), the LM training micro-step "
-                         "(graph replays), or the weight-gradient kernel at the layer's two shapes")
+                         "(graph replays), the weight-gradient kernel at the layer's two shapes, or the head-dim-128 "
+                         "scan steps of `wide_bench`")
     ap.add_argument("--phase-rates", action="store_true",
                     help="measure the MFMA rate inside the scan kernels' per-chunk phases from the instrumented "
                          "build (libpragnosia_stamps.so), print its JSON and exit")
@@ -878,11 +879,15 @@ def cpu_baselines_more(args, seconds=5.0):
 def profile_workload(name, reps=10):
     """The workloads behind the layer, LM and weight-gradient traces in profiles/: `reps` graph replays of the
     carrier layer step (AssocCarrier(768), B16 T512, bf16 autocast, fused plumbing) or of the LM training micro-step
-    (d704 L12 mlp4 ctx2048 micro-batch 4, as lm_train_bench), after three eager warm-up steps on a side stream; or
-    `reps` calls of the weight-gradient kernel at 8192 x 2328 x 768 and 8192 x 768 x 768."""
+    (d704 L12 mlp4 ctx2048 micro-batch 4, as lm_train_bench), after three eager warm-up steps on a side stream;
+    `reps` calls of the weight-gradient kernel at 8192 x 2328 x 768 and 8192 x 768 x 768; or `wide_bench` as it
+    runs in the secondary measurements (head128)."""
     import torch
     from pragnosia_amd import assoc, ops
     torch.manual_seed(7)
+    if name == "head128":
+        print(json.dumps(wide_bench()), flush=True)
+        return
     if name == "wgrad":
         for M in (2328, 768):
             A = torch.randn(8192, M, device="cuda").bfloat16()

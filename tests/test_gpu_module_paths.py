@@ -165,7 +165,8 @@ def test_head_dim_128_mixers_lm(mixer):
     assert all(torch.isfinite(p.grad).all() for p in lm.parameters() if p.grad is not None)
     lm.eval()
     dec = GreedyDecoder(lm, 2, steps_per_graph=4)
-    assert not dec.fused
+    assert dec.fused == (mixer != "sdspin")  # the fused step at 128 (raw output, RMSNorm in the o-projection GEMV)
     toks_g = dec.generate(ids[:, :30].cuda(), 12)
+    toks_u = GreedyDecoder(lm, 2, steps_per_graph=4, fused=False).generate(ids[:, :30].cuda(), 12)
     toks_e, _ = greedy_eager(lm, ids[:, :30].cuda(), 12)
-    assert torch.equal(toks_g, toks_e)
+    assert torch.equal(toks_g, toks_e) and torch.equal(toks_u, toks_e)
