@@ -373,8 +373,8 @@ int pragnosia_aspin_decode_step(const float* S, float* S_out, const float* qp, c
  * non-NULL), the gate logit + gate_bias[h], beta = max(sigmoid(logit + beta_bias[h]), beta_min), then runs the step of
  * pragnosia_aspin_decode_step (S_out may equal S: in place) and writes the output per-head RMS-normalised and
  * token-major: o[b][h D + j] = (o_j r) on_weight[j], r = 1 / sqrt(mean_j o_j^2 + on_eps); with on_weight NULL the
- * output is written raw, o[b][h D + j] = o_j (D / 16 workgroups per head; the consumer applies the RMSNorm, e.g.
- * pragnosia_decode_gemv_rms). D = 64, or 128 with on_weight NULL (PRAGNOSIA_ERR_UNSUPPORTED otherwise). Replaces,
+ * output is written raw, o[b][h D + j] = o_j (D / 16 workgroups per head below 256 heads, one past it; the consumer
+ * applies the RMSNorm, e.g. pragnosia_decode_gemv_rms). D = 64, or 128 with on_weight NULL (PRAGNOSIA_ERR_UNSUPPORTED otherwise). Replaces,
  * inside the reference's graphed decode (src/bench.py:241-317), the T = 1 path of `AssocCarrier.forward` from its
  * projections to `self.on(o).transpose(1, 2).reshape(B, T, D)` (src/assoc.py:384-505). */
 int pragnosia_aspin_decode_proj(const float* S, float* S_out, const float* P, int64_t np, int64_t la_col,

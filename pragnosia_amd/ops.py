@@ -1562,8 +1562,8 @@ def aspin_decode_proj_(S: Tensor, P: Tensor, H: int, la_bias: Tensor, A: Tensor,
     """The carrier's recurrent step from one projection GEMV's output P (B, 3 H D + H [+ H]) (q, k, v, decay
     logits, then the write-gate (gated) or write-strength logits), updating the carried state S (B, H, D, D) fp32 in
     place. Returns the output token-major, (B, H * D) fp32: RMS-normalised per head with on_weight (D = 64), or raw
-    when on_weight is None (D = 64 or 128, D / 16 workgroups per head; decode_gemv_rms or decode_gemm then applies
-    the RMSNorm)."""
+    when on_weight is None (D = 64 or 128; D / 16 workgroups per head below 256 heads, one past it; decode_gemv_rms
+    or decode_gemm then applies the RMSNorm)."""
     _require_gpu(S, P, la_bias, A, theta, on_weight)
     if not (S.is_contiguous() and S.dtype == torch.float32):
         raise PragnosiaError("aspin_decode_proj_: the state must be a contiguous fp32 tensor (it is updated in place)")

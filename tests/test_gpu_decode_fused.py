@@ -93,22 +93,24 @@ def test_decode_proj_matches_module_step(delta, write_all, hl_floor):
 
 
 @pytest.mark.parametrize("delta,write_all", [(False, False), (False, True), (True, False), (True, True)])
-@pytest.mark.parametrize("B", [2, 40])  # the GEMV consumer (B <= 4) and decode_gemm's (past it)
-def test_decode_proj_wide_matches_module_step(delta, write_all, B):
-    """The 128-dim step (raw output, eight workgroups per head) with its RMSNorm in the consumer (the o-projection's
-    GEMV, or decode_gemm's 128-channel RMS mode with the weight folded in) against the module's own T = 1 path
-    (its projections, the torch step at 128, nn.RMSNorm), from a rebased carried state, twice in a row."""
+@pytest.mark.parametrize("dk,B", [(128, 2), (128, 40), (128, 80), (64, 40), (64, 80)])
+def test_decode_proj_raw_matches_module_step(delta, write_all, dk, B):
+    """The step with the raw output and its RMSNorm in the consumer (the o-projection's GEMV up to 4 sequences, else
+    decode_gemm's 64- or 128-channel RMS mode with the weight folded in) against the module's own T = 1 path (its
+    projections, the step, nn.RMSNorm), from a rebased carried state, twice in a row. d 512: at dk 128 the step runs
+    split (B 2, 40: 8 or 160 heads) or one workgroup a head (B 80: 320 heads); at dk 64 one workgroup a head (320 and
+    640 heads)."""
     from pragnosia_amd import ops
     from pragnosia_amd.assoc import AssocCarrier
     op = torch.ops.pragnosia
     torch.manual_seed(5)
     d = 512
-    m = AssocCarrier(d, delta=delta, write_all=write_all, head_dim=128).cuda().eval()
+    m = AssocCarrier(d, delta=delta, write_all=write_all, head_dim=dk).cuda().eval()
     with torch.no_grad():
         for p in m.parameters():
             p.add_(torch.randn_like(p) * 0.05)
         H = m.h
-        S = torch.randn(B, H, 128, 128, device="cuda") * 0.1
+        S = torch.randn(B, H, dk, dk, device="cuda") * 0.1
         S_f = S.clone()
         p0 = torch.tensor([7.0], device="cuda")
         gated = not (delta or write_all)
@@ -128,7 +130,7 @@ def test_decode_proj_wide_matches_module_step(delta, write_all, B):
             if B <= 4:
                 y = op.decode_gemv_rms(o, m.o.weight, m.on.weight, eps, None, sig, 0, x.reshape(B, d))
             else:
-                y = op.decode_gemm(o, Wt, d, 3, None, eps, None, sig, 0, x.reshape(B, d))
+                y = op.decode_gemm(o, Wt, d, 2 if dk == 64 else 3, None, eps, None, sig, 0, x.reshape(B, d))
             p0.fill_(1.0)
             assert rel(y - x.reshape(B, d), y_mod.reshape(B, d) - x.reshape(B, d)) < 1e-4, step
             assert rel(S_f, st[0]) < 1e-4, step
@@ -161,7 +163,8 @@ def test_decode_gemv_rms_matches_torch(B, K, N, bias, act, G):
 
 @pytest.mark.parametrize("d,mixer", [(128, "aspin"), (128, "dspin"), (256, "aspin"), (256, "dspin"),
                                      (256, "hspin"), (256, "hdspin"), (512, "hspin1")])
-@pytest.mark.parametrize("B", [1, 3, 40])  # 1, 3: GEMV dense layers; 40: decode_gemm or torch GEMMs
+@pytest.mark.parametrize("B", [1, 3, 40, 64])  # 1, 3: GEMV dense layers; 40, 64: decode_gemm or torch GEMMs
+# (at 64 and d >= 256 the step runs one workgroup a head)
 def test_fused_graphed_decode_equals_unfused_and_eager(mixer, B, d):
     """d 256 and 64-dim heads: the per-head RMSNorm inside the o-projection's GEMV at B <= 4; 128-dim heads (hspin,
     hdspin, hspin1): the raw-output step with the RMSNorm in the GEMV or in decode_gemm's 128-channel mode."""
