@@ -629,7 +629,8 @@ def summarize(r, rule):
 
 def lds_contraction_bench():
     """LDS-resident contraction microbenchmark (csrc/microbench/contract.hip): bf16 MFMA throughput of the scan
-    kernels' operand patterns with every operand on chip, at 8 and 16 waves per CU. Bounds what the contraction phases
+    kernels' operand patterns with every operand on chip, at 8 and 16 waves per CU, on the 16 x 16 x 32 MFMA the
+    kernels use and on the 32 x 32 x 16 one (half the operand bytes per flop). Bounds what the contraction phases
     could reach with no HBM traffic and no chunk chain."""
     import ctypes
     import torch
@@ -640,11 +641,13 @@ def lds_contraction_bench():
     fn.restype = ctypes.c_int
     stream = torch.cuda.current_stream()
     iters, waves = 2000, 8
-    names = {0: "registers only", 1: "one LDS operand per MFMA", 2: "LDS operand + accumulator->operand chain"}
+    names = {0: "registers only", 1: "one LDS operand per MFMA", 2: "LDS operand + accumulator->operand chain",
+             3: "32x32x16: registers only", 4: "32x32x16: one LDS operand per MFMA",
+             5: "32x32x16: LDS operand + accumulator->operand chain"}
     out = {}
     for per_cu, nwg in ((8, 256), (16, 512)):
         buf = torch.empty(nwg * 64 * waves, device="cuda")
-        for var in (0, 1, 2):
+        for var in range(6):
             call = lambda: fn(var, waves, iters, nwg, ctypes.c_void_p(buf.data_ptr()),
                               ctypes.c_void_p(stream.cuda_stream))
             assert call() == 0
