@@ -259,8 +259,10 @@ int64_t pragnosia_aspin_delta_bwd_workspace_bytes(int64_t B, int64_t H, int64_t 
 
 /* Backward of pragnosia_aspin_delta_fwd. dO (B, H, T, D) bf16; dS_final fp32 or NULL (zero). Writes dq, dk, dv
  * (bf16), dla and dbeta (fp32, (B, H, T)) and, if non-NULL, dS0 (fp32). `workspace` is caller-allocated device
- * memory of at least pragnosia_aspin_delta_bwd_workspace_bytes(...) bytes (no alignment beyond 256 B needed); at
- * D = 128 it also holds the second value-half scan's parts of dq, dk, dla and dbeta, which one more kernel adds.
+ * memory of at least pragnosia_aspin_delta_bwd_workspace_bytes(...) bytes (no alignment beyond 256 B needed). At
+ * D = 64 the backward is one kernel that passes the per-chunk state gradients and drhs between its waves on chip (the
+ * workspace is a token 256 bytes); at D = 128 the workspace holds them between two kernels, and the second value-half
+ * scan's parts of dq, dk, dla and dbeta, which one more kernel adds.
  * Replaces the registered backward of `delta_loop_fwd`, `delta_inv` and `assoc_out`
  * (`_delta_loop_bwd`, `_inv_bwd`, `_bwd_chunk` of src/assoc_kernel.py:73-116, :389-509, :625-704). */
 int pragnosia_aspin_delta_bwd(const void* q, const void* k, const void* v, const float* la, const float* beta,

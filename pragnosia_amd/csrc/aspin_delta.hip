@@ -1608,6 +1608,576 @@ __global__ __launch_bounds__(512) void aspin_delta_bwd_local(
 #undef DL_STAMP
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// backward in one kernel (64-wide heads): the chain and the chunk-local work of a scan in one workgroup of 16 waves,
+// chunks in reverse, so the per-chunk state gradient and drhs pass from the chain to the local work through LDS
+// instead of memory, and the staged Q, K, S_c and dO serve both. Waves 0-3 carry dS and waves 4-7 serve them, as in
+// aspin_delta_bwd_chain; waves 8-11 and 12-15 do aspin_delta_bwd_local's work for the same chunk, wave 8 + b owning
+// token block b in the query role (dQ, row sums, dV) and wave 12 + b in the key role (dK, column sums). Three barriers
+// per chunk:
+//   B1  A^T complete. Before it: the chain's dS-side products, the service waves' scores, the query role's dA, dP and
+//       whole dQ, the key role's dA and dP;
+//   B2  drhs ready: the chain's dW and drhs (into LDS) and its row sums; meanwhile the service waves stage the next
+//       chunk (Q, K, S_c, V, X, W double-buffered; dO read before B1 only) and the query role forms K K^T;
+//   end the chain's dS update (into LDS as the next chunk's dS), the query role's dN terms and dV = beta drhs, the
+//       key role's whole dK (its registers would not hold partial sums across the barriers) and its column sums.
+// The chunk's dla and dbeta are finished by wave 8 at the start of the next iteration (the last chunk's after the
+// loop) from the local waves' per-token sums and the chain's row sums. 16 waves hold at most 128 VGPRs each. LDS: dO,
+// A^T, drhs single; Q, S_c, K, V, X, W, dS double-buffered; the chain's and the local waves' per-token vectors, two
+// sets each: 156 KB.
+constexpr int kFusedTiles = 17;
+constexpr int kFusedLVec = 4 * C + 4;  // rowT, dbe2, colS, dwv per token; sdot per token block
+constexpr size_t fused_smem() {
+  return kFusedTiles * TILE * sizeof(__bf16) + (2 * kChainVec + 2 * kFusedLVec) * sizeof(float);
+}
+
+__global__ __launch_bounds__(1024) void aspin_delta_bwd_fused(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const float* __restrict__ la, const float* __restrict__ be, const __bf16* __restrict__ X,
+    const __bf16* __restrict__ sent, const __bf16* __restrict__ Win, const __bf16* __restrict__ dO,
+    const float* __restrict__ dSfin, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
+    float* __restrict__ dla, float* __restrict__ dbe, float* __restrict__ dS0, int T, int NC) {
+  constexpr int DKEY = 64;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __bf16* Os = reinterpret_cast<__bf16*>(smem);  // dO of the current chunk (read before B1 only)
+  __bf16* AT = Os + TILE;                          // AT[t][s] = A[s][t]
+  __bf16* Rs = AT + TILE;                          // drhs (t, j) of the current chunk
+  __bf16* Qb = Rs + TILE;                          // chunk c in set c & 1:
+  __bf16* Sb = Qb + 2 * TILE;                      //   S_c transposed (j, d)
+  __bf16* Kb = Sb + 2 * TILE;
+  __bf16* Vb = Kb + 2 * TILE;
+  __bf16* Xb = Vb + 2 * TILE;
+  __bf16* Wb = Xb + 2 * TILE;
+  __bf16* dSb = Wb + 2 * TILE;                     //   the gradient on the state leaving chunk c, transposed (j, d)
+  float* vec = reinterpret_cast<float*>(dSb + 2 * TILE);  // chain vector sets: L, eL, w, beta; row sums
+  float* lvec = vec + 2 * kChainVec;                       // local vector sets: rowT, dbe2, colS, dwv, sdot
+
+  const WaveIdx x = wave_idx();
+  const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
+  const DeltaRows<1> R(blockIdx.x);
+
+  if (w < 4) {
+    // ================= chain waves: value columns j = 16w + i; dS rows 16 db + 4g + r
+    const int j = 16 * w + i;
+    f32x4 dS[4];
+    {
+      const __amdgpu_buffer_rsrc_t dv_ = f32_view(dSfin ? dSfin + R.state() : nullptr, DKEY * DKEY);
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dS[db][r] = load_f32(dv_, (16 * db + 4 * g + r) * DKEY + j);
+    }
+    {
+      // the last chunk's dS for the local waves
+      __bf16* dst = dSb + ((NC - 1) & 1) * TILE + j * kPitch + 4 * g;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) *reinterpret_cast<bf16x4*>(dst + 16 * db) = to_bf16x4(dS[db]);
+    }
+    __syncthreads();
+    for (int cc = NC - 1; cc >= 0; --cc) {
+      const int h = cc & 1;
+      const __bf16* Qs = Qb + h * TILE;
+      const __bf16* Ss = Sb + h * TILE;
+      const __bf16* Ks = Kb + h * TILE;
+      const __bf16* Vs = Vb + h * TILE;
+      const __bf16* Xs = Xb + h * TILE;
+      float* vs = vec + h * kChainVec;
+      const float* Ls = vs;
+      const float* eLs = vs + C;
+      const float* ws = vs + 2 * C;
+      const float* bs = vs + 3 * C;
+      float* redV = vs + 4 * C;
+      float* redU = vs + 8 * C;
+      // products that do not need A^T: y = K dS, U = K S_c, Yc = (Q o eL)^T dO, on this wave's columns
+      bf16x8 dp[2], scf[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        dp[m] = pack(dS[2 * m], dS[2 * m + 1]);
+        scf[m] = frag(Ss, 16 * w + i, m, g);  // S_c[d][j], staged (j, d)
+      }
+      const bf16x8 oc0 = frag_tr(Os, 16 * w, 0, g, i), oc1 = frag_tr(Os, 16 * w, 1, g, i);  // dO[t][j]
+      f32x4 y[4], U[4], Yc[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        y[tb] = zero4();
+        U[tb] = zero4();
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const bf16x8 kk = frag(Ks, 16 * tb + i, m, g);
+          y[tb] = pgn_mfma(kk, dp[m], y[tb]);
+          U[tb] = pgn_mfma(kk, scf[m], U[tb]);
+        }
+      }
+      const bf16x8 oe0 = scale_frag_k(oc0, *reinterpret_cast<const f32x4*>(eLs + 4 * g),
+                                      *reinterpret_cast<const f32x4*>(eLs + 16 + 4 * g));
+      const bf16x8 oe1 = scale_frag_k(oc1, *reinterpret_cast<const f32x4*>(eLs + 32 + 4 * g),
+                                      *reinterpret_cast<const f32x4*>(eLs + 48 + 4 * g));
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        Yc[db] = pgn_mfma(frag_tr(Qs, 16 * db, 0, g, i), oe0, zero4());
+        Yc[db] = pgn_mfma(frag_tr(Qs, 16 * db, 1, g, i), oe1, Yc[db]);
+      }
+      __syncthreads();  // B1: A^T complete
+
+      // dW = A^T dO + w o (K dS); drhs = X^T dW into LDS; dU = -beta eL drhs; per-row partial sums
+      f32x4 dW[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        f32x4 acc = zero4();
+        if (tb < 2) acc = pgn_mfma(frag(AT, 16 * tb + i, 0, g), oc0, acc);
+        acc = pgn_mfma(frag(AT, 16 * tb + i, 1, g), oc1, acc);
+        const f32x4 wv = *reinterpret_cast<const f32x4*>(ws + 16 * tb + 4 * g);
+        dW[tb] = acc + wv * y[tb];
+      }
+      const bf16x8 w01 = pack(dW[0], dW[1]), w23 = pack(dW[2], dW[3]);
+      f32x4 dU[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        f32x4 acc = zero4();
+        if (tb < 2) acc = pgn_mfma(frag_tr(Xs, 16 * tb, 0, g, i), w01, acc);
+        acc = pgn_mfma(frag_tr(Xs, 16 * tb, 1, g, i), w23, acc);
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
+        const f32x4 ev = *reinterpret_cast<const f32x4*>(eLs + 16 * tb + 4 * g);
+        const f32x4 vv = to_f32x4(ds_read_tr(Vs + (16 * tb + 4 * g + (i >> 2)) * kPitch + 16 * w + 4 * (i & 3)));
+        float pr[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tl = 16 * tb + 4 * g + r;
+          dU[tb][r] = -bv[r] * ev[r] * acc[r];
+          pr[r] = acc[r] * vv[r];
+          pr[4 + r] = acc[r] * U[tb][r];
+          Rs[tl * kPitch + j] = (__bf16)acc[r];
+        }
+        const float tot = row_totals16x8(pr, i);
+        ((i & 8) ? redU : redV)[w * C + 16 * tb + 4 * g + ((i >> 1) & 3)] = tot;
+      }
+      __syncthreads();  // B2: drhs and the row sums ready
+
+      // dS_prev = a dS + (Q o eL)^T dO + K^T dU, kept in registers and written to LDS as the next chunk's dS
+      const float a_c = __expf(Ls[C - 1]);
+      const bf16x8 u01 = pack(dU[0], dU[1]), u23 = pack(dU[2], dU[3]);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        f32x4 acc = dS[db] * a_c + Yc[db];
+        acc = pgn_mfma(frag_tr(Ks, 16 * db, 0, g, i), u01, acc);
+        acc = pgn_mfma(frag_tr(Ks, 16 * db, 1, g, i), u23, acc);
+        dS[db] = acc;
+      }
+      {
+        __bf16* dst = dSb + (h ^ 1) * TILE + j * kPitch + 4 * g;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) *reinterpret_cast<bf16x4*>(dst + 16 * db) = to_bf16x4(dS[db]);
+      }
+      __syncthreads();  // end of the chunk
+    }
+    if (dS0) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dS0[R.state() + (size_t)(16 * db + 4 * g + r) * DKEY + j] = dS[db][r];
+    }
+  } else if (w < 8) {
+    // ================= service waves: thread b carries 16-byte row segments b and b + 256 of each staged tile:
+    // dO (single), then Q, S_c, K, V, X, W (into the chunk's set)
+    const int a = w - 4;
+    const int b = tid & 255;
+    constexpr int NT = 7;
+    bf16x8 sg[NT][2];
+    float pla = 0.f, pbe = 0.f;
+    auto load = [&](int cn) {
+      const int n0 = cn * C, nr = min(C, T - n0);
+#pragma unroll
+      for (int u = 0; u < NT; ++u) {
+        const __bf16* src;
+        int rows = nr;
+        if (u == 0) src = dO + R.vals(T) + (size_t)n0 * DKEY;
+        else if (u == 1) src = q + R.rows(T) + (size_t)n0 * DKEY;
+        else if (u == 2) { src = sent + R.stateT(NC, cn); rows = DK; }
+        else if (u == 3) src = k + R.rows(T) + (size_t)n0 * DKEY;
+        else if (u == 4) src = v + R.vals(T) + (size_t)n0 * DKEY;
+        else if (u == 5) { src = X + ((size_t)R.hw * NC + cn) * C * C; rows = C; }
+        else src = Win + R.vals(T) + (size_t)n0 * DKEY;
+        sg[u][0] = load_seg(src, rows, b);
+        sg[u][1] = load_seg(src, rows, b + 256);
+      }
+      pla = load_f32_lane(la + R.tok(T) + n0, nr, x.l);
+      pbe = load_f32_lane(be + R.tok(T) + n0, nr, x.l);
+    };
+    auto stage = [&](int hh) {
+#pragma unroll
+      for (int u = 0; u < NT; ++u) {
+        __bf16* dst = u == 0 ? Os : (u == 1 ? Qb : u == 2 ? Sb : u == 3 ? Kb : u == 4 ? Vb : u == 5 ? Xb : Wb) +
+                                        hh * TILE;
+        put_seg(dst, sg[u][0], b);
+        put_seg(dst, sg[u][1], b + 256);
+      }
+      if (a == 0) {
+        float* vs = vec + hh * kChainVec;
+        chunk_decays(pla, x.l, vs, vs + C, vs + 2 * C);
+        vs[3 * C + x.l] = pbe;
+      }
+    };
+    load(NC - 1);
+    stage((NC - 1) & 1);
+    load(max(NC - 2, 0));
+    __syncthreads();
+    for (int cc = NC - 1; cc >= 0; --cc) {
+      const int h = cc & 1;
+      const __bf16* Qs = Qb + h * TILE;
+      const __bf16* Ks = Kb + h * TILE;
+      const float* Ls = vec + h * kChainVec;
+      // scores, transposed: AT[t][s] = (q_s . k_t) exp(L_s - L_t), s >= t, zero below (split 2, 3, 3, 2)
+      {
+        auto score = [&](int ta, int sb, const bf16x8* kf, float Lt) {
+          f32x4 sc = zero4();
+#pragma unroll
+          for (int m = 0; m < 2; ++m) sc = pgn_mfma(frag(Qs, 16 * sb + i, m, g), kf[m], sc);
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[r] *= masked_decay(Lsv[r] - Lt, 16 * sb + 4 * g + r >= 16 * ta + i);
+          store_T(AT, 16 * ta, 16 * sb, g, i, sc);
+        };
+        const int t = 16 * a + i;
+        bf16x8 kf[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) kf[m] = frag(Ks, t, m, g);
+        const float Lt = Ls[t];
+        const int last = a == 0 ? 1 : 3;
+        for (int sb = 0; sb < 4; ++sb) {
+          if (sb < a) store_T(AT, 16 * a, 16 * sb, g, i, zero4());
+          else if (sb <= last) score(a, sb, kf, Lt);
+        }
+        if (a >= 2) {
+          bf16x8 kf0[2];
+#pragma unroll
+          for (int m = 0; m < 2; ++m) kf0[m] = frag(Ks, i, m, g);
+          score(0, a, kf0, Ls[i]);
+        }
+      }
+      __syncthreads();  // B1
+      // the next chunk's tiles (loaded a chunk ago: dO is free after B1, the other sets since the end of the
+      // previous chunk), then the loads of the one after (unconditional: the last ones re-read the first chunk)
+      if (cc > 0) stage(h ^ 1);
+      load(max(cc - 2, 0));
+      __syncthreads();  // B2
+      __syncthreads();  // end of the chunk
+    }
+  } else {
+    // ================= local waves
+    // the finished chunk's dla and dbeta (wave 8), from its vector sets
+    auto finish = [&](int cn) {
+      const int hh = cn & 1, t = x.l, t0 = cn * C, nr = min(C, T - t0);
+      const float* vs = vec + hh * kChainVec;
+      const float* lv = lvec + hh * kFusedLVec;
+      const float* redV = vs + 4 * C;
+      const float* redU = vs + 8 * C;
+      const float pv = redV[t] + redV[C + t] + redV[2 * C + t] + redV[3 * C + t];
+      const float pu = redU[t] + redU[C + t] + redU[2 * C + t] + redU[3 * C + t];
+      const float r0 = pv - vs[C + t] * pu, r1 = -vs[3 * C + t] * pu;
+      const float wdw = vs[2 * C + t] * lv[3 * C + t];
+      float dL = lv[t] - lv[2 * C + t] + vs[C + t] * r1 - wdw;
+      const float tot = wave_sum(wdw);
+      const float a_c = __expf(vs[C - 1]);
+      if (t == C - 1) dL += tot + a_c * (lv[4 * C] + lv[4 * C + 1] + lv[4 * C + 2] + lv[4 * C + 3]);
+      dL = rev_scan64(dL, t);
+      if (t < nr) {
+        const size_t ti = R.tok(T) + t0 + t;
+        dla[ti] = dL;
+        dbe[ti] = r0 + lv[C + t];
+      }
+    };
+    // ---------------- query role, token block WL (lane t = me): dQ whole before B1; the row sums; dV
+    auto qrole = [&](auto wl_c) {
+      constexpr int WL = decltype(wl_c)::value;
+      const int me = 16 * WL + i;
+      const int lt = tid - 512;  // 0 .. 255
+      __syncthreads();
+      for (int cc = NC - 1; cc >= 0; --cc) {
+        const int h = cc & 1, t0 = cc * C, nr = min(C, T - t0);
+        if (WL == 0 && cc < NC - 1) finish(cc + 1);
+        const __bf16* Qs = Qb + h * TILE;
+        const __bf16* Ss = Sb + h * TILE;
+        const __bf16* Ks = Kb + h * TILE;
+        const __bf16* Ws = Wb + h * TILE;
+        const float* vs = vec + h * kChainVec;
+        const float* Ls = vs;
+        const float* eLs = vs + C;
+        const float* bs = vs + 3 * C;
+        float* lv = lvec + h * kFusedLVec;
+        const int out_bytes = nr * DKEY * (int)sizeof(__bf16);
+        const float Lt = Ls[me], bt = bs[me], eLt = eLs[me];
+        bf16x8 qf[2], kf[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          qf[m] = frag(Qs, me, m, g);
+          kf[m] = frag(Ks, me, m, g);
+        }
+        const bf16x8 of0 = frag(Os, me, 0, g), of1 = frag(Os, me, 1, g);
+        // rows s, lane t: P[t][s], dA[t][s] for s <= t
+        float rowacc = 0.f;
+        f32x4 dPT[4];
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+          dPT[sb] = zero4();
+          if (sb <= WL) {
+            f32x4 P = zero4(), dA = zero4();
+#pragma unroll
+            for (int m = 0; m < 2; ++m) P = pgn_mfma(frag(Ks, 16 * sb + i, m, g), qf[m], P);
+            dA = pgn_mfma(frag(Ws, 16 * sb + i, 0, g), of0, dA);
+            dA = pgn_mfma(frag(Ws, 16 * sb + i, 1, g), of1, dA);
+            const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float dec = masked_decay(Lt - Lsv[r], 16 * sb + 4 * g + r <= me);
+              rowacc += dA[r] * P[r] * dec;
+              dPT[sb][r] = dA[r] * dec;
+            }
+          }
+        }
+        float qzt = 0.f;
+        {
+          // dQ = dP K + eL o (dO S^T), whole; rows past the chunk's end dropped
+          const bf16x8 b0 = pack(dPT[0], dPT[1]), b1 = pack(dPT[2], dPT[3]);
+          const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+              dq + R.rows(T) + (size_t)t0 * DKEY, (short)0, out_bytes, 0x00020000);
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            const int n0 = 16 * dt;
+            f32x4 acc = zero4(), Z = zero4();
+            acc = pgn_mfma(frag_tr(Ks, n0, 0, g, i), b0, acc);
+            if (WL >= 2) acc = pgn_mfma(frag_tr(Ks, n0, 1, g, i), b1, acc);
+            Z = pgn_mfma(frag_tr(Ss, n0, 0, g, i), of0, Z);
+            Z = pgn_mfma(frag_tr(Ss, n0, 1, g, i), of1, Z);
+            const f32x4 qq = to_f32x4(*reinterpret_cast<const bf16x4*>(Qs + me * kPitch + n0 + 4 * g));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) qzt += qq[r] * Z[r];
+            acc = acc + Z * eLt;
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), out,
+                                                  (me * DKEY + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+          }
+        }
+        __syncthreads();  // B1
+        // K K^T blocks s <= t against this lane's token, while the chain forms drhs
+        f32x4 KK[WL + 1];
+#pragma unroll
+        for (int sb = 0; sb <= WL; ++sb) {
+          KK[sb] = zero4();
+#pragma unroll
+          for (int m = 0; m < 2; ++m) KK[sb] = pgn_mfma(frag(Ks, 16 * sb + i, m, g), kf[m], KK[sb]);
+        }
+        __syncthreads();  // B2
+        // dN[t][s] = -sum_j drhs[t][j] W[s][j], s < t; rows s, lane t
+        const bf16x8 rf0 = frag(Rs, me, 0, g), rf1 = frag(Rs, me, 1, g);
+        float db2 = 0.f;
+#pragma unroll
+        for (int sb = 0; sb <= WL; ++sb) {
+          f32x4 dN = zero4();
+          dN = pgn_mfma(frag(Ws, 16 * sb + i, 0, g), rf0, dN);
+          dN = pgn_mfma(frag(Ws, 16 * sb + i, 1, g), rf1, dN);
+          const f32x4 Lsv = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int s_ = 16 * sb + 4 * g + r;
+            const float dec = masked_decay(Lt - Lsv[r], s_ <= me);
+            const float dnM = -dN[r] * KK[sb][r] * dec * (s_ < me ? 1.f : 0.f);  // dN M, strictly lower
+            db2 += dnM;
+            rowacc += bt * dnM;
+          }
+        }
+        rowacc = sum_groups(rowacc);
+        db2 = sum_groups(db2);
+        qzt = sum_groups(qzt);
+        if (g == 0) {
+          lv[me] = rowacc + eLt * qzt;  // rowsum(dA o A) + rowsum(dKK o KK) + eL q.(S dO)
+          lv[C + me] = db2;             // sum_{s<t} dN M
+        }
+        {
+          // dV = beta drhs, 16-byte row segments lt and lt + 256 of the LDS drhs (rows past the chunk's end dropped)
+          const __amdgpu_buffer_rsrc_t dv_out = __builtin_amdgcn_make_buffer_rsrc(
+              dv + R.vals(T) + (size_t)t0 * DKEY, (short)0, out_bytes, 0x00020000);
+#pragma unroll
+          for (int e2 = 0; e2 < 2; ++e2) {
+            const int e = lt + 256 * e2, row = e >> 3, c8 = 8 * (e & 7);
+            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(Rs + row * kPitch + c8);
+            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(Rs + row * kPitch + c8 + 4);
+            const float bb = bs[row];
+            bf16x8 o8;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              o8[u] = (__bf16)(bb * (float)lo[u]);
+              o8[4 + u] = (__bf16)(bb * (float)hi[u]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, o8), dv_out,
+                                                   (row * DKEY + c8) * (int)sizeof(__bf16), 0, 0);
+          }
+        }
+        __syncthreads();  // end of the chunk
+      }
+      if (WL == 0) finish(0);
+    };
+    // ---------------- key role, token block WL (lane s = me): dA and dP before B1, the whole dK after B2
+    auto krole = [&](auto wl_c) {
+      constexpr int WL = decltype(wl_c)::value;
+      const int me = 16 * WL + i;
+      __syncthreads();
+      for (int cc = NC - 1; cc >= 0; --cc) {
+        const int h = cc & 1, t0 = cc * C, nr = min(C, T - t0);
+        const __bf16* Qs = Qb + h * TILE;
+        const __bf16* Ss = Sb + h * TILE;
+        const __bf16* Ks = Kb + h * TILE;
+        const __bf16* Ws = Wb + h * TILE;
+        const __bf16* dSs = dSb + h * TILE;
+        const float* vs = vec + h * kChainVec;
+        const float* Ls = vs;
+        const float* eLs = vs + C;
+        const float* ws = vs + 2 * C;
+        const float* bs = vs + 3 * C;
+        float* lv = lvec + h * kFusedLVec;
+        const int out_bytes = nr * DKEY * (int)sizeof(__bf16);
+        const float Lsm = Ls[me];
+        // rows t, lane s: P[t][s], dA[t][s] for t >= s
+        float colacc = 0.f;
+        bf16x8 p0, p1;
+        {
+          bf16x8 kf[2];
+#pragma unroll
+          for (int m = 0; m < 2; ++m) kf[m] = frag(Ks, me, m, g);
+          const bf16x8 wf0 = frag(Ws, me, 0, g), wf1 = frag(Ws, me, 1, g);
+          f32x4 dPt[4];
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            dPt[tb] = zero4();
+            if (tb >= WL) {
+              f32x4 P = zero4(), dA = zero4();
+#pragma unroll
+              for (int m = 0; m < 2; ++m) P = pgn_mfma(frag(Qs, 16 * tb + i, m, g), kf[m], P);
+              dA = pgn_mfma(frag(Os, 16 * tb + i, 0, g), wf0, dA);
+              dA = pgn_mfma(frag(Os, 16 * tb + i, 1, g), wf1, dA);
+              const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float dec = masked_decay(Ltv[r] - Lsm, 16 * tb + 4 * g + r >= me);
+                colacc += dA[r] * P[r] * dec;
+                dPt[tb][r] = dA[r] * dec;
+              }
+            }
+          }
+          p0 = pack(dPt[0], dPt[1]);
+          p1 = pack(dPt[2], dPt[3]);
+        }
+        __syncthreads();  // B1
+        // K K^T blocks t >= s against this lane's token, while the chain forms drhs
+        f32x4 KK[4];
+        {
+          bf16x8 kf[2];
+#pragma unroll
+          for (int m = 0; m < 2; ++m) kf[m] = frag(Ks, me, m, g);
+#pragma unroll
+          for (int tb = WL; tb < 4; ++tb) {
+            KK[tb] = zero4();
+#pragma unroll
+            for (int m = 0; m < 2; ++m) KK[tb] = pgn_mfma(frag(Ks, 16 * tb + i, m, g), kf[m], KK[tb]);
+          }
+        }
+        __syncthreads();  // B2
+        const float bsm = bs[me], wsm = ws[me], eLsm = eLs[me];
+        const bf16x8 wf0 = frag(Ws, me, 0, g), wf1 = frag(Ws, me, 1, g);
+        const bf16x8 rf0 = frag(Rs, me, 0, g), rf1 = frag(Rs, me, 1, g);
+        f32x4 Gt[4];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          Gt[tb] = zero4();
+          if (tb >= WL) {
+            // rows t, lane s: dN[t][s] = -sum_j drhs[t][j] W[s][j]
+            f32x4 dN = zero4();
+            dN = pgn_mfma(frag(Rs, 16 * tb + i, 0, g), wf0, dN);
+            dN = pgn_mfma(frag(Rs, 16 * tb + i, 1, g), wf1, dN);
+            const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+            const f32x4 btv = *reinterpret_cast<const f32x4*>(bs + 16 * tb + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = 16 * tb + 4 * g + r;
+              const float dec = masked_decay(Ltv[r] - Lsm, t >= me);
+              const float dkk = -btv[r] * dN[r] * dec * (t > me ? 1.f : 0.f);  // dKK[t][s], strictly lower
+              colacc += dkk * KK[tb][r];
+              Gt[tb][r] = dkk;
+            }
+          }
+          if (tb <= WL) {
+            // rows t, lane s: dN[s][t] = -sum_j W[t][j] drhs[s][j], for t < s
+            f32x4 dN = zero4();
+            dN = pgn_mfma(frag(Ws, 16 * tb + i, 0, g), rf0, dN);
+            dN = pgn_mfma(frag(Ws, 16 * tb + i, 1, g), rf1, dN);
+            const f32x4 Ltv = *reinterpret_cast<const f32x4*>(Ls + 16 * tb + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = 16 * tb + 4 * g + r;
+              Gt[tb][r] += -bsm * dN[r] * masked_decay(Lsm - Ltv[r], t < me);  // dKK[s][t]
+            }
+          }
+        }
+        colacc = sum_groups(colacc);
+        const bf16x8 g0 = pack(Gt[0], Gt[1]), g1 = pack(Gt[2], Gt[3]);
+        const float us = -bsm * eLsm;  // dU[s] = us * drhs[s]
+        const bf16x8 du0 = frag_scaled(Rs, me, 0, g, us), du1 = frag_scaled(Rs, me, 1, g, us);
+        const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+            dk + R.rows(T) + (size_t)t0 * DKEY, (short)0, out_bytes, 0x00020000);
+        float dw = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          // dK = dP^T Q + G K + dU S^T + w o (W dS^T), whole; rows past the chunk's end dropped
+          const int n0 = 16 * dt;
+          f32x4 acc = zero4(), Y = zero4();
+          if (WL < 2) acc = pgn_mfma(frag_tr(Qs, n0, 0, g, i), p0, acc);
+          acc = pgn_mfma(frag_tr(Qs, n0, 1, g, i), p1, acc);
+          acc = pgn_mfma(frag_tr(Ks, n0, 0, g, i), g0, acc);
+          acc = pgn_mfma(frag_tr(Ks, n0, 1, g, i), g1, acc);
+          acc = pgn_mfma(frag_tr(Ss, n0, 0, g, i), du0, acc);
+          acc = pgn_mfma(frag_tr(Ss, n0, 1, g, i), du1, acc);
+          Y = pgn_mfma(frag_tr(dSs, n0, 0, g, i), wf0, Y);
+          Y = pgn_mfma(frag_tr(dSs, n0, 1, g, i), wf1, Y);
+          const f32x4 kk = to_f32x4(*reinterpret_cast<const bf16x4*>(Ks + me * kPitch + n0 + 4 * g));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dw += kk[r] * Y[r];
+          acc = acc + Y * wsm;
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc)), out,
+                                                (me * DKEY + 16 * dt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+        }
+        dw = sum_groups(dw);
+        if (g == 0) {
+          lv[2 * C + me] = colacc;  // colsum(dA o A) + colsum(dKK o KK)
+          lv[3 * C + me] = dw;      // k_s . (dS W_s)
+        }
+        {
+          // <S_c, dS> over key rows 16 WL .. (both staged transposed: a plain read of row 16 jt + i)
+          float sd = 0.f;
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) {
+            const int off = (16 * jt + i) * kPitch + 16 * WL + 4 * g;
+            const f32x4 sv = to_f32x4(*reinterpret_cast<const bf16x4*>(Ss + off));
+            const f32x4 dv_ = to_f32x4(*reinterpret_cast<const bf16x4*>(dSs + off));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sd += sv[r] * dv_[r];
+          }
+          sd = wave_sum(sd);
+          if (x.l == 0) lv[4 * C + WL] = sd;
+        }
+        __syncthreads();  // end of the chunk
+      }
+    };
+    switch (w) {
+      case 8: qrole(std::integral_constant<int, 0>{}); break;
+      case 9: qrole(std::integral_constant<int, 1>{}); break;
+      case 10: qrole(std::integral_constant<int, 2>{}); break;
+      case 11: qrole(std::integral_constant<int, 3>{}); break;
+      case 12: krole(std::integral_constant<int, 0>{}); break;
+      case 13: krole(std::integral_constant<int, 1>{}); break;
+      case 14: krole(std::integral_constant<int, 2>{}); break;
+      default: krole(std::integral_constant<int, 3>{}); break;
+    }
+  }
+}
+
 // The slot sums of the 128-wide backward: x[p][i] <- x[p][i] + y[p][i] for the bf16 pairs (dq, dk; the fp32 sum of
 // two bf16 values rounded once, as a bf16 tensor add rounds) over n elements (n % 8 == 0), and f[p][i] <- f[p][i] +
 // e[p][i] for the fp32 pairs (dla, dbeta) over m elements (m <= n / 8). Thread u covers elements 8u .. 8u + 7 of
@@ -1732,22 +2302,22 @@ int set_smem(const void* fn, size_t bytes) { return (int)pgn_lds_limit(fn, bytes
 
 int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
-// The backward's workspace: drhs (B, H, T, D) bf16, the per-chunk state gradients (B, H, NC, D, D) bf16 and the
-// per-scan row sums (B H D / 64 scans, T, 2) fp32; at D = 128 then the second slots of dq and dk ((B, H, T, D) bf16)
-// and of dla and dbeta ((B, H, T) fp32).
+// The backward's workspace. At D = 64 the one-kernel backward keeps everything on chip: a token 256 bytes. At D = 128:
+// drhs (B, H, T, D) bf16, the per-chunk state gradients (B, H, NC, D, D) bf16 and the per-scan row sums (B H D / 64
+// scans, T, 2) fp32, then the second slots of dq and dk ((B, H, T, D) bf16) and of dla and dbeta ((B, H, T) fp32).
 struct BwdWorkspace {
   int64_t drhs, dsc, rsum, dq1, dk1, dla1, dbe1, total;
   BwdWorkspace(int64_t B, int64_t H, int64_t T, int64_t D) {
     const int64_t NC = (T + C - 1) / C, KH = D / DK;
+    if (KH == 1) {
+      drhs = dsc = rsum = dq1 = dk1 = dla1 = dbe1 = -1;
+      total = 256;
+      return;
+    }
     drhs = 0;
     dsc = align256(B * H * T * D * 2);
     rsum = dsc + align256(B * H * NC * D * D * 2);
     const int64_t rs = B * H * KH * T * 2 * 4;
-    if (KH == 1) {
-      dq1 = dk1 = dla1 = dbe1 = -1;
-      total = rsum + rs;
-      return;
-    }
     dq1 = rsum + align256(rs);
     dk1 = dq1 + align256(B * H * T * D * 2);
     dla1 = dk1 + align256(B * H * T * D * 2);
@@ -1787,6 +2357,16 @@ int delta_bwd(const void* q, const void* k, const void* v, const float* la, cons
               const void* W, const void* X, const void* dO, const float* dS_final, void* dq, void* dk, void* dv,
               float* dla, float* dbeta, float* dS0, void* workspace, int64_t B, int64_t H, int64_t T,
               hipStream_t st) {
+  if constexpr (KH == 1) {  // one kernel: the chain and the chunk-local work share the workgroup, nothing in memory
+    const int rc = set_smem((const void*)aspin_delta_bwd_fused, fused_smem());
+    if (rc) return rc;
+    hipLaunchKernelGGL(aspin_delta_bwd_fused, dim3((unsigned)(B * H)), dim3(1024), fused_smem(), st,
+                       (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, beta, (const __bf16*)X,
+                       (const __bf16*)sent, (const __bf16*)W, (const __bf16*)dO, dS_final, (__bf16*)dq, (__bf16*)dk,
+                       (__bf16*)dv, dla, dbeta, dS0, (int)T, (int)((T + C - 1) / C));
+    (void)workspace;
+    PGN_RETURN_LAUNCH();
+  }
   int rc = set_smem((const void*)aspin_delta_bwd_chain<KH>, chain_smem<KH>());
   if (rc) return rc;
   rc = set_smem((const void*)aspin_delta_bwd_local<KH>, local_smem<KH>());

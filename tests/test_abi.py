@@ -106,11 +106,11 @@ def test_wide_arguments(L):
 
 
 def test_delta_workspace_both_widths(L):
-    """The delta backward's workspace: drhs, the per-chunk state gradients and the per-scan row sums; at head dim 128
-    also the second slots of dq, dk, dla and dbeta (each head runs as two value-half scans whose parts are summed)."""
+    """The delta backward's workspace: at head dim 64 a token (the one-kernel backward keeps its per-chunk state
+    gradients and drhs on chip); at 128 drhs, the per-chunk state gradients and the per-scan row sums, then the second
+    slots of dq, dk, dla and dbeta (each head runs as two value-half scans whose parts are summed)."""
     q = L.pragnosia_aspin_delta_bwd_workspace_bytes
-    # B2 H3 T100 (2 chunks), D 64: drhs 76800 + state gradients 98304 + row sums 4800
-    assert q(2, 3, 100, 64, 64) == 76800 + 98304 + 4800
+    assert q(2, 3, 100, 64, 64) == 256 and q(16, 12, 512, 64, 64) == 256
     # D 128: drhs 153600 + state gradients 393216 + row sums 9600 (to 9728) + dq, dk 153600 each + dla 2400 (to
     # 2560) + dbeta 2400
     assert q(2, 3, 100, 128, 64) == 153600 + 393216 + 9728 + 2 * 153600 + 2560 + 2400
