@@ -197,16 +197,16 @@ def aspin_bench(rule, steps, warmup):
         bwd_bytes = 7 * 2 * elem + 2 * sent_n + 16 * ht + 8 * state
         # what this implementation moves besides, as a formula (the counter-measured bytes, where the traffic table
         # has them, replace it in op_roofline): in the forward (one kernel, the inverses formed on chip; the inverse
-        # waves' key reads hit L2) X (bf16 C x C per chunk) and W written for the backward; in the backward X read,
-        # W read, the chain/local hand-off (drhs and per-chunk dS, bf16) written once and read once, and the entering
-        # states read a second time (the two backward kernels also both read q, k and dO, which the counters include)
+        # waves' key reads hit L2) X (bf16 C x C per chunk) and W written for the backward; in the backward (one
+        # kernel, the chain and the chunk-local work passing drhs and the per-chunk dS through LDS) X and W read
         x_n = B * H * NC * C * C
         impl_fwd = fwd_bytes + 2 * x_n + 2 * elem
-        impl_bwd = bwd_bytes + 2 * x_n + 2 * elem + 2 * sent_n + 2 * (2 * elem + 2 * sent_n)
+        impl_bwd = bwd_bytes + 2 * x_n + 2 * elem
         fwd_flops = (4 * D * (C + D) + 2 * C * D + 2 * D * D + 2 * C * C) * ht
         bwd_flops = (10 * D * (C + D) + 6 * C * D + 4 * D * D + 4 * C * C) * ht
-        names = ("aspin_delta_fwd_inv (one kernel, inverses on chip)", "aspin_delta_bwd (chain + local kernels)")
-        counted = ("aspin_delta_fwd_inv", "aspin_delta_bwd_chain", "aspin_delta_bwd_local")
+        names = ("aspin_delta_fwd_inv (one kernel, inverses on chip)",
+                 "aspin_delta_bwd_fused (one kernel: the chain and the chunk-local work)")
+        counted = ("aspin_delta_fwd_inv", "aspin_delta_bwd_fused")
     cold = _rotating_bwd(rule, stream, x)
     return dict(B=B, H=H, T=T, D=D, C=C, wall=wall, eager=eager, t_fwd=t_fwd, t_bwd=t_bwd, fwd_bytes=fwd_bytes,
                 bwd_bytes=bwd_bytes, impl_fwd_bytes=impl_fwd, impl_bwd_bytes=impl_bwd, fwd_flops=fwd_flops,
