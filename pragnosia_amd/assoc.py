@@ -249,13 +249,17 @@ class AssocCarrier(nn.Module):
 
     @property
     def sent(self):
-        """The bf16 state entering every 64-token chunk of the last kernel-path call, (B, H, NC, dk, dk), or None (the
-        reference's `self.sent`, `src/assoc.py:349,510`, which its retrieval layers read). The 128-wide scan keeps it
-        per 64 x 64 block; it is assembled on first read."""
+        """The bf16 state entering every chunk of the last kernel-path call, (B, H, NC, dk, dk), or None (the
+        reference's `self.sent`, `src/assoc.py:349,510`, which its retrieval layers read). The kernels run 64-token
+        chunks; a delta carrier built with chunk=128 (the reference's 128-token delta kernel, `src/assoc.py:494-495`)
+        gets the states entering every 128-token chunk, those of every other 64-token one (the result does not depend
+        on the chunk). The 128-wide scan keeps it per 64 x 64 block; it is assembled on first read."""
         s = self.__dict__.get("_sent")
         if s is not None and s.dim() == 6:
             s = _op_mod.wide_sent(s)
             self.__dict__["_sent"] = s
+        if s is not None and self.delta and self.chunk == 128:
+            s = s[:, :, ::2]
         return s
 
     @sent.setter

@@ -165,3 +165,28 @@ def test_beta_scale_and_hl_floor(kernel):
     floor = (-math.log(2.0) / torch.logspace(math.log10(8.0), math.log10(131072.0), mod.h)).double()
     assert torch.allclose(mod.la_floor.cpu().double(), floor)
     _check(mod, g, True, (2e-2, 5e-2) if kernel else (1e-4, 1e-4), la_floor=floor, beta_scale=bs.double())
+
+
+def test_delta_chunk128_entering_states():
+    """A delta carrier built with chunk=128 (the reference's 128-token delta kernel, `src/assoc.py:494-495`) returns
+    the same output and final state as at chunk 64 (the result does not depend on the chunk) and exposes the states
+    entering every 128-token chunk: those of every other 64-token chunk, ceil(T / 128) of them, each against the
+    fp64 oracle's chunk-128 entering states (bf16 kernel tolerance)."""
+    from oracle import aspin as OA
+    m64, g = _carrier(91, delta=True)
+    m128, _ = _carrier(91, delta=True, chunk=128)
+    x = torch.randn(2, 300, 128, generator=g).cuda()
+    with torch.no_grad():
+        y64, (S64, _) = m64(x)
+        y128, (S128, _) = m128(x)
+    assert torch.equal(y64, y128) and torch.equal(S64, S128)
+    s64, s128 = m64.sent, m128.sent
+    assert s128.shape == (2, m64.h, 3, 64, 64) and torch.equal(s128, s64[:, :, ::2])
+    # the oracle's chunk-128 scan on the kernel's own inputs (its prep), entering states of every 128-token chunk
+    with torch.no_grad():
+        from pragnosia_amd.assoc import _positions
+        z = m64._norm_in(x)
+        q, k, v, la, bt, _, _ = m64._scan_inputs(z, _positions(300, x.device, None), None)
+    _, _, ent, _ = OA.scan_twopass_delta(q.double().cpu(), k.double().cpu(), v.double().cpu(), la.double().cpu(),
+                                         bt.double().cpu(), torch.zeros(2, m64.h, 64, 64, dtype=torch.float64), 128)
+    assert rel(s128.float(), ent.float()) < 2e-2
