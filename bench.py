@@ -1007,7 +1007,8 @@ COPY_BYTES = 256 << 20
 # below the diagonal). Plain backward: group K 152 (P and dA 4 per block WL..3, then 4 dV^T and 4 dK^T tiles of 3 or
 # 4), group D 128 (P^T and dA^T 4 per block 0..WL, 4 dQ^T tiles of 3 or 4, the dS update 4 x 2). Delta forward
 # chain: 4 chain waves x 36 (U = K S 8, W = X rhs 6, O 14, state update 8) and the scores 20 (the inverse waves' bf16
-# products, 20 a chunk, run in other phases and are not counted). Delta backward chain:
+# products, 20 a chunk, run in other phases and are not counted). Delta backward chain (the chain and service waves
+# of the one-kernel backward; its eight chunk-local waves' products are not counted):
 # 4 chain waves x 44 (K dS 8, K S_c 8, (Q o eL)^T dO 8, dW 6, drhs 6, dS update 8) and the transposed scores 20.
 PHASE_MFMAS = {"plain_fwd": {"output": 88, "score": 20}, "plain_bwd": 280, "delta_fwd": 164, "delta_bwd_chain": 196}
 MFMA_FLOPS = 16 * 16 * 32 * 2

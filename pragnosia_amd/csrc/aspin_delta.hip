@@ -1655,9 +1655,14 @@ __global__ __launch_bounds__(1024) void aspin_delta_bwd_fused(
   const WaveIdx x = wave_idx();
   const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
   const DeltaRows<1> R(blockIdx.x);
+  // instrumented build, as aspin_delta_bwd_chain's (waves 0-7): per wave, clocks where its role's branch starts
+  // (entries 0, 1) and at the kernel's end (2, 3), then the start and end of its phase for chunk cc (4 + 2 cc, 5 + 2 cc)
+#define DB_STAMP(k) PGN_STAMP((blockIdx.x * 8 + w) * (4 + 2 * NC) + (k))
+#define DB_CLOCKS(k) PGN_STAMP_CLOCKS((blockIdx.x * 8 + w) * (4 + 2 * NC) + (k))
 
   if (w < 4) {
     // ================= chain waves: value columns j = 16w + i; dS rows 16 db + 4g + r
+    DB_CLOCKS(0);
     const int j = 16 * w + i;
     f32x4 dS[4];
     {
@@ -1675,6 +1680,7 @@ __global__ __launch_bounds__(1024) void aspin_delta_bwd_fused(
     }
     __syncthreads();
     for (int cc = NC - 1; cc >= 0; --cc) {
+      DB_STAMP(4 + 2 * cc);  // the chunk's phase: operand reads, contractions, result stores (across B1 and B2)
       const int h = cc & 1;
       const __bf16* Qs = Qb + h * TILE;
       const __bf16* Ss = Sb + h * TILE;
@@ -1768,6 +1774,7 @@ __global__ __launch_bounds__(1024) void aspin_delta_bwd_fused(
 #pragma unroll
         for (int db = 0; db < 4; ++db) *reinterpret_cast<bf16x4*>(dst + 16 * db) = to_bf16x4(dS[db]);
       }
+      DB_STAMP(5 + 2 * cc);
       __syncthreads();  // end of the chunk
     }
     if (dS0) {
@@ -1779,6 +1786,7 @@ __global__ __launch_bounds__(1024) void aspin_delta_bwd_fused(
   } else if (w < 8) {
     // ================= service waves: thread b carries 16-byte row segments b and b + 256 of each staged tile:
     // dO (single), then Q, S_c, K, V, X, W (into the chunk's set)
+    DB_CLOCKS(0);
     const int a = w - 4;
     const int b = tid & 255;
     constexpr int NT = 7;
@@ -1827,6 +1835,7 @@ __global__ __launch_bounds__(1024) void aspin_delta_bwd_fused(
       const __bf16* Ks = Kb + h * TILE;
       const float* Ls = vec + h * kChainVec;
       // scores, transposed: AT[t][s] = (q_s . k_t) exp(L_s - L_t), s >= t, zero below (split 2, 3, 3, 2)
+      DB_STAMP(4 + 2 * cc);
       {
         auto score = [&](int ta, int sb, const bf16x8* kf, float Lt) {
           f32x4 sc = zero4();
@@ -1854,6 +1863,7 @@ __global__ __launch_bounds__(1024) void aspin_delta_bwd_fused(
           score(0, a, kf0, Ls[i]);
         }
       }
+      DB_STAMP(5 + 2 * cc);
       __syncthreads();  // B1
       // the next chunk's tiles (loaded a chunk ago: dO is free after B1, the other sets since the end of the
       // previous chunk), then the loads of the one after (unconditional: the last ones re-read the first chunk)
@@ -2176,6 +2186,9 @@ __global__ __launch_bounds__(1024) void aspin_delta_bwd_fused(
       default: krole(std::integral_constant<int, 3>{}); break;
     }
   }
+  if (w < 8) DB_CLOCKS(2);
+#undef DB_STAMP
+#undef DB_CLOCKS
 }
 
 // The slot sums of the 128-wide backward: x[p][i] <- x[p][i] + y[p][i] for the bf16 pairs (dq, dk; the fp32 sum of
