@@ -2255,59 +2255,82 @@ bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
 // with zero values (both from the forward's state pass, all windows at once). Successive windows restart their
 // positions, so the state is rebased between them by -shift theta (key-row pairs rotated, `src/assoc.py:399-402`):
 //     S_in[0] = S0,   S_in[w + 1] = Rot(M[w] S_in[w] + R[w]).
-// One workgroup of 256 threads per (batch, head) walks the windows, fp32 throughout: thread (value column j, row
-// group rg) forms rows 16 rg .. 16 rg + 15 of column j over the 64 keys, M's rows read from LDS (the 64 lanes of a
-// wave read the same entries: broadcasts), then rotates its row pairs and writes S_in[w + 1] to memory and to LDS.
+// Four workgroups of 256 threads per (batch, head) walk the windows, fp32 throughout, each owning 16 value columns
+// (the map acts on the key rows, so the columns' chains are independent): thread (column 16 part + jl, row group rg)
+// forms rows 4 rg .. 4 rg + 3 of its column over the 64 keys, M's rows read from LDS (the 16 lanes of a row group read
+// the same entries: broadcasts), then rotates its two row pairs and writes S_in[w + 1] to memory and to LDS. Every
+// M[w] and R[w] is known before the walk, so those of the window after next are loaded into registers while this one
+// is formed (the walk waits on no memory round trip), and the products are summed in the order the one-workgroup form
+// used.
 // M, R, S_in: (BH, NW, 64, 64) fp32; S0: (BH, 64, 64) fp32 or NULL (zero).
+constexpr int kPrefixParts = 4;
+
 __global__ __launch_bounds__(256) void delta_window_prefix(const float* __restrict__ M, const float* __restrict__ R,
                                                            const float* __restrict__ S0,
                                                            const float* __restrict__ theta, float shift,
                                                            float* __restrict__ Sin, int H, int NW) {
-  __shared__ float Ss[64][65];
-  __shared__ __align__(16) float Ms[64 * 64];
-  const int bh = blockIdx.x, h = bh % H;
-  const int tid = threadIdx.x, j = tid & 63, rg = tid >> 6;
-  float sn[8], cs[8];
+  __shared__ float Ss[64][17];                // S_in[w], this part's 16 columns, key rows
+  __shared__ __align__(16) float Ms[64 * 64];  // M[w]
+  const int bh = blockIdx.x / kPrefixParts, part = blockIdx.x % kPrefixParts, h = bh % H;
+  const int tid = threadIdx.x, jl = tid & 15, rg = tid >> 4, j = 16 * part + jl;
+  float sn[2], cs[2];
 #pragma unroll
-  for (int pr = 0; pr < 8; ++pr) sincosf(-shift * theta[h * 32 + 8 * rg + pr], &sn[pr], &cs[pr]);
+  for (int pr = 0; pr < 2; ++pr) sincosf(-shift * theta[h * 32 + 2 * rg + pr], &sn[pr], &cs[pr]);
   const size_t base = (size_t)bh * NW * 4096;
-  float x[16];
+  float x[4];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    x[r] = S0 ? S0[(size_t)bh * 4096 + (16 * rg + r) * 64 + j] : 0.f;
-    Ss[16 * rg + r][j] = x[r];
-    Sin[base + (16 * rg + r) * 64 + j] = x[r];
+  for (int r = 0; r < 4; ++r) {
+    x[r] = S0 ? S0[(size_t)bh * 4096 + (4 * rg + r) * 64 + j] : 0.f;
+    Ss[4 * rg + r][jl] = x[r];
+    Sin[base + (4 * rg + r) * 64 + j] = x[r];
   }
-  for (int w = 0; w + 1 < NW; ++w) {
+  // two register sets of M and R, two windows ahead: the walk waits on no memory round trip
+  f32x4 ma[4], mb[4];
+  float ra[4], rb[4];
+  auto fetch = [&](f32x4 (&mreg)[4], float (&rreg)[4], int w) {  // M[w] (16-byte pieces) and this thread's R[w]
     const float* Mw = M + base + (size_t)w * 4096;
     const float* Rw = R + base + (size_t)w * 4096;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] = Rw[(16 * rg + r) * 64 + j];
+    for (int u = 0; u < 4; ++u) mreg[u] = *reinterpret_cast<const f32x4*>(Mw + 4 * (tid + 256 * u));
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      *reinterpret_cast<f32x4*>(Ms + 4 * (tid + 256 * u)) = *reinterpret_cast<const f32x4*>(Mw + 4 * (tid + 256 * u));
+    for (int r = 0; r < 4; ++r) rreg[r] = Rw[(4 * rg + r) * 64 + j];
+  };
+  // window w from the register set holding it, which then takes window w + 2 while this one is formed
+  auto step = [&](f32x4 (&mreg)[4], float (&rreg)[4], int w) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) *reinterpret_cast<f32x4*>(Ms + 4 * (tid + 256 * u)) = mreg[u];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = rreg[r];
+    if (w + 3 < NW) fetch(mreg, rreg, w + 2);
     __syncthreads();  // M[w] staged; S_in[w] (written at the end of the previous window) visible
-    for (int k4 = 0; k4 < 64; k4 += 4) {
-      const float s0 = Ss[k4][j], s1 = Ss[k4 + 1][j], s2 = Ss[k4 + 2][j], s3 = Ss[k4 + 3][j];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const f32x4 m = *reinterpret_cast<const f32x4*>(Ms + (16 * rg + r) * 64 + k4);
+    for (int k4 = 0; k4 < 64; k4 += 4) {
+      const float s0 = Ss[k4][jl], s1 = Ss[k4 + 1][jl], s2 = Ss[k4 + 2][jl], s3 = Ss[k4 + 3][jl];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const f32x4 m = *reinterpret_cast<const f32x4*>(Ms + (4 * rg + r) * 64 + k4);
         x[r] += m[0] * s0 + m[1] * s1 + m[2] * s2 + m[3] * s3;
       }
     }
     __syncthreads();  // every read of S_in[w] and M[w] done before they are overwritten
 #pragma unroll
-    for (int pr = 0; pr < 8; ++pr) {
+    for (int pr = 0; pr < 2; ++pr) {
       const float a = x[2 * pr], b = x[2 * pr + 1];
       x[2 * pr] = a * cs[pr] - b * sn[pr];
       x[2 * pr + 1] = a * sn[pr] + b * cs[pr];
     }
     float* dst = Sin + base + (size_t)(w + 1) * 4096;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      Ss[16 * rg + r][j] = x[r];
-      dst[(16 * rg + r) * 64 + j] = x[r];
+    for (int r = 0; r < 4; ++r) {
+      Ss[4 * rg + r][jl] = x[r];
+      dst[(4 * rg + r) * 64 + j] = x[r];
     }
+  };
+  if (NW > 1) fetch(ma, ra, 0);
+  if (NW > 2) fetch(mb, rb, 1);
+  for (int w = 0; w + 1 < NW; w += 2) {
+    step(ma, ra, w);
+    if (w + 2 < NW) step(mb, rb, w + 1);
   }
 }
 
@@ -2465,9 +2488,9 @@ extern "C" int pragnosia_aspin_delta_window_prefix(const float* M, const float* 
                                                    float shift, float* S_in, int64_t BH, int64_t H, int64_t NW,
                                                    void* stream) {
   PGN_CHECK_ARG(M && R && theta && S_in && BH > 0 && H > 0 && NW > 0 && BH % H == 0);
-  PGN_CHECK_ARG(BH < ((int64_t)1 << 31) && BH * NW < ((int64_t)1 << 40));
+  PGN_CHECK_ARG(BH * kPrefixParts < ((int64_t)1 << 31) && BH * NW < ((int64_t)1 << 40));
   PGN_CHECK_ARG(((uintptr_t)M | (uintptr_t)R) % 16 == 0);
-  hipLaunchKernelGGL(delta_window_prefix, dim3((unsigned)BH), dim3(256), 0, (hipStream_t)stream, M, R, S0, theta,
-                     shift, S_in, (int)H, (int)NW);
+  hipLaunchKernelGGL(delta_window_prefix, dim3((unsigned)(BH * kPrefixParts)), dim3(256), 0, (hipStream_t)stream, M,
+                     R, S0, theta, shift, S_in, (int)H, (int)NW);
   PGN_RETURN_LAUNCH();
 }
