@@ -2256,12 +2256,14 @@ bool shape_ok(int64_t B, int64_t H, int64_t T, int64_t D, int64_t Cc) {
 // positions, so the state is rebased between them by -shift theta (key-row pairs rotated, `src/assoc.py:399-402`):
 //     S_in[0] = S0,   S_in[w + 1] = Rot(M[w] S_in[w] + R[w]).
 // Four workgroups of 256 threads per (batch, head) walk the windows, fp32 throughout, each owning 16 value columns
-// (the map acts on the key rows, so the columns' chains are independent): thread (column 16 part + jl, row group rg)
-// forms rows 4 rg .. 4 rg + 3 of its column over the 64 keys, M's rows read from LDS (the 16 lanes of a row group read
-// the same entries: broadcasts), then rotates its two row pairs and writes S_in[w + 1] to memory and to LDS. Every
-// M[w] and R[w] is known before the walk, so those of the window after next are loaded into registers while this one
-// is formed (the walk waits on no memory round trip), and the products are summed in the order the one-workgroup form
-// used.
+// (the map acts on the key rows, so the columns' chains are independent). Wave wv forms key rows 16 wv .. 16 wv + 15
+// of the 16 columns on fp32 MFMA (v_mfma_f32_16x16x4f32: A[r][k] in lane r + 16 k, B[k][c] in lane c + 16 k,
+// D[4 g + e][c] in lane c + 16 g): lane (r, g) holds M[w]'s row 16 wv + r over keys 16 g .. 16 g + 15 in registers,
+// the s-th of them the A operand of product s, whose B operand is S_in[w]'s key row 16 g + s from LDS, so 16 products
+// over K = 4 cover the 64 keys, and R[w] is added to their sum. Each lane then rotates its two row pairs and writes
+// S_in[w + 1] to memory and to the other LDS buffer: one barrier a window, and M never passes through LDS. Every M[w]
+// and R[w] is known before the walk, so those of the window after next are loaded while this one is formed, into
+// registers read only by the products (no copy of a register still in flight, so no wait on those loads).
 // M, R, S_in: (BH, NW, 64, 64) fp32; S0: (BH, 64, 64) fp32 or NULL (zero).
 constexpr int kPrefixParts = 4;
 
@@ -2269,69 +2271,65 @@ __global__ __launch_bounds__(256) void delta_window_prefix(const float* __restri
                                                            const float* __restrict__ S0,
                                                            const float* __restrict__ theta, float shift,
                                                            float* __restrict__ Sin, int H, int NW) {
-  __shared__ float Ss[64][17];                // S_in[w], this part's 16 columns, key rows
-  __shared__ __align__(16) float Ms[64 * 64];  // M[w]
+  constexpr int P = 68;                       // LDS pitch of a column (floats)
+  __shared__ __align__(16) float St[2][16 * P];  // S_in[w] by window parity, column-major: St[c][key]
   const int bh = blockIdx.x / kPrefixParts, part = blockIdx.x % kPrefixParts, h = bh % H;
-  const int tid = threadIdx.x, jl = tid & 15, rg = tid >> 4, j = 16 * part + jl;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 15, g = lane >> 4;
+  const int j = 16 * part + c;      // value column
+  const int row0 = 16 * wv + 4 * g;  // output key rows row0 .. row0 + 3 (two rotation pairs)
   float sn[2], cs[2];
 #pragma unroll
-  for (int pr = 0; pr < 2; ++pr) sincosf(-shift * theta[h * 32 + 2 * rg + pr], &sn[pr], &cs[pr]);
+  for (int pr = 0; pr < 2; ++pr) sincosf(-shift * theta[h * 32 + row0 / 2 + pr], &sn[pr], &cs[pr]);
   const size_t base = (size_t)bh * NW * 4096;
-  float x[4];
+  f32x4 x;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    x[r] = S0 ? S0[(size_t)bh * 4096 + (4 * rg + r) * 64 + j] : 0.f;
-    Ss[4 * rg + r][jl] = x[r];
-    Sin[base + (4 * rg + r) * 64 + j] = x[r];
+  for (int e = 0; e < 4; ++e) {
+    x[e] = S0 ? S0[(size_t)bh * 4096 + (row0 + e) * 64 + j] : 0.f;
+    Sin[base + (row0 + e) * 64 + j] = x[e];
   }
-  // two register sets of M and R, two windows ahead: the walk waits on no memory round trip
-  f32x4 ma[4], mb[4];
-  float ra[4], rb[4];
-  auto fetch = [&](f32x4 (&mreg)[4], float (&rreg)[4], int w) {  // M[w] (16-byte pieces) and this thread's R[w]
-    const float* Mw = M + base + (size_t)w * 4096;
-    const float* Rw = R + base + (size_t)w * 4096;
+  *reinterpret_cast<f32x4*>(&St[0][c * P + row0]) = x;
+  if (NW < 2) return;
+  f32x4 ma[4], mb[4], ra, rb;
+  auto fetch = [&](f32x4 (&mreg)[4], f32x4& rreg, int w) {  // M[w] row 16 wv + c, keys 16 g ..; R[w] rows row0 ..
+    const float* Mw = M + base + (size_t)w * 4096 + (16 * wv + c) * 64 + 16 * g;
+    const float* Rw = R + base + (size_t)w * 4096 + row0 * 64 + j;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) mreg[u] = *reinterpret_cast<const f32x4*>(Mw + 4 * (tid + 256 * u));
+    for (int u = 0; u < 4; ++u) mreg[u] = *reinterpret_cast<const f32x4*>(Mw + 4 * u);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) rreg[r] = Rw[(4 * rg + r) * 64 + j];
+    for (int e = 0; e < 4; ++e) rreg[e] = Rw[e * 64];
   };
-  // window w from the register set holding it, which then takes window w + 2 while this one is formed
-  auto step = [&](f32x4 (&mreg)[4], float (&rreg)[4], int w) {
+  auto step = [&](f32x4 (&mreg)[4], f32x4& rreg, int w) {
+    __syncthreads();  // S_in[w] in buffer w & 1; every read of the other buffer (window w - 1) done
+    const float* Sb = &St[w & 1][c * P + 16 * g];
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 4; ++u) *reinterpret_cast<f32x4*>(Ms + 4 * (tid + 256 * u)) = mreg[u];
+    for (int u = 0; u < 4; ++u) {
+      const f32x4 b = *reinterpret_cast<const f32x4*>(Sb + 4 * u);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) x[r] = rreg[r];
-    if (w + 3 < NW) fetch(mreg, rreg, w + 2);
-    __syncthreads();  // M[w] staged; S_in[w] (written at the end of the previous window) visible
-#pragma unroll
-    for (int k4 = 0; k4 < 64; k4 += 4) {
-      const float s0 = Ss[k4][jl], s1 = Ss[k4 + 1][jl], s2 = Ss[k4 + 2][jl], s3 = Ss[k4 + 3][jl];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const f32x4 m = *reinterpret_cast<const f32x4*>(Ms + (4 * rg + r) * 64 + k4);
-        x[r] += m[0] * s0 + m[1] * s1 + m[2] * s2 + m[3] * s3;
-      }
+      for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(mreg[u][t], b[t], acc, 0, 0, 0);
     }
-    __syncthreads();  // every read of S_in[w] and M[w] done before they are overwritten
+    acc += rreg;  // after the products: R is read once they are done, two windows after its load was issued
+    // the set is refilled unconditionally (a spare load at the end) for the window after next
+    fetch(mreg, rreg, min(w + 2, NW - 1));
 #pragma unroll
     for (int pr = 0; pr < 2; ++pr) {
-      const float a = x[2 * pr], b = x[2 * pr + 1];
-      x[2 * pr] = a * cs[pr] - b * sn[pr];
-      x[2 * pr + 1] = a * sn[pr] + b * cs[pr];
+      const float a0 = acc[2 * pr], a1 = acc[2 * pr + 1];
+      x[2 * pr] = a0 * cs[pr] - a1 * sn[pr];
+      x[2 * pr + 1] = a0 * sn[pr] + a1 * cs[pr];
     }
-    float* dst = Sin + base + (size_t)(w + 1) * 4096;
+    *reinterpret_cast<f32x4*>(&St[(w + 1) & 1][c * P + row0]) = x;
+    float* dst = Sin + base + (size_t)(w + 1) * 4096 + row0 * 64 + j;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      Ss[4 * rg + r][jl] = x[r];
-      dst[(4 * rg + r) * 64 + j] = x[r];
-    }
+    for (int e = 0; e < 4; ++e) dst[e * 64] = x[e];
   };
-  if (NW > 1) fetch(ma, ra, 0);
-  if (NW > 2) fetch(mb, rb, 1);
-  for (int w = 0; w + 1 < NW; w += 2) {
+  fetch(ma, ra, 0);
+  fetch(mb, rb, min(1, NW - 1));
+  int w = 0;
+  for (; w + 2 < NW; w += 2) {
     step(ma, ra, w);
-    if (w + 2 < NW) step(mb, rb, w + 1);
+    step(mb, rb, w + 1);
   }
+  if (w + 1 < NW) step(ma, ra, w);
 }
 
 int set_smem(const void* fn, size_t bytes) { return (int)pgn_lds_limit(fn, bytes); }
