@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (17); bumped on any change of the entry points. */
+/* ABI version of this header (18); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -282,6 +282,16 @@ int pragnosia_aspin_delta_bwd(const void* q, const void* k, const void* v, const
  * carriers. */
 int pragnosia_aspin_delta_window_prefix(const float* M, const float* R, const float* S0, const float* theta,
                                         float shift, float* S_in, int64_t BH, int64_t H, int64_t NW, void* stream);
+
+/* The R and M state passes above in one launch, head dim 64, chunk 64: N sequences (N = BH NW windows, each a
+ * sequence of its own) of T tokens with q, k, v (N, T, 64) bf16, la and beta (N, T) fp32 as for
+ * pragnosia_aspin_delta_fwd. RM (2N, 64, 64) fp32 receives R (entries 0 .. N - 1: each sequence's final state from a
+ * zero entering state) then M (entries N .. 2N - 1: its final state from the identity with zero values), the inputs
+ * pragnosia_aspin_delta_window_prefix takes as R = RM and M = RM + N 64 64. One launch of 2N workgroups instead of
+ * two of N (the workgroups fill the compute units' rounds better), and neither zero values nor identity states are
+ * read from memory. Part of the same replacement of `LM.forward_carried`'s window loop (src/model.py:842-864). */
+int pragnosia_aspin_delta_window_maps(const void* q, const void* k, const void* v, const float* la,
+                                      const float* beta, float* RM, int64_t N, int64_t T, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * The plumbing between the carrier's projections and the scan (head dim D = 64): per (b, t, h) row, unit-normalise

@@ -45,6 +45,7 @@ SIGNATURES = {
     "pragnosia_aspin_delta_bwd_workspace_bytes": [_i64] * 5,
     "pragnosia_aspin_delta_bwd": [_p] * 17 + [_i64] * 6 + [_p],
     "pragnosia_aspin_delta_window_prefix": [_p] * 4 + [_f32, _p] + [_i64] * 3 + [_p],
+    "pragnosia_aspin_delta_window_maps": [_p] * 6 + [_i64] * 2 + [_p],
     "pragnosia_aspin_prep_fwd": [_p] * 9 + [_i64] * 5 + [_i32, _p],
     "pragnosia_aspin_prep_theta_partials": [_i64] * 2,
     "pragnosia_aspin_prep_bwd": [_p] * 14 + [_i64] * 5 + [_i32, _p],

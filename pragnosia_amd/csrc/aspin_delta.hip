@@ -562,7 +562,7 @@ __global__ __launch_bounds__(64 * (8 + kNIW)) void aspin_delta_fwd_inv(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ la, const float* __restrict__ be, const float* __restrict__ S0, __bf16* __restrict__ o,
     __bf16* __restrict__ Wout, float* __restrict__ Sfin, __bf16* __restrict__ sent, __bf16* __restrict__ Xout, int T,
-    int NC) {
+    int NC, int maps) {
   constexpr int KH = 1, DKEY = 64;
   constexpr int kStage = 4 * TILE;  // Q, K, V, X
   extern __shared__ __align__(16) unsigned char smem[];
@@ -573,7 +573,10 @@ __global__ __launch_bounds__(64 * (8 + kNIW)) void aspin_delta_fwd_inv(
 
   const WaveIdx x = wave_idx();
   const int w = x.w, tid = threadIdx.x;
-  const DeltaRows<KH> R(blockIdx.x);
+  // maps > 0 (the state pass of carried windows' affine maps): workgroup maps + n reruns sequence n with zero values
+  // from the identity state, so its final state is the sequence's state map, written after the first maps states
+  const bool idm = maps > 0 && (int)blockIdx.x >= maps;
+  const DeltaRows<KH> R(idm ? (int)blockIdx.x - maps : (int)blockIdx.x);
   const size_t voff = R.vals(T);
   // instrumented build: as aspin_delta_fwd's, for the chain and service waves (first buffer: per wave, clocks where
   // its role's branch starts (entries 0, 1) and at the kernel's end (2, 3), then the start and end of its phase for
@@ -590,11 +593,14 @@ __global__ __launch_bounds__(64 * (8 + kNIW)) void aspin_delta_fwd_inv(
     f32x4 S[4];
     {
       const int g = x.g, j = 16 * w + x.i;
-      const __amdgpu_buffer_rsrc_t sv = f32_view(S0 ? S0 + R.state() : nullptr, DKEY * DKEY);
+      const __amdgpu_buffer_rsrc_t sv = f32_view(S0 && !idm ? S0 + R.state() : nullptr, DKEY * DKEY);
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) S[db][r] = load_f32(sv, (16 * db + 4 * g + r) * DKEY + j);
+        for (int r = 0; r < 4; ++r) {
+          const int d = 16 * db + 4 * g + r;
+          S[db][r] = idm ? (d == j ? 1.f : 0.f) : load_f32(sv, d * DKEY + j);
+        }
     }
     for (int it = 0; it < 2 * kNIW; ++it) __syncthreads();  // the kNIW iterations that form X_0
     for (int c = 0; c < NC; ++c) {
@@ -685,10 +691,11 @@ __global__ __launch_bounds__(64 * (8 + kNIW)) void aspin_delta_fwd_inv(
     }
     {
       const int g = x.g, j = 16 * w + x.i;
+      float* const Sf = Sfin + (idm ? (size_t)maps * DKEY * DKEY : 0) + R.state();
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Sfin[R.state() + (size_t)(16 * db + 4 * g + r) * DKEY + j] = S[db][r];
+        for (int r = 0; r < 4; ++r) Sf[(size_t)(16 * db + 4 * g + r) * DKEY + j] = S[db][r];
     }
   } else if (w < 8) {
     // ================= service waves: thread b carries 16-byte row segments b and b + 256 of Q, K and V
@@ -707,8 +714,9 @@ __global__ __launch_bounds__(64 * (8 + kNIW)) void aspin_delta_fwd_inv(
         const __bf16* src = u == 0 ? q + R.rows(T) + (size_t)n0 * DKEY
                           : u == 1 ? k + R.rows(T) + (size_t)n0 * DKEY
                                    : v + voff + (size_t)n0 * DKEY;
-        sg[u][0] = load_seg(src, nr, b);
-        sg[u][1] = load_seg(src, nr, b + 256);
+        const int rows = u == 2 && idm ? 0 : nr;  // a state map's values are zero: an empty range reads zero
+        sg[u][0] = load_seg(src, rows, b);
+        sg[u][1] = load_seg(src, rows, b + 256);
       }
       pla = load_f32_lane(la + R.tok(T) + n0, nr, x.l);
       pbe = load_f32_lane(be + R.tok(T) + n0, nr, x.l);
@@ -2371,7 +2379,7 @@ int delta_fwd(const void* q, const void* k, const void* v, const float* la, cons
     if (rc) return rc;
     hipLaunchKernelGGL(aspin_delta_fwd_inv, dim3((unsigned)heads), dim3(64 * (8 + kNIW)), fwd_inv_smem(), st, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, la, beta, S0, (__bf16*)o, (__bf16*)W, S_final,
-                       (__bf16*)sent, (__bf16*)X, (int)T, NC);
+                       (__bf16*)sent, (__bf16*)X, (int)T, NC, 0);
     PGN_RETURN_LAUNCH();
   }
   hipLaunchKernelGGL(aspin_delta_inv<KH>, dim3((unsigned)(heads * NC)), dim3(256), 0, st, (const __bf16*)k, la, beta,
@@ -2480,6 +2488,19 @@ extern "C" int pragnosia_aspin_delta_bwd(const void* q, const void* k, const voi
                                 B, H, T, st)
                  : delta_bwd<2>(q, k, v, la, beta, sent, W, X, dO, dS_final, dq, dk, dv, dla, dbeta, dS0, workspace,
                                 B, H, T, st);
+}
+
+extern "C" int pragnosia_aspin_delta_window_maps(const void* q, const void* k, const void* v, const float* la,
+                                                 const float* beta, float* RM, int64_t N, int64_t T, void* stream) {
+  PGN_CHECK_ARG(shape_ok(2 * N, 1, T, DK, C));
+  PGN_CHECK_ARG(q && k && v && la && beta && RM);
+  hipStream_t st = (hipStream_t)stream;
+  const int rc = set_smem((const void*)aspin_delta_fwd_inv, fwd_inv_smem());
+  if (rc) return rc;
+  hipLaunchKernelGGL(aspin_delta_fwd_inv, dim3((unsigned)(2 * N)), dim3(64 * (8 + kNIW)), fwd_inv_smem(), st,
+                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, beta, nullptr, nullptr, nullptr, RM,
+                     nullptr, nullptr, (int)T, (int)((T + C - 1) / C), (int)N);
+  PGN_RETURN_LAUNCH();
 }
 
 extern "C" int pragnosia_aspin_delta_window_prefix(const float* M, const float* R, const float* S0, const float* theta,

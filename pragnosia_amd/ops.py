@@ -854,15 +854,17 @@ def aspin_delta_windows(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tenso
     rebased by -window * theta there: what aspin_delta over each window in turn, with aspin_rebase between, computes
     (the reference's carried windows, `src/model.py:842-864` over `src/assoc.py:391-405`), with every window at once.
     Given X the rule is linear in the state and independent per value column, so each window maps its entering state
-    affinely, S_out = M S_in + R: two state passes over all windows (R from zero entering states; M from identity
-    states with zero values), the entering states chained by `pragnosia_aspin_delta_window_prefix`, then one pass with
-    outputs from the true entering states. A partial last window runs zero-padded (zero keys, values, decay and
+    affinely, S_out = M S_in + R: the state passes over all windows (R from zero entering states; M from identity
+    states with zero values) in one launch (`pragnosia_aspin_delta_window_maps`), the entering states chained by
+    `pragnosia_aspin_delta_window_prefix`, then one pass with outputs from the true entering states. A partial last window runs zero-padded (zero keys, values, decay and
     strength leave the state unchanged). Head dim 64. S0 enters the first window. Returns (o bf16, S after the last
     window fp32, in its positions)."""
     _require_gpu(q, k, v, la, beta, S0, theta)
     _expect_scan("aspin_delta_windows", q, k, v, la, beta=beta, S0=S0, theta=theta)
     if window <= 0 or window % CHUNK:
         raise PragnosiaError(f"aspin_delta_windows: window {window} must be a positive multiple of {CHUNK}")
+    if q.shape[-1] != 64:
+        raise PragnosiaError(f"aspin_delta_windows: head dim {q.shape[-1]}; the window maps are built for 64")
     q, k, v, la, beta, S0, theta = _bf16(q), _bf16(k), _bf16(v), _f32(la), _f32(beta), _f32(S0), _f32(theta)
     B, H, T, D = q.shape
     NW = (T + window - 1) // window
@@ -873,12 +875,13 @@ def aspin_delta_windows(q: Tensor, k: Tensor, v: Tensor, la: Tensor, beta: Tenso
     BW = B * H * NW  # every window of every (batch, head) a sequence of its own: contiguous views
     qw, kw, vw = (t.view(BW, 1, window, D) for t in (q, k, v))
     lw, bw = la.view(BW, 1, window), beta.view(BW, 1, window)
-    _, R, _, _, _ = _delta_pass(qw, kw, vw, lw, bw, None, False, False)
-    eye = torch.eye(D, device=q.device, dtype=torch.float32).expand(BW, 1, D, D).contiguous()
-    _, M, _, _, _ = _delta_pass(qw, kw, torch.zeros_like(vw), lw, bw, eye, False, False)
+    RM = torch.empty(2, BW, D, D, device=q.device, dtype=torch.float32)  # R, then M: both state passes, one launch
+    check(lib().pragnosia_aspin_delta_window_maps(_ptr(qw), _ptr(kw), _ptr(vw), _ptr(lw), _ptr(bw), _ptr(RM), BW, window,
+                                                  _stream(q)), "pragnosia_aspin_delta_window_maps")
     Sin = torch.empty(BW, 1, D, D, device=q.device, dtype=torch.float32)
-    check(lib().pragnosia_aspin_delta_window_prefix(_ptr(M), _ptr(R), _ptr(S0), _ptr(theta), float(window), _ptr(Sin),
-                                                    B * H, H, NW, _stream(q)), "pragnosia_aspin_delta_window_prefix")
+    check(lib().pragnosia_aspin_delta_window_prefix(_ptr(RM[1]), _ptr(RM[0]), _ptr(S0), _ptr(theta), float(window),
+                                                    _ptr(Sin), B * H, H, NW, _stream(q)),
+          "pragnosia_aspin_delta_window_prefix")
     o, Sf, _, _, _ = _delta_pass(qw, kw, vw, lw, bw, Sin, True, False)
     o = o.view(B, H, Tp, D)[:, :, :T]
     return (o if Tp == T else o.contiguous()), Sf.view(B, H, NW, D, D)[:, :, -1].contiguous()
