@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (18); bumped on any change of the entry points. */
+/* ABI version of this header (19); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -394,6 +394,23 @@ int pragnosia_aspin_decode_proj(const float* S, float* S_out, const float* P, in
                                 const float* la_floor, const float* gate_bias, const float* beta_bias, float beta_min,
                                 const float* theta, const float* p0_dev, float p0, const float* on_weight,
                                 float on_eps, float* o, int64_t B, int64_t H, int64_t D, void* stream);
+
+/* pragnosia_aspin_decode_proj with on_weight, followed by the gated o-projection and residual, in one launch: for
+ * D = 64 (PRAGNOSIA_ERR_UNSUPPORTED otherwise) and the small batches of the GEMV decode, y (B, N) += scale *
+ * (Wo o_n) with o_n the per-head RMS-normalised step output (as pragnosia_aspin_decode_proj writes it), Wo (N, H D)
+ * row-major, scale a device scalar or NULL (1). One workgroup per (sequence, head, 64 rows of Wo) runs the head's step and adds its
+ * 64 columns' products to its rows of y with atomics: y holds the residual on entry and equals the residual plus the
+ * projection to fp32 rounding, with the heads summed in arrival order (not bit-identical from run to run). Every
+ * workgroup reads the old state, so S_out must be a different buffer from S (the new state goes there). Replaces,
+ * inside the reference's graphed decode (src/bench.py:241-317), the T = 1 path of `AssocCarrier.forward` from its
+ * projections to `x + F.linear(o, self.o.weight) * sigmoid(self.gate)` (src/assoc.py:384-512), as
+ * pragnosia_aspin_decode_proj + pragnosia_decode_gemv_rms do in two launches. */
+int pragnosia_aspin_decode_oproj(const float* S, float* S_out, const float* P, int64_t np, int64_t la_col,
+                                 int64_t gate_col, int64_t beta_col, const float* la_bias, const float* A,
+                                 const float* la_floor, const float* gate_bias, const float* beta_bias,
+                                 float beta_min, const float* theta, const float* p0_dev, float p0,
+                                 const float* on_weight, float on_eps, const float* Wo, int64_t N,
+                                 const float* scale, float* y, int64_t B, int64_t H, int64_t D, void* stream);
 
 /* One dense layer of the decode step over B sequences: y (B, N) = act(scale * (W z) + bias) + resid, with W (N, K)
  * row-major, z = LayerNorm(x) with ln_weight / ln_bias (may be NULL) / ln_eps when ln_weight is non-NULL (K <= 1024),

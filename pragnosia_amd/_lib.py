@@ -57,6 +57,8 @@ SIGNATURES = {
     "pragnosia_aspin_decode_step": [_p] * 10 + [_f32, _p] + [_i64] * 3 + [_p],
     "pragnosia_aspin_decode_proj": [_p] * 3 + [_i64] * 4 + [_p] * 5 + [_f32] + [_p] * 2 + [_f32, _p, _f32, _p]
                                    + [_i64] * 3 + [_p],
+    "pragnosia_aspin_decode_oproj": [_p] * 3 + [_i64] * 4 + [_p] * 5 + [_f32] + [_p] * 2 + [_f32, _p, _f32, _p, _i64]
+                                    + [_p] * 2 + [_i64] * 3 + [_p],
     "pragnosia_decode_gemv": [_p, _i64, _i64, _p, _p, _f32, _p, _i64, _p, _p, _i32, _p, _p, _p],
     "pragnosia_decode_gemv_rms": [_p, _i64, _i64, _p, _i64, _f32, _p, _i64, _p, _p, _i32, _p, _p, _p],
     "pragnosia_decode_tail": [_p, _i64, _i64, _p, _p, _i64, _i64] + [_p] * 5 + [_i64, _p, _p, _p, _i64, _p, _p],

@@ -148,34 +148,22 @@ __global__ __launch_bounds__(256) void aspin_decode(const float* S, float* Sout,
   }
 }
 
-// The step for D = 64 or 128 with the work of a head split over D / 16 workgroups (for latency: a one-token step is
-// short, and D / 16 workgroups per head fill the chip at small batches): workgroup (b, h, part) owns value columns
-// 16 part .. 16 part + 15, thread (jj, rg) column 16 part + jj and key rows (D / 16) rg .. (D / 16) rg + D / 16 - 1
-// (D / 32 rotation pairs). Every global load (the projections, the state slice, theta, p0, the gate parameters) is
-// issued at the start; the key-row reductions (the delta read and the output) go through LDS. The output is written
-// raw, token-major o[b][h D + j] (the per-head RMSNorm is applied by the consumer, pragnosia_decode_gemv_rms or
-// pragnosia_decode_gemm). A head's parts are numbered 8 apart, so they run on one XCD (workgroup i goes to XCD i mod
-// 8) and the 128-byte lines of the state rows they share are fetched into one L2 only.
+// The step for D = 64 or 128 with the work of a head split over D / 16 parts of 16 value columns (for latency: a
+// one-token step is short, and D / 16 workgroups per head fill the chip at small batches): thread (jj, rg) of part
+// `part` owns column 16 part + jj and key rows (D / 16) rg .. (D / 16) rg + D / 16 - 1 (D / 32 rotation pairs), holding
+// them in x (loaded by the caller first, so their latency overlaps what follows) and ending with the new state there.
+// `nt` is the thread's index within its part (the first 192 of a part's 256 threads normalise q, k and v; `norm`
+// selects the part that does), red the part's 16 x 17 LDS block. Returns the thread's share of output column j (the
+// sum over its rows of S_new[d][j] q[d]; the part's 16 row groups are added by the caller, red[.][jj] in order).
+// Every thread of the workgroup calls this (barriers inside).
 template <int DH>
-__global__ __launch_bounds__(256) void aspin_decode_split(const float* S, float* Sout, StepIn in,
-                                                          const float* __restrict__ theta,
-                                                          const float* __restrict__ p0d, float p0h,
-                                                          float* __restrict__ o, int H, int nbh) {
-  constexpr int NP = DH / 16;  // parts per head (workgroups of 16 value columns)
+PGN_DEVICE float split_step(float (&x)[DH / 16], const StepIn& in, const float* __restrict__ theta,
+                            const float* __restrict__ p0d, float p0h, int H, int b, int h, int part, int nt,
+                            bool norm, float* qs, float* ks, float* vs, float (*red)[17]) {
   constexpr int RT = DH / 16;  // key rows per thread
-  __shared__ float qs[DH], ks[DH], vs[DH];
-  __shared__ float red[16][17];
-  const int i = blockIdx.x, part = (i >> 3) % NP, bh = (i / (8 * NP)) * 8 + (i & 7);
-  if (bh >= nbh) return;  // padding of the last group of 8 heads
-  const int h = bh % H, b = bh / H;
-  const int tid = threadIdx.x, jj = tid & 15, rg = tid >> 4;
+  const int jj = nt & 15, rg = nt >> 4;
   const int j = 16 * part + jj;
   const float* prow = in.P + (size_t)b * in.np;
-  // independent loads first
-  const float* Sbh = S + (size_t)bh * DH * DH;
-  float x[RT];
-#pragma unroll
-  for (int r = 0; r < RT; ++r) x[r] = Sbh[(RT * rg + r) * DH + j];
   float th[RT / 2];
 #pragma unroll
   for (int pr = 0; pr < RT / 2; ++pr) th[pr] = theta[h * (DH / 2) + (RT / 2) * rg + pr];
@@ -188,8 +176,8 @@ __global__ __launch_bounds__(256) void aspin_decode_split(const float* S, float*
   // q, k, v unit-normalised (k also gated) by waves 0, 1, 2, D / 64 channels a lane
   constexpr int CL = DH / 64;
   float xin[CL];
-  if (tid < 3 * 64) {
-    const int vec = tid >> 6, l = tid & 63;
+  if (norm && nt < 3 * 64) {
+    const int vec = nt >> 6, l = nt & 63;
 #pragma unroll
     for (int e = 0; e < CL; ++e) xin[e] = prow[vec * H * DH + h * DH + 64 * e + l];
     float n = 0.f;
@@ -234,6 +222,33 @@ __global__ __launch_bounds__(256) void aspin_decode_split(const float* S, float*
     x[r] += ks[RT * rg + r] * wv;
     y += x[r] * qs[RT * rg + r];
   }
+  return y;
+}
+
+// The split step as D / 16 workgroups of 256 threads per head, raw output token-major o[b][h D + j] (the per-head
+// RMSNorm is applied by the consumer, pragnosia_decode_gemv_rms or pragnosia_decode_gemm). Every global load (the
+// state slice, the projections, theta, p0, the gate parameters) is issued at the start; the key-row reductions (the
+// delta read and the output) go through LDS. A head's parts are numbered 8 apart, so they run on one XCD (workgroup i
+// goes to XCD i mod 8) and the 128-byte lines of the state rows they share are fetched into one L2 only.
+template <int DH>
+__global__ __launch_bounds__(256) void aspin_decode_split(const float* S, float* Sout, StepIn in,
+                                                          const float* __restrict__ theta,
+                                                          const float* __restrict__ p0d, float p0h,
+                                                          float* __restrict__ o, int H, int nbh) {
+  constexpr int NP = DH / 16;  // parts per head (workgroups of 16 value columns)
+  constexpr int RT = DH / 16;  // key rows per thread
+  __shared__ float qs[DH], ks[DH], vs[DH];
+  __shared__ float red[16][17];
+  const int i = blockIdx.x, part = (i >> 3) % NP, bh = (i / (8 * NP)) * 8 + (i & 7);
+  if (bh >= nbh) return;  // padding of the last group of 8 heads
+  const int h = bh % H, b = bh / H;
+  const int tid = threadIdx.x, jj = tid & 15, rg = tid >> 4;
+  const int j = 16 * part + jj;
+  const float* Sbh = S + (size_t)bh * DH * DH;
+  float x[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) x[r] = Sbh[(RT * rg + r) * DH + j];
+  const float y = split_step<DH>(x, in, theta, p0d, p0h, H, b, h, part, tid, true, qs, ks, vs, red);
   red[rg][jj] = y;
   float* Sob = Sout + (size_t)bh * DH * DH;
 #pragma unroll
@@ -245,6 +260,66 @@ __global__ __launch_bounds__(256) void aspin_decode_split(const float* S, float*
     for (int g = 0; g < 16; ++g) ov += red[g][jj];
     o[(size_t)b * H * DH + h * DH + j] = ov;
   }
+}
+
+// The step, the per-head RMSNorm and this head's share of the gated o-projection in one kernel (64-wide heads, at
+// most a few sequences: the small-batch decode, where every launch is a fixed latency). Workgroup (b, h, slice) of
+// 1024 threads runs head h's step as the split step's four parts side by side (part = thread / 256, the same
+// operations: the new state is the split kernel's), sums each column's row groups, normalises the head's output
+// (nn.RMSNorm(dk), `src/assoc.py:505`), then adds scale sum_j Wo[n][64 h + j] o_n[j] to y[b][n] for the kOprojRows
+// rows n of its slice (scale: the gate's sigmoid, a device scalar): row n0 + (thread / 16), a 16-byte piece of W_o
+// per thread (loaded first, with the state), the row's 16 pieces summed by lane exchange. Every slice reads the old
+// state and slice 0 writes the new one to Sout, which must not be S. y holds the residual on entry; the heads'
+// contributions are added with atomics in the order they arrive, so y is exact to fp32 rounding in some order of the
+// heads, not the same bits from run to run.
+constexpr int kOprojRows = 64;
+
+__global__ __launch_bounds__(1024) void aspin_decode_oproj(const float* __restrict__ S, float* __restrict__ Sout,
+                                                           StepIn in, const float* __restrict__ theta,
+                                                           const float* __restrict__ p0d, float p0h,
+                                                           const float* __restrict__ on, float on_eps,
+                                                           const float* __restrict__ Wo, int N,
+                                                           const float* __restrict__ scale, float* __restrict__ y,
+                                                           int H, int NS) {
+  constexpr int RT = 4;
+  __shared__ float qs[D], ks[D], vs[D];
+  __shared__ float red[4][16][17];
+  __shared__ float onrm[D];
+  const int slice = blockIdx.x % NS, bh = blockIdx.x / NS, h = bh % H, b = bh / H;
+  const int tid = threadIdx.x, part = tid >> 8, nt = tid & 255, jj = nt & 15, rg = nt >> 4;
+  const int j = 16 * part + jj;
+  const float* Sbh = S + (size_t)bh * D * D;
+  float x[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) x[r] = Sbh[(RT * rg + r) * D + j];
+  // row n0 + tid / 16 of W_o, input columns 64 h + 4 (tid & 15) .. + 3 (rows past N read row N - 1, not added)
+  const int n = slice * kOprojRows + (tid >> 4), c4 = tid & 15;
+  const f32x4 w4 = *reinterpret_cast<const f32x4*>(Wo + (size_t)min(n, N - 1) * (H * D) + h * D + 4 * c4);
+  const float yp = split_step<D>(x, in, theta, p0d, p0h, H, b, h, part, nt, part == 0, qs, ks, vs, red[part]);
+  red[part][rg][jj] = yp;
+  if (slice == 0) {
+    float* Sob = Sout + (size_t)bh * D * D;
+#pragma unroll
+    for (int r = 0; r < RT; ++r) Sob[(RT * rg + r) * D + j] = x[r];
+  }
+  __syncthreads();
+  if (tid < 64) {  // wave 0: lane j sums column j's row groups, then the head's RMSNorm
+    const float(*rp)[17] = red[tid >> 4];
+    float ov = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) ov += rp[g][tid & 15];
+    float ss = ov * ov;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
+    const float rr = 1.f / sqrtf(ss * (1.f / D) + on_eps);
+    onrm[tid] = (ov * rr) * on[tid];
+  }
+  __syncthreads();
+  const f32x4 o4 = *reinterpret_cast<const f32x4*>(onrm + 4 * c4);
+  float acc = (w4[0] * o4[0] + w4[1] * o4[1]) + (w4[2] * o4[2] + w4[3] * o4[3]);
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off);
+  if (c4 == 0 && n < N) atomicAdd(y + (size_t)b * N + n, (scale ? *scale : 1.f) * acc);
 }
 
 // The step for many heads (large batches), raw output, D = 64 or 128: one workgroup per (batch, head) and 16-byte
@@ -409,5 +484,37 @@ extern "C" int pragnosia_aspin_decode_proj(const float* S, float* S_out, const f
   } else
     hipLaunchKernelGGL(aspin_decode<true>, dim3((unsigned)(B * H)), dim3(256), 0, (hipStream_t)stream, S, S_out, in,
                        theta, p0_dev, p0, on_weight, on_eps, o, (int)H);
+  PGN_RETURN_LAUNCH();
+}
+
+extern "C" int pragnosia_aspin_decode_oproj(const float* S, float* S_out, const float* P, int64_t np, int64_t la_col,
+                                            int64_t gate_col, int64_t beta_col, const float* la_bias, const float* A,
+                                            const float* la_floor, const float* gate_bias, const float* beta_bias,
+                                            float beta_min, const float* theta, const float* p0_dev, float p0,
+                                            const float* on_weight, float on_eps, const float* Wo, int64_t N,
+                                            const float* scale, float* y, int64_t B, int64_t H, int64_t Dh,
+                                            void* stream) {
+  if (Dh != D) return PRAGNOSIA_ERR_UNSUPPORTED;
+  PGN_CHECK_ARG(B > 0 && H > 0 && N > 0);
+  PGN_CHECK_ARG(S && S_out && S != S_out && P && la_bias && A && theta && on_weight && Wo && y);
+  PGN_CHECK_ARG(!(gate_col >= 0 && beta_col >= 0));
+  PGN_CHECK_ARG(la_col >= 3 * H * Dh && la_col + H <= np && gate_col + H <= np && beta_col + H <= np);
+  const int64_t NS = (N + kOprojRows - 1) / kOprojRows;
+  PGN_CHECK_ARG(B * H * NS < ((int64_t)1 << 31) && N * H * Dh < ((int64_t)1 << 31) && B * N < ((int64_t)1 << 31));
+  PGN_CHECK_ARG((uintptr_t)Wo % 16 == 0);
+  StepIn in{};
+  in.P = P;
+  in.np = (int)np;
+  in.la_col = (int)la_col;
+  in.gate_col = (int)gate_col;
+  in.beta_col = (int)beta_col;
+  in.la_b = la_bias;
+  in.A = A;
+  in.floor = la_floor;
+  in.gate_b = gate_bias;
+  in.beta_b = beta_bias;
+  in.beta_min = beta_min;
+  hipLaunchKernelGGL(aspin_decode_oproj, dim3((unsigned)(B * H * NS)), dim3(1024), 0, (hipStream_t)stream, S, S_out,
+                     in, theta, p0_dev, p0, on_weight, on_eps, Wo, (int)N, scale, y, (int)H, (int)NS);
   PGN_RETURN_LAUNCH();
 }

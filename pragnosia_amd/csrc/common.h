@@ -107,6 +107,32 @@ PGN_DEVICE float pgn_exp(float x) { return __expf(x); }
 // GELU, erf form (torch's default F.gelu): 0.5 x (1 + erf(x / sqrt 2)).
 PGN_DEVICE float pgn_gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
 
+// Sum over the 64 lanes of a wave of NV values per lane (NV a power of two <= 16): the lanes exchange halves, so the
+// sums take 6 + NV - 1 exchanges instead of 6 NV. Lane l ends with the sum of value l >> (6 - log2 NV) in v[0].
+template <int NV>
+PGN_DEVICE void wave_sum_many(float (&v)[NV], int l) {
+  int len = NV;
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    if (len > 1) {
+      const int half = len / 2;
+      const bool hi = (l & s) != 0;
+#pragma unroll
+      for (int m = 0; m < half; ++m) {
+        const float send = hi ? v[m] : v[m + half];
+        const float keep = hi ? v[m + half] : v[m];
+        v[m] = keep + __shfl_xor(send, s);
+      }
+      len = half;
+    } else {
+      v[0] += __shfl_xor(v[0], s);
+    }
+  }
+}
+
+template <int NV>
+constexpr int log2_of() { return NV == 1 ? 0 : NV == 2 ? 1 : NV == 4 ? 2 : NV == 8 ? 3 : 4; }
+
 // sin and cos of x. The hardware sine/cosine (through __sincosf) take the argument in revolutions: scaling x to
 // revolutions in fp32 costs about |x| * 2^-24 rad of absolute angle error, so they are used for |x| < 64 rad (at
 // most ~4e-6 rad; measured 1.3e-6 relative on the diagonal scan's outputs for angles in [-pi, pi]) and the precise

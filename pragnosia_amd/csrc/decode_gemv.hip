@@ -139,32 +139,6 @@ __global__ __launch_bounds__(256) void gemv(const float* __restrict__ x, int B, 
   }
 }
 
-// Sum over the 64 lanes of a wave of NV values per lane (NV a power of two <= 16): the lanes exchange halves, so the
-// sums take 6 + NV - 1 exchanges instead of 6 NV. Lane l ends with the sum of value l >> (6 - log2 NV) in v[0].
-template <int NV>
-PGN_DEVICE void wave_sum_many(float (&v)[NV], int l) {
-  int len = NV;
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) {
-    if (len > 1) {
-      const int half = len / 2;
-      const bool hi = (l & s) != 0;
-#pragma unroll
-      for (int m = 0; m < half; ++m) {
-        const float send = hi ? v[m] : v[m + half];
-        const float keep = hi ? v[m + half] : v[m];
-        v[m] = keep + __shfl_xor(send, s);
-      }
-      len = half;
-    } else {
-      v[0] += __shfl_xor(v[0], s);
-    }
-  }
-}
-
-template <int NV>
-constexpr int log2_of() { return NV == 1 ? 0 : NV == 2 ? 1 : NV == 4 ? 2 : NV == 8 ? 3 : 4; }
-
 // The decode GEMV for B <= 4 sequences and K = 256 KV: one wave per RPW output rows (a one-wave workgroup, so
 // hundreds to thousands of them cover the chip and one round of loads covers the whole weight). Lane l reads the
 // 16-byte pieces 4 l + 256 u of each of its rows, so one load instruction reads 1 KiB contiguous; all RPW KV pieces

@@ -3,7 +3,7 @@
 // modulo the position table, the next input x = tok_emb[tok] + pos_emb[pos]), plus this build's per-step device state
 // (the generated-token buffer and its row counter, the carried states' position offsets reset to 1).
 //
-// One workgroup of 256 threads per sequence b:
+// One workgroup of 1024 threads per sequence b:
 //   tok = argmax_v logits[b][v] (the first index among equal maxima, NaN above every number: torch.argmax's rule),
 //   out[c][b] = tok (c = *ctr_in, row c of the generated-token buffer, skipped past its n_rows), tok_out[b] = tok,
 //   p = (*pos_in + 1) mod ctx, h[b] = emb[tok] + pemb[p] (fp32, one add per element as torch's),
@@ -23,29 +23,49 @@ PGN_DEVICE bool better(float av, int ai, float bv, int bi) {
   return av > bv || (av == bv && ai < bi);
 }
 
-__global__ __launch_bounds__(256) void decode_tail(const float* __restrict__ logits, int V,
-                                                   const float* __restrict__ emb, const float* __restrict__ pemb,
-                                                   int d, int ctx, const int64_t* __restrict__ ctr_in,
-                                                   int64_t* __restrict__ ctr_out, const int64_t* __restrict__ pos_in,
-                                                   int64_t* __restrict__ pos_out, int64_t* __restrict__ out,
-                                                   int64_t n_rows, int64_t* __restrict__ tok_out,
-                                                   float* __restrict__ h, float* __restrict__ p0s, int L,
-                                                   float* __restrict__ lrec, int B) {
-  __shared__ float bv_s[4];
-  __shared__ int bi_s[4];
+constexpr int kTailThreads = 1024;
+constexpr int kTailLoads = 8;  // logits a thread loads before it compares any: one memory round trip per 8192
+
+__global__ __launch_bounds__(kTailThreads) void decode_tail(const float* __restrict__ logits, int V,
+                                                            const float* __restrict__ emb,
+                                                            const float* __restrict__ pemb, int d, int ctx,
+                                                            const int64_t* __restrict__ ctr_in,
+                                                            int64_t* __restrict__ ctr_out,
+                                                            const int64_t* __restrict__ pos_in,
+                                                            int64_t* __restrict__ pos_out, int64_t* __restrict__ out,
+                                                            int64_t n_rows, int64_t* __restrict__ tok_out,
+                                                            float* __restrict__ h, float* __restrict__ p0s, int L,
+                                                            float* __restrict__ lrec, int B) {
+  constexpr int NW = kTailThreads / 64;
+  __shared__ float bv_s[NW];
+  __shared__ int bi_s[NW];
   __shared__ int tok_s;
   const int b = blockIdx.x, tid = threadIdx.x, l = tid & 63, w = tid >> 6;
   const float* row = logits + (size_t)b * V;
   const int64_t c = *ctr_in;
+  const bool rec = lrec && c < n_rows;
   float bv = 0.f;
   int bi = -1;
-  for (int v = tid; v < V; v += 256) {
-    const float x = row[v];
-    if (bi < 0 || better(x, v, bv, bi)) {
-      bv = x;
-      bi = v;
+  // kTailLoads logits a thread (v = v0 + tid + kTailThreads u), all loaded before any comparison, so a pass over
+  // kTailThreads kTailLoads logits costs one memory round trip; each thread keeps the better of its values
+  for (int v0 = 0; v0 < V; v0 += kTailThreads * kTailLoads) {
+    float xs[kTailLoads];
+#pragma unroll
+    for (int u = 0; u < kTailLoads; ++u) {
+      const int v = v0 + tid + kTailThreads * u;
+      xs[u] = v < V ? row[v] : 0.f;
     }
-    if (lrec && c < n_rows) lrec[((size_t)c * B + b) * V + v] = x;
+#pragma unroll
+    for (int u = 0; u < kTailLoads; ++u) {
+      const int v = v0 + tid + kTailThreads * u;
+      if (v < V) {
+        if (bi < 0 || better(xs[u], v, bv, bi)) {
+          bv = xs[u];
+          bi = v;
+        }
+        if (rec) lrec[((size_t)c * B + b) * V + v] = xs[u];
+      }
+    }
   }
   // wave, then workgroup: (value, index) pairs, the better one kept
 #pragma unroll
@@ -63,7 +83,7 @@ __global__ __launch_bounds__(256) void decode_tail(const float* __restrict__ log
   }
   __syncthreads();
   if (tid == 0) {
-    for (int u = 1; u < 4; ++u)
+    for (int u = 1; u < NW; ++u)
       if (bi_s[u] >= 0 && (bi < 0 || better(bv_s[u], bi_s[u], bv, bi))) {
         bv = bv_s[u];
         bi = bi_s[u];
@@ -78,13 +98,13 @@ __global__ __launch_bounds__(256) void decode_tail(const float* __restrict__ log
   const float* er = emb + (size_t)t * d;
   const float* pr = pemb + (size_t)p * d;
   float* hr = h + (size_t)b * d;
-  for (int k = tid; k < d; k += 256) hr[k] = er[k] + pr[k];
+  for (int k = tid; k < d; k += kTailThreads) hr[k] = er[k] + pr[k];
   if (b == 0) {
     if (tid == 0) {
       *pos_out = p;
       *ctr_out = c + 1;
     }
-    for (int k = tid; k < L; k += 256) p0s[k] = 1.f;
+    for (int k = tid; k < L; k += kTailThreads) p0s[k] = 1.f;
   }
 }
 
@@ -96,11 +116,11 @@ extern "C" int pragnosia_decode_tail(const float* logits, int64_t B, int64_t V, 
                                      int64_t* tok, float* h, float* p0s, int64_t L, float* logits_rec, void* stream) {
   PGN_CHECK_ARG(logits && emb && pemb && ctr_in && ctr_out && pos_in && pos_out && out && tok && h);
   PGN_CHECK_ARG(B > 0 && V > 0 && d > 0 && ctx > 0 && n_rows > 0 && L >= 0 && (L == 0 || p0s));
-  PGN_CHECK_ARG(B < (1 << 20) && V < ((int64_t)1 << 31) && d < (1 << 30) && ctx < (1 << 30) && L < (1 << 30));
+  PGN_CHECK_ARG(B < (1 << 20) && V < ((int64_t)1 << 30) && d < (1 << 30) && ctx < (1 << 30) && L < (1 << 30));
   PGN_CHECK_ARG(B * V < ((int64_t)1 << 40) && n_rows * B * V < ((int64_t)1 << 62));
   PGN_CHECK_ARG(ctr_in != ctr_out && pos_in != pos_out);
-  hipLaunchKernelGGL(decode_tail, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, logits, (int)V, emb, pemb,
-                     (int)d, (int)ctx, ctr_in, ctr_out, pos_in, pos_out, out, n_rows, tok, h, p0s, (int)L, logits_rec,
-                     (int)B);
+  hipLaunchKernelGGL(decode_tail, dim3((unsigned)B), dim3(kTailThreads), 0, (hipStream_t)stream, logits, (int)V, emb,
+                     pemb, (int)d, (int)ctx, ctr_in, ctr_out, pos_in, pos_out, out, n_rows, tok, h, p0s, (int)L,
+                     logits_rec, (int)B);
   PGN_RETURN_LAUNCH();
 }

@@ -233,12 +233,25 @@ class GreedyDecoder:
         m, op = self.m, torch.ops.pragnosia
         h = self.h
         for i, (mx, mp) in enumerate(zip(m.mix, m.mlp)):
-            # at small batches the per-head RMSNorm moves into the o-projection's GEMV, so the carrier step can run
-            # dk / 16 workgroups per head (always so for 128-dim heads, whose step writes only the raw output)
-            rms_in_gemv = self.B <= GEMV_MAX_BATCH and _rms_gemv_ok(mx.h * mx.dk)
             gated = not (mx.delta or mx.write_all)
             P = self._dense(h, self.wcat[i], mx.ln)
             on_eps = mx.on.eps if mx.on.eps is not None else torch.finfo(torch.float32).eps
+            if self.st2[i] is not None:
+                # 64-wide heads at small batches: the step, the per-head RMSNorm and the gated o-projection in one
+                # launch, added into h in place (h becomes x1); the state alternates between two buffers by step
+                # parity (every workgroup of a head reads the old state), ending in st[i][0] after an even count
+                src, dst = (self.st[i][0], self.st2[i]) if par == 0 else (self.st2[i], self.st[i][0])
+                op.aspin_decode_oproj_(src, dst, P, mx.h, mx.wa.bias, mx.A, mx.la_floor if mx.hl_floor else None,
+                                       mx.wi.bias if gated else None, mx.wb.bias if mx.delta else None,
+                                       0.75 if (mx.delta and mx.write_all) else 0.0, gated, mx.theta,
+                                       self.p0s[i:i + 1], 0.0, mx.on.weight, on_eps, mx.o.weight, self.sig[i], h)
+                x1 = h
+                hm = self._dense(x1, mp.a.weight, mp.n, bias=mp.a.bias, act=1)
+                h = self._dense(hm, mp.b.weight, None, bias=mp.b.bias, resid=x1)
+                continue
+            # at small batches the per-head RMSNorm moves into the o-projection's GEMV, so the carrier step can run
+            # dk / 16 workgroups per head (always so for 128-dim heads, whose step writes only the raw output)
+            rms_in_gemv = self.B <= GEMV_MAX_BATCH and _rms_gemv_ok(mx.h * mx.dk)
             o = op.aspin_decode_proj_(self.st[i][0], P, mx.h, mx.wa.bias, mx.A,
                                       mx.la_floor if mx.hl_floor else None, mx.wi.bias if gated else None,
                                       mx.wb.bias if mx.delta else None, 0.75 if (mx.delta and mx.write_all) else 0.0,
@@ -261,6 +274,10 @@ class GreedyDecoder:
             self.gemm = self._gemm_ok()
             self._fused_weights()
             self.p0s = torch.stack([st[1].reshape(()) for st in self.st]).float().contiguous()
+            # the one-launch step + o-projection (64-wide heads, GEMV batch sizes) writes the new state to a second
+            # buffer, the two swapping roles every step
+            self.st2 = [torch.empty_like(st[0]) if (not self.gemm and self.B <= GEMV_MAX_BATCH and mx.dk == 64)
+                        else None for st, mx in zip(self.st, self.m.mix)]
         self.tok = torch.zeros(self.B, 1, dtype=torch.long, device=dev)
         self.pos = torch.zeros(1, dtype=torch.long, device=dev)
         self.out = torch.zeros(n_max + self.K, self.B, dtype=torch.long, device=dev)

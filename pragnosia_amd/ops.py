@@ -1594,3 +1594,47 @@ def aspin_decode_proj_(S: Tensor, P: Tensor, H: int, la_bias: Tensor, A: Tensor,
 @aspin_decode_proj_.register_fake
 def _(S, P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, p0_dev, p0, on_weight, on_eps):
     return P.new_empty(P.shape[0], H * S.shape[-1], dtype=torch.float32)
+
+
+@torch.library.custom_op("pragnosia::aspin_decode_oproj_", mutates_args=("S_out", "y"))
+def aspin_decode_oproj_(S: Tensor, S_out: Tensor, P: Tensor, H: int, la_bias: Tensor, A: Tensor,
+                        la_floor: Optional[Tensor], gate_bias: Optional[Tensor], beta_bias: Optional[Tensor],
+                        beta_min: float, gated: bool, theta: Tensor, p0_dev: Optional[Tensor], p0: float,
+                        on_weight: Tensor, on_eps: float, Wo: Tensor, scale: Optional[Tensor], y: Tensor) -> None:
+    """aspin_decode_proj_ with the per-head RMSNorm, then the gated o-projection and residual, in one launch (64-wide
+    heads): reads the carried state S (B, H, 64, 64), writes the new state to S_out (a different buffer: every
+    workgroup reads the old state) and adds scale * (Wo o_n) to y (B, N), which holds the residual on entry; Wo (N,
+    H 64), scale a one-element tensor (the gate's sigmoid) or None. The heads' contributions are added with atomics in
+    arrival order: y equals the two-launch result to fp32 rounding, not bit for bit, and not the same bits from run
+    to run."""
+    _require_gpu(S, S_out, P, la_bias, A, theta, on_weight, Wo, scale, y)
+    for name, t in (("S", S), ("S_out", S_out), ("y", y)):
+        if not (t.is_contiguous() and t.dtype == torch.float32):
+            raise PragnosiaError(f"aspin_decode_oproj_: {name} must be a contiguous fp32 tensor")
+    if P.dim() != 2:
+        raise PragnosiaError(f"aspin_decode_oproj_: P must be (B, W), got {tuple(P.shape)}")
+    if S.data_ptr() == S_out.data_ptr():
+        raise PragnosiaError("aspin_decode_oproj_: S_out must be another buffer than S")
+    B = P.shape[0]
+    N = Wo.shape[0] if Wo.dim() == 2 else -1
+    _expect_proj("aspin_decode_oproj_", P, H, gated, la_bias, A, la_floor, gate_bias, beta_bias, theta, D=64)
+    _expect("aspin_decode_oproj_", P.device, S=(S, (B, H, 64, 64)), S_out=(S_out, (B, H, 64, 64)),
+            p0_dev=(p0_dev, ()), on_weight=(on_weight, (64,)), Wo=(Wo, (N, H * 64)), y=(y, (B, N)),
+            scale=(scale, ()))
+    P, la_bias, A, la_floor, theta = _f32(P), _f32(la_bias), _f32(A), _f32(la_floor), _f32(theta)
+    gate_bias, beta_bias, p0_dev, on_weight = _f32(gate_bias), _f32(beta_bias), _f32(p0_dev), _f32(on_weight)
+    Wo, scale = _f32(Wo), _f32(scale)
+    np_ = P.shape[1]
+    has_beta = not gated and np_ > 3 * H * 64 + H
+    acol, gcol, bcol = _proj_cols(H, gated, has_beta, 64)
+    check(lib().pragnosia_aspin_decode_oproj(_ptr(S), _ptr(S_out), _ptr(P), np_, acol, gcol, bcol, _ptr(la_bias),
+                                             _ptr(A), _ptr(la_floor), _ptr(gate_bias), _ptr(beta_bias),
+                                             float(beta_min), _ptr(theta), _ptr(p0_dev), float(p0), _ptr(on_weight),
+                                             float(on_eps), _ptr(Wo), N, _ptr(scale), _ptr(y), B, H, 64, _stream(P)),
+          "pragnosia_aspin_decode_oproj")
+
+
+@aspin_decode_oproj_.register_fake
+def _(S, S_out, P, H, la_bias, A, la_floor, gate_bias, beta_bias, beta_min, gated, theta, p0_dev, p0, on_weight,
+      on_eps, Wo, scale, y):
+    return None

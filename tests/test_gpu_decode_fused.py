@@ -52,7 +52,11 @@ def test_decode_gemv_matches_torch(B, K, N, ln, act, res):
                                                       (True, False, False), (True, True, True)])
 def test_decode_proj_matches_module_step(delta, write_all, hl_floor):
     """One carrier step through the projection GEMV + the fused step kernel against the module's T = 1 path (its
-    projections, aspin_decode_step, nn.RMSNorm), from a rebased carried state, twice in a row (in-place state)."""
+    projections, aspin_decode_step, nn.RMSNorm), from a rebased carried state, twice in a row (in-place state). Also
+    the step with the o-projection in the same launch (aspin_decode_oproj_, state into the other of two buffers,
+    output added into the residual with atomics): its new state bit-identical to the split step's (the raw-output
+    aspin_decode_proj_: the same operations), its output within 1e-5 of the two-launch result (the heads summed in
+    another order)."""
     from pragnosia_amd.assoc import AssocCarrier
     op = torch.ops.pragnosia
     torch.manual_seed(3)
@@ -63,6 +67,7 @@ def test_decode_proj_matches_module_step(delta, write_all, hl_floor):
         B = 3
         S = torch.randn(B, 4, 64, 64, device="cuda") * 0.1
         S_f, S_r = S.clone(), S.clone()
+        S_o = [S.clone(), torch.full_like(S, float("nan"))]  # the one-launch form's two state buffers
         p0 = torch.tensor([7.0], device="cuda")
         gated = not (delta or write_all)
         extra = [m.wi.weight] if gated else ([m.wb.weight] if delta else [])
@@ -85,7 +90,15 @@ def test_decode_proj_matches_module_step(delta, write_all, hl_floor):
                                         torch.finfo(torch.float32).eps)
             y_r = op.decode_gemv_rms(o_r, m.o.weight, m.on.weight, torch.finfo(torch.float32).eps, None,
                                      torch.sigmoid(m.gate).reshape(1), 0, x.reshape(B, 256))
+            y_o = x.reshape(B, 256).clone()
+            op.aspin_decode_oproj_(S_o[step % 2], S_o[1 - step % 2], P, 4, m.wa.bias, m.A,
+                                   m.la_floor if hl_floor else None, m.wi.bias if gated else None,
+                                   m.wb.bias if delta else None, 0.75 if (delta and write_all) else 0.0, gated,
+                                   m.theta, p0, 0.0, m.on.weight, torch.finfo(torch.float32).eps, m.o.weight,
+                                   torch.sigmoid(m.gate).reshape(1), y_o)
             p0.fill_(1.0)
+            assert torch.equal(S_o[1 - step % 2], S_r), step
+            assert rel(y_o - x.reshape(B, 256), y_f - x.reshape(B, 256)) < 1e-5, step
             assert rel(y_f - x.reshape(B, 256), y_mod.reshape(B, 256) - x.reshape(B, 256)) < 1e-4, step
             assert rel(S_f, st[0]) < 1e-4, step
             assert rel(y_r - x.reshape(B, 256), y_mod.reshape(B, 256) - x.reshape(B, 256)) < 1e-4, step

@@ -196,6 +196,32 @@ def test_delta_carried_windows_equal_one_pass(delta):
     assert rel(torch.cat([a, b], 2), y) < TOL_OUT and rel(Sb, S) < TOL_OUT
 
 
+@pytest.mark.parametrize("N,T", [(5, 192), (3, 130)])
+def test_delta_window_maps_equal_state_passes(delta, N, T):
+    """pragnosia_aspin_delta_window_maps (through the C ABI) writes, for N sequences, R (the final state from a zero
+    entering state) then M (from the identity with zero values) in one launch: bit-identical to the forward's state
+    pass run twice, once with no entering state and once with identity states and a zero value tensor (the same
+    kernel and the same operations, the identity and the zero values formed on chip instead of read). Also M's meaning
+    on a ragged length: M S0 + R is the final state from S0, to the scan's tolerance."""
+    from pragnosia_amd._lib import lib, check
+    q, k, v, la, be, S0 = _inputs(1, N, T, 64, seed=17)
+    q, k, v = (t.cuda().bfloat16().contiguous() for t in (q, k, v))
+    la, be, S0 = (t.cuda().float().contiguous() for t in (la, be, S0))
+    RM = torch.full((2, N, 64, 64), float("nan"), device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    check(lib().pragnosia_aspin_delta_window_maps(q.data_ptr(), k.data_ptr(), v.data_ptr(), la.data_ptr(),
+                                                  be.data_ptr(), RM.data_ptr(), N, T, st),
+          "pragnosia_aspin_delta_window_maps")
+    with torch.no_grad():
+        _, R, *_ = delta(q, k, v, la, be, None, False)
+        eye = torch.eye(64, device="cuda").expand(1, N, 64, 64).contiguous()
+        _, M, *_ = delta(q, k, torch.zeros_like(v), la, be, eye, False)
+        _, S, *_ = delta(q, k, v, la, be, S0, False)
+    torch.cuda.synchronize()
+    assert torch.equal(RM[0], R[0]) and torch.equal(RM[1], M[0])
+    assert rel(RM[1] @ S0[0] + RM[0], S[0]) < TOL_OUT
+
+
 # ---- head dim 128 (the reference's hdspin / sdspin / tspin / aspin1 carriers, `src/model.py:651-660`): each head runs
 # as two scans over its value halves sharing X; dq, dk, dla and dbeta are the sums of the two scans' parts.
 @pytest.mark.parametrize("T,s0", [(64, False), (200, True), (1, True), (130, True)])
