@@ -104,6 +104,9 @@ def _samples():
                                 th, torch.tensor(1.0, device=dev), 0.0, 1 + 0.1 * r(64), 1e-6)),
         ("aspin_decode_proj_", (r(B, H, D, D), r(B, 3 * H * D + 2 * H), H, r(H), r(H), None, r(H), None, 0.0, True,
                                 th, torch.tensor(1.0, device=dev), 0.0, None, 1e-6)),
+        ("aspin_decode_oproj_", (r(B, H, D, D), r(B, H, D, D), r(B, 3 * H * D + 2 * H), H, r(H), r(H), None, r(H),
+                                 None, 0.0, True, th, torch.tensor(1.0, device=dev), 0.0, 1 + 0.1 * r(64), 1e-6,
+                                 r(100, H * D), r(1), r(B, 100))),
         ("decode_gemv_rms", (r(3, 256), r(50, 256), 1 + 0.1 * r(64), 1e-6, r(50), r(1), 1, r(3, 50))),
         ("decode_gemm", (r(20, 256), r(64 * 256), 50, 1, r(50), 1e-5, r(50), None, 1, r(20, 50))),
         ("decode_gemm", (r(20, 256), r(64 * 256), 50, 2, None, 1e-6, None, r(1), 0, None)),
