@@ -9,10 +9,12 @@
 //
 // At 64 sequences every weight element is used 64 times a step (32 flop per byte read), so the fp32 matrix-core rate
 // matters as much as HBM, and at these sizes a workgroup's own latency (its loads, then its products, then its
-// reduction) sets the kernel's time. Work split: a workgroup owns 16 output columns (one column tile) of 16 rows (one
-// row block), all of K: its KW waves (at most 16) split K into 16-wide steps, S consecutive steps a chunk and C chunks
-// a wave. So a layer at 64 rows is 4 x ceil(N / 16) workgroups; those of one column tile are numbered 8 apart, so
-// they run on one XCD (workgroup i goes to XCD i mod 8) and read the tile's weight from one L2. A wave issues its
+// reduction) sets the kernel's time. Work split: a workgroup owns NC column tiles of 16 output columns (NC = 1, or 3
+// where that still leaves 192 workgroups: each input piece then feeds three products, a third fewer operand bytes
+// per CU from L2) of 16 rows (one row block), all of K: its KW waves (at most 16) split K into 16-wide steps, S
+// consecutive steps a chunk and C chunks a wave. So a layer at 64 rows is 4 x ceil(N / 16 NC) workgroups; those of
+// one column group are numbered 8 apart, so they run on one XCD (workgroup i goes to XCD i mod 8) and read the
+// group's weight from one L2. A wave issues its
 // first chunk's loads before any product and each next chunk's loads before the current chunk's products (register
 // double buffering): S weight pieces, each one contiguous 1 KiB, and S input pieces. The weight (N, K) comes
 // pre-tiled: Wt[((t KS + s) 64 + l) 4 + e] = W[16 t + l % 16][16 s + 4 (l / 16) + e] for column tile t, 16-wide step
@@ -35,7 +37,7 @@ namespace {
 
 constexpr int MAXW = 16;  // waves per workgroup
 
-template <int S, int C, int MODE>
+template <int S, int C, int MODE, int NC>
 __global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ x, int B, int K,
                                                       const float* __restrict__ csum, float eps,
                                                       const float* __restrict__ Wt, int N, int NT, int ZB,
@@ -43,28 +45,32 @@ __global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ 
                                                       const float* __restrict__ scale, int act,
                                                       const float* __restrict__ resid, float* __restrict__ y) {
   static_assert(MODE != 2 || C == 1, "the RMS mode holds one channel group per wave");
-  __shared__ __align__(16) float red[MAXW * 256];
+  __shared__ __align__(16) float red[NC * MAXW * 256];
   __shared__ float2 stat[MAXW][16];
   const int KW = blockDim.x >> 6;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, r16 = l & 15, k4 = l >> 4;
-  // workgroup i -> (column tile, row block): the ZB row blocks of a tile are 8 apart (one XCD)
+  // workgroup i -> (column group of NC tiles, row block): the ZB row blocks of a group are 8 apart (one XCD)
   const int i = blockIdx.x;
-  const int nt = (i / (8 * ZB)) * 8 + (i & 7), zb = (i >> 3) % ZB;
-  if (nt >= NT) return;  // padding workgroups of the last group of 8 tiles
+  const int ng = (i / (8 * ZB)) * 8 + (i & 7), zb = (i >> 3) % ZB;
+  if (ng * NC >= NT) return;  // padding workgroups of the last group of 8
+  const int nt0 = ng * NC;    // the group's first column tile
   const int KS = K >> 4;
   const int s0 = w * S * C;  // the wave's first 16-wide step
   const int row = 16 * zb + r16;
   const bool live = row < B;
   const float* xrow = x + (size_t)min(row, B - 1) * K;
   const float* xr = xrow + 16 * s0 + 4 * k4;
-  const float* wp = Wt + ((size_t)nt * KS + s0) * 256 + 4 * l;
+  const float* wp[NC];  // tiles past the last are read from the last one and not written
+#pragma unroll
+  for (int t = 0; t < NC; ++t) wp[t] = Wt + ((size_t)min(nt0 + t, NT - 1) * KS + s0) * 256 + 4 * l;
 
-  f32x4 wv[2][S], z[2][S];
+  f32x4 wv[2][S][NC], z[2][S];
   auto load = [&](int c, int b) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      wv[b][s] = *reinterpret_cast<const f32x4*>(wp + 256 * (c * S + s));
+#pragma unroll
+      for (int t = 0; t < NC; ++t) wv[b][s][t] = *reinterpret_cast<const f32x4*>(wp[t] + 256 * (c * S + s));
       const f32x4 v = *reinterpret_cast<const f32x4*>(xr + 16 * (c * S + s));
       z[b][s] = live ? v : f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -73,8 +79,13 @@ __global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ 
   // cancellation against mean * csum at the size of the row's spread); the row's moments are formed beside them
   const float x0 = MODE == 1 && live ? xrow[0] : 0.f;
   load(0, 0);
+  // three tiles a workgroup run one workgroup a compute unit (two waves a SIMD): every load of the first chunk is
+  // kept ahead of the products, so the wave's whole operand stream is in flight at once
+  if constexpr (NC > 1) __builtin_amdgcn_sched_barrier(0);
   float mw = 0.f, m2w = 0.f;  // this wave's mean and sum of squared deviations of the row (LayerNorm mode)
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[NC];
+#pragma unroll
+  for (int t = 0; t < NC; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     if (c + 1 < C) load(c + 1, (c + 1) & 1);
@@ -129,20 +140,25 @@ __global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ 
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(z[b][s][e], wv[b][s][e], acc, 0, 0, 0);
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int t = 0; t < NC; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(z[b][s][e], wv[b][s][t][e], acc[t], 0, 0, 0);
   }
 
   // wave partials (and the LayerNorm moments) through LDS; output v = 16 i + c (row i, column c of the block) sits
   // in lane c + 16 (i / 4), entry i % 4
-  *reinterpret_cast<f32x4*>(red + w * 256 + 4 * l) = acc;
+#pragma unroll
+  for (int t = 0; t < NC; ++t) *reinterpret_cast<f32x4*>(red + (t * KW + w) * 256 + 4 * l) = acc[t];
   if (MODE == 1 && k4 == 0) stat[w][r16] = float2{mw, m2w};
   __syncthreads();
-  for (int v = threadIdx.x; v < 256; v += blockDim.x) {  // a workgroup of fewer than 4 waves takes two rounds
-    const int ri = v >> 4, cc = v & 15;
+  for (int v = threadIdx.x; v < 256 * NC; v += blockDim.x) {  // fewer than 4 NC waves take more rounds
+    const int tt = v >> 8, ri = (v >> 4) & 15, cc = v & 15;
     const int src = 4 * (cc + 16 * (ri >> 2)) + (ri & 3);
+    const float* rt = red + tt * KW * 256;
     float t = 0.f;
-    for (int u = 0; u < KW; ++u) t += red[u * 256 + src];
-    const int orow = 16 * zb + ri, col = 16 * nt + cc;
+    for (int u = 0; u < KW; ++u) t += rt[u * 256 + src];
+    const int orow = 16 * zb + ri, col = 16 * (nt0 + tt) + cc;
     if (orow < B && col < N) {
       if constexpr (MODE == 1) {
         // the row's mean (of x - x0) and variance from the waves' pairs in wave order (equal counts); the products
@@ -198,14 +214,29 @@ bool make_plan(int64_t K, int mode, Plan& p) {
   return false;
 }
 
+template <int S, int C, int MODE, int NC>
+int launch_nc(const Plan& p, const float* x, int B, int K, const float* csum, float eps, const float* Wt, int N,
+              const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
+  const int NT = (N + 15) / 16, ZB = (B + 15) / 16;
+  const int64_t groups = ((NT + NC - 1) / NC + 7) / 8;  // column groups in sets of 8, each set's ZB row blocks together
+  hipLaunchKernelGGL((decode_gemm_k<S, C, MODE, NC>), dim3((unsigned)(groups * 8 * ZB)), dim3((unsigned)(64 * p.KW)),
+                     0, st, x, B, K, csum, eps, Wt, N, NT, ZB, bias, scale, act, resid, y);
+  PGN_RETURN_LAUNCH();
+}
+
+// Workgroups of three column tiles (each x piece feeds three products: a third fewer operand bytes per CU from L2,
+// which is what bounds these layers) when that still leaves this many workgroups; else one tile a workgroup.
+constexpr int64_t kWideGroups = 192;
+
 template <int S, int C, int MODE>
 int launch(const Plan& p, const float* x, int B, int K, const float* csum, float eps, const float* Wt, int N,
            const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
-  const int NT = (N + 15) / 16, ZB = (B + 15) / 16;
-  const int64_t groups = (NT + 7) / 8;  // tiles in groups of 8, each group's ZB row blocks together
-  hipLaunchKernelGGL((decode_gemm_k<S, C, MODE>), dim3((unsigned)(groups * 8 * ZB)), dim3((unsigned)(64 * p.KW)), 0,
-                     st, x, B, K, csum, eps, Wt, N, NT, ZB, bias, scale, act, resid, y);
-  PGN_RETURN_LAUNCH();
+  if constexpr (C == 1 && MODE < 2) {
+    const int64_t NT = (N + 15) / 16, ZB = (B + 15) / 16;
+    if (ZB * ((NT + 2) / 3) >= kWideGroups)
+      return launch_nc<S, C, MODE, 3>(p, x, B, K, csum, eps, Wt, N, bias, scale, act, resid, y, st);
+  }
+  return launch_nc<S, C, MODE, 1>(p, x, B, K, csum, eps, Wt, N, bias, scale, act, resid, y, st);
 }
 
 template <int C, int MODE>

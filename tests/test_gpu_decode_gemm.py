@@ -76,6 +76,7 @@ SHAPES = [(768, 2328, 1, 0, False),   # the carrier's projections (LayerNorm)
           (1024, 640, 1, 0, False),   # LayerNorm over 16 waves of 4 steps
           (3072, 520, 1, 0, True),    # LayerNorm moments merged over 2 chunks a wave
           (4096, 300, 1, 1, True),    # ... and over 4 chunks a wave
+          (768, 4000, 0, 1, True),    # no normalisation, three column tiles a workgroup from 64 rows (a partial last group)
           (4096, 520, 0, 0, True)]    # 16 waves of 4 chunks of 4 steps
 
 
