@@ -401,7 +401,8 @@ int pragnosia_aspin_decode_proj(const float* S, float* S_out, const float* P, in
  * row-major, scale a device scalar or NULL (1). One workgroup per (sequence, head, 64 rows of Wo) runs the head's step and adds its
  * 64 columns' products to its rows of y with atomics: y holds the residual on entry and equals the residual plus the
  * projection to fp32 rounding, with the heads summed in arrival order (not bit-identical from run to run). Every
- * workgroup reads the old state, so S_out must be a different buffer from S (the new state goes there). Replaces,
+ * workgroup reads the old state, so S_out must not overlap S (the new state goes there), and y must not overlap P or
+ * S (PRAGNOSIA_ERR_INVALID_ARGUMENT otherwise). Replaces,
  * inside the reference's graphed decode (src/bench.py:241-317), the T = 1 path of `AssocCarrier.forward` from its
  * projections to `x + F.linear(o, self.o.weight) * sigmoid(self.gate)` (src/assoc.py:384-512), as
  * pragnosia_aspin_decode_proj + pragnosia_decode_gemv_rms do in two launches. */

@@ -502,6 +502,16 @@ extern "C" int pragnosia_aspin_decode_oproj(const float* S, float* S_out, const 
   const int64_t NS = (N + kOprojRows - 1) / kOprojRows;
   PGN_CHECK_ARG(B * H * NS < ((int64_t)1 << 31) && N * H * Dh < ((int64_t)1 << 31) && B * N < ((int64_t)1 << 31));
   PGN_CHECK_ARG((uintptr_t)Wo % 16 == 0);
+  // every workgroup reads the old state while slice 0 writes the new one, and the atomics into y run while other
+  // workgroups still read P: the byte ranges must not overlap
+  const auto apart = [](const void* a, int64_t na, const void* b, int64_t nb) {
+    const uintptr_t x = (uintptr_t)a, z = (uintptr_t)b;
+    return x + (uintptr_t)na <= z || z + (uintptr_t)nb <= x;
+  };
+  const int64_t sbytes = B * H * Dh * Dh * (int64_t)sizeof(float);
+  PGN_CHECK_ARG(apart(S, sbytes, S_out, sbytes));
+  PGN_CHECK_ARG(apart(y, B * N * (int64_t)sizeof(float), P, B * np * (int64_t)sizeof(float)));
+  PGN_CHECK_ARG(apart(y, B * N * (int64_t)sizeof(float), S, sbytes));
   StepIn in{};
   in.P = P;
   in.np = (int)np;

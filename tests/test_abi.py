@@ -173,6 +173,25 @@ def test_decode_gemm_plans_and_rejections(L):
     assert rms(96) == -1 and rms(0) == -1                              # heads of 64 or 128 only
 
 
+def test_decode_oproj_rejects_overlaps(L):
+    """The one-launch decode step + o-projection refuses, before any launch, a new-state buffer overlapping the old
+    state (every workgroup reads the old state while one writes the new) and a residual overlapping P or the state
+    (its atomics run while other workgroups still read them), and heads other than 64."""
+    null = ctypes.c_void_p(0)
+    B, H, N = 1, 2, 128
+    sb, np_ = B * H * 64 * 64 * 4, 3 * H * 64 + 2 * H
+    S, P, y, W = 1 << 20, 1 << 24, 1 << 26, 1 << 28
+    call = lambda S_, So, P_, y_, D=64: L.pragnosia_aspin_decode_oproj(
+        ctypes.c_void_p(S_), ctypes.c_void_p(So), ctypes.c_void_p(P_), np_, 3 * H * 64, 3 * H * 64 + H, -1,
+        ctypes.c_void_p(W), ctypes.c_void_p(W), null, ctypes.c_void_p(W), null, 0.0, ctypes.c_void_p(W), null, 0.0,
+        ctypes.c_void_p(W), 1e-6, ctypes.c_void_p(W), N, null, ctypes.c_void_p(y_), B, H, D, null)
+    assert call(S, S, P, y) == -1                      # the same state buffer
+    assert call(S, S + sb - 256, P, y) == -1           # overlapping state buffers
+    assert call(S, S + sb, P, P + 16) == -1            # residual inside P
+    assert call(S, S + sb, P, S + 64) == -1            # residual inside the state
+    assert call(S, S + sb, P, y, D=128) == -2          # heads of 64 only
+
+
 def test_product_never_imports_oracle():
     pkg = os.path.join(ROOT, "pragnosia_amd")
     for dp, _, files in os.walk(pkg):
