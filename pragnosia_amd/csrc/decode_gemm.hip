@@ -37,33 +37,39 @@ namespace {
 
 constexpr int MAXW = 16;  // waves per workgroup
 
-template <int S, int C, int MODE, int NC>
+// ACC: the K split over SK groups of workgroups (split ks over K range ks K .. ks K + K - 1 of rows of ldx = SK K
+// entries), each adding its partial products (and, for split 0, the bias) to y with atomics: y holds the residual.
+template <int S, int C, int MODE, int NC, bool ACC>
 __global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ x, int B, int K,
                                                       const float* __restrict__ csum, float eps,
                                                       const float* __restrict__ Wt, int N, int NT, int ZB,
                                                       const float* __restrict__ bias,
                                                       const float* __restrict__ scale, int act,
-                                                      const float* __restrict__ resid, float* __restrict__ y) {
+                                                      const float* __restrict__ resid, float* __restrict__ y,
+                                                      int SK) {
   static_assert(MODE != 2 || C == 1, "the RMS mode holds one channel group per wave");
+  static_assert(!ACC || MODE == 0, "the split-K form takes the input as is");
   __shared__ __align__(16) float red[NC * MAXW * 256];
   __shared__ float2 stat[MAXW][16];
   const int KW = blockDim.x >> 6;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, r16 = l & 15, k4 = l >> 4;
-  // workgroup i -> (column group of NC tiles, row block): the ZB row blocks of a group are 8 apart (one XCD)
-  const int i = blockIdx.x;
+  // workgroup i -> (K split, column group of NC tiles, row block): the ZB row blocks of a group are 8 apart (one XCD)
+  const int per_split = (int)(gridDim.x / SK);
+  const int ks = ACC ? (int)blockIdx.x / per_split : 0;
+  const int i = (int)blockIdx.x - ks * per_split;
   const int ng = (i / (8 * ZB)) * 8 + (i & 7), zb = (i >> 3) % ZB;
   if (ng * NC >= NT) return;  // padding workgroups of the last group of 8
   const int nt0 = ng * NC;    // the group's first column tile
-  const int KS = K >> 4;
+  const int KS = K >> 4, KSt = KS * SK;  // 16-wide steps of this workgroup's K range, of the whole row
   const int s0 = w * S * C;  // the wave's first 16-wide step
   const int row = 16 * zb + r16;
   const bool live = row < B;
-  const float* xrow = x + (size_t)min(row, B - 1) * K;
+  const float* xrow = x + (size_t)min(row, B - 1) * K * SK + (size_t)ks * K;
   const float* xr = xrow + 16 * s0 + 4 * k4;
   const float* wp[NC];  // tiles past the last are read from the last one and not written
 #pragma unroll
-  for (int t = 0; t < NC; ++t) wp[t] = Wt + ((size_t)min(nt0 + t, NT - 1) * KS + s0) * 256 + 4 * l;
+  for (int t = 0; t < NC; ++t) wp[t] = Wt + ((size_t)min(nt0 + t, NT - 1) * KSt + ks * KS + s0) * 256 + 4 * l;
 
   f32x4 wv[2][S][NC], z[2][S];
   auto load = [&](int c, int b) {
@@ -175,11 +181,15 @@ __global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ 
         }
         t = (t - mean * csum[col]) * (1.f / sqrtf(m2 / K + eps));
       }
-      float r = (scale ? *scale : 1.f) * t + (bias ? bias[col] : 0.f);
-      if (act == 1) r = pgn_gelu_erf(r);
       const size_t off = (size_t)orow * N + col;
-      if (resid) r += resid[off];
-      y[off] = r;
+      if constexpr (ACC) {
+        atomicAdd(y + off, (scale ? *scale : 1.f) * t + (bias && ks == 0 ? bias[col] : 0.f));
+      } else {
+        float r = (scale ? *scale : 1.f) * t + (bias ? bias[col] : 0.f);
+        if (act == 1) r = pgn_gelu_erf(r);
+        if (resid) r += resid[off];
+        y[off] = r;
+      }
     }
   }
 }
@@ -214,13 +224,15 @@ bool make_plan(int64_t K, int mode, Plan& p) {
   return false;
 }
 
-template <int S, int C, int MODE, int NC>
+template <int S, int C, int MODE, int NC, bool ACC = false>
 int launch_nc(const Plan& p, const float* x, int B, int K, const float* csum, float eps, const float* Wt, int N,
-              const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
+              const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st,
+              int SK = 1) {
   const int NT = (N + 15) / 16, ZB = (B + 15) / 16;
   const int64_t groups = ((NT + NC - 1) / NC + 7) / 8;  // column groups in sets of 8, each set's ZB row blocks together
-  hipLaunchKernelGGL((decode_gemm_k<S, C, MODE, NC>), dim3((unsigned)(groups * 8 * ZB)), dim3((unsigned)(64 * p.KW)),
-                     0, st, x, B, K, csum, eps, Wt, N, NT, ZB, bias, scale, act, resid, y);
+  hipLaunchKernelGGL((decode_gemm_k<S, C, MODE, NC, ACC>), dim3((unsigned)(groups * 8 * ZB * SK)),
+                     dim3((unsigned)(64 * p.KW)), 0, st, x, B, K, csum, eps, Wt, N, NT, ZB, bias, scale, act, resid, y,
+                     SK);
   PGN_RETURN_LAUNCH();
 }
 
@@ -258,6 +270,38 @@ int dispatch_s(const Plan& p, const float* x, int B, int K, const float* csum, f
 #undef PGN_S
 }
 
+// The split-K accumulating form (MODE 0): SK splits of Kp = K / SK each, three column tiles a workgroup where that
+// still leaves kWideGroups workgroups.
+template <int S, int C>
+int launch_acc(const Plan& p, const float* x, int B, int Kp, const float* Wt, int N, const float* bias,
+               const float* scale, float* y, hipStream_t st, int SK) {
+  if constexpr (C == 1) {
+    const int64_t NT = (N + 15) / 16, ZB = (B + 15) / 16;
+    if (ZB * ((NT + 2) / 3) * SK >= kWideGroups)
+      return launch_nc<S, C, 0, 3, true>(p, x, B, Kp, nullptr, 0.f, Wt, N, bias, scale, 0, nullptr, y, st, SK);
+  }
+  return launch_nc<S, C, 0, 1, true>(p, x, B, Kp, nullptr, 0.f, Wt, N, bias, scale, 0, nullptr, y, st, SK);
+}
+
+template <int C>
+int acc_s(const Plan& p, const float* x, int B, int Kp, const float* Wt, int N, const float* bias,
+          const float* scale, float* y, hipStream_t st, int SK) {
+  switch (p.S) {
+    case 1: return launch_acc<1, C>(p, x, B, Kp, Wt, N, bias, scale, y, st, SK);
+    case 2: return launch_acc<2, C>(p, x, B, Kp, Wt, N, bias, scale, y, st, SK);
+    case 3: return launch_acc<3, C>(p, x, B, Kp, Wt, N, bias, scale, y, st, SK);
+    case 4: return launch_acc<4, C>(p, x, B, Kp, Wt, N, bias, scale, y, st, SK);
+    default: return launch_acc<6, C>(p, x, B, Kp, Wt, N, bias, scale, y, st, SK);
+  }
+}
+
+// K split for the accumulating form: four or two splits when each keeps at least 512 of K (whole 16-wide steps)
+int acc_splits(int64_t K) {
+  for (int c : {4, 2})
+    if (K % (16 * c) == 0 && K / c >= 512) return c;
+  return 1;
+}
+
 }  // namespace
 
 extern "C" int pragnosia_decode_gemm_waves(int64_t K, int mode) {
@@ -293,4 +337,25 @@ extern "C" int pragnosia_decode_gemm(const float* x, int64_t B, int64_t K, int m
   if (mode == 1) return dispatch_c<1>(p, x, b, k, csum, eps, Wt, n, bias, scale, act, resid, y, st);
   if (mode >= 2) return dispatch_s<1, 2>(p, x, b, k, nullptr, eps, Wt, n, bias, scale, act, resid, y, st);
   return dispatch_c<0>(p, x, b, k, nullptr, eps, Wt, n, bias, scale, act, resid, y, st);
+}
+
+extern "C" int pragnosia_decode_gemm_acc(const float* x, int64_t B, int64_t K, const float* Wt, int64_t N,
+                                         const float* bias, const float* scale, float* y, void* stream) {
+  PGN_CHECK_ARG(x && Wt && y && B > 0 && K > 0 && N > 0);
+  PGN_CHECK_ARG(B * N < ((int64_t)1 << 31) && B * K < ((int64_t)1 << 31) &&
+                ((N + 15) / 16) * 16 * K < ((int64_t)1 << 31) && ((N + 127) / 128) * 8 * ((B + 15) / 16) < (1 << 27));
+  PGN_CHECK_ARG(((uintptr_t)x | (uintptr_t)Wt) % 16 == 0);
+  // the atomics into y run while other workgroups still read x
+  const uintptr_t xa = (uintptr_t)x, ya = (uintptr_t)y;
+  PGN_CHECK_ARG(xa + (uintptr_t)(B * K * 4) <= ya || ya + (uintptr_t)(B * N * 4) <= xa);
+  const int SK = acc_splits(K);
+  Plan p;
+  if (!make_plan(K / SK, 0, p)) return PRAGNOSIA_ERR_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  const int b = (int)B, kp = (int)(K / SK), n = (int)N;
+  switch (p.C) {
+    case 1: return acc_s<1>(p, x, b, kp, Wt, n, bias, scale, y, st, SK);
+    case 2: return acc_s<2>(p, x, b, kp, Wt, n, bias, scale, y, st, SK);
+    default: return acc_s<4>(p, x, b, kp, Wt, n, bias, scale, y, st, SK);
+  }
 }

@@ -35,6 +35,10 @@ from .ops import decode_gemm_ln, decode_gemm_ok, decode_gemm_tile, decode_tail, 
 # / 0.83; the unfused step with torch GEMMs: 1.45-1.57. The one-wave GEMV (up to 4 sequences) and the split carrier
 # step bring batch 1 to 0.31.
 GEMV_MAX_BATCH = 4
+# On the decode_gemm path, a dense layer with a residual and at least this input width (the MLP's second layer, K =
+# 4 d) runs as decode_gemm_acc_: its K split over groups of workgroups adding into the residual in place, so its
+# column tiles' workgroups fill more compute units.
+GEMM_ACC_MIN_K = 1024
 
 
 def _rms_gemv_ok(K: int) -> bool:
@@ -215,7 +219,11 @@ class GreedyDecoder:
                                       gated, mx.theta, self.p0s[i:i + 1], 0.0, None, on_eps)
             x1 = op.decode_gemm(o, to, m.d, 2 if mx.dk == 64 else 3, None, on_eps, None, sig, 0, h)
             hm = op.decode_gemm(x1, ta, ca.shape[0], 1, ca, mp.n.eps, ba, None, 1, None)
-            h = op.decode_gemm(hm, tb, m.d, 0, None, 0.0, mp.b.bias, None, 0, x1)
+            if hm.shape[1] >= GEMM_ACC_MIN_K:
+                op.decode_gemm_acc_(hm, tb, mp.b.bias, None, x1)  # x1 += W hm + bias: the residual in place
+                h = x1
+            else:
+                h = op.decode_gemm(hm, tb, m.d, 0, None, 0.0, mp.b.bias, None, 0, x1)
         th, ch, bh = self.wbuf[-1]
         self._tail(op.decode_gemm(h, th, ch.shape[0], 1, ch, m.n.eps, bh, None, 0, None), par)
 

@@ -1531,6 +1531,32 @@ def _(x, Wt, N, mode, csum, eps, bias, scale, act, resid):
     return x.new_empty(x.shape[0], N, dtype=torch.float32)
 
 
+@torch.library.custom_op("pragnosia::decode_gemm_acc_", mutates_args=("y",))
+def decode_gemm_acc_(x: Tensor, Wt: Tensor, bias: Optional[Tensor], scale: Optional[Tensor], y: Tensor) -> None:
+    """y (B, N) += scale * (W x) + bias in place, W given tiled (`decode_gemm_tile`): `decode_gemm` mode 0 with its
+    K split over groups of workgroups that add their partial products into y (which holds the residual), so a deep
+    layer spreads over more compute units. Adds in varying order: not bit-deterministic. Not differentiable."""
+    _require_gpu(x, Wt, bias, scale, y)
+    if x.dim() != 2 or y.dim() != 2 or y.shape[0] != x.shape[0]:
+        raise PragnosiaError(f"decode_gemm_acc_: x (B, K) and y (B, N) expected, got {tuple(x.shape)}, "
+                             f"{tuple(y.shape)}")
+    B_, K_ = x.shape
+    N = y.shape[1]
+    if K_ % 16 or Wt.numel() != ((N + 15) // 16) * 16 * K_:
+        raise PragnosiaError(f"decode_gemm_acc_: tiled weight of {Wt.numel()} values does not fit N {N} and K {K_}")
+    if y.dtype != torch.float32 or not y.is_contiguous():
+        raise PragnosiaError("decode_gemm_acc_: y must be contiguous fp32 (it is added into in place)")
+    _expect("decode_gemm_acc_", x.device, bias=(bias, (N,)), scale=(scale, ()), y=(y, (B_, N)))
+    x, Wt, bias, scale = _f32(x), _f32(Wt), _f32(bias), _f32(scale)
+    check(lib().pragnosia_decode_gemm_acc(_ptr(x), B_, K_, _ptr(Wt), N, _ptr(bias), _ptr(scale), _ptr(y),
+                                          _stream(x)), "pragnosia_decode_gemm_acc")
+
+
+@decode_gemm_acc_.register_fake
+def _(x, Wt, bias, scale, y):
+    return None
+
+
 def decode_tail(logits: Tensor, emb: Tensor, pemb: Tensor, ctr_in: Tensor, ctr_out: Tensor, pos_in: Tensor,
                 pos_out: Tensor, out: Tensor, tok: Tensor, h: Tensor, p0s: Optional[Tensor],
                 logits_rec: Optional[Tensor]) -> None:

@@ -158,3 +158,69 @@ def test_graph_replay_with_new_inputs():
         want = chain(x.clone())
         torch.cuda.synchronize()
         assert torch.equal(out, want), rep
+
+
+ACC_SHAPES = [(3072, 768),   # the MLP's second layer at d 768: four splits of 768
+              (2816, 704),   # d 704: four splits of 704
+              (1024, 300),   # two splits of 512, a ragged last column tile
+              (4096, 2048),  # four splits of 1024, three column tiles a workgroup
+              (768, 520)]    # one split: a plain atomic add into the residual
+
+
+@pytest.mark.parametrize("B", [5, 64, 100])
+@pytest.mark.parametrize("K,N", ACC_SHAPES)
+def test_decode_gemm_acc_adds_into_residual(B, K, N):
+    """decode_gemm_acc_ (y += scale * W x + bias, K split over workgroups that add with atomics) against fp64 torch
+    and against decode_gemm's residual epilogue at the same tolerance; the adds' order varies, so two calls agree to
+    the tolerance, not bit for bit."""
+    from pragnosia_amd import ops
+    x, W, _, _, bias, scale, resid = inputs(B, K, N, 0, 1, True, 3 * B + K + N)
+    Wt = ops.decode_gemm_tile(W)
+    r = reference(x, W, 0, None, None, 0.0, bias, scale, 0, resid)
+    y = resid.clone()
+    torch.ops.pragnosia.decode_gemm_acc_(x, Wt, bias, scale, y)
+    assert rel(y, r) < 1e-5, (B, K, N)
+    y2 = resid.clone()
+    torch.ops.pragnosia.decode_gemm_acc_(x, Wt, None, None, y2)
+    assert rel(y2, reference(x, W, 0, None, None, 0.0, None, None, 0, resid)) < 1e-5
+    full = torch.ops.pragnosia.decode_gemm(x, Wt, N, 0, None, 0.0, bias, scale, 0, resid)
+    assert rel(y, full) < 1e-5
+
+
+def test_decode_gemm_acc_graph_replay():
+    """The MLP's two layers with the second added into the residual in place, captured and replayed with new inputs
+    and eager work between replays: every replay within 1e-5 of the eager result."""
+    from pragnosia_amd import ops
+    op = torch.ops.pragnosia
+    B, d = 64, 768
+    g = torch.Generator(device="cuda").manual_seed(12)
+    W1 = torch.randn(3072, d, device="cuda", generator=g) * 0.05
+    W2 = torch.randn(d, 3072, device="cuda", generator=g) * 0.05
+    lw, lb = 1 + 0.1 * torch.randn(d, device="cuda", generator=g), torch.randn(d, device="cuda", generator=g)
+    b1, b2 = torch.randn(3072, device="cuda", generator=g), torch.randn(d, device="cuda", generator=g)
+    T1, c1, b1f = ops.decode_gemm_ln(W1, lw, lb, b1)
+    T2 = ops.decode_gemm_tile(W2)
+    x = torch.randn(B, d, device="cuda", generator=g)
+
+    def mlp(x):
+        h = op.decode_gemm(x, T1, 3072, 1, c1, 1e-5, b1f, None, 1, None)
+        y = x.clone()
+        op.decode_gemm_acc_(h, T2, b2, None, y)
+        return y
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mlp(x)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = mlp(x)
+    for i in range(3):
+        x.copy_(torch.randn(B, d, device="cuda", generator=g) * (1 + i))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = mlp(x.clone())
+        torch.cuda.synchronize()
+        assert rel(out, want) < 1e-5, i
