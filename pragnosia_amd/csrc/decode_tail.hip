@@ -44,6 +44,11 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail(const float* __restr
   const float* row = logits + (size_t)b * V;
   const int64_t c = *ctr_in;
   const bool rec = lrec && c < n_rows;
+  // the next position and its embedding entry do not depend on the argmax: loaded with the logits, so only the token
+  // embedding's load follows the reduction
+  const int p = (int)((*pos_in + 1) % ctx);
+  const float* pr = pemb + (size_t)p * d;
+  const float pr0 = tid < d ? pr[tid] : 0.f;
   float bv = 0.f;
   int bi = -1;
   // kTailLoads logits a thread (v = v0 + tid + kTailThreads u), all loaded before any comparison, so a pass over
@@ -94,11 +99,10 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail(const float* __restr
   }
   __syncthreads();
   const int t = tok_s;
-  const int p = (int)((*pos_in + 1) % ctx);
   const float* er = emb + (size_t)t * d;
-  const float* pr = pemb + (size_t)p * d;
   float* hr = h + (size_t)b * d;
-  for (int k = tid; k < d; k += kTailThreads) hr[k] = er[k] + pr[k];
+  if (tid < d) hr[tid] = er[tid] + pr0;
+  for (int k = tid + kTailThreads; k < d; k += kTailThreads) hr[k] = er[k] + pr[k];
   if (b == 0) {
     if (tid == 0) {
       *pos_out = p;

@@ -156,7 +156,7 @@ def test_wgrad_workspace_and_rejections(L):
 def test_decode_gemm_plans_and_rejections(L):
     """The decode GEMM's plan (waves a workgroup per input width and mode) and its host-side rejections."""
     q = L.pragnosia_decode_gemm_waves
-    assert q(768, 1) == 8 and q(768, 0) == 8 and q(3072, 0) == 16    # 8 waves of 6 steps; 3072: 2 chunks each
+    assert q(768, 1) == 16 and q(768, 0) == 16 and q(3072, 0) == 16  # 16 waves of 3 steps; 3072: 2 chunks each
     assert q(768, 2) == 12 and q(1024, 2) == 16 and q(1088, 2) == -1   # one 64-channel group a wave
     assert q(3072, 1) == 16 and q(4096, 1) == 16 and q(128, 0) == 2
     assert q(768, 3) == 6 and q(2048, 3) == 16 and q(2176, 3) == -1 and q(704, 3) == -1  # one 128-group a wave
