@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (20); bumped on any change of the entry points. */
+/* ABI version of this header (21); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -465,16 +465,18 @@ int pragnosia_decode_gemm(const float* x, int64_t B, int64_t K, int mode, const 
                           const float* Wt, int64_t N, const float* bias, const float* scale, int act,
                           const float* resid, float* y, void* stream);
 
-/* y (B, N) += scale * (W x) + bias, mode 0 of pragnosia_decode_gemm with K split over 4 or 2 groups of workgroups
- * (each split at least 512 of K, whole 16-wide steps; 1 where neither fits), each adding its partial products (the
+/* y (B, N) += scale * (W z) + bias, with z = x (mode 0) or each 64-channel (mode 2) or 128-channel (mode 3) group
+ * RMS-scaled as in pragnosia_decode_gemm, K split over groups of workgroups, each adding its partial products (the
  * first split also the bias) into y with fp32 atomics: y holds the residual on entry, so the layer's residual add
- * needs no read of a separate tensor and a deep layer (the MLP's second layer, K = 4 d) spreads over more compute
- * units than its column tiles give. x and y must not overlap; calls that write one y on one stream are ordered, the
- * adds within a call are not (the sum's rounding order varies run to run: not bit-deterministic). W tiled as for
- * pragnosia_decode_gemm. Replaces the MLP's second nn.Linear + residual (src/model.py:552-560) in the reference's
- * batched graphed decode (src/bench.py:241-317). */
-int pragnosia_decode_gemm_acc(const float* x, int64_t B, int64_t K, const float* Wt, int64_t N, const float* bias,
-                              const float* scale, float* y, void* stream);
+ * needs no read of a separate tensor and the layer spreads over more compute units than its column tiles give.
+ * Splits: mode 0 four or two (each at least 512 of K, whole 16-wide steps), the RMS modes up to four of whole channel
+ * groups (at least four groups a split); 1 where none fits. x and y must not overlap; calls that write one y on one
+ * stream are ordered, the adds within a call are not (the sum's rounding order varies run to run: not
+ * bit-deterministic). W tiled (and the RMSNorm's weight folded) as for pragnosia_decode_gemm. Replaces the MLP's
+ * second nn.Linear + residual and the carrier's RMSNorm + gated output projection + residual (src/model.py:552-560,
+ * src/assoc.py:384-512) in the reference's batched graphed decode (src/bench.py:241-317). */
+int pragnosia_decode_gemm_acc(const float* x, int64_t B, int64_t K, int mode, float eps, const float* Wt, int64_t N,
+                              const float* bias, const float* scale, float* y, void* stream);
 
 #ifdef __cplusplus
 }

@@ -25,7 +25,9 @@
 // merges them (Chan, Golub and LeVeque's pairwise update); the waves' pairs meet in the epilogue, in wave order, with
 // the products' partials. MODE 2 (S = 4 or 8, C = 1) has each wave own one group of 16 S channels, so the group's
 // sum of squares is a two-step lane exchange before its products. The wave partials are summed through LDS in wave
-// order: deterministic, no atomics, nothing shared between workgroups, no workspace.
+// order: deterministic, no atomics, nothing shared between workgroups, no workspace. The accumulating form (ACC) splits
+// K over groups of workgroups instead (whole channel groups in the RMS mode) and adds each split's sums into the
+// output, which holds the residual, with fp32 atomics: more workgroups for the deep layers, not bit-deterministic.
 //
 // Operand layout of v_mfma_f32_16x16x4f32: A[r][k] in lane r + 16 k, B[k][c] in lane c + 16 k, D[4 g + e][c] in
 // lane c + 16 g, e = 0..3. A lane holds four consecutive K entries of a row (one 16-byte piece): product e of a
@@ -48,7 +50,7 @@ __global__ __launch_bounds__(1024) void decode_gemm_k(const float* __restrict__ 
                                                       const float* __restrict__ resid, float* __restrict__ y,
                                                       int SK) {
   static_assert(MODE != 2 || C == 1, "the RMS mode holds one channel group per wave");
-  static_assert(!ACC || MODE == 0, "the split-K form takes the input as is");
+  static_assert(!ACC || MODE != 1, "the split-K form needs no whole-row statistics");
   __shared__ __align__(16) float red[NC * MAXW * 256];
   __shared__ float2 stat[MAXW][16];
   const int KW = blockDim.x >> 6;
@@ -277,33 +279,45 @@ int dispatch_s(const Plan& p, const float* x, int B, int K, const float* csum, f
 #undef PGN_S
 }
 
-// The split-K accumulating form (MODE 0): SK splits of Kp = K / SK each, three column tiles a workgroup where that
-// still leaves kWideGroups workgroups.
-template <int S, int C>
-int launch_acc(const Plan& p, const float* x, int B, int Kp, const float* Wt, int N, const float* bias,
+// The split-K accumulating form: SK splits of Kp = K / SK each; mode 0 with three column tiles a workgroup where that
+// still leaves kWideGroups workgroups, the RMS mode (MODE 2, whole channel groups a split) one tile.
+template <int S, int C, int MODE>
+int launch_acc(const Plan& p, const float* x, int B, int Kp, float eps, const float* Wt, int N, const float* bias,
                const float* scale, float* y, hipStream_t st, int SK) {
-  if constexpr (C == 1) {
+  if constexpr (C == 1 && MODE == 0) {
     const int64_t NT = (N + 15) / 16, ZB = (B + 15) / 16;
     if (ZB * ((NT + 2) / 3) * SK >= kWideGroups)
       return launch_nc<S, C, 0, 3, true>(p, x, B, Kp, nullptr, 0.f, Wt, N, bias, scale, 0, nullptr, y, st, SK);
   }
-  return launch_nc<S, C, 0, 1, true>(p, x, B, Kp, nullptr, 0.f, Wt, N, bias, scale, 0, nullptr, y, st, SK);
+  return launch_nc<S, C, MODE, 1, true>(p, x, B, Kp, nullptr, eps, Wt, N, bias, scale, 0, nullptr, y, st, SK);
 }
 
 template <int C>
 int acc_s(const Plan& p, const float* x, int B, int Kp, const float* Wt, int N, const float* bias,
           const float* scale, float* y, hipStream_t st, int SK) {
   switch (p.S) {
-    case 1: return launch_acc<1, C>(p, x, B, Kp, Wt, N, bias, scale, y, st, SK);
-    case 2: return launch_acc<2, C>(p, x, B, Kp, Wt, N, bias, scale, y, st, SK);
-    case 3: return launch_acc<3, C>(p, x, B, Kp, Wt, N, bias, scale, y, st, SK);
-    case 4: return launch_acc<4, C>(p, x, B, Kp, Wt, N, bias, scale, y, st, SK);
-    default: return launch_acc<6, C>(p, x, B, Kp, Wt, N, bias, scale, y, st, SK);
+    case 1: return launch_acc<1, C, 0>(p, x, B, Kp, 0.f, Wt, N, bias, scale, y, st, SK);
+    case 2: return launch_acc<2, C, 0>(p, x, B, Kp, 0.f, Wt, N, bias, scale, y, st, SK);
+    case 3: return launch_acc<3, C, 0>(p, x, B, Kp, 0.f, Wt, N, bias, scale, y, st, SK);
+    case 4: return launch_acc<4, C, 0>(p, x, B, Kp, 0.f, Wt, N, bias, scale, y, st, SK);
+    default: return launch_acc<6, C, 0>(p, x, B, Kp, 0.f, Wt, N, bias, scale, y, st, SK);
   }
 }
 
-// K split for the accumulating form: four or two splits when each keeps at least 512 of K (whole 16-wide steps)
-int acc_splits(int64_t K) {
+// K split for the accumulating form. Mode 0: four or two splits when each keeps at least 512 of K (whole 16-wide
+// steps). RMS modes (groups of G channels): the most splits, of at most four, that keep whole groups and at least
+// four of them a split (each group is one wave of the split's workgroup). At 64 rows and 12 heads of 64, batch-64
+// step on one box: one split 0.4853 ms, two of six heads 0.4856-0.4860, three of four 0.4815, four of three
+// 0.4837-0.4840.
+constexpr int64_t kRmsSplitGroups = 4;
+int acc_splits(int64_t K, int mode) {
+  if (mode >= 2) {
+    const int64_t G = mode == 2 ? 64 : 128;
+    if (K % G) return 1;
+    for (int c : {4, 3, 2})
+      if ((K / G) % c == 0 && K / G / c >= kRmsSplitGroups) return c;
+    return 1;
+  }
   for (int c : {4, 2})
     if (K % (16 * c) == 0 && K / c >= 512) return c;
   return 1;
@@ -346,20 +360,25 @@ extern "C" int pragnosia_decode_gemm(const float* x, int64_t B, int64_t K, int m
   return dispatch_c<0>(p, x, b, k, nullptr, eps, Wt, n, bias, scale, act, resid, y, st);
 }
 
-extern "C" int pragnosia_decode_gemm_acc(const float* x, int64_t B, int64_t K, const float* Wt, int64_t N,
-                                         const float* bias, const float* scale, float* y, void* stream) {
+extern "C" int pragnosia_decode_gemm_acc(const float* x, int64_t B, int64_t K, int mode, float eps, const float* Wt,
+                                         int64_t N, const float* bias, const float* scale, float* y, void* stream) {
   PGN_CHECK_ARG(x && Wt && y && B > 0 && K > 0 && N > 0);
+  PGN_CHECK_ARG(mode == 0 || mode == 2 || mode == 3);
   PGN_CHECK_ARG(B * N < ((int64_t)1 << 31) && B * K < ((int64_t)1 << 31) &&
                 ((N + 15) / 16) * 16 * K < ((int64_t)1 << 31) && ((N + 127) / 128) * 8 * ((B + 15) / 16) < (1 << 27));
   PGN_CHECK_ARG(((uintptr_t)x | (uintptr_t)Wt) % 16 == 0);
   // the atomics into y run while other workgroups still read x
   const uintptr_t xa = (uintptr_t)x, ya = (uintptr_t)y;
   PGN_CHECK_ARG(xa + (uintptr_t)(B * K * 4) <= ya || ya + (uintptr_t)(B * N * 4) <= xa);
-  const int SK = acc_splits(K);
+  const int SK = acc_splits(K, mode);
   Plan p;
-  if (!make_plan(K / SK, 0, p)) return PRAGNOSIA_ERR_UNSUPPORTED;
+  if (!make_plan(K / SK, mode, p)) return PRAGNOSIA_ERR_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
   const int b = (int)B, kp = (int)(K / SK), n = (int)N;
+  if (mode >= 2) {  // one G-channel group a wave (S = G / 16)
+    if (p.S == 8) return launch_acc<8, 1, 2>(p, x, b, kp, eps, Wt, n, bias, scale, y, st, SK);
+    return launch_acc<4, 1, 2>(p, x, b, kp, eps, Wt, n, bias, scale, y, st, SK);
+  }
   switch (p.C) {
     case 1: return acc_s<1>(p, x, b, kp, Wt, n, bias, scale, y, st, SK);
     case 2: return acc_s<2>(p, x, b, kp, Wt, n, bias, scale, y, st, SK);

@@ -39,6 +39,8 @@ GEMV_MAX_BATCH = 4
 # 4 d) runs as decode_gemm_acc_: its K split over groups of workgroups adding into the residual in place, so its
 # column tiles' workgroups fill more compute units.
 GEMM_ACC_MIN_K = 1024
+# ... and the carrier's RMSNorm + gated o-projection adds into the residual in place, its K split over head groups.
+OPROJ_ACC = True
 
 
 def _rms_gemv_ok(K: int) -> bool:
@@ -217,10 +219,16 @@ class GreedyDecoder:
                                       mx.la_floor if mx.hl_floor else None, mx.wi.bias if gated else None,
                                       mx.wb.bias if mx.delta else None, 0.75 if (mx.delta and mx.write_all) else 0.0,
                                       gated, mx.theta, self.p0s[i:i + 1], 0.0, None, on_eps)
-            x1 = op.decode_gemm(o, to, m.d, 2 if mx.dk == 64 else 3, None, on_eps, None, sig, 0, h)
+            if OPROJ_ACC:
+                # h += sigmoid(g) W_o RMSNorm(o): the residual in place (h is not read again this step: the
+                # projection above has consumed it, and the tail rewrites the step's input)
+                op.decode_gemm_acc_(o, to, 2 if mx.dk == 64 else 3, on_eps, None, sig, h)
+                x1 = h
+            else:
+                x1 = op.decode_gemm(o, to, m.d, 2 if mx.dk == 64 else 3, None, on_eps, None, sig, 0, h)
             hm = op.decode_gemm(x1, ta, ca.shape[0], 1, ca, mp.n.eps, ba, None, 1, None)
             if hm.shape[1] >= GEMM_ACC_MIN_K:
-                op.decode_gemm_acc_(hm, tb, mp.b.bias, None, x1)  # x1 += W hm + bias: the residual in place
+                op.decode_gemm_acc_(hm, tb, 0, 0.0, mp.b.bias, None, x1)  # x1 += W hm + bias: the residual in place
                 h = x1
             else:
                 h = op.decode_gemm(hm, tb, m.d, 0, None, 0.0, mp.b.bias, None, 0, x1)

@@ -1532,10 +1532,12 @@ def _(x, Wt, N, mode, csum, eps, bias, scale, act, resid):
 
 
 @torch.library.custom_op("pragnosia::decode_gemm_acc_", mutates_args=("y",))
-def decode_gemm_acc_(x: Tensor, Wt: Tensor, bias: Optional[Tensor], scale: Optional[Tensor], y: Tensor) -> None:
-    """y (B, N) += scale * (W x) + bias in place, W given tiled (`decode_gemm_tile`): `decode_gemm` mode 0 with its
-    K split over groups of workgroups that add their partial products into y (which holds the residual), so a deep
-    layer spreads over more compute units. Adds in varying order: not bit-deterministic. Not differentiable."""
+def decode_gemm_acc_(x: Tensor, Wt: Tensor, group_mode: int, eps: float, bias: Optional[Tensor],
+                     scale: Optional[Tensor], y: Tensor) -> None:
+    """y (B, N) += scale * (W z) + bias in place, W given tiled (`decode_gemm_tile`): `decode_gemm` mode 0 (z = x) or
+    2 / 3 (z = x RMS-scaled per 64- / 128-channel group, the RMSNorm's weight folded into the tiled W) with its K split
+    over groups of workgroups that add their partial products into y (which holds the residual), so the layer spreads
+    over more compute units. Adds in varying order: not bit-deterministic. Not differentiable."""
     _require_gpu(x, Wt, bias, scale, y)
     if x.dim() != 2 or y.dim() != 2 or y.shape[0] != x.shape[0]:
         raise PragnosiaError(f"decode_gemm_acc_: x (B, K) and y (B, N) expected, got {tuple(x.shape)}, "
@@ -1546,14 +1548,16 @@ def decode_gemm_acc_(x: Tensor, Wt: Tensor, bias: Optional[Tensor], scale: Optio
         raise PragnosiaError(f"decode_gemm_acc_: tiled weight of {Wt.numel()} values does not fit N {N} and K {K_}")
     if y.dtype != torch.float32 or not y.is_contiguous():
         raise PragnosiaError("decode_gemm_acc_: y must be contiguous fp32 (it is added into in place)")
+    if group_mode not in (0, 2, 3):
+        raise PragnosiaError(f"decode_gemm_acc_: group_mode {group_mode} (0, 2 or 3 expected)")
     _expect("decode_gemm_acc_", x.device, bias=(bias, (N,)), scale=(scale, ()), y=(y, (B_, N)))
     x, Wt, bias, scale = _f32(x), _f32(Wt), _f32(bias), _f32(scale)
-    check(lib().pragnosia_decode_gemm_acc(_ptr(x), B_, K_, _ptr(Wt), N, _ptr(bias), _ptr(scale), _ptr(y),
-                                          _stream(x)), "pragnosia_decode_gemm_acc")
+    check(lib().pragnosia_decode_gemm_acc(_ptr(x), B_, K_, int(group_mode), float(eps), _ptr(Wt), N, _ptr(bias),
+                                          _ptr(scale), _ptr(y), _stream(x)), "pragnosia_decode_gemm_acc")
 
 
 @decode_gemm_acc_.register_fake
-def _(x, Wt, bias, scale, y):
+def _(x, Wt, group_mode, eps, bias, scale, y):
     return None
 
 

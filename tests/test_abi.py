@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 20
+    assert L.pragnosia_abi_version() == 21
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 
@@ -171,13 +171,14 @@ def test_decode_gemm_plans_and_rejections(L):
     rms = lambda G: L.pragnosia_decode_gemv_rms(one, 2, 768, one, G, 1e-6, one, 768, null, null, 0, null,
                                                ctypes.c_void_p(32), null)
     assert rms(96) == -1 and rms(0) == -1                              # heads of 64 or 128 only
-    acc = lambda x, B, K, y: L.pragnosia_decode_gemm_acc(ctypes.c_void_p(x), B, K, one, 768, null, null,
-                                                         ctypes.c_void_p(y), null)
+    acc = lambda x, B, K, y, mode=0: L.pragnosia_decode_gemm_acc(ctypes.c_void_p(x), B, K, mode, 1e-6, one, 768, null,
+                                                                 null, ctypes.c_void_p(y), null)
     X, Y = 1 << 24, 1 << 26
     assert acc(X, 64, 3072, X + 64 * 3072 * 4 - 4) == -1              # y overlapping the input's end
     assert acc(X, 64, 3072, X - 64 * 768 * 4 + 4) == -1                # y's end overlapping the input
     assert acc(X + 8, 64, 3072, Y) == -1                               # misaligned input
     assert acc(X, 64, 760, Y) == -2 and acc(X, 0, 3072, Y) == -1       # K not whole 16-wide steps; no rows
+    assert acc(X, 64, 768, Y, 1) == -1 and acc(X, 64, 1088, Y, 2) == -2   # no LayerNorm mode; 17 groups of 64
 
 
 def test_decode_oproj_rejects_overlaps(L):

@@ -178,13 +178,39 @@ def test_decode_gemm_acc_adds_into_residual(B, K, N):
     Wt = ops.decode_gemm_tile(W)
     r = reference(x, W, 0, None, None, 0.0, bias, scale, 0, resid)
     y = resid.clone()
-    torch.ops.pragnosia.decode_gemm_acc_(x, Wt, bias, scale, y)
+    torch.ops.pragnosia.decode_gemm_acc_(x, Wt, 0, 0.0, bias, scale, y)
     assert rel(y, r) < 1e-5, (B, K, N)
     y2 = resid.clone()
-    torch.ops.pragnosia.decode_gemm_acc_(x, Wt, None, None, y2)
+    torch.ops.pragnosia.decode_gemm_acc_(x, Wt, 0, 0.0, None, None, y2)
     assert rel(y2, reference(x, W, 0, None, None, 0.0, None, None, 0, resid)) < 1e-5
     full = torch.ops.pragnosia.decode_gemm(x, Wt, N, 0, None, 0.0, bias, scale, 0, resid)
     assert rel(y, full) < 1e-5
+
+
+RMS_ACC_SHAPES = [(768, 768, 2),    # the o-projection at d 768, heads of 64: three splits of four heads
+                  (1536, 768, 2),   # 24 heads of 64: four splits of six
+                  (1024, 300, 2),   # 16 heads: four splits of four, a ragged last column tile
+                  (1536, 520, 3),   # 12 heads of 128: three splits of four
+                  (768, 768, 3),    # 6 heads of 128: one split
+                  (640, 300, 2)]    # 10 heads of 64: two splits of five
+
+
+@pytest.mark.parametrize("B", [5, 64, 100])
+@pytest.mark.parametrize("K,N,mode", RMS_ACC_SHAPES)
+def test_decode_gemm_acc_rms_groups(B, K, N, mode):
+    """The accumulating form in the RMS modes (the carrier's per-head RMSNorm + gated o-projection added into the
+    residual, K split at head boundaries) against fp64 torch and against decode_gemm's residual epilogue, 1e-5."""
+    from pragnosia_amd import ops
+    x, W, nw, _, _, scale, resid = inputs(B, K, N, mode, 0, True, 5 * B + K + N + mode)
+    eps = torch.finfo(torch.float32).eps
+    Wt = ops.decode_gemm_tile(W, nw)
+    r = reference(x, W, mode, nw, None, eps, None, scale, 0, resid)
+    y = resid.clone()
+    torch.ops.pragnosia.decode_gemm_acc_(x, Wt, mode, eps, None, scale, y)
+    assert rel(y, r) < 1e-5, (B, K, N, mode)
+    if ops.decode_gemm_ok(K, mode):  # 24 heads of 64 exceed the unsplit form's 16 waves; each split holds six
+        full = torch.ops.pragnosia.decode_gemm(x, Wt, N, mode, None, eps, None, scale, 0, resid)
+        assert rel(y, full) < 1e-5
 
 
 def test_decode_gemm_acc_graph_replay():
@@ -205,7 +231,7 @@ def test_decode_gemm_acc_graph_replay():
     def mlp(x):
         h = op.decode_gemm(x, T1, 3072, 1, c1, 1e-5, b1f, None, 1, None)
         y = x.clone()
-        op.decode_gemm_acc_(h, T2, b2, None, y)
+        op.decode_gemm_acc_(h, T2, 0, 0.0, b2, None, y)
         return y
 
     side = torch.cuda.Stream()
