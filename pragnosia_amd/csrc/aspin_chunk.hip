@@ -369,6 +369,300 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 #undef FWD_STAMP
 }
 
+// Forward at 128 keys, native: one workgroup of 16 waves per (batch-head hw, value half vh) holds the 128 x 64 state
+// S[:, 64 vh ..] (both key halves) and writes its 64 columns of o whole, o = ((Q K^T) o dec) V + (Q o eL) S with
+// every contraction over keys running over all 128, so no output is a sum of two scans' outputs (the wide mode's four
+// 64 x 64 scans per head read q, k and v twice and o once more to add their halves). Q, K and V of a chunk take 5
+// tiles (Q and K as two 64-column halves), so the input sets are double-buffered and each chunk has two barriers:
+//   phase 1: output waves 0-7 (t block tb, value columns j0 .. j0 + 31, both key halves' 16 x 32 state slices as
+//       accumulators) form eL_t (S^T Q^T) for their tokens from the chunk's S^T tiles, write the entering state to
+//       `sent` and update S <- a S + (K o w)^T V in registers; score waves 8-11 form the chunk's decayed scores A (t
+//       block a, 128-deep) into the A tile, wave 8 also the next chunk's decay scan; load waves 12-15 stage the next
+//       chunk into the other input set and issue the loads of the one after;
+//   phase 2 (after the A barrier): output waves add V^T A^T and store o, then write the next chunk's S^T tiles (every
+//       read of the current ones was before the barrier).
+// `sent` keeps the wide mode's per-scan layout, (B, 4H, NC, 64, 64) at scan 4 hw + 2 kh + vh, so the wide backward
+// reads it unchanged. Unsegmented only (one workgroup walks all chunks of its scan).
+#ifndef PGN_NATIVE128_FWD
+#define PGN_NATIVE128_FWD 1
+#endif
+constexpr bool kNative128Fwd = PGN_NATIVE128_FWD;  // the unsegmented 128-key forward as aspin_plain_fwd128
+constexpr int kN128Buf = 5 * TILE * (int)sizeof(__bf16) + 3 * C * (int)sizeof(float);  // Q0, Q1, K0, K1, V, vectors
+constexpr size_t kN128Smem = 2 * (size_t)kN128Buf + 3 * TILE * sizeof(__bf16);       // two sets, A, S^T x 2
+
+__global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd128(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const float* __restrict__ la, const float* __restrict__ S0, __bf16* __restrict__ o, float* __restrict__ Sfin,
+    __bf16* __restrict__ sent, int T, int NC) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int ld = 128;
+  auto Qb = [&](int h, int kh) { return reinterpret_cast<__bf16*>(smem + h * kN128Buf) + kh * TILE; };
+  auto Kb = [&](int h, int kh) { return Qb(h, 0) + (2 + kh) * TILE; };
+  auto Vb = [&](int h) { return Qb(h, 0) + 4 * TILE; };
+  auto Vecb = [&](int h) { return reinterpret_cast<float*>(Qb(h, 0) + 5 * TILE); };
+  __bf16* const At = reinterpret_cast<__bf16*>(smem + 2 * kN128Buf);
+  auto STb = [&](int kh) { return At + (1 + kh) * TILE; };
+
+  const WaveIdx x = wave_idx();
+  const int w = x.w, g = x.g, i = x.i, tid = threadIdx.x;
+  const int hw = blockIdx.x >> 1, vh = blockIdx.x & 1;
+  const size_t koff = (size_t)hw * T * ld, voff = koff + 64 * vh;
+  const size_t soff = (size_t)hw * ld * ld + 64 * vh;  // the (B, H, 128, 128) state's block: rows 64 kh .., columns
+                                                       // 64 vh ..
+
+  if (w < 8) {
+    // ================= output waves
+    const int tb = w < 4 ? 3 - w : w - 4, j0 = 32 * (w >> 2);
+    f32x4 S[2][2];  // [key half][value block]: rows 64 kh + 16 tb + 4 g + r, columns j0 + 16 jt + i
+    const __amdgpu_buffer_rsrc_t s0v = f32_view(S0 ? S0 + soff : nullptr, ld * ld);
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[kh][jt][r] = load_f32(s0v, (64 * kh + 16 * tb + 4 * g + r) * ld + j0 + 16 * jt + i);
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) store_T(STb(kh), j0 + 16 * jt, 16 * tb, g, i, S[kh][jt]);
+    __bf16* const obase = o + voff;
+    auto o_rows = [&](int c) {
+      const int t0 = c * C;
+      return __builtin_amdgcn_make_buffer_rsrc(obase + (size_t)t0 * ld, (short)0,
+                                               min(C, T - t0) * ld * (int)sizeof(__bf16), 0x00020000);
+    };
+    __syncthreads();
+    auto oloop = [&](auto tb_c) {
+      constexpr int TB = decltype(tb_c)::value;
+      const int tq = 16 * TB + i;
+      for (int c = 0; c < NC; ++c) {
+        const int h = c & 1;
+        const float* Ls = Vecb(h);
+        const float* eLs = Ls + C;
+        const float* ws = Ls + 2 * C;
+        // operands in two groups (all of them at once would not fit the registers of 16 waves): the state read's
+        // Q and S^T fragments with V's, then K's and the chunk weights for the update
+        bf16x8 qf[2][2], sf[2][2][2], vf[2][2], kt[2][2];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            qf[kh][m] = frag(Qb(h, kh), tq, m, g);
+#pragma unroll
+            for (int jt = 0; jt < 2; ++jt) sf[kh][jt][m] = frag(STb(kh), j0 + 16 * jt + i, m, g);
+          }
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+          for (int m = 0; m < 2; ++m) vf[jt][m] = frag_tr(Vb(h), j0 + 16 * jt, m, g, i);
+        const float eLt = eLs[tq], LC = Ls[C - 1];
+        __builtin_amdgcn_sched_barrier(0);
+        // the state read eL_t (S^T Q^T) over all 128 keys, before S moves on
+        f32x4 acc[2];
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) {
+          f32x4 qs = zero4();
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh) {
+            qs = pgn_mfma(sf[kh][jt][0], qf[kh][0], qs);
+            qs = pgn_mfma(sf[kh][jt][1], qf[kh][1], qs);
+          }
+          acc[jt] = eLt * qs;
+        }
+        // the entering states, bf16 (d, j) per key half, through range-checked buffers (a uniform base, the lane
+        // offsets shared by both halves; no buffer: an empty range, the stores dropped)
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+              sent ? sent + ((size_t)(4 * hw + 2 * kh + vh) * NC + c) * DK * DK : nullptr, (short)0,
+              sent ? DK * DK * (int)sizeof(__bf16) : 0, 0x00020000);
+#pragma unroll
+          for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (__bf16)S[kh][jt][r]), sr,
+                                                    ((16 * TB + 4 * g + r) * DK + j0 + 16 * jt + i) *
+                                                        (int)sizeof(__bf16), 0, 0);
+        }
+        // S <- a S + (K o w)^T V, both key halves
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int m = 0; m < 2; ++m) kt[kh][m] = frag_tr(Kb(h, kh), 16 * TB, m, g, i);
+        const f32x4 w00 = *reinterpret_cast<const f32x4*>(ws + 4 * g);
+        const f32x4 w01 = *reinterpret_cast<const f32x4*>(ws + 16 + 4 * g);
+        const f32x4 w10 = *reinterpret_cast<const f32x4*>(ws + 32 + 4 * g);
+        const f32x4 w11 = *reinterpret_cast<const f32x4*>(ws + 48 + 4 * g);
+        const float a_c = exp2_hw(LC);
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const bf16x8 kw0 = scale_frag_k(kt[kh][0], w00, w01);
+          const bf16x8 kw1 = scale_frag_k(kt[kh][1], w10, w11);
+#pragma unroll
+          for (int jt = 0; jt < 2; ++jt) {
+            S[kh][jt] = S[kh][jt] * a_c;
+            S[kh][jt] = pgn_mfma(kw0, vf[jt][0], S[kh][jt]);
+            S[kh][jt] = pgn_mfma(kw1, vf[jt][1], S[kh][jt]);
+          }
+        }
+        __syncthreads();  // A complete; every read of this chunk's S^T tiles done
+        const bf16x8 af0 = frag(At, tq, 0, g);
+        const bf16x8 af1 = TB >= 2 ? frag(At, tq, 1, g) : af0;
+        const __amdgpu_buffer_rsrc_t o_out = o_rows(c);
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) {
+          acc[jt] = pgn_mfma(vf[jt][0], af0, acc[jt]);
+          if (TB >= 2) acc[jt] = pgn_mfma(vf[jt][1], af1, acc[jt]);
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, to_bf16x4(acc[jt])), o_out,
+                                                (tq * ld + j0 + 16 * jt + 4 * g) * (int)sizeof(__bf16), 0, 0);
+        }
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int jt = 0; jt < 2; ++jt) store_T(STb(kh), j0 + 16 * jt, 16 * TB, g, i, S[kh][jt]);
+        __syncthreads();  // end of the chunk
+      }
+    };
+    switch (tb) {
+      case 0: oloop(std::integral_constant<int, 0>{}); break;
+      case 1: oloop(std::integral_constant<int, 1>{}); break;
+      case 2: oloop(std::integral_constant<int, 2>{}); break;
+      default: oloop(std::integral_constant<int, 3>{}); break;
+    }
+    if (Sfin) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            Sfin[soff + (size_t)(64 * kh + 16 * tb + 4 * g + r) * ld + j0 + 16 * jt + i] = S[kh][jt][r];
+    }
+  } else if (w < 12) {
+    // ================= score waves: t block a of the current chunk; wave 8 also the next chunk's decay scan
+    const bool scan = w == 8;
+    auto la_of = [&](int c) {  // chunk c's log-decays (zero past T): a load with no branch
+      const int n0 = c * C;
+      return load_f32_lane(la + (size_t)hw * T + n0, c < NC ? min(C, T - n0) : 0, x.l);
+    };
+    auto run_scan = [&](float la_t, int h) {
+      const float L = wave_prefix_sum(la_t, x.l);
+      const float LC = lane_value(L, 63);
+      float* vs = Vecb(h);
+      vs[x.l] = L * kLog2e;
+      vs[C + x.l] = __expf(L);
+      vs[2 * C + x.l] = __expf(fminf(LC - L, 0.f));
+    };
+    auto sloop = [&](auto a_c) {
+      constexpr int a = decltype(a_c)::value;
+      if (scan) run_scan(la_of(0), 0);
+      __syncthreads();
+      for (int c = 0; c < NC; ++c) {
+        const int h = c & 1;
+        const float la_t = la_of(c + 1);
+        const float* Ls = Vecb(h);
+        const int tq = 16 * a + i;
+        bf16x8 qf[2][2];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int m = 0; m < 2; ++m) qf[kh][m] = frag(Qb(h, kh), tq, m, g);
+        const float Lt = Ls[tq];
+        // K fragments of s blocks read two at a time (all four blocks' would not fit the registers)
+        bf16x8 kf[2][2][2];
+        f32x4 Lsv[2];
+        auto read_k = [&](int sb) {
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int m = 0; m < 2; ++m) kf[sb & 1][kh][m] = frag(Kb(h, kh), 16 * sb + i, m, g);
+          Lsv[sb & 1] = *reinterpret_cast<const f32x4*>(Ls + 16 * sb + 4 * g);
+        };
+        read_k(0);
+        if (a >= 1) read_k(1);
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+          f32x4 pt = zero4();
+          if (sb <= a) {
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+              pt = pgn_mfma(kf[sb & 1][kh][0], qf[kh][0], pt);
+              pt = pgn_mfma(kf[sb & 1][kh][1], qf[kh][1], pt);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int s = 16 * sb + 4 * g + r;
+              if (sb < a)
+                pt[r] *= exp2_hw(Lt - Lsv[sb & 1][r]);
+              else
+                pt[r] = (s <= tq) ? pt[r] * exp2_hw(fminf(Lt - Lsv[sb & 1][r], 0.f)) : 0.f;
+            }
+            if (sb + 2 <= a) read_k(sb + 2);  // into the buffers block sb has finished with (K and decays)
+          }
+          store_T(At, 16 * a, 16 * sb, g, i, pt);
+        }
+        if (scan && c + 1 < NC) run_scan(la_t, h ^ 1);
+        __syncthreads();  // A complete
+        __syncthreads();  // end of the chunk
+      }
+    };
+    switch (w - 8) {
+      case 0: sloop(std::integral_constant<int, 0>{}); break;
+      case 1: sloop(std::integral_constant<int, 1>{}); break;
+      case 2: sloop(std::integral_constant<int, 2>{}); break;
+      default: sloop(std::integral_constant<int, 3>{}); break;
+    }
+  } else {
+    // ================= load waves: thread b carries 16-byte segments b and b + 256 of each of Q0, Q1, K0, K1, V;
+    // two register sets alternate, so a chunk's loads are issued a chunk before it is staged
+    const int b = tid & 255;
+    struct Regs {
+      bf16x8 q[2][2], k[2][2], v[2];
+    };
+    Regs ra, rb;
+    auto load = [&](Regs& r, int c) {
+      const int n0 = c * C, nr = min(C, T - n0);
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          r.q[kh][u] = load_seg(q + koff + (size_t)n0 * ld + 64 * kh, nr, b + 256 * u, ld);
+          r.k[kh][u] = load_seg(k + koff + (size_t)n0 * ld + 64 * kh, nr, b + 256 * u, ld);
+        }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) r.v[u] = load_seg(v + voff + (size_t)n0 * ld, nr, b + 256 * u, ld);
+    };
+    auto stage = [&](const Regs& r, int h) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          put_seg(Qb(h, kh), r.q[kh][u], b + 256 * u);
+          put_seg(Kb(h, kh), r.k[kh][u], b + 256 * u);
+        }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) put_seg(Vb(h), r.v[u], b + 256 * u);
+    };
+    // every load unconditional (chunk indices clamped to the last chunk), so the counter waits stay exact
+    load(ra, 0);
+    load(rb, min(1, NC - 1));
+    stage(ra, 0);
+    load(ra, min(2, NC - 1));
+    __syncthreads();
+    // chunk c: stage chunk c + 1 from the set loaded a chunk ago, then reload that set with chunk c + 3
+    auto phase = [&](Regs& r, int c) {
+      if (c + 1 < NC) stage(r, (c + 1) & 1);
+      load(r, min(c + 3, NC - 1));
+      __syncthreads();  // A complete
+      __syncthreads();  // end of the chunk
+    };
+    for (int c = 0; c < NC; c += 2) {
+      phase(rb, c);
+      if (c + 1 < NC) phase(ra, c + 1);
+    }
+  }
+}
+
 // Segment-parallel forward, for few heads over long sequences: the chunks of each head are split into segments of
 // P chunks that run as separate workgroups of the forward above, once each segment's entering state is known. The
 // state a segment leaves is an affine function of the one it enters, S_out = e^{l} S_in + E, with l the segment's
@@ -1345,6 +1639,15 @@ extern "C" int pragnosia_aspin_chunk_fwd_wide(const void* q, const void* k, cons
   PGN_CHECK_ARG(q && k && v && la && o && S_final && workspace);
   PGN_CHECK_ARG(workspace_bytes >= wide_workspace_bytes(B, H, T, seg_chunks, false));
   char* ws = (char*)workspace;
+  if (kNative128Fwd && seg_chunks >= (T + C - 1) / C) {
+    // one workgroup per (head, value half) over all 128 keys: o written once, no partial sums
+    const hipError_t e = pgn_lds_limit((const void*)aspin_plain_fwd128, kN128Smem);
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL(aspin_plain_fwd128, dim3((unsigned)(2 * B * H)), dim3(kFwdWaves * 64), kN128Smem,
+                       (hipStream_t)stream, (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, S0, (__bf16*)o,
+                       S_final, (__bf16*)sent, (int)T, (int)((T + C - 1) / C));
+    PGN_RETURN_LAUNCH();
+  }
   if (seg_chunks >= (T + C - 1) / C) {
     // two launches of two scans per head, the second adding its o to the first's
     int rc = launch_fwd<true, 1>(q, k, v, la, S0, nullptr, 0, o, nullptr, S_final, sent, nullptr, 2 * B * H, 4 * H, T,
