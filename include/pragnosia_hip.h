@@ -31,7 +31,7 @@ extern "C" {
 /* Tokens per checkpointed state of the exact scan's forward. */
 #define PRAGNOSIA_EXACT_CKPT_TOKENS 8
 
-/* ABI version of this header (21); bumped on any change of the entry points. */
+/* ABI version of this header (22); bumped on any change of the entry points. */
 int pragnosia_abi_version(void);
 
 /* Human-readable name of a return code (static storage). */
@@ -475,6 +475,15 @@ int pragnosia_decode_gemm(const float* x, int64_t B, int64_t K, int mode, const 
  * bit-deterministic). W tiled (and the RMSNorm's weight folded) as for pragnosia_decode_gemm. Replaces the MLP's
  * second nn.Linear + residual and the carrier's RMSNorm + gated output projection + residual (src/model.py:552-560,
  * src/assoc.py:384-512) in the reference's batched graphed decode (src/bench.py:241-317). */
+/* y (B, N) += scale * (W x) + bias for B <= 4, W (N, K) row-major fp32 as for pragnosia_decode_gemv, K a multiple of
+ * 256 up to 4096: one-wave workgroups per (row, K split), two splits when each keeps at least 768 of K (else one),
+ * each adding its partial sum (the first split also the bias) into y with an fp32 atomic: y holds the residual on
+ * entry. x and y must not overlap; not bit-deterministic (the adds' order varies). Replaces the MLP's
+ * second nn.Linear + residual (src/model.py:552-560) in the reference's graphed decode (src/bench.py:241-317) at the
+ * one-wave GEMV's batch sizes. */
+int pragnosia_decode_gemv_acc(const float* x, int64_t B, int64_t K, const float* W, int64_t N, const float* bias,
+                              const float* scale, float* y, void* stream);
+
 int pragnosia_decode_gemm_acc(const float* x, int64_t B, int64_t K, int mode, float eps, const float* Wt, int64_t N,
                               const float* bias, const float* scale, float* y, void* stream);
 

@@ -65,6 +65,7 @@ SIGNATURES = {
     "pragnosia_decode_gemm_waves": [_i64, _i32],
     "pragnosia_decode_gemm": [_p, _i64, _i64, _i32, _p, _f32, _p, _i64, _p, _p, _i32, _p, _p, _p],
     "pragnosia_decode_gemm_acc": [_p, _i64, _i64, _i32, _f32, _p, _i64, _p, _p, _p, _p],
+    "pragnosia_decode_gemv_acc": [_p, _i64, _i64, _p, _i64, _p, _p, _p, _p],
 }
 
 # entry points that return a size (int64) rather than a status code

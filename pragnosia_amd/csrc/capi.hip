@@ -1,7 +1,7 @@
 // Library-level entry points: ABI version and return-code names.
 #include "common.h"
 
-extern "C" int pragnosia_abi_version(void) { return 21; }
+extern "C" int pragnosia_abi_version(void) { return 22; }
 
 extern "C" const char* pragnosia_error_string(int code) {
   if (code == PRAGNOSIA_OK) return "ok";

@@ -258,6 +258,40 @@ __global__ __launch_bounds__(64) void gemv_wave(const float* __restrict__ x, int
   }
 }
 
+// The accumulating GEMV (no normalisation) for B <= 4: y[b][n] += scale * (W x_b)[n] + bias[n], K = 256 KV split
+// SK ways: workgroup (n, ks) of one wave reads the pieces 4 l + 256 u, u in [ks KV, ks KV + KV), of row n and of each
+// input row, sums them over the wave and adds into y (which holds the residual) with an fp32 atomic, the bias with the
+// first split. SK times the workgroups of gemv_wave, each a 1 / SK share of the row.
+template <int NB, int KV>
+__global__ __launch_bounds__(64) void gemv_wave_acc(const float* __restrict__ x, int B, int K,
+                                                    const float* __restrict__ W, int N,
+                                                    const float* __restrict__ bias,
+                                                    const float* __restrict__ scale, float* __restrict__ y) {
+  const int l = threadIdx.x;
+  const int n = blockIdx.x % N, ks = blockIdx.x / N;
+  const float* wr = W + (size_t)n * K + 256 * KV * ks + 4 * l;
+  f32x4 w[KV];
+#pragma unroll
+  for (int u = 0; u < KV; ++u) w[u] = *reinterpret_cast<const f32x4*>(wr + 256 * u);
+  float acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = 0.f;
+#pragma unroll
+  for (int u = 0; u < KV; ++u)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const f32x4 z = b < B ? *reinterpret_cast<const f32x4*>(x + (size_t)b * K + 256 * KV * ks + 4 * l + 256 * u)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+      acc[b] += w[u][0] * z[0] + w[u][1] * z[1] + w[u][2] * z[2] + w[u][3] * z[3];
+    }
+  wave_sum_many<NB>(acc, l);
+  constexpr int sh = 6 - log2_of<NB>();
+  if ((l & ((1 << sh) - 1)) == 0) {
+    const int b = l >> sh;
+    if (b < B) atomicAdd(y + (size_t)b * N + n, (scale ? *scale : 1.f) * acc[0] + (bias && ks == 0 ? bias[n] : 0.f));
+  }
+}
+
 template <int RPW, int NB, int KV, int MODE>
 int launch_wave(const float* x, int B, const float* lnw, const float* lnb, float eps, const float* W, int N,
                 const float* bias, const float* scale, int act, const float* resid, float* y, hipStream_t st) {
@@ -359,4 +393,48 @@ extern "C" int pragnosia_decode_gemv_rms(const float* x, int64_t B, int64_t K, c
                            resid, y, (hipStream_t)stream);
   return dispatch_rpw<2>((int)(K / 256), x, (int)B, rms_weight, nullptr, rms_eps, W, (int)N, bias, scale, act, resid,
                          y, (hipStream_t)stream);
+}
+
+// K split of the accumulating GEMV: two when that keeps at least 3 pieces a lane (768 of K), else none. At batch 1 on
+// the d 768 LM (K 3072), step 0.2653 ms with the residual-epilogue GEMV, 0.2612-0.2624 unsplit in place, 0.2612-0.2615
+// with two splits, 0.2648 with three, 0.2687-0.2691 with four (variant builds, one box, A/B twice).
+extern "C" int pragnosia_decode_gemv_acc(const float* x, int64_t B, int64_t K, const float* W, int64_t N,
+                                         const float* bias, const float* scale, float* y, void* stream) {
+  PGN_CHECK_ARG(x && W && y && B > 0 && B <= 4 && K > 0 && N > 0 && K % 256 == 0 && K <= 4096);
+  PGN_CHECK_ARG(N * 4 < ((int64_t)1 << 31) && B * K < ((int64_t)1 << 31) && N * K < ((int64_t)1 << 31));
+  PGN_CHECK_ARG(((uintptr_t)x | (uintptr_t)W) % 16 == 0);
+  // the atomics into y run while other workgroups still read x
+  const uintptr_t xa = (uintptr_t)x, ya = (uintptr_t)y;
+  PGN_CHECK_ARG(xa + (uintptr_t)(B * K * 4) <= ya || ya + (uintptr_t)(B * N * 4) <= xa);
+  const int KV = (int)(K / 256);
+  const int SK = KV % 2 == 0 && KV / 2 >= 3 ? 2 : 1;
+  const int kv = KV / SK;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)(N * SK));
+#define PGN_ACC_KV(V)                                                                                              \
+  if (kv == V) {                                                                                                   \
+    if (B == 1)                                                                                                    \
+      hipLaunchKernelGGL((gemv_wave_acc<1, V>), grid, dim3(64), 0, st, x, (int)B, (int)K, W, (int)N, bias, scale, y); \
+    else                                                                                                           \
+      hipLaunchKernelGGL((gemv_wave_acc<4, V>), grid, dim3(64), 0, st, x, (int)B, (int)K, W, (int)N, bias, scale, y); \
+    PGN_RETURN_LAUNCH();                                                                                           \
+  }
+  PGN_ACC_KV(1)
+  PGN_ACC_KV(2)
+  PGN_ACC_KV(3)
+  PGN_ACC_KV(4)
+  PGN_ACC_KV(5)
+  PGN_ACC_KV(6)
+  PGN_ACC_KV(7)
+  PGN_ACC_KV(8)
+  PGN_ACC_KV(9)
+  PGN_ACC_KV(10)
+  PGN_ACC_KV(11)
+  PGN_ACC_KV(12)
+  PGN_ACC_KV(13)
+  PGN_ACC_KV(14)
+  PGN_ACC_KV(15)
+  PGN_ACC_KV(16)
+#undef PGN_ACC_KV
+  return PRAGNOSIA_ERR_UNSUPPORTED;
 }

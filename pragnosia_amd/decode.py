@@ -41,6 +41,9 @@ GEMV_MAX_BATCH = 4
 GEMM_ACC_MIN_K = 1024
 # ... and the carrier's RMSNorm + gated o-projection adds into the residual in place, its K split over head groups.
 OPROJ_ACC = True
+# Up to GEMV_MAX_BATCH sequences, the MLP's second layer as the accumulating one-wave GEMV (decode_gemv_acc_: K split
+# over workgroups adding into the residual in place).
+GEMV_ACC = True
 
 
 def _rms_gemv_ok(K: int) -> bool:
@@ -263,7 +266,11 @@ class GreedyDecoder:
                                        self.p0s[i:i + 1], 0.0, mx.on.weight, on_eps, mx.o.weight, self.sig[i], h)
                 x1 = h
                 hm = self._dense(x1, mp.a.weight, mp.n, bias=mp.a.bias, act=1)
-                h = self._dense(hm, mp.b.weight, None, bias=mp.b.bias, resid=x1)
+                if GEMV_ACC and hm.shape[1] % 256 == 0 and hm.shape[1] <= 4096:
+                    op.decode_gemv_acc_(hm, mp.b.weight, mp.b.bias, None, x1)  # x1 += W hm + bias, in place
+                    h = x1
+                else:
+                    h = self._dense(hm, mp.b.weight, None, bias=mp.b.bias, resid=x1)
                 continue
             # at small batches the per-head RMSNorm moves into the o-projection's GEMV, so the carrier step can run
             # dk / 16 workgroups per head (always so for 128-dim heads, whose step writes only the raw output)

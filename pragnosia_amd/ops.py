@@ -1531,6 +1531,32 @@ def _(x, Wt, N, mode, csum, eps, bias, scale, act, resid):
     return x.new_empty(x.shape[0], N, dtype=torch.float32)
 
 
+@torch.library.custom_op("pragnosia::decode_gemv_acc_", mutates_args=("y",))
+def decode_gemv_acc_(x: Tensor, W: Tensor, bias: Optional[Tensor], scale: Optional[Tensor], y: Tensor) -> None:
+    """y (B, N) += scale * (W x) + bias in place for B <= 4, W (N, K) fp32 row-major, K a multiple of 256 up to 4096:
+    the one-wave GEMV with its K split over workgroups that add their partial sums into y (which holds the residual).
+    Adds in varying order: not bit-deterministic. Not differentiable."""
+    _require_gpu(x, W, bias, scale, y)
+    if x.dim() != 2 or y.dim() != 2 or y.shape[0] != x.shape[0] or not 1 <= x.shape[0] <= 4:
+        raise PragnosiaError(f"decode_gemv_acc_: x (B, K) and y (B, N) with B <= 4 expected, got {tuple(x.shape)}, "
+                             f"{tuple(y.shape)}")
+    B_, K_ = x.shape
+    N = y.shape[1]
+    if K_ % 256 or K_ > 4096:
+        raise PragnosiaError(f"decode_gemv_acc_: K = {K_} must be a multiple of 256 up to 4096")
+    if y.dtype != torch.float32 or not y.is_contiguous():
+        raise PragnosiaError("decode_gemv_acc_: y must be contiguous fp32 (it is added into in place)")
+    _expect("decode_gemv_acc_", x.device, W=(W, (N, K_)), bias=(bias, (N,)), scale=(scale, ()), y=(y, (B_, N)))
+    x, W, bias, scale = _f32(x), _f32(W), _f32(bias), _f32(scale)
+    check(lib().pragnosia_decode_gemv_acc(_ptr(x), B_, K_, _ptr(W), N, _ptr(bias), _ptr(scale), _ptr(y),
+                                          _stream(x)), "pragnosia_decode_gemv_acc")
+
+
+@decode_gemv_acc_.register_fake
+def _(x, W, bias, scale, y):
+    return None
+
+
 @torch.library.custom_op("pragnosia::decode_gemm_acc_", mutates_args=("y",))
 def decode_gemm_acc_(x: Tensor, Wt: Tensor, group_mode: int, eps: float, bias: Optional[Tensor],
                      scale: Optional[Tensor], y: Tensor) -> None:

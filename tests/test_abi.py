@@ -41,7 +41,7 @@ def test_binding_matches_header():
 
 
 def test_abi_version_and_error_strings(L):
-    assert L.pragnosia_abi_version() == 21
+    assert L.pragnosia_abi_version() == 22
     assert L.pragnosia_error_string(0) == b"ok"
     assert b"invalid argument" in L.pragnosia_error_string(-1)
 
@@ -179,6 +179,10 @@ def test_decode_gemm_plans_and_rejections(L):
     assert acc(X + 8, 64, 3072, Y) == -1                               # misaligned input
     assert acc(X, 64, 760, Y) == -2 and acc(X, 0, 3072, Y) == -1       # K not whole 16-wide steps; no rows
     assert acc(X, 64, 768, Y, 1) == -1 and acc(X, 64, 1088, Y, 2) == -2   # no LayerNorm mode; 17 groups of 64
+    gacc = lambda x, B, K, y: L.pragnosia_decode_gemv_acc(ctypes.c_void_p(x), B, K, one, 768, null, null,
+                                                          ctypes.c_void_p(y), null)
+    assert gacc(X, 5, 3072, Y) == -1 and gacc(X, 1, 3000, Y) == -1     # more than 4 rows; K not 256 KV
+    assert gacc(X, 1, 4352, Y) == -1 and gacc(X, 1, 3072, X + 64) == -1  # K past 4096; y inside x
 
 
 def test_decode_oproj_rejects_overlaps(L):

@@ -242,3 +242,23 @@ def test_decode_tail_matches_torch(B, V):
     ctr[0] = n_rows
     decode_tail(lg, emb, pemb, ctr[0], ctr[1], pos[1], pos[0], out, tok, h, None, None)
     assert int(ctr[1]) == n_rows + 1 and int(pos[0]) == 1 and torch.equal(out[3], want)
+
+
+@pytest.mark.parametrize("B", [1, 3, 4])
+@pytest.mark.parametrize("K,N", [(3072, 768), (2816, 704), (1024, 300), (256, 64), (4096, 100)])
+def test_decode_gemv_acc_adds_into_residual(B, K, N):
+    """decode_gemv_acc_ (y += scale * W x + bias in place, K split over one-wave workgroups adding with atomics)
+    against fp64 torch at 1e-5 (3072: two splits of 1536; 2816: one; 1024: one; 4096: two of 2048)."""
+    g = torch.Generator(device="cuda").manual_seed(B + K + N)
+    x = torch.randn(B, K, device="cuda", generator=g)
+    W = torch.randn(N, K, device="cuda", generator=g) * 0.05
+    bias = torch.randn(N, device="cuda", generator=g)
+    scale = torch.rand(1, device="cuda", generator=g)
+    resid = torch.randn(B, N, device="cuda", generator=g)
+    y = resid.clone()
+    torch.ops.pragnosia.decode_gemv_acc_(x, W, bias, scale, y)
+    ref = resid.double() + scale.double() * (x.double() @ W.double().t()) + bias.double()
+    assert rel(y, ref) < 1e-5, (B, K, N)
+    y2 = resid.clone()
+    torch.ops.pragnosia.decode_gemv_acc_(x, W, None, None, y2)
+    assert rel(y2, resid.double() + x.double() @ W.double().t()) < 1e-5

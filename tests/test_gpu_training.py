@@ -111,6 +111,7 @@ def _samples():
         ("decode_gemm", (r(20, 256), r(64 * 256), 50, 1, r(50), 1e-5, r(50), None, 1, r(20, 50))),
         ("decode_gemm", (r(20, 256), r(64 * 256), 50, 2, None, 1e-6, None, r(1), 0, None)),
         ("decode_gemm_acc_", (r(20, 1024), r(64 * 1024), 0, 0.0, r(50), r(1), r(20, 50))),   # two K splits of 512
+        ("decode_gemv_acc_", (r(2, 1536), r(50, 1536), r(50), r(1), r(2, 50))),   # two K splits of 768
         ("decode_gemm_acc_", (r(20, 768), r(64 * 768), 2, 1e-6, None, r(1), r(20, 50))),     # three splits of 4 heads
         ("aspin_delta_windows", (q.detach(), k.detach(), v.detach(), la.detach(), be.detach(), S0.detach(), th, 64)),
     ]
