@@ -967,6 +967,10 @@ def profile_kernels(reps=10):
                 ops._delta_pass(*args, True, False)
             for _ in range(reps):
                 ops._delta_pass(*args, False, True)
+    # the plain rule at head dim 128 (configs[2]'s width as 6 heads of 128): the native forward
+    x = aspin_inputs(16, 6, 512, 128, 3, "plain", dev)
+    for _ in range(reps):
+        op.aspin_chunk_wide(x["q"], x["k"], x["v"], x["la"], None, True)
     B, T, D = 16, 512, 768
     u, lm, an, gy = (torch.randn(B, T, D, device=dev) for _ in range(4))
     lm = -lm.abs()

@@ -625,8 +625,8 @@ def _wide_workspace(op: str, B: int, H: int, T: int, P: int, backward: bool, dev
 @torch.library.custom_op("pragnosia::aspin_chunk_wide", mutates_args=())
 def aspin_chunk_wide(q: Tensor, k: Tensor, v: Tensor, la: Tensor, S0: Optional[Tensor],
                      want_sent: bool) -> tuple[Tensor, Tensor, Tensor]:
-    """Plain-rule chunked scan at head dim 128, as four 64 x 64 scans per head (key half x value half) that read
-    the 128-wide rows in place. q, k, v (B, H, T, 128) (cast to bf16), la (B, H, T) fp32, S0 (B, H, 128, 128) fp32 or
+    """Plain-rule chunked scan at head dim 128: one pass per (head, value half) over all 128 keys where each head is
+    one segment, else four 64 x 64 scans per head (key half x value half) that read the 128-wide rows in place. q, k, v (B, H, T, 128) (cast to bf16), la (B, H, T) fp32, S0 (B, H, 128, 128) fp32 or
     None. Returns (o bf16 (B, H, T, 128), S_final fp32 (B, H, 128, 128), sent bf16 (B, H, 4, NC, 64, 64): the state
     entering every chunk per scan, scan 2 kh + vh holding block (rows 64 kh.., columns 64 vh..); or an empty tensor
     if not wanted). `wide_sent` turns sent into (B, H, NC, 128, 128)."""
