@@ -211,3 +211,30 @@ def test_wide_lm_forward_carried_and_graphed_decode():
     assert torch.equal(toks_g.cpu(), toks_e.cpu()) and torch.equal(toks_u.cpu(), toks_e.cpu())
     _, lgs_r = M.greedy_decode(sd, prompt, 13, layers=2, mixer="hspin", heads=2, forced=toks_e.cpu())
     assert rel(lgs_e, lgs_r) < TOL_OUT
+
+
+def test_wide_native_forward_full_shape():
+    """The native 128-key forward (one workgroup per head and value half, the pair numbered 8 apart) at configs[2]'s
+    width, B16 H6 T512 with an entering state, through the C ABI with whole-sequence segments: o, the final state and
+    every entering state against the fp64 oracle (2e-2)."""
+    from pragnosia_amd import ops
+    from pragnosia_amd._lib import lib
+    L = lib()
+    B, H, T, D = 16, 6, 512, 128
+    NC = T // 64
+    q, k, v, la, S0, _, _ = _wide_inputs(B, H, T, 128)
+    o_r, S_r, sent_r = OA.scan_twopass(*(t.double() for t in (q, k, v, la, S0)), 64)
+    q, k, v, la, S0 = (t.cuda().contiguous() for t in (q, k, v, la, S0))
+    o = torch.empty(B, H, T, D, device="cuda", dtype=torch.bfloat16)
+    S = torch.empty(B, H, D, D, device="cuda")
+    sent = torch.empty(B, H, 4, NC, 64, 64, device="cuda", dtype=torch.bfloat16)
+    ws = torch.empty(L.pragnosia_aspin_chunk_wide_workspace_bytes(B, H, T, D, 64, NC, 0), device="cuda",
+                     dtype=torch.uint8)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    print(f"wide native fwd B{B} H{H} T{T}", flush=True)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert L.pragnosia_aspin_chunk_fwd_wide(P(q), P(k), P(v), P(la), P(S0), P(o), P(S), P(sent), P(ws), ws.numel(),
+                                            B, H, T, D, 64, NC, st) == 0
+    torch.cuda.synchronize()
+    assert rel(o, o_r) < TOL_OUT and rel(S, S_r) < TOL_OUT
+    assert rel(ops.wide_sent(sent).float(), sent_r) < TOL_OUT
