@@ -383,10 +383,6 @@ __global__ __launch_bounds__(kFwdWaves * 64) void aspin_plain_fwd(
 //       read of the current ones was before the barrier).
 // `sent` keeps the wide mode's per-scan layout, (B, 4H, NC, 64, 64) at scan 4 hw + 2 kh + vh, so the wide backward
 // reads it unchanged. Unsegmented only (one workgroup walks all chunks of its scan).
-#ifndef PGN_NATIVE128_FWD
-#define PGN_NATIVE128_FWD 1
-#endif
-constexpr bool kNative128Fwd = PGN_NATIVE128_FWD;  // the unsegmented 128-key forward as aspin_plain_fwd128
 constexpr int kN128Buf = 5 * TILE * (int)sizeof(__bf16) + 3 * C * (int)sizeof(float);  // Q0, Q1, K0, K1, V, vectors
 constexpr size_t kN128Smem = 2 * (size_t)kN128Buf + 3 * TILE * sizeof(__bf16);       // two sets, A, S^T x 2
 
@@ -1642,7 +1638,7 @@ extern "C" int pragnosia_aspin_chunk_fwd_wide(const void* q, const void* k, cons
   PGN_CHECK_ARG(q && k && v && la && o && S_final && workspace);
   PGN_CHECK_ARG(workspace_bytes >= wide_workspace_bytes(B, H, T, seg_chunks, false));
   char* ws = (char*)workspace;
-  if (kNative128Fwd && seg_chunks >= (T + C - 1) / C) {
+  if (seg_chunks >= (T + C - 1) / C) {
     // one workgroup per (head, value half) over all 128 keys: o written once, no partial sums
     const hipError_t e = pgn_lds_limit((const void*)aspin_plain_fwd128, kN128Smem);
     if (e != hipSuccess) return (int)e;
@@ -1651,14 +1647,6 @@ extern "C" int pragnosia_aspin_chunk_fwd_wide(const void* q, const void* k, cons
                        (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, la, S0, (__bf16*)o, S_final,
                        (__bf16*)sent, (int)T, (int)((T + C - 1) / C), (int)(B * H));
     PGN_RETURN_LAUNCH();
-  }
-  if (seg_chunks >= (T + C - 1) / C) {
-    // two launches of two scans per head, the second adding its o to the first's
-    int rc = launch_fwd<true, 1>(q, k, v, la, S0, nullptr, 0, o, nullptr, S_final, sent, nullptr, 2 * B * H, 4 * H, T,
-                                 seg_chunks, (hipStream_t)stream);
-    if (rc != PRAGNOSIA_OK) return rc;
-    return launch_fwd<true, 2>(q, k, v, la, S0, nullptr, 0, o, nullptr, S_final, sent, nullptr, 2 * B * H, 4 * H, T,
-                               seg_chunks, (hipStream_t)stream);
   }
   void* o1 = ws;
   const int rc = launch_fwd<true>(q, k, v, la, S0, nullptr, 0, o, o1, S_final, sent, ws + wide_slot_bytes(B, H, T),
