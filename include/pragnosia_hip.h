@@ -140,7 +140,9 @@ int pragnosia_aspin_chunk_bwd_seg(const void* q, const void* k, const void* v, c
  * (S0, dS_final, dS0 may be NULL); sent: the entering states per scan, (B, H, 4, NC, 64, 64) bf16 (scan 2 kh + vh
  * holds block rows 64 kh.., columns 64 vh..; NC = ceil(T / 64)), written by the forward when not NULL and read by the
  * backward. seg_chunks: the segment length of the segment-parallel passes (as pragnosia_aspin_chunk_fwd_seg, no
- * windows); at least NC runs one workgroup per scan. `workspace`: caller-allocated device memory of at least
+ * windows); at least NC runs one workgroup per scan: the forward then as one workgroup per (head, value half) over
+ * all 128 keys (o written once, no partial; the workspace unused), the backward as two launches of two scans per head,
+ * the second adding the first's partial outputs. `workspace`: caller-allocated device memory of at least
  * pragnosia_aspin_chunk_wide_workspace_bytes(..., backward) bytes. */
 int64_t pragnosia_aspin_chunk_wide_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk,
                                                    int64_t seg_chunks, int32_t backward);
