@@ -142,7 +142,7 @@ int pragnosia_aspin_chunk_bwd_seg(const void* q, const void* k, const void* v, c
  * backward. seg_chunks: the segment length of the segment-parallel passes (as pragnosia_aspin_chunk_fwd_seg, no
  * windows); at least NC runs one workgroup per scan: the forward then as one workgroup per (head, value half) over
  * all 128 keys (o written once, no partial; the workspace unused), the backward as two launches of two scans per head,
- * the second adding the first's partial outputs. `workspace`: caller-allocated device memory of at least
+ * the second adding the first's partial outputs (dla with fp32 atomics: not the same bits run to run). `workspace`: caller-allocated device memory of at least
  * pragnosia_aspin_chunk_wide_workspace_bytes(..., backward) bytes. */
 int64_t pragnosia_aspin_chunk_wide_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int64_t chunk,
                                                    int64_t seg_chunks, int32_t backward);

@@ -844,6 +844,7 @@ constexpr int kVec = 11 * C;
 // dla of one chunk from its vector set: dL_t = rowM_t - colM_t + eL_t qz_t - w_t dwv_t, the chunk's last token adds
 // sum_s w_s dwv_s + a <S_c, dS>, and dla is the reverse inclusive cumulative sum of dL (plus `part`, lane t's partial
 // from an earlier launch, when accumulating). One wave, lane = t.
+template <bool ATOMIC = false>
 PGN_DEVICE void plain_dla(const float* vs, int lane, __amdgpu_buffer_rsrc_t out, float part = 0.f) {
   const float* Ls = vs;
   const float* eLs = vs + C;
@@ -860,7 +861,10 @@ PGN_DEVICE void plain_dla(const float* vs, int lane, __amdgpu_buffer_rsrc_t out,
   const float sd = wave_sum((sdot[t] + sdot[C + t]) + (sdot[2 * C + t] + sdot[3 * C + t]));
   if (t == C - 1) dL += wdw + exp2_hw(Ls[C - 1]) * sd;
   dL = wave_suffix_sum(dL, t) + part;
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, dL), out, 4 * t, 0, 0);
+  if constexpr (ATOMIC)
+    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(dL, out, 4 * t, 0, 0);
+  else
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, dL), out, 4 * t, 0, 0);
 }
 
 // L (inclusive cumulative sum of the chunk's la, lane = t, stored in base 2: L log2 e), e^L and w = exp(L_C - L) into a
@@ -905,13 +909,18 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
   constexpr int ld = Rows::ld;
   const size_t koff = R.keys(T), voff = R.vals(T);
   // dla slots: narrow heads one; wide heads in one launch four (slot s = bh & 3: dla, then dla1 s - 1 of nwide heads
-  // each); in two launches two (slot kh)
+  // each); in two launches, the first writes slot kh (dla, dla1) and the second adds its terms into dla with fp32
+  // atomics, the key-half-1 scan with the first launch's dla1 (so no pass sums the slots; two adds an element, in
+  // arrival order)
   float* dlar = dla + (size_t)R.hw * T;
+  const float* dlapr = nullptr;  // where the second launch's partial comes from (none: a zero-size range)
   if constexpr (WIDE && PASS == 0) {
     const int nwide = (int)(gridDim.x / nseg) >> 2;  // wide heads in the launch
     if (bh & 3) dlar = dla1 + ((size_t)((bh & 3) - 1) * nwide + R.hw) * T;
-  } else if constexpr (WIDE) {
+  } else if constexpr (WIDE && PASS == 1) {
     if (R.kh) dlar = dla1 + (size_t)R.hw * T;
+  } else if constexpr (WIDE) {
+    if (R.kh) dlapr = dla1 + (size_t)R.hw * T;
   }
 
   // The two groups run separate loops (the branch is on a wave-uniform value) that meet at the same barriers: each
@@ -1189,9 +1198,12 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         load(max(cc - 1, c0));
         // wave 0: this chunk's dla partial, used when its dla is written after the next chunk's phase
         float dlap_next = 0.f;
-        if constexpr (Rows::kAccumulate && WL == 0)
-          dlap_next = __builtin_bit_cast(
-              float, __builtin_amdgcn_raw_buffer_load_b32(dla_rows(cc), 4 * x.l, 0, 0));
+        if constexpr (Rows::kAccumulate && WL == 0) {
+          const int t0p = cc * C;
+          const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+              const_cast<float*>(dlapr ? dlapr + t0p : dla), (short)0, dlapr ? 4 * min(C, T - t0p) : 0, 0x00020000);
+          dlap_next = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, 4 * x.l, 0, 0));
+        }
         BWD_STAMP(4 + 2 * cc);  // the chunk's phase: operand reads, contractions, result stores
         const int t0 = cc * C, h = cc & 1;
         const __bf16* Qs = stg + h * kBwdStage;
@@ -1322,7 +1334,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
         });
         BWD_STAMP(5 + 2 * cc);
         if (w == 0 && cc < cl)  // the later chunk's dla, from the other vector set (before the scan below)
-          plain_dla(vec + (h ^ 1) * kVec, x.l, dla_rows(cc + 1), dlap);
+          plain_dla<Rows::kAccumulate>(vec + (h ^ 1) * kVec, x.l, dla_rows(cc + 1), dlap);
         dlap = dlap_next;
         if (cc > c0) stage(h ^ 1);
         __syncthreads();
@@ -1335,7 +1347,7 @@ __global__ __launch_bounds__(512) void aspin_plain_bwd(
       default: dloop(std::integral_constant<int, 3>{}); break;
     }
     if (w == 0)  // the first chunk's dla (its vector set)
-      plain_dla(vec + (c0 & 1) * kVec, x.l, dla_rows(c0), dlap);
+      plain_dla<Rows::kAccumulate>(vec + (c0 & 1) * kVec, x.l, dla_rows(c0), dlap);
     if (dS0) {
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt)
@@ -1677,15 +1689,8 @@ extern "C" int pragnosia_aspin_chunk_bwd_wide(const void* q, const void* k, cons
     int rc = launch_bwd<true, 1>(q, k, v, la, sent, dO, dS_final, dq, nullptr, dk, nullptr, dv, nullptr, dla, dla1,
                                  dS0, nullptr, 2 * B * H, T, seg_chunks, (hipStream_t)stream);
     if (rc != PRAGNOSIA_OK) return rc;
-    rc = launch_bwd<true, 2>(q, k, v, la, sent, dO, dS_final, dq, nullptr, dk, nullptr, dv, nullptr, dla, dla1, dS0,
-                             nullptr, 2 * B * H, T, seg_chunks, (hipStream_t)stream);
-    if (rc != PRAGNOSIA_OK) return rc;
-    JoinArgs a = {};
-    a.dla = dla;
-    a.w = dla1;
-    a.m = B * H * T;
-    a.nw = 1;
-    return launch_join(a, (hipStream_t)stream);
+    return launch_bwd<true, 2>(q, k, v, la, sent, dO, dS_final, dq, nullptr, dk, nullptr, dv, nullptr, dla, dla1,
+                               dS0, nullptr, 2 * B * H, T, seg_chunks, (hipStream_t)stream);
   }
   void* segws = ws + 3 * slot + align256(3 * B * H * T * (int64_t)sizeof(float));
   const int rc = launch_bwd<true>(q, k, v, la, sent, dO, dS_final, dq, dq1, dk, dk1, dv, dv1, dla, dla1, dS0, segws,
